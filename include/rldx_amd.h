@@ -1,0 +1,173 @@
+/*
+ * rldx_amd — C ABI of the MI355X (gfx950) kernels for RLDX-1's real-time
+ * inference hot path: fused SwiGLU, fused QK-RMSNorm + RoPE (rotate-half and
+ * interleaved), and flash attention (MSAT joint attention, GQA causal prefill).
+ *
+ * Conventions shared by every entry point
+ *   - All tensor pointers are DEVICE pointers owned by the caller.  bf16 data is
+ *     passed as raw 16-bit words (uint16_t storage, IEEE bfloat16 bits).
+ *   - Strides are in ELEMENTS; the innermost (head_dim / feature) dimension is
+ *     contiguous.  Vector paths need 16-byte aligned rows; the functions
+ *     validate and return hipErrorInvalidValue instead of guessing.
+ *   - No entry point allocates, synchronises the host or keeps mutable state:
+ *     each only enqueues kernels on `stream`, so all of them are reentrant and
+ *     can be captured into a hipGraph.
+ *   - Errors: argument validation -> hipErrorInvalidValue (nothing enqueued);
+ *     otherwise the result of hipGetLastError() after the launch.
+ *
+ * Reference interfaces replaced (paths relative to the RLDX-1 repository):
+ *   see the comment above each function.
+ */
+#ifndef RLDX_AMD_H_
+#define RLDX_AMD_H_
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* SwiGLU                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * y[r, j] = bf16( bf16(silu(g)) * u ),  g = x[r, j] (+ bias[j]),
+ *                                        u = x[r, n_half + j] (+ bias[n_half + j])
+ * for r < rows, j < n_half.  Matches eager `F.silu(x1) * x2` bit for bit
+ * (two bf16 roundings); with `bias` (nullable, [2*n_half] bf16) each half is
+ * first rounded as bf16(x + b).
+ *
+ * Replaces: SwiGLUFFN.forward activation (rldx/model/modules/action_model/ops.py:157-161),
+ *   SS-block / LLM-chain `F.silu(x1) * x2`
+ *   (rldx/inference/action_model/single_stream/engine/custom_single_stream_chain.py:54-55,
+ *    rldx/inference/backbone/llm/engine/custom_llm_chain.py:133-135).
+ */
+hipError_t rldx_swiglu_bf16(const void* x, int64_t ldx, const void* bias, void* y, int64_t ldy, int64_t rows,
+                            int64_t n_half, hipStream_t stream);
+
+/*
+ * Two SwiGLU groups (SA and VL) in ONE launch; x rows are contiguous
+ * [m, 2*n_half], outputs [m, n_half].  Biases are both given or both null.
+ *
+ * Replaces: fused_grouped_swiglu(sa_w12_out, sa_bias, vl_w12_out, vl_bias, ...)
+ *   (rldx/inference/action_model/double_stream/engine/kernels/grouped_swiglu.py:212-257)
+ *   behind ds::grouped_swiglu (.../double_stream/engine/ops/op_grouped_swiglu.py:12-49).
+ */
+hipError_t rldx_grouped_swiglu_bf16(const void* sa_x, const void* sa_bias, const void* vl_x, const void* vl_bias,
+                                    void* sa_y, void* vl_y, int64_t m_sa, int64_t m_vl, int64_t n_half_sa,
+                                    int64_t n_half_vl, hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* QK-RMSNorm + rotate-half RoPE (Qwen3-VL convention)                       */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * q' = apply_rotary_pos_emb(q_norm(q)), k' likewise, for q [B, S, Hq, D] and
+ * k [B, S, Hk, D] with strides {batch, seq, head} (3 int64 each; D contiguous).
+ * cos/sin are [B or 1, S, D] tables (strides {batch, seq}; batch stride 0
+ * broadcasts) built on the host.  head_dim 64 or 128.  eps as in the model.
+ * fp32 variant: every step in fp32.  bf16 variant: eager bf16 rounding order
+ * (bf16(x*rsqrt) -> bf16(w*.) -> bf16(y*cos), bf16(rot*sin) -> bf16(sum)).
+ *
+ * Replaces: Qwen3VLTextRMSNorm.forward + apply_rotary_pos_emb
+ *   (rldx/model/modules/backbone/modeling_qwen3_vl.py:356-371, :377-401),
+ *   the QK prologue of fused_llm_attention (.../backbone/llm/engine/kernels/fused_llm_attention.py:617-647).
+ */
+hipError_t rldx_qk_rmsnorm_rope_half_f32(const float* q, const float* k, const float* q_w, const float* k_w,
+                                         const float* cos, const float* sin, float* q_out, float* k_out,
+                                         int64_t batch, int64_t seq, int64_t q_heads, int64_t k_heads,
+                                         int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
+                                         const int64_t* q_out_strides, const int64_t* k_out_strides,
+                                         const int64_t* cos_strides, float eps, hipStream_t stream);
+
+hipError_t rldx_qk_rmsnorm_rope_half_bf16(const void* q, const void* k, const void* q_w, const void* k_w,
+                                          const void* cos, const void* sin, void* q_out, void* k_out,
+                                          int64_t batch, int64_t seq, int64_t q_heads, int64_t k_heads,
+                                          int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
+                                          const int64_t* q_out_strides, const int64_t* k_out_strides,
+                                          const int64_t* cos_strides, float eps, hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* MSAT multi-stream QKV gather + QK-RMSNorm + interleaved RoPE             */
+/* ------------------------------------------------------------------------ */
+
+/* One stream of the joint sequence (VL / SA / P), in joint-sequence order. */
+typedef struct rldx_msat_stream {
+  const void* qkv;         /* [rows, >= 3*H*D] bf16, packed Q | K | V columns        */
+  int64_t qkv_row_stride;  /* elements                                                */
+  int64_t rows;            /* tokens in this stream                                   */
+  const void* q_norm_w;    /* [D] bf16 RMSNorm weight of this stream's Q              */
+  const void* k_norm_w;    /* [D] bf16                                                */
+  const float* rope_cos;   /* [rows, D/2] fp32 cos table, or NULL: no rotary          */
+  const float* rope_sin;   /* [rows, D/2] fp32 sin table (NULL iff rope_cos is NULL)  */
+  int64_t rope_row_stride; /* elements                                                */
+} rldx_msat_stream_t;
+
+/*
+ * For 1..3 streams concatenated in order (M = sum of rows), writes Q, K, V of
+ * layout (H, M, D) at q_out/k_out/v_out with strides {out_head_stride,
+ * out_row_stride}:
+ *   Q/K = to_bf16(w * (x * rsqrt(mean(x^2) + eps)))       (one rounding)
+ *   then, on streams with tables, the interleaved complex rotation in fp32,
+ *   rounded once; V is copied.
+ *
+ * Replaces: rmsnorm_rope_kernel (ds) / rmsnorm_rope_kernel_3way
+ *   (rldx/inference/action_model/double_stream/engine/kernels/rmsnorm_rope_ds.py:11-231,
+ *    rmsnorm_rope_ds_3way.py:22-386), their ss counterparts
+ *   (.../single_stream/engine/kernels/rmsnorm_rope_ss.py:11-192, rmsnorm_rope_ss_3way.py:17-343),
+ *   with the eager semantics of RMSNorm (rldx/model/modules/norms.py:18-22) and
+ *   apply_rotary_emb (rldx/model/modules/action_model/ops.py:48-67).
+ */
+hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* streams, int32_t num_streams, int64_t heads,
+                                        int64_t head_dim, void* q_out, void* k_out, void* v_out,
+                                        int64_t out_head_stride, int64_t out_row_stride, float eps,
+                                        hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Attention                                                                */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * O = softmax(Q K^T * scale + key_bias[b, key] (+ causal)) V, bf16 in/out,
+ * fp32 softmax.  Q [B, Hq, Sq, D], K/V [B, Hkv, Sk, D], O [B, Hq, Sq, D] given
+ * by strides {batch, head, seq} (3 int64 each, D contiguous; any permutation of
+ * the outer dims works, e.g. token-major [S, H, D]).  Query head h reads KV
+ * head h / (Hq / Hkv) (GQA; Hq % Hkv == 0).  key_bias is an optional fp32
+ * [B, Sk] additive mask (0 / -inf for key padding), row stride
+ * key_bias_batch_stride.  causal != 0: key j visible to query i iff j <= i
+ * (top-left aligned, as SDPA's is_causal).  head_dim 64 or 128.
+ *
+ * Replaces: F.scaled_dot_product_attention inside ds::fused_attention_2way /
+ *   _3way and ss::fused_attention_2way / _3way
+ *   (rldx/inference/action_model/double_stream/engine/ops/op_fused_attention.py:77-82,
+ *    op_fused_attention_3way.py:111-116), eager joint attention
+ *   (rldx/model/modules/action_model/blocks.py:577-579, :866), and the causal
+ *   GQA core of fused_llm_attention_direct_kernel
+ *   (rldx/inference/backbone/llm/engine/kernels/fused_llm_attention.py:379-770).
+ */
+hipError_t rldx_attention_fwd_bf16(const void* q, const void* k, const void* v, void* o, int64_t batch,
+                                   int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k,
+                                   int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
+                                   const int64_t* v_strides, const int64_t* o_strides, const float* key_bias,
+                                   int64_t key_bias_batch_stride, float scale, int32_t causal,
+                                   hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Host-side diagnostics (no reference counterpart)                         */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Runs the SwiGLU element function the GPU kernels use, on the CPU, for n
+ * (gate, up) bf16 pairs.  Exists so that the CPU test suite can verify the
+ * silu/product rounding exhaustively over all 65536 bf16 inputs without a GPU.
+ * Not used by any product path.  Returns 0 on success.
+ */
+int rldx_host_swiglu_bf16(const uint16_t* g, const uint16_t* u, uint16_t* y, int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RLDX_AMD_H_ */

@@ -1,0 +1,185 @@
+"""CPU oracle: a restatement of RLDX-1's eager PyTorch formulas for the hot path.
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, by __graft_entry__.smoke() as the
+checker, and by bench.py's cpu_baseline leg as the timed CPU path.  No product
+code imports it; the HIP kernels never route through it.
+
+Every function follows the cited reference source line by line in its
+arithmetic (same ops, same dtypes, same rounding points), written out here in
+plain torch so it runs on the CPU without the reference package, diffusers or
+transformers.  How each function is pinned independently of itself
+(closed forms, invariants, fp64 brute force, exhaustive bf16 sweeps) is listed
+in tests/test_oracle.py.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+
+# ---------------------------------------------------------------------------
+# Qwen3-VL text attention pieces
+# ---------------------------------------------------------------------------
+def qwen_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """Qwen3VLTextRMSNorm.forward — modeling_qwen3_vl.py:366-371."""
+    input_dtype = x.dtype
+    h = x.to(torch.float32)
+    variance = h.pow(2).mean(-1, keepdim=True)
+    h = h * torch.rsqrt(variance + eps)
+    return w * h.to(input_dtype)
+
+
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    """modeling_qwen3_vl.py:118-122."""
+    x1 = x[..., : x.shape[-1] // 2]
+    x2 = x[..., x.shape[-1] // 2:]
+    return torch.cat((-x2, x1), dim=-1)
+
+
+def apply_rotary_pos_emb(q, k, cos, sin, unsqueeze_dim: int = 1):
+    """modeling_qwen3_vl.py:377-401."""
+    cos = cos.unsqueeze(unsqueeze_dim)
+    sin = sin.unsqueeze(unsqueeze_dim)
+    q_embed = (q * cos) + (rotate_half(q) * sin)
+    k_embed = (k * cos) + (rotate_half(k) * sin)
+    return q_embed, k_embed
+
+
+def qk_rmsnorm_rope_half(q, k, q_w, k_w, cos, sin, eps: float = 1e-6):
+    """q_norm/k_norm then RoPE on [B, S, H, D] tensors, cos/sin [S, D] or [B, S, D]
+    (Qwen3VLTextAttention.forward, modeling_qwen3_vl.py:449-456, with the head
+    axis kept at position 2: unsqueeze_dim=2)."""
+    if cos.dim() == 2:
+        cos, sin = cos.unsqueeze(0), sin.unsqueeze(0)
+    return apply_rotary_pos_emb(qwen_rmsnorm(q, q_w, eps), qwen_rmsnorm(k, k_w, eps), cos, sin, unsqueeze_dim=2)
+
+
+def repeat_kv(x: torch.Tensor, n_rep: int) -> torch.Tensor:
+    """modeling_qwen3_vl.py:139-150 ([B, Hkv, S, D] -> [B, Hkv*n_rep, S, D])."""
+    b, h, s, d = x.shape
+    if n_rep == 1:
+        return x
+    return x[:, :, None].expand(b, h, n_rep, s, d).reshape(b, h * n_rep, s, d)
+
+
+def llm_fused_attention(qkv, q_norm_w, k_norm_w, cos, sin, num_heads, num_kv_heads, head_dim, eps=1e-6):
+    """Eager equivalent of rldx_backbone::fused_attention: packed (M, QKV_DIM)
+    bf16 -> (M, Hq*D).  q/k norm + rotate-half RoPE (modeling_qwen3_vl.py:449-456),
+    causal SDPA with repeated KV (:139-176; flash/sdpa path is_causal)."""
+    M = qkv.shape[0]
+    Hq, Hkv, D = num_heads, num_kv_heads, head_dim
+    q = qkv[:, : Hq * D].reshape(1, M, Hq, D)
+    k = qkv[:, Hq * D:(Hq + Hkv) * D].reshape(1, M, Hkv, D)
+    v = qkv[:, (Hq + Hkv) * D:].reshape(1, M, Hkv, D)
+    q, k = qk_rmsnorm_rope_half(q, k, q_norm_w, k_norm_w, cos, sin, eps)
+    q, k, v = (t.transpose(1, 2) for t in (q, k, v))
+    o = sdpa(q, repeat_kv(k, Hq // Hkv), repeat_kv(v, Hq // Hkv), causal=True)
+    return o.transpose(1, 2).reshape(M, Hq * D)
+
+
+# ---------------------------------------------------------------------------
+# MSAT pieces
+# ---------------------------------------------------------------------------
+def msat_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """RMSNorm.forward — rldx/model/modules/norms.py:18-22 (one rounding)."""
+    input_dtype = x.dtype
+    x_float = x.float()
+    x_normed = x_float * torch.rsqrt(x_float.pow(2).mean(-1, keepdim=True) + eps)
+    return (w * x_normed).to(input_dtype)
+
+
+def apply_rotary_emb(xq: torch.Tensor, xk: torch.Tensor, freqs_cis: torch.Tensor):
+    """Interleaved complex RoPE — rldx/model/modules/action_model/ops.py:48-67.
+    xq, xk [B, H, N, D]; freqs_cis complex64 [B, N, D/2]."""
+    xq_ = torch.view_as_complex(xq.float().reshape(*xq.shape[:-1], -1, 2))
+    xk_ = torch.view_as_complex(xk.float().reshape(*xk.shape[:-1], -1, 2))
+    fc = freqs_cis.unsqueeze(1)
+    xq_out = torch.view_as_real(xq_ * fc).flatten(3)
+    xk_out = torch.view_as_real(xk_ * fc).flatten(3)
+    return xq_out.type_as(xq), xk_out.type_as(xk)
+
+
+def split_heads(x: torch.Tensor, num_heads: int) -> torch.Tensor:
+    """ops.py:167-171."""
+    B, N, D = x.shape
+    return x.view(B, N, num_heads, D // num_heads).permute(0, 2, 1, 3).contiguous()
+
+
+def merge_heads(x: torch.Tensor) -> torch.Tensor:
+    """ops.py:174-177."""
+    B, H, N, Dh = x.shape
+    return x.permute(0, 2, 1, 3).contiguous().view(B, N, H * Dh)
+
+
+def msat_qkv_norm_rope(streams, num_heads: int, head_dim: int, eps: float = 1e-6):
+    """Per-stream QK RMSNorm then joint interleaved RoPE, eager order of
+    ExpandedDoubleStreamBlock.forward (blocks.py:804-833): split heads, norm each
+    stream, concat [s0 | s1 | s2], apply_rotary_emb with a per-row table (rows
+    without a table get the identity rotation, i.e. position 0).
+
+    streams: list of (qkv [n, >=3*inner] bf16, q_w, k_w, cos or None, sin or None).
+    Returns q, k, v (H, M, D) bf16."""
+    inner = num_heads * head_dim
+    qs, ks, vs, pes = [], [], [], []
+    for qkv, q_w, k_w, cos, sin in streams:
+        n = qkv.shape[0]
+        x = qkv[:, : 3 * inner].unsqueeze(0)
+        q, k, v = (split_heads(t, num_heads) for t in x.chunk(3, dim=-1))
+        B, H, _, Dh = q.shape
+        q = msat_rmsnorm(q.reshape(B * H, n, Dh), q_w, eps).reshape(B, H, n, Dh)
+        k = msat_rmsnorm(k.reshape(B * H, n, Dh), k_w, eps).reshape(B, H, n, Dh)
+        qs.append(q), ks.append(k), vs.append(v)
+        if cos is None:
+            pes.append(torch.polar(torch.ones(n, head_dim // 2), torch.zeros(n, head_dim // 2)))
+        else:
+            pes.append(torch.complex(cos.float(), sin.float()))
+    q = torch.cat(qs, dim=2)
+    k = torch.cat(ks, dim=2)
+    v = torch.cat(vs, dim=2)
+    pe = torch.cat(pes, dim=0).unsqueeze(0)
+    q, k = apply_rotary_emb(q, k, pe)
+    return q[0], k[0], v[0]
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU
+# ---------------------------------------------------------------------------
+def swiglu(x: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """SwiGLUFFN activation — ops.py:157-161 (`x12.chunk(2, -1)`, `F.silu(x1) * x2`).
+    With bias: the bias-added w12 output, rounded like an eager bf16 add."""
+    if bias is not None:
+        x = x + bias
+    x1, x2 = x.chunk(2, dim=-1)
+    return F.silu(x1) * x2
+
+
+# ---------------------------------------------------------------------------
+# Attention
+# ---------------------------------------------------------------------------
+def sdpa(q, k, v, key_bias: Optional[torch.Tensor] = None, causal: bool = False, scale: Optional[float] = None):
+    """F.scaled_dot_product_attention as called on the path (blocks.py:577-579, :866).
+
+    key_bias: [B, Sk] additive mask in the eager dtype convention: cast to
+    q.dtype and broadcast as [B, 1, 1, Sk] (blocks.py:843-864)."""
+    mask = None
+    if key_bias is not None:
+        kb = key_bias if key_bias.dim() == 2 else key_bias.unsqueeze(0)
+        mask = kb[:, None, None, :].to(q.dtype)
+    return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=causal, scale=scale)
+
+
+def mask_to_bias(kv_mask: torch.Tensor) -> torch.Tensor:
+    """1 visible / 0 masked -> 0 / -inf (blocks.py:843-864)."""
+    return torch.where(kv_mask == 0, torch.tensor(float("-inf")), torch.tensor(0.0)).float()
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm without affine (pre-norm of the MSAT blocks)
+# ---------------------------------------------------------------------------
+def layer_norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """nn.LayerNorm(dim, elementwise_affine=False, eps) — norms.py:35-36."""
+    return F.layer_norm(x, (x.shape[-1],), eps=eps)

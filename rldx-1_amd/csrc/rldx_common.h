@@ -1,0 +1,89 @@
+// Shared device/host helpers for the rldx_amd HIP kernels (gfx950 / CDNA4).
+//
+// Everything here is written for one target: AMD CDNA4, wave64.  The numeric
+// helpers are __host__ __device__ so that the very same IEEE operation
+// sequence can be executed on the CPU (exhaustive self-checks) and on the GPU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define RLDX_HD __host__ __device__ __forceinline__
+
+namespace rldx {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// bf16 <-> fp32 (bit-level, round-to-nearest-even, NaN quieted).  PyTorch's
+// c10::BFloat16 conversion uses the same rule, so rounding here is identical to
+// what eager bf16 tensors do after every op.
+// ---------------------------------------------------------------------------
+RLDX_HD float bf16_bits_to_f32(uint16_t b) {
+  uint32_t u = static_cast<uint32_t>(b) << 16;
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+
+RLDX_HD uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+RLDX_HD float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+// ---------------------------------------------------------------------------
+// exp(a) with |error| < 1 ulp on the range where silu needs it.
+//
+// Cody-Waite reduction a = n*ln2 + r (|r| <= ~0.347), degree-7 Taylor
+// polynomial evaluated by Horner with explicit fmaf, exact scaling by 2^n via
+// ldexpf.  Truncation error r^8/8! < 5.3e-9 relative; the final fma rounds
+// once, so the total stays below one ulp.  All steps are explicit IEEE
+// operations (no contraction is left to the compiler), so host and device
+// produce identical bits.
+// ---------------------------------------------------------------------------
+RLDX_HD float exp_f32_1ulp(float a) {
+#pragma clang fp contract(off)
+  if (a > 88.72283935546875f) return __builtin_inff();
+  if (a < -104.0f) return 0.0f;
+  const float kLog2e = 1.44269502162933349609375f;
+  const float kLn2Hi = 0.693145751953125f;           // 0x3f317200: 12 significant bits
+  const float kLn2Lo = 1.428606765330187045e-06f;    // ln2 - kLn2Hi
+  float n = __builtin_rintf(a * kLog2e);
+  float r = __builtin_fmaf(-n, kLn2Hi, a);
+  r = __builtin_fmaf(-n, kLn2Lo, r);
+  float p = 1.98412698412698412526e-4f;              // 1/5040
+  p = __builtin_fmaf(p, r, 1.38888888888888894189e-3f);  // 1/720
+  p = __builtin_fmaf(p, r, 8.33333333333333321769e-3f);  // 1/120
+  p = __builtin_fmaf(p, r, 4.16666666666666643537e-2f);  // 1/24
+  p = __builtin_fmaf(p, r, 1.66666666666666657415e-1f);  // 1/6
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  return __builtin_ldexpf(p, static_cast<int>(n));
+}
+
+// silu(x) = x / (1 + exp(-x)) in fp32, the formula PyTorch's silu kernel uses
+// for reduced-precision inputs (opmath float).  IEEE division (HIP's default
+// correctly-rounded fp32 divide).
+RLDX_HD float silu_f32(float x) {
+#pragma clang fp contract(off)
+  float e = exp_f32_1ulp(-x);
+  float d = 1.0f + e;
+  return x / d;
+}
+
+// Eager bf16 SwiGLU element: y = bf16( bf16(silu(g)) * u ), two roundings,
+// exactly as `F.silu(x1) * x2` on bf16 tensors.  The product of two bf16
+// values is exact in fp32, so the only rounding-sensitive step is silu.
+RLDX_HD uint16_t swiglu_bf16_bits(uint16_t g, uint16_t u) {
+#pragma clang fp contract(off)
+  float s = round_bf16(silu_f32(bf16_bits_to_f32(g)));
+  return f32_to_bf16_bits(s * bf16_bits_to_f32(u));
+}
+
+}  // namespace rldx

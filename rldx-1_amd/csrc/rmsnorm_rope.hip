@@ -1,0 +1,371 @@
+// Fused per-head RMSNorm + rotary embedding for gfx950.
+//
+// Two conventions live on the RLDX-1 inference path and both are here:
+//
+//  * rotate-half (Qwen3-VL text attention):
+//      y   = w * to_dtype(x * rsqrt(mean(x^2) + eps))
+//      out = y*cos + rotate_half(y)*sin,  rotate_half(y) = cat(-y[D/2:], y[:D/2])
+//    rldx/model/modules/backbone/modeling_qwen3_vl.py:118-122 (rotate_half),
+//    :356-371 (Qwen3VLTextRMSNorm), :377-401 (apply_rotary_pos_emb).
+//
+//  * interleaved (MSAT joint attention, Llama/complex style), per stream:
+//      y   = to_bf16( float(w) * (x * rsqrt(mean(x^2) + eps)) )    (one rounding)
+//      (y[2i] + i*y[2i+1]) * (cos_i + i*sin_i), fp32, rounded once to bf16
+//    rldx/model/modules/norms.py:18-22 (RMSNorm), action_model/ops.py:48-67
+//    (apply_rotary_emb); fused form of the per-stream QKV gather in
+//    rldx/inference/action_model/double_stream/engine/kernels/rmsnorm_rope_ds.py:11-231
+//    and rmsnorm_rope_ds_3way.py:22-386.
+//
+// Layout: one row (token, head) of D elements is owned by a group of
+// D*sizeof(T)/16 lanes, each holding 16 contiguous bytes (128-bit loads and
+// stores).  The sum of squares is reduced with xor-shuffles inside the group;
+// the rotate-half partner d +- D/2 lives in lane (i ^ group/2), one shuffle;
+// interleaved pairs (2i, 2i+1) are adjacent inside a lane, no shuffle at all.
+#include "rldx_amd.h"
+#include "rldx_common.h"
+
+namespace rldx {
+namespace {
+
+template <typename T>
+struct Vec16;
+template <>
+struct Vec16<float> {
+  static constexpr int N = 4;
+};
+template <>
+struct Vec16<uint16_t> {
+  static constexpr int N = 8;
+};
+
+template <typename T>
+__device__ __forceinline__ float load_elem(const T* p, int i);
+template <>
+__device__ __forceinline__ float load_elem<float>(const float* p, int i) { return p[i]; }
+template <>
+__device__ __forceinline__ float load_elem<uint16_t>(const uint16_t* p, int i) { return bf16_bits_to_f32(p[i]); }
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, kWave); }
+
+// ---------------------------------------------------------------------------
+// rotate-half (Qwen) variant
+// ---------------------------------------------------------------------------
+struct HalfArgs {
+  const void* q;
+  const void* k;
+  const void* q_w;
+  const void* k_w;
+  const void* cos;
+  const void* sin;
+  void* q_out;
+  void* k_out;
+  int64_t batch, seq, hq, hk;
+  int64_t q_sb, q_ss, q_sh;    // input strides (elements)
+  int64_t k_sb, k_ss, k_sh;
+  int64_t qo_sb, qo_ss, qo_sh; // output strides
+  int64_t ko_sb, ko_ss, ko_sh;
+  int64_t c_sb, c_ss;          // cos/sin strides ([B or 1, S, D])
+  float eps;
+  int64_t total_rows;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void rmsnorm_rope_half_kernel(HalfArgs a) {
+  constexpr int V = Vec16<T>::N;   // elements per lane
+  constexpr int LPR = D / V;       // lanes per row
+  static_assert(LPR >= 2 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "unsupported head_dim");
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int lane_in_row = static_cast<int>(tid % LPR);
+  const int64_t row = tid / LPR;
+  const bool valid = row < a.total_rows;
+  const int64_t r = valid ? row : 0;
+
+  const int64_t per_tok = a.hq + a.hk;
+  const int64_t tok = r / per_tok;
+  const int64_t hh = r - tok * per_tok;
+  const int64_t b = tok / a.seq;
+  const int64_t s = tok - b * a.seq;
+  const bool is_q = hh < a.hq;
+  const int64_t h = is_q ? hh : hh - a.hq;
+
+  const T* src = is_q ? static_cast<const T*>(a.q) + b * a.q_sb + s * a.q_ss + h * a.q_sh
+                      : static_cast<const T*>(a.k) + b * a.k_sb + s * a.k_ss + h * a.k_sh;
+  T* dst = is_q ? static_cast<T*>(a.q_out) + b * a.qo_sb + s * a.qo_ss + h * a.qo_sh
+                : static_cast<T*>(a.k_out) + b * a.ko_sb + s * a.ko_ss + h * a.ko_sh;
+  const T* w = static_cast<const T*>(is_q ? a.q_w : a.k_w);
+  const T* cs = static_cast<const T*>(a.cos) + b * a.c_sb + s * a.c_ss;
+  const T* sn = static_cast<const T*>(a.sin) + b * a.c_sb + s * a.c_ss;
+  const int d0 = lane_in_row * V;
+
+  float x[V];
+  {
+    uint4 raw = valid ? *reinterpret_cast<const uint4*>(src + d0) : make_uint4(0, 0, 0, 0);
+    const T* e = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+    for (int i = 0; i < V; ++i) x[i] = load_elem<T>(e, i);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) ss += x[i] * x[i];
+#pragma unroll
+  for (int m = LPR / 2; m >= 1; m >>= 1) ss += shfl_xor_f(ss, m);
+
+  float y[V];
+  {
+#pragma clang fp contract(off)
+    const float rinv = 1.0f / __builtin_sqrtf(ss * (1.0f / D) + a.eps);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      float xn = x[i] * rinv;
+      if constexpr (sizeof(T) == 2) {
+        // w * bf16(xn): bf16 x bf16 product, rounded to bf16.
+        y[i] = round_bf16(load_elem<T>(w, d0 + i) * round_bf16(xn));
+      } else {
+        y[i] = load_elem<T>(w, d0 + i) * xn;
+      }
+    }
+  }
+  // rotate_half partner: element d +- D/2 sits in lane (lane_in_row ^ LPR/2).
+  float part[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) part[i] = shfl_xor_f(y[i], LPR / 2);
+  const bool first_half = lane_in_row < LPR / 2;
+
+  uint4 outraw;
+  T* o = reinterpret_cast<T*>(&outraw);
+  {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float rot = first_half ? -part[i] : part[i];
+      const float c = load_elem<T>(cs, d0 + i);
+      const float sv = load_elem<T>(sn, d0 + i);
+      if constexpr (sizeof(T) == 2) {
+        const float t1 = round_bf16(y[i] * c);
+        const float t2 = round_bf16(rot * sv);
+        o[i] = f32_to_bf16_bits(t1 + t2);
+      } else {
+        const float t1 = y[i] * c;
+        const float t2 = rot * sv;
+        o[i] = t1 + t2;
+      }
+    }
+  }
+  if (valid) *reinterpret_cast<uint4*>(dst + d0) = outraw;
+}
+
+// ---------------------------------------------------------------------------
+// MSAT multi-stream interleaved variant
+// ---------------------------------------------------------------------------
+struct MsatStream {
+  const uint16_t* qkv;   // [n, >= 3*H*D] bf16 packed Q|K|V
+  int64_t ld;            // row stride (elements)
+  int64_t n;             // rows
+  int64_t m_begin;       // first row in the joint sequence
+  const uint16_t* q_w;   // [D] bf16
+  const uint16_t* k_w;   // [D] bf16
+  const float* cos;      // [n, D/2] fp32 or nullptr (no rotary on this stream)
+  const float* sin;
+  int64_t rope_ld;       // row stride of cos/sin (elements)
+};
+
+struct MsatArgs {
+  MsatStream s[3];
+  int num_streams;
+  int64_t heads;
+  int64_t m_total;
+  uint16_t* q_out;  // (H, M, D) with strides
+  uint16_t* k_out;
+  uint16_t* v_out;
+  int64_t o_sh, o_sm;  // output strides (head, row) in elements, shared by q/k/v
+  float eps;
+  int64_t total_items;  // 3 * H * M rows of D
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void msat_qkv_norm_rope_kernel(MsatArgs a) {
+  constexpr int V = 8;
+  constexpr int LPR = D / V;
+  static_assert(LPR >= 2 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "unsupported head_dim");
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int lane_in_row = static_cast<int>(tid % LPR);
+  const int64_t item = tid / LPR;
+  const bool valid = item < a.total_items;
+  const int64_t it = valid ? item : 0;
+  // item -> (which, m, h); h fastest so a wave walks consecutive heads of one token.
+  const int64_t per_kind = a.m_total * a.heads;
+  const int which = static_cast<int>(it / per_kind);  // 0=q 1=k 2=v
+  const int64_t rem = it - which * per_kind;
+  const int64_t m = rem / a.heads;
+  const int64_t h = rem - m * a.heads;
+  int si = 0;
+  if (a.num_streams > 1 && m >= a.s[1].m_begin) si = 1;
+  if (a.num_streams > 2 && m >= a.s[2].m_begin) si = 2;
+  const MsatStream& S = a.s[si];
+  const int64_t row = m - S.m_begin;
+  const int64_t inner = a.heads * D;
+  const int d0 = lane_in_row * V;
+  const uint16_t* src = S.qkv + row * S.ld + which * inner + h * D + d0;
+  uint16_t* dst = (which == 0 ? a.q_out : which == 1 ? a.k_out : a.v_out) + h * a.o_sh + m * a.o_sm + d0;
+
+  uint4 raw = valid ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
+  if (which == 2) {  // V passthrough (uniform per row group, but shuffles below need all lanes)
+    if (valid) *reinterpret_cast<uint4*>(dst) = raw;
+  }
+  const uint16_t* e = reinterpret_cast<const uint16_t*>(&raw);
+  float x[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) x[i] = bf16_bits_to_f32(e[i]);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) ss += x[i] * x[i];
+#pragma unroll
+  for (int mm = LPR / 2; mm >= 1; mm >>= 1) ss += shfl_xor_f(ss, mm);
+  if (which == 2 || !valid) return;
+
+  const uint16_t* w = which == 0 ? S.q_w : S.k_w;
+  float y[V];
+  {
+#pragma clang fp contract(off)
+    const float rinv = 1.0f / __builtin_sqrtf(ss * (1.0f / D) + a.eps);
+#pragma unroll
+    for (int i = 0; i < V; ++i) y[i] = round_bf16(bf16_bits_to_f32(w[d0 + i]) * (x[i] * rinv));
+  }
+  uint4 outraw;
+  uint16_t* o = reinterpret_cast<uint16_t*>(&outraw);
+  if (S.cos != nullptr) {
+#pragma clang fp contract(off)
+    const float* cp = S.cos + row * S.rope_ld + d0 / 2;
+    const float* sp = S.sin + row * S.rope_ld + d0 / 2;
+#pragma unroll
+    for (int p = 0; p < V / 2; ++p) {
+      const float c = cp[p], s = sp[p];
+      const float re = y[2 * p], im = y[2 * p + 1];
+      const float ore = re * c - im * s;
+      const float oim = re * s + im * c;
+      o[2 * p] = f32_to_bf16_bits(ore);
+      o[2 * p + 1] = f32_to_bf16_bits(oim);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i) o[i] = f32_to_bf16_bits(y[i]);
+  }
+  *reinterpret_cast<uint4*>(dst) = outraw;
+}
+
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <typename T>
+hipError_t launch_half(const HalfArgs& a, int64_t head_dim, hipStream_t stream) {
+  constexpr int V = Vec16<T>::N;
+  const int64_t threads = a.total_rows * (head_dim / V);
+  const int grid = static_cast<int>((threads + 255) / 256);
+  if (grid == 0) return hipSuccess;
+  if (head_dim == 64)
+    hipLaunchKernelGGL((rmsnorm_rope_half_kernel<T, 64>), dim3(grid), dim3(256), 0, stream, a);
+  else if (head_dim == 128)
+    hipLaunchKernelGGL((rmsnorm_rope_half_kernel<T, 128>), dim3(grid), dim3(256), 0, stream, a);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t half_entry(const void* q, const void* k, const void* q_w, const void* k_w, const void* cos,
+                      const void* sin, void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t hq,
+                      int64_t hk, int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
+                      const int64_t* qo_strides, const int64_t* ko_strides, const int64_t* cs_strides, float eps,
+                      hipStream_t stream) {
+  if (head_dim != 64 && head_dim != 128) return hipErrorInvalidValue;
+  if (batch < 0 || seq < 0 || hq < 0 || hk < 0) return hipErrorInvalidValue;
+  if (!q_strides || !k_strides || !qo_strides || !ko_strides || !cs_strides) return hipErrorInvalidValue;
+  if (batch == 0 || seq == 0 || hq + hk == 0) return hipSuccess;
+  if (!cos || !sin) return hipErrorInvalidValue;
+  if (hq > 0 && (!q || !q_w || !q_out)) return hipErrorInvalidValue;
+  if (hk > 0 && (!k || !k_w || !k_out)) return hipErrorInvalidValue;
+  const int V = Vec16<T>::N;
+  const void* ptrs[] = {q, k, q_out, k_out, cos, sin};
+  for (const void* p : ptrs)
+    if (p && !al16(p)) return hipErrorInvalidValue;
+  const int64_t* all[] = {q_strides, k_strides, qo_strides, ko_strides};
+  for (const int64_t* st : all)
+    for (int i = 0; i < 3; ++i)
+      if (st[i] % V != 0) return hipErrorInvalidValue;
+  if (cs_strides[0] % V != 0 || cs_strides[1] % V != 0) return hipErrorInvalidValue;
+  HalfArgs a{q, k, q_w, k_w, cos, sin, q_out, k_out, batch, seq, hq, hk,
+             q_strides[0], q_strides[1], q_strides[2], k_strides[0], k_strides[1], k_strides[2],
+             qo_strides[0], qo_strides[1], qo_strides[2], ko_strides[0], ko_strides[1], ko_strides[2],
+             cs_strides[0], cs_strides[1], eps, batch * seq * (hq + hk)};
+  return launch_half<T>(a, head_dim, stream);
+}
+
+}  // namespace
+}  // namespace rldx
+
+using namespace rldx;
+
+extern "C" hipError_t rldx_qk_rmsnorm_rope_half_f32(
+    const float* q, const float* k, const float* q_w, const float* k_w, const float* cos, const float* sin,
+    float* q_out, float* k_out, int64_t batch, int64_t seq, int64_t q_heads, int64_t k_heads, int64_t head_dim,
+    const int64_t* q_strides, const int64_t* k_strides, const int64_t* q_out_strides,
+    const int64_t* k_out_strides, const int64_t* cos_strides, float eps, hipStream_t stream) {
+  return half_entry<float>(q, k, q_w, k_w, cos, sin, q_out, k_out, batch, seq, q_heads, k_heads, head_dim,
+                           q_strides, k_strides, q_out_strides, k_out_strides, cos_strides, eps, stream);
+}
+
+extern "C" hipError_t rldx_qk_rmsnorm_rope_half_bf16(
+    const void* q, const void* k, const void* q_w, const void* k_w, const void* cos, const void* sin,
+    void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t q_heads, int64_t k_heads, int64_t head_dim,
+    const int64_t* q_strides, const int64_t* k_strides, const int64_t* q_out_strides,
+    const int64_t* k_out_strides, const int64_t* cos_strides, float eps, hipStream_t stream) {
+  return half_entry<uint16_t>(q, k, q_w, k_w, cos, sin, q_out, k_out, batch, seq, q_heads, k_heads, head_dim,
+                              q_strides, k_strides, q_out_strides, k_out_strides, cos_strides, eps, stream);
+}
+
+extern "C" hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* streams, int32_t num_streams,
+                                                   int64_t heads, int64_t head_dim, void* q_out, void* k_out,
+                                                   void* v_out, int64_t out_head_stride, int64_t out_row_stride,
+                                                   float eps, hipStream_t stream) {
+  if (streams == nullptr || num_streams < 1 || num_streams > 3) return hipErrorInvalidValue;
+  if (head_dim != 64 && head_dim != 128) return hipErrorInvalidValue;
+  if (heads <= 0 || !q_out || !k_out || !v_out) return hipErrorInvalidValue;
+  if (!al16(q_out) || !al16(k_out) || !al16(v_out) || out_head_stride % 8 || out_row_stride % 8)
+    return hipErrorInvalidValue;
+  MsatArgs a{};
+  int64_t m = 0;
+  int k = 0;
+  for (int i = 0; i < num_streams; ++i) {
+    const rldx_msat_stream_t& s = streams[i];
+    if (s.rows < 0) return hipErrorInvalidValue;
+    if (s.rows == 0) continue;
+    if (!s.qkv || !s.q_norm_w || !s.k_norm_w || !al16(s.qkv)) return hipErrorInvalidValue;
+    if (s.qkv_row_stride < 3 * heads * head_dim || s.qkv_row_stride % 8) return hipErrorInvalidValue;
+    if ((s.rope_cos == nullptr) != (s.rope_sin == nullptr)) return hipErrorInvalidValue;
+    if (s.rope_cos && (!al16(s.rope_cos) || !al16(s.rope_sin) || s.rope_row_stride < head_dim / 2 ||
+                       s.rope_row_stride % 4))
+      return hipErrorInvalidValue;
+    a.s[k] = MsatStream{static_cast<const uint16_t*>(s.qkv), s.qkv_row_stride, s.rows, m,
+                        static_cast<const uint16_t*>(s.q_norm_w), static_cast<const uint16_t*>(s.k_norm_w),
+                        s.rope_cos, s.rope_sin, s.rope_row_stride};
+    m += s.rows;
+    ++k;
+  }
+  if (k == 0) return hipSuccess;
+  a.num_streams = k;
+  a.heads = heads;
+  a.m_total = m;
+  a.q_out = static_cast<uint16_t*>(q_out);
+  a.k_out = static_cast<uint16_t*>(k_out);
+  a.v_out = static_cast<uint16_t*>(v_out);
+  a.o_sh = out_head_stride;
+  a.o_sm = out_row_stride;
+  a.eps = eps;
+  a.total_items = 3 * heads * m;
+  const int64_t threads = a.total_items * (head_dim / 8);
+  const int grid = static_cast<int>((threads + 255) / 256);
+  if (head_dim == 64)
+    hipLaunchKernelGGL(msat_qkv_norm_rope_kernel<64>, dim3(grid), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL(msat_qkv_norm_rope_kernel<128>, dim3(grid), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}

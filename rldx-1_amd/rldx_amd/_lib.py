@@ -1,0 +1,107 @@
+"""ctypes binding of librldx_amd.so, the gfx950 C-ABI library (include/rldx_amd.h).
+
+The library is the only compute path: if it is missing or fails to load,
+every operator raises.  There is no CPU or PyTorch fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "librldx_amd.so"
+
+c_i64 = ctypes.c_int64
+c_i32 = ctypes.c_int32
+c_f32 = ctypes.c_float
+c_vp = ctypes.c_void_p
+c_i64p = ctypes.POINTER(ctypes.c_int64)
+
+
+class MsatStream(ctypes.Structure):
+    """Mirror of `rldx_msat_stream_t`."""
+
+    _fields_ = [
+        ("qkv", c_vp),
+        ("qkv_row_stride", c_i64),
+        ("rows", c_i64),
+        ("q_norm_w", c_vp),
+        ("k_norm_w", c_vp),
+        ("rope_cos", c_vp),
+        ("rope_sin", c_vp),
+        ("rope_row_stride", c_i64),
+    ]
+
+
+# name -> (restype, argtypes); must stay in sync with include/rldx_amd.h
+SIGNATURES = {
+    "rldx_swiglu_bf16": (c_i32, [c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp]),
+    "rldx_grouped_swiglu_bf16": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp]),
+    "rldx_qk_rmsnorm_rope_half_f32": (
+        c_i32,
+        [c_vp] * 8 + [c_i64] * 5 + [c_i64p] * 5 + [c_f32, c_vp],
+    ),
+    "rldx_qk_rmsnorm_rope_half_bf16": (
+        c_i32,
+        [c_vp] * 8 + [c_i64] * 5 + [c_i64p] * 5 + [c_f32, c_vp],
+    ),
+    "rldx_msat_qkv_norm_rope_bf16": (
+        c_i32,
+        [ctypes.POINTER(MsatStream), c_i32, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, c_f32, c_vp],
+    ),
+    "rldx_attention_fwd_bf16": (
+        c_i32,
+        [c_vp] * 4 + [c_i64] * 6 + [c_i64p] * 4 + [c_vp, c_i64, c_f32, c_i32, c_vp],
+    ),
+    "rldx_host_swiglu_bf16": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64]),
+}
+
+_lib = None
+_hip = None
+
+
+def lib_path() -> Path:
+    return LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Load librldx_amd.so once; raise a clear error if it was never built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"rldx_amd: {LIB_PATH} not found. Build it with `make -C rldx-1_amd` "
+            "(or __graft_entry__.build()); there is no fallback path."
+        )
+    lib = ctypes.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | os.RTLD_GLOBAL)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _hip_runtime() -> ctypes.CDLL:
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so", mode=os.RTLD_NOW | os.RTLD_GLOBAL)
+        _hip.hipGetErrorString.restype = ctypes.c_char_p
+        _hip.hipGetErrorString.argtypes = [ctypes.c_int]
+    return _hip
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        try:
+            msg = _hip_runtime().hipGetErrorString(status).decode()
+        except OSError:
+            msg = "unknown"
+        raise RuntimeError(f"rldx_amd: {what} failed with hipError {status} ({msg})")
+
+
+def i64_array(values) -> ctypes.Array:
+    arr = (ctypes.c_int64 * len(values))(*[int(v) for v in values])
+    return arr

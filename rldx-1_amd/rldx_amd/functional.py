@@ -1,0 +1,348 @@
+"""Tensor-level launchers for the gfx950 kernels.
+
+Each function validates its tensors on the host (dtype, device, shapes,
+strides), then calls the C ABI of librldx_amd.so on the current HIP stream.
+PyTorch only provides device memory and the stream.  Outputs are allocated
+with `torch.empty` (caching allocator, hipGraph-safe) unless `out=` is given.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+
+BF16 = torch.bfloat16
+F32 = torch.float32
+
+
+def _stream_ptr(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(f"rldx_amd: {msg}")
+
+
+def _on_gpu(*ts: Optional[torch.Tensor]) -> None:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        _require(t.is_cuda, "tensors must live on a ROCm device (the HIP kernels are the only path)")
+        if dev is None:
+            dev = t.device
+        _require(t.device == dev, "all tensors must be on the same device")
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _rows_view(x: torch.Tensor, what: str):
+    """Describe x[..., C] as (rows, row_stride) without copying."""
+    _require(x.dim() >= 1 and x.stride(-1) == 1, f"{what}: last dimension must be contiguous")
+    if x.dim() == 1:
+        return 1, x.shape[-1]
+    lead = x.shape[:-1]
+    rows = int(math.prod(lead))
+    ld = x.stride(-2)
+    # leading dims must collapse into one strided dimension
+    expect = ld
+    for size, stride in zip(reversed(lead), reversed(x.stride()[:-1])):
+        if size != 1:
+            _require(stride == expect, f"{what}: leading dimensions must collapse to one row stride")
+        expect = stride * size
+    return rows, ld
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU
+# ---------------------------------------------------------------------------
+def swiglu(x: torch.Tensor, bias: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """`F.silu(x1) * x2` with `x1, x2 = x.chunk(2, -1)`, bf16, eager rounding.
+
+    rldx/model/modules/action_model/ops.py:157-161.  With `bias` ([2*N] bf16)
+    each half is first rounded as bf16(x + b)."""
+    _on_gpu(x, bias, out)
+    _require(x.dtype == BF16, "swiglu expects bfloat16 input")
+    _require(x.shape[-1] % 2 == 0, "swiglu: last dimension must be even")
+    n_half = x.shape[-1] // 2
+    rows, ldx = _rows_view(x, "swiglu input")
+    if bias is not None:
+        _require(bias.dtype == BF16 and bias.dim() == 1 and bias.shape[0] == 2 * n_half and bias.is_contiguous(),
+                 "swiglu bias must be contiguous bf16 [2*N]")
+    if out is None:
+        out = torch.empty((*x.shape[:-1], n_half), dtype=BF16, device=x.device)
+    _require(out.shape == (*x.shape[:-1], n_half) and out.dtype == BF16, "swiglu out has the wrong shape/dtype")
+    _, ldy = _rows_view(out, "swiglu out")
+    if rows == 0 or n_half == 0:
+        return out
+    lib = _lib.load()
+    _lib.check(lib.rldx_swiglu_bf16(x.data_ptr(), ldx, _ptr(bias), out.data_ptr(), ldy, rows, n_half,
+                                    _stream_ptr(x)), "rldx_swiglu_bf16")
+    return out
+
+
+def grouped_swiglu(sa_w12: torch.Tensor, sa_bias: Optional[torch.Tensor], vl_w12: torch.Tensor,
+                   vl_bias: Optional[torch.Tensor], m_sa: int, m_vl: int, n_half_sa: int, n_half_vl: int):
+    """Two-group SwiGLU in one launch (ds::grouped_swiglu semantics, eager rounding)."""
+    _on_gpu(sa_w12, sa_bias, vl_w12, vl_bias)
+    for t, m, nh, name in ((sa_w12, m_sa, n_half_sa, "sa_w12"), (vl_w12, m_vl, n_half_vl, "vl_w12")):
+        _require(t.dtype == BF16 and t.is_contiguous(), f"{name} must be contiguous bf16")
+        _require(t.numel() == m * 2 * nh, f"{name} must hold ({m}, {2 * nh}) elements")
+    for b, nh, name in ((sa_bias, n_half_sa, "sa_bias"), (vl_bias, n_half_vl, "vl_bias")):
+        if b is not None:
+            _require(b.dtype == BF16 and b.is_contiguous() and b.numel() == 2 * nh, f"{name} must be bf16 [{2 * nh}]")
+    _require((sa_bias is None) == (vl_bias is None), "biases must be both given or both None")
+    sa_out = torch.empty((m_sa, n_half_sa), dtype=BF16, device=sa_w12.device)
+    vl_out = torch.empty((m_vl, n_half_vl), dtype=BF16, device=sa_w12.device)
+    lib = _lib.load()
+    _lib.check(lib.rldx_grouped_swiglu_bf16(sa_w12.data_ptr(), _ptr(sa_bias), vl_w12.data_ptr(), _ptr(vl_bias),
+                                            sa_out.data_ptr(), vl_out.data_ptr(), m_sa, m_vl, n_half_sa, n_half_vl,
+                                            _stream_ptr(sa_w12)), "rldx_grouped_swiglu_bf16")
+    return sa_out, vl_out
+
+
+# ---------------------------------------------------------------------------
+# rotate-half QK-RMSNorm + RoPE
+# ---------------------------------------------------------------------------
+def qk_rmsnorm_rope_half(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
+                         cos: torch.Tensor, sin: torch.Tensor, eps: float = 1e-6, *, sin_is_signed: bool = False,
+                         q_out: Optional[torch.Tensor] = None, k_out: Optional[torch.Tensor] = None):
+    """Qwen3-VL q_norm/k_norm followed by rotate-half RoPE, fused.
+
+    q: [B, S, Hq, D], k: [B, S, Hk, D] (any strides with D contiguous);
+    cos/sin: [S, D] or [B, S, D].  fp32 or bf16 (all tensors one dtype).
+    `sin_is_signed`: `sin` is the pre-signed table of
+    fused_llm_attention.prepare_signed_sin (first half negated).
+    rldx/model/modules/backbone/modeling_qwen3_vl.py:356-401."""
+    _on_gpu(q, k, q_weight, k_weight, cos, sin, q_out, k_out)
+    dt = q.dtype
+    _require(dt in (F32, BF16), "qk_rmsnorm_rope_half supports float32 and bfloat16")
+    for t in (k, q_weight, k_weight, cos, sin):
+        _require(t.dtype == dt, "all inputs must share one dtype")
+    _require(q.dim() == 4 and k.dim() == 4, "q and k must be [B, S, H, D]")
+    B, S, Hq, D = q.shape
+    _require(k.shape[0] == B and k.shape[1] == S and k.shape[3] == D, "k must be [B, S, Hk, D] matching q")
+    Hk = k.shape[2]
+    _require(D in (64, 128), "head_dim must be 64 or 128")
+    _require(q_weight.shape == (D,) and k_weight.shape == (D,), "norm weights must be [D]")
+    _require(q_weight.is_contiguous() and k_weight.is_contiguous(), "norm weights must be contiguous")
+    if cos.dim() == 2:
+        cos = cos.unsqueeze(0)
+        sin = sin.unsqueeze(0)
+    _require(cos.dim() == 3 and cos.shape[1:] == (S, D) and cos.shape[0] in (1, B), "cos must be [S, D] or [B, S, D]")
+    _require(sin.shape == cos.shape and sin.stride() == cos.stride(), "sin must match cos in shape and strides")
+    _require(q.stride(-1) == 1 and k.stride(-1) == 1 and cos.stride(-1) == 1, "last dims must be contiguous")
+    if q_out is None:
+        q_out = torch.empty((B, S, Hq, D), dtype=dt, device=q.device)
+    if k_out is None:
+        k_out = torch.empty((B, S, Hk, D), dtype=dt, device=q.device)
+    _require(q_out.shape == q.shape and k_out.shape == k.shape, "output shapes must match inputs")
+    cb = cos.stride(0) if cos.shape[0] == B and B > 1 else 0
+    qs = _lib.i64_array([q.stride(0), q.stride(1), q.stride(2)])
+    ks = _lib.i64_array([k.stride(0), k.stride(1), k.stride(2)])
+    qos = _lib.i64_array([q_out.stride(0), q_out.stride(1), q_out.stride(2)])
+    kos = _lib.i64_array([k_out.stride(0), k_out.stride(1), k_out.stride(2)])
+    css = _lib.i64_array([cb, cos.stride(1)])
+    if B * S == 0:
+        return q_out, k_out
+    lib = _lib.load()
+    fn = lib.rldx_qk_rmsnorm_rope_half_f32 if dt == F32 else lib.rldx_qk_rmsnorm_rope_half_bf16
+    sin_arg = sin
+    if sin_is_signed:
+        # Undo the pre-applied rotate_half sign (negation is exact in any float format).
+        half = D // 2
+        sign = torch.ones(D, dtype=dt, device=sin.device)
+        sign[:half] = -1
+        sin_arg = (sin * sign).contiguous()
+        css = _lib.i64_array([cb if sin_arg.shape[0] == B and B > 1 else 0, sin_arg.stride(1)])
+        _require(sin_arg.stride() == cos.stride(), "cos must be contiguous when sin_is_signed")
+    _lib.check(fn(q.data_ptr(), k.data_ptr(), q_weight.data_ptr(), k_weight.data_ptr(), cos.data_ptr(),
+                  sin_arg.data_ptr(), q_out.data_ptr(), k_out.data_ptr(), B, S, Hq, Hk, D, qs, ks, qos, kos, css,
+                  float(eps), _stream_ptr(q)), "rldx_qk_rmsnorm_rope_half")
+    return q_out, k_out
+
+
+# ---------------------------------------------------------------------------
+# MSAT multi-stream QKV gather + QK-RMSNorm + interleaved RoPE
+# ---------------------------------------------------------------------------
+class StreamSpec:
+    """One stream of the MSAT joint sequence: packed QKV rows + norm weights + optional tables."""
+
+    __slots__ = ("qkv", "q_w", "k_w", "cos", "sin")
+
+    def __init__(self, qkv: torch.Tensor, q_w: torch.Tensor, k_w: torch.Tensor,
+                 cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None):
+        self.qkv, self.q_w, self.k_w, self.cos, self.sin = qkv, q_w, k_w, cos, sin
+
+
+def msat_qkv_norm_rope(streams: Sequence[StreamSpec], num_heads: int, head_dim: int, eps: float = 1e-6,
+                       out: Optional[tuple] = None):
+    """Gather Q/K/V of 1-3 streams into (H, M, D) bf16 with per-stream QK RMSNorm
+    (one rounding) and interleaved RoPE on the streams that carry tables.
+
+    rmsnorm_rope_ds.py:11-231 / rmsnorm_rope_ds_3way.py:22-386 fused layout,
+    eager semantics of norms.py:18-22 and action_model/ops.py:48-67."""
+    _require(1 <= len(streams) <= 3, "between 1 and 3 streams")
+    inner = num_heads * head_dim
+    descs = (_lib.MsatStream * len(streams))()
+    M = 0
+    dev = streams[0].qkv.device
+    keep = []
+    for i, s in enumerate(streams):
+        _on_gpu(s.qkv, s.q_w, s.k_w, s.cos, s.sin)
+        _require(s.qkv.device == dev, "all streams on one device")
+        _require(s.qkv.dtype == BF16 and s.qkv.dim() == 2 and s.qkv.stride(1) == 1, "qkv must be 2-D bf16 rows")
+        _require(s.qkv.shape[1] >= 3 * inner, "qkv rows must hold Q|K|V of num_heads*head_dim each")
+        _require(s.q_w.dtype == BF16 and s.k_w.dtype == BF16 and s.q_w.numel() == head_dim and
+                 s.k_w.numel() == head_dim and s.q_w.is_contiguous() and s.k_w.is_contiguous(),
+                 "norm weights must be contiguous bf16 [head_dim]")
+        n = s.qkv.shape[0]
+        cos_p = sin_p = None
+        rope_ld = 0
+        if s.cos is not None:
+            _require(s.sin is not None, "cos and sin go together")
+            c = s.cos.to(F32).contiguous() if s.cos.dtype != F32 or not s.cos.is_contiguous() else s.cos
+            sn = s.sin.to(F32).contiguous() if s.sin.dtype != F32 or not s.sin.is_contiguous() else s.sin
+            _require(c.shape == (n, head_dim // 2) and sn.shape == (n, head_dim // 2),
+                     "rope tables must be [rows, head_dim/2]")
+            keep += [c, sn]
+            cos_p, sin_p, rope_ld = c.data_ptr(), sn.data_ptr(), c.stride(0)
+        descs[i] = _lib.MsatStream(s.qkv.data_ptr(), s.qkv.stride(0), n, s.q_w.data_ptr(), s.k_w.data_ptr(),
+                                   cos_p, sin_p, rope_ld)
+        M += n
+    if out is None:
+        q = torch.empty((num_heads, M, head_dim), dtype=BF16, device=dev)
+        k = torch.empty_like(q)
+        v = torch.empty_like(q)
+    else:
+        q, k, v = out
+        _require(all(t.shape == (num_heads, M, head_dim) and t.stride() == q.stride() for t in (q, k, v)),
+                 "out tensors must be (H, M, D) with equal strides")
+    if M == 0:
+        return q, k, v
+    lib = _lib.load()
+    _lib.check(lib.rldx_msat_qkv_norm_rope_bf16(descs, len(streams), num_heads, head_dim, q.data_ptr(), k.data_ptr(),
+                                                v.data_ptr(), q.stride(0), q.stride(1), float(eps),
+                                                _stream_ptr(q)), "rldx_msat_qkv_norm_rope_bf16")
+    return q, k, v
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+def _bhs_strides(t: torch.Tensor, layout: str):
+    if layout == "bhsd":
+        return [t.stride(0), t.stride(1), t.stride(2)]
+    if layout == "bshd":
+        return [t.stride(0), t.stride(2), t.stride(1)]
+    raise ValueError(f"unknown layout {layout}")
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, key_bias: Optional[torch.Tensor] = None,
+              causal: bool = False, scale: Optional[float] = None, layout: str = "bhsd",
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """softmax(Q K^T * scale + key_bias (+ causal)) V with GQA, bf16.
+
+    layout "bhsd": tensors [B, H, S, D]; "bshd": [B, S, H, D].  key_bias: fp32
+    [B, Sk] or [Sk] additive (0 / -inf).  scale defaults to 1/sqrt(D)."""
+    _on_gpu(q, k, v, key_bias, out)
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _require(t.dtype == BF16 and t.dim() == 4 and t.stride(-1) == 1, f"{n} must be 4-D bf16, last dim contiguous")
+    if layout == "bhsd":
+        B, Hq, Sq, D = q.shape
+        _, Hkv, Sk, _ = k.shape
+    else:
+        B, Sq, Hq, D = q.shape
+        _, Sk, Hkv, _ = k.shape
+    _require(D in (64, 128), "head_dim must be 64 or 128")
+    _require(k.shape == v.shape, "k and v must have the same shape")
+    _require(k.shape[0] == B and k.shape[3] == D, "k batch/head_dim must match q")
+    _require(Hkv > 0 and Hq % Hkv == 0, "q heads must be a multiple of kv heads")
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    _require(out.shape == q.shape and out.dtype == BF16 and out.stride(-1) == 1, "out must match q")
+    kb_ptr, kb_stride = None, 0
+    if key_bias is not None:
+        _require(key_bias.dtype == F32 and key_bias.stride(-1) == 1, "key_bias must be fp32 with contiguous keys")
+        if key_bias.dim() == 1:
+            _require(key_bias.shape[0] == Sk, "key_bias must have seq_k entries")
+            kb_stride = 0
+        else:
+            _require(key_bias.dim() == 2 and key_bias.shape[1] == Sk and key_bias.shape[0] in (1, B),
+                     "key_bias must be [B, Sk]")
+            kb_stride = key_bias.stride(0) if key_bias.shape[0] == B and B > 1 else 0
+        kb_ptr = key_bias.data_ptr()
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    qs = _lib.i64_array(_bhs_strides(q, layout))
+    ks = _lib.i64_array(_bhs_strides(k, layout))
+    vs = _lib.i64_array(_bhs_strides(v, layout))
+    os_ = _lib.i64_array(_bhs_strides(out, layout))
+    lib = _lib.load()
+    _lib.check(lib.rldx_attention_fwd_bf16(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, Hq, Hkv, Sq, Sk,
+                                           D, qs, ks, vs, os_, kb_ptr, kb_stride, float(scale), int(bool(causal)),
+                                           _stream_ptr(q)), "rldx_attention_fwd_bf16")
+    return out
+
+
+def attention_raw(q_ptr_tensor: torch.Tensor, k_base: torch.Tensor, v_base: torch.Tensor, o_base: torch.Tensor, *,
+                  batch: int, q_heads: int, kv_heads: int, seq_q: int, seq_k: int, head_dim: int,
+                  q_strides, k_strides, v_strides, o_strides, key_bias: Optional[torch.Tensor] = None,
+                  key_bias_batch_stride: int = 0, scale: Optional[float] = None, causal: bool = False,
+                  q_offset: int = 0, k_offset: int = 0, v_offset: int = 0, o_offset: int = 0) -> None:
+    """Strided attention over views into packed buffers (element offsets/strides).
+
+    Used by the packed-QKV operators, where Q, K and V are column slices of one
+    row-major buffer.  Bounds are checked against each base tensor's storage."""
+    _on_gpu(q_ptr_tensor, k_base, v_base, o_base, key_bias)
+    for t in (q_ptr_tensor, k_base, v_base, o_base):
+        _require(t.dtype == BF16, "attention_raw expects bf16 buffers")
+
+    def _extent(off, strides, nb, nh, ns):
+        return off + (nb - 1) * strides[0] + (nh - 1) * strides[1] + (ns - 1) * strides[2] + head_dim
+
+    _require(_extent(q_offset, q_strides, batch, q_heads, seq_q) <= q_ptr_tensor.numel(), "q view out of bounds")
+    _require(_extent(k_offset, k_strides, batch, kv_heads, seq_k) <= k_base.numel(), "k view out of bounds")
+    _require(_extent(v_offset, v_strides, batch, kv_heads, seq_k) <= v_base.numel(), "v view out of bounds")
+    _require(_extent(o_offset, o_strides, batch, q_heads, seq_q) <= o_base.numel(), "o view out of bounds")
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    esz = 2
+    lib = _lib.load()
+    _lib.check(lib.rldx_attention_fwd_bf16(q_ptr_tensor.data_ptr() + q_offset * esz, k_base.data_ptr() + k_offset * esz,
+                                           v_base.data_ptr() + v_offset * esz, o_base.data_ptr() + o_offset * esz,
+                                           batch, q_heads, kv_heads, seq_q, seq_k, head_dim,
+                                           _lib.i64_array(q_strides), _lib.i64_array(k_strides),
+                                           _lib.i64_array(v_strides), _lib.i64_array(o_strides),
+                                           _ptr(key_bias), key_bias_batch_stride, float(scale), int(bool(causal)),
+                                           _stream_ptr(o_base)), "rldx_attention_fwd_bf16")
+
+
+def mask_to_key_bias(kv_mask: torch.Tensor) -> torch.Tensor:
+    """1 = visible / 0 = masked (the eager encoder_attention_mask convention,
+    blocks.py:843-864) -> fp32 additive bias 0 / -inf."""
+    m = kv_mask if kv_mask.dim() == 2 else kv_mask.unsqueeze(0)
+    return torch.where(m == 0, torch.tensor(float("-inf"), device=m.device),
+                       torch.tensor(0.0, device=m.device)).to(F32).contiguous()
+
+
+def host_swiglu_bf16_bits(g_bits, u_bits):
+    """Run the device SwiGLU element function on the CPU (numpy uint16 arrays)."""
+    import numpy as np
+
+    g = np.ascontiguousarray(g_bits, dtype=np.uint16)
+    u = np.ascontiguousarray(u_bits, dtype=np.uint16)
+    y = np.empty_like(g)
+    lib = _lib.load()
+    rc = lib.rldx_host_swiglu_bf16(g.ctypes.data_as(ctypes.c_void_p), u.ctypes.data_as(ctypes.c_void_p),
+                                   y.ctypes.data_as(ctypes.c_void_p), g.size)
+    _require(rc == 0, "rldx_host_swiglu_bf16 failed")
+    return y

@@ -1,0 +1,303 @@
+"""`torch.library` operators under the reference's own qualified names.
+
+Importing this module registers, backed by the gfx950 kernels of librldx_amd.so:
+
+  ds::fused_attention_2way   ds::fused_attention_3way   ds::grouped_swiglu
+  ss::fused_attention_2way   ss::fused_attention_3way
+  rldx_backbone::fused_attention
+  rldx_amd::swiglu           (the eager `F.silu(x1) * x2` the chains inline)
+
+Argument order and defaults follow the reference registrations
+(rldx/inference/action_model/{double,single}_stream/engine/ops/*.py,
+rldx/inference/backbone/llm/engine/ops/op_fused_llm_attention.py).  Additive,
+optional keyword arguments: `num_heads` / `head_dim` (the reference hard-codes
+24 x 64), `num_kv_heads` for the backbone op (reference: 32 / 8 / 128 with a
+fixed 4096-wide output), and `kv_mask` on the 3-way ops (1 = visible key,
+0 = padded key, the eager encoder/physics mask convention).  Every op has a
+`register_fake` so `torch.compile` can trace it.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import functional as Fn
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+
+
+def _attn_from_qkv(q, k, v, key_bias, M, H, D):
+    """(H, M, D) Q/K/V -> (1, M, H*D) bf16, written directly in token-major order."""
+    out = torch.empty((1, M, H, D), dtype=torch.bfloat16, device=q.device)
+    Fn.attention(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0), key_bias=key_bias, layout="bhsd",
+                 out=out.permute(0, 2, 1, 3))
+    return out.view(1, M, H * D)
+
+
+def _qkv_cols(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dim() == 2 else t.reshape(-1, t.shape[-1])
+
+
+# ---------------------------------------------------------------------------
+# ds::  (DoubleStreamBlock / ExpandedDoubleStreamBlock)
+# ---------------------------------------------------------------------------
+
+
+@torch.library.custom_op("ds::fused_attention_2way", mutates_args=())
+def ds_fused_attention_2way(
+    sa_qkv: torch.Tensor,
+    vl_qkv: torch.Tensor,
+    q_norm_sa_weight: torch.Tensor,
+    k_norm_sa_weight: torch.Tensor,
+    q_norm_vl_weight: torch.Tensor,
+    k_norm_vl_weight: torch.Tensor,
+    rope_cos: torch.Tensor,
+    rope_sin: torch.Tensor,
+    n_sa: int,
+    n_vl: int,
+    num_heads: int = 24,
+    head_dim: int = 64,
+) -> torch.Tensor:
+    """QK-RMSNorm + interleaved RoPE (SA rows) + joint attention over [VL | SA].
+
+    Reference: op_fused_attention.py:12-82 (double_stream)."""
+    H, D = num_heads, head_dim
+    streams = [
+        Fn.StreamSpec(_qkv_cols(vl_qkv)[:n_vl], q_norm_vl_weight, k_norm_vl_weight),
+        Fn.StreamSpec(_qkv_cols(sa_qkv)[:n_sa], q_norm_sa_weight, k_norm_sa_weight, rope_cos, rope_sin),
+    ]
+    q, k, v = Fn.msat_qkv_norm_rope(streams, H, D)
+    return _attn_from_qkv(q, k, v, None, n_vl + n_sa, H, D)
+
+
+@ds_fused_attention_2way.register_fake
+def _(sa_qkv, vl_qkv, q_norm_sa_weight, k_norm_sa_weight, q_norm_vl_weight, k_norm_vl_weight, rope_cos, rope_sin,
+      n_sa, n_vl, num_heads=24, head_dim=64):
+    return sa_qkv.new_empty((1, n_sa + n_vl, num_heads * head_dim))
+
+
+@torch.library.custom_op("ds::fused_attention_3way", mutates_args=())
+def ds_fused_attention_3way(
+    sa_qkv: torch.Tensor,
+    vl_qkv: torch.Tensor,
+    p_qkv: torch.Tensor,
+    q_norm_sa_weight: torch.Tensor,
+    k_norm_sa_weight: torch.Tensor,
+    q_norm_vl_weight: torch.Tensor,
+    k_norm_vl_weight: torch.Tensor,
+    q_norm_p_weight: torch.Tensor,
+    k_norm_p_weight: torch.Tensor,
+    sa_rope_cos: torch.Tensor,
+    sa_rope_sin: torch.Tensor,
+    p_rope_cos: torch.Tensor,
+    p_rope_sin: torch.Tensor,
+    n_sa: int,
+    n_vl: int,
+    n_p: int,
+    num_heads: int = 24,
+    head_dim: int = 64,
+    kv_mask: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Three-stream [VL | SA | P] version; `kv_mask` [1, M] masks padded keys.
+
+    Reference: op_fused_attention_3way.py:13-116 (double_stream); mask semantics
+    of ExpandedDoubleStreamBlock.forward (blocks.py:843-866)."""
+    H, D = num_heads, head_dim
+    streams = [
+        Fn.StreamSpec(_qkv_cols(vl_qkv)[:n_vl], q_norm_vl_weight, k_norm_vl_weight),
+        Fn.StreamSpec(_qkv_cols(sa_qkv)[:n_sa], q_norm_sa_weight, k_norm_sa_weight, sa_rope_cos, sa_rope_sin),
+        Fn.StreamSpec(_qkv_cols(p_qkv)[:n_p], q_norm_p_weight, k_norm_p_weight, p_rope_cos, p_rope_sin),
+    ]
+    q, k, v = Fn.msat_qkv_norm_rope(streams, H, D)
+    bias = Fn.mask_to_key_bias(kv_mask) if kv_mask is not None else None
+    return _attn_from_qkv(q, k, v, bias, n_vl + n_sa + n_p, H, D)
+
+
+@ds_fused_attention_3way.register_fake
+def _(sa_qkv, vl_qkv, p_qkv, q_norm_sa_weight, k_norm_sa_weight, q_norm_vl_weight, k_norm_vl_weight,
+      q_norm_p_weight, k_norm_p_weight, sa_rope_cos, sa_rope_sin, p_rope_cos, p_rope_sin, n_sa, n_vl, n_p,
+      num_heads=24, head_dim=64, kv_mask=None):
+    return sa_qkv.new_empty((1, n_sa + n_vl + n_p, num_heads * head_dim))
+
+
+@torch.library.custom_op("ds::grouped_swiglu", mutates_args=())
+def ds_grouped_swiglu(
+    sa_w12: torch.Tensor,
+    sa_bias: torch.Tensor,
+    vl_w12: torch.Tensor,
+    vl_bias: torch.Tensor,
+    m_sa: int,
+    m_vl: int,
+    n_half_sa: int,
+    n_half_vl: int,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """SiLU(x[:, :N] + b[:N]) * (x[:, N:] + b[N:]) for the SA and VL groups in one launch.
+
+    Reference: op_grouped_swiglu.py:12-49.  Rounds like eager bf16 tensors
+    (bias add, silu and product each rounded to bf16)."""
+    return Fn.grouped_swiglu(sa_w12, sa_bias, vl_w12, vl_bias, m_sa, m_vl, n_half_sa, n_half_vl)
+
+
+@ds_grouped_swiglu.register_fake
+def _(sa_w12, sa_bias, vl_w12, vl_bias, m_sa, m_vl, n_half_sa, n_half_vl):
+    return sa_w12.new_empty((m_sa, n_half_sa)), vl_w12.new_empty((m_vl, n_half_vl))
+
+
+# ---------------------------------------------------------------------------
+# ss::  (SingleStreamBlock / ExpandedSingleStreamBlock)
+# ---------------------------------------------------------------------------
+
+
+@torch.library.custom_op("ss::fused_attention_2way", mutates_args=())
+def ss_fused_attention_2way(
+    qkv: torch.Tensor,
+    q_norm_weight: torch.Tensor,
+    k_norm_weight: torch.Tensor,
+    rope_cos: torch.Tensor,
+    rope_sin: torch.Tensor,
+    n_sa: int,
+    num_heads: int = 24,
+    head_dim: int = 64,
+) -> torch.Tensor:
+    """One packed `linear1` buffer [M, >= 3*inner]; RoPE on its last n_sa rows.
+
+    Reference: single_stream/engine/ops/op_fused_attention.py:12-65."""
+    H, D = num_heads, head_dim
+    x = _qkv_cols(qkv)
+    M = x.shape[0]
+    streams = []
+    if M - n_sa > 0:
+        streams.append(Fn.StreamSpec(x[: M - n_sa], q_norm_weight, k_norm_weight))
+    if n_sa > 0:
+        streams.append(Fn.StreamSpec(x[M - n_sa:], q_norm_weight, k_norm_weight, rope_cos, rope_sin))
+    q, k, v = Fn.msat_qkv_norm_rope(streams, H, D)
+    return _attn_from_qkv(q, k, v, None, M, H, D)
+
+
+@ss_fused_attention_2way.register_fake
+def _(qkv, q_norm_weight, k_norm_weight, rope_cos, rope_sin, n_sa, num_heads=24, head_dim=64):
+    return qkv.new_empty((1, qkv.shape[0], num_heads * head_dim))
+
+
+@torch.library.custom_op("ss::fused_attention_3way", mutates_args=())
+def ss_fused_attention_3way(
+    x_qkv: torch.Tensor,
+    p_qkv: torch.Tensor,
+    x_q_norm_weight: torch.Tensor,
+    x_k_norm_weight: torch.Tensor,
+    p_q_norm_weight: torch.Tensor,
+    p_k_norm_weight: torch.Tensor,
+    sa_rope_cos: torch.Tensor,
+    sa_rope_sin: torch.Tensor,
+    p_rope_cos: torch.Tensor,
+    p_rope_sin: torch.Tensor,
+    n_x: int,
+    n_sa: int,
+    n_p: int,
+    num_heads: int = 24,
+    head_dim: int = 64,
+    kv_mask: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """[VL+SA | P]: RoPE on the last n_sa rows of x and on all P rows.
+
+    Reference: single_stream/engine/ops/op_fused_attention_3way.py:13-129."""
+    H, D = num_heads, head_dim
+    x = _qkv_cols(x_qkv)[:n_x]
+    p = _qkv_cols(p_qkv)[:n_p]
+    streams = []
+    if n_x - n_sa > 0:
+        streams.append(Fn.StreamSpec(x[: n_x - n_sa], x_q_norm_weight, x_k_norm_weight))
+    if n_sa > 0:
+        streams.append(Fn.StreamSpec(x[n_x - n_sa:], x_q_norm_weight, x_k_norm_weight, sa_rope_cos, sa_rope_sin))
+    if n_p > 0:
+        streams.append(Fn.StreamSpec(p, p_q_norm_weight, p_k_norm_weight, p_rope_cos, p_rope_sin))
+    q, k, v = Fn.msat_qkv_norm_rope(streams, H, D)
+    bias = Fn.mask_to_key_bias(kv_mask) if kv_mask is not None else None
+    return _attn_from_qkv(q, k, v, bias, n_x + n_p, H, D)
+
+
+@ss_fused_attention_3way.register_fake
+def _(x_qkv, p_qkv, x_q_norm_weight, x_k_norm_weight, p_q_norm_weight, p_k_norm_weight, sa_rope_cos, sa_rope_sin,
+      p_rope_cos, p_rope_sin, n_x, n_sa, n_p, num_heads=24, head_dim=64, kv_mask=None):
+    return x_qkv.new_empty((1, n_x + n_p, num_heads * head_dim))
+
+
+# ---------------------------------------------------------------------------
+# rldx_backbone::  (Qwen3-VL LLM decoder)
+# ---------------------------------------------------------------------------
+
+
+def llm_fused_attention(qkv, q_norm_w, q_norm_w_rot, k_norm_w, k_norm_w_rot, cos, signed_sin, num_heads=32,
+                        num_kv_heads=8, head_dim=128, out=None):
+    """QK-RMSNorm + rotate-half RoPE + causal GQA attention on a packed
+    (M, (Hq + 2*Hkv) * D) QKV buffer -> (M, Hq*D).
+
+    Same Python signature as fused_llm_attention.forward
+    (rldx/inference/backbone/llm/engine/kernels/fused_llm_attention.py:1005-1057).
+    `q_norm_w_rot` / `k_norm_w_rot` are accepted for signature compatibility;
+    the kernel reads the rotate-half partner directly, which gives the same
+    values (w_rot[d] * x[d +- D/2] == w[d +- D/2] * x[d +- D/2])."""
+    M = qkv.shape[0]
+    Hq, Hkv, D = num_heads, num_kv_heads, head_dim
+    qkv_dim = (Hq + 2 * Hkv) * D
+    if qkv.dim() != 2 or qkv.shape[1] != qkv_dim or qkv.stride(1) != 1:
+        raise RuntimeError(f"rldx_amd: qkv must be (M, {qkv_dim}) with contiguous columns")
+    if out is None:
+        out = torch.empty((M, Hq * D), dtype=torch.bfloat16, device=qkv.device)
+    ld = qkv.stride(0)
+    # 1) QK-RMSNorm + RoPE into a (M, Hq + Hkv, D) workspace
+    ws = torch.empty((M, Hq + Hkv, D), dtype=torch.bfloat16, device=qkv.device)
+    q_view = qkv.as_strided((1, M, Hq, D), (0, ld, D, 1))
+    k_view = qkv.as_strided((1, M, Hkv, D), (0, ld, D, 1), qkv.storage_offset() + Hq * D)
+    Fn.qk_rmsnorm_rope_half(q_view, k_view, q_norm_w, k_norm_w, cos, signed_sin, 1e-6, sin_is_signed=True,
+                            q_out=ws[None, :, :Hq], k_out=ws[None, :, Hq:])
+    # 2) causal GQA attention; V read in place from the packed buffer
+    wsd = (Hq + Hkv) * D
+    Fn.attention_raw(ws, ws, qkv, out, batch=1, q_heads=Hq, kv_heads=Hkv, seq_q=M, seq_k=M, head_dim=D,
+                     q_strides=[0, D, wsd], k_strides=[0, D, wsd], v_strides=[0, D, ld], o_strides=[0, D, out.stride(0)],
+                     causal=True, k_offset=Hq * D, v_offset=(Hq + Hkv) * D)
+    return out
+
+
+@torch.library.custom_op("rldx_backbone::fused_attention", mutates_args=())
+def rldx_backbone_fused_attention(
+    qkv: torch.Tensor,
+    q_norm_w: torch.Tensor,
+    q_norm_w_rot: torch.Tensor,
+    k_norm_w: torch.Tensor,
+    k_norm_w_rot: torch.Tensor,
+    cos: torch.Tensor,
+    signed_sin: torch.Tensor,
+    num_heads: int = 32,
+    num_kv_heads: int = 8,
+    head_dim: int = 128,
+) -> torch.Tensor:
+    """Reference: backbone/llm/engine/ops/op_fused_llm_attention.py:13-45."""
+    return llm_fused_attention(qkv, q_norm_w, q_norm_w_rot, k_norm_w, k_norm_w_rot, cos, signed_sin, num_heads,
+                               num_kv_heads, head_dim)
+
+
+@rldx_backbone_fused_attention.register_fake
+def _(qkv, q_norm_w, q_norm_w_rot, k_norm_w, k_norm_w_rot, cos, signed_sin, num_heads=32, num_kv_heads=8,
+      head_dim=128):
+    return qkv.new_empty((qkv.shape[0], num_heads * head_dim))
+
+
+# ---------------------------------------------------------------------------
+# rldx_amd::swiglu  (the activation of SwiGLUFFN and the chains' inline SwiGLU)
+# ---------------------------------------------------------------------------
+
+
+@torch.library.custom_op("rldx_amd::swiglu", mutates_args=())
+def swiglu_op(x: torch.Tensor) -> torch.Tensor:
+    """`F.silu(x1) * x2` with `x1, x2 = x.chunk(2, -1)` (action_model/ops.py:157-161)."""
+    return Fn.swiglu(x)
+
+
+@swiglu_op.register_fake
+def _(x):
+    return x.new_empty((*x.shape[:-1], x.shape[-1] // 2))

@@ -1,0 +1,107 @@
+"""CPU tests of the C ABI library: it loads, exports every declared symbol, the
+device SwiGLU element function is exact on all bf16 inputs (run on the host),
+and argument validation rejects bad calls before any GPU work."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cpu_reference as ref
+from rldx_amd import _lib
+from rldx_amd import functional as Fn
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "rldx_amd.h"
+HIP_INVALID_VALUE = 1
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:hipError_t|int)\s+(rldx_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    assert "rldx_attention_fwd_bf16" in names and len(names) >= 7, names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in rldx_amd.h but not exported"
+    assert set(declared_functions()) == set(_lib.SIGNATURES), "ctypes signature table out of sync with the header"
+
+
+def test_host_swiglu_exhaustive_bitexact():
+    """All 65536 bf16 gate values x several up values: the exact device element
+    function, executed on the CPU, reproduces eager `F.silu(x1) * x2` bit for bit."""
+    gates = np.arange(65536, dtype=np.uint16)
+    g_t = torch.from_numpy(gates.view(np.int16).copy()).view(torch.bfloat16)
+    for up in (1.0, -1.0, 2.5, -0.0078125, 7.0, 1e30):
+        u_t = torch.full((65536,), up, dtype=torch.bfloat16)
+        ups = u_t.view(torch.int16).numpy().view(np.uint16)
+        mine = Fn.host_swiglu_bf16_bits(gates, ups)
+        r = ref.swiglu(torch.cat([g_t, u_t])[None, :])[0]
+        rb = r.view(torch.int16).numpy().view(np.uint16)
+        nan = np.isnan(r.float().numpy()) & np.isnan(torch.from_numpy(mine.view(np.int16)).view(torch.bfloat16).float().numpy())
+        bad = (mine != rb) & ~nan
+        assert not bad.any(), f"up={up}: {int(bad.sum())} mismatches, first gate bits {gates[bad][:5]}"
+
+
+def test_host_swiglu_random_pairs():
+    rng = np.random.default_rng(0)
+    g = rng.integers(0, 65536, size=200000, dtype=np.uint16)
+    u = rng.integers(0, 65536, size=200000, dtype=np.uint16)
+    mine = Fn.host_swiglu_bf16_bits(g, u)
+    gt = torch.from_numpy(g.view(np.int16).copy()).view(torch.bfloat16)
+    ut = torch.from_numpy(u.view(np.int16).copy()).view(torch.bfloat16)
+    r = ref.swiglu(torch.cat([gt, ut])[None, :])[0]
+    rb = r.view(torch.int16).numpy().view(np.uint16)
+    both_nan = np.isnan(r.float().numpy()) & np.isnan(torch.from_numpy(mine.view(np.int16)).view(torch.bfloat16).float().numpy())
+    assert not ((mine != rb) & ~both_nan).any()
+
+
+def test_capi_rejects_bad_arguments_without_launching():
+    lib = _lib.load()
+    # ldx smaller than 2*n_half
+    assert lib.rldx_swiglu_bf16(16, 4, None, 16, 8, 2, 8, None) == HIP_INVALID_VALUE
+    # negative rows
+    assert lib.rldx_swiglu_bf16(16, 16, None, 16, 8, -1, 8, None) == HIP_INVALID_VALUE
+    # null pointers with work to do
+    assert lib.rldx_swiglu_bf16(None, 16, None, None, 8, 2, 8, None) == HIP_INVALID_VALUE
+    st = _lib.i64_array([0, 0, 0])
+    # unsupported head_dim
+    assert lib.rldx_attention_fwd_bf16(16, 16, 16, 16, 1, 1, 1, 4, 4, 96, st, st, st, st, None, 0, 1.0, 0,
+                                       None) == HIP_INVALID_VALUE
+    # q heads not a multiple of kv heads
+    assert lib.rldx_attention_fwd_bf16(16, 16, 16, 16, 1, 3, 2, 4, 4, 128, st, st, st, st, None, 0, 1.0, 0,
+                                       None) == HIP_INVALID_VALUE
+    # misaligned pointer
+    assert lib.rldx_attention_fwd_bf16(18, 16, 16, 16, 1, 2, 2, 4, 4, 128, st, st, st, st, None, 0, 1.0, 0,
+                                       None) == HIP_INVALID_VALUE
+    assert lib.rldx_msat_qkv_norm_rope_bf16(None, 1, 12, 128, 16, 16, 16, 0, 0, 1e-6, None) == HIP_INVALID_VALUE
+    s = _lib.MsatStream(16, 100, 4, 16, 16, None, None, 0)  # row stride < 3*H*D
+    assert lib.rldx_msat_qkv_norm_rope_bf16(ctypes.byref(s), 1, 12, 128, 16, 16, 16, 0, 0, 1e-6,
+                                            None) == HIP_INVALID_VALUE
+    assert lib.rldx_qk_rmsnorm_rope_half_f32(16, 16, 16, 16, 16, 16, 16, 16, 1, 4, 2, 2, 96, st, st, st, st, st,
+                                             1e-6, None) == HIP_INVALID_VALUE
+
+
+def test_zero_sized_calls_are_noops():
+    lib = _lib.load()
+    st = _lib.i64_array([0, 0, 0])
+    assert lib.rldx_swiglu_bf16(None, 0, None, None, 0, 0, 8, None) == 0
+    assert lib.rldx_attention_fwd_bf16(None, None, None, None, 0, 2, 2, 4, 4, 128, st, st, st, st, None, 0, 1.0, 0,
+                                       None) == 0
+
+
+def test_python_wrappers_refuse_cpu_tensors():
+    x = torch.zeros(2, 16, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        Fn.swiglu(x)
+    q = torch.zeros(1, 2, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError):
+        Fn.attention(q, q, q)
