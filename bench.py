@@ -1,0 +1,290 @@
+"""Benchmark: ms per MSAT action step (batch 1, one MI355X) + kernel roofline fractions.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Workload (value): the synthetic MSAT action step — 16 triple-stream blocks,
+hidden 1536, 12 heads x 128, SwiGLU 4096, 512 cognition / 64 action / 32 physics
+tokens, 4 Euler denoising iterations, bf16, random-init weights — captured as
+one hipGraph; K replays are timed after W warm-up replays.
+
+Kernel lines (roofline): each hand-written kernel at its workload shape is
+captured N times back to back into a hipGraph and timed with HIP events on the
+launch stream; achieved = algorithmic bytes or flops per launch / mean launch
+time.  `roofline` is the dominant hand-written kernel of the step (joint
+attention at 12 x 608 x 128).  cpu_baseline: the CPU oracle of the same step
+(torch bf16 on the host cores).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT, ROOT / "rldx-1_amd"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--kernel-reps", type=int, default=50)
+    return ap.parse_args()
+
+
+def graph_time_ms(fn, reps: int, torch) -> float:
+    """Mean duration of one `fn()` launch sequence: `reps` copies captured into a
+    hipGraph, replayed, timed with events on the capture/launch stream."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    best = math.inf
+    for _ in range(3):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        e1.synchronize()
+        best = min(best, e0.elapsed_time(e1) / reps)
+    return best
+
+
+def kernel_lines(torch, reps: int):
+    from oracle import cpu_reference as ref  # noqa: F401  (not used for timing; keeps import errors early)
+    from rldx_amd import functional as Fn
+    from rldx_amd import workloads as W
+    from rldx_amd.msat_step import MsatStepCfg
+
+    dev = torch.device("cuda:0")
+    out = {}
+
+    # SwiGLU 2048 x 11008 (rotate 3 input copies so the 256 MB MALL cannot hold them)
+    cfg = W.SwigluCfg()
+    x = W.swiglu_inputs(cfg)["x"].to(dev)
+    xs = [x] + [x.clone() for _ in range(2)]
+    ys = [torch.empty(cfg.tokens, cfg.n_half, dtype=torch.bfloat16, device=dev) for _ in range(3)]
+    it = {"i": 0}
+
+    def sw():
+        i = it["i"] % 3
+        it["i"] += 1
+        Fn.swiglu(xs[i], out=ys[i])
+
+    ms = graph_time_ms(sw, 30, torch)
+    gbs = W.swiglu_bytes(cfg) / (ms * 1e-3) / 1e9
+    out["swiglu_2048x11008"] = dict(us=ms * 1e3, achieved=gbs, unit="GB/s", bound="hbm", peak=HBM_PEAK_GBS,
+                                    frac=gbs / HBM_PEAK_GBS, bytes=W.swiglu_bytes(cfg))
+    del xs, ys, x
+    cfg64 = W.SwigluCfg(tokens=64)
+    x64 = W.swiglu_inputs(cfg64)["x"].to(dev)
+    y64 = torch.empty(64, cfg64.n_half, dtype=torch.bfloat16, device=dev)
+    ms = graph_time_ms(lambda: Fn.swiglu(x64, out=y64), reps, torch)
+    gbs = W.swiglu_bytes(cfg64) / (ms * 1e-3) / 1e9
+    out["swiglu_64x11008"] = dict(us=ms * 1e3, achieved=gbs, unit="GB/s", bound="hbm", peak=HBM_PEAK_GBS,
+                                  frac=gbs / HBM_PEAK_GBS, bytes=W.swiglu_bytes(cfg64))
+
+    # RMSNorm + rotate-half RoPE, fp32, q/k [1, 256, 16, 64]
+    rc = W.RmsRopeCfg()
+    ri = {k: v.to(dev) for k, v in W.rmsnorm_rope_inputs(rc).items()}
+    qo = torch.empty_like(ri["q"])
+    ko = torch.empty_like(ri["k"])
+    ms = graph_time_ms(lambda: Fn.qk_rmsnorm_rope_half(ri["q"], ri["k"], ri["w"], ri["w"], ri["cos"], ri["sin"],
+                                                       rc.eps, q_out=qo, k_out=ko), reps, torch)
+    gbs = W.rmsnorm_rope_bytes(rc) / (ms * 1e-3) / 1e9
+    out["rmsnorm_rope_f32_256x16x64"] = dict(us=ms * 1e3, achieved=gbs, unit="GB/s", bound="hbm", peak=HBM_PEAK_GBS,
+                                             frac=gbs / HBM_PEAK_GBS, bytes=W.rmsnorm_rope_bytes(rc))
+
+    # MSAT joint attention 16 x 608 x 128, masked
+    jc = W.JointAttnCfg()
+    ji = W.joint_attn_inputs(jc)
+    q, k, v = (ji[n].to(dev) for n in ("q", "k", "v"))
+    bias = torch.where(ji["kv_mask"] == 0, float("-inf"), 0.0).float().to(dev)
+    o = torch.empty_like(q)
+    ms = graph_time_ms(lambda: Fn.attention(q, k, v, key_bias=bias, out=o), reps, torch)
+    tf = W.joint_attn_flops(jc) / (ms * 1e-3) / 1e12
+    out["joint_attention_16x608x128"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s", bound="mfma",
+                                              peak=BF16_MFMA_PEAK_TFLOPS, frac=tf / BF16_MFMA_PEAK_TFLOPS,
+                                              flops=W.joint_attn_flops(jc))
+
+    # GQA causal prefill 28/4 x 1280 x 128 (rldx_backbone::fused_attention: prologue + attention)
+    import rldx_amd.ops as ops
+
+    gc = W.GqaCfg()
+    gi = W.gqa_inputs(gc)
+    qkv = gi["qkv"].to(dev)
+    args = (qkv, gi["q_norm_w"].to(dev), None, gi["k_norm_w"].to(dev), None, gi["cos"].to(dev),
+            W.signed_sin(gi["sin"]).to(dev))
+    ob = torch.empty(gc.seq, gc.q_heads * gc.head_dim, dtype=torch.bfloat16, device=dev)
+    ms = graph_time_ms(lambda: ops.llm_fused_attention(*args, num_heads=gc.q_heads, num_kv_heads=gc.kv_heads,
+                                                       head_dim=gc.head_dim, out=ob), reps, torch)
+    tf = W.gqa_flops(gc) / (ms * 1e-3) / 1e12
+    out["gqa_prefill_op_28x4x1280x128"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s", bound="mfma",
+                                               peak=BF16_MFMA_PEAK_TFLOPS, frac=tf / BF16_MFMA_PEAK_TFLOPS,
+                                               flops=W.gqa_flops(gc))
+    # attention kernel alone on pre-normalised Q/K
+    M, Hq, Hkv, D = gc.seq, gc.q_heads, gc.kv_heads, gc.head_dim
+    qn = torch.randn(1, M, Hq, D, device=dev).to(torch.bfloat16)
+    kn = torch.randn(1, M, Hkv, D, device=dev).to(torch.bfloat16)
+    vn = torch.randn(1, M, Hkv, D, device=dev).to(torch.bfloat16)
+    on = torch.empty_like(qn)
+    ms = graph_time_ms(lambda: Fn.attention(qn, kn, vn, causal=True, layout="bshd", out=on), reps, torch)
+    tf = W.gqa_flops(gc) / (ms * 1e-3) / 1e12
+    out["gqa_attention_28x4x1280x128"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s", bound="mfma",
+                                              peak=BF16_MFMA_PEAK_TFLOPS, frac=tf / BF16_MFMA_PEAK_TFLOPS,
+                                              flops=W.gqa_flops(gc))
+
+    # the step's own attention shape: 12 x 608 x 128, masked
+    sc = MsatStepCfg()
+    n = sc.tokens
+    qs = torch.randn(1, sc.heads, n, sc.head_dim, device=dev).to(torch.bfloat16)
+    ks = torch.randn(1, sc.heads, n, sc.head_dim, device=dev).to(torch.bfloat16)
+    vs = torch.randn(1, sc.heads, n, sc.head_dim, device=dev).to(torch.bfloat16)
+    bs = torch.zeros(n, device=dev)
+    bs[n - sc.n_p_pad:] = float("-inf")
+    os_ = torch.empty_like(qs)
+    ms = graph_time_ms(lambda: Fn.attention(qs, ks, vs, key_bias=bs, out=os_), reps, torch)
+    fl = 4 * sc.heads * n * n * sc.head_dim
+    tf = fl / (ms * 1e-3) / 1e12
+    out["step_joint_attention_12x608x128"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s", bound="mfma",
+                                                  peak=BF16_MFMA_PEAK_TFLOPS, frac=tf / BF16_MFMA_PEAK_TFLOPS,
+                                                  flops=fl)
+    return out
+
+
+def cpu_baseline(torch, cfg, weights, inputs, budget_s: float = 20.0):
+    """Time the CPU oracle step on the host cores; bounded sample, scaled to ms per action step."""
+    from oracle import msat_step_ref as R
+
+    cores = os.cpu_count() or 1
+    cores = min(cores, 64)
+    torch.set_num_threads(cores)
+    w = {k: v.cpu() for k, v in weights.items()}
+    inp = {k: v.cpu() for k, v in inputs.items()}
+    # one iteration of one block first, to size the sample
+    R.action_step(cfg, w, inp, steps=1, blocks=1)
+    t0 = time.perf_counter()
+    R.action_step(cfg, w, inp, steps=1, blocks=1)
+    one = time.perf_counter() - t0
+    per_step_est = one * cfg.blocks * cfg.steps
+    if per_step_est <= budget_s / 2:
+        reps = max(1, int(budget_s / 2 / max(per_step_est, 1e-3)))
+        reps = min(reps, 5)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            R.action_step(cfg, w, inp)
+        ms = (time.perf_counter() - t0) / reps * 1e3
+        sample = f"{reps} full action step(s) ({cfg.blocks} blocks x {cfg.steps} iterations)"
+    else:
+        blocks = max(1, min(cfg.blocks, int(budget_s / max(one, 1e-3))))
+        t0 = time.perf_counter()
+        R.action_step(cfg, w, inp, steps=1, blocks=blocks)
+        ms = (time.perf_counter() - t0) * cfg.blocks * cfg.steps / blocks * 1e3
+        sample = f"1 iteration x {blocks} blocks, scaled x{cfg.blocks * cfg.steps / blocks:.1f} to a full step"
+    return dict(value=ms, unit="ms per MSAT action step", cores=torch.get_num_threads(), kind="port",
+                sample=sample + " of the CPU oracle (torch bf16 eager restatement)")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the action step is batch-1 single-GPU; multi-GPU would be data parallel over sessions).",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import rldx_amd
+    from rldx_amd.msat_step import MsatActionStep, MsatStepCfg, make_inputs, make_weights
+
+    rldx_amd.load()
+    dev = torch.device("cuda:0")
+    cfg = MsatStepCfg()
+    print(f"[bench] building step weights ({cfg.weight_bytes() / 1e9:.2f} GB bf16)", file=sys.stderr, flush=True)
+    weights = make_weights(cfg, dev)
+    inputs = make_inputs(cfg, dev)
+    step = MsatActionStep(cfg, weights, inputs)
+    step.capture()
+    print("[bench] graph captured", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        step.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    act = step.act.float()
+    assert torch.isfinite(act).all(), "non-finite actions"
+    print(f"[bench] action step {ms:.3f} ms", file=sys.stderr, flush=True)
+
+    kl = kernel_lines(torch, args.kernel_reps)
+    print("[bench] kernel lines done", file=sys.stderr, flush=True)
+    dom = kl["step_joint_attention_12x608x128"]
+    roofline = dict(kernel="attn_fwd_kernel<128,false,true> (joint attention 12 heads x 608 x 128, masked)",
+                    bound="mfma", achieved=dom["achieved"], peak=dom["peak"], unit="TFLOP/s", frac=dom["frac"],
+                    traffic=None)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(torch, cfg, weights, inputs)
+        print(f"[bench] cpu baseline {cpu['value']:.1f} ms", file=sys.stderr, flush=True)
+
+    line = {
+        "metric": "ms per MSAT action step (bs=1, 1 GPU); kernel % HBM/MFMA roofline",
+        "value": ms,
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded randn inputs, random-init weights N(0, 0.02))",
+        "config": {
+            "workload": "msat_action_step",
+            "blocks": cfg.blocks, "hidden": cfg.hidden, "heads": cfg.heads, "head_dim": cfg.head_dim,
+            "ffn": cfg.ffn, "tokens": {"cognition": cfg.n_vl, "action": cfg.n_sa, "physics": cfg.n_p,
+                                       "physics_padded": cfg.n_p_pad},
+            "denoise_iterations": cfg.steps, "batch": 1, "graph": "one hipGraph per action step",
+            "step_tflop": cfg.flops_per_step() / 1e12, "weight_gb": cfg.weight_bytes() / 1e9,
+        },
+        "roofline": roofline,
+        "kernels": kl,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()
