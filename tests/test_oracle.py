@@ -1,0 +1,381 @@
+"""CPU tests that pin the oracle (oracle/cpu_reference.py, oracle/msat_step_ref.py)
+independently of its own formulas.
+
+The reference ships no tests, golden vectors or fixtures for this path, so each
+oracle function is pinned by what the mathematics fixes: fp64 brute force,
+closed forms, invariants (identity at position 0, norm preservation, relative
+position, masked keys carry zero weight, permutation equivariance), and the
+bf16 rounding recipe checked against fp64 values rounded once / twice.  Each
+check is chosen so that a plausible mistake (dropped term, wrong sign or
+index, transposed operand, wrong rounding point) fails it.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import cpu_reference as ref
+from rldx_amd import workloads as W
+
+torch.manual_seed(0)
+
+
+def f64(t):
+    return t.detach().double()
+
+
+# ---------------------------------------------------------------------------
+# Qwen RMSNorm (modeling_qwen3_vl.py:366-371)
+# ---------------------------------------------------------------------------
+def test_qwen_rmsnorm_fp32_matches_fp64_closed_form():
+    x = torch.randn(64, 128)
+    w = 1 + 0.1 * torch.randn(128)
+    y = ref.qwen_rmsnorm(x, w, 1e-6)
+    y64 = f64(w) * f64(x) / torch.sqrt((f64(x) ** 2).mean(-1, keepdim=True) + 1e-6)
+    assert (y.double() - y64).abs().max() < 3e-6
+
+
+def test_qwen_rmsnorm_unit_weight_gives_unit_rms_and_is_scale_invariant():
+    x = torch.randn(32, 64)
+    y = ref.qwen_rmsnorm(x, torch.ones(64), 0.0)
+    assert torch.allclose(y.pow(2).mean(-1), torch.ones(32), atol=1e-5)
+    assert torch.allclose(ref.qwen_rmsnorm(7.5 * x, torch.ones(64), 0.0), y, atol=1e-5)
+
+
+def test_qwen_rmsnorm_bf16_rounds_before_weight():
+    """bf16 path: w * bf16(x * rsqrt) — two roundings.  Pinned against fp64 values
+    rounded in that order; rounding once would differ on a measurable share."""
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(256, 128, generator=g).to(torch.bfloat16)
+    w = (1 + 0.3 * torch.randn(128, generator=g)).to(torch.bfloat16)
+    y = ref.qwen_rmsnorm(x, w, 1e-6)
+    n64 = f64(x) / torch.sqrt((f64(x) ** 2).mean(-1, keepdim=True) + 1e-6)
+    two = (f64(w) * n64.to(torch.bfloat16).double()).to(torch.bfloat16)
+    one = (f64(w) * n64).to(torch.bfloat16)
+    agree_two = (y == two).float().mean().item()
+    agree_one = (y == one).float().mean().item()
+    assert agree_two > 0.999 and agree_one < agree_two - 0.01, (agree_two, agree_one)
+
+
+# ---------------------------------------------------------------------------
+# rotate-half RoPE (modeling_qwen3_vl.py:118-122, :377-401) and its tables
+# ---------------------------------------------------------------------------
+def test_rotate_half_closed_form():
+    x = torch.arange(8.0)
+    assert torch.equal(ref.rotate_half(x), torch.tensor([-4.0, -5, -6, -7, 0, 1, 2, 3]))
+
+
+def test_qwen_rope_tables_closed_form():
+    cos, sin = W.qwen_rope_cos_sin(300, 64, 1e4)
+    pos = torch.arange(300, dtype=torch.float64)[:, None]
+    i = torch.arange(32, dtype=torch.float64)[None, :]
+    ang = pos * (1e4 ** (-(2 * i) / 64))
+    ang = torch.cat([ang, ang], dim=1)
+    # fp32 angle rounding grows with position: |d cos| <= |angle| * 2^-24
+    tol = 300 * 2.0 ** -23 + 1e-6
+    assert (cos.double() - ang.cos()).abs().max() < tol
+    assert (sin.double() - ang.sin()).abs().max() < tol
+
+
+def test_rope_half_identity_norm_and_relative_position():
+    D = 64
+    cos, sin = W.qwen_rope_cos_sin(40, D, 1e4)
+    cos64, sin64 = cos.double(), sin.double()
+    q = torch.randn(40, D, dtype=torch.float64)
+    k = torch.randn(40, D, dtype=torch.float64)
+    qe, ke = ref.apply_rotary_pos_emb(q[None], k[None], cos64, sin64, unsqueeze_dim=0)
+    qe, ke = qe[0], ke[0]
+    assert torch.allclose(qe[0], q[0])  # position 0 is the identity
+    pair = lambda t: t[:, : D // 2] ** 2 + t[:, D // 2:] ** 2  # noqa: E731
+    assert torch.allclose(pair(qe), pair(q), atol=1e-9)  # each (d, d+D/2) pair keeps its norm
+    # <R_m q, R_n k> depends on m - n only
+    qq = q[5].expand(40, D)
+    kk = k[9].expand(40, D)
+    a, b = ref.apply_rotary_pos_emb(qq[None], kk[None], cos64, sin64, unsqueeze_dim=0)
+    d1 = (a[0, 20] * b[0, 17]).sum()
+    d2 = (a[0, 30] * b[0, 27]).sum()
+    assert abs(d1 - d2) < 1e-5
+
+
+def test_qk_rmsnorm_rope_half_sign_convention():
+    """A wrong rotate_half sign or a d <-> d+D/2 swap breaks the 2x2 rotation form."""
+    D = 4
+    x = torch.tensor([[[[1.0, 0.0, 0.0, 0.0]]]])
+    ang = torch.tensor(0.3)
+    cos = torch.tensor([[ang.cos(), 1.0, ang.cos(), 1.0]])
+    sin = torch.tensor([[ang.sin(), 0.0, ang.sin(), 0.0]])
+    q, _ = ref.qk_rmsnorm_rope_half(x, x, torch.full((D,), 0.5), torch.ones(D), cos, sin, eps=0.0)
+    # normalised x = [2, 0, 0, 0] -> weighted [1, 0, 0, 0]; rotation puts sin into element D/2
+    assert torch.allclose(q[0, 0, 0], torch.tensor([ang.cos(), 0.0, ang.sin(), 0.0]), atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# MSAT RMSNorm (norms.py:18-22) and interleaved RoPE (ops.py:11-67)
+# ---------------------------------------------------------------------------
+def test_msat_rmsnorm_rounds_once():
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(512, 64, generator=g).to(torch.bfloat16)
+    w = (1 + 0.3 * torch.randn(64, generator=g)).to(torch.bfloat16)
+    y = ref.msat_rmsnorm(x, w, 1e-6)
+    n64 = f64(x) / torch.sqrt((f64(x) ** 2).mean(-1, keepdim=True) + 1e-6)
+    one = (f64(w) * n64).to(torch.bfloat16)
+    two = (f64(w) * n64.to(torch.bfloat16).double()).to(torch.bfloat16)
+    agree_one = (y == one).float().mean().item()
+    agree_two = (y == two).float().mean().item()
+    assert agree_one > 0.999 and agree_two < agree_one - 0.01, (agree_one, agree_two)
+
+
+def test_msat_freqs_cis_closed_form():
+    fc = W.msat_freqs_cis(48, 100, 1e4)
+    t = torch.arange(100, dtype=torch.float64)[:, None]
+    i = torch.arange(24, dtype=torch.float64)[None, :]
+    ang = t * 1e4 ** (-(2 * i) / 48)
+    assert (fc.real.double() - ang.cos()).abs().max() < 1e-4
+    assert (fc.imag.double() - ang.sin()).abs().max() < 1e-4
+
+
+def test_msat_rope_tables_axes():
+    """rope_sa_only: first D/4 columns follow axis 0, the remaining 3D/4 axis 1."""
+    D = 128
+    ids = torch.tensor([[0, 0], [0, 5], [1, 0], [1, 7]])
+    cos, sin = W.msat_rope_tables(ids, D)
+    assert torch.allclose(cos[0], torch.ones(D // 2)) and torch.allclose(sin[0], torch.zeros(D // 2))
+    assert torch.allclose(cos[1, : D // 8], torch.ones(D // 8))  # axis 0 = 0 -> identity part
+    assert not torch.allclose(cos[1, D // 8:], torch.ones(3 * D // 8))
+    assert torch.allclose(cos[2, D // 8:], torch.ones(3 * D // 8))  # axis 1 = 0
+    assert torch.allclose(cos[2, 0], torch.tensor(math.cos(1.0)), atol=1e-6)  # axis 0 = 1, freq 1
+
+
+def test_apply_rotary_emb_is_pairwise_rotation():
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(1, 2, 6, 8, generator=g)
+    ang = torch.randn(1, 6, 4, generator=g)
+    fc = torch.polar(torch.ones_like(ang), ang)
+    qo, _ = ref.apply_rotary_emb(q, q, fc)
+    e, o = f64(q)[..., 0::2], f64(q)[..., 1::2]
+    c, s = ang.double().cos()[:, None], ang.double().sin()[:, None]
+    re = e * c - o * s
+    im = e * s + o * c
+    assert torch.allclose(qo[..., 0::2].double(), re, atol=1e-6)
+    assert torch.allclose(qo[..., 1::2].double(), im, atol=1e-6)
+
+
+def test_msat_qkv_norm_rope_structure():
+    """V passes through untouched; rows without a table get norm only; the stream
+    order is the concatenation order."""
+    g = torch.Generator().manual_seed(4)
+    H, D = 2, 64
+    a = torch.randn(5, 3 * H * D, generator=g).to(torch.bfloat16)
+    b = torch.randn(3, 3 * H * D, generator=g).to(torch.bfloat16)
+    wa = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    wb = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    ids = torch.zeros(3, 2, dtype=torch.long)
+    ids[:, 1] = torch.arange(3) + 4
+    cos, sin = W.msat_rope_tables(ids, D)
+    q, k, v = ref.msat_qkv_norm_rope([(a, wa, wa, None, None), (b, wb, wb, cos, sin)], H, D)
+    assert q.shape == (H, 8, D)
+    assert torch.equal(v[0, :5], a[:, 2 * H * D:2 * H * D + D])
+    assert torch.equal(v[1, 5:], b[:, 2 * H * D + D:])
+    assert torch.equal(q[1, :5], ref.msat_rmsnorm(a[:, D:2 * D], wa))
+    assert not torch.equal(q[0, 5:], ref.msat_rmsnorm(b[:, :D], wb))
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU (ops.py:157-161)
+# ---------------------------------------------------------------------------
+def test_swiglu_closed_form_and_special_values():
+    x = torch.tensor([[0.0, 30.0, -30.0, 2.0, 1.0, 1.0, 1.0, 3.0]])
+    y = ref.swiglu(x)
+    assert y[0, 0] == 0
+    assert torch.allclose(y[0, 1], torch.tensor(30.0))
+    assert abs(float(y[0, 2])) < 1e-10
+    assert torch.allclose(y[0, 3], torch.tensor(3 * 2 / (1 + math.exp(-2))), atol=1e-6)
+
+
+def test_swiglu_bf16_is_two_roundings_exhaustive():
+    """All 65536 bf16 gates: silu rounded to bf16 (from fp64) matches, except for
+    double-rounding ties, and the product is rounded again."""
+    u = np.arange(65536, dtype=np.uint32) << 16
+    g = torch.from_numpy(u.view(np.float32).copy()).to(torch.bfloat16)
+    fin = torch.isfinite(g) & (g.float().abs() < 80)
+    g = g[fin]
+    up = torch.full_like(g, 3.0)
+    y = ref.swiglu(torch.cat([g, up])[None])[0]
+    s64 = f64(g) / (1 + torch.exp(-f64(g)))
+    two = (s64.to(torch.bfloat16).double() * 3.0).to(torch.bfloat16)
+    agree = (y == two).float().mean().item()
+    assert agree > 0.9995, agree
+    one = (s64 * 3.0).to(torch.bfloat16)
+    assert (y == one).float().mean().item() < agree - 0.05
+
+
+def test_swiglu_bias_rounds_the_sum_first():
+    x = torch.tensor([[1.0, 2.0]], dtype=torch.bfloat16)
+    b = torch.tensor([0.00390625, 0.0], dtype=torch.bfloat16)  # 1 + 2^-8 rounds back to 1 in bf16
+    assert torch.equal(ref.swiglu(x, b), ref.swiglu(x))
+
+
+# ---------------------------------------------------------------------------
+# SDPA (blocks.py:577-579, :843-866; modeling_qwen3_vl.py:139-176)
+# ---------------------------------------------------------------------------
+def brute_attention(q, k, v, bias=None, causal=False):
+    q, k, v = f64(q), f64(k), f64(v)
+    s = q @ k.transpose(-1, -2) / math.sqrt(q.shape[-1])
+    if bias is not None:
+        s = s + f64(bias)[:, None, None, :]
+    if causal:
+        n, m = s.shape[-2:]
+        s = s.masked_fill(torch.ones(n, m, dtype=torch.bool).triu(1), float("-inf"))
+    return torch.softmax(s, dim=-1) @ v
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("causal,masked", [(False, False), (False, True), (True, False)])
+def test_sdpa_matches_fp64_brute_force(dtype, tol, causal, masked):
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(2, 3, 19, 32, generator=g).to(dtype)
+    k = torch.randn(2, 3, 19, 32, generator=g).to(dtype)
+    v = torch.randn(2, 3, 19, 32, generator=g).to(dtype)
+    bias = None
+    if masked:
+        m = torch.ones(2, 19)
+        m[0, -4:] = 0
+        m[1, :2] = 0
+        bias = ref.mask_to_bias(m)
+    o = ref.sdpa(q, k, v, key_bias=bias, causal=causal)
+    assert (o.double() - brute_attention(q, k, v, bias, causal)).abs().max() < tol
+
+
+def test_sdpa_masked_keys_carry_no_weight_and_constant_keys_average():
+    g = torch.Generator().manual_seed(6)
+    q = torch.randn(1, 2, 7, 16, generator=g)
+    k = torch.randn(1, 2, 7, 16, generator=g)
+    v = torch.randn(1, 2, 7, 16, generator=g)
+    m = torch.ones(1, 7)
+    m[0, 5:] = 0
+    b = ref.mask_to_bias(m)
+    o1 = ref.sdpa(q, k, v, key_bias=b)
+    v2 = v.clone()
+    v2[:, :, 5:] = 1e6
+    assert torch.equal(o1, ref.sdpa(q, k, v2, key_bias=b))
+    kc = torch.zeros_like(k)
+    assert torch.allclose(ref.sdpa(q, kc, v), v.mean(dim=2, keepdim=True).expand_as(v), atol=1e-6)
+    oc = ref.sdpa(q, k, v, causal=True)
+    assert torch.allclose(oc[:, :, 0], v[:, :, 0])
+
+
+def test_gqa_with_replicated_kv_equals_mha():
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(1, 6, 11, 32, generator=g)
+    k = torch.randn(1, 2, 11, 32, generator=g)
+    v = torch.randn(1, 2, 11, 32, generator=g)
+    o = ref.sdpa(q, ref.repeat_kv(k, 3), ref.repeat_kv(v, 3), causal=True)
+    for h in range(6):
+        oh = brute_attention(q[:, h:h + 1], k[:, h // 3:h // 3 + 1], v[:, h // 3:h // 3 + 1], causal=True)
+        assert (o[:, h:h + 1].double() - oh).abs().max() < 1e-5
+
+
+def test_llm_fused_attention_composition():
+    """Packed-QKV op == per-head norm + rope + causal GQA on the unpacked tensors."""
+    cfg = W.GqaCfg(q_heads=4, kv_heads=2, head_dim=64, seq=20)
+    inp = W.gqa_inputs(cfg)
+    o = ref.llm_fused_attention(inp["qkv"], inp["q_norm_w"], inp["k_norm_w"], inp["cos"], inp["sin"], 4, 2, 64)
+    qkv = inp["qkv"].float()
+    q = qkv[:, :256].reshape(20, 4, 64)
+    k = qkv[:, 256:384].reshape(20, 2, 64)
+    v = qkv[:, 384:].reshape(20, 2, 64)
+    qn = ref.qwen_rmsnorm(q, inp["q_norm_w"].float())
+    kn = ref.qwen_rmsnorm(k, inp["k_norm_w"].float())
+    c, s = inp["cos"].float()[:, None], inp["sin"].float()[:, None]
+    qr = qn * c + ref.rotate_half(qn) * s
+    kr = kn * c + ref.rotate_half(kn) * s
+    o64 = brute_attention(qr.transpose(0, 1)[None], ref.repeat_kv(kr.transpose(0, 1)[None], 2),
+                          ref.repeat_kv(v.transpose(0, 1)[None], 2), causal=True)
+    o64 = o64[0].transpose(0, 1).reshape(20, 256)
+    assert (o.double() - o64).abs().max() < 0.05
+
+
+def test_signed_sin_and_rotated_weight_reproduce_rotate_half():
+    """prepare_signed_sin / prepare_norm_weight_rot (fused_llm_attention.py:787-804):
+    y*cos + y_rot*ssin with y_rot = w_rot * n[d +- D/2] equals y*cos + rotate_half(y)*sin."""
+    D = 8
+    n = torch.randn(D)
+    w = torch.randn(D)
+    cos, sin = torch.randn(D), torch.randn(D)
+    y = w * n
+    lhs = y * cos + ref.rotate_half(y) * sin
+    n_rot = torch.cat([n[D // 2:], n[: D // 2]])
+    rhs = y * cos + (W.norm_weight_rot(w) * n_rot) * W.signed_sin(sin)
+    assert torch.allclose(lhs, rhs)
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm and the MSAT step oracle
+# ---------------------------------------------------------------------------
+def test_layer_norm_closed_form():
+    x = torch.randn(4, 1536)
+    y = ref.layer_norm(x, 1e-6)
+    x64 = f64(x)
+    y64 = (x64 - x64.mean(-1, keepdim=True)) / torch.sqrt(x64.var(-1, unbiased=False, keepdim=True) + 1e-6)
+    assert (y.double() - y64).abs().max() < 1e-5
+
+
+@pytest.fixture(scope="module")
+def small_step():
+    from rldx_amd.msat_step import MsatStepCfg, make_inputs, make_weights
+
+    cfg = MsatStepCfg(blocks=2, hidden=256, heads=2, head_dim=128, ffn=512, n_vl=24, n_sa=8, n_p=8, n_p_pad=3,
+                      action_dim=8, steps=2)
+    return cfg, make_weights(cfg, "cpu"), make_inputs(cfg, "cpu")
+
+
+def test_step_oracle_ignores_padded_physics_tokens(small_step):
+    """Padded physics keys are masked in every block, so their content cannot reach
+    the actions: changing them leaves the output bit-identical."""
+    from oracle import msat_step_ref as R
+
+    cfg, w, inp = small_step
+    a = R.action_step(cfg, w, inp)
+    inp2 = dict(inp)
+    p = inp["p"].clone()
+    p[-cfg.n_p_pad:] = torch.randn(cfg.n_p_pad, cfg.hidden).to(torch.bfloat16) * 10
+    inp2["p"] = p
+    assert torch.equal(a, R.action_step(cfg, w, inp2))
+    p3 = inp["p"].clone()
+    p3[0] += 1
+    inp3 = dict(inp)
+    inp3["p"] = p3
+    assert not torch.equal(a, R.action_step(cfg, w, inp3))
+
+
+def test_step_oracle_cognition_permutation_invariance(small_step):
+    """Cognition tokens carry no rotary position, so permuting them leaves the
+    actions unchanged up to summation order."""
+    from oracle import msat_step_ref as R
+
+    cfg, w, inp = small_step
+    a = R.action_step(cfg, w, inp).float()
+    perm = torch.randperm(cfg.n_vl, generator=torch.Generator().manual_seed(0))
+    inp2 = dict(inp)
+    inp2["vl"] = inp["vl"][perm]
+    b = R.action_step(cfg, w, inp2).float()
+    assert (a - b).abs().max() < 0.05 * a.abs().max()
+
+
+def test_step_oracle_euler_schedule(small_step):
+    """With zero output weights and bias the velocity is 0 and x stays at x0;
+    with zero weights and bias c it moves by exactly steps * dt * c."""
+    from oracle import msat_step_ref as R
+
+    cfg, w, inp = small_step
+    w2 = dict(w)
+    w2["act_out.w"] = torch.zeros_like(w["act_out.w"])
+    w2["act_out.b"] = torch.zeros_like(w["act_out.b"])
+    assert torch.equal(R.action_step(cfg, w2, inp), inp["x0"])
+    w2["act_out.b"] = torch.full_like(w["act_out.b"], 0.5)
+    out = R.action_step(cfg, w2, inp)
+    expect = inp["x0"].float() + cfg.steps * (1.0 / cfg.steps) * 0.5
+    assert (out.float() - expect).abs().max() < 0.02
