@@ -63,6 +63,11 @@ hipError_t rldx_grouped_swiglu_bf16(const void* sa_x, const void* sa_bias, const
 /* QK-RMSNorm + rotate-half RoPE (Qwen3-VL convention)                       */
 /* ------------------------------------------------------------------------ */
 
+/* flags bit: `sin` is the pre-signed table of prepare_signed_sin
+ * (rldx/inference/backbone/llm/engine/kernels/fused_llm_attention.py:787-796),
+ * i.e. its first half already carries rotate_half's minus sign. */
+#define RLDX_ROPE_SIN_SIGNED 1
+
 /*
  * q' = apply_rotary_pos_emb(q_norm(q)), k' likewise, for q [B, S, Hq, D] and
  * k [B, S, Hk, D] with strides {batch, seq, head} (3 int64 each; D contiguous).
@@ -70,6 +75,8 @@ hipError_t rldx_grouped_swiglu_bf16(const void* sa_x, const void* sa_bias, const
  * broadcasts) built on the host.  head_dim 64 or 128.  eps as in the model.
  * fp32 variant: every step in fp32.  bf16 variant: eager bf16 rounding order
  * (bf16(x*rsqrt) -> bf16(w*.) -> bf16(y*cos), bf16(rot*sin) -> bf16(sum)).
+ * q_heads or k_heads may be 0 (then q/q_w/q_out, resp. k/k_w/k_out, may be NULL).
+ * flags: RLDX_ROPE_SIN_SIGNED or 0.
  *
  * Replaces: Qwen3VLTextRMSNorm.forward + apply_rotary_pos_emb
  *   (rldx/model/modules/backbone/modeling_qwen3_vl.py:356-371, :377-401),
@@ -80,14 +87,16 @@ hipError_t rldx_qk_rmsnorm_rope_half_f32(const float* q, const float* k, const f
                                          int64_t batch, int64_t seq, int64_t q_heads, int64_t k_heads,
                                          int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
                                          const int64_t* q_out_strides, const int64_t* k_out_strides,
-                                         const int64_t* cos_strides, float eps, hipStream_t stream);
+                                         const int64_t* cos_strides, float eps, int32_t flags,
+                                         hipStream_t stream);
 
 hipError_t rldx_qk_rmsnorm_rope_half_bf16(const void* q, const void* k, const void* q_w, const void* k_w,
                                           const void* cos, const void* sin, void* q_out, void* k_out,
                                           int64_t batch, int64_t seq, int64_t q_heads, int64_t k_heads,
                                           int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
                                           const int64_t* q_out_strides, const int64_t* k_out_strides,
-                                          const int64_t* cos_strides, float eps, hipStream_t stream);
+                                          const int64_t* cos_strides, float eps, int32_t flags,
+                                          hipStream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* MSAT multi-stream QKV gather + QK-RMSNorm + interleaved RoPE             */
@@ -112,6 +121,10 @@ typedef struct rldx_msat_stream {
  *   Q/K = to_bf16(w * (x * rsqrt(mean(x^2) + eps)))       (one rounding)
  *   then, on streams with tables, the interleaved complex rotation in fp32,
  *   rounded once; V is copied.
+ * If vt_out is non-NULL, V is written instead (v_out may be NULL) in the V^T
+ * layout rldx_attention_vt_fwd_bf16 reads: [H, D, >= round_up(M, 64)] with
+ * strides {vt_head_stride, vt_d_stride}, keys permuted inside each group of 16,
+ * padding keys zero — in the same launch.
  *
  * Replaces: rmsnorm_rope_kernel (ds) / rmsnorm_rope_kernel_3way
  *   (rldx/inference/action_model/double_stream/engine/kernels/rmsnorm_rope_ds.py:11-231,
@@ -122,12 +135,36 @@ typedef struct rldx_msat_stream {
  */
 hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* streams, int32_t num_streams, int64_t heads,
                                         int64_t head_dim, void* q_out, void* k_out, void* v_out,
-                                        int64_t out_head_stride, int64_t out_row_stride, float eps,
+                                        int64_t out_head_stride, int64_t out_row_stride, void* vt_out,
+                                        int64_t vt_head_stride, int64_t vt_d_stride, float eps,
                                         hipStream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Attention                                                                */
 /* ------------------------------------------------------------------------ */
+
+/*
+ * V^T layout used by the attention kernels: for each (batch, kv head), D rows of
+ * Skp >= round_up(Sk, 64) keys (strides {batch, head, d}, keys contiguous), the
+ * keys inside every group of 16 stored in the order
+ *   positions 0..7  -> keys 0, 1, 2, 3, 8, 9, 10, 11   of the group
+ *   positions 8..15 -> keys 4, 5, 6, 7, 12, 13, 14, 15 of the group
+ * and padding keys (>= Sk) holding zeros.  This is the row order of
+ * the P^T accumulator of v_mfma_f32_32x32x16_bf16, so every MFMA operand of the
+ * P.V product is one contiguous 16-byte load.
+ */
+
+/* Bytes of workspace rldx_attention_fwd_bf16 needs (its V^T copy). */
+int64_t rldx_attention_workspace_bytes(int64_t batch, int64_t kv_heads, int64_t seq_k, int64_t head_dim);
+
+/*
+ * V [B, Hkv, Sk, D] (strides {batch, head, seq}, D contiguous) -> V^T in the
+ * layout above (strides {batch, head, d}; d stride >= round_up(Sk, 64)).
+ * No reference counterpart: layout preparation for the attention kernels.
+ */
+hipError_t rldx_v_transpose_bf16(const void* v, const int64_t* v_strides, void* vt, const int64_t* vt_strides,
+                                 int64_t batch, int64_t kv_heads, int64_t seq_k, int64_t head_dim,
+                                 hipStream_t stream);
 
 /*
  * O = softmax(Q K^T * scale + key_bias[b, key] (+ causal)) V, bf16 in/out,
@@ -138,6 +175,9 @@ hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* streams, int32
  * [B, Sk] additive mask (0 / -inf for key padding), row stride
  * key_bias_batch_stride.  causal != 0: key j visible to query i iff j <= i
  * (top-left aligned, as SDPA's is_causal).  head_dim 64 or 128.
+ * Two launches: V -> V^T into `workspace` (>= rldx_attention_workspace_bytes,
+ * 16-byte aligned, caller-owned), then the attention kernel.  seq_k must be
+ * >= 1 when seq_q >= 1.
  *
  * Replaces: F.scaled_dot_product_attention inside ds::fused_attention_2way /
  *   _3way and ss::fused_attention_2way / _3way
@@ -151,8 +191,47 @@ hipError_t rldx_attention_fwd_bf16(const void* q, const void* k, const void* v, 
                                    int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k,
                                    int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
                                    const int64_t* v_strides, const int64_t* o_strides, const float* key_bias,
-                                   int64_t key_bias_batch_stride, float scale, int32_t causal,
-                                   hipStream_t stream);
+                                   int64_t key_bias_batch_stride, float scale, int32_t causal, void* workspace,
+                                   int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Same operator with V already in the V^T layout (vt_strides {batch, head, d}),
+ * one launch.  Used on the MSAT path, where rldx_msat_qkv_norm_rope_bf16 writes
+ * V^T directly.
+ */
+hipError_t rldx_attention_vt_fwd_bf16(const void* q, const void* k, const void* vt, void* o, int64_t batch,
+                                      int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k,
+                                      int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
+                                      const int64_t* vt_strides, const int64_t* o_strides, const float* key_bias,
+                                      int64_t key_bias_batch_stride, float scale, int32_t causal,
+                                      hipStream_t stream);
+
+/*
+ * The complete rldx_backbone::fused_attention operator: packed QKV
+ * (seq, >= (Hq + 2*Hkv)*D) bf16 -> out (seq, Hq*D) bf16 with q_norm/k_norm
+ * (Qwen3VLTextRMSNorm, eps) + rotate-half RoPE (cos / sin tables [seq, D] bf16,
+ * row stride cos_row_stride; sin pre-signed iff sin_is_signed) + causal GQA
+ * attention, scale 1/sqrt(D).  Three launches: K normalisation and V^T into
+ * `workspace` (>= rldx_llm_fused_attention_workspace_bytes(seq, Hkv, D) bytes,
+ * 16-byte aligned, caller-owned), then attention with the Q normalisation fused
+ * into its prologue.
+ *
+ * Replaces: fused_llm_attention.forward(qkv, q_norm_w, q_norm_w_rot, k_norm_w,
+ *   k_norm_w_rot, cos, signed_sin, num_heads, num_kv_heads, head_dim, out)
+ *   (rldx/inference/backbone/llm/engine/kernels/fused_llm_attention.py:1005-1057)
+ *   behind rldx_backbone::fused_attention (.../llm/engine/ops/op_fused_llm_attention.py:13-45).
+ *   The rotated norm weights of the reference are not needed: the kernel reads
+ *   the rotate-half partner directly.
+ */
+hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv_row_stride, const void* q_norm_w,
+                                         const void* k_norm_w, const void* cos, const void* sin,
+                                         int64_t cos_row_stride, int32_t sin_is_signed, void* out,
+                                         int64_t out_row_stride, int64_t seq, int64_t q_heads, int64_t kv_heads,
+                                         int64_t head_dim, float eps, void* workspace, int64_t workspace_bytes,
+                                         hipStream_t stream);
+
+/* Workspace bytes rldx_llm_fused_attention_bf16 needs (normalised K + V^T). */
+int64_t rldx_llm_fused_attention_workspace_bytes(int64_t seq, int64_t kv_heads, int64_t head_dim);
 
 /* ------------------------------------------------------------------------ */
 /* Host-side diagnostics (no reference counterpart)                         */

@@ -66,6 +66,7 @@ struct HalfArgs {
   int64_t ko_sb, ko_ss, ko_sh;
   int64_t c_sb, c_ss;          // cos/sin strides ([B or 1, S, D])
   float eps;
+  int sin_signed;              // sin table already carries the rotate_half sign
   int64_t total_rows;
 };
 
@@ -137,7 +138,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_half_kernel(HalfArgs a) {
 #pragma clang fp contract(off)
 #pragma unroll
     for (int i = 0; i < V; ++i) {
-      const float rot = first_half ? -part[i] : part[i];
+      const float rot = (first_half && !a.sin_signed) ? -part[i] : part[i];
       const float c = load_elem<T>(cs, d0 + i);
       const float sv = load_elem<T>(sn, d0 + i);
       if constexpr (sizeof(T) == 2) {
@@ -179,14 +180,66 @@ struct MsatArgs {
   uint16_t* v_out;
   int64_t o_sh, o_sm;  // output strides (head, row) in elements, shared by q/k/v
   float eps;
-  int64_t total_items;  // 3 * H * M rows of D
+  int64_t total_items;  // rows of D handled by the norm/copy role: 3*H*M, or 2*H*M with vt_out
+  // optional V^T output [H, D, >= round_up(M, 64)] (keys permuted inside groups of 16,
+  // zero padded), written by workgroups [qk_blocks, qk_blocks + H * v_blocks)
+  uint16_t* vt_out;
+  int64_t vt_sh, vt_sd;
+  int64_t qk_blocks;
+  int64_t v_blocks;  // 32-token blocks per head
 };
+
+// Position -> key inside one group of 16 keys of a V^T row (the P^T accumulator order
+// of the attention kernel: lane half g holds keys {4g..4g+3, 8+4g..8+4g+3}).
+__device__ __forceinline__ int vt_key_of_pos(int p) {
+  const int gp = (p & 15) >> 3, ip = p & 7;
+  return (p & ~15) + (ip < 4 ? 4 * gp + ip : 8 + 4 * gp + (ip - 4));
+}
+
+template <int D>
+__device__ void msat_v_transpose_block(const MsatArgs& a, int64_t vb) {
+  constexpr int PITCH = D + 8;
+  constexpr int CH = D / 8;
+  __shared__ __attribute__((aligned(16))) uint16_t tile[32 * PITCH];
+  const int64_t h = vb / a.v_blocks;
+  const int64_t k0 = (vb - h * a.v_blocks) * 32;
+  const int64_t inner = a.heads * D;
+  for (int c = threadIdx.x; c < 32 * CH; c += 256) {
+    const int r = c / CH, col = (c % CH) * 8;
+    const int64_t m = k0 + r;
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (m < a.m_total) {
+      int si = 0;
+      if (a.num_streams > 1 && m >= a.s[1].m_begin) si = 1;
+      if (a.num_streams > 2 && m >= a.s[2].m_begin) si = 2;
+      const MsatStream& S = a.s[si];
+      val = *reinterpret_cast<const uint4*>(S.qkv + (m - S.m_begin) * S.ld + 2 * inner + h * D + col);
+    }
+    *reinterpret_cast<uint4*>(&tile[r * PITCH + col]) = val;
+  }
+  __syncthreads();
+  uint16_t* dst = a.vt_out + h * a.vt_sh + k0;
+  for (int c = threadIdx.x; c < D * 4; c += 256) {
+    const int d = c >> 2, q = c & 3;
+    uint4 out;
+    uint32_t* ow = reinterpret_cast<uint32_t*>(&out);
+#pragma unroll
+    for (int i = 0; i < 8; i += 2)
+      ow[i >> 1] = static_cast<uint32_t>(tile[vt_key_of_pos(q * 8 + i) * PITCH + d]) |
+                   (static_cast<uint32_t>(tile[vt_key_of_pos(q * 8 + i + 1) * PITCH + d]) << 16);
+    *reinterpret_cast<uint4*>(dst + static_cast<int64_t>(d) * a.vt_sd + q * 8) = out;
+  }
+}
 
 template <int D>
 __global__ __launch_bounds__(256) void msat_qkv_norm_rope_kernel(MsatArgs a) {
   constexpr int V = 8;
   constexpr int LPR = D / V;
   static_assert(LPR >= 2 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "unsupported head_dim");
+  if (a.vt_out != nullptr && static_cast<int64_t>(blockIdx.x) >= a.qk_blocks) {
+    msat_v_transpose_block<D>(a, static_cast<int64_t>(blockIdx.x) - a.qk_blocks);
+    return;
+  }
   const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int lane_in_row = static_cast<int>(tid % LPR);
   const int64_t item = tid / LPR;
@@ -275,7 +328,7 @@ hipError_t half_entry(const void* q, const void* k, const void* q_w, const void*
                       const void* sin, void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t hq,
                       int64_t hk, int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
                       const int64_t* qo_strides, const int64_t* ko_strides, const int64_t* cs_strides, float eps,
-                      hipStream_t stream) {
+                      int32_t flags, hipStream_t stream) {
   if (head_dim != 64 && head_dim != 128) return hipErrorInvalidValue;
   if (batch < 0 || seq < 0 || hq < 0 || hk < 0) return hipErrorInvalidValue;
   if (!q_strides || !k_strides || !qo_strides || !ko_strides || !cs_strides) return hipErrorInvalidValue;
@@ -295,7 +348,8 @@ hipError_t half_entry(const void* q, const void* k, const void* q_w, const void*
   HalfArgs a{q, k, q_w, k_w, cos, sin, q_out, k_out, batch, seq, hq, hk,
              q_strides[0], q_strides[1], q_strides[2], k_strides[0], k_strides[1], k_strides[2],
              qo_strides[0], qo_strides[1], qo_strides[2], ko_strides[0], ko_strides[1], ko_strides[2],
-             cs_strides[0], cs_strides[1], eps, batch * seq * (hq + hk)};
+             cs_strides[0], cs_strides[1], eps, (flags & RLDX_ROPE_SIN_SIGNED) ? 1 : 0,
+             batch * seq * (hq + hk)};
   return launch_half<T>(a, head_dim, stream);
 }
 
@@ -308,29 +362,31 @@ extern "C" hipError_t rldx_qk_rmsnorm_rope_half_f32(
     const float* q, const float* k, const float* q_w, const float* k_w, const float* cos, const float* sin,
     float* q_out, float* k_out, int64_t batch, int64_t seq, int64_t q_heads, int64_t k_heads, int64_t head_dim,
     const int64_t* q_strides, const int64_t* k_strides, const int64_t* q_out_strides,
-    const int64_t* k_out_strides, const int64_t* cos_strides, float eps, hipStream_t stream) {
+    const int64_t* k_out_strides, const int64_t* cos_strides, float eps, int32_t flags, hipStream_t stream) {
   return half_entry<float>(q, k, q_w, k_w, cos, sin, q_out, k_out, batch, seq, q_heads, k_heads, head_dim,
-                           q_strides, k_strides, q_out_strides, k_out_strides, cos_strides, eps, stream);
+                           q_strides, k_strides, q_out_strides, k_out_strides, cos_strides, eps, flags, stream);
 }
 
 extern "C" hipError_t rldx_qk_rmsnorm_rope_half_bf16(
     const void* q, const void* k, const void* q_w, const void* k_w, const void* cos, const void* sin,
     void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t q_heads, int64_t k_heads, int64_t head_dim,
     const int64_t* q_strides, const int64_t* k_strides, const int64_t* q_out_strides,
-    const int64_t* k_out_strides, const int64_t* cos_strides, float eps, hipStream_t stream) {
+    const int64_t* k_out_strides, const int64_t* cos_strides, float eps, int32_t flags, hipStream_t stream) {
   return half_entry<uint16_t>(q, k, q_w, k_w, cos, sin, q_out, k_out, batch, seq, q_heads, k_heads, head_dim,
-                              q_strides, k_strides, q_out_strides, k_out_strides, cos_strides, eps, stream);
+                              q_strides, k_strides, q_out_strides, k_out_strides, cos_strides, eps, flags, stream);
 }
 
 extern "C" hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* streams, int32_t num_streams,
                                                    int64_t heads, int64_t head_dim, void* q_out, void* k_out,
                                                    void* v_out, int64_t out_head_stride, int64_t out_row_stride,
+                                                   void* vt_out, int64_t vt_head_stride, int64_t vt_d_stride,
                                                    float eps, hipStream_t stream) {
   if (streams == nullptr || num_streams < 1 || num_streams > 3) return hipErrorInvalidValue;
   if (head_dim != 64 && head_dim != 128) return hipErrorInvalidValue;
-  if (heads <= 0 || !q_out || !k_out || !v_out) return hipErrorInvalidValue;
-  if (!al16(q_out) || !al16(k_out) || !al16(v_out) || out_head_stride % 8 || out_row_stride % 8)
-    return hipErrorInvalidValue;
+  if (heads <= 0 || !q_out || !k_out || (!v_out && !vt_out)) return hipErrorInvalidValue;
+  if (!al16(q_out) || !al16(k_out) || out_head_stride % 8 || out_row_stride % 8) return hipErrorInvalidValue;
+  if (v_out && !al16(v_out)) return hipErrorInvalidValue;
+  if (vt_out && (!al16(vt_out) || vt_head_stride % 8 || vt_d_stride % 8)) return hipErrorInvalidValue;
   MsatArgs a{};
   int64_t m = 0;
   int k = 0;
@@ -360,9 +416,15 @@ extern "C" hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* str
   a.o_sh = out_head_stride;
   a.o_sm = out_row_stride;
   a.eps = eps;
-  a.total_items = 3 * heads * m;
+  a.total_items = (vt_out ? 2 : 3) * heads * m;
   const int64_t threads = a.total_items * (head_dim / 8);
-  const int grid = static_cast<int>((threads + 255) / 256);
+  a.qk_blocks = (threads + 255) / 256;
+  a.vt_out = static_cast<uint16_t*>(vt_out);
+  a.vt_sh = vt_head_stride;
+  a.vt_sd = vt_d_stride;
+  a.v_blocks = (m + 63) / 64 * 2;  // V^T keys padded (with zeros) to a multiple of 64
+  if (vt_out && (vt_d_stride < a.v_blocks * 32 || vt_head_stride < head_dim * vt_d_stride)) return hipErrorInvalidValue;
+  const int grid = static_cast<int>(a.qk_blocks + (vt_out ? heads * a.v_blocks : 0));
   if (head_dim == 64)
     hipLaunchKernelGGL(msat_qkv_norm_rope_kernel<64>, dim3(grid), dim3(256), 0, stream, a);
   else

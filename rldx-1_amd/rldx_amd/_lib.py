@@ -40,22 +40,37 @@ SIGNATURES = {
     "rldx_grouped_swiglu_bf16": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp]),
     "rldx_qk_rmsnorm_rope_half_f32": (
         c_i32,
-        [c_vp] * 8 + [c_i64] * 5 + [c_i64p] * 5 + [c_f32, c_vp],
+        [c_vp] * 8 + [c_i64] * 5 + [c_i64p] * 5 + [c_f32, c_i32, c_vp],
     ),
     "rldx_qk_rmsnorm_rope_half_bf16": (
         c_i32,
-        [c_vp] * 8 + [c_i64] * 5 + [c_i64p] * 5 + [c_f32, c_vp],
+        [c_vp] * 8 + [c_i64] * 5 + [c_i64p] * 5 + [c_f32, c_i32, c_vp],
     ),
     "rldx_msat_qkv_norm_rope_bf16": (
         c_i32,
-        [ctypes.POINTER(MsatStream), c_i32, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, c_f32, c_vp],
+        [ctypes.POINTER(MsatStream), c_i32, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_f32,
+         c_vp],
     ),
+    "rldx_attention_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64]),
+    "rldx_v_transpose_bf16": (c_i32, [c_vp, c_i64p, c_vp, c_i64p, c_i64, c_i64, c_i64, c_i64, c_vp]),
     "rldx_attention_fwd_bf16": (
+        c_i32,
+        [c_vp] * 4 + [c_i64] * 6 + [c_i64p] * 4 + [c_vp, c_i64, c_f32, c_i32, c_vp, c_i64, c_vp],
+    ),
+    "rldx_attention_vt_fwd_bf16": (
         c_i32,
         [c_vp] * 4 + [c_i64] * 6 + [c_i64p] * 4 + [c_vp, c_i64, c_f32, c_i32, c_vp],
     ),
+    "rldx_llm_fused_attention_bf16": (
+        c_i32,
+        [c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_f32, c_vp,
+         c_i64, c_vp],
+    ),
+    "rldx_llm_fused_attention_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64]),
     "rldx_host_swiglu_bf16": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64]),
 }
+
+ROPE_SIN_SIGNED = 1  # RLDX_ROPE_SIN_SIGNED
 
 _lib = None
 _hip = None

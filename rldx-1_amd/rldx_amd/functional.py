@@ -155,18 +155,10 @@ def qk_rmsnorm_rope_half(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tenso
         return q_out, k_out
     lib = _lib.load()
     fn = lib.rldx_qk_rmsnorm_rope_half_f32 if dt == F32 else lib.rldx_qk_rmsnorm_rope_half_bf16
-    sin_arg = sin
-    if sin_is_signed:
-        # Undo the pre-applied rotate_half sign (negation is exact in any float format).
-        half = D // 2
-        sign = torch.ones(D, dtype=dt, device=sin.device)
-        sign[:half] = -1
-        sin_arg = (sin * sign).contiguous()
-        css = _lib.i64_array([cb if sin_arg.shape[0] == B and B > 1 else 0, sin_arg.stride(1)])
-        _require(sin_arg.stride() == cos.stride(), "cos must be contiguous when sin_is_signed")
+    flags = _lib.ROPE_SIN_SIGNED if sin_is_signed else 0
     _lib.check(fn(q.data_ptr(), k.data_ptr(), q_weight.data_ptr(), k_weight.data_ptr(), cos.data_ptr(),
-                  sin_arg.data_ptr(), q_out.data_ptr(), k_out.data_ptr(), B, S, Hq, Hk, D, qs, ks, qos, kos, css,
-                  float(eps), _stream_ptr(q)), "rldx_qk_rmsnorm_rope_half")
+                  sin.data_ptr(), q_out.data_ptr(), k_out.data_ptr(), B, S, Hq, Hk, D, qs, ks, qos, kos, css,
+                  float(eps), flags, _stream_ptr(q)), "rldx_qk_rmsnorm_rope_half")
     return q_out, k_out
 
 
@@ -184,9 +176,12 @@ class StreamSpec:
 
 
 def msat_qkv_norm_rope(streams: Sequence[StreamSpec], num_heads: int, head_dim: int, eps: float = 1e-6,
-                       out: Optional[tuple] = None):
+                       out: Optional[tuple] = None, v_transposed: bool = False):
     """Gather Q/K/V of 1-3 streams into (H, M, D) bf16 with per-stream QK RMSNorm
     (one rounding) and interleaved RoPE on the streams that carry tables.
+
+    With `v_transposed`, the third output is V^T (H, D, round_up(M, 64)) in the
+    layout `attention_vt` reads (keys permuted inside groups of 16, zero padded).
 
     rmsnorm_rope_ds.py:11-231 / rmsnorm_rope_ds_3way.py:22-386 fused layout,
     eager semantics of norms.py:18-22 and action_model/ops.py:48-67."""
@@ -218,20 +213,31 @@ def msat_qkv_norm_rope(streams: Sequence[StreamSpec], num_heads: int, head_dim: 
         descs[i] = _lib.MsatStream(s.qkv.data_ptr(), s.qkv.stride(0), n, s.q_w.data_ptr(), s.k_w.data_ptr(),
                                    cos_p, sin_p, rope_ld)
         M += n
+    Mp = (M + 63) // 64 * 64
     if out is None:
         q = torch.empty((num_heads, M, head_dim), dtype=BF16, device=dev)
         k = torch.empty_like(q)
-        v = torch.empty_like(q)
+        v = torch.empty((num_heads, head_dim, Mp), dtype=BF16, device=dev) if v_transposed else torch.empty_like(q)
     else:
         q, k, v = out
-        _require(all(t.shape == (num_heads, M, head_dim) and t.stride() == q.stride() for t in (q, k, v)),
-                 "out tensors must be (H, M, D) with equal strides")
+        _require(q.shape == (num_heads, M, head_dim) and k.shape == q.shape and k.stride() == q.stride(),
+                 "q/k out tensors must be (H, M, D) with equal strides")
+        if v_transposed:
+            _require(v.shape[:2] == (num_heads, head_dim) and v.shape[2] >= Mp and v.stride(2) == 1,
+                     "vt out must be (H, D, >= round_up(M, 64)) with contiguous keys")
+        else:
+            _require(v.shape == q.shape and v.stride() == q.stride(), "v out must match q")
     if M == 0:
         return q, k, v
     lib = _lib.load()
+    if v_transposed:
+        args = (None, 0, 0, v.data_ptr(), v.stride(0), v.stride(1))
+    else:
+        args = (v.data_ptr(), q.stride(0), q.stride(1), None, 0, 0)
     _lib.check(lib.rldx_msat_qkv_norm_rope_bf16(descs, len(streams), num_heads, head_dim, q.data_ptr(), k.data_ptr(),
-                                                v.data_ptr(), q.stride(0), q.stride(1), float(eps),
-                                                _stream_ptr(q)), "rldx_msat_qkv_norm_rope_bf16")
+                                                args[0], q.stride(0) if v_transposed else args[1],
+                                                q.stride(1) if v_transposed else args[2], args[3], args[4], args[5],
+                                                float(eps), _stream_ptr(q)), "rldx_msat_qkv_norm_rope_bf16")
     return q, k, v
 
 
@@ -246,15 +252,19 @@ def _bhs_strides(t: torch.Tensor, layout: str):
     raise ValueError(f"unknown layout {layout}")
 
 
-def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, key_bias: Optional[torch.Tensor] = None,
-              causal: bool = False, scale: Optional[float] = None, layout: str = "bhsd",
-              out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """softmax(Q K^T * scale + key_bias (+ causal)) V with GQA, bf16.
+def _key_bias_args(key_bias: Optional[torch.Tensor], B: int, Sk: int):
+    if key_bias is None:
+        return None, 0
+    _require(key_bias.dtype == F32 and key_bias.stride(-1) == 1, "key_bias must be fp32 with contiguous keys")
+    if key_bias.dim() == 1:
+        _require(key_bias.shape[0] == Sk, "key_bias must have seq_k entries")
+        return key_bias.data_ptr(), 0
+    _require(key_bias.dim() == 2 and key_bias.shape[1] == Sk and key_bias.shape[0] in (1, B), "key_bias must be [B, Sk]")
+    return key_bias.data_ptr(), (key_bias.stride(0) if key_bias.shape[0] == B and B > 1 else 0)
 
-    layout "bhsd": tensors [B, H, S, D]; "bshd": [B, S, H, D].  key_bias: fp32
-    [B, Sk] or [Sk] additive (0 / -inf).  scale defaults to 1/sqrt(D)."""
-    _on_gpu(q, k, v, key_bias, out)
-    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+
+def _attn_dims(q, k, layout):
+    for t, n in ((q, "q"), (k, "k")):
         _require(t.dtype == BF16 and t.dim() == 4 and t.stride(-1) == 1, f"{n} must be 4-D bf16, last dim contiguous")
     if layout == "bhsd":
         B, Hq, Sq, D = q.shape
@@ -263,67 +273,110 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, key_bias: Op
         B, Sq, Hq, D = q.shape
         _, Sk, Hkv, _ = k.shape
     _require(D in (64, 128), "head_dim must be 64 or 128")
-    _require(k.shape == v.shape, "k and v must have the same shape")
     _require(k.shape[0] == B and k.shape[3] == D, "k batch/head_dim must match q")
     _require(Hkv > 0 and Hq % Hkv == 0, "q heads must be a multiple of kv heads")
+    return B, Hq, Hkv, Sq, Sk, D
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, key_bias: Optional[torch.Tensor] = None,
+              causal: bool = False, scale: Optional[float] = None, layout: str = "bhsd",
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """softmax(Q K^T * scale + key_bias (+ causal)) V with GQA, bf16.
+
+    layout "bhsd": tensors [B, H, S, D]; "bshd": [B, S, H, D].  key_bias: fp32
+    [B, Sk] or [Sk] additive (0 / -inf).  scale defaults to 1/sqrt(D)."""
+    _on_gpu(q, k, v, key_bias, out)
+    B, Hq, Hkv, Sq, Sk, D = _attn_dims(q, k, layout)
+    _require(v.dtype == BF16 and k.shape == v.shape and v.stride(-1) == 1, "v must match k")
     if out is None:
         out = torch.empty_like(q, memory_format=torch.contiguous_format)
     _require(out.shape == q.shape and out.dtype == BF16 and out.stride(-1) == 1, "out must match q")
-    kb_ptr, kb_stride = None, 0
-    if key_bias is not None:
-        _require(key_bias.dtype == F32 and key_bias.stride(-1) == 1, "key_bias must be fp32 with contiguous keys")
-        if key_bias.dim() == 1:
-            _require(key_bias.shape[0] == Sk, "key_bias must have seq_k entries")
-            kb_stride = 0
-        else:
-            _require(key_bias.dim() == 2 and key_bias.shape[1] == Sk and key_bias.shape[0] in (1, B),
-                     "key_bias must be [B, Sk]")
-            kb_stride = key_bias.stride(0) if key_bias.shape[0] == B and B > 1 else 0
-        kb_ptr = key_bias.data_ptr()
+    kb_ptr, kb_stride = _key_bias_args(key_bias, B, Sk)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    qs = _lib.i64_array(_bhs_strides(q, layout))
-    ks = _lib.i64_array(_bhs_strides(k, layout))
-    vs = _lib.i64_array(_bhs_strides(v, layout))
-    os_ = _lib.i64_array(_bhs_strides(out, layout))
     lib = _lib.load()
+    ws_bytes = int(lib.rldx_attention_workspace_bytes(B, Hkv, Sk, D))
+    ws = torch.empty(max(ws_bytes // 2, 8), dtype=BF16, device=q.device)
     _lib.check(lib.rldx_attention_fwd_bf16(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, Hq, Hkv, Sq, Sk,
-                                           D, qs, ks, vs, os_, kb_ptr, kb_stride, float(scale), int(bool(causal)),
-                                           _stream_ptr(q)), "rldx_attention_fwd_bf16")
+                                           D, _lib.i64_array(_bhs_strides(q, layout)),
+                                           _lib.i64_array(_bhs_strides(k, layout)),
+                                           _lib.i64_array(_bhs_strides(v, layout)),
+                                           _lib.i64_array(_bhs_strides(out, layout)), kb_ptr, kb_stride, float(scale),
+                                           int(bool(causal)), ws.data_ptr(), ws.numel() * 2, _stream_ptr(q)),
+               "rldx_attention_fwd_bf16")
     return out
 
 
-def attention_raw(q_ptr_tensor: torch.Tensor, k_base: torch.Tensor, v_base: torch.Tensor, o_base: torch.Tensor, *,
-                  batch: int, q_heads: int, kv_heads: int, seq_q: int, seq_k: int, head_dim: int,
-                  q_strides, k_strides, v_strides, o_strides, key_bias: Optional[torch.Tensor] = None,
-                  key_bias_batch_stride: int = 0, scale: Optional[float] = None, causal: bool = False,
-                  q_offset: int = 0, k_offset: int = 0, v_offset: int = 0, o_offset: int = 0) -> None:
-    """Strided attention over views into packed buffers (element offsets/strides).
-
-    Used by the packed-QKV operators, where Q, K and V are column slices of one
-    row-major buffer.  Bounds are checked against each base tensor's storage."""
-    _on_gpu(q_ptr_tensor, k_base, v_base, o_base, key_bias)
-    for t in (q_ptr_tensor, k_base, v_base, o_base):
-        _require(t.dtype == BF16, "attention_raw expects bf16 buffers")
-
-    def _extent(off, strides, nb, nh, ns):
-        return off + (nb - 1) * strides[0] + (nh - 1) * strides[1] + (ns - 1) * strides[2] + head_dim
-
-    _require(_extent(q_offset, q_strides, batch, q_heads, seq_q) <= q_ptr_tensor.numel(), "q view out of bounds")
-    _require(_extent(k_offset, k_strides, batch, kv_heads, seq_k) <= k_base.numel(), "k view out of bounds")
-    _require(_extent(v_offset, v_strides, batch, kv_heads, seq_k) <= v_base.numel(), "v view out of bounds")
-    _require(_extent(o_offset, o_strides, batch, q_heads, seq_q) <= o_base.numel(), "o view out of bounds")
-    if scale is None:
-        scale = 1.0 / math.sqrt(head_dim)
-    esz = 2
+def v_transpose(v: torch.Tensor, layout: str = "bhsd") -> torch.Tensor:
+    """V [B, H, S, D] (or [B, S, H, D]) -> V^T [B, H, D, round_up(S, 64)] in the
+    permuted-key layout the attention kernels read (padding keys zero)."""
+    _on_gpu(v)
+    _require(v.dtype == BF16 and v.dim() == 4 and v.stride(-1) == 1, "v must be 4-D bf16, last dim contiguous")
+    if layout == "bhsd":
+        B, H, S, D = v.shape
+    else:
+        B, S, H, D = v.shape
+    Sp = (S + 63) // 64 * 64
+    vt = torch.empty((B, H, D, Sp), dtype=BF16, device=v.device)
     lib = _lib.load()
-    _lib.check(lib.rldx_attention_fwd_bf16(q_ptr_tensor.data_ptr() + q_offset * esz, k_base.data_ptr() + k_offset * esz,
-                                           v_base.data_ptr() + v_offset * esz, o_base.data_ptr() + o_offset * esz,
-                                           batch, q_heads, kv_heads, seq_q, seq_k, head_dim,
-                                           _lib.i64_array(q_strides), _lib.i64_array(k_strides),
-                                           _lib.i64_array(v_strides), _lib.i64_array(o_strides),
-                                           _ptr(key_bias), key_bias_batch_stride, float(scale), int(bool(causal)),
-                                           _stream_ptr(o_base)), "rldx_attention_fwd_bf16")
+    _lib.check(lib.rldx_v_transpose_bf16(v.data_ptr(), _lib.i64_array(_bhs_strides(v, layout)), vt.data_ptr(),
+                                         _lib.i64_array([vt.stride(0), vt.stride(1), vt.stride(2)]), B, H, S, D,
+                                         _stream_ptr(v)), "rldx_v_transpose_bf16")
+    return vt
+
+
+def attention_vt(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, *, key_bias: Optional[torch.Tensor] = None,
+                 causal: bool = False, scale: Optional[float] = None, layout: str = "bhsd",
+                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Attention with V given as V^T [B, Hkv, D, >= round_up(Sk, 64)] (see v_transpose)."""
+    _on_gpu(q, k, vt, key_bias, out)
+    B, Hq, Hkv, Sq, Sk, D = _attn_dims(q, k, layout)
+    _require(vt.dtype == BF16 and vt.dim() == 4 and vt.shape[:3] == (B, Hkv, D) and vt.stride(-1) == 1 and
+             vt.shape[3] >= (Sk + 63) // 64 * 64, "vt must be [B, Hkv, D, >= round_up(Sk, 64)]")
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    _require(out.shape == q.shape and out.dtype == BF16 and out.stride(-1) == 1, "out must match q")
+    kb_ptr, kb_stride = _key_bias_args(key_bias, B, Sk)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    lib = _lib.load()
+    _lib.check(lib.rldx_attention_vt_fwd_bf16(q.data_ptr(), k.data_ptr(), vt.data_ptr(), out.data_ptr(), B, Hq, Hkv, Sq,
+                                              Sk, D, _lib.i64_array(_bhs_strides(q, layout)),
+                                              _lib.i64_array(_bhs_strides(k, layout)),
+                                              _lib.i64_array([vt.stride(0), vt.stride(1), vt.stride(2)]),
+                                              _lib.i64_array(_bhs_strides(out, layout)), kb_ptr, kb_stride,
+                                              float(scale), int(bool(causal)), _stream_ptr(q)),
+               "rldx_attention_vt_fwd_bf16")
+    return out
+
+
+def llm_fused_attention(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor, cos: torch.Tensor,
+                        sin: torch.Tensor, num_heads: int, num_kv_heads: int, head_dim: int, *,
+                        sin_is_signed: bool = True, eps: float = 1e-6,
+                        out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Packed QKV (M, (Hq + 2*Hkv)*D) -> (M, Hq*D): q_norm/k_norm + rotate-half RoPE +
+    causal GQA attention (rldx_backbone::fused_attention semantics)."""
+    _on_gpu(qkv, q_norm_w, k_norm_w, cos, sin, out)
+    M = qkv.shape[0]
+    Hq, Hkv, D = num_heads, num_kv_heads, head_dim
+    _require(qkv.dtype == BF16 and qkv.dim() == 2 and qkv.stride(1) == 1, "qkv must be 2-D bf16 rows")
+    _require(qkv.shape[1] >= (Hq + 2 * Hkv) * D, f"qkv rows must hold (Hq + 2*Hkv)*D = {(Hq + 2 * Hkv) * D} columns")
+    for t, n in ((q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w")):
+        _require(t.dtype == BF16 and t.is_contiguous() and t.numel() == D, f"{n} must be contiguous bf16 [D]")
+    _require(cos.dtype == BF16 and sin.dtype == BF16 and cos.shape == (M, D) and sin.shape == (M, D),
+             "cos / sin must be bf16 [M, D]")
+    _require(cos.stride(1) == 1 and sin.stride() == cos.stride(), "cos / sin must share a row-major layout")
+    if out is None:
+        out = torch.empty((M, Hq * D), dtype=BF16, device=qkv.device)
+    _require(out.dtype == BF16 and out.shape == (M, Hq * D) and out.stride(1) == 1, "out must be bf16 (M, Hq*D)")
+    lib = _lib.load()
+    ws_bytes = int(lib.rldx_llm_fused_attention_workspace_bytes(M, Hkv, D))
+    ws = torch.empty(max(ws_bytes // 2, 8), dtype=BF16, device=qkv.device)
+    _lib.check(lib.rldx_llm_fused_attention_bf16(qkv.data_ptr(), qkv.stride(0), q_norm_w.data_ptr(), k_norm_w.data_ptr(),
+                                                 cos.data_ptr(), sin.data_ptr(), cos.stride(0), int(bool(sin_is_signed)),
+                                                 out.data_ptr(), out.stride(0), M, Hq, Hkv, D, float(eps), ws.data_ptr(),
+                                                 ws.numel() * 2, _stream_ptr(qkv)), "rldx_llm_fused_attention_bf16")
+    return out
 
 
 def mask_to_key_bias(kv_mask: torch.Tensor) -> torch.Tensor:

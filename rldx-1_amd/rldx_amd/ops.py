@@ -30,11 +30,11 @@ from . import functional as Fn
 # ---------------------------------------------------------------------------
 
 
-def _attn_from_qkv(q, k, v, key_bias, M, H, D):
-    """(H, M, D) Q/K/V -> (1, M, H*D) bf16, written directly in token-major order."""
+def _attn_from_qkv(q, k, vt, key_bias, M, H, D):
+    """(H, M, D) Q/K + V^T (H, D, Mp) -> (1, M, H*D) bf16, written directly in token-major order."""
     out = torch.empty((1, M, H, D), dtype=torch.bfloat16, device=q.device)
-    Fn.attention(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0), key_bias=key_bias, layout="bhsd",
-                 out=out.permute(0, 2, 1, 3))
+    Fn.attention_vt(q.unsqueeze(0), k.unsqueeze(0), vt.unsqueeze(0), key_bias=key_bias, layout="bhsd",
+                    out=out.permute(0, 2, 1, 3))
     return out.view(1, M, H * D)
 
 
@@ -70,7 +70,7 @@ def ds_fused_attention_2way(
         Fn.StreamSpec(_qkv_cols(vl_qkv)[:n_vl], q_norm_vl_weight, k_norm_vl_weight),
         Fn.StreamSpec(_qkv_cols(sa_qkv)[:n_sa], q_norm_sa_weight, k_norm_sa_weight, rope_cos, rope_sin),
     ]
-    q, k, v = Fn.msat_qkv_norm_rope(streams, H, D)
+    q, k, v = Fn.msat_qkv_norm_rope(streams, H, D, v_transposed=True)
     return _attn_from_qkv(q, k, v, None, n_vl + n_sa, H, D)
 
 
@@ -112,7 +112,7 @@ def ds_fused_attention_3way(
         Fn.StreamSpec(_qkv_cols(sa_qkv)[:n_sa], q_norm_sa_weight, k_norm_sa_weight, sa_rope_cos, sa_rope_sin),
         Fn.StreamSpec(_qkv_cols(p_qkv)[:n_p], q_norm_p_weight, k_norm_p_weight, p_rope_cos, p_rope_sin),
     ]
-    q, k, v = Fn.msat_qkv_norm_rope(streams, H, D)
+    q, k, v = Fn.msat_qkv_norm_rope(streams, H, D, v_transposed=True)
     bias = Fn.mask_to_key_bias(kv_mask) if kv_mask is not None else None
     return _attn_from_qkv(q, k, v, bias, n_vl + n_sa + n_p, H, D)
 
@@ -174,7 +174,7 @@ def ss_fused_attention_2way(
         streams.append(Fn.StreamSpec(x[: M - n_sa], q_norm_weight, k_norm_weight))
     if n_sa > 0:
         streams.append(Fn.StreamSpec(x[M - n_sa:], q_norm_weight, k_norm_weight, rope_cos, rope_sin))
-    q, k, v = Fn.msat_qkv_norm_rope(streams, H, D)
+    q, k, v = Fn.msat_qkv_norm_rope(streams, H, D, v_transposed=True)
     return _attn_from_qkv(q, k, v, None, M, H, D)
 
 
@@ -215,7 +215,7 @@ def ss_fused_attention_3way(
         streams.append(Fn.StreamSpec(x[n_x - n_sa:], x_q_norm_weight, x_k_norm_weight, sa_rope_cos, sa_rope_sin))
     if n_p > 0:
         streams.append(Fn.StreamSpec(p, p_q_norm_weight, p_k_norm_weight, p_rope_cos, p_rope_sin))
-    q, k, v = Fn.msat_qkv_norm_rope(streams, H, D)
+    q, k, v = Fn.msat_qkv_norm_rope(streams, H, D, v_transposed=True)
     bias = Fn.mask_to_key_bias(kv_mask) if kv_mask is not None else None
     return _attn_from_qkv(q, k, v, bias, n_x + n_p, H, D)
 
@@ -239,28 +239,10 @@ def llm_fused_attention(qkv, q_norm_w, q_norm_w_rot, k_norm_w, k_norm_w_rot, cos
     Same Python signature as fused_llm_attention.forward
     (rldx/inference/backbone/llm/engine/kernels/fused_llm_attention.py:1005-1057).
     `q_norm_w_rot` / `k_norm_w_rot` are accepted for signature compatibility;
-    the kernel reads the rotate-half partner directly, which gives the same
+    the kernels read the rotate-half partner directly, which gives the same
     values (w_rot[d] * x[d +- D/2] == w[d +- D/2] * x[d +- D/2])."""
-    M = qkv.shape[0]
-    Hq, Hkv, D = num_heads, num_kv_heads, head_dim
-    qkv_dim = (Hq + 2 * Hkv) * D
-    if qkv.dim() != 2 or qkv.shape[1] != qkv_dim or qkv.stride(1) != 1:
-        raise RuntimeError(f"rldx_amd: qkv must be (M, {qkv_dim}) with contiguous columns")
-    if out is None:
-        out = torch.empty((M, Hq * D), dtype=torch.bfloat16, device=qkv.device)
-    ld = qkv.stride(0)
-    # 1) QK-RMSNorm + RoPE into a (M, Hq + Hkv, D) workspace
-    ws = torch.empty((M, Hq + Hkv, D), dtype=torch.bfloat16, device=qkv.device)
-    q_view = qkv.as_strided((1, M, Hq, D), (0, ld, D, 1))
-    k_view = qkv.as_strided((1, M, Hkv, D), (0, ld, D, 1), qkv.storage_offset() + Hq * D)
-    Fn.qk_rmsnorm_rope_half(q_view, k_view, q_norm_w, k_norm_w, cos, signed_sin, 1e-6, sin_is_signed=True,
-                            q_out=ws[None, :, :Hq], k_out=ws[None, :, Hq:])
-    # 2) causal GQA attention; V read in place from the packed buffer
-    wsd = (Hq + Hkv) * D
-    Fn.attention_raw(ws, ws, qkv, out, batch=1, q_heads=Hq, kv_heads=Hkv, seq_q=M, seq_k=M, head_dim=D,
-                     q_strides=[0, D, wsd], k_strides=[0, D, wsd], v_strides=[0, D, ld], o_strides=[0, D, out.stride(0)],
-                     causal=True, k_offset=Hq * D, v_offset=(Hq + Hkv) * D)
-    return out
+    return Fn.llm_fused_attention(qkv, q_norm_w, k_norm_w, cos, signed_sin, num_heads, num_kv_heads, head_dim,
+                                  sin_is_signed=True, out=out)
 
 
 @torch.library.custom_op("rldx_backbone::fused_attention", mutates_args=())

@@ -132,6 +132,10 @@ def test_msat_qkv_norm_rope(dev, D, H, sizes):
     assert torch.equal(v.cpu(), rv)
     assert_bf16_close(q, rq, "q")
     assert_bf16_close(k, rk, "k")
+    # V^T output mode: same Q/K, V equal to the standalone transpose of V
+    q2, k2, vt = Fn.msat_qkv_norm_rope(specs, H, D, v_transposed=True)
+    assert torch.equal(q2, q) and torch.equal(k2, k)
+    assert torch.equal(vt, Fn.v_transpose(v.unsqueeze(0))[0])
 
 
 # ---------------------------------------------------------------------------
@@ -167,6 +171,9 @@ def test_gqa_prefill_workload(dev):
     (1, 2, 1, 1, 1, 128, True, False),
     (1, 2, 2, 200, 65, 128, False, True),
     (2, 7, 1, 64, 64, 64, True, False),
+    # grids of >= 512 workgroups take the single-key-group (128-query) variant
+    (4, 32, 8, 512, 512, 128, True, False),
+    (4, 32, 32, 520, 520, 64, False, True),
 ])
 def test_attention_shapes(dev, B, Hq, Hkv, Sq, Sk, D, causal, masked):
     g = torch.Generator().manual_seed(B * 100 + Sq + Sk + D)
@@ -181,6 +188,32 @@ def test_attention_shapes(dev, B, Hq, Hkv, Sq, Sk, D, causal, masked):
     o = Fn.attention(q.to(dev), k.to(dev), v.to(dev), key_bias=None if bias is None else bias.to(dev), causal=causal)
     r = ref.sdpa(q, ref.repeat_kv(k, Hq // Hkv), ref.repeat_kv(v, Hq // Hkv), key_bias=bias, causal=causal)
     assert_bf16_close(o, r, "attention")
+
+
+@pytest.mark.parametrize("S,D", [(608, 128), (77, 64), (1, 128), (1280, 128)])
+def test_v_transpose_layout(dev, S, D):
+    """V^T layout: row d holds keys in groups of 16 ordered {0-3, 8-11, 4-7, 12-15}, zero padded."""
+    g = torch.Generator().manual_seed(S)
+    v = torch.randn(2, 3, S, D, generator=g).to(torch.bfloat16)
+    vt = Fn.v_transpose(v.to(dev)).cpu()
+    Sp = (S + 63) // 64 * 64
+    perm = torch.tensor([0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15])
+    keys = (torch.arange(Sp) // 16) * 16 + perm[torch.arange(Sp) % 16]
+    vp = torch.zeros(2, 3, Sp, D, dtype=torch.bfloat16)
+    vp[:, :, :S] = v
+    assert torch.equal(vt, vp[:, :, keys].transpose(2, 3))
+
+
+def test_attention_vt_matches_attention(dev):
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(1, 12, 608, 128, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(1, 12, 608, 128, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(1, 12, 608, 128, generator=g).to(torch.bfloat16).to(dev)
+    bias = torch.zeros(608, device=dev)
+    bias[-8:] = float("-inf")
+    a = Fn.attention(q, k, v, key_bias=bias)
+    b = Fn.attention_vt(q, k, Fn.v_transpose(v), key_bias=bias)
+    assert torch.equal(a, b)
 
 
 # ---------------------------------------------------------------------------
@@ -199,6 +232,20 @@ def test_backbone_fused_attention_op(dev):
     r = ref.llm_fused_attention(inp["qkv"], inp["q_norm_w"], inp["k_norm_w"], inp["cos"], inp["sin"],
                                 cfg.q_heads, cfg.kv_heads, cfg.head_dim)
     assert o.shape == (cfg.seq, cfg.q_heads * cfg.head_dim)
+    assert_bf16_close(o, r, "rldx_backbone::fused_attention")
+
+
+@pytest.mark.parametrize("M,Hq,Hkv,D", [(100, 4, 2, 64), (333, 14, 2, 128)])
+def test_backbone_fused_attention_op_shapes(dev, M, Hq, Hkv, D):
+    import rldx_amd.ops  # noqa: F401
+
+    cfg = W.GqaCfg(q_heads=Hq, kv_heads=Hkv, head_dim=D, seq=M, seed=M)
+    inp = W.gqa_inputs(cfg)
+    args = (inp["qkv"], inp["q_norm_w"], W.norm_weight_rot(inp["q_norm_w"]), inp["k_norm_w"],
+            W.norm_weight_rot(inp["k_norm_w"]), inp["cos"], W.signed_sin(inp["sin"]))
+    o = torch.ops.rldx_backbone.fused_attention(*(t.to(dev) for t in args), num_heads=Hq, num_kv_heads=Hkv,
+                                                head_dim=D)
+    r = ref.llm_fused_attention(inp["qkv"], inp["q_norm_w"], inp["k_norm_w"], inp["cos"], inp["sin"], Hq, Hkv, D)
     assert_bf16_close(o, r, "rldx_backbone::fused_attention")
 
 
