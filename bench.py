@@ -124,15 +124,15 @@ def kernel_lines(torch, reps: int):
     q, k, v = (ji[n].to(dev) for n in ("q", "k", "v"))
     bias = torch.where(ji["kv_mask"] == 0, float("-inf"), 0.0).float().to(dev)
     o = torch.empty_like(q)
-    vt = Fn.v_transpose(v)  # V^T layout, as the MSAT QKV kernel produces it
-    ms = graph_time_ms(lambda: Fn.attention_vt(q, k, vt, key_bias=bias, out=o), reps, torch)
+    kvp = Fn.kv_pack(k, v)  # packed K/V tiles, as the MSAT QKV kernel produces them
+    ms = graph_time_ms(lambda: Fn.attention_packed(q, kvp, jc.tokens, key_bias=bias, out=o), reps, torch)
     tf = W.joint_attn_flops(jc) / (ms * 1e-3) / 1e12
     out["joint_attention_16x608x128"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s", bound="mfma",
                                               peak=BF16_MFMA_PEAK_TFLOPS, frac=tf / BF16_MFMA_PEAK_TFLOPS,
                                               flops=W.joint_attn_flops(jc))
     ms = graph_time_ms(lambda: Fn.attention(q, k, v, key_bias=bias, out=o), reps, torch)
     tf = W.joint_attn_flops(jc) / (ms * 1e-3) / 1e12
-    out["joint_attention_16x608x128_with_v_transpose"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s",
+    out["joint_attention_16x608x128_with_kv_pack"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s",
                                                                bound="mfma", peak=BF16_MFMA_PEAK_TFLOPS,
                                                                frac=tf / BF16_MFMA_PEAK_TFLOPS,
                                                                flops=W.joint_attn_flops(jc))
@@ -158,8 +158,8 @@ def kernel_lines(torch, reps: int):
     kn = torch.randn(1, M, Hkv, D, device=dev).to(torch.bfloat16)
     vn = torch.randn(1, M, Hkv, D, device=dev).to(torch.bfloat16)
     on = torch.empty_like(qn)
-    vtn = Fn.v_transpose(vn, layout="bshd")
-    ms = graph_time_ms(lambda: Fn.attention_vt(qn, kn, vtn, causal=True, layout="bshd", out=on), reps, torch)
+    kvpn = Fn.kv_pack(kn, vn, layout="bshd")
+    ms = graph_time_ms(lambda: Fn.attention_packed(qn, kvpn, M, causal=True, layout="bshd", out=on), reps, torch)
     tf = W.gqa_flops(gc) / (ms * 1e-3) / 1e12
     out["gqa_attention_28x4x1280x128"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s", bound="mfma",
                                               peak=BF16_MFMA_PEAK_TFLOPS, frac=tf / BF16_MFMA_PEAK_TFLOPS,
@@ -174,8 +174,8 @@ def kernel_lines(torch, reps: int):
     bs = torch.zeros(n, device=dev)
     bs[n - sc.n_p_pad:] = float("-inf")
     os_ = torch.empty_like(qs)
-    vts = Fn.v_transpose(vs)
-    ms = graph_time_ms(lambda: Fn.attention_vt(qs, ks, vts, key_bias=bs, out=os_), reps, torch)
+    kvps = Fn.kv_pack(ks, vs)
+    ms = graph_time_ms(lambda: Fn.attention_packed(qs, kvps, n, key_bias=bs, out=os_), reps, torch)
     fl = 4 * sc.heads * n * n * sc.head_dim
     tf = fl / (ms * 1e-3) / 1e12
     out["step_joint_attention_12x608x128"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s", bound="mfma",
@@ -258,7 +258,7 @@ def main():
     kl = kernel_lines(torch, args.kernel_reps)
     print("[bench] kernel lines done", file=sys.stderr, flush=True)
     dom = kl["step_joint_attention_12x608x128"]
-    roofline = dict(kernel="attn_fwd_kernel<128,false,true,false> (joint attention 12 heads x 608 x 128, masked)",
+    roofline = dict(kernel="attn_fwd_kernel<128,1,false,true,false> (joint attention 12 heads x 608 x 128, masked)",
                     bound="mfma", achieved=dom["achieved"], peak=dom["peak"], unit="TFLOP/s", frac=dom["frac"],
                     traffic=None)
 

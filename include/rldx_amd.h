@@ -121,10 +121,10 @@ typedef struct rldx_msat_stream {
  *   Q/K = to_bf16(w * (x * rsqrt(mean(x^2) + eps)))       (one rounding)
  *   then, on streams with tables, the interleaved complex rotation in fp32,
  *   rounded once; V is copied.
- * If vt_out is non-NULL, V is written instead (v_out may be NULL) in the V^T
- * layout rldx_attention_vt_fwd_bf16 reads: [H, D, >= round_up(M, 64)] with
- * strides {vt_head_stride, vt_d_stride}, keys permuted inside each group of 16,
- * padding keys zero — in the same launch.
+ * If kv_packed is non-NULL, K and V are written instead (k_out / v_out may be
+ * NULL) as the packed K/V tiles rldx_attention_packed_fwd_bf16 reads, head h at
+ * kv_packed + h * kv_packed_head_stride (elements, >=
+ * rldx_attention_kv_packed_elems(M, D)), padding keys zero — in the same launch.
  *
  * Replaces: rmsnorm_rope_kernel (ds) / rmsnorm_rope_kernel_3way
  *   (rldx/inference/action_model/double_stream/engine/kernels/rmsnorm_rope_ds.py:11-231,
@@ -135,36 +135,43 @@ typedef struct rldx_msat_stream {
  */
 hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* streams, int32_t num_streams, int64_t heads,
                                         int64_t head_dim, void* q_out, void* k_out, void* v_out,
-                                        int64_t out_head_stride, int64_t out_row_stride, void* vt_out,
-                                        int64_t vt_head_stride, int64_t vt_d_stride, float eps,
-                                        hipStream_t stream);
+                                        int64_t out_head_stride, int64_t out_row_stride, void* kv_packed,
+                                        int64_t kv_packed_head_stride, float eps, hipStream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Attention                                                                */
 /* ------------------------------------------------------------------------ */
 
 /*
- * V^T layout used by the attention kernels: for each (batch, kv head), D rows of
- * Skp >= round_up(Sk, 64) keys (strides {batch, head, d}, keys contiguous), the
- * keys inside every group of 16 stored in the order
- *   positions 0..7  -> keys 0, 1, 2, 3, 8, 9, 10, 11   of the group
- *   positions 8..15 -> keys 4, 5, 6, 7, 12, 13, 14, 15 of the group
- * and padding keys (>= Sk) holding zeros.  This is the row order of
- * the P^T accumulator of v_mfma_f32_32x32x16_bf16, so every MFMA operand of the
- * P.V product is one contiguous 16-byte load.
+ * Packed K/V tiles read by the attention kernels.  For each (batch, kv head),
+ * ceil(Sk / 32) tiles of 32 keys, 128*D bytes each, contiguous; inside tile t
+ * (element offsets, D = head_dim, lane l in 0..63, i in 0..7):
+ *   K part: (ks*64 + l)*8 + i            = K[32t + l%32][16 ks + 8 (l/32) + i],  ks < D/16
+ *   V part: 32 D + ((2 db + s2)*64 + l)*8 + i
+ *                                        = V[32t + 16 s2 + 8 (i/4) + 4 (l/32) + i%4][32 db + l%32],
+ *                                          db < D/32, s2 < 2
+ * Keys >= Sk hold zeros.  Each 1 KB chunk is one wave's MFMA operand for one
+ * v_mfma_f32_32x32x16_bf16 (K for S^T = K Q^T, V^T for O^T = V^T P^T, keys in
+ * the row order of the P^T accumulator), so the attention kernel loads every
+ * operand with one coalesced 16-byte load per lane.
  */
 
-/* Bytes of workspace rldx_attention_fwd_bf16 needs (its V^T copy). */
+/* Elements (bf16) of the packed tiles of one (batch, kv head). */
+int64_t rldx_attention_kv_packed_elems(int64_t seq_k, int64_t head_dim);
+
+/* Bytes of workspace rldx_attention_fwd_bf16 needs (its packed K/V copy). */
 int64_t rldx_attention_workspace_bytes(int64_t batch, int64_t kv_heads, int64_t seq_k, int64_t head_dim);
 
 /*
- * V [B, Hkv, Sk, D] (strides {batch, head, seq}, D contiguous) -> V^T in the
- * layout above (strides {batch, head, d}; d stride >= round_up(Sk, 64)).
+ * K, V [B, Hkv, Sk, D] (strides {batch, head, seq}, D contiguous) -> packed
+ * tiles, packed_strides {batch, head} in elements (head stride >=
+ * rldx_attention_kv_packed_elems).
  * No reference counterpart: layout preparation for the attention kernels.
  */
-hipError_t rldx_v_transpose_bf16(const void* v, const int64_t* v_strides, void* vt, const int64_t* vt_strides,
-                                 int64_t batch, int64_t kv_heads, int64_t seq_k, int64_t head_dim,
-                                 hipStream_t stream);
+hipError_t rldx_attention_kv_pack_bf16(const void* k, const int64_t* k_strides, const void* v,
+                                       const int64_t* v_strides, void* kv_packed, const int64_t* packed_strides,
+                                       int64_t batch, int64_t kv_heads, int64_t seq_k, int64_t head_dim,
+                                       hipStream_t stream);
 
 /*
  * O = softmax(Q K^T * scale + key_bias[b, key] (+ causal)) V, bf16 in/out,
@@ -174,10 +181,10 @@ hipError_t rldx_v_transpose_bf16(const void* v, const int64_t* v_strides, void* 
  * head h / (Hq / Hkv) (GQA; Hq % Hkv == 0).  key_bias is an optional fp32
  * [B, Sk] additive mask (0 / -inf for key padding), row stride
  * key_bias_batch_stride.  causal != 0: key j visible to query i iff j <= i
- * (top-left aligned, as SDPA's is_causal).  head_dim 64 or 128.
- * Two launches: V -> V^T into `workspace` (>= rldx_attention_workspace_bytes,
- * 16-byte aligned, caller-owned), then the attention kernel.  seq_k must be
- * >= 1 when seq_q >= 1.
+ * (top-left aligned, as SDPA's is_causal).  head_dim 64 or 128; scale > 0.
+ * Two launches: K, V -> packed tiles in `workspace` (>=
+ * rldx_attention_workspace_bytes, 16-byte aligned, caller-owned), then the
+ * attention kernel.  seq_k must be >= 1 when seq_q >= 1.
  *
  * Replaces: F.scaled_dot_product_attention inside ds::fused_attention_2way /
  *   _3way and ss::fused_attention_2way / _3way
@@ -195,23 +202,23 @@ hipError_t rldx_attention_fwd_bf16(const void* q, const void* k, const void* v, 
                                    int64_t workspace_bytes, hipStream_t stream);
 
 /*
- * Same operator with V already in the V^T layout (vt_strides {batch, head, d}),
+ * Same operator with K and V already packed (packed_strides {batch, head}),
  * one launch.  Used on the MSAT path, where rldx_msat_qkv_norm_rope_bf16 writes
- * V^T directly.
+ * the packed tiles directly.
  */
-hipError_t rldx_attention_vt_fwd_bf16(const void* q, const void* k, const void* vt, void* o, int64_t batch,
-                                      int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k,
-                                      int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
-                                      const int64_t* vt_strides, const int64_t* o_strides, const float* key_bias,
-                                      int64_t key_bias_batch_stride, float scale, int32_t causal,
-                                      hipStream_t stream);
+hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* kv_packed, const int64_t* packed_strides,
+                                          void* o, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                                          int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
+                                          const int64_t* o_strides, const float* key_bias,
+                                          int64_t key_bias_batch_stride, float scale, int32_t causal,
+                                          hipStream_t stream);
 
 /*
  * The complete rldx_backbone::fused_attention operator: packed QKV
  * (seq, >= (Hq + 2*Hkv)*D) bf16 -> out (seq, Hq*D) bf16 with q_norm/k_norm
  * (Qwen3VLTextRMSNorm, eps) + rotate-half RoPE (cos / sin tables [seq, D] bf16,
  * row stride cos_row_stride; sin pre-signed iff sin_is_signed) + causal GQA
- * attention, scale 1/sqrt(D).  Three launches: K normalisation and V^T into
+ * attention, scale 1/sqrt(D).  Three launches: K normalisation and K/V packing into
  * `workspace` (>= rldx_llm_fused_attention_workspace_bytes(seq, Hkv, D) bytes,
  * 16-byte aligned, caller-owned), then attention with the Q normalisation fused
  * into its prologue.
@@ -230,7 +237,7 @@ hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv_row_stride
                                          int64_t head_dim, float eps, void* workspace, int64_t workspace_bytes,
                                          hipStream_t stream);
 
-/* Workspace bytes rldx_llm_fused_attention_bf16 needs (normalised K + V^T). */
+/* Workspace bytes rldx_llm_fused_attention_bf16 needs (normalised K + packed K/V). */
 int64_t rldx_llm_fused_attention_workspace_bytes(int64_t seq, int64_t kv_heads, int64_t head_dim);
 
 /* ------------------------------------------------------------------------ */

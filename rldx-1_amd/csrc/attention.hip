@@ -11,30 +11,42 @@
 //     rldx/inference/backbone/llm/engine/kernels/fused_llm_attention.py:379-770).
 //
 // Design (short sequences: 608 / 1280 tokens, batch 1)
-//   * A workgroup has 4 waves = QW query sub-blocks of 32 queries x KW key
-//     groups.  KW = 2 (64-query workgroups) doubles the number of workgroups for
-//     the short sequences of this path so the grid reaches the 256 CUs; the two
-//     key groups walk interleaved key tiles and are merged through LDS at the end.
-//   * K and V^T tiles are staged in LDS with coalesced 16-byte loads (global ->
-//     VGPR -> LDS, double-buffered: one barrier per tile, the next tile's loads in
-//     flight during the current tile's math) and shared by the QW waves of the
-//     key group.  Loads use clamped addresses, never per-lane predication, so the
-//     compiler keeps exact vmcnt waits.
-//   * S^T = K Q^T: A = K rows from LDS, B = Q^T kept in VGPRs for the whole
-//     kernel.  Each lane owns one query column, so the online-softmax max / sum /
-//     rescale are lane-local (one xor-32 exchange per tile for the max).
-//   * O^T = V^T P^T: B = P^T is the exp'd score accumulator packed to bf16 (the
-//     accumulator row order permutes the key index inside each group of 16); A
-//     = V^T from a pre-transposed copy of V whose keys are stored in that same
-//     permuted order, so every operand is one 16-byte LDS read.  The V^T copy is
-//     made once per V (by the producing kernel, or by `vt_transpose_kernel`
-//     here), not once per query block.
+//   * K and V are read in a packed tile layout (below) in which every MFMA
+//     operand of a 32-key tile is one contiguous 1 KB block: lane l reads the
+//     16 bytes at l*16.  Operands therefore go straight from global memory into
+//     VGPRs with fully coalesced buffer loads (scalar tile offset, constant
+//     immediate offsets) — no LDS staging, no swizzle arithmetic, no barrier in
+//     the main loop.  The packed copy is written once per K/V by the producing
+//     kernel (the MSAT QKV kernel, or `kv_pack_kernel` here), not once per
+//     query block.
+//   * A workgroup = 32*NSUB queries of one head and 4 waves that split the key
+//     range (wave w walks tiles w, w+4, ...); the 4 partial softmax states are
+//     merged through LDS at the end.  NSUB = 2 doubles the reuse of every loaded
+//     K/V operand; NSUB = 1 doubles the number of workgroups for small problems.
+//   * S^T = K Q^T: A = K operand, B = Q^T kept in VGPRs.  Each lane owns one
+//     query column, so the online-softmax max / sum / rescale are lane-local.
+//   * O^T = V^T P^T: B = P^T is the exp'd score accumulator packed to bf16; the
+//     V part of a packed tile stores the keys in the accumulator's row order.
+//   * The next tile's K operands are loaded as soon as the S MFMAs have read the
+//     current ones, its V operands as soon as the P.V MFMAs have.
+//   * Workgroups are mapped XCD-aware: the query blocks of a head run on one XCD
+//     and share its L2.
 //   * Softmax in the exp2 domain with the scale folded into one FMA; tiles with
 //     no masked key skip all masking; the O / l rescale is lazy (the reference
 //     max moves only when a tile max exceeds it by more than 2^8), exact up to
-//     rounding because softmax is shift-invariant.
+//     rounding because softmax is shift-invariant; the two lanes of a query only
+//     exchange their maxima (v_permlane32_swap) when a rescale is due.
 //   * P is rounded to bf16 before the P.V product, the same rounding point as
 //     the eager CPU flash-attention kernel.
+//
+// Packed K/V tile t (keys 32t .. 32t+31) of one (batch, kv head), D = head_dim,
+// 128*D bytes, tiles of a head contiguous:
+//   K part, bytes [0, 64 D):     1 KB chunk ks (0 <= ks < D/16), lane l, element i
+//                                = K[32t + (l & 31)][16 ks + 8 (l >> 5) + i]
+//   V part, bytes [64 D, 128 D): 1 KB chunk 2 db + s2 (0 <= db < D/32, s2 < 2),
+//                                lane l, element i
+//                                = V[32t + 16 s2 + 8 (i >> 2) + 4 (l >> 5) + (i & 3)][32 db + (l & 31)]
+//   keys >= Sk hold zeros.
 #include "rldx_amd.h"
 #include "rldx_common.h"
 
@@ -45,25 +57,58 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyThreshold = 8.0f;  // log2 units: rescale only when the max grows by > 2^8
 constexpr int kXcds = 8;                // MI355X: 8 XCDs x 32 CUs, one L2 per XCD
+constexpr int kTileKeys = 32;
+constexpr int kBufWord3 = 0x00020000;   // gfx9 raw buffer descriptor, word 3 (untyped dword data)
+
+__host__ __device__ constexpr int64_t kv_tile_elems(int64_t d) { return 64 * d; }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufWord3);
+}
+
+// max(x of this lane, x of lane ^ 32)
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                  false, false);
+  return fmaxf(__builtin_bit_cast(float, static_cast<uint32_t>(r[0])),
+               __builtin_bit_cast(float, static_cast<uint32_t>(r[1])));
+}
+
+// x of this lane + x of lane ^ 32
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                  false, false);
+  return __builtin_bit_cast(float, static_cast<uint32_t>(r[0])) +
+         __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+}
+
+// The 16 bias values of a lane's S^T accumulator rows: keys key0 + 8*qq + c,
+// qq, c in 0..3, with key0 = tile start + 4 * (lane half).
+__device__ __forceinline__ void load_bias(floatx4 (&out)[4], __amdgpu_buffer_rsrc_t r, int key0) {
+#pragma unroll
+  for (int qq = 0; qq < 4; ++qq)
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc)
+      out[qq][cc] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, key0 * 4 + 32 * qq + 4 * cc, 0, 0));
+}
 
 struct AttnArgs {
   const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* vt;  // V^T, keys permuted within groups of 16, zero-padded to a multiple of 32
+  const uint16_t* kv;  // packed K/V tiles
   uint16_t* o;
   int64_t q_sb, q_sh, q_ss;
-  int64_t k_sb, k_sh, k_ss;
-  int64_t vt_sb, vt_sh, vt_sd;
+  int64_t kv_sb, kv_sh;  // element strides of the packed tiles per batch / kv head
   int64_t o_sb, o_sh, o_ss;
   const float* key_bias;  // [batch, sk] additive (natural-log units) or nullptr
   int64_t kb_sb;
   int hq, hkv, group, sq, sk;
   int num_q_blocks;
-  float scale_log2;  // softmax scale * log2(e)
+  float scale_log2;  // softmax scale * log2(e), > 0
   // fused Q RMSNorm + rotate-half RoPE (Qwen3-VL), used when kQNorm
   const uint16_t* q_norm_w;  // [D] bf16
   const uint16_t* cos;       // [sq, D] bf16
@@ -93,7 +138,7 @@ __device__ __forceinline__ void qnorm_rope_operands(bf16x8 (&qreg)[D / 16], cons
       ss += x[ks][i] * x[ks][i];
     }
   }
-  ss += __shfl_xor(ss, 32, 64);
+  ss = pair_sum(ss);
   float y[KS][8];
   {
 #pragma clang fp contract(off)
@@ -136,40 +181,22 @@ __device__ __forceinline__ void qnorm_rope_operands(bf16x8 (&qreg)[D / 16], cons
   }
 }
 
-template <int D, int KW, bool kCausal, bool kBias, bool kQNorm>
-__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
-  constexpr int QW = 4 / KW;             // query sub-blocks (waves) per key group
-  constexpr int BMW = 32 * QW;           // queries per workgroup
-  constexpr int BNT = KW == 1 ? 64 : 32; // keys per tile
-  constexpr int KB = BNT / 32;           // 32-key blocks of S^T per tile
-  constexpr int PSTEPS = BNT / 16;       // 16-key MFMA steps of O^T per tile
-  constexpr int KSTEPS = D / 16;         // MFMA k-steps over head_dim for S^T
-  constexpr int DBLK = D / 32;           // 32-row blocks of O^T
-  constexpr int KPITCH = D + 8;          // LDS row pitch of K (elements): conflict-free 16-byte reads
-  constexpr int VPITCH = BNT + 8;        // LDS row pitch of V^T (elements)
-  constexpr int GT = 256 / KW;           // threads per key group
-  constexpr int KCH = D / 8;             // 16-byte chunks per K row
-  constexpr int VCH = BNT / 8;           // 16-byte chunks per V^T row
-  constexpr int KL = BNT * KCH / GT;     // K chunks per thread per tile
-  constexpr int VL = D * VCH / GT;       // V^T chunks per thread per tile
-  static_assert(KL >= 1 && VL >= 1 && KL * GT == BNT * KCH && VL * GT == D * VCH, "tile shape");
-  constexpr int K_ELEMS = BNT * KPITCH;
-  constexpr int V_ELEMS = D * VPITCH;
-  constexpr int BUF_BYTES = (K_ELEMS + V_ELEMS) * 2 + BNT * 4;  // one buffer of one key group
-  constexpr int MERGE = DBLK * 16 + 2;                           // floats per lane in the merge
-  constexpr int MERGE_BYTES = KW > 1 ? QW * 64 * MERGE * 4 : 0;
-  constexpr int TILE_BYTES = KW * 2 * BUF_BYTES;
-  constexpr int LDS_BYTES = TILE_BYTES > MERGE_BYTES ? TILE_BYTES : MERGE_BYTES;
-  __shared__ __attribute__((aligned(16))) unsigned char smem[LDS_BYTES];
+template <int D, int NSUB, bool kCausal, bool kBias, bool kQNorm>
+__global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
+  constexpr int NW = 4;           // waves per workgroup; each walks its own key tiles
+  constexpr int BN = kTileKeys;   // keys per tile
+  constexpr int BMW = 32 * NSUB;  // queries per workgroup (shared by the 4 waves)
+  constexpr int KSTEPS = D / 16;  // MFMA k-steps over head_dim for S^T
+  constexpr int DBLK = D / 32;    // 32-row blocks of O^T
+  constexpr int TILE_BYTES = 128 * D;
+  constexpr int VPART = 64 * D;
+  constexpr int G4 = DBLK * 4 + 1;  // float4 groups per lane and sub-block in the merge: O + (m, l)
+  __shared__ floatx4 merge[NW * NSUB * G4 * 64];
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int l32 = lane & 31;
   const int g = lane >> 5;
-  const int kg = wave / QW;  // key group of this wave
-  const int qw = wave % QW;  // query sub-block of this wave
-  const int gt = tid - kg * GT;
 
   // XCD-aware work mapping.  Workgroups are dispatched round-robin over the 8
   // XCDs (workgroup i runs on XCD i % 8), each with its own L2.  Work items are
@@ -190,342 +217,340 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     b = p / (nqb * a.hq);
   }
   const int hk = h / a.group;
+  const int q_first = qb * BMW;
+  const int k_end = kCausal ? min(a.sk, min(a.sq, q_first + BMW)) : a.sk;
+  const int ntiles = (k_end + BN - 1) / BN;  // >= 1: q_first < sq and sk >= 1
+  const int head_tiles = (a.sk + BN - 1) / BN;
 
-  const uint16_t* kbase = a.k + b * a.k_sb + hk * a.k_sh;
-  const uint16_t* vtbase = a.vt + b * a.vt_sb + hk * a.vt_sh;
-  const float* bias = kBias ? a.key_bias + b * a.kb_sb : nullptr;
+  // Every load below stays inside this head's packed tiles: tile indices are
+  // clamped to [0, ntiles), and ntiles <= head_tiles.
+  const __amdgpu_buffer_rsrc_t kvr = make_rsrc(a.kv + b * a.kv_sb + hk * a.kv_sh, head_tiles * TILE_BYTES);
+  const int voff = lane * 16;
+  // Bias: lane reads the 16 keys of its accumulator rows (4 runs of 4 keys); a
+  // dword past sk is out of the descriptor's range and reads as 0.
+  __amdgpu_buffer_rsrc_t bsr;
+  if constexpr (kBias) bsr = make_rsrc(a.key_bias + b * a.kb_sb, a.sk * 4);
 
-  // ---- Q^T operand: lane holds query l32 of this wave's sub-block, d-chunk (2*ks + g) ----
-  // Global loads use clamped, always-valid addresses (no per-lane predication), so the
-  // loop stays branch-free around its loads and vmcnt accounting stays precise.
-  const int q_first = qb * BMW + qw * 32;
-  const int q_idx = q_first + l32;
-  const bool q_valid = q_idx < a.sq;
-  bf16x8 qreg[KSTEPS];
+  u32x4 kop[KSTEPS], vop[2 * DBLK];
+  floatx4 bnext[4];
   {
-    const uint16_t* qrow = a.q + b * a.q_sb + h * a.q_sh + static_cast<int64_t>(min(q_idx, a.sq - 1)) * a.q_ss + g * 8;
+    const int t0 = min(wave, ntiles - 1);
+    const int s0 = t0 * TILE_BYTES;
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks)
-      qreg[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qrow + ks * 16));
-    if constexpr (kQNorm) qnorm_rope_operands<D>(qreg, a, q_idx, q_valid);
+    for (int ks = 0; ks < KSTEPS; ++ks) kop[ks] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + ks * 1024, s0, 0);
+#pragma unroll
+    for (int c = 0; c < 2 * DBLK; ++c)
+      vop[c] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + VPART + c * 1024, s0, 0);
+    if constexpr (kBias) load_bias(bnext, bsr, t0 * BN + 4 * g);
   }
 
-  const int k_end = kCausal ? min(a.sk, min(a.sq, qb * BMW + BMW)) : a.sk;
-  const int ntiles = (k_end + BNT - 1) / BNT;
-  const int iters = (ntiles + KW - 1) / KW;  // tiles per key group (group kg takes tiles kg, kg+KW, ...)
-  const int last_key = a.sk - 1;
+  // ---- Q^T operands: sub-block j, lane holds query l32 and d-chunk (2*ks + g) ----
+  int q_idx[NSUB];
+  bf16x8 qreg[NSUB][KSTEPS];
+#pragma unroll
+  for (int j = 0; j < NSUB; ++j) {
+    q_idx[j] = q_first + 32 * j + l32;
+    const uint16_t* qrow =
+        a.q + b * a.q_sb + h * a.q_sh + static_cast<int64_t>(min(q_idx[j], a.sq - 1)) * a.q_ss + g * 8;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks)
+      qreg[j][ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qrow + ks * 16));
+    if constexpr (kQNorm) qnorm_rope_operands<D>(qreg[j], a, q_idx[j], q_idx[j] < a.sq);
+  }
 
-  // ---- global -> register staging of one tile of this key group (coalesced 16-byte loads) ----
-  u32x4 kreg[KL], vreg[VL];
-  float breg = 0.f;
-  auto fetch = [&](int t) {
-    const int k0 = t * BNT;
+  floatx16 oacc[NSUB][DBLK];
+  float m_ref[NSUB], l_part[NSUB];
 #pragma unroll
-    for (int i = 0; i < KL; ++i) {
-      const int c = i * GT + gt;
-      const int key = min(k0 + c / KCH, last_key);  // keys past the end are masked in the softmax
-      kreg[i] = *reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(key) * a.k_ss + (c % KCH) * 8);
-    }
+  for (int j = 0; j < NSUB; ++j) {
 #pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      const int c = i * GT + gt;
-      vreg[i] = *reinterpret_cast<const u32x4*>(vtbase + static_cast<int64_t>(c / VCH) * a.vt_sd + k0 + (c % VCH) * 8);
-    }
-    if constexpr (kBias) breg = bias[min(k0 + (gt % BNT), last_key)] * kLog2e;
-  };
-  auto stash = [&](int buf) {
-    unsigned char* base = smem + (kg * 2 + buf) * BUF_BYTES;
-    uint16_t* Ks = reinterpret_cast<uint16_t*>(base);
-    uint16_t* Vs = Ks + K_ELEMS;
-#pragma unroll
-    for (int i = 0; i < KL; ++i) {
-      const int c = i * GT + gt;
-      *reinterpret_cast<u32x4*>(&Ks[(c / KCH) * KPITCH + (c % KCH) * 8]) = kreg[i];
-    }
-#pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      const int c = i * GT + gt;
-      *reinterpret_cast<u32x4*>(&Vs[(c / VCH) * VPITCH + (c % VCH) * 8]) = vreg[i];
-    }
-    if (kBias && gt < BNT) reinterpret_cast<float*>(Vs + V_ELEMS)[gt] = breg;
-  };
-
-  floatx16 oacc[DBLK];
-#pragma unroll
-  for (int i = 0; i < DBLK; ++i) oacc[i] = floatx16{};
-  float m_ref = -__builtin_inff();  // reference max (log2 units) used for exp
-  float l_part = 0.f;
+    for (int db = 0; db < DBLK; ++db) oacc[j][db] = floatx16{};
+    m_ref[j] = -__builtin_inff();  // reference max (log2 units) used for exp
+    l_part[j] = 0.f;               // this lane's share of the row sum
+  }
   const float c = a.scale_log2;
 
-  // prologue: tile kg -> LDS buffer 0, tile kg+KW -> registers
-  const int t_last = ntiles > 0 ? ntiles - 1 : 0;
-  fetch(min(kg, t_last));
-  stash(0);
-  __syncthreads();
-  fetch(min(kg + KW, t_last));
+  for (int t = wave; t < ntiles; t += NW) {
+    const int k0 = t * BN;
+    const int sn = min(t + NW, ntiles - 1) * TILE_BYTES;  // next tile of this wave (clamped)
 
-  for (int it = 0; it < iters; ++it) {
-    const int t = it * KW + kg;
-    const int buf = it & 1;
-    const int k0 = t * BNT;
-    // a wave with no tile (ragged split) or whose queries all precede the tile has nothing to do
-    const bool active = (t < ntiles) && !(kCausal && k0 > q_first + 31);
-    if (active) {
-      const uint16_t* Ks = reinterpret_cast<const uint16_t*>(smem + (kg * 2 + buf) * BUF_BYTES);
-      const uint16_t* Vs = Ks + K_ELEMS;
-      const float* bs = reinterpret_cast<const float*>(Vs + V_ELEMS);
-      // ---- S^T = K Q^T ----
-      floatx16 sacc[KB];
+    // ---- S^T = K Q^T, one independent MFMA chain per sub-block ----
+    floatx16 sacc[NSUB];
+    bool active[NSUB];
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        const uint16_t* krow = &Ks[(kb * 32 + l32) * KPITCH + g * 8];
-        floatx16 sa = floatx16{}, sb = floatx16{};
+    for (int j = 0; j < NSUB; ++j) {
+      active[j] = !(kCausal && k0 > q_first + 32 * j + 31);  // whole tile in this sub-block's future
+      sacc[j] = floatx16{};
+      if (active[j]) {
 #pragma unroll
-        for (int ks = 0; ks < KSTEPS; ks += 2) {
-          sa = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(krow + ks * 16)), qreg[ks], sa, 0, 0, 0);
-          sb = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(krow + ks * 16 + 16)), qreg[ks + 1], sb, 0,
-              0, 0);
-        }
-        sacc[kb] = sa + sb;
+        for (int ks = 0; ks < KSTEPS; ++ks)
+          sacc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kop[ks]), qreg[j][ks],
+                                                            sacc[j], 0, 0, 0);
       }
-      // ---- softmax (log2 domain, lane = one query) ----
-      bool edge = (k0 + BNT > a.sk) || (kCausal && k0 + BNT - 1 > q_first);
-      if (kBias) edge = edge || __any(bs[lane % BNT] != 0.f);
+    }
+    // ---- next tile's K operands, in flight during the softmax and P.V below ----
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) kop[ks] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + ks * 1024, sn, 0);
+    floatx4 bq[4];
+    bool bias_tile = false;
+    if constexpr (kBias) {
+      float any_nz = 0.f;
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        bq[qq] = bnext[qq];
+        any_nz = fmaxf(any_nz, fmaxf(fmaxf(__builtin_fabsf(bq[qq][0]), __builtin_fabsf(bq[qq][1])),
+                                     fmaxf(__builtin_fabsf(bq[qq][2]), __builtin_fabsf(bq[qq][3]))));
+      }
+      bias_tile = __any(any_nz != 0.f);
+      load_bias(bnext, bsr, sn / TILE_BYTES * BN + 4 * g);
+    }
+
+#pragma unroll
+    for (int j = 0; j < NSUB; ++j) {
+      if (!active[j]) continue;
+      const int qf = q_first + 32 * j;  // first query of this sub-block
+      // ---- softmax (log2 domain, lane = one query, 16 of the tile's keys) ----
+      const bool edge = (k0 + BN > a.sk) || (kCausal && k0 + BN - 1 > qf) || bias_tile;
       float mt = -__builtin_inff();
       if (!edge) {
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) mt = fmaxf(mt, sacc[kb][j]);
+        for (int e = 0; e < 16; ++e) mt = fmaxf(mt, sacc[j][e]);
         mt *= c;
       } else {
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int kl = kb * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
-            const int key = k0 + kl;
-            float s = kBias ? __builtin_fmaf(sacc[kb][j], c, bs[kl]) : sacc[kb][j] * c;
-            bool ok = key < a.sk;
-            if (kCausal) ok = ok && (key <= q_idx);
-            s = ok ? s : -__builtin_inff();
-            sacc[kb][j] = s;
-            mt = fmaxf(mt, s);
-          }
+        for (int e = 0; e < 16; ++e) {
+          const int key = k0 + 8 * (e >> 2) + 4 * g + (e & 3);
+          float sv = sacc[j][e] * c;
+          if constexpr (kBias) sv += bq[e >> 2][e & 3] * kLog2e;
+          bool ok = key < a.sk;
+          if constexpr (kCausal) ok = ok && (key <= q_idx[j]);
+          sv = ok ? sv : -__builtin_inff();
+          sacc[j][e] = sv;
+          mt = fmaxf(mt, sv);
+        }
       }
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      const bool need = mt > m_ref + kLazyThreshold;
-      if (__any(need)) {
-        const float new_ref = need ? mt : m_ref;
-        const float alpha = (m_ref == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(m_ref - new_ref);
-        m_ref = new_ref;
-        l_part *= alpha;
+      if (__any(mt > m_ref[j] + kLazyThreshold)) {
+        // both lanes of a query see the same pair maximum, so they keep the same reference
+        const float mq = pair_max(mt);
+        const float new_ref = mq > m_ref[j] + kLazyThreshold ? mq : m_ref[j];
+        const float alpha = (m_ref[j] == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(m_ref[j] - new_ref);
+        m_ref[j] = new_ref;
+        l_part[j] *= alpha;
 #pragma unroll
-        for (int db = 0; db < DBLK; ++db) oacc[db] *= alpha;
+        for (int db = 0; db < DBLK; ++db) oacc[j][db] *= alpha;
       }
-      const float m_use = (m_ref == -__builtin_inff()) ? 0.f : m_ref;
+      const float m_use = (m_ref[j] == -__builtin_inff()) ? 0.f : m_ref[j];
       float psum = 0.f;
       if (!edge) {
         const float nm = -m_use;
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][j], c, nm));
-            sacc[kb][j] = p;
-            psum += p;
-          }
+        for (int e = 0; e < 16; ++e) {
+          const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e], c, nm));
+          sacc[j][e] = pe;
+          psum += pe;
+        }
       } else {
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const float p = __builtin_amdgcn_exp2f(sacc[kb][j] - m_use);
-            sacc[kb][j] = p;
-            psum += p;
-          }
-      }
-      l_part += psum;
-      // ---- O^T += V^T P^T, 16-key steps ----
-#pragma unroll
-      for (int s = 0; s < PSTEPS; ++s) {
-        floatx8 pv;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) pv[i] = sacc[s >> 1][(s & 1) * 8 + i];
-        const bf16x8 pop = __builtin_convertvector(pv, bf16x8);
-#pragma unroll
-        for (int db = 0; db < DBLK; ++db) {
-          const u32x4 vv = *reinterpret_cast<const u32x4*>(&Vs[(db * 32 + l32) * VPITCH + s * 16 + g * 8]);
-          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vv), pop, oacc[db], 0, 0, 0);
+        for (int e = 0; e < 16; ++e) {
+          const float pe = __builtin_amdgcn_exp2f(sacc[j][e] - m_use);
+          sacc[j][e] = pe;
+          psum += pe;
         }
       }
+      l_part[j] += psum;
+      // ---- O^T += V^T P^T, two 16-key steps ----
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        floatx8 pv;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] = sacc[j][s2 * 8 + e];
+        const bf16x8 pop = __builtin_convertvector(pv, bf16x8);
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db)
+          oacc[j][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vop[db * 2 + s2]), pop,
+                                                                oacc[j][db], 0, 0, 0);
+      }
     }
-    // next tile of this group: registers -> the other LDS buffer, then prefetch the one after
-    if (it + 1 < iters) {
-      stash(buf ^ 1);
-      __syncthreads();
-      fetch(min(t + 2 * KW, t_last));
-    }
+    // ---- next tile's V operands ----
+#pragma unroll
+    for (int cc = 0; cc < 2 * DBLK; ++cc)
+      vop[cc] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + VPART + cc * 1024, sn, 0);
   }
 
-  // ---- merge key groups through LDS (group 1 hands its partial state to group 0) ----
-  if constexpr (KW > 1) {
-    __syncthreads();
-    float* mb = reinterpret_cast<float*>(smem) + qw * (64 * MERGE);
-    if (kg == 1) {
+  // ---- merge the 4 waves' partial states; wave w finalises d-blocks w, w+4, ... ----
+  // LDS layout: [wave][sub-block][float4 group][lane] -> 16-byte, conflict-free accesses.
 #pragma unroll
-      for (int db = 0; db < DBLK; ++db)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) mb[(db * 16 + j) * 64 + lane] = oacc[db][j];
-      mb[(DBLK * 16) * 64 + lane] = m_ref;
-      mb[(DBLK * 16 + 1) * 64 + lane] = l_part;
-    }
-    __syncthreads();
-    if (kg != 0) return;
-    const float m1 = mb[(DBLK * 16) * 64 + lane];
-    const float l1 = mb[(DBLK * 16 + 1) * 64 + lane];
-    const float m = fmaxf(m_ref, m1);
-    const float a0 = (m_ref == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(m_ref - m);
-    const float a1 = (m1 == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
-    l_part = l_part * a0 + l1 * a1;
+  for (int j = 0; j < NSUB; ++j) {
+    floatx4* mine = merge + (wave * NSUB + j) * (G4 * 64);
 #pragma unroll
     for (int db = 0; db < DBLK; ++db)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) oacc[db][j] = oacc[db][j] * a0 + mb[(db * 16 + j) * 64 + lane] * a1;
+      for (int q4 = 0; q4 < 4; ++q4)
+        mine[(db * 4 + q4) * 64 + lane] =
+            floatx4{oacc[j][db][q4 * 4], oacc[j][db][q4 * 4 + 1], oacc[j][db][q4 * 4 + 2], oacc[j][db][q4 * 4 + 3]};
+    mine[(DBLK * 4) * 64 + lane] = floatx4{m_ref[j], l_part[j], 0.f, 0.f};
   }
-
-  // ---- normalise and store: lane holds query l32, d = 32db + 8jj + 4g + (0..3) ----
-  const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
-  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  if (q_valid) {
-    uint16_t* orow = a.o + b * a.o_sb + h * a.o_sh + static_cast<int64_t>(q_idx) * a.o_ss;
+  __syncthreads();
 #pragma unroll
-    for (int db = 0; db < DBLK; ++db) {
+  for (int j = 0; j < NSUB; ++j) {
+    float wgt[NW];
+    float lw[NW];
+    float m = -__builtin_inff();
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int d = db * 32 + jj * 8 + g * 4;
-        uint2 w;
-        w.x = static_cast<uint32_t>(f32_to_bf16_bits(oacc[db][jj * 4 + 0] * inv)) |
-              (static_cast<uint32_t>(f32_to_bf16_bits(oacc[db][jj * 4 + 1] * inv)) << 16);
-        w.y = static_cast<uint32_t>(f32_to_bf16_bits(oacc[db][jj * 4 + 2] * inv)) |
-              (static_cast<uint32_t>(f32_to_bf16_bits(oacc[db][jj * 4 + 3] * inv)) << 16);
-        *reinterpret_cast<uint2*>(orow + d) = w;
+    for (int w = 0; w < NW; ++w) {
+      const floatx4 ml = merge[(w * NSUB + j) * (G4 * 64) + (DBLK * 4) * 64 + lane];
+      wgt[w] = ml[0];
+      lw[w] = ml[1];
+      m = fmaxf(m, wgt[w]);
+    }
+    float l = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      wgt[w] = (wgt[w] == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(wgt[w] - m);
+      l += lw[w] * wgt[w];
+    }
+    l = pair_sum(l);
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    if (q_idx[j] < a.sq) {
+      uint16_t* orow = a.o + b * a.o_sb + h * a.o_sh + static_cast<int64_t>(q_idx[j]) * a.o_ss;
+      for (int db = wave; db < DBLK; db += NW) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          floatx4 acc = floatx4{};
+#pragma unroll
+          for (int w = 0; w < NW; ++w) acc += merge[(w * NSUB + j) * (G4 * 64) + (db * 4 + q4) * 64 + lane] * wgt[w];
+          acc *= inv;
+          const int d = db * 32 + q4 * 8 + g * 4;
+          uint2 wv;
+          wv.x = static_cast<uint32_t>(f32_to_bf16_bits(acc[0])) | (static_cast<uint32_t>(f32_to_bf16_bits(acc[1])) << 16);
+          wv.y = static_cast<uint32_t>(f32_to_bf16_bits(acc[2])) | (static_cast<uint32_t>(f32_to_bf16_bits(acc[3])) << 16);
+          *reinterpret_cast<uint2*>(orow + d) = wv;
+        }
       }
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// V [B, H, Sk, D] -> V^T [B, H, D, Skp] with keys permuted inside each group of
-// 16 (the P^T accumulator order) and zero padding up to Skp (multiple of 64).
-// One workgroup per (32-key block, head, batch), transposed through LDS.
+// K [B, H, Sk, D], V [B, H, Sk, D] (strided) -> packed K/V tiles (layout at the
+// top of this file).  One workgroup per (32-key tile, head, batch); V is
+// transposed through LDS.
 // ---------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(256) void vt_transpose_kernel(const uint16_t* __restrict__ v, int64_t v_sb, int64_t v_sh,
-                                                           int64_t v_ss, uint16_t* __restrict__ vt, int64_t vt_sb,
-                                                           int64_t vt_sh, int64_t vt_sd, int sk) {
+__global__ __launch_bounds__(256) void kv_pack_kernel(const uint16_t* __restrict__ k, int64_t k_sb, int64_t k_sh,
+                                                      int64_t k_ss, const uint16_t* __restrict__ v, int64_t v_sb,
+                                                      int64_t v_sh, int64_t v_ss, uint16_t* __restrict__ kvp,
+                                                      int64_t p_sb, int64_t p_sh, int sk) {
   constexpr int PITCH = D + 8;
-  constexpr int CH = D / 8;  // 16-byte chunks per V row
+  constexpr int CH = D / 8;      // 16-byte chunks per V row
+  constexpr int NCH = D / 16;    // 1 KB chunks per part
   __shared__ __attribute__((aligned(16))) uint16_t tile[32 * PITCH];
-  const int k0 = blockIdx.x * 32;
-  const uint16_t* src = v + blockIdx.z * v_sb + blockIdx.y * v_sh;
-  uint16_t* dst = vt + blockIdx.z * vt_sb + blockIdx.y * vt_sh + k0;
-  for (int c = threadIdx.x; c < 32 * CH; c += 256) {
-    const int r = c / CH, col = (c % CH) * 8;
+  const int k0 = blockIdx.x * kTileKeys;
+  const uint16_t* ksrc = k + blockIdx.z * k_sb + blockIdx.y * k_sh;
+  const uint16_t* vsrc = v + blockIdx.z * v_sb + blockIdx.y * v_sh;
+  uint16_t* dst = kvp + blockIdx.z * p_sb + blockIdx.y * p_sh + static_cast<int64_t>(blockIdx.x) * kv_tile_elems(D);
+  for (int cidx = threadIdx.x; cidx < 32 * CH; cidx += 256) {
+    const int r = cidx / CH, col = (cidx % CH) * 8;
     const int key = k0 + r;
-    u32x4 val = key < sk ? *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(key) * v_ss + col)
-                         : u32x4{0, 0, 0, 0};
+    const u32x4 val = key < sk ? *reinterpret_cast<const u32x4*>(vsrc + static_cast<int64_t>(key) * v_ss + col)
+                               : u32x4{0, 0, 0, 0};
     *reinterpret_cast<u32x4*>(&tile[r * PITCH + col]) = val;
   }
+  // K part: straight 16-byte copies into operand order
+  for (int idx = threadIdx.x; idx < NCH * 64; idx += 256) {
+    const int ks = idx >> 6, l = idx & 63;
+    const int key = k0 + (l & 31);
+    const u32x4 val = key < sk ? *reinterpret_cast<const u32x4*>(ksrc + static_cast<int64_t>(key) * k_ss + 16 * ks +
+                                                                 8 * (l >> 5))
+                               : u32x4{0, 0, 0, 0};
+    *reinterpret_cast<u32x4*>(dst + idx * 8) = val;
+  }
   __syncthreads();
-  for (int c = threadIdx.x; c < D * 4; c += 256) {
-    const int d = c >> 2, q = c & 3;  // output row d, 8-position chunk q of the 32-key block
+  // V part: gather 8 keys of one column per lane
+  for (int idx = threadIdx.x; idx < NCH * 64; idx += 256) {
+    const int cc = idx >> 6, l = idx & 63;
+    const int db = cc >> 1, s2 = cc & 1;
+    const int d = 32 * db + (l & 31);
     u32x4 out;
 #pragma unroll
     for (int i = 0; i < 8; i += 2) {
-      uint32_t w = 0;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int p = q * 8 + i + hh;            // position in the block
-        const int gp = (p & 15) >> 3, ip = p & 7;  // lane half / element inside the 16-group
-        const int key = (p & ~15) + (ip < 4 ? 4 * gp + ip : 8 + 4 * gp + (ip - 4));
-        w |= static_cast<uint32_t>(tile[key * PITCH + d]) << (16 * hh);
-      }
-      out[i >> 1] = w;
+      const int r0 = 16 * s2 + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
+      out[i >> 1] = static_cast<uint32_t>(tile[r0 * PITCH + d]) | (static_cast<uint32_t>(tile[(r0 + 1) * PITCH + d]) << 16);
     }
-    *reinterpret_cast<u32x4*>(dst + static_cast<int64_t>(d) * vt_sd + q * 8) = out;
+    *reinterpret_cast<u32x4*>(dst + NCH * 512 + idx * 8) = out;
   }
 }
 
-template <int D, int KW, bool kQNorm>
-hipError_t launch_attn_d(const AttnArgs& a, int batch, bool causal, bool has_bias, hipStream_t stream) {
+template <int D, int NSUB, bool kQNorm>
+void launch_attn_d(const AttnArgs& a, int batch, bool causal, bool has_bias, hipStream_t stream) {
   dim3 grid(static_cast<unsigned>(a.num_q_blocks) * a.hq * batch);
   dim3 block(256);
   if (causal) {
     if (has_bias)
-      hipLaunchKernelGGL((attn_fwd_kernel<D, KW, true, true, kQNorm>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((attn_fwd_kernel<D, NSUB, true, true, kQNorm>), grid, block, 0, stream, a);
     else
-      hipLaunchKernelGGL((attn_fwd_kernel<D, KW, true, false, kQNorm>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((attn_fwd_kernel<D, NSUB, true, false, kQNorm>), grid, block, 0, stream, a);
   } else {
     if (has_bias)
-      hipLaunchKernelGGL((attn_fwd_kernel<D, KW, false, true, kQNorm>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((attn_fwd_kernel<D, NSUB, false, true, kQNorm>), grid, block, 0, stream, a);
     else
-      hipLaunchKernelGGL((attn_fwd_kernel<D, KW, false, false, kQNorm>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((attn_fwd_kernel<D, NSUB, false, false, kQNorm>), grid, block, 0, stream, a);
+  }
+}
+
+constexpr int kNumCus = 256;
+
+template <bool kQNorm>
+hipError_t launch_attn(AttnArgs a, int64_t head_dim, int batch, bool causal, bool has_bias, hipStream_t stream) {
+  // 64 queries per workgroup when that still gives every CU a workgroup; else 32.
+  const int64_t wg64 = static_cast<int64_t>((a.sq + 63) / 64) * a.hq * batch;
+  const bool big = wg64 >= kNumCus;
+  a.num_q_blocks = big ? (a.sq + 63) / 64 : (a.sq + 31) / 32;
+  if (head_dim == 128) {
+    if (big)
+      launch_attn_d<128, 2, kQNorm>(a, batch, causal, has_bias, stream);
+    else
+      launch_attn_d<128, 1, kQNorm>(a, batch, causal, has_bias, stream);
+  } else {
+    if (big)
+      launch_attn_d<64, 2, kQNorm>(a, batch, causal, has_bias, stream);
+    else
+      launch_attn_d<64, 1, kQNorm>(a, batch, causal, has_bias, stream);
   }
   return hipGetLastError();
 }
 
-// Two key groups (64-query workgroups) unless one group already gives >= 2
-// workgroups per CU (then 128-query workgroups keep K/V reuse per LDS tile high).
-int choose_kw(int64_t sq, int64_t heads_x_batch) {
-  return ((sq + 127) / 128) * heads_x_batch >= 512 ? 1 : 2;
-}
-
-template <bool kQNorm>
-hipError_t launch_attn(AttnArgs a, int64_t head_dim, int batch, bool causal, bool has_bias, hipStream_t stream) {
-  const int kw = choose_kw(a.sq, static_cast<int64_t>(a.hq) * batch);
-  const int bm = kw == 1 ? 128 : 64;
-  a.num_q_blocks = (a.sq + bm - 1) / bm;
-  if (head_dim == 128)
-    return kw == 1 ? launch_attn_d<128, 1, kQNorm>(a, batch, causal, has_bias, stream)
-                   : launch_attn_d<128, 2, kQNorm>(a, batch, causal, has_bias, stream);
-  return kw == 1 ? launch_attn_d<64, 1, kQNorm>(a, batch, causal, has_bias, stream)
-                 : launch_attn_d<64, 2, kQNorm>(a, batch, causal, has_bias, stream);
-}
-
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int64_t round_up64(int64_t x) { return (x + 63) / 64 * 64; }
+int64_t tiles_of(int64_t sk) { return (sk + kTileKeys - 1) / kTileKeys; }
 
-// Shared validation of the q/k/o side; V^T validated by the callers.
-hipError_t check_qko(const void* q, const void* k, void* o, int64_t batch, int64_t q_heads, int64_t kv_heads,
-                     int64_t seq_q, int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
-                     const int64_t* k_strides, const int64_t* o_strides) {
+// Shared validation of the q/o side and the sizes.
+hipError_t check_qo(const void* q, void* o, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                    int64_t seq_k, int64_t head_dim, const int64_t* q_strides, const int64_t* o_strides,
+                    float scale) {
   if (head_dim != 64 && head_dim != 128) return hipErrorInvalidValue;
   if (batch < 0 || q_heads < 0 || kv_heads <= 0 || seq_q < 0 || seq_k < 0) return hipErrorInvalidValue;
   if (q_heads % kv_heads != 0) return hipErrorInvalidValue;
-  if (!q_strides || !k_strides || !o_strides) return hipErrorInvalidValue;
+  if (!q_strides || !o_strides) return hipErrorInvalidValue;
+  if (!(scale > 0.f) || scale == __builtin_inff()) return hipErrorInvalidValue;
   if (batch == 0 || q_heads == 0 || seq_q == 0) return hipSuccess;
   if (seq_k == 0) return hipErrorInvalidValue;  // softmax over an empty key set is undefined
-  if (!q || !k || !o) return hipErrorInvalidValue;
-  if (!a16(q) || !a16(k) || reinterpret_cast<uintptr_t>(o) % 8) return hipErrorInvalidValue;
+  if (!q || !o) return hipErrorInvalidValue;
+  if (!a16(q) || reinterpret_cast<uintptr_t>(o) % 8) return hipErrorInvalidValue;
   for (int i = 0; i < 3; ++i)
-    if (q_strides[i] % 8 || k_strides[i] % 8 || o_strides[i] % 4) return hipErrorInvalidValue;
-  if (seq_q > (1 << 24) || seq_k > (1 << 30) || q_heads > 65535 || batch > 65535) return hipErrorInvalidValue;
+    if (q_strides[i] % 8 || o_strides[i] % 4) return hipErrorInvalidValue;
+  // per-head packed tiles are addressed with 32-bit byte offsets
+  if (seq_q > (1 << 24) || tiles_of(seq_k) * 128 * head_dim > (int64_t{1} << 31) - 1 || q_heads > 65535 ||
+      batch > 65535)
+    return hipErrorInvalidValue;
   if (((seq_q + 31) / 32) * q_heads * batch > (int64_t{1} << 31) - 1) return hipErrorInvalidValue;  // 1-D grid
   return hipSuccess;
 }
 
-void fill_qko(AttnArgs& a, const void* q, const void* k, void* o, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
-              int64_t seq_k, const int64_t* qs, const int64_t* ks, const int64_t* os, const float* key_bias,
-              int64_t kb_sb, float scale) {
+void fill_qo(AttnArgs& a, const void* q, void* o, int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k,
+             const int64_t* qs, const int64_t* os, const float* key_bias, int64_t kb_sb, float scale) {
   a.q = static_cast<const uint16_t*>(q);
-  a.k = static_cast<const uint16_t*>(k);
   a.o = static_cast<uint16_t*>(o);
   a.q_sb = qs[0]; a.q_sh = qs[1]; a.q_ss = qs[2];
-  a.k_sb = ks[0]; a.k_sh = ks[1]; a.k_ss = ks[2];
   a.o_sb = os[0]; a.o_sh = os[1]; a.o_ss = os[2];
   a.key_bias = key_bias;
   a.kb_sb = kb_sb;
@@ -542,53 +567,66 @@ void fill_qko(AttnArgs& a, const void* q, const void* k, void* o, int64_t q_head
 
 using namespace rldx;
 
-extern "C" int64_t rldx_attention_workspace_bytes(int64_t batch, int64_t kv_heads, int64_t seq_k, int64_t head_dim) {
-  if (batch < 0 || kv_heads < 0 || seq_k < 0 || head_dim < 0) return -1;
-  return batch * kv_heads * head_dim * round_up64(seq_k) * 2;
+extern "C" int64_t rldx_attention_kv_packed_elems(int64_t seq_k, int64_t head_dim) {
+  if (seq_k < 0 || head_dim < 0) return -1;
+  return tiles_of(seq_k) * kv_tile_elems(head_dim);
 }
 
-extern "C" hipError_t rldx_v_transpose_bf16(const void* v, const int64_t* v_strides, void* vt,
-                                            const int64_t* vt_strides, int64_t batch, int64_t kv_heads,
-                                            int64_t seq_k, int64_t head_dim, hipStream_t stream) {
+extern "C" int64_t rldx_attention_workspace_bytes(int64_t batch, int64_t kv_heads, int64_t seq_k, int64_t head_dim) {
+  if (batch < 0 || kv_heads < 0 || seq_k < 0 || head_dim < 0) return -1;
+  return batch * kv_heads * rldx_attention_kv_packed_elems(seq_k, head_dim) * 2;
+}
+
+extern "C" hipError_t rldx_attention_kv_pack_bf16(const void* k, const int64_t* k_strides, const void* v,
+                                                  const int64_t* v_strides, void* kv_packed,
+                                                  const int64_t* packed_strides, int64_t batch, int64_t kv_heads,
+                                                  int64_t seq_k, int64_t head_dim, hipStream_t stream) {
   if (head_dim != 64 && head_dim != 128) return hipErrorInvalidValue;
-  if (batch < 0 || kv_heads < 0 || seq_k < 0 || !v_strides || !vt_strides) return hipErrorInvalidValue;
+  if (batch < 0 || kv_heads < 0 || seq_k < 0 || !k_strides || !v_strides || !packed_strides)
+    return hipErrorInvalidValue;
   if (batch == 0 || kv_heads == 0 || seq_k == 0) return hipSuccess;
-  if (!v || !vt || !a16(v) || !a16(vt)) return hipErrorInvalidValue;
+  if (!k || !v || !kv_packed || !a16(k) || !a16(v) || !a16(kv_packed)) return hipErrorInvalidValue;
   for (int i = 0; i < 3; ++i)
-    if (v_strides[i] % 8 || vt_strides[i] % 8) return hipErrorInvalidValue;
-  if (vt_strides[2] < round_up64(seq_k) || batch > 65535 || kv_heads > 65535) return hipErrorInvalidValue;
-  dim3 grid(static_cast<unsigned>(round_up64(seq_k) / 32), static_cast<unsigned>(kv_heads),
-            static_cast<unsigned>(batch));
+    if (k_strides[i] % 8 || v_strides[i] % 8) return hipErrorInvalidValue;
+  const int64_t head_elems = rldx_attention_kv_packed_elems(seq_k, head_dim);
+  if (packed_strides[0] % 8 || packed_strides[1] % 8 || packed_strides[1] < head_elems ||
+      (batch > 1 && packed_strides[0] < kv_heads * packed_strides[1]))
+    return hipErrorInvalidValue;
+  if (batch > 65535 || kv_heads > 65535 || tiles_of(seq_k) > (int64_t{1} << 31) - 1) return hipErrorInvalidValue;
+  dim3 grid(static_cast<unsigned>(tiles_of(seq_k)), static_cast<unsigned>(kv_heads), static_cast<unsigned>(batch));
   if (head_dim == 128)
-    hipLaunchKernelGGL(vt_transpose_kernel<128>, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(v),
-                       v_strides[0], v_strides[1], v_strides[2], static_cast<uint16_t*>(vt), vt_strides[0],
-                       vt_strides[1], vt_strides[2], static_cast<int>(seq_k));
+    hipLaunchKernelGGL(kv_pack_kernel<128>, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(k), k_strides[0],
+                       k_strides[1], k_strides[2], static_cast<const uint16_t*>(v), v_strides[0], v_strides[1],
+                       v_strides[2], static_cast<uint16_t*>(kv_packed), packed_strides[0], packed_strides[1],
+                       static_cast<int>(seq_k));
   else
-    hipLaunchKernelGGL(vt_transpose_kernel<64>, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(v),
-                       v_strides[0], v_strides[1], v_strides[2], static_cast<uint16_t*>(vt), vt_strides[0],
-                       vt_strides[1], vt_strides[2], static_cast<int>(seq_k));
+    hipLaunchKernelGGL(kv_pack_kernel<64>, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(k), k_strides[0],
+                       k_strides[1], k_strides[2], static_cast<const uint16_t*>(v), v_strides[0], v_strides[1],
+                       v_strides[2], static_cast<uint16_t*>(kv_packed), packed_strides[0], packed_strides[1],
+                       static_cast<int>(seq_k));
   return hipGetLastError();
 }
 
-extern "C" hipError_t rldx_attention_vt_fwd_bf16(const void* q, const void* k, const void* vt, void* o,
-                                                 int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
-                                                 int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
-                                                 const int64_t* k_strides, const int64_t* vt_strides,
-                                                 const int64_t* o_strides, const float* key_bias,
-                                                 int64_t key_bias_batch_stride, float scale, int32_t causal,
-                                                 hipStream_t stream) {
-  hipError_t e = check_qko(q, k, o, batch, q_heads, kv_heads, seq_q, seq_k, head_dim, q_strides, k_strides,
-                           o_strides);
+extern "C" hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* kv_packed,
+                                                     const int64_t* packed_strides, void* o, int64_t batch,
+                                                     int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k,
+                                                     int64_t head_dim, const int64_t* q_strides,
+                                                     const int64_t* o_strides, const float* key_bias,
+                                                     int64_t key_bias_batch_stride, float scale, int32_t causal,
+                                                     hipStream_t stream) {
+  hipError_t e = check_qo(q, o, batch, q_heads, kv_heads, seq_q, seq_k, head_dim, q_strides, o_strides, scale);
   if (e != hipSuccess || batch == 0 || q_heads == 0 || seq_q == 0) return e;
-  if (!vt || !vt_strides || !a16(vt)) return hipErrorInvalidValue;
-  for (int i = 0; i < 3; ++i)
-    if (vt_strides[i] % 8) return hipErrorInvalidValue;
-  if (vt_strides[2] < round_up64(seq_k)) return hipErrorInvalidValue;
+  if (!kv_packed || !packed_strides || !a16(kv_packed)) return hipErrorInvalidValue;
+  if (packed_strides[0] % 8 || packed_strides[1] % 8 ||
+      packed_strides[1] < rldx_attention_kv_packed_elems(seq_k, head_dim) ||
+      (batch > 1 && packed_strides[0] < kv_heads * packed_strides[1]))
+    return hipErrorInvalidValue;
+  if (key_bias && reinterpret_cast<uintptr_t>(key_bias) % 4) return hipErrorInvalidValue;
   AttnArgs a{};
-  fill_qko(a, q, k, o, q_heads, kv_heads, seq_q, seq_k, q_strides, k_strides, o_strides, key_bias,
-           key_bias_batch_stride, scale);
-  a.vt = static_cast<const uint16_t*>(vt);
-  a.vt_sb = vt_strides[0]; a.vt_sh = vt_strides[1]; a.vt_sd = vt_strides[2];
+  fill_qo(a, q, o, q_heads, kv_heads, seq_q, seq_k, q_strides, o_strides, key_bias, key_bias_batch_stride, scale);
+  a.kv = static_cast<const uint16_t*>(kv_packed);
+  a.kv_sb = packed_strides[0];
+  a.kv_sh = packed_strides[1];
   return launch_attn<false>(a, head_dim, static_cast<int>(batch), causal != 0, key_bias != nullptr, stream);
 }
 
@@ -599,27 +637,24 @@ extern "C" hipError_t rldx_attention_fwd_bf16(const void* q, const void* k, cons
                                               const int64_t* o_strides, const float* key_bias,
                                               int64_t key_bias_batch_stride, float scale, int32_t causal,
                                               void* workspace, int64_t workspace_bytes, hipStream_t stream) {
-  hipError_t e = check_qko(q, k, o, batch, q_heads, kv_heads, seq_q, seq_k, head_dim, q_strides, k_strides,
-                           o_strides);
+  hipError_t e = check_qo(q, o, batch, q_heads, kv_heads, seq_q, seq_k, head_dim, q_strides, o_strides, scale);
   if (e != hipSuccess || batch == 0 || q_heads == 0 || seq_q == 0) return e;
-  if (!v || !v_strides || !a16(v)) return hipErrorInvalidValue;
-  for (int i = 0; i < 3; ++i)
-    if (v_strides[i] % 8) return hipErrorInvalidValue;
+  if (!k || !v || !k_strides || !v_strides) return hipErrorInvalidValue;
   const int64_t need = rldx_attention_workspace_bytes(batch, kv_heads, seq_k, head_dim);
   if (!workspace || workspace_bytes < need || !a16(workspace)) return hipErrorInvalidValue;
-  const int64_t skp = round_up64(seq_k);
-  const int64_t vts[3] = {kv_heads * head_dim * skp, head_dim * skp, skp};
-  e = rldx_v_transpose_bf16(v, v_strides, workspace, vts, batch, kv_heads, seq_k, head_dim, stream);
+  const int64_t head_elems = rldx_attention_kv_packed_elems(seq_k, head_dim);
+  const int64_t ps[2] = {kv_heads * head_elems, head_elems};
+  e = rldx_attention_kv_pack_bf16(k, k_strides, v, v_strides, workspace, ps, batch, kv_heads, seq_k, head_dim,
+                                  stream);
   if (e != hipSuccess) return e;
-  return rldx_attention_vt_fwd_bf16(q, k, workspace, o, batch, q_heads, kv_heads, seq_q, seq_k, head_dim, q_strides,
-                                    k_strides, vts, o_strides, key_bias, key_bias_batch_stride, scale, causal,
-                                    stream);
+  return rldx_attention_packed_fwd_bf16(q, workspace, ps, o, batch, q_heads, kv_heads, seq_q, seq_k, head_dim,
+                                        q_strides, o_strides, key_bias, key_bias_batch_stride, scale, causal, stream);
 }
 
 extern "C" int64_t rldx_llm_fused_attention_workspace_bytes(int64_t seq, int64_t kv_heads, int64_t head_dim) {
   if (seq < 0 || kv_heads < 0 || head_dim < 0) return -1;
-  // normalised K [seq, Hkv, D] followed by V^T [Hkv, D, round_up64(seq)]
-  return seq * kv_heads * head_dim * 2 + kv_heads * head_dim * round_up64(seq) * 2;
+  // normalised K [seq, Hkv, D], then the packed K/V tiles of the Hkv heads
+  return seq * kv_heads * head_dim * 2 + kv_heads * rldx_attention_kv_packed_elems(seq, head_dim) * 2;
 }
 
 extern "C" hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv_row_stride, const void* q_norm_w,
@@ -638,11 +673,11 @@ extern "C" hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv
   if (workspace_bytes < rldx_llm_fused_attention_workspace_bytes(seq, kv_heads, head_dim))
     return hipErrorInvalidValue;
   if (!a16(qkv) || !a16(out) || !a16(cos) || !a16(sin) || !a16(workspace)) return hipErrorInvalidValue;
-  if (seq > (1 << 30) || q_heads > 65535) return hipErrorInvalidValue;
+  if (seq > (1 << 24) || q_heads > 65535) return hipErrorInvalidValue;
   const uint16_t* base = static_cast<const uint16_t*>(qkv);
   uint16_t* kws = static_cast<uint16_t*>(workspace);  // normalised K, [seq, kv_heads, D]
-  uint16_t* vtws = kws + seq * kv_heads * head_dim;    // V^T, [kv_heads, D, round_up64(seq)]
-  const int64_t skp = round_up64(seq);
+  uint16_t* kvp = kws + seq * kv_heads * head_dim;    // packed K/V tiles
+  const int64_t head_elems = rldx_attention_kv_packed_elems(seq, head_dim);
   // 1) K: RMSNorm + rotate-half RoPE into the workspace (Q is done inside the attention kernel)
   const int64_t k_strides[3] = {0, qkv_row_stride, head_dim};
   const int64_t ko_strides[3] = {0, kv_heads * head_dim, head_dim};
@@ -652,21 +687,22 @@ extern "C" hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv
                                                 nullptr, kws, 1, seq, 0, kv_heads, head_dim, zero3, k_strides, zero3,
                                                 ko_strides, cs, eps, sin_is_signed ? RLDX_ROPE_SIN_SIGNED : 0, stream);
   if (e != hipSuccess) return e;
-  // 2) V^T of the packed V columns
+  // 2) pack the normalised K and the packed V columns
+  const int64_t kk_strides[3] = {0, head_dim, kv_heads * head_dim};
   const int64_t v_strides[3] = {0, head_dim, qkv_row_stride};
-  const int64_t vt_strides[3] = {0, head_dim * skp, skp};
-  e = rldx_v_transpose_bf16(base + (q_heads + kv_heads) * head_dim, v_strides, vtws, vt_strides, 1, kv_heads, seq,
-                            head_dim, stream);
+  const int64_t ps[2] = {0, head_elems};
+  e = rldx_attention_kv_pack_bf16(kws, kk_strides, base + (q_heads + kv_heads) * head_dim, v_strides, kvp, ps, 1,
+                                  kv_heads, seq, head_dim, stream);
   if (e != hipSuccess) return e;
   // 3) causal GQA attention, Q normalised in the prologue
   AttnArgs a{};
   const int64_t q_strides[3] = {0, head_dim, qkv_row_stride};
-  const int64_t kk_strides[3] = {0, head_dim, kv_heads * head_dim};
   const int64_t o_strides[3] = {0, head_dim, out_row_stride};
-  fill_qko(a, base, kws, out, q_heads, kv_heads, seq, seq, q_strides, kk_strides, o_strides, nullptr, 0,
-           1.0f / __builtin_sqrtf(static_cast<float>(head_dim)));
-  a.vt = vtws;
-  a.vt_sb = 0; a.vt_sh = head_dim * skp; a.vt_sd = skp;
+  fill_qo(a, base, out, q_heads, kv_heads, seq, seq, q_strides, o_strides, nullptr, 0,
+          1.0f / __builtin_sqrtf(static_cast<float>(head_dim)));
+  a.kv = kvp;
+  a.kv_sb = 0;
+  a.kv_sh = head_elems;
   a.q_norm_w = static_cast<const uint16_t*>(q_norm_w);
   a.cos = static_cast<const uint16_t*>(cos);
   a.sin = static_cast<const uint16_t*>(sin);

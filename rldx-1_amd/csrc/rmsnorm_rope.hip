@@ -180,29 +180,33 @@ struct MsatArgs {
   uint16_t* v_out;
   int64_t o_sh, o_sm;  // output strides (head, row) in elements, shared by q/k/v
   float eps;
-  int64_t total_items;  // rows of D handled by the norm/copy role: 3*H*M, or 2*H*M with vt_out
-  // optional V^T output [H, D, >= round_up(M, 64)] (keys permuted inside groups of 16,
-  // zero padded), written by workgroups [qk_blocks, qk_blocks + H * v_blocks)
-  uint16_t* vt_out;
-  int64_t vt_sh, vt_sd;
+  int64_t total_items;  // rows of D handled by the norm/copy role: 3*H*M, or 2*H*M with kvp
+  // optional packed K/V tiles of the attention kernels (32 keys per tile, 128*D
+  // bytes, K operand chunks then V operand chunks, keys >= M zero): K rows are
+  // scattered into them by the norm role; V and the K padding are written by
+  // workgroups [qk_blocks, qk_blocks + H * kv_tiles)
+  uint16_t* kvp;
+  int64_t kvp_sh;  // head stride in elements
   int64_t qk_blocks;
-  int64_t v_blocks;  // 32-token blocks per head
+  int64_t kv_tiles;  // 32-token tiles per head
 };
 
-// Position -> key inside one group of 16 keys of a V^T row (the P^T accumulator order
-// of the attention kernel: lane half g holds keys {4g..4g+3, 8+4g..8+4g+3}).
-__device__ __forceinline__ int vt_key_of_pos(int p) {
-  const int gp = (p & 15) >> 3, ip = p & 7;
-  return (p & ~15) + (ip < 4 ? 4 * gp + ip : 8 + 4 * gp + (ip - 4));
+// Element offset of K[key][d0 .. d0+7] inside the packed tiles of one head:
+// tile key/32, 1 KB chunk d0/16, lane (key % 32) + 32 * ((d0 / 8) % 2).
+__device__ __forceinline__ int64_t packed_k_offset(int64_t key, int d0, int D) {
+  const int lane = static_cast<int>(key & 31) + 32 * ((d0 >> 3) & 1);
+  return (key >> 5) * (64 * D) + ((d0 >> 4) * 64 + lane) * 8;
 }
 
 template <int D>
-__device__ void msat_v_transpose_block(const MsatArgs& a, int64_t vb) {
+__device__ void msat_kv_pack_block(const MsatArgs& a, int64_t vb) {
   constexpr int PITCH = D + 8;
-  constexpr int CH = D / 8;
+  constexpr int CH = D / 8;    // 16-byte chunks per V row
+  constexpr int NCH = D / 16;  // 1 KB chunks per part of a tile
   __shared__ __attribute__((aligned(16))) uint16_t tile[32 * PITCH];
-  const int64_t h = vb / a.v_blocks;
-  const int64_t k0 = (vb - h * a.v_blocks) * 32;
+  const int64_t h = vb / a.kv_tiles;
+  const int64_t t = vb - h * a.kv_tiles;
+  const int64_t k0 = t * 32;
   const int64_t inner = a.heads * D;
   for (int c = threadIdx.x; c < 32 * CH; c += 256) {
     const int r = c / CH, col = (c % CH) * 8;
@@ -217,17 +221,24 @@ __device__ void msat_v_transpose_block(const MsatArgs& a, int64_t vb) {
     }
     *reinterpret_cast<uint4*>(&tile[r * PITCH + col]) = val;
   }
+  uint16_t* dst = a.kvp + h * a.kvp_sh + t * (64 * D);
+  // K rows past the end of the sequence read as zeros
+  for (int idx = threadIdx.x; idx < NCH * 64; idx += 256)
+    if (k0 + (idx & 31) >= a.m_total) *reinterpret_cast<uint4*>(dst + idx * 8) = make_uint4(0, 0, 0, 0);
   __syncthreads();
-  uint16_t* dst = a.vt_out + h * a.vt_sh + k0;
-  for (int c = threadIdx.x; c < D * 4; c += 256) {
-    const int d = c >> 2, q = c & 3;
+  // V part: chunk 2*db + s2, lane l, element i = V[k0 + 16 s2 + 8 (i/4) + 4 (l/32) + i%4][32 db + l%32]
+  for (int idx = threadIdx.x; idx < NCH * 64; idx += 256) {
+    const int cc = idx >> 6, l = idx & 63;
+    const int d = 32 * (cc >> 1) + (l & 31);
+    const int rb = 16 * (cc & 1) + 4 * (l >> 5);
     uint4 out;
     uint32_t* ow = reinterpret_cast<uint32_t*>(&out);
 #pragma unroll
-    for (int i = 0; i < 8; i += 2)
-      ow[i >> 1] = static_cast<uint32_t>(tile[vt_key_of_pos(q * 8 + i) * PITCH + d]) |
-                   (static_cast<uint32_t>(tile[vt_key_of_pos(q * 8 + i + 1) * PITCH + d]) << 16);
-    *reinterpret_cast<uint4*>(dst + static_cast<int64_t>(d) * a.vt_sd + q * 8) = out;
+    for (int i = 0; i < 8; i += 2) {
+      const int r0 = rb + 8 * (i >> 2) + (i & 3);
+      ow[i >> 1] = static_cast<uint32_t>(tile[r0 * PITCH + d]) | (static_cast<uint32_t>(tile[(r0 + 1) * PITCH + d]) << 16);
+    }
+    *reinterpret_cast<uint4*>(dst + NCH * 512 + idx * 8) = out;
   }
 }
 
@@ -236,8 +247,8 @@ __global__ __launch_bounds__(256) void msat_qkv_norm_rope_kernel(MsatArgs a) {
   constexpr int V = 8;
   constexpr int LPR = D / V;
   static_assert(LPR >= 2 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "unsupported head_dim");
-  if (a.vt_out != nullptr && static_cast<int64_t>(blockIdx.x) >= a.qk_blocks) {
-    msat_v_transpose_block<D>(a, static_cast<int64_t>(blockIdx.x) - a.qk_blocks);
+  if (a.kvp != nullptr && static_cast<int64_t>(blockIdx.x) >= a.qk_blocks) {
+    msat_kv_pack_block<D>(a, static_cast<int64_t>(blockIdx.x) - a.qk_blocks);
     return;
   }
   const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -259,7 +270,9 @@ __global__ __launch_bounds__(256) void msat_qkv_norm_rope_kernel(MsatArgs a) {
   const int64_t inner = a.heads * D;
   const int d0 = lane_in_row * V;
   const uint16_t* src = S.qkv + row * S.ld + which * inner + h * D + d0;
-  uint16_t* dst = (which == 0 ? a.q_out : which == 1 ? a.k_out : a.v_out) + h * a.o_sh + m * a.o_sm + d0;
+  uint16_t* dst = (a.kvp != nullptr && which == 1)
+                      ? a.kvp + h * a.kvp_sh + packed_k_offset(m, d0, D)
+                      : (which == 0 ? a.q_out : which == 1 ? a.k_out : a.v_out) + h * a.o_sh + m * a.o_sm + d0;
 
   uint4 raw = valid ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
   if (which == 2) {  // V passthrough (uniform per row group, but shuffles below need all lanes)
@@ -379,14 +392,15 @@ extern "C" hipError_t rldx_qk_rmsnorm_rope_half_bf16(
 extern "C" hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* streams, int32_t num_streams,
                                                    int64_t heads, int64_t head_dim, void* q_out, void* k_out,
                                                    void* v_out, int64_t out_head_stride, int64_t out_row_stride,
-                                                   void* vt_out, int64_t vt_head_stride, int64_t vt_d_stride,
-                                                   float eps, hipStream_t stream) {
+                                                   void* kv_packed, int64_t kv_packed_head_stride, float eps,
+                                                   hipStream_t stream) {
   if (streams == nullptr || num_streams < 1 || num_streams > 3) return hipErrorInvalidValue;
   if (head_dim != 64 && head_dim != 128) return hipErrorInvalidValue;
-  if (heads <= 0 || !q_out || !k_out || (!v_out && !vt_out)) return hipErrorInvalidValue;
-  if (!al16(q_out) || !al16(k_out) || out_head_stride % 8 || out_row_stride % 8) return hipErrorInvalidValue;
-  if (v_out && !al16(v_out)) return hipErrorInvalidValue;
-  if (vt_out && (!al16(vt_out) || vt_head_stride % 8 || vt_d_stride % 8)) return hipErrorInvalidValue;
+  if (heads <= 0 || !q_out) return hipErrorInvalidValue;
+  if (!kv_packed && (!k_out || !v_out)) return hipErrorInvalidValue;
+  if (!al16(q_out) || out_head_stride % 8 || out_row_stride % 8) return hipErrorInvalidValue;
+  if (!kv_packed && (!al16(k_out) || !al16(v_out))) return hipErrorInvalidValue;
+  if (kv_packed && (!al16(kv_packed) || kv_packed_head_stride % 8)) return hipErrorInvalidValue;
   MsatArgs a{};
   int64_t m = 0;
   int k = 0;
@@ -416,15 +430,14 @@ extern "C" hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* str
   a.o_sh = out_head_stride;
   a.o_sm = out_row_stride;
   a.eps = eps;
-  a.total_items = (vt_out ? 2 : 3) * heads * m;
+  a.total_items = (kv_packed ? 2 : 3) * heads * m;
   const int64_t threads = a.total_items * (head_dim / 8);
   a.qk_blocks = (threads + 255) / 256;
-  a.vt_out = static_cast<uint16_t*>(vt_out);
-  a.vt_sh = vt_head_stride;
-  a.vt_sd = vt_d_stride;
-  a.v_blocks = (m + 63) / 64 * 2;  // V^T keys padded (with zeros) to a multiple of 64
-  if (vt_out && (vt_d_stride < a.v_blocks * 32 || vt_head_stride < head_dim * vt_d_stride)) return hipErrorInvalidValue;
-  const int grid = static_cast<int>(a.qk_blocks + (vt_out ? heads * a.v_blocks : 0));
+  a.kvp = static_cast<uint16_t*>(kv_packed);
+  a.kvp_sh = kv_packed_head_stride;
+  a.kv_tiles = (m + 31) / 32;
+  if (kv_packed && kv_packed_head_stride < a.kv_tiles * 64 * head_dim) return hipErrorInvalidValue;
+  const int grid = static_cast<int>(a.qk_blocks + (kv_packed ? heads * a.kv_tiles : 0));
   if (head_dim == 64)
     hipLaunchKernelGGL(msat_qkv_norm_rope_kernel<64>, dim3(grid), dim3(256), 0, stream, a);
   else

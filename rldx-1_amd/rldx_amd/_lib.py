@@ -48,18 +48,18 @@ SIGNATURES = {
     ),
     "rldx_msat_qkv_norm_rope_bf16": (
         c_i32,
-        [ctypes.POINTER(MsatStream), c_i32, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_f32,
-         c_vp],
+        [ctypes.POINTER(MsatStream), c_i32, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp, c_i64, c_f32, c_vp],
     ),
+    "rldx_attention_kv_packed_elems": (c_i64, [c_i64, c_i64]),
     "rldx_attention_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64]),
-    "rldx_v_transpose_bf16": (c_i32, [c_vp, c_i64p, c_vp, c_i64p, c_i64, c_i64, c_i64, c_i64, c_vp]),
+    "rldx_attention_kv_pack_bf16": (c_i32, [c_vp, c_i64p, c_vp, c_i64p, c_vp, c_i64p, c_i64, c_i64, c_i64, c_i64, c_vp]),
     "rldx_attention_fwd_bf16": (
         c_i32,
         [c_vp] * 4 + [c_i64] * 6 + [c_i64p] * 4 + [c_vp, c_i64, c_f32, c_i32, c_vp, c_i64, c_vp],
     ),
-    "rldx_attention_vt_fwd_bf16": (
+    "rldx_attention_packed_fwd_bf16": (
         c_i32,
-        [c_vp] * 4 + [c_i64] * 6 + [c_i64p] * 4 + [c_vp, c_i64, c_f32, c_i32, c_vp],
+        [c_vp, c_vp, c_i64p, c_vp] + [c_i64] * 6 + [c_i64p] * 2 + [c_vp, c_i64, c_f32, c_i32, c_vp],
     ),
     "rldx_llm_fused_attention_bf16": (
         c_i32,

@@ -176,12 +176,14 @@ class StreamSpec:
 
 
 def msat_qkv_norm_rope(streams: Sequence[StreamSpec], num_heads: int, head_dim: int, eps: float = 1e-6,
-                       out: Optional[tuple] = None, v_transposed: bool = False):
+                       out: Optional[tuple] = None, kv_packed: bool = False):
     """Gather Q/K/V of 1-3 streams into (H, M, D) bf16 with per-stream QK RMSNorm
     (one rounding) and interleaved RoPE on the streams that carry tables.
 
-    With `v_transposed`, the third output is V^T (H, D, round_up(M, 64)) in the
-    layout `attention_vt` reads (keys permuted inside groups of 16, zero padded).
+    Returns (q, k, v).  With `kv_packed`, returns (q, kvp) instead: K and V are
+    written as the packed K/V tiles `attention_packed` reads, kvp of shape
+    (H, kv_packed_elems(M, D)) bf16.  `out` gives the output tensors in the
+    same form.
 
     rmsnorm_rope_ds.py:11-231 / rmsnorm_rope_ds_3way.py:22-386 fused layout,
     eager semantics of norms.py:18-22 and action_model/ops.py:48-67."""
@@ -213,32 +215,37 @@ def msat_qkv_norm_rope(streams: Sequence[StreamSpec], num_heads: int, head_dim: 
         descs[i] = _lib.MsatStream(s.qkv.data_ptr(), s.qkv.stride(0), n, s.q_w.data_ptr(), s.k_w.data_ptr(),
                                    cos_p, sin_p, rope_ld)
         M += n
-    Mp = (M + 63) // 64 * 64
     if out is None:
         q = torch.empty((num_heads, M, head_dim), dtype=BF16, device=dev)
-        k = torch.empty_like(q)
-        v = torch.empty((num_heads, head_dim, Mp), dtype=BF16, device=dev) if v_transposed else torch.empty_like(q)
+        rest = ((torch.empty((num_heads, kv_packed_elems(M, head_dim)), dtype=BF16, device=dev),) if kv_packed
+                else (torch.empty_like(q), torch.empty_like(q)))
     else:
-        q, k, v = out
-        _require(q.shape == (num_heads, M, head_dim) and k.shape == q.shape and k.stride() == q.stride(),
-                 "q/k out tensors must be (H, M, D) with equal strides")
-        if v_transposed:
-            _require(v.shape[:2] == (num_heads, head_dim) and v.shape[2] >= Mp and v.stride(2) == 1,
-                     "vt out must be (H, D, >= round_up(M, 64)) with contiguous keys")
+        q, *rest = out
+        _require(q.shape == (num_heads, M, head_dim), "q out must be (H, M, D)")
+        if kv_packed:
+            _require(len(rest) == 1, "packed mode takes out=(q, kvp)")
+            kvp = rest[0]
+            _require(kvp.dtype == BF16 and kvp.dim() == 2 and kvp.shape[0] == num_heads and
+                     kvp.shape[1] >= kv_packed_elems(M, head_dim) and kvp.stride(1) == 1,
+                     "kvp out must be (H, >= kv_packed_elems(M, D)) bf16")
         else:
-            _require(v.shape == q.shape and v.stride() == q.stride(), "v out must match q")
+            _require(len(rest) == 2, "out=(q, k, v)")
+            for t in rest:
+                _require(t.shape == q.shape and t.stride() == q.stride(), "k/v out tensors must match q")
     if M == 0:
-        return q, k, v
+        return (q, *rest)
     lib = _lib.load()
-    if v_transposed:
-        args = (None, 0, 0, v.data_ptr(), v.stride(0), v.stride(1))
+    if kv_packed:
+        kvp = rest[0]
+        _lib.check(lib.rldx_msat_qkv_norm_rope_bf16(descs, len(streams), num_heads, head_dim, q.data_ptr(), None, None,
+                                                    q.stride(0), q.stride(1), kvp.data_ptr(), kvp.stride(0),
+                                                    float(eps), _stream_ptr(q)), "rldx_msat_qkv_norm_rope_bf16")
     else:
-        args = (v.data_ptr(), q.stride(0), q.stride(1), None, 0, 0)
-    _lib.check(lib.rldx_msat_qkv_norm_rope_bf16(descs, len(streams), num_heads, head_dim, q.data_ptr(), k.data_ptr(),
-                                                args[0], q.stride(0) if v_transposed else args[1],
-                                                q.stride(1) if v_transposed else args[2], args[3], args[4], args[5],
-                                                float(eps), _stream_ptr(q)), "rldx_msat_qkv_norm_rope_bf16")
-    return q, k, v
+        k, v = rest
+        _lib.check(lib.rldx_msat_qkv_norm_rope_bf16(descs, len(streams), num_heads, head_dim, q.data_ptr(),
+                                                    k.data_ptr(), v.data_ptr(), q.stride(0), q.stride(1), None, 0,
+                                                    float(eps), _stream_ptr(q)), "rldx_msat_qkv_norm_rope_bf16")
+    return (q, *rest)
 
 
 # ---------------------------------------------------------------------------
@@ -307,46 +314,62 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, key_bias: Op
     return out
 
 
-def v_transpose(v: torch.Tensor, layout: str = "bhsd") -> torch.Tensor:
-    """V [B, H, S, D] (or [B, S, H, D]) -> V^T [B, H, D, round_up(S, 64)] in the
-    permuted-key layout the attention kernels read (padding keys zero)."""
-    _on_gpu(v)
-    _require(v.dtype == BF16 and v.dim() == 4 and v.stride(-1) == 1, "v must be 4-D bf16, last dim contiguous")
+def kv_packed_elems(seq_k: int, head_dim: int) -> int:
+    """bf16 elements of the packed K/V tiles of one (batch, kv head): ceil(Sk/32) * 64 * D."""
+    return (seq_k + 31) // 32 * 64 * head_dim
+
+
+def kv_pack(k: torch.Tensor, v: torch.Tensor, layout: str = "bhsd") -> torch.Tensor:
+    """K, V [B, H, S, D] (or [B, S, H, D]) -> packed K/V tiles [B, H, kv_packed_elems(S, D)]
+    (32 keys per tile; every MFMA operand of the attention kernel is one 1 KB block)."""
+    _on_gpu(k, v)
+    for t in (k, v):
+        _require(t.dtype == BF16 and t.dim() == 4 and t.stride(-1) == 1, "k/v must be 4-D bf16, last dim contiguous")
+    _require(k.shape == v.shape, "k and v must have one shape")
     if layout == "bhsd":
-        B, H, S, D = v.shape
+        B, H, S, D = k.shape
     else:
-        B, S, H, D = v.shape
-    Sp = (S + 63) // 64 * 64
-    vt = torch.empty((B, H, D, Sp), dtype=BF16, device=v.device)
+        B, S, H, D = k.shape
+    kvp = torch.empty((B, H, kv_packed_elems(S, D)), dtype=BF16, device=k.device)
     lib = _lib.load()
-    _lib.check(lib.rldx_v_transpose_bf16(v.data_ptr(), _lib.i64_array(_bhs_strides(v, layout)), vt.data_ptr(),
-                                         _lib.i64_array([vt.stride(0), vt.stride(1), vt.stride(2)]), B, H, S, D,
-                                         _stream_ptr(v)), "rldx_v_transpose_bf16")
-    return vt
+    _lib.check(lib.rldx_attention_kv_pack_bf16(k.data_ptr(), _lib.i64_array(_bhs_strides(k, layout)), v.data_ptr(),
+                                               _lib.i64_array(_bhs_strides(v, layout)), kvp.data_ptr(),
+                                               _lib.i64_array([kvp.stride(0), kvp.stride(1)]), B, H, S, D,
+                                               _stream_ptr(k)), "rldx_attention_kv_pack_bf16")
+    return kvp
 
 
-def attention_vt(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, *, key_bias: Optional[torch.Tensor] = None,
-                 causal: bool = False, scale: Optional[float] = None, layout: str = "bhsd",
-                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Attention with V given as V^T [B, Hkv, D, >= round_up(Sk, 64)] (see v_transpose)."""
-    _on_gpu(q, k, vt, key_bias, out)
-    B, Hq, Hkv, Sq, Sk, D = _attn_dims(q, k, layout)
-    _require(vt.dtype == BF16 and vt.dim() == 4 and vt.shape[:3] == (B, Hkv, D) and vt.stride(-1) == 1 and
-             vt.shape[3] >= (Sk + 63) // 64 * 64, "vt must be [B, Hkv, D, >= round_up(Sk, 64)]")
+def attention_packed(q: torch.Tensor, kvp: torch.Tensor, seq_k: int, *, key_bias: Optional[torch.Tensor] = None,
+                     causal: bool = False, scale: Optional[float] = None, layout: str = "bhsd",
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Attention with K/V given as packed tiles [B, Hkv, >= kv_packed_elems(seq_k, D)]
+    (see kv_pack; the MSAT QKV kernel writes them directly)."""
+    _on_gpu(q, kvp, key_bias, out)
+    _require(q.dtype == BF16 and q.dim() == 4 and q.stride(-1) == 1, "q must be 4-D bf16, last dim contiguous")
+    if layout == "bhsd":
+        B, Hq, Sq, D = q.shape
+    elif layout == "bshd":
+        B, Sq, Hq, D = q.shape
+    else:
+        raise ValueError(f"unknown layout {layout}")
+    _require(D in (64, 128), "head_dim must be 64 or 128")
+    _require(kvp.dtype == BF16 and kvp.dim() == 3 and kvp.shape[0] == B and kvp.stride(2) == 1 and
+             kvp.shape[2] >= kv_packed_elems(seq_k, D), "kvp must be [B, Hkv, >= kv_packed_elems(seq_k, D)] bf16")
+    Hkv = kvp.shape[1]
+    _require(Hkv > 0 and Hq % Hkv == 0, "q heads must be a multiple of kv heads")
     if out is None:
         out = torch.empty_like(q, memory_format=torch.contiguous_format)
     _require(out.shape == q.shape and out.dtype == BF16 and out.stride(-1) == 1, "out must match q")
-    kb_ptr, kb_stride = _key_bias_args(key_bias, B, Sk)
+    kb_ptr, kb_stride = _key_bias_args(key_bias, B, seq_k)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     lib = _lib.load()
-    _lib.check(lib.rldx_attention_vt_fwd_bf16(q.data_ptr(), k.data_ptr(), vt.data_ptr(), out.data_ptr(), B, Hq, Hkv, Sq,
-                                              Sk, D, _lib.i64_array(_bhs_strides(q, layout)),
-                                              _lib.i64_array(_bhs_strides(k, layout)),
-                                              _lib.i64_array([vt.stride(0), vt.stride(1), vt.stride(2)]),
-                                              _lib.i64_array(_bhs_strides(out, layout)), kb_ptr, kb_stride,
-                                              float(scale), int(bool(causal)), _stream_ptr(q)),
-               "rldx_attention_vt_fwd_bf16")
+    _lib.check(lib.rldx_attention_packed_fwd_bf16(q.data_ptr(), kvp.data_ptr(),
+                                                  _lib.i64_array([kvp.stride(0), kvp.stride(1)]), out.data_ptr(), B,
+                                                  Hq, Hkv, Sq, seq_k, D, _lib.i64_array(_bhs_strides(q, layout)),
+                                                  _lib.i64_array(_bhs_strides(out, layout)), kb_ptr, kb_stride,
+                                                  float(scale), int(bool(causal)), _stream_ptr(q)),
+               "rldx_attention_packed_fwd_bf16")
     return out
 
 

@@ -156,8 +156,8 @@ class MsatActionStep:
         e = lambda *s: torch.empty(*s, dtype=BF16, device=dev)  # noqa: E731
         self.x = e(n, d)            # residual stream, rows VL | SA | P
         self.qkv = e(n, 3 * cfg.inner)
-        self.q, self.k = e(H, n, D), e(H, n, D)
-        self.vt = e(H, D, (n + 63) // 64 * 64)  # V^T in the attention kernel's layout
+        self.q = e(H, n, D)
+        self.kvp = e(H, Fn.kv_packed_elems(n, D))  # K/V in the attention kernel's packed tiles
         self.att = e(n, H, D)       # attention output, token-major
         self.y = e(n, d)            # projection / FFN output
         self.u = e(n, 2 * cfg.ffn)  # w12 output
@@ -181,10 +181,9 @@ class MsatActionStep:
             Fn.StreamSpec(self.qkv[cfg.rows("p")], w["p.q_norm"][L], w["p.k_norm"][L],
                           self.inp["p_cos"], self.inp["p_sin"]),
         ]
-        Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.k, self.vt),
-                              v_transposed=True)
-        Fn.attention_vt(self.q.unsqueeze(0), self.k.unsqueeze(0), self.vt.unsqueeze(0), key_bias=self.inp["key_bias"],
-                        out=self.att.unsqueeze(0).permute(0, 2, 1, 3))
+        Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
+        Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), cfg.tokens, key_bias=self.inp["key_bias"],
+                            out=self.att.unsqueeze(0).permute(0, 2, 1, 3))
         att2 = self.att.view(cfg.tokens, cfg.inner)
         for s in STREAMS:
             r = cfg.rows(s)

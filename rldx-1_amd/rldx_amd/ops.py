@@ -30,11 +30,11 @@ from . import functional as Fn
 # ---------------------------------------------------------------------------
 
 
-def _attn_from_qkv(q, k, vt, key_bias, M, H, D):
-    """(H, M, D) Q/K + V^T (H, D, Mp) -> (1, M, H*D) bf16, written directly in token-major order."""
+def _attn_from_qkv(q, kvp, key_bias, M, H, D):
+    """(H, M, D) Q + packed K/V tiles (H, E) -> (1, M, H*D) bf16, written directly in token-major order."""
     out = torch.empty((1, M, H, D), dtype=torch.bfloat16, device=q.device)
-    Fn.attention_vt(q.unsqueeze(0), k.unsqueeze(0), vt.unsqueeze(0), key_bias=key_bias, layout="bhsd",
-                    out=out.permute(0, 2, 1, 3))
+    Fn.attention_packed(q.unsqueeze(0), kvp.unsqueeze(0), M, key_bias=key_bias, layout="bhsd",
+                        out=out.permute(0, 2, 1, 3))
     return out.view(1, M, H * D)
 
 
@@ -70,8 +70,8 @@ def ds_fused_attention_2way(
         Fn.StreamSpec(_qkv_cols(vl_qkv)[:n_vl], q_norm_vl_weight, k_norm_vl_weight),
         Fn.StreamSpec(_qkv_cols(sa_qkv)[:n_sa], q_norm_sa_weight, k_norm_sa_weight, rope_cos, rope_sin),
     ]
-    q, k, v = Fn.msat_qkv_norm_rope(streams, H, D, v_transposed=True)
-    return _attn_from_qkv(q, k, v, None, n_vl + n_sa, H, D)
+    q, kvp = Fn.msat_qkv_norm_rope(streams, H, D, kv_packed=True)
+    return _attn_from_qkv(q, kvp, None, n_vl + n_sa, H, D)
 
 
 @ds_fused_attention_2way.register_fake
@@ -112,9 +112,9 @@ def ds_fused_attention_3way(
         Fn.StreamSpec(_qkv_cols(sa_qkv)[:n_sa], q_norm_sa_weight, k_norm_sa_weight, sa_rope_cos, sa_rope_sin),
         Fn.StreamSpec(_qkv_cols(p_qkv)[:n_p], q_norm_p_weight, k_norm_p_weight, p_rope_cos, p_rope_sin),
     ]
-    q, k, v = Fn.msat_qkv_norm_rope(streams, H, D, v_transposed=True)
+    q, kvp = Fn.msat_qkv_norm_rope(streams, H, D, kv_packed=True)
     bias = Fn.mask_to_key_bias(kv_mask) if kv_mask is not None else None
-    return _attn_from_qkv(q, k, v, bias, n_vl + n_sa + n_p, H, D)
+    return _attn_from_qkv(q, kvp, bias, n_vl + n_sa + n_p, H, D)
 
 
 @ds_fused_attention_3way.register_fake
@@ -174,8 +174,8 @@ def ss_fused_attention_2way(
         streams.append(Fn.StreamSpec(x[: M - n_sa], q_norm_weight, k_norm_weight))
     if n_sa > 0:
         streams.append(Fn.StreamSpec(x[M - n_sa:], q_norm_weight, k_norm_weight, rope_cos, rope_sin))
-    q, k, v = Fn.msat_qkv_norm_rope(streams, H, D, v_transposed=True)
-    return _attn_from_qkv(q, k, v, None, M, H, D)
+    q, kvp = Fn.msat_qkv_norm_rope(streams, H, D, kv_packed=True)
+    return _attn_from_qkv(q, kvp, None, M, H, D)
 
 
 @ss_fused_attention_2way.register_fake
@@ -215,9 +215,9 @@ def ss_fused_attention_3way(
         streams.append(Fn.StreamSpec(x[n_x - n_sa:], x_q_norm_weight, x_k_norm_weight, sa_rope_cos, sa_rope_sin))
     if n_p > 0:
         streams.append(Fn.StreamSpec(p, p_q_norm_weight, p_k_norm_weight, p_rope_cos, p_rope_sin))
-    q, k, v = Fn.msat_qkv_norm_rope(streams, H, D, v_transposed=True)
+    q, kvp = Fn.msat_qkv_norm_rope(streams, H, D, kv_packed=True)
     bias = Fn.mask_to_key_bias(kv_mask) if kv_mask is not None else None
-    return _attn_from_qkv(q, k, v, bias, n_x + n_p, H, D)
+    return _attn_from_qkv(q, kvp, bias, n_x + n_p, H, D)
 
 
 @ss_fused_attention_3way.register_fake

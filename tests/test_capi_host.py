@@ -83,27 +83,32 @@ def test_capi_rejects_bad_arguments_without_launching():
     # misaligned pointer
     assert lib.rldx_attention_fwd_bf16(18, 16, 16, 16, 1, 2, 2, 4, 4, 128, st, st, st, st, None, 0, 1.0, 0, 16, big,
                                        None) == HIP_INVALID_VALUE
-    # workspace too small for the V^T copy
+    # workspace too small for the packed K/V copy (1 tile of 32 keys x 2 heads)
     need = lib.rldx_attention_workspace_bytes(1, 2, 4, 128)
-    assert need == 2 * 128 * 64 * 2
+    assert need == 2 * 64 * 128 * 2
+    assert lib.rldx_attention_kv_packed_elems(33, 64) == 2 * 64 * 64
     assert lib.rldx_attention_fwd_bf16(16, 16, 16, 16, 1, 2, 2, 4, 4, 128, st, st, st, st, None, 0, 1.0, 0, 16,
                                        need - 2, None) == HIP_INVALID_VALUE
-    # V^T row stride shorter than round_up(seq_k, 64)
-    vts = _lib.i64_array([0, 0, 16])
-    assert lib.rldx_attention_vt_fwd_bf16(16, 16, 16, 16, 1, 2, 2, 4, 20, 128, st, st, vts, st, None, 0, 1.0, 0,
-                                          None) == HIP_INVALID_VALUE
-    assert lib.rldx_v_transpose_bf16(16, st, 16, vts, 1, 1, 20, 128, None) == HIP_INVALID_VALUE
-    assert lib.rldx_msat_qkv_norm_rope_bf16(None, 1, 12, 128, 16, 16, 16, 0, 0, None, 0, 0, 1e-6,
+    # non-positive softmax scale
+    assert lib.rldx_attention_fwd_bf16(16, 16, 16, 16, 1, 2, 2, 4, 4, 128, st, st, st, st, None, 0, 0.0, 0, 16,
+                                       need, None) == HIP_INVALID_VALUE
+    # packed head stride shorter than the tiles of seq_k = 40 (2 tiles)
+    ps = _lib.i64_array([0, 64 * 128])
+    assert lib.rldx_attention_packed_fwd_bf16(16, 16, ps, 16, 1, 2, 2, 4, 40, 128, st, st, None, 0, 1.0, 0,
+                                              None) == HIP_INVALID_VALUE
+    assert lib.rldx_attention_kv_pack_bf16(16, st, 16, st, 16, ps, 1, 1, 40, 128, None) == HIP_INVALID_VALUE
+    assert lib.rldx_msat_qkv_norm_rope_bf16(None, 1, 12, 128, 16, 16, 16, 0, 0, None, 0, 1e-6,
                                             None) == HIP_INVALID_VALUE
     s = _lib.MsatStream(16, 100, 4, 16, 16, None, None, 0)  # row stride < 3*H*D
-    assert lib.rldx_msat_qkv_norm_rope_bf16(ctypes.byref(s), 1, 12, 128, 16, 16, 16, 0, 0, None, 0, 0, 1e-6,
+    assert lib.rldx_msat_qkv_norm_rope_bf16(ctypes.byref(s), 1, 12, 128, 16, 16, 16, 0, 0, None, 0, 1e-6,
                                             None) == HIP_INVALID_VALUE
-    s = _lib.MsatStream(16, 4608, 40, 16, 16, None, None, 0)  # V^T d stride < round_up(40, 64)
-    assert lib.rldx_msat_qkv_norm_rope_bf16(ctypes.byref(s), 1, 12, 128, 16, 16, None, 0, 0, 16, 128 * 64, 48,
+    s = _lib.MsatStream(16, 4608, 40, 16, 16, None, None, 0)  # packed head stride < 2 tiles
+    assert lib.rldx_msat_qkv_norm_rope_bf16(ctypes.byref(s), 1, 12, 128, 16, None, None, 0, 0, 16, 64 * 128,
                                             1e-6, None) == HIP_INVALID_VALUE
     # empty key set with queries present
-    assert lib.rldx_attention_vt_fwd_bf16(16, 16, 16, 16, 1, 2, 2, 4, 0, 128, st, st, vts, st, None, 0, 1.0, 0,
-                                          None) == HIP_INVALID_VALUE
+    ps = _lib.i64_array([0, 0])
+    assert lib.rldx_attention_packed_fwd_bf16(16, 16, ps, 16, 1, 2, 2, 4, 0, 128, st, st, None, 0, 1.0, 0,
+                                              None) == HIP_INVALID_VALUE
     assert lib.rldx_qk_rmsnorm_rope_half_f32(16, 16, 16, 16, 16, 16, 16, 16, 1, 4, 2, 2, 96, st, st, st, st, st,
                                              1e-6, 0, None) == HIP_INVALID_VALUE
     # fused LLM attention: workspace too small / kv heads not dividing q heads
@@ -111,7 +116,7 @@ def test_capi_rejects_bad_arguments_without_launching():
                                              8, None) == HIP_INVALID_VALUE
     assert lib.rldx_llm_fused_attention_bf16(16, 4608, 16, 16, 16, 16, 128, 1, 16, 3584, 1280, 28, 3, 128, 1e-6, 16,
                                              1 << 30, None) == HIP_INVALID_VALUE
-    assert lib.rldx_llm_fused_attention_workspace_bytes(1280, 4, 128) == 2 * 1280 * 4 * 128 * 2
+    assert lib.rldx_llm_fused_attention_workspace_bytes(1280, 4, 128) == 1280 * 4 * 128 * 2 + 4 * 40 * 64 * 128 * 2
 
 
 def test_zero_sized_calls_are_noops():

@@ -18,6 +18,29 @@ from tolerances import assert_bf16_close, assert_fp32_close
 pytestmark = pytest.mark.gpu
 
 
+def packed_kv_layout(k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """CPU construction of the packed K/V tiles from their definition: for tile t,
+    lane l, element i, K chunk ks holds K[32t + l%32][16 ks + 8 (l//32) + i] and V
+    chunk 2 db + s2 holds V[32t + 16 s2 + 8 (i//4) + 4 (l//32) + i%4][32 db + l%32];
+    keys past the end are zero.  k, v: [B, H, S, D] bf16 -> [B, H, tiles * 64 * D]."""
+    B, H, S, D = k.shape
+    T = (S + 31) // 32
+    kp = torch.zeros(B, H, T * 32, D, dtype=k.dtype)
+    vp = torch.zeros_like(kp)
+    kp[:, :, :S], vp[:, :, :S] = k, v
+    kp, vp = kp.view(B, H, T, 32, D), vp.view(B, H, T, 32, D)
+    lane = torch.arange(64)[None, :, None]
+    i = torch.arange(8)[None, None, :]
+    c = torch.arange(D // 16)[:, None, None]
+    k_key = (lane % 32).expand(D // 16, 64, 8)
+    k_d = 16 * c + 8 * (lane // 32) + i
+    v_key = 16 * (c % 2) + 8 * (i // 4) + 4 * (lane // 32) + i % 4
+    v_d = (32 * (c // 2) + lane % 32).expand(D // 16, 64, 8)
+    kpart = kp[:, :, :, k_key, k_d].reshape(B, H, T, -1)
+    vpart = vp[:, :, :, v_key, v_d].reshape(B, H, T, -1)
+    return torch.cat([kpart, vpart], dim=3).reshape(B, H, -1)
+
+
 def _all_bf16():
     u = np.arange(65536, dtype=np.uint32) << 16
     return torch.from_numpy(u.view(np.float32).copy()).to(torch.bfloat16)
@@ -132,10 +155,11 @@ def test_msat_qkv_norm_rope(dev, D, H, sizes):
     assert torch.equal(v.cpu(), rv)
     assert_bf16_close(q, rq, "q")
     assert_bf16_close(k, rk, "k")
-    # V^T output mode: same Q/K, V equal to the standalone transpose of V
-    q2, k2, vt = Fn.msat_qkv_norm_rope(specs, H, D, v_transposed=True)
-    assert torch.equal(q2, q) and torch.equal(k2, k)
-    assert torch.equal(vt, Fn.v_transpose(v.unsqueeze(0))[0])
+    # packed K/V output mode: same Q, K/V tiles equal to the standalone packing of K and V
+    q2, kvp = Fn.msat_qkv_norm_rope(specs, H, D, kv_packed=True)
+    assert torch.equal(q2, q)
+    assert torch.equal(kvp, Fn.kv_pack(k.unsqueeze(0), v.unsqueeze(0))[0])
+    assert torch.equal(kvp.cpu(), packed_kv_layout(k.cpu().unsqueeze(0), v.cpu().unsqueeze(0))[0])
 
 
 # ---------------------------------------------------------------------------
@@ -190,21 +214,21 @@ def test_attention_shapes(dev, B, Hq, Hkv, Sq, Sk, D, causal, masked):
     assert_bf16_close(o, r, "attention")
 
 
-@pytest.mark.parametrize("S,D", [(608, 128), (77, 64), (1, 128), (1280, 128)])
-def test_v_transpose_layout(dev, S, D):
-    """V^T layout: row d holds keys in groups of 16 ordered {0-3, 8-11, 4-7, 12-15}, zero padded."""
-    g = torch.Generator().manual_seed(S)
+@pytest.mark.parametrize("S,D,layout", [(608, 128, "bhsd"), (77, 64, "bshd"), (1, 128, "bhsd"), (1280, 128, "bshd")])
+def test_kv_pack_layout(dev, S, D, layout):
+    """Packed K/V tiles, element for element, against the layout definition."""
+    g = torch.Generator().manual_seed(S + D)
+    k = torch.randn(2, 3, S, D, generator=g).to(torch.bfloat16)
     v = torch.randn(2, 3, S, D, generator=g).to(torch.bfloat16)
-    vt = Fn.v_transpose(v.to(dev)).cpu()
-    Sp = (S + 63) // 64 * 64
-    perm = torch.tensor([0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15])
-    keys = (torch.arange(Sp) // 16) * 16 + perm[torch.arange(Sp) % 16]
-    vp = torch.zeros(2, 3, Sp, D, dtype=torch.bfloat16)
-    vp[:, :, :S] = v
-    assert torch.equal(vt, vp[:, :, keys].transpose(2, 3))
+    if layout == "bshd":
+        kd, vd = k.transpose(1, 2).contiguous().to(dev), v.transpose(1, 2).contiguous().to(dev)
+    else:
+        kd, vd = k.to(dev), v.to(dev)
+    kvp = Fn.kv_pack(kd, vd, layout=layout).cpu()
+    assert torch.equal(kvp, packed_kv_layout(k, v))
 
 
-def test_attention_vt_matches_attention(dev):
+def test_attention_packed_matches_attention(dev):
     g = torch.Generator().manual_seed(21)
     q = torch.randn(1, 12, 608, 128, generator=g).to(torch.bfloat16).to(dev)
     k = torch.randn(1, 12, 608, 128, generator=g).to(torch.bfloat16).to(dev)
@@ -212,7 +236,7 @@ def test_attention_vt_matches_attention(dev):
     bias = torch.zeros(608, device=dev)
     bias[-8:] = float("-inf")
     a = Fn.attention(q, k, v, key_bias=bias)
-    b = Fn.attention_vt(q, k, Fn.v_transpose(v), key_bias=bias)
+    b = Fn.attention_packed(q, Fn.kv_pack(k, v), 608, key_bias=bias)
     assert torch.equal(a, b)
 
 
