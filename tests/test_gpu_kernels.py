@@ -195,7 +195,7 @@ def test_gqa_prefill_workload(dev):
     (1, 2, 1, 1, 1, 128, True, False),
     (1, 2, 2, 200, 65, 128, False, True),
     (2, 7, 1, 64, 64, 64, True, False),
-    # grids of >= 512 workgroups take the single-key-group (128-query) variant
+    # large grids (several workgroups per CU)
     (4, 32, 8, 512, 512, 128, True, False),
     (4, 32, 32, 520, 520, 64, False, True),
 ])
