@@ -204,10 +204,14 @@ hipError_t rldx_attention_fwd_bf16(const void* q, const void* k, const void* v, 
 /*
  * Same operator with K and V already packed (packed_strides {batch, head}),
  * one launch.  Used on the MSAT path, where rldx_msat_qkv_norm_rope_bf16 writes
- * the packed tiles directly.
+ * the packed tiles directly.  out_packed != 0 (batch 1): O is written as the
+ * [seq_q, q_heads*head_dim] matrix in the packed activation order the grouped
+ * GEMM reads (o_strides ignored, o 16-byte aligned, rldx_act_packed_elems
+ * elements).
  */
 hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* kv_packed, const int64_t* packed_strides,
-                                          void* o, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                                          void* o, int32_t out_packed, int64_t batch, int64_t q_heads,
+                                          int64_t kv_heads, int64_t seq_q,
                                           int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
                                           const int64_t* o_strides, const float* key_bias,
                                           int64_t key_bias_batch_stride, float scale, int32_t causal,
@@ -239,6 +243,75 @@ hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv_row_stride
 
 /* Workspace bytes rldx_llm_fused_attention_bf16 needs (normalised K + packed K/V). */
 int64_t rldx_llm_fused_attention_workspace_bytes(int64_t seq, int64_t kv_heads, int64_t head_dim);
+
+/* ------------------------------------------------------------------------ */
+/* Grouped GEMM of the MSAT block linears                                   */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Packs a weight W [n, k] bf16 (row stride ldw elements, k contiguous) into
+ * the MFMA operand order rldx_grouped_gemm_bf16 reads (n*k elements): 1 KB
+ * chunk (nb, kb), nb-major, holds W[32 nb + l%32][16 kb + 8 (l/32) + i] at
+ * element (nb*(k/16) + kb)*512 + l*8 + i.  With swiglu_pairs != 0, W = [gate;
+ * up] (n = 2*N_half) and packed block 2p holds gate rows 32p.., block 2p+1 up
+ * rows N_half + 32p.. .  n % 32 == 0 (% 64 with swiglu_pairs), k % 16 == 0.
+ * No reference counterpart: one-time weight preparation.
+ */
+hipError_t rldx_gemm_pack_weight_bf16(const void* w, int64_t ldw, int64_t n, int64_t k, int32_t swiglu_pairs,
+                                      void* packed, hipStream_t stream);
+
+/*
+ * Packed activation order read by rldx_grouped_gemm_bf16 for its A operand:
+ * A [m, k] stored as 1 KB chunks (mb, kb), mb-major, chunk (mb, kb) at element
+ * (mb*(k/16) + kb)*512 holding A[32 mb + l%32][16 kb + 8 (l/32) + i] at l*8 + i.
+ * Rows are padded to a multiple of 32 (padding never reaches an output).
+ */
+int64_t rldx_act_packed_elems(int64_t m, int64_t k);
+
+/* Row-major x [m, k] (row stride ldx) -> packed activation order.  k % 16 == 0. */
+hipError_t rldx_act_pack_bf16(const void* x, int64_t ldx, int64_t m, int64_t k, void* packed, hipStream_t stream);
+
+/*
+ * LayerNorm without affine parameters, y = (x - mean) * rsqrt(var + eps) per
+ * row (fp32 statistics, one rounding), written in the packed activation order.
+ * k % 16 == 0, k <= 8192.
+ * Replaces: the pre-norms of an MSAT block, nn.LayerNorm(dim, elementwise_affine=False)
+ *   (rldx/model/modules/action_model/blocks.py:705-891; rldx/model/modules/action_model/msat.py:883-893).
+ */
+hipError_t rldx_layernorm_pack_bf16(const void* x, int64_t ldx, int64_t m, int64_t k, float eps, void* packed,
+                                    hipStream_t stream);
+
+/* One stream of a grouped GEMM. */
+typedef struct rldx_gemm_group {
+  const void* a_packed;  /* [m, k] bf16 activations in the packed activation order */
+  int64_t m;             /* rows (0: group skipped)                              */
+  const void* w_packed;  /* packed weight [n, k] of this stream                  */
+  const void* bias;      /* [n] bf16 or NULL ([gate; up] order for SwiGLU)       */
+  void* out;             /* [m, n] bf16 ([m, n/2] for SwiGLU), row stride ldo;   */
+                         /* packed activation order for SWIGLU_PACKED           */
+  int64_t ldo;
+  const void* residual;  /* [m, n] bf16, row stride ldr (RESIDUAL epilogue; may  */
+  int64_t ldr;           /* alias out)                                           */
+} rldx_gemm_group_t;
+
+#define RLDX_GEMM_EPI_BIAS 0     /* out = bf16(a W^T + bias)                      */
+#define RLDX_GEMM_EPI_RESIDUAL 1 /* out = bf16(residual + bf16(a W^T + bias))     */
+#define RLDX_GEMM_EPI_SWIGLU 2   /* out = swiglu(bf16(gate), bf16(up)), n/2 cols  */
+#define RLDX_GEMM_EPI_SWIGLU_PACKED 3 /* same, out in the packed activation order */
+
+/*
+ * y_s = a_s W_s^T (+ bias_s) with the epilogue above, for 1..3 groups that
+ * share n and k (the three streams of an MSAT block), fp32 accumulation.
+ * n % 64 == 0, k % 512 == 0.  Groups of more than 64 rows use 128-row tiles,
+ * the others 64-row tiles (two launches at most).  Deterministic.
+ * Replaces: the per-stream nn.Linear calls of an MSAT block
+ *   (rldx/model/modules/action_model/blocks.py:705-891), and
+ *   fused_mlp_swiglu(x, weight, bias) behind ss::fused_mlp_swiglu
+ *   (rldx/inference/action_model/single_stream/engine/kernels/fused_mlp_swiglu.py:199-267)
+ *   with the SwiGLU epilogue.
+ */
+hipError_t rldx_grouped_gemm_bf16(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, int64_t k,
+                                  int32_t epilogue, hipStream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Host-side diagnostics (no reference counterpart)                         */

@@ -105,6 +105,7 @@ struct AttnArgs {
   int64_t q_sb, q_sh, q_ss;
   int64_t kv_sb, kv_sh;  // element strides of the packed tiles per batch / kv head
   int64_t o_sb, o_sh, o_ss;
+  int64_t o_packed_k;  // > 0: O written as the packed activations of [sq, hq * D] (batch 1)
   const float* key_bias;  // [batch, sk] additive (natural-log units) or nullptr
   int64_t kb_sb;
   int hq, hkv, group, sq, sk;
@@ -424,7 +425,10 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
           uint2 wv;
           wv.x = static_cast<uint32_t>(f32_to_bf16_bits(acc[0])) | (static_cast<uint32_t>(f32_to_bf16_bits(acc[1])) << 16);
           wv.y = static_cast<uint32_t>(f32_to_bf16_bits(acc[2])) | (static_cast<uint32_t>(f32_to_bf16_bits(acc[3])) << 16);
-          *reinterpret_cast<uint2*>(orow + d) = wv;
+          if (a.o_packed_k > 0)  // 4 consecutive columns stay inside one 8-element run
+            *reinterpret_cast<uint2*>(a.o + packed_act_offset(q_idx[j], static_cast<int64_t>(h) * D + d, a.o_packed_k)) = wv;
+          else
+            *reinterpret_cast<uint2*>(orow + d) = wv;
         }
       }
     }
@@ -602,12 +606,17 @@ extern "C" hipError_t rldx_attention_kv_pack_bf16(const void* k, const int64_t* 
 }
 
 extern "C" hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* kv_packed,
-                                                     const int64_t* packed_strides, void* o, int64_t batch,
-                                                     int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k,
-                                                     int64_t head_dim, const int64_t* q_strides,
+                                                     const int64_t* packed_strides, void* o, int32_t out_packed,
+                                                     int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                                                     int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
                                                      const int64_t* o_strides, const float* key_bias,
                                                      int64_t key_bias_batch_stride, float scale, int32_t causal,
                                                      hipStream_t stream) {
+  const int64_t zero3[3] = {0, 0, 0};
+  if (out_packed) {
+    if (batch > 1 || reinterpret_cast<uintptr_t>(o) % 16) return hipErrorInvalidValue;
+    o_strides = zero3;
+  }
   hipError_t e = check_qo(q, o, batch, q_heads, kv_heads, seq_q, seq_k, head_dim, q_strides, o_strides, scale);
   if (e != hipSuccess || batch == 0 || q_heads == 0 || seq_q == 0) return e;
   if (!kv_packed || !packed_strides || !a16(kv_packed)) return hipErrorInvalidValue;
@@ -618,6 +627,7 @@ extern "C" hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* 
   if (key_bias && reinterpret_cast<uintptr_t>(key_bias) % 4) return hipErrorInvalidValue;
   AttnArgs a{};
   fill_qo(a, q, o, q_heads, kv_heads, seq_q, seq_k, q_strides, o_strides, key_bias, key_bias_batch_stride, scale);
+  a.o_packed_k = out_packed ? q_heads * head_dim : 0;
   a.kv = static_cast<const uint16_t*>(kv_packed);
   a.kv_sb = packed_strides[0];
   a.kv_sh = packed_strides[1];
@@ -641,7 +651,7 @@ extern "C" hipError_t rldx_attention_fwd_bf16(const void* q, const void* k, cons
   e = rldx_attention_kv_pack_bf16(k, k_strides, v, v_strides, workspace, ps, batch, kv_heads, seq_k, head_dim,
                                   stream);
   if (e != hipSuccess) return e;
-  return rldx_attention_packed_fwd_bf16(q, workspace, ps, o, batch, q_heads, kv_heads, seq_q, seq_k, head_dim,
+  return rldx_attention_packed_fwd_bf16(q, workspace, ps, o, 0, batch, q_heads, kv_heads, seq_q, seq_k, head_dim,
                                         q_strides, o_strides, key_bias, key_bias_batch_stride, scale, causal, stream);
 }
 

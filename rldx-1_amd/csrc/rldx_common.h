@@ -86,4 +86,11 @@ RLDX_HD uint16_t swiglu_bf16_bits(uint16_t g, uint16_t u) {
   return f32_to_bf16_bits(s * bf16_bits_to_f32(u));
 }
 
+// Element offset of A[row][col] in the packed activation order (the A operand
+// of the grouped GEMM) of a matrix with k columns: 1 KB chunk (row / 32,
+// col / 16), lane row % 32 + 32 * (col / 8 % 2), element col % 8.
+RLDX_HD int64_t packed_act_offset(int64_t row, int64_t col, int64_t k) {
+  return ((row >> 5) * (k >> 4) + (col >> 4)) * 512 + ((row & 31) + 32 * ((col >> 3) & 1)) * 8 + (col & 7);
+}
+
 }  // namespace rldx

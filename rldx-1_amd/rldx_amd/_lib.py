@@ -19,6 +19,21 @@ c_vp = ctypes.c_void_p
 c_i64p = ctypes.POINTER(ctypes.c_int64)
 
 
+class GemmGroup(ctypes.Structure):
+    """rldx_gemm_group_t"""
+
+    _fields_ = [
+        ("a_packed", ctypes.c_void_p),
+        ("m", ctypes.c_int64),
+        ("w_packed", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("ldo", ctypes.c_int64),
+        ("residual", ctypes.c_void_p),
+        ("ldr", ctypes.c_int64),
+    ]
+
+
 class MsatStream(ctypes.Structure):
     """Mirror of `rldx_msat_stream_t`."""
 
@@ -59,7 +74,7 @@ SIGNATURES = {
     ),
     "rldx_attention_packed_fwd_bf16": (
         c_i32,
-        [c_vp, c_vp, c_i64p, c_vp] + [c_i64] * 6 + [c_i64p] * 2 + [c_vp, c_i64, c_f32, c_i32, c_vp],
+        [c_vp, c_vp, c_i64p, c_vp, c_i32] + [c_i64] * 6 + [c_i64p] * 2 + [c_vp, c_i64, c_f32, c_i32, c_vp],
     ),
     "rldx_llm_fused_attention_bf16": (
         c_i32,
@@ -67,10 +82,16 @@ SIGNATURES = {
          c_i64, c_vp],
     ),
     "rldx_llm_fused_attention_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64]),
+    "rldx_gemm_pack_weight_bf16": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_i32, c_vp, c_vp]),
+    "rldx_act_packed_elems": (c_i64, [c_i64, c_i64]),
+    "rldx_act_pack_bf16": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp]),
+    "rldx_layernorm_pack_bf16": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_f32, c_vp, c_vp]),
+    "rldx_grouped_gemm_bf16": (c_i32, [ctypes.POINTER(GemmGroup), c_i32, c_i64, c_i64, c_i32, c_vp]),
     "rldx_host_swiglu_bf16": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64]),
 }
 
 ROPE_SIN_SIGNED = 1  # RLDX_ROPE_SIN_SIGNED
+GEMM_EPI_BIAS, GEMM_EPI_RESIDUAL, GEMM_EPI_SWIGLU, GEMM_EPI_SWIGLU_PACKED = 0, 1, 2, 3
 
 _lib = None
 _hip = None

@@ -341,10 +341,12 @@ def kv_pack(k: torch.Tensor, v: torch.Tensor, layout: str = "bhsd") -> torch.Ten
 
 def attention_packed(q: torch.Tensor, kvp: torch.Tensor, seq_k: int, *, key_bias: Optional[torch.Tensor] = None,
                      causal: bool = False, scale: Optional[float] = None, layout: str = "bhsd",
-                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     out=None):
     """Attention with K/V given as packed tiles [B, Hkv, >= kv_packed_elems(seq_k, D)]
-    (see kv_pack; the MSAT QKV kernel writes them directly)."""
-    _on_gpu(q, kvp, key_bias, out)
+    (see kv_pack; the MSAT QKV kernel writes them directly).  `out` may be a
+    PackedAct [Sq, Hq*D] (batch 1): O is then written in the grouped GEMM's
+    packed activation order."""
+    _on_gpu(q, kvp, key_bias)
     _require(q.dtype == BF16 and q.dim() == 4 and q.stride(-1) == 1, "q must be 4-D bf16, last dim contiguous")
     if layout == "bhsd":
         B, Hq, Sq, D = q.shape
@@ -357,18 +359,26 @@ def attention_packed(q: torch.Tensor, kvp: torch.Tensor, seq_k: int, *, key_bias
              kvp.shape[2] >= kv_packed_elems(seq_k, D), "kvp must be [B, Hkv, >= kv_packed_elems(seq_k, D)] bf16")
     Hkv = kvp.shape[1]
     _require(Hkv > 0 and Hq % Hkv == 0, "q heads must be a multiple of kv heads")
-    if out is None:
-        out = torch.empty_like(q, memory_format=torch.contiguous_format)
-    _require(out.shape == q.shape and out.dtype == BF16 and out.stride(-1) == 1, "out must match q")
+    packed_out = isinstance(out, PackedAct)
+    if packed_out:
+        _on_gpu(out.data)
+        _require(B == 1 and out.m == Sq and out.k == Hq * D, "packed out must be a PackedAct [Sq, Hq*D], batch 1")
+        o_ptr, o_strides = out.data.data_ptr(), [0, 0, 0]
+    else:
+        if out is None:
+            out = torch.empty_like(q, memory_format=torch.contiguous_format)
+        _on_gpu(out)
+        _require(out.shape == q.shape and out.dtype == BF16 and out.stride(-1) == 1, "out must match q")
+        o_ptr, o_strides = out.data_ptr(), _bhs_strides(out, layout)
     kb_ptr, kb_stride = _key_bias_args(key_bias, B, seq_k)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     lib = _lib.load()
     _lib.check(lib.rldx_attention_packed_fwd_bf16(q.data_ptr(), kvp.data_ptr(),
-                                                  _lib.i64_array([kvp.stride(0), kvp.stride(1)]), out.data_ptr(), B,
-                                                  Hq, Hkv, Sq, seq_k, D, _lib.i64_array(_bhs_strides(q, layout)),
-                                                  _lib.i64_array(_bhs_strides(out, layout)), kb_ptr, kb_stride,
-                                                  float(scale), int(bool(causal)), _stream_ptr(q)),
+                                                  _lib.i64_array([kvp.stride(0), kvp.stride(1)]), o_ptr,
+                                                  int(packed_out), B, Hq, Hkv, Sq, seq_k, D,
+                                                  _lib.i64_array(_bhs_strides(q, layout)), _lib.i64_array(o_strides),
+                                                  kb_ptr, kb_stride, float(scale), int(bool(causal)), _stream_ptr(q)),
                "rldx_attention_packed_fwd_bf16")
     return out
 
@@ -400,6 +410,125 @@ def llm_fused_attention(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: tor
                                                  out.data_ptr(), out.stride(0), M, Hq, Hkv, D, float(eps), ws.data_ptr(),
                                                  ws.numel() * 2, _stream_ptr(qkv)), "rldx_llm_fused_attention_bf16")
     return out
+
+
+# ---------------------------------------------------------------------------
+# grouped GEMM (MSAT block linears)
+# ---------------------------------------------------------------------------
+class PackedWeight:
+    """A weight W [n, k] bf16 packed once into the grouped GEMM's operand order."""
+
+    __slots__ = ("data", "n", "k", "swiglu_pairs")
+
+    def __init__(self, data: torch.Tensor, n: int, k: int, swiglu_pairs: bool):
+        self.data, self.n, self.k, self.swiglu_pairs = data, n, k, swiglu_pairs
+
+
+def pack_weight(w: torch.Tensor, swiglu_pairs: bool = False) -> PackedWeight:
+    """nn.Linear weight [out_features, in_features] bf16 -> PackedWeight.  With
+    swiglu_pairs, w = [gate; up] and the GEMM's SwiGLU epilogue can be used."""
+    _on_gpu(w)
+    _require(w.dtype == BF16 and w.dim() == 2 and w.stride(1) == 1, "weight must be 2-D bf16, rows contiguous")
+    n, k = w.shape
+    _require(n % (64 if swiglu_pairs else 32) == 0 and k % 16 == 0, "weight shape not tileable")
+    out = torch.empty(n * k, dtype=BF16, device=w.device)
+    lib = _lib.load()
+    _lib.check(lib.rldx_gemm_pack_weight_bf16(w.data_ptr(), w.stride(0), n, k, int(swiglu_pairs), out.data_ptr(),
+                                              _stream_ptr(w)), "rldx_gemm_pack_weight_bf16")
+    return PackedWeight(out, n, k, swiglu_pairs)
+
+
+class PackedAct:
+    """Activations [m, k] bf16 in the grouped GEMM's packed operand order
+    (32-row x 16-column chunks, rows padded to a multiple of 32)."""
+
+    __slots__ = ("data", "m", "k")
+
+    def __init__(self, data: torch.Tensor, m: int, k: int):
+        self.data, self.m, self.k = data, m, k
+
+    @staticmethod
+    def empty(m: int, k: int, device) -> "PackedAct":
+        return PackedAct(torch.empty((m + 31) // 32 * 32 * k, dtype=BF16, device=device), m, k)
+
+    def rows(self, start: int, stop: int) -> "PackedAct":
+        """Rows [start, stop) as a PackedAct view; start must be a multiple of 32."""
+        _require(start % 32 == 0 and 0 <= start <= stop <= self.m, "row range must start on a 32-row boundary")
+        return PackedAct(self.data[start * self.k:], stop - start, self.k)
+
+    def unpack(self) -> torch.Tensor:
+        """Row-major copy (for tests and debugging)."""
+        m, k = self.m, self.k
+        mp = (m + 31) // 32
+        t = self.data[: mp * 32 * k].view(mp, k // 16, 2, 32, 8)  # mb, kb, half, row, i
+        return t.permute(0, 3, 1, 2, 4).reshape(mp * 32, k)[:m]
+
+
+def pack_act(x: torch.Tensor, out: Optional[PackedAct] = None) -> PackedAct:
+    """Row-major x [m, k] -> PackedAct."""
+    _on_gpu(x)
+    _require(x.dtype == BF16 and x.dim() == 2 and x.stride(1) == 1, "x must be 2-D bf16, rows contiguous")
+    m, k = x.shape
+    out = PackedAct.empty(m, k, x.device) if out is None else out
+    _require(out.m == m and out.k == k, "out shape mismatch")
+    lib = _lib.load()
+    _lib.check(lib.rldx_act_pack_bf16(x.data_ptr(), x.stride(0), m, k, out.data.data_ptr(), _stream_ptr(x)),
+               "rldx_act_pack_bf16")
+    return out
+
+
+def layernorm_pack(x: torch.Tensor, eps: float = 1e-6, out: Optional[PackedAct] = None) -> PackedAct:
+    """LayerNorm without affine parameters over the last dim of x [m, k], packed."""
+    _on_gpu(x)
+    _require(x.dtype == BF16 and x.dim() == 2 and x.stride(1) == 1, "x must be 2-D bf16, rows contiguous")
+    m, k = x.shape
+    out = PackedAct.empty(m, k, x.device) if out is None else out
+    _require(out.m == m and out.k == k, "out shape mismatch")
+    lib = _lib.load()
+    _lib.check(lib.rldx_layernorm_pack_bf16(x.data_ptr(), x.stride(0), m, k, float(eps), out.data.data_ptr(),
+                                            _stream_ptr(x)), "rldx_layernorm_pack_bf16")
+    return out
+
+
+def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias") -> None:
+    """One launch (two when row counts differ a lot) of y_s = a_s W_s^T + bias_s for
+    up to 3 streams sharing n and k.  items: (a PackedAct [m, k] or row-major
+    tensor (packed first), PackedWeight, bias [n] or None, out, residual or None).
+    epilogue: "bias" (out = y), "residual" (out = residual + y, residual may be
+    out), "swiglu" (out [m, n/2] = swiglu(y)) or "swiglu_packed" (out a PackedAct)."""
+    epi = {"bias": _lib.GEMM_EPI_BIAS, "residual": _lib.GEMM_EPI_RESIDUAL, "swiglu": _lib.GEMM_EPI_SWIGLU,
+           "swiglu_packed": _lib.GEMM_EPI_SWIGLU_PACKED}[epilogue]
+    _require(1 <= len(items) <= 3, "between 1 and 3 groups")
+    n, k = items[0][1].n, items[0][1].k
+    groups = (_lib.GemmGroup * len(items))()
+    keep = []
+    for i, (a, w, bias, out, res) in enumerate(items):
+        if not isinstance(a, PackedAct):
+            a = pack_act(a)
+            keep.append(a)
+        _on_gpu(a.data, w.data, bias, res)
+        _require(w.n == n and w.k == k and a.k == k, "groups must share n and k")
+        _require(epi < _lib.GEMM_EPI_SWIGLU or w.swiglu_pairs, "SwiGLU epilogue needs a swiglu_pairs weight")
+        m = a.m
+        n_out = n // 2 if epi >= _lib.GEMM_EPI_SWIGLU else n
+        if epi == _lib.GEMM_EPI_SWIGLU_PACKED:
+            _require(isinstance(out, PackedAct) and out.m == m and out.k == n_out, "out must be a PackedAct [m, n/2]")
+            out_ptr, ldo = out.data.data_ptr(), 0
+        else:
+            _require(out.dtype == BF16 and out.dim() == 2 and out.stride(1) == 1 and tuple(out.shape) == (m, n_out),
+                     "out must be [m, n_out] bf16")
+            out_ptr, ldo = out.data_ptr(), out.stride(0)
+        if bias is not None:
+            _require(bias.dtype == BF16 and bias.is_contiguous() and bias.numel() == n, "bias must be [n] bf16")
+        if epi == _lib.GEMM_EPI_RESIDUAL:
+            _require(res is not None and res.dtype == BF16 and res.dim() == 2 and res.stride(1) == 1 and
+                     tuple(res.shape) == (m, n), "residual must be [m, n] bf16")
+        groups[i] = _lib.GemmGroup(a.data.data_ptr(), m, w.data.data_ptr(), _ptr(bias), out_ptr, ldo,
+                                   _ptr(res) if epi == _lib.GEMM_EPI_RESIDUAL else None,
+                                   res.stride(0) if epi == _lib.GEMM_EPI_RESIDUAL else 0)
+    lib = _lib.load()
+    _lib.check(lib.rldx_grouped_gemm_bf16(groups, len(items), n, k, epi, _stream_ptr(w.data)),
+               "rldx_grouped_gemm_bf16")
 
 
 def mask_to_key_bias(kv_mask: torch.Tensor) -> torch.Tensor:

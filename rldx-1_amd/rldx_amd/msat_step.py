@@ -19,10 +19,11 @@ rldx/inference/action_model/model/graph_safe_action_model.py:430-485):
     SA tokens = ActionIn(x_t) + temb[t] + pos     (temb precomputed per step)
     v         = ActionOut(LayerNorm(SA out));   x_{t+1} = x_t + dt * v
 
-GEMMs run on hipBLASLt through torch.addmm; the named operators (QK-RMSNorm +
-RoPE, joint attention, SwiGLU) run on the rldx_amd HIP kernels.  Activations of
-the three streams share one [608, 1536] buffer (rows VL | SA | P) so every
-row-wise kernel is one launch for all streams.
+Every block runs on the rldx_amd HIP kernels (LayerNorm, grouped GEMMs with
+fused bias / residual / SwiGLU epilogues, QK-RMSNorm + RoPE, joint attention);
+only the tiny action in/out projections around the blocks use torch.addmm.
+Activations of the three streams share one [608, 1536] buffer (rows VL | SA |
+P) so every launch covers all streams.
 """
 
 from __future__ import annotations
@@ -147,7 +148,18 @@ def make_inputs(cfg: MsatStepCfg, device) -> dict:
 
 class MsatActionStep:
     """Static-buffer executor of one action step; `run()` launches it eagerly,
-    `capture()` records the same launches into one hipGraph."""
+    `capture()` records the same launches into one hipGraph.
+
+    Per block, every launch covers all three streams:
+        LayerNorm -> packed h          rldx_layernorm_pack_bf16
+        QKV linears (+ bias)           rldx_grouped_gemm_bf16
+        QK-RMSNorm + RoPE, K/V tiles   rldx_msat_qkv_norm_rope_bf16
+        joint attention -> packed o    rldx_attention_packed_fwd_bf16
+        Proj linears, x += (in place)  rldx_grouped_gemm_bf16 (residual epilogue)
+        LayerNorm -> packed h
+        W12 linears + SwiGLU -> packed rldx_grouped_gemm_bf16 (SwiGLU epilogue)
+        W3 linears, x += (in place)    rldx_grouped_gemm_bf16 (residual epilogue)
+    The weights are packed once, at construction, into the GEMM's operand order."""
 
     def __init__(self, cfg: MsatStepCfg, weights: dict, inputs: dict):
         self.cfg, self.w, self.inp = cfg, weights, inputs
@@ -158,22 +170,26 @@ class MsatActionStep:
         self.qkv = e(n, 3 * cfg.inner)
         self.q = e(H, n, D)
         self.kvp = e(H, Fn.kv_packed_elems(n, D))  # K/V in the attention kernel's packed tiles
-        self.att = e(n, H, D)       # attention output, token-major
-        self.y = e(n, d)            # projection / FFN output
-        self.u = e(n, 2 * cfg.ffn)  # w12 output
-        self.gl = e(n, cfg.ffn)     # SwiGLU output
+        self.h = Fn.PackedAct.empty(n, d, dev)           # LayerNorm output, GEMM operand order
+        self.att = Fn.PackedAct.empty(n, cfg.inner, dev)  # attention output, GEMM operand order
+        self.gl = Fn.PackedAct.empty(n, cfg.ffn, dev)     # SwiGLU output, GEMM operand order
         self.act = e(cfg.n_sa, cfg.action_dim)   # x_t, updated in place
         self.vel = e(cfg.n_sa, cfg.action_dim)
         self.sa_in = e(cfg.n_sa, d)
+        self.pw = {}
+        for s in STREAMS:
+            for name in ("qkv", "proj", "w12", "w3"):
+                self.pw[f"{s}.{name}"] = [Fn.pack_weight(weights[f"{s}.{name}.w"][L], swiglu_pairs=(name == "w12"))
+                                          for L in range(cfg.blocks)]
         self.graph = None
 
     # -- one block -----------------------------------------------------------
     def _block(self, L: int) -> None:
-        cfg, w = self.cfg, self.w
-        h = F.layer_norm(self.x, (cfg.hidden,), eps=cfg.eps)
-        for s in STREAMS:
-            r = cfg.rows(s)
-            torch.addmm(w[f"{s}.qkv.b"][L], h[r], w[f"{s}.qkv.w"][L].t(), out=self.qkv[r])
+        cfg, w, pw = self.cfg, self.w, self.pw
+        rows = [(s, cfg.rows(s)) for s in STREAMS]
+        Fn.layernorm_pack(self.x, cfg.eps, out=self.h)
+        Fn.grouped_gemm([(self.h.rows(r.start, r.stop), pw[f"{s}.qkv"][L], w[f"{s}.qkv.b"][L], self.qkv[r], None)
+                         for s, r in rows], "bias")
         specs = [
             Fn.StreamSpec(self.qkv[cfg.rows("vl")], w["vl.q_norm"][L], w["vl.k_norm"][L]),
             Fn.StreamSpec(self.qkv[cfg.rows("sa")], w["sa.q_norm"][L], w["sa.k_norm"][L],
@@ -183,21 +199,14 @@ class MsatActionStep:
         ]
         Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
         Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), cfg.tokens, key_bias=self.inp["key_bias"],
-                            out=self.att.unsqueeze(0).permute(0, 2, 1, 3))
-        att2 = self.att.view(cfg.tokens, cfg.inner)
-        for s in STREAMS:
-            r = cfg.rows(s)
-            torch.addmm(w[f"{s}.proj.b"][L], att2[r], w[f"{s}.proj.w"][L].t(), out=self.y[r])
-        self.x.add_(self.y)
-        h = F.layer_norm(self.x, (cfg.hidden,), eps=cfg.eps)
-        for s in STREAMS:
-            r = cfg.rows(s)
-            torch.addmm(w[f"{s}.w12.b"][L], h[r], w[f"{s}.w12.w"][L].t(), out=self.u[r])
-        Fn.swiglu(self.u, out=self.gl)
-        for s in STREAMS:
-            r = cfg.rows(s)
-            torch.addmm(w[f"{s}.w3.b"][L], self.gl[r], w[f"{s}.w3.w"][L].t(), out=self.y[r])
-        self.x.add_(self.y)
+                            out=self.att)
+        Fn.grouped_gemm([(self.att.rows(r.start, r.stop), pw[f"{s}.proj"][L], w[f"{s}.proj.b"][L], self.x[r],
+                          self.x[r]) for s, r in rows], "residual")
+        Fn.layernorm_pack(self.x, cfg.eps, out=self.h)
+        Fn.grouped_gemm([(self.h.rows(r.start, r.stop), pw[f"{s}.w12"][L], w[f"{s}.w12.b"][L],
+                          self.gl.rows(r.start, r.stop), None) for s, r in rows], "swiglu_packed")
+        Fn.grouped_gemm([(self.gl.rows(r.start, r.stop), pw[f"{s}.w3"][L], w[f"{s}.w3.b"][L], self.x[r], self.x[r])
+                         for s, r in rows], "residual")
 
     # -- one action step ------------------------------------------------------
     def run(self, steps: int | None = None, blocks: int | None = None) -> torch.Tensor:

@@ -94,7 +94,10 @@ def test_capi_rejects_bad_arguments_without_launching():
                                        need, None) == HIP_INVALID_VALUE
     # packed head stride shorter than the tiles of seq_k = 40 (2 tiles)
     ps = _lib.i64_array([0, 64 * 128])
-    assert lib.rldx_attention_packed_fwd_bf16(16, 16, ps, 16, 1, 2, 2, 4, 40, 128, st, st, None, 0, 1.0, 0,
+    assert lib.rldx_attention_packed_fwd_bf16(16, 16, ps, 16, 0, 1, 2, 2, 4, 40, 128, st, st, None, 0, 1.0, 0,
+                                              None) == HIP_INVALID_VALUE
+    # packed output needs batch 1
+    assert lib.rldx_attention_packed_fwd_bf16(16, 16, ps, 16, 1, 2, 2, 2, 4, 32, 128, st, st, None, 0, 1.0, 0,
                                               None) == HIP_INVALID_VALUE
     assert lib.rldx_attention_kv_pack_bf16(16, st, 16, st, 16, ps, 1, 1, 40, 128, None) == HIP_INVALID_VALUE
     assert lib.rldx_msat_qkv_norm_rope_bf16(None, 1, 12, 128, 16, 16, 16, 0, 0, None, 0, 1e-6,
@@ -107,7 +110,7 @@ def test_capi_rejects_bad_arguments_without_launching():
                                             1e-6, None) == HIP_INVALID_VALUE
     # empty key set with queries present
     ps = _lib.i64_array([0, 0])
-    assert lib.rldx_attention_packed_fwd_bf16(16, 16, ps, 16, 1, 2, 2, 4, 0, 128, st, st, None, 0, 1.0, 0,
+    assert lib.rldx_attention_packed_fwd_bf16(16, 16, ps, 16, 0, 1, 2, 2, 4, 0, 128, st, st, None, 0, 1.0, 0,
                                               None) == HIP_INVALID_VALUE
     assert lib.rldx_qk_rmsnorm_rope_half_f32(16, 16, 16, 16, 16, 16, 16, 16, 1, 4, 2, 2, 96, st, st, st, st, st,
                                              1e-6, 0, None) == HIP_INVALID_VALUE

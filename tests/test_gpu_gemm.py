@@ -1,0 +1,161 @@
+"""GPU parity tests of the grouped GEMM (MSAT block linears) through the C ABI.
+
+Reference: the same GEMM in fp32 on the CPU from the same bf16 operands, then
+the eager rounding chain (bf16 output; residual add in bf16; SwiGLU of the bf16
+gate / up values with the oracle's SwiGLU).  Tolerance: bf16 max-abs <= 2e-2 and
+relative L2 <= 1e-2 (accumulation order differs from the CPU's).
+"""
+
+import pytest
+import torch
+
+from oracle import cpu_reference as ref
+from rldx_amd import functional as Fn
+from tolerances import assert_bf16_close
+
+pytestmark = pytest.mark.gpu
+BF16 = torch.bfloat16
+
+
+def packed_weight_layout(w: torch.Tensor, swiglu_pairs: bool) -> torch.Tensor:
+    """CPU construction of the packed weight from its definition: chunk (nb, kb),
+    lane l, element i = W[row(nb, l % 32)][16 kb + 8 (l // 32) + i], where row is
+    32 nb + l % 32, or with swiglu_pairs (nb % 2) * n/2 + 32 (nb // 2) + l % 32."""
+    n, k = w.shape
+    nb = torch.arange(n // 32)[:, None, None, None]
+    kb = torch.arange(k // 16)[None, :, None, None]
+    lane = torch.arange(64)[None, None, :, None]
+    i = torch.arange(8)[None, None, None, :]
+    if swiglu_pairs:
+        row = (nb % 2) * (n // 2) + 32 * (nb // 2) + lane % 32
+    else:
+        row = 32 * nb + lane % 32
+    col = 16 * kb + 8 * (lane // 32) + i
+    return w[row.expand(-1, k // 16, 64, 8), col.expand(n // 32, -1, 64, 8)].reshape(-1)
+
+
+def _rand(shape, g, std=1.0):
+    return (std * torch.randn(*shape, generator=g)).to(BF16)
+
+
+def _linear_ref(a, w, bias):
+    y = a.float() @ w.float().t()
+    if bias is not None:
+        y = y + bias.float()
+    return y.to(BF16)
+
+
+@pytest.mark.parametrize("n,k,pairs", [(4608, 1536, False), (192, 512, False), (8192, 1536, True)])
+def test_pack_weight_layout(dev, n, k, pairs):
+    g = torch.Generator().manual_seed(n + k)
+    w = _rand((n, k), g)
+    p = Fn.pack_weight(w.to(dev), swiglu_pairs=pairs)
+    assert torch.equal(p.data.cpu(), packed_weight_layout(w, pairs))
+
+
+@pytest.mark.parametrize("ms,n,k", [((512, 64, 32), 4608, 1536), ((5, 100, 130), 192, 512), ((1,), 64, 512)])
+def test_grouped_gemm_bias(dev, ms, n, k):
+    g = torch.Generator().manual_seed(sum(ms) + n)
+    items, refs = [], []
+    for m in ms:
+        a, w, b = _rand((m, k), g), _rand((n, k), g, 0.02), _rand((n,), g, 0.1)
+        out = torch.empty(m, n, dtype=BF16, device=dev)
+        items.append((a.to(dev), Fn.pack_weight(w.to(dev)), b.to(dev), out, None))
+        refs.append(_linear_ref(a, w, b))
+    Fn.grouped_gemm(items, "bias")
+    for (_, _, _, out, _), r in zip(items, refs):
+        assert_bf16_close(out, r, "grouped gemm")
+
+
+def test_grouped_gemm_residual_in_place(dev):
+    """x_s += W3_s(h_s): K = 4096, the output aliases the residual (rows of one buffer)."""
+    g = torch.Generator().manual_seed(7)
+    n, k = 1536, 4096
+    x = _rand((608, n), g)
+    h = _rand((608, k), g)
+    xd, hd = x.to(dev), h.to(dev)
+    items, refs = [], []
+    for lo, hi in ((0, 512), (512, 576), (576, 608)):
+        w, b = _rand((n, k), g, 0.02), _rand((n,), g, 0.1)
+        items.append((hd[lo:hi], Fn.pack_weight(w.to(dev)), b.to(dev), xd[lo:hi], xd[lo:hi]))
+        refs.append((x[lo:hi].float() + _linear_ref(h[lo:hi], w, b).float()).to(BF16))
+    Fn.grouped_gemm(items, "residual")
+    assert_bf16_close(xd, torch.cat(refs), "residual gemm")
+
+
+def test_grouped_gemm_swiglu(dev):
+    g = torch.Generator().manual_seed(9)
+    n, k = 8192, 1536
+    items, refs = [], []
+    for m in (512, 64, 32):
+        a, w, b = _rand((m, k), g), _rand((n, k), g, 0.02), _rand((n,), g, 0.1)
+        out = torch.empty(m, n // 2, dtype=BF16, device=dev)
+        items.append((a.to(dev), Fn.pack_weight(w.to(dev), swiglu_pairs=True), b.to(dev), out, None))
+        refs.append(ref.swiglu(_linear_ref(a, w, b)))
+    Fn.grouped_gemm(items, "swiglu")
+    for (_, _, _, out, _), r in zip(items, refs):
+        assert_bf16_close(out, r, "gemm + swiglu")
+
+
+def test_grouped_gemm_deterministic(dev):
+    g = torch.Generator().manual_seed(3)
+    a = _rand((512, 1536), g).to(dev)
+    w = Fn.pack_weight(_rand((1536, 1536), g, 0.02).to(dev))
+    o1 = torch.empty(512, 1536, dtype=BF16, device=dev)
+    o2 = torch.empty_like(o1)
+    Fn.grouped_gemm([(a, w, None, o1, None)])
+    Fn.grouped_gemm([(a, w, None, o2, None)])
+    assert torch.equal(o1, o2)
+
+
+@pytest.mark.parametrize("m,k", [(608, 1536), (5, 4096), (33, 64)])
+def test_act_pack_roundtrip(dev, m, k):
+    g = torch.Generator().manual_seed(m + k)
+    x = _rand((m, k + 8), g)[:, :k]  # strided rows
+    p = Fn.pack_act(x.to(dev))
+    assert torch.equal(p.unpack().cpu(), x)
+    # layout definition, element by element, on a few rows
+    d = p.data.cpu()
+    for r in (0, m - 1, m // 2):
+        for c in (0, k - 1, k // 3):
+            off = ((r // 32) * (k // 16) + c // 16) * 512 + ((r % 32) + 32 * ((c // 8) % 2)) * 8 + c % 8
+            assert d[off] == x[r, c]
+
+
+@pytest.mark.parametrize("m,k", [(608, 1536), (7, 4096), (64, 512)])
+def test_layernorm_pack(dev, m, k):
+    g = torch.Generator().manual_seed(k - m)
+    x = (3 * torch.randn(m, k, generator=g) + 0.5).to(BF16)
+    p = Fn.layernorm_pack(x.to(dev), 1e-6)
+    r = torch.nn.functional.layer_norm(x, (k,), eps=1e-6)
+    assert_bf16_close(p.unpack(), r, "layernorm")
+
+
+def test_swiglu_packed_epilogue_matches_row_major(dev):
+    g = torch.Generator().manual_seed(13)
+    n, k = 8192, 1536
+    a = _rand((608, k), g).to(dev)
+    w = Fn.pack_weight(_rand((n, k), g, 0.02).to(dev), swiglu_pairs=True)
+    b = _rand((n,), g, 0.1).to(dev)
+    ap = Fn.pack_act(a)
+    rm = torch.empty(608, n // 2, dtype=BF16, device=dev)
+    pk = Fn.PackedAct.empty(608, n // 2, dev)
+    rows = ((0, 512), (512, 576), (576, 608))
+    Fn.grouped_gemm([(ap.rows(lo, hi), w, b, rm[lo:hi], None) for lo, hi in rows], "swiglu")
+    Fn.grouped_gemm([(ap.rows(lo, hi), w, b, pk.rows(lo, hi), None) for lo, hi in rows], "swiglu_packed")
+    assert torch.equal(pk.unpack(), rm)
+
+
+def test_attention_packed_output(dev):
+    g = torch.Generator().manual_seed(17)
+    H, S, D = 12, 608, 128
+    q = torch.randn(1, H, S, D, generator=g).to(BF16).to(dev)
+    k = torch.randn(1, H, S, D, generator=g).to(BF16).to(dev)
+    v = torch.randn(1, H, S, D, generator=g).to(BF16).to(dev)
+    bias = torch.zeros(S, device=dev)
+    bias[-8:] = float("-inf")
+    kvp = Fn.kv_pack(k, v)
+    o = torch.empty(1, S, H, D, dtype=BF16, device=dev)
+    Fn.attention_packed(q, kvp, S, key_bias=bias, out=o.permute(0, 2, 1, 3))
+    op = Fn.attention_packed(q, kvp, S, key_bias=bias, out=Fn.PackedAct.empty(S, H * D, dev))
+    assert torch.equal(op.unpack(), o.view(S, H * D))
