@@ -245,6 +245,208 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
 
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// s_waitcnt vmcnt(N), every other counter left alone (gfx9 encoding)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit field");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// Epilogue of one 32x32 accumulator block (row block rb, packed column block cb).
+template <int EPI>
+__device__ __forceinline__ void store_block(const Group& G, const floatx16& acc, int rb, int cb, int lane) {
+  const int l32 = lane & 31, g = lane >> 5;
+  const int col = 32 * cb + l32;
+  const float bias = G.bias ? bf(G.bias[col]) : 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int row = 32 * rb + 8 * (e >> 2) + 4 * g + (e & 3);
+    if (row < G.m) {
+      uint16_t y = f32_to_bf16_bits(acc[e] + bias);
+      if constexpr (EPI == kEpiResidual) y = f32_to_bf16_bits(bf(G.res[static_cast<int64_t>(row) * G.ldr + col]) + bf(y));
+      G.out[static_cast<int64_t>(row) * G.ldo + col] = y;
+    }
+  }
+}
+
+// SwiGLU epilogue of a (gate, up) pair of 32x32 blocks: packed column blocks
+// 2p and 2p+1 hold gate columns 32p.. and up columns n/2 + 32p.. .
+template <int EPI>
+__device__ __forceinline__ void store_swiglu_pair(const Group& G, int n, const floatx16& ga, const floatx16& ua,
+                                                  int rb, int p, int lane) {
+  const int l32 = lane & 31, g = lane >> 5;
+  const int nh = n / 2, col = 32 * p + l32;
+  const float bg = G.bias ? bf(G.bias[col]) : 0.f;
+  const float bu = G.bias ? bf(G.bias[nh + col]) : 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int row = 32 * rb + 8 * (e >> 2) + 4 * g + (e & 3);
+    if (row < G.m) {
+      const uint16_t y = swiglu_bf16_bits(f32_to_bf16_bits(ga[e] + bg), f32_to_bf16_bits(ua[e] + bu));
+      if constexpr (EPI == kEpiSwigluPacked)
+        G.out[packed_act_offset(row, col, nh)] = y;
+      else
+        G.out[static_cast<int64_t>(row) * G.ldo + col] = y;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Large-M path (the 512-token stream): a workgroup computes a (32 TMB) x
+// (32 TNB) tile with its 4 waves in a 2 x 2 arrangement, each wave a
+// (32 TMB/2) x (32 TNB/2) sub-tile over the whole K range, so no cross-wave
+// reduction is needed.  Per k-step the workgroup moves TMB + TNB 1 KB operand
+// chunks global -> LDS with direct-to-LDS buffer loads (no VGPR staging) into a
+// P-stage ring, and each operand chunk is then read from LDS by the two waves
+// that share it: L2 -> CU traffic per MFMA is halved against per-wave loads.
+// Synchronisation per stage: wait for the own loads of the stage, one barrier
+// (all waves' loads landed, and all waves done with the ring slot refilled
+// next), then the loads P-1 stages ahead.  Loads past the last stage re-read it
+// (in bounds), so the wait counts are constants.
+// ---------------------------------------------------------------------------
+template <int TMB, int TNB, int U, int P, int EPI>
+__global__ __launch_bounds__(256, 2) void gemm_lds_kernel(GemmArgs a) {
+  constexpr int WM = TMB / 2, WN = TNB / 2;  // per-wave m / column blocks
+  constexpr int CH = TMB + TNB;              // 1 KB operand chunks per k-step
+  constexpr int PER_WAVE = CH * U / 4;       // chunks each wave moves per stage
+  constexpr int STAGE = CH * U * 1024;
+  static_assert((CH * U) % 4 == 0, "stage chunks split evenly over 4 waves");
+  static_assert((EPI != kEpiSwiglu && EPI != kEpiSwigluPacked) || WN % 2 == 0, "SwiGLU pairs per wave");
+  __shared__ __attribute__((aligned(1024))) unsigned char ring[P * STAGE];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  int item;
+  {
+    const int total = static_cast<int>(gridDim.x);
+    const int i = static_cast<int>(blockIdx.x);
+    const int per = total / kXcds, rem = total % kXcds;
+    const int xcd = i % kXcds, kk = i / kXcds;
+    item = xcd < rem ? xcd * (per + 1) + kk : rem * (per + 1) + (xcd - rem) * per + kk;
+  }
+  int gi = 0;
+  if (a.num_groups > 1 && item >= a.item_end[0]) gi = 1;
+  if (a.num_groups > 2 && item >= a.item_end[1]) gi = 2;
+  const Group& G = a.g[gi];
+  const int local = item - (gi ? a.item_end[gi - 1] : 0);
+  const int mt = local % a.m_tiles[gi], nt = local / a.m_tiles[gi];
+  const int ksteps = a.k / 16;
+  const int stages = ksteps / U;
+  const int mblocks = (G.m + 31) / 32;
+
+  const __amdgpu_buffer_rsrc_t ar =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(G.a), 0, mblocks * ksteps * 1024, kBufWord3);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(G.w + static_cast<int64_t>(nt * TNB) * ksteps * 512), 0, TNB * ksteps * 1024, kBufWord3);
+  const int voff = lane * 16;
+
+  auto issue = [&](int st) {
+    const int sc = min(st, stages - 1);
+    unsigned char* base = ring + (st % P) * STAGE;
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+      const int q = wave * PER_WAVE + i;  // chunk of the stage: k-step q / CH, operand q % CH
+      const int c = q % CH;
+      const int ks = sc * U + q / CH;
+      const lds_ptr_t dst = (lds_ptr_t)(base + q * 1024);
+      if (c < TMB)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, dst, 16, voff, (min(mt * TMB + c, mblocks - 1) * ksteps + ks) * 1024,
+                                                 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, dst, 16, voff, ((c - TMB) * ksteps + ks) * 1024, 0, 0);
+    }
+  };
+
+  floatx16 acc[WM][WN];
+#pragma unroll
+  for (int mb = 0; mb < WM; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < WN; ++nb) acc[mb][nb] = floatx16{};
+
+  auto compute = [&](int st) {
+    const unsigned char* base = ring + (st % P) * STAGE + lane * 16;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      u32x4 av[WM], wv[WN];
+#pragma unroll
+      for (int mb = 0; mb < WM; ++mb) av[mb] = *reinterpret_cast<const u32x4*>(base + (u * CH + wm * WM + mb) * 1024);
+#pragma unroll
+      for (int nb = 0; nb < WN; ++nb)
+        wv[nb] = *reinterpret_cast<const u32x4*>(base + (u * CH + TMB + wn * WN + nb) * 1024);
+#pragma unroll
+      for (int mb = 0; mb < WM; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < WN; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av[mb]),
+                                                                __builtin_bit_cast(bf16x8, wv[nb]), acc[mb][nb], 0, 0,
+                                                                0);
+    }
+  };
+
+  for (int st = 0; st < P - 1; ++st) issue(st);
+  for (int st = 0; st < stages; ++st) {
+    wait_vmcnt<(P - 2) * PER_WAVE>();  // this wave's loads of stage st have landed
+    __builtin_amdgcn_s_barrier();      // ... and every wave's; slot (st - 1) % P is free
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    issue(st + P - 1);
+    compute(st);
+  }
+  wait_vmcnt<0>();
+
+  const int rb0 = mt * TMB + wm * WM, cb0 = nt * TNB + wn * WN;
+  if constexpr (EPI == kEpiSwiglu || EPI == kEpiSwigluPacked) {
+#pragma unroll
+    for (int mb = 0; mb < WM; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < WN; nb += 2)
+        store_swiglu_pair<EPI>(G, a.n, acc[mb][nb], acc[mb][nb + 1], rb0 + mb, (cb0 + nb) / 2, lane);
+  } else {
+#pragma unroll
+    for (int mb = 0; mb < WM; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < WN; ++nb) store_block<EPI>(G, acc[mb][nb], rb0 + mb, cb0 + nb, lane);
+  }
+}
+
+
+
+template <int TMB, int TNB, int U, int P>
+hipError_t launch_lds_groups(const rldx_gemm_group_t* gs, const int* idx, int count, int64_t n, int64_t k, int epi,
+                             hipStream_t stream) {
+  if (count == 0) return hipSuccess;
+  GemmArgs a{};
+  a.num_groups = count;
+  a.n = static_cast<int>(n);
+  a.k = static_cast<int>(k);
+  const int n_tiles = static_cast<int>(n / (32 * TNB));
+  int64_t items = 0;
+  for (int j = 0; j < count; ++j) {
+    const rldx_gemm_group_t& s = gs[idx[j]];
+    a.g[j] = Group{static_cast<const uint16_t*>(s.a_packed), static_cast<int>(s.m),
+                   static_cast<const uint16_t*>(s.w_packed), static_cast<const uint16_t*>(s.bias),
+                   static_cast<uint16_t*>(s.out), s.ldo, static_cast<const uint16_t*>(s.residual), s.ldr};
+    a.m_tiles[j] = static_cast<int>((s.m + 32 * TMB - 1) / (32 * TMB));
+    items += static_cast<int64_t>(a.m_tiles[j]) * n_tiles;
+    if (items > (int64_t{1} << 31) - 1) return hipErrorInvalidValue;
+    a.item_end[j] = static_cast<int>(items);
+  }
+  const dim3 grid(static_cast<unsigned>(items)), block(256);
+  if (epi == kEpiBias)
+    hipLaunchKernelGGL((gemm_lds_kernel<TMB, TNB, U, P, kEpiBias>), grid, block, 0, stream, a);
+  else if (epi == kEpiResidual)
+    hipLaunchKernelGGL((gemm_lds_kernel<TMB, TNB, U, P, kEpiResidual>), grid, block, 0, stream, a);
+  else if (epi == kEpiSwiglu)
+    hipLaunchKernelGGL((gemm_lds_kernel<TMB, TNB, U, P, kEpiSwiglu>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((gemm_lds_kernel<TMB, TNB, U, P, kEpiSwigluPacked>), grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
 template <int MB, int NB, int U>
 hipError_t launch_groups(const rldx_gemm_group_t* gs, const int* idx, int count, int64_t n, int64_t k, int epi,
                          hipStream_t stream) {
@@ -398,7 +600,7 @@ extern "C" hipError_t rldx_grouped_gemm_bf16(const rldx_gemm_group_t* groups, in
   if (n > (1 << 30) || k > (1 << 30)) return hipErrorInvalidValue;
   const bool swiglu = epilogue == kEpiSwiglu || epilogue == kEpiSwigluPacked;
   const int64_t n_out = swiglu ? n / 2 : n;
-  int big[3], small[3], nb = 0, ns = 0;
+  int order[3], cnt = 0;
   for (int i = 0; i < num_groups; ++i) {
     const rldx_gemm_group_t& s = groups[i];
     if (s.m < 0 || s.m > (1 << 24)) return hipErrorInvalidValue;
@@ -411,18 +613,19 @@ extern "C" hipError_t rldx_grouped_gemm_bf16(const rldx_gemm_group_t* groups, in
       return hipErrorInvalidValue;
     if (epilogue != kEpiSwigluPacked && s.ldo < n_out) return hipErrorInvalidValue;
     if (epilogue == kEpiResidual && (!s.residual || s.ldr < n_out)) return hipErrorInvalidValue;
-    if (s.m > 64)
-      big[nb++] = i;
-    else
-      small[ns++] = i;
+    order[cnt++] = i;
   }
-  // 128-row tiles for the big (MFMA-bound) groups; 64-row tiles, 32-column
-  // tiles where the epilogue allows and deeper prefetch for the small
-  // (weight-streaming) groups.
-  hipError_t e = launch_groups<4, 2, 4>(groups, big, nb, n, k, epilogue, stream);
-  if (e != hipSuccess) return e;
-  if (swiglu) return launch_groups<2, 2, 4>(groups, small, ns, n, k, epilogue, stream);
-  return launch_groups<2, 1, 8>(groups, small, ns, n, k, epilogue, stream);
+  // One launch for all groups, smallest first: the weight-streaming tiles of
+  // the short streams are dispatched first and overlap the MFMA-bound tiles of
+  // the long one.  64 x 64 tiles: measured best for the MSAT shapes (enough
+  // workgroups to fill 256 CUs twice over, two workgroups per CU).
+  for (int i = 1; i < cnt; ++i)
+    for (int j = i; j > 0 && groups[order[j]].m < groups[order[j - 1]].m; --j) {
+      const int t = order[j];
+      order[j] = order[j - 1];
+      order[j - 1] = t;
+    }
+  return launch_groups<2, 2, 4>(groups, order, cnt, n, k, epilogue, stream);
 }
 
 extern "C" int64_t rldx_act_packed_elems(int64_t m, int64_t k) {

@@ -71,12 +71,15 @@ def test_grouped_gemm_residual_in_place(dev):
     """x_s += W3_s(h_s): K = 4096, the output aliases the residual (rows of one buffer)."""
     g = torch.Generator().manual_seed(7)
     n, k = 1536, 4096
-    x = _rand((608, n), g)
+    # unit-scale data (|out| < 4): the absolute bf16 bound of 2e-2 is below one
+    # bf16 ulp from magnitude 4 on, where any change of accumulation order can
+    # flip a rounding
+    x = _rand((608, n), g, 0.5)
     h = _rand((608, k), g)
     xd, hd = x.to(dev), h.to(dev)
     items, refs = [], []
     for lo, hi in ((0, 512), (512, 576), (576, 608)):
-        w, b = _rand((n, k), g, 0.02), _rand((n,), g, 0.1)
+        w, b = _rand((n, k), g, 0.008), _rand((n,), g, 0.1)
         items.append((hd[lo:hi], Fn.pack_weight(w.to(dev)), b.to(dev), xd[lo:hi], xd[lo:hi]))
         refs.append((x[lo:hi].float() + _linear_ref(h[lo:hi], w, b).float()).to(BF16))
     Fn.grouped_gemm(items, "residual")
