@@ -136,7 +136,16 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
     for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = floatx16{};
 
   u32x4 wa[U][NB], xa[U][MB], wb[U][NB], xb[U][MB];
-  auto load = [&](u32x4(&w)[U][NB], u32x4(&x)[U][MB], int kb) {  // kb: first k-step of the stage, wave-relative
+  // Workgroups start their K walk at different stages (rotated by column tile):
+  // the activation chunks are shared by every column tile, and workgroups that
+  // walk K in lockstep request the same chunk at the same time, all from one
+  // L2 channel.  The summation order stays fixed per tile.
+  const int stages = kw / U;
+  const int rot = nt % stages;
+  auto load = [&](u32x4(&w)[U][NB], u32x4(&x)[U][MB], int st) {  // st: stage in walk order
+    int sr = st + rot;
+    if (sr >= stages) sr -= stages;
+    const int kb = sr * U;  // first k-step of the stage, wave-relative
     const int ks = kb0 + kb;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -162,15 +171,14 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
   // stage's loads ahead of the previous stage's MFMAs (the scheduler would
   // otherwise sink them next to their uses).  A load past the last stage
   // re-reads the last stage (in bounds, never used).
-  const int stages = kw / U;
   load(wa, xa, 0);
   int st = 0;
   for (; st + 2 <= stages; st += 2) {
-    load(wb, xb, min(st + 1, stages - 1) * U);
+    load(wb, xb, min(st + 1, stages - 1));
     __builtin_amdgcn_sched_barrier(0);
     mma(wa, xa);
     __builtin_amdgcn_sched_barrier(0);
-    load(wa, xa, min(st + 2, stages - 1) * U);
+    load(wa, xa, min(st + 2, stages - 1));
     __builtin_amdgcn_sched_barrier(0);
     mma(wb, xb);
     __builtin_amdgcn_sched_barrier(0);
@@ -195,257 +203,68 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
     for (int w = 1; w < kWaves; ++w) s += red[((w * BLK + blk) * 4 + q4) * 64 + lane];
     return s;
   };
-  const int row0 = mt * 32 * MB;
-  if constexpr (EPI == kEpiSwiglu || EPI == kEpiSwigluPacked) {
+  // ---- epilogue: bias / SwiGLU on the reduced sums -> bf16 tile in LDS ->
+  // 16-byte, row-contiguous stores (a 2-byte store per accumulator element
+  // scatters every store instruction over 2-8 segments; measured to cost more
+  // than the whole K loop) ----
+  constexpr bool kSwiglu = EPI == kEpiSwiglu || EPI == kEpiSwigluPacked;
+  constexpr int TR = MB * 32;                      // tile rows
+  constexpr int TC = kSwiglu ? NB * 16 : NB * 32;  // tile output columns
+  constexpr int OP = TC + 8;                       // LDS row pitch in elements (16-byte multiple)
+  __shared__ __attribute__((aligned(16))) uint16_t otile[TR * OP];
+  if constexpr (kSwiglu) {
     const int nh = a.n / 2;
     for (int pi = wave; pi < MB * NB / 2; pi += kWaves) {
-      const int mb = pi / (NB / 2), p = nt * (NB / 2) + pi % (NB / 2);
-      const int blk_g = mb * NB + 2 * (pi % (NB / 2));
-      const int col = 32 * p + l32;
+      const int mb = pi / (NB / 2), pp = pi % (NB / 2);
+      const int col = 32 * (nt * (NB / 2) + pp) + l32;
       const float bg = G.bias ? bf(G.bias[col]) : 0.f;
       const float bu = G.bias ? bf(G.bias[nh + col]) : 0.f;
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
-        const floatx4 sg = reduced(blk_g, q4), su = reduced(blk_g + 1, q4);
+        const floatx4 sg = reduced(mb * NB + 2 * pp, q4), su = reduced(mb * NB + 2 * pp + 1, q4);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int row = row0 + 32 * mb + 8 * q4 + 4 * g + e;
-          if (row < G.m) {
-            const uint16_t y = swiglu_bf16_bits(f32_to_bf16_bits(sg[e] + bg), f32_to_bf16_bits(su[e] + bu));
-            if constexpr (EPI == kEpiSwigluPacked)
-              G.out[packed_act_offset(row, col, nh)] = y;
-            else
-              G.out[static_cast<int64_t>(row) * G.ldo + col] = y;
-          }
-        }
+        for (int e = 0; e < 4; ++e)
+          otile[(32 * mb + 8 * q4 + 4 * g + e) * OP + 32 * pp + l32] =
+              swiglu_bf16_bits(f32_to_bf16_bits(sg[e] + bg), f32_to_bf16_bits(su[e] + bu));
       }
     }
   } else {
     for (int blk = wave; blk < BLK; blk += kWaves) {
       const int mb = blk / NB, nb = blk % NB;
-      const int col = 32 * (nt * NB + nb) + l32;
-      const float bias = G.bias ? bf(G.bias[col]) : 0.f;
+      const float bias = G.bias ? bf(G.bias[32 * (nt * NB + nb) + l32]) : 0.f;
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const floatx4 s = reduced(blk, q4);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int row = row0 + 32 * mb + 8 * q4 + 4 * g + e;
-          if (row < G.m) {
-            uint16_t y = f32_to_bf16_bits(s[e] + bias);
-            if constexpr (EPI == kEpiResidual)
-              y = f32_to_bf16_bits(bf(G.res[static_cast<int64_t>(row) * G.ldr + col]) + bf(y));
-            G.out[static_cast<int64_t>(row) * G.ldo + col] = y;
-          }
-        }
+        for (int e = 0; e < 4; ++e)
+          otile[(32 * mb + 8 * q4 + 4 * g + e) * OP + 32 * nb + l32] = f32_to_bf16_bits(s[e] + bias);
       }
     }
+  }
+  __syncthreads();
+  const int row0 = mt * 32 * MB, col0 = nt * TC;
+  for (int t = threadIdx.x; t < TR * TC / 8; t += 256) {
+    const int r = t / (TC / 8), c = 8 * (t % (TC / 8));
+    const int row = row0 + r, col = col0 + c;
+    if (row >= G.m) continue;
+    u32x4 v = *reinterpret_cast<const u32x4*>(&otile[r * OP + c]);
+    if constexpr (EPI == kEpiResidual) {
+      const u32x4 rv = *reinterpret_cast<const u32x4*>(G.res + static_cast<int64_t>(row) * G.ldr + col);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = f32_to_bf16_bits(bf(static_cast<uint16_t>(rv[i] & 0xffffu)) + bf(static_cast<uint16_t>(v[i] & 0xffffu)));
+        const uint32_t hi = f32_to_bf16_bits(bf(static_cast<uint16_t>(rv[i] >> 16)) + bf(static_cast<uint16_t>(v[i] >> 16)));
+        v[i] = lo | (hi << 16);
+      }
+    }
+    if constexpr (EPI == kEpiSwigluPacked)
+      *reinterpret_cast<u32x4*>(G.out + packed_act_offset(row, col, a.n / 2)) = v;
+    else
+      *reinterpret_cast<u32x4*>(G.out + static_cast<int64_t>(row) * G.ldo + col) = v;
   }
 }
 
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-// s_waitcnt vmcnt(N), every other counter left alone (gfx9 encoding)
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit field");
-  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
-}
-
-// Epilogue of one 32x32 accumulator block (row block rb, packed column block cb).
-template <int EPI>
-__device__ __forceinline__ void store_block(const Group& G, const floatx16& acc, int rb, int cb, int lane) {
-  const int l32 = lane & 31, g = lane >> 5;
-  const int col = 32 * cb + l32;
-  const float bias = G.bias ? bf(G.bias[col]) : 0.f;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const int row = 32 * rb + 8 * (e >> 2) + 4 * g + (e & 3);
-    if (row < G.m) {
-      uint16_t y = f32_to_bf16_bits(acc[e] + bias);
-      if constexpr (EPI == kEpiResidual) y = f32_to_bf16_bits(bf(G.res[static_cast<int64_t>(row) * G.ldr + col]) + bf(y));
-      G.out[static_cast<int64_t>(row) * G.ldo + col] = y;
-    }
-  }
-}
-
-// SwiGLU epilogue of a (gate, up) pair of 32x32 blocks: packed column blocks
-// 2p and 2p+1 hold gate columns 32p.. and up columns n/2 + 32p.. .
-template <int EPI>
-__device__ __forceinline__ void store_swiglu_pair(const Group& G, int n, const floatx16& ga, const floatx16& ua,
-                                                  int rb, int p, int lane) {
-  const int l32 = lane & 31, g = lane >> 5;
-  const int nh = n / 2, col = 32 * p + l32;
-  const float bg = G.bias ? bf(G.bias[col]) : 0.f;
-  const float bu = G.bias ? bf(G.bias[nh + col]) : 0.f;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const int row = 32 * rb + 8 * (e >> 2) + 4 * g + (e & 3);
-    if (row < G.m) {
-      const uint16_t y = swiglu_bf16_bits(f32_to_bf16_bits(ga[e] + bg), f32_to_bf16_bits(ua[e] + bu));
-      if constexpr (EPI == kEpiSwigluPacked)
-        G.out[packed_act_offset(row, col, nh)] = y;
-      else
-        G.out[static_cast<int64_t>(row) * G.ldo + col] = y;
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Large-M path (the 512-token stream): a workgroup computes a (32 TMB) x
-// (32 TNB) tile with its 4 waves in a 2 x 2 arrangement, each wave a
-// (32 TMB/2) x (32 TNB/2) sub-tile over the whole K range, so no cross-wave
-// reduction is needed.  Per k-step the workgroup moves TMB + TNB 1 KB operand
-// chunks global -> LDS with direct-to-LDS buffer loads (no VGPR staging) into a
-// P-stage ring, and each operand chunk is then read from LDS by the two waves
-// that share it: L2 -> CU traffic per MFMA is halved against per-wave loads.
-// Synchronisation per stage: wait for the own loads of the stage, one barrier
-// (all waves' loads landed, and all waves done with the ring slot refilled
-// next), then the loads P-1 stages ahead.  Loads past the last stage re-read it
-// (in bounds), so the wait counts are constants.
-// ---------------------------------------------------------------------------
-template <int TMB, int TNB, int U, int P, int EPI>
-__global__ __launch_bounds__(256, 2) void gemm_lds_kernel(GemmArgs a) {
-  constexpr int WM = TMB / 2, WN = TNB / 2;  // per-wave m / column blocks
-  constexpr int CH = TMB + TNB;              // 1 KB operand chunks per k-step
-  constexpr int PER_WAVE = CH * U / 4;       // chunks each wave moves per stage
-  constexpr int STAGE = CH * U * 1024;
-  static_assert((CH * U) % 4 == 0, "stage chunks split evenly over 4 waves");
-  static_assert((EPI != kEpiSwiglu && EPI != kEpiSwigluPacked) || WN % 2 == 0, "SwiGLU pairs per wave");
-  __shared__ __attribute__((aligned(1024))) unsigned char ring[P * STAGE];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-
-  int item;
-  {
-    const int total = static_cast<int>(gridDim.x);
-    const int i = static_cast<int>(blockIdx.x);
-    const int per = total / kXcds, rem = total % kXcds;
-    const int xcd = i % kXcds, kk = i / kXcds;
-    item = xcd < rem ? xcd * (per + 1) + kk : rem * (per + 1) + (xcd - rem) * per + kk;
-  }
-  int gi = 0;
-  if (a.num_groups > 1 && item >= a.item_end[0]) gi = 1;
-  if (a.num_groups > 2 && item >= a.item_end[1]) gi = 2;
-  const Group& G = a.g[gi];
-  const int local = item - (gi ? a.item_end[gi - 1] : 0);
-  const int mt = local % a.m_tiles[gi], nt = local / a.m_tiles[gi];
-  const int ksteps = a.k / 16;
-  const int stages = ksteps / U;
-  const int mblocks = (G.m + 31) / 32;
-
-  const __amdgpu_buffer_rsrc_t ar =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(G.a), 0, mblocks * ksteps * 1024, kBufWord3);
-  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(G.w + static_cast<int64_t>(nt * TNB) * ksteps * 512), 0, TNB * ksteps * 1024, kBufWord3);
-  const int voff = lane * 16;
-
-  auto issue = [&](int st) {
-    const int sc = min(st, stages - 1);
-    unsigned char* base = ring + (st % P) * STAGE;
-#pragma unroll
-    for (int i = 0; i < PER_WAVE; ++i) {
-      const int q = wave * PER_WAVE + i;  // chunk of the stage: k-step q / CH, operand q % CH
-      const int c = q % CH;
-      const int ks = sc * U + q / CH;
-      const lds_ptr_t dst = (lds_ptr_t)(base + q * 1024);
-      if (c < TMB)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, dst, 16, voff, (min(mt * TMB + c, mblocks - 1) * ksteps + ks) * 1024,
-                                                 0, 0);
-      else
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, dst, 16, voff, ((c - TMB) * ksteps + ks) * 1024, 0, 0);
-    }
-  };
-
-  floatx16 acc[WM][WN];
-#pragma unroll
-  for (int mb = 0; mb < WM; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < WN; ++nb) acc[mb][nb] = floatx16{};
-
-  auto compute = [&](int st) {
-    const unsigned char* base = ring + (st % P) * STAGE + lane * 16;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      u32x4 av[WM], wv[WN];
-#pragma unroll
-      for (int mb = 0; mb < WM; ++mb) av[mb] = *reinterpret_cast<const u32x4*>(base + (u * CH + wm * WM + mb) * 1024);
-#pragma unroll
-      for (int nb = 0; nb < WN; ++nb)
-        wv[nb] = *reinterpret_cast<const u32x4*>(base + (u * CH + TMB + wn * WN + nb) * 1024);
-#pragma unroll
-      for (int mb = 0; mb < WM; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < WN; ++nb)
-          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av[mb]),
-                                                                __builtin_bit_cast(bf16x8, wv[nb]), acc[mb][nb], 0, 0,
-                                                                0);
-    }
-  };
-
-  for (int st = 0; st < P - 1; ++st) issue(st);
-  for (int st = 0; st < stages; ++st) {
-    wait_vmcnt<(P - 2) * PER_WAVE>();  // this wave's loads of stage st have landed
-    __builtin_amdgcn_s_barrier();      // ... and every wave's; slot (st - 1) % P is free
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    issue(st + P - 1);
-    compute(st);
-  }
-  wait_vmcnt<0>();
-
-  const int rb0 = mt * TMB + wm * WM, cb0 = nt * TNB + wn * WN;
-  if constexpr (EPI == kEpiSwiglu || EPI == kEpiSwigluPacked) {
-#pragma unroll
-    for (int mb = 0; mb < WM; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < WN; nb += 2)
-        store_swiglu_pair<EPI>(G, a.n, acc[mb][nb], acc[mb][nb + 1], rb0 + mb, (cb0 + nb) / 2, lane);
-  } else {
-#pragma unroll
-    for (int mb = 0; mb < WM; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < WN; ++nb) store_block<EPI>(G, acc[mb][nb], rb0 + mb, cb0 + nb, lane);
-  }
-}
-
-
-
-template <int TMB, int TNB, int U, int P>
-hipError_t launch_lds_groups(const rldx_gemm_group_t* gs, const int* idx, int count, int64_t n, int64_t k, int epi,
-                             hipStream_t stream) {
-  if (count == 0) return hipSuccess;
-  GemmArgs a{};
-  a.num_groups = count;
-  a.n = static_cast<int>(n);
-  a.k = static_cast<int>(k);
-  const int n_tiles = static_cast<int>(n / (32 * TNB));
-  int64_t items = 0;
-  for (int j = 0; j < count; ++j) {
-    const rldx_gemm_group_t& s = gs[idx[j]];
-    a.g[j] = Group{static_cast<const uint16_t*>(s.a_packed), static_cast<int>(s.m),
-                   static_cast<const uint16_t*>(s.w_packed), static_cast<const uint16_t*>(s.bias),
-                   static_cast<uint16_t*>(s.out), s.ldo, static_cast<const uint16_t*>(s.residual), s.ldr};
-    a.m_tiles[j] = static_cast<int>((s.m + 32 * TMB - 1) / (32 * TMB));
-    items += static_cast<int64_t>(a.m_tiles[j]) * n_tiles;
-    if (items > (int64_t{1} << 31) - 1) return hipErrorInvalidValue;
-    a.item_end[j] = static_cast<int>(items);
-  }
-  const dim3 grid(static_cast<unsigned>(items)), block(256);
-  if (epi == kEpiBias)
-    hipLaunchKernelGGL((gemm_lds_kernel<TMB, TNB, U, P, kEpiBias>), grid, block, 0, stream, a);
-  else if (epi == kEpiResidual)
-    hipLaunchKernelGGL((gemm_lds_kernel<TMB, TNB, U, P, kEpiResidual>), grid, block, 0, stream, a);
-  else if (epi == kEpiSwiglu)
-    hipLaunchKernelGGL((gemm_lds_kernel<TMB, TNB, U, P, kEpiSwiglu>), grid, block, 0, stream, a);
-  else
-    hipLaunchKernelGGL((gemm_lds_kernel<TMB, TNB, U, P, kEpiSwigluPacked>), grid, block, 0, stream, a);
-  return hipGetLastError();
-}
 
 template <int MB, int NB, int U>
 hipError_t launch_groups(const rldx_gemm_group_t* gs, const int* idx, int count, int64_t n, int64_t k, int epi,
@@ -609,10 +428,11 @@ extern "C" hipError_t rldx_grouped_gemm_bf16(const rldx_gemm_group_t* groups, in
     // packed operands are addressed with 32-bit byte offsets
     if ((s.m + 31) / 32 * 32 * k * 2 > (int64_t{1} << 31) - 1 || n * k * 2 > (int64_t{1} << 31) - 1)
       return hipErrorInvalidValue;
-    if (reinterpret_cast<uintptr_t>(s.out) % 2 || (s.bias && reinterpret_cast<uintptr_t>(s.bias) % 2))
+    // the epilogue stores (and reads the residual) in 16-byte pieces
+    if (!a16(s.out) || (s.bias && reinterpret_cast<uintptr_t>(s.bias) % 2)) return hipErrorInvalidValue;
+    if (epilogue != kEpiSwigluPacked && (s.ldo < n_out || s.ldo % 8)) return hipErrorInvalidValue;
+    if (epilogue == kEpiResidual && (!s.residual || !a16(s.residual) || s.ldr < n_out || s.ldr % 8))
       return hipErrorInvalidValue;
-    if (epilogue != kEpiSwigluPacked && s.ldo < n_out) return hipErrorInvalidValue;
-    if (epilogue == kEpiResidual && (!s.residual || s.ldr < n_out)) return hipErrorInvalidValue;
     order[cnt++] = i;
   }
   // One launch for all groups, smallest first: the weight-streaming tiles of
