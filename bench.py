@@ -10,9 +10,20 @@ one hipGraph; K replays are timed after W warm-up replays.
 Kernel lines (roofline): each hand-written kernel at its workload shape is
 captured N times back to back into a hipGraph and timed with HIP events on the
 launch stream; achieved = algorithmic bytes or flops per launch / mean launch
-time.  `roofline` is the dominant hand-written kernel of the step (joint
-attention at 12 x 608 x 128).  cpu_baseline: the CPU oracle of the same step
-(torch bf16 on the host cores).
+time.  The step's four grouped GEMMs are timed on the step's own packed
+weights, one launch per block (16 weight sets, 1.2-2.9 GB, so every launch
+streams its weights from HBM as in the step).  `roofline` is the dominant kernel
+of the step: the W12 + SwiGLU grouped GEMM (3 streams x [8192 x 1536] weights),
+whose arithmetic intensity (~186 flop/B) puts it under the HBM roof.
+`roofline.traffic` is the measured HBM bytes per launch of that kernel
+(rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by the same counters' reading for a
+copy of known size), read from profiles/gemm_w12_swiglu_traffic.json when that
+file is present.  cpu_baseline: the CPU oracle of the same step (torch bf16 on
+the host cores).
+
+Profiling helpers (no JSON line):
+    python bench.py --profile-kernel w12    # the dominant kernel alone, 4 x 16 launches
+    python bench.py --copy-calibration      # one 256 MiB device copy, 4 times
 """
 
 from __future__ import annotations
@@ -41,6 +52,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--kernel-reps", type=int, default=50)
+    ap.add_argument("--profile-kernel", choices=["qkv", "proj", "w12", "w3"], default=None,
+                    help="run one of the step's grouped GEMMs alone (for counter passes) and exit")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run a 256 MiB device-to-device copy 4 times (traffic counter calibration) and exit")
     return ap.parse_args()
 
 
@@ -184,6 +199,65 @@ def kernel_lines(torch, reps: int):
     return out
 
 
+def step_gemms(step):
+    """The four grouped-GEMM launches of a block of `step`, as {name: (launch(L), flops, bytes)}:
+    algorithmic flops and HBM bytes (weights + biases of the 3 streams, activations
+    in, outputs out, residual in) of one launch."""
+    from rldx_amd import functional as Fn
+
+    cfg, w, pw = step.cfg, step.w, step.pw
+    n, d, inner, ffn = cfg.tokens, cfg.hidden, cfg.inner, cfg.ffn
+    rows = [(s, cfg.rows(s)) for s in ("vl", "sa", "p")]
+
+    def qkv(L):
+        Fn.grouped_gemm([(step.h.rows(r.start, r.stop), pw[f"{s}.qkv"][L], w[f"{s}.qkv.b"][L], step.qkv[r], None)
+                         for s, r in rows], "bias")
+
+    def proj(L):
+        Fn.grouped_gemm([(step.att.rows(r.start, r.stop), pw[f"{s}.proj"][L], w[f"{s}.proj.b"][L], step.x[r],
+                          step.x[r]) for s, r in rows], "residual")
+
+    def w12(L):
+        Fn.grouped_gemm([(step.h.rows(r.start, r.stop), pw[f"{s}.w12"][L], w[f"{s}.w12.b"][L],
+                          step.gl.rows(r.start, r.stop), None) for s, r in rows], "swiglu_packed")
+
+    def w3(L):
+        Fn.grouped_gemm([(step.gl.rows(r.start, r.stop), pw[f"{s}.w3"][L], w[f"{s}.w3.b"][L], step.x[r], step.x[r])
+                         for s, r in rows], "residual")
+
+    def cost(nn, k, n_out, residual):
+        flops = 2 * n * nn * k
+        byts = 2 * (3 * (nn * k + nn) + n * k + n * n_out + (n * n_out if residual else 0))
+        return flops, byts
+
+    return {
+        "qkv": (qkv, *cost(3 * inner, d, 3 * inner, False)),
+        "proj": (proj, *cost(d, inner, d, True)),
+        "w12": (w12, *cost(2 * ffn, d, ffn, False)),
+        "w3": (w3, *cost(d, ffn, d, True)),
+    }
+
+
+def gemm_lines(torch, step) -> dict:
+    """Mean launch time of each grouped GEMM over the 16 blocks' weights (graph of 16 launches)."""
+    out = {}
+    blocks = step.cfg.blocks
+    for name, (fn, flops, byts) in step_gemms(step).items():
+        it = {"L": 0}
+
+        def run():
+            fn(it["L"] % blocks)
+            it["L"] += 1
+
+        ms = graph_time_ms(run, blocks, torch)
+        t = ms * 1e-3
+        roof_t = max(flops / (BF16_MFMA_PEAK_TFLOPS * 1e12), byts / (HBM_PEAK_GBS * 1e9))
+        bound = "hbm" if byts / (HBM_PEAK_GBS * 1e9) >= flops / (BF16_MFMA_PEAK_TFLOPS * 1e12) else "mfma"
+        out[f"gemm_{name}"] = dict(us=ms * 1e3, flops=flops, bytes=byts, tflops=flops / t / 1e12,
+                                   gbs=byts / t / 1e9, bound=bound, roofline_us=roof_t * 1e6, frac=roof_t / t)
+    return out
+
+
 def cpu_baseline(torch, cfg, weights, inputs, budget_s: float = 20.0):
     """Time the CPU oracle step on the host cores; bounded sample, scaled to ms per action step."""
     from oracle import msat_step_ref as R
@@ -231,11 +305,28 @@ def main():
 
     rldx_amd.load()
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        a = torch.empty(128 << 20, dtype=torch.bfloat16, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(4):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print("[bench] copied 4 x 256 MiB", file=sys.stderr, flush=True)
+        return
     cfg = MsatStepCfg()
     print(f"[bench] building step weights ({cfg.weight_bytes() / 1e9:.2f} GB bf16)", file=sys.stderr, flush=True)
     weights = make_weights(cfg, dev)
     inputs = make_inputs(cfg, dev)
     step = MsatActionStep(cfg, weights, inputs)
+    if args.profile_kernel:
+        step.run(steps=1, blocks=1)  # fills the activation buffers
+        fn = step_gemms(step)[args.profile_kernel][0]
+        for _ in range(4):
+            for L in range(cfg.blocks):
+                fn(L)
+        torch.cuda.synchronize()
+        print(f"[bench] {args.profile_kernel}: {4 * cfg.blocks} launches", file=sys.stderr, flush=True)
+        return
     step.capture()
     print("[bench] graph captured", file=sys.stderr, flush=True)
     for _ in range(args.warmup):
@@ -255,12 +346,20 @@ def main():
     assert torch.isfinite(act).all(), "non-finite actions"
     print(f"[bench] action step {ms:.3f} ms", file=sys.stderr, flush=True)
 
+    gl = gemm_lines(torch, step)
     kl = kernel_lines(torch, args.kernel_reps)
+    kl.update(gl)
     print("[bench] kernel lines done", file=sys.stderr, flush=True)
-    dom = kl["step_joint_attention_12x608x128"]
-    roofline = dict(kernel="attn_fwd_kernel<128,1,false,true,false> (joint attention 12 heads x 608 x 128, masked)",
-                    bound="mfma", achieved=dom["achieved"], peak=dom["peak"], unit="TFLOP/s", frac=dom["frac"],
-                    traffic=None)
+    dom = gl["gemm_w12"]
+    traffic = None
+    tf = ROOT / "profiles" / "gemm_w12_swiglu_traffic.json"
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+    roofline = dict(kernel="gemm_kernel<2,2,4,SWIGLU_PACKED>: W12 + SwiGLU grouped GEMM, 3 streams "
+                           "(512/64/32 rows) x [8192 x 1536] weights",
+                    bound="hbm", achieved=dom["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=dom["gbs"] / HBM_PEAK_GBS, traffic=traffic, algorithmic_bytes=dom["bytes"],
+                    flops=dom["flops"], us=dom["us"])
 
     cpu = None
     if not args.no_cpu:

@@ -3,7 +3,7 @@
 Importing this module registers, backed by the gfx950 kernels of librldx_amd.so:
 
   ds::fused_attention_2way   ds::fused_attention_3way   ds::grouped_swiglu
-  ss::fused_attention_2way   ss::fused_attention_3way
+  ss::fused_attention_2way   ss::fused_attention_3way   ss::fused_mlp_swiglu
   rldx_backbone::fused_attention
   rldx_amd::swiglu           (the eager `F.silu(x1) * x2` the chains inline)
 
@@ -19,6 +19,7 @@ fixed 4096-wide output), and `kv_mask` on the 3-way ops (1 = visible key,
 
 from __future__ import annotations
 
+import weakref
 from typing import Optional
 
 import torch
@@ -283,3 +284,49 @@ def swiglu_op(x: torch.Tensor) -> torch.Tensor:
 @swiglu_op.register_fake
 def _(x):
     return x.new_empty((*x.shape[:-1], x.shape[-1] // 2))
+
+
+# ---------------------------------------------------------------------------
+# ss::fused_mlp_swiglu — GEMM + bias + SwiGLU
+# ---------------------------------------------------------------------------
+# The grouped GEMM reads weights in its packed operand order.  Weights are
+# static, so each one is packed once and the packed copy is kept for as long as
+# the weight tensor lives; an in-place update of the weight (version change)
+# packs it again.
+_packed_weights: dict = {}  # id(weight) -> (weakref to weight, version, swiglu_pairs, PackedWeight)
+
+
+def _packed_weight(w: torch.Tensor, swiglu_pairs: bool) -> Fn.PackedWeight:
+    hit = _packed_weights.get(id(w))
+    if hit is not None and hit[0]() is w and hit[1] == w._version and hit[2] == swiglu_pairs:
+        return hit[3]
+    pw = Fn.pack_weight(w if w.stride(1) == 1 else w.contiguous(), swiglu_pairs=swiglu_pairs)
+    if hit is None or hit[0]() is not w:
+        weakref.finalize(w, _packed_weights.pop, id(w), None)
+    _packed_weights[id(w)] = (weakref.ref(w), w._version, swiglu_pairs, pw)
+    return pw
+
+
+@torch.library.custom_op("ss::fused_mlp_swiglu", mutates_args=())
+def ss_fused_mlp_swiglu(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, split_k: int = 1) -> torch.Tensor:
+    """silu(x W_gate^T + b_gate) * (x W_up^T + b_up), W = [W_gate; W_up] (2*N_half, K).
+
+    rldx/inference/action_model/single_stream/engine/ops/op_fused_mlp_swiglu.py:13-43
+    (kernel fused_mlp_swiglu.py:199-267).  `split_k` is accepted for signature
+    compatibility; the kernel always splits K over the 4 waves of a workgroup.
+    Rounding: the eager chain (GEMM output rounded to bf16, then SwiGLU's two
+    roundings).  Needs K % 512 == 0 and N_half % 32 == 0."""
+    del split_k
+    M, K = x.shape
+    nh = weight.shape[0] // 2
+    out = torch.empty((M, nh), dtype=torch.bfloat16, device=x.device)
+    if M == 0:
+        return out
+    xx = x if x.stride(1) == 1 else x.contiguous()
+    Fn.grouped_gemm([(xx, _packed_weight(weight, True), bias.contiguous(), out, None)], "swiglu")
+    return out
+
+
+@ss_fused_mlp_swiglu.register_fake
+def _(x, weight, bias, split_k=1):
+    return x.new_empty((x.shape[0], weight.shape[0] // 2))

@@ -162,3 +162,19 @@ def test_attention_packed_output(dev):
     Fn.attention_packed(q, kvp, S, key_bias=bias, out=o.permute(0, 2, 1, 3))
     op = Fn.attention_packed(q, kvp, S, key_bias=bias, out=Fn.PackedAct.empty(S, H * D, dev))
     assert torch.equal(op.unpack(), o.view(S, H * D))
+
+
+def test_ss_fused_mlp_swiglu_op(dev):
+    import rldx_amd.ops  # noqa: F401  registers ss::fused_mlp_swiglu
+
+    g = torch.Generator().manual_seed(19)
+    M, K, NH = 82, 1536, 4096
+    x, w, b = _rand((M, K), g), _rand((2 * NH, K), g, 0.02), _rand((2 * NH,), g, 0.1)
+    xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
+    y = torch.ops.ss.fused_mlp_swiglu(xd, wd, bd, 1)
+    assert y.shape == (M, NH)
+    assert_bf16_close(y, ref.swiglu(_linear_ref(x, w, b)), "ss::fused_mlp_swiglu")
+    assert torch.equal(torch.ops.ss.fused_mlp_swiglu(xd, wd, bd, 1), y)  # packed-weight cache hit
+    wd.mul_(0.5)  # in-place update -> repacked
+    assert_bf16_close(torch.ops.ss.fused_mlp_swiglu(xd, wd, bd, 1), ref.swiglu(_linear_ref(x, (w.float() * 0.5).to(BF16), b)),
+                      "after weight update")
