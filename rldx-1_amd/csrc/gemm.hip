@@ -172,6 +172,47 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
   // otherwise sink them next to their uses).  A load past the last stage
   // re-reads the last stage (in bounds, never used).
   load(wa, xa, 0);
+
+  // Epilogue operands, fetched behind the first stage so their latency hides
+  // under the K loop: the bias of the output columns this wave finalises, and
+  // the residual chunks of this thread's 16-byte stores (each chunk is read and
+  // written by the same thread, so the residual may alias the output).
+  constexpr bool kSwiglu = EPI == kEpiSwiglu || EPI == kEpiSwigluPacked;
+  constexpr int TR = MB * 32;                      // tile rows
+  constexpr int TC = kSwiglu ? NB * 16 : NB * 32;  // tile output columns
+  constexpr int BLK = MB * NB;
+  // epilogue work units per wave: 32x32 blocks, or for SwiGLU (gate, up) block
+  // pairs split into their 4 row quarters (the SwiGLU math is the costly part)
+  constexpr int UNITS = kSwiglu ? (BLK / 2) * 4 : BLK;
+  constexpr int PER_WAVE = (UNITS + kWaves - 1) / kWaves;
+  constexpr int NCHUNK = (TR * TC / 8 + 255) / 256;  // 16-byte output chunks per thread
+  float pb0[PER_WAVE], pb1[PER_WAVE];
+#pragma unroll
+  for (int j = 0; j < PER_WAVE; ++j) {
+    const int id = wave + j * kWaves;
+    pb0[j] = pb1[j] = 0.f;
+    if constexpr (kSwiglu) {
+      if (G.bias && id < UNITS) {
+        const int col = 32 * (nt * (NB / 2) + (id / 4) % (NB / 2)) + l32;
+        pb0[j] = bf(G.bias[col]);
+        pb1[j] = bf(G.bias[a.n / 2 + col]);
+      }
+    } else {
+      if (G.bias && id < BLK) pb0[j] = bf(G.bias[32 * (nt * NB + id % NB) + l32]);
+    }
+  }
+  u32x4 pres[NCHUNK];
+  if constexpr (EPI == kEpiResidual) {
+#pragma unroll
+    for (int j = 0; j < NCHUNK; ++j) {
+      const int t = static_cast<int>(threadIdx.x) + 256 * j;
+      const int row = mt * TR + t / (TC / 8), col = nt * TC + 8 * (t % (TC / 8));
+      pres[j] = (t < TR * TC / 8 && row < G.m)
+                    ? *reinterpret_cast<const u32x4*>(G.res + static_cast<int64_t>(row) * G.ldr + col)
+                    : u32x4{0, 0, 0, 0};
+    }
+  }
+
   int st = 0;
   for (; st + 2 <= stages; st += 2) {
     load(wb, xb, min(st + 1, stages - 1));
@@ -186,7 +227,6 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
   if (st < stages) mma(wa, xa);
 
   // ---- reduce the 4 waves' partial tiles through LDS, in wave order ----
-  constexpr int BLK = MB * NB;
   __shared__ floatx4 red[kWaves * BLK * 4 * 64];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
@@ -207,31 +247,29 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
   // 16-byte, row-contiguous stores (a 2-byte store per accumulator element
   // scatters every store instruction over 2-8 segments; measured to cost more
   // than the whole K loop) ----
-  constexpr bool kSwiglu = EPI == kEpiSwiglu || EPI == kEpiSwigluPacked;
-  constexpr int TR = MB * 32;                      // tile rows
-  constexpr int TC = kSwiglu ? NB * 16 : NB * 32;  // tile output columns
   constexpr int OP = TC + 8;                       // LDS row pitch in elements (16-byte multiple)
   __shared__ __attribute__((aligned(16))) uint16_t otile[TR * OP];
   if constexpr (kSwiglu) {
-    const int nh = a.n / 2;
-    for (int pi = wave; pi < MB * NB / 2; pi += kWaves) {
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j) {
+      const int u = wave + j * kWaves;
+      if (u >= UNITS) break;
+      const int pi = u / 4, q4 = u % 4;
       const int mb = pi / (NB / 2), pp = pi % (NB / 2);
-      const int col = 32 * (nt * (NB / 2) + pp) + l32;
-      const float bg = G.bias ? bf(G.bias[col]) : 0.f;
-      const float bu = G.bias ? bf(G.bias[nh + col]) : 0.f;
+      const float bg = pb0[j], bu = pb1[j];
+      const floatx4 sg = reduced(mb * NB + 2 * pp, q4), su = reduced(mb * NB + 2 * pp + 1, q4);
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const floatx4 sg = reduced(mb * NB + 2 * pp, q4), su = reduced(mb * NB + 2 * pp + 1, q4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          otile[(32 * mb + 8 * q4 + 4 * g + e) * OP + 32 * pp + l32] =
-              swiglu_bf16_bits(f32_to_bf16_bits(sg[e] + bg), f32_to_bf16_bits(su[e] + bu));
-      }
+      for (int e = 0; e < 4; ++e)
+        otile[(32 * mb + 8 * q4 + 4 * g + e) * OP + 32 * pp + l32] =
+            swiglu_bf16_bits(f32_to_bf16_bits(sg[e] + bg), f32_to_bf16_bits(su[e] + bu));
     }
   } else {
-    for (int blk = wave; blk < BLK; blk += kWaves) {
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j) {
+      const int blk = wave + j * kWaves;
+      if (blk >= BLK) break;
       const int mb = blk / NB, nb = blk % NB;
-      const float bias = G.bias ? bf(G.bias[32 * (nt * NB + nb) + l32]) : 0.f;
+      const float bias = pb0[j];
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const floatx4 s = reduced(blk, q4);
@@ -242,14 +280,16 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
     }
   }
   __syncthreads();
-  const int row0 = mt * 32 * MB, col0 = nt * TC;
-  for (int t = threadIdx.x; t < TR * TC / 8; t += 256) {
+  const int row0 = mt * TR, col0 = nt * TC;
+#pragma unroll
+  for (int j = 0; j < NCHUNK; ++j) {
+    const int t = static_cast<int>(threadIdx.x) + 256 * j;
     const int r = t / (TC / 8), c = 8 * (t % (TC / 8));
     const int row = row0 + r, col = col0 + c;
-    if (row >= G.m) continue;
+    if (t >= TR * TC / 8 || row >= G.m) continue;
     u32x4 v = *reinterpret_cast<const u32x4*>(&otile[r * OP + c]);
     if constexpr (EPI == kEpiResidual) {
-      const u32x4 rv = *reinterpret_cast<const u32x4*>(G.res + static_cast<int64_t>(row) * G.ldr + col);
+      const u32x4 rv = pres[j];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t lo = f32_to_bf16_bits(bf(static_cast<uint16_t>(rv[i] & 0xffffu)) + bf(static_cast<uint16_t>(v[i] & 0xffffu)));
