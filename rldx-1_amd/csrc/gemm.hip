@@ -186,19 +186,21 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
   constexpr int UNITS = kSwiglu ? (BLK / 2) * 4 : BLK;
   constexpr int PER_WAVE = (UNITS + kWaves - 1) / kWaves;
   constexpr int NCHUNK = (TR * TC / 8 + 255) / 256;  // 16-byte output chunks per thread
-  float pb0[PER_WAVE], pb1[PER_WAVE];
+  // (raw bf16 bits: converting here would make the loads' results needed, and
+  // with in-order load counters wait for the first stage too)
+  uint16_t pb0[PER_WAVE], pb1[PER_WAVE];
 #pragma unroll
   for (int j = 0; j < PER_WAVE; ++j) {
     const int id = wave + j * kWaves;
-    pb0[j] = pb1[j] = 0.f;
+    pb0[j] = pb1[j] = 0;
     if constexpr (kSwiglu) {
       if (G.bias && id < UNITS) {
         const int col = 32 * (nt * (NB / 2) + (id / 4) % (NB / 2)) + l32;
-        pb0[j] = bf(G.bias[col]);
-        pb1[j] = bf(G.bias[a.n / 2 + col]);
+        pb0[j] = G.bias[col];
+        pb1[j] = G.bias[a.n / 2 + col];
       }
     } else {
-      if (G.bias && id < BLK) pb0[j] = bf(G.bias[32 * (nt * NB + id % NB) + l32]);
+      if (G.bias && id < BLK) pb0[j] = G.bias[32 * (nt * NB + id % NB) + l32];
     }
   }
   u32x4 pres[NCHUNK];
@@ -256,7 +258,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
       if (u >= UNITS) break;
       const int pi = u / 4, q4 = u % 4;
       const int mb = pi / (NB / 2), pp = pi % (NB / 2);
-      const float bg = pb0[j], bu = pb1[j];
+      const float bg = bf(pb0[j]), bu = bf(pb1[j]);
       const floatx4 sg = reduced(mb * NB + 2 * pp, q4), su = reduced(mb * NB + 2 * pp + 1, q4);
 #pragma unroll
       for (int e = 0; e < 4; ++e)
@@ -269,7 +271,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
       const int blk = wave + j * kWaves;
       if (blk >= BLK) break;
       const int mb = blk / NB, nb = blk % NB;
-      const float bias = pb0[j];
+      const float bias = bf(pb0[j]);
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const floatx4 s = reduced(blk, q4);
