@@ -261,9 +261,13 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
       const float bg = bf(pb0[j]), bu = bf(pb1[j]);
       const floatx4 sg = reduced(mb * NB + 2 * pp, q4), su = reduced(mb * NB + 2 * pp + 1, q4);
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        otile[(32 * mb + 8 * q4 + 4 * g + e) * OP + 32 * pp + l32] =
-            swiglu_bf16_bits(f32_to_bf16_bits(sg[e] + bg), f32_to_bf16_bits(su[e] + bu));
+      for (int e = 0; e < 4; e += 2) {
+        const uint32_t gp = pack_bf16x2(sg[e] + bg, sg[e + 1] + bg);
+        const uint32_t up = pack_bf16x2(su[e] + bu, su[e + 1] + bu);
+        const uint32_t y = swiglu_bf16x2(bf16x2_lo(gp), bf16x2_hi(gp), bf16x2_lo(up), bf16x2_hi(up));
+        otile[(32 * mb + 8 * q4 + 4 * g + e) * OP + 32 * pp + l32] = static_cast<uint16_t>(y);
+        otile[(32 * mb + 8 * q4 + 4 * g + e + 1) * OP + 32 * pp + l32] = static_cast<uint16_t>(y >> 16);
+      }
     }
   } else {
 #pragma unroll

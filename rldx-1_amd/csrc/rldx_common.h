@@ -86,6 +86,57 @@ RLDX_HD uint16_t swiglu_bf16_bits(uint16_t g, uint16_t u) {
   return f32_to_bf16_bits(s * bf16_bits_to_f32(u));
 }
 
+// ---------------------------------------------------------------------------
+// Device SwiGLU with the hardware exp2 / reciprocal, bit-identical to
+// swiglu_bf16_bits.
+//
+// Only the bf16 rounding of silu reaches the output, so silu may be evaluated
+// by any method whose fp32 value rounds like silu_f32's.  The fast form is
+// x * rcp(1 + exp2(-x log2e)) with v_exp_f32 and v_rcp_f32 (1 ulp each);
+// log2e = kL2eHi + lo, kL2eHi holding 16 significant bits so that x * kL2eHi
+// is exact for the 8-bit significand of a bf16 x, and exp2(-x lo) is applied
+// to first order (|x lo ln2| < 4e-4 for |x| <= 80).  Over every bf16 x with
+// |x| <= 80 the fast value lies within 5 ulps of silu_f32's, with either
+// hardware op off by one ulp in either direction.  Where it lies within
+// kSiluFastMargin ulps of a bf16 rounding midpoint (low 16 bits 0x8000), or
+// x is outside [-80, 80] (inf and NaN included), silu_f32 is evaluated
+// instead; elsewhere no midpoint separates the two values and both round to
+// the same bf16.  About 1 element in 2000 takes the exact branch.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// (lo, hi) -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+__device__ __forceinline__ float bf16x2_lo(uint32_t p) { return __builtin_bit_cast(float, p << 16); }
+__device__ __forceinline__ float bf16x2_hi(uint32_t p) { return __builtin_bit_cast(float, p & 0xffff0000u); }
+
+constexpr uint32_t kSiluFastMargin = 16;
+
+__device__ __forceinline__ float silu_bf16_input(float x) {
+#pragma clang fp contract(off)
+  const float kL2eHi = 1.44268798828125f;            // log2(e) to 16 significant bits
+  const float kL2eLoLn2 = 4.888495368504664e-06f;    // (log2(e) - kL2eHi) * ln(2)
+  const float e1 = __builtin_amdgcn_exp2f(x * -kL2eHi);
+  const float e = __builtin_fmaf(e1, x * -kL2eLoLn2, e1);
+  float s = x * __builtin_amdgcn_rcpf(1.0f + e);
+  const uint32_t b = __builtin_bit_cast(uint32_t, s);
+  const bool near_mid = static_cast<uint16_t>(b + (kSiluFastMargin - 0x8000u)) <= 2 * kSiluFastMargin;
+  if (__builtin_expect(near_mid || !(__builtin_fabsf(x) <= 80.0f), 0)) s = silu_f32(x);
+  return s;
+}
+
+// Two SwiGLU elements: g0, g1, u0, u1 are bf16 values held as fp32; returns
+// the packed bf16 pair bf16(bf16(silu(g)) * u), as swiglu_bf16_bits.
+__device__ __forceinline__ uint32_t swiglu_bf16x2(float g0, float g1, float u0, float u1) {
+#pragma clang fp contract(off)
+  const uint32_t s = pack_bf16x2(silu_bf16_input(g0), silu_bf16_input(g1));
+  return pack_bf16x2(bf16x2_lo(s) * u0, bf16x2_hi(s) * u1);
+}
+
 // Element offset of A[row][col] in the packed activation order (the A operand
 // of the grouped GEMM) of a matrix with k columns: 1 KB chunk (row / 32,
 // col / 16), lane row % 32 + 32 * (col / 8 % 2), element col % 8.

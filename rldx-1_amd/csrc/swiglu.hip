@@ -2,9 +2,13 @@
 // gate = x[r, 0:n_half], up = x[r, n_half:2*n_half]  (the `x12.chunk(2, -1)`
 // split of rldx/model/modules/action_model/ops.py:157-161).
 //
-// Memory-bound: every thread moves 16 B of gate, 16 B of up and writes 16 B of
-// y (8 elements) with 128-bit global loads/stores.  Work is a flat list of
-// 8-element chunks over all groups, walked with a grid-stride loop, so any row
+// Memory-bound once silu is cheap: the vectorised kernel evaluates silu with
+// the hardware exp2 / reciprocal (swiglu_bf16x2, about 15 VALU operations per
+// element instead of about 60 for the IEEE-division form, which made the
+// kernel VALU-bound), bit-identical to the exact element function.  Every
+// thread moves 16 B of gate, 16 B of up and writes 16 B of y (8 elements) with
+// 128-bit global loads/stores, two chunks per thread with all four loads issued
+// before any arithmetic; one workgroup per 512 chunks of a group, so any row
 // count fills all 256 CUs.
 //
 // Optional per-column bias (the `ds::grouped_swiglu` form,
@@ -24,60 +28,101 @@ struct SwigluGroup {
   uint16_t* y;           // [rows, >= n_half] bf16, row stride ldy elements
   int64_t ldx, ldy;
   int64_t rows, n_half;
-  int64_t chunks_per_row;  // n_half / 8
-  int64_t chunk_begin;     // first flat chunk index of this group
 };
 
-struct SwigluArgs {
-  SwigluGroup g[3];
-  int num_groups;
-  int64_t total_chunks;
+// Unsigned 32-bit division by an invariant divisor d >= 1 (Granlund and
+// Montgomery, "Division by invariant integers using multiplication", PLDI
+// 1994, figure 4.1): q = (t + ((n - t) >> sh1)) >> sh2 with t = mulhi(m, n),
+// exact for every 32-bit n.
+struct DivMagic {
+  uint32_t m, sh1, sh2;
 };
 
+DivMagic div_magic(uint32_t d) {
+  uint32_t l = 0;
+  while ((uint64_t{1} << l) < d) ++l;
+  DivMagic r;
+  r.m = static_cast<uint32_t>((uint64_t{1} << 32) * ((uint64_t{1} << l) - d) / d + 1);
+  r.sh1 = l < 1 ? l : 1;
+  r.sh2 = l < 1 ? 0 : l - 1;
+  return r;
+}
+
+__device__ __forceinline__ uint32_t div_u32(uint32_t n, const DivMagic& dm) {
+  const uint32_t t = __umulhi(dm.m, n);
+  return (t + ((n - t) >> dm.sh1)) >> dm.sh2;
+}
+
+// One group of the vectorised kernel: rows of n_half elements cut into
+// 8-element chunks; workgroups [block_begin, block_begin + blocks) cover it.
+struct VecGroup {
+  const uint16_t* x;
+  const uint16_t* bias;
+  uint16_t* y;
+  int64_t ldx, ldy, n_half;
+  uint32_t chunks;        // rows * n_half / 8 (< 2^31)
+  uint32_t cpr;           // chunks per row
+  DivMagic div;           // division by cpr
+  uint32_t block_begin;   // first workgroup; 0xffffffff for an unused slot
+};
+
+struct VecArgs {
+  VecGroup g[3];
+};
+
+constexpr int kVecThreads = 256;
+constexpr int kVecChunks = 2;  // 8-element chunks per thread, all loads issued before any math
+
+// Two elements per 32-bit word: (lo, hi) bf16 halves.
 __device__ __forceinline__ uint32_t swiglu_pair(uint32_t g2, uint32_t u2) {
-  uint16_t lo = swiglu_bf16_bits(static_cast<uint16_t>(g2 & 0xffffu), static_cast<uint16_t>(u2 & 0xffffu));
-  uint16_t hi = swiglu_bf16_bits(static_cast<uint16_t>(g2 >> 16), static_cast<uint16_t>(u2 >> 16));
-  return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+  return swiglu_bf16x2(bf16x2_lo(g2), bf16x2_hi(g2), bf16x2_lo(u2), bf16x2_hi(u2));
 }
 
 __device__ __forceinline__ uint32_t add_bias_pair(uint32_t x2, uint32_t b2) {
-  uint16_t lo = f32_to_bf16_bits(bf16_bits_to_f32(static_cast<uint16_t>(x2 & 0xffffu)) +
-                                 bf16_bits_to_f32(static_cast<uint16_t>(b2 & 0xffffu)));
-  uint16_t hi = f32_to_bf16_bits(bf16_bits_to_f32(static_cast<uint16_t>(x2 >> 16)) +
-                                 bf16_bits_to_f32(static_cast<uint16_t>(b2 >> 16)));
-  return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+  return pack_bf16x2(bf16x2_lo(x2) + bf16x2_lo(b2), bf16x2_hi(x2) + bf16x2_hi(b2));
 }
 
+// The group is uniform per workgroup (scalar selection); within a group the
+// chunk index is 32-bit and the row comes from the invariant-divisor multiply.
+// Chunk loads past the end of a group are clamped to its last chunk (in
+// bounds) and their stores skipped.
 template <bool kHasBias>
-__global__ __launch_bounds__(256) void swiglu_vec8_kernel(SwigluArgs args) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; c < args.total_chunks;
-       c += stride) {
-    int gi = 0;
-    if (args.num_groups > 1 && c >= args.g[1].chunk_begin) gi = 1;
-    if (args.num_groups > 2 && c >= args.g[2].chunk_begin) gi = 2;
-    const SwigluGroup& G = args.g[gi];
-    const int64_t local = c - G.chunk_begin;
-    const int64_t r = local / G.chunks_per_row;
-    const int64_t j = (local - r * G.chunks_per_row) * 8;
-    const u32x4* gp = reinterpret_cast<const u32x4*>(G.x + r * G.ldx + j);
-    const u32x4* up = reinterpret_cast<const u32x4*>(G.x + r * G.ldx + G.n_half + j);
-    u32x4 gv = __builtin_nontemporal_load(gp);
-    u32x4 uv = __builtin_nontemporal_load(up);
+__global__ __launch_bounds__(kVecThreads) void swiglu_vec8_kernel(VecArgs a) {
+  const uint32_t blk = blockIdx.x;
+  const int gi = (blk >= a.g[1].block_begin) + (blk >= a.g[2].block_begin);
+  const VecGroup& G = a.g[gi];
+  const uint32_t c0 = (blk - G.block_begin) * (kVecThreads * kVecChunks) + threadIdx.x;
+  u32x4 gv[kVecChunks], uv[kVecChunks], bg[kVecChunks], bu[kVecChunks];
+  int64_t yoff[kVecChunks];
+#pragma unroll
+  for (int i = 0; i < kVecChunks; ++i) {
+    const uint32_t c = min(c0 + i * kVecThreads, G.chunks - 1);
+    const uint32_t r = div_u32(c, G.div);
+    const int64_t j = static_cast<int64_t>(c - r * G.cpr) * 8;
+    const uint16_t* xr = G.x + r * G.ldx + j;
+    gv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xr));
+    uv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xr + G.n_half));
     if constexpr (kHasBias) {
-      u32x4 bg = *reinterpret_cast<const u32x4*>(G.bias + j);
-      u32x4 bu = *reinterpret_cast<const u32x4*>(G.bias + G.n_half + j);
-      gv.x = add_bias_pair(gv.x, bg.x); gv.y = add_bias_pair(gv.y, bg.y);
-      gv.z = add_bias_pair(gv.z, bg.z); gv.w = add_bias_pair(gv.w, bg.w);
-      uv.x = add_bias_pair(uv.x, bu.x); uv.y = add_bias_pair(uv.y, bu.y);
-      uv.z = add_bias_pair(uv.z, bu.z); uv.w = add_bias_pair(uv.w, bu.w);
+      bg[i] = *reinterpret_cast<const u32x4*>(G.bias + j);
+      bu[i] = *reinterpret_cast<const u32x4*>(G.bias + G.n_half + j);
+    }
+    yoff[i] = r * G.ldy + j;
+  }
+#pragma unroll
+  for (int i = 0; i < kVecChunks; ++i) {
+    u32x4 gx = gv[i], ux = uv[i];
+    if constexpr (kHasBias) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        gx[w] = add_bias_pair(gx[w], bg[i][w]);
+        ux[w] = add_bias_pair(ux[w], bu[i][w]);
+      }
     }
     u32x4 out;
-    out.x = swiglu_pair(gv.x, uv.x);
-    out.y = swiglu_pair(gv.y, uv.y);
-    out.z = swiglu_pair(gv.z, uv.z);
-    out.w = swiglu_pair(gv.w, uv.w);
-    __builtin_nontemporal_store(out, reinterpret_cast<u32x4*>(G.y + r * G.ldy + j));
+#pragma unroll
+    for (int w = 0; w < 4; ++w) out[w] = swiglu_pair(gx[w], ux[w]);
+    if (c0 + i * kVecThreads < G.chunks)
+      __builtin_nontemporal_store(out, reinterpret_cast<u32x4*>(G.y + yoff[i]));
   }
 }
 
@@ -104,11 +149,11 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 bool vec_ok(const SwigluGroup& G) {
   return (G.n_half % 8 == 0) && (G.ldx % 8 == 0) && (G.ldy % 8 == 0) && aligned16(G.x) && aligned16(G.y) &&
-         (G.bias == nullptr || aligned16(G.bias));
+         (G.bias == nullptr || aligned16(G.bias)) && G.rows * (G.n_half / 8) < (int64_t{1} << 31);
 }
 
 int grid_for(int64_t work_items) {
-  // 256 CUs x 8 resident 256-thread groups; the grid-stride loop covers the rest.
+  // Scalar kernel: 256 CUs x 8 resident 256-thread groups; a grid-stride loop covers the rest.
   const int64_t max_blocks = 256 * 8;
   int64_t b = (work_items + 255) / 256;
   if (b > max_blocks) b = max_blocks;
@@ -124,25 +169,33 @@ hipError_t launch_groups(SwigluGroup* gs, int n, hipStream_t stream) {
     all_vec = all_vec && vec_ok(gs[i]);
   }
   if (all_vec) {
-    SwigluArgs a{};
-    int64_t begin = 0;
+    VecArgs a{};
+    for (auto& v : a.g) v.block_begin = 0xffffffffu;
+    int64_t blocks = 0;
     int k = 0;
     for (int i = 0; i < n; ++i) {
       if (gs[i].rows == 0 || gs[i].n_half == 0) continue;
-      a.g[k] = gs[i];
-      a.g[k].chunks_per_row = gs[i].n_half / 8;
-      a.g[k].chunk_begin = begin;
-      begin += gs[i].rows * a.g[k].chunks_per_row;
-      ++k;
+      VecGroup& v = a.g[k++];
+      v.x = gs[i].x;
+      v.bias = gs[i].bias;
+      v.y = gs[i].y;
+      v.ldx = gs[i].ldx;
+      v.ldy = gs[i].ldy;
+      v.n_half = gs[i].n_half;
+      v.cpr = static_cast<uint32_t>(gs[i].n_half / 8);
+      v.chunks = static_cast<uint32_t>(gs[i].rows * v.cpr);
+      v.div = div_magic(v.cpr);
+      v.block_begin = static_cast<uint32_t>(blocks);
+      blocks += (v.chunks + kVecThreads * kVecChunks - 1) / (kVecThreads * kVecChunks);
     }
     if (k == 0) return hipSuccess;
-    a.num_groups = k;
-    a.total_chunks = begin;
-    const int grid = grid_for(begin);
+    if (blocks >= 0xffffffffll) return hipErrorInvalidValue;
     if (has_bias)
-      hipLaunchKernelGGL(swiglu_vec8_kernel<true>, dim3(grid), dim3(256), 0, stream, a);
+      hipLaunchKernelGGL(swiglu_vec8_kernel<true>, dim3(static_cast<uint32_t>(blocks)), dim3(kVecThreads), 0,
+                         stream, a);
     else
-      hipLaunchKernelGGL(swiglu_vec8_kernel<false>, dim3(grid), dim3(256), 0, stream, a);
+      hipLaunchKernelGGL(swiglu_vec8_kernel<false>, dim3(static_cast<uint32_t>(blocks)), dim3(kVecThreads), 0,
+                         stream, a);
     return hipGetLastError();
   }
   for (int i = 0; i < n; ++i) {
@@ -175,7 +228,7 @@ extern "C" hipError_t rldx_swiglu_bf16(const void* x, int64_t ldx, const void* b
                                        int64_t rows, int64_t n_half, hipStream_t stream) {
   if (!group_valid(x, y, ldx, ldy, rows, n_half)) return hipErrorInvalidValue;
   SwigluGroup g{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y),
-                ldx, ldy, rows, n_half, 0, 0};
+                ldx, ldy, rows, n_half};
   return launch_groups(&g, 1, stream);
 }
 
@@ -188,9 +241,9 @@ extern "C" hipError_t rldx_grouped_swiglu_bf16(const void* sa_x, const void* sa_
   if ((sa_bias == nullptr) != (vl_bias == nullptr)) return hipErrorInvalidValue;
   SwigluGroup g[2] = {
       {static_cast<const uint16_t*>(sa_x), static_cast<const uint16_t*>(sa_bias), static_cast<uint16_t*>(sa_y),
-       2 * n_half_sa, n_half_sa, m_sa, n_half_sa, 0, 0},
+       2 * n_half_sa, n_half_sa, m_sa, n_half_sa},
       {static_cast<const uint16_t*>(vl_x), static_cast<const uint16_t*>(vl_bias), static_cast<uint16_t*>(vl_y),
-       2 * n_half_vl, n_half_vl, m_vl, n_half_vl, 0, 0},
+       2 * n_half_vl, n_half_vl, m_vl, n_half_vl},
   };
   return launch_groups(g, 2, stream);
 }

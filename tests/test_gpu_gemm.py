@@ -6,6 +6,7 @@ gate / up values with the oracle's SwiGLU).  Tolerance: bf16 max-abs <= 2e-2 and
 relative L2 <= 1e-2 (accumulation order differs from the CPU's).
 """
 
+import numpy as np
 import pytest
 import torch
 
@@ -98,6 +99,36 @@ def test_grouped_gemm_swiglu(dev):
     Fn.grouped_gemm(items, "swiglu")
     for (_, _, _, out, _), r in zip(items, refs):
         assert_bf16_close(out, r, "gemm + swiglu")
+
+
+def test_grouped_gemm_swiglu_epilogue_all_gates_bitexact(dev):
+    """The SwiGLU epilogue on every finite normal bf16 gate value.  One-hot A rows
+    make each GEMM output exactly one weight element (every other product is 0),
+    so with a zero bias the result must equal eager `F.silu(g) * u` of those
+    values bit for bit.  Zeros, denormals (the matrix cores may flush them),
+    inf and NaN are left out: 0 * inf in the other products would be NaN."""
+    bits = np.arange(65536, dtype=np.uint16)
+    expo = (bits >> 7) & 0xFF
+    keep = (expo != 0) & (expo != 0xFF)
+    gates = torch.from_numpy(bits[keep].view(np.int16).copy()).view(BF16)
+    n_half, k = 4096, 512
+    m = -(-gates.numel() // n_half)
+    gate_vals = torch.zeros(m * n_half, dtype=BF16)
+    gate_vals[: gates.numel()] = gates
+    gate_vals = gate_vals.view(m, n_half)
+    up_vals = _rand((m, n_half), torch.Generator().manual_seed(23))
+    a = torch.zeros(m, k, dtype=BF16)
+    w = torch.zeros(2 * n_half, k, dtype=BF16)
+    for r in range(m):
+        a[r, 32 * r] = 1.0
+        w[:n_half, 32 * r] = gate_vals[r]
+        w[n_half:, 32 * r] = up_vals[r]
+    out = torch.empty(m, n_half, dtype=BF16, device=dev)
+    zero_bias = torch.zeros(2 * n_half, dtype=BF16, device=dev)
+    Fn.grouped_gemm([(a.to(dev), Fn.pack_weight(w.to(dev), swiglu_pairs=True), zero_bias, out, None)], "swiglu")
+    expect = ref.swiglu(torch.cat([gate_vals, up_vals], dim=1))
+    bad = out.cpu().view(torch.int16) != expect.view(torch.int16)
+    assert not bool(bad.any()), f"{int(bad.sum())} mismatching words, gates {gate_vals[bad][:4].tolist()}"
 
 
 def test_grouped_gemm_deterministic(dev):

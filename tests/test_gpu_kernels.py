@@ -49,11 +49,14 @@ def _all_bf16():
 # ---------------------------------------------------------------------------
 # SwiGLU
 # ---------------------------------------------------------------------------
-def test_swiglu_exhaustive_gate_bitexact(dev):
-    """Every bf16 gate value, several up values: bit-identical to eager CPU."""
-    g = _all_bf16()
-    for up_val in (1.0, -3.0, 0.3125):
-        x = torch.cat([g[None, :], torch.full((1, 65536), up_val, dtype=torch.bfloat16)], dim=1)
+@pytest.mark.parametrize("rows", [1, 64, 1024])
+def test_swiglu_exhaustive_gate_bitexact(dev, rows):
+    """Every bf16 gate value, several up values (3e-30 gives fp32 denormal
+    products): bit-identical to eager CPU.  rows > 1 spreads the gates over a
+    [rows, 65536 / rows] layout (row index from the chunk index)."""
+    g = _all_bf16().view(rows, -1)
+    for up_val in (1.0, -3.0, 0.3125, 3e-30):
+        x = torch.cat([g, torch.full_like(g, up_val)], dim=1)
         y = Fn.swiglu(x.to(dev)).cpu()
         r = ref.swiglu(x)
         same = (y.view(torch.int16) == r.view(torch.int16)) | (torch.isnan(y) & torch.isnan(r))
@@ -70,7 +73,7 @@ def test_swiglu_workload_bitexact(dev, tokens):
     assert torch.equal(y.view(torch.int16), r.view(torch.int16))
 
 
-@pytest.mark.parametrize("rows,n_half", [(0, 64), (1, 8), (3, 13), (5, 1000), (7, 4096)])
+@pytest.mark.parametrize("rows,n_half", [(0, 64), (1, 8), (3, 13), (5, 1000), (7, 4096), (333, 1384), (2, 8 * 4099)])
 def test_swiglu_ragged(dev, rows, n_half):
     g = torch.Generator().manual_seed(rows * 1000 + n_half)
     x = (3 * torch.randn(rows, 2 * n_half, generator=g)).to(torch.bfloat16)
