@@ -196,6 +196,29 @@ def kernel_lines(torch, reps: int):
     out["step_joint_attention_12x608x128"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s", bound="mfma",
                                                   peak=BF16_MFMA_PEAK_TFLOPS, frac=tf / BF16_MFMA_PEAK_TFLOPS,
                                                   flops=fl)
+
+    # residual-add + norm epilogues: the reference's block-boundary shapes (launch-bound)
+    # and the Qwen3-VL prefill shape 1280 x 2048 (HBM-bound)
+    def rows(m, d, std=1.0):
+        return (std * torch.randn(m, d, device=dev)).to(torch.bfloat16)
+
+    def hbm_line(name, fn, nbytes):
+        t = graph_time_ms(fn, reps, torch)
+        g = nbytes / (t * 1e-3) / 1e9
+        out[name] = dict(us=t * 1e3, achieved=g, unit="GB/s", bound="hbm", peak=HBM_PEAK_GBS, frac=g / HBM_PEAK_GBS,
+                         bytes=nbytes)
+
+    sr, sp, sb = rows(18, 1536), rows(18, 1536), rows(1, 1536)[0]
+    vr, vp, vb = rows(128, 4096), rows(128, 4096), rows(1, 4096)[0]
+    hbm_line("grouped_res_ln_18x1536+128x4096",
+             lambda: Fn.fused_grouped_res_ln(sr, sb, sp, vr, vb, vp),
+             3 * 2 * (18 * 1536 + 128 * 4096) + 2 * (1536 + 4096))
+    nv, lv = torch.empty_like(vr), torch.empty_like(vr)
+    hbm_line("vl_epilogue_ln_128x4096",
+             lambda: Fn.fused_vl_epilogue_ln(vr, vb, vb, vp, new_vl_out=nv, ln_vl_out=lv),
+             4 * 2 * 128 * 4096 + 2 * 2 * 4096)
+    lh, lr, lw = rows(1280, 2048), rows(1280, 2048), rows(1, 2048)[0]
+    hbm_line("add2_rmsnorm_1280x2048", lambda: Fn.fused_add2_rmsnorm(lh, lr, lw), 4 * 2 * 1280 * 2048 + 2 * 2048)
     return out
 
 

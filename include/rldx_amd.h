@@ -325,6 +325,63 @@ hipError_t rldx_grouped_gemm_bf16(const rldx_gemm_group_t* groups, int32_t num_g
  */
 int rldx_host_swiglu_bf16(const uint16_t* g, const uint16_t* u, uint16_t* y, int64_t n);
 
+/* ------------------------------------------------------------------------- */
+/* Residual-add + norm epilogues at block boundaries.  Rows are contiguous     */
+/* (row stride = dim), bf16; dim <= 8192.  Outputs may alias inputs exactly   */
+/* (same pointer, same layout), e.g. an in-place residual update.  The fast   */
+/* path needs dim % 8 == 0 and 16-byte aligned rows; other shapes take a      */
+/* slower scalar path.                                                        */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * Per stream s in {sa, vl}: out_s = LayerNorm(res_s + proj_s + bias_s) without
+ * affine; the three-term sum is kept in fp32 (no intermediate rounding), fp32
+ * statistics, one rounding.  bias_s is a [dim_s] vector broadcast over rows.
+ * Replaces: ds::grouped_res_ln / fused_grouped_res_ln
+ *   (rldx/inference/action_model/double_stream/engine/ops/op_grouped_res_ln.py:13-45,
+ *    rldx/inference/action_model/double_stream/engine/kernels/grouped_res_ln.py:40-211).
+ */
+hipError_t rldx_grouped_res_ln_bf16(const void* sa_res, const void* sa_bias, const void* sa_proj, void* sa_out,
+                                    const void* vl_res, const void* vl_bias, const void* vl_proj, void* vl_out,
+                                    int64_t m_sa, int64_t m_vl, int64_t sa_dim, int64_t vl_dim, float eps,
+                                    hipStream_t stream);
+
+/*
+ * new_vl = ((vl_res + proj_bias) + w3_bias) + w3_out, each add rounded to bf16
+ * (eager bf16 tensor adds); ln_vl = LayerNorm(new_vl) without affine.
+ * proj_bias, w3_bias: [dim] vectors broadcast over rows.
+ * Replaces: ds::vl_epilogue_ln / fused_vl_epilogue_ln
+ *   (rldx/inference/action_model/double_stream/engine/ops/op_vl_epilogue_ln.py:13-45,
+ *    rldx/inference/action_model/double_stream/engine/kernels/vl_epilogue_ln.py:31-183).
+ */
+hipError_t rldx_vl_epilogue_ln_bf16(const void* vl_res, const void* proj_bias, const void* w3_bias,
+                                    const void* w3_out, void* new_vl, void* ln_vl, int64_t m, int64_t dim,
+                                    float eps, hipStream_t stream);
+
+/*
+ * With residual: new_hidden = bf16(hidden + residual), ln_out = LayerNorm(new_hidden).
+ * residual == NULL: ln_out = LayerNorm(hidden) and new_hidden is not written
+ * (the hidden state is already final).  LayerNorm without affine.
+ * Replaces: ss::fused_epilogue_ln / fused_ss_epilogue_ln
+ *   (rldx/inference/action_model/single_stream/engine/ops/op_fused_epilogue_ln.py:11-35,
+ *    rldx/inference/action_model/single_stream/engine/kernels/ss_epilogue_ln.py:33-205).
+ */
+hipError_t rldx_ss_epilogue_ln_bf16(const void* hidden, const void* residual, void* new_hidden, void* ln_out,
+                                    int64_t m, int64_t dim, float eps, hipStream_t stream);
+
+/*
+ * new_hidden = bf16(hidden + residual), then bf16(new_hidden + deepstack) when
+ * deepstack != NULL; normed = bf16(weight * bf16(new_hidden * rsqrt(mean(new_hidden^2) + eps)))
+ * (Qwen3VLTextRMSNorm on the rounded sum, the eager arithmetic).
+ * Replaces: rldx_backbone::fused_epilogue_add2_rmsnorm and ::fused_epilogue_add3_rmsnorm
+ *   (rldx/inference/backbone/llm/engine/ops/op_fused_epilogue_add2_rmsnorm.py:20-45,
+ *    op_fused_epilogue_add3_rmsnorm.py:20-47; kernels/fused_add2_rmsnorm.py:29-115,
+ *    kernels/fused_add3_rmsnorm.py:31-83).
+ */
+hipError_t rldx_add_rmsnorm_bf16(const void* hidden, const void* residual, const void* deepstack,
+                                 const void* weight, void* new_hidden, void* normed, int64_t m, int64_t dim,
+                                 float eps, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

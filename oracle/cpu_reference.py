@@ -183,3 +183,51 @@ def mask_to_bias(kv_mask: torch.Tensor) -> torch.Tensor:
 def layer_norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """nn.LayerNorm(dim, elementwise_affine=False, eps) — norms.py:35-36."""
     return F.layer_norm(x, (x.shape[-1],), eps=eps)
+
+
+# ---------------------------------------------------------------------------
+# Residual-add + norm epilogues at block boundaries
+# ---------------------------------------------------------------------------
+def _ln_rows_fp32(x: torch.Tensor, eps: float) -> torch.Tensor:
+    """LayerNorm without affine on fp32 rows, as the reference epilogue kernels
+    write it: mean = sum / D, var = sum((x - mean)^2) / D,
+    out = (x - mean) * (1 / sqrt(var + eps)) (grouped_res_ln.py:81-108)."""
+    d = x.shape[-1]
+    mean = x.sum(-1, keepdim=True) / d
+    diff = x - mean
+    var = (diff * diff).sum(-1, keepdim=True) / d
+    return diff * (1.0 / torch.sqrt(var + eps))
+
+
+def grouped_res_ln(res: torch.Tensor, proj: torch.Tensor, bias: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """One stream of ds::grouped_res_ln — grouped_res_ln.py:74-113: x = res + proj + bias
+    summed in fp32 (no intermediate rounding), LayerNorm, one rounding to bf16."""
+    x = res.float() + proj.float() + bias.float()
+    return _ln_rows_fp32(x, eps).to(torch.bfloat16)
+
+
+def vl_epilogue_ln(res: torch.Tensor, proj_bias: torch.Tensor, w3_bias: torch.Tensor, w3_out: torch.Tensor,
+                   eps: float = 1e-6):
+    """ds::vl_epilogue_ln — vl_epilogue_ln.py:62-85: new = ((res + proj_bias) + w3_bias) + w3_out
+    as bf16 tensor adds (each rounded), ln = LayerNorm(new) in fp32, one rounding."""
+    new = ((res + proj_bias) + w3_bias) + w3_out
+    return new, _ln_rows_fp32(new.float(), eps).to(torch.bfloat16)
+
+
+def ss_epilogue_ln(hidden: torch.Tensor, residual: Optional[torch.Tensor] = None, eps: float = 1e-6):
+    """ss::fused_epilogue_ln — ss_epilogue_ln.py:60-79: new = hidden + residual (bf16 add),
+    ln = LayerNorm(new); without residual ln = LayerNorm(hidden)."""
+    new = hidden + residual if residual is not None else hidden
+    return new, _ln_rows_fp32(new.float(), eps).to(torch.bfloat16)
+
+
+def add_rmsnorm(hidden: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                deepstack: Optional[torch.Tensor] = None, eps: float = 1e-6):
+    """rldx_backbone::fused_epilogue_add{2,3}_rmsnorm in the eager arithmetic the op files
+    promise (op_fused_epilogue_add2_rmsnorm.py:7-10): the decoder layer's
+    `residual + hidden_states` (bf16), the DeepStack add (bf16,
+    Qwen3-VL `_deepstack_process`), then Qwen3VLTextRMSNorm (modeling_qwen3_vl.py:366-371)."""
+    new = residual + hidden
+    if deepstack is not None:
+        new = new + deepstack
+    return new, qwen_rmsnorm(new, weight, eps)

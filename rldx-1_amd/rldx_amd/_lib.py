@@ -88,6 +88,11 @@ SIGNATURES = {
     "rldx_layernorm_pack_bf16": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_f32, c_vp, c_vp]),
     "rldx_grouped_gemm_bf16": (c_i32, [ctypes.POINTER(GemmGroup), c_i32, c_i64, c_i64, c_i32, c_vp]),
     "rldx_host_swiglu_bf16": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64]),
+    "rldx_grouped_res_ln_bf16": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                         c_i64, c_i64, c_i64, c_i64, c_f32, c_vp]),
+    "rldx_vl_epilogue_ln_bf16": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_f32, c_vp]),
+    "rldx_ss_epilogue_ln_bf16": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_f32, c_vp]),
+    "rldx_add_rmsnorm_bf16": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_f32, c_vp]),
 }
 
 ROPE_SIN_SIGNED = 1  # RLDX_ROPE_SIN_SIGNED

@@ -531,6 +531,155 @@ def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias") -> None:
                "rldx_grouped_gemm_bf16")
 
 
+# ---------------------------------------------------------------------------
+# Residual-add + norm epilogues (block boundaries)
+# ---------------------------------------------------------------------------
+def _rows_of(t: torch.Tensor, m: int, d: int, what: str, reshape: bool = False) -> torch.Tensor:
+    """t as contiguous [m, d] bf16 rows: the reference launchers' `.view(M, DIM)`
+    (contiguous input required), or with reshape=True their `.reshape(M, D)`
+    (a strided input is first copied on the device)."""
+    _require(t.dtype == BF16, f"{what} must be bfloat16")
+    _require(t.numel() == m * d, f"{what} must hold {m} x {d} elements")
+    if reshape:
+        return t.reshape(m, d).contiguous()
+    _require(t.is_contiguous(), f"{what} must be contiguous")
+    return t.view(m, d)
+
+
+def _vec_of(t: torch.Tensor, d: int, what: str) -> torch.Tensor:
+    _require(t.dtype == BF16 and t.dim() == 1 and t.shape[0] == d and t.is_contiguous(),
+             f"{what} must be a contiguous bf16 [{d}] vector")
+    return t
+
+
+def _out_rows(out: Optional[torch.Tensor], m: int, d: int, like: torch.Tensor, what: str) -> torch.Tensor:
+    if out is None:
+        return torch.empty((1, m, d), dtype=BF16, device=like.device)
+    _on_gpu(out, like)
+    _rows_of(out, m, d, what)
+    return out
+
+
+def _lead_rows(t: torch.Tensor):
+    return t.shape[1] if t.dim() == 3 else t.shape[0]
+
+
+def fused_grouped_res_ln(sa_residual: torch.Tensor, sa_proj_bias: torch.Tensor, sa_proj_out: torch.Tensor,
+                         vl_residual: torch.Tensor, vl_proj_bias: torch.Tensor, vl_proj_out: torch.Tensor,
+                         M_sa: Optional[int] = None, M_vl: Optional[int] = None, SA_DIM: Optional[int] = None,
+                         VL_DIM: Optional[int] = None, eps: float = 1e-6):
+    """Per stream: LayerNorm(residual + proj_out + proj_bias), fp32 sum, no affine.
+
+    Mirrors fused_grouped_res_ln, rldx/inference/action_model/double_stream/engine/
+    kernels/grouped_res_ln.py:151-211 (eps 1e-6 there, fixed).  Returns
+    (sa_out [1, M_sa, SA_DIM], vl_out [1, M_vl, VL_DIM])."""
+    _on_gpu(sa_residual, sa_proj_bias, sa_proj_out, vl_residual, vl_proj_bias, vl_proj_out)
+    M_sa = _lead_rows(sa_residual) if M_sa is None else M_sa
+    M_vl = _lead_rows(vl_residual) if M_vl is None else M_vl
+    SA_DIM = sa_residual.shape[-1] if SA_DIM is None else SA_DIM
+    VL_DIM = vl_residual.shape[-1] if VL_DIM is None else VL_DIM
+    sr = _rows_of(sa_residual, M_sa, SA_DIM, "sa_residual")
+    sp = _rows_of(sa_proj_out, M_sa, SA_DIM, "sa_proj_out")
+    sb = _vec_of(sa_proj_bias, SA_DIM, "sa_proj_bias")
+    vr = _rows_of(vl_residual, M_vl, VL_DIM, "vl_residual")
+    vp = _rows_of(vl_proj_out, M_vl, VL_DIM, "vl_proj_out")
+    vb = _vec_of(vl_proj_bias, VL_DIM, "vl_proj_bias")
+    sa_out = torch.empty((1, M_sa, SA_DIM), dtype=BF16, device=sr.device)
+    vl_out = torch.empty((1, M_vl, VL_DIM), dtype=BF16, device=sr.device)
+    lib = _lib.load()
+    _lib.check(lib.rldx_grouped_res_ln_bf16(sr.data_ptr(), sb.data_ptr(), sp.data_ptr(), sa_out.data_ptr(),
+                                            vr.data_ptr(), vb.data_ptr(), vp.data_ptr(), vl_out.data_ptr(),
+                                            M_sa, M_vl, SA_DIM, VL_DIM, eps, _stream_ptr(sr)),
+               "rldx_grouped_res_ln_bf16")
+    return sa_out, vl_out
+
+
+def fused_vl_epilogue_ln(vl_residual: torch.Tensor, proj_bias: torch.Tensor, w3_bias: torch.Tensor,
+                         w3_out: torch.Tensor, M: Optional[int] = None, DIM: Optional[int] = None,
+                         new_vl_out: Optional[torch.Tensor] = None, ln_vl_out: Optional[torch.Tensor] = None,
+                         eps: float = 1e-6):
+    """new_vl = ((residual + proj_bias) + w3_bias) + w3_out (bf16 adds); ln_vl = LayerNorm(new_vl).
+
+    Mirrors fused_vl_epilogue_ln, rldx/inference/action_model/double_stream/engine/
+    kernels/vl_epilogue_ln.py:128-183, including the static `new_vl_out` /
+    `ln_vl_out` buffers.  Returns (new_vl, ln_vl), both [1, M, DIM]."""
+    _on_gpu(vl_residual, proj_bias, w3_bias, w3_out)
+    M = _lead_rows(vl_residual) if M is None else M
+    DIM = vl_residual.shape[-1] if DIM is None else DIM
+    r = _rows_of(vl_residual, M, DIM, "vl_residual")
+    w3 = _rows_of(w3_out, M, DIM, "w3_out")
+    pb = _vec_of(proj_bias, DIM, "proj_bias")
+    wb = _vec_of(w3_bias, DIM, "w3_bias")
+    new_vl = _out_rows(new_vl_out, M, DIM, r, "new_vl_out")
+    ln_vl = _out_rows(ln_vl_out, M, DIM, r, "ln_vl_out")
+    lib = _lib.load()
+    _lib.check(lib.rldx_vl_epilogue_ln_bf16(r.data_ptr(), pb.data_ptr(), wb.data_ptr(), w3.data_ptr(),
+                                            new_vl.data_ptr(), ln_vl.data_ptr(), M, DIM, eps, _stream_ptr(r)),
+               "rldx_vl_epilogue_ln_bf16")
+    return new_vl, ln_vl
+
+
+def fused_ss_epilogue_ln(hidden: torch.Tensor, M: Optional[int] = None, DIM: Optional[int] = None,
+                         residual: Optional[torch.Tensor] = None, new_hidden_out: Optional[torch.Tensor] = None,
+                         ln_out_out: Optional[torch.Tensor] = None, eps: float = 1e-6):
+    """With residual: new_hidden = hidden + residual (bf16), ln = LayerNorm(new_hidden);
+    without: new_hidden = hidden (no copy), ln = LayerNorm(hidden).
+
+    Mirrors fused_ss_epilogue_ln, rldx/inference/action_model/single_stream/engine/
+    kernels/ss_epilogue_ln.py:146-205.  Returns (new_hidden [1, M, DIM], ln [1, M, DIM])."""
+    _on_gpu(hidden, residual)
+    M = _lead_rows(hidden) if M is None else M
+    DIM = hidden.shape[-1] if DIM is None else DIM
+    h = _rows_of(hidden, M, DIM, "hidden")
+    if residual is not None:
+        r = _rows_of(residual, M, DIM, "residual")
+        new_hidden = _out_rows(new_hidden_out, M, DIM, h, "new_hidden_out")
+        r_ptr, n_ptr = r.data_ptr(), new_hidden.data_ptr()
+    else:
+        new_hidden = hidden if hidden.dim() == 3 else hidden.view(1, M, DIM)
+        r_ptr, n_ptr = None, None
+    ln = _out_rows(ln_out_out, M, DIM, h, "ln_out_out")
+    lib = _lib.load()
+    _lib.check(lib.rldx_ss_epilogue_ln_bf16(h.data_ptr(), r_ptr, n_ptr, ln.data_ptr(), M, DIM, eps, _stream_ptr(h)),
+               "rldx_ss_epilogue_ln_bf16")
+    return new_hidden, ln
+
+
+def fused_add_rmsnorm(hidden: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                      deepstack: Optional[torch.Tensor] = None, eps: float = 1e-6):
+    """new_hidden = hidden + residual [+ deepstack] (bf16 adds, in that order);
+    normed = Qwen3VLTextRMSNorm(new_hidden) = bf16(weight * bf16(x * rsqrt(mean(x^2) + eps))).
+
+    The `forward` of rldx/inference/backbone/llm/engine/kernels/fused_add2_rmsnorm.py:86-115
+    (deepstack=None) and fused_add3_rmsnorm.py (with deepstack), with the eager
+    rounding of modeling_qwen3_vl.py:366-371.  Returns (new_hidden, normed) shaped like hidden."""
+    _on_gpu(hidden, residual, weight, deepstack)
+    shape = hidden.shape
+    D = shape[-1]
+    M = hidden.numel() // D if D else 0
+    h = _rows_of(hidden, M, D, "hidden", reshape=True)
+    r = _rows_of(residual, M, D, "residual", reshape=True)
+    ds = None if deepstack is None else _rows_of(deepstack, M, D, "deepstack", reshape=True)
+    w = _vec_of(weight, D, "weight")
+    new_hidden = torch.empty_like(h)
+    normed = torch.empty_like(h)
+    lib = _lib.load()
+    _lib.check(lib.rldx_add_rmsnorm_bf16(h.data_ptr(), r.data_ptr(), _ptr(ds), w.data_ptr(), new_hidden.data_ptr(),
+                                         normed.data_ptr(), M, D, eps, _stream_ptr(h)),
+               "rldx_add_rmsnorm_bf16")
+    return new_hidden.view(shape), normed.view(shape)
+
+
+def fused_add2_rmsnorm(hidden: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor):
+    """fused_add2_rmsnorm.forward(hidden, residual, weight) (fused_add2_rmsnorm.py:86-115)."""
+    return fused_add_rmsnorm(hidden, residual, weight)
+
+
+def fused_add3_rmsnorm(hidden: torch.Tensor, residual: torch.Tensor, deepstack: torch.Tensor, weight: torch.Tensor):
+    """fused_add3_rmsnorm.forward(hidden, residual, deepstack, weight) (fused_add3_rmsnorm.py:86-117)."""
+    return fused_add_rmsnorm(hidden, residual, weight, deepstack)
+
+
 def mask_to_key_bias(kv_mask: torch.Tensor) -> torch.Tensor:
     """1 = visible / 0 = masked (the eager encoder_attention_mask convention,
     blocks.py:843-864) -> fp32 additive bias 0 / -inf."""

@@ -3,8 +3,11 @@
 Importing this module registers, backed by the gfx950 kernels of librldx_amd.so:
 
   ds::fused_attention_2way   ds::fused_attention_3way   ds::grouped_swiglu
+  ds::grouped_res_ln         ds::vl_epilogue_ln
   ss::fused_attention_2way   ss::fused_attention_3way   ss::fused_mlp_swiglu
+  ss::fused_epilogue_ln
   rldx_backbone::fused_attention
+  rldx_backbone::fused_epilogue_add2_rmsnorm   rldx_backbone::fused_epilogue_add3_rmsnorm
   rldx_amd::swiglu           (the eager `F.silu(x1) * x2` the chains inline)
 
 Argument order and defaults follow the reference registrations
@@ -330,3 +333,103 @@ def ss_fused_mlp_swiglu(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tenso
 @ss_fused_mlp_swiglu.register_fake
 def _(x, weight, bias, split_k=1):
     return x.new_empty((x.shape[0], weight.shape[0] // 2))
+
+
+# ---------------------------------------------------------------------------
+# Residual-add + norm epilogues at block boundaries
+# ---------------------------------------------------------------------------
+
+
+@torch.library.custom_op("ds::grouped_res_ln", mutates_args=())
+def ds_grouped_res_ln(
+    sa_res: torch.Tensor,
+    sa_bias: torch.Tensor,
+    sa_proj: torch.Tensor,
+    vl_res: torch.Tensor,
+    vl_bias: torch.Tensor,
+    vl_proj: torch.Tensor,
+    m_sa: int,
+    m_vl: int,
+    sa_dim: int,
+    vl_dim: int,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per stream LayerNorm(residual + proj_output + proj_bias), no affine, fp32 sum.
+
+    Reference: op_grouped_res_ln.py:13-45 (kernel grouped_res_ln.py:40-148)."""
+    return Fn.fused_grouped_res_ln(sa_res, sa_bias, sa_proj, vl_res, vl_bias, vl_proj, M_sa=m_sa, M_vl=m_vl,
+                                   SA_DIM=sa_dim, VL_DIM=vl_dim)
+
+
+@ds_grouped_res_ln.register_fake
+def _(sa_res, sa_bias, sa_proj, vl_res, vl_bias, vl_proj, m_sa, m_vl, sa_dim, vl_dim):
+    return sa_res.new_empty((1, m_sa, sa_dim)), vl_res.new_empty((1, m_vl, vl_dim))
+
+
+@torch.library.custom_op("ds::vl_epilogue_ln", mutates_args=())
+def ds_vl_epilogue_ln(
+    vl_res: torch.Tensor,
+    proj_bias: torch.Tensor,
+    w3_bias: torch.Tensor,
+    w3_out: torch.Tensor,
+    m: int,
+    dim: int,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """new_vl = ((vl_res + proj_bias) + w3_bias) + w3_out (bf16 adds); ln_vl = LayerNorm(new_vl).
+
+    Reference: op_vl_epilogue_ln.py:13-45 (kernel vl_epilogue_ln.py:31-125)."""
+    return Fn.fused_vl_epilogue_ln(vl_res, proj_bias, w3_bias, w3_out, M=m, DIM=dim)
+
+
+@ds_vl_epilogue_ln.register_fake
+def _(vl_res, proj_bias, w3_bias, w3_out, m, dim):
+    return vl_res.new_empty((1, m, dim)), vl_res.new_empty((1, m, dim))
+
+
+@torch.library.custom_op("ss::fused_epilogue_ln", mutates_args=())
+def ss_fused_epilogue_ln(hidden: torch.Tensor, residual: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """new_hidden = hidden + residual (bf16); ln_out = LayerNorm(new_hidden).
+
+    Reference: single_stream/engine/ops/op_fused_epilogue_ln.py:11-35, which fixes
+    DIM = 1536; here DIM is hidden.shape[-1] (M = hidden.shape[1] as there)."""
+    new_hidden, ln = Fn.fused_ss_epilogue_ln(hidden, M=hidden.shape[1], DIM=hidden.shape[-1], residual=residual)
+    return new_hidden.view(hidden.shape), ln.view(hidden.shape)
+
+
+@ss_fused_epilogue_ln.register_fake
+def _(hidden, residual):
+    return torch.empty_like(hidden), torch.empty_like(hidden)
+
+
+@torch.library.custom_op("rldx_backbone::fused_epilogue_add2_rmsnorm", mutates_args=())
+def rldx_backbone_fused_epilogue_add2_rmsnorm(
+    hidden: torch.Tensor,
+    residual: torch.Tensor,
+    weight: torch.Tensor,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """new_hidden = hidden + residual (bf16); normed = RMSNorm(new_hidden) (Qwen3-VL, eager rounding).
+
+    Reference: backbone/llm/engine/ops/op_fused_epilogue_add2_rmsnorm.py:20-45."""
+    return Fn.fused_add2_rmsnorm(hidden, residual, weight)
+
+
+@rldx_backbone_fused_epilogue_add2_rmsnorm.register_fake
+def _(hidden, residual, weight):
+    return torch.empty_like(hidden), torch.empty_like(hidden)
+
+
+@torch.library.custom_op("rldx_backbone::fused_epilogue_add3_rmsnorm", mutates_args=())
+def rldx_backbone_fused_epilogue_add3_rmsnorm(
+    hidden: torch.Tensor,
+    residual: torch.Tensor,
+    deepStack: torch.Tensor,
+    weight: torch.Tensor,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """new_hidden = (hidden + residual) + deepStack (bf16 adds); normed = RMSNorm(new_hidden).
+
+    Reference: backbone/llm/engine/ops/op_fused_epilogue_add3_rmsnorm.py:20-47."""
+    return Fn.fused_add3_rmsnorm(hidden, residual, deepStack, weight)
+
+
+@rldx_backbone_fused_epilogue_add3_rmsnorm.register_fake
+def _(hidden, residual, deepStack, weight):
+    return torch.empty_like(hidden), torch.empty_like(hidden)

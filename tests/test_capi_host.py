@@ -64,6 +64,29 @@ def test_host_swiglu_random_pairs():
     assert not ((mine != rb) & ~both_nan).any()
 
 
+def test_epilogue_norm_abi_rejects_bad_arguments_without_launching():
+    lib = _lib.load()
+    p = 16  # stand-in device address: every call below must fail validation before any launch
+    # row wider than 8192
+    assert lib.rldx_grouped_res_ln_bf16(p, p, p, p, p, p, p, p, 1, 1, 8200, 16, 1e-6, None) == HIP_INVALID_VALUE
+    # negative rows, null operand with work to do, negative eps
+    assert lib.rldx_grouped_res_ln_bf16(p, p, p, p, p, p, p, p, -1, 1, 16, 16, 1e-6, None) == HIP_INVALID_VALUE
+    assert lib.rldx_grouped_res_ln_bf16(p, None, p, p, p, p, p, p, 2, 0, 16, 16, 1e-6, None) == HIP_INVALID_VALUE
+    assert lib.rldx_grouped_res_ln_bf16(p, p, p, p, p, p, p, p, 2, 2, 16, 16, -1.0, None) == HIP_INVALID_VALUE
+    # zero-width rows with work to do
+    assert lib.rldx_ss_epilogue_ln_bf16(p, None, None, p, 3, 0, 1e-6, None) == HIP_INVALID_VALUE
+    # missing new-hidden output
+    assert lib.rldx_vl_epilogue_ln_bf16(p, p, p, p, None, p, 2, 16, 1e-6, None) == HIP_INVALID_VALUE
+    assert lib.rldx_ss_epilogue_ln_bf16(p, p, None, p, 2, 16, 1e-6, None) == HIP_INVALID_VALUE
+    assert lib.rldx_add_rmsnorm_bf16(p, p, None, p, None, p, 2, 16, 1e-6, None) == HIP_INVALID_VALUE
+    # RMSNorm without a weight
+    assert lib.rldx_add_rmsnorm_bf16(p, p, None, None, p, p, 2, 16, 1e-6, None) == HIP_INVALID_VALUE
+    # nothing to do
+    assert lib.rldx_grouped_res_ln_bf16(None, None, None, None, None, None, None, None, 0, 0, 16, 16, 1e-6,
+                                        None) == 0
+    assert lib.rldx_add_rmsnorm_bf16(None, None, None, None, None, None, 0, 2048, 1e-6, None) == 0
+
+
 def test_capi_rejects_bad_arguments_without_launching():
     lib = _lib.load()
     # ldx smaller than 2*n_half
