@@ -225,7 +225,7 @@ hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* kv_packed, 
  * attention, scale 1/sqrt(D).  Three launches: K normalisation and K/V packing into
  * `workspace` (>= rldx_llm_fused_attention_workspace_bytes(seq, Hkv, D) bytes,
  * 16-byte aligned, caller-owned), then attention with the Q normalisation fused
- * into its prologue.
+ * into its prologue.  qkv, out, cos, sin and q_norm_w are 16-byte aligned.
  *
  * Replaces: fused_llm_attention.forward(qkv, q_norm_w, q_norm_w_rot, k_norm_w,
  *   k_norm_w_rot, cos, signed_sin, num_heads, num_kv_heads, head_dim, out)

@@ -122,65 +122,80 @@ struct AttnArgs {
 
 __device__ __forceinline__ float bf(uint16_t b) { return bf16_bits_to_f32(b); }
 
-template <int D>
-__device__ __forceinline__ void qnorm_rope_operands(bf16x8 (&qreg)[D / 16], const AttnArgs& a, int pos, bool valid) {
-  // Lane holds d = 16*ks + 8*g + i (g = lane half).  Row sum: own D/2 values + lane ^ 32.
-  // The rotate-half partner of d is d +- D/2, i.e. ks +- D/32 in the same lane.
-  constexpr int KS = D / 16;
-  const int g = (threadIdx.x & 63) >> 5;
-  float x[KS][8];
+// Q RMSNorm (Qwen3VLTextRMSNorm: y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))))
+// + rotate-half RoPE (bf16(bf16(y * cos) + bf16(rot(y) * sin))) of the
+// workgroup's 32 query rows, done once per workgroup: wave w < KS/2 computes
+// column chunks w and w + KS/2 (a rotate-half pair, so no other chunk is
+// needed) and writes them to `qsh`; after the barrier every wave loads its Q
+// operands from there.  Lane holds d = 16*ks + 8*g + i (g = lane half); the
+// row sum of squares is over the lane's own D/2 values + those of lane ^ 32.
+// Roundings to bf16 use v_cvt_pk_bf16_f32 (round to nearest even).  The chunk
+// index is a template parameter: a run-time index into the register array
+// would compile to select chains over every chunk.
+template <int D, int K0>
+__device__ __forceinline__ void qnorm_rope_pair(const bf16x8 (&qreg)[D / 16], const AttnArgs& a, int pos, bool valid,
+                                                u32x4* qsh) {
+#pragma clang fp contract(off)
+  constexpr int KS = D / 16, K1 = K0 + KS / 2;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 5;
+  const uint16_t* cr = a.cos + static_cast<int64_t>(valid ? pos : 0) * a.cs_ss + g * 8;
+  const uint16_t* sr = a.sin + static_cast<int64_t>(valid ? pos : 0) * a.cs_ss + g * 8;
+  const u32x4 w0 = *reinterpret_cast<const u32x4*>(a.q_norm_w + K0 * 16 + g * 8);
+  const u32x4 w1 = *reinterpret_cast<const u32x4*>(a.q_norm_w + K1 * 16 + g * 8);
+  const u32x4 c0 = *reinterpret_cast<const u32x4*>(cr + K0 * 16), c1 = *reinterpret_cast<const u32x4*>(cr + K1 * 16);
+  const u32x4 s0 = *reinterpret_cast<const u32x4*>(sr + K0 * 16), s1 = *reinterpret_cast<const u32x4*>(sr + K1 * 16);
   float ss = 0.f;
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     const u32x4 raw = __builtin_bit_cast(u32x4, qreg[ks]);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t w = raw[i >> 1];
-      x[ks][i] = bf(static_cast<uint16_t>((i & 1) ? (w >> 16) : (w & 0xffffu)));
-      ss += x[ks][i] * x[ks][i];
+    for (int j = 0; j < 4; ++j) {
+      const float lo = bf16x2_lo(raw[j]), hi = bf16x2_hi(raw[j]);
+      ss += lo * lo;
+      ss += hi * hi;
     }
   }
   ss = pair_sum(ss);
-  float y[KS][8];
-  {
-#pragma clang fp contract(off)
-    const float rinv = 1.0f / __builtin_sqrtf(ss * (1.0f / D) + a.eps);
+  const float rinv = 1.0f / __builtin_sqrtf(ss * (1.0f / D) + a.eps);
+  const u32x4 x0 = __builtin_bit_cast(u32x4, qreg[K0]), x1 = __builtin_bit_cast(u32x4, qreg[K1]);
+  u32x4 o0, o1;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int d = ks * 16 + g * 8 + i;
-        y[ks][i] = round_bf16(bf(a.q_norm_w[d]) * round_bf16(x[ks][i] * rinv));
-      }
+  for (int j = 0; j < 4; ++j) {
+    // y = bf16(w * bf16(x * rinv)) for the two elements of word j of both chunks
+    const uint32_t n0 = pack_bf16x2(bf16x2_lo(x0[j]) * rinv, bf16x2_hi(x0[j]) * rinv);
+    const uint32_t n1 = pack_bf16x2(bf16x2_lo(x1[j]) * rinv, bf16x2_hi(x1[j]) * rinv);
+    const uint32_t y0 = pack_bf16x2(bf16x2_lo(w0[j]) * bf16x2_lo(n0), bf16x2_hi(w0[j]) * bf16x2_hi(n0));
+    const uint32_t y1 = pack_bf16x2(bf16x2_lo(w1[j]) * bf16x2_lo(n1), bf16x2_hi(w1[j]) * bf16x2_hi(n1));
+    const float y0l = bf16x2_lo(y0), y0h = bf16x2_hi(y0), y1l = bf16x2_lo(y1), y1h = bf16x2_hi(y1);
+    // chunk K0 (first half): partner -y1 (+y1 with a pre-signed sin); chunk K1: partner +y0
+    const float r0l = a.sin_signed ? y1l : -y1l, r0h = a.sin_signed ? y1h : -y1h;
+    const uint32_t t0 = pack_bf16x2(y0l * bf16x2_lo(c0[j]), y0h * bf16x2_hi(c0[j]));
+    const uint32_t u0 = pack_bf16x2(r0l * bf16x2_lo(s0[j]), r0h * bf16x2_hi(s0[j]));
+    const uint32_t t1 = pack_bf16x2(y1l * bf16x2_lo(c1[j]), y1h * bf16x2_hi(c1[j]));
+    const uint32_t u1 = pack_bf16x2(y0l * bf16x2_lo(s1[j]), y0h * bf16x2_hi(s1[j]));
+    o0[j] = pack_bf16x2(bf16x2_lo(t0) + bf16x2_lo(u0), bf16x2_hi(t0) + bf16x2_hi(u0));
+    o1[j] = pack_bf16x2(bf16x2_lo(t1) + bf16x2_lo(u1), bf16x2_hi(t1) + bf16x2_hi(u1));
   }
-  const uint16_t* cr = a.cos + static_cast<int64_t>(valid ? pos : 0) * a.cs_ss + g * 8;
-  const uint16_t* sr = a.sin + static_cast<int64_t>(valid ? pos : 0) * a.cs_ss + g * 8;
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    const int pks = ks < KS / 2 ? ks + KS / 2 : ks - KS / 2;
-    const u32x4 craw = *reinterpret_cast<const u32x4*>(cr + ks * 16);
-    const u32x4 sraw = *reinterpret_cast<const u32x4*>(sr + ks * 16);
-    u32x4 outraw;
-#pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-      uint32_t packed = 0;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-#pragma clang fp contract(off)
-        const int ii = i + h;
-        const uint32_t cw = craw[ii >> 1], sw = sraw[ii >> 1];
-        const float cv = bf(static_cast<uint16_t>(h ? (cw >> 16) : (cw & 0xffffu)));
-        const float sv = bf(static_cast<uint16_t>(h ? (sw >> 16) : (sw & 0xffffu)));
-        const float part = y[pks][ii];
-        const float rot = (a.sin_signed || ks >= KS / 2) ? part : -part;
-        const float t1 = round_bf16(y[ks][ii] * cv);
-        const float t2 = round_bf16(rot * sv);
-        packed |= static_cast<uint32_t>(f32_to_bf16_bits(t1 + t2)) << (16 * h);
-      }
-      outraw[i >> 1] = packed;
-    }
-    qreg[ks] = __builtin_bit_cast(bf16x8, outraw);
+  qsh[K0 * 64 + lane] = o0;
+  qsh[K1 * 64 + lane] = o1;
+}
+
+template <int D>
+__device__ __forceinline__ void qnorm_rope_shared(bf16x8 (&qreg)[D / 16], const AttnArgs& a, int pos, bool valid,
+                                                  int wave, u32x4* qsh) {
+  constexpr int KS = D / 16;
+  static_assert(KS / 2 <= 4, "one rotate-half chunk pair per wave");
+  if (wave == 0) qnorm_rope_pair<D, 0>(qreg, a, pos, valid, qsh);
+  else if (wave == 1) qnorm_rope_pair<D, 1>(qreg, a, pos, valid, qsh);
+  else if constexpr (KS / 2 > 2) {
+    if (wave == 2) qnorm_rope_pair<D, 2>(qreg, a, pos, valid, qsh);
+    else if (wave == 3) qnorm_rope_pair<D, 3>(qreg, a, pos, valid, qsh);
   }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) qreg[ks] = __builtin_bit_cast(bf16x8, qsh[ks * 64 + lane]);
 }
 
 template <int D, int NSUB, bool kCausal, bool kBias, bool kQNorm>
@@ -257,7 +272,11 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks)
       qreg[j][ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qrow + ks * 16));
-    if constexpr (kQNorm) qnorm_rope_operands<D>(qreg[j], a, q_idx[j], q_idx[j] < a.sq);
+    if constexpr (kQNorm) {
+      static_assert(NSUB == 1, "the fused Q normalisation handles one 32-query sub-block");
+      __shared__ u32x4 qsh[KSTEPS * 64];
+      qnorm_rope_shared<D>(qreg[j], a, q_idx[j], q_idx[j] < a.sq, wave, qsh);
+    }
   }
 
   floatx16 oacc[NSUB][DBLK];
@@ -676,7 +695,8 @@ extern "C" hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv
     return hipErrorInvalidValue;
   if (workspace_bytes < rldx_llm_fused_attention_workspace_bytes(seq, kv_heads, head_dim))
     return hipErrorInvalidValue;
-  if (!a16(qkv) || !a16(out) || !a16(cos) || !a16(sin) || !a16(workspace)) return hipErrorInvalidValue;
+  if (!a16(qkv) || !a16(out) || !a16(cos) || !a16(sin) || !a16(workspace) || !a16(q_norm_w))
+    return hipErrorInvalidValue;
   if (seq > (1 << 24) || q_heads > 65535) return hipErrorInvalidValue;
   const uint16_t* base = static_cast<const uint16_t*>(qkv);
   uint16_t* kws = static_cast<uint16_t*>(workspace);  // normalised K, [seq, kv_heads, D]
