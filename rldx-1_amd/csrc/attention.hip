@@ -247,9 +247,27 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
   // dword past sk is out of the descriptor's range and reads as 0.
   __amdgpu_buffer_rsrc_t bsr;
   if constexpr (kBias) bsr = make_rsrc(a.key_bias + b * a.kb_sb, a.sk * 4);
+  // Per-wave bias flags: bit i of `wbias` is set when tile wave + 4 i (the
+  // wave's i-th tile) has a bias entry that is not +0 / -0 (a key-padding mask
+  // is zero almost everywhere).  Only flagged tiles load and add the bias; the
+  // scan covers a wave's first 2 * kScanLoads tiles, later tiles are always
+  // treated as flagged.  The scan loads are issued first, so the wait for Q
+  // and K (in-order load counter) covers them too, and no barrier is needed.
+  constexpr int kScanLoads = 16;
+  const int my_tiles = (ntiles - wave + NW - 1) / NW;
+  uint64_t wbias = 0;
+  float bscan[kScanLoads];
+  if constexpr (kBias) {
+#pragma unroll
+    for (int r = 0; r < kScanLoads; ++r) {
+      bscan[r] = 0.f;
+      if (2 * r < my_tiles)  // lanes 0-31: tile slot 2r, lanes 32-63: slot 2r + 1
+        bscan[r] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(bsr, ((wave + NW * (2 * r + g)) * BN + l32) * 4, 0, 0));
+    }
+  }
 
   u32x4 kop[KSTEPS], vop[2 * DBLK];
-  floatx4 bnext[4];
   {
     const int t0 = min(wave, ntiles - 1);
     const int s0 = t0 * TILE_BYTES;
@@ -258,7 +276,6 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
     for (int c = 0; c < 2 * DBLK; ++c)
       vop[c] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + VPART + c * 1024, s0, 0);
-    if constexpr (kBias) load_bias(bnext, bsr, t0 * BN + 4 * g);
   }
 
   // ---- Q^T operands: sub-block j, lane holds query l32 and d-chunk (2*ks + g) ----
@@ -279,6 +296,20 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
     }
   }
 
+  // bias flags (NaN != 0 is true: a NaN bias is applied, not skipped), and the
+  // bias of the wave's first tile when it is flagged
+  floatx4 bnext[4] = {};
+  if constexpr (kBias) {
+#pragma unroll
+    for (int r = 0; r < kScanLoads; ++r) {
+      const uint64_t bal = __ballot(bscan[r] != 0.f);
+      if (bal & 0xffffffffull) wbias |= 1ull << (2 * r);
+      if (bal >> 32) wbias |= 1ull << (2 * r + 1);
+    }
+    if (my_tiles > 2 * kScanLoads) wbias |= ~0ull << (2 * kScanLoads);
+    if ((wbias & 1ull) && my_tiles > 0) load_bias(bnext, bsr, wave * BN + 4 * g);
+  }
+
   floatx16 oacc[NSUB][DBLK];
   float m_ref[NSUB], l_part[NSUB];
 #pragma unroll
@@ -290,7 +321,7 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
   }
   const float c = a.scale_log2;
 
-  for (int t = wave; t < ntiles; t += NW) {
+  for (int t = wave, ti = 0; t < ntiles; t += NW, ++ti) {
     const int k0 = t * BN;
     const int sn = min(t + NW, ntiles - 1) * TILE_BYTES;  // next tile of this wave (clamped)
 
@@ -311,18 +342,16 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
     // ---- next tile's K operands, in flight during the softmax and P.V below ----
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) kop[ks] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + ks * 1024, sn, 0);
-    floatx4 bq[4];
+    floatx4 bq[4] = {};
     bool bias_tile = false;
     if constexpr (kBias) {
-      float any_nz = 0.f;
+      bias_tile = ti >= 64 || ((wbias >> ti) & 1ull);
+      if (bias_tile) {
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        bq[qq] = bnext[qq];
-        any_nz = fmaxf(any_nz, fmaxf(fmaxf(__builtin_fabsf(bq[qq][0]), __builtin_fabsf(bq[qq][1])),
-                                     fmaxf(__builtin_fabsf(bq[qq][2]), __builtin_fabsf(bq[qq][3]))));
+        for (int qq = 0; qq < 4; ++qq) bq[qq] = bnext[qq];
       }
-      bias_tile = __any(any_nz != 0.f);
-      load_bias(bnext, bsr, sn / TILE_BYTES * BN + 4 * g);
+      // the next flagged tile's bias, in flight during this tile's softmax and P.V
+      if (ti + 1 < my_tiles && (ti + 1 >= 64 || ((wbias >> (ti + 1)) & 1ull))) load_bias(bnext, bsr, sn / TILE_BYTES * BN + 4 * g);
     }
 
 #pragma unroll
@@ -413,37 +442,50 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < NSUB; ++j) {
+    // every LDS read of this lane is issued before the arithmetic that uses it
+    floatx4 ml[NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) ml[w] = merge[(w * NSUB + j) * (G4 * 64) + (DBLK * 4) * 64 + lane];
+    constexpr int DPW = (DBLK + NW - 1) / NW;  // d-blocks finalised per wave
+    floatx4 part[DPW][4][NW];
+#pragma unroll
+    for (int r = 0; r < DPW; ++r) {
+      const int db = wave + r * NW;
+      if (db < DBLK) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+          for (int w = 0; w < NW; ++w) part[r][q4][w] = merge[(w * NSUB + j) * (G4 * 64) + (db * 4 + q4) * 64 + lane];
+      }
+    }
     float wgt[NW];
-    float lw[NW];
     float m = -__builtin_inff();
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const floatx4 ml = merge[(w * NSUB + j) * (G4 * 64) + (DBLK * 4) * 64 + lane];
-      wgt[w] = ml[0];
-      lw[w] = ml[1];
-      m = fmaxf(m, wgt[w]);
-    }
+    for (int w = 0; w < NW; ++w) m = fmaxf(m, ml[w][0]);
     float l = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      wgt[w] = (wgt[w] == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(wgt[w] - m);
-      l += lw[w] * wgt[w];
+      wgt[w] = (ml[w][0] == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(ml[w][0] - m);
+      l += ml[w][1] * wgt[w];
     }
     l = pair_sum(l);
     const float inv = l > 0.f ? 1.0f / l : 0.f;
     if (q_idx[j] < a.sq) {
       uint16_t* orow = a.o + b * a.o_sb + h * a.o_sh + static_cast<int64_t>(q_idx[j]) * a.o_ss;
-      for (int db = wave; db < DBLK; db += NW) {
+#pragma unroll
+      for (int r = 0; r < DPW; ++r) {
+        const int db = wave + r * NW;
+        if (db >= DBLK) break;
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
-          floatx4 acc = floatx4{};
+          floatx4 acc = part[r][q4][0] * wgt[0];
 #pragma unroll
-          for (int w = 0; w < NW; ++w) acc += merge[(w * NSUB + j) * (G4 * 64) + (db * 4 + q4) * 64 + lane] * wgt[w];
+          for (int w = 1; w < NW; ++w) acc += part[r][q4][w] * wgt[w];
           acc *= inv;
           const int d = db * 32 + q4 * 8 + g * 4;
           uint2 wv;
-          wv.x = static_cast<uint32_t>(f32_to_bf16_bits(acc[0])) | (static_cast<uint32_t>(f32_to_bf16_bits(acc[1])) << 16);
-          wv.y = static_cast<uint32_t>(f32_to_bf16_bits(acc[2])) | (static_cast<uint32_t>(f32_to_bf16_bits(acc[3])) << 16);
+          wv.x = pack_bf16x2(acc[0], acc[1]);
+          wv.y = pack_bf16x2(acc[2], acc[3]);
           if (a.o_packed_k > 0)  // 4 consecutive columns stay inside one 8-element run
             *reinterpret_cast<uint2*>(a.o + packed_act_offset(q_idx[j], static_cast<int64_t>(h) * D + d, a.o_packed_k)) = wv;
           else

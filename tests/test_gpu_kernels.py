@@ -217,6 +217,25 @@ def test_attention_shapes(dev, B, Hq, Hkv, Sq, Sk, D, causal, masked):
     assert_bf16_close(o, r, "attention")
 
 
+@pytest.mark.parametrize("D,causal", [(128, False), (64, False), (128, True)])
+def test_attention_bias_patterns(dev, D, causal):
+    """Key bias with a different pattern per batch: dense float values (every
+    tile carries bias), and a sparse row (masked keys in middle tiles, one
+    positive entry in the first tile, zeros elsewhere)."""
+    g = torch.Generator().manual_seed(D + 7 * causal)
+    B, Hq, Hkv, S = 2, 4, 2, 300
+    q = torch.randn(B, Hq, S, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    bias = torch.zeros(B, S)
+    bias[0] = 0.5 * torch.randn(S, generator=g)
+    bias[1, 100:141] = float("-inf")
+    bias[1, 7] = 1.5
+    o = Fn.attention(q.to(dev), k.to(dev), v.to(dev), key_bias=bias.to(dev), causal=causal)
+    r = ref.sdpa(q, ref.repeat_kv(k, Hq // Hkv), ref.repeat_kv(v, Hq // Hkv), key_bias=bias, causal=causal)
+    assert_bf16_close(o, r, "attention bias patterns")
+
+
 @pytest.mark.parametrize("S,D,layout", [(608, 128, "bhsd"), (77, 64, "bshd"), (1, 128, "bhsd"), (1280, 128, "bshd")])
 def test_kv_pack_layout(dev, S, D, layout):
     """Packed K/V tiles, element for element, against the layout definition."""
