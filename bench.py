@@ -132,6 +132,21 @@ def kernel_lines(torch, reps: int):
     gbs = W.rmsnorm_rope_bytes(rc) / (ms * 1e-3) / 1e9
     out["rmsnorm_rope_f32_256x16x64"] = dict(us=ms * 1e3, achieved=gbs, unit="GB/s", bound="hbm", peak=HBM_PEAK_GBS,
                                              frac=gbs / HBM_PEAK_GBS, bytes=W.rmsnorm_rope_bytes(rc))
+    # the same kernel on long sequences (the 256-token case above is launch-bound)
+    for seq in (16384, 65536):
+        rs = W.RmsRopeCfg(seq=seq)
+        shape = (rs.batch, rs.seq, rs.heads, rs.head_dim)
+        qs_, ks_ = torch.randn(shape, device=dev), torch.randn(shape, device=dev)
+        cs_, sn_ = (t.to(dev) for t in W.qwen_rope_cos_sin(rs.seq, rs.head_dim, rs.theta))
+        ws_ = ri["w"]
+        qo_, ko_ = torch.empty_like(qs_), torch.empty_like(ks_)
+        ms = graph_time_ms(lambda: Fn.qk_rmsnorm_rope_half(qs_, ks_, ws_, ws_, cs_, sn_, rs.eps, q_out=qo_, k_out=ko_),
+                           reps, torch)
+        gbs = W.rmsnorm_rope_bytes(rs) / (ms * 1e-3) / 1e9
+        out[f"rmsnorm_rope_f32_{seq}x16x64"] = dict(us=ms * 1e3, achieved=gbs, unit="GB/s", bound="hbm",
+                                                    peak=HBM_PEAK_GBS, frac=gbs / HBM_PEAK_GBS,
+                                                    bytes=W.rmsnorm_rope_bytes(rs))
+        del qs_, ks_, qo_, ko_
 
     # MSAT joint attention 16 x 608 x 128, masked
     jc = W.JointAttnCfg()

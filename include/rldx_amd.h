@@ -76,6 +76,8 @@ hipError_t rldx_grouped_swiglu_bf16(const void* sa_x, const void* sa_bias, const
  * fp32 variant: every step in fp32.  bf16 variant: eager bf16 rounding order
  * (bf16(x*rsqrt) -> bf16(w*.) -> bf16(y*cos), bf16(rot*sin) -> bf16(sum)).
  * q_heads or k_heads may be 0 (then q/q_w/q_out, resp. k/k_w/k_out, may be NULL).
+ * Tensors, norm weights and tables are 16-byte aligned, strides multiples of
+ * 16 bytes; (q_heads + k_heads) * B * S * D / 4 (fp32) or / 8 (bf16) < 2^31.
  * flags: RLDX_ROPE_SIN_SIGNED or 0.
  *
  * Replaces: Qwen3VLTextRMSNorm.forward + apply_rotary_pos_emb

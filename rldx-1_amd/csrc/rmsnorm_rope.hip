@@ -67,92 +67,114 @@ struct HalfArgs {
   int64_t c_sb, c_ss;          // cos/sin strides ([B or 1, S, D])
   float eps;
   int sin_signed;              // sin table already carries the rotate_half sign
-  int64_t total_rows;
+  int64_t total_rows;          // batch * seq * (hq + hk); total_rows * D / V < 2^31
+  DivMagic per_tok_div;        // division by hq + hk
+  DivMagic seq_div;            // division by seq
 };
 
-template <typename T, int D>
+// One thread: V consecutive elements of R heads of one token (the R heads
+// share the token's cos / sin and, within q or within k, the norm weight, so
+// those are loaded once for R rows).  R divides both hq and hk.
+template <typename T, int D, int R>
 __global__ __launch_bounds__(256) void rmsnorm_rope_half_kernel(HalfArgs a) {
   constexpr int V = Vec16<T>::N;   // elements per lane
   constexpr int LPR = D / V;       // lanes per row
   static_assert(LPR >= 2 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "unsupported head_dim");
-  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  // 32-bit index math with invariant-divisor multiplies (a 64-bit division by
+  // a run-time value costs ~130 instructions, more than the rows' arithmetic)
+  const uint32_t tid = blockIdx.x * blockDim.x + threadIdx.x;
   const int lane_in_row = static_cast<int>(tid % LPR);
-  const int64_t row = tid / LPR;
-  const bool valid = row < a.total_rows;
-  const int64_t r = valid ? row : 0;
+  const uint32_t item = tid / LPR;  // (token, group of R heads)
+  const bool valid = item < a.total_rows / R;
+  const uint32_t r = valid ? item * R : 0u;  // first row of the group
 
-  const int64_t per_tok = a.hq + a.hk;
-  const int64_t tok = r / per_tok;
+  const uint32_t per_tok = static_cast<uint32_t>(a.hq + a.hk);
+  const uint32_t tok = div_u32(r, a.per_tok_div);
   const int64_t hh = r - tok * per_tok;
-  const int64_t b = tok / a.seq;
-  const int64_t s = tok - b * a.seq;
-  const bool is_q = hh < a.hq;
+  const uint32_t b32 = div_u32(tok, a.seq_div);
+  const int64_t b = b32;
+  const int64_t s = tok - b32 * static_cast<uint32_t>(a.seq);
+  const bool is_q = hh < a.hq;  // the whole group: R divides hq
   const int64_t h = is_q ? hh : hh - a.hq;
 
   const T* src = is_q ? static_cast<const T*>(a.q) + b * a.q_sb + s * a.q_ss + h * a.q_sh
                       : static_cast<const T*>(a.k) + b * a.k_sb + s * a.k_ss + h * a.k_sh;
+  const int64_t src_h = is_q ? a.q_sh : a.k_sh;
   T* dst = is_q ? static_cast<T*>(a.q_out) + b * a.qo_sb + s * a.qo_ss + h * a.qo_sh
                 : static_cast<T*>(a.k_out) + b * a.ko_sb + s * a.ko_ss + h * a.ko_sh;
+  const int64_t dst_h = is_q ? a.qo_sh : a.ko_sh;
   const T* w = static_cast<const T*>(is_q ? a.q_w : a.k_w);
   const T* cs = static_cast<const T*>(a.cos) + b * a.c_sb + s * a.c_ss;
   const T* sn = static_cast<const T*>(a.sin) + b * a.c_sb + s * a.c_ss;
   const int d0 = lane_in_row * V;
 
-  float x[V];
-  {
-    uint4 raw = valid ? *reinterpret_cast<const uint4*>(src + d0) : make_uint4(0, 0, 0, 0);
-    const T* e = reinterpret_cast<const T*>(&raw);
+  // every load of the thread is issued before any arithmetic
+  uint4 raw[R];
 #pragma unroll
-    for (int i = 0; i < V; ++i) x[i] = load_elem<T>(e, i);
-  }
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < V; ++i) ss += x[i] * x[i];
-#pragma unroll
-  for (int m = LPR / 2; m >= 1; m >>= 1) ss += shfl_xor_f(ss, m);
-
-  float y[V];
-  {
-#pragma clang fp contract(off)
-    const float rinv = 1.0f / __builtin_sqrtf(ss * (1.0f / D) + a.eps);
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      float xn = x[i] * rinv;
-      if constexpr (sizeof(T) == 2) {
-        // w * bf16(xn): bf16 x bf16 product, rounded to bf16.
-        y[i] = round_bf16(load_elem<T>(w, d0 + i) * round_bf16(xn));
-      } else {
-        y[i] = load_elem<T>(w, d0 + i) * xn;
-      }
-    }
-  }
-  // rotate_half partner: element d +- D/2 sits in lane (lane_in_row ^ LPR/2).
-  float part[V];
-#pragma unroll
-  for (int i = 0; i < V; ++i) part[i] = shfl_xor_f(y[i], LPR / 2);
+  for (int j = 0; j < R; ++j)
+    raw[j] = valid ? *reinterpret_cast<const uint4*>(src + j * src_h + d0) : make_uint4(0, 0, 0, 0);
+  const uint4 wraw = *reinterpret_cast<const uint4*>(w + d0);
+  const uint4 craw = *reinterpret_cast<const uint4*>(cs + d0);
+  const uint4 sraw = *reinterpret_cast<const uint4*>(sn + d0);
+  const T* we = reinterpret_cast<const T*>(&wraw);
+  const T* ce = reinterpret_cast<const T*>(&craw);
+  const T* se = reinterpret_cast<const T*>(&sraw);
   const bool first_half = lane_in_row < LPR / 2;
 
-  uint4 outraw;
-  T* o = reinterpret_cast<T*>(&outraw);
-  {
-#pragma clang fp contract(off)
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const float rot = (first_half && !a.sin_signed) ? -part[i] : part[i];
-      const float c = load_elem<T>(cs, d0 + i);
-      const float sv = load_elem<T>(sn, d0 + i);
-      if constexpr (sizeof(T) == 2) {
-        const float t1 = round_bf16(y[i] * c);
-        const float t2 = round_bf16(rot * sv);
-        o[i] = f32_to_bf16_bits(t1 + t2);
-      } else {
-        const float t1 = y[i] * c;
-        const float t2 = rot * sv;
-        o[i] = t1 + t2;
+  for (int j = 0; j < R; ++j) {
+    float x[V];
+    const T* e = reinterpret_cast<const T*>(&raw[j]);
+#pragma unroll
+    for (int i = 0; i < V; ++i) x[i] = load_elem<T>(e, i);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) ss += x[i] * x[i];
+#pragma unroll
+    for (int m = LPR / 2; m >= 1; m >>= 1) ss += shfl_xor_f(ss, m);
+
+    float y[V];
+    {
+#pragma clang fp contract(off)
+      const float rinv = 1.0f / __builtin_sqrtf(ss * (1.0f / D) + a.eps);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        float xn = x[i] * rinv;
+        if constexpr (sizeof(T) == 2) {
+          // w * bf16(xn): bf16 x bf16 product, rounded to bf16.
+          y[i] = round_bf16(load_elem<T>(we, i) * round_bf16(xn));
+        } else {
+          y[i] = load_elem<T>(we, i) * xn;
+        }
       }
     }
+    // rotate_half partner: element d +- D/2 sits in lane (lane_in_row ^ LPR/2).
+    float part[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) part[i] = shfl_xor_f(y[i], LPR / 2);
+
+    uint4 outraw;
+    T* o = reinterpret_cast<T*>(&outraw);
+    {
+#pragma clang fp contract(off)
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float rot = (first_half && !a.sin_signed) ? -part[i] : part[i];
+        const float c = load_elem<T>(ce, i);
+        const float sv = load_elem<T>(se, i);
+        if constexpr (sizeof(T) == 2) {
+          const float t1 = round_bf16(y[i] * c);
+          const float t2 = round_bf16(rot * sv);
+          o[i] = f32_to_bf16_bits(t1 + t2);
+        } else {
+          const float t1 = y[i] * c;
+          const float t2 = rot * sv;
+          o[i] = t1 + t2;
+        }
+      }
+    }
+    if (valid) *reinterpret_cast<uint4*>(dst + j * dst_h + d0) = outraw;
   }
-  if (valid) *reinterpret_cast<uint4*>(dst + d0) = outraw;
 }
 
 // ---------------------------------------------------------------------------
@@ -321,19 +343,31 @@ __global__ __launch_bounds__(256) void msat_qkv_norm_rope_kernel(MsatArgs a) {
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <typename T>
-hipError_t launch_half(const HalfArgs& a, int64_t head_dim, hipStream_t stream) {
+template <typename T, int D>
+hipError_t launch_half_d(const HalfArgs& a, hipStream_t stream) {
   constexpr int V = Vec16<T>::N;
-  const int64_t threads = a.total_rows * (head_dim / V);
+  // Heads per thread: 4 on large launches (fewer loads per element, measured
+  // +5% of HBM rate at 16K-64K tokens); small launches are latency-bound and
+  // keep one head per thread for the most parallelism.
+  const bool large = a.total_rows * (D / V) >= (int64_t{1} << 21);
+  const int R = !large ? 1 : (a.hq % 4 == 0 && a.hk % 4 == 0) ? 4 : (a.hq % 2 == 0 && a.hk % 2 == 0) ? 2 : 1;
+  const int64_t threads = a.total_rows / R * (D / V);
   const int grid = static_cast<int>((threads + 255) / 256);
   if (grid == 0) return hipSuccess;
-  if (head_dim == 64)
-    hipLaunchKernelGGL((rmsnorm_rope_half_kernel<T, 64>), dim3(grid), dim3(256), 0, stream, a);
-  else if (head_dim == 128)
-    hipLaunchKernelGGL((rmsnorm_rope_half_kernel<T, 128>), dim3(grid), dim3(256), 0, stream, a);
+  if (R == 4)
+    hipLaunchKernelGGL((rmsnorm_rope_half_kernel<T, D, 4>), dim3(grid), dim3(256), 0, stream, a);
+  else if (R == 2)
+    hipLaunchKernelGGL((rmsnorm_rope_half_kernel<T, D, 2>), dim3(grid), dim3(256), 0, stream, a);
   else
-    return hipErrorInvalidValue;
+    hipLaunchKernelGGL((rmsnorm_rope_half_kernel<T, D, 1>), dim3(grid), dim3(256), 0, stream, a);
   return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_half(const HalfArgs& a, int64_t head_dim, hipStream_t stream) {
+  if (head_dim == 64) return launch_half_d<T, 64>(a, stream);
+  if (head_dim == 128) return launch_half_d<T, 128>(a, stream);
+  return hipErrorInvalidValue;
 }
 
 template <typename T>
@@ -350,7 +384,7 @@ hipError_t half_entry(const void* q, const void* k, const void* q_w, const void*
   if (hq > 0 && (!q || !q_w || !q_out)) return hipErrorInvalidValue;
   if (hk > 0 && (!k || !k_w || !k_out)) return hipErrorInvalidValue;
   const int V = Vec16<T>::N;
-  const void* ptrs[] = {q, k, q_out, k_out, cos, sin};
+  const void* ptrs[] = {q, k, q_out, k_out, cos, sin, q_w, k_w};
   for (const void* p : ptrs)
     if (p && !al16(p)) return hipErrorInvalidValue;
   const int64_t* all[] = {q_strides, k_strides, qo_strides, ko_strides};
@@ -358,11 +392,13 @@ hipError_t half_entry(const void* q, const void* k, const void* q_w, const void*
     for (int i = 0; i < 3; ++i)
       if (st[i] % V != 0) return hipErrorInvalidValue;
   if (cs_strides[0] % V != 0 || cs_strides[1] % V != 0) return hipErrorInvalidValue;
+  const int64_t rows = batch * seq * (hq + hk);
+  if (rows * (head_dim / V) >= (int64_t{1} << 31) - 256) return hipErrorInvalidValue;
   HalfArgs a{q, k, q_w, k_w, cos, sin, q_out, k_out, batch, seq, hq, hk,
              q_strides[0], q_strides[1], q_strides[2], k_strides[0], k_strides[1], k_strides[2],
              qo_strides[0], qo_strides[1], qo_strides[2], ko_strides[0], ko_strides[1], ko_strides[2],
              cs_strides[0], cs_strides[1], eps, (flags & RLDX_ROPE_SIN_SIGNED) ? 1 : 0,
-             batch * seq * (hq + hk)};
+             rows, div_magic(static_cast<uint32_t>(hq + hk)), div_magic(static_cast<uint32_t>(seq))};
   return launch_half<T>(a, head_dim, stream);
 }
 

@@ -30,29 +30,6 @@ struct SwigluGroup {
   int64_t rows, n_half;
 };
 
-// Unsigned 32-bit division by an invariant divisor d >= 1 (Granlund and
-// Montgomery, "Division by invariant integers using multiplication", PLDI
-// 1994, figure 4.1): q = (t + ((n - t) >> sh1)) >> sh2 with t = mulhi(m, n),
-// exact for every 32-bit n.
-struct DivMagic {
-  uint32_t m, sh1, sh2;
-};
-
-DivMagic div_magic(uint32_t d) {
-  uint32_t l = 0;
-  while ((uint64_t{1} << l) < d) ++l;
-  DivMagic r;
-  r.m = static_cast<uint32_t>((uint64_t{1} << 32) * ((uint64_t{1} << l) - d) / d + 1);
-  r.sh1 = l < 1 ? l : 1;
-  r.sh2 = l < 1 ? 0 : l - 1;
-  return r;
-}
-
-__device__ __forceinline__ uint32_t div_u32(uint32_t n, const DivMagic& dm) {
-  const uint32_t t = __umulhi(dm.m, n);
-  return (t + ((n - t) >> dm.sh1)) >> dm.sh2;
-}
-
 // One group of the vectorised kernel: rows of n_half elements cut into
 // 8-element chunks; workgroups [block_begin, block_begin + blocks) cover it.
 struct VecGroup {
