@@ -304,8 +304,9 @@ typedef struct rldx_gemm_group {
 /*
  * y_s = a_s W_s^T (+ bias_s) with the epilogue above, for 1..3 groups that
  * share n and k (the three streams of an MSAT block), fp32 accumulation.
- * n % 64 == 0, k % 512 == 0.  Groups of more than 64 rows use 128-row tiles,
- * the others 64-row tiles (two launches at most).  Deterministic.
+ * n % 64 == 0, k % 128 == 0.  One launch; per group 128 x 128 tiles (at least
+ * 256 rows and 128 tiles), 64 x 64 tiles (more than 32 rows) or 32 x 64 tiles.
+ * Deterministic (fixed summation order for a given shape).
  * Replaces: the per-stream nn.Linear calls of an MSAT block
  *   (rldx/model/modules/action_model/blocks.py:705-891), and
  *   fused_mlp_swiglu(x, weight, bias) behind ss::fused_mlp_swiglu

@@ -11,29 +11,40 @@
 // _fused_mlp_swiglu_kernel behind ss::fused_mlp_swiglu
 // (rldx/inference/action_model/single_stream/engine/kernels/fused_mlp_swiglu.py:199-267).
 //
-// Design
-//   * Weights are static, so they are packed once (pack_weight_kernel) into the
-//     MFMA B-operand order: 1 KB chunk (nb, kb) holds W[32 nb + l%32][16 kb +
-//     8 (l/32) + i] for lane l, element i, and the chunks of one 32-column block
-//     are contiguous along K.  Every weight load is one coalesced 16-byte load
-//     per lane; a wave streams its K range of a column block front to back.
-//   * A workgroup computes a (32*MB rows) x (32*NB columns) tile; its 4 waves
-//     split K into quarters (no operand is loaded twice inside a workgroup) and
-//     the partial accumulators are reduced through LDS in a fixed order, so the
-//     result is deterministic.
-//   * Activations are read in the same packed operand order (chunk (mb, kb) =
-//     rows 32 mb.., k 16 kb..), written so by their producers (the LayerNorm
-//     pack kernel below, the attention kernel's packed output, the SwiGLU
-//     epilogue): a row-major A costs 32 cache lines per load instruction and
-//     measured 2-4x slower.
-//   * Operands go straight from memory into VGPRs, double-buffered U k-steps
-//     deep: the next stage's loads are in flight during the current stage's
-//     MFMAs.  The activations (a few hundred KB) stay in L2; the weights stream
-//     from HBM once per workgroup row.
-//   * MB = 4 (128-row tiles) for the 512-token cognition stream, whose GEMMs are
-//     MFMA-bound; MB = 2 for the 64 / 32-token action and physics streams, whose
-//     GEMMs are weight-streaming (HBM-bound).  Work items are mapped XCD-aware:
-//     the m-tiles of one column block run on one XCD and share its L2.
+// Design (the limits it is built around, measured on MI355X: a CU's vector
+// memory path delivers ~48 B/clk from L2, ~32 TB/s over the chip; ds_read_b128
+// ~228 B/clk per CU, ds_write_b128 only ~74 B/clk)
+//   * Operands are stored in the MFMA operand order: 1 KB chunks, one wave-wide
+//     16-byte load per chunk.  Weights are packed once (pack_weight_kernel):
+//     chunk (nb, kb) holds W[32 nb + l%32][16 kb + 8 (l/32) + i] for lane l,
+//     element i, the chunks of one 32-column block contiguous along K.
+//     Activations arrive packed the same way from their producers (the
+//     LayerNorm-pack kernel, the attention kernel, the SwiGLU epilogue).
+//   * A workgroup of 8 waves computes a (32 MB) x (32 NB) tile.  Per k-step the
+//     tile's MB + NB chunks are loaded once, straight into LDS (buffer_load ...
+//     lds: no VGPR staging, no ds_write), into a ring of NSLOT stages of two
+//     k-steps; every wave reads the chunks of its m-block and n-blocks with
+//     ds_read_b128 one stage ahead.  Sharing operands through LDS is what cuts
+//     the L2 -> CU traffic: a 128 x 128 tile moves half the bytes per flop of a
+//     64 x 64 one.
+//   * Tile shapes: 128 x 128 (waves 4 x 2, 32 x 64 each) for long streams with
+//     enough tiles; 64 x 64 (waves 2 x 2 in two K-groups) and 32 x 64 (waves
+//     1 x 2 in four K-groups) for the short streams and the N = 1536 GEMMs.
+//     K-groups take alternate stages; their partial tiles are summed in a
+//     fixed order, so results are deterministic.
+//   * Stage pipeline per wave: issue the loads of stage s + NSLOT - 1, MFMAs of
+//     the first k-step of stage s, wait for stage s + 1 and barrier, read stage
+//     s + 1 from LDS, MFMAs of the second k-step (they cover the read latency).
+//   * MFMAs take (W chunk, A chunk), so each accumulator holds a transposed
+//     block: lane l32 = row, (q4, g, e) = 4 consecutive columns.  Epilogue:
+//     fp32 tiles in LDS, then every thread reduces the K-groups for 8
+//     consecutive columns of a row, applies the epilogue and stores 16 bytes.
+//   * Launch: workgroup b runs on XCD b % 8.  Each stream's workgroups start at
+//     a multiple of 8 and give each XCD a contiguous run of tiles (the m-tiles
+//     of a column block share its weight panel in that XCD's L2).  Streams are
+//     launched heaviest first; two workgroups fit on a CU (<= 72 KB LDS,
+//     <= 128 VGPRs), so the short streams' weight streaming runs beside the
+//     long stream's tiles.
 #include "rldx_amd.h"
 #include "rldx_common.h"
 
@@ -46,11 +57,11 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kXcds = 8;
-constexpr int kWaves = 4;
+constexpr int kThreads = 512;          // 8 waves per workgroup
 constexpr int kBufWord3 = 0x00020000;  // gfx9 raw buffer descriptor, word 3 (untyped dword data)
 
 enum { kEpiBias = 0, kEpiResidual = 1, kEpiSwiglu = 2, kEpiSwigluPacked = 3 };
-
+enum { kTile128 = 0, kTile64 = 1, kTile32 = 2 };
 
 __device__ __forceinline__ float bf(uint16_t b) { return bf16_bits_to_f32(b); }
 
@@ -69,283 +80,271 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __rest
   *reinterpret_cast<u32x4*>(out + chunk * 512 + lane * 8) = v;
 }
 
+// Tile configuration: MB x NB blocks of 32 x 32; each wave covers one m-block
+// and BNW n-blocks; the 8 waves form KG K-groups (stage s of group g covers
+// k-steps (s KG + g) U .. + U - 1); NSLOT stages of the LDS ring.
+template <int MB_, int NB_, int BNW_, int NSLOT_>
+struct TileCfg {
+  static constexpr int MB = MB_, NB = NB_, BNW = BNW_, NSLOT = NSLOT_;
+  static constexpr int U = 2;                       // k-steps per stage
+  static constexpr int WN = NB / BNW;               // waves along n
+  static constexpr int WPG = MB * WN;               // waves per K-group
+  static constexpr int KG = 8 / WPG;                // K-groups
+  static constexpr int CH = MB + NB;                // 1 KB chunks per k-step
+  static constexpr int ND = U * CH / WPG;           // chunks each wave loads per stage
+  static constexpr int RING = KG * NSLOT * U * CH;  // ring size in chunks
+  static constexpr int TP = 32 * NB + 4;            // fp32 tile pitch (rows shift 4 banks)
+  static constexpr int TILE = 32 * MB * TP;         // floats per K-group tile
+  static_assert(WPG * KG == 8 && (U * CH) % WPG == 0, "tile configuration");
+  static_assert(NB % 2 == 0, "SwiGLU tiles pair gate / up blocks");
+};
+using Cfg128 = TileCfg<4, 4, 2, 4>;
+using Cfg64 = TileCfg<2, 2, 1, 4>;
+using Cfg32 = TileCfg<1, 2, 1, 3>;
+
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+template <class C>
+constexpr int lds_bytes() { return cmax(C::RING * 1024, C::KG * C::TILE * 4); }
+constexpr int kLdsBytes = cmax(lds_bytes<Cfg128>(), cmax(lds_bytes<Cfg64>(), lds_bytes<Cfg32>()));
+static_assert(kLdsBytes <= 80 * 1024, "two workgroups per CU");
+
 struct Group {
   const uint16_t* a;  // packed activations
-  int m;
-  const uint16_t* w;
+  const uint16_t* w;  // packed weight
   const uint16_t* bias;
   uint16_t* out;
-  int64_t ldo;
   const uint16_t* res;
-  int64_t ldr;
+  int64_t ldo, ldr;
+  int m, cfg, m_tiles, items;
+  int wg_begin, per_xcd;  // first workgroup (multiple of 8); tiles per XCD
 };
 
 struct GemmArgs {
   Group g[3];
   int num_groups;
-  int n, k;           // n = rows of W (2 * N_half with the SwiGLU epilogue)
-  int m_tiles[3];
-  int item_end[3];    // cumulative work items per group
+  int n, k;  // n = rows of W (2 * N_half with the SwiGLU epilogue)
 };
 
-template <int MB, int NB, int U, int EPI>
-__global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
-  static_assert((EPI != kEpiSwiglu && EPI != kEpiSwigluPacked) || NB % 2 == 0, "SwiGLU tiles pair gate / up blocks");
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const uint16_t* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p), 0, bytes, kBufWord3);
+}
+
+// Wait until at most N of this wave's loads are in flight, then barrier.  Inline
+// assembly: a release fence would also wait for every LDS-bound load.
+template <int N>
+__device__ __forceinline__ void wait_barrier() {
+  static_assert(N == 0 || N == 3 || N == 4, "vmcnt immediate");
+  if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (N == 3) asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <class C, int EPI>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int item, u32x4* lds) {
+  constexpr bool kSwiglu = EPI == kEpiSwiglu || EPI == kEpiSwigluPacked;
+  constexpr int MB = C::MB, NB = C::NB, BNW = C::BNW, U = C::U, CH = C::CH, NSLOT = C::NSLOT;
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-  const int l32 = lane & 31;
-  const int g = lane >> 5;
-
-  // XCD-aware work mapping (workgroup i runs on XCD i % 8): consecutive items —
-  // the m-tiles of one column block — land on one XCD.
-  int item;
-  {
-    const int total = static_cast<int>(gridDim.x);
-    const int i = static_cast<int>(blockIdx.x);
-    const int per = total / kXcds, rem = total % kXcds;
-    const int xcd = i % kXcds, kk = i / kXcds;
-    item = xcd < rem ? xcd * (per + 1) + kk : rem * (per + 1) + (xcd - rem) * per + kk;
-  }
-  int gi = 0;
-  if (a.num_groups > 1 && item >= a.item_end[0]) gi = 1;
-  if (a.num_groups > 2 && item >= a.item_end[1]) gi = 2;
-  const Group& G = a.g[gi];
-  const int local = item - (gi ? a.item_end[gi - 1] : 0);
-  const int mt = local % a.m_tiles[gi], nt = local / a.m_tiles[gi];
+  const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int grp = wv / C::WPG, wl = wv % C::WPG;
+  const int wm = wl / C::WN, wn = wl % C::WN;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int mt = item % G.m_tiles, nt = item / G.m_tiles;
   const int ksteps = a.k / 16;
-  const int kw = ksteps / kWaves;  // k-steps of this wave
-  const int kb0 = wave * kw;
+  const int lstages = ksteps / (U * C::KG);
+  const int mblocks = (G.m + 31) / 32, nblocks = a.n / 32;
 
-  // Buffer descriptors: per-lane 32-bit offsets, the k-stage offset in an SGPR
-  // and the k-step within a stage as an immediate, so a load costs no VALU.
-  const int mblocks = (G.m + 31) / 32;
-  const __amdgpu_buffer_rsrc_t ar =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(G.a), 0, mblocks * ksteps * 1024, kBufWord3);
-  int aoff[MB];
+  // The chunks this wave loads per stage: q = wl + j WPG, k-step q / CH, chunk
+  // q % CH (m-blocks first, then n-blocks; blocks past the edge re-read the
+  // last one: rows / columns that are never stored).
+  __amdgpu_buffer_rsrc_t rs[C::ND];
+  int qoff[C::ND];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)  // m-blocks past the end re-read the last one (rows never stored)
-    aoff[mb] = (min(mt * MB + mb, mblocks - 1) * ksteps + kb0) * 1024 + lane * 16;
-  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(G.w + static_cast<int64_t>(nt * NB) * ksteps * 512), 0, NB * ksteps * 1024, kBufWord3);
-  const int woff = lane * 16;
-
-  floatx16 acc[MB][NB];
+  for (int j = 0; j < C::ND; ++j) {
+    const int q = wl + j * C::WPG, u = q / CH, c = q % CH;
+    if (c < MB) {
+      rs[j] = rsrc(G.a, mblocks * ksteps * 1024);
+      qoff[j] = (min(mt * MB + c, mblocks - 1) * ksteps + u) * 1024;
+    } else {
+      rs[j] = rsrc(G.w, nblocks * ksteps * 1024);
+      qoff[j] = (min(nt * NB + c - MB, nblocks - 1) * ksteps + u) * 1024;
+    }
+  }
+  u32x4* ring = lds + grp * NSLOT * U * CH * 64;
+  auto dma = [&](int st, int slot) {
+    const int ks = (min(st, lstages - 1) * C::KG + grp) * U * 1024;
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = floatx16{};
-
-  u32x4 wa[U][NB], xa[U][MB], wb[U][NB], xb[U][MB];
-  // Workgroups start their K walk at different stages (rotated by column tile):
-  // the activation chunks are shared by every column tile, and workgroups that
-  // walk K in lockstep request the same chunk at the same time, all from one
-  // L2 channel.  The summation order stays fixed per tile.
-  const int stages = kw / U;
-  const int rot = nt % stages;
-  auto load = [&](u32x4(&w)[U][NB], u32x4(&x)[U][MB], int st) {  // st: stage in walk order
-    int sr = st + rot;
-    if (sr >= stages) sr -= stages;
-    const int kb = sr * U;  // first k-step of the stage, wave-relative
-    const int ks = kb0 + kb;
+    for (int j = 0; j < C::ND; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs[j], (__attribute__((address_space(3))) void*)(ring + (slot * U * CH + wl + j * C::WPG) * 64), 16,
+          lane * 16, qoff[j] + ks, 0, 0);
+  };
+  u32x4 xa[2][U], xw[2][U][BNW];
+  auto lread = [&](int b, int slot) {
+    const u32x4* s = ring + slot * U * CH * 64 + lane;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      xa[b][u] = s[(u * CH + wm) * 64];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-        w[u][nb] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff + u * 1024, (nb * ksteps + ks) * 1024, 0);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) x[u][mb] = __builtin_amdgcn_raw_buffer_load_b128(ar, aoff[mb] + u * 1024, kb * 1024, 0);
+      for (int bb = 0; bb < BNW; ++bb) xw[b][u][bb] = s[(u * CH + MB + wn * BNW + bb) * 64];
     }
   };
-  auto mma = [&](u32x4(&w)[U][NB], u32x4(&x)[U][MB]) {
+  floatx16 acc[BNW];
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+  for (int bb = 0; bb < BNW; ++bb) acc[bb] = floatx16{};
+  auto mma = [&](int b, int u) {
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, x[u][mb]),
-                                                                __builtin_bit_cast(bf16x8, w[u][nb]), acc[mb][nb], 0,
-                                                                0, 0);
+    for (int bb = 0; bb < BNW; ++bb)
+      acc[bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xw[b][u][bb]),
+                                                        __builtin_bit_cast(bf16x8, xa[b][u]), acc[bb], 0, 0, 0);
   };
-  // Stages of U k-steps, double-buffered.  The scheduling barriers keep each
-  // stage's loads ahead of the previous stage's MFMAs (the scheduler would
-  // otherwise sink them next to their uses).  A load past the last stage
-  // re-reads the last stage (in bounds, never used).
-  load(wa, xa, 0);
 
-  // Epilogue operands, fetched behind the first stage so their latency hides
-  // under the K loop: the bias of the output columns this wave finalises, and
-  // the residual chunks of this thread's 16-byte stores (each chunk is read and
-  // written by the same thread, so the residual may alias the output).
-  constexpr bool kSwiglu = EPI == kEpiSwiglu || EPI == kEpiSwigluPacked;
-  constexpr int TR = MB * 32;                      // tile rows
-  constexpr int TC = kSwiglu ? NB * 16 : NB * 32;  // tile output columns
-  constexpr int BLK = MB * NB;
-  // epilogue work units per wave: 32x32 blocks, or for SwiGLU (gate, up) block
-  // pairs split into their 4 row quarters (the SwiGLU math is the costly part)
-  constexpr int UNITS = kSwiglu ? (BLK / 2) * 4 : BLK;
-  constexpr int PER_WAVE = (UNITS + kWaves - 1) / kWaves;
-  constexpr int NCHUNK = (TR * TC / 8 + 255) / 256;  // 16-byte output chunks per thread
-  // (raw bf16 bits: converting here would make the loads' results needed, and
-  // with in-order load counters wait for the first stage too)
-  uint16_t pb0[PER_WAVE], pb1[PER_WAVE];
 #pragma unroll
-  for (int j = 0; j < PER_WAVE; ++j) {
-    const int id = wave + j * kWaves;
-    pb0[j] = pb1[j] = 0;
-    if constexpr (kSwiglu) {
-      if (G.bias && id < UNITS) {
-        const int col = 32 * (nt * (NB / 2) + (id / 4) % (NB / 2)) + l32;
-        pb0[j] = G.bias[col];
-        pb1[j] = G.bias[a.n / 2 + col];
-      }
-    } else {
-      if (G.bias && id < BLK) pb0[j] = G.bias[32 * (nt * NB + id % NB) + l32];
+  for (int s = 0; s < NSLOT - 1; ++s) dma(s, s);
+  wait_barrier<(NSLOT - 2) * C::ND>();
+  lread(0, 0);
+  int slot_next = 1, slot_dma = NSLOT - 1;  // ring slots of stages st + 1, st + NSLOT - 1
+  for (int st = 0; st < lstages; st += 2) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      if (st + r >= lstages) break;
+      dma(st + r + NSLOT - 1, slot_dma);  // past the last stage: re-loads it into a free slot
+      __builtin_amdgcn_sched_barrier(0);
+      mma(r, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_barrier<(NSLOT - 2) * C::ND>();  // stage st + r + 1 is in LDS
+      __builtin_amdgcn_sched_barrier(0);
+      lread(r ^ 1, slot_next);  // past the last stage: read, never used
+      __builtin_amdgcn_sched_barrier(0);
+      mma(r, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      slot_next = slot_next + 1 == NSLOT ? 0 : slot_next + 1;
+      slot_dma = slot_dma + 1 == NSLOT ? 0 : slot_dma + 1;
     }
   }
-  u32x4 pres[NCHUNK];
+
+  // ---- epilogue ----
+  constexpr int R = 32 * MB;                       // tile rows
+  constexpr int OC = kSwiglu ? 16 * NB : 32 * NB;  // tile output columns
+  constexpr int CPR = OC / 8;                      // 16-byte output chunks per row
+  constexpr int PER = (R * CPR + kThreads - 1) / kThreads;
+  static_assert(kThreads % CPR == 0, "a thread keeps its column chunk");
+  const int n_out = kSwiglu ? a.n / 2 : a.n;
+  const int cc = 8 * (static_cast<int>(threadIdx.x) % CPR);
+  const int col = nt * OC + cc;  // global output column of this thread's chunks
+  const bool col_ok = col < n_out;
+  // residual chunks (each is read and written by this thread, so it may alias the output)
+  u32x4 pres[PER];
   if constexpr (EPI == kEpiResidual) {
 #pragma unroll
-    for (int j = 0; j < NCHUNK; ++j) {
-      const int t = static_cast<int>(threadIdx.x) + 256 * j;
-      const int row = mt * TR + t / (TC / 8), col = nt * TC + 8 * (t % (TC / 8));
-      pres[j] = (t < TR * TC / 8 && row < G.m)
+    for (int i = 0; i < PER; ++i) {
+      const int t = static_cast<int>(threadIdx.x) + kThreads * i;
+      const int row = mt * R + t / CPR;
+      pres[i] = (t < R * CPR && row < G.m && col_ok)
                     ? *reinterpret_cast<const u32x4*>(G.res + static_cast<int64_t>(row) * G.ldr + col)
                     : u32x4{0, 0, 0, 0};
     }
   }
-
-  int st = 0;
-  for (; st + 2 <= stages; st += 2) {
-    load(wb, xb, min(st + 1, stages - 1));
-    __builtin_amdgcn_sched_barrier(0);
-    mma(wa, xa);
-    __builtin_amdgcn_sched_barrier(0);
-    load(wa, xa, min(st + 2, stages - 1));
-    __builtin_amdgcn_sched_barrier(0);
-    mma(wb, xb);
-    __builtin_amdgcn_sched_barrier(0);
+  float bg[8], bu[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    bg[i] = G.bias && col_ok ? bf(G.bias[col + i]) : 0.f;
+    bu[i] = kSwiglu && G.bias && col_ok ? bf(G.bias[a.n / 2 + col + i]) : 0.f;
   }
-  if (st < stages) mma(wa, xa);
-
-  // ---- reduce the 4 waves' partial tiles through LDS, in wave order ----
-  __shared__ floatx4 red[kWaves * BLK * 4 * 64];
+  wait_barrier<0>();  // the ring's last reads and loads are done; LDS becomes the fp32 tiles
+  float* tiles = reinterpret_cast<float*>(lds);
+  {
+    float* t = tiles + grp * C::TILE;
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
+    for (int bb = 0; bb < BNW; ++bb)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4)
-        red[((wave * BLK + mb * NB + nb) * 4 + q4) * 64 + lane] =
-            floatx4{acc[mb][nb][4 * q4], acc[mb][nb][4 * q4 + 1], acc[mb][nb][4 * q4 + 2], acc[mb][nb][4 * q4 + 3]};
-  __syncthreads();
-  auto reduced = [&](int blk, int q4) {
-    floatx4 s = red[(blk * 4 + q4) * 64 + lane];
+        *reinterpret_cast<floatx4*>(&t[(32 * wm + l32) * C::TP + 32 * (wn * BNW + bb) + 8 * q4 + 4 * g]) =
+            floatx4{acc[bb][4 * q4], acc[bb][4 * q4 + 1], acc[bb][4 * q4 + 2], acc[bb][4 * q4 + 3]};
+  }
+  wait_barrier<0>();
+  // 8 consecutive fp32 sums (K-groups in order) of tile row r from tile column tc
+  auto sum8 = [&](int r, int tc, float (&v)[8]) {
+    floatx4 lo = *reinterpret_cast<const floatx4*>(&tiles[r * C::TP + tc]);
+    floatx4 hi = *reinterpret_cast<const floatx4*>(&tiles[r * C::TP + tc + 4]);
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) s += red[((w * BLK + blk) * 4 + q4) * 64 + lane];
-    return s;
-  };
-  // ---- epilogue: bias / SwiGLU on the reduced sums -> bf16 tile in LDS ->
-  // 16-byte, row-contiguous stores (a 2-byte store per accumulator element
-  // scatters every store instruction over 2-8 segments; measured to cost more
-  // than the whole K loop) ----
-  constexpr int OP = TC + 8;                       // LDS row pitch in elements (16-byte multiple)
-  __shared__ __attribute__((aligned(16))) uint16_t otile[TR * OP];
-  if constexpr (kSwiglu) {
-#pragma unroll
-    for (int j = 0; j < PER_WAVE; ++j) {
-      const int u = wave + j * kWaves;
-      if (u >= UNITS) break;
-      const int pi = u / 4, q4 = u % 4;
-      const int mb = pi / (NB / 2), pp = pi % (NB / 2);
-      const float bg = bf(pb0[j]), bu = bf(pb1[j]);
-      const floatx4 sg = reduced(mb * NB + 2 * pp, q4), su = reduced(mb * NB + 2 * pp + 1, q4);
-#pragma unroll
-      for (int e = 0; e < 4; e += 2) {
-        const uint32_t gp = pack_bf16x2(sg[e] + bg, sg[e + 1] + bg);
-        const uint32_t up = pack_bf16x2(su[e] + bu, su[e + 1] + bu);
-        const uint32_t y = swiglu_bf16x2(bf16x2_lo(gp), bf16x2_hi(gp), bf16x2_lo(up), bf16x2_hi(up));
-        otile[(32 * mb + 8 * q4 + 4 * g + e) * OP + 32 * pp + l32] = static_cast<uint16_t>(y);
-        otile[(32 * mb + 8 * q4 + 4 * g + e + 1) * OP + 32 * pp + l32] = static_cast<uint16_t>(y >> 16);
-      }
+    for (int kg = 1; kg < C::KG; ++kg) {
+      lo += *reinterpret_cast<const floatx4*>(&tiles[kg * C::TILE + r * C::TP + tc]);
+      hi += *reinterpret_cast<const floatx4*>(&tiles[kg * C::TILE + r * C::TP + tc + 4]);
     }
-  } else {
 #pragma unroll
-    for (int j = 0; j < PER_WAVE; ++j) {
-      const int blk = wave + j * kWaves;
-      if (blk >= BLK) break;
-      const int mb = blk / NB, nb = blk % NB;
-      const float bias = bf(pb0[j]);
+    for (int i = 0; i < 4; ++i) {
+      v[i] = lo[i];
+      v[4 + i] = hi[i];
+    }
+  };
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const floatx4 s = reduced(blk, q4);
+  for (int i = 0; i < PER; ++i) {
+    const int t = static_cast<int>(threadIdx.x) + kThreads * i;
+    const int r = t / CPR, row = mt * R + r;
+    if (t >= R * CPR || row >= G.m || !col_ok) continue;
+    u32x4 o;
+    if constexpr (kSwiglu) {
+      // gate / up blocks alternate in the packed weight: output columns 32 p .. of
+      // the tile come from tile columns 64 p (gate) and 64 p + 32 (up)
+      const int tc = 64 * (cc / 32) + cc % 32;
+      float gv[8], uv[8];
+      sum8(r, tc, gv);
+      sum8(r, tc + 32, uv);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t gp = pack_bf16x2(gv[2 * e] + bg[2 * e], gv[2 * e + 1] + bg[2 * e + 1]);
+        const uint32_t up = pack_bf16x2(uv[2 * e] + bu[2 * e], uv[2 * e + 1] + bu[2 * e + 1]);
+        o[e] = swiglu_bf16x2(bf16x2_lo(gp), bf16x2_hi(gp), bf16x2_lo(up), bf16x2_hi(up));
+      }
+    } else {
+      float v[8];
+      sum8(r, cc, v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(v[2 * e] + bg[2 * e], v[2 * e + 1] + bg[2 * e + 1]);
+      if constexpr (EPI == kEpiResidual) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          otile[(32 * mb + 8 * q4 + 4 * g + e) * OP + 32 * nb + l32] = f32_to_bf16_bits(s[e] + bias);
-      }
-    }
-  }
-  __syncthreads();
-  const int row0 = mt * TR, col0 = nt * TC;
-#pragma unroll
-  for (int j = 0; j < NCHUNK; ++j) {
-    const int t = static_cast<int>(threadIdx.x) + 256 * j;
-    const int r = t / (TC / 8), c = 8 * (t % (TC / 8));
-    const int row = row0 + r, col = col0 + c;
-    if (t >= TR * TC / 8 || row >= G.m) continue;
-    u32x4 v = *reinterpret_cast<const u32x4*>(&otile[r * OP + c]);
-    if constexpr (EPI == kEpiResidual) {
-      const u32x4 rv = pres[j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = f32_to_bf16_bits(bf(static_cast<uint16_t>(rv[i] & 0xffffu)) + bf(static_cast<uint16_t>(v[i] & 0xffffu)));
-        const uint32_t hi = f32_to_bf16_bits(bf(static_cast<uint16_t>(rv[i] >> 16)) + bf(static_cast<uint16_t>(v[i] >> 16)));
-        v[i] = lo | (hi << 16);
+          o[e] = pack_bf16x2(bf16x2_lo(pres[i][e]) + bf16x2_lo(o[e]), bf16x2_hi(pres[i][e]) + bf16x2_hi(o[e]));
       }
     }
     if constexpr (EPI == kEpiSwigluPacked)
-      *reinterpret_cast<u32x4*>(G.out + packed_act_offset(row, col, a.n / 2)) = v;
+      *reinterpret_cast<u32x4*>(G.out + packed_act_offset(row, col, n_out)) = o;
     else
-      *reinterpret_cast<u32x4*>(G.out + static_cast<int64_t>(row) * G.ldo + col) = v;
+      *reinterpret_cast<u32x4*>(G.out + static_cast<int64_t>(row) * G.ldo + col) = o;
   }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) u32x4 lds[kLdsBytes / 16];
+  const int b = static_cast<int>(blockIdx.x);
+  int gi = 0;
+  if (a.num_groups > 1 && b >= a.g[1].wg_begin) gi = 1;
+  if (a.num_groups > 2 && b >= a.g[2].wg_begin) gi = 2;
+  const Group& G = a.g[gi];
+  const int r = b - G.wg_begin;
+  const int item = (r % kXcds) * G.per_xcd + r / kXcds;  // XCD r % 8 takes a contiguous run of tiles
+  if (item >= G.items) return;
+  if (G.cfg == kTile128)
+    gemm_tile<Cfg128, EPI>(a, G, item, lds);
+  else if (G.cfg == kTile64)
+    gemm_tile<Cfg64, EPI>(a, G, item, lds);
+  else
+    gemm_tile<Cfg32, EPI>(a, G, item, lds);
 }
 
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <int MB, int NB, int U>
-hipError_t launch_groups(const rldx_gemm_group_t* gs, const int* idx, int count, int64_t n, int64_t k, int epi,
-                         hipStream_t stream) {
-  if (count == 0) return hipSuccess;
-  GemmArgs a{};
-  a.num_groups = count;
-  a.n = static_cast<int>(n);
-  a.k = static_cast<int>(k);
-  const int n_tiles = static_cast<int>(n / (32 * NB));
-  int64_t items = 0;
-  for (int j = 0; j < count; ++j) {
-    const rldx_gemm_group_t& s = gs[idx[j]];
-    a.g[j] = Group{static_cast<const uint16_t*>(s.a_packed), static_cast<int>(s.m),
-                   static_cast<const uint16_t*>(s.w_packed), static_cast<const uint16_t*>(s.bias),
-                   static_cast<uint16_t*>(s.out), s.ldo, static_cast<const uint16_t*>(s.residual), s.ldr};
-    a.m_tiles[j] = static_cast<int>((s.m + 32 * MB - 1) / (32 * MB));
-    items += static_cast<int64_t>(a.m_tiles[j]) * n_tiles;
-    if (items > (int64_t{1} << 31) - 1) return hipErrorInvalidValue;
-    a.item_end[j] = static_cast<int>(items);
-  }
-  const dim3 grid(static_cast<unsigned>(items)), block(256);
-  if (epi == kEpiBias)
-    hipLaunchKernelGGL((gemm_kernel<MB, NB, U, kEpiBias>), grid, block, 0, stream, a);
-  else if (epi == kEpiResidual)
-    hipLaunchKernelGGL((gemm_kernel<MB, NB, U, kEpiResidual>), grid, block, 0, stream, a);
-  else if constexpr (NB % 2 == 0) {
-    if (epi == kEpiSwiglu)
-      hipLaunchKernelGGL((gemm_kernel<MB, NB, U, kEpiSwiglu>), grid, block, 0, stream, a);
-    else
-      hipLaunchKernelGGL((gemm_kernel<MB, NB, U, kEpiSwigluPacked>), grid, block, 0, stream, a);
-  } else {
-    return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+template <class C>
+void tiles_of(int64_t m, int64_t n, int& m_tiles, int& n_tiles) {
+  m_tiles = static_cast<int>((m + 32 * C::MB - 1) / (32 * C::MB));
+  n_tiles = static_cast<int>((n / 32 + C::NB - 1) / C::NB);
+}
+
+// L2 -> CU bytes a workgroup of configuration cfg moves for one tile.
+int64_t tile_bytes(int cfg, int64_t k) {
+  const int ch = cfg == kTile128 ? Cfg128::CH : cfg == kTile64 ? Cfg64::CH : Cfg32::CH;
+  return ch * k * 64;  // ch chunks of 1 KB per 16 columns of K
 }
 
 // ---------------------------------------------------------------------------
@@ -460,12 +459,15 @@ extern "C" hipError_t rldx_grouped_gemm_bf16(const rldx_gemm_group_t* groups, in
                                              int64_t k, int32_t epilogue, hipStream_t stream) {
   if (!groups || num_groups < 1 || num_groups > 3) return hipErrorInvalidValue;
   if (epilogue < kEpiBias || epilogue > kEpiSwigluPacked) return hipErrorInvalidValue;
-  // k: whole stages of 8 k-steps per wave; n: whole 64-column tiles
-  if (n <= 0 || k <= 0 || n % 64 != 0 || k % (kWaves * 16 * 8) != 0) return hipErrorInvalidValue;
+  // k: whole stages of every K-group split (4 K-groups x 2 k-steps); n: whole 64-column blocks
+  if (n <= 0 || k <= 0 || n % 64 != 0 || k % 128 != 0) return hipErrorInvalidValue;
   if (n > (1 << 30) || k > (1 << 30)) return hipErrorInvalidValue;
   const bool swiglu = epilogue == kEpiSwiglu || epilogue == kEpiSwigluPacked;
   const int64_t n_out = swiglu ? n / 2 : n;
-  int order[3], cnt = 0;
+  GemmArgs args{};
+  args.n = static_cast<int>(n);
+  args.k = static_cast<int>(k);
+  int cnt = 0;
   for (int i = 0; i < num_groups; ++i) {
     const rldx_gemm_group_t& s = groups[i];
     if (s.m < 0 || s.m > (1 << 24)) return hipErrorInvalidValue;
@@ -479,19 +481,56 @@ extern "C" hipError_t rldx_grouped_gemm_bf16(const rldx_gemm_group_t* groups, in
     if (epilogue != kEpiSwigluPacked && (s.ldo < n_out || s.ldo % 8)) return hipErrorInvalidValue;
     if (epilogue == kEpiResidual && (!s.residual || !a16(s.residual) || s.ldr < n_out || s.ldr % 8))
       return hipErrorInvalidValue;
-    order[cnt++] = i;
-  }
-  // One launch for all groups, smallest first: the weight-streaming tiles of
-  // the short streams are dispatched first and overlap the MFMA-bound tiles of
-  // the long one.  64 x 64 tiles: measured best for the MSAT shapes (enough
-  // workgroups to fill 256 CUs twice over, two workgroups per CU).
-  for (int i = 1; i < cnt; ++i)
-    for (int j = i; j > 0 && groups[order[j]].m < groups[order[j - 1]].m; --j) {
-      const int t = order[j];
-      order[j] = order[j - 1];
-      order[j - 1] = t;
+    // Tile shape: 128 x 128 where the stream has rows and tiles enough to
+    // occupy the chip (half the L2 traffic per flop of 64 x 64), else 64 x 64,
+    // or 32 x 64 for streams of at most 32 rows.
+    int mt, nt, cfg;
+    tiles_of<Cfg128>(s.m, n, mt, nt);
+    if (s.m >= 256 && static_cast<int64_t>(mt) * nt >= 128) {
+      cfg = kTile128;
+    } else if (s.m > 32) {
+      cfg = kTile64;
+      tiles_of<Cfg64>(s.m, n, mt, nt);
+    } else {
+      cfg = kTile32;
+      tiles_of<Cfg32>(s.m, n, mt, nt);
     }
-  return launch_groups<2, 2, 4>(groups, order, cnt, n, k, epilogue, stream);
+    Group& G = args.g[cnt++];
+    G = Group{static_cast<const uint16_t*>(s.a_packed), static_cast<const uint16_t*>(s.w_packed),
+              static_cast<const uint16_t*>(s.bias), static_cast<uint16_t*>(s.out),
+              static_cast<const uint16_t*>(s.residual), s.ldo, s.ldr, static_cast<int>(s.m), cfg, mt, 0, 0, 0};
+    const int64_t items = static_cast<int64_t>(mt) * nt;
+    if (items > (int64_t{1} << 28)) return hipErrorInvalidValue;
+    G.items = static_cast<int>(items);
+  }
+  if (cnt == 0) return hipSuccess;
+  // One launch for all groups, heaviest tiles first (their workgroups take the
+  // first slot of every CU; the short streams' tiles fill the second).
+  for (int i = 1; i < cnt; ++i)
+    for (int j = i; j > 0 && tile_bytes(args.g[j].cfg, k) > tile_bytes(args.g[j - 1].cfg, k); --j) {
+      const Group t = args.g[j];
+      args.g[j] = args.g[j - 1];
+      args.g[j - 1] = t;
+    }
+  int64_t wgs = 0;
+  for (int i = 0; i < cnt; ++i) {
+    Group& G = args.g[i];
+    G.wg_begin = static_cast<int>(wgs);
+    G.per_xcd = (G.items + kXcds - 1) / kXcds;
+    wgs += static_cast<int64_t>(G.per_xcd) * kXcds;
+  }
+  if (wgs > (int64_t{1} << 31) - 1) return hipErrorInvalidValue;
+  args.num_groups = cnt;
+  const dim3 grid(static_cast<unsigned>(wgs)), block(kThreads);
+  if (epilogue == kEpiBias)
+    hipLaunchKernelGGL(gemm_kernel<kEpiBias>, grid, block, 0, stream, args);
+  else if (epilogue == kEpiResidual)
+    hipLaunchKernelGGL(gemm_kernel<kEpiResidual>, grid, block, 0, stream, args);
+  else if (epilogue == kEpiSwiglu)
+    hipLaunchKernelGGL(gemm_kernel<kEpiSwiglu>, grid, block, 0, stream, args);
+  else
+    hipLaunchKernelGGL(gemm_kernel<kEpiSwigluPacked>, grid, block, 0, stream, args);
+  return hipGetLastError();
 }
 
 extern "C" int64_t rldx_act_packed_elems(int64_t m, int64_t k) {

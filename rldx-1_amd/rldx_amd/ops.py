@@ -316,9 +316,9 @@ def ss_fused_mlp_swiglu(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tenso
 
     rldx/inference/action_model/single_stream/engine/ops/op_fused_mlp_swiglu.py:13-43
     (kernel fused_mlp_swiglu.py:199-267).  `split_k` is accepted for signature
-    compatibility; the kernel always splits K over the 4 waves of a workgroup.
-    Rounding: the eager chain (GEMM output rounded to bf16, then SwiGLU's two
-    roundings).  Needs K % 512 == 0 and N_half % 32 == 0."""
+    compatibility; the tile shape and the K split inside a workgroup are chosen
+    from M and N.  Rounding: the eager chain (GEMM output rounded to bf16, then
+    SwiGLU's two roundings).  Needs K % 128 == 0 and N_half % 32 == 0."""
     del split_k
     M, K = x.shape
     nh = weight.shape[0] // 2
