@@ -316,6 +316,35 @@ typedef struct rldx_gemm_group {
 hipError_t rldx_grouped_gemm_bf16(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, int64_t k,
                                   int32_t epilogue, hipStream_t stream);
 
+/*
+ * Workspace bytes rldx_grouped_gemm_ws_bf16 needs for these groups, shapes and
+ * split_k (0 when nothing is split), or -1 if the call would be rejected.
+ */
+int64_t rldx_grouped_gemm_workspace_bytes(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, int64_t k,
+                                          int32_t epilogue, int32_t split_k);
+
+/*
+ * rldx_grouped_gemm_bf16 with split-K across workgroups: every group has its K
+ * range split over S workgroups, S the largest power of two <= split_k that
+ * divides the group's stages (split_k <= 1: no split).  Each split streams its
+ * part of the operands; the partial tiles are summed in split
+ * order by the last workgroup to finish the tile, so results do not depend on
+ * timing (they differ from the unsplit sum by fp32 rounding only).  The splits
+ * of a tile run on one XCD and meet in its L2.
+ * workspace: device memory, 256-byte aligned, at least
+ * rldx_grouped_gemm_workspace_bytes(...) bytes, zero-filled before its first
+ * use; each launch leaves it ready for the next, whatever its shapes (the first
+ * 64 KB hold tile counters, at most 16384 split tiles per launch; partials
+ * follow).  Launches that share a workspace must not overlap in time.  Too
+ * small, missing or misaligned: hipErrorInvalidValue.
+ * Replaces: the split_k argument of fused_mlp_swiglu(x, weight, bias, split_k)
+ *   (rldx/inference/action_model/single_stream/engine/ops/op_fused_mlp_swiglu.py:13-43)
+ *   and the per-stream nn.Linear calls of an MSAT block, as rldx_grouped_gemm_bf16.
+ */
+hipError_t rldx_grouped_gemm_ws_bf16(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, int64_t k,
+                                     int32_t epilogue, int32_t split_k, void* workspace, int64_t workspace_bytes,
+                                     hipStream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Host-side diagnostics (no reference counterpart)                         */
 /* ------------------------------------------------------------------------ */

@@ -101,12 +101,20 @@ struct TileCfg {
 using Cfg128 = TileCfg<4, 4, 2, 4>;
 using Cfg64 = TileCfg<2, 2, 1, 4>;
 using Cfg32 = TileCfg<1, 2, 1, 3>;
+// Deep rings for launches of at most one workgroup per CU: one workgroup alone
+// on a CU is latency-bound with the rings above (~48 KB of loads in flight,
+// about half of what a CU can stream); these keep ~96-112 KB in flight.
+using Cfg128D = TileCfg<4, 4, 2, 8>;
+using Cfg64D = TileCfg<2, 2, 1, 8>;
+using Cfg32D = TileCfg<1, 2, 1, 6>;
 
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 template <class C>
 constexpr int lds_bytes() { return cmax(C::RING * 1024, C::KG * C::TILE * 4); }
 constexpr int kLdsBytes = cmax(lds_bytes<Cfg128>(), cmax(lds_bytes<Cfg64>(), lds_bytes<Cfg32>()));
 static_assert(kLdsBytes <= 80 * 1024, "two workgroups per CU");
+constexpr int kLdsDeep = cmax(lds_bytes<Cfg128D>(), cmax(lds_bytes<Cfg64D>(), lds_bytes<Cfg32D>()));
+static_assert(kLdsDeep <= 160 * 1024 && kLdsDeep >= kLdsBytes, "one workgroup per CU");
 
 struct Group {
   const uint16_t* a;  // packed activations
@@ -115,8 +123,11 @@ struct Group {
   uint16_t* out;
   const uint16_t* res;
   int64_t ldo, ldr;
-  int m, cfg, m_tiles, items;
-  int wg_begin, per_xcd;  // first workgroup (multiple of 8); tiles per XCD
+  int m, cfg, m_tiles, items;  // items = tiles x splits
+  int wg_begin, per_xcd;        // first workgroup (multiple of 8); items per XCD
+  int splits, ls_per;           // K splits across workgroups; K-group stages per split
+  float* part;                  // split partials [tile][split][PER][512 threads][V]
+  unsigned* cnt;                // per-tile arrival counters (zero between launches)
 };
 
 struct GemmArgs {
@@ -133,7 +144,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const uint16_t* p, int by
 // assembly: a release fence would also wait for every LDS-bound load.
 template <int N>
 __device__ __forceinline__ void wait_barrier() {
-  static_assert(N == 0 || N == 3 || N == 4, "vmcnt immediate");
+  static_assert(N == 0 || N == 3 || N == 4 || N == 12, "vmcnt immediate");
+  if constexpr (N == 12) asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if constexpr (N == 3) asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -148,9 +160,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   const int grp = wv / C::WPG, wl = wv % C::WPG;
   const int wm = wl / C::WN, wn = wl % C::WN;
   const int l32 = lane & 31, g = lane >> 5;
-  const int mt = item % G.m_tiles, nt = item / G.m_tiles;
+  const int tile = item / G.splits, split = item % G.splits;
+  const int mt = tile % G.m_tiles, nt = tile / G.m_tiles;
   const int ksteps = a.k / 16;
-  const int lstages = ksteps / (U * C::KG);
+  const int lstages = G.ls_per;         // K-group stages of this split
+  const int st0 = split * G.ls_per;     // its first stage
   const int mblocks = (G.m + 31) / 32, nblocks = a.n / 32;
 
   // The chunks this wave loads per stage: q = wl + j WPG, k-step q / CH, chunk
@@ -171,7 +185,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   }
   u32x4* ring = lds + grp * NSLOT * U * CH * 64;
   auto dma = [&](int st, int slot) {
-    const int ks = (min(st, lstages - 1) * C::KG + grp) * U * 1024;
+    const int ks = ((st0 + min(st, lstages - 1)) * C::KG + grp) * U * 1024;
 #pragma unroll
     for (int j = 0; j < C::ND; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -277,6 +291,70 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
       v[4 + i] = hi[i];
     }
   };
+  // fp32 sums of this thread's chunks: 8 columns, or 8 gate + 8 up columns
+  constexpr int V = kSwiglu ? 16 : 8;
+  const int tc = kSwiglu ? 64 * (cc / 32) + cc % 32 : cc;
+  float y[PER][V];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int r = (static_cast<int>(threadIdx.x) + kThreads * i) / CPR;
+    float lo[8];
+    sum8(r < R ? r : 0, tc, lo);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[i][e] = lo[e];
+    if constexpr (kSwiglu) {
+      float hi[8];
+      sum8(r < R ? r : 0, tc + 32, hi);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[i][8 + e] = hi[e];
+    }
+  }
+  if (G.splits > 1) {
+    // Split-K.  The splits of a tile run on one XCD (the launch gives every XCD
+    // whole tiles), so that XCD's L2 is their meeting point: each split stores
+    // its fp32 partial, waits until the stores have reached L2, then counts in
+    // with an L2 atomic; the last to arrive reads the other partials past its
+    // L1, sums all of them in split order (the same order whichever split
+    // arrives last), applies the epilogue and re-arms the counter.
+    const int part_bytes = G.items * PER * kThreads * V * 4;  // < 2^31 (host check)
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(G.part, 0, part_bytes, kBufWord3);
+    auto slot = [&](int sp, int i) { return (((tile * G.splits + sp) * PER + i) * kThreads + threadIdx.x) * V * 4; };
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+#pragma unroll
+      for (int e = 0; e < V; e += 4)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4, floatx4{y[i][e], y[i][e + 1], y[i][e + 2], y[i][e + 3]}), prs,
+            slot(split, i) + 4 * e, 0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    int* last = reinterpret_cast<int*>(lds) + kLdsBytes / 4 - 1;  // past every epilogue tile, in both kernels' LDS
+    if (threadIdx.x == 0)
+      *last = __hip_atomic_fetch_add(G.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
+              static_cast<unsigned>(G.splits - 1);
+    __syncthreads();
+    if (!*last) return;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      float sum[V];
+#pragma unroll
+      for (int e = 0; e < V; ++e) sum[e] = 0.f;
+      for (int sp = 0; sp < G.splits; ++sp) {
+#pragma unroll
+        for (int e = 0; e < V; e += 4) {
+          const floatx4 v =
+              sp == split ? floatx4{y[i][e], y[i][e + 1], y[i][e + 2], y[i][e + 3]}
+                          : __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(prs, slot(sp, i) + 4 * e,
+                                                                                              0, 1 /* sc0: past L1 */));
+#pragma unroll
+          for (int f = 0; f < 4; ++f) sum[e + f] += v[f];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < V; ++e) y[i][e] = sum[e];
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(G.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int t = static_cast<int>(threadIdx.x) + kThreads * i;
@@ -284,23 +362,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     if (t >= R * CPR || row >= G.m || !col_ok) continue;
     u32x4 o;
     if constexpr (kSwiglu) {
-      // gate / up blocks alternate in the packed weight: output columns 32 p .. of
-      // the tile come from tile columns 64 p (gate) and 64 p + 32 (up)
-      const int tc = 64 * (cc / 32) + cc % 32;
-      float gv[8], uv[8];
-      sum8(r, tc, gv);
-      sum8(r, tc + 32, uv);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t gp = pack_bf16x2(gv[2 * e] + bg[2 * e], gv[2 * e + 1] + bg[2 * e + 1]);
-        const uint32_t up = pack_bf16x2(uv[2 * e] + bu[2 * e], uv[2 * e + 1] + bu[2 * e + 1]);
+        const uint32_t gp = pack_bf16x2(y[i][2 * e] + bg[2 * e], y[i][2 * e + 1] + bg[2 * e + 1]);
+        const uint32_t up = pack_bf16x2(y[i][8 + 2 * e] + bu[2 * e], y[i][8 + 2 * e + 1] + bu[2 * e + 1]);
         o[e] = swiglu_bf16x2(bf16x2_lo(gp), bf16x2_hi(gp), bf16x2_lo(up), bf16x2_hi(up));
       }
     } else {
-      float v[8];
-      sum8(r, cc, v);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(v[2 * e] + bg[2 * e], v[2 * e + 1] + bg[2 * e + 1]);
+      for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(y[i][2 * e] + bg[2 * e], y[i][2 * e + 1] + bg[2 * e + 1]);
       if constexpr (EPI == kEpiResidual) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -314,9 +384,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   }
 }
 
-template <int EPI>
-__global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) u32x4 lds[kLdsBytes / 16];
+template <int EPI, bool DEEP>
+__global__ __launch_bounds__(kThreads, DEEP ? 1 : 2) void gemm_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) u32x4 lds[(DEEP ? kLdsDeep : kLdsBytes) / 16];
   const int b = static_cast<int>(blockIdx.x);
   int gi = 0;
   if (a.num_groups > 1 && b >= a.g[1].wg_begin) gi = 1;
@@ -325,12 +395,21 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs a) {
   const int r = b - G.wg_begin;
   const int item = (r % kXcds) * G.per_xcd + r / kXcds;  // XCD r % 8 takes a contiguous run of tiles
   if (item >= G.items) return;
-  if (G.cfg == kTile128)
-    gemm_tile<Cfg128, EPI>(a, G, item, lds);
-  else if (G.cfg == kTile64)
-    gemm_tile<Cfg64, EPI>(a, G, item, lds);
-  else
-    gemm_tile<Cfg32, EPI>(a, G, item, lds);
+  if constexpr (DEEP) {
+    if (G.cfg == kTile128)
+      gemm_tile<Cfg128D, EPI>(a, G, item, lds);
+    else if (G.cfg == kTile64)
+      gemm_tile<Cfg64D, EPI>(a, G, item, lds);
+    else
+      gemm_tile<Cfg32D, EPI>(a, G, item, lds);
+  } else {
+    if (G.cfg == kTile128)
+      gemm_tile<Cfg128, EPI>(a, G, item, lds);
+    else if (G.cfg == kTile64)
+      gemm_tile<Cfg64, EPI>(a, G, item, lds);
+    else
+      gemm_tile<Cfg32, EPI>(a, G, item, lds);
+  }
 }
 
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -345,6 +424,152 @@ void tiles_of(int64_t m, int64_t n, int& m_tiles, int& n_tiles) {
 int64_t tile_bytes(int cfg, int64_t k) {
   const int ch = cfg == kTile128 ? Cfg128::CH : cfg == kTile64 ? Cfg64::CH : Cfg32::CH;
   return ch * k * 64;  // ch chunks of 1 KB per 16 columns of K
+}
+
+template <class C>
+void cfg_dims(int epi, int& kg, int& per, int& v) {
+  const bool swiglu = epi == kEpiSwiglu || epi == kEpiSwigluPacked;
+  const int cpr = (swiglu ? 16 * C::NB : 32 * C::NB) / 8;
+  kg = C::KG;
+  per = (32 * C::MB * cpr + kThreads - 1) / kThreads;
+  v = swiglu ? 16 : 8;
+}
+
+constexpr int64_t kWsAlign = 256;
+int64_t align_up(int64_t x) { return (x + kWsAlign - 1) / kWsAlign * kWsAlign; }
+// Every plan keeps its tile counters in the first kCounterBytes of the
+// workspace and its partials after them: calls with different shapes can share
+// one workspace without one call's partials landing on another call's counters
+// (which must read zero when a launch starts).
+constexpr int64_t kCounterBytes = 65536;
+
+// Validates the call and fills the launch arguments.  split_k > 1 splits the K
+// range of every group over that many workgroups (the largest power of two
+// <= split_k that divides its stages);
+// *ws_bytes receives the workspace the plan needs (counters, then fp32 partials).
+hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, int64_t k, int32_t epilogue,
+                int split_k, GemmArgs& args, int64_t* ws_bytes, int64_t* cnt_off, int64_t* part_off) {
+  if (!groups || num_groups < 1 || num_groups > 3) return hipErrorInvalidValue;
+  if (epilogue < kEpiBias || epilogue > kEpiSwigluPacked) return hipErrorInvalidValue;
+  // k: whole stages of every K-group split (4 K-groups x 2 k-steps); n: whole 64-column blocks
+  if (n <= 0 || k <= 0 || n % 64 != 0 || k % 128 != 0) return hipErrorInvalidValue;
+  if (n > (1 << 30) || k > (1 << 30)) return hipErrorInvalidValue;
+  const bool swiglu = epilogue == kEpiSwiglu || epilogue == kEpiSwigluPacked;
+  const int64_t n_out = swiglu ? n / 2 : n;
+  args = GemmArgs{};
+  args.n = static_cast<int>(n);
+  args.k = static_cast<int>(k);
+  const int ksteps = static_cast<int>(k / 16);
+  int cnt = 0;
+  for (int i = 0; i < num_groups; ++i) {
+    const rldx_gemm_group_t& s = groups[i];
+    if (s.m < 0 || s.m > (1 << 24)) return hipErrorInvalidValue;
+    if (s.m == 0) continue;
+    if (!s.a_packed || !s.w_packed || !s.out || !a16(s.a_packed) || !a16(s.w_packed)) return hipErrorInvalidValue;
+    // packed operands are addressed with 32-bit byte offsets
+    if ((s.m + 31) / 32 * 32 * k * 2 > (int64_t{1} << 31) - 1 || n * k * 2 > (int64_t{1} << 31) - 1)
+      return hipErrorInvalidValue;
+    // the epilogue stores (and reads the residual) in 16-byte pieces
+    if (!a16(s.out) || (s.bias && reinterpret_cast<uintptr_t>(s.bias) % 2)) return hipErrorInvalidValue;
+    if (epilogue != kEpiSwigluPacked && (s.ldo < n_out || s.ldo % 8)) return hipErrorInvalidValue;
+    if (epilogue == kEpiResidual && (!s.residual || !a16(s.residual) || s.ldr < n_out || s.ldr % 8))
+      return hipErrorInvalidValue;
+    // Tile shape: 128 x 128 where the stream has rows and tiles enough to
+    // occupy the chip (half the L2 traffic per flop of 64 x 64), else 64 x 64,
+    // or 32 x 64 for streams of at most 32 rows.
+    int mt, nt, cfg, kg;
+    tiles_of<Cfg128>(s.m, n, mt, nt);
+    if (s.m >= 256 && static_cast<int64_t>(mt) * nt >= 128) {
+      cfg = kTile128;
+      kg = Cfg128::KG;
+    } else if (s.m > 32) {
+      cfg = kTile64;
+      kg = Cfg64::KG;
+      tiles_of<Cfg64>(s.m, n, mt, nt);
+    } else {
+      cfg = kTile32;
+      kg = Cfg32::KG;
+      tiles_of<Cfg32>(s.m, n, mt, nt);
+    }
+    const int64_t tiles = static_cast<int64_t>(mt) * nt;
+    if (tiles > (int64_t{1} << 24)) return hipErrorInvalidValue;
+    const int lstages = ksteps / (2 * kg);
+    int sp = 1;
+    while (sp * 2 <= split_k && lstages % (sp * 2) == 0) sp *= 2;
+    Group& G = args.g[cnt++];
+    G = Group{static_cast<const uint16_t*>(s.a_packed), static_cast<const uint16_t*>(s.w_packed),
+              static_cast<const uint16_t*>(s.bias), static_cast<uint16_t*>(s.out),
+              static_cast<const uint16_t*>(s.residual), s.ldo, s.ldr, static_cast<int>(s.m), cfg, mt,
+              static_cast<int>(tiles * sp), 0, 0, sp, lstages / sp, nullptr, nullptr};
+  }
+  args.num_groups = cnt;
+  if (cnt == 0) return hipSuccess;
+  // heaviest workgroups first (they take the first slot of every CU; the short
+  // streams' workgroups fill the second)
+  for (int i = 1; i < cnt; ++i)
+    for (int j = i; j > 0 && tile_bytes(args.g[j].cfg, k) / args.g[j].splits >
+                                 tile_bytes(args.g[j - 1].cfg, k) / args.g[j - 1].splits;
+         --j) {
+      const Group t = args.g[j];
+      args.g[j] = args.g[j - 1];
+      args.g[j - 1] = t;
+    }
+  int64_t wgs = 0, ws = kCounterBytes, counters = 0;
+  for (int i = 0; i < cnt; ++i) {
+    Group& G = args.g[i];
+    G.wg_begin = static_cast<int>(wgs);
+    // whole tiles per XCD: the splits of a tile meet in one L2
+    G.per_xcd = (G.items / G.splits + kXcds - 1) / kXcds * G.splits;
+    wgs += static_cast<int64_t>(G.per_xcd) * kXcds;
+    if (wgs > (int64_t{1} << 31) - 1) return hipErrorInvalidValue;
+    cnt_off[i] = part_off[i] = -1;
+    if (G.splits > 1) {
+      int kgd, per, v;
+      if (G.cfg == kTile128)
+        cfg_dims<Cfg128>(epilogue, kgd, per, v);
+      else if (G.cfg == kTile64)
+        cfg_dims<Cfg64>(epilogue, kgd, per, v);
+      else
+        cfg_dims<Cfg32>(epilogue, kgd, per, v);
+      cnt_off[i] = counters * 4;
+      counters += G.items / G.splits;
+      part_off[i] = ws;
+      const int64_t pb = static_cast<int64_t>(G.items) * per * kThreads * v * 4;
+      if (pb > (int64_t{1} << 31) - 1) return hipErrorInvalidValue;  // 32-bit buffer offsets
+      ws = align_up(ws + pb);
+    }
+  }
+  if (counters * 4 > kCounterBytes) return hipErrorInvalidValue;
+  *ws_bytes = counters ? ws : 0;
+  return hipSuccess;
+}
+
+hipError_t launch(const GemmArgs& args, int epilogue, hipStream_t stream) {
+  if (args.num_groups == 0) return hipSuccess;
+  const Group& last = args.g[args.num_groups - 1];
+  const int wgs = last.wg_begin + last.per_xcd * kXcds;
+  const dim3 grid(static_cast<unsigned>(wgs)), block(kThreads);
+  // at most one workgroup per CU (256 CUs): the deep-ring kernel
+  if (wgs <= 256) {
+    if (epilogue == kEpiBias)
+      hipLaunchKernelGGL((gemm_kernel<kEpiBias, true>), grid, block, 0, stream, args);
+    else if (epilogue == kEpiResidual)
+      hipLaunchKernelGGL((gemm_kernel<kEpiResidual, true>), grid, block, 0, stream, args);
+    else if (epilogue == kEpiSwiglu)
+      hipLaunchKernelGGL((gemm_kernel<kEpiSwiglu, true>), grid, block, 0, stream, args);
+    else
+      hipLaunchKernelGGL((gemm_kernel<kEpiSwigluPacked, true>), grid, block, 0, stream, args);
+  } else {
+    if (epilogue == kEpiBias)
+      hipLaunchKernelGGL((gemm_kernel<kEpiBias, false>), grid, block, 0, stream, args);
+    else if (epilogue == kEpiResidual)
+      hipLaunchKernelGGL((gemm_kernel<kEpiResidual, false>), grid, block, 0, stream, args);
+    else if (epilogue == kEpiSwiglu)
+      hipLaunchKernelGGL((gemm_kernel<kEpiSwiglu, false>), grid, block, 0, stream, args);
+    else
+      hipLaunchKernelGGL((gemm_kernel<kEpiSwigluPacked, false>), grid, block, 0, stream, args);
+  }
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -457,80 +682,39 @@ extern "C" hipError_t rldx_gemm_pack_weight_bf16(const void* w, int64_t ldw, int
 
 extern "C" hipError_t rldx_grouped_gemm_bf16(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n,
                                              int64_t k, int32_t epilogue, hipStream_t stream) {
-  if (!groups || num_groups < 1 || num_groups > 3) return hipErrorInvalidValue;
-  if (epilogue < kEpiBias || epilogue > kEpiSwigluPacked) return hipErrorInvalidValue;
-  // k: whole stages of every K-group split (4 K-groups x 2 k-steps); n: whole 64-column blocks
-  if (n <= 0 || k <= 0 || n % 64 != 0 || k % 128 != 0) return hipErrorInvalidValue;
-  if (n > (1 << 30) || k > (1 << 30)) return hipErrorInvalidValue;
-  const bool swiglu = epilogue == kEpiSwiglu || epilogue == kEpiSwigluPacked;
-  const int64_t n_out = swiglu ? n / 2 : n;
-  GemmArgs args{};
-  args.n = static_cast<int>(n);
-  args.k = static_cast<int>(k);
-  int cnt = 0;
-  for (int i = 0; i < num_groups; ++i) {
-    const rldx_gemm_group_t& s = groups[i];
-    if (s.m < 0 || s.m > (1 << 24)) return hipErrorInvalidValue;
-    if (s.m == 0) continue;
-    if (!s.a_packed || !s.w_packed || !s.out || !a16(s.a_packed) || !a16(s.w_packed)) return hipErrorInvalidValue;
-    // packed operands are addressed with 32-bit byte offsets
-    if ((s.m + 31) / 32 * 32 * k * 2 > (int64_t{1} << 31) - 1 || n * k * 2 > (int64_t{1} << 31) - 1)
+  GemmArgs args;
+  int64_t ws, co[3], po[3];
+  const hipError_t e = plan(groups, num_groups, n, k, epilogue, 1, args, &ws, co, po);
+  if (e != hipSuccess) return e;
+  return launch(args, epilogue, stream);
+}
+
+extern "C" int64_t rldx_grouped_gemm_workspace_bytes(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n,
+                                                     int64_t k, int32_t epilogue, int32_t split_k) {
+  GemmArgs args;
+  int64_t ws, co[3], po[3];
+  if (plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po) != hipSuccess) return -1;
+  return ws;
+}
+
+extern "C" hipError_t rldx_grouped_gemm_ws_bf16(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n,
+                                                int64_t k, int32_t epilogue, int32_t split_k, void* workspace,
+                                                int64_t workspace_bytes, hipStream_t stream) {
+  GemmArgs args;
+  int64_t ws, co[3], po[3];
+  const hipError_t e = plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po);
+  if (e != hipSuccess) return e;
+  if (ws > 0) {
+    if (!workspace || workspace_bytes < ws || reinterpret_cast<uintptr_t>(workspace) % kWsAlign)
       return hipErrorInvalidValue;
-    // the epilogue stores (and reads the residual) in 16-byte pieces
-    if (!a16(s.out) || (s.bias && reinterpret_cast<uintptr_t>(s.bias) % 2)) return hipErrorInvalidValue;
-    if (epilogue != kEpiSwigluPacked && (s.ldo < n_out || s.ldo % 8)) return hipErrorInvalidValue;
-    if (epilogue == kEpiResidual && (!s.residual || !a16(s.residual) || s.ldr < n_out || s.ldr % 8))
-      return hipErrorInvalidValue;
-    // Tile shape: 128 x 128 where the stream has rows and tiles enough to
-    // occupy the chip (half the L2 traffic per flop of 64 x 64), else 64 x 64,
-    // or 32 x 64 for streams of at most 32 rows.
-    int mt, nt, cfg;
-    tiles_of<Cfg128>(s.m, n, mt, nt);
-    if (s.m >= 256 && static_cast<int64_t>(mt) * nt >= 128) {
-      cfg = kTile128;
-    } else if (s.m > 32) {
-      cfg = kTile64;
-      tiles_of<Cfg64>(s.m, n, mt, nt);
-    } else {
-      cfg = kTile32;
-      tiles_of<Cfg32>(s.m, n, mt, nt);
-    }
-    Group& G = args.g[cnt++];
-    G = Group{static_cast<const uint16_t*>(s.a_packed), static_cast<const uint16_t*>(s.w_packed),
-              static_cast<const uint16_t*>(s.bias), static_cast<uint16_t*>(s.out),
-              static_cast<const uint16_t*>(s.residual), s.ldo, s.ldr, static_cast<int>(s.m), cfg, mt, 0, 0, 0};
-    const int64_t items = static_cast<int64_t>(mt) * nt;
-    if (items > (int64_t{1} << 28)) return hipErrorInvalidValue;
-    G.items = static_cast<int>(items);
+    char* base = static_cast<char*>(workspace);
+    for (int i = 0; i < args.num_groups; ++i)
+      if (args.g[i].splits > 1) {
+        args.g[i].cnt = reinterpret_cast<unsigned*>(base + co[i]);
+        args.g[i].part = reinterpret_cast<float*>(base + po[i]);
+      }
   }
-  if (cnt == 0) return hipSuccess;
-  // One launch for all groups, heaviest tiles first (their workgroups take the
-  // first slot of every CU; the short streams' tiles fill the second).
-  for (int i = 1; i < cnt; ++i)
-    for (int j = i; j > 0 && tile_bytes(args.g[j].cfg, k) > tile_bytes(args.g[j - 1].cfg, k); --j) {
-      const Group t = args.g[j];
-      args.g[j] = args.g[j - 1];
-      args.g[j - 1] = t;
-    }
-  int64_t wgs = 0;
-  for (int i = 0; i < cnt; ++i) {
-    Group& G = args.g[i];
-    G.wg_begin = static_cast<int>(wgs);
-    G.per_xcd = (G.items + kXcds - 1) / kXcds;
-    wgs += static_cast<int64_t>(G.per_xcd) * kXcds;
-  }
-  if (wgs > (int64_t{1} << 31) - 1) return hipErrorInvalidValue;
-  args.num_groups = cnt;
-  const dim3 grid(static_cast<unsigned>(wgs)), block(kThreads);
-  if (epilogue == kEpiBias)
-    hipLaunchKernelGGL(gemm_kernel<kEpiBias>, grid, block, 0, stream, args);
-  else if (epilogue == kEpiResidual)
-    hipLaunchKernelGGL(gemm_kernel<kEpiResidual>, grid, block, 0, stream, args);
-  else if (epilogue == kEpiSwiglu)
-    hipLaunchKernelGGL(gemm_kernel<kEpiSwiglu>, grid, block, 0, stream, args);
-  else
-    hipLaunchKernelGGL(gemm_kernel<kEpiSwigluPacked>, grid, block, 0, stream, args);
-  return hipGetLastError();
+  return launch(args, epilogue, stream);
 }
 
 extern "C" int64_t rldx_act_packed_elems(int64_t m, int64_t k) {

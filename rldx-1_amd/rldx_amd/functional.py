@@ -490,22 +490,38 @@ def layernorm_pack(x: torch.Tensor, eps: float = 1e-6, out: Optional[PackedAct] 
     return out
 
 
-def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias") -> None:
-    """One launch (two when row counts differ a lot) of y_s = a_s W_s^T + bias_s for
-    up to 3 streams sharing n and k.  items: (a PackedAct [m, k] or row-major
-    tensor (packed first), PackedWeight, bias [n] or None, out, residual or None).
-    epilogue: "bias" (out = y), "residual" (out = residual + y, residual may be
-    out), "swiglu" (out [m, n/2] = swiglu(y)) or "swiglu_packed" (out a PackedAct)."""
-    epi = {"bias": _lib.GEMM_EPI_BIAS, "residual": _lib.GEMM_EPI_RESIDUAL, "swiglu": _lib.GEMM_EPI_SWIGLU,
-           "swiglu_packed": _lib.GEMM_EPI_SWIGLU_PACKED}[epilogue]
+class GemmWorkspace:
+    """Device scratch of the split-K grouped GEMM: per-tile arrival counters and
+    fp32 partial tiles.  Zero-filled once here; every launch leaves its counters
+    at zero again, so one workspace serves any number of grouped_gemm calls that
+    run one after another on one stream (calls that overlap in time need their own)."""
+
+    __slots__ = ("data",)
+
+    COUNTER_BYTES = 65536  # the tile counters; the fp32 partials follow and need no initial value
+
+    def __init__(self, nbytes: int, device):
+        self.data = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        self.data[: self.COUNTER_BYTES].zero_()
+
+
+_GEMM_EPI = {"bias": _lib.GEMM_EPI_BIAS, "residual": _lib.GEMM_EPI_RESIDUAL, "swiglu": _lib.GEMM_EPI_SWIGLU,
+             "swiglu_packed": _lib.GEMM_EPI_SWIGLU_PACKED}
+
+
+def _gemm_groups(items: Sequence[tuple], epi: int, pack: bool):
     _require(1 <= len(items) <= 3, "between 1 and 3 groups")
     n, k = items[0][1].n, items[0][1].k
     groups = (_lib.GemmGroup * len(items))()
     keep = []
     for i, (a, w, bias, out, res) in enumerate(items):
         if not isinstance(a, PackedAct):
-            a = pack_act(a)
-            keep.append(a)
+            _require(isinstance(a, torch.Tensor) and a.dim() == 2, "a must be a PackedAct or a 2-D tensor")
+            if not pack:  # shape-only query
+                a = PackedAct(a, a.shape[0], a.shape[1])
+            else:
+                a = pack_act(a)
+                keep.append(a)
         _on_gpu(a.data, w.data, bias, res)
         _require(w.n == n and w.k == k and a.k == k, "groups must share n and k")
         _require(epi < _lib.GEMM_EPI_SWIGLU or w.swiglu_pairs, "SwiGLU epilogue needs a swiglu_pairs weight")
@@ -526,9 +542,38 @@ def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias") -> None:
         groups[i] = _lib.GemmGroup(a.data.data_ptr(), m, w.data.data_ptr(), _ptr(bias), out_ptr, ldo,
                                    _ptr(res) if epi == _lib.GEMM_EPI_RESIDUAL else None,
                                    res.stride(0) if epi == _lib.GEMM_EPI_RESIDUAL else 0)
+    return groups, n, k, keep, w.data
+
+
+def grouped_gemm_workspace_bytes(items: Sequence[tuple], epilogue: str = "bias", split_k: int = 1) -> int:
+    """Workspace bytes grouped_gemm(items, epilogue, split_k, workspace) needs (0: no split)."""
+    epi = _GEMM_EPI[epilogue]
+    groups, n, k, _, _ = _gemm_groups(items, epi, pack=False)
+    r = _lib.load().rldx_grouped_gemm_workspace_bytes(groups, len(items), n, k, epi, int(split_k))
+    _require(r >= 0, "grouped GEMM shape not supported")
+    return int(r)
+
+
+def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias", split_k: int = 1,
+                 workspace: Optional[GemmWorkspace] = None) -> None:
+    """One launch of y_s = a_s W_s^T + bias_s for up to 3 streams sharing n and k.
+    items: (a PackedAct [m, k] or row-major tensor (packed first), PackedWeight,
+    bias [n] or None, out, residual or None).  epilogue: "bias" (out = y),
+    "residual" (out = residual + y, residual may be out), "swiglu" (out [m, n/2] =
+    swiglu(y)) or "swiglu_packed" (out a PackedAct).  split_k > 1 splits the K
+    range of every stream over that many workgroups (partials summed in a fixed
+    order: deterministic); it needs a workspace of grouped_gemm_workspace_bytes(...)
+    bytes."""
+    epi = _GEMM_EPI[epilogue]
+    groups, n, k, keep, wt = _gemm_groups(items, epi, pack=True)
     lib = _lib.load()
-    _lib.check(lib.rldx_grouped_gemm_bf16(groups, len(items), n, k, epi, _stream_ptr(w.data)),
-               "rldx_grouped_gemm_bf16")
+    if split_k <= 1:
+        _lib.check(lib.rldx_grouped_gemm_bf16(groups, len(items), n, k, epi, _stream_ptr(wt)), "rldx_grouped_gemm_bf16")
+    else:
+        _require(workspace is not None, "split_k > 1 needs a GemmWorkspace")
+        _on_gpu(workspace.data)
+        _lib.check(lib.rldx_grouped_gemm_ws_bf16(groups, len(items), n, k, epi, int(split_k), workspace.data.data_ptr(),
+                                                 workspace.data.numel(), _stream_ptr(wt)), "rldx_grouped_gemm_ws_bf16")
 
 
 # ---------------------------------------------------------------------------

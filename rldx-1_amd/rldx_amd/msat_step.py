@@ -183,13 +183,27 @@ class MsatActionStep:
                                           for L in range(cfg.blocks)]
         self.graph = None
 
-    # -- one block -----------------------------------------------------------
-    def _block(self, L: int) -> None:
+    def _gemms(self, L: int) -> dict:
+        """The four grouped GEMMs of block L: (items, epilogue)."""
         cfg, w, pw = self.cfg, self.w, self.pw
         rows = [(s, cfg.rows(s)) for s in STREAMS]
+        return {
+            "qkv": ([(self.h.rows(r.start, r.stop), pw[f"{s}.qkv"][L], w[f"{s}.qkv.b"][L], self.qkv[r], None)
+                     for s, r in rows], "bias"),
+            "proj": ([(self.att.rows(r.start, r.stop), pw[f"{s}.proj"][L], w[f"{s}.proj.b"][L], self.x[r], self.x[r])
+                      for s, r in rows], "residual"),
+            "w12": ([(self.h.rows(r.start, r.stop), pw[f"{s}.w12"][L], w[f"{s}.w12.b"][L],
+                      self.gl.rows(r.start, r.stop), None) for s, r in rows], "swiglu_packed"),
+            "w3": ([(self.gl.rows(r.start, r.stop), pw[f"{s}.w3"][L], w[f"{s}.w3.b"][L], self.x[r], self.x[r])
+                    for s, r in rows], "residual"),
+        }
+
+    # -- one block -----------------------------------------------------------
+    def _block(self, L: int) -> None:
+        cfg, w = self.cfg, self.w
+        gemm = self._gemms(L)
         Fn.layernorm_pack(self.x, cfg.eps, out=self.h)
-        Fn.grouped_gemm([(self.h.rows(r.start, r.stop), pw[f"{s}.qkv"][L], w[f"{s}.qkv.b"][L], self.qkv[r], None)
-                         for s, r in rows], "bias")
+        Fn.grouped_gemm(*gemm["qkv"])
         specs = [
             Fn.StreamSpec(self.qkv[cfg.rows("vl")], w["vl.q_norm"][L], w["vl.k_norm"][L]),
             Fn.StreamSpec(self.qkv[cfg.rows("sa")], w["sa.q_norm"][L], w["sa.k_norm"][L],
@@ -200,13 +214,10 @@ class MsatActionStep:
         Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
         Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), cfg.tokens, key_bias=self.inp["key_bias"],
                             out=self.att)
-        Fn.grouped_gemm([(self.att.rows(r.start, r.stop), pw[f"{s}.proj"][L], w[f"{s}.proj.b"][L], self.x[r],
-                          self.x[r]) for s, r in rows], "residual")
+        Fn.grouped_gemm(*gemm["proj"])
         Fn.layernorm_pack(self.x, cfg.eps, out=self.h)
-        Fn.grouped_gemm([(self.h.rows(r.start, r.stop), pw[f"{s}.w12"][L], w[f"{s}.w12.b"][L],
-                          self.gl.rows(r.start, r.stop), None) for s, r in rows], "swiglu_packed")
-        Fn.grouped_gemm([(self.gl.rows(r.start, r.stop), pw[f"{s}.w3"][L], w[f"{s}.w3.b"][L], self.x[r], self.x[r])
-                         for s, r in rows], "residual")
+        Fn.grouped_gemm(*gemm["w12"])
+        Fn.grouped_gemm(*gemm["w3"])
 
     # -- one action step ------------------------------------------------------
     def run(self, steps: int | None = None, blocks: int | None = None) -> torch.Tensor:

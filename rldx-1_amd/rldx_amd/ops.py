@@ -315,18 +315,24 @@ def ss_fused_mlp_swiglu(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tenso
     """silu(x W_gate^T + b_gate) * (x W_up^T + b_up), W = [W_gate; W_up] (2*N_half, K).
 
     rldx/inference/action_model/single_stream/engine/ops/op_fused_mlp_swiglu.py:13-43
-    (kernel fused_mlp_swiglu.py:199-267).  `split_k` is accepted for signature
-    compatibility; the tile shape and the K split inside a workgroup are chosen
-    from M and N.  Rounding: the eager chain (GEMM output rounded to bf16, then
-    SwiGLU's two roundings).  Needs K % 128 == 0 and N_half % 32 == 0."""
-    del split_k
+    (kernel fused_mlp_swiglu.py:199-267).  split_k > 1 splits K across
+    workgroups (fp32 partials in a workspace allocated per call, as the
+    reference's launcher does; the last workgroup of each tile sums them in
+    split order and applies the epilogue), the largest power of two <= split_k
+    that divides the K stages.  Rounding: the eager chain (GEMM output rounded to
+    bf16, then SwiGLU's two roundings).  Needs K % 128 == 0 and N_half % 32 == 0."""
     M, K = x.shape
     nh = weight.shape[0] // 2
     out = torch.empty((M, nh), dtype=torch.bfloat16, device=x.device)
     if M == 0:
         return out
     xx = x if x.stride(1) == 1 else x.contiguous()
-    Fn.grouped_gemm([(xx, _packed_weight(weight, True), bias.contiguous(), out, None)], "swiglu")
+    items = [(xx, _packed_weight(weight, True), bias.contiguous(), out, None)]
+    ws = None
+    if split_k > 1:
+        need = Fn.grouped_gemm_workspace_bytes(items, "swiglu", split_k)
+        ws = Fn.GemmWorkspace(need, x.device) if need > 0 else None
+    Fn.grouped_gemm(items, "swiglu", split_k=split_k if ws is not None else 1, workspace=ws)
     return out
 
 

@@ -145,6 +145,39 @@ def test_capi_rejects_bad_arguments_without_launching():
     assert lib.rldx_llm_fused_attention_workspace_bytes(1280, 4, 128) == 1280 * 4 * 128 * 2 + 4 * 40 * 64 * 128 * 2
 
 
+def _gemm_groups(ms, a_ptr=256, w_ptr=512, out_ptr=1024, ldo=8192):
+    groups = (_lib.GemmGroup * len(ms))()
+    for i, m in enumerate(ms):
+        groups[i] = _lib.GemmGroup(a_ptr, m, w_ptr, None, out_ptr, ldo, out_ptr, ldo)
+    return groups
+
+
+def test_grouped_gemm_split_plan_and_rejections():
+    """The split-K plan is a host-side function of the shapes and split_k: every
+    group's K stages are split by the largest power of two <= split_k dividing
+    them; a too small, missing or misaligned workspace and unsupported shapes are
+    rejected before anything is launched."""
+    lib = _lib.load()
+    msat = (512, 64, 32)
+    # W3 shapes (n 1536, k 4096): 512 rows -> 192 tiles of 64 x 64, 64 rows -> 24,
+    # 32 rows -> 24 tiles of 32 x 64; 16 KB of partials per tile and split
+    w3 = lib.rldx_grouped_gemm_workspace_bytes(_gemm_groups(msat), 3, 1536, 4096, 1, 8)
+    assert w3 == 65536 + (192 + 24 + 24) * 8 * 16384
+    assert lib.rldx_grouped_gemm_workspace_bytes(_gemm_groups(msat), 3, 1536, 4096, 1, 1) == 0
+    # split_k 6 -> 4; k 1536 gives 12 stages in the 32 x 64 tiles' four K-groups: 8 does not divide them
+    assert lib.rldx_grouped_gemm_workspace_bytes(_gemm_groups((32,)), 1, 1536, 4096, 1, 6) == 65536 + 24 * 4 * 16384
+    assert lib.rldx_grouped_gemm_workspace_bytes(_gemm_groups((32,)), 1, 1536, 1536, 1, 8) == 65536 + 24 * 4 * 16384
+    assert lib.rldx_grouped_gemm_workspace_bytes(_gemm_groups(msat), 3, 8192, 1000, 3, 2) == -1   # k % 128
+    assert lib.rldx_grouped_gemm_workspace_bytes(_gemm_groups(msat), 3, 8160, 1536, 0, 2) == -1   # n % 64
+    g = _gemm_groups(msat)
+    assert lib.rldx_grouped_gemm_ws_bf16(g, 3, 1536, 4096, 1, 8, 4096, w3 - 256, None) == HIP_INVALID_VALUE
+    assert lib.rldx_grouped_gemm_ws_bf16(g, 3, 1536, 4096, 1, 8, 4096 + 16, w3, None) == HIP_INVALID_VALUE
+    assert lib.rldx_grouped_gemm_ws_bf16(g, 3, 1536, 4096, 1, 8, None, w3, None) == HIP_INVALID_VALUE
+    assert lib.rldx_grouped_gemm_ws_bf16(_gemm_groups(msat, a_ptr=264), 3, 1536, 4096, 1, 8, 4096, w3,
+                                         None) == HIP_INVALID_VALUE
+    assert lib.rldx_grouped_gemm_bf16(_gemm_groups(msat), 3, 1536, 4096, 7, None) == HIP_INVALID_VALUE
+
+
 def test_zero_sized_calls_are_noops():
     lib = _lib.load()
     st = _lib.i64_array([0, 0, 0])

@@ -142,6 +142,98 @@ def test_grouped_gemm_deterministic(dev):
     assert torch.equal(o1, o2)
 
 
+@pytest.mark.parametrize("epilogue,n,k,split_k", [("residual", 1536, 4096, 8), ("bias", 1536, 1536, 4),
+                                                  ("bias", 4608, 1536, 2), ("swiglu", 1536, 1024, 8),
+                                                  ("swiglu_packed", 3072, 1536, 4)])
+def test_grouped_gemm_split_k(dev, epilogue, n, k, split_k):
+    """split_k splits every stream's K range across workgroups (partials summed in
+    split order by the last workgroup of a tile): same bf16 tolerance against the
+    fp32 reference, bit-identical on repeated launches that share one workspace
+    (the tile counters are re-armed), close to the unsplit result."""
+    g = torch.Generator().manual_seed(n + k)
+    swiglu = epilogue.startswith("swiglu")
+    n_out = n // 2 if swiglu else n
+    items, refs, outs = [], [], []
+    for m in (512, 64, 32):
+        a, w, b = _rand((m, k), g), _rand((n, k), g, 0.5 / k ** 0.5), _rand((n,), g, 0.1)
+        res = _rand((m, n_out), g, 0.5) if epilogue == "residual" else None
+        y = _linear_ref(a, w, b)
+        if swiglu:
+            r = ref.swiglu(y)
+        elif res is not None:
+            r = (res.float() + y.float()).to(BF16)
+        else:
+            r = y
+        refs.append(r)
+        if epilogue == "swiglu_packed":
+            out = Fn.PackedAct.empty(m, n_out, dev)
+        else:
+            out = res.to(dev) if res is not None else torch.empty(m, n_out, dtype=BF16, device=dev)
+        outs.append(out)
+        items.append((a.to(dev), Fn.pack_weight(w.to(dev), swiglu_pairs=swiglu), b.to(dev), out,
+                      out if res is not None else None))
+    need = Fn.grouped_gemm_workspace_bytes(items, epilogue, split_k)
+    assert need > 0
+    ws = Fn.GemmWorkspace(need, dev)
+
+    def result():
+        return [o.unpack().clone() if isinstance(o, Fn.PackedAct) else o.clone() for o in outs]
+
+    base = [o.clone() for o in outs] if epilogue == "residual" else None
+
+    def reset():
+        if base is not None:
+            for o, b0 in zip(outs, base):
+                o.copy_(b0)
+
+    Fn.grouped_gemm(items, epilogue, split_k=split_k, workspace=ws)
+    first = result()
+    for got, r in zip(first, refs):
+        assert_bf16_close(got, r, f"split-K gemm {epilogue}")
+    for _ in range(3):  # counters re-armed, partials overwritten: identical results
+        reset()
+        Fn.grouped_gemm(items, epilogue, split_k=split_k, workspace=ws)
+        for x, y in zip(result(), first):
+            assert torch.equal(x, y)
+    reset()
+    Fn.grouped_gemm(items, epilogue)  # no split
+    for x, y in zip(result(), first):
+        assert_bf16_close(x, y, "split vs unsplit")
+    assert int(ws.data[:65536].count_nonzero()) == 0  # every tile counter back at zero
+
+
+def test_grouped_gemm_split_k_workspace_shared_across_shapes(dev):
+    """One workspace serves split GEMMs of different shapes in turn (their plans
+    place partials at different offsets, counters in the common area): every call
+    matches its first result bit for bit and the bf16 reference."""
+    g = torch.Generator().manual_seed(77)
+    calls = []
+    for n, k, epilogue in ((4608, 1536, "bias"), (1536, 1536, "bias"), (1536, 4096, "bias")):
+        items, refs = [], []
+        for m in (512, 64, 32):
+            a, w, b = _rand((m, k), g), _rand((n, k), g, 0.5 / k ** 0.5), _rand((n,), g, 0.1)
+            items.append((a.to(dev), Fn.pack_weight(w.to(dev)), b.to(dev), torch.empty(m, n, dtype=BF16, device=dev),
+                          None))
+            refs.append(_linear_ref(a, w, b))
+        calls.append((items, refs, epilogue))
+    ws = Fn.GemmWorkspace(max(Fn.grouped_gemm_workspace_bytes(it, ep, 4) for it, _, ep in calls), dev)
+    first = None
+    for rnd in range(3):
+        got = []
+        for items, refs, ep in calls:
+            Fn.grouped_gemm(items, ep, split_k=4, workspace=ws)
+            got.append([it[3].clone() for it in items])
+            if rnd == 0:
+                for o, r in zip(got[-1], refs):
+                    assert_bf16_close(o, r, "split-K, shared workspace")
+        if first is None:
+            first = got
+        else:
+            for xs, ys in zip(got, first):
+                for x, y in zip(xs, ys):
+                    assert torch.equal(x, y)
+
+
 @pytest.mark.parametrize("m,k", [(608, 1536), (5, 4096), (33, 64)])
 def test_act_pack_roundtrip(dev, m, k):
     g = torch.Generator().manual_seed(m + k)
@@ -206,6 +298,9 @@ def test_ss_fused_mlp_swiglu_op(dev):
     assert y.shape == (M, NH)
     assert_bf16_close(y, ref.swiglu(_linear_ref(x, w, b)), "ss::fused_mlp_swiglu")
     assert torch.equal(torch.ops.ss.fused_mlp_swiglu(xd, wd, bd, 1), y)  # packed-weight cache hit
+    ys = torch.ops.ss.fused_mlp_swiglu(xd, wd, bd, 4)  # split-K: partials summed in a fixed order
+    assert_bf16_close(ys, ref.swiglu(_linear_ref(x, w, b)), "ss::fused_mlp_swiglu split_k=4")
+    assert torch.equal(torch.ops.ss.fused_mlp_swiglu(xd, wd, bd, 4), ys)
     wd.mul_(0.5)  # in-place update -> repacked
     assert_bf16_close(torch.ops.ss.fused_mlp_swiglu(xd, wd, bd, 1), ref.swiglu(_linear_ref(x, (w.float() * 0.5).to(BF16), b)),
                       "after weight update")
