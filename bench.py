@@ -393,8 +393,8 @@ def main():
     tf = ROOT / "profiles" / "gemm_w12_swiglu_traffic.json"
     if tf.exists():
         traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
-    roofline = dict(kernel="gemm_kernel<2,2,4,SWIGLU_PACKED>: W12 + SwiGLU grouped GEMM, 3 streams "
-                           "(512/64/32 rows) x [8192 x 1536] weights",
+    roofline = dict(kernel="gemm_kernel<SWIGLU_PACKED>: W12 + SwiGLU grouped GEMM, 3 streams "
+                           "(512/64/32 rows: 128x128 / 64x64 / 32x64 tiles) x [8192 x 1536] weights",
                     bound="hbm", achieved=dom["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=dom["gbs"] / HBM_PEAK_GBS, traffic=traffic, algorithmic_bytes=dom["bytes"],
                     flops=dom["flops"], us=dom["us"])
