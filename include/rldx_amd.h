@@ -246,6 +246,44 @@ hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv_row_stride
 /* Workspace bytes rldx_llm_fused_attention_bf16 needs (normalised K + packed K/V). */
 int64_t rldx_llm_fused_attention_workspace_bytes(int64_t seq, int64_t kv_heads, int64_t head_dim);
 
+/*
+ * The rldx_backbone::vision_attention operator (Qwen3-VL ViT blocks): fused
+ * QKV rows (total_tokens, 3*num_heads*head_dim) bf16, contiguous -> out
+ * (total_tokens, num_heads*head_dim) bf16, contiguous.  Per head, the Q and K
+ * columns get rotate-half RoPE in fp32 with the baked tables rope_cos /
+ * rope_sin (total_tokens, head_dim) fp32, contiguous (sin's first half already
+ * negated):  y[d] = bf16(x[d] * cos[d] + x[d +- head_dim/2] * sin[d]);  then
+ * non-causal softmax(Q K^T * scaling) V over each sequence
+ * [cu_seqlens[s], cu_seqlens[s+1]) (cu_seqlens: num_seqs + 1 int32 in device
+ * memory, ascending, cu_seqlens[num_seqs] <= total_tokens), fp32 scores and
+ * softmax, P rounded to bf16 before P.V.  Rows outside every sequence are not
+ * written.  Sequences may have any lengths; the launch depends only on
+ * total_tokens and num_seqs, never on the cu_seqlens values (graph
+ * capturable); out-of-range cu_seqlens values are clamped to [0, total_tokens]
+ * on the device.  head_dim % 8 == 0, 8 <= head_dim <= 128 (computed at 64,
+ * 96 or 128 columns with zero padding).  qkv, rope_cos, rope_sin, workspace
+ * 16-byte aligned, out 8-byte aligned.  Two launches: RoPE + K/V packing into
+ * `workspace` (>= rldx_vision_attention_workspace_bytes bytes, caller-owned;
+ * layout: RoPE'd Q [num_heads][total_tokens][64|96|128] bf16 at offset 0,
+ * then the packed K/V tiles), then the attention kernel.
+ *
+ * Replaces: fused_vision_attention.forward(qkv, rope_cos, rope_sin, cu_seqlens,
+ *   scaling, num_heads, head_dim)
+ *   (rldx/inference/backbone/vision_encoder/engine/kernels/fused_vision_attention.py:622-645)
+ *   behind rldx_backbone::vision_attention
+ *   (.../vision_encoder/engine/ops/op_fused_vision_attention.py:14-42).  The
+ *   reference sizes its grid for equal-length sequences (M // num_seqs, :490);
+ *   here every sequence is covered whatever its length.
+ */
+hipError_t rldx_vision_attention_bf16(const void* qkv, const float* rope_cos, const float* rope_sin,
+                                      const int32_t* cu_seqlens, int64_t num_seqs, void* out, int64_t total_tokens,
+                                      int64_t num_heads, int64_t head_dim, float scaling, void* workspace,
+                                      int64_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes rldx_vision_attention_bf16 needs; -1 for an unsupported head_dim. */
+int64_t rldx_vision_attention_workspace_bytes(int64_t total_tokens, int64_t num_seqs, int64_t num_heads,
+                                              int64_t head_dim);
+
 /* ------------------------------------------------------------------------ */
 /* Grouped GEMM of the MSAT block linears                                   */
 /* ------------------------------------------------------------------------ */

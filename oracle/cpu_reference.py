@@ -82,6 +82,84 @@ def llm_fused_attention(qkv, q_norm_w, k_norm_w, cos, sin, num_heads, num_kv_hea
 
 
 # ---------------------------------------------------------------------------
+# Vision tower (Qwen3-VL ViT) attention
+# ---------------------------------------------------------------------------
+def vision_rope(x: torch.Tensor, rope_cos: torch.Tensor, rope_sin: torch.Tensor) -> torch.Tensor:
+    """Baked rotate-half RoPE of the Qwen3-VL vision tower as the fused op applies it
+    (fused_vision_attention.py:47-80, :117-139): x [M, H, D] bf16, rope_cos / rope_sin
+    [M, D] fp32 with rotate_half's sign folded into the first half of rope_sin
+    (custom_vision_encoder_chain.py:101-108):
+        y[d] = bf16(x[d] * cos[d] + x[d +- D/2] * sin_baked[d])   in fp32.
+    Equal, product by product, to apply_rotary_pos_emb_vision (modeling_qwen3_vl.py:125-136)
+    with the unbaked sin."""
+    D = x.shape[-1]
+    half = D // 2
+    rot = torch.cat([torch.arange(half, D), torch.arange(0, half)])
+    xf = x.float()
+    c = rope_cos.float()[:, None, :]
+    sn = rope_sin.float()[:, None, :]
+    return (xf * c + xf[..., rot] * sn).to(torch.bfloat16)
+
+
+def vision_attention(qkv: torch.Tensor, rope_cos: torch.Tensor, rope_sin: torch.Tensor, cu_seqlens: torch.Tensor,
+                     scaling: float, num_heads: int, head_dim: int) -> torch.Tensor:
+    """rldx_backbone::vision_attention (op_fused_vision_attention.py:13-45; kernel
+    fused_vision_attention.py:83-159, :206-320, :622-645): qkv [M, 3 H D] bf16 with
+    columns Q | K | V (head h at h D), baked RoPE on Q and K (vision_rope), then
+    non-causal attention inside each sequence [cu_seqlens[s], cu_seqlens[s+1]):
+    S = Q K^T (fp32 sums of bf16 products) * scaling, softmax in fp32, P rounded to
+    bf16 for the P.V product, fp32 sums, output rounded to bf16.  Returns [M, H D]."""
+    M = qkv.shape[0]
+    H, D = num_heads, head_dim
+    q, k, v = qkv.reshape(M, 3, H, D).unbind(1)
+    qr = vision_rope(q, rope_cos, rope_sin)
+    kr = vision_rope(k, rope_cos, rope_sin)
+    out = torch.zeros(M, H, D, dtype=torch.float32)
+    cu = [int(x) for x in cu_seqlens.tolist()]
+    for s in range(len(cu) - 1):
+        a, b = cu[s], cu[s + 1]
+        if b <= a:
+            continue
+        qs = qr[a:b].float().transpose(0, 1)  # [H, L, D]
+        ks = kr[a:b].float().transpose(0, 1)
+        vs = v[a:b].float().transpose(0, 1)
+        sc = torch.matmul(qs, ks.transpose(1, 2)) * scaling
+        m = sc.amax(dim=-1, keepdim=True)
+        pe = torch.exp(sc - m)
+        l = pe.sum(dim=-1, keepdim=True)
+        o = torch.matmul(pe.to(torch.bfloat16).float(), vs) / l
+        out[a:b] = o.transpose(0, 1)
+    return out.to(torch.bfloat16).reshape(M, H * D)
+
+
+def vision_attention_eager(qkv: torch.Tensor, rope_cos: torch.Tensor, rope_sin: torch.Tensor,
+                           cu_seqlens: torch.Tensor, scaling: float, num_heads: int, head_dim: int) -> torch.Tensor:
+    """The eager path the fused op replaces: Qwen3VLVisionAttention.forward without
+    flash attention (modeling_qwen3_vl.py:193-262) with apply_rotary_pos_emb_vision
+    (:125-136) and eager_attention_forward (:153-176): bf16 score matmul, softmax in
+    fp32 rounded back to bf16, bf16 P.V.  Used to pin vision_attention (they differ
+    by the score and probability roundings)."""
+    M = qkv.shape[0]
+    H, D = num_heads, head_dim
+    q, k, v = qkv.reshape(M, 3, H, D).permute(1, 0, 2, 3).unbind(0)
+    half = D // 2
+    sin = rope_sin.clone()
+    sin[:, :half] = -sin[:, :half]
+    cos_, sin_ = rope_cos.unsqueeze(-2).float(), sin.unsqueeze(-2).float()
+    qe = (q.float() * cos_ + rotate_half(q.float()) * sin_).to(q.dtype)
+    ke = (k.float() * cos_ + rotate_half(k.float()) * sin_).to(k.dtype)
+    qe, ke, ve = (t.transpose(0, 1).unsqueeze(0) for t in (qe, ke, v))
+    lengths = (cu_seqlens[1:] - cu_seqlens[:-1]).tolist()
+    outs = []
+    for qs, ks, vs in zip(torch.split(qe, lengths, dim=2), torch.split(ke, lengths, dim=2),
+                          torch.split(ve, lengths, dim=2)):
+        w = torch.matmul(qs, ks.transpose(2, 3)) * scaling
+        w = F.softmax(w, dim=-1, dtype=torch.float32).to(qs.dtype)
+        outs.append(torch.matmul(w, vs).transpose(1, 2))
+    return torch.cat(outs, dim=1).reshape(M, H * D)
+
+
+# ---------------------------------------------------------------------------
 # MSAT pieces
 # ---------------------------------------------------------------------------
 def msat_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:

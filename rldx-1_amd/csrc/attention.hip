@@ -118,7 +118,45 @@ struct AttnArgs {
   int64_t cs_ss;             // row stride of cos/sin
   float eps;
   int sin_signed;
+  // variable-length sequences (kVarlen): query / key rows of sequence s are
+  // [cu_seqlens[s], cu_seqlens[s+1]) of q / o; its packed K/V tiles start at
+  // tile slot seq_slot_base(s) of each head
+  const int32_t* cu_seqlens;
+  int num_seqs;
+  int total_rows;
+  int d_store;  // output columns written per head (<= D)
 };
+
+// Sequence s of a variable-length batch (rows [c_s, c_{s+1}) with
+// c_s = clamp(cu_seqlens[s], 0, rows)) owns the 32-row slots
+// [base_s, base_s + ceil(len_s / 32)) with base_s = floor((c_s + 31 s) / 32).
+// base_{s+1} - base_s >= ceil(len_s / 32), so the slot ranges of the
+// sequences do not overlap, and every slot is below
+// floor((rows + 31 num_seqs) / 32) whatever the cu_seqlens values are: no
+// scan of cu_seqlens is needed to place a sequence, and a slot finds its
+// sequence by a binary search over log2(num_seqs) entries.
+struct SeqSlot {
+  int start, len, base;
+};
+
+__host__ __device__ constexpr int64_t seq_slot_count(int64_t rows, int64_t num_seqs) {
+  return (rows + 31 * num_seqs) / 32;
+}
+
+__device__ __forceinline__ int clamp_row(int32_t c, int rows) { return c < 0 ? 0 : (c > rows ? rows : c); }
+
+__device__ __forceinline__ SeqSlot find_seq_slot(const int32_t* cu, int num_seqs, int rows, int slot) {
+  int lo = 0, hi = num_seqs - 1;  // last s with base_s <= slot (0 when there is none)
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    const int64_t base = (static_cast<int64_t>(clamp_row(cu[mid], rows)) + 31 * static_cast<int64_t>(mid)) / 32;
+    if (base <= slot) lo = mid;
+    else hi = mid - 1;
+  }
+  const int c0 = clamp_row(cu[lo], rows), c1 = clamp_row(cu[lo + 1], rows);
+  return SeqSlot{c0, c1 > c0 ? c1 - c0 : 0,
+                 static_cast<int>((static_cast<int64_t>(c0) + 31 * static_cast<int64_t>(lo)) / 32)};
+}
 
 __device__ __forceinline__ float bf(uint16_t b) { return bf16_bits_to_f32(b); }
 
@@ -198,8 +236,10 @@ __device__ __forceinline__ void qnorm_rope_shared(bf16x8 (&qreg)[D / 16], const 
   for (int ks = 0; ks < KS; ++ks) qreg[ks] = __builtin_bit_cast(bf16x8, qsh[ks * 64 + lane]);
 }
 
-template <int D, int NSUB, bool kCausal, bool kBias, bool kQNorm>
+template <int D, int NSUB, bool kCausal, bool kBias, bool kQNorm, bool kVarlen = false>
 __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
+  static_assert(!kVarlen || (NSUB == 1 && !kCausal && !kBias && !kQNorm),
+                "variable-length mode: 32-query blocks, no mask, no fused Q normalisation");
   constexpr int NW = 4;           // waves per workgroup; each walks its own key tiles
   constexpr int BN = kTileKeys;   // keys per tile
   constexpr int BMW = 32 * NSUB;  // queries per workgroup (shared by the 4 waves)
@@ -233,15 +273,30 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
     h = (p / nqb) % a.hq;
     b = p / (nqb * a.hq);
   }
+  // Query / key range of the workgroup: the whole batch entry, or (kVarlen)
+  // the sequence that owns 32-row slot qb; an unused slot exits here, before
+  // any barrier.
+  int sq = a.sq, sk = a.sk;
+  int64_t row0 = 0, tile0 = 0;
+  if constexpr (kVarlen) {
+    const SeqSlot ss = find_seq_slot(a.cu_seqlens, a.num_seqs, a.total_rows, qb);
+    const int lq = qb - ss.base;
+    if (lq < 0 || lq >= (ss.len + BN - 1) / BN) return;
+    qb = lq;
+    sq = sk = ss.len;
+    row0 = ss.start;
+    tile0 = ss.base;
+  }
   const int hk = h / a.group;
   const int q_first = qb * BMW;
-  const int k_end = kCausal ? min(a.sk, min(a.sq, q_first + BMW)) : a.sk;
+  const int k_end = kCausal ? min(sk, min(sq, q_first + BMW)) : sk;
   const int ntiles = (k_end + BN - 1) / BN;  // >= 1: q_first < sq and sk >= 1
-  const int head_tiles = (a.sk + BN - 1) / BN;
+  const int head_tiles = (sk + BN - 1) / BN;
 
-  // Every load below stays inside this head's packed tiles: tile indices are
-  // clamped to [0, ntiles), and ntiles <= head_tiles.
-  const __amdgpu_buffer_rsrc_t kvr = make_rsrc(a.kv + b * a.kv_sb + hk * a.kv_sh, head_tiles * TILE_BYTES);
+  // Every load below stays inside this head's (sequence's) packed tiles: tile
+  // indices are clamped to [0, ntiles), and ntiles <= head_tiles.
+  const __amdgpu_buffer_rsrc_t kvr =
+      make_rsrc(a.kv + b * a.kv_sb + hk * a.kv_sh + tile0 * kv_tile_elems(D), head_tiles * TILE_BYTES);
   const int voff = lane * 16;
   // Bias: lane reads the 16 keys of its accumulator rows (4 runs of 4 keys); a
   // dword past sk is out of the descriptor's range and reads as 0.
@@ -285,14 +340,14 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
   for (int j = 0; j < NSUB; ++j) {
     q_idx[j] = q_first + 32 * j + l32;
     const uint16_t* qrow =
-        a.q + b * a.q_sb + h * a.q_sh + static_cast<int64_t>(min(q_idx[j], a.sq - 1)) * a.q_ss + g * 8;
+        a.q + b * a.q_sb + h * a.q_sh + (row0 + min(q_idx[j], sq - 1)) * a.q_ss + g * 8;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks)
       qreg[j][ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qrow + ks * 16));
     if constexpr (kQNorm) {
       static_assert(NSUB == 1, "the fused Q normalisation handles one 32-query sub-block");
       __shared__ u32x4 qsh[KSTEPS * 64];
-      qnorm_rope_shared<D>(qreg[j], a, q_idx[j], q_idx[j] < a.sq, wave, qsh);
+      qnorm_rope_shared<D>(qreg[j], a, q_idx[j], q_idx[j] < sq, wave, qsh);
     }
   }
 
@@ -359,7 +414,7 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
       if (!active[j]) continue;
       const int qf = q_first + 32 * j;  // first query of this sub-block
       // ---- softmax (log2 domain, lane = one query, 16 of the tile's keys) ----
-      const bool edge = (k0 + BN > a.sk) || (kCausal && k0 + BN - 1 > qf) || bias_tile;
+      const bool edge = (k0 + BN > sk) || (kCausal && k0 + BN - 1 > qf) || bias_tile;
       float mt = -__builtin_inff();
       if (!edge) {
 #pragma unroll
@@ -371,7 +426,7 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
           const int key = k0 + 8 * (e >> 2) + 4 * g + (e & 3);
           float sv = sacc[j][e] * c;
           if constexpr (kBias) sv += bq[e >> 2][e & 3] * kLog2e;
-          bool ok = key < a.sk;
+          bool ok = key < sk;
           if constexpr (kCausal) ok = ok && (key <= q_idx[j]);
           sv = ok ? sv : -__builtin_inff();
           sacc[j][e] = sv;
@@ -470,8 +525,8 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
     }
     l = pair_sum(l);
     const float inv = l > 0.f ? 1.0f / l : 0.f;
-    if (q_idx[j] < a.sq) {
-      uint16_t* orow = a.o + b * a.o_sb + h * a.o_sh + static_cast<int64_t>(q_idx[j]) * a.o_ss;
+    if (q_idx[j] < sq) {
+      uint16_t* orow = a.o + b * a.o_sb + h * a.o_sh + (row0 + q_idx[j]) * a.o_ss;
 #pragma unroll
       for (int r = 0; r < DPW; ++r) {
         const int db = wave + r * NW;
@@ -483,6 +538,7 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
           for (int w = 1; w < NW; ++w) acc += part[r][q4][w] * wgt[w];
           acc *= inv;
           const int d = db * 32 + q4 * 8 + g * 4;
+          if (kVarlen && d >= a.d_store) continue;  // zero padding columns of a head_dim < D
           uint2 wv;
           wv.x = pack_bf16x2(acc[0], acc[1]);
           wv.y = pack_bf16x2(acc[2], acc[3]);
@@ -544,6 +600,123 @@ __global__ __launch_bounds__(256) void kv_pack_kernel(const uint16_t* __restrict
     }
     *reinterpret_cast<u32x4*>(dst + NCH * 512 + idx * 8) = out;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Vision attention front end (Qwen3-VL ViT blocks, variable-length images).
+// Fused QKV rows [rows, 3 * H * hd] -> (1) rotate-half RoPE'd Q rows, zero
+// padded to DP columns, [H][rows][DP]; (2) the packed K/V tiles (D = DP, layout
+// at the top of this file) of every (head, sequence), K RoPE'd, keys and
+// columns past the sequence / hd zero.  Tile lt of sequence s sits in slot
+// base_s + lt of its head (SeqSlot).  One workgroup per (slot, head); an unused
+// slot exits at once.
+// RoPE (fused_vision_attention.py:47-80, :117-139), fp32, each product rounded:
+//   y[d] = bf16(x[d] * cos[d] + x[d +- hd/2] * sin_baked[d]),
+// the sign of rotate_half's first half folded into sin_baked
+// (custom_vision_encoder_chain.py:101-108).
+// ---------------------------------------------------------------------------
+struct VitArgs {
+  const uint16_t* qkv;  // [rows, 3 * heads * hd]
+  const float* cos;     // [rows, hd]
+  const float* sin;     // [rows, hd], baked sign
+  const int32_t* cu_seqlens;
+  uint16_t* qpad;       // [heads][rows][DP]
+  uint16_t* kvp;        // [heads][slots] packed tiles
+  int64_t kv_sh;        // elements per head of kvp
+  int num_seqs, rows, heads, hd;
+};
+
+__device__ __forceinline__ uint2 vit_rope4(uint2 x, uint2 p, floatx4 c, floatx4 s) {
+#pragma clang fp contract(off)
+  const float y0 = bf16x2_lo(x.x) * c[0] + bf16x2_lo(p.x) * s[0];
+  const float y1 = bf16x2_hi(x.x) * c[1] + bf16x2_hi(p.x) * s[1];
+  const float y2 = bf16x2_lo(x.y) * c[2] + bf16x2_lo(p.y) * s[2];
+  const float y3 = bf16x2_hi(x.y) * c[3] + bf16x2_hi(p.y) * s[3];
+  return uint2{pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)};
+}
+
+template <int DP>
+__global__ __launch_bounds__(256) void vit_pack_kernel(VitArgs v) {
+  constexpr int PITCH = DP + 8;  // 16-byte aligned LDS rows
+  constexpr int G = DP / 4;      // 4-column groups per padded row
+  constexpr int NCH = DP / 16;   // 1 KB chunks per K / V part
+  __shared__ __attribute__((aligned(16))) uint16_t tq[32 * PITCH];
+  __shared__ __attribute__((aligned(16))) uint16_t tk[32 * PITCH];
+  __shared__ __attribute__((aligned(16))) uint16_t tv[32 * PITCH];
+  const int slot = static_cast<int>(blockIdx.x), h = static_cast<int>(blockIdx.y);
+  const SeqSlot ss = find_seq_slot(v.cu_seqlens, v.num_seqs, v.rows, slot);
+  const int lt = slot - ss.base;
+  if (lt < 0 || lt >= (ss.len + 31) / 32) return;
+  const int r0 = ss.start + 32 * lt;           // first row of the tile
+  const int nrows = min(32, ss.len - 32 * lt);  // rows of the sequence in it
+  const int hd = v.hd, half = hd >> 1;
+  const int64_t qkv_ss = 3LL * v.heads * hd;
+  const uint16_t* qsrc = v.qkv + static_cast<int64_t>(h) * hd;
+  const uint16_t* ksrc = qsrc + static_cast<int64_t>(v.heads) * hd;
+  const uint16_t* vsrc = ksrc + static_cast<int64_t>(v.heads) * hd;
+  // rows r0 .. r0 + nrows - 1 < rows and columns < hd: every read is inside
+  // qkv / cos / sin (4-column groups never straddle hd or hd / 2: hd % 8 == 0)
+  for (int u = threadIdx.x; u < 32 * G; u += 256) {
+    const int r = u / G, d4 = (u % G) * 4;
+    uint2 oq{0, 0}, ok{0, 0}, ov{0, 0};
+    if (r < nrows && d4 < hd) {
+      const int64_t row = r0 + r;
+      const int pd = d4 < half ? d4 + half : d4 - half;
+      const uint16_t* qr = qsrc + row * qkv_ss;
+      const uint16_t* kr = ksrc + row * qkv_ss;
+      const floatx4 c = *reinterpret_cast<const floatx4*>(v.cos + row * hd + d4);
+      const floatx4 sn = *reinterpret_cast<const floatx4*>(v.sin + row * hd + d4);
+      oq = vit_rope4(*reinterpret_cast<const uint2*>(qr + d4), *reinterpret_cast<const uint2*>(qr + pd), c, sn);
+      ok = vit_rope4(*reinterpret_cast<const uint2*>(kr + d4), *reinterpret_cast<const uint2*>(kr + pd), c, sn);
+      ov = *reinterpret_cast<const uint2*>(vsrc + row * qkv_ss + d4);
+    }
+    *reinterpret_cast<uint2*>(&tq[r * PITCH + d4]) = oq;
+    *reinterpret_cast<uint2*>(&tk[r * PITCH + d4]) = ok;
+    *reinterpret_cast<uint2*>(&tv[r * PITCH + d4]) = ov;
+  }
+  __syncthreads();
+  // Q rows of the sequence -> qpad (DP columns, the padding included)
+  uint16_t* qdst = v.qpad + (static_cast<int64_t>(h) * v.rows + r0) * DP;
+  for (int c = threadIdx.x; c < nrows * (DP / 8); c += 256) {
+    const int r = c / (DP / 8), col = (c % (DP / 8)) * 8;
+    *reinterpret_cast<u32x4*>(qdst + r * DP + col) = *reinterpret_cast<const u32x4*>(&tq[r * PITCH + col]);
+  }
+  uint16_t* dst = v.kvp + static_cast<int64_t>(h) * v.kv_sh + static_cast<int64_t>(slot) * kv_tile_elems(DP);
+  // K part: chunk ks, lane l = key (l & 31), columns 16 ks + 8 (l >> 5) .. + 7
+  for (int idx = threadIdx.x; idx < NCH * 64; idx += 256) {
+    const int ks = idx >> 6, l = idx & 63;
+    *reinterpret_cast<u32x4*>(dst + idx * 8) =
+        *reinterpret_cast<const u32x4*>(&tk[(l & 31) * PITCH + 16 * ks + 8 * (l >> 5)]);
+  }
+  // V part: 8 keys of one column per lane
+  for (int idx = threadIdx.x; idx < NCH * 64; idx += 256) {
+    const int cc = idx >> 6, l = idx & 63;
+    const int db = cc >> 1, s2 = cc & 1;
+    const int d = 32 * db + (l & 31);
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      const int rr = 16 * s2 + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
+      o[i >> 1] = static_cast<uint32_t>(tv[rr * PITCH + d]) | (static_cast<uint32_t>(tv[(rr + 1) * PITCH + d]) << 16);
+    }
+    *reinterpret_cast<u32x4*>(dst + NCH * 512 + idx * 8) = o;
+  }
+}
+
+// head_dim -> padded K/V tile width (a multiple of 32 the attention kernel is
+// built for), 0 when unsupported
+constexpr int vit_padded_dim(int64_t hd) {
+  return (hd < 8 || hd > 128 || hd % 8) ? 0 : (hd <= 64 ? 64 : (hd <= 96 ? 96 : 128));
+}
+
+template <int DP>
+hipError_t launch_vit(const VitArgs& v, AttnArgs a, int64_t slots, hipStream_t stream) {
+  hipLaunchKernelGGL(vit_pack_kernel<DP>, dim3(static_cast<unsigned>(slots), static_cast<unsigned>(v.heads)),
+                     dim3(256), 0, stream, v);
+  a.num_q_blocks = static_cast<int>(slots);
+  hipLaunchKernelGGL((attn_fwd_kernel<DP, 1, false, false, false, true>),
+                     dim3(static_cast<unsigned>(slots * v.heads)), dim3(256), 0, stream, a);
+  return hipGetLastError();
 }
 
 template <int D, int NSUB, bool kQNorm>
@@ -776,4 +949,67 @@ extern "C" hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv
   a.eps = eps;
   a.sin_signed = sin_is_signed ? 1 : 0;
   return launch_attn<true>(a, head_dim, 1, true, false, stream);
+}
+
+extern "C" int64_t rldx_vision_attention_workspace_bytes(int64_t total_tokens, int64_t num_seqs, int64_t num_heads,
+                                                          int64_t head_dim) {
+  const int dp = vit_padded_dim(head_dim);
+  if (total_tokens < 0 || num_seqs < 0 || num_heads < 0 || dp == 0) return -1;
+  // padded Q [H][rows][DP] (rounded up to 256 bytes), then the packed K/V slots of the H heads
+  const int64_t q_bytes = (num_heads * total_tokens * dp * 2 + 255) / 256 * 256;
+  return q_bytes + num_heads * seq_slot_count(total_tokens, num_seqs) * kv_tile_elems(dp) * 2;
+}
+
+extern "C" hipError_t rldx_vision_attention_bf16(const void* qkv, const float* rope_cos, const float* rope_sin,
+                                                 const int32_t* cu_seqlens, int64_t num_seqs, void* out,
+                                                 int64_t total_tokens, int64_t num_heads, int64_t head_dim,
+                                                 float scaling, void* workspace, int64_t workspace_bytes,
+                                                 hipStream_t stream) {
+  const int dp = vit_padded_dim(head_dim);
+  if (dp == 0 || total_tokens < 0 || num_heads <= 0 || num_seqs <= 0) return hipErrorInvalidValue;
+  if (!(scaling > 0.f) || scaling == __builtin_inff()) return hipErrorInvalidValue;
+  if (total_tokens == 0) return hipSuccess;
+  if (!qkv || !rope_cos || !rope_sin || !cu_seqlens || !out || !workspace) return hipErrorInvalidValue;
+  if (!a16(qkv) || !a16(rope_cos) || !a16(rope_sin) || !a16(workspace) || reinterpret_cast<uintptr_t>(out) % 8 ||
+      reinterpret_cast<uintptr_t>(cu_seqlens) % 4)
+    return hipErrorInvalidValue;
+  if (total_tokens > (1 << 24) || num_seqs > (1 << 24) || num_heads > 65535) return hipErrorInvalidValue;
+  const int64_t slots = seq_slot_count(total_tokens, num_seqs);
+  // 1-D attention grid, 32-bit byte offsets inside a head's packed tiles
+  if (slots * num_heads > (int64_t{1} << 31) - 1 || slots * kv_tile_elems(dp) * 2 > (int64_t{1} << 31) - 1)
+    return hipErrorInvalidValue;
+  if (workspace_bytes < rldx_vision_attention_workspace_bytes(total_tokens, num_seqs, num_heads, head_dim))
+    return hipErrorInvalidValue;
+  const int64_t q_bytes = (num_heads * total_tokens * dp * 2 + 255) / 256 * 256;
+  VitArgs v{};
+  v.qkv = static_cast<const uint16_t*>(qkv);
+  v.cos = rope_cos;
+  v.sin = rope_sin;
+  v.cu_seqlens = cu_seqlens;
+  v.qpad = static_cast<uint16_t*>(workspace);
+  v.kvp = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + q_bytes);
+  v.kv_sh = slots * kv_tile_elems(dp);
+  v.num_seqs = static_cast<int>(num_seqs);
+  v.rows = static_cast<int>(total_tokens);
+  v.heads = static_cast<int>(num_heads);
+  v.hd = static_cast<int>(head_dim);
+  AttnArgs a{};
+  a.q = v.qpad;
+  a.q_sh = total_tokens * dp;
+  a.q_ss = dp;
+  a.kv = v.kvp;
+  a.kv_sh = v.kv_sh;
+  a.o = static_cast<uint16_t*>(out);
+  a.o_sh = head_dim;
+  a.o_ss = num_heads * head_dim;
+  a.hq = a.hkv = v.heads;
+  a.group = 1;
+  a.scale_log2 = scaling * kLog2e;
+  a.cu_seqlens = cu_seqlens;
+  a.num_seqs = v.num_seqs;
+  a.total_rows = v.rows;
+  a.d_store = v.hd;
+  if (dp == 64) return launch_vit<64>(v, a, slots, stream);
+  if (dp == 96) return launch_vit<96>(v, a, slots, stream);
+  return launch_vit<128>(v, a, slots, stream);
 }

@@ -412,6 +412,50 @@ def llm_fused_attention(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: tor
     return out
 
 
+def vision_attention_workspace_bytes(total_tokens: int, num_seqs: int, num_heads: int, head_dim: int) -> int:
+    n = int(_lib.load().rldx_vision_attention_workspace_bytes(total_tokens, num_seqs, num_heads, head_dim))
+    _require(n >= 0, f"vision attention: unsupported head_dim {head_dim} (multiple of 8 in [8, 128])")
+    return n
+
+
+def vision_attention(qkv: torch.Tensor, rope_cos: torch.Tensor, rope_sin: torch.Tensor, cu_seqlens: torch.Tensor,
+                     scaling: float, num_heads: int, head_dim: int, *, out: Optional[torch.Tensor] = None,
+                     workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Fused QKV (M, 3*H*D) bf16 -> (M, H*D) bf16: rotate-half RoPE with the
+    baked fp32 tables (sin's first half negated) on Q and K, then non-causal
+    attention within each cu_seqlens segment (rldx_backbone::vision_attention
+    semantics).  `workspace` (uint8, >= vision_attention_workspace_bytes) may
+    be passed in to keep the call allocation-free."""
+    _on_gpu(qkv, rope_cos, rope_sin, cu_seqlens, out, workspace)
+    H, D = int(num_heads), int(head_dim)
+    _require(qkv.dtype == BF16 and qkv.dim() == 2 and qkv.is_contiguous() and qkv.shape[1] == 3 * H * D,
+             f"qkv must be contiguous bf16 (M, 3*H*D = {3 * H * D})")
+    M = qkv.shape[0]
+    if rope_cos.dtype != F32:
+        rope_cos = rope_cos.float()
+    if rope_sin.dtype != F32:
+        rope_sin = rope_sin.float()
+    rope_cos, rope_sin = rope_cos.contiguous(), rope_sin.contiguous()
+    _require(rope_cos.shape == (M, D) and rope_sin.shape == (M, D), f"rope_cos / rope_sin must be (M, D) = ({M}, {D})")
+    _require(cu_seqlens.dtype == torch.int32 and cu_seqlens.dim() == 1 and cu_seqlens.numel() >= 2 and
+             cu_seqlens.is_contiguous(), "cu_seqlens must be contiguous int32 (num_seqs + 1,)")
+    S = cu_seqlens.numel() - 1
+    if out is None:
+        out = torch.empty((M, H * D), dtype=BF16, device=qkv.device)
+    _require(out.dtype == BF16 and out.shape == (M, H * D) and out.is_contiguous(), "out must be contiguous bf16 (M, H*D)")
+    need = vision_attention_workspace_bytes(M, S, H, D)
+    if workspace is None:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=qkv.device)
+    _require(workspace.dtype == torch.uint8 and workspace.is_contiguous() and workspace.numel() >= need,
+             f"workspace must be contiguous uint8 with >= {need} bytes")
+    lib = _lib.load()
+    _lib.check(lib.rldx_vision_attention_bf16(qkv.data_ptr(), rope_cos.data_ptr(), rope_sin.data_ptr(),
+                                              cu_seqlens.data_ptr(), S, out.data_ptr(), M, H, D, float(scaling),
+                                              workspace.data_ptr(), workspace.numel(), _stream_ptr(qkv)),
+               "rldx_vision_attention_bf16")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # grouped GEMM (MSAT block linears)
 # ---------------------------------------------------------------------------

@@ -6,13 +6,14 @@ Importing this module registers, backed by the gfx950 kernels of librldx_amd.so:
   ds::grouped_res_ln         ds::vl_epilogue_ln
   ss::fused_attention_2way   ss::fused_attention_3way   ss::fused_mlp_swiglu
   ss::fused_epilogue_ln
-  rldx_backbone::fused_attention
+  rldx_backbone::fused_attention   rldx_backbone::vision_attention
   rldx_backbone::fused_epilogue_add2_rmsnorm   rldx_backbone::fused_epilogue_add3_rmsnorm
   rldx_amd::swiglu           (the eager `F.silu(x1) * x2` the chains inline)
 
 Argument order and defaults follow the reference registrations
 (rldx/inference/action_model/{double,single}_stream/engine/ops/*.py,
-rldx/inference/backbone/llm/engine/ops/op_fused_llm_attention.py).  Additive,
+rldx/inference/backbone/llm/engine/ops/op_fused_llm_attention.py,
+rldx/inference/backbone/vision_encoder/engine/ops/op_fused_vision_attention.py).  Additive,
 optional keyword arguments: `num_heads` / `head_dim` (the reference hard-codes
 24 x 64), `num_kv_heads` for the backbone op (reference: 32 / 8 / 128 with a
 fixed 4096-wide output), and `kv_mask` on the 3-way ops (1 = visible key,
@@ -270,6 +271,28 @@ def rldx_backbone_fused_attention(
 @rldx_backbone_fused_attention.register_fake
 def _(qkv, q_norm_w, q_norm_w_rot, k_norm_w, k_norm_w_rot, cos, signed_sin, num_heads=32, num_kv_heads=8,
       head_dim=128):
+    return qkv.new_empty((qkv.shape[0], num_heads * head_dim))
+
+
+@torch.library.custom_op("rldx_backbone::vision_attention", mutates_args=())
+def rldx_backbone_vision_attention(
+    qkv: torch.Tensor,
+    rope_cos: torch.Tensor,
+    rope_sin: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    scaling: float,
+    num_heads: int,
+    head_dim: int,
+) -> torch.Tensor:
+    """Fused vision RoPE (baked cos / signed sin) + non-causal attention per
+    cu_seqlens segment on a fused (M, 3*H*D) QKV buffer -> (M, H*D).
+
+    Reference: backbone/vision_encoder/engine/ops/op_fused_vision_attention.py:14-42."""
+    return Fn.vision_attention(qkv, rope_cos, rope_sin, cu_seqlens, scaling, num_heads, head_dim)
+
+
+@rldx_backbone_vision_attention.register_fake
+def _(qkv, rope_cos, rope_sin, cu_seqlens, scaling, num_heads, head_dim):
     return qkv.new_empty((qkv.shape[0], num_heads * head_dim))
 
 

@@ -180,6 +180,79 @@ def gqa_flops(cfg: GqaCfg = GqaCfg()) -> int:
     return 4 * cfg.q_heads * cfg.head_dim * cfg.seq * (cfg.seq + 1) // 2
 
 
+# ---------------------------------------------------------------------------
+# ViT attention (Qwen3-VL vision tower): fused QKV of several images, baked
+# 2-D rotary tables, one cu_seqlens segment per image
+# ---------------------------------------------------------------------------
+@dataclass
+class VitAttnCfg:
+    images: int = 2
+    grid_h: int = 14
+    grid_w: int = 14
+    heads: int = 16
+    head_dim: int = 72
+    merge: int = 2
+    theta: float = 10000.0
+    seed: int = 6
+    lengths: tuple = ()  # explicit per-sequence lengths (ragged batches); positions row-major in grid_w columns
+
+    @property
+    def seq_lengths(self) -> list:
+        return list(self.lengths) if self.lengths else [self.grid_h * self.grid_w] * self.images
+
+    @property
+    def tokens(self) -> int:
+        return sum(self.seq_lengths)
+
+
+def vit_positions(cfg: VitAttnCfg) -> torch.Tensor:
+    """(row, col) patch coordinates per token, Qwen3VLVisionModel.rot_pos_emb order
+    (modeling_qwen3_vl.py:787-824): merge x merge blocks row-major, patches
+    row-major inside a block.  Explicit lengths use plain row-major coordinates."""
+    if cfg.lengths:
+        return torch.cat([torch.stack((torch.arange(n) // cfg.grid_w, torch.arange(n) % cfg.grid_w), dim=-1)
+                          for n in cfg.lengths])
+    m = cfg.merge
+    bh, bw = cfg.grid_h // m, cfg.grid_w // m
+    rows = (torch.arange(bh)[:, None, None, None] * m + torch.arange(m)[None, None, :, None]).expand(bh, bw, m, m)
+    cols = (torch.arange(bw)[None, :, None, None] * m + torch.arange(m)[None, None, None, :]).expand(bh, bw, m, m)
+    one = torch.stack((rows.reshape(-1), cols.reshape(-1)), dim=-1)
+    return one.repeat(cfg.images, 1)
+
+
+def vit_rope_tables(cfg: VitAttnCfg):
+    """Baked fp32 cos / sin [M, head_dim]: Qwen3VLVisionRotaryEmbedding(head_dim // 2)
+    frequencies looked up at the (row, col) coordinates, emb = cat(f, f)
+    (modeling_qwen3_vl.py:84-95, :912-918), rotate_half's sign folded into the
+    first half of sin (custom_vision_encoder_chain.py:101-108)."""
+    dim = cfg.head_dim // 2
+    inv_freq = 1.0 / (cfg.theta ** (torch.arange(0, dim, 2, dtype=torch.float32) / dim))
+    pos = vit_positions(cfg)
+    table = torch.outer(torch.arange(int(pos.max()) + 1, dtype=torch.float32), inv_freq)
+    freqs = table[pos].flatten(1)  # [M, dim]
+    emb = torch.cat((freqs, freqs), dim=-1)
+    cos, sin = emb.cos(), emb.sin()
+    sin[:, : cfg.head_dim // 2] = -sin[:, : cfg.head_dim // 2]
+    return cos.contiguous(), sin.contiguous()
+
+
+def vit_attention_inputs(cfg: VitAttnCfg = VitAttnCfg()):
+    """Fused QKV (M, 3 * H * D) bf16 ~ N(0, 1), baked rope tables, cu_seqlens
+    int32 and scaling = D ** -0.5."""
+    g = torch.Generator().manual_seed(cfg.seed)
+    M = cfg.tokens
+    qkv = torch.randn(M, 3 * cfg.heads * cfg.head_dim, generator=g).to(torch.bfloat16)
+    cos, sin = vit_rope_tables(cfg)
+    cu = torch.tensor([0] + cfg.seq_lengths, dtype=torch.int64).cumsum(0).to(torch.int32)
+    return dict(qkv=qkv, rope_cos=cos, rope_sin=sin, cu_seqlens=cu, scaling=cfg.head_dim ** -0.5,
+                num_heads=cfg.heads, head_dim=cfg.head_dim)
+
+
+def vit_attention_flops(cfg: VitAttnCfg = VitAttnCfg()) -> int:
+    """Q K^T and P V of every sequence at the true head_dim."""
+    return 4 * cfg.heads * cfg.head_dim * sum(n * n for n in cfg.seq_lengths)
+
+
 def signed_sin(sin: torch.Tensor) -> torch.Tensor:
     """prepare_signed_sin (fused_llm_attention.py:787-796): first half negated."""
     D = sin.shape[-1]

@@ -178,6 +178,38 @@ def test_grouped_gemm_split_plan_and_rejections():
     assert lib.rldx_grouped_gemm_bf16(_gemm_groups(msat), 3, 1536, 4096, 7, None) == HIP_INVALID_VALUE
 
 
+def test_vision_attention_workspace_and_rejections():
+    lib = _lib.load()
+    # 2 x 196 tokens, 16 heads x 72 (padded to 96): Q 16*392*96*2 bytes, 14 slots of 128*96-byte tiles per head
+    assert lib.rldx_vision_attention_workspace_bytes(392, 2, 16, 72) == 16 * 392 * 96 * 2 + 16 * 14 * 128 * 96
+    assert lib.rldx_vision_attention_workspace_bytes(100, 3, 2, 64) == 25600 + 2 * ((100 + 93) // 32) * 128 * 64
+    for hd in (0, 4, 68, 136, -8):
+        assert lib.rldx_vision_attention_workspace_bytes(392, 2, 16, hd) == -1
+    big = 1 << 30
+    ok = dict(qkv=256, cos=512, sin=768, cu=1024, S=2, out=2048, M=392, H=16, D=72, sc=0.1, ws=4096, wsb=big)
+
+    def call(**kw):
+        a = {**ok, **kw}
+        return lib.rldx_vision_attention_bf16(a["qkv"], a["cos"], a["sin"], a["cu"], a["S"], a["out"], a["M"], a["H"],
+                                              a["D"], a["sc"], a["ws"], a["wsb"], None)
+
+    assert call(D=70) == HIP_INVALID_VALUE             # head_dim % 8
+    assert call(D=136) == HIP_INVALID_VALUE            # head_dim > 128
+    assert call(S=0) == HIP_INVALID_VALUE              # no sequence
+    assert call(H=0) == HIP_INVALID_VALUE
+    assert call(sc=0.0) == HIP_INVALID_VALUE
+    assert call(sc=float("inf")) == HIP_INVALID_VALUE
+    assert call(qkv=None) == HIP_INVALID_VALUE
+    assert call(cu=None) == HIP_INVALID_VALUE
+    assert call(qkv=264) == HIP_INVALID_VALUE          # 16-byte alignment
+    assert call(cos=520) == HIP_INVALID_VALUE
+    assert call(out=2052) == HIP_INVALID_VALUE         # 8-byte alignment
+    assert call(cu=1026) == HIP_INVALID_VALUE
+    assert call(wsb=16 * 392 * 96 * 2) == HIP_INVALID_VALUE  # workspace too small
+    assert call(M=(1 << 24) + 1) == HIP_INVALID_VALUE
+    assert call(M=0, qkv=None, out=None) == 0          # nothing to do
+
+
 def test_zero_sized_calls_are_noops():
     lib = _lib.load()
     st = _lib.i64_array([0, 0, 0])

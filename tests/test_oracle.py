@@ -313,6 +313,115 @@ def test_signed_sin_and_rotated_weight_reproduce_rotate_half():
 
 
 # ---------------------------------------------------------------------------
+# Vision tower attention (fused_vision_attention.py; modeling_qwen3_vl.py:125-262)
+# ---------------------------------------------------------------------------
+def _vit(lengths, heads=2, head_dim=72, seed=11):
+    return W.vit_attention_inputs(W.VitAttnCfg(lengths=tuple(lengths), heads=heads, head_dim=head_dim, seed=seed))
+
+
+def test_vision_rope_equals_unbaked_rotate_half_bitwise():
+    """Baked sin (first half negated) times the partner == rotate_half with the
+    plain sin, product by product (apply_rotary_pos_emb_vision, :125-136)."""
+    inp = _vit([37, 20], heads=3)
+    M, H, D = 57, 3, 72
+    x = inp["qkv"][:, : H * D].reshape(M, H, D)
+    sin = inp["rope_sin"].clone()
+    sin[:, : D // 2] = -sin[:, : D // 2]
+    eager = (x.float() * inp["rope_cos"][:, None] + ref.rotate_half(x.float()) * sin[:, None]).to(torch.bfloat16)
+    assert torch.equal(ref.vision_rope(x, inp["rope_cos"], inp["rope_sin"]).view(torch.int16), eager.view(torch.int16))
+
+
+def test_vision_rope_identity_at_zero_angle_and_pair_rotation():
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(5, 2, 72, generator=g).to(torch.bfloat16)
+    one, zero = torch.ones(5, 72), torch.zeros(5, 72)
+    assert torch.equal(ref.vision_rope(x, one, zero), x)
+    # angle pi/2 on every pair: (a, b) -> (-b, a) exactly
+    sin = torch.ones(5, 72)
+    sin[:, :36] = -1
+    y = ref.vision_rope(x, zero, sin)
+    assert torch.equal(y[..., :36], -x[..., 36:]) and torch.equal(y[..., 36:], x[..., :36])
+    # the table's 2-D angles: token at patch (0, 0) has angle 0 (cos 1, sin 0)
+    cos_t, sin_t = W.vit_rope_tables(W.VitAttnCfg(images=1))
+    assert torch.equal(cos_t[0], torch.ones(72)) and torch.equal(sin_t[0], torch.zeros(72))
+
+
+def test_vision_rope_tables_closed_form():
+    """cos/sin at patch (r, c): column j < 18 uses r * inv_freq[j], 18 <= j < 36
+    uses c * inv_freq[j - 18], repeated for the second half; sin's first half negated."""
+    cfg = W.VitAttnCfg(images=1, grid_h=4, grid_w=6)
+    cos_t, sin_t = W.vit_rope_tables(cfg)
+    pos = W.vit_positions(cfg)
+    # merge order: first 4 tokens are the 2x2 block at (0, 0)
+    assert pos[:4].tolist() == [[0, 0], [0, 1], [1, 0], [1, 1]] and pos[4].tolist() == [0, 2]
+    inv = [1.0 / 10000 ** (2 * i / 36) for i in range(18)]
+    for t in (5, 13, 23):
+        r, c = pos[t].tolist()
+        ang = [r * f for f in inv] + [c * f for f in inv]
+        ang = ang + ang
+        for j in (0, 7, 17, 18, 30, 36, 53, 71):
+            assert abs(cos_t[t, j].item() - math.cos(ang[j])) < 1e-6
+            sgn = -1.0 if j < 36 else 1.0
+            assert abs(sin_t[t, j].item() - sgn * math.sin(ang[j])) < 1e-6
+
+
+def test_vision_attention_single_sequence_matches_fp64_brute_force():
+    inp = _vit([45], heads=2, head_dim=64)
+    M, H, D = 45, 2, 64
+    o = ref.vision_attention(**inp)
+    q, k, v = inp["qkv"].reshape(M, 3, H, D).unbind(1)
+    qr = ref.vision_rope(q, inp["rope_cos"], inp["rope_sin"])
+    kr = ref.vision_rope(k, inp["rope_cos"], inp["rope_sin"])
+    o64 = brute_attention(qr.transpose(0, 1)[None], kr.transpose(0, 1)[None], v.transpose(0, 1)[None])
+    o64 = o64[0].transpose(0, 1).reshape(M, H * D)
+    assert (o.double() - o64).abs().max() < 2e-2
+
+
+def test_vision_attention_scaling_is_applied():
+    inp = _vit([30], heads=1, head_dim=64)
+    M, D = 30, 64
+    o = ref.vision_attention(**{**inp, "scaling": 0.5 / math.sqrt(D)})
+    q, k, v = inp["qkv"].reshape(M, 3, 1, D).unbind(1)
+    qr = ref.vision_rope(q, inp["rope_cos"], inp["rope_sin"])
+    kr = ref.vision_rope(k, inp["rope_cos"], inp["rope_sin"])
+    o64 = brute_attention(0.5 * f64(qr).transpose(0, 1)[None], kr.transpose(0, 1)[None], v.transpose(0, 1)[None])
+    assert (o.double() - o64[0].transpose(0, 1).reshape(M, D)).abs().max() < 2e-2
+
+
+def test_vision_attention_segments_are_independent():
+    """Each cu_seqlens segment sees only its own keys: the output equals the
+    segments run alone (bitwise), and changing one segment's K/V leaves the
+    others unchanged."""
+    lengths = [17, 40, 1, 33]
+    inp = _vit(lengths)
+    o = ref.vision_attention(**inp)
+    cu = inp["cu_seqlens"].tolist()
+    for s, n in enumerate(lengths):
+        a, b = cu[s], cu[s + 1]
+        sub = _vit([n])
+        sub.update(qkv=inp["qkv"][a:b], rope_cos=inp["rope_cos"][a:b], rope_sin=inp["rope_sin"][a:b])
+        assert torch.equal(ref.vision_attention(**sub).view(torch.int16), o[a:b].view(torch.int16))
+    qkv2 = inp["qkv"].clone()
+    qkv2[cu[1]:cu[2], 2 * 72:] = 7.0  # K and V columns of segment 1
+    o2 = ref.vision_attention(**{**inp, "qkv": qkv2})
+    keep = torch.ones(o.shape[0], dtype=torch.bool)
+    keep[cu[1]:cu[2]] = False
+    assert torch.equal(o[keep].view(torch.int16), o2[keep].view(torch.int16))
+    # a single-token segment attends to itself only: out = its V
+    v_last = inp["qkv"][cu[2], 2 * 2 * 72:].reshape(2, 72)
+    assert torch.equal(o[cu[2]].reshape(2, 72), v_last)
+
+
+def test_vision_attention_close_to_the_eager_path():
+    """The eager Qwen3VLVisionAttention path (bf16 scores / probabilities)
+    agrees within the bf16 rounding of its extra steps."""
+    inp = _vit([50, 23], heads=3)
+    o = ref.vision_attention(**inp).double()
+    e = ref.vision_attention_eager(**inp).double()
+    assert (o - e).abs().max() < 4e-2 and (o - e).norm() / e.norm() < 1e-2
+
+
+# ---------------------------------------------------------------------------
 # LayerNorm and the MSAT step oracle
 # ---------------------------------------------------------------------------
 def test_layer_norm_closed_form():
