@@ -280,6 +280,28 @@ hipError_t rldx_vision_attention_bf16(const void* qkv, const float* rope_cos, co
                                       int64_t num_heads, int64_t head_dim, float scaling, void* workspace,
                                       int64_t workspace_bytes, hipStream_t stream);
 
+/*
+ * The mem::fused_attention operator (TransformerMemory layers): fused QKV rows
+ * (tokens, 3*num_heads*head_dim) bf16, contiguous -> out (tokens,
+ * num_heads*head_dim) bf16, contiguous.  Q and K get rotate-half RoPE in bf16
+ * arithmetic, each step rounded to bf16 as the eager module does:
+ *   y[d] = bf16(bf16(x[d] * cos[d]) + bf16(x[d +- head_dim/2] * signed_sin[d]))
+ * (cos / signed_sin (tokens, head_dim) bf16, contiguous, sin's first half
+ * negated); then softmax(Q K^T / sqrt(head_dim)) V with the block-causal mask:
+ * query i sees key j iff j / block_attn_size <= i / block_attn_size.  fp32
+ * scores and softmax, P rounded to bf16 before P.V.  head_dim 64, 128 or 256;
+ * block_attn_size >= 1.  qkv, cos, signed_sin 16-byte aligned, out 8-byte
+ * aligned.  One launch, no workspace.
+ *
+ * Replaces: fused_memory_attention.forward(qkv, cos, signed_sin, num_heads,
+ *   head_dim, block_attn_size)
+ *   (rldx/inference/memory/engine/kernels/fused_memory_attention.py:220-264)
+ *   behind mem::fused_attention (.../memory/engine/ops/op_fused_memory_attention.py:12-36).
+ */
+hipError_t rldx_memory_attention_bf16(const void* qkv, const void* cos, const void* signed_sin, void* out,
+                                      int64_t tokens, int64_t num_heads, int64_t head_dim, int64_t block_attn_size,
+                                      hipStream_t stream);
+
 /* Workspace bytes rldx_vision_attention_bf16 needs; -1 for an unsupported head_dim. */
 int64_t rldx_vision_attention_workspace_bytes(int64_t total_tokens, int64_t num_seqs, int64_t num_heads,
                                               int64_t head_dim);

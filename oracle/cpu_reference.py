@@ -160,6 +160,59 @@ def vision_attention_eager(qkv: torch.Tensor, rope_cos: torch.Tensor, rope_sin: 
 
 
 # ---------------------------------------------------------------------------
+# TransformerMemory attention (block-causal)
+# ---------------------------------------------------------------------------
+def memory_rope(x: torch.Tensor, cos: torch.Tensor, signed_sin: torch.Tensor) -> torch.Tensor:
+    """bf16 rotate-half RoPE of the memory module, every step rounded to bf16 as the
+    eager apply_rotary_pos_emb does on bf16 tensors (memory.py:45-57;
+    fused_memory_attention.py:84-108, :124-138): x [M, H, D] bf16, cos / signed_sin
+    [M, D] bf16 with rotate_half's sign folded into the first half of signed_sin
+    (fused_memory_attention.py:185-195):
+        y[d] = bf16(bf16(x[d] * cos[d]) + bf16(x[d +- D/2] * signed_sin[d]))."""
+    D = x.shape[-1]
+    half = D // 2
+    rot = torch.cat([torch.arange(half, D), torch.arange(0, half)])
+    c = cos.to(torch.bfloat16)[:, None, :]
+    sn = signed_sin.to(torch.bfloat16)[:, None, :]
+    return x * c + x[..., rot] * sn
+
+
+def memory_attention(qkv: torch.Tensor, cos: torch.Tensor, signed_sin: torch.Tensor, num_heads: int, head_dim: int,
+                     block_attn_size: int) -> torch.Tensor:
+    """mem::fused_attention (op_fused_memory_attention.py:12-36; kernel
+    fused_memory_attention.py:35-173): qkv [M, 3 H D] bf16 (Q | K | V, head h at
+    h D), bf16 RoPE on Q and K (memory_rope), then softmax(Q K^T / sqrt(D)) V with
+    the block-causal mask: query i sees key j iff j // B <= i // B
+    (memory.py:214-226).  fp32 scores and softmax, P rounded to bf16 for P.V, fp32
+    sums, output rounded to bf16.  Returns [M, H D]."""
+    M = qkv.shape[0]
+    H, D, B = num_heads, head_dim, block_attn_size
+    q, k, v = qkv.reshape(M, 3, H, D).unbind(1)
+    qr = memory_rope(q, cos, signed_sin).float().transpose(0, 1)  # [H, M, D]
+    kr = memory_rope(k, cos, signed_sin).float().transpose(0, 1)
+    vs = v.float().transpose(0, 1)
+    idx = torch.arange(M)
+    visible = (idx[None, :] // B) <= (idx[:, None] // B)
+    sc = torch.matmul(qr, kr.transpose(1, 2)) * (1.0 / math.sqrt(D))
+    sc = sc.masked_fill(~visible, float("-inf"))
+    m = sc.amax(dim=-1, keepdim=True)
+    pe = torch.exp(sc - m)
+    l = pe.sum(dim=-1, keepdim=True)
+    o = torch.matmul(pe.to(torch.bfloat16).float(), vs) / l
+    return o.transpose(0, 1).to(torch.bfloat16).reshape(M, H * D)
+
+
+def memory_block_mask(M: int, block_attn_size: int) -> torch.Tensor:
+    """_make_causal_mask(..., use_causal_attn=False) (memory.py:214-226): [M, M]
+    additive bf16 mask, 0 where key j is visible to query i, finfo.min elsewhere."""
+    mask = torch.full((M, M), torch.finfo(torch.bfloat16).min)
+    for i in range(0, M, block_attn_size):
+        end = min(i + block_attn_size, M)
+        mask[i:end, :end] = 0
+    return mask.to(torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------
 # MSAT pieces
 # ---------------------------------------------------------------------------
 def msat_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:

@@ -703,6 +703,205 @@ __global__ __launch_bounds__(256) void vit_pack_kernel(VitArgs v) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// TransformerMemory attention (mem::fused_attention): bf16 rotate-half RoPE on
+// Q and K + softmax(Q K^T / sqrt(D)) V with the block-causal mask
+// (query i sees key j iff j / B <= i / B), fused QKV rows [M, 3 H D].
+// The problem is tiny (M = 4 timesteps x 16 cognition tokens, 16 heads x 256)
+// and latency-bound, so a workgroup (32 queries of one head, 4 waves) stages
+// its RoPE'd Q, then chunks of 64 RoPE'd keys and the transposed V chunk in
+// LDS; every wave computes the full score tile S^T = K Q^T (lane = query
+// column) and its own d-blocks of O^T = V^T P^T, so no cross-wave merge is
+// needed.  Online softmax in the exp2 domain across key tiles.
+// RoPE (fused_memory_attention.py:84-108, :124-138; memory.py:52-57), every
+// step rounded to bf16:  y = bf16(bf16(x * cos) + bf16(x[d +- D/2] * signed_sin)).
+// ---------------------------------------------------------------------------
+struct MemArgs {
+  const uint16_t* qkv;         // [M, 3 * heads * D]
+  const uint16_t* cos;         // [M, D] bf16
+  const uint16_t* signed_sin;  // [M, D] bf16, first half negated
+  uint16_t* out;               // [M, heads * D]
+  int m, heads;
+  int64_t block;               // block_attn_size >= 1
+  float scale_log2;            // log2(e) / sqrt(D)
+};
+
+__device__ __forceinline__ uint32_t mem_rope_bf16x2(uint32_t x, uint32_t p, uint32_t c, uint32_t s) {
+#pragma clang fp contract(off)
+  const uint32_t t = pack_bf16x2(bf16x2_lo(x) * bf16x2_lo(c), bf16x2_hi(x) * bf16x2_hi(c));
+  const uint32_t u = pack_bf16x2(bf16x2_lo(p) * bf16x2_lo(s), bf16x2_hi(p) * bf16x2_hi(s));
+  return pack_bf16x2(bf16x2_lo(t) + bf16x2_lo(u), bf16x2_hi(t) + bf16x2_hi(u));
+}
+
+// RoPE'd 8-column chunk c8 of row `row` of the head's Q (col0 = h D) or K
+// (col0 = (H + h) D) columns.
+template <int D>
+__device__ __forceinline__ u32x4 mem_rope_chunk(const MemArgs& a, int64_t row, int64_t col0, int c8) {
+  constexpr int HALF8 = D / 16;  // rotate-half partner: 8-column chunks are D/16 apart
+  const int64_t ld = 3LL * a.heads * D;
+  const int pc = c8 < HALF8 ? c8 + HALF8 : c8 - HALF8;
+  const uint16_t* r = a.qkv + row * ld + col0;
+  const u32x4 x = *reinterpret_cast<const u32x4*>(r + 8 * c8);
+  const u32x4 p = *reinterpret_cast<const u32x4*>(r + 8 * pc);
+  const u32x4 c = *reinterpret_cast<const u32x4*>(a.cos + row * D + 8 * c8);
+  const u32x4 sn = *reinterpret_cast<const u32x4*>(a.signed_sin + row * D + 8 * c8);
+  u32x4 y;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) y[j] = mem_rope_bf16x2(x[j], p[j], c[j], sn[j]);
+  return y;
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void mem_attn_kernel(MemArgs a) {
+  constexpr int KSTEPS = D / 16;
+  constexpr int DBLK = D / 32;
+  constexpr int DPW = (DBLK + 3) / 4;  // d-blocks of O per wave (wave w: w, w + 4, ...)
+  constexpr int CH = D / 8;            // 8-column chunks per row
+  constexpr int QP = D + 8;            // LDS pitch of Q / K rows (elements)
+  constexpr int KC = 64;               // keys per staged chunk
+  constexpr int VP = KC + 4;           // LDS pitch of transposed V rows (elements; conflict-free b64 reads)
+  __shared__ __attribute__((aligned(16))) uint16_t qs[32 * QP];
+  __shared__ __attribute__((aligned(16))) uint16_t ks[KC * QP];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[D * VP];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, g = lane >> 5;
+  const int h = static_cast<int>(blockIdx.y);
+  const int q0 = static_cast<int>(blockIdx.x) * 32;
+  const int m = a.m;
+  const int64_t qcol = static_cast<int64_t>(h) * D, kcol = static_cast<int64_t>(a.heads + h) * D,
+                vcol = static_cast<int64_t>(2 * a.heads + h) * D;
+  const int64_t ld = 3LL * a.heads * D;
+  // keys visible to the block's last row (all rows of the block see keys below it only)
+  const int64_t q_last = min(q0 + 31, m - 1);
+  const int k_end = static_cast<int>(min<int64_t>(m, (q_last / a.block + 1) * a.block));
+  // this lane's query and its key limit: keys j < lim are visible
+  const int qi = min(q0 + l32, m - 1);
+  const int lim = static_cast<int>(min<int64_t>(m, (qi / a.block + 1) * a.block));
+
+  // ---- RoPE'd Q rows (rows past m are zero) ----
+  for (int u = tid; u < 32 * CH; u += 256) {
+    const int r = u / CH, c8 = u % CH;
+    u32x4 y{0, 0, 0, 0};
+    if (q0 + r < m) y = mem_rope_chunk<D>(a, q0 + r, qcol, c8);
+    *reinterpret_cast<u32x4*>(&qs[r * QP + 8 * c8]) = y;
+  }
+  __syncthreads();
+  bf16x8 qreg[KSTEPS];
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk)
+    qreg[kk] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&qs[l32 * QP + 16 * kk + 8 * g]));
+
+  floatx16 oacc[DPW];
+#pragma unroll
+  for (int r = 0; r < DPW; ++r) oacc[r] = floatx16{};
+  float m_run = -__builtin_inff(), l_part = 0.f;
+  const float c = a.scale_log2;
+
+  for (int c0 = 0; c0 < k_end; c0 += KC) {
+    __syncthreads();  // the previous chunk's K / V reads are done
+    // ---- K chunk, RoPE'd, row-major (rows >= k_end zero) ----
+    for (int u = tid; u < KC * CH; u += 256) {
+      const int r = u / CH, c8 = u % CH;
+      u32x4 y{0, 0, 0, 0};
+      if (c0 + r < k_end) y = mem_rope_chunk<D>(a, c0 + r, kcol, c8);
+      *reinterpret_cast<u32x4*>(&ks[r * QP + 8 * c8]) = y;
+    }
+    // ---- V chunk, transposed: vt[d][key], two keys per 32-bit LDS write ----
+    for (int u = tid; u < (KC / 2) * CH; u += 256) {
+      const int p = u % (KC / 2), c8 = u / (KC / 2);
+      const int j0 = c0 + 2 * p;
+      u32x4 v0{0, 0, 0, 0}, v1{0, 0, 0, 0};
+      if (j0 < k_end) v0 = *reinterpret_cast<const u32x4*>(a.qkv + static_cast<int64_t>(j0) * ld + vcol + 8 * c8);
+      if (j0 + 1 < k_end)
+        v1 = *reinterpret_cast<const u32x4*>(a.qkv + static_cast<int64_t>(j0 + 1) * ld + vcol + 8 * c8);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t e0 = (v0[i >> 1] >> (16 * (i & 1))) & 0xffffu;
+        const uint32_t e1 = (v1[i >> 1] >> (16 * (i & 1))) & 0xffffu;
+        *reinterpret_cast<uint32_t*>(&vt[(8 * c8 + i) * VP + 2 * p]) = e0 | (e1 << 16);
+      }
+    }
+    __syncthreads();
+    const int ntile = min(KC, k_end - c0 + 31) / 32;  // tiles of this chunk holding keys < k_end
+    for (int t = 0; t < ntile; ++t) {
+      // ---- S^T = K Q^T ----
+      floatx16 sacc = floatx16{};
+#pragma unroll
+      for (int kk = 0; kk < KSTEPS; ++kk) {
+        const u32x4 kop = *reinterpret_cast<const u32x4*>(&ks[(32 * t + l32) * QP + 16 * kk + 8 * g]);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kop), qreg[kk], sacc, 0, 0, 0);
+      }
+      // ---- online softmax (log2 domain); lane = query l32, keys 8 (e/4) + 4 g + e%4 of the tile ----
+      const int kb = c0 + 32 * t + 4 * g;
+      float mt = -__builtin_inff();
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int key = kb + 8 * (e >> 2) + (e & 3);
+        const float sv = key < lim ? sacc[e] * c : -__builtin_inff();
+        sacc[e] = sv;
+        mt = fmaxf(mt, sv);
+      }
+      const float m_new = fmaxf(m_run, pair_max(mt));  // finite: key 0 of tile 0 is visible to every row
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_part *= alpha;
+#pragma unroll
+      for (int r = 0; r < DPW; ++r) oacc[r] *= alpha;
+      float psum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float pe = __builtin_amdgcn_exp2f(sacc[e] - m_new);
+        sacc[e] = pe;
+        psum += pe;
+      }
+      l_part += psum;
+      // ---- O^T += V^T P^T over this wave's d-blocks ----
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        floatx8 pv;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] = sacc[s2 * 8 + e];
+        const bf16x8 pop = __builtin_convertvector(pv, bf16x8);
+#pragma unroll
+        for (int r = 0; r < DPW; ++r) {
+          const int db = wave + 4 * r;
+          if (db < DBLK) {
+            // keys 16 s2 + 8 (i / 4) + 4 g + i % 4 of the tile for element i: two runs of 4
+            const uint16_t* vrow = &vt[(32 * db + l32) * VP + 32 * t + 16 * s2 + 4 * g];
+            const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+            const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
+            const u32x4 vop{lo.x, lo.y, hi.x, hi.y};
+            oacc[r] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vop), pop, oacc[r], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+
+  // ---- normalise and store this wave's columns of the 32 rows ----
+  const float l = pair_sum(l_part);
+  const float inv = 1.0f / l;
+  if (q0 + l32 < m) {
+    uint16_t* orow = a.out + static_cast<int64_t>(q0 + l32) * a.heads * D + qcol;
+#pragma unroll
+    for (int r = 0; r < DPW; ++r) {
+      const int db = wave + 4 * r;
+      if (db >= DBLK) break;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = db * 32 + q4 * 8 + g * 4;
+        uint2 wv;
+        wv.x = pack_bf16x2(oacc[r][q4 * 4] * inv, oacc[r][q4 * 4 + 1] * inv);
+        wv.y = pack_bf16x2(oacc[r][q4 * 4 + 2] * inv, oacc[r][q4 * 4 + 3] * inv);
+        *reinterpret_cast<uint2*>(orow + d) = wv;
+      }
+    }
+  }
+}
+
 // head_dim -> padded K/V tile width (a multiple of 32 the attention kernel is
 // built for), 0 when unsupported
 constexpr int vit_padded_dim(int64_t hd) {
@@ -1012,4 +1211,32 @@ extern "C" hipError_t rldx_vision_attention_bf16(const void* qkv, const float* r
   if (dp == 64) return launch_vit<64>(v, a, slots, stream);
   if (dp == 96) return launch_vit<96>(v, a, slots, stream);
   return launch_vit<128>(v, a, slots, stream);
+}
+
+extern "C" hipError_t rldx_memory_attention_bf16(const void* qkv, const void* cos, const void* signed_sin, void* out,
+                                                 int64_t tokens, int64_t num_heads, int64_t head_dim,
+                                                 int64_t block_attn_size, hipStream_t stream) {
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return hipErrorInvalidValue;
+  if (tokens < 0 || num_heads <= 0 || block_attn_size <= 0) return hipErrorInvalidValue;
+  if (tokens == 0) return hipSuccess;
+  if (!qkv || !cos || !signed_sin || !out) return hipErrorInvalidValue;
+  if (!a16(qkv) || !a16(cos) || !a16(signed_sin) || reinterpret_cast<uintptr_t>(out) % 8) return hipErrorInvalidValue;
+  if (tokens > (1 << 24) || num_heads > 65535) return hipErrorInvalidValue;
+  MemArgs a{};
+  a.qkv = static_cast<const uint16_t*>(qkv);
+  a.cos = static_cast<const uint16_t*>(cos);
+  a.signed_sin = static_cast<const uint16_t*>(signed_sin);
+  a.out = static_cast<uint16_t*>(out);
+  a.m = static_cast<int>(tokens);
+  a.heads = static_cast<int>(num_heads);
+  a.block = block_attn_size;
+  a.scale_log2 = kLog2e / __builtin_sqrtf(static_cast<float>(head_dim));
+  const dim3 grid(static_cast<unsigned>((tokens + 31) / 32), static_cast<unsigned>(num_heads));
+  if (head_dim == 64)
+    hipLaunchKernelGGL(mem_attn_kernel<64>, grid, dim3(256), 0, stream, a);
+  else if (head_dim == 128)
+    hipLaunchKernelGGL(mem_attn_kernel<128>, grid, dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL(mem_attn_kernel<256>, grid, dim3(256), 0, stream, a);
+  return hipGetLastError();
 }

@@ -86,6 +86,7 @@ SIGNATURES = {
         c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_f32, c_vp, c_i64, c_vp]
     ),
     "rldx_vision_attention_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64]),
+    "rldx_memory_attention_bf16": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp]),
     "rldx_gemm_pack_weight_bf16": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_i32, c_vp, c_vp]),
     "rldx_act_packed_elems": (c_i64, [c_i64, c_i64]),
     "rldx_act_pack_bf16": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp]),

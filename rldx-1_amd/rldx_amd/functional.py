@@ -456,6 +456,29 @@ def vision_attention(qkv: torch.Tensor, rope_cos: torch.Tensor, rope_sin: torch.
     return out
 
 
+def memory_attention(qkv: torch.Tensor, cos: torch.Tensor, signed_sin: torch.Tensor, num_heads: int,
+                     head_dim: int, block_attn_size: int, *, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Fused QKV (M, 3*H*D) bf16 -> (M, H*D) bf16: bf16 rotate-half RoPE on Q and K
+    (cos / signed_sin (M, D) bf16), then block-causal attention (query i sees key j
+    iff j // block_attn_size <= i // block_attn_size); mem::fused_attention semantics."""
+    _on_gpu(qkv, cos, signed_sin, out)
+    H, D = int(num_heads), int(head_dim)
+    _require(D in (64, 128, 256), f"memory attention: head_dim {D} not in (64, 128, 256)")
+    _require(int(block_attn_size) >= 1, "block_attn_size must be >= 1")
+    _require(qkv.dtype == BF16 and qkv.dim() == 2 and qkv.is_contiguous() and qkv.shape[1] == 3 * H * D,
+             f"qkv must be contiguous bf16 (M, 3*H*D = {3 * H * D})")
+    M = qkv.shape[0]
+    for t, n in ((cos, "cos"), (signed_sin, "signed_sin")):
+        _require(t.dtype == BF16 and t.is_contiguous() and t.shape == (M, D), f"{n} must be contiguous bf16 (M, D)")
+    if out is None:
+        out = torch.empty((M, H * D), dtype=BF16, device=qkv.device)
+    _require(out.dtype == BF16 and out.shape == (M, H * D) and out.is_contiguous(), "out must be contiguous bf16 (M, H*D)")
+    _lib.check(_lib.load().rldx_memory_attention_bf16(qkv.data_ptr(), cos.data_ptr(), signed_sin.data_ptr(),
+                                                      out.data_ptr(), M, H, D, int(block_attn_size), _stream_ptr(qkv)),
+               "rldx_memory_attention_bf16")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # grouped GEMM (MSAT block linears)
 # ---------------------------------------------------------------------------

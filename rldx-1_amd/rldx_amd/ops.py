@@ -6,14 +6,15 @@ Importing this module registers, backed by the gfx950 kernels of librldx_amd.so:
   ds::grouped_res_ln         ds::vl_epilogue_ln
   ss::fused_attention_2way   ss::fused_attention_3way   ss::fused_mlp_swiglu
   ss::fused_epilogue_ln
-  rldx_backbone::fused_attention   rldx_backbone::vision_attention
+  rldx_backbone::fused_attention   rldx_backbone::vision_attention   mem::fused_attention
   rldx_backbone::fused_epilogue_add2_rmsnorm   rldx_backbone::fused_epilogue_add3_rmsnorm
   rldx_amd::swiglu           (the eager `F.silu(x1) * x2` the chains inline)
 
 Argument order and defaults follow the reference registrations
 (rldx/inference/action_model/{double,single}_stream/engine/ops/*.py,
 rldx/inference/backbone/llm/engine/ops/op_fused_llm_attention.py,
-rldx/inference/backbone/vision_encoder/engine/ops/op_fused_vision_attention.py).  Additive,
+rldx/inference/backbone/vision_encoder/engine/ops/op_fused_vision_attention.py,
+rldx/inference/memory/engine/ops/op_fused_memory_attention.py).  Additive,
 optional keyword arguments: `num_heads` / `head_dim` (the reference hard-codes
 24 x 64), `num_kv_heads` for the backbone op (reference: 32 / 8 / 128 with a
 fixed 4096-wide output), and `kv_mask` on the 3-way ops (1 = visible key,
@@ -293,6 +294,27 @@ def rldx_backbone_vision_attention(
 
 @rldx_backbone_vision_attention.register_fake
 def _(qkv, rope_cos, rope_sin, cu_seqlens, scaling, num_heads, head_dim):
+    return qkv.new_empty((qkv.shape[0], num_heads * head_dim))
+
+
+@torch.library.custom_op("mem::fused_attention", mutates_args=())
+def mem_fused_attention(
+    qkv: torch.Tensor,
+    cos: torch.Tensor,
+    signed_sin: torch.Tensor,
+    num_heads: int,
+    head_dim: int,
+    block_attn_size: int,
+) -> torch.Tensor:
+    """bf16 RoPE + block-causal attention of the TransformerMemory layers on a
+    fused (M, 3*H*D) QKV buffer -> (M, H*D).
+
+    Reference: memory/engine/ops/op_fused_memory_attention.py:12-36."""
+    return Fn.memory_attention(qkv, cos, signed_sin, num_heads, head_dim, block_attn_size)
+
+
+@mem_fused_attention.register_fake
+def _(qkv, cos, signed_sin, num_heads, head_dim, block_attn_size):
     return qkv.new_empty((qkv.shape[0], num_heads * head_dim))
 
 

@@ -253,6 +253,54 @@ def vit_attention_flops(cfg: VitAttnCfg = VitAttnCfg()) -> int:
     return 4 * cfg.heads * cfg.head_dim * sum(n * n for n in cfg.seq_lengths)
 
 
+# ---------------------------------------------------------------------------
+# TransformerMemory block-causal attention: memory_length timesteps x
+# n_cog cognition tokens, 16 heads x 256 (Qwen3-VL-8B text width 4096)
+# ---------------------------------------------------------------------------
+@dataclass
+class MemAttnCfg:
+    memory_length: int = 4
+    n_cog: int = 16  # block_attn_size
+    heads: int = 16
+    head_dim: int = 256
+    theta: float = 10000.0
+    seed: int = 7
+
+    @property
+    def tokens(self) -> int:
+        return self.memory_length * self.n_cog
+
+
+def memory_rope_tables(cfg: MemAttnCfg):
+    """cos / signed_sin [M, D] bf16: RotaryEmbedding(head_dim) at the block-wise
+    positions arange(M) // block_attn_size (memory.py:21-42, :327-334), cast to
+    bf16, sin's first half negated (prepare_rope_buffers / prepare_signed_sin,
+    fused_memory_attention.py:185-217)."""
+    D = cfg.head_dim
+    inv_freq = 1.0 / (cfg.theta ** (torch.arange(0, D, 2).float() / D))
+    pos = (torch.arange(cfg.tokens) // cfg.n_cog).float()
+    freqs = torch.outer(pos, inv_freq)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    cos, sin = emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+    return cos.contiguous(), signed_sin(sin)
+
+
+def memory_attention_inputs(cfg: MemAttnCfg = MemAttnCfg()):
+    """Fused QKV (M, 3 * H * D) bf16 ~ N(0, 1) and the bf16 rope tables."""
+    g = torch.Generator().manual_seed(cfg.seed)
+    qkv = torch.randn(cfg.tokens, 3 * cfg.heads * cfg.head_dim, generator=g).to(torch.bfloat16)
+    cos, ssin = memory_rope_tables(cfg)
+    return dict(qkv=qkv, cos=cos, signed_sin=ssin, num_heads=cfg.heads, head_dim=cfg.head_dim,
+                block_attn_size=cfg.n_cog)
+
+
+def memory_attention_flops(cfg: MemAttnCfg = MemAttnCfg()) -> int:
+    """Q K^T and P V over the visible (query, key) pairs of the block-causal mask."""
+    M, B = cfg.tokens, cfg.n_cog
+    pairs = sum(min(M, (i // B + 1) * B) for i in range(M))
+    return 4 * cfg.heads * cfg.head_dim * pairs
+
+
 def signed_sin(sin: torch.Tensor) -> torch.Tensor:
     """prepare_signed_sin (fused_llm_attention.py:787-796): first half negated."""
     D = sin.shape[-1]

@@ -210,6 +210,24 @@ def test_vision_attention_workspace_and_rejections():
     assert call(M=0, qkv=None, out=None) == 0          # nothing to do
 
 
+def test_memory_attention_rejections():
+    lib = _lib.load()
+
+    def call(qkv=256, cos=512, ssin=768, out=1024, M=64, H=16, D=256, B=16):
+        return lib.rldx_memory_attention_bf16(qkv, cos, ssin, out, M, H, D, B, None)
+
+    assert call(D=96) == HIP_INVALID_VALUE      # head_dim not 64 / 128 / 256
+    assert call(D=512) == HIP_INVALID_VALUE
+    assert call(B=0) == HIP_INVALID_VALUE       # block_attn_size >= 1
+    assert call(H=0) == HIP_INVALID_VALUE
+    assert call(M=-1) == HIP_INVALID_VALUE
+    assert call(qkv=None) == HIP_INVALID_VALUE
+    assert call(cos=520) == HIP_INVALID_VALUE   # 16-byte alignment
+    assert call(out=1026) == HIP_INVALID_VALUE  # 8-byte alignment
+    assert call(M=(1 << 24) + 1) == HIP_INVALID_VALUE
+    assert call(M=0, qkv=None, out=None) == 0
+
+
 def test_zero_sized_calls_are_noops():
     lib = _lib.load()
     st = _lib.i64_array([0, 0, 0])

@@ -422,6 +422,90 @@ def test_vision_attention_close_to_the_eager_path():
 
 
 # ---------------------------------------------------------------------------
+# TransformerMemory block-causal attention (memory.py; fused_memory_attention.py)
+# ---------------------------------------------------------------------------
+def _mem(T=3, n_cog=8, heads=2, head_dim=64, seed=13):
+    cfg = W.MemAttnCfg(memory_length=T, n_cog=n_cog, heads=heads, head_dim=head_dim, seed=seed)
+    return cfg, W.memory_attention_inputs(cfg)
+
+
+def test_memory_rope_equals_eager_apply_rotary_bitwise():
+    """signed_sin * partner == rotate_half(x) * sin in bf16, step by step
+    (apply_rotary_pos_emb on bf16 tensors, memory.py:52-57)."""
+    cfg, inp = _mem(heads=3)
+    M, H, D = cfg.tokens, 3, 64
+    x = inp["qkv"][:, : H * D].reshape(M, H, D)
+    sin = inp["signed_sin"].clone()
+    sin[:, : D // 2] = -sin[:, : D // 2]
+    c, sn = inp["cos"][:, None], sin[:, None]
+    eager = (x * c) + (ref.rotate_half(x) * sn)
+    got = ref.memory_rope(x, inp["cos"], inp["signed_sin"])
+    assert got.dtype == torch.bfloat16
+    assert torch.equal(got.view(torch.int16), eager.view(torch.int16))
+    # three bf16 roundings, not one fp32 rope rounded once
+    once = (x.float() * c.float() + ref.rotate_half(x.float()) * sn.float()).to(torch.bfloat16)
+    assert not torch.equal(got.view(torch.int16), once.view(torch.int16))
+
+
+def test_memory_rope_tables_closed_form():
+    cfg = W.MemAttnCfg(memory_length=4, n_cog=16, heads=1, head_dim=256)
+    cos, ssin = W.memory_rope_tables(cfg)
+    assert cos.dtype == ssin.dtype == torch.bfloat16 and cos.shape == (64, 256)
+    for i in (0, 15, 16, 40, 63):
+        p = i // 16
+        for j in (0, 5, 127, 128, 200, 255):
+            f = 1.0 / 10000 ** ((2 * (j % 128)) / 256)
+            assert abs(cos[i, j].item() - math.cos(p * f)) <= 4e-3
+            sgn = -1.0 if j < 128 else 1.0
+            assert abs(ssin[i, j].item() - sgn * math.sin(p * f)) <= 4e-3
+    # every token of a block shares its position: rows 16..31 identical
+    assert torch.equal(cos[16], cos[31]) and not torch.equal(cos[15], cos[16])
+
+
+def test_memory_attention_matches_fp64_brute_force_with_the_eager_mask():
+    cfg, inp = _mem(T=3, n_cog=8, heads=2, head_dim=64)
+    M, H, D = cfg.tokens, 2, 64
+    o = ref.memory_attention(**inp)
+    q, k, v = inp["qkv"].reshape(M, 3, H, D).unbind(1)
+    qr = ref.memory_rope(q, inp["cos"], inp["signed_sin"])
+    kr = ref.memory_rope(k, inp["cos"], inp["signed_sin"])
+    mask = ref.memory_block_mask(M, 8).double()
+    s = f64(qr).transpose(0, 1) @ f64(kr).transpose(0, 1).transpose(1, 2) / math.sqrt(D) + mask
+    o64 = (torch.softmax(s, dim=-1) @ f64(v).transpose(0, 1)).transpose(0, 1).reshape(M, H * D)
+    assert (o.double() - o64).abs().max() < 2e-2
+
+
+def test_memory_attention_block_structure():
+    """Rows of block b ignore keys of later blocks (bitwise) and see every key of
+    their own block, later positions included."""
+    cfg, inp = _mem(T=4, n_cog=8, heads=2, head_dim=64)
+    H, D = 2, 64
+    o = ref.memory_attention(**inp)
+    qkv2 = inp["qkv"].clone()
+    qkv2[16:, H * D:] = 5.0  # K and V of blocks 2, 3
+    o2 = ref.memory_attention(**{**inp, "qkv": qkv2})
+    assert torch.equal(o[:16].view(torch.int16), o2[:16].view(torch.int16))
+    qkv3 = inp["qkv"].clone()
+    qkv3[15, 2 * H * D:] = 9.0  # V of the last key of block 1
+    o3 = ref.memory_attention(**{**inp, "qkv": qkv3})
+    assert not torch.equal(o[8:16], o3[8:16])  # row 8 sees key 15 (same block)
+    assert torch.equal(o[:8].view(torch.int16), o3[:8].view(torch.int16))
+
+
+def test_memory_attention_block_sizes_reduce_to_causal_and_full():
+    cfg, inp = _mem(T=2, n_cog=10, heads=1, head_dim=64)
+    M, D = cfg.tokens, 64
+    q, k, v = inp["qkv"].reshape(M, 3, 1, D).unbind(1)
+    qr = ref.memory_rope(q, inp["cos"], inp["signed_sin"]).transpose(0, 1)[None]
+    kr = ref.memory_rope(k, inp["cos"], inp["signed_sin"]).transpose(0, 1)[None]
+    vv = v.transpose(0, 1)[None]
+    causal = ref.memory_attention(**{**inp, "block_attn_size": 1})
+    assert (causal.double() - brute_attention(qr, kr, vv, causal=True)[0, 0]).abs().max() < 2e-2
+    full = ref.memory_attention(**{**inp, "block_attn_size": M})
+    assert (full.double() - brute_attention(qr, kr, vv)[0, 0]).abs().max() < 2e-2
+
+
+# ---------------------------------------------------------------------------
 # LayerNorm and the MSAT step oracle
 # ---------------------------------------------------------------------------
 def test_layer_norm_closed_form():
