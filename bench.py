@@ -212,6 +212,31 @@ def kernel_lines(torch, reps: int):
                                                   peak=BF16_MFMA_PEAK_TFLOPS, frac=tf / BF16_MFMA_PEAK_TFLOPS,
                                                   flops=fl)
 
+    # ViT attention, 2 images x 196 patches, 16 heads x 72 (RoPE + K/V packing + varlen attention)
+    vc = W.VitAttnCfg()
+    vi = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in W.vit_attention_inputs(vc).items()}
+    vws = torch.empty(Fn.vision_attention_workspace_bytes(vc.tokens, vc.images, vc.heads, vc.head_dim),
+                      dtype=torch.uint8, device=dev)
+    vo = torch.empty(vc.tokens, vc.heads * vc.head_dim, dtype=torch.bfloat16, device=dev)
+    ms = graph_time_ms(lambda: Fn.vision_attention(vi["qkv"], vi["rope_cos"], vi["rope_sin"], vi["cu_seqlens"],
+                                                   vi["scaling"], vc.heads, vc.head_dim, out=vo, workspace=vws),
+                       reps, torch)
+    tf = W.vit_attention_flops(vc) / (ms * 1e-3) / 1e12
+    out["vit_attention_op_2x196_16x72"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s", bound="mfma",
+                                               peak=BF16_MFMA_PEAK_TFLOPS, frac=tf / BF16_MFMA_PEAK_TFLOPS,
+                                               flops=W.vit_attention_flops(vc))
+    # TransformerMemory attention, 4 x 16 tokens, 16 heads x 256, block-causal (block 16)
+    mc = W.MemAttnCfg()
+    mi = W.memory_attention_inputs(mc)
+    mq, mcos, msin = mi["qkv"].to(dev), mi["cos"].to(dev), mi["signed_sin"].to(dev)
+    mo = torch.empty(mc.tokens, mc.heads * mc.head_dim, dtype=torch.bfloat16, device=dev)
+    ms = graph_time_ms(lambda: Fn.memory_attention(mq, mcos, msin, mc.heads, mc.head_dim, mc.n_cog, out=mo),
+                       reps, torch)
+    tf = W.memory_attention_flops(mc) / (ms * 1e-3) / 1e12
+    out["memory_attention_op_64_16x256_block16"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s", bound="mfma",
+                                                        peak=BF16_MFMA_PEAK_TFLOPS, frac=tf / BF16_MFMA_PEAK_TFLOPS,
+                                                        flops=W.memory_attention_flops(mc))
+
     # residual-add + norm epilogues: the reference's block-boundary shapes (launch-bound)
     # and the Qwen3-VL prefill shape 1280 x 2048 (HBM-bound)
     def rows(m, d, std=1.0):

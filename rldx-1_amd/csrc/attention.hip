@@ -134,7 +134,7 @@ struct AttnArgs {
 // sequences do not overlap, and every slot is below
 // floor((rows + 31 num_seqs) / 32) whatever the cu_seqlens values are: no
 // scan of cu_seqlens is needed to place a sequence, and a slot finds its
-// sequence by a binary search over log2(num_seqs) entries.
+// sequence with one load per lane (up to 63 sequences) or a binary search.
 struct SeqSlot {
   int start, len, base;
 };
@@ -145,7 +145,20 @@ __host__ __device__ constexpr int64_t seq_slot_count(int64_t rows, int64_t num_s
 
 __device__ __forceinline__ int clamp_row(int32_t c, int rows) { return c < 0 ? 0 : (c > rows ? rows : c); }
 
+// Called with the whole wave active.
 __device__ __forceinline__ SeqSlot find_seq_slot(const int32_t* cu, int num_seqs, int rows, int slot) {
+  if (num_seqs <= 63) {
+    // one load per lane: lane s holds c_s (lanes past num_seqs repeat c_num_seqs);
+    // the sequence is the last s < num_seqs with base_s <= slot
+    const int lane = static_cast<int>(threadIdx.x & 63);
+    const int c = clamp_row(cu[min(lane, num_seqs)], rows);
+    const int64_t base = (static_cast<int64_t>(c) + 31 * static_cast<int64_t>(lane)) / 32;
+    const uint64_t cand = __ballot(lane < num_seqs && base <= slot);
+    const int s = cand ? 63 - __builtin_clzll(cand) : 0;
+    const int c0 = __builtin_amdgcn_readlane(c, s), c1 = __builtin_amdgcn_readlane(c, s + 1);
+    return SeqSlot{c0, c1 > c0 ? c1 - c0 : 0,
+                   static_cast<int>((static_cast<int64_t>(c0) + 31 * static_cast<int64_t>(s)) / 32)};
+  }
   int lo = 0, hi = num_seqs - 1;  // last s with base_s <= slot (0 when there is none)
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
@@ -639,6 +652,7 @@ template <int DP>
 __global__ __launch_bounds__(256) void vit_pack_kernel(VitArgs v) {
   constexpr int PITCH = DP + 8;  // 16-byte aligned LDS rows
   constexpr int G = DP / 4;      // 4-column groups per padded row
+  static_assert((32 * G) % 256 == 0, "whole groups per thread");
   constexpr int NCH = DP / 16;   // 1 KB chunks per K / V part
   __shared__ __attribute__((aligned(16))) uint16_t tq[32 * PITCH];
   __shared__ __attribute__((aligned(16))) uint16_t tk[32 * PITCH];
@@ -654,25 +668,38 @@ __global__ __launch_bounds__(256) void vit_pack_kernel(VitArgs v) {
   const uint16_t* qsrc = v.qkv + static_cast<int64_t>(h) * hd;
   const uint16_t* ksrc = qsrc + static_cast<int64_t>(v.heads) * hd;
   const uint16_t* vsrc = ksrc + static_cast<int64_t>(v.heads) * hd;
-  // rows r0 .. r0 + nrows - 1 < rows and columns < hd: every read is inside
-  // qkv / cos / sin (4-column groups never straddle hd or hd / 2: hd % 8 == 0)
-  for (int u = threadIdx.x; u < 32 * G; u += 256) {
+  // Every read uses a row clamped into the sequence's rows of the tile and a
+  // column group clamped below hd (so the unrolled loads are unconditional and
+  // issue back to back); groups outside are replaced by zeros afterwards.
+  // 4-column groups never straddle hd or hd / 2 (hd % 8 == 0).
+  constexpr int NU = 32 * G / 256;  // groups per thread
+  uint2 xq[NU], pq[NU], xk[NU], pk[NU], xv[NU];
+  floatx4 cs[NU], sn[NU];
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    const int u = threadIdx.x + 256 * i;
+    const int64_t row = r0 + min(u / G, nrows - 1);
+    const int d4 = min((u % G) * 4, hd - 4);
+    const int pd = d4 < half ? d4 + half : d4 - half;
+    const uint16_t* qr = qsrc + row * qkv_ss;
+    const uint16_t* kr = ksrc + row * qkv_ss;
+    xq[i] = *reinterpret_cast<const uint2*>(qr + d4);
+    pq[i] = *reinterpret_cast<const uint2*>(qr + pd);
+    xk[i] = *reinterpret_cast<const uint2*>(kr + d4);
+    pk[i] = *reinterpret_cast<const uint2*>(kr + pd);
+    xv[i] = *reinterpret_cast<const uint2*>(vsrc + row * qkv_ss + d4);
+    cs[i] = *reinterpret_cast<const floatx4*>(v.cos + row * hd + d4);
+    sn[i] = *reinterpret_cast<const floatx4*>(v.sin + row * hd + d4);
+  }
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    const int u = threadIdx.x + 256 * i;
     const int r = u / G, d4 = (u % G) * 4;
-    uint2 oq{0, 0}, ok{0, 0}, ov{0, 0};
-    if (r < nrows && d4 < hd) {
-      const int64_t row = r0 + r;
-      const int pd = d4 < half ? d4 + half : d4 - half;
-      const uint16_t* qr = qsrc + row * qkv_ss;
-      const uint16_t* kr = ksrc + row * qkv_ss;
-      const floatx4 c = *reinterpret_cast<const floatx4*>(v.cos + row * hd + d4);
-      const floatx4 sn = *reinterpret_cast<const floatx4*>(v.sin + row * hd + d4);
-      oq = vit_rope4(*reinterpret_cast<const uint2*>(qr + d4), *reinterpret_cast<const uint2*>(qr + pd), c, sn);
-      ok = vit_rope4(*reinterpret_cast<const uint2*>(kr + d4), *reinterpret_cast<const uint2*>(kr + pd), c, sn);
-      ov = *reinterpret_cast<const uint2*>(vsrc + row * qkv_ss + d4);
-    }
-    *reinterpret_cast<uint2*>(&tq[r * PITCH + d4]) = oq;
-    *reinterpret_cast<uint2*>(&tk[r * PITCH + d4]) = ok;
-    *reinterpret_cast<uint2*>(&tv[r * PITCH + d4]) = ov;
+    const bool in = r < nrows && d4 < hd;
+    const uint2 z{0, 0};
+    *reinterpret_cast<uint2*>(&tq[r * PITCH + d4]) = in ? vit_rope4(xq[i], pq[i], cs[i], sn[i]) : z;
+    *reinterpret_cast<uint2*>(&tk[r * PITCH + d4]) = in ? vit_rope4(xk[i], pk[i], cs[i], sn[i]) : z;
+    *reinterpret_cast<uint2*>(&tv[r * PITCH + d4]) = in ? xv[i] : z;
   }
   __syncthreads();
   // Q rows of the sequence -> qpad (DP columns, the padding included)
@@ -708,11 +735,12 @@ __global__ __launch_bounds__(256) void vit_pack_kernel(VitArgs v) {
 // Q and K + softmax(Q K^T / sqrt(D)) V with the block-causal mask
 // (query i sees key j iff j / B <= i / B), fused QKV rows [M, 3 H D].
 // The problem is tiny (M = 4 timesteps x 16 cognition tokens, 16 heads x 256)
-// and latency-bound, so a workgroup (32 queries of one head, 4 waves) stages
+// and latency-bound, so a workgroup (32 queries of one head, 8 waves) stages
 // its RoPE'd Q, then chunks of 64 RoPE'd keys and the transposed V chunk in
-// LDS; every wave computes the full score tile S^T = K Q^T (lane = query
-// column) and its own d-blocks of O^T = V^T P^T, so no cross-wave merge is
-// needed.  Online softmax in the exp2 domain across key tiles.
+// LDS, each thread issuing all of its loads before the first use; every wave
+// computes the full score tile S^T = K Q^T (lane = query column) and its own
+// d-blocks of O^T = V^T P^T, so no cross-wave merge is needed.  Online softmax
+// in the exp2 domain across key tiles.
 // RoPE (fused_memory_attention.py:84-108, :124-138; memory.py:52-57), every
 // step rounded to bf16:  y = bf16(bf16(x * cos) + bf16(x[d +- D/2] * signed_sin)).
 // ---------------------------------------------------------------------------
@@ -733,33 +761,49 @@ __device__ __forceinline__ uint32_t mem_rope_bf16x2(uint32_t x, uint32_t p, uint
   return pack_bf16x2(bf16x2_lo(t) + bf16x2_lo(u), bf16x2_hi(t) + bf16x2_hi(u));
 }
 
-// RoPE'd 8-column chunk c8 of row `row` of the head's Q (col0 = h D) or K
-// (col0 = (H + h) D) columns.
+// Operands of the RoPE of one 8-column chunk (self, rotate-half partner, cos,
+// signed sin), loaded together so that a thread's loads are all in flight
+// before the first use.
+struct RopeIn {
+  u32x4 x, p, c, s;
+};
+
+// Chunk c8 of row `row` of the head's Q (col0 = h D) or K (col0 = (H + h) D) columns.
 template <int D>
-__device__ __forceinline__ u32x4 mem_rope_chunk(const MemArgs& a, int64_t row, int64_t col0, int c8) {
+__device__ __forceinline__ RopeIn mem_rope_load(const MemArgs& a, int64_t row, int64_t col0, int c8) {
   constexpr int HALF8 = D / 16;  // rotate-half partner: 8-column chunks are D/16 apart
   const int64_t ld = 3LL * a.heads * D;
   const int pc = c8 < HALF8 ? c8 + HALF8 : c8 - HALF8;
   const uint16_t* r = a.qkv + row * ld + col0;
-  const u32x4 x = *reinterpret_cast<const u32x4*>(r + 8 * c8);
-  const u32x4 p = *reinterpret_cast<const u32x4*>(r + 8 * pc);
-  const u32x4 c = *reinterpret_cast<const u32x4*>(a.cos + row * D + 8 * c8);
-  const u32x4 sn = *reinterpret_cast<const u32x4*>(a.signed_sin + row * D + 8 * c8);
+  RopeIn in;
+  in.x = *reinterpret_cast<const u32x4*>(r + 8 * c8);
+  in.p = *reinterpret_cast<const u32x4*>(r + 8 * pc);
+  in.c = *reinterpret_cast<const u32x4*>(a.cos + row * D + 8 * c8);
+  in.s = *reinterpret_cast<const u32x4*>(a.signed_sin + row * D + 8 * c8);
+  return in;
+}
+
+__device__ __forceinline__ u32x4 mem_rope_apply(const RopeIn& in) {
   u32x4 y;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) y[j] = mem_rope_bf16x2(x[j], p[j], c[j], sn[j]);
+  for (int j = 0; j < 4; ++j) y[j] = mem_rope_bf16x2(in.x[j], in.p[j], in.c[j], in.s[j]);
   return y;
 }
 
 template <int D>
-__global__ __launch_bounds__(256) void mem_attn_kernel(MemArgs a) {
+__global__ __launch_bounds__(512) void mem_attn_kernel(MemArgs a) {
+  constexpr int NT = 512;              // 8 waves
+  constexpr int NW = NT / 64;
   constexpr int KSTEPS = D / 16;
   constexpr int DBLK = D / 32;
-  constexpr int DPW = (DBLK + 3) / 4;  // d-blocks of O per wave (wave w: w, w + 4, ...)
+  constexpr int DPW = (DBLK + NW - 1) / NW;  // d-blocks of O per wave (wave w: w, w + 8, ...)
   constexpr int CH = D / 8;            // 8-column chunks per row
   constexpr int QP = D + 8;            // LDS pitch of Q / K rows (elements)
   constexpr int KC = 64;               // keys per staged chunk
   constexpr int VP = KC + 4;           // LDS pitch of transposed V rows (elements; conflict-free b64 reads)
+  constexpr int QU = (32 * CH + NT - 1) / NT;        // Q chunks per thread
+  constexpr int KU = (KC * CH + NT - 1) / NT;        // K chunks per thread
+  constexpr int VU = ((KC / 2) * CH + NT - 1) / NT;  // V key-pair chunks per thread
   __shared__ __attribute__((aligned(16))) uint16_t qs[32 * QP];
   __shared__ __attribute__((aligned(16))) uint16_t ks[KC * QP];
   __shared__ __attribute__((aligned(16))) uint16_t vt[D * VP];
@@ -781,13 +825,73 @@ __global__ __launch_bounds__(256) void mem_attn_kernel(MemArgs a) {
   const int qi = min(q0 + l32, m - 1);
   const int lim = static_cast<int>(min<int64_t>(m, (qi / a.block + 1) * a.block));
 
-  // ---- RoPE'd Q rows (rows past m are zero) ----
-  for (int u = tid; u < 32 * CH; u += 256) {
-    const int r = u / CH, c8 = u % CH;
-    u32x4 y{0, 0, 0, 0};
-    if (q0 + r < m) y = mem_rope_chunk<D>(a, q0 + r, qcol, c8);
-    *reinterpret_cast<u32x4*>(&qs[r * QP + 8 * c8]) = y;
+  // Staging.  Every global load reads a row clamped into [0, limit) (so it is
+  // unconditional and the unrolled loads issue back to back); rows past the
+  // limit are replaced by zeros afterwards.
+  RopeIn qin[QU];
+#pragma unroll
+  for (int i = 0; i < QU; ++i) {
+    const int u = min(tid + NT * i, 32 * CH - 1);
+    qin[i] = mem_rope_load<D>(a, min(q0 + u / CH, m - 1), qcol, u % CH);
   }
+  RopeIn kin[KU];
+  u32x4 va[VU], vb[VU];
+  auto load_kv = [&](int c0) {
+#pragma unroll
+    for (int i = 0; i < KU; ++i) {
+      const int u = min(tid + NT * i, KC * CH - 1);
+      kin[i] = mem_rope_load<D>(a, min(c0 + u / CH, k_end - 1), kcol, u % CH);
+    }
+#pragma unroll
+    for (int i = 0; i < VU; ++i) {
+      const int u = min(tid + NT * i, (KC / 2) * CH - 1);
+      const int j0 = c0 + 2 * (u % (KC / 2)), c8 = u / (KC / 2);
+      va[i] = *reinterpret_cast<const u32x4*>(a.qkv + static_cast<int64_t>(min(j0, k_end - 1)) * ld + vcol + 8 * c8);
+      vb[i] = *reinterpret_cast<const u32x4*>(a.qkv + static_cast<int64_t>(min(j0 + 1, k_end - 1)) * ld + vcol +
+                                              8 * c8);
+    }
+  };
+  auto store_kv = [&](int c0) {
+    // K chunk, RoPE'd, row-major (rows >= k_end zero)
+#pragma unroll
+    for (int i = 0; i < KU; ++i) {
+      const int u = tid + NT * i;
+      if (u < KC * CH) {
+        const int r = u / CH, c8 = u % CH;
+        const u32x4 y = c0 + r < k_end ? mem_rope_apply(kin[i]) : u32x4{0, 0, 0, 0};
+        *reinterpret_cast<u32x4*>(&ks[r * QP + 8 * c8]) = y;
+      }
+    }
+    // V chunk, transposed: vt[d][key], two keys per 32-bit LDS write (keys >= k_end zero)
+#pragma unroll
+    for (int i = 0; i < VU; ++i) {
+      const int u = tid + NT * i;
+      if (u < (KC / 2) * CH) {
+        const int p = u % (KC / 2), c8 = u / (KC / 2);
+        const int j0 = c0 + 2 * p;
+        const u32x4 v0 = j0 < k_end ? va[i] : u32x4{0, 0, 0, 0};
+        const u32x4 v1 = j0 + 1 < k_end ? vb[i] : u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t e0 = (v0[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+          const uint32_t e1 = (v1[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+          *reinterpret_cast<uint32_t*>(&vt[(8 * c8 + e) * VP + 2 * p]) = e0 | (e1 << 16);
+        }
+      }
+    }
+  };
+  load_kv(0);
+  // RoPE'd Q rows (rows past m zero)
+#pragma unroll
+  for (int i = 0; i < QU; ++i) {
+    const int u = tid + NT * i;
+    if (u < 32 * CH) {
+      const int r = u / CH, c8 = u % CH;
+      const u32x4 y = q0 + r < m ? mem_rope_apply(qin[i]) : u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&qs[r * QP + 8 * c8]) = y;
+    }
+  }
+  store_kv(0);
   __syncthreads();
   bf16x8 qreg[KSTEPS];
 #pragma unroll
@@ -801,30 +905,12 @@ __global__ __launch_bounds__(256) void mem_attn_kernel(MemArgs a) {
   const float c = a.scale_log2;
 
   for (int c0 = 0; c0 < k_end; c0 += KC) {
-    __syncthreads();  // the previous chunk's K / V reads are done
-    // ---- K chunk, RoPE'd, row-major (rows >= k_end zero) ----
-    for (int u = tid; u < KC * CH; u += 256) {
-      const int r = u / CH, c8 = u % CH;
-      u32x4 y{0, 0, 0, 0};
-      if (c0 + r < k_end) y = mem_rope_chunk<D>(a, c0 + r, kcol, c8);
-      *reinterpret_cast<u32x4*>(&ks[r * QP + 8 * c8]) = y;
+    if (c0 > 0) {  // next 64-key chunk (M > 64)
+      __syncthreads();  // the previous chunk's K / V reads are done
+      load_kv(c0);
+      store_kv(c0);
+      __syncthreads();
     }
-    // ---- V chunk, transposed: vt[d][key], two keys per 32-bit LDS write ----
-    for (int u = tid; u < (KC / 2) * CH; u += 256) {
-      const int p = u % (KC / 2), c8 = u / (KC / 2);
-      const int j0 = c0 + 2 * p;
-      u32x4 v0{0, 0, 0, 0}, v1{0, 0, 0, 0};
-      if (j0 < k_end) v0 = *reinterpret_cast<const u32x4*>(a.qkv + static_cast<int64_t>(j0) * ld + vcol + 8 * c8);
-      if (j0 + 1 < k_end)
-        v1 = *reinterpret_cast<const u32x4*>(a.qkv + static_cast<int64_t>(j0 + 1) * ld + vcol + 8 * c8);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t e0 = (v0[i >> 1] >> (16 * (i & 1))) & 0xffffu;
-        const uint32_t e1 = (v1[i >> 1] >> (16 * (i & 1))) & 0xffffu;
-        *reinterpret_cast<uint32_t*>(&vt[(8 * c8 + i) * VP + 2 * p]) = e0 | (e1 << 16);
-      }
-    }
-    __syncthreads();
     const int ntile = min(KC, k_end - c0 + 31) / 32;  // tiles of this chunk holding keys < k_end
     for (int t = 0; t < ntile; ++t) {
       // ---- S^T = K Q^T ----
@@ -867,7 +953,7 @@ __global__ __launch_bounds__(256) void mem_attn_kernel(MemArgs a) {
         const bf16x8 pop = __builtin_convertvector(pv, bf16x8);
 #pragma unroll
         for (int r = 0; r < DPW; ++r) {
-          const int db = wave + 4 * r;
+          const int db = wave + NW * r;
           if (db < DBLK) {
             // keys 16 s2 + 8 (i / 4) + 4 g + i % 4 of the tile for element i: two runs of 4
             const uint16_t* vrow = &vt[(32 * db + l32) * VP + 32 * t + 16 * s2 + 4 * g];
@@ -888,7 +974,7 @@ __global__ __launch_bounds__(256) void mem_attn_kernel(MemArgs a) {
     uint16_t* orow = a.out + static_cast<int64_t>(q0 + l32) * a.heads * D + qcol;
 #pragma unroll
     for (int r = 0; r < DPW; ++r) {
-      const int db = wave + 4 * r;
+      const int db = wave + NW * r;
       if (db >= DBLK) break;
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
@@ -1233,10 +1319,10 @@ extern "C" hipError_t rldx_memory_attention_bf16(const void* qkv, const void* co
   a.scale_log2 = kLog2e / __builtin_sqrtf(static_cast<float>(head_dim));
   const dim3 grid(static_cast<unsigned>((tokens + 31) / 32), static_cast<unsigned>(num_heads));
   if (head_dim == 64)
-    hipLaunchKernelGGL(mem_attn_kernel<64>, grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(mem_attn_kernel<64>, grid, dim3(512), 0, stream, a);
   else if (head_dim == 128)
-    hipLaunchKernelGGL(mem_attn_kernel<128>, grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(mem_attn_kernel<128>, grid, dim3(512), 0, stream, a);
   else
-    hipLaunchKernelGGL(mem_attn_kernel<256>, grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(mem_attn_kernel<256>, grid, dim3(512), 0, stream, a);
   return hipGetLastError();
 }

@@ -77,8 +77,11 @@ def test_vision_workspace_rope_and_packing_bitexact(dev, lengths, H, D):
 
 @pytest.mark.parametrize("lengths,H,D", [((1,), 1, 72), ((33, 1, 64, 95), 2, 72), ((300, 17), 3, 64),
                                          ((5, 0, 40), 2, 80), ((129,), 2, 128), ((31, 32, 33), 1, 8),
-                                         ((2, 200, 3), 2, 120), ((64,) * 8, 4, 72)])
+                                         ((2, 200, 3), 2, 120), ((64,) * 8, 4, 72),
+                                         (tuple((37 * i) % 50 for i in range(70)), 2, 72)])
 def test_vision_attention_ragged(dev, lengths, H, D):
+    """Ragged, empty and single-token sequences; 70 sequences take the
+    binary-search lookup (up to 63 use one load per lane)."""
     cfg = W.VitAttnCfg(lengths=lengths, heads=H, head_dim=D, seed=len(lengths) * 100 + D)
     inp = W.vit_attention_inputs(cfg)
     o = _run(inp, dev)
