@@ -206,10 +206,13 @@ hipError_t rldx_attention_fwd_bf16(const void* q, const void* k, const void* v, 
 /*
  * Same operator with K and V already packed (packed_strides {batch, head}),
  * one launch.  Used on the MSAT path, where rldx_msat_qkv_norm_rope_bf16 writes
- * the packed tiles directly.  out_packed != 0 (batch 1): O is written as the
+ * the packed tiles directly.  out_packed == 1 (batch 1): O is written as the
  * [seq_q, q_heads*head_dim] matrix in the packed activation order the grouped
  * GEMM reads (o_strides ignored, o 16-byte aligned, rldx_act_packed_elems
- * elements).
+ * elements); out_packed > 1 (a multiple of 16, >= q_heads*head_dim): O is
+ * written as columns [0, q_heads*head_dim) relative to `o` of a packed matrix
+ * out_packed columns wide, `o` pointing at the 16-column chunk where they start
+ * (the attention half of a concatenated GEMM operand).
  */
 hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* kv_packed, const int64_t* packed_strides,
                                           void* o, int32_t out_packed, int64_t batch, int64_t q_heads,
@@ -350,8 +353,10 @@ typedef struct rldx_gemm_group {
   const void* w_packed;  /* packed weight [n, k] of this stream                  */
   const void* bias;      /* [n] bf16 or NULL ([gate; up] order for SwiGLU)       */
   void* out;             /* [m, n] bf16 ([m, n/2] for SwiGLU), row stride ldo;   */
-                         /* packed activation order for SWIGLU_PACKED           */
-  int64_t ldo;
+                         /* packed activation order for the *_PACKED epilogues: */
+  int64_t ldo;           /* then ldo = 0 (a packed [m, n_out] matrix) or the     */
+                         /* width (% 16) of a wider packed matrix whose 16-col  */
+                         /* chunk at `out` is the first output column           */
   const void* residual;  /* [m, n] bf16, row stride ldr (RESIDUAL epilogue; may  */
   int64_t ldr;           /* alias out)                                           */
 } rldx_gemm_group_t;
@@ -360,6 +365,7 @@ typedef struct rldx_gemm_group {
 #define RLDX_GEMM_EPI_RESIDUAL 1 /* out = bf16(residual + bf16(a W^T + bias))     */
 #define RLDX_GEMM_EPI_SWIGLU 2   /* out = swiglu(bf16(gate), bf16(up)), n/2 cols  */
 #define RLDX_GEMM_EPI_SWIGLU_PACKED 3 /* same, out in the packed activation order */
+#define RLDX_GEMM_EPI_BIAS_PACKED 4   /* out = bf16(a W^T + bias), packed order     */
 
 /*
  * y_s = a_s W_s^T (+ bias_s) with the epilogue above, for 1..3 groups that

@@ -1,0 +1,131 @@
+"""CPU oracle of the RLDX-1 MSAT forward (no add-ons) — TEST INFRASTRUCTURE ONLY.
+
+Eager restatement, in CPU bf16 torch, of MSAT._forward_inner with the
+`input_token` time conditioning and `rope_sa_only` positions
+(rldx/model/modules/action_model/msat.py:291-556, :777-781), its
+DoubleStreamBlock.forward and SingleStreamBlock.forward with identity
+modulation (rldx/model/modules/action_model/blocks.py:166-254, :383-609), the
+RoPE embedder and rotary product (rldx/model/modules/action_model/ops.py:11-119),
+RMSNorm (rldx/model/modules/norms.py:7-22) and SwiGLUFFN (ops.py:137-161).
+
+Weights are a state dict under the reference module's own names
+(`double_blocks.{i}.sa_qkv.weight`, `single_blocks.{i}.linear1.bias`, ...).
+The time embedding `temb` and the time token are inputs, as in the reference's
+inference chain (custom_msat_chain.py:109-126), which bakes them per step.
+With identity modulation, (1 + 0) * y + 0 and 1 * y reproduce y exactly in
+bf16, so the modulation products are not spelled out.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from .cpu_reference import apply_rotary_emb, layer_norm, merge_heads, msat_rmsnorm, sdpa, split_heads, swiglu
+
+
+def rope_freq_tables(head_dim: int, theta: float, max_seq_len: int, bf16_quirk: bool):
+    """RoPEEmbedder1D buffers for axes [D/4, 3D/4] (msat.py:883-893; ops.py:11-25,
+    :82-103): precompute_freqs_cis per axis, complex64 [max_seq_len, axis_dim/2].
+    bf16_quirk: the buffers of a model loaded with torch_dtype=bfloat16 — the cast
+    keeps the real part (cos) in bf16 and drops the imaginary part
+    (custom_msat_chain.py:15-54)."""
+    tables = []
+    for dim in (head_dim // 4, head_dim - head_dim // 4):
+        freqs = 1.0 / (theta ** (torch.arange(0, dim, 2)[: (dim // 2)].float() / dim))
+        t = torch.arange(max_seq_len)
+        freqs = torch.outer(t, freqs).float()
+        fc = torch.polar(torch.ones_like(freqs), freqs)
+        tables.append(fc.real.to(torch.bfloat16) if bf16_quirk else fc)
+    return tables
+
+
+def rope_pe(tables, ids: torch.Tensor) -> torch.Tensor:
+    """RoPEEmbedder1D.forward (ops.py:105-118): ids [B, N, 2] -> [B, N, D/2]."""
+    return torch.cat([tables[i][ids[..., i]] for i in range(len(tables))], dim=-1)
+
+
+def _linear(x, sd, name):
+    return F.linear(x, sd[f"{name}.weight"], sd.get(f"{name}.bias"))
+
+
+def _swiglu_ffn(x, sd, name):
+    """SwiGLUFFN.forward (ops.py:155-161): w3(silu(x1) * x2), x1 | x2 = w12(x)."""
+    return _linear(swiglu(_linear(x, sd, f"{name}.w12")), sd, f"{name}.w3")
+
+
+def _qk_norm(x, w):
+    """per-head RMSNorm over [B, H, N, Dh] (blocks.py:525-537)."""
+    return msat_rmsnorm(x, w)
+
+
+def ds_block(sd: dict, p: str, sa: torch.Tensor, vl: torch.Tensor, pe: torch.Tensor, heads: int):
+    """DoubleStreamBlock.forward, identity modulation (blocks.py:383-609).
+    sa [B, N_sa, sa_dim] (time token first), vl [B, N_vl, vl_dim]; pe [B, N_vl + N_sa, Dh/2]."""
+    sa_qkv = _linear(layer_norm(sa), sd, f"{p}sa_qkv")
+    vl_qkv = _linear(layer_norm(vl), sd, f"{p}vl_qkv")
+    sa_q, sa_k, sa_v = (split_heads(t, heads) for t in sa_qkv.chunk(3, dim=-1))
+    vl_q, vl_k, vl_v = (split_heads(t, heads) for t in vl_qkv.chunk(3, dim=-1))
+    sa_q, sa_k = _qk_norm(sa_q, sd[f"{p}q_norm_sa.weight"]), _qk_norm(sa_k, sd[f"{p}k_norm_sa.weight"])
+    vl_q, vl_k = _qk_norm(vl_q, sd[f"{p}q_norm_vl.weight"]), _qk_norm(vl_k, sd[f"{p}k_norm_vl.weight"])
+    q = torch.cat([vl_q, sa_q], dim=2)
+    k = torch.cat([vl_k, sa_k], dim=2)
+    v = torch.cat([vl_v, sa_v], dim=2)
+    q, k = apply_rotary_emb(q, k, pe)
+    o = sdpa(q, k, v)
+    n_vl = vl.shape[1]
+    sa = sa + _linear(merge_heads(o[:, :, n_vl:]), sd, f"{p}sa_proj")
+    vl = vl + _linear(merge_heads(o[:, :, :n_vl]), sd, f"{p}vl_proj")
+    sa = sa + _swiglu_ffn(layer_norm(sa), sd, f"{p}sa_mlp")
+    vl = vl + _swiglu_ffn(layer_norm(vl), sd, f"{p}vl_mlp")
+    return sa, vl
+
+
+def ss_block(sd: dict, p: str, x: torch.Tensor, pe: torch.Tensor, heads: int):
+    """SingleStreamBlock.forward with SwiGLU, identity modulation (blocks.py:166-254)."""
+    inner = sd[f"{p}linear2.weight"].shape[1] - sd[f"{p}mlp_proj.weight"].shape[0]
+    h = _linear(layer_norm(x), sd, f"{p}linear1")
+    qkv, mlp = h[..., : 3 * inner], h[..., 3 * inner:]
+    q, k, v = (split_heads(t, heads) for t in qkv.chunk(3, dim=-1))
+    q, k = _qk_norm(q, sd[f"{p}q_norm.weight"]), _qk_norm(k, sd[f"{p}k_norm.weight"])
+    q, k = apply_rotary_emb(q, k, pe)
+    attn = merge_heads(sdpa(q, k, v))
+    mlp_out = _linear(swiglu(mlp), sd, f"{p}mlp_proj")
+    return x + _linear(torch.cat([attn, mlp_out], dim=-1), sd, f"{p}linear2")
+
+
+def msat_forward(sd: dict, sa_embs: torch.Tensor, vl_embs: torch.Tensor, temb: torch.Tensor,
+                 time_token: torch.Tensor, *, heads: int, head_dim: int, ds_blocks: int, ss_blocks: int,
+                 theta: float = 10000.0, max_seq_len: int = 1024, bf16_quirk: bool = True) -> torch.Tensor:
+    """MSAT._forward_inner, non-physics path, temb_type input_token, rope_sa_only
+    (msat.py:291-556) and _output_projection (:777-781).
+    sa_embs [B, N_sa_pure, sa_dim], vl_embs [B, N_vl, vl_dim], temb [B, inner],
+    time_token [B, num_temb_tokens, sa_dim]; returns [B, N_sa_pure, output_dim]."""
+    tables = rope_freq_tables(head_dim, theta, max_seq_len, bf16_quirk)
+    num_temb = time_token.shape[1]
+    B, n_vl = vl_embs.shape[:2]
+    sa = torch.cat([time_token, sa_embs], dim=1)
+    n_sa = sa.shape[1]
+    # position ids (msat.py:376-422): VL rows (0, 0); time tokens axis 1 = 0..; SA rows after them
+    ids = torch.zeros(B, n_vl + n_sa, 2, dtype=torch.long)
+    ids[:, n_vl:n_vl + num_temb, 1] = torch.arange(num_temb)
+    ids[:, n_vl + num_temb:, 1] = torch.arange(num_temb, n_sa)
+    pe = rope_pe(tables, ids)
+    vl = vl_embs
+    for i in range(ds_blocks):
+        sa, vl = ds_block(sd, f"double_blocks.{i}.", sa, vl, pe, heads)
+    time_tok = sa[:, :num_temb]
+    sa = sa[:, num_temb:]
+    x = torch.cat([_linear(vl, sd, "vl_proj_to_sa"), time_tok, sa], dim=1)
+    # single-stream position ids (msat.py:465-487): time tokens 0..; action rows from num_temb + 1
+    n_pure = sa.shape[1]
+    ids_s = torch.zeros(B, x.shape[1], 2, dtype=torch.long)
+    ids_s[:, n_vl:n_vl + num_temb, 1] = torch.arange(num_temb)
+    ids_s[:, x.shape[1] - n_pure:, 1] = torch.arange(num_temb + 1, num_temb + 1 + n_pure)
+    pe_s = rope_pe(tables, ids_s)
+    for i in range(ss_blocks):
+        x = ss_block(sd, f"single_blocks.{i}.", x, pe_s, heads)
+    sa = x[:, -n_pure:]
+    shift, scale = _linear(F.silu(temb), sd, "proj_out_1").chunk(2, dim=1)
+    sa = layer_norm(sa) * (1 + scale[:, None]) + shift[:, None]
+    return _linear(sa, sd, "proj_out_2")

@@ -1133,7 +1133,12 @@ extern "C" hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* 
                                                      hipStream_t stream) {
   const int64_t zero3[3] = {0, 0, 0};
   if (out_packed) {
+    // 1: O is the packed [seq_q, q_heads*head_dim] matrix; > 1: O is the
+    // column range of a packed matrix out_packed columns wide that starts at
+    // the 16-column chunk `o`
     if (batch > 1 || reinterpret_cast<uintptr_t>(o) % 16) return hipErrorInvalidValue;
+    if (out_packed < 0 || (out_packed > 1 && (out_packed % 16 || out_packed < q_heads * head_dim)))
+      return hipErrorInvalidValue;
     o_strides = zero3;
   }
   hipError_t e = check_qo(q, o, batch, q_heads, kv_heads, seq_q, seq_k, head_dim, q_strides, o_strides, scale);
@@ -1146,7 +1151,7 @@ extern "C" hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* 
   if (key_bias && reinterpret_cast<uintptr_t>(key_bias) % 4) return hipErrorInvalidValue;
   AttnArgs a{};
   fill_qo(a, q, o, q_heads, kv_heads, seq_q, seq_k, q_strides, o_strides, key_bias, key_bias_batch_stride, scale);
-  a.o_packed_k = out_packed ? q_heads * head_dim : 0;
+  a.o_packed_k = out_packed > 1 ? out_packed : (out_packed ? q_heads * head_dim : 0);
   a.kv = static_cast<const uint16_t*>(kv_packed);
   a.kv_sb = packed_strides[0];
   a.kv_sh = packed_strides[1];

@@ -60,7 +60,8 @@ constexpr int kXcds = 8;
 constexpr int kThreads = 512;          // 8 waves per workgroup
 constexpr int kBufWord3 = 0x00020000;  // gfx9 raw buffer descriptor, word 3 (untyped dword data)
 
-enum { kEpiBias = 0, kEpiResidual = 1, kEpiSwiglu = 2, kEpiSwigluPacked = 3 };
+enum { kEpiBias = 0, kEpiResidual = 1, kEpiSwiglu = 2, kEpiSwigluPacked = 3, kEpiBiasPacked = 4 };
+constexpr bool packed_out(int epi) { return epi == kEpiSwigluPacked || epi == kEpiBiasPacked; }
 enum { kTile128 = 0, kTile64 = 1, kTile32 = 2 };
 
 __device__ __forceinline__ float bf(uint16_t b) { return bf16_bits_to_f32(b); }
@@ -377,8 +378,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
           o[e] = pack_bf16x2(bf16x2_lo(pres[i][e]) + bf16x2_lo(o[e]), bf16x2_hi(pres[i][e]) + bf16x2_hi(o[e]));
       }
     }
-    if constexpr (EPI == kEpiSwigluPacked)
-      *reinterpret_cast<u32x4*>(G.out + packed_act_offset(row, col, n_out)) = o;
+    if constexpr (packed_out(EPI))  // ldo = width of the packed matrix the output columns belong to
+      *reinterpret_cast<u32x4*>(G.out + packed_act_offset(row, col, G.ldo)) = o;
     else
       *reinterpret_cast<u32x4*>(G.out + static_cast<int64_t>(row) * G.ldo + col) = o;
   }
@@ -450,7 +451,7 @@ constexpr int64_t kCounterBytes = 65536;
 hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, int64_t k, int32_t epilogue,
                 int split_k, GemmArgs& args, int64_t* ws_bytes, int64_t* cnt_off, int64_t* part_off) {
   if (!groups || num_groups < 1 || num_groups > 3) return hipErrorInvalidValue;
-  if (epilogue < kEpiBias || epilogue > kEpiSwigluPacked) return hipErrorInvalidValue;
+  if (epilogue < kEpiBias || epilogue > kEpiBiasPacked) return hipErrorInvalidValue;
   // k: whole stages of every K-group split (4 K-groups x 2 k-steps); n: whole 64-column blocks
   if (n <= 0 || k <= 0 || n % 64 != 0 || k % 128 != 0) return hipErrorInvalidValue;
   if (n > (1 << 30) || k > (1 << 30)) return hipErrorInvalidValue;
@@ -471,7 +472,11 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
       return hipErrorInvalidValue;
     // the epilogue stores (and reads the residual) in 16-byte pieces
     if (!a16(s.out) || (s.bias && reinterpret_cast<uintptr_t>(s.bias) % 2)) return hipErrorInvalidValue;
-    if (epilogue != kEpiSwigluPacked && (s.ldo < n_out || s.ldo % 8)) return hipErrorInvalidValue;
+    if (!packed_out(epilogue) && (s.ldo < n_out || s.ldo % 8)) return hipErrorInvalidValue;
+    // packed output: ldo 0 (= n_out) or the width of a wider packed matrix whose
+    // 16-column chunk at `out` starts the output columns
+    if (packed_out(epilogue) && (s.ldo < 0 || s.ldo % 16 || (s.ldo > 0 && s.ldo < n_out) || s.ldo > (1 << 30)))
+      return hipErrorInvalidValue;
     if (epilogue == kEpiResidual && (!s.residual || !a16(s.residual) || s.ldr < n_out || s.ldr % 8))
       return hipErrorInvalidValue;
     // Tile shape: 128 x 128 where the stream has rows and tiles enough to
@@ -499,7 +504,8 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
     Group& G = args.g[cnt++];
     G = Group{static_cast<const uint16_t*>(s.a_packed), static_cast<const uint16_t*>(s.w_packed),
               static_cast<const uint16_t*>(s.bias), static_cast<uint16_t*>(s.out),
-              static_cast<const uint16_t*>(s.residual), s.ldo, s.ldr, static_cast<int>(s.m), cfg, mt,
+              static_cast<const uint16_t*>(s.residual), packed_out(epilogue) && s.ldo == 0 ? n_out : s.ldo, s.ldr,
+              static_cast<int>(s.m), cfg, mt,
               static_cast<int>(tiles * sp), 0, 0, sp, lstages / sp, nullptr, nullptr};
   }
   args.num_groups = cnt;
@@ -557,8 +563,10 @@ hipError_t launch(const GemmArgs& args, int epilogue, hipStream_t stream) {
       hipLaunchKernelGGL((gemm_kernel<kEpiResidual, true>), grid, block, 0, stream, args);
     else if (epilogue == kEpiSwiglu)
       hipLaunchKernelGGL((gemm_kernel<kEpiSwiglu, true>), grid, block, 0, stream, args);
-    else
+    else if (epilogue == kEpiSwigluPacked)
       hipLaunchKernelGGL((gemm_kernel<kEpiSwigluPacked, true>), grid, block, 0, stream, args);
+    else
+      hipLaunchKernelGGL((gemm_kernel<kEpiBiasPacked, true>), grid, block, 0, stream, args);
   } else {
     if (epilogue == kEpiBias)
       hipLaunchKernelGGL((gemm_kernel<kEpiBias, false>), grid, block, 0, stream, args);
@@ -566,8 +574,10 @@ hipError_t launch(const GemmArgs& args, int epilogue, hipStream_t stream) {
       hipLaunchKernelGGL((gemm_kernel<kEpiResidual, false>), grid, block, 0, stream, args);
     else if (epilogue == kEpiSwiglu)
       hipLaunchKernelGGL((gemm_kernel<kEpiSwiglu, false>), grid, block, 0, stream, args);
-    else
+    else if (epilogue == kEpiSwigluPacked)
       hipLaunchKernelGGL((gemm_kernel<kEpiSwigluPacked, false>), grid, block, 0, stream, args);
+    else
+      hipLaunchKernelGGL((gemm_kernel<kEpiBiasPacked, false>), grid, block, 0, stream, args);
   }
   return hipGetLastError();
 }

@@ -104,7 +104,7 @@ SIGNATURES = {
 }
 
 ROPE_SIN_SIGNED = 1  # RLDX_ROPE_SIN_SIGNED
-GEMM_EPI_BIAS, GEMM_EPI_RESIDUAL, GEMM_EPI_SWIGLU, GEMM_EPI_SWIGLU_PACKED = 0, 1, 2, 3
+GEMM_EPI_BIAS, GEMM_EPI_RESIDUAL, GEMM_EPI_SWIGLU, GEMM_EPI_SWIGLU_PACKED, GEMM_EPI_BIAS_PACKED = 0, 1, 2, 3, 4
 
 _lib = None
 _hip = None

@@ -344,8 +344,8 @@ def attention_packed(q: torch.Tensor, kvp: torch.Tensor, seq_k: int, *, key_bias
                      out=None):
     """Attention with K/V given as packed tiles [B, Hkv, >= kv_packed_elems(seq_k, D)]
     (see kv_pack; the MSAT QKV kernel writes them directly).  `out` may be a
-    PackedAct [Sq, Hq*D] (batch 1): O is then written in the grouped GEMM's
-    packed activation order."""
+    PackedAct [Sq, Hq*D] (batch 1), or a column view of a wider one: O is then
+    written in the grouped GEMM's packed activation order."""
     _on_gpu(q, kvp, key_bias)
     _require(q.dtype == BF16 and q.dim() == 4 and q.stride(-1) == 1, "q must be 4-D bf16, last dim contiguous")
     if layout == "bhsd":
@@ -362,7 +362,8 @@ def attention_packed(q: torch.Tensor, kvp: torch.Tensor, seq_k: int, *, key_bias
     packed_out = isinstance(out, PackedAct)
     if packed_out:
         _on_gpu(out.data)
-        _require(B == 1 and out.m == Sq and out.k == Hq * D, "packed out must be a PackedAct [Sq, Hq*D], batch 1")
+        _require(B == 1 and out.m == Sq and out.k == Hq * D,
+                 "packed out must be a PackedAct [Sq, Hq*D] (or a column view of that width), batch 1")
         o_ptr, o_strides = out.data.data_ptr(), [0, 0, 0]
     else:
         if out is None:
@@ -376,7 +377,8 @@ def attention_packed(q: torch.Tensor, kvp: torch.Tensor, seq_k: int, *, key_bias
     lib = _lib.load()
     _lib.check(lib.rldx_attention_packed_fwd_bf16(q.data_ptr(), kvp.data_ptr(),
                                                   _lib.i64_array([kvp.stride(0), kvp.stride(1)]), o_ptr,
-                                                  int(packed_out), B, Hq, Hkv, Sq, seq_k, D,
+                                                  (out.ld if out.ld != out.k else 1) if packed_out else 0,
+                                                  B, Hq, Hkv, Sq, seq_k, D,
                                                   _lib.i64_array(_bhs_strides(q, layout)), _lib.i64_array(o_strides),
                                                   kb_ptr, kb_stride, float(scale), int(bool(causal)), _stream_ptr(q)),
                "rldx_attention_packed_fwd_bf16")
@@ -507,12 +509,14 @@ def pack_weight(w: torch.Tensor, swiglu_pairs: bool = False) -> PackedWeight:
 
 class PackedAct:
     """Activations [m, k] bf16 in the grouped GEMM's packed operand order
-    (32-row x 16-column chunks, rows padded to a multiple of 32)."""
+    (32-row x 16-column chunks, rows padded to a multiple of 32).  A column
+    view (`cols`) covers columns of a wider packed matrix `ld` columns wide."""
 
-    __slots__ = ("data", "m", "k")
+    __slots__ = ("data", "m", "k", "ld")
 
-    def __init__(self, data: torch.Tensor, m: int, k: int):
+    def __init__(self, data: torch.Tensor, m: int, k: int, ld: Optional[int] = None):
         self.data, self.m, self.k = data, m, k
+        self.ld = k if ld is None else ld
 
     @staticmethod
     def empty(m: int, k: int, device) -> "PackedAct":
@@ -521,10 +525,18 @@ class PackedAct:
     def rows(self, start: int, stop: int) -> "PackedAct":
         """Rows [start, stop) as a PackedAct view; start must be a multiple of 32."""
         _require(start % 32 == 0 and 0 <= start <= stop <= self.m, "row range must start on a 32-row boundary")
-        return PackedAct(self.data[start * self.k:], stop - start, self.k)
+        return PackedAct(self.data[start * self.ld:], stop - start, self.k, self.ld)
+
+    def cols(self, start: int, stop: int) -> "PackedAct":
+        """Columns [start, stop) as an output view (a write target of the packed
+        GEMM epilogues and the attention kernel); start must be a multiple of 16."""
+        _require(self.k == self.ld, "column view of a column view")
+        _require(start % 16 == 0 and 0 <= start < stop <= self.k, "column range must start on a 16-column chunk")
+        return PackedAct(self.data[start // 16 * 512:], self.m, stop - start, self.ld)
 
     def unpack(self) -> torch.Tensor:
         """Row-major copy (for tests and debugging)."""
+        _require(self.k == self.ld, "unpack a whole packed matrix")
         m, k = self.m, self.k
         mp = (m + 31) // 32
         t = self.data[: mp * 32 * k].view(mp, k // 16, 2, 32, 8)  # mb, kb, half, row, i
@@ -573,7 +585,8 @@ class GemmWorkspace:
 
 
 _GEMM_EPI = {"bias": _lib.GEMM_EPI_BIAS, "residual": _lib.GEMM_EPI_RESIDUAL, "swiglu": _lib.GEMM_EPI_SWIGLU,
-             "swiglu_packed": _lib.GEMM_EPI_SWIGLU_PACKED}
+             "swiglu_packed": _lib.GEMM_EPI_SWIGLU_PACKED, "bias_packed": _lib.GEMM_EPI_BIAS_PACKED}
+_PACKED_EPI = (_lib.GEMM_EPI_SWIGLU_PACKED, _lib.GEMM_EPI_BIAS_PACKED)
 
 
 def _gemm_groups(items: Sequence[tuple], epi: int, pack: bool):
@@ -590,13 +603,15 @@ def _gemm_groups(items: Sequence[tuple], epi: int, pack: bool):
                 a = pack_act(a)
                 keep.append(a)
         _on_gpu(a.data, w.data, bias, res)
-        _require(w.n == n and w.k == k and a.k == k, "groups must share n and k")
-        _require(epi < _lib.GEMM_EPI_SWIGLU or w.swiglu_pairs, "SwiGLU epilogue needs a swiglu_pairs weight")
+        _require(w.n == n and w.k == k and a.k == k and a.ld == k, "groups must share n and k")
+        swiglu = epi in (_lib.GEMM_EPI_SWIGLU, _lib.GEMM_EPI_SWIGLU_PACKED)
+        _require(not swiglu or w.swiglu_pairs, "SwiGLU epilogue needs a swiglu_pairs weight")
         m = a.m
-        n_out = n // 2 if epi >= _lib.GEMM_EPI_SWIGLU else n
-        if epi == _lib.GEMM_EPI_SWIGLU_PACKED:
-            _require(isinstance(out, PackedAct) and out.m == m and out.k == n_out, "out must be a PackedAct [m, n/2]")
-            out_ptr, ldo = out.data.data_ptr(), 0
+        n_out = n // 2 if swiglu else n
+        if epi in _PACKED_EPI:
+            _require(isinstance(out, PackedAct) and out.m == m and out.k == n_out,
+                     "out must be a PackedAct [m, n_out] (or a column view of that width)")
+            out_ptr, ldo = out.data.data_ptr(), (0 if out.ld == out.k else out.ld)
         else:
             _require(out.dtype == BF16 and out.dim() == 2 and out.stride(1) == 1 and tuple(out.shape) == (m, n_out),
                      "out must be [m, n_out] bf16")
@@ -627,7 +642,8 @@ def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias", split_k: int = 
     items: (a PackedAct [m, k] or row-major tensor (packed first), PackedWeight,
     bias [n] or None, out, residual or None).  epilogue: "bias" (out = y),
     "residual" (out = residual + y, residual may be out), "swiglu" (out [m, n/2] =
-    swiglu(y)) or "swiglu_packed" (out a PackedAct).  split_k > 1 splits the K
+    swiglu(y)), "swiglu_packed" or "bias_packed" (out a PackedAct, or a column view
+    of a wider one: PackedAct.cols).  split_k > 1 splits the K
     range of every stream over that many workgroups (partials summed in a fixed
     order: deterministic); it needs a workspace of grouped_gemm_workspace_bytes(...)
     bytes."""

@@ -1,0 +1,433 @@
+"""The RLDX-1 MSAT (no add-ons) on the rldx_amd kernels, built from the
+reference's own weights.
+
+`RldxMsat` is the counterpart of the reference's CustomOpMSAT
+(rldx/inference/action_model/engine/custom_msat_chain.py:56-126): the same
+forward(hidden_states, encoder_hidden_states, temb, time_token) with the time
+embedding and time token baked by the caller, 4 DoubleStreamBlocks over
+[VL | time | SA] and 8 SingleStreamBlocks over [VL->SA | time | SA]
+(rldx/model/modules/action_model/blocks.py:166-254, :383-609; msat.py:291-556),
+then the AdaLN output projection (msat.py:777-781).  It is built from a state
+dict under the reference module's names (`double_blocks.0.sa_qkv.weight`, ...),
+read from local safetensors files by `load_msat_state_dict` (no hub access), or
+taken from a live module by `install`.
+
+RoPE: the rope_sa_only tables of RoPEEmbedder1D.  A model loaded in bfloat16
+has its complex frequency buffers cast to bf16, which keeps cos and drops sin;
+`bf16_quirk=True` (the default, as the reference chain assumes) reproduces that
+(cos rounded to bf16, sin = 0), False uses the exact fp32 tables.
+
+Per DoubleStreamBlock (14 launches; the SA and VL streams have different
+widths, so each GEMM runs once per stream):
+    LayerNorm -> packed h_s            rldx_layernorm_pack_bf16           x2
+    QKV linears (+ bias)               rldx_grouped_gemm_bf16             x2
+    QK-RMSNorm + RoPE (SA rows) + K/V  rldx_msat_qkv_norm_rope_bf16
+    joint attention -> packed o        rldx_attention_packed_fwd_bf16
+    proj + residual (in place)         rldx_grouped_gemm_bf16 (residual)  x2
+    LayerNorm -> packed h_s                                               x2
+    w12 + SwiGLU -> packed             rldx_grouped_gemm_bf16 (swiglu)    x2
+    w3 + residual (in place)           rldx_grouped_gemm_bf16 (residual)  x2
+Per SingleStreamBlock (7 launches):
+    LayerNorm -> packed h; linear1's QKV columns (+ bias); linear1's MLP columns
+    + SwiGLU -> packed; QK-RMSNorm + RoPE; attention -> columns [0, inner) of
+    the packed linear2 operand; mlp_proj (+ bias) -> its columns [inner, ...);
+    linear2 + residual (in place).
+The SwiGLU widths of the double-stream FFNs (SA 4096, VL 10922) are padded
+with zero weight rows / columns to a multiple of 128 (silu(0) * 0 = 0, so the
+padding contributes nothing).  The output projection's tiny modulation
+(F.silu(temb) -> proj_out_1, LayerNorm * (1 + scale) + shift) runs as torch ops.
+"""
+
+from __future__ import annotations
+
+import math
+import os
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+from . import functional as Fn
+from .workloads import msat_freqs_cis
+
+BF16 = torch.bfloat16
+
+
+@dataclass
+class RldxMsatCfg:
+    """MSAT dimensions (rldx/configs/model/rldx.py:94-112; Appendix values of the
+    RLDX-1 release: 24 x 64 heads, 4 + 8 blocks, SA 1536, VL 4096)."""
+
+    heads: int = 24
+    head_dim: int = 64
+    ds_blocks: int = 4
+    ss_blocks: int = 8
+    sa_dim: int = 1536
+    vl_dim: int = 4096
+    mlp_ratio: float = 4.0
+    vl_mlp_ratio: Optional[float] = None
+    output_dim: int = 1024
+    n_vl: int = 64          # cognition tokens
+    n_sa_pure: int = 17     # state token + action horizon 16
+    num_temb_tokens: int = 1
+    rope_theta: float = 10000.0
+    max_seq_len: int = 1024
+    eps: float = 1e-6
+
+    @property
+    def inner(self) -> int:
+        return self.heads * self.head_dim
+
+    @property
+    def sa_ffn(self) -> int:  # blocks.py:317-319
+        return int(2 / 3 * int(self.sa_dim * self.mlp_ratio))
+
+    @property
+    def vl_ffn(self) -> int:  # blocks.py:349-351
+        r = self.vl_mlp_ratio if self.vl_mlp_ratio is not None else self.mlp_ratio
+        return int(2 / 3 * int(self.vl_dim * r))
+
+    @property
+    def ss_expanded(self) -> int:  # blocks.py:100-114
+        return int(self.sa_dim * self.mlp_ratio)
+
+    @property
+    def ss_hidden(self) -> int:
+        return int(2 / 3 * self.ss_expanded)
+
+    @property
+    def n_sa(self) -> int:
+        return self.n_sa_pure + self.num_temb_tokens
+
+    @property
+    def tokens(self) -> int:
+        return self.n_vl + self.n_sa
+
+    def param_shapes(self) -> dict:
+        """Parameter names and shapes of the reference MSAT (no add-ons,
+        temb_type input_token, qk_norm rms_norm, SwiGLU) that the chain reads."""
+        d, v, i = self.sa_dim, self.vl_dim, self.inner
+        s = {}
+        for b in range(self.ds_blocks):
+            p = f"double_blocks.{b}."
+            s.update({p + "sa_qkv.weight": (3 * i, d), p + "sa_qkv.bias": (3 * i,),
+                      p + "vl_qkv.weight": (3 * i, v), p + "vl_qkv.bias": (3 * i,),
+                      p + "sa_proj.weight": (d, i), p + "sa_proj.bias": (d,),
+                      p + "vl_proj.weight": (v, i), p + "vl_proj.bias": (v,),
+                      p + "sa_mlp.w12.weight": (2 * self.sa_ffn, d), p + "sa_mlp.w12.bias": (2 * self.sa_ffn,),
+                      p + "sa_mlp.w3.weight": (d, self.sa_ffn), p + "sa_mlp.w3.bias": (d,),
+                      p + "vl_mlp.w12.weight": (2 * self.vl_ffn, v), p + "vl_mlp.w12.bias": (2 * self.vl_ffn,),
+                      p + "vl_mlp.w3.weight": (v, self.vl_ffn), p + "vl_mlp.w3.bias": (v,)})
+            for n in ("q_norm_sa", "k_norm_sa", "q_norm_vl", "k_norm_vl"):
+                s[p + n + ".weight"] = (self.head_dim,)
+        e, hs = self.ss_expanded, self.ss_hidden
+        for b in range(self.ss_blocks):
+            p = f"single_blocks.{b}."
+            s.update({p + "linear1.weight": (3 * i + 2 * e, d), p + "linear1.bias": (3 * i + 2 * e,),
+                      p + "mlp_proj.weight": (hs, e), p + "mlp_proj.bias": (hs,),
+                      p + "linear2.weight": (d, i + hs), p + "linear2.bias": (d,),
+                      p + "q_norm.weight": (self.head_dim,), p + "k_norm.weight": (self.head_dim,)})
+        s.update({"vl_proj_to_sa.weight": (d, v), "vl_proj_to_sa.bias": (d,),
+                  "proj_out_1.weight": (2 * d, i), "proj_out_1.bias": (2 * d,),
+                  "proj_out_2.weight": (self.output_dim, d), "proj_out_2.bias": (self.output_dim,)})
+        return s
+
+    @staticmethod
+    def from_state_dict(sd: dict, **overrides) -> "RldxMsatCfg":
+        """Dimensions read off the parameter shapes (token counts from overrides)."""
+        ds = sum(1 for k in sd if k.startswith("double_blocks.") and k.endswith(".sa_qkv.weight"))
+        ss = sum(1 for k in sd if k.startswith("single_blocks.") and k.endswith(".linear1.weight"))
+        hd = sd["double_blocks.0.q_norm_sa.weight"].shape[0]
+        inner = sd["double_blocks.0.sa_qkv.weight"].shape[0] // 3
+        sa_dim, vl_dim = sd["double_blocks.0.sa_qkv.weight"].shape[1], sd["double_blocks.0.vl_qkv.weight"].shape[1]
+        kw = dict(heads=inner // hd, head_dim=hd, ds_blocks=ds, ss_blocks=ss, sa_dim=sa_dim, vl_dim=vl_dim,
+                  output_dim=sd["proj_out_2.weight"].shape[0],
+                  mlp_ratio=sd["double_blocks.0.sa_mlp.w12.weight"].shape[0] * 3 / 4 / sa_dim)
+        kw.update(overrides)
+        cfg = RldxMsatCfg(**kw)
+        if int(cfg.sa_dim * cfg.mlp_ratio) != sd["double_blocks.0.sa_mlp.w12.weight"].shape[0] * 3 // 4:
+            cfg.mlp_ratio = 4.0  # the ratio is only recoverable up to the int() of blocks.py; the release uses 4
+        vl_w12 = sd["double_blocks.0.vl_mlp.w12.weight"].shape[0] // 2
+        if cfg.vl_ffn != vl_w12:
+            cfg.vl_mlp_ratio = math.ceil(vl_w12 * 3 / 2) / vl_dim
+        return cfg
+
+
+def make_state_dict(cfg: RldxMsatCfg, device, seed: int = 11, std: float = 0.02) -> dict:
+    """Random-init parameters under the reference names: weights and biases
+    ~ N(0, std), norm weights 1 + N(0, 0.02); bf16 on `device`."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    sd = {}
+    for k, shape in cfg.param_shapes().items():
+        r = torch.randn(*shape, generator=g, device=device, dtype=torch.float32)
+        sd[k] = (1.0 + 0.02 * r if "norm" in k else std * r).to(BF16)
+    return sd
+
+
+def make_inputs(cfg: RldxMsatCfg, device, seed: int = 12) -> dict:
+    """SA embeddings (state + action tokens), VL (cognition) tokens, a time
+    embedding and its time token, bf16, batch 1."""
+    g = torch.Generator(device=device).manual_seed(seed)
+
+    def rnd(*shape, std=1.0):
+        return (std * torch.randn(*shape, generator=g, device=device, dtype=torch.float32)).to(BF16)
+
+    return dict(sa=rnd(1, cfg.n_sa_pure, cfg.sa_dim), vl=rnd(1, cfg.n_vl, cfg.vl_dim),
+                temb=rnd(1, cfg.inner, std=0.5), time_token=rnd(1, cfg.num_temb_tokens, cfg.sa_dim, std=0.5))
+
+
+def load_msat_state_dict(path: str, prefix: str = "action_model.model.", device="cpu") -> dict:
+    """MSAT parameters from local safetensors file(s) (a file, or every
+    *.safetensors file of a directory) of an RLDX checkpoint: keys under
+    `prefix` (the MSAT of RLDX.action_model, rldx/model/core/rldx.py:75, :892),
+    prefix stripped, cast to bf16.  Reads tensors only (no code is executed)."""
+    from safetensors.torch import load_file
+
+    files = [path] if os.path.isfile(path) else sorted(
+        os.path.join(path, f) for f in os.listdir(path) if f.endswith(".safetensors"))
+    Fn._require(len(files) > 0, f"no .safetensors file at {path}")
+    sd = {}
+    for f in files:
+        for k, v in load_file(f, device=str(device)).items():
+            if k.startswith(prefix):
+                sd[k[len(prefix):]] = v.to(BF16)
+    Fn._require(len(sd) > 0, f"no parameter under prefix '{prefix}' in {path}")
+    return sd
+
+
+def rope_tables(cfg: RldxMsatCfg, positions: torch.Tensor, bf16_quirk: bool):
+    """fp32 cos / sin [N, D/2] of the rope_sa_only embedder (axes [D/4, 3D/4],
+    axis 0 at position 0) for axis-1 positions (RoPEEmbedder1D, ops.py:70-119);
+    with bf16_quirk, cos rounded to bf16 and sin = 0 (custom_msat_chain.py:15-54)."""
+    parts = []
+    for i, ad in enumerate((cfg.head_dim // 4, cfg.head_dim - cfg.head_dim // 4)):
+        fc = msat_freqs_cis(ad, cfg.max_seq_len, cfg.rope_theta)
+        idx = torch.zeros_like(positions) if i == 0 else positions
+        parts.append(fc[idx])
+    pe = torch.cat(parts, dim=-1)
+    if bf16_quirk:
+        return pe.real.to(BF16).float().contiguous(), torch.zeros(pe.shape, dtype=torch.float32)
+    return pe.real.float().contiguous(), pe.imag.float().contiguous()
+
+
+def _pad_rows(w: torch.Tensor, rows: int) -> torch.Tensor:
+    return w if w.shape[0] == rows else torch.cat([w, w.new_zeros(rows - w.shape[0], *w.shape[1:])])
+
+
+def _pad_cols(w: torch.Tensor, cols: int) -> torch.Tensor:
+    return w if w.shape[1] == cols else torch.cat([w, w.new_zeros(w.shape[0], cols - w.shape[1])], dim=1)
+
+
+def _round_up(x: int, m: int) -> int:
+    return (x + m - 1) // m * m
+
+
+class RldxMsat:
+    """Static-buffer executor of the RLDX-1 MSAT forward; `forward` launches it
+    eagerly (capturable in a hipGraph), `capture` / `replay` record and replay it."""
+
+    def __init__(self, sd: dict, cfg: RldxMsatCfg, device, bf16_quirk: bool = True):
+        self.cfg, self.dev = cfg, torch.device(device)
+        H, D, inner = cfg.heads, cfg.head_dim, cfg.inner
+        Fn._require(D in (64, 128), "head_dim must be 64 or 128")
+        Fn._require(cfg.n_vl % 32 == 0, "the VL token count must be a multiple of 32 (packed row blocks)")
+        for k, shape in cfg.param_shapes().items():
+            Fn._require(k in sd, f"missing parameter {k}")
+            Fn._require(tuple(sd[k].shape) == tuple(shape), f"{k}: shape {tuple(sd[k].shape)}, expected {shape}")
+        w = {k: sd[k].to(device=self.dev, dtype=BF16).contiguous() for k in cfg.param_shapes()}
+        self.w = w
+        self.sa_ffn_p, self.vl_ffn_p = _round_up(cfg.sa_ffn, 128), _round_up(cfg.vl_ffn, 128)
+        for dim in (cfg.sa_dim, cfg.vl_dim, inner, cfg.ss_expanded, cfg.ss_hidden + inner, cfg.output_dim):
+            Fn._require(dim % 64 == 0, f"width {dim} is not a multiple of 64")
+        for dim in (cfg.sa_dim, cfg.vl_dim, inner, cfg.ss_expanded, inner + cfg.ss_hidden):
+            Fn._require(dim % 128 == 0, f"GEMM depth {dim} is not a multiple of 128")
+
+        def swiglu_w(w12, b12, ffn, ffn_p):
+            g, u = w12[:ffn], w12[ffn:]
+            gb, ub = b12[:ffn], b12[ffn:]
+            wp = torch.cat([_pad_rows(g, ffn_p), _pad_rows(u, ffn_p)])
+            bp = torch.cat([_pad_rows(gb[:, None], ffn_p)[:, 0], _pad_rows(ub[:, None], ffn_p)[:, 0]])
+            return Fn.pack_weight(wp, swiglu_pairs=True), bp.contiguous()
+
+        self.ds = []
+        for b in range(cfg.ds_blocks):
+            p = f"double_blocks.{b}."
+            blk = {n: w[p + n] for n in ("q_norm_sa.weight", "k_norm_sa.weight", "q_norm_vl.weight",
+                                          "k_norm_vl.weight", "sa_qkv.bias", "vl_qkv.bias", "sa_proj.bias",
+                                          "vl_proj.bias", "sa_mlp.w3.bias", "vl_mlp.w3.bias")}
+            for n in ("sa_qkv", "vl_qkv", "sa_proj", "vl_proj"):
+                blk[n] = Fn.pack_weight(w[p + n + ".weight"])
+            blk["sa_w12"], blk["sa_w12.bias"] = swiglu_w(w[p + "sa_mlp.w12.weight"], w[p + "sa_mlp.w12.bias"],
+                                                          cfg.sa_ffn, self.sa_ffn_p)
+            blk["vl_w12"], blk["vl_w12.bias"] = swiglu_w(w[p + "vl_mlp.w12.weight"], w[p + "vl_mlp.w12.bias"],
+                                                          cfg.vl_ffn, self.vl_ffn_p)
+            blk["sa_w3"] = Fn.pack_weight(_pad_cols(w[p + "sa_mlp.w3.weight"], self.sa_ffn_p))
+            blk["vl_w3"] = Fn.pack_weight(_pad_cols(w[p + "vl_mlp.w3.weight"], self.vl_ffn_p))
+            self.ds.append(blk)
+        self.ss = []
+        e = cfg.ss_expanded
+        for b in range(cfg.ss_blocks):
+            p = f"single_blocks.{b}."
+            w1, b1 = w[p + "linear1.weight"], w[p + "linear1.bias"]
+            blk = {"q_norm": w[p + "q_norm.weight"], "k_norm": w[p + "k_norm.weight"],
+                   "qkv": Fn.pack_weight(w1[: 3 * inner].contiguous()), "qkv.bias": b1[: 3 * inner].contiguous(),
+                   "mlp": Fn.pack_weight(w1[3 * inner:].contiguous(), swiglu_pairs=True),
+                   "mlp.bias": b1[3 * inner:].contiguous(),
+                   "mlp_proj": Fn.pack_weight(w[p + "mlp_proj.weight"]), "mlp_proj.bias": w[p + "mlp_proj.bias"],
+                   "linear2": Fn.pack_weight(w[p + "linear2.weight"]), "linear2.bias": w[p + "linear2.bias"]}
+            self.ss.append(blk)
+        self.vl_proj_to_sa = Fn.pack_weight(w["vl_proj_to_sa.weight"])
+        self.proj_out_2 = Fn.pack_weight(w["proj_out_2.weight"])
+        # RoPE: DS rows [time | SA] at axis-1 positions 0 .. n_sa - 1; SS rows [time | SA]
+        # at 0 and num_temb + 1 ... (custom_msat_chain.py:81-105, the eager ids of msat.py:376-487)
+        nt = cfg.num_temb_tokens
+        ds_pos = torch.arange(cfg.n_sa)
+        ss_pos = torch.cat([torch.arange(nt), torch.arange(nt + 1, nt + 1 + cfg.n_sa_pure)])
+        self.ds_cos, self.ds_sin = (t.to(self.dev) for t in rope_tables(cfg, ds_pos, bf16_quirk))
+        self.ss_cos, self.ss_sin = (t.to(self.dev) for t in rope_tables(cfg, ss_pos, bf16_quirk))
+        # activations
+        N, nv, ns = cfg.tokens, cfg.n_vl, cfg.n_sa
+        ebuf = lambda *s: torch.empty(*s, dtype=BF16, device=self.dev)  # noqa: E731
+        self.x_sa, self.x_vl = ebuf(ns, cfg.sa_dim), ebuf(nv, cfg.vl_dim)
+        self.h_sa, self.h_vl = Fn.PackedAct.empty(ns, cfg.sa_dim, self.dev), Fn.PackedAct.empty(nv, cfg.vl_dim,
+                                                                                                 self.dev)
+        self.qkv_sa, self.qkv_vl = ebuf(ns, 3 * inner), ebuf(nv, 3 * inner)
+        self.q = ebuf(H, N, D)
+        self.kvp = ebuf(H, Fn.kv_packed_elems(N, D))
+        self.att = Fn.PackedAct.empty(N, inner, self.dev)
+        self.gl_sa = Fn.PackedAct.empty(ns, self.sa_ffn_p, self.dev)
+        self.gl_vl = Fn.PackedAct.empty(nv, self.vl_ffn_p, self.dev)
+        self.vl_packed = Fn.PackedAct.empty(nv, cfg.vl_dim, self.dev)
+        self.x = ebuf(N, cfg.sa_dim)
+        self.h = Fn.PackedAct.empty(N, cfg.sa_dim, self.dev)
+        self.qkv = ebuf(N, 3 * inner)
+        self.gl = Fn.PackedAct.empty(N, e, self.dev)
+        self.cat = Fn.PackedAct.empty(N, inner + cfg.ss_hidden, self.dev)
+        self.mod = ebuf(cfg.n_sa_pure, cfg.sa_dim)
+        self.mod_packed = Fn.PackedAct.empty(cfg.n_sa_pure, cfg.sa_dim, self.dev)
+        self.out = ebuf(1, cfg.n_sa_pure, cfg.output_dim)
+        self.inputs = dict(sa=ebuf(1, cfg.n_sa_pure, cfg.sa_dim), vl=ebuf(1, nv, cfg.vl_dim),
+                           temb=ebuf(1, inner), time_token=ebuf(1, nt, cfg.sa_dim))
+        self.graph = None
+
+    # -- blocks ---------------------------------------------------------------
+    def _ds_block(self, blk: dict) -> None:
+        cfg = self.cfg
+        nv, N = cfg.n_vl, cfg.tokens
+        Fn.layernorm_pack(self.x_sa, cfg.eps, out=self.h_sa)
+        Fn.layernorm_pack(self.x_vl, cfg.eps, out=self.h_vl)
+        Fn.grouped_gemm([(self.h_sa, blk["sa_qkv"], blk["sa_qkv.bias"], self.qkv_sa, None)], "bias")
+        Fn.grouped_gemm([(self.h_vl, blk["vl_qkv"], blk["vl_qkv.bias"], self.qkv_vl, None)], "bias")
+        specs = [Fn.StreamSpec(self.qkv_vl, blk["q_norm_vl.weight"], blk["k_norm_vl.weight"]),
+                 Fn.StreamSpec(self.qkv_sa, blk["q_norm_sa.weight"], blk["k_norm_sa.weight"], self.ds_cos,
+                               self.ds_sin)]
+        Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
+        Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), N, out=self.att)
+        Fn.grouped_gemm([(self.att.rows(nv, N), blk["sa_proj"], blk["sa_proj.bias"], self.x_sa, self.x_sa)],
+                        "residual")
+        Fn.grouped_gemm([(self.att.rows(0, nv), blk["vl_proj"], blk["vl_proj.bias"], self.x_vl, self.x_vl)],
+                        "residual")
+        Fn.layernorm_pack(self.x_sa, cfg.eps, out=self.h_sa)
+        Fn.layernorm_pack(self.x_vl, cfg.eps, out=self.h_vl)
+        Fn.grouped_gemm([(self.h_sa, blk["sa_w12"], blk["sa_w12.bias"], self.gl_sa, None)], "swiglu_packed")
+        Fn.grouped_gemm([(self.h_vl, blk["vl_w12"], blk["vl_w12.bias"], self.gl_vl, None)], "swiglu_packed")
+        Fn.grouped_gemm([(self.gl_sa, blk["sa_w3"], blk["sa_mlp.w3.bias"], self.x_sa, self.x_sa)], "residual")
+        Fn.grouped_gemm([(self.gl_vl, blk["vl_w3"], blk["vl_mlp.w3.bias"], self.x_vl, self.x_vl)], "residual")
+
+    def _ss_block(self, blk: dict) -> None:
+        cfg = self.cfg
+        nv, N, inner = cfg.n_vl, cfg.tokens, cfg.inner
+        Fn.layernorm_pack(self.x, cfg.eps, out=self.h)
+        Fn.grouped_gemm([(self.h, blk["qkv"], blk["qkv.bias"], self.qkv, None)], "bias")
+        Fn.grouped_gemm([(self.h, blk["mlp"], blk["mlp.bias"], self.gl, None)], "swiglu_packed")
+        specs = [Fn.StreamSpec(self.qkv[:nv], blk["q_norm"], blk["k_norm"]),
+                 Fn.StreamSpec(self.qkv[nv:], blk["q_norm"], blk["k_norm"], self.ss_cos, self.ss_sin)]
+        Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
+        Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), N, out=self.cat.cols(0, inner))
+        Fn.grouped_gemm([(self.gl, blk["mlp_proj"], blk["mlp_proj.bias"],
+                          self.cat.cols(inner, inner + cfg.ss_hidden), None)], "bias_packed")
+        Fn.grouped_gemm([(self.cat, blk["linear2"], blk["linear2.bias"], self.x, self.x)], "residual")
+
+    # -- forward --------------------------------------------------------------
+    def forward(self, hidden_states: torch.Tensor, encoder_hidden_states: torch.Tensor, temb: torch.Tensor,
+                time_token: torch.Tensor) -> torch.Tensor:
+        """CustomOpMSAT.forward (custom_msat_chain.py:109-126): hidden_states
+        [1, n_sa_pure, sa_dim], encoder_hidden_states [1, n_vl, vl_dim], temb
+        [1, inner], time_token [1, num_temb_tokens, sa_dim] -> [1, n_sa_pure,
+        output_dim] (a static buffer, overwritten by the next call)."""
+        cfg = self.cfg
+        nt, nv = cfg.num_temb_tokens, cfg.n_vl
+        Fn._require(tuple(hidden_states.shape) == (1, cfg.n_sa_pure, cfg.sa_dim) and
+                    tuple(encoder_hidden_states.shape) == (1, nv, cfg.vl_dim) and
+                    tuple(temb.shape) == (1, cfg.inner) and tuple(time_token.shape) == (1, nt, cfg.sa_dim),
+                    "input shapes do not match the chain's configuration (batch 1)")
+        self.x_sa[:nt].copy_(time_token[0])
+        self.x_sa[nt:].copy_(hidden_states[0])
+        self.x_vl.copy_(encoder_hidden_states[0])
+        for blk in self.ds:
+            self._ds_block(blk)
+        # x = [vl_proj_to_sa(vl) | time token | SA]
+        Fn.pack_act(self.x_vl, out=self.vl_packed)
+        Fn.grouped_gemm([(self.vl_packed, self.vl_proj_to_sa, self.w["vl_proj_to_sa.bias"], self.x[:nv], None)],
+                        "bias")
+        self.x[nv:].copy_(self.x_sa)
+        for blk in self.ss:
+            self._ss_block(blk)
+        # AdaLN output projection (msat.py:777-781)
+        shift, scale = F.linear(F.silu(temb), self.w["proj_out_1.weight"], self.w["proj_out_1.bias"]).chunk(2, dim=1)
+        sa = F.layer_norm(self.x[cfg.tokens - cfg.n_sa_pure:], (cfg.sa_dim,), eps=1e-6)
+        torch.add(sa * (1 + scale), shift, out=self.mod)
+        Fn.pack_act(self.mod, out=self.mod_packed)
+        Fn.grouped_gemm([(self.mod_packed, self.proj_out_2, self.w["proj_out_2.bias"], self.out[0], None)], "bias")
+        return self.out
+
+    __call__ = forward
+
+    def capture(self, warmup: int = 2) -> None:
+        """Record forward() on the static `inputs` buffers into one hipGraph."""
+        i = self.inputs
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(warmup):
+                self.forward(i["sa"], i["vl"], i["temb"], i["time_token"])
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.forward(i["sa"], i["vl"], i["temb"], i["time_token"])
+        torch.cuda.synchronize()
+
+    def replay(self) -> torch.Tensor:
+        self.graph.replay()
+        return self.out
+
+
+def install(msat: torch.nn.Module, n_vl: int, n_sa_pure: int, bf16_quirk: Optional[bool] = None) -> RldxMsat:
+    """Replace a live MSAT module's forward by the rldx_amd chain (what the
+    reference's path-D dispatcher does with CustomOpMSAT,
+    rldx/inference/serve_optimization.py:251-601).  The chain is built from
+    msat.state_dict(); msat.forward(hidden_states, encoder_hidden_states,
+    timestep) keeps its signature: the module's own timestep_encoder and
+    time_token_proj make temb and the time token.  bf16_quirk=None detects it
+    from the RoPE buffers (real-valued: the model was cast to bf16)."""
+    sd = {k: v for k, v in msat.state_dict().items()}
+    rope = getattr(msat, "rope_embedder", None)
+    if bf16_quirk is None:
+        bf16_quirk = rope is not None and not getattr(rope, "freqs_cis_0").is_complex()
+    overrides = dict(n_vl=n_vl, n_sa_pure=n_sa_pure)
+    if rope is not None:
+        overrides.update(rope_theta=float(rope.theta), max_seq_len=int(rope.max_seq_len))
+    cfg = RldxMsatCfg.from_state_dict(sd, **overrides)
+    dev = next(iter(sd.values())).device
+    chain = RldxMsat(sd, cfg, dev, bf16_quirk=bf16_quirk)
+
+    def forward(hidden_states, encoder_hidden_states, timestep=None, **kwargs):
+        temb = msat.timestep_encoder(timestep)
+        tt = msat.time_token_proj(temb).unsqueeze(1).repeat(1, cfg.num_temb_tokens, 1)
+        return chain.forward(hidden_states, encoder_hidden_states, temb, tt)
+
+    msat.forward = forward
+    msat.rldx_amd_chain = chain
+    return chain

@@ -228,6 +228,25 @@ def test_memory_attention_rejections():
     assert call(M=0, qkv=None, out=None) == 0
 
 
+def test_packed_output_widths_validated():
+    """Packed GEMM outputs take ldo 0 or a packed width (multiple of 16, >= the
+    output columns); attention's out_packed 1 or such a width."""
+    lib = _lib.load()
+    g = _gemm_groups((82,), ldo=0)
+    assert lib.rldx_grouped_gemm_workspace_bytes(g, 1, 4096, 6144, 4, 1) == 0      # bias_packed, ldo 0
+    g = _gemm_groups((82,), ldo=5632)
+    assert lib.rldx_grouped_gemm_workspace_bytes(g, 1, 4096, 6144, 4, 1) == 0      # into a wider matrix
+    for bad in (5640, 4080, -16):  # not a multiple of 16, narrower than the output, negative
+        g = _gemm_groups((82,), ldo=bad)
+        assert lib.rldx_grouped_gemm_workspace_bytes(g, 1, 4096, 6144, 4, 1) == -1
+    assert lib.rldx_grouped_gemm_workspace_bytes(_gemm_groups((82,)), 1, 4096, 6144, 5, 1) == -1  # no epilogue 5
+    st = _lib.i64_array([0, 0, 0])
+    ps = _lib.i64_array([0, 24 * 64 * 64 * 3])
+    for bad in (-1, 1000, 1536 - 16):
+        assert lib.rldx_attention_packed_fwd_bf16(256, 512, ps, 1024, bad, 1, 24, 24, 82, 82, 64, st, st, None, 0,
+                                                  0.125, 0, None) == HIP_INVALID_VALUE
+
+
 def test_zero_sized_calls_are_noops():
     lib = _lib.load()
     st = _lib.i64_array([0, 0, 0])

@@ -287,6 +287,42 @@ def test_attention_packed_output(dev):
     assert torch.equal(op.unpack(), o.view(S, H * D))
 
 
+def test_concatenated_packed_operand_from_attention_and_bias_packed_gemm(dev):
+    """The single-stream block's linear2 operand cat([attention, mlp_proj(...)]):
+    the attention kernel writes columns [0, 1536) and a bias_packed GEMM columns
+    [1536, 5632) of one packed [82, 5632] matrix, each equal bit for bit to its
+    row-major output; a swiglu_packed GEMM into a column view likewise."""
+    g = torch.Generator().manual_seed(19)
+    H, S, D, n2, k2 = 24, 82, 64, 4096, 6144
+    q = torch.randn(1, H, S, D, generator=g).to(BF16).to(dev)
+    kk = torch.randn(1, H, S, D, generator=g).to(BF16).to(dev)
+    v = torch.randn(1, H, S, D, generator=g).to(BF16).to(dev)
+    kvp = Fn.kv_pack(kk, v)
+    o = torch.empty(1, S, H, D, dtype=BF16, device=dev)
+    Fn.attention_packed(q, kvp, S, out=o.permute(0, 2, 1, 3))
+    a = _rand((S, k2), g).to(dev)
+    w = Fn.pack_weight(_rand((n2, k2), g, 0.02).to(dev))
+    b = _rand((n2,), g, 0.1).to(dev)
+    rm = torch.empty(S, n2, dtype=BF16, device=dev)
+    ap = Fn.pack_act(a)
+    Fn.grouped_gemm([(ap, w, b, rm, None)], "bias")
+    cat = Fn.PackedAct.empty(S, H * D + n2, dev)
+    cat.data.fill_(7.0)
+    Fn.attention_packed(q, kvp, S, out=cat.cols(0, H * D))
+    Fn.grouped_gemm([(ap, w, b, cat.cols(H * D, H * D + n2), None)], "bias_packed")
+    full = cat.unpack()
+    assert torch.equal(full[:, : H * D], o.view(S, H * D))
+    assert torch.equal(full[:, H * D:], rm)
+    # swiglu_packed into the right half of a wider packed matrix
+    w12 = Fn.pack_weight(_rand((2 * 1024, k2), g, 0.02).to(dev), swiglu_pairs=True)
+    b12 = _rand((2 * 1024,), g, 0.1).to(dev)
+    sw = torch.empty(S, 1024, dtype=BF16, device=dev)
+    Fn.grouped_gemm([(ap, w12, b12, sw, None)], "swiglu")
+    wide = Fn.PackedAct.empty(S, 2048, dev)
+    Fn.grouped_gemm([(ap, w12, b12, wide.cols(1024, 2048), None)], "swiglu_packed")
+    assert torch.equal(wide.unpack()[:, 1024:], sw)
+
+
 def test_ss_fused_mlp_swiglu_op(dev):
     import rldx_amd.ops  # noqa: F401  registers ss::fused_mlp_swiglu
 

@@ -1,0 +1,121 @@
+"""GPU parity of the RLDX-1 MSAT chain (rldx_amd.rldx_msat.RldxMsat: the
+reference's own 24 x 64, 4 DS + 8 SS architecture on the rldx_amd kernels)
+against the CPU oracle (oracle/rldx_msat_ref.py) on the same weights."""
+
+import pytest
+import torch
+
+from oracle import rldx_msat_ref as R
+from rldx_amd import rldx_msat as RM
+from tolerances import assert_bf16_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle(sd, inp, cfg, quirk):
+    cpu = {k: v.cpu() for k, v in sd.items()}
+    return R.msat_forward(cpu, inp["sa"].cpu(), inp["vl"].cpu(), inp["temb"].cpu(), inp["time_token"].cpu(),
+                          heads=cfg.heads, head_dim=cfg.head_dim, ds_blocks=cfg.ds_blocks, ss_blocks=cfg.ss_blocks,
+                          theta=cfg.rope_theta, max_seq_len=cfg.max_seq_len, bf16_quirk=quirk)
+
+
+@pytest.mark.parametrize("quirk", [True, False])
+def test_rldx_msat_one_block_each(dev, quirk):
+    """Bound: the bf16 contract (max-abs 2e-2, rel-L2 1e-2), which presumes
+    unit-scale outputs: proj_out_2 is drawn with std 0.01 so that |y| stays
+    below 2 (with 0.02 the outputs reach 3, where one bf16 ulp is 0.0156 and
+    independently rounded sums differ by up to 0.023)."""
+    cfg = RM.RldxMsatCfg(ds_blocks=1, ss_blocks=1)
+    sd = RM.make_state_dict(cfg, dev, seed=21)
+    sd["proj_out_2.weight"] = (sd["proj_out_2.weight"].float() * 0.5).to(torch.bfloat16)
+    inp = RM.make_inputs(cfg, dev, seed=22)
+    chain = RM.RldxMsat(sd, cfg, dev, bf16_quirk=quirk)
+    o = chain.forward(inp["sa"], inp["vl"], inp["temb"], inp["time_token"]).clone()
+    assert_bf16_close(o, _oracle(sd, inp, cfg, quirk), f"RLDX MSAT 1 DS + 1 SS, quirk={quirk}")
+
+
+def _rel(a, b):
+    return ((a - b).norm() / b.norm()).item()
+
+
+def assert_as_accurate_as_eager_bf16(o, sd, inp, cfg, quirk, what):
+    """Over several blocks the bf16 roundings of any evaluation order compound
+    (the bf16 oracle itself is 6e-3 / 8e-3 / 1.5e-2 rel-L2 from an fp32
+    evaluation at 1+1 / 2+2 / 4+8 blocks).  Bound: the GPU chain is no further
+    from the fp32 evaluation of the same weights and inputs than 1.5x the eager
+    bf16 evaluation is, and its cosine to the bf16 oracle is >= 0.999."""
+    o = o.detach().cpu().double()
+    r16 = _oracle(sd, inp, cfg, quirk).double()
+    sd32 = {k: v.float() for k, v in sd.items()}
+    inp32 = {k: v.float() for k, v in inp.items()}
+    r32 = _oracle(sd32, inp32, cfg, quirk).double()
+    floor, got = _rel(r16, r32), _rel(o, r32)
+    cos = torch.nn.functional.cosine_similarity(o.flatten(), r16.flatten(), dim=0).item()
+    print(f"{what}: rel-L2 to fp32 {got:.2e} (eager bf16: {floor:.2e}), to the bf16 oracle {_rel(o, r16):.2e}, "
+          f"cos {cos:.6f}")
+    assert torch.isfinite(o).all() and got <= 1.5 * floor and cos >= 0.999, what
+
+
+def test_rldx_msat_full_model(dev):
+    """4 DS + 8 SS blocks at the release dimensions."""
+    cfg = RM.RldxMsatCfg()
+    sd = RM.make_state_dict(cfg, dev, seed=31)
+    inp = RM.make_inputs(cfg, dev, seed=32)
+    chain = RM.RldxMsat(sd, cfg, dev)
+    o = chain.forward(inp["sa"], inp["vl"], inp["temb"], inp["time_token"]).clone()
+    assert_as_accurate_as_eager_bf16(o, sd, inp, cfg, True, "full MSAT")
+
+
+def test_rldx_msat_graph_replay(dev):
+    cfg = RM.RldxMsatCfg(ds_blocks=2, ss_blocks=2)
+    sd = RM.make_state_dict(cfg, dev, seed=41)
+    chain = RM.RldxMsat(sd, cfg, dev)
+    chain.capture()
+    for rep in range(3):
+        inp = RM.make_inputs(cfg, dev, seed=50 + rep)
+        for k in ("sa", "vl", "temb", "time_token"):
+            chain.inputs[k].copy_(inp[k])
+        got = chain.replay().clone()
+        torch.cuda.synchronize()
+        eager = chain.forward(inp["sa"], inp["vl"], inp["temb"], inp["time_token"]).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), eager.view(torch.int16)), f"replay {rep}"
+    assert_as_accurate_as_eager_bf16(got, sd, inp, cfg, True, "graph replay, 2 DS + 2 SS")
+
+
+def _module_tree(sd):
+    """nn.Module tree whose state_dict() has exactly the keys of `sd` (what a
+    loaded reference MSAT exposes)."""
+    root = torch.nn.Module()
+    for k, v in sd.items():
+        *path, leaf = k.split(".")
+        m = root
+        for part in path:
+            if not hasattr(m, part):
+                m.add_module(part, torch.nn.Module())
+            m = getattr(m, part)
+        m.register_parameter(leaf, torch.nn.Parameter(v, requires_grad=False))
+    return root
+
+
+def test_install_on_a_module_tree(dev):
+    """install() builds the chain from a live module's state dict and keeps the
+    module's forward(hidden_states, encoder_hidden_states, timestep) signature,
+    with the module's own time embedding and time-token projection."""
+    cfg = RM.RldxMsatCfg(ds_blocks=1, ss_blocks=2)
+    sd = RM.make_state_dict(cfg, dev, seed=61)
+    msat = _module_tree(sd)
+    g = torch.Generator(device=dev).manual_seed(62)
+    wt = (0.02 * torch.randn(cfg.inner, 1, generator=g, device=dev)).to(torch.bfloat16)
+    wtt = (0.02 * torch.randn(cfg.sa_dim, cfg.inner, generator=g, device=dev)).to(torch.bfloat16)
+    msat.timestep_encoder = lambda t: (t[:, None].to(torch.bfloat16) @ wt.t())
+    msat.time_token_proj = lambda temb: temb @ wtt.t()
+    chain = RM.install(msat, n_vl=cfg.n_vl, n_sa_pure=cfg.n_sa_pure, bf16_quirk=True)
+    assert chain.cfg.param_shapes() == cfg.param_shapes()
+    inp = RM.make_inputs(cfg, dev, seed=63)
+    t = torch.tensor([0.25], device=dev)
+    o = msat(inp["sa"], inp["vl"], t).clone()
+    temb = msat.timestep_encoder(t)
+    tt = msat.time_token_proj(temb).unsqueeze(1)
+    ref_inp = dict(sa=inp["sa"], vl=inp["vl"], temb=temb, time_token=tt)
+    assert_as_accurate_as_eager_bf16(o, sd, ref_inp, cfg, True, "installed MSAT forward, 1 DS + 2 SS")

@@ -1,0 +1,129 @@
+"""CPU tests of the RLDX-1 MSAT chain's host side: parameter names and shapes,
+local safetensors loading, RoPE tables against the oracle's eager position ids
+(with and without the bf16 quirk), and the oracle's block structure."""
+
+import torch
+
+from oracle import rldx_msat_ref as R
+from rldx_amd import rldx_msat as RM
+
+
+def _small():
+    return RM.RldxMsatCfg(ds_blocks=1, ss_blocks=1)
+
+
+def test_param_count_matches_the_release():
+    """4 DS + 8 SS blocks at 24 x 64, SA 1536, VL 4096: 1241.9 M parameters read by
+    the chain; the reference reports 1244.6 M for the MSAT with its timestep
+    encoder and time-token projection (rldx/inference/action_model/README.md:11),
+    which the chain takes as inputs (2.7 M)."""
+    n = sum(torch.Size(s).numel() for s in RM.RldxMsatCfg().param_shapes().values())
+    assert n == 1_241_871_184
+    assert 2.0e6 < 1_244_600_000 - n < 3.5e6
+
+
+def test_cfg_from_state_dict_roundtrip():
+    cfg = RM.RldxMsatCfg(ds_blocks=2, ss_blocks=3)
+    shapes = {k: torch.empty(s) for k, s in cfg.param_shapes().items()}
+    got = RM.RldxMsatCfg.from_state_dict(shapes)
+    assert got.param_shapes() == cfg.param_shapes()
+    assert (got.heads, got.head_dim, got.ds_blocks, got.ss_blocks, got.vl_ffn) == (24, 64, 2, 3, 10922)
+
+
+def test_load_msat_state_dict_from_local_safetensors(tmp_path):
+    from safetensors.torch import save_file
+
+    cfg = _small()
+    sd = RM.make_state_dict(cfg, "cpu", seed=3)
+    full = {f"action_model.model.{k}": v for k, v in sd.items()}
+    full["backbone.some.weight"] = torch.zeros(4, dtype=torch.bfloat16)
+    keys = sorted(full)
+    save_file({k: full[k] for k in keys[: len(keys) // 2]}, str(tmp_path / "model-00001.safetensors"))
+    save_file({k: full[k] for k in keys[len(keys) // 2:]}, str(tmp_path / "model-00002.safetensors"))
+    got = RM.load_msat_state_dict(str(tmp_path))
+    assert set(got) == set(sd)
+    assert all(torch.equal(got[k], sd[k]) for k in sd)
+
+
+def _eager_pe(cfg, quirk, single):
+    tabs = R.rope_freq_tables(cfg.head_dim, cfg.rope_theta, cfg.max_seq_len, quirk)
+    N, nv, nt = cfg.tokens, cfg.n_vl, cfg.num_temb_tokens
+    ids = torch.zeros(1, N, 2, dtype=torch.long)
+    ids[:, nv:nv + nt, 1] = torch.arange(nt)
+    start = nt + 1 if single else nt
+    ids[:, nv + nt:, 1] = torch.arange(start, start + cfg.n_sa_pure)
+    return R.rope_pe(tabs, ids)[0]
+
+
+def test_rope_tables_equal_the_eager_embedder_rows():
+    """The chain's DS / SS tables (SA rows) are the eager RoPEEmbedder1D values at
+    the eager position ids (msat.py:376-487); VL rows are the identity there."""
+    cfg = RM.RldxMsatCfg()
+    for quirk in (True, False):
+        for single, pos in ((False, torch.arange(cfg.n_sa)),
+                            (True, torch.cat([torch.arange(1), torch.arange(2, 2 + cfg.n_sa_pure)]))):
+            pe = _eager_pe(cfg, quirk, single)
+            c, s = RM.rope_tables(cfg, pos, quirk)
+            sa = pe[cfg.n_vl:]
+            if quirk:
+                assert sa.dtype == torch.bfloat16
+                assert torch.equal(sa.float(), c) and not s.any()
+                assert torch.equal(pe[: cfg.n_vl].float(), torch.ones_like(pe[: cfg.n_vl].float()))
+            else:
+                assert torch.equal(sa.real, c) and torch.equal(sa.imag, s)
+                assert torch.equal(pe[: cfg.n_vl], torch.ones_like(pe[: cfg.n_vl]))
+
+
+def test_bf16_quirk_is_the_complex_to_bf16_cast():
+    """A bf16 cast of the complex64 buffers keeps the real part (what
+    model.to(torch.bfloat16) does to RoPEEmbedder1D's buffers)."""
+    exact = R.rope_freq_tables(64, 1e4, 64, False)
+    quirk = R.rope_freq_tables(64, 1e4, 64, True)
+    for e, q in zip(exact, quirk):
+        assert torch.equal(e.real.to(torch.bfloat16), q)
+        assert torch.equal(e.to(torch.bfloat16), q)  # torch's complex -> real cast discards imag
+
+
+def test_oracle_blocks_are_residual_with_zero_weights():
+    """With every linear weight and bias zero, a DS block and an SS block return
+    their inputs bit for bit (residual structure; identity modulation)."""
+    cfg = _small()
+    sd = {k: (v if "norm" in k else torch.zeros_like(v)) for k, v in RM.make_state_dict(cfg, "cpu").items()}
+    inp = RM.make_inputs(cfg, "cpu")
+    sa = torch.cat([inp["time_token"], inp["sa"]], dim=1)
+    pe = _eager_pe(cfg, True, False)[None]
+    sa2, vl2 = R.ds_block(sd, "double_blocks.0.", sa, inp["vl"], pe, cfg.heads)
+    assert torch.equal(sa2, sa) and torch.equal(vl2, inp["vl"])
+    x = torch.randn(1, cfg.tokens, cfg.sa_dim).to(torch.bfloat16)
+    assert torch.equal(R.ss_block(sd, "single_blocks.0.", x, pe, cfg.heads), x)
+
+
+def test_oracle_output_projection_closed_form():
+    """Zero blocks: out = proj_out_2(LN(sa) * (1 + scale) + shift), shift | scale =
+    proj_out_1(silu(temb)) — checked in fp64 against the oracle's bf16 chain."""
+    cfg = RM.RldxMsatCfg(ds_blocks=0, ss_blocks=0)
+    sd = RM.make_state_dict(cfg, "cpu", seed=5, std=0.05)
+    inp = RM.make_inputs(cfg, "cpu")
+    o = R.msat_forward(sd, inp["sa"], inp["vl"], inp["temb"], inp["time_token"], heads=24, head_dim=64,
+                       ds_blocks=0, ss_blocks=0)
+    t = inp["temb"].double()
+    ss = torch.nn.functional.silu(t) @ sd["proj_out_1.weight"].double().t() + sd["proj_out_1.bias"].double()
+    shift, scale = ss[:, :1536], ss[:, 1536:]
+    sa = inp["sa"].double()[0]
+    ln = (sa - sa.mean(-1, keepdim=True)) / torch.sqrt(sa.var(-1, unbiased=False, keepdim=True) + 1e-6)
+    y = (ln * (1 + scale) + shift) @ sd["proj_out_2.weight"].double().t() + sd["proj_out_2.bias"].double()
+    assert (o[0].double() - y).abs().max() < 0.05 * y.abs().max()
+
+
+def test_oracle_sa_output_invariant_to_vl_token_order():
+    """VL rows carry identity RoPE and no mask, so the action outputs cannot
+    depend on the order of the cognition tokens (a swapped [VL | SA] order or
+    RoPE on the wrong rows breaks this)."""
+    cfg = RM.RldxMsatCfg(ds_blocks=1, ss_blocks=1)
+    sd = RM.make_state_dict(cfg, "cpu", seed=7)
+    inp = RM.make_inputs(cfg, "cpu", seed=8)
+    kw = dict(heads=24, head_dim=64, ds_blocks=1, ss_blocks=1, bf16_quirk=False)
+    o = R.msat_forward(sd, inp["sa"], inp["vl"], inp["temb"], inp["time_token"], **kw).double()
+    perm = torch.randperm(cfg.n_vl, generator=torch.Generator().manual_seed(0))
+    op = R.msat_forward(sd, inp["sa"], inp["vl"][:, perm], inp["temb"], inp["time_token"], **kw).double()
+    assert (o - op).norm() / o.norm() < 1e-2
