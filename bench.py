@@ -237,6 +237,25 @@ def kernel_lines(torch, reps: int):
                                                         peak=BF16_MFMA_PEAK_TFLOPS, frac=tf / BF16_MFMA_PEAK_TFLOPS,
                                                         flops=W.memory_attention_flops(mc))
 
+    # RLDX-1 action head at the release MSAT shape (24 x 64 heads, 4 DS + 8 SS blocks, SA 1536,
+    # VL 4096, 64 + 18 tokens): state encoder + 4 x (action encoder, MSAT, decoder, Euler), one hipGraph
+    from rldx_amd import rldx_msat as RM
+
+    rmc, rhc = RM.RldxMsatCfg(), RM.RldxHeadCfg()
+    rhead = RM.RldxActionHead(RM.RldxMsat(RM.make_state_dict(rmc, dev), rmc, dev),
+                              RM.make_head_state_dict(rmc, rhc, dev), rhc)
+    gr = torch.Generator(device=dev).manual_seed(14)
+    for t in (rhead.vl, rhead.state, rhead.x0):
+        t.copy_(torch.randn(t.shape, generator=gr, device=dev))
+    ms = graph_time_ms(rhead.run, 1, torch)
+    msat_ms = graph_time_ms(lambda: rhead.msat.forward(rhead.sa, rhead.vl, rhead.sd["static_tembs"][0],
+                                                       rhead.sd["static_time_tokens"][0]), 4, torch)
+    out["rldx_action_head_release_shape"] = dict(
+        ms=ms, msat_forward_ms=msat_ms, unit="ms per action (4 denoising steps)",
+        reference_published_ms=9.66, reference_hardware="RTX 5090, path D (rldx/inference/action_model/README.md:11-18)",
+        msat_params=sum(torch.Size(s_).numel() for s_ in rmc.param_shapes().values()))
+    del rhead
+
     # residual-add + norm epilogues: the reference's block-boundary shapes (launch-bound)
     # and the Qwen3-VL prefill shape 1280 x 2048 (HBM-bound)
     def rows(m, d, std=1.0):

@@ -431,3 +431,115 @@ def install(msat: torch.nn.Module, n_vl: int, n_sa_pure: int, bf16_quirk: Option
     msat.forward = forward
     msat.rldx_amd_chain = chain
     return chain
+
+
+# ---------------------------------------------------------------------------
+# The action head around the MSAT: CustomActionHeadChain.forward without the
+# RTC prefix (rldx/inference/action_model/engine/custom_action_model_chain.py:
+# 81-171): state encoder once, then per denoising step action encoder + baked
+# position embedding, MSAT, action decoder and the Euler update.
+# ---------------------------------------------------------------------------
+@dataclass
+class RldxHeadCfg:
+    """rldx/configs/model/rldx.py:80-112, :111-118."""
+
+    state_dim: int = 64       # max_state_dim
+    action_dim: int = 64      # max_action_dim
+    action_horizon: int = 16
+    hidden_size: int = 1024   # decoder width (= MSAT output_dim)
+    num_embodiments: int = 32
+    steps: int = 4
+
+
+def make_head_state_dict(msat_cfg: RldxMsatCfg, cfg: RldxHeadCfg, device, seed: int = 13) -> dict:
+    """Per-embodiment encoder / decoder parameters under the reference names
+    (embodiment_conditioned_mlp.py CategorySpecificLinear W [E, in, out], b
+    [E, out]; rldx/model/core/rldx.py:82-106), the position embedding, and
+    per-step baked time embeddings / time tokens; bf16."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    E, d, hs = cfg.num_embodiments, msat_cfg.sa_dim, cfg.hidden_size
+
+    def rnd(*shape, std=0.02):
+        return (std * torch.randn(*shape, generator=g, device=device, dtype=torch.float32)).to(BF16)
+
+    sd = {"state_encoder.layer1.W": rnd(E, cfg.state_dim, hs), "state_encoder.layer1.b": rnd(E, hs),
+          "state_encoder.layer2.W": rnd(E, hs, d), "state_encoder.layer2.b": rnd(E, d),
+          "action_encoder.W1.W": rnd(E, cfg.action_dim, d), "action_encoder.W1.b": rnd(E, d),
+          "action_encoder.W2.W": rnd(E, 2 * d, d), "action_encoder.W2.b": rnd(E, d),
+          "action_encoder.W3.W": rnd(E, d, d), "action_encoder.W3.b": rnd(E, d),
+          "action_decoder.layer1.W": rnd(E, msat_cfg.output_dim, hs), "action_decoder.layer1.b": rnd(E, hs),
+          "action_decoder.layer2.W": rnd(E, hs, cfg.action_dim), "action_decoder.layer2.b": rnd(E, cfg.action_dim),
+          "position_embedding.weight": rnd(cfg.action_horizon, d),
+          "static_tembs": rnd(cfg.steps, 1, msat_cfg.inner, std=0.5),
+          "static_time_tokens": rnd(cfg.steps, 1, msat_cfg.num_temb_tokens, d, std=0.5)}
+    return sd
+
+
+def _cat_linear(x, sd, name, e):
+    """CategorySpecificLinear.forward for batch 1 (embodiment_conditioned_mlp.py:49-58)."""
+    return torch.addmm(sd[f"{name}.b"][e], x, sd[f"{name}.W"][e])
+
+
+def sinusoidal_time(t: torch.Tensor, width: int) -> torch.Tensor:
+    """SinusoidalPositionalEncoding.forward (embodiment_conditioned_mlp.py:14-33): [T] -> [T, width] fp32."""
+    half = width // 2
+    exponent = -torch.arange(half, dtype=torch.float, device=t.device) * (torch.log(torch.tensor(10000.0)) / half)
+    freqs = t.float().unsqueeze(-1) * exponent.exp()
+    return torch.cat([torch.sin(freqs), torch.cos(freqs)], dim=-1)
+
+
+class RldxActionHead:
+    """Flow-matching action head of RLDX-1 with the MSAT on the rldx_amd chain;
+    `run` launches one action inference (state encoder + `steps` denoising
+    iterations) on static buffers, `capture` / `replay` as one hipGraph."""
+
+    def __init__(self, msat: RldxMsat, head_sd: dict, cfg: RldxHeadCfg, embodiment: int = 0):
+        self.msat, self.cfg, self.sd, self.e = msat, cfg, head_sd, embodiment
+        dev, mc = msat.dev, msat.cfg
+        Fn._require(mc.n_sa_pure == 1 + cfg.action_horizon, "MSAT SA tokens = state token + action horizon")
+        Fn._require(mc.output_dim == cfg.hidden_size, "MSAT output_dim feeds the action decoder")
+        self.dt = 1.0 / cfg.steps
+        self.timesteps = [t / cfg.steps for t in range(cfg.steps)]
+        e = lambda *s: torch.empty(*s, dtype=BF16, device=dev)  # noqa: E731
+        self.vl, self.state = e(1, mc.n_vl, mc.vl_dim), e(1, 1, cfg.state_dim)
+        self.x0 = e(1, cfg.action_horizon, cfg.action_dim)
+        self.act = e(1, cfg.action_horizon, cfg.action_dim)
+        self.sa = e(1, mc.n_sa_pure, mc.sa_dim)
+        # tau encodings of each step's time, baked (same every call)
+        self.tau = [sinusoidal_time(torch.full((cfg.action_horizon,), t, device=dev), mc.sa_dim).to(BF16)
+                    for t in self.timesteps]
+        self.graph = None
+
+    def run(self) -> torch.Tensor:
+        sd, e, mc = self.sd, self.e, self.msat.cfg
+        h = F.relu(_cat_linear(self.state[0], sd, "state_encoder.layer1", e))
+        self.sa[0, :1].copy_(_cat_linear(h, sd, "state_encoder.layer2", e))
+        self.act.copy_(self.x0)
+        for i in range(self.cfg.steps):
+            a = _cat_linear(self.act[0], sd, "action_encoder.W1", e)
+            x = _cat_linear(torch.cat([a, self.tau[i]], dim=-1), sd, "action_encoder.W2", e)
+            x = x * torch.sigmoid(x)
+            a = _cat_linear(x, sd, "action_encoder.W3", e)
+            torch.add(a, sd["position_embedding.weight"], out=self.sa[0, 1:])
+            out = self.msat.forward(self.sa, self.vl, sd["static_tembs"][i], sd["static_time_tokens"][i])
+            hd = F.relu(_cat_linear(out[0], sd, "action_decoder.layer1", e))
+            v = _cat_linear(hd, sd, "action_decoder.layer2", e)[-self.cfg.action_horizon:]
+            self.act[0].add_(v, alpha=self.dt)
+        return self.act
+
+    def capture(self, warmup: int = 2) -> None:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(warmup):
+                self.run()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.run()
+        torch.cuda.synchronize()
+
+    def replay(self) -> torch.Tensor:
+        self.graph.replay()
+        return self.act

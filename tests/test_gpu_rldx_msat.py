@@ -119,3 +119,56 @@ def test_install_on_a_module_tree(dev):
     tt = msat.time_token_proj(temb).unsqueeze(1)
     ref_inp = dict(sa=inp["sa"], vl=inp["vl"], temb=temb, time_token=tt)
     assert_as_accurate_as_eager_bf16(o, sd, ref_inp, cfg, True, "installed MSAT forward, 1 DS + 2 SS")
+
+
+def _head_reference(head_sd, msat_sd, hc, mc, vl, state, x0, e=0):
+    """CPU composition of CustomActionHeadChain.forward (custom_action_model_chain.py:81-171)
+    from the oracle MSAT and the per-embodiment MLPs of embodiment_conditioned_mlp.py."""
+    f = {k: v.cpu().float() for k, v in head_sd.items()}
+    sd32 = {k: v.cpu().float() for k, v in msat_sd.items()}
+
+    def lin(x, name):  # CategorySpecificLinear, batch 1
+        return x @ f[f"{name}.W"][e] + f[f"{name}.b"][e]
+
+    def tau(t, width):  # SinusoidalPositionalEncoding
+        half = width // 2
+        ex = torch.exp(-torch.arange(half, dtype=torch.float) * (torch.log(torch.tensor(10000.0)) / half))
+        fr = torch.full((hc.action_horizon, 1), t) * ex
+        return torch.cat([torch.sin(fr), torch.cos(fr)], dim=-1)
+
+    state_feat = lin(torch.relu(lin(state.cpu().float()[0], "state_encoder.layer1")), "state_encoder.layer2")
+    act = x0.cpu().float()[0]
+    for i in range(hc.steps):
+        a = lin(act, "action_encoder.W1")
+        x = lin(torch.cat([a, tau(i / hc.steps, mc.sa_dim)], dim=-1), "action_encoder.W2")
+        a = lin(x * torch.sigmoid(x), "action_encoder.W3") + f["position_embedding.weight"]
+        sa = torch.cat([state_feat, a])[None]
+        out = R.msat_forward(sd32, sa, vl.cpu().float(), f["static_tembs"][i], f["static_time_tokens"][i],
+                             heads=mc.heads, head_dim=mc.head_dim, ds_blocks=mc.ds_blocks, ss_blocks=mc.ss_blocks)
+        v = lin(torch.relu(lin(out[0], "action_decoder.layer1")), "action_decoder.layer2")[-hc.action_horizon:]
+        act = act + v / hc.steps
+    return act
+
+
+def test_rldx_action_head_graph_matches_fp32_composition(dev):
+    """State encoder + 2 denoising steps of action encoder, MSAT (1 DS + 1 SS),
+    decoder and Euler update as one hipGraph, against an fp32 CPU composition:
+    the actions agree to rel-L2 <= 2e-2 (bf16 path vs fp32) and replays are bitwise stable."""
+    mc = RM.RldxMsatCfg(ds_blocks=1, ss_blocks=1)
+    hc = RM.RldxHeadCfg(steps=2, num_embodiments=4)
+    sd = RM.make_state_dict(mc, dev, seed=71)
+    hsd = RM.make_head_state_dict(mc, hc, dev, seed=72)
+    head = RM.RldxActionHead(RM.RldxMsat(sd, mc, dev), hsd, hc, embodiment=1)
+    g = torch.Generator(device=dev).manual_seed(73)
+    head.vl.copy_(torch.randn(head.vl.shape, generator=g, device=dev))
+    head.state.copy_(torch.randn(head.state.shape, generator=g, device=dev))
+    head.x0.copy_(torch.randn(head.x0.shape, generator=g, device=dev))
+    head.capture()
+    a1 = head.replay().clone()
+    a2 = head.replay().clone()
+    torch.cuda.synchronize()
+    assert torch.equal(a1.view(torch.int16), a2.view(torch.int16))
+    r = _head_reference(hsd, sd, hc, mc, head.vl, head.state, head.x0, e=1).double()
+    rel = _rel(a1[0].cpu().double(), r)
+    print(f"action head: rel-L2 to the fp32 composition {rel:.2e}")
+    assert torch.isfinite(a1).all() and rel <= 2e-2
