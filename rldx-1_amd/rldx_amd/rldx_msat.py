@@ -32,6 +32,9 @@ Per SingleStreamBlock (7 launches):
     + SwiGLU -> packed; QK-RMSNorm + RoPE; attention -> columns [0, inner) of
     the packed linear2 operand; mlp_proj (+ bias) -> its columns [inner, ...);
     linear2 + residual (in place).
+The GEMMs have 18, 64 or 82 rows, so their launches have only 24-144 output
+tiles: each is split over K (split_for) towards 256 workgroups, partials summed
+in a fixed order in one shared workspace.
 The SwiGLU widths of the double-stream FFNs (SA 4096, VL 10922) are padded
 with zero weight rows / columns to a multiple of 128 (silu(0) * 0 = 0, so the
 padding contributes nothing).  The output projection's tiny modulation
@@ -310,44 +313,110 @@ class RldxMsat:
         self.inputs = dict(sa=ebuf(1, cfg.n_sa_pure, cfg.sa_dim), vl=ebuf(1, nv, cfg.vl_dim),
                            temb=ebuf(1, inner), time_token=ebuf(1, nt, cfg.sa_dim))
         self.graph = None
+        # every GEMM of the forward on its static buffers, with its split-K factor
+        self.ds_gemms = [self._ds_gemm_items(blk) for blk in self.ds]
+        self.ss_gemms = [self._ss_gemm_items(blk) for blk in self.ss]
+        self.vl_proj_gemm = self._planned(
+            [(self.vl_packed, self.vl_proj_to_sa, self.w["vl_proj_to_sa.bias"], self.x[:nv], None)], "bias")
+        self.out_gemm = self._planned(
+            [(self.mod_packed, self.proj_out_2, self.w["proj_out_2.bias"], self.out[0], None)], "bias")
+        plans = [g for d in self.ds_gemms + self.ss_gemms for g in d.values()] + [self.vl_proj_gemm, self.out_gemm]
+        self.ws = Fn.GemmWorkspace(max(Fn.grouped_gemm_workspace_bytes(it, epi, sk) for it, epi, sk in plans),
+                                   self.dev)
 
-    # -- blocks ---------------------------------------------------------------
-    def _ds_block(self, blk: dict) -> None:
+    @staticmethod
+    def split_for(m: int, n: int, k: int) -> int:
+        """Split-K factor for a launch: the 82-, 64- and 18-row GEMMs of this
+        model have 24-344 output tiles; where K is long (>= 4096) a tile
+        streams a long slice of K on one CU, and splitting K by the largest
+        power of two <= min(8, K / 1024) that keeps tiles x split <= 256 (one
+        workgroup per CU) pays; with shorter K the partial-sum traffic costs
+        more than the added workgroups gain.  Measured per GEMM at the release
+        shape (us per launch, weights streaming from HBM, split 1 / chosen):
+        vl_qkv 15.3 / 12.7, sa_w3 11.7 / 9.1, vl_w3 52.1 / 23.9, mlp_proj
+        26.3 / 19.3, linear2 17.1 / 11.1; the short-K GEMMs were fastest
+        unsplit.  Tiles as the planner cuts them: 32 x 64 for up to 32 rows,
+        else 64 x 64."""
+        if k < 4096:
+            return 1
+        tiles = ((m + 31) // 32 if m <= 32 else (m + 63) // 64) * (n // 64)
+        split = 1
+        while split < 8 and split * 2 <= k // 1024 and tiles * split * 2 <= 256:
+            split *= 2
+        return split
+
+    def _planned(self, items, epi):
+        a, w = items[0][0], items[0][1]
+        return (items, epi, self.split_for(a.m, w.n, w.k))
+
+    def _ds_gemm_items(self, blk: dict) -> dict:
         cfg = self.cfg
         nv, N = cfg.n_vl, cfg.tokens
+        return {
+            "sa_qkv": self._planned([(self.h_sa, blk["sa_qkv"], blk["sa_qkv.bias"], self.qkv_sa, None)], "bias"),
+            "vl_qkv": self._planned([(self.h_vl, blk["vl_qkv"], blk["vl_qkv.bias"], self.qkv_vl, None)], "bias"),
+            "sa_proj": self._planned([(self.att.rows(nv, N), blk["sa_proj"], blk["sa_proj.bias"], self.x_sa,
+                                       self.x_sa)], "residual"),
+            "vl_proj": self._planned([(self.att.rows(0, nv), blk["vl_proj"], blk["vl_proj.bias"], self.x_vl,
+                                       self.x_vl)], "residual"),
+            "sa_w12": self._planned([(self.h_sa, blk["sa_w12"], blk["sa_w12.bias"], self.gl_sa, None)],
+                                    "swiglu_packed"),
+            "vl_w12": self._planned([(self.h_vl, blk["vl_w12"], blk["vl_w12.bias"], self.gl_vl, None)],
+                                    "swiglu_packed"),
+            "sa_w3": self._planned([(self.gl_sa, blk["sa_w3"], blk["sa_mlp.w3.bias"], self.x_sa, self.x_sa)],
+                                   "residual"),
+            "vl_w3": self._planned([(self.gl_vl, blk["vl_w3"], blk["vl_mlp.w3.bias"], self.x_vl, self.x_vl)],
+                                   "residual"),
+        }
+
+    def _ss_gemm_items(self, blk: dict) -> dict:
+        inner, hs = self.cfg.inner, self.cfg.ss_hidden
+        return {
+            "qkv": self._planned([(self.h, blk["qkv"], blk["qkv.bias"], self.qkv, None)], "bias"),
+            "mlp": self._planned([(self.h, blk["mlp"], blk["mlp.bias"], self.gl, None)], "swiglu_packed"),
+            "mlp_proj": self._planned([(self.gl, blk["mlp_proj"], blk["mlp_proj.bias"], self.cat.cols(inner, inner + hs),
+                                        None)], "bias_packed"),
+            "linear2": self._planned([(self.cat, blk["linear2"], blk["linear2.bias"], self.x, self.x)], "residual"),
+        }
+
+    def _gemm(self, plan) -> None:
+        items, epi, split = plan
+        Fn.grouped_gemm(items, epi, split_k=split, workspace=self.ws if split > 1 else None)
+
+    # -- blocks ---------------------------------------------------------------
+    def _ds_block(self, blk: dict, gm: dict) -> None:
+        cfg = self.cfg
+        N = cfg.tokens
         Fn.layernorm_pack(self.x_sa, cfg.eps, out=self.h_sa)
         Fn.layernorm_pack(self.x_vl, cfg.eps, out=self.h_vl)
-        Fn.grouped_gemm([(self.h_sa, blk["sa_qkv"], blk["sa_qkv.bias"], self.qkv_sa, None)], "bias")
-        Fn.grouped_gemm([(self.h_vl, blk["vl_qkv"], blk["vl_qkv.bias"], self.qkv_vl, None)], "bias")
+        self._gemm(gm["sa_qkv"])
+        self._gemm(gm["vl_qkv"])
         specs = [Fn.StreamSpec(self.qkv_vl, blk["q_norm_vl.weight"], blk["k_norm_vl.weight"]),
                  Fn.StreamSpec(self.qkv_sa, blk["q_norm_sa.weight"], blk["k_norm_sa.weight"], self.ds_cos,
                                self.ds_sin)]
         Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
         Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), N, out=self.att)
-        Fn.grouped_gemm([(self.att.rows(nv, N), blk["sa_proj"], blk["sa_proj.bias"], self.x_sa, self.x_sa)],
-                        "residual")
-        Fn.grouped_gemm([(self.att.rows(0, nv), blk["vl_proj"], blk["vl_proj.bias"], self.x_vl, self.x_vl)],
-                        "residual")
+        self._gemm(gm["sa_proj"])
+        self._gemm(gm["vl_proj"])
         Fn.layernorm_pack(self.x_sa, cfg.eps, out=self.h_sa)
         Fn.layernorm_pack(self.x_vl, cfg.eps, out=self.h_vl)
-        Fn.grouped_gemm([(self.h_sa, blk["sa_w12"], blk["sa_w12.bias"], self.gl_sa, None)], "swiglu_packed")
-        Fn.grouped_gemm([(self.h_vl, blk["vl_w12"], blk["vl_w12.bias"], self.gl_vl, None)], "swiglu_packed")
-        Fn.grouped_gemm([(self.gl_sa, blk["sa_w3"], blk["sa_mlp.w3.bias"], self.x_sa, self.x_sa)], "residual")
-        Fn.grouped_gemm([(self.gl_vl, blk["vl_w3"], blk["vl_mlp.w3.bias"], self.x_vl, self.x_vl)], "residual")
+        self._gemm(gm["sa_w12"])
+        self._gemm(gm["vl_w12"])
+        self._gemm(gm["sa_w3"])
+        self._gemm(gm["vl_w3"])
 
-    def _ss_block(self, blk: dict) -> None:
+    def _ss_block(self, blk: dict, gm: dict) -> None:
         cfg = self.cfg
         nv, N, inner = cfg.n_vl, cfg.tokens, cfg.inner
         Fn.layernorm_pack(self.x, cfg.eps, out=self.h)
-        Fn.grouped_gemm([(self.h, blk["qkv"], blk["qkv.bias"], self.qkv, None)], "bias")
-        Fn.grouped_gemm([(self.h, blk["mlp"], blk["mlp.bias"], self.gl, None)], "swiglu_packed")
+        self._gemm(gm["qkv"])
+        self._gemm(gm["mlp"])
         specs = [Fn.StreamSpec(self.qkv[:nv], blk["q_norm"], blk["k_norm"]),
                  Fn.StreamSpec(self.qkv[nv:], blk["q_norm"], blk["k_norm"], self.ss_cos, self.ss_sin)]
         Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
         Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), N, out=self.cat.cols(0, inner))
-        Fn.grouped_gemm([(self.gl, blk["mlp_proj"], blk["mlp_proj.bias"],
-                          self.cat.cols(inner, inner + cfg.ss_hidden), None)], "bias_packed")
-        Fn.grouped_gemm([(self.cat, blk["linear2"], blk["linear2.bias"], self.x, self.x)], "residual")
+        self._gemm(gm["mlp_proj"])
+        self._gemm(gm["linear2"])
 
     # -- forward --------------------------------------------------------------
     def forward(self, hidden_states: torch.Tensor, encoder_hidden_states: torch.Tensor, temb: torch.Tensor,
@@ -365,21 +434,20 @@ class RldxMsat:
         self.x_sa[:nt].copy_(time_token[0])
         self.x_sa[nt:].copy_(hidden_states[0])
         self.x_vl.copy_(encoder_hidden_states[0])
-        for blk in self.ds:
-            self._ds_block(blk)
+        for blk, gm in zip(self.ds, self.ds_gemms):
+            self._ds_block(blk, gm)
         # x = [vl_proj_to_sa(vl) | time token | SA]
         Fn.pack_act(self.x_vl, out=self.vl_packed)
-        Fn.grouped_gemm([(self.vl_packed, self.vl_proj_to_sa, self.w["vl_proj_to_sa.bias"], self.x[:nv], None)],
-                        "bias")
+        self._gemm(self.vl_proj_gemm)
         self.x[nv:].copy_(self.x_sa)
-        for blk in self.ss:
-            self._ss_block(blk)
+        for blk, gm in zip(self.ss, self.ss_gemms):
+            self._ss_block(blk, gm)
         # AdaLN output projection (msat.py:777-781)
         shift, scale = F.linear(F.silu(temb), self.w["proj_out_1.weight"], self.w["proj_out_1.bias"]).chunk(2, dim=1)
         sa = F.layer_norm(self.x[cfg.tokens - cfg.n_sa_pure:], (cfg.sa_dim,), eps=1e-6)
         torch.add(sa * (1 + scale), shift, out=self.mod)
         Fn.pack_act(self.mod, out=self.mod_packed)
-        Fn.grouped_gemm([(self.mod_packed, self.proj_out_2, self.w["proj_out_2.bias"], self.out[0], None)], "bias")
+        self._gemm(self.out_gemm)
         return self.out
 
     __call__ = forward
