@@ -631,11 +631,8 @@ __global__ __launch_bounds__(256) void rows_pack_kernel(const uint16_t* __restri
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
 #pragma unroll
-      for (int i = 0; i < 8; i += 2) {
-        const uint32_t lo = f32_to_bf16_bits((v[c][i] - mean) * rstd);
-        const uint32_t hi = f32_to_bf16_bits((v[c][i + 1] - mean) * rstd);
-        raw[c][i >> 1] = lo | (hi << 16);
-      }
+      for (int i = 0; i < 8; i += 2)  // one RNE rounding per element (v_cvt_pk_bf16_f32)
+        raw[c][i >> 1] = pack_bf16x2((v[c][i] - mean) * rstd, (v[c][i + 1] - mean) * rstd);
     }
   }
 #pragma unroll

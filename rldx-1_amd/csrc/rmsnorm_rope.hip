@@ -192,6 +192,8 @@ struct MsatStream {
   int64_t rope_ld;       // row stride of cos/sin (elements)
 };
 
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
 struct MsatArgs {
   MsatStream s[3];
   int num_streams;
@@ -211,6 +213,9 @@ struct MsatArgs {
   int64_t kvp_sh;  // head stride in elements
   int64_t qk_blocks;
   int64_t kv_tiles;  // 32-token tiles per head
+  // 32-bit index math of the norm role (host-checked: its threads < 2^31)
+  uint32_t per_kind;  // m_total * heads
+  DivMagic dm_kind, dm_heads;
 };
 
 // Element offset of K[key][d0 .. d0+7] inside the packed tiles of one head:
@@ -273,25 +278,26 @@ __global__ __launch_bounds__(256) void msat_qkv_norm_rope_kernel(MsatArgs a) {
     msat_kv_pack_block<D>(a, static_cast<int64_t>(blockIdx.x) - a.qk_blocks);
     return;
   }
-  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  // 32-bit index math with invariant-divisor multiplies (a 64-bit division by
+  // the run-time row / head counts costs a few hundred instructions per thread)
+  const uint32_t tid = blockIdx.x * blockDim.x + threadIdx.x;
   const int lane_in_row = static_cast<int>(tid % LPR);
-  const int64_t item = tid / LPR;
-  const bool valid = item < a.total_items;
-  const int64_t it = valid ? item : 0;
+  const uint32_t item = tid / LPR;
+  const bool valid = item < static_cast<uint64_t>(a.total_items);
+  const uint32_t it = valid ? item : 0;
   // item -> (which, m, h); h fastest so a wave walks consecutive heads of one token.
-  const int64_t per_kind = a.m_total * a.heads;
-  const int which = static_cast<int>(it / per_kind);  // 0=q 1=k 2=v
-  const int64_t rem = it - which * per_kind;
-  const int64_t m = rem / a.heads;
-  const int64_t h = rem - m * a.heads;
+  const uint32_t which = div_u32(it, a.dm_kind);  // 0=q 1=k 2=v
+  const uint32_t rem = it - which * a.per_kind;
+  const uint32_t m = div_u32(rem, a.dm_heads);
+  const uint32_t h = rem - m * static_cast<uint32_t>(a.heads);
   int si = 0;
   if (a.num_streams > 1 && m >= a.s[1].m_begin) si = 1;
   if (a.num_streams > 2 && m >= a.s[2].m_begin) si = 2;
   const MsatStream& S = a.s[si];
-  const int64_t row = m - S.m_begin;
+  const int64_t row = static_cast<int64_t>(m) - S.m_begin;
   const int64_t inner = a.heads * D;
   const int d0 = lane_in_row * V;
-  const uint16_t* src = S.qkv + row * S.ld + which * inner + h * D + d0;
+  const uint16_t* src = S.qkv + row * S.ld + which * inner + static_cast<int64_t>(h) * D + d0;
   uint16_t* dst = (a.kvp != nullptr && which == 1)
                       ? a.kvp + h * a.kvp_sh + packed_k_offset(m, d0, D)
                       : (which == 0 ? a.q_out : which == 1 ? a.k_out : a.v_out) + h * a.o_sh + m * a.o_sm + d0;
@@ -300,10 +306,13 @@ __global__ __launch_bounds__(256) void msat_qkv_norm_rope_kernel(MsatArgs a) {
   if (which == 2) {  // V passthrough (uniform per row group, but shuffles below need all lanes)
     if (valid) *reinterpret_cast<uint4*>(dst) = raw;
   }
-  const uint16_t* e = reinterpret_cast<const uint16_t*>(&raw);
+  const uint32_t* e = reinterpret_cast<const uint32_t*>(&raw);
   float x[V];
 #pragma unroll
-  for (int i = 0; i < V; ++i) x[i] = bf16_bits_to_f32(e[i]);
+  for (int i = 0; i < V / 2; ++i) {
+    x[2 * i] = bf16x2_lo(e[i]);
+    x[2 * i + 1] = bf16x2_hi(e[i]);
+  }
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < V; ++i) ss += x[i] * x[i];
@@ -311,32 +320,36 @@ __global__ __launch_bounds__(256) void msat_qkv_norm_rope_kernel(MsatArgs a) {
   for (int mm = LPR / 2; mm >= 1; mm >>= 1) ss += shfl_xor_f(ss, mm);
   if (which == 2 || !valid) return;
 
-  const uint16_t* w = which == 0 ? S.q_w : S.k_w;
+  const uint4 wraw = *reinterpret_cast<const uint4*>((which == 0 ? S.q_w : S.k_w) + d0);
+  const uint32_t* wv = reinterpret_cast<const uint32_t*>(&wraw);
   float y[V];
   {
 #pragma clang fp contract(off)
     const float rinv = 1.0f / __builtin_sqrtf(ss * (1.0f / D) + a.eps);
 #pragma unroll
-    for (int i = 0; i < V; ++i) y[i] = round_bf16(bf16_bits_to_f32(w[d0 + i]) * (x[i] * rinv));
+    for (int i = 0; i < V / 2; ++i) {
+      // y = bf16(w * (x * rinv)) (one rounding, RNE)
+      const uint32_t yp = pack_bf16x2(bf16x2_lo(wv[i]) * (x[2 * i] * rinv), bf16x2_hi(wv[i]) * (x[2 * i + 1] * rinv));
+      y[2 * i] = bf16x2_lo(yp);
+      y[2 * i + 1] = bf16x2_hi(yp);
+    }
   }
   uint4 outraw;
-  uint16_t* o = reinterpret_cast<uint16_t*>(&outraw);
+  uint32_t* o = reinterpret_cast<uint32_t*>(&outraw);
   if (S.cos != nullptr) {
 #pragma clang fp contract(off)
-    const float* cp = S.cos + row * S.rope_ld + d0 / 2;
-    const float* sp = S.sin + row * S.rope_ld + d0 / 2;
+    const floatx4 c = *reinterpret_cast<const floatx4*>(S.cos + row * S.rope_ld + d0 / 2);
+    const floatx4 sn = *reinterpret_cast<const floatx4*>(S.sin + row * S.rope_ld + d0 / 2);
 #pragma unroll
     for (int p = 0; p < V / 2; ++p) {
-      const float c = cp[p], s = sp[p];
       const float re = y[2 * p], im = y[2 * p + 1];
-      const float ore = re * c - im * s;
-      const float oim = re * s + im * c;
-      o[2 * p] = f32_to_bf16_bits(ore);
-      o[2 * p + 1] = f32_to_bf16_bits(oim);
+      const float ore = re * c[p] - im * sn[p];
+      const float oim = re * sn[p] + im * c[p];
+      o[p] = pack_bf16x2(ore, oim);
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < V; ++i) o[i] = f32_to_bf16_bits(y[i]);
+    for (int p = 0; p < V / 2; ++p) o[p] = pack_bf16x2(y[2 * p], y[2 * p + 1]);
   }
   *reinterpret_cast<uint4*>(dst) = outraw;
 }
@@ -444,7 +457,8 @@ extern "C" hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* str
     const rldx_msat_stream_t& s = streams[i];
     if (s.rows < 0) return hipErrorInvalidValue;
     if (s.rows == 0) continue;
-    if (!s.qkv || !s.q_norm_w || !s.k_norm_w || !al16(s.qkv)) return hipErrorInvalidValue;
+    if (!s.qkv || !s.q_norm_w || !s.k_norm_w || !al16(s.qkv) || !al16(s.q_norm_w) || !al16(s.k_norm_w))
+      return hipErrorInvalidValue;
     if (s.qkv_row_stride < 3 * heads * head_dim || s.qkv_row_stride % 8) return hipErrorInvalidValue;
     if ((s.rope_cos == nullptr) != (s.rope_sin == nullptr)) return hipErrorInvalidValue;
     if (s.rope_cos && (!al16(s.rope_cos) || !al16(s.rope_sin) || s.rope_row_stride < head_dim / 2 ||
@@ -469,6 +483,10 @@ extern "C" hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* str
   a.total_items = (kv_packed ? 2 : 3) * heads * m;
   const int64_t threads = a.total_items * (head_dim / 8);
   a.qk_blocks = (threads + 255) / 256;
+  if (a.qk_blocks * 256 + heads * ((m + 31) / 32) * 256 > (int64_t{1} << 31) - 1) return hipErrorInvalidValue;
+  a.per_kind = static_cast<uint32_t>(m * heads);
+  a.dm_kind = div_magic(a.per_kind);
+  a.dm_heads = div_magic(static_cast<uint32_t>(heads));
   a.kvp = static_cast<uint16_t*>(kv_packed);
   a.kvp_sh = kv_packed_head_stride;
   a.kv_tiles = (m + 31) / 32;
