@@ -54,8 +54,12 @@ def test_pack_weight_layout(dev, n, k, pairs):
     assert torch.equal(p.data.cpu(), packed_weight_layout(w, pairs))
 
 
-@pytest.mark.parametrize("ms,n,k", [((512, 64, 32), 4608, 1536), ((5, 100, 130), 192, 512), ((1,), 64, 512)])
+@pytest.mark.parametrize("ms,n,k", [((512, 64, 32), 4608, 1536), ((5, 100, 130), 192, 512), ((1,), 64, 512),
+                                    ((20,), 128, 384), ((300, 40), 256, 640)])
 def test_grouped_gemm_bias(dev, ms, n, k):
+    """Includes K ranges of an odd number of 2-k-step stages (20 rows, K 384:
+    3 stages of the 32-row tiles' four K-groups), which the one-workgroup-per-CU
+    launches run in 2-k-step stages instead of 4."""
     g = torch.Generator().manual_seed(sum(ms) + n)
     items, refs = [], []
     for m in ms:
