@@ -84,10 +84,10 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __rest
 // Tile configuration: MB x NB blocks of 32 x 32; each wave covers one m-block
 // and BNW n-blocks; the 8 waves form KG K-groups (stage s of group g covers
 // k-steps (s KG + g) U .. + U - 1); NSLOT stages of the LDS ring.
-template <int MB_, int NB_, int BNW_, int NSLOT_, int U_ = 2>
+template <int MB_, int NB_, int BNW_, int NSLOT_>
 struct TileCfg {
   static constexpr int MB = MB_, NB = NB_, BNW = BNW_, NSLOT = NSLOT_;
-  static constexpr int U = U_;                      // k-steps per stage
+  static constexpr int U = 2;                       // k-steps per stage
   static constexpr int WN = NB / BNW;               // waves along n
   static constexpr int WPG = MB * WN;               // waves per K-group
   static constexpr int KG = 8 / WPG;                // K-groups
@@ -104,23 +104,17 @@ using Cfg64 = TileCfg<2, 2, 1, 4>;
 using Cfg32 = TileCfg<1, 2, 1, 3>;
 // Deep rings for launches of at most one workgroup per CU: one workgroup alone
 // on a CU is latency-bound with the rings above (~48 KB of loads in flight,
-// about half of what a CU can stream); these keep ~96-112 KB in flight, in
-// stages of 4 k-steps (half the barriers per byte of 2-k-step stages) where a
-// split's K range holds whole 4-k-step stages, else in 2-k-step stages.
-using Cfg128D = TileCfg<4, 4, 2, 4, 4>;
-using Cfg64D = TileCfg<2, 2, 1, 4, 4>;
-using Cfg32D = TileCfg<1, 2, 1, 3, 4>;
-using Cfg128D2 = TileCfg<4, 4, 2, 8>;
-using Cfg64D2 = TileCfg<2, 2, 1, 8>;
-using Cfg32D2 = TileCfg<1, 2, 1, 6>;
+// about half of what a CU can stream); these keep ~96-112 KB in flight.
+using Cfg128D = TileCfg<4, 4, 2, 8>;
+using Cfg64D = TileCfg<2, 2, 1, 8>;
+using Cfg32D = TileCfg<1, 2, 1, 6>;
 
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 template <class C>
 constexpr int lds_bytes() { return cmax(C::RING * 1024, C::KG * C::TILE * 4); }
 constexpr int kLdsBytes = cmax(lds_bytes<Cfg128>(), cmax(lds_bytes<Cfg64>(), lds_bytes<Cfg32>()));
 static_assert(kLdsBytes <= 80 * 1024, "two workgroups per CU");
-constexpr int kLdsDeep = cmax(cmax(lds_bytes<Cfg128D>(), cmax(lds_bytes<Cfg64D>(), lds_bytes<Cfg32D>())),
-                               cmax(lds_bytes<Cfg128D2>(), cmax(lds_bytes<Cfg64D2>(), lds_bytes<Cfg32D2>())));
+constexpr int kLdsDeep = cmax(lds_bytes<Cfg128D>(), cmax(lds_bytes<Cfg64D>(), lds_bytes<Cfg32D>()));
 static_assert(kLdsDeep <= 160 * 1024 && kLdsDeep >= kLdsBytes, "one workgroup per CU");
 
 struct Group {
@@ -151,10 +145,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const uint16_t* p, int by
 // assembly: a release fence would also wait for every LDS-bound load.
 template <int N>
 __device__ __forceinline__ void wait_barrier() {
-  static_assert(N == 0 || N == 3 || N == 4 || N == 6 || N == 8 || N == 12, "vmcnt immediate");
+  static_assert(N == 0 || N == 3 || N == 4 || N == 12, "vmcnt immediate");
   if constexpr (N == 12) asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if constexpr (N == 3) asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -172,11 +164,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   const int tile = item / G.splits, split = item % G.splits;
   const int mt = tile % G.m_tiles, nt = tile / G.m_tiles;
   const int ksteps = a.k / 16;
-  // G.ls_per counts stages of 2 k-steps (the planner's unit); a configuration
-  // with U-k-step stages has ls_per * 2 / U of them (its dispatch checks that
-  // this divides)
-  const int lstages = G.ls_per * 2 / U;  // K-group stages of this split
-  const int st0 = split * lstages;       // its first stage
+  const int lstages = G.ls_per;         // K-group stages of this split
+  const int st0 = split * G.ls_per;     // its first stage
   const int mblocks = (G.m + 31) / 32, nblocks = a.n / 32;
 
   // The chunks this wave loads per stage: q = wl + j WPG, k-step q / CH, chunk
@@ -235,14 +224,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
       if (st + r >= lstages) break;
       dma(st + r + NSLOT - 1, slot_dma);  // past the last stage: re-loads it into a free slot
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int u = 0; u < U - 1; ++u) mma(r, u);
+      mma(r, 0);
       __builtin_amdgcn_sched_barrier(0);
       wait_barrier<(NSLOT - 2) * C::ND>();  // stage st + r + 1 is in LDS
       __builtin_amdgcn_sched_barrier(0);
       lread(r ^ 1, slot_next);  // past the last stage: read, never used
       __builtin_amdgcn_sched_barrier(0);
-      mma(r, U - 1);
+      mma(r, 1);
       __builtin_amdgcn_sched_barrier(0);
       slot_next = slot_next + 1 == NSLOT ? 0 : slot_next + 1;
       slot_dma = slot_dma + 1 == NSLOT ? 0 : slot_dma + 1;
@@ -409,17 +397,12 @@ __global__ __launch_bounds__(kThreads, DEEP ? 1 : 2) void gemm_kernel(GemmArgs a
   const int item = (r % kXcds) * G.per_xcd + r / kXcds;  // XCD r % 8 takes a contiguous run of tiles
   if (item >= G.items) return;
   if constexpr (DEEP) {
-    const bool u4 = G.ls_per % 2 == 0;  // whole 4-k-step stages in the split's K range
-    if (G.cfg == kTile128) {
-      if (u4) gemm_tile<Cfg128D, EPI>(a, G, item, lds);
-      else gemm_tile<Cfg128D2, EPI>(a, G, item, lds);
-    } else if (G.cfg == kTile64) {
-      if (u4) gemm_tile<Cfg64D, EPI>(a, G, item, lds);
-      else gemm_tile<Cfg64D2, EPI>(a, G, item, lds);
-    } else {
-      if (u4) gemm_tile<Cfg32D, EPI>(a, G, item, lds);
-      else gemm_tile<Cfg32D2, EPI>(a, G, item, lds);
-    }
+    if (G.cfg == kTile128)
+      gemm_tile<Cfg128D, EPI>(a, G, item, lds);
+    else if (G.cfg == kTile64)
+      gemm_tile<Cfg64D, EPI>(a, G, item, lds);
+    else
+      gemm_tile<Cfg32D, EPI>(a, G, item, lds);
   } else {
     if (G.cfg == kTile128)
       gemm_tile<Cfg128, EPI>(a, G, item, lds);
