@@ -411,6 +411,29 @@ hipError_t rldx_grouped_gemm_ws_bf16(const rldx_gemm_group_t* groups, int32_t nu
                                      int32_t epilogue, int32_t split_k, void* workspace, int64_t workspace_bytes,
                                      hipStream_t stream);
 
+/*
+ * The QKV linears of an MSAT block with the QK-RMSNorm + RoPE + K/V tiling of
+ * rldx_msat_qkv_norm_rope_bf16 in the GEMM's epilogue (one launch instead of
+ * two): for 1..3 groups in joint-sequence order, y_s = a_s W_s^T + bias_s with
+ * W_s [3 * heads * 128, k] packed, y = [Q | K | V] per row; groups[i].out / ldo /
+ * residual are unused.  norms[i] gives stream i's Q / K norm weights and RoPE
+ * tables (its qkv / qkv_row_stride are unused; rows == groups[i].m).  Q is
+ * written as (H, M, 128) at q_out with strides {q_head_stride, q_row_stride},
+ * K and V as the packed K/V tiles at kv_packed + h * kv_packed_head_stride
+ * (padding keys zero).  Every group but the last non-empty one has rows % 32 == 0
+ * (a 32-key tile holds one stream); head_dim == 128; k % 128 == 0.  Results are
+ * bit-identical to rldx_grouped_gemm_bf16 (RLDX_GEMM_EPI_BIAS) followed by
+ * rldx_msat_qkv_norm_rope_bf16 with kv_packed.
+ * Replaces: the QKV nn.Linear calls of an MSAT block followed by its
+ *   QK-RMSNorm + RoPE kernel (rldx/model/modules/action_model/blocks.py:525-537;
+ *   rldx/inference/action_model/double_stream/engine/kernels/rmsnorm_rope_ds_3way.py:22-386).
+ */
+hipError_t rldx_grouped_gemm_qkv_norm_rope_bf16(const rldx_gemm_group_t* groups, const rldx_msat_stream_t* norms,
+                                                int32_t num_groups, int64_t heads, int64_t head_dim, int64_t k,
+                                                void* q_out, int64_t q_head_stride, int64_t q_row_stride,
+                                                void* kv_packed, int64_t kv_packed_head_stride, float eps,
+                                                hipStream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Host-side diagnostics (no reference counterpart)                         */
 /* ------------------------------------------------------------------------ */

@@ -45,6 +45,8 @@
 //     launched heaviest first; two workgroups fit on a CU (<= 72 KB LDS,
 //     <= 128 VGPRs), so the short streams' weight streaming runs beside the
 //     long stream's tiles.
+#include <type_traits>
+
 #include "rldx_amd.h"
 #include "rldx_common.h"
 
@@ -60,9 +62,9 @@ constexpr int kXcds = 8;
 constexpr int kThreads = 512;          // 8 waves per workgroup
 constexpr int kBufWord3 = 0x00020000;  // gfx9 raw buffer descriptor, word 3 (untyped dword data)
 
-enum { kEpiBias = 0, kEpiResidual = 1, kEpiSwiglu = 2, kEpiSwigluPacked = 3, kEpiBiasPacked = 4 };
+enum { kEpiBias = 0, kEpiResidual = 1, kEpiSwiglu = 2, kEpiSwigluPacked = 3, kEpiBiasPacked = 4, kEpiQkv = 5 };
 constexpr bool packed_out(int epi) { return epi == kEpiSwigluPacked || epi == kEpiBiasPacked; }
-enum { kTile128 = 0, kTile64 = 1, kTile32 = 2 };
+enum { kTile128 = 0, kTile64 = 1, kTile32 = 2, kTile64x128 = 3, kTile32x128 = 4 };
 
 __device__ __forceinline__ float bf(uint16_t b) { return bf16_bits_to_f32(b); }
 
@@ -102,12 +104,20 @@ struct TileCfg {
 using Cfg128 = TileCfg<4, 4, 2, 4>;
 using Cfg64 = TileCfg<2, 2, 1, 4>;
 using Cfg32 = TileCfg<1, 2, 1, 3>;
+// Whole 128-column heads for the QKV epilogue on streams too short for 128 x
+// 128 tiles: 64 x 128 (waves 2 x 2, two K-groups) and 32 x 128 (waves 1 x 2,
+// four K-groups) -- the K-groups of 64 x 64 and 32 x 64, so the sums are the
+// same as theirs, bit for bit.
+using Cfg64x128 = TileCfg<2, 4, 2, 3>;
+using Cfg32x128 = TileCfg<1, 4, 2, 2>;
 // Deep rings for launches of at most one workgroup per CU: one workgroup alone
 // on a CU is latency-bound with the rings above (~48 KB of loads in flight,
 // about half of what a CU can stream); these keep ~96-112 KB in flight.
 using Cfg128D = TileCfg<4, 4, 2, 8>;
 using Cfg64D = TileCfg<2, 2, 1, 8>;
 using Cfg32D = TileCfg<1, 2, 1, 6>;
+using Cfg64x128D = TileCfg<2, 4, 2, 6>;
+using Cfg32x128D = TileCfg<1, 4, 2, 3>;
 
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 template <class C>
@@ -116,6 +126,9 @@ constexpr int kLdsBytes = cmax(lds_bytes<Cfg128>(), cmax(lds_bytes<Cfg64>(), lds
 static_assert(kLdsBytes <= 80 * 1024, "two workgroups per CU");
 constexpr int kLdsDeep = cmax(lds_bytes<Cfg128D>(), cmax(lds_bytes<Cfg64D>(), lds_bytes<Cfg32D>()));
 static_assert(kLdsDeep <= 160 * 1024 && kLdsDeep >= kLdsBytes, "one workgroup per CU");
+constexpr int kLdsQkv = cmax(lds_bytes<Cfg128>(), cmax(lds_bytes<Cfg64x128>(), lds_bytes<Cfg32x128>()));
+constexpr int kLdsQkvDeep = cmax(lds_bytes<Cfg128D>(), cmax(lds_bytes<Cfg64x128D>(), lds_bytes<Cfg32x128D>()));
+static_assert(kLdsQkv <= 80 * 1024 && kLdsQkvDeep <= 160 * 1024, "QKV epilogue tiles");
 
 struct Group {
   const uint16_t* a;  // packed activations
@@ -129,12 +142,28 @@ struct Group {
   int splits, ls_per;           // K splits across workgroups; K-group stages per split
   float* part;                  // split partials [tile][split][PER][512 threads][V]
   unsigned* cnt;                // per-tile arrival counters (zero between launches)
+  // QKV epilogue: first row of the stream in the joint sequence, its Q / K
+  // RMSNorm weights [128] and fp32 RoPE tables [m, 64] (row stride rope_ld) or null
+  int m_begin, rope_ld;
+  const uint16_t *qn_w, *kn_w;
+  const float *cos, *sin;
+};
+
+// Outputs of the QKV epilogue: Q (H, M, 128) with strides (q_sh, q_sm), and the
+// packed K/V tiles of the attention kernel, head h at kvp + h * kvp_sh.
+struct QkvOut {
+  uint16_t* q;
+  uint16_t* kvp;
+  int64_t q_sh, q_sm, kvp_sh;
+  int inner;  // heads * 128: columns of each of Q, K, V
+  float eps;
 };
 
 struct GemmArgs {
   Group g[3];
   int num_groups;
   int n, k;  // n = rows of W (2 * N_half with the SwiGLU epilogue)
+  QkvOut qkv;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const uint16_t* p, int bytes) {
@@ -145,8 +174,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const uint16_t* p, int by
 // assembly: a release fence would also wait for every LDS-bound load.
 template <int N>
 __device__ __forceinline__ void wait_barrier() {
-  static_assert(N == 0 || N == 3 || N == 4 || N == 12, "vmcnt immediate");
+  static_assert(N == 0 || N == 3 || N == 4 || N == 5 || N == 12, "vmcnt immediate");  // (NSLOT - 2) * ND
   if constexpr (N == 12) asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (N == 5) asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if constexpr (N == 3) asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -292,6 +322,111 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
       v[4 + i] = hi[i];
     }
   };
+  if constexpr (EPI == kEpiQkv) {
+    // The tile's 128 columns are one head of Q, K or V (columns n0.. of
+    // [Q | K | V]).  Q / K rows: x = bf16(acc + bias), then the per-head RMSNorm
+    // y = bf16(w * (x * rsqrt(mean(x^2) + eps))) and, on streams with tables, the
+    // interleaved RoPE rounded once: msat_qkv_norm_rope_kernel's arithmetic with
+    // its partition of a row (16 lanes of 8 columns), so the result is the same
+    // bit for bit as this GEMM's bias epilogue followed by that kernel.  Q goes to
+    // (H, M, 128); K rows to their lanes of the packed tiles.  V is read down the
+    // fp32 tile's columns (8 keys of one column per 16-byte chunk) straight into
+    // the packed V chunks.  Keys of the stream's last 32-key tile past its rows
+    // are written as zeros (padding keys of the attention).
+    static_assert(OC == 128 && R * CPR == PER * kThreads, "QKV tiles are whole 128-column heads");
+    constexpr int D = OC;
+    const QkvOut& O = a.qkv;
+    const int n0 = nt * D;
+    const int which = n0 / O.inner;  // uniform per tile
+    const int h = (n0 - which * O.inner) / D;
+    uint16_t* kvh = O.kvp + h * O.kvp_sh;
+    if (which == 2) {
+      constexpr int NCH = D / 16;  // 1 KB chunks per K or V part of a tile
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int s = static_cast<int>(threadIdx.x) + kThreads * i;
+        const int kt = s / (NCH * 64), idx = s % (NCH * 64);
+        const int cx = idx >> 6, l = idx & 63;
+        // chunk cx = 2 db + s2, lane l, element e: V[16 s2 + 8 (e / 4) + 4 (l / 32) + e % 4][32 db + l % 32]
+        const int d = 32 * (cx >> 1) + (l & 31);
+        const int rb = 32 * kt + 16 * (cx & 1) + 4 * (l >> 5);
+        const int row0 = mt * R + 32 * kt;  // first stream row of this 32-key tile
+        if (row0 >= G.m) continue;
+        const float bd = G.bias ? bf(G.bias[n0 + d]) : 0.f;
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = rb + 8 * (e >> 1) + 2 * (e & 1);
+          float lo = tiles[r * C::TP + d], hi = tiles[(r + 1) * C::TP + d];
+#pragma unroll
+          for (int kg = 1; kg < C::KG; ++kg) {
+            lo += tiles[kg * C::TILE + r * C::TP + d];
+            hi += tiles[kg * C::TILE + (r + 1) * C::TP + d];
+          }
+          o[e] = pack_bf16x2(mt * R + r < G.m ? lo + bd : 0.f, mt * R + r + 1 < G.m ? hi + bd : 0.f);
+        }
+        *reinterpret_cast<u32x4*>(kvh + ((G.m_begin + row0) >> 5) * (64 * D) + NCH * 512 + idx * 8) = o;
+      }
+      return;
+    }
+    const int c8 = 8 * (static_cast<int>(threadIdx.x) % CPR);
+    float bq[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) bq[e] = G.bias ? bf(G.bias[n0 + c8 + e]) : 0.f;
+    const u32x4 wraw = *reinterpret_cast<const u32x4*>((which == 0 ? G.qn_w : G.kn_w) + c8);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int r = (static_cast<int>(threadIdx.x) + kThreads * i) / CPR, row = mt * R + r;
+      float x[8];
+      sum8(r, c8, x);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t xp = pack_bf16x2(x[2 * e] + bq[2 * e], x[2 * e + 1] + bq[2 * e + 1]);
+        x[2 * e] = bf16x2_lo(xp);
+        x[2 * e + 1] = bf16x2_hi(xp);
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+#pragma unroll
+      for (int mm = CPR / 2; mm >= 1; mm >>= 1) ss += __shfl_xor(ss, mm, 64);  // every lane takes part
+      u32x4 o;
+      {
+#pragma clang fp contract(off)
+        const float rinv = 1.0f / __builtin_sqrtf(ss * (1.0f / D) + O.eps);
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t yp = pack_bf16x2(bf16x2_lo(wraw[e]) * (x[2 * e] * rinv), bf16x2_hi(wraw[e]) * (x[2 * e + 1] * rinv));
+          y[2 * e] = bf16x2_lo(yp);
+          y[2 * e + 1] = bf16x2_hi(yp);
+        }
+        if (G.cos != nullptr) {
+          const int64_t rr = min(row, G.m - 1);
+          const floatx4 c = *reinterpret_cast<const floatx4*>(G.cos + rr * G.rope_ld + c8 / 2);
+          const floatx4 sn = *reinterpret_cast<const floatx4*>(G.sin + rr * G.rope_ld + c8 / 2);
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const float re = y[2 * p], im = y[2 * p + 1];
+            o[p] = pack_bf16x2(re * c[p] - im * sn[p], re * sn[p] + im * c[p]);
+          }
+        } else {
+#pragma unroll
+          for (int p = 0; p < 4; ++p) o[p] = pack_bf16x2(y[2 * p], y[2 * p + 1]);
+        }
+      }
+      const int64_t key = static_cast<int64_t>(G.m_begin) + row;
+      if (row < G.m) {
+        if (which == 0)
+          *reinterpret_cast<u32x4*>(O.q + h * O.q_sh + key * O.q_sm + c8) = o;
+        else
+          *reinterpret_cast<u32x4*>(kvh + packed_k_offset(key, c8, D)) = o;
+      } else if (which == 1 && (row & ~31) < G.m) {
+        *reinterpret_cast<u32x4*>(kvh + packed_k_offset(key, c8, D)) = u32x4{0, 0, 0, 0};
+      }
+    }
+    return;
+  }
   // fp32 sums of this thread's chunks: 8 columns, or 8 gate + 8 up columns
   constexpr int V = kSwiglu ? 16 : 8;
   const int tc = kSwiglu ? 64 * (cc / 32) + cc % 32 : cc;
@@ -387,7 +522,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
 
 template <int EPI, bool DEEP>
 __global__ __launch_bounds__(kThreads, DEEP ? 1 : 2) void gemm_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) u32x4 lds[(DEEP ? kLdsDeep : kLdsBytes) / 16];
+  constexpr int kLds = EPI == kEpiQkv ? (DEEP ? kLdsQkvDeep : kLdsQkv) : (DEEP ? kLdsDeep : kLdsBytes);
+  __shared__ __attribute__((aligned(16))) u32x4 lds[kLds / 16];
   const int b = static_cast<int>(blockIdx.x);
   int gi = 0;
   if (a.num_groups > 1 && b >= a.g[1].wg_begin) gi = 1;
@@ -396,7 +532,14 @@ __global__ __launch_bounds__(kThreads, DEEP ? 1 : 2) void gemm_kernel(GemmArgs a
   const int r = b - G.wg_begin;
   const int item = (r % kXcds) * G.per_xcd + r / kXcds;  // XCD r % 8 takes a contiguous run of tiles
   if (item >= G.items) return;
-  if constexpr (DEEP) {
+  if constexpr (EPI == kEpiQkv) {  // whole 128-column heads: 128 x 128 or 64 x 128 tiles
+    if (G.cfg == kTile128)
+      gemm_tile<typename std::conditional<DEEP, Cfg128D, Cfg128>::type, EPI>(a, G, item, lds);
+    else if (G.cfg == kTile64x128)
+      gemm_tile<typename std::conditional<DEEP, Cfg64x128D, Cfg64x128>::type, EPI>(a, G, item, lds);
+    else
+      gemm_tile<typename std::conditional<DEEP, Cfg32x128D, Cfg32x128>::type, EPI>(a, G, item, lds);
+  } else if constexpr (DEEP) {
     if (G.cfg == kTile128)
       gemm_tile<Cfg128D, EPI>(a, G, item, lds);
     else if (G.cfg == kTile64)
@@ -423,7 +566,11 @@ void tiles_of(int64_t m, int64_t n, int& m_tiles, int& n_tiles) {
 
 // L2 -> CU bytes a workgroup of configuration cfg moves for one tile.
 int64_t tile_bytes(int cfg, int64_t k) {
-  const int ch = cfg == kTile128 ? Cfg128::CH : cfg == kTile64 ? Cfg64::CH : Cfg32::CH;
+  const int ch = cfg == kTile128      ? Cfg128::CH
+                 : cfg == kTile64     ? Cfg64::CH
+                 : cfg == kTile64x128 ? Cfg64x128::CH
+                 : cfg == kTile32x128 ? Cfg32x128::CH
+                                      : Cfg32::CH;
   return ch * k * 64;  // ch chunks of 1 KB per 16 columns of K
 }
 
@@ -448,10 +595,15 @@ constexpr int64_t kCounterBytes = 65536;
 // range of every group over that many workgroups (the largest power of two
 // <= split_k that divides its stages);
 // *ws_bytes receives the workspace the plan needs (counters, then fp32 partials).
+// The QKV epilogue (kEpiQkv) takes each group's norm weights and RoPE tables
+// from norms[i] (the caller has checked them) and never splits.
 hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, int64_t k, int32_t epilogue,
-                int split_k, GemmArgs& args, int64_t* ws_bytes, int64_t* cnt_off, int64_t* part_off) {
+                int split_k, GemmArgs& args, int64_t* ws_bytes, int64_t* cnt_off, int64_t* part_off,
+                const rldx_msat_stream_t* norms = nullptr) {
   if (!groups || num_groups < 1 || num_groups > 3) return hipErrorInvalidValue;
-  if (epilogue < kEpiBias || epilogue > kEpiBiasPacked) return hipErrorInvalidValue;
+  if (epilogue < kEpiBias || epilogue > kEpiQkv) return hipErrorInvalidValue;
+  const bool qkv = epilogue == kEpiQkv;
+  if (qkv && (norms == nullptr || split_k > 1)) return hipErrorInvalidValue;
   // k: whole stages of every K-group split (4 K-groups x 2 k-steps); n: whole 64-column blocks
   if (n <= 0 || k <= 0 || n % 64 != 0 || k % 128 != 0) return hipErrorInvalidValue;
   if (n > (1 << 30) || k > (1 << 30)) return hipErrorInvalidValue;
@@ -462,17 +614,19 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
   args.k = static_cast<int>(k);
   const int ksteps = static_cast<int>(k / 16);
   int cnt = 0;
+  int64_t m_begin = 0;  // joint-sequence row of the group (QKV epilogue)
   for (int i = 0; i < num_groups; ++i) {
     const rldx_gemm_group_t& s = groups[i];
     if (s.m < 0 || s.m > (1 << 24)) return hipErrorInvalidValue;
     if (s.m == 0) continue;
-    if (!s.a_packed || !s.w_packed || !s.out || !a16(s.a_packed) || !a16(s.w_packed)) return hipErrorInvalidValue;
+    if (!s.a_packed || !s.w_packed || (!qkv && !s.out) || !a16(s.a_packed) || !a16(s.w_packed))
+      return hipErrorInvalidValue;
     // packed operands are addressed with 32-bit byte offsets
     if ((s.m + 31) / 32 * 32 * k * 2 > (int64_t{1} << 31) - 1 || n * k * 2 > (int64_t{1} << 31) - 1)
       return hipErrorInvalidValue;
     // the epilogue stores (and reads the residual) in 16-byte pieces
-    if (!a16(s.out) || (s.bias && reinterpret_cast<uintptr_t>(s.bias) % 2)) return hipErrorInvalidValue;
-    if (!packed_out(epilogue) && (s.ldo < n_out || s.ldo % 8)) return hipErrorInvalidValue;
+    if ((!qkv && !a16(s.out)) || (s.bias && reinterpret_cast<uintptr_t>(s.bias) % 2)) return hipErrorInvalidValue;
+    if (!qkv && !packed_out(epilogue) && (s.ldo < n_out || s.ldo % 8)) return hipErrorInvalidValue;
     // packed output: ldo 0 (= n_out) or the width of a wider packed matrix whose
     // 16-column chunk at `out` starts the output columns
     if (packed_out(epilogue) && (s.ldo < 0 || s.ldo % 16 || (s.ldo > 0 && s.ldo < n_out) || s.ldo > (1 << 30)))
@@ -482,11 +636,21 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
     // Tile shape: 128 x 128 where the stream has rows and tiles enough to
     // occupy the chip (half the L2 traffic per flop of 64 x 64), else 64 x 64,
     // or 32 x 64 for streams of at most 32 rows.
+    // The QKV epilogue needs whole 128-column heads: 64 x 128 and 32 x 128 in
+    // place of 64 x 64 and 32 x 64 (same K-groups).
     int mt, nt, cfg, kg;
     tiles_of<Cfg128>(s.m, n, mt, nt);
     if (s.m >= 256 && static_cast<int64_t>(mt) * nt >= 128) {
       cfg = kTile128;
       kg = Cfg128::KG;
+    } else if (qkv && s.m > 32) {
+      cfg = kTile64x128;
+      kg = Cfg64x128::KG;
+      tiles_of<Cfg64x128>(s.m, n, mt, nt);
+    } else if (qkv) {
+      cfg = kTile32x128;
+      kg = Cfg32x128::KG;
+      tiles_of<Cfg32x128>(s.m, n, mt, nt);
     } else if (s.m > 32) {
       cfg = kTile64;
       kg = Cfg64::KG;
@@ -507,6 +671,15 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
               static_cast<const uint16_t*>(s.residual), packed_out(epilogue) && s.ldo == 0 ? n_out : s.ldo, s.ldr,
               static_cast<int>(s.m), cfg, mt,
               static_cast<int>(tiles * sp), 0, 0, sp, lstages / sp, nullptr, nullptr};
+    if (qkv) {
+      G.m_begin = static_cast<int>(m_begin);
+      G.qn_w = static_cast<const uint16_t*>(norms[i].q_norm_w);
+      G.kn_w = static_cast<const uint16_t*>(norms[i].k_norm_w);
+      G.cos = norms[i].rope_cos;
+      G.sin = norms[i].rope_sin;
+      G.rope_ld = static_cast<int>(norms[i].rope_row_stride);
+    }
+    m_begin += s.m;
   }
   args.num_groups = cnt;
   if (cnt == 0) return hipSuccess;
@@ -556,7 +729,12 @@ hipError_t launch(const GemmArgs& args, int epilogue, hipStream_t stream) {
   const int wgs = last.wg_begin + last.per_xcd * kXcds;
   const dim3 grid(static_cast<unsigned>(wgs)), block(kThreads);
   // at most one workgroup per CU (256 CUs): the deep-ring kernel
-  if (wgs <= 256) {
+  if (epilogue == kEpiQkv) {
+    if (wgs <= 256)
+      hipLaunchKernelGGL((gemm_kernel<kEpiQkv, true>), grid, block, 0, stream, args);
+    else
+      hipLaunchKernelGGL((gemm_kernel<kEpiQkv, false>), grid, block, 0, stream, args);
+  } else if (wgs <= 256) {
     if (epilogue == kEpiBias)
       hipLaunchKernelGGL((gemm_kernel<kEpiBias, true>), grid, block, 0, stream, args);
     else if (epilogue == kEpiResidual)
@@ -691,6 +869,7 @@ extern "C" hipError_t rldx_grouped_gemm_bf16(const rldx_gemm_group_t* groups, in
                                              int64_t k, int32_t epilogue, hipStream_t stream) {
   GemmArgs args;
   int64_t ws, co[3], po[3];
+  if (epilogue == kEpiQkv) return hipErrorInvalidValue;  // rldx_grouped_gemm_qkv_norm_rope_bf16
   const hipError_t e = plan(groups, num_groups, n, k, epilogue, 1, args, &ws, co, po);
   if (e != hipSuccess) return e;
   return launch(args, epilogue, stream);
@@ -700,7 +879,8 @@ extern "C" int64_t rldx_grouped_gemm_workspace_bytes(const rldx_gemm_group_t* gr
                                                      int64_t k, int32_t epilogue, int32_t split_k) {
   GemmArgs args;
   int64_t ws, co[3], po[3];
-  if (plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po) != hipSuccess) return -1;
+  if (epilogue == kEpiQkv || plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po) != hipSuccess)
+    return -1;
   return ws;
 }
 
@@ -709,6 +889,7 @@ extern "C" hipError_t rldx_grouped_gemm_ws_bf16(const rldx_gemm_group_t* groups,
                                                 int64_t workspace_bytes, hipStream_t stream) {
   GemmArgs args;
   int64_t ws, co[3], po[3];
+  if (epilogue == kEpiQkv) return hipErrorInvalidValue;
   const hipError_t e = plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po);
   if (e != hipSuccess) return e;
   if (ws > 0) {
@@ -737,4 +918,44 @@ extern "C" hipError_t rldx_act_pack_bf16(const void* x, int64_t ldx, int64_t m, 
 extern "C" hipError_t rldx_layernorm_pack_bf16(const void* x, int64_t ldx, int64_t m, int64_t k, float eps,
                                                void* packed, hipStream_t stream) {
   return rows_pack(x, ldx, m, k, eps, true, packed, stream);
+}
+
+extern "C" hipError_t rldx_grouped_gemm_qkv_norm_rope_bf16(const rldx_gemm_group_t* groups,
+                                                           const rldx_msat_stream_t* norms, int32_t num_groups,
+                                                           int64_t heads, int64_t head_dim, int64_t k, void* q_out,
+                                                           int64_t q_head_stride, int64_t q_row_stride,
+                                                           void* kv_packed, int64_t kv_packed_head_stride, float eps,
+                                                           hipStream_t stream) {
+  if (!groups || !norms || num_groups < 1 || num_groups > 3) return hipErrorInvalidValue;
+  if (head_dim != 128 || heads <= 0 || heads > 4096) return hipErrorInvalidValue;
+  if (!q_out || !kv_packed || !a16(q_out) || !a16(kv_packed)) return hipErrorInvalidValue;
+  if (q_head_stride < 0 || q_row_stride < 0 || q_head_stride % 8 || q_row_stride % 8 || kv_packed_head_stride % 8)
+    return hipErrorInvalidValue;
+  int64_t m = 0;
+  int last = -1;
+  for (int i = 0; i < num_groups; ++i)
+    if (groups[i].m > 0) last = i;
+  for (int i = 0; i < num_groups; ++i) {
+    const rldx_gemm_group_t& g = groups[i];
+    const rldx_msat_stream_t& s = norms[i];
+    if (g.m < 0 || s.rows != g.m) return hipErrorInvalidValue;
+    if (g.m == 0) continue;
+    // a 32-key tile of the packed K/V holds the rows of one stream only
+    if (i != last && g.m % 32) return hipErrorInvalidValue;
+    if (!s.q_norm_w || !s.k_norm_w || !a16(s.q_norm_w) || !a16(s.k_norm_w)) return hipErrorInvalidValue;
+    if ((s.rope_cos == nullptr) != (s.rope_sin == nullptr)) return hipErrorInvalidValue;
+    if (s.rope_cos && (!a16(s.rope_cos) || !a16(s.rope_sin) || s.rope_row_stride < head_dim / 2 ||
+                       s.rope_row_stride % 4 || s.rope_row_stride > (1 << 24)))
+      return hipErrorInvalidValue;
+    m += g.m;
+  }
+  if (m == 0) return hipSuccess;
+  if (kv_packed_head_stride < (m + 31) / 32 * 64 * head_dim) return hipErrorInvalidValue;
+  GemmArgs args;
+  int64_t ws, co[3], po[3];
+  const hipError_t e = plan(groups, num_groups, 3 * heads * head_dim, k, kEpiQkv, 1, args, &ws, co, po, norms);
+  if (e != hipSuccess) return e;
+  args.qkv = QkvOut{static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(kv_packed), q_head_stride, q_row_stride,
+                    kv_packed_head_stride, static_cast<int>(heads * head_dim), eps};
+  return launch(args, kEpiQkv, stream);
 }

@@ -167,4 +167,12 @@ RLDX_HD int64_t packed_act_offset(int64_t row, int64_t col, int64_t k) {
   return ((row >> 5) * (k >> 4) + (col >> 4)) * 512 + ((row & 31) + 32 * ((col >> 3) & 1)) * 8 + (col & 7);
 }
 
+// Element offset of K[key][d0 .. d0+7] (d0 % 8 == 0) inside the packed K/V
+// tiles of one head (32 keys per tile, 128 * D bytes, K chunks then V chunks):
+// tile key / 32, 1 KB chunk d0 / 16, lane key % 32 + 32 * (d0 / 8 % 2).
+RLDX_HD int64_t packed_k_offset(int64_t key, int d0, int D) {
+  const int lane = static_cast<int>(key & 31) + 32 * ((d0 >> 3) & 1);
+  return (key >> 5) * (64 * D) + ((d0 >> 4) * 64 + lane) * 8;
+}
+
 }  // namespace rldx

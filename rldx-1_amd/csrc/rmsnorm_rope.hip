@@ -218,13 +218,6 @@ struct MsatArgs {
   DivMagic dm_kind, dm_heads;
 };
 
-// Element offset of K[key][d0 .. d0+7] inside the packed tiles of one head:
-// tile key/32, 1 KB chunk d0/16, lane (key % 32) + 32 * ((d0 / 8) % 2).
-__device__ __forceinline__ int64_t packed_k_offset(int64_t key, int d0, int D) {
-  const int lane = static_cast<int>(key & 31) + 32 * ((d0 >> 3) & 1);
-  return (key >> 5) * (64 * D) + ((d0 >> 4) * 64 + lane) * 8;
-}
-
 template <int D>
 __device__ void msat_kv_pack_block(const MsatArgs& a, int64_t vb) {
   constexpr int PITCH = D + 8;

@@ -95,6 +95,9 @@ SIGNATURES = {
     "rldx_grouped_gemm_workspace_bytes": (c_i64, [ctypes.POINTER(GemmGroup), c_i32, c_i64, c_i64, c_i32, c_i32]),
     "rldx_grouped_gemm_ws_bf16": (c_i32, [ctypes.POINTER(GemmGroup), c_i32, c_i64, c_i64, c_i32, c_i32, c_vp, c_i64,
                                           c_vp]),
+    "rldx_grouped_gemm_qkv_norm_rope_bf16": (c_i32, [ctypes.POINTER(GemmGroup), ctypes.POINTER(MsatStream), c_i32,
+                                                     c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_f32,
+                                                     c_vp]),
     "rldx_host_swiglu_bf16": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64]),
     "rldx_grouped_res_ln_bf16": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                          c_i64, c_i64, c_i64, c_i64, c_f32, c_vp]),

@@ -175,6 +175,26 @@ class StreamSpec:
         self.qkv, self.q_w, self.k_w, self.cos, self.sin = qkv, q_w, k_w, cos, sin
 
 
+def _rope_tables(s: StreamSpec, rows: int, head_dim: int, keep: list):
+    """(cos, sin, row stride) of a stream's fp32 RoPE tables [rows, head_dim/2], or (None, None, 0)."""
+    if s.cos is None:
+        _require(s.sin is None, "cos and sin go together")
+        return None, None, 0
+    _require(s.sin is not None, "cos and sin go together")
+    c = s.cos.to(F32).contiguous() if s.cos.dtype != F32 or not s.cos.is_contiguous() else s.cos
+    sn = s.sin.to(F32).contiguous() if s.sin.dtype != F32 or not s.sin.is_contiguous() else s.sin
+    _require(c.shape == (rows, head_dim // 2) and sn.shape == (rows, head_dim // 2),
+             "rope tables must be [rows, head_dim/2]")
+    keep += [c, sn]
+    return c.data_ptr(), sn.data_ptr(), c.stride(0)
+
+
+def _check_kvp_out(kvp: torch.Tensor, num_heads: int, M: int, head_dim: int) -> None:
+    _require(kvp.dtype == BF16 and kvp.dim() == 2 and kvp.shape[0] == num_heads and
+             kvp.shape[1] >= kv_packed_elems(M, head_dim) and kvp.stride(1) == 1,
+             "kvp out must be (H, >= kv_packed_elems(M, D)) bf16")
+
+
 def msat_qkv_norm_rope(streams: Sequence[StreamSpec], num_heads: int, head_dim: int, eps: float = 1e-6,
                        out: Optional[tuple] = None, kv_packed: bool = False):
     """Gather Q/K/V of 1-3 streams into (H, M, D) bf16 with per-stream QK RMSNorm
@@ -202,16 +222,7 @@ def msat_qkv_norm_rope(streams: Sequence[StreamSpec], num_heads: int, head_dim: 
                  s.k_w.numel() == head_dim and s.q_w.is_contiguous() and s.k_w.is_contiguous(),
                  "norm weights must be contiguous bf16 [head_dim]")
         n = s.qkv.shape[0]
-        cos_p = sin_p = None
-        rope_ld = 0
-        if s.cos is not None:
-            _require(s.sin is not None, "cos and sin go together")
-            c = s.cos.to(F32).contiguous() if s.cos.dtype != F32 or not s.cos.is_contiguous() else s.cos
-            sn = s.sin.to(F32).contiguous() if s.sin.dtype != F32 or not s.sin.is_contiguous() else s.sin
-            _require(c.shape == (n, head_dim // 2) and sn.shape == (n, head_dim // 2),
-                     "rope tables must be [rows, head_dim/2]")
-            keep += [c, sn]
-            cos_p, sin_p, rope_ld = c.data_ptr(), sn.data_ptr(), c.stride(0)
+        cos_p, sin_p, rope_ld = _rope_tables(s, n, head_dim, keep)
         descs[i] = _lib.MsatStream(s.qkv.data_ptr(), s.qkv.stride(0), n, s.q_w.data_ptr(), s.k_w.data_ptr(),
                                    cos_p, sin_p, rope_ld)
         M += n
@@ -224,10 +235,7 @@ def msat_qkv_norm_rope(streams: Sequence[StreamSpec], num_heads: int, head_dim: 
         _require(q.shape == (num_heads, M, head_dim), "q out must be (H, M, D)")
         if kv_packed:
             _require(len(rest) == 1, "packed mode takes out=(q, kvp)")
-            kvp = rest[0]
-            _require(kvp.dtype == BF16 and kvp.dim() == 2 and kvp.shape[0] == num_heads and
-                     kvp.shape[1] >= kv_packed_elems(M, head_dim) and kvp.stride(1) == 1,
-                     "kvp out must be (H, >= kv_packed_elems(M, D)) bf16")
+            _check_kvp_out(rest[0], num_heads, M, head_dim)
         else:
             _require(len(rest) == 2, "out=(q, k, v)")
             for t in rest:
@@ -657,6 +665,51 @@ def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias", split_k: int = 
         _on_gpu(workspace.data)
         _lib.check(lib.rldx_grouped_gemm_ws_bf16(groups, len(items), n, k, epi, int(split_k), workspace.data.data_ptr(),
                                                  workspace.data.numel(), _stream_ptr(wt)), "rldx_grouped_gemm_ws_bf16")
+
+
+def grouped_gemm_qkv_norm_rope(items: Sequence[tuple], norms: Sequence[StreamSpec], num_heads: int,
+                               head_dim: int, eps: float = 1e-6, out: Optional[tuple] = None):
+    """The QKV linears of 1-3 streams (joint-sequence order) with the QK RMSNorm +
+    RoPE + K/V tiling of `msat_qkv_norm_rope` in the GEMM epilogue: one launch,
+    the same bits as grouped_gemm(items, "bias") followed by
+    msat_qkv_norm_rope(..., kv_packed=True).  items: (a PackedAct [m, k],
+    PackedWeight [3 H D, k], bias [3 H D] or None); norms: one StreamSpec per item
+    (norm weights and tables; its qkv is not read, pass None).  Every stream but
+    the last has rows % 32 == 0.  Returns (q (H, M, D), kvp (H, kv_packed_elems(M,
+    D))); `out` gives them."""
+    _require(1 <= len(items) <= 3 and len(norms) == len(items), "1-3 groups, one StreamSpec each")
+    _require(head_dim == 128, "the fused QKV epilogue needs head_dim 128")
+    inner = num_heads * head_dim
+    n, k = 3 * inner, items[0][1].k
+    groups = (_lib.GemmGroup * len(items))()
+    descs = (_lib.MsatStream * len(items))()
+    keep, M = [], 0
+    for i, ((a, w, bias), s) in enumerate(zip(items, norms)):
+        _require(isinstance(a, PackedAct) and a.ld == a.k, "a must be a PackedAct")
+        _on_gpu(a.data, w.data, bias, s.q_w, s.k_w, s.cos, s.sin)
+        _require(w.n == n and w.k == k and a.k == k and not w.swiglu_pairs, "weights must be [3 H D, k], shared k")
+        if bias is not None:
+            _require(bias.dtype == BF16 and bias.is_contiguous() and bias.numel() == n, "bias must be [n] bf16")
+        _require(s.q_w.dtype == BF16 and s.k_w.dtype == BF16 and s.q_w.numel() == head_dim and
+                 s.k_w.numel() == head_dim and s.q_w.is_contiguous() and s.k_w.is_contiguous(),
+                 "norm weights must be contiguous bf16 [head_dim]")
+        cos_p, sin_p, rope_ld = _rope_tables(s, a.m, head_dim, keep)
+        groups[i] = _lib.GemmGroup(a.data.data_ptr(), a.m, w.data.data_ptr(), _ptr(bias), None, 0, None, 0)
+        descs[i] = _lib.MsatStream(None, 0, a.m, s.q_w.data_ptr(), s.k_w.data_ptr(), cos_p, sin_p, rope_ld)
+        M += a.m
+    dev = items[0][0].data.device
+    if out is None:
+        q = torch.empty((num_heads, M, head_dim), dtype=BF16, device=dev)
+        kvp = torch.empty((num_heads, kv_packed_elems(M, head_dim)), dtype=BF16, device=dev)
+    else:
+        q, kvp = out
+        _require(q.dtype == BF16 and q.shape == (num_heads, M, head_dim) and q.stride(2) == 1, "q out must be (H, M, D)")
+        _check_kvp_out(kvp, num_heads, M, head_dim)
+    _on_gpu(q, kvp)
+    _lib.check(_lib.load().rldx_grouped_gemm_qkv_norm_rope_bf16(
+        groups, descs, len(items), num_heads, head_dim, k, q.data_ptr(), q.stride(0), q.stride(1), kvp.data_ptr(),
+        kvp.stride(0), float(eps), _stream_ptr(q)), "rldx_grouped_gemm_qkv_norm_rope_bf16")
+    return q, kvp
 
 
 # ---------------------------------------------------------------------------

@@ -152,8 +152,9 @@ class MsatActionStep:
 
     Per block, every launch covers all three streams:
         LayerNorm -> packed h          rldx_layernorm_pack_bf16
-        QKV linears (+ bias)           rldx_grouped_gemm_bf16
-        QK-RMSNorm + RoPE, K/V tiles   rldx_msat_qkv_norm_rope_bf16
+        QKV linears (+ bias) with      rldx_grouped_gemm_qkv_norm_rope_bf16
+          QK-RMSNorm + RoPE, K/V tiles   (fused_qkv=False: rldx_grouped_gemm_bf16,
+                                          then rldx_msat_qkv_norm_rope_bf16)
         joint attention -> packed o    rldx_attention_packed_fwd_bf16
         Proj linears, x += (in place)  rldx_grouped_gemm_bf16 (residual epilogue)
         LayerNorm -> packed h
@@ -161,8 +162,9 @@ class MsatActionStep:
         W3 linears, x += (in place)    rldx_grouped_gemm_bf16 (residual epilogue)
     The weights are packed once, at construction, into the GEMM's operand order."""
 
-    def __init__(self, cfg: MsatStepCfg, weights: dict, inputs: dict):
+    def __init__(self, cfg: MsatStepCfg, weights: dict, inputs: dict, fused_qkv: bool = True):
         self.cfg, self.w, self.inp = cfg, weights, inputs
+        self.fused_qkv = fused_qkv
         dev = inputs["vl"].device
         n, d, H, D = cfg.tokens, cfg.hidden, cfg.heads, cfg.head_dim
         e = lambda *s: torch.empty(*s, dtype=BF16, device=dev)  # noqa: E731
@@ -203,7 +205,6 @@ class MsatActionStep:
         cfg, w = self.cfg, self.w
         gemm = self._gemms(L)
         Fn.layernorm_pack(self.x, cfg.eps, out=self.h)
-        Fn.grouped_gemm(*gemm["qkv"])
         specs = [
             Fn.StreamSpec(self.qkv[cfg.rows("vl")], w["vl.q_norm"][L], w["vl.k_norm"][L]),
             Fn.StreamSpec(self.qkv[cfg.rows("sa")], w["sa.q_norm"][L], w["sa.k_norm"][L],
@@ -211,7 +212,12 @@ class MsatActionStep:
             Fn.StreamSpec(self.qkv[cfg.rows("p")], w["p.q_norm"][L], w["p.k_norm"][L],
                           self.inp["p_cos"], self.inp["p_sin"]),
         ]
-        Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
+        if self.fused_qkv:
+            items = [(a, wt, b) for a, wt, b, _, _ in gemm["qkv"][0]]
+            Fn.grouped_gemm_qkv_norm_rope(items, specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp))
+        else:
+            Fn.grouped_gemm(*gemm["qkv"])
+            Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
         Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), cfg.tokens, key_bias=self.inp["key_bias"],
                             out=self.att)
         Fn.grouped_gemm(*gemm["proj"])

@@ -178,6 +178,37 @@ def test_grouped_gemm_split_plan_and_rejections():
     assert lib.rldx_grouped_gemm_bf16(_gemm_groups(msat), 3, 1536, 4096, 7, None) == HIP_INVALID_VALUE
 
 
+def _msat_norms(ms, rope_ld=0):
+    d = (_lib.MsatStream * len(ms))()
+    for i, m in enumerate(ms):
+        d[i] = _lib.MsatStream(None, 0, m, 4096, 4352, 8192 if rope_ld else None, 12288 if rope_ld else None, rope_ld)
+    return d
+
+
+def test_grouped_gemm_qkv_norm_rope_rejections():
+    """The fused QKV entry checks its arguments before anything is launched; the
+    generic grouped GEMM entries do not accept its epilogue."""
+    lib = _lib.load()
+    msat = (512, 64, 32)
+
+    def call(ms=msat, norm_ms=None, H=12, D=128, k=1536, q=1 << 20, qsh=608 * 128, qsm=128, kvp=1 << 24,
+             kvsh=19 * 64 * 128, rope_ld=0):
+        return lib.rldx_grouped_gemm_qkv_norm_rope_bf16(_gemm_groups(ms), _msat_norms(norm_ms or ms, rope_ld), len(ms),
+                                                        H, D, k, q, qsh, qsm, kvp, kvsh, 1e-6, None)
+
+    assert call(norm_ms=(512, 64, 31)) == HIP_INVALID_VALUE        # rows differ from the GEMM group's
+    assert call(ms=(500, 64, 32)) == HIP_INVALID_VALUE             # a stream before the last with rows % 32
+    assert call(D=64) == HIP_INVALID_VALUE                          # head_dim 128 only
+    assert call(k=1000) == HIP_INVALID_VALUE                        # k % 128
+    assert call(kvsh=19 * 64 * 128 - 8) == HIP_INVALID_VALUE        # packed K/V head stride too small
+    assert call(q=(1 << 20) + 8) == HIP_INVALID_VALUE               # Q not 16-byte aligned
+    assert call(qsm=132) == HIP_INVALID_VALUE                       # Q row stride % 8
+    assert call(rope_ld=60) == HIP_INVALID_VALUE                    # RoPE rows shorter than head_dim / 2
+    assert call(H=0) == HIP_INVALID_VALUE
+    assert lib.rldx_grouped_gemm_bf16(_gemm_groups(msat), 3, 4608, 1536, 5, None) == HIP_INVALID_VALUE
+    assert lib.rldx_grouped_gemm_workspace_bytes(_gemm_groups(msat), 3, 4608, 1536, 5, 1) == -1
+
+
 def test_vision_attention_workspace_and_rejections():
     lib = _lib.load()
     # 2 x 196 tokens, 16 heads x 72 (padded to 96): Q 16*392*96*2 bytes, 14 slots of 128*96-byte tiles per head

@@ -327,6 +327,46 @@ def test_concatenated_packed_operand_from_attention_and_bias_packed_gemm(dev):
     assert torch.equal(wide.unpack()[:, 1024:], sw)
 
 
+@pytest.mark.parametrize("ms,H,k", [((512, 64, 32), 12, 1536), ((1024, 64, 32), 12, 256),
+                                   ((64, 32, 20), 2, 256), ((40,), 3, 384), ((0, 96, 64), 2, 128)])
+def test_grouped_gemm_qkv_norm_rope_matches_two_launches(dev, ms, H, k):
+    """The QKV epilogue (QK RMSNorm + RoPE + packed K/V tiles in the GEMM) is
+    bit-identical to the bias GEMM followed by rldx_msat_qkv_norm_rope_bf16:
+    Q (H, M, 128) and every element of the packed K/V tiles, including the zero
+    padding keys of a last stream whose rows are not a multiple of 32.  Shapes:
+    the action step's streams (128 x 128 and 64 x 128 tiles, one workgroup per
+    CU), 1024 rows (more than 256 workgroups: two per CU), short and single
+    streams, an empty stream."""
+    from rldx_amd.msat_step import msat_rope_tables
+
+    g = torch.Generator().manual_seed(sum(ms) + H + k)
+    D, n = 128, 3 * H * 128
+    items, specs, qkv_items = [], [], []
+    for i, m in enumerate(ms):
+        a = Fn.pack_act(_rand((m, k), g).to(dev)) if m else Fn.PackedAct.empty(0, k, dev)
+        w = Fn.pack_weight(_rand((n, k), g, std=k ** -0.5).to(dev))
+        b = _rand((n,), g, std=0.5).to(dev)
+        qw, kw = (1 + 0.2 * torch.randn(D, generator=g)).to(BF16).to(dev), (1 + 0.2 * torch.randn(D, generator=g)).to(BF16).to(dev)
+        cos = sin = None
+        if i > 0 and m:  # streams after the first carry RoPE tables
+            ids = torch.stack([torch.zeros(m, dtype=torch.long), torch.arange(m) + 3 * i], dim=-1)
+            cos, sin = (t.to(dev) for t in msat_rope_tables(ids, D, 10000.0))
+        qkv = torch.empty(m, n, dtype=BF16, device=dev)
+        items.append((a, w, b))
+        qkv_items.append((a, w, b, qkv, None))
+        specs.append(Fn.StreamSpec(qkv, qw, kw, cos, sin))
+    M = sum(ms)
+    q = torch.full((H, M, D), 7.0, dtype=BF16, device=dev)
+    kvp = torch.full((H, Fn.kv_packed_elems(M, D)), 5.0, dtype=BF16, device=dev)
+    Fn.grouped_gemm_qkv_norm_rope(items, specs, H, D, 1e-6, out=(q, kvp))
+    Fn.grouped_gemm([it for it in qkv_items if it[0].m], "bias")
+    live = [s for s in specs if s.qkv.shape[0]]
+    q2, kvp2 = Fn.msat_qkv_norm_rope(live, H, D, 1e-6, kv_packed=True)
+    torch.cuda.synchronize()
+    assert torch.equal(q.view(torch.int16), q2.view(torch.int16))
+    assert torch.equal(kvp.view(torch.int16), kvp2.view(torch.int16))
+
+
 def test_ss_fused_mlp_swiglu_op(dev):
     import rldx_amd.ops  # noqa: F401  registers ss::fused_mlp_swiglu
 

@@ -69,3 +69,12 @@ def test_graph_replay_matches_eager_and_follows_inputs(setup):
     inp["x0"].copy_(x0_old)
     assert torch.equal(r_new, eager_new)
     assert not torch.equal(r_new, eager)
+
+
+def test_fused_qkv_epilogue_step_is_bit_identical(setup):
+    """QKV GEMM with the QK-norm / RoPE / K/V tiling in its epilogue (one launch)
+    against the GEMM + rldx_msat_qkv_norm_rope_bf16 pair, over a whole step."""
+    cfg, w, inp, wc, ic = setup
+    fused = MsatActionStep(cfg, w, inp).run().clone()
+    split = MsatActionStep(cfg, w, inp, fused_qkv=False).run().clone()
+    assert torch.equal(fused.view(torch.int16), split.view(torch.int16))
