@@ -291,9 +291,12 @@ def step_gemms(step):
     n, d, inner, ffn = cfg.tokens, cfg.hidden, cfg.inner, cfg.ffn
     rows = [(s, cfg.rows(s)) for s in ("vl", "sa", "p")]
 
-    def qkv(L):
-        Fn.grouped_gemm([(step.h.rows(r.start, r.stop), pw[f"{s}.qkv"][L], w[f"{s}.qkv.b"][L], step.qkv[r], None)
-                         for s, r in rows], "bias")
+    def qkv(L):  # with the QK-norm / RoPE / K/V-tile epilogue, as in the step
+        specs = [Fn.StreamSpec(None, w[f"{s}.q_norm"][L], w[f"{s}.k_norm"][L],
+                               *((step.inp[f"{s}_cos"], step.inp[f"{s}_sin"]) if s != "vl" else ())) for s, _ in rows]
+        Fn.grouped_gemm_qkv_norm_rope([(step.h.rows(r.start, r.stop), pw[f"{s}.qkv"][L], w[f"{s}.qkv.b"][L])
+                                       for s, r in rows], specs, cfg.heads, cfg.head_dim, cfg.eps,
+                                      out=(step.q, step.kvp))
 
     def proj(L):
         Fn.grouped_gemm([(step.att.rows(r.start, r.stop), pw[f"{s}.proj"][L], w[f"{s}.proj.b"][L], step.x[r],
