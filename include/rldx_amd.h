@@ -227,10 +227,11 @@ hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* kv_packed, 
  * (seq, >= (Hq + 2*Hkv)*D) bf16 -> out (seq, Hq*D) bf16 with q_norm/k_norm
  * (Qwen3VLTextRMSNorm, eps) + rotate-half RoPE (cos / sin tables [seq, D] bf16,
  * row stride cos_row_stride; sin pre-signed iff sin_is_signed) + causal GQA
- * attention, scale 1/sqrt(D).  Three launches: K normalisation and K/V packing into
- * `workspace` (>= rldx_llm_fused_attention_workspace_bytes(seq, Hkv, D) bytes,
+ * attention, scale 1/sqrt(D).  Two launches: K normalisation + RoPE written
+ * straight into the packed K/V tiles, with the V tiles packed by the same launch,
+ * in `workspace` (>= rldx_llm_fused_attention_workspace_bytes(seq, Hkv, D) bytes,
  * 16-byte aligned, caller-owned), then attention with the Q normalisation fused
- * into its prologue.  qkv, out, cos, sin and q_norm_w are 16-byte aligned.
+ * into its prologue.  qkv, out, cos, sin, q_norm_w and k_norm_w are 16-byte aligned.
  *
  * Replaces: fused_llm_attention.forward(qkv, q_norm_w, q_norm_w_rot, k_norm_w,
  *   k_norm_w_rot, cos, signed_sin, num_heads, num_kv_heads, head_dim, out)
@@ -246,7 +247,7 @@ hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv_row_stride
                                          int64_t head_dim, float eps, void* workspace, int64_t workspace_bytes,
                                          hipStream_t stream);
 
-/* Workspace bytes rldx_llm_fused_attention_bf16 needs (normalised K + packed K/V). */
+/* Workspace bytes rldx_llm_fused_attention_bf16 needs (the packed K/V tiles). */
 int64_t rldx_llm_fused_attention_workspace_bytes(int64_t seq, int64_t kv_heads, int64_t head_dim);
 
 /*

@@ -1181,8 +1181,8 @@ extern "C" hipError_t rldx_attention_fwd_bf16(const void* q, const void* k, cons
 
 extern "C" int64_t rldx_llm_fused_attention_workspace_bytes(int64_t seq, int64_t kv_heads, int64_t head_dim) {
   if (seq < 0 || kv_heads < 0 || head_dim < 0) return -1;
-  // normalised K [seq, Hkv, D], then the packed K/V tiles of the Hkv heads
-  return seq * kv_heads * head_dim * 2 + kv_heads * rldx_attention_kv_packed_elems(seq, head_dim) * 2;
+  // the packed K/V tiles of the Hkv heads
+  return kv_heads * rldx_attention_kv_packed_elems(seq, head_dim) * 2;
 }
 
 extern "C" hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv_row_stride, const void* q_norm_w,
@@ -1200,30 +1200,21 @@ extern "C" hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv
     return hipErrorInvalidValue;
   if (workspace_bytes < rldx_llm_fused_attention_workspace_bytes(seq, kv_heads, head_dim))
     return hipErrorInvalidValue;
-  if (!a16(qkv) || !a16(out) || !a16(cos) || !a16(sin) || !a16(workspace) || !a16(q_norm_w))
+  if (!a16(qkv) || !a16(out) || !a16(cos) || !a16(sin) || !a16(workspace) || !a16(q_norm_w) || !a16(k_norm_w))
     return hipErrorInvalidValue;
   if (seq > (1 << 24) || q_heads > 65535) return hipErrorInvalidValue;
   const uint16_t* base = static_cast<const uint16_t*>(qkv);
-  uint16_t* kws = static_cast<uint16_t*>(workspace);  // normalised K, [seq, kv_heads, D]
-  uint16_t* kvp = kws + seq * kv_heads * head_dim;    // packed K/V tiles
+  uint16_t* kvp = static_cast<uint16_t*>(workspace);  // packed K/V tiles
   const int64_t head_elems = rldx_attention_kv_packed_elems(seq, head_dim);
-  // 1) K: RMSNorm + rotate-half RoPE into the workspace (Q is done inside the attention kernel)
-  const int64_t k_strides[3] = {0, qkv_row_stride, head_dim};
-  const int64_t ko_strides[3] = {0, kv_heads * head_dim, head_dim};
-  const int64_t zero3[3] = {0, 0, 0};
-  const int64_t cs[2] = {0, cos_row_stride};
-  hipError_t e = rldx_qk_rmsnorm_rope_half_bf16(nullptr, base + q_heads * head_dim, nullptr, k_norm_w, cos, sin,
-                                                nullptr, kws, 1, seq, 0, kv_heads, head_dim, zero3, k_strides, zero3,
-                                                ko_strides, cs, eps, sin_is_signed ? RLDX_ROPE_SIN_SIGNED : 0, stream);
+  // 1) K: RMSNorm + rotate-half RoPE straight into the packed tiles, V packed by
+  //    the same launch (Q is done inside the attention kernel)
+  hipError_t e = gqa_k_norm_rope_kv_pack(base + q_heads * head_dim, base + (q_heads + kv_heads) * head_dim,
+                                         qkv_row_stride, static_cast<const uint16_t*>(k_norm_w),
+                                         static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin),
+                                         cos_row_stride, sin_is_signed != 0, seq, kv_heads, head_dim, eps, kvp,
+                                         head_elems, stream);
   if (e != hipSuccess) return e;
-  // 2) pack the normalised K and the packed V columns
-  const int64_t kk_strides[3] = {0, head_dim, kv_heads * head_dim};
-  const int64_t v_strides[3] = {0, head_dim, qkv_row_stride};
-  const int64_t ps[2] = {0, head_elems};
-  e = rldx_attention_kv_pack_bf16(kws, kk_strides, base + (q_heads + kv_heads) * head_dim, v_strides, kvp, ps, 1,
-                                  kv_heads, seq, head_dim, stream);
-  if (e != hipSuccess) return e;
-  // 3) causal GQA attention, Q normalised in the prologue
+  // 2) causal GQA attention, Q normalised in the prologue
   AttnArgs a{};
   const int64_t q_strides[3] = {0, head_dim, qkv_row_stride};
   const int64_t o_strides[3] = {0, head_dim, out_row_stride};

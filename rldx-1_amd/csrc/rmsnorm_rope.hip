@@ -70,16 +70,72 @@ struct HalfArgs {
   int64_t total_rows;          // batch * seq * (hq + hk); total_rows * D / V < 2^31
   DivMagic per_tok_div;        // division by hq + hk
   DivMagic seq_div;            // division by seq
+  // Packed K/V mode (kernel template PK; bf16, batch 1, K heads only, R == 1):
+  // K rows go into the attention kernels' packed K/V tiles of head h at
+  // kvp + h * kvp_sh, and workgroups [norm_blocks, norm_blocks + hk * kv_tiles)
+  // pack the V tiles from v (row stride v_ss, head stride v_sh) and zero the K
+  // rows of the padding keys.
+  uint16_t* kvp;
+  int64_t kvp_sh, norm_blocks, kv_tiles;
+  const uint16_t* v;
+  int64_t v_ss, v_sh;
 };
+
+// One 32-key tile of the packed K/V layout (32 keys, 128 * D bytes: K operand
+// chunks, then V operand chunks) at dst: V rows k0 .. k0 + 31 (vrow(m) points at
+// V[m][0 .. D), keys >= m_total read as zeros) go to the V chunks; the K rows of
+// keys >= m_total are zeroed (the K rows of real keys are written by the norm
+// role).  V chunk 2 db + s2, lane l, element i holds
+// V[k0 + 16 s2 + 8 (i / 4) + 4 (l / 32) + i % 4][32 db + l % 32].
+template <int D, class RowFn>
+__device__ void kv_tile_pack(RowFn vrow, int64_t m_total, int64_t k0, uint16_t* dst) {
+  constexpr int PITCH = D + 8;
+  constexpr int CH = D / 8;    // 16-byte chunks per V row
+  constexpr int NCH = D / 16;  // 1 KB chunks per part of a tile
+  __shared__ __attribute__((aligned(16))) uint16_t tile[32 * PITCH];
+  for (int c = threadIdx.x; c < 32 * CH; c += blockDim.x) {
+    const int r = c / CH, col = (c % CH) * 8;
+    const int64_t m = k0 + r;
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (m < m_total) val = *reinterpret_cast<const uint4*>(vrow(m) + col);
+    *reinterpret_cast<uint4*>(&tile[r * PITCH + col]) = val;
+  }
+  for (int idx = threadIdx.x; idx < NCH * 64; idx += blockDim.x)
+    if (k0 + (idx & 31) >= m_total) *reinterpret_cast<uint4*>(dst + idx * 8) = make_uint4(0, 0, 0, 0);
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < NCH * 64; idx += blockDim.x) {
+    const int cc = idx >> 6, l = idx & 63;
+    const int d = 32 * (cc >> 1) + (l & 31);
+    const int rb = 16 * (cc & 1) + 4 * (l >> 5);
+    uint4 out;
+    uint32_t* ow = reinterpret_cast<uint32_t*>(&out);
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      const int r0 = rb + 8 * (i >> 2) + (i & 3);
+      ow[i >> 1] = static_cast<uint32_t>(tile[r0 * PITCH + d]) | (static_cast<uint32_t>(tile[(r0 + 1) * PITCH + d]) << 16);
+    }
+    *reinterpret_cast<uint4*>(dst + NCH * 512 + idx * 8) = out;
+  }
+}
 
 // One thread: V consecutive elements of R heads of one token (the R heads
 // share the token's cos / sin and, within q or within k, the norm weight, so
 // those are loaded once for R rows).  R divides both hq and hk.
-template <typename T, int D, int R>
+template <typename T, int D, int R, bool PK = false>
 __global__ __launch_bounds__(256) void rmsnorm_rope_half_kernel(HalfArgs a) {
   constexpr int V = Vec16<T>::N;   // elements per lane
   constexpr int LPR = D / V;       // lanes per row
   static_assert(LPR >= 2 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "unsupported head_dim");
+  static_assert(!PK || (sizeof(T) == 2 && R == 1), "packed K/V mode: bf16, one head per thread");
+  if constexpr (PK) {
+    if (static_cast<int64_t>(blockIdx.x) >= a.norm_blocks) {  // a V tile (whole workgroups take this branch)
+      const int64_t vb = static_cast<int64_t>(blockIdx.x) - a.norm_blocks;
+      const int64_t h = vb / a.kv_tiles, t = vb - h * a.kv_tiles;
+      const uint16_t* vh = a.v + h * a.v_sh;
+      kv_tile_pack<D>([&](int64_t m) { return vh + m * a.v_ss; }, a.seq, t * 32, a.kvp + h * a.kvp_sh + t * (64 * D));
+      return;
+    }
+  }
   // 32-bit index math with invariant-divisor multiplies (a 64-bit division by
   // a run-time value costs ~130 instructions, more than the rows' arithmetic)
   const uint32_t tid = blockIdx.x * blockDim.x + threadIdx.x;
@@ -173,7 +229,11 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_half_kernel(HalfArgs a) {
         }
       }
     }
-    if (valid) *reinterpret_cast<uint4*>(dst + j * dst_h + d0) = outraw;
+    if constexpr (PK) {
+      if (valid) *reinterpret_cast<uint4*>(a.kvp + h * a.kvp_sh + packed_k_offset(s, d0, D)) = outraw;
+    } else {
+      if (valid) *reinterpret_cast<uint4*>(dst + j * dst_h + d0) = outraw;
+    }
   }
 }
 
@@ -220,46 +280,17 @@ struct MsatArgs {
 
 template <int D>
 __device__ void msat_kv_pack_block(const MsatArgs& a, int64_t vb) {
-  constexpr int PITCH = D + 8;
-  constexpr int CH = D / 8;    // 16-byte chunks per V row
-  constexpr int NCH = D / 16;  // 1 KB chunks per part of a tile
-  __shared__ __attribute__((aligned(16))) uint16_t tile[32 * PITCH];
   const int64_t h = vb / a.kv_tiles;
   const int64_t t = vb - h * a.kv_tiles;
-  const int64_t k0 = t * 32;
   const int64_t inner = a.heads * D;
-  for (int c = threadIdx.x; c < 32 * CH; c += 256) {
-    const int r = c / CH, col = (c % CH) * 8;
-    const int64_t m = k0 + r;
-    uint4 val = make_uint4(0, 0, 0, 0);
-    if (m < a.m_total) {
-      int si = 0;
-      if (a.num_streams > 1 && m >= a.s[1].m_begin) si = 1;
-      if (a.num_streams > 2 && m >= a.s[2].m_begin) si = 2;
-      const MsatStream& S = a.s[si];
-      val = *reinterpret_cast<const uint4*>(S.qkv + (m - S.m_begin) * S.ld + 2 * inner + h * D + col);
-    }
-    *reinterpret_cast<uint4*>(&tile[r * PITCH + col]) = val;
-  }
-  uint16_t* dst = a.kvp + h * a.kvp_sh + t * (64 * D);
-  // K rows past the end of the sequence read as zeros
-  for (int idx = threadIdx.x; idx < NCH * 64; idx += 256)
-    if (k0 + (idx & 31) >= a.m_total) *reinterpret_cast<uint4*>(dst + idx * 8) = make_uint4(0, 0, 0, 0);
-  __syncthreads();
-  // V part: chunk 2*db + s2, lane l, element i = V[k0 + 16 s2 + 8 (i/4) + 4 (l/32) + i%4][32 db + l%32]
-  for (int idx = threadIdx.x; idx < NCH * 64; idx += 256) {
-    const int cc = idx >> 6, l = idx & 63;
-    const int d = 32 * (cc >> 1) + (l & 31);
-    const int rb = 16 * (cc & 1) + 4 * (l >> 5);
-    uint4 out;
-    uint32_t* ow = reinterpret_cast<uint32_t*>(&out);
-#pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-      const int r0 = rb + 8 * (i >> 2) + (i & 3);
-      ow[i >> 1] = static_cast<uint32_t>(tile[r0 * PITCH + d]) | (static_cast<uint32_t>(tile[(r0 + 1) * PITCH + d]) << 16);
-    }
-    *reinterpret_cast<uint4*>(dst + NCH * 512 + idx * 8) = out;
-  }
+  auto vrow = [&](int64_t m) {
+    int si = 0;
+    if (a.num_streams > 1 && m >= a.s[1].m_begin) si = 1;
+    if (a.num_streams > 2 && m >= a.s[2].m_begin) si = 2;
+    const MsatStream& S = a.s[si];
+    return S.qkv + (m - S.m_begin) * S.ld + 2 * inner + h * D;
+  };
+  kv_tile_pack<D>(vrow, a.m_total, t * 32, a.kvp + h * a.kvp_sh + t * (64 * D));
 }
 
 template <int D>
@@ -409,6 +440,54 @@ hipError_t half_entry(const void* q, const void* k, const void* q_w, const void*
 }
 
 }  // namespace
+
+// K of a GQA prefill (rows [seq] of stride row_stride, head h at k + h * D):
+// RMSNorm + rotate-half RoPE straight into the packed K/V tiles, and the V tiles
+// (v + h * D) packed by further workgroups of the same launch.  Arguments are
+// validated by the caller (rldx_llm_fused_attention_bf16).
+hipError_t gqa_k_norm_rope_kv_pack(const uint16_t* k, const uint16_t* v, int64_t row_stride, const uint16_t* k_w,
+                                   const uint16_t* cos, const uint16_t* sin, int64_t cos_row_stride, bool sin_signed,
+                                   int64_t seq, int64_t kv_heads, int64_t head_dim, float eps, uint16_t* kvp,
+                                   int64_t kvp_sh, hipStream_t stream) {
+  const int64_t rows = seq * kv_heads;
+  if (rows * (head_dim / 8) >= (int64_t{1} << 31) - 256 || kv_heads > 65535) return hipErrorInvalidValue;
+  HalfArgs a{};
+  a.k = k;
+  a.k_w = k_w;
+  a.cos = cos;
+  a.sin = sin;
+  a.batch = 1;
+  a.seq = seq;
+  a.hq = 0;
+  a.hk = kv_heads;
+  a.k_ss = row_stride;
+  a.k_sh = head_dim;
+  a.c_ss = cos_row_stride;
+  a.eps = eps;
+  a.sin_signed = sin_signed ? 1 : 0;
+  a.total_rows = rows;
+  a.per_tok_div = div_magic(static_cast<uint32_t>(kv_heads));
+  a.seq_div = div_magic(static_cast<uint32_t>(seq));
+  a.kvp = kvp;
+  a.kvp_sh = kvp_sh;
+  a.kv_tiles = (seq + 31) / 32;
+  a.v = v;
+  a.v_ss = row_stride;
+  a.v_sh = head_dim;
+  a.norm_blocks = (rows * (head_dim / 8) + 255) / 256;
+  const int64_t grid = a.norm_blocks + kv_heads * a.kv_tiles;
+  if (grid > (int64_t{1} << 31) - 1) return hipErrorInvalidValue;
+  if (head_dim == 64)
+    hipLaunchKernelGGL((rmsnorm_rope_half_kernel<uint16_t, 64, 1, true>), dim3(static_cast<unsigned>(grid)), dim3(256),
+                       0, stream, a);
+  else if (head_dim == 128)
+    hipLaunchKernelGGL((rmsnorm_rope_half_kernel<uint16_t, 128, 1, true>), dim3(static_cast<unsigned>(grid)),
+                       dim3(256), 0, stream, a);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
 }  // namespace rldx
 
 using namespace rldx;

@@ -142,7 +142,7 @@ def test_capi_rejects_bad_arguments_without_launching():
                                              8, None) == HIP_INVALID_VALUE
     assert lib.rldx_llm_fused_attention_bf16(16, 4608, 16, 16, 16, 16, 128, 1, 16, 3584, 1280, 28, 3, 128, 1e-6, 16,
                                              1 << 30, None) == HIP_INVALID_VALUE
-    assert lib.rldx_llm_fused_attention_workspace_bytes(1280, 4, 128) == 1280 * 4 * 128 * 2 + 4 * 40 * 64 * 128 * 2
+    assert lib.rldx_llm_fused_attention_workspace_bytes(1280, 4, 128) == 4 * 40 * 64 * 128 * 2
 
 
 def _gemm_groups(ms, a_ptr=256, w_ptr=512, out_ptr=1024, ldo=8192):
