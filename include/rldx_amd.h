@@ -412,6 +412,24 @@ hipError_t rldx_grouped_gemm_ws_bf16(const rldx_gemm_group_t* groups, int32_t nu
                                      int32_t epilogue, int32_t split_k, void* workspace, int64_t workspace_bytes,
                                      hipStream_t stream);
 
+#define RLDX_GEMM_WIDE_TILES 1 /* 64 x 128 / 32 x 128 tiles for streams below the 128 x 128 threshold */
+
+/*
+ * rldx_grouped_gemm_ws_bf16 with flags: RLDX_GEMM_WIDE_TILES gives the streams
+ * that would take 64 x 64 or 32 x 64 tiles 64 x 128 or 32 x 128 tiles instead
+ * (half the workgroups, each streaming a 128-column weight panel).  The K-groups
+ * are those of the narrow tiles, so the results are the same bit for bit; which
+ * is faster depends on the shape (wide: 64 x 22016 x 4096 SwiGLU 47.9 -> 42.2 us,
+ * 64 x 4096 x 11008 split 4: 23.9 -> 31.1 us on MI355X).  Other flag bits are
+ * rejected.  rldx_grouped_gemm_ex_workspace_bytes is the matching workspace query.
+ * Replaces: as rldx_grouped_gemm_bf16.
+ */
+hipError_t rldx_grouped_gemm_ex_bf16(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, int64_t k,
+                                     int32_t epilogue, int32_t split_k, int32_t flags, void* workspace,
+                                     int64_t workspace_bytes, hipStream_t stream);
+int64_t rldx_grouped_gemm_ex_workspace_bytes(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n,
+                                             int64_t k, int32_t epilogue, int32_t split_k, int32_t flags);
+
 /*
  * The QKV linears of an MSAT block with the QK-RMSNorm + RoPE + K/V tiling of
  * rldx_msat_qkv_norm_rope_bf16 in the GEMM's epilogue (one launch instead of

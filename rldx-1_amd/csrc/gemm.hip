@@ -45,8 +45,6 @@
 //     launched heaviest first; two workgroups fit on a CU (<= 72 KB LDS,
 //     <= 128 VGPRs), so the short streams' weight streaming runs beside the
 //     long stream's tiles.
-#include <type_traits>
-
 #include "rldx_amd.h"
 #include "rldx_common.h"
 
@@ -182,7 +180,10 @@ __device__ __forceinline__ void wait_barrier() {
   if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <class C, int EPI>
+// K (the kernel's WIDE) only keeps the tile specializations of the wide and
+// narrow kernels apart: the host compilation pass rejects a second caller of a
+// specialization whose body holds the 16-byte LDS-load builtin.
+template <class C, int EPI, bool K>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int item, u32x4* lds) {
   constexpr bool kSwiglu = EPI == kEpiSwiglu || EPI == kEpiSwigluPacked;
   constexpr int MB = C::MB, NB = C::NB, BNW = C::BNW, U = C::U, CH = C::CH, NSLOT = C::NSLOT;
@@ -520,9 +521,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   }
 }
 
-template <int EPI, bool DEEP>
+// WIDE: the plan uses 128 x 128, 64 x 128 and 32 x 128 tiles (always with the
+// QKV epilogue; on request for the others).
+template <int EPI, bool DEEP, bool WIDE>
 __global__ __launch_bounds__(kThreads, DEEP ? 1 : 2) void gemm_kernel(GemmArgs a) {
-  constexpr int kLds = EPI == kEpiQkv ? (DEEP ? kLdsQkvDeep : kLdsQkv) : (DEEP ? kLdsDeep : kLdsBytes);
+  constexpr int kLds = WIDE ? (DEEP ? kLdsQkvDeep : kLdsQkv) : (DEEP ? kLdsDeep : kLdsBytes);
   __shared__ __attribute__((aligned(16))) u32x4 lds[kLds / 16];
   const int b = static_cast<int>(blockIdx.x);
   int gi = 0;
@@ -532,27 +535,34 @@ __global__ __launch_bounds__(kThreads, DEEP ? 1 : 2) void gemm_kernel(GemmArgs a
   const int r = b - G.wg_begin;
   const int item = (r % kXcds) * G.per_xcd + r / kXcds;  // XCD r % 8 takes a contiguous run of tiles
   if (item >= G.items) return;
-  if constexpr (EPI == kEpiQkv) {  // whole 128-column heads: 128 x 128 or 64 x 128 tiles
+  if constexpr (WIDE && DEEP) {  // 128-column tiles (whole heads for the QKV epilogue)
     if (G.cfg == kTile128)
-      gemm_tile<typename std::conditional<DEEP, Cfg128D, Cfg128>::type, EPI>(a, G, item, lds);
+      gemm_tile<Cfg128D, EPI, WIDE>(a, G, item, lds);
     else if (G.cfg == kTile64x128)
-      gemm_tile<typename std::conditional<DEEP, Cfg64x128D, Cfg64x128>::type, EPI>(a, G, item, lds);
+      gemm_tile<Cfg64x128D, EPI, WIDE>(a, G, item, lds);
     else
-      gemm_tile<typename std::conditional<DEEP, Cfg32x128D, Cfg32x128>::type, EPI>(a, G, item, lds);
+      gemm_tile<Cfg32x128D, EPI, WIDE>(a, G, item, lds);
+  } else if constexpr (WIDE) {
+    if (G.cfg == kTile128)
+      gemm_tile<Cfg128, EPI, WIDE>(a, G, item, lds);
+    else if (G.cfg == kTile64x128)
+      gemm_tile<Cfg64x128, EPI, WIDE>(a, G, item, lds);
+    else
+      gemm_tile<Cfg32x128, EPI, WIDE>(a, G, item, lds);
   } else if constexpr (DEEP) {
     if (G.cfg == kTile128)
-      gemm_tile<Cfg128D, EPI>(a, G, item, lds);
+      gemm_tile<Cfg128D, EPI, WIDE>(a, G, item, lds);
     else if (G.cfg == kTile64)
-      gemm_tile<Cfg64D, EPI>(a, G, item, lds);
+      gemm_tile<Cfg64D, EPI, WIDE>(a, G, item, lds);
     else
-      gemm_tile<Cfg32D, EPI>(a, G, item, lds);
+      gemm_tile<Cfg32D, EPI, WIDE>(a, G, item, lds);
   } else {
     if (G.cfg == kTile128)
-      gemm_tile<Cfg128, EPI>(a, G, item, lds);
+      gemm_tile<Cfg128, EPI, WIDE>(a, G, item, lds);
     else if (G.cfg == kTile64)
-      gemm_tile<Cfg64, EPI>(a, G, item, lds);
+      gemm_tile<Cfg64, EPI, WIDE>(a, G, item, lds);
     else
-      gemm_tile<Cfg32, EPI>(a, G, item, lds);
+      gemm_tile<Cfg32, EPI, WIDE>(a, G, item, lds);
   }
 }
 
@@ -599,10 +609,11 @@ constexpr int64_t kCounterBytes = 65536;
 // from norms[i] (the caller has checked them) and never splits.
 hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, int64_t k, int32_t epilogue,
                 int split_k, GemmArgs& args, int64_t* ws_bytes, int64_t* cnt_off, int64_t* part_off,
-                const rldx_msat_stream_t* norms = nullptr) {
+                const rldx_msat_stream_t* norms = nullptr, bool wide_tiles = false) {
   if (!groups || num_groups < 1 || num_groups > 3) return hipErrorInvalidValue;
   if (epilogue < kEpiBias || epilogue > kEpiQkv) return hipErrorInvalidValue;
   const bool qkv = epilogue == kEpiQkv;
+  const bool wide = qkv || wide_tiles;
   if (qkv && (norms == nullptr || split_k > 1)) return hipErrorInvalidValue;
   // k: whole stages of every K-group split (4 K-groups x 2 k-steps); n: whole 64-column blocks
   if (n <= 0 || k <= 0 || n % 64 != 0 || k % 128 != 0) return hipErrorInvalidValue;
@@ -636,18 +647,19 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
     // Tile shape: 128 x 128 where the stream has rows and tiles enough to
     // occupy the chip (half the L2 traffic per flop of 64 x 64), else 64 x 64,
     // or 32 x 64 for streams of at most 32 rows.
-    // The QKV epilogue needs whole 128-column heads: 64 x 128 and 32 x 128 in
-    // place of 64 x 64 and 32 x 64 (same K-groups).
+    // Wide plans (the QKV epilogue needs whole 128-column heads): 64 x 128 and
+    // 32 x 128 in place of 64 x 64 and 32 x 64, with the same K-groups (so the
+    // same sums, bit for bit).
     int mt, nt, cfg, kg;
     tiles_of<Cfg128>(s.m, n, mt, nt);
     if (s.m >= 256 && static_cast<int64_t>(mt) * nt >= 128) {
       cfg = kTile128;
       kg = Cfg128::KG;
-    } else if (qkv && s.m > 32) {
+    } else if (wide && s.m > 32) {
       cfg = kTile64x128;
       kg = Cfg64x128::KG;
       tiles_of<Cfg64x128>(s.m, n, mt, nt);
-    } else if (qkv) {
+    } else if (wide) {
       cfg = kTile32x128;
       kg = Cfg32x128::KG;
       tiles_of<Cfg32x128>(s.m, n, mt, nt);
@@ -704,7 +716,11 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
     cnt_off[i] = part_off[i] = -1;
     if (G.splits > 1) {
       int kgd, per, v;
-      if (G.cfg == kTile128)
+      if (G.cfg == kTile64x128)
+        cfg_dims<Cfg64x128>(epilogue, kgd, per, v);
+      else if (G.cfg == kTile32x128)
+        cfg_dims<Cfg32x128>(epilogue, kgd, per, v);
+      else if (G.cfg == kTile128)
         cfg_dims<Cfg128>(epilogue, kgd, per, v);
       else if (G.cfg == kTile64)
         cfg_dims<Cfg64>(epilogue, kgd, per, v);
@@ -723,39 +739,66 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
   return hipSuccess;
 }
 
-hipError_t launch(const GemmArgs& args, int epilogue, hipStream_t stream) {
+hipError_t launch(const GemmArgs& args, int epilogue, hipStream_t stream, bool wide = false) {
   if (args.num_groups == 0) return hipSuccess;
   const Group& last = args.g[args.num_groups - 1];
   const int wgs = last.wg_begin + last.per_xcd * kXcds;
   const dim3 grid(static_cast<unsigned>(wgs)), block(kThreads);
   // at most one workgroup per CU (256 CUs): the deep-ring kernel
+  const bool deep = wgs <= 256;
   if (epilogue == kEpiQkv) {
-    if (wgs <= 256)
-      hipLaunchKernelGGL((gemm_kernel<kEpiQkv, true>), grid, block, 0, stream, args);
+    if (deep)
+      hipLaunchKernelGGL((gemm_kernel<kEpiQkv, true, true>), grid, block, 0, stream, args);
     else
-      hipLaunchKernelGGL((gemm_kernel<kEpiQkv, false>), grid, block, 0, stream, args);
-  } else if (wgs <= 256) {
-    if (epilogue == kEpiBias)
-      hipLaunchKernelGGL((gemm_kernel<kEpiBias, true>), grid, block, 0, stream, args);
-    else if (epilogue == kEpiResidual)
-      hipLaunchKernelGGL((gemm_kernel<kEpiResidual, true>), grid, block, 0, stream, args);
-    else if (epilogue == kEpiSwiglu)
-      hipLaunchKernelGGL((gemm_kernel<kEpiSwiglu, true>), grid, block, 0, stream, args);
-    else if (epilogue == kEpiSwigluPacked)
-      hipLaunchKernelGGL((gemm_kernel<kEpiSwigluPacked, true>), grid, block, 0, stream, args);
-    else
-      hipLaunchKernelGGL((gemm_kernel<kEpiBiasPacked, true>), grid, block, 0, stream, args);
+      hipLaunchKernelGGL((gemm_kernel<kEpiQkv, false, true>), grid, block, 0, stream, args);
+  } else if (wide) {
+    if (deep) {
+      if (epilogue == kEpiBias)
+        hipLaunchKernelGGL((gemm_kernel<kEpiBias, true, true>), grid, block, 0, stream, args);
+      else if (epilogue == kEpiResidual)
+        hipLaunchKernelGGL((gemm_kernel<kEpiResidual, true, true>), grid, block, 0, stream, args);
+      else if (epilogue == kEpiSwiglu)
+        hipLaunchKernelGGL((gemm_kernel<kEpiSwiglu, true, true>), grid, block, 0, stream, args);
+      else if (epilogue == kEpiSwigluPacked)
+        hipLaunchKernelGGL((gemm_kernel<kEpiSwigluPacked, true, true>), grid, block, 0, stream, args);
+      else
+        hipLaunchKernelGGL((gemm_kernel<kEpiBiasPacked, true, true>), grid, block, 0, stream, args);
+    } else {
+      if (epilogue == kEpiBias)
+        hipLaunchKernelGGL((gemm_kernel<kEpiBias, false, true>), grid, block, 0, stream, args);
+      else if (epilogue == kEpiResidual)
+        hipLaunchKernelGGL((gemm_kernel<kEpiResidual, false, true>), grid, block, 0, stream, args);
+      else if (epilogue == kEpiSwiglu)
+        hipLaunchKernelGGL((gemm_kernel<kEpiSwiglu, false, true>), grid, block, 0, stream, args);
+      else if (epilogue == kEpiSwigluPacked)
+        hipLaunchKernelGGL((gemm_kernel<kEpiSwigluPacked, false, true>), grid, block, 0, stream, args);
+      else
+        hipLaunchKernelGGL((gemm_kernel<kEpiBiasPacked, false, true>), grid, block, 0, stream, args);
+    }
   } else {
-    if (epilogue == kEpiBias)
-      hipLaunchKernelGGL((gemm_kernel<kEpiBias, false>), grid, block, 0, stream, args);
-    else if (epilogue == kEpiResidual)
-      hipLaunchKernelGGL((gemm_kernel<kEpiResidual, false>), grid, block, 0, stream, args);
-    else if (epilogue == kEpiSwiglu)
-      hipLaunchKernelGGL((gemm_kernel<kEpiSwiglu, false>), grid, block, 0, stream, args);
-    else if (epilogue == kEpiSwigluPacked)
-      hipLaunchKernelGGL((gemm_kernel<kEpiSwigluPacked, false>), grid, block, 0, stream, args);
-    else
-      hipLaunchKernelGGL((gemm_kernel<kEpiBiasPacked, false>), grid, block, 0, stream, args);
+    if (deep) {
+      if (epilogue == kEpiBias)
+        hipLaunchKernelGGL((gemm_kernel<kEpiBias, true, false>), grid, block, 0, stream, args);
+      else if (epilogue == kEpiResidual)
+        hipLaunchKernelGGL((gemm_kernel<kEpiResidual, true, false>), grid, block, 0, stream, args);
+      else if (epilogue == kEpiSwiglu)
+        hipLaunchKernelGGL((gemm_kernel<kEpiSwiglu, true, false>), grid, block, 0, stream, args);
+      else if (epilogue == kEpiSwigluPacked)
+        hipLaunchKernelGGL((gemm_kernel<kEpiSwigluPacked, true, false>), grid, block, 0, stream, args);
+      else
+        hipLaunchKernelGGL((gemm_kernel<kEpiBiasPacked, true, false>), grid, block, 0, stream, args);
+    } else {
+      if (epilogue == kEpiBias)
+        hipLaunchKernelGGL((gemm_kernel<kEpiBias, false, false>), grid, block, 0, stream, args);
+      else if (epilogue == kEpiResidual)
+        hipLaunchKernelGGL((gemm_kernel<kEpiResidual, false, false>), grid, block, 0, stream, args);
+      else if (epilogue == kEpiSwiglu)
+        hipLaunchKernelGGL((gemm_kernel<kEpiSwiglu, false, false>), grid, block, 0, stream, args);
+      else if (epilogue == kEpiSwigluPacked)
+        hipLaunchKernelGGL((gemm_kernel<kEpiSwigluPacked, false, false>), grid, block, 0, stream, args);
+      else
+        hipLaunchKernelGGL((gemm_kernel<kEpiBiasPacked, false, false>), grid, block, 0, stream, args);
+    }
   }
   return hipGetLastError();
 }
@@ -884,13 +927,14 @@ extern "C" int64_t rldx_grouped_gemm_workspace_bytes(const rldx_gemm_group_t* gr
   return ws;
 }
 
-extern "C" hipError_t rldx_grouped_gemm_ws_bf16(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n,
-                                                int64_t k, int32_t epilogue, int32_t split_k, void* workspace,
-                                                int64_t workspace_bytes, hipStream_t stream) {
+namespace {
+hipError_t gemm_ws(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, int64_t k, int32_t epilogue,
+                   int32_t split_k, int32_t flags, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   GemmArgs args;
   int64_t ws, co[3], po[3];
-  if (epilogue == kEpiQkv) return hipErrorInvalidValue;
-  const hipError_t e = plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po);
+  if (epilogue == kEpiQkv || (flags & ~RLDX_GEMM_WIDE_TILES)) return hipErrorInvalidValue;
+  const bool wide = (flags & RLDX_GEMM_WIDE_TILES) != 0;
+  const hipError_t e = plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po, nullptr, wide);
   if (e != hipSuccess) return e;
   if (ws > 0) {
     if (!workspace || workspace_bytes < ws || reinterpret_cast<uintptr_t>(workspace) % kWsAlign)
@@ -902,7 +946,32 @@ extern "C" hipError_t rldx_grouped_gemm_ws_bf16(const rldx_gemm_group_t* groups,
         args.g[i].part = reinterpret_cast<float*>(base + po[i]);
       }
   }
-  return launch(args, epilogue, stream);
+  return launch(args, epilogue, stream, wide);
+}
+}  // namespace
+
+extern "C" hipError_t rldx_grouped_gemm_ws_bf16(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n,
+                                                int64_t k, int32_t epilogue, int32_t split_k, void* workspace,
+                                                int64_t workspace_bytes, hipStream_t stream) {
+  return gemm_ws(groups, num_groups, n, k, epilogue, split_k, 0, workspace, workspace_bytes, stream);
+}
+
+extern "C" hipError_t rldx_grouped_gemm_ex_bf16(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n,
+                                                int64_t k, int32_t epilogue, int32_t split_k, int32_t flags,
+                                                void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  return gemm_ws(groups, num_groups, n, k, epilogue, split_k, flags, workspace, workspace_bytes, stream);
+}
+
+extern "C" int64_t rldx_grouped_gemm_ex_workspace_bytes(const rldx_gemm_group_t* groups, int32_t num_groups,
+                                                        int64_t n, int64_t k, int32_t epilogue, int32_t split_k,
+                                                        int32_t flags) {
+  GemmArgs args;
+  int64_t ws, co[3], po[3];
+  if (epilogue == kEpiQkv || (flags & ~RLDX_GEMM_WIDE_TILES) ||
+      plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po, nullptr,
+           (flags & RLDX_GEMM_WIDE_TILES) != 0) != hipSuccess)
+    return -1;
+  return ws;
 }
 
 extern "C" int64_t rldx_act_packed_elems(int64_t m, int64_t k) {

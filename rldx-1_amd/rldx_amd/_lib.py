@@ -95,6 +95,10 @@ SIGNATURES = {
     "rldx_grouped_gemm_workspace_bytes": (c_i64, [ctypes.POINTER(GemmGroup), c_i32, c_i64, c_i64, c_i32, c_i32]),
     "rldx_grouped_gemm_ws_bf16": (c_i32, [ctypes.POINTER(GemmGroup), c_i32, c_i64, c_i64, c_i32, c_i32, c_vp, c_i64,
                                           c_vp]),
+    "rldx_grouped_gemm_ex_bf16": (c_i32, [ctypes.POINTER(GemmGroup), c_i32, c_i64, c_i64, c_i32, c_i32, c_i32, c_vp,
+                                          c_i64, c_vp]),
+    "rldx_grouped_gemm_ex_workspace_bytes": (c_i64, [ctypes.POINTER(GemmGroup), c_i32, c_i64, c_i64, c_i32, c_i32,
+                                                     c_i32]),
     "rldx_grouped_gemm_qkv_norm_rope_bf16": (c_i32, [ctypes.POINTER(GemmGroup), ctypes.POINTER(MsatStream), c_i32,
                                                      c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_f32,
                                                      c_vp]),
@@ -108,6 +112,7 @@ SIGNATURES = {
 
 ROPE_SIN_SIGNED = 1  # RLDX_ROPE_SIN_SIGNED
 GEMM_EPI_BIAS, GEMM_EPI_RESIDUAL, GEMM_EPI_SWIGLU, GEMM_EPI_SWIGLU_PACKED, GEMM_EPI_BIAS_PACKED = 0, 1, 2, 3, 4
+GEMM_WIDE_TILES = 1  # RLDX_GEMM_WIDE_TILES
 
 _lib = None
 _hip = None

@@ -635,17 +635,19 @@ def _gemm_groups(items: Sequence[tuple], epi: int, pack: bool):
     return groups, n, k, keep, w.data
 
 
-def grouped_gemm_workspace_bytes(items: Sequence[tuple], epilogue: str = "bias", split_k: int = 1) -> int:
-    """Workspace bytes grouped_gemm(items, epilogue, split_k, workspace) needs (0: no split)."""
+def grouped_gemm_workspace_bytes(items: Sequence[tuple], epilogue: str = "bias", split_k: int = 1,
+                                 wide_tiles: bool = False) -> int:
+    """Workspace bytes grouped_gemm(items, epilogue, split_k, workspace, wide_tiles) needs (0: no split)."""
     epi = _GEMM_EPI[epilogue]
     groups, n, k, _, _ = _gemm_groups(items, epi, pack=False)
-    r = _lib.load().rldx_grouped_gemm_workspace_bytes(groups, len(items), n, k, epi, int(split_k))
+    r = _lib.load().rldx_grouped_gemm_ex_workspace_bytes(groups, len(items), n, k, epi, int(split_k),
+                                                         _lib.GEMM_WIDE_TILES if wide_tiles else 0)
     _require(r >= 0, "grouped GEMM shape not supported")
     return int(r)
 
 
 def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias", split_k: int = 1,
-                 workspace: Optional[GemmWorkspace] = None) -> None:
+                 workspace: Optional[GemmWorkspace] = None, wide_tiles: bool = False) -> None:
     """One launch of y_s = a_s W_s^T + bias_s for up to 3 streams sharing n and k.
     items: (a PackedAct [m, k] or row-major tensor (packed first), PackedWeight,
     bias [n] or None, out, residual or None).  epilogue: "bias" (out = y),
@@ -654,11 +656,20 @@ def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias", split_k: int = 
     of a wider one: PackedAct.cols).  split_k > 1 splits the K
     range of every stream over that many workgroups (partials summed in a fixed
     order: deterministic); it needs a workspace of grouped_gemm_workspace_bytes(...)
-    bytes."""
+    bytes.  wide_tiles: 64 x 128 / 32 x 128 tiles for the streams below the 128 x
+    128 threshold (RLDX_GEMM_WIDE_TILES; the same results, faster or slower by
+    shape)."""
     epi = _GEMM_EPI[epilogue]
     groups, n, k, keep, wt = _gemm_groups(items, epi, pack=True)
     lib = _lib.load()
-    if split_k <= 1:
+    if wide_tiles:
+        _require(split_k <= 1 or workspace is not None, "split_k > 1 needs a GemmWorkspace")
+        ws_ptr, ws_n = (workspace.data.data_ptr(), workspace.data.numel()) if split_k > 1 else (None, 0)
+        if split_k > 1:
+            _on_gpu(workspace.data)
+        _lib.check(lib.rldx_grouped_gemm_ex_bf16(groups, len(items), n, k, epi, int(split_k), _lib.GEMM_WIDE_TILES,
+                                                 ws_ptr, ws_n, _stream_ptr(wt)), "rldx_grouped_gemm_ex_bf16")
+    elif split_k <= 1:
         _lib.check(lib.rldx_grouped_gemm_bf16(groups, len(items), n, k, epi, _stream_ptr(wt)), "rldx_grouped_gemm_bf16")
     else:
         _require(workspace is not None, "split_k > 1 needs a GemmWorkspace")

@@ -321,7 +321,7 @@ class RldxMsat:
         self.out_gemm = self._planned(
             [(self.mod_packed, self.proj_out_2, self.w["proj_out_2.bias"], self.out[0], None)], "bias")
         plans = [g for d in self.ds_gemms + self.ss_gemms for g in d.values()] + [self.vl_proj_gemm, self.out_gemm]
-        self.ws = Fn.GemmWorkspace(max(Fn.grouped_gemm_workspace_bytes(it, epi, sk) for it, epi, sk in plans),
+        self.ws = Fn.GemmWorkspace(max(Fn.grouped_gemm_workspace_bytes(it, epi, sk, wide) for it, epi, sk, wide in plans),
                                    self.dev)
 
     @staticmethod
@@ -345,9 +345,19 @@ class RldxMsat:
             split *= 2
         return split
 
+    @staticmethod
+    def wide_for(n: int, epi: str, split: int) -> bool:
+        """64 x 128 / 32 x 128 tiles (RLDX_GEMM_WIDE_TILES, the same results bit
+        for bit) for the wide unsplit SwiGLU GEMMs: measured per GEMM at the
+        release shape, DS vl_w12 (64 x 22016 x 4096) 47.9 -> 42.2 us and SS mlp
+        (82 x 12288 x 1536) 17.6 -> 16.2 us; every other GEMM of the model was
+        slower with them (vl_w3 23.9 -> 31.1, sa_w12 9.7 -> 11.6)."""
+        return epi.startswith("swiglu") and n >= 12288 and split == 1
+
     def _planned(self, items, epi):
         a, w = items[0][0], items[0][1]
-        return (items, epi, self.split_for(a.m, w.n, w.k))
+        split = self.split_for(a.m, w.n, w.k)
+        return (items, epi, split, self.wide_for(w.n, epi, split))
 
     def _ds_gemm_items(self, blk: dict) -> dict:
         cfg = self.cfg
@@ -380,8 +390,8 @@ class RldxMsat:
         }
 
     def _gemm(self, plan) -> None:
-        items, epi, split = plan
-        Fn.grouped_gemm(items, epi, split_k=split, workspace=self.ws if split > 1 else None)
+        items, epi, split, wide = plan
+        Fn.grouped_gemm(items, epi, split_k=split, workspace=self.ws if split > 1 else None, wide_tiles=wide)
 
     # -- blocks ---------------------------------------------------------------
     def _ds_block(self, blk: dict, gm: dict) -> None:

@@ -367,6 +367,38 @@ def test_grouped_gemm_qkv_norm_rope_matches_two_launches(dev, ms, H, k):
     assert torch.equal(kvp.view(torch.int16), kvp2.view(torch.int16))
 
 
+@pytest.mark.parametrize("epilogue,ms,n,k,split", [("swiglu_packed", (64,), 22016, 512, 1),
+                                                   ("swiglu_packed", (82, 18), 12288, 256, 1),
+                                                   ("residual", (64, 18), 1536, 1024, 4),
+                                                   ("bias", (512, 64, 32), 1536, 256, 1),
+                                                   ("bias_packed", (40,), 4096, 256, 2)])
+def test_grouped_gemm_wide_tiles_bit_identical(dev, epilogue, ms, n, k, split):
+    """64 x 128 / 32 x 128 tiles (RLDX_GEMM_WIDE_TILES) keep the K-groups of 64 x 64
+    / 32 x 64, so every epilogue gives the same bits as the default plan, with and
+    without split-K."""
+    swiglu = epilogue.startswith("swiglu")
+    n_out = n // 2 if swiglu else n
+    packed = epilogue.endswith("packed")
+    outs = []
+    for wide in (False, True):
+        items = []
+        gg = torch.Generator().manual_seed(n + k)
+        for m in ms:
+            a = Fn.pack_act(_rand((m, k), gg).to(dev))
+            w = Fn.pack_weight(_rand((n, k), gg, std=k ** -0.5).to(dev), swiglu_pairs=swiglu)
+            b = _rand((n,), gg, std=0.5).to(dev)
+            res = _rand((m, n_out), gg).to(dev) if epilogue == "residual" else None
+            out = Fn.PackedAct.empty(m, n_out, dev) if packed else (res if res is not None else
+                                                                   torch.empty(m, n_out, dtype=BF16, device=dev))
+            items.append((a, w, b, out, res))
+        ws = Fn.GemmWorkspace(Fn.grouped_gemm_workspace_bytes(items, epilogue, split, wide), dev) if split > 1 else None
+        Fn.grouped_gemm(items, epilogue, split_k=split, workspace=ws, wide_tiles=wide)
+        torch.cuda.synchronize()
+        outs.append([(it[3].unpack() if packed else it[3]).clone() for it in items])  # rows < m only
+    for x, y in zip(*outs):
+        assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+
+
 def test_ss_fused_mlp_swiglu_op(dev):
     import rldx_amd.ops  # noqa: F401  registers ss::fused_mlp_swiglu
 
