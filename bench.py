@@ -52,11 +52,72 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--kernel-reps", type=int, default=50)
-    ap.add_argument("--profile-kernel", choices=["qkv", "proj", "w12", "w3"], default=None,
-                    help="run one of the step's grouped GEMMs alone (for counter passes) and exit")
+    ap.add_argument("--profile-kernel", choices=["qkv", "proj", "w12", "w3"] + list(PROFILE_KERNELS), default=None,
+                    help="run one kernel alone, 64 launches (for counter passes), and exit")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a 256 MiB device-to-device copy 4 times (traffic counter calibration) and exit")
     return ap.parse_args()
+
+
+PROFILE_KERNELS = ("joint_attn", "gqa_attn", "gqa_op", "step_attn", "swiglu", "rmsnorm_rope")
+
+
+def profile_launch(name: str, torch):
+    """A zero-argument launcher of one kernel at its workload shape, for counter
+    passes (inputs built once; every call is one launch of the kernel under test,
+    plus the K-side launch of the backbone operator for gqa_op)."""
+    from rldx_amd import functional as Fn
+    from rldx_amd import workloads as W
+    from rldx_amd.msat_step import MsatStepCfg
+
+    dev = torch.device("cuda:0")
+    if name == "swiglu":  # 2048 x 11008
+        x = W.swiglu_inputs(W.SwigluCfg())["x"].to(dev)
+        y = torch.empty(x.shape[0], x.shape[1] // 2, dtype=torch.bfloat16, device=dev)
+        return lambda: Fn.swiglu(x, out=y)
+    if name == "rmsnorm_rope":  # fp32 16384 x 16 x 64 (the HBM-bound sweep point)
+        rs = W.RmsRopeCfg(seq=16384)
+        shape = (rs.batch, rs.seq, rs.heads, rs.head_dim)
+        q, k = torch.randn(shape, device=dev), torch.randn(shape, device=dev)
+        cs, sn = (t.to(dev) for t in W.qwen_rope_cos_sin(rs.seq, rs.head_dim, rs.theta))
+        w = torch.ones(rs.head_dim, device=dev)
+        qo, ko = torch.empty_like(q), torch.empty_like(k)
+        return lambda: Fn.qk_rmsnorm_rope_half(q, k, w, w, cs, sn, rs.eps, q_out=qo, k_out=ko)
+    if name == "joint_attn":  # 16 x 608 x 128, 8 masked keys
+        jc = W.JointAttnCfg()
+        ji = W.joint_attn_inputs(jc)
+        q, k, v = (ji[n].to(dev) for n in ("q", "k", "v"))
+        bias = torch.where(ji["kv_mask"] == 0, float("-inf"), 0.0).float().to(dev)
+        o = torch.empty_like(q)
+        kvp = Fn.kv_pack(k, v)
+        return lambda: Fn.attention_packed(q, kvp, jc.tokens, key_bias=bias, out=o)
+    if name == "step_attn":  # 12 x 608 x 128, 8 masked keys
+        sc = MsatStepCfg()
+        n = sc.tokens
+        q, k, v = (torch.randn(1, sc.heads, n, sc.head_dim, device=dev).to(torch.bfloat16) for _ in range(3))
+        bias = torch.zeros(n, device=dev)
+        bias[n - sc.n_p_pad:] = float("-inf")
+        o = torch.empty_like(q)
+        kvp = Fn.kv_pack(k, v)
+        return lambda: Fn.attention_packed(q, kvp, n, key_bias=bias, out=o)
+    gc = W.GqaCfg()
+    if name == "gqa_attn":  # causal 28/4 x 1280 x 128 on pre-normalised Q/K
+        M, Hq, Hkv, D = gc.seq, gc.q_heads, gc.kv_heads, gc.head_dim
+        q = torch.randn(1, M, Hq, D, device=dev).to(torch.bfloat16)
+        k = torch.randn(1, M, Hkv, D, device=dev).to(torch.bfloat16)
+        v = torch.randn(1, M, Hkv, D, device=dev).to(torch.bfloat16)
+        o = torch.empty_like(q)
+        kvp = Fn.kv_pack(k, v, layout="bshd")
+        return lambda: Fn.attention_packed(q, kvp, M, causal=True, layout="bshd", out=o)
+    # gqa_op: rldx_backbone::fused_attention (K norm + K/V tiles, then attention with the Q norm)
+    import rldx_amd.ops as ops
+
+    gi = W.gqa_inputs(gc)
+    args = (gi["qkv"].to(dev), gi["q_norm_w"].to(dev), None, gi["k_norm_w"].to(dev), None, gi["cos"].to(dev),
+            W.signed_sin(gi["sin"]).to(dev))
+    ob = torch.empty(gc.seq, gc.q_heads * gc.head_dim, dtype=torch.bfloat16, device=dev)
+    return lambda: ops.llm_fused_attention(*args, num_heads=gc.q_heads, num_kv_heads=gc.kv_heads,
+                                           head_dim=gc.head_dim, out=ob)
 
 
 def graph_time_ms(fn, reps: int, torch) -> float:
@@ -390,6 +451,13 @@ def main():
 
     rldx_amd.load()
     dev = torch.device("cuda:0")
+    if args.profile_kernel in PROFILE_KERNELS:
+        fn = profile_launch(args.profile_kernel, torch)
+        for _ in range(64):
+            fn()
+        torch.cuda.synchronize()
+        print(f"[bench] {args.profile_kernel}: 64 launches", file=sys.stderr, flush=True)
+        return
     if args.copy_calibration:
         a = torch.empty(128 << 20, dtype=torch.bfloat16, device=dev)
         b = torch.empty_like(a)

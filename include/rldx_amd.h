@@ -397,7 +397,9 @@ int64_t rldx_grouped_gemm_workspace_bytes(const rldx_gemm_group_t* groups, int32
  * part of the operands; the partial tiles are summed in split
  * order by the last workgroup to finish the tile, so results do not depend on
  * timing (they differ from the unsplit sum by fp32 rounding only).  The splits
- * of a tile run on one XCD and meet in its L2.
+ * exchange partials with device-scope stores, loads and counter atomics, so the
+ * hand-off holds on whichever XCDs they run; the launch places the splits of a
+ * tile on one XCD, where the exchange stays close to that XCD's L2.
  * workspace: device memory, 256-byte aligned, at least
  * rldx_grouped_gemm_workspace_bytes(...) bytes, zero-filled before its first
  * use; each launch leaves it ready for the next, whatever its shapes (the first
@@ -413,6 +415,7 @@ hipError_t rldx_grouped_gemm_ws_bf16(const rldx_gemm_group_t* groups, int32_t nu
                                      hipStream_t stream);
 
 #define RLDX_GEMM_WIDE_TILES 1 /* 64 x 128 / 32 x 128 tiles for streams below the 128 x 128 threshold */
+#define RLDX_GEMM_SPLITS_ACROSS_XCDS 2 /* the splits of a tile on different XCDs (tests of the split hand-off) */
 
 /*
  * rldx_grouped_gemm_ws_bf16 with flags: RLDX_GEMM_WIDE_TILES gives the streams
@@ -420,8 +423,10 @@ hipError_t rldx_grouped_gemm_ws_bf16(const rldx_gemm_group_t* groups, int32_t nu
  * (half the workgroups, each streaming a 128-column weight panel).  The K-groups
  * are those of the narrow tiles, so the results are the same bit for bit; which
  * is faster depends on the shape (wide: 64 x 22016 x 4096 SwiGLU 47.9 -> 42.2 us,
- * 64 x 4096 x 11008 split 4: 23.9 -> 31.1 us on MI355X).  Other flag bits are
- * rejected.  rldx_grouped_gemm_ex_workspace_bytes is the matching workspace query.
+ * 64 x 4096 x 11008 split 4: 23.9 -> 31.1 us on MI355X).
+ * RLDX_GEMM_SPLITS_ACROSS_XCDS places the splits of each tile on consecutive
+ * workgroups (different XCDs) instead of on one XCD: the same results bit for
+ * bit, for tests of the cross-XCD hand-off.  Other flag bits are rejected.  rldx_grouped_gemm_ex_workspace_bytes is the matching workspace query.
  * Replaces: as rldx_grouped_gemm_bf16.
  */
 hipError_t rldx_grouped_gemm_ex_bf16(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, int64_t k,

@@ -59,9 +59,18 @@ def _qk_norm(x, w):
     return msat_rmsnorm(x, w)
 
 
-def ds_block(sd: dict, p: str, sa: torch.Tensor, vl: torch.Tensor, pe: torch.Tensor, heads: int):
+def key_bias_of(mask: torch.Tensor, n_rest: int, dtype) -> torch.Tensor:
+    """Joint-attention key mask of an encoder (VL) mask: cat([mask, ones]) then
+    -inf where 0 and 0 elsewhere, in the activation dtype (blocks.py:558-575,
+    msat.py:517-531).  mask [B, N_vl] -> [B, N_vl + n_rest]."""
+    kv = torch.cat([mask, torch.ones(mask.shape[0], n_rest, dtype=mask.dtype)], dim=1)
+    return torch.where(kv == 0, torch.tensor(float("-inf"), dtype=dtype), torch.tensor(0.0, dtype=dtype))
+
+
+def ds_block(sd: dict, p: str, sa: torch.Tensor, vl: torch.Tensor, pe: torch.Tensor, heads: int, key_bias=None):
     """DoubleStreamBlock.forward, identity modulation (blocks.py:383-609).
-    sa [B, N_sa, sa_dim] (time token first), vl [B, N_vl, vl_dim]; pe [B, N_vl + N_sa, Dh/2]."""
+    sa [B, N_sa, sa_dim] (time token first), vl [B, N_vl, vl_dim]; pe [B, N_vl + N_sa, Dh/2];
+    key_bias [B, N_vl + N_sa] additive or None."""
     sa_qkv = _linear(layer_norm(sa), sd, f"{p}sa_qkv")
     vl_qkv = _linear(layer_norm(vl), sd, f"{p}vl_qkv")
     sa_q, sa_k, sa_v = (split_heads(t, heads) for t in sa_qkv.chunk(3, dim=-1))
@@ -72,7 +81,7 @@ def ds_block(sd: dict, p: str, sa: torch.Tensor, vl: torch.Tensor, pe: torch.Ten
     k = torch.cat([vl_k, sa_k], dim=2)
     v = torch.cat([vl_v, sa_v], dim=2)
     q, k = apply_rotary_emb(q, k, pe)
-    o = sdpa(q, k, v)
+    o = sdpa(q, k, v, key_bias=key_bias)
     n_vl = vl.shape[1]
     sa = sa + _linear(merge_heads(o[:, :, n_vl:]), sd, f"{p}sa_proj")
     vl = vl + _linear(merge_heads(o[:, :, :n_vl]), sd, f"{p}vl_proj")
@@ -81,7 +90,7 @@ def ds_block(sd: dict, p: str, sa: torch.Tensor, vl: torch.Tensor, pe: torch.Ten
     return sa, vl
 
 
-def ss_block(sd: dict, p: str, x: torch.Tensor, pe: torch.Tensor, heads: int):
+def ss_block(sd: dict, p: str, x: torch.Tensor, pe: torch.Tensor, heads: int, key_bias=None):
     """SingleStreamBlock.forward with SwiGLU, identity modulation (blocks.py:166-254)."""
     inner = sd[f"{p}linear2.weight"].shape[1] - sd[f"{p}mlp_proj.weight"].shape[0]
     h = _linear(layer_norm(x), sd, f"{p}linear1")
@@ -89,18 +98,20 @@ def ss_block(sd: dict, p: str, x: torch.Tensor, pe: torch.Tensor, heads: int):
     q, k, v = (split_heads(t, heads) for t in qkv.chunk(3, dim=-1))
     q, k = _qk_norm(q, sd[f"{p}q_norm.weight"]), _qk_norm(k, sd[f"{p}k_norm.weight"])
     q, k = apply_rotary_emb(q, k, pe)
-    attn = merge_heads(sdpa(q, k, v))
+    attn = merge_heads(sdpa(q, k, v, key_bias=key_bias))
     mlp_out = _linear(swiglu(mlp), sd, f"{p}mlp_proj")
     return x + _linear(torch.cat([attn, mlp_out], dim=-1), sd, f"{p}linear2")
 
 
 def msat_forward(sd: dict, sa_embs: torch.Tensor, vl_embs: torch.Tensor, temb: torch.Tensor,
                  time_token: torch.Tensor, *, heads: int, head_dim: int, ds_blocks: int, ss_blocks: int,
-                 theta: float = 10000.0, max_seq_len: int = 1024, bf16_quirk: bool = True) -> torch.Tensor:
+                 theta: float = 10000.0, max_seq_len: int = 1024, bf16_quirk: bool = True,
+                 encoder_attention_mask=None) -> torch.Tensor:
     """MSAT._forward_inner, non-physics path, temb_type input_token, rope_sa_only
     (msat.py:291-556) and _output_projection (:777-781).
     sa_embs [B, N_sa_pure, sa_dim], vl_embs [B, N_vl, vl_dim], temb [B, inner],
-    time_token [B, num_temb_tokens, sa_dim]; returns [B, N_sa_pure, output_dim]."""
+    time_token [B, num_temb_tokens, sa_dim]; encoder_attention_mask [B, N_vl]
+    (1 = visible) or None; returns [B, N_sa_pure, output_dim]."""
     tables = rope_freq_tables(head_dim, theta, max_seq_len, bf16_quirk)
     num_temb = time_token.shape[1]
     B, n_vl = vl_embs.shape[:2]
@@ -111,9 +122,10 @@ def msat_forward(sd: dict, sa_embs: torch.Tensor, vl_embs: torch.Tensor, temb: t
     ids[:, n_vl:n_vl + num_temb, 1] = torch.arange(num_temb)
     ids[:, n_vl + num_temb:, 1] = torch.arange(num_temb, n_sa)
     pe = rope_pe(tables, ids)
+    kb = None if encoder_attention_mask is None else key_bias_of(encoder_attention_mask, n_sa, vl_embs.dtype)
     vl = vl_embs
     for i in range(ds_blocks):
-        sa, vl = ds_block(sd, f"double_blocks.{i}.", sa, vl, pe, heads)
+        sa, vl = ds_block(sd, f"double_blocks.{i}.", sa, vl, pe, heads, kb)
     time_tok = sa[:, :num_temb]
     sa = sa[:, num_temb:]
     x = torch.cat([_linear(vl, sd, "vl_proj_to_sa"), time_tok, sa], dim=1)
@@ -124,7 +136,7 @@ def msat_forward(sd: dict, sa_embs: torch.Tensor, vl_embs: torch.Tensor, temb: t
     ids_s[:, x.shape[1] - n_pure:, 1] = torch.arange(num_temb + 1, num_temb + 1 + n_pure)
     pe_s = rope_pe(tables, ids_s)
     for i in range(ss_blocks):
-        x = ss_block(sd, f"single_blocks.{i}.", x, pe_s, heads)
+        x = ss_block(sd, f"single_blocks.{i}.", x, pe_s, heads, kb)
     sa = x[:, -n_pure:]
     shift, scale = _linear(F.silu(temb), sd, "proj_out_1").chunk(2, dim=1)
     sa = layer_norm(sa) * (1 + scale[:, None]) + shift[:, None]

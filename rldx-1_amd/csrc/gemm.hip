@@ -57,6 +57,9 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kXcds = 8;
+// Cache-policy immediate of a buffer load / store at device scope: SC1 = 1,
+// SC0 = 0 (the instruction's own access is coherent across the XCDs' L2s).
+constexpr int kCpolDevice = 16;
 constexpr int kThreads = 512;          // 8 waves per workgroup
 constexpr int kBufWord3 = 0x00020000;  // gfx9 raw buffer descriptor, word 3 (untyped dword data)
 
@@ -162,6 +165,7 @@ struct GemmArgs {
   int num_groups;
   int n, k;  // n = rows of W (2 * N_half with the SwiGLU epilogue)
   QkvOut qkv;
+  int spread;  // != 0: the splits of a tile on different XCDs (RLDX_GEMM_SPLITS_ACROSS_XCDS)
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const uint16_t* p, int bytes) {
@@ -447,12 +451,16 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     }
   }
   if (G.splits > 1) {
-    // Split-K.  The splits of a tile run on one XCD (the launch gives every XCD
-    // whole tiles), so that XCD's L2 is their meeting point: each split stores
-    // its fp32 partial, waits until the stores have reached L2, then counts in
-    // with an L2 atomic; the last to arrive reads the other partials past its
-    // L1, sums all of them in split order (the same order whichever split
-    // arrives last), applies the epilogue and re-arms the counter.
+    // Split-K.  Each split stores its fp32 partial with device-scope stores
+    // (SC1: written through to the device coherence point, not held in this
+    // XCD's L2), waits until they are complete, then counts in with a
+    // device-scope atomic; the last to arrive reads the other partials with
+    // device-scope loads (SC1: not served from a possibly stale L1 / L2), sums
+    // all of them in split order (the same order whichever split arrives last),
+    // applies the epilogue and re-arms the counter.  This holds wherever the
+    // splits run; the launch normally gives every XCD whole tiles, so the
+    // splits of a tile share one L2 (RLDX_GEMM_SPLITS_ACROSS_XCDS places them
+    // on different XCDs, for tests).
     const int part_bytes = G.items * PER * kThreads * V * 4;  // < 2^31 (host check)
     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(G.part, 0, part_bytes, kBufWord3);
     auto slot = [&](int sp, int i) { return (((tile * G.splits + sp) * PER + i) * kThreads + threadIdx.x) * V * 4; };
@@ -462,12 +470,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
       for (int e = 0; e < V; e += 4)
         __builtin_amdgcn_raw_buffer_store_b128(
             __builtin_bit_cast(u32x4, floatx4{y[i][e], y[i][e + 1], y[i][e + 2], y[i][e + 3]}), prs,
-            slot(split, i) + 4 * e, 0, 0);
+            slot(split, i) + 4 * e, 0, kCpolDevice);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     int* last = reinterpret_cast<int*>(lds) + kLdsBytes / 4 - 1;  // past every epilogue tile, in both kernels' LDS
     if (threadIdx.x == 0)
-      *last = __hip_atomic_fetch_add(G.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
+      *last = __hip_atomic_fetch_add(G.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
               static_cast<unsigned>(G.splits - 1);
     __syncthreads();
     if (!*last) return;
@@ -482,7 +490,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
           const floatx4 v =
               sp == split ? floatx4{y[i][e], y[i][e + 1], y[i][e + 2], y[i][e + 3]}
                           : __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(prs, slot(sp, i) + 4 * e,
-                                                                                              0, 1 /* sc0: past L1 */));
+                                                                                              0, kCpolDevice));
 #pragma unroll
           for (int f = 0; f < 4; ++f) sum[e + f] += v[f];
         }
@@ -490,7 +498,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
 #pragma unroll
       for (int e = 0; e < V; ++e) y[i][e] = sum[e];
     }
-    if (threadIdx.x == 0) __hip_atomic_store(G.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (threadIdx.x == 0) __hip_atomic_store(G.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
@@ -533,7 +541,9 @@ __global__ __launch_bounds__(kThreads, DEEP ? 1 : 2) void gemm_kernel(GemmArgs a
   if (a.num_groups > 2 && b >= a.g[2].wg_begin) gi = 2;
   const Group& G = a.g[gi];
   const int r = b - G.wg_begin;
-  const int item = (r % kXcds) * G.per_xcd + r / kXcds;  // XCD r % 8 takes a contiguous run of tiles
+  // XCD r % 8 takes a contiguous run of tiles; spread: consecutive items (the
+  // splits of a tile) on consecutive workgroups, i.e. on different XCDs
+  const int item = a.spread ? r : (r % kXcds) * G.per_xcd + r / kXcds;
   if (item >= G.items) return;
   if constexpr (WIDE && DEEP) {  // 128-column tiles (whole heads for the QKV epilogue)
     if (G.cfg == kTile128)
@@ -932,10 +942,12 @@ hipError_t gemm_ws(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t 
                    int32_t split_k, int32_t flags, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   GemmArgs args;
   int64_t ws, co[3], po[3];
-  if (epilogue == kEpiQkv || (flags & ~RLDX_GEMM_WIDE_TILES)) return hipErrorInvalidValue;
+  if (epilogue == kEpiQkv || (flags & ~(RLDX_GEMM_WIDE_TILES | RLDX_GEMM_SPLITS_ACROSS_XCDS)))
+    return hipErrorInvalidValue;
   const bool wide = (flags & RLDX_GEMM_WIDE_TILES) != 0;
   const hipError_t e = plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po, nullptr, wide);
   if (e != hipSuccess) return e;
+  args.spread = (flags & RLDX_GEMM_SPLITS_ACROSS_XCDS) != 0;
   if (ws > 0) {
     if (!workspace || workspace_bytes < ws || reinterpret_cast<uintptr_t>(workspace) % kWsAlign)
       return hipErrorInvalidValue;
@@ -967,7 +979,7 @@ extern "C" int64_t rldx_grouped_gemm_ex_workspace_bytes(const rldx_gemm_group_t*
                                                         int32_t flags) {
   GemmArgs args;
   int64_t ws, co[3], po[3];
-  if (epilogue == kEpiQkv || (flags & ~RLDX_GEMM_WIDE_TILES) ||
+  if (epilogue == kEpiQkv || (flags & ~(RLDX_GEMM_WIDE_TILES | RLDX_GEMM_SPLITS_ACROSS_XCDS)) ||
       plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po, nullptr,
            (flags & RLDX_GEMM_WIDE_TILES) != 0) != hipSuccess)
     return -1;

@@ -113,6 +113,7 @@ SIGNATURES = {
 ROPE_SIN_SIGNED = 1  # RLDX_ROPE_SIN_SIGNED
 GEMM_EPI_BIAS, GEMM_EPI_RESIDUAL, GEMM_EPI_SWIGLU, GEMM_EPI_SWIGLU_PACKED, GEMM_EPI_BIAS_PACKED = 0, 1, 2, 3, 4
 GEMM_WIDE_TILES = 1  # RLDX_GEMM_WIDE_TILES
+GEMM_SPLITS_ACROSS_XCDS = 2  # RLDX_GEMM_SPLITS_ACROSS_XCDS
 
 _lib = None
 _hip = None

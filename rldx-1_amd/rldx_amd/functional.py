@@ -647,7 +647,8 @@ def grouped_gemm_workspace_bytes(items: Sequence[tuple], epilogue: str = "bias",
 
 
 def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias", split_k: int = 1,
-                 workspace: Optional[GemmWorkspace] = None, wide_tiles: bool = False) -> None:
+                 workspace: Optional[GemmWorkspace] = None, wide_tiles: bool = False,
+                 splits_across_xcds: bool = False) -> None:
     """One launch of y_s = a_s W_s^T + bias_s for up to 3 streams sharing n and k.
     items: (a PackedAct [m, k] or row-major tensor (packed first), PackedWeight,
     bias [n] or None, out, residual or None).  epilogue: "bias" (out = y),
@@ -658,16 +659,18 @@ def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias", split_k: int = 
     order: deterministic); it needs a workspace of grouped_gemm_workspace_bytes(...)
     bytes.  wide_tiles: 64 x 128 / 32 x 128 tiles for the streams below the 128 x
     128 threshold (RLDX_GEMM_WIDE_TILES; the same results, faster or slower by
-    shape)."""
+    shape).  splits_across_xcds: the splits of each tile on different XCDs
+    (RLDX_GEMM_SPLITS_ACROSS_XCDS; the same results, for tests)."""
     epi = _GEMM_EPI[epilogue]
     groups, n, k, keep, wt = _gemm_groups(items, epi, pack=True)
     lib = _lib.load()
-    if wide_tiles:
+    flags = (_lib.GEMM_WIDE_TILES if wide_tiles else 0) | (_lib.GEMM_SPLITS_ACROSS_XCDS if splits_across_xcds else 0)
+    if flags:
         _require(split_k <= 1 or workspace is not None, "split_k > 1 needs a GemmWorkspace")
         ws_ptr, ws_n = (workspace.data.data_ptr(), workspace.data.numel()) if split_k > 1 else (None, 0)
         if split_k > 1:
             _on_gpu(workspace.data)
-        _lib.check(lib.rldx_grouped_gemm_ex_bf16(groups, len(items), n, k, epi, int(split_k), _lib.GEMM_WIDE_TILES,
+        _lib.check(lib.rldx_grouped_gemm_ex_bf16(groups, len(items), n, k, epi, int(split_k), flags,
                                                  ws_ptr, ws_n, _stream_ptr(wt)), "rldx_grouped_gemm_ex_bf16")
     elif split_k <= 1:
         _lib.check(lib.rldx_grouped_gemm_bf16(groups, len(items), n, k, epi, _stream_ptr(wt)), "rldx_grouped_gemm_bf16")

@@ -24,6 +24,7 @@ fixed 4096-wide output), and `kv_mask` on the 3-way ops (1 = visible key,
 
 from __future__ import annotations
 
+import math
 import weakref
 from typing import Optional
 
@@ -186,7 +187,8 @@ def ss_fused_attention_2way(
 
 @ss_fused_attention_2way.register_fake
 def _(qkv, q_norm_weight, k_norm_weight, rope_cos, rope_sin, n_sa, num_heads=24, head_dim=64):
-    return qkv.new_empty((1, qkv.shape[0], num_heads * head_dim))
+    # the op flattens every leading dim of qkv into the token count, as _qkv_cols does
+    return qkv.new_empty((1, math.prod(qkv.shape[:-1]), num_heads * head_dim))
 
 
 @torch.library.custom_op("ss::fused_attention_3way", mutates_args=())

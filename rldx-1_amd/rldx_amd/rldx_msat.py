@@ -32,6 +32,12 @@ Per SingleStreamBlock (7 launches):
     + SwiGLU -> packed; QK-RMSNorm + RoPE; attention -> columns [0, inner) of
     the packed linear2 operand; mlp_proj (+ bias) -> its columns [inner, ...);
     linear2 + residual (in place).
+VL rows are padded to a multiple of 32 (whole 32-row blocks of the packed
+activations, so the SA rows of a packed matrix start at a block boundary); the
+padding rows start at zero every forward and their keys carry a -inf key bias,
+so they never reach a real row.  The same key-bias vector carries the
+`encoder_attention_mask` of the eager MSAT (1 = visible VL token, 0 = masked;
+msat.py:517-531, blocks.py:558-575) when the chain is built with vl_mask=True.
 The GEMMs have 18, 64 or 82 rows, so their launches have only 24-144 output
 tiles: each is split over K (split_for) towards 256 workgroups, partials summed
 in a fixed order in one shared workspace.
@@ -230,11 +236,16 @@ class RldxMsat:
     """Static-buffer executor of the RLDX-1 MSAT forward; `forward` launches it
     eagerly (capturable in a hipGraph), `capture` / `replay` record and replay it."""
 
-    def __init__(self, sd: dict, cfg: RldxMsatCfg, device, bf16_quirk: bool = True):
+    def __init__(self, sd: dict, cfg: RldxMsatCfg, device, bf16_quirk: bool = True, vl_mask: bool = False):
         self.cfg, self.dev = cfg, torch.device(device)
         H, D, inner = cfg.heads, cfg.head_dim, cfg.inner
         Fn._require(D in (64, 128), "head_dim must be 64 or 128")
-        Fn._require(cfg.n_vl % 32 == 0, "the VL token count must be a multiple of 32 (packed row blocks)")
+        Fn._require(cfg.n_vl >= 1 and cfg.n_sa_pure >= 1, "the chain needs VL and SA tokens")
+        # VL rows padded to whole 32-row packed blocks; N = padded token count of the joint attention
+        self.nv = _round_up(cfg.n_vl, 32)
+        self.N = self.nv + cfg.n_sa
+        self.vl_mask = vl_mask
+        self.masked = vl_mask or self.nv != cfg.n_vl
         for k, shape in cfg.param_shapes().items():
             Fn._require(k in sd, f"missing parameter {k}")
             Fn._require(tuple(sd[k].shape) == tuple(shape), f"{k}: shape {tuple(sd[k].shape)}, expected {shape}")
@@ -290,7 +301,7 @@ class RldxMsat:
         self.ds_cos, self.ds_sin = (t.to(self.dev) for t in rope_tables(cfg, ds_pos, bf16_quirk))
         self.ss_cos, self.ss_sin = (t.to(self.dev) for t in rope_tables(cfg, ss_pos, bf16_quirk))
         # activations
-        N, nv, ns = cfg.tokens, cfg.n_vl, cfg.n_sa
+        N, nv, ns = self.N, self.nv, cfg.n_sa
         ebuf = lambda *s: torch.empty(*s, dtype=BF16, device=self.dev)  # noqa: E731
         self.x_sa, self.x_vl = ebuf(ns, cfg.sa_dim), ebuf(nv, cfg.vl_dim)
         self.h_sa, self.h_vl = Fn.PackedAct.empty(ns, cfg.sa_dim, self.dev), Fn.PackedAct.empty(nv, cfg.vl_dim,
@@ -310,8 +321,15 @@ class RldxMsat:
         self.mod = ebuf(cfg.n_sa_pure, cfg.sa_dim)
         self.mod_packed = Fn.PackedAct.empty(cfg.n_sa_pure, cfg.sa_dim, self.dev)
         self.out = ebuf(1, cfg.n_sa_pure, cfg.output_dim)
-        self.inputs = dict(sa=ebuf(1, cfg.n_sa_pure, cfg.sa_dim), vl=ebuf(1, nv, cfg.vl_dim),
+        self.inputs = dict(sa=ebuf(1, cfg.n_sa_pure, cfg.sa_dim), vl=ebuf(1, cfg.n_vl, cfg.vl_dim),
                            temb=ebuf(1, inner), time_token=ebuf(1, nt, cfg.sa_dim))
+        if vl_mask:
+            self.inputs["vl_mask"] = torch.ones(1, cfg.n_vl, dtype=torch.float32, device=self.dev)
+        # additive key bias over the N attention rows: 0, or -inf on padding and masked VL keys
+        self.key_bias = torch.zeros(N, dtype=torch.float32, device=self.dev)
+        self.key_bias[cfg.n_vl:nv] = float("-inf")
+        self._ninf = torch.full((), float("-inf"), dtype=torch.float32, device=self.dev)
+        self._zero = torch.zeros((), dtype=torch.float32, device=self.dev)
         self.graph = None
         # every GEMM of the forward on its static buffers, with its split-K factor
         self.ds_gemms = [self._ds_gemm_items(blk) for blk in self.ds]
@@ -360,8 +378,7 @@ class RldxMsat:
         return (items, epi, split, self.wide_for(w.n, epi, split))
 
     def _ds_gemm_items(self, blk: dict) -> dict:
-        cfg = self.cfg
-        nv, N = cfg.n_vl, cfg.tokens
+        nv, N = self.nv, self.N
         return {
             "sa_qkv": self._planned([(self.h_sa, blk["sa_qkv"], blk["sa_qkv.bias"], self.qkv_sa, None)], "bias"),
             "vl_qkv": self._planned([(self.h_vl, blk["vl_qkv"], blk["vl_qkv.bias"], self.qkv_vl, None)], "bias"),
@@ -394,9 +411,12 @@ class RldxMsat:
         Fn.grouped_gemm(items, epi, split_k=split, workspace=self.ws if split > 1 else None, wide_tiles=wide)
 
     # -- blocks ---------------------------------------------------------------
+    def _kb(self):
+        return self.key_bias if self.masked else None
+
     def _ds_block(self, blk: dict, gm: dict) -> None:
         cfg = self.cfg
-        N = cfg.tokens
+        N = self.N
         Fn.layernorm_pack(self.x_sa, cfg.eps, out=self.h_sa)
         Fn.layernorm_pack(self.x_vl, cfg.eps, out=self.h_vl)
         self._gemm(gm["sa_qkv"])
@@ -405,7 +425,7 @@ class RldxMsat:
                  Fn.StreamSpec(self.qkv_sa, blk["q_norm_sa.weight"], blk["k_norm_sa.weight"], self.ds_cos,
                                self.ds_sin)]
         Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
-        Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), N, out=self.att)
+        Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), N, key_bias=self._kb(), out=self.att)
         self._gemm(gm["sa_proj"])
         self._gemm(gm["vl_proj"])
         Fn.layernorm_pack(self.x_sa, cfg.eps, out=self.h_sa)
@@ -417,44 +437,59 @@ class RldxMsat:
 
     def _ss_block(self, blk: dict, gm: dict) -> None:
         cfg = self.cfg
-        nv, N, inner = cfg.n_vl, cfg.tokens, cfg.inner
+        nv, N, inner = self.nv, self.N, cfg.inner
         Fn.layernorm_pack(self.x, cfg.eps, out=self.h)
         self._gemm(gm["qkv"])
         self._gemm(gm["mlp"])
         specs = [Fn.StreamSpec(self.qkv[:nv], blk["q_norm"], blk["k_norm"]),
                  Fn.StreamSpec(self.qkv[nv:], blk["q_norm"], blk["k_norm"], self.ss_cos, self.ss_sin)]
         Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
-        Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), N, out=self.cat.cols(0, inner))
+        Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), N, key_bias=self._kb(),
+                            out=self.cat.cols(0, inner))
         self._gemm(gm["mlp_proj"])
         self._gemm(gm["linear2"])
 
     # -- forward --------------------------------------------------------------
     def forward(self, hidden_states: torch.Tensor, encoder_hidden_states: torch.Tensor, temb: torch.Tensor,
-                time_token: torch.Tensor) -> torch.Tensor:
+                time_token: torch.Tensor, encoder_attention_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         """CustomOpMSAT.forward (custom_msat_chain.py:109-126): hidden_states
         [1, n_sa_pure, sa_dim], encoder_hidden_states [1, n_vl, vl_dim], temb
         [1, inner], time_token [1, num_temb_tokens, sa_dim] -> [1, n_sa_pure,
-        output_dim] (a static buffer, overwritten by the next call)."""
+        output_dim] (a static buffer, overwritten by the next call).
+        encoder_attention_mask [1, n_vl] (1 = visible, 0 = masked; a chain built
+        with vl_mask=True): masks VL keys in every block as the eager MSAT does
+        (msat.py:517-531, blocks.py:558-575); None = every VL token visible."""
         cfg = self.cfg
         nt, nv = cfg.num_temb_tokens, cfg.n_vl
         Fn._require(tuple(hidden_states.shape) == (1, cfg.n_sa_pure, cfg.sa_dim) and
                     tuple(encoder_hidden_states.shape) == (1, nv, cfg.vl_dim) and
                     tuple(temb.shape) == (1, cfg.inner) and tuple(time_token.shape) == (1, nt, cfg.sa_dim),
                     "input shapes do not match the chain's configuration (batch 1)")
+        if self.vl_mask:
+            if encoder_attention_mask is None:
+                self.key_bias[:nv].zero_()
+            else:
+                Fn._require(tuple(encoder_attention_mask.shape) == (1, nv), "encoder_attention_mask must be [1, n_vl]")
+                torch.where(encoder_attention_mask[0] == 0, self._ninf, self._zero, out=self.key_bias[:nv])
+        else:
+            Fn._require(encoder_attention_mask is None,
+                        "encoder_attention_mask needs a chain built with vl_mask=True")
         self.x_sa[:nt].copy_(time_token[0])
         self.x_sa[nt:].copy_(hidden_states[0])
-        self.x_vl.copy_(encoder_hidden_states[0])
+        self.x_vl[:nv].copy_(encoder_hidden_states[0])
+        if self.nv > nv:
+            self.x_vl[nv:].zero_()
         for blk, gm in zip(self.ds, self.ds_gemms):
             self._ds_block(blk, gm)
         # x = [vl_proj_to_sa(vl) | time token | SA]
         Fn.pack_act(self.x_vl, out=self.vl_packed)
         self._gemm(self.vl_proj_gemm)
-        self.x[nv:].copy_(self.x_sa)
+        self.x[self.nv:].copy_(self.x_sa)
         for blk, gm in zip(self.ss, self.ss_gemms):
             self._ss_block(blk, gm)
         # AdaLN output projection (msat.py:777-781)
         shift, scale = F.linear(F.silu(temb), self.w["proj_out_1.weight"], self.w["proj_out_1.bias"]).chunk(2, dim=1)
-        sa = F.layer_norm(self.x[cfg.tokens - cfg.n_sa_pure:], (cfg.sa_dim,), eps=1e-6)
+        sa = F.layer_norm(self.x[self.N - cfg.n_sa_pure:], (cfg.sa_dim,), eps=1e-6)
         torch.add(sa * (1 + scale), shift, out=self.mod)
         Fn.pack_act(self.mod, out=self.mod_packed)
         self._gemm(self.out_gemm)
@@ -462,19 +497,23 @@ class RldxMsat:
 
     __call__ = forward
 
-    def capture(self, warmup: int = 2) -> None:
-        """Record forward() on the static `inputs` buffers into one hipGraph."""
+    def _forward_static(self):
         i = self.inputs
+        return self.forward(i["sa"], i["vl"], i["temb"], i["time_token"], i.get("vl_mask"))
+
+    def capture(self, warmup: int = 2) -> None:
+        """Record forward() on the static `inputs` buffers (with the `vl_mask`
+        buffer when built with vl_mask=True) into one hipGraph."""
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             for _ in range(warmup):
-                self.forward(i["sa"], i["vl"], i["temb"], i["time_token"])
+                self._forward_static()
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            self.forward(i["sa"], i["vl"], i["temb"], i["time_token"])
+            self._forward_static()
         torch.cuda.synchronize()
 
     def replay(self) -> torch.Tensor:
@@ -482,33 +521,138 @@ class RldxMsat:
         return self.out
 
 
-def install(msat: torch.nn.Module, n_vl: int, n_sa_pure: int, bf16_quirk: Optional[bool] = None) -> RldxMsat:
-    """Replace a live MSAT module's forward by the rldx_amd chain (what the
+class MsatDispatcher:
+    """Replacement of a live MSAT module's forward by the rldx_amd chain, with
+    the behaviour of the reference's path-D dispatcher (_CompiledDispatcher,
+    rldx/inference/serve_optimization.py:251-516) at the MSAT boundary:
+
+    * the first call is served by the module's own forward while the chain is
+      built from msat.state_dict() for that call's token counts (and, with
+      graph=True, captured as one hipGraph);
+    * later calls compute temb / the time token with the module's own
+      timestep_encoder / time_token_proj, copy every input into the chain's
+      static buffers and run (or replay) the chain;
+    * calls the chain does not serve go to the module's own forward:
+      return_all_hidden_states=True, physics tokens on a physics-enabled module,
+      a batch other than 1, or token counts other than the chain's (shape
+      drift would corrupt the static buffers);
+    * a failure while building or running switches the dispatcher to the
+      module's own forward for good, as the reference does.
+    encoder_attention_mask is served: the chain is built with vl_mask=True.
+    The returned tensor is the chain's static output buffer, overwritten by the
+    next call."""
+
+    def __init__(self, msat: torch.nn.Module, bf16_quirk: Optional[bool] = None, graph: bool = False,
+                 verbose: bool = False):
+        self.msat, self.orig = msat, msat.forward
+        self.bf16_quirk, self.graph, self.verbose = bf16_quirk, graph, verbose
+        self.chain: Optional[RldxMsat] = None
+        self.failed = False
+        self.served = 0      # calls run on the chain
+        self.fallbacks = 0   # calls sent to the module's own forward
+
+    def _log(self, msg: str) -> None:
+        if self.verbose:
+            print(f"[rldx_amd.MsatDispatcher] {msg}", flush=True)
+
+    def build(self, n_vl: int, n_sa_pure: int) -> RldxMsat:
+        msat = self.msat
+        sd = {k: v for k, v in msat.state_dict().items()}
+        rope = getattr(msat, "rope_embedder", None)
+        quirk = self.bf16_quirk
+        if quirk is None:
+            quirk = rope is not None and not getattr(rope, "freqs_cis_0").is_complex()
+        overrides = dict(n_vl=n_vl, n_sa_pure=n_sa_pure)
+        if rope is not None:
+            overrides.update(rope_theta=float(rope.theta), max_seq_len=int(rope.max_seq_len))
+        cfg = RldxMsatCfg.from_state_dict(sd, **overrides)
+        dev = next(iter(sd.values())).device
+        chain = RldxMsat(sd, cfg, dev, bf16_quirk=quirk, vl_mask=True)
+        if self.graph:
+            chain.capture()
+        self.chain = chain
+        return chain
+
+    def _unserved(self, hidden_states, encoder_hidden_states, return_all_hidden_states, physics_embs,
+                  physics_attention_mask) -> Optional[str]:
+        if return_all_hidden_states:
+            return "return_all_hidden_states"
+        if getattr(self.msat, "use_physics", False) and physics_embs is not None:
+            return "physics tokens"
+        if hidden_states.dim() != 3 or hidden_states.shape[0] != 1 or encoder_hidden_states.shape[0] != 1:
+            return "batch other than 1"
+        c = self.chain
+        if c is not None and (encoder_hidden_states.shape[1] != c.cfg.n_vl or hidden_states.shape[1] != c.cfg.n_sa_pure):
+            return "token counts differ from the chain's"
+        return None
+
+    def __call__(self, hidden_states, encoder_hidden_states, timestep=None, return_all_hidden_states=False,
+                 encoder_attention_mask=None, physics_embs=None, physics_attention_mask=None):
+        args = (hidden_states, encoder_hidden_states, timestep, return_all_hidden_states, encoder_attention_mask,
+                physics_embs, physics_attention_mask)
+        if self.failed:
+            self.fallbacks += 1
+            return self.orig(*args)
+        why = self._unserved(hidden_states, encoder_hidden_states, return_all_hidden_states, physics_embs,
+                             physics_attention_mask)
+        if why is not None:
+            self._log(f"served by the module's own forward: {why}")
+            self.fallbacks += 1
+            return self.orig(*args)
+        if self.chain is None:
+            out = self.orig(*args)
+            self.fallbacks += 1
+            try:
+                self.build(encoder_hidden_states.shape[1], hidden_states.shape[1])
+            except Exception as e:  # noqa: BLE001 — any build failure means the module's own forward from now on
+                self.failed = True
+                self._log(f"build failed ({e}); the module's own forward serves every call")
+            return out
+        try:
+            c = self.chain
+            msat = self.msat
+            temb = msat.timestep_encoder(timestep)
+            tt = msat.time_token_proj(temb).unsqueeze(1).repeat(1, c.cfg.num_temb_tokens, 1)
+            mask = encoder_attention_mask
+            if self.graph:
+                i = c.inputs
+                i["sa"].copy_(hidden_states)
+                i["vl"].copy_(encoder_hidden_states)
+                i["temb"].copy_(temb)
+                i["time_token"].copy_(tt)
+                if mask is None:
+                    i["vl_mask"].fill_(1.0)
+                else:
+                    i["vl_mask"].copy_(mask.reshape(1, -1))
+                out = c.replay()
+            else:
+                out = c.forward(hidden_states, encoder_hidden_states, temb, tt, mask)
+            self.served += 1
+            return out
+        except Exception as e:  # noqa: BLE001 — as the reference: fall back for good on a hot-path failure
+            self.failed = True
+            self._log(f"hot-path failure ({e}); the module's own forward serves every call")
+            self.fallbacks += 1
+            return self.orig(*args)
+
+
+def install(msat: torch.nn.Module, n_vl: Optional[int] = None, n_sa_pure: Optional[int] = None,
+            bf16_quirk: Optional[bool] = None, graph: bool = False, verbose: bool = False) -> MsatDispatcher:
+    """Route a live MSAT module's forward through an MsatDispatcher (what the
     reference's path-D dispatcher does with CustomOpMSAT,
-    rldx/inference/serve_optimization.py:251-601).  The chain is built from
-    msat.state_dict(); msat.forward(hidden_states, encoder_hidden_states,
-    timestep) keeps its signature: the module's own timestep_encoder and
-    time_token_proj make temb and the time token.  bf16_quirk=None detects it
+    rldx/inference/serve_optimization.py:251-601).  With n_vl and n_sa_pure the
+    chain is built now; without them, on the first call (served by the
+    module's own forward).  msat.forward keeps the reference signature
+    forward(hidden_states, encoder_hidden_states, timestep,
+    return_all_hidden_states, encoder_attention_mask, physics_embs,
+    physics_attention_mask) (msat.py:1058-1082).  bf16_quirk=None detects it
     from the RoPE buffers (real-valued: the model was cast to bf16)."""
-    sd = {k: v for k, v in msat.state_dict().items()}
-    rope = getattr(msat, "rope_embedder", None)
-    if bf16_quirk is None:
-        bf16_quirk = rope is not None and not getattr(rope, "freqs_cis_0").is_complex()
-    overrides = dict(n_vl=n_vl, n_sa_pure=n_sa_pure)
-    if rope is not None:
-        overrides.update(rope_theta=float(rope.theta), max_seq_len=int(rope.max_seq_len))
-    cfg = RldxMsatCfg.from_state_dict(sd, **overrides)
-    dev = next(iter(sd.values())).device
-    chain = RldxMsat(sd, cfg, dev, bf16_quirk=bf16_quirk)
-
-    def forward(hidden_states, encoder_hidden_states, timestep=None, **kwargs):
-        temb = msat.timestep_encoder(timestep)
-        tt = msat.time_token_proj(temb).unsqueeze(1).repeat(1, cfg.num_temb_tokens, 1)
-        return chain.forward(hidden_states, encoder_hidden_states, temb, tt)
-
-    msat.forward = forward
-    msat.rldx_amd_chain = chain
-    return chain
+    d = MsatDispatcher(msat, bf16_quirk=bf16_quirk, graph=graph, verbose=verbose)
+    if n_vl is not None and n_sa_pure is not None:
+        d.build(n_vl, n_sa_pure)
+    msat.forward = d
+    msat.rldx_amd_dispatcher = d
+    return d
 
 
 # ---------------------------------------------------------------------------

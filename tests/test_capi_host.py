@@ -181,15 +181,17 @@ def test_grouped_gemm_split_plan_and_rejections():
 def test_grouped_gemm_wide_tiles_plan():
     """RLDX_GEMM_WIDE_TILES: streams below the 128 x 128 threshold take 64 x 128 /
     32 x 128 tiles (W3 shapes, split 8: 96 + 12 tiles of 64 x 128 with 32 KB of
-    partials per split, 12 tiles of 32 x 128 with 16 KB); unknown flag bits and
-    the QKV epilogue are rejected."""
+    partials per split, 12 tiles of 32 x 128 with 16 KB); RLDX_GEMM_SPLITS_ACROSS_XCDS
+    needs no other workspace; unknown flag bits and the QKV epilogue are rejected."""
     lib = _lib.load()
     msat = (512, 64, 32)
     wide = lib.rldx_grouped_gemm_ex_workspace_bytes(_gemm_groups(msat), 3, 1536, 4096, 1, 8, 1)
     assert wide == 65536 + (96 + 12) * 8 * 32768 + 12 * 8 * 16384
     assert lib.rldx_grouped_gemm_ex_workspace_bytes(_gemm_groups(msat), 3, 1536, 4096, 1, 8, 0) == \
         lib.rldx_grouped_gemm_workspace_bytes(_gemm_groups(msat), 3, 1536, 4096, 1, 8)
-    assert lib.rldx_grouped_gemm_ex_workspace_bytes(_gemm_groups(msat), 3, 1536, 4096, 1, 8, 2) == -1
+    # RLDX_GEMM_SPLITS_ACROSS_XCDS moves workgroups, not partials: the same workspace
+    assert lib.rldx_grouped_gemm_ex_workspace_bytes(_gemm_groups(msat), 3, 1536, 4096, 1, 8, 3) == wide
+    assert lib.rldx_grouped_gemm_ex_workspace_bytes(_gemm_groups(msat), 3, 1536, 4096, 1, 8, 4) == -1
     assert lib.rldx_grouped_gemm_ex_workspace_bytes(_gemm_groups(msat), 3, 4608, 1536, 5, 1, 1) == -1
     assert lib.rldx_grouped_gemm_ex_bf16(_gemm_groups(msat), 3, 1536, 4096, 1, 1, 4, None, 0, None) == HIP_INVALID_VALUE
     assert lib.rldx_grouped_gemm_ex_bf16(_gemm_groups(msat), 3, 1536, 4096, 1, 8, 1, 4096, wide - 256,

@@ -199,6 +199,11 @@ def test_grouped_gemm_split_k(dev, epilogue, n, k, split_k):
         Fn.grouped_gemm(items, epilogue, split_k=split_k, workspace=ws)
         for x, y in zip(result(), first):
             assert torch.equal(x, y)
+    for _ in range(3):  # the splits of every tile on different XCDs: the same bits (device-scope hand-off)
+        reset()
+        Fn.grouped_gemm(items, epilogue, split_k=split_k, workspace=ws, splits_across_xcds=True)
+        for x, y in zip(result(), first):
+            assert torch.equal(x, y), "splits across XCDs differ from splits on one XCD"
     reset()
     Fn.grouped_gemm(items, epilogue)  # no split
     for x, y in zip(result(), first):

@@ -1,12 +1,14 @@
 """GPU tests of the synthetic MSAT action step: parity with the CPU oracle and
 hipGraph replay semantics.
 
-Step tolerance: the GPU step and the CPU oracle run the same bf16 composition
-but different GEMM libraries (hipBLASLt vs oneDNN), whose fp32 accumulation
-orders differ; the bf16 roundings of 64 block applications then drift apart.
-Bound: relative L2 <= 1e-2 and max-abs <= 2e-2 on the truncated 2-block step,
-and relative L2 <= 2e-2, cosine >= 0.999 on the full 16-block x 4-iteration
-action chunk (values of order 1).
+Step tolerance: the GPU step (its own MFMA GEMMs and attention) and the CPU
+oracle (torch CPU matmuls) run the same bf16 composition with different fp32
+accumulation orders, so their bf16 roundings differ from the first GEMM on and
+compound over 64 block applications.  Bounds: the bf16 contract (max-abs
+<= 2e-2, relative L2 <= 1e-2) on the truncated 2-block step; on the full
+16-block x 4-iteration action chunk, the referee is an fp32 evaluation of the
+same weights and inputs: the GPU result must be no further from it than 1.5x
+the eager-bf16 oracle is, and within cosine 0.999 of the bf16 oracle.
 """
 
 import pytest
@@ -41,13 +43,22 @@ def test_step_two_blocks_one_iteration(setup):
 def test_step_full_chunk(setup):
     cfg, w, inp, wc, ic = setup
     step = MsatActionStep(cfg, w, inp)
-    out = step.run().clone().cpu()
-    ref = R.action_step(cfg, wc, ic)
-    s = stats(out, ref)
-    cos = torch.nn.functional.cosine_similarity(out.float().flatten(), ref.float().flatten(), dim=0).item()
-    print(f"full action step vs CPU oracle: {s}, cos={cos:.6f}")
-    assert torch.isfinite(out.float()).all()
-    assert s["rel_l2"] <= 2e-2 and cos >= 0.999, (s, cos)
+    out = step.run().clone().cpu().double()
+    torch.set_num_threads(max(1, min(16, torch.get_num_threads())))
+    r16 = R.action_step(cfg, wc, ic).double()
+    r32 = R.action_step(cfg, {k: v.float() for k, v in wc.items()}, {k: v.float() for k, v in ic.items()}).double()
+
+    def rel(a, b):
+        return ((a - b).norm() / b.norm()).item()
+
+    floor, got = rel(r16, r32), rel(out, r32)
+    s = stats(out, r16)
+    cos = torch.nn.functional.cosine_similarity(out.flatten(), r16.flatten(), dim=0).item()
+    print(f"full action step: rel-L2 to fp32 {got:.3e} (bf16 oracle: {floor:.3e}); to the bf16 oracle "
+          f"max-abs {s['max_abs']:.3e}, rel-L2 {s['rel_l2']:.3e}, cos {cos:.6f}; "
+          f"max-abs to fp32 {(out - r32).abs().max().item():.3e} (bf16 oracle: {(r16 - r32).abs().max().item():.3e})")
+    assert torch.isfinite(out).all()
+    assert got <= 1.5 * floor and cos >= 0.999, (got, floor, cos)
 
 
 def test_graph_replay_matches_eager_and_follows_inputs(setup):

@@ -12,11 +12,12 @@ from tolerances import assert_bf16_close
 pytestmark = pytest.mark.gpu
 
 
-def _oracle(sd, inp, cfg, quirk):
+def _oracle(sd, inp, cfg, quirk, mask=None):
     cpu = {k: v.cpu() for k, v in sd.items()}
     return R.msat_forward(cpu, inp["sa"].cpu(), inp["vl"].cpu(), inp["temb"].cpu(), inp["time_token"].cpu(),
                           heads=cfg.heads, head_dim=cfg.head_dim, ds_blocks=cfg.ds_blocks, ss_blocks=cfg.ss_blocks,
-                          theta=cfg.rope_theta, max_seq_len=cfg.max_seq_len, bf16_quirk=quirk)
+                          theta=cfg.rope_theta, max_seq_len=cfg.max_seq_len, bf16_quirk=quirk,
+                          encoder_attention_mask=None if mask is None else mask.cpu())
 
 
 @pytest.mark.parametrize("quirk", [True, False])
@@ -38,17 +39,17 @@ def _rel(a, b):
     return ((a - b).norm() / b.norm()).item()
 
 
-def assert_as_accurate_as_eager_bf16(o, sd, inp, cfg, quirk, what):
+def assert_as_accurate_as_eager_bf16(o, sd, inp, cfg, quirk, what, mask=None):
     """Over several blocks the bf16 roundings of any evaluation order compound
     (the bf16 oracle itself is 6e-3 / 8e-3 / 1.5e-2 rel-L2 from an fp32
     evaluation at 1+1 / 2+2 / 4+8 blocks).  Bound: the GPU chain is no further
     from the fp32 evaluation of the same weights and inputs than 1.5x the eager
     bf16 evaluation is, and its cosine to the bf16 oracle is >= 0.999."""
     o = o.detach().cpu().double()
-    r16 = _oracle(sd, inp, cfg, quirk).double()
+    r16 = _oracle(sd, inp, cfg, quirk, mask).double()
     sd32 = {k: v.float() for k, v in sd.items()}
     inp32 = {k: v.float() for k, v in inp.items()}
-    r32 = _oracle(sd32, inp32, cfg, quirk).double()
+    r32 = _oracle(sd32, inp32, cfg, quirk, mask).double()
     floor, got = _rel(r16, r32), _rel(o, r32)
     cos = torch.nn.functional.cosine_similarity(o.flatten(), r16.flatten(), dim=0).item()
     print(f"{what}: rel-L2 to fp32 {got:.2e} (eager bf16: {floor:.2e}), to the bf16 oracle {_rel(o, r16):.2e}, "
@@ -98,27 +99,92 @@ def _module_tree(sd):
     return root
 
 
-def test_install_on_a_module_tree(dev):
-    """install() builds the chain from a live module's state dict and keeps the
-    module's forward(hidden_states, encoder_hidden_states, timestep) signature,
-    with the module's own time embedding and time-token projection."""
-    cfg = RM.RldxMsatCfg(ds_blocks=1, ss_blocks=2)
-    sd = RM.make_state_dict(cfg, dev, seed=61)
+def _tree_with_time_modules(cfg, sd, dev, seed):
+    """A module tree with the reference MSAT's state-dict keys, a timestep encoder,
+    a time-token projection, and (as its own forward) the oracle evaluated on the
+    CPU: the dispatcher's fallback path then returns the reference's result."""
     msat = _module_tree(sd)
-    g = torch.Generator(device=dev).manual_seed(62)
+    g = torch.Generator(device=dev).manual_seed(seed)
     wt = (0.02 * torch.randn(cfg.inner, 1, generator=g, device=dev)).to(torch.bfloat16)
     wtt = (0.02 * torch.randn(cfg.sa_dim, cfg.inner, generator=g, device=dev)).to(torch.bfloat16)
     msat.timestep_encoder = lambda t: (t[:, None].to(torch.bfloat16) @ wt.t())
     msat.time_token_proj = lambda temb: temb @ wtt.t()
-    chain = RM.install(msat, n_vl=cfg.n_vl, n_sa_pure=cfg.n_sa_pure, bf16_quirk=True)
-    assert chain.cfg.param_shapes() == cfg.param_shapes()
+    msat.calls = []
+
+    def own_forward(hidden_states, encoder_hidden_states, timestep=None, return_all_hidden_states=False,
+                    encoder_attention_mask=None, physics_embs=None, physics_attention_mask=None):
+        msat.calls.append(dict(return_all_hidden_states=return_all_hidden_states,
+                               masked=encoder_attention_mask is not None))
+        temb = msat.timestep_encoder(timestep)
+        tt = msat.time_token_proj(temb).unsqueeze(1)
+        c = RM.RldxMsatCfg.from_state_dict(sd, n_vl=encoder_hidden_states.shape[1],
+                                           n_sa_pure=hidden_states.shape[1])
+        inp = dict(sa=hidden_states, vl=encoder_hidden_states, temb=temb, time_token=tt)
+        out = _oracle(sd, inp, c, True, mask=encoder_attention_mask).to(dev)
+        return (out, []) if return_all_hidden_states else out
+
+    msat.forward = own_forward
+    return msat
+
+
+def _time_inputs(msat, t):
+    temb = msat.timestep_encoder(t)
+    return temb, msat.time_token_proj(temb).unsqueeze(1)
+
+
+def test_install_on_a_module_tree(dev):
+    """install() with token counts builds the chain now; msat(...) keeps the
+    reference forward signature and uses the module's own time embedding and
+    time-token projection."""
+    cfg = RM.RldxMsatCfg(ds_blocks=1, ss_blocks=2)
+    sd = RM.make_state_dict(cfg, dev, seed=61)
+    msat = _tree_with_time_modules(cfg, sd, dev, 62)
+    d = RM.install(msat, n_vl=cfg.n_vl, n_sa_pure=cfg.n_sa_pure, bf16_quirk=True)
+    assert d.chain.cfg.param_shapes() == cfg.param_shapes()
     inp = RM.make_inputs(cfg, dev, seed=63)
     t = torch.tensor([0.25], device=dev)
     o = msat(inp["sa"], inp["vl"], t).clone()
-    temb = msat.timestep_encoder(t)
-    tt = msat.time_token_proj(temb).unsqueeze(1)
+    assert d.served == 1 and msat.calls == []
+    temb, tt = _time_inputs(msat, t)
     ref_inp = dict(sa=inp["sa"], vl=inp["vl"], temb=temb, time_token=tt)
     assert_as_accurate_as_eager_bf16(o, sd, ref_inp, cfg, True, "installed MSAT forward, 1 DS + 2 SS")
+
+
+@pytest.mark.parametrize("n_vl", [64, 80])
+def test_dispatcher_serves_masks_and_falls_back(dev, n_vl):
+    """The lazy dispatcher (graph replay): the first call is the module's own
+    forward; then encoder_attention_mask is served by the chain (masked VL keys
+    carry -inf); return_all_hidden_states and token counts other than the
+    chain's go to the module's own forward.  n_vl = 80 is not a multiple of 32:
+    the chain pads the VL rows with masked keys."""
+    cfg = RM.RldxMsatCfg(ds_blocks=1, ss_blocks=1, n_vl=n_vl)
+    sd = RM.make_state_dict(cfg, dev, seed=64)
+    msat = _tree_with_time_modules(cfg, sd, dev, 65)
+    d = RM.install(msat, bf16_quirk=True, graph=True)  # the tree has no RoPE buffers to detect the quirk from
+    inp = RM.make_inputs(cfg, dev, seed=66)
+    t = torch.tensor([0.5], device=dev)
+    first = msat(inp["sa"], inp["vl"], t).clone()
+    assert d.chain is not None and d.served == 0 and len(msat.calls) == 1
+    temb, tt = _time_inputs(msat, t)
+    ref_inp = dict(sa=inp["sa"], vl=inp["vl"], temb=temb, time_token=tt)
+    o = msat(inp["sa"], inp["vl"], t).clone()
+    assert d.served == 1 and len(msat.calls) == 1
+    assert_as_accurate_as_eager_bf16(o, sd, ref_inp, cfg, True, f"dispatcher, n_vl={n_vl}")
+    mask = torch.ones(1, n_vl, device=dev)
+    mask[:, 5:n_vl:3] = 0
+    om = msat(inp["sa"], inp["vl"], t, encoder_attention_mask=mask).clone()
+    assert d.served == 2 and len(msat.calls) == 1
+    assert_as_accurate_as_eager_bf16(om, sd, ref_inp, cfg, True, f"dispatcher with a VL mask, n_vl={n_vl}",
+                                     mask=mask)
+    assert (om.float() - o.float()).abs().max() > 1e-2, "the mask changed nothing"
+    # unchanged inputs without the mask replay the unmasked result bit for bit
+    o2 = msat(inp["sa"], inp["vl"], t).clone()
+    assert torch.equal(o2.view(torch.int16), o.view(torch.int16))
+    msat(inp["sa"], inp["vl"], t, return_all_hidden_states=True)
+    assert len(msat.calls) == 2 and msat.calls[-1]["return_all_hidden_states"]
+    short = RM.make_inputs(RM.RldxMsatCfg(ds_blocks=1, ss_blocks=1, n_vl=32), dev, seed=67)
+    msat(inp["sa"], short["vl"], t)
+    assert len(msat.calls) == 3 and d.served == 3 and not d.failed
 
 
 def _head_reference(head_sd, msat_sd, hc, mc, vl, state, x0, e=0):

@@ -127,3 +127,68 @@ def test_oracle_sa_output_invariant_to_vl_token_order():
     perm = torch.randperm(cfg.n_vl, generator=torch.Generator().manual_seed(0))
     op = R.msat_forward(sd, inp["sa"], inp["vl"][:, perm], inp["temb"], inp["time_token"], **kw).double()
     assert (o - op).norm() / o.norm() < 1e-2
+
+
+def _tiny_oracle_inputs(seed, n_vl=5):
+    cfg = RM.RldxMsatCfg(heads=2, head_dim=64, ds_blocks=1, ss_blocks=1, sa_dim=128, vl_dim=128, output_dim=64,
+                         n_vl=n_vl, n_sa_pure=3)
+    sd = RM.make_state_dict(cfg, "cpu", seed=seed)
+    inp = RM.make_inputs(cfg, "cpu", seed=seed + 1)
+    return cfg, sd, inp
+
+
+def _run(cfg, sd, inp, mask=None, vl=None):
+    return R.msat_forward(sd, inp["sa"], inp["vl"] if vl is None else vl, inp["temb"], inp["time_token"],
+                          heads=cfg.heads, head_dim=cfg.head_dim, ds_blocks=cfg.ds_blocks, ss_blocks=cfg.ss_blocks,
+                          encoder_attention_mask=mask)
+
+
+def test_oracle_vl_mask_semantics():
+    """encoder_attention_mask in the oracle (blocks.py:558-575, msat.py:517-531):
+    an all-ones mask equals no mask bit for bit; masked VL tokens cannot reach
+    the output (changing their values leaves it bit-identical), while the same
+    change without the mask does change it."""
+    cfg, sd, inp = _tiny_oracle_inputs(81)
+    base = _run(cfg, sd, inp)
+    assert torch.equal(_run(cfg, sd, inp, torch.ones(1, 5)), base)
+    mask = torch.tensor([[1.0, 0.0, 1.0, 0.0, 1.0]])
+    vl2 = inp["vl"].clone()
+    vl2[:, [1, 3]] = 5.0 * torch.randn(1, 2, cfg.vl_dim).to(vl2.dtype)
+    assert torch.equal(_run(cfg, sd, inp, mask), _run(cfg, sd, inp, mask, vl=vl2))
+    assert not torch.equal(_run(cfg, sd, inp), _run(cfg, sd, inp, vl=vl2))
+
+
+def test_dispatcher_falls_back_for_good_when_the_build_fails():
+    """MsatDispatcher on a CPU module: the first call is served by the module's own
+    forward; building the chain needs the GPU kernels and fails here, so every
+    later call stays on the module's own forward (serve_optimization.py:464-472)."""
+    cfg = RM.RldxMsatCfg(ds_blocks=1, ss_blocks=1)
+    shapes = cfg.param_shapes()
+    root = torch.nn.Module()
+    for k, s in shapes.items():
+        *path, leaf = k.split(".")
+        m = root
+        for part in path:
+            if not hasattr(m, part):
+                m.add_module(part, torch.nn.Module())
+            m = getattr(m, part)
+        m.register_buffer(leaf, torch.zeros(s, dtype=torch.bfloat16))
+    calls = []
+    root.forward = lambda *a, **k: calls.append((a, k)) or "own"
+    d = RM.install(root)
+    sa, vl = torch.zeros(1, cfg.n_sa_pure, cfg.sa_dim), torch.zeros(1, cfg.n_vl, cfg.vl_dim)
+    assert root(sa, vl, torch.zeros(1)) == "own" and d.failed and d.chain is None
+    assert root(sa, vl, torch.zeros(1), encoder_attention_mask=torch.ones(1, cfg.n_vl)) == "own"
+    assert len(calls) == 2 and d.served == 0 and d.fallbacks == 2
+    # the reference keyword arguments reach the module's own forward unchanged
+    assert calls[1][0][4] is not None
+
+
+def test_dispatcher_unserved_calls():
+    d = RM.MsatDispatcher(torch.nn.Module())
+    x3 = torch.zeros(1, 17, 8)
+    assert d._unserved(x3, x3, True, None, None) == "return_all_hidden_states"
+    assert d._unserved(torch.zeros(2, 17, 8), torch.zeros(2, 64, 8), False, None, None) == "batch other than 1"
+    assert d._unserved(x3, x3, False, torch.zeros(1, 4, 8), None) is None  # module without use_physics ignores them
+    d.msat.use_physics = True
+    assert d._unserved(x3, x3, False, torch.zeros(1, 4, 8), None) == "physics tokens"
