@@ -250,6 +250,30 @@ hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv_row_stride
 /* Workspace bytes rldx_llm_fused_attention_bf16 needs (the packed K/V tiles). */
 int64_t rldx_llm_fused_attention_workspace_bytes(int64_t seq, int64_t kv_heads, int64_t head_dim);
 
+/* Scratch bytes of the allocation-free variant below, per GPU (16 MiB: e.g. 8 KV
+ * heads x 4096 tokens at head_dim 128). */
+#define RLDX_LLM_ATTN_NOALLOC_MAX_BYTES (16 << 20)
+
+/*
+ * rldx_llm_fused_attention_bf16 without a workspace argument: it allocates
+ * nothing.  No counterpart in the reference: for callers that cannot allocate
+ * device memory (code under hipGraph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  The packed K/V tiles go to a file-scope device array
+ * of RLDX_LLM_ATTN_NOALLOC_MAX_BYTES that each GPU the library runs on holds
+ * until the process ends (its address is resolved once per device, on the
+ * first call there, with that device current).  Calls whose
+ * rldx_llm_fused_attention_workspace_bytes(seq, kv_heads, head_dim) exceeds it
+ * return hipErrorInvalidValue with nothing enqueued.  Every call on a GPU shares
+ * that GPU's array: calls that overlap in time on one GPU (other streams, other
+ * threads) race and must be serialised by the caller.  Same results as
+ * rldx_llm_fused_attention_bf16 (the same kernels).
+ */
+hipError_t rldx_llm_fused_attention_noalloc_bf16(const void* qkv, int64_t qkv_row_stride, const void* q_norm_w,
+                                                 const void* k_norm_w, const void* cos, const void* sin,
+                                                 int64_t cos_row_stride, int32_t sin_is_signed, void* out,
+                                                 int64_t out_row_stride, int64_t seq, int64_t q_heads,
+                                                 int64_t kv_heads, int64_t head_dim, float eps, hipStream_t stream);
+
 /*
  * The rldx_backbone::vision_attention operator (Qwen3-VL ViT blocks): fused
  * QKV rows (total_tokens, 3*num_heads*head_dim) bf16, contiguous -> out

@@ -48,6 +48,8 @@
 //                                lane l, element i
 //                                = V[32t + 16 s2 + 8 (i >> 2) + 4 (l >> 5) + (i & 3)][32 db + (l & 31)]
 //   keys >= Sk hold zeros.
+#include <mutex>
+
 #include "rldx_amd.h"
 #include "rldx_common.h"
 
@@ -1230,6 +1232,58 @@ extern "C" hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv
   a.eps = eps;
   a.sin_signed = sin_is_signed ? 1 : 0;
   return launch_attn<true>(a, head_dim, 1, true, false, stream);
+}
+
+// ---------------------------------------------------------------------------
+// rldx_backbone::fused_attention without allocation: the packed K/V tiles live
+// in a file-scope device array instead of a caller workspace.  Each GPU holds
+// its own copy of the array (RLDX_LLM_ATTN_NOALLOC_MAX_BYTES) until the
+// process ends; host code reaches it only through the per-device address that
+// hipGetSymbolAddress returns (the array's name is a host-side stand-in).
+// ---------------------------------------------------------------------------
+namespace {
+static __device__ __align__(256) unsigned char scratch[RLDX_LLM_ATTN_NOALLOC_MAX_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch address on the current device, resolved on the first call there.
+hipError_t scratch_on_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (p == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+}  // namespace
+
+extern "C" hipError_t rldx_llm_fused_attention_noalloc_bf16(const void* qkv, int64_t qkv_row_stride,
+                                                            const void* q_norm_w, const void* k_norm_w,
+                                                            const void* cos, const void* sin, int64_t cos_row_stride,
+                                                            int32_t sin_is_signed, void* out, int64_t out_row_stride,
+                                                            int64_t seq, int64_t q_heads, int64_t kv_heads,
+                                                            int64_t head_dim, float eps, hipStream_t stream) {
+  const int64_t need = rldx_llm_fused_attention_workspace_bytes(seq, kv_heads, head_dim);
+  if (need < 0 || need > RLDX_LLM_ATTN_NOALLOC_MAX_BYTES) return hipErrorInvalidValue;  // beyond the scratch array
+  if (seq == 0) return rldx_llm_fused_attention_bf16(qkv, qkv_row_stride, q_norm_w, k_norm_w, cos, sin,
+                                                     cos_row_stride, sin_is_signed, out, out_row_stride, seq, q_heads,
+                                                     kv_heads, head_dim, eps, nullptr, 0, stream);
+  void* ws = nullptr;
+  const hipError_t e = scratch_on_current_device(&ws);
+  if (e != hipSuccess) return e;
+  return rldx_llm_fused_attention_bf16(qkv, qkv_row_stride, q_norm_w, k_norm_w, cos, sin, cos_row_stride,
+                                       sin_is_signed, out, out_row_stride, seq, q_heads, kv_heads, head_dim, eps, ws,
+                                       RLDX_LLM_ATTN_NOALLOC_MAX_BYTES, stream);
 }
 
 extern "C" int64_t rldx_vision_attention_workspace_bytes(int64_t total_tokens, int64_t num_seqs, int64_t num_heads,

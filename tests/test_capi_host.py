@@ -313,3 +313,20 @@ def test_python_wrappers_refuse_cpu_tensors():
     q = torch.zeros(1, 2, 8, 128, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError):
         Fn.attention(q, q, q)
+
+
+def test_llm_attention_noalloc_rejects_sizes_beyond_its_scratch():
+    """rldx_llm_fused_attention_noalloc_bf16 checks the packed K/V size against its
+    scratch array (RLDX_LLM_ATTN_NOALLOC_MAX_BYTES = 16 MiB) before anything else:
+    one key more than fits is rejected with hipErrorInvalidValue, without touching
+    a device (this host has none)."""
+    lib = _lib.load()
+    max_bytes = 16 << 20
+    fits = max_bytes // (8 * 4 * 128)  # 8 KV heads, K + V bf16 = 4 * D bytes per key and head
+    assert lib.rldx_llm_fused_attention_workspace_bytes(fits, 8, 128) == max_bytes
+    assert lib.rldx_llm_fused_attention_workspace_bytes(fits + 1, 8, 128) > max_bytes
+    p = 4096  # never dereferenced: the call must fail on the size first
+    assert lib.rldx_llm_fused_attention_noalloc_bf16(p, 48 * 128, p, p, p, p, 128, 1, p, 32 * 128, fits + 1, 32, 8, 128,
+                                                    1e-6, None) == HIP_INVALID_VALUE
+    assert lib.rldx_llm_fused_attention_noalloc_bf16(p, 48 * 128, p, p, p, p, 128, 1, p, 32 * 128, 1 << 20, 32, 8, 128,
+                                                    1e-6, None) == HIP_INVALID_VALUE
