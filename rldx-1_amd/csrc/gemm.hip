@@ -57,9 +57,6 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kXcds = 8;
-// Cache-policy immediate of a buffer load / store at device scope: SC1 = 1,
-// SC0 = 0 (the instruction's own access is coherent across the XCDs' L2s).
-constexpr int kCpolDevice = 16;
 constexpr int kThreads = 512;          // 8 waves per workgroup
 constexpr int kBufWord3 = 0x00020000;  // gfx9 raw buffer descriptor, word 3 (untyped dword data)
 

@@ -107,6 +107,10 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 // (lo, hi) -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
+// Cache-policy immediate of a buffer load / store at device scope: SC1 = 1,
+// SC0 = 0 (the instruction's own access is coherent across the XCDs' L2s).
+constexpr int kCpolDevice = 16;
+
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   const f32x2_t v = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
@@ -171,7 +175,7 @@ RLDX_HD int64_t packed_act_offset(int64_t row, int64_t col, int64_t k) {
 hipError_t gqa_k_norm_rope_kv_pack(const uint16_t* k, const uint16_t* v, int64_t row_stride, const uint16_t* k_w,
                                    const uint16_t* cos, const uint16_t* sin, int64_t cos_row_stride, bool sin_signed,
                                    int64_t seq, int64_t kv_heads, int64_t head_dim, float eps, uint16_t* kvp,
-                                   int64_t kvp_sh, hipStream_t stream);
+                                   int64_t kvp_sh, unsigned* zero, int64_t zero_n, hipStream_t stream);
 
 // Element offset of K[key][d0 .. d0+7] (d0 % 8 == 0) inside the packed K/V
 // tiles of one head (32 keys per tile, 128 * D bytes, K chunks then V chunks):
