@@ -228,14 +228,10 @@ hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* kv_packed, 
  * (Qwen3VLTextRMSNorm, eps) + rotate-half RoPE (cos / sin tables [seq, D] bf16,
  * row stride cos_row_stride; sin pre-signed iff sin_is_signed) + causal GQA
  * attention, scale 1/sqrt(D).  Two launches: K normalisation + RoPE written
- * straight into the packed K/V tiles, with the V tiles packed by the same
- * launch, in `workspace` (>= rldx_llm_fused_attention_workspace_bytes(seq,
- * Hq, Hkv, D) bytes, 256-byte aligned, caller-owned, contents irrelevant), then
- * attention with the Q normalisation fused into its prologue.  With 4 to 8
- * query heads per KV head the heads of a group share every K/V tile in one
- * workgroup (the longest causal rows split over two workgroups, merged through
- * the workspace); otherwise one workgroup per query head.  qkv, out, cos, sin,
- * q_norm_w and k_norm_w are 16-byte aligned.
+ * straight into the packed K/V tiles, with the V tiles packed by the same launch,
+ * in `workspace` (>= rldx_llm_fused_attention_workspace_bytes(seq, Hkv, D) bytes,
+ * 16-byte aligned, caller-owned), then attention with the Q normalisation fused
+ * into its prologue.  qkv, out, cos, sin, q_norm_w and k_norm_w are 16-byte aligned.
  *
  * Replaces: fused_llm_attention.forward(qkv, q_norm_w, q_norm_w_rot, k_norm_w,
  *   k_norm_w_rot, cos, signed_sin, num_heads, num_kv_heads, head_dim, out)
@@ -251,14 +247,12 @@ hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv_row_stride
                                          int64_t head_dim, float eps, void* workspace, int64_t workspace_bytes,
                                          hipStream_t stream);
 
-/* Workspace bytes rldx_llm_fused_attention_bf16 needs: the packed K/V tiles,
- * and for 4-8 query heads per KV head the arrival counters and the partial
- * results of split query blocks (-1: invalid sizes). */
-int64_t rldx_llm_fused_attention_workspace_bytes(int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim);
+/* Workspace bytes rldx_llm_fused_attention_bf16 needs (the packed K/V tiles). */
+int64_t rldx_llm_fused_attention_workspace_bytes(int64_t seq, int64_t kv_heads, int64_t head_dim);
 
-/* Scratch bytes of the allocation-free variant below, per GPU (64 MiB: e.g. 28 / 4
- * heads x 1280 tokens needs 22.1 MB, 32 / 8 heads x 16384 tokens 64 MiB at head_dim 128). */
-#define RLDX_LLM_ATTN_NOALLOC_MAX_BYTES (64 << 20)
+/* Scratch bytes of the allocation-free variant below, per GPU (16 MiB: e.g. 8 KV
+ * heads x 4096 tokens at head_dim 128). */
+#define RLDX_LLM_ATTN_NOALLOC_MAX_BYTES (16 << 20)
 
 /*
  * rldx_llm_fused_attention_bf16 without a workspace argument: it allocates
@@ -268,7 +262,7 @@ int64_t rldx_llm_fused_attention_workspace_bytes(int64_t seq, int64_t q_heads, i
  * of RLDX_LLM_ATTN_NOALLOC_MAX_BYTES that each GPU the library runs on holds
  * until the process ends (its address is resolved once per device, on the
  * first call there, with that device current).  Calls whose
- * rldx_llm_fused_attention_workspace_bytes(seq, q_heads, kv_heads, head_dim) exceeds it
+ * rldx_llm_fused_attention_workspace_bytes(seq, kv_heads, head_dim) exceeds it
  * return hipErrorInvalidValue with nothing enqueued.  Every call on a GPU shares
  * that GPU's array: calls that overlap in time on one GPU (other streams, other
  * threads) race and must be serialised by the caller.  Same results as

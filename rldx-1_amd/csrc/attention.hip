@@ -48,7 +48,6 @@
 //                                lane l, element i
 //                                = V[32t + 16 s2 + 8 (i >> 2) + 4 (l >> 5) + (i & 3)][32 db + (l & 31)]
 //   keys >= Sk hold zeros.
-#include <cstdlib>
 #include <mutex>
 
 #include "rldx_amd.h"
@@ -569,406 +568,6 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// GQA attention with the query heads of a KV group sharing every K/V tile.
-//
-// Workgroup = (batch, KV head hk, 32-query block qb, key chunk j): NW compute
-// waves, wave w owning query head hk * NW + w (NW = Hq / Hkv), plus one loader
-// wave.  The loader copies each 32-key packed K/V tile of the chunk once from
-// L2 into an LDS ring with buffer_load ... lds (no VGPR staging); after one
-// barrier per tile all NW compute waves read their K / V operands from LDS
-// (ds_read_b128, conflict-free 16 bytes per lane of each 1 KB chunk), so the
-// tile crosses from L2 once per group instead of once per query head.  Each
-// compute wave keeps its own online-softmax state (m, l, O) for its 32 queries
-// exactly as attn_fwd_kernel's waves do.
-// Causal rows of qb reach key tiles 0..qb; the host cuts them into chunks of
-// at most `chunk` tiles (the longest query blocks into two or more
-// workgroups).  A single-chunk block is finalised in place; the chunks of a
-// split block store their (O, m, l) with device-scope stores, count in on a
-// per-block counter with a device-scope atomic (the counters are cleared by
-// the launch before, which packs the K/V tiles), and the last to arrive merges
-// every chunk in chunk order (the same result whichever arrives last) and
-// writes the output.
-// ---------------------------------------------------------------------------
-struct GqaArgs {
-  const uint16_t* q;
-  uint16_t* o;
-  const uint16_t* kv;  // packed K/V tiles
-  int64_t q_sb, q_sh, q_ss;
-  int64_t o_sb, o_sh, o_ss;
-  int64_t kv_sb, kv_sh;
-  int hkv, sq, sk, nqb, ntk;  // key tiles ntk = ceil(sk / 32)
-  int chunk;                  // max key tiles per workgroup
-  int items_per_head;         // workgroups per (batch, KV head)
-  int slots_per_head;         // partial slots per (batch, KV head): chunks of split blocks
-  int items;
-  float scale_log2;
-  // fused Q RMSNorm + rotate-half RoPE (kQNorm)
-  const uint16_t* q_norm_w;
-  const uint16_t* cos;
-  const uint16_t* sin;
-  int64_t cs_ss;
-  float eps;
-  int sin_signed;
-  float* part;   // [slot][wave][17][64] floatx4: O accumulators, then (m, l)
-  unsigned* cnt; // [batch * hkv * nqb] arrival counters, zero at launch
-};
-
-__host__ __device__ inline int gqa_block_tiles(int qb, int ntk, bool causal) { return causal ? min(qb + 1, ntk) : ntk; }
-__host__ __device__ inline int gqa_chunks(int tiles, int chunk) { return (tiles + chunk - 1) / chunk; }
-
-// Q RMSNorm + rotate-half RoPE of a wave's 32 query rows, in registers (every
-// chunk pair of the head; the arithmetic of qnorm_rope_pair).
-template <int D, int K0>
-__device__ __forceinline__ void qnorm_rope_regs_pair(bf16x8 (&qreg)[D / 16], const bf16x8 (&x)[D / 16],
-                                                     const GqaArgs& a, int pos, bool valid, float rinv) {
-#pragma clang fp contract(off)
-  constexpr int KS = D / 16, K1 = K0 + KS / 2;
-  const int g = (threadIdx.x & 63) >> 5;
-  const uint16_t* cr = a.cos + static_cast<int64_t>(valid ? pos : 0) * a.cs_ss + g * 8;
-  const uint16_t* sr = a.sin + static_cast<int64_t>(valid ? pos : 0) * a.cs_ss + g * 8;
-  const u32x4 w0 = *reinterpret_cast<const u32x4*>(a.q_norm_w + K0 * 16 + g * 8);
-  const u32x4 w1 = *reinterpret_cast<const u32x4*>(a.q_norm_w + K1 * 16 + g * 8);
-  const u32x4 c0 = *reinterpret_cast<const u32x4*>(cr + K0 * 16), c1 = *reinterpret_cast<const u32x4*>(cr + K1 * 16);
-  const u32x4 s0 = *reinterpret_cast<const u32x4*>(sr + K0 * 16), s1 = *reinterpret_cast<const u32x4*>(sr + K1 * 16);
-  const u32x4 x0 = __builtin_bit_cast(u32x4, x[K0]), x1 = __builtin_bit_cast(u32x4, x[K1]);
-  u32x4 o0, o1;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t n0 = pack_bf16x2(bf16x2_lo(x0[j]) * rinv, bf16x2_hi(x0[j]) * rinv);
-    const uint32_t n1 = pack_bf16x2(bf16x2_lo(x1[j]) * rinv, bf16x2_hi(x1[j]) * rinv);
-    const uint32_t y0 = pack_bf16x2(bf16x2_lo(w0[j]) * bf16x2_lo(n0), bf16x2_hi(w0[j]) * bf16x2_hi(n0));
-    const uint32_t y1 = pack_bf16x2(bf16x2_lo(w1[j]) * bf16x2_lo(n1), bf16x2_hi(w1[j]) * bf16x2_hi(n1));
-    const float y0l = bf16x2_lo(y0), y0h = bf16x2_hi(y0), y1l = bf16x2_lo(y1), y1h = bf16x2_hi(y1);
-    const float r0l = a.sin_signed ? y1l : -y1l, r0h = a.sin_signed ? y1h : -y1h;
-    const uint32_t t0 = pack_bf16x2(y0l * bf16x2_lo(c0[j]), y0h * bf16x2_hi(c0[j]));
-    const uint32_t u0 = pack_bf16x2(r0l * bf16x2_lo(s0[j]), r0h * bf16x2_hi(s0[j]));
-    const uint32_t t1 = pack_bf16x2(y1l * bf16x2_lo(c1[j]), y1h * bf16x2_hi(c1[j]));
-    const uint32_t u1 = pack_bf16x2(y0l * bf16x2_lo(s1[j]), y0h * bf16x2_hi(s1[j]));
-    o0[j] = pack_bf16x2(bf16x2_lo(t0) + bf16x2_lo(u0), bf16x2_hi(t0) + bf16x2_hi(u0));
-    o1[j] = pack_bf16x2(bf16x2_lo(t1) + bf16x2_lo(u1), bf16x2_hi(t1) + bf16x2_hi(u1));
-  }
-  qreg[K0] = __builtin_bit_cast(bf16x8, o0);
-  qreg[K1] = __builtin_bit_cast(bf16x8, o1);
-}
-
-template <int D>
-__device__ __forceinline__ void qnorm_rope_regs(bf16x8 (&qreg)[D / 16], const GqaArgs& a, int pos, bool valid) {
-#pragma clang fp contract(off)
-  constexpr int KS = D / 16;
-  bf16x8 x[KS];
-  float ss = 0.f;
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    x[ks] = qreg[ks];
-    const u32x4 raw = __builtin_bit_cast(u32x4, qreg[ks]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float lo = bf16x2_lo(raw[j]), hi = bf16x2_hi(raw[j]);
-      ss += lo * lo;
-      ss += hi * hi;
-    }
-  }
-  ss = pair_sum(ss);
-  const float rinv = 1.0f / __builtin_sqrtf(ss * (1.0f / D) + a.eps);
-  qnorm_rope_regs_pair<D, 0>(qreg, x, a, pos, valid, rinv);
-  qnorm_rope_regs_pair<D, 1>(qreg, x, a, pos, valid, rinv);
-  if constexpr (KS / 2 > 2) {
-    qnorm_rope_regs_pair<D, 2>(qreg, x, a, pos, valid, rinv);
-    qnorm_rope_regs_pair<D, 3>(qreg, x, a, pos, valid, rinv);
-  }
-}
-
-// s_waitcnt vmcnt(N) for the loader wave: N = loads of the tiles after the
-// current one that are still allowed in flight (0, 1 or 2 tiles of CH loads)
-template <int CH>
-__device__ __forceinline__ void gqa_wait_tiles(int ahead) {
-  static_assert(CH == 8 || CH == 16, "1 KB chunks per tile: D / 8");
-  if constexpr (CH == 16) {
-    if (ahead >= 2) asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
-    else if (ahead == 1) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  } else {
-    if (ahead >= 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else if (ahead == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  }
-}
-
-// The loader wave's copy of K/V tile t into ring slot `slot`: CH loads of 1 KB
-// straight into LDS.  Templated on every parameter of its kernel: the host
-// compilation pass drops a kernel whose body reaches one specialization of a
-// function holding the LDS-load builtin from several kernels.
-template <int D, int NW, bool kCausal, bool kQNorm, bool kLds>
-__device__ __forceinline__ void gqa_dma_tile(__amdgpu_buffer_rsrc_t kvr, u32x4* ring, int slot, int t) {
-  constexpr int TILE_BYTES = 128 * D;
-  constexpr int CH = TILE_BYTES / 1024;
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int c = 0; c < CH; ++c)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(kvr, (__attribute__((address_space(3))) void*)(ring + (slot * CH + c) * 64),
-                                             16, lane * 16, t * TILE_BYTES + c * 1024, 0, 0);
-}
-
-// kLds: K/V tiles through the LDS ring (a loader wave, one barrier per tile);
-// otherwise every compute wave loads its operands straight into VGPRs (the
-// next tile's K after the S products, its V after the P.V products) and the
-// waves of the group share the tiles through the CU's L1, without barriers.
-template <int D, int NW, bool kCausal, bool kQNorm, bool kLds>
-__global__ __launch_bounds__(64 * (NW + (kLds ? 1 : 0)), 1) void gqa_attn_kernel(GqaArgs a) {
-  constexpr int BN = kTileKeys;
-  constexpr int KSTEPS = D / 16;
-  constexpr int DBLK = D / 32;
-  constexpr int TILE_BYTES = 128 * D;
-  constexpr int CH = TILE_BYTES / 1024;  // 1 KB chunks per tile (K chunks, then V^T chunks)
-  constexpr int NBUF = 3;                // LDS ring of K/V tiles
-  constexpr int G4 = DBLK * 4 + 1;       // float4 groups per lane of a partial: O, then (m, l)
-  __shared__ __attribute__((aligned(16))) u32x4 ring[kLds ? NBUF * CH * 64 : 1];
-  __shared__ int last_flag;
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-  const bool loader = kLds && wave == NW;
-  const int l32 = lane & 31;
-  const int g = lane >> 5;
-
-  // ---- work item: XCD-aware order (contiguous item ranges per XCD, one KV head's
-  //      blocks together), then (batch, kv head), longest query blocks first ----
-  int p;
-  {
-    const int total = static_cast<int>(gridDim.x);
-    const int i = static_cast<int>(blockIdx.x);
-    const int per = total / kXcds, rem = total % kXcds;
-    const int xcd = i % kXcds, k = i / kXcds;
-    p = xcd < rem ? xcd * (per + 1) + k : rem * (per + 1) + (xcd - rem) * per + k;
-  }
-  const int bh = p / a.items_per_head;  // batch * hkv + hk
-  int r = p % a.items_per_head;
-  int qb = a.nqb - 1, slot0 = 0, nch = 1;
-  for (;; --qb) {  // terminates: the items of a head sum to items_per_head
-    nch = gqa_chunks(gqa_block_tiles(qb, a.ntk, kCausal), a.chunk);
-    if (r < nch) break;
-    r -= nch;
-    if (nch > 1) slot0 += nch;
-  }
-  const int j = r;
-  const int b = bh / a.hkv, hk = bh % a.hkv;
-  const int tiles = gqa_block_tiles(qb, a.ntk, kCausal);
-  const int t_begin = j * tiles / nch, t_end = (j + 1) * tiles / nch;  // >= 1 tile: nch <= tiles
-  const int q_first = qb * 32;
-  const int h = hk * NW + (loader ? 0 : wave);
-  const int head_tiles = a.ntk;
-  const __amdgpu_buffer_rsrc_t kvr =
-      make_rsrc(a.kv + b * a.kv_sb + hk * a.kv_sh, head_tiles * TILE_BYTES);
-  auto dma = [&](int t) { gqa_dma_tile<D, NW, kCausal, kQNorm, kLds>(kvr, ring, t % NBUF, t); };  // the loader wave
-  const int voff = lane * 16;
-  u32x4 kop[KSTEPS], vop[2 * DBLK];  // direct mode: the operands of the next tile, in flight
-  if constexpr (!kLds) {
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks)
-      kop[ks] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + ks * 1024, t_begin * TILE_BYTES, 0);
-#pragma unroll
-    for (int cc = 0; cc < 2 * DBLK; ++cc)
-      vop[cc] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + (KSTEPS + cc) * 1024, t_begin * TILE_BYTES, 0);
-  }
-
-  // ---- Q^T operands of the wave's head (lane: query l32, d-chunk 2 ks + g) ----
-  const int q_idx = q_first + l32;
-  bf16x8 qreg[KSTEPS];
-  if (loader) {
-    if constexpr (kLds)
-      for (int t = t_begin; t < min(t_end, t_begin + NBUF - 1); ++t) dma(t);
-  } else {
-    const uint16_t* qrow = a.q + b * a.q_sb + h * a.q_sh + min(q_idx, a.sq - 1) * a.q_ss + g * 8;
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks)
-      qreg[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qrow + ks * 16));
-    if constexpr (kQNorm) qnorm_rope_regs<D>(qreg, a, q_idx, q_idx < a.sq);
-  }
-
-  floatx16 oacc[DBLK];
-#pragma unroll
-  for (int db = 0; db < DBLK; ++db) oacc[db] = floatx16{};
-  float m_ref = -__builtin_inff(), l_part = 0.f;
-  const float c = a.scale_log2;
-
-  for (int t = t_begin; t < t_end; ++t) {
-    const int tn = min(t + 1, t_end - 1) * TILE_BYTES;  // direct mode: the next tile (clamped)
-    const u32x4* sl = ring + (t % NBUF) * CH * 64 + lane;
-    if constexpr (kLds) {
-      if (loader) gqa_wait_tiles<CH>(min(t_end - 1 - t, NBUF - 2));
-      asm volatile("s_barrier" ::: "memory");  // tile t is in LDS; every wave is done with tile t - 1
-      if (loader) {
-        if (t + NBUF - 1 < t_end) dma(t + NBUF - 1);  // into the slot of tile t - 1
-        continue;
-      }
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) kop[ks] = sl[ks * 64];
-    }
-    floatx16 sacc = floatx16{};
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks)
-      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kop[ks]), qreg[ks], sacc, 0, 0, 0);
-    if constexpr (kLds) {
-#pragma unroll
-      for (int cc = 0; cc < 2 * DBLK; ++cc) vop[cc] = sl[(KSTEPS + cc) * 64];
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) kop[ks] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + ks * 1024, tn, 0);
-    }
-    const int k0 = t * BN;
-    const bool edge = (k0 + BN > a.sk) || (kCausal && k0 + BN - 1 > q_first);
-    float mt = -__builtin_inff();
-    if (!edge) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) mt = fmaxf(mt, sacc[e]);
-      mt *= c;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int key = k0 + 8 * (e >> 2) + 4 * g + (e & 3);
-        bool ok = key < a.sk;
-        if constexpr (kCausal) ok = ok && (key <= q_idx);
-        const float sv = ok ? sacc[e] * c : -__builtin_inff();
-        sacc[e] = sv;
-        mt = fmaxf(mt, sv);
-      }
-    }
-    if (__any(mt > m_ref + kLazyThreshold)) {
-      const float mq = pair_max(mt);
-      const float new_ref = mq > m_ref + kLazyThreshold ? mq : m_ref;
-      const float alpha = (m_ref == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(m_ref - new_ref);
-      m_ref = new_ref;
-      l_part *= alpha;
-#pragma unroll
-      for (int db = 0; db < DBLK; ++db) oacc[db] *= alpha;
-    }
-    const float m_use = (m_ref == -__builtin_inff()) ? 0.f : m_ref;
-    float psum = 0.f;
-    if (!edge) {
-      const float nm = -m_use;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[e], c, nm));
-        sacc[e] = pe;
-        psum += pe;
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float pe = __builtin_amdgcn_exp2f(sacc[e] - m_use);
-        sacc[e] = pe;
-        psum += pe;
-      }
-    }
-    l_part += psum;
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      floatx8 pv;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pv[e] = sacc[s2 * 8 + e];
-      const bf16x8 pop = __builtin_convertvector(pv, bf16x8);
-#pragma unroll
-      for (int db = 0; db < DBLK; ++db)
-        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vop[db * 2 + s2]), pop,
-                                                           oacc[db], 0, 0, 0);
-    }
-    if constexpr (!kLds) {
-#pragma unroll
-      for (int cc = 0; cc < 2 * DBLK; ++cc)
-        vop[cc] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + (KSTEPS + cc) * 1024, tn, 0);
-    }
-  }
-
-  // ---- split blocks: publish this chunk, the last to arrive merges ----
-  if (nch > 1) {
-    // partials of the block's chunks: [chunk][wave][G4][lane] float4, written and
-    // read with device-scope buffer operations (coherent across the XCDs' L2s)
-    constexpr int kSlotBytes = NW * G4 * 64 * 16;
-    const int64_t slot_base = static_cast<int64_t>(bh) * a.slots_per_head + slot0;
-    const __amdgpu_buffer_rsrc_t prs =
-        make_rsrc(reinterpret_cast<const char*>(a.part) + slot_base * kSlotBytes, nch * kSlotBytes);
-    auto off = [&](int jj, int g4) { return ((jj * NW + wave) * G4 + g4) * 1024 + lane * 16; };
-    if (!loader) {
-#pragma unroll
-      for (int db = 0; db < DBLK; ++db)
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4)
-          __builtin_amdgcn_raw_buffer_store_b128(
-              __builtin_bit_cast(u32x4, floatx4{oacc[db][q4 * 4], oacc[db][q4 * 4 + 1], oacc[db][q4 * 4 + 2],
-                                                oacc[db][q4 * 4 + 3]}),
-              prs, off(j, db * 4 + q4), 0, kCpolDevice);
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, floatx4{m_ref, l_part, 0.f, 0.f}), prs,
-                                             off(j, DBLK * 4), 0, kCpolDevice);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial is complete at device scope
-    }
-    __syncthreads();
-    unsigned* cnt = a.cnt + bh * a.nqb + qb;
-    if (threadIdx.x == 0)
-      last_flag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                  static_cast<unsigned>(nch - 1);
-    __syncthreads();
-    if (!last_flag || loader) return;
-    // merge every chunk in chunk order: M = max m_j, O = sum 2^(m_j - M) O_j, l likewise
-    // (separate products and sums: the same operations for a chunk's registers and its stored copy)
-    {
-#pragma clang fp contract(off)
-    auto load = [&](int jj, int g4) {
-      return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(prs, off(jj, g4), 0, kCpolDevice));
-    };
-    float mmax = -__builtin_inff();
-    for (int jj = 0; jj < nch; ++jj) mmax = fmaxf(mmax, jj == j ? m_ref : load(jj, DBLK * 4)[0]);
-    floatx16 osum[DBLK];
-#pragma unroll
-    for (int db = 0; db < DBLK; ++db) osum[db] = floatx16{};
-    float lsum = 0.f;
-    for (int jj = 0; jj < nch; ++jj) {
-      if (jj == j) {
-        const float wgt = m_ref == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m_ref - mmax);
-#pragma unroll
-        for (int db = 0; db < DBLK; ++db) osum[db] += oacc[db] * wgt;
-        lsum += l_part * wgt;
-      } else {
-        const floatx4 ml = load(jj, DBLK * 4);
-        floatx4 v[DBLK * 4];
-#pragma unroll
-        for (int g4 = 0; g4 < DBLK * 4; ++g4) v[g4] = load(jj, g4);
-        const float wgt = ml[0] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(ml[0] - mmax);
-#pragma unroll
-        for (int db = 0; db < DBLK; ++db)
-#pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4)
-#pragma unroll
-            for (int f = 0; f < 4; ++f) osum[db][q4 * 4 + f] += v[db * 4 + q4][f] * wgt;
-        lsum += ml[1] * wgt;
-      }
-    }
-#pragma unroll
-    for (int db = 0; db < DBLK; ++db) oacc[db] = osum[db];
-    l_part = lsum;
-    }
-  } else if (loader) {
-    return;
-  }
-
-  // ---- finalise: O / l, bf16, 8-byte stores of 4 consecutive columns ----
-  const float l = pair_sum(l_part);
-  const float inv = l > 0.f ? 1.0f / l : 0.f;
-  if (q_idx < a.sq) {
-    uint16_t* orow = a.o + b * a.o_sb + h * a.o_sh + static_cast<int64_t>(q_idx) * a.o_ss;
-#pragma unroll
-    for (int db = 0; db < DBLK; ++db)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int d = db * 32 + q4 * 8 + g * 4;
-        uint2 wv;
-        wv.x = pack_bf16x2(oacc[db][q4 * 4] * inv, oacc[db][q4 * 4 + 1] * inv);
-        wv.y = pack_bf16x2(oacc[db][q4 * 4 + 2] * inv, oacc[db][q4 * 4 + 3] * inv);
-        *reinterpret_cast<uint2*>(orow + d) = wv;
-      }
-  }
-}
-
-// ---------------------------------------------------------------------------
 // K [B, H, Sk, D], V [B, H, Sk, D] (strided) -> packed K/V tiles (layout at the
 // top of this file).  One workgroup per (32-key tile, head, batch); V is
 // transposed through LDS.
@@ -1482,72 +1081,6 @@ void fill_qo(AttnArgs& a, const void* q, void* o, int64_t q_heads, int64_t kv_he
   a.scale_log2 = scale * kLog2e;
 }
 
-// Launch plan of gqa_attn_kernel for the causal GQA prefill (seq_q == seq_k).
-struct GqaPlan {
-  int nqb, ntk, chunk, items_per_head, slots_per_head;
-  int64_t items, cnt_bytes, part_bytes;
-};
-
-// Query heads per KV head that share K/V tiles in one workgroup (one wave each).
-bool gqa_shared_group(int64_t q_heads, int64_t kv_heads) {
-  const int64_t g = q_heads / kv_heads;
-  return g >= 4 && g <= 8;
-}
-
-// Causal rows are cut into chunks of at most `chunk` key tiles.  When one
-// workgroup per (KV head, query block) leaves CUs idle (fewer than 256
-// workgroups) and the longest row has at least 16 tiles, the longer half of
-// the rows is split in two (measured on MI355X: 28 / 4 heads x 1280 tokens
-// 45.2 -> 34.7 us); shorter problems are not split (their merge costs more than
-// the added workgroups gain: 32 / 8 heads x 169 tokens 15.6 -> 17.5 us when
-// split).  RLDX_GQA_CHUNK overrides the chunk (tuning).
-GqaPlan gqa_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq, int64_t head_dim) {
-  GqaPlan P{};
-  P.nqb = static_cast<int>((seq + 31) / 32);
-  P.ntk = P.nqb;
-  int chunk = P.ntk;
-  if (batch * kv_heads * P.nqb < 256 && P.ntk >= 16) chunk = (P.ntk + 1) / 2;
-  if (const char* env = getenv("RLDX_GQA_CHUNK")) {
-    const int c = atoi(env);
-    if (c > 0) chunk = c;
-  }
-  P.chunk = chunk < 1 ? 1 : chunk;
-  for (int qb = 0; qb < P.nqb; ++qb) {
-    const int n = gqa_chunks(gqa_block_tiles(qb, P.ntk, true), P.chunk);
-    P.items_per_head += n;
-    if (n > 1) P.slots_per_head += n;
-  }
-  const int64_t group = q_heads / kv_heads;
-  P.items = batch * kv_heads * P.items_per_head;
-  P.cnt_bytes = (batch * kv_heads * P.nqb * 4 + 255) / 256 * 256;
-  P.part_bytes = batch * kv_heads * P.slots_per_head * group * (head_dim / 8 + 1) * 1024;
-  return P;
-}
-
-template <int D, int NW>
-void launch_gqa_nw(const GqaArgs& g, hipStream_t stream) {
-  static const int mode = [] {  // RLDX_GQA_LDS=0: operands straight into VGPRs (tuning)
-    const char* e = getenv("RLDX_GQA_LDS");
-    return e ? atoi(e) : 1;
-  }();
-  if (mode)
-    hipLaunchKernelGGL((gqa_attn_kernel<D, NW, true, true, true>), dim3(static_cast<unsigned>(g.items)),
-                       dim3(64 * (NW + 1)), 0, stream, g);
-  else
-    hipLaunchKernelGGL((gqa_attn_kernel<D, NW, true, true, false>), dim3(static_cast<unsigned>(g.items)),
-                       dim3(64 * NW), 0, stream, g);
-}
-
-template <int D>
-void launch_gqa_d(const GqaArgs& g, int nw, hipStream_t stream) {
-  switch (nw) {
-    case 4: launch_gqa_nw<D, 4>(g, stream); break;
-    case 5: launch_gqa_nw<D, 5>(g, stream); break;
-    case 6: launch_gqa_nw<D, 6>(g, stream); break;
-    case 7: launch_gqa_nw<D, 7>(g, stream); break;
-    default: launch_gqa_nw<D, 8>(g, stream); break;
-  }
-}
 }  // namespace
 }  // namespace rldx
 
@@ -1648,16 +1181,10 @@ extern "C" hipError_t rldx_attention_fwd_bf16(const void* q, const void* k, cons
                                         q_strides, o_strides, key_bias, key_bias_batch_stride, scale, causal, stream);
 }
 
-
-extern "C" int64_t rldx_llm_fused_attention_workspace_bytes(int64_t seq, int64_t q_heads, int64_t kv_heads,
-                                                            int64_t head_dim) {
-  if (seq < 0 || q_heads <= 0 || kv_heads <= 0 || head_dim < 0 || q_heads % kv_heads) return -1;
-  // the packed K/V tiles of the Hkv heads, then (query groups of 4-8 heads) the
-  // arrival counters and the partial results of split query blocks
-  const int64_t kv_bytes = (kv_heads * rldx_attention_kv_packed_elems(seq, head_dim) * 2 + 255) / 256 * 256;
-  if (seq == 0 || !gqa_shared_group(q_heads, kv_heads)) return kv_bytes;
-  const GqaPlan P = gqa_plan(1, q_heads, kv_heads, seq, head_dim);
-  return kv_bytes + P.cnt_bytes + P.part_bytes;
+extern "C" int64_t rldx_llm_fused_attention_workspace_bytes(int64_t seq, int64_t kv_heads, int64_t head_dim) {
+  if (seq < 0 || kv_heads < 0 || head_dim < 0) return -1;
+  // the packed K/V tiles of the Hkv heads
+  return kv_heads * rldx_attention_kv_packed_elems(seq, head_dim) * 2;
 }
 
 extern "C" hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv_row_stride, const void* q_norm_w,
@@ -1673,71 +1200,28 @@ extern "C" hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv
   if (qkv_row_stride < (q_heads + 2 * kv_heads) * head_dim || qkv_row_stride % 8 || out_row_stride % 8 ||
       out_row_stride < q_heads * head_dim || cos_row_stride < head_dim || cos_row_stride % 8)
     return hipErrorInvalidValue;
-  if (workspace_bytes < rldx_llm_fused_attention_workspace_bytes(seq, q_heads, kv_heads, head_dim))
+  if (workspace_bytes < rldx_llm_fused_attention_workspace_bytes(seq, kv_heads, head_dim))
     return hipErrorInvalidValue;
-  if (!a16(qkv) || !a16(out) || !a16(cos) || !a16(sin) || reinterpret_cast<uintptr_t>(workspace) % 256 ||
-      !a16(q_norm_w) || !a16(k_norm_w))
+  if (!a16(qkv) || !a16(out) || !a16(cos) || !a16(sin) || !a16(workspace) || !a16(q_norm_w) || !a16(k_norm_w))
     return hipErrorInvalidValue;
   if (seq > (1 << 24) || q_heads > 65535) return hipErrorInvalidValue;
   const uint16_t* base = static_cast<const uint16_t*>(qkv);
   uint16_t* kvp = static_cast<uint16_t*>(workspace);  // packed K/V tiles
   const int64_t head_elems = rldx_attention_kv_packed_elems(seq, head_dim);
-  const bool shared = gqa_shared_group(q_heads, kv_heads);
-  GqaPlan P{};
-  const int64_t kv_bytes = (kv_heads * head_elems * 2 + 255) / 256 * 256;
-  unsigned* cnt = nullptr;
-  if (shared) {
-    P = gqa_plan(1, q_heads, kv_heads, seq, head_dim);
-    // 32-bit byte offsets inside a head's tiles and one split block's partials; 1-D grid
-    if (head_elems * 2 > (int64_t{1} << 31) - 1 || P.items > (int64_t{1} << 31) - 1) return hipErrorInvalidValue;
-    cnt = reinterpret_cast<unsigned*>(static_cast<char*>(workspace) + kv_bytes);
-  }
   // 1) K: RMSNorm + rotate-half RoPE straight into the packed tiles, V packed by
   //    the same launch (Q is done inside the attention kernel)
   hipError_t e = gqa_k_norm_rope_kv_pack(base + q_heads * head_dim, base + (q_heads + kv_heads) * head_dim,
                                          qkv_row_stride, static_cast<const uint16_t*>(k_norm_w),
                                          static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin),
                                          cos_row_stride, sin_is_signed != 0, seq, kv_heads, head_dim, eps, kvp,
-                                         head_elems, cnt, shared ? kv_heads * P.nqb : 0, stream);
+                                         head_elems, stream);
   if (e != hipSuccess) return e;
-  const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(head_dim));
-  if (shared) {
-    // 2) causal GQA attention, the heads of a KV group sharing each K/V tile
-    char* ws = static_cast<char*>(workspace);
-    GqaArgs g{};
-    g.q = base;
-    g.o = static_cast<uint16_t*>(out);
-    g.kv = kvp;
-    g.q_sb = 0; g.q_sh = head_dim; g.q_ss = qkv_row_stride;
-    g.o_sb = 0; g.o_sh = head_dim; g.o_ss = out_row_stride;
-    g.kv_sb = 0; g.kv_sh = head_elems;
-    g.hkv = static_cast<int>(kv_heads);
-    g.sq = g.sk = static_cast<int>(seq);
-    g.nqb = P.nqb; g.ntk = P.ntk; g.chunk = P.chunk;
-    g.items_per_head = P.items_per_head;
-    g.slots_per_head = P.slots_per_head;
-    g.items = static_cast<int>(P.items);
-    g.scale_log2 = scale * kLog2e;
-    g.q_norm_w = static_cast<const uint16_t*>(q_norm_w);
-    g.cos = static_cast<const uint16_t*>(cos);
-    g.sin = static_cast<const uint16_t*>(sin);
-    g.cs_ss = cos_row_stride;
-    g.eps = eps;
-    g.sin_signed = sin_is_signed ? 1 : 0;
-    g.cnt = cnt;  // cleared by the K launch above
-    g.part = reinterpret_cast<float*>(ws + kv_bytes + P.cnt_bytes);
-    const int nw = static_cast<int>(q_heads / kv_heads);
-    if (head_dim == 128)
-      launch_gqa_d<128>(g, nw, stream);
-    else
-      launch_gqa_d<64>(g, nw, stream);
-    return hipGetLastError();
-  }
-  // 2) causal GQA attention, one query head per workgroup, Q normalised in the prologue
+  // 2) causal GQA attention, Q normalised in the prologue
   AttnArgs a{};
   const int64_t q_strides[3] = {0, head_dim, qkv_row_stride};
   const int64_t o_strides[3] = {0, head_dim, out_row_stride};
-  fill_qo(a, base, out, q_heads, kv_heads, seq, seq, q_strides, o_strides, nullptr, 0, scale);
+  fill_qo(a, base, out, q_heads, kv_heads, seq, seq, q_strides, o_strides, nullptr, 0,
+          1.0f / __builtin_sqrtf(static_cast<float>(head_dim)));
   a.kv = kvp;
   a.kv_sb = 0;
   a.kv_sh = head_elems;
@@ -1789,7 +1273,7 @@ extern "C" hipError_t rldx_llm_fused_attention_noalloc_bf16(const void* qkv, int
                                                             int32_t sin_is_signed, void* out, int64_t out_row_stride,
                                                             int64_t seq, int64_t q_heads, int64_t kv_heads,
                                                             int64_t head_dim, float eps, hipStream_t stream) {
-  const int64_t need = rldx_llm_fused_attention_workspace_bytes(seq, q_heads, kv_heads, head_dim);
+  const int64_t need = rldx_llm_fused_attention_workspace_bytes(seq, kv_heads, head_dim);
   if (need < 0 || need > RLDX_LLM_ATTN_NOALLOC_MAX_BYTES) return hipErrorInvalidValue;  // beyond the scratch array
   if (seq == 0) return rldx_llm_fused_attention_bf16(qkv, qkv_row_stride, q_norm_w, k_norm_w, cos, sin,
                                                      cos_row_stride, sin_is_signed, out, out_row_stride, seq, q_heads,

@@ -175,7 +175,7 @@ RLDX_HD int64_t packed_act_offset(int64_t row, int64_t col, int64_t k) {
 hipError_t gqa_k_norm_rope_kv_pack(const uint16_t* k, const uint16_t* v, int64_t row_stride, const uint16_t* k_w,
                                    const uint16_t* cos, const uint16_t* sin, int64_t cos_row_stride, bool sin_signed,
                                    int64_t seq, int64_t kv_heads, int64_t head_dim, float eps, uint16_t* kvp,
-                                   int64_t kvp_sh, unsigned* zero, int64_t zero_n, hipStream_t stream);
+                                   int64_t kvp_sh, hipStream_t stream);
 
 // Element offset of K[key][d0 .. d0+7] (d0 % 8 == 0) inside the packed K/V
 // tiles of one head (32 keys per tile, 128 * D bytes, K chunks then V chunks):

@@ -79,8 +79,6 @@ struct HalfArgs {
   int64_t kvp_sh, norm_blocks, kv_tiles;
   const uint16_t* v;
   int64_t v_ss, v_sh;
-  unsigned* zero;  // packed K/V mode: zero_n words the first V-tile workgroup clears (or nullptr)
-  int zero_n;
 };
 
 // One 32-key tile of the packed K/V layout (32 keys, 128 * D bytes: K operand
@@ -132,8 +130,6 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_half_kernel(HalfArgs a) {
   if constexpr (PK) {
     if (static_cast<int64_t>(blockIdx.x) >= a.norm_blocks) {  // a V tile (whole workgroups take this branch)
       const int64_t vb = static_cast<int64_t>(blockIdx.x) - a.norm_blocks;
-      if (vb == 0 && a.zero)  // the next launch's arrival counters
-        for (int i = static_cast<int>(threadIdx.x); i < a.zero_n; i += 256) a.zero[i] = 0u;
       const int64_t h = vb / a.kv_tiles, t = vb - h * a.kv_tiles;
       const uint16_t* vh = a.v + h * a.v_sh;
       kv_tile_pack<D>([&](int64_t m) { return vh + m * a.v_ss; }, a.seq, t * 32, a.kvp + h * a.kvp_sh + t * (64 * D));
@@ -447,15 +443,13 @@ hipError_t half_entry(const void* q, const void* k, const void* q_w, const void*
 
 // K of a GQA prefill (rows [seq] of stride row_stride, head h at k + h * D):
 // RMSNorm + rotate-half RoPE straight into the packed K/V tiles, and the V tiles
-// (v + h * D) packed by further workgroups of the same launch, the first of
-// which also clears zero[0 .. zero_n) (the attention launch's arrival
-// counters).  Arguments are validated by the caller (rldx_llm_fused_attention_bf16).
+// (v + h * D) packed by further workgroups of the same launch.  Arguments are
+// validated by the caller (rldx_llm_fused_attention_bf16).
 hipError_t gqa_k_norm_rope_kv_pack(const uint16_t* k, const uint16_t* v, int64_t row_stride, const uint16_t* k_w,
                                    const uint16_t* cos, const uint16_t* sin, int64_t cos_row_stride, bool sin_signed,
                                    int64_t seq, int64_t kv_heads, int64_t head_dim, float eps, uint16_t* kvp,
-                                   int64_t kvp_sh, unsigned* zero, int64_t zero_n, hipStream_t stream) {
+                                   int64_t kvp_sh, hipStream_t stream) {
   const int64_t rows = seq * kv_heads;
-  if (zero_n < 0 || zero_n > (1 << 24)) return hipErrorInvalidValue;
   if (rows * (head_dim / 8) >= (int64_t{1} << 31) - 256 || kv_heads > 65535) return hipErrorInvalidValue;
   HalfArgs a{};
   a.k = k;
@@ -480,8 +474,6 @@ hipError_t gqa_k_norm_rope_kv_pack(const uint16_t* k, const uint16_t* v, int64_t
   a.v = v;
   a.v_ss = row_stride;
   a.v_sh = head_dim;
-  a.zero = zero;
-  a.zero_n = static_cast<int>(zero_n);
   a.norm_blocks = (rows * (head_dim / 8) + 255) / 256;
   const int64_t grid = a.norm_blocks + kv_heads * a.kv_tiles;
   if (grid > (int64_t{1} << 31) - 1) return hipErrorInvalidValue;

@@ -81,7 +81,7 @@ SIGNATURES = {
         [c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_f32, c_vp,
          c_i64, c_vp],
     ),
-    "rldx_llm_fused_attention_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64]),
+    "rldx_llm_fused_attention_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64]),
     "rldx_llm_fused_attention_noalloc_bf16": (
         c_i32,
         [c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_f32, c_vp],

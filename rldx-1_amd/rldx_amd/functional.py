@@ -413,13 +413,12 @@ def llm_fused_attention(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: tor
         out = torch.empty((M, Hq * D), dtype=BF16, device=qkv.device)
     _require(out.dtype == BF16 and out.shape == (M, Hq * D) and out.stride(1) == 1, "out must be bf16 (M, Hq*D)")
     lib = _lib.load()
-    ws_bytes = int(lib.rldx_llm_fused_attention_workspace_bytes(M, Hq, Hkv, D))
-    _require(ws_bytes >= 0, "unsupported attention sizes")
-    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=qkv.device)
+    ws_bytes = int(lib.rldx_llm_fused_attention_workspace_bytes(M, Hkv, D))
+    ws = torch.empty(max(ws_bytes // 2, 8), dtype=BF16, device=qkv.device)
     _lib.check(lib.rldx_llm_fused_attention_bf16(qkv.data_ptr(), qkv.stride(0), q_norm_w.data_ptr(), k_norm_w.data_ptr(),
                                                  cos.data_ptr(), sin.data_ptr(), cos.stride(0), int(bool(sin_is_signed)),
                                                  out.data_ptr(), out.stride(0), M, Hq, Hkv, D, float(eps), ws.data_ptr(),
-                                                 ws.numel(), _stream_ptr(qkv)), "rldx_llm_fused_attention_bf16")
+                                                 ws.numel() * 2, _stream_ptr(qkv)), "rldx_llm_fused_attention_bf16")
     return out
 
 

@@ -142,14 +142,7 @@ def test_capi_rejects_bad_arguments_without_launching():
                                              8, None) == HIP_INVALID_VALUE
     assert lib.rldx_llm_fused_attention_bf16(16, 4608, 16, 16, 16, 16, 128, 1, 16, 3584, 1280, 28, 3, 128, 1e-6, 16,
                                              1 << 30, None) == HIP_INVALID_VALUE
-    # packed K/V tiles; with 4-8 query heads per KV head also the counters (4 heads x 40 blocks,
-    # 256-byte rounded) and, with fewer than 256 (KV head, query block) pairs, the partials of the
-    # 20 two-chunk blocks per head (7 waves x 17 KB each); 32 / 8 heads: 320 pairs, no split
-    assert lib.rldx_llm_fused_attention_workspace_bytes(1280, 32, 8, 128) == 8 * 40 * 64 * 128 * 2 + 1280
-    assert lib.rldx_llm_fused_attention_workspace_bytes(1280, 4, 4, 128) == 4 * 40 * 64 * 128 * 2
-    assert lib.rldx_llm_fused_attention_workspace_bytes(1280, 28, 4, 128) == \
-        4 * 40 * 64 * 128 * 2 + 768 + 4 * 40 * 7 * 17 * 1024
-    assert lib.rldx_llm_fused_attention_workspace_bytes(1280, 30, 4, 128) == -1
+    assert lib.rldx_llm_fused_attention_workspace_bytes(1280, 4, 128) == 4 * 40 * 64 * 128 * 2
 
 
 def _gemm_groups(ms, a_ptr=256, w_ptr=512, out_ptr=1024, ldo=8192):
@@ -323,17 +316,17 @@ def test_python_wrappers_refuse_cpu_tensors():
 
 
 def test_llm_attention_noalloc_rejects_sizes_beyond_its_scratch():
-    """rldx_llm_fused_attention_noalloc_bf16 checks its workspace size against its
-    scratch array (RLDX_LLM_ATTN_NOALLOC_MAX_BYTES = 64 MiB) before anything else:
-    a size that does not fit is rejected with hipErrorInvalidValue, without
-    touching a device (this host has none)."""
+    """rldx_llm_fused_attention_noalloc_bf16 checks the packed K/V size against its
+    scratch array (RLDX_LLM_ATTN_NOALLOC_MAX_BYTES = 16 MiB) before anything else:
+    one key more than fits is rejected with hipErrorInvalidValue, without touching
+    a device (this host has none)."""
     lib = _lib.load()
-    max_bytes = 64 << 20
-    fits = max(s for s in range(32, 32768, 32)
-               if lib.rldx_llm_fused_attention_workspace_bytes(s, 32, 8, 128) <= max_bytes)
-    assert 8192 <= fits < 32768 - 32
-    assert lib.rldx_llm_fused_attention_workspace_bytes(fits + 32, 32, 8, 128) > max_bytes
+    max_bytes = 16 << 20
+    fits = max_bytes // (8 * 4 * 128)  # 8 KV heads, K + V bf16 = 4 * D bytes per key and head
+    assert lib.rldx_llm_fused_attention_workspace_bytes(fits, 8, 128) == max_bytes
+    assert lib.rldx_llm_fused_attention_workspace_bytes(fits + 1, 8, 128) > max_bytes
     p = 4096  # never dereferenced: the call must fail on the size first
-    for seq in (fits + 32, 1 << 20):
-        assert lib.rldx_llm_fused_attention_noalloc_bf16(p, 48 * 128, p, p, p, p, 128, 1, p, 32 * 128, seq, 32, 8, 128,
-                                                        1e-6, None) == HIP_INVALID_VALUE
+    assert lib.rldx_llm_fused_attention_noalloc_bf16(p, 48 * 128, p, p, p, p, 128, 1, p, 32 * 128, fits + 1, 32, 8, 128,
+                                                    1e-6, None) == HIP_INVALID_VALUE
+    assert lib.rldx_llm_fused_attention_noalloc_bf16(p, 48 * 128, p, p, p, p, 128, 1, p, 32 * 128, 1 << 20, 32, 8, 128,
+                                                    1e-6, None) == HIP_INVALID_VALUE

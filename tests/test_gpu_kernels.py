@@ -282,7 +282,7 @@ def test_backbone_fused_attention_op(dev):
 
 
 @pytest.mark.parametrize("M,Hq,Hkv,D", [(100, 4, 2, 64), (333, 14, 2, 128), (257, 16, 2, 64), (169, 32, 8, 128),
-                                        (70, 12, 2, 128), (1, 8, 2, 128)])
+                                        (70, 12, 2, 128), (150, 10, 2, 128), (1, 8, 2, 128)])
 def test_backbone_fused_attention_op_shapes(dev, M, Hq, Hkv, D):
     """Groups of 2 (one workgroup per query head) and of 4-8 query heads per KV
     head (the heads of a group sharing K/V tiles; causal rows split over
