@@ -404,6 +404,87 @@ def gemm_lines(torch, step) -> dict:
     return out
 
 
+def host_info(torch) -> dict:
+    """The host the CPU legs ran on: CPU model, logical cores, torch threads used."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return dict(cpu_model=model, logical_cores=os.cpu_count(), torch_threads=torch.get_num_threads())
+
+
+def _median_ms(fn, reps: int) -> float:
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def cpu_kernel_baselines(torch) -> dict:
+    """The CPU oracle of configs 1-4 (the eager formulas in torch on the host
+    cores, the same seeded inputs as the GPU lines): 3 warm-ups, median of 10
+    runs (5 for the GQA prefill).  Reported beside the GPU lines, never a gate."""
+    from oracle import cpu_reference as ref
+    from rldx_amd import workloads as W
+
+    cores = min(os.cpu_count() or 1, 64)
+    torch.set_num_threads(cores)
+    out = {}
+
+    def leg(name, fn, inputs, reps=10):
+        for _ in range(3):
+            fn()
+        out[name] = dict(ms=_median_ms(fn, reps), cores=torch.get_num_threads(), kind="port",
+                         inputs_sha256=W.sha256_of(*inputs))
+
+    rc = W.RmsRopeCfg()
+    ri = W.rmsnorm_rope_inputs(rc)
+    leg("rmsnorm_rope_f32_256x16x64",
+        lambda: ref.qk_rmsnorm_rope_half(ri["q"], ri["k"], ri["w"], ri["w"], ri["cos"], ri["sin"], rc.eps),
+        [ri["q"], ri["k"], ri["w"]])
+    sx = W.swiglu_inputs(W.SwigluCfg())["x"]
+    leg("swiglu_2048x11008", lambda: ref.swiglu(sx), [sx])
+    jc = W.JointAttnCfg()
+    ji = W.joint_attn_inputs(jc)
+    jb = ref.mask_to_bias(ji["kv_mask"])
+    leg("joint_attention_16x608x128", lambda: ref.sdpa(ji["q"], ji["k"], ji["v"], key_bias=jb),
+        [ji["q"], ji["k"], ji["v"], ji["kv_mask"]])
+    gc = W.GqaCfg()
+    gi = W.gqa_inputs(gc)
+    leg("gqa_prefill_op_28x4x1280x128",
+        lambda: ref.llm_fused_attention(gi["qkv"], gi["q_norm_w"], gi["k_norm_w"], gi["cos"], gi["sin"], gc.q_heads,
+                                        gc.kv_heads, gc.head_dim),
+        [gi["qkv"], gi["q_norm_w"], gi["k_norm_w"]], reps=5)
+    return out
+
+
+def measured_peaks(torch) -> dict:
+    """Peaks measured on this GPU, beside the published ones: device-to-device
+    copy bandwidth (1 GiB, read + write bytes) and the bf16 MFMA throughput of a
+    library GEMM (torch.matmul 8192 x 8192 x 8192, hipBLASLt)."""
+    dev = torch.device("cuda:0")
+    a = torch.empty(512 << 20, dtype=torch.bfloat16, device=dev)
+    b = torch.empty_like(a)
+    ms = graph_time_ms(lambda: b.copy_(a), 8, torch)
+    copy_gbs = 2 * a.numel() * 2 / (ms * 1e-3) / 1e9
+    del a, b
+    n = 8192
+    x = torch.randn(n, n, device=dev).to(torch.bfloat16)
+    y = torch.randn(n, n, device=dev).to(torch.bfloat16)
+    z = torch.empty(n, n, dtype=torch.bfloat16, device=dev)
+    ms = graph_time_ms(lambda: torch.matmul(x, y, out=z), 8, torch)
+    tflops = 2 * n ** 3 / (ms * 1e-3) / 1e12
+    return dict(copy_gbs=copy_gbs, matmul_bf16_tflops=tflops,
+                published=dict(hbm_gbs=HBM_PEAK_GBS, bf16_mfma_tflops=BF16_MFMA_PEAK_TFLOPS))
+
+
 def cpu_baseline(torch, cfg, weights, inputs, budget_s: float = 20.0):
     """Time the CPU oracle step on the host cores; bounded sample, scaled to ms per action step."""
     from oracle import msat_step_ref as R
@@ -433,8 +514,11 @@ def cpu_baseline(torch, cfg, weights, inputs, budget_s: float = 20.0):
         R.action_step(cfg, w, inp, steps=1, blocks=blocks)
         ms = (time.perf_counter() - t0) * cfg.blocks * cfg.steps / blocks * 1e3
         sample = f"1 iteration x {blocks} blocks, scaled x{cfg.blocks * cfg.steps / blocks:.1f} to a full step"
+    from rldx_amd import workloads as W
+
     return dict(value=ms, unit="ms per MSAT action step", cores=torch.get_num_threads(), kind="port",
-                sample=sample + " of the CPU oracle (torch bf16 eager restatement)")
+                sample=sample + " of the CPU oracle (torch bf16 eager restatement)",
+                inputs_sha256=W.sha256_of(*(inp[k] for k in sorted(inp))))
 
 
 def main():
@@ -514,10 +598,27 @@ def main():
                     frac=dom["gbs"] / HBM_PEAK_GBS, traffic=traffic, algorithmic_bytes=dom["bytes"],
                     flops=dom["flops"], us=dom["us"])
 
+    peaks = measured_peaks(torch)
+    for v in kl.values():  # fractions against the measured peaks as well
+        if isinstance(v, dict) and v.get("unit") == "GB/s":
+            v["frac_of_measured_copy"] = v["achieved"] / peaks["copy_gbs"]
+        elif isinstance(v, dict) and v.get("unit") == "TFLOP/s":
+            v["frac_of_measured_matmul"] = v["achieved"] / peaks["matmul_bf16_tflops"]
+    print(f"[bench] measured peaks: copy {peaks['copy_gbs']:.0f} GB/s, bf16 matmul {peaks['matmul_bf16_tflops']:.0f} "
+          "TFLOP/s", file=sys.stderr, flush=True)
+
     cpu = None
+    host = None
     if not args.no_cpu:
         cpu = cpu_baseline(torch, cfg, weights, inputs)
         print(f"[bench] cpu baseline {cpu['value']:.1f} ms", file=sys.stderr, flush=True)
+        for name, leg in cpu_kernel_baselines(torch).items():
+            kl[name]["cpu"] = leg
+            if "us" in kl[name]:
+                kl[name]["gpu_speedup_vs_cpu"] = leg["ms"] * 1e3 / kl[name]["us"]
+        host = host_info(torch)
+        cpu["cpu_model"] = host["cpu_model"]
+        print("[bench] cpu kernel baselines done", file=sys.stderr, flush=True)
 
     line = {
         "metric": "ms per MSAT action step (bs=1, 1 GPU); kernel % HBM/MFMA roofline",
@@ -541,8 +642,10 @@ def main():
             "step_tflop": cfg.flops_per_step() / 1e12, "weight_gb": cfg.weight_bytes() / 1e9,
         },
         "roofline": roofline,
+        "measured_peaks": peaks,
         "kernels": kl,
         "cpu_baseline": cpu,
+        "host": host,
     }
     print(json.dumps(line))
 
