@@ -1,4 +1,4 @@
-"""CPU oracle of the RLDX-1 MSAT forward (no add-ons) — TEST INFRASTRUCTURE ONLY.
+"""CPU oracle of the RLDX-1 MSAT forward — TEST INFRASTRUCTURE ONLY.
 
 Eager restatement, in CPU bf16 torch, of MSAT._forward_inner with the
 `input_token` time conditioning and `rope_sa_only` positions
@@ -7,6 +7,11 @@ DoubleStreamBlock.forward and SingleStreamBlock.forward with identity
 modulation (rldx/model/modules/action_model/blocks.py:166-254, :383-609), the
 RoPE embedder and rotary product (rldx/model/modules/action_model/ops.py:11-119),
 RMSNorm (rldx/model/modules/norms.py:7-22) and SwiGLUFFN (ops.py:137-161).
+
+The all-add-ons forward (`msat_forward_physics`) restates MSAT._forward_physics
+(msat.py:558-775) with ExpandedDoubleStreamBlock.forward over [VL | SA | P]
+(blocks.py:705-891) and ExpandedSingleStreamBlock.forward over [VL+SA | P]
+(blocks.py:970-1089), identity modulation on every stream.
 
 Weights are a state dict under the reference module's own names
 (`double_blocks.{i}.sa_qkv.weight`, `single_blocks.{i}.linear1.bias`, ...).
@@ -141,3 +146,123 @@ def msat_forward(sd: dict, sa_embs: torch.Tensor, vl_embs: torch.Tensor, temb: t
     shift, scale = _linear(F.silu(temb), sd, "proj_out_1").chunk(2, dim=1)
     sa = layer_norm(sa) * (1 + scale[:, None]) + shift[:, None]
     return _linear(sa, sd, "proj_out_2")
+
+
+# ---------------------------------------------------------------------------
+# All add-ons: physics (P) stream
+# ---------------------------------------------------------------------------
+def key_bias_3(vl_mask, n_vl: int, n_sa: int, physics_mask, n_p: int, dtype):
+    """Key mask of the [VL | SA | P] (or [VL+SA | P]) joint sequence
+    (blocks.py:843-864, msat.py:716-743): VL rows from encoder_attention_mask
+    [B, n_vl] (1 visible) or ones, the n_sa rows after them ones, the n_p physics
+    rows the per-sample physics_attention_mask [B] broadcast over them, or ones;
+    -inf where 0, 0 elsewhere, in the activation dtype.  None when both masks
+    are None (the eager blocks then pass attn_mask=None)."""
+    if vl_mask is None and physics_mask is None:
+        return None
+    B = (vl_mask if vl_mask is not None else physics_mask).shape[0]
+    vm = vl_mask if vl_mask is not None else torch.ones(B, n_vl, dtype=dtype)
+    pm = physics_mask[:, None].expand(-1, n_p).to(vm.dtype) if physics_mask is not None else \
+        torch.ones(B, n_p, dtype=vm.dtype)
+    kv = torch.cat([vm, torch.ones(B, n_sa, dtype=vm.dtype), pm], dim=1)
+    return torch.where(kv == 0, torch.tensor(float("-inf"), dtype=dtype), torch.tensor(0.0, dtype=dtype))
+
+
+def expanded_ds_block(sd: dict, p: str, sa, vl, ph, pe, heads: int, key_bias=None):
+    """ExpandedDoubleStreamBlock.forward with p_tokens, identity modulation
+    (blocks.py:729-891): per-stream pre-LN and QKV, per-stream QK-RMSNorm
+    (q_norm_p / k_norm_p on P), joint attention over [VL | SA | P] with RoPE from
+    pe [B, N_vl + N_sa + N_p, Dh/2], then per-stream proj + residual and SwiGLU
+    MLP + residual.  Returns (sa, vl, ph)."""
+    n_vl, n_sa = vl.shape[1], sa.shape[1]
+    qkvs = [_linear(layer_norm(x), sd, f"{p}{n}_qkv") for x, n in ((vl, "vl"), (sa, "sa"), (ph, "p"))]
+    q, k, v = [], [], []
+    for t, n in zip(qkvs, ("vl", "sa", "p")):
+        tq, tk, tv = (split_heads(u, heads) for u in t.chunk(3, dim=-1))
+        q.append(_qk_norm(tq, sd[f"{p}q_norm_{n}.weight"]))
+        k.append(_qk_norm(tk, sd[f"{p}k_norm_{n}.weight"]))
+        v.append(tv)
+    q, k = apply_rotary_emb(torch.cat(q, dim=2), torch.cat(k, dim=2), pe)
+    o = sdpa(q, k, torch.cat(v, dim=2), key_bias=key_bias)
+    vl = vl + _linear(merge_heads(o[:, :, :n_vl]), sd, f"{p}vl_proj")
+    sa = sa + _linear(merge_heads(o[:, :, n_vl:n_vl + n_sa]), sd, f"{p}sa_proj")
+    ph = ph + _linear(merge_heads(o[:, :, n_vl + n_sa:]), sd, f"{p}p_proj")
+    sa = sa + _swiglu_ffn(layer_norm(sa), sd, f"{p}sa_mlp")
+    vl = vl + _swiglu_ffn(layer_norm(vl), sd, f"{p}vl_mlp")
+    ph = ph + _swiglu_ffn(layer_norm(ph), sd, f"{p}p_mlp")
+    return sa, vl, ph
+
+
+def expanded_ss_block(sd: dict, p: str, x, ph, pe, heads: int, key_bias=None):
+    """ExpandedSingleStreamBlock.forward with p_tokens, SwiGLU, identity
+    modulation (blocks.py:970-1089): linear1 / p_linear1 split into QKV | MLP,
+    QK-RMSNorm (q_norm, k_norm / p_q_norm, p_k_norm), joint attention over
+    [x | P] with RoPE from pe [B, N_x + N_p, Dh/2], then linear2 / p_linear2 of
+    [attention | mlp_proj(SwiGLU)] + residual.  Returns (x, ph)."""
+    inner = sd[f"{p}linear2.weight"].shape[1] - sd[f"{p}mlp_proj.weight"].shape[0]
+    n_x = x.shape[1]
+    h = _linear(layer_norm(x), sd, f"{p}linear1")
+    hp = _linear(layer_norm(ph), sd, f"{p}p_linear1")
+    q, k, v = [], [], []
+    for t, qn, kn in ((h, "q_norm", "k_norm"), (hp, "p_q_norm", "p_k_norm")):
+        tq, tk, tv = (split_heads(u, heads) for u in t[..., : 3 * inner].chunk(3, dim=-1))
+        q.append(_qk_norm(tq, sd[f"{p}{qn}.weight"]))
+        k.append(_qk_norm(tk, sd[f"{p}{kn}.weight"]))
+        v.append(tv)
+    q, k = apply_rotary_emb(torch.cat(q, dim=2), torch.cat(k, dim=2), pe)
+    o = sdpa(q, k, torch.cat(v, dim=2), key_bias=key_bias)
+    x_mlp = _linear(swiglu(h[..., 3 * inner:]), sd, f"{p}mlp_proj")
+    p_mlp = _linear(swiglu(hp[..., 3 * inner:]), sd, f"{p}p_mlp_proj")
+    x = x + _linear(torch.cat([merge_heads(o[:, :, :n_x]), x_mlp], dim=-1), sd, f"{p}linear2")
+    ph = ph + _linear(torch.cat([merge_heads(o[:, :, n_x:]), p_mlp], dim=-1), sd, f"{p}p_linear2")
+    return x, ph
+
+
+def _adaln_out(x, temb, sd, proj1: str, proj2: str):
+    """AdaLN-zero output projection (msat.py:771-781): LN(x) * (1 + scale) + shift,
+    shift | scale = proj1(silu(temb)), then proj2."""
+    shift, scale = _linear(F.silu(temb), sd, proj1).chunk(2, dim=1)
+    return _linear(layer_norm(x) * (1 + scale[:, None]) + shift[:, None], sd, proj2)
+
+
+def msat_forward_physics(sd: dict, sa_embs, vl_embs, p_embs, temb, time_token, *, heads: int, head_dim: int,
+                         ds_blocks: int, ss_blocks: int, theta: float = 10000.0, max_seq_len: int = 1024,
+                         bf16_quirk: bool = True, encoder_attention_mask=None, physics_attention_mask=None):
+    """MSAT._forward_physics, temb_type input_token, rope_sa_only (msat.py:558-775).
+    sa_embs [B, N_sa_pure, sa_dim], vl_embs [B, N_vl, vl_dim], p_embs [B, N_p,
+    sa_dim], temb [B, inner], time_token [B, num_temb, sa_dim];
+    encoder_attention_mask [B, N_vl] and physics_attention_mask [B] (1 visible)
+    or None.  Returns (action [B, N_sa_pure, output_dim], physics [B, N_p,
+    output_dim])."""
+    tables = rope_freq_tables(head_dim, theta, max_seq_len, bf16_quirk)
+    num_temb = time_token.shape[1]
+    B, n_vl = vl_embs.shape[:2]
+    n_p = p_embs.shape[1]
+    sa = torch.cat([time_token, sa_embs], dim=1)
+    n_sa = sa.shape[1]
+    # lower ids (msat.py:595-639): SA axis 1 = 0 .. n_sa - 1; P axis 0 = 1, axis 1 = 0 .. n_p - 1
+    ids = torch.zeros(B, n_vl + n_sa + n_p, 2, dtype=torch.long)
+    ids[:, n_vl:n_vl + n_sa, 1] = torch.arange(n_sa)
+    ids[:, n_vl + n_sa:, 0] = 1
+    ids[:, n_vl + n_sa:, 1] = torch.arange(n_p)
+    pe = rope_pe(tables, ids)
+    kb = key_bias_3(encoder_attention_mask, n_vl, n_sa, physics_attention_mask, n_p, vl_embs.dtype)
+    vl, ph = vl_embs, p_embs
+    for i in range(ds_blocks):
+        sa, vl, ph = expanded_ds_block(sd, f"double_blocks.{i}.", sa, vl, ph, pe, heads, kb)
+    time_tok, sa = sa[:, :num_temb], sa[:, num_temb:]
+    x = torch.cat([_linear(vl, sd, "vl_proj_to_sa"), time_tok, sa], dim=1)
+    n_pure, n_x = sa.shape[1], x.shape[1]
+    # upper ids (msat.py:679-712): time tokens 0 ..; action rows from num_temb + 1; P as below
+    ids_s = torch.zeros(B, n_x + n_p, 2, dtype=torch.long)
+    ids_s[:, n_vl:n_vl + num_temb, 1] = torch.arange(num_temb)
+    ids_s[:, n_x - n_pure:n_x, 1] = torch.arange(num_temb + 1, num_temb + 1 + n_pure)
+    ids_s[:, n_x:, 0] = 1
+    ids_s[:, n_x:, 1] = torch.arange(n_p)
+    pe_s = rope_pe(tables, ids_s)
+    kb_s = key_bias_3(encoder_attention_mask, n_vl, n_x - n_vl, physics_attention_mask, n_p, vl_embs.dtype)
+    for i in range(ss_blocks):
+        x, ph = expanded_ss_block(sd, f"single_blocks.{i}.", x, ph, pe_s, heads, kb_s)
+    action = _adaln_out(x[:, -n_pure:], temb, sd, "proj_out_1", "proj_out_2")
+    physics = _adaln_out(ph, temb, sd, "proj_out_physics_1", "proj_out_physics_2")
+    return action, physics

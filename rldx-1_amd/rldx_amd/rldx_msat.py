@@ -83,6 +83,8 @@ class RldxMsatCfg:
     rope_theta: float = 10000.0
     max_seq_len: int = 1024
     eps: float = 1e-6
+    use_physics: bool = False  # Expanded blocks with a P stream (msat.py:928-989)
+    n_physics: int = 0         # P tokens per call (physics history + future); 0 = no P stream
 
     @property
     def inner(self) -> int:
@@ -140,6 +142,33 @@ class RldxMsatCfg:
         s.update({"vl_proj_to_sa.weight": (d, v), "vl_proj_to_sa.bias": (d,),
                   "proj_out_1.weight": (2 * d, i), "proj_out_1.bias": (2 * d,),
                   "proj_out_2.weight": (self.output_dim, d), "proj_out_2.bias": (self.output_dim,)})
+        if self.use_physics:
+            s.update(self.physics_param_shapes())
+        return s
+
+    def physics_param_shapes(self) -> dict:
+        """The P-stream parameters of the all-add-ons MSAT (p_dim = sa_dim,
+        msat.py:938-989): ExpandedDoubleStreamBlock p_* (blocks.py:665-697, the P
+        SwiGLU width that of SA), ExpandedSingleStreamBlock p_* (blocks.py:942-964)
+        and the physics output projection."""
+        d, i, hd = self.sa_dim, self.inner, self.head_dim
+        s = {}
+        for b in range(self.ds_blocks):
+            p = f"double_blocks.{b}."
+            s.update({p + "p_qkv.weight": (3 * i, d), p + "p_qkv.bias": (3 * i,),
+                      p + "p_proj.weight": (d, i), p + "p_proj.bias": (d,),
+                      p + "p_mlp.w12.weight": (2 * self.sa_ffn, d), p + "p_mlp.w12.bias": (2 * self.sa_ffn,),
+                      p + "p_mlp.w3.weight": (d, self.sa_ffn), p + "p_mlp.w3.bias": (d,),
+                      p + "q_norm_p.weight": (hd,), p + "k_norm_p.weight": (hd,)})
+        e, hs = self.ss_expanded, self.ss_hidden
+        for b in range(self.ss_blocks):
+            p = f"single_blocks.{b}."
+            s.update({p + "p_linear1.weight": (3 * i + 2 * e, d), p + "p_linear1.bias": (3 * i + 2 * e,),
+                      p + "p_mlp_proj.weight": (hs, e), p + "p_mlp_proj.bias": (hs,),
+                      p + "p_linear2.weight": (d, i + hs), p + "p_linear2.bias": (d,),
+                      p + "p_q_norm.weight": (hd,), p + "p_k_norm.weight": (hd,)})
+        s.update({"proj_out_physics_1.weight": (2 * d, i), "proj_out_physics_1.bias": (2 * d,),
+                  "proj_out_physics_2.weight": (self.output_dim, d), "proj_out_physics_2.bias": (self.output_dim,)})
         return s
 
     @staticmethod
@@ -151,7 +180,7 @@ class RldxMsatCfg:
         inner = sd["double_blocks.0.sa_qkv.weight"].shape[0] // 3
         sa_dim, vl_dim = sd["double_blocks.0.sa_qkv.weight"].shape[1], sd["double_blocks.0.vl_qkv.weight"].shape[1]
         kw = dict(heads=inner // hd, head_dim=hd, ds_blocks=ds, ss_blocks=ss, sa_dim=sa_dim, vl_dim=vl_dim,
-                  output_dim=sd["proj_out_2.weight"].shape[0],
+                  output_dim=sd["proj_out_2.weight"].shape[0], use_physics="proj_out_physics_2.weight" in sd,
                   mlp_ratio=sd["double_blocks.0.sa_mlp.w12.weight"].shape[0] * 3 / 4 / sa_dim)
         kw.update(overrides)
         cfg = RldxMsatCfg(**kw)
@@ -176,14 +205,18 @@ def make_state_dict(cfg: RldxMsatCfg, device, seed: int = 11, std: float = 0.02)
 
 def make_inputs(cfg: RldxMsatCfg, device, seed: int = 12) -> dict:
     """SA embeddings (state + action tokens), VL (cognition) tokens, a time
-    embedding and its time token, bf16, batch 1."""
+    embedding and its time token, and with n_physics > 0 the physics tokens
+    `p` [1, n_physics, sa_dim]; bf16, batch 1."""
     g = torch.Generator(device=device).manual_seed(seed)
 
     def rnd(*shape, std=1.0):
         return (std * torch.randn(*shape, generator=g, device=device, dtype=torch.float32)).to(BF16)
 
-    return dict(sa=rnd(1, cfg.n_sa_pure, cfg.sa_dim), vl=rnd(1, cfg.n_vl, cfg.vl_dim),
-                temb=rnd(1, cfg.inner, std=0.5), time_token=rnd(1, cfg.num_temb_tokens, cfg.sa_dim, std=0.5))
+    inp = dict(sa=rnd(1, cfg.n_sa_pure, cfg.sa_dim), vl=rnd(1, cfg.n_vl, cfg.vl_dim),
+               temb=rnd(1, cfg.inner, std=0.5), time_token=rnd(1, cfg.num_temb_tokens, cfg.sa_dim, std=0.5))
+    if cfg.n_physics > 0:
+        inp["p"] = rnd(1, cfg.n_physics, cfg.sa_dim)
+    return inp
 
 
 def load_msat_state_dict(path: str, prefix: str = "action_model.model.", device="cpu") -> dict:
@@ -205,14 +238,15 @@ def load_msat_state_dict(path: str, prefix: str = "action_model.model.", device=
     return sd
 
 
-def rope_tables(cfg: RldxMsatCfg, positions: torch.Tensor, bf16_quirk: bool):
-    """fp32 cos / sin [N, D/2] of the rope_sa_only embedder (axes [D/4, 3D/4],
-    axis 0 at position 0) for axis-1 positions (RoPEEmbedder1D, ops.py:70-119);
-    with bf16_quirk, cos rounded to bf16 and sin = 0 (custom_msat_chain.py:15-54)."""
+def rope_tables(cfg: RldxMsatCfg, positions: torch.Tensor, bf16_quirk: bool, axis0: int = 0):
+    """fp32 cos / sin [N, D/2] of the rope_sa_only embedder (axes [D/4, 3D/4])
+    at axis-0 position `axis0` (0 for SA rows, 1 for physics rows) and the
+    given axis-1 positions (RoPEEmbedder1D, ops.py:70-119); with bf16_quirk,
+    cos rounded to bf16 and sin = 0 (custom_msat_chain.py:15-54)."""
     parts = []
     for i, ad in enumerate((cfg.head_dim // 4, cfg.head_dim - cfg.head_dim // 4)):
         fc = msat_freqs_cis(ad, cfg.max_seq_len, cfg.rope_theta)
-        idx = torch.zeros_like(positions) if i == 0 else positions
+        idx = torch.full_like(positions, axis0) if i == 0 else positions
         parts.append(fc[idx])
     pe = torch.cat(parts, dim=-1)
     if bf16_quirk:
@@ -234,22 +268,43 @@ def _round_up(x: int, m: int) -> int:
 
 class RldxMsat:
     """Static-buffer executor of the RLDX-1 MSAT forward; `forward` launches it
-    eagerly (capturable in a hipGraph), `capture` / `replay` record and replay it."""
+    eagerly (capturable in a hipGraph), `capture` / `replay` record and replay it.
+
+    With cfg.use_physics and cfg.n_physics > 0 it is the all-add-ons MSAT
+    (CustomOpExpandedMSAT, rldx/inference/action_model/engine/
+    custom_expanded_msat_chain.py:19-115; eager MSAT._forward_physics,
+    msat.py:558-775): 4 ExpandedDoubleStreamBlocks over [VL | SA | P] and 8
+    ExpandedSingleStreamBlocks over [VL+SA | P].  The P stream has the SA
+    stream's widths, so every SA GEMM and its P counterpart run as one grouped
+    launch (two groups sharing n and k), as do the x and P GEMMs of the single
+    blocks and the two output projections; the joint attention is one launch
+    over [VL | SA | P].  The SA rows of the joint sequence are padded to a
+    multiple of 32 so that the P rows of the packed attention output start on
+    a 32-row block (the A operand of the P GEMMs): padding rows of Q/K/V are
+    zero and their keys carry -inf."""
 
     def __init__(self, sd: dict, cfg: RldxMsatCfg, device, bf16_quirk: bool = True, vl_mask: bool = False):
         self.cfg, self.dev = cfg, torch.device(device)
         H, D, inner = cfg.heads, cfg.head_dim, cfg.inner
         Fn._require(D in (64, 128), "head_dim must be 64 or 128")
         Fn._require(cfg.n_vl >= 1 and cfg.n_sa_pure >= 1, "the chain needs VL and SA tokens")
-        # VL rows padded to whole 32-row packed blocks; N = padded token count of the joint attention
+        self.phys = cfg.use_physics and cfg.n_physics > 0
+        Fn._require(cfg.n_physics == 0 or cfg.use_physics, "physics tokens need the P-stream parameters")
+        # joint sequence: [VL padded to 32 | SA (padded to 32 with a P stream) | P]
         self.nv = _round_up(cfg.n_vl, 32)
-        self.N = self.nv + cfg.n_sa
+        self.ns = _round_up(cfg.n_sa, 32) if self.phys else cfg.n_sa
+        self.np_ = cfg.n_physics if self.phys else 0
+        self.p0 = self.nv + self.ns                  # first P row
+        self.N = self.p0 + self.np_
+        self.nx = self.nv + cfg.n_sa                 # rows of the single-stream x = [VL->SA | time | SA]
         self.vl_mask = vl_mask
-        self.masked = vl_mask or self.nv != cfg.n_vl
+        self.masked = vl_mask or self.nv != cfg.n_vl or self.phys
         for k, shape in cfg.param_shapes().items():
             Fn._require(k in sd, f"missing parameter {k}")
             Fn._require(tuple(sd[k].shape) == tuple(shape), f"{k}: shape {tuple(sd[k].shape)}, expected {shape}")
-        w = {k: sd[k].to(device=self.dev, dtype=BF16).contiguous() for k in cfg.param_shapes()}
+        names = cfg.param_shapes() if self.phys else {k: v for k, v in cfg.param_shapes().items()
+                                                      if k not in cfg.physics_param_shapes()}
+        w = {k: sd[k].to(device=self.dev, dtype=BF16).contiguous() for k in names}
         self.w = w
         self.sa_ffn_p, self.vl_ffn_p = _round_up(cfg.sa_ffn, 128), _round_up(cfg.vl_ffn, 128)
         for dim in (cfg.sa_dim, cfg.vl_dim, inner, cfg.ss_expanded, cfg.ss_hidden + inner, cfg.output_dim):
@@ -264,70 +319,105 @@ class RldxMsat:
             bp = torch.cat([_pad_rows(gb[:, None], ffn_p)[:, 0], _pad_rows(ub[:, None], ffn_p)[:, 0]])
             return Fn.pack_weight(wp, swiglu_pairs=True), bp.contiguous()
 
+        streams = ("sa", "vl", "p") if self.phys else ("sa", "vl")
         self.ds = []
         for b in range(cfg.ds_blocks):
             p = f"double_blocks.{b}."
-            blk = {n: w[p + n] for n in ("q_norm_sa.weight", "k_norm_sa.weight", "q_norm_vl.weight",
-                                          "k_norm_vl.weight", "sa_qkv.bias", "vl_qkv.bias", "sa_proj.bias",
-                                          "vl_proj.bias", "sa_mlp.w3.bias", "vl_mlp.w3.bias")}
-            for n in ("sa_qkv", "vl_qkv", "sa_proj", "vl_proj"):
-                blk[n] = Fn.pack_weight(w[p + n + ".weight"])
-            blk["sa_w12"], blk["sa_w12.bias"] = swiglu_w(w[p + "sa_mlp.w12.weight"], w[p + "sa_mlp.w12.bias"],
-                                                          cfg.sa_ffn, self.sa_ffn_p)
-            blk["vl_w12"], blk["vl_w12.bias"] = swiglu_w(w[p + "vl_mlp.w12.weight"], w[p + "vl_mlp.w12.bias"],
-                                                          cfg.vl_ffn, self.vl_ffn_p)
-            blk["sa_w3"] = Fn.pack_weight(_pad_cols(w[p + "sa_mlp.w3.weight"], self.sa_ffn_p))
-            blk["vl_w3"] = Fn.pack_weight(_pad_cols(w[p + "vl_mlp.w3.weight"], self.vl_ffn_p))
+            blk = {}
+            for st in streams:
+                ffn, ffn_p = (cfg.vl_ffn, self.vl_ffn_p) if st == "vl" else (cfg.sa_ffn, self.sa_ffn_p)
+                for n in ("q_norm", "k_norm"):
+                    blk[f"{n}_{st}.weight"] = w[f"{p}{n}_{st}.weight"]
+                for n in ("qkv", "proj"):
+                    blk[f"{st}_{n}"] = Fn.pack_weight(w[f"{p}{st}_{n}.weight"])
+                    blk[f"{st}_{n}.bias"] = w[f"{p}{st}_{n}.bias"]
+                blk[f"{st}_w12"], blk[f"{st}_w12.bias"] = swiglu_w(w[f"{p}{st}_mlp.w12.weight"],
+                                                                  w[f"{p}{st}_mlp.w12.bias"], ffn, ffn_p)
+                blk[f"{st}_w3"] = Fn.pack_weight(_pad_cols(w[f"{p}{st}_mlp.w3.weight"], ffn_p))
+                blk[f"{st}_mlp.w3.bias"] = w[f"{p}{st}_mlp.w3.bias"]
             self.ds.append(blk)
         self.ss = []
-        e = cfg.ss_expanded
         for b in range(cfg.ss_blocks):
             p = f"single_blocks.{b}."
-            w1, b1 = w[p + "linear1.weight"], w[p + "linear1.bias"]
-            blk = {"q_norm": w[p + "q_norm.weight"], "k_norm": w[p + "k_norm.weight"],
-                   "qkv": Fn.pack_weight(w1[: 3 * inner].contiguous()), "qkv.bias": b1[: 3 * inner].contiguous(),
-                   "mlp": Fn.pack_weight(w1[3 * inner:].contiguous(), swiglu_pairs=True),
-                   "mlp.bias": b1[3 * inner:].contiguous(),
-                   "mlp_proj": Fn.pack_weight(w[p + "mlp_proj.weight"]), "mlp_proj.bias": w[p + "mlp_proj.bias"],
-                   "linear2": Fn.pack_weight(w[p + "linear2.weight"]), "linear2.bias": w[p + "linear2.bias"]}
+            blk = {}
+            for pre in (("", "p_") if self.phys else ("",)):
+                w1, b1 = w[f"{p}{pre}linear1.weight"], w[f"{p}{pre}linear1.bias"]
+                blk.update({f"{pre}q_norm": w[f"{p}{pre}q_norm.weight"], f"{pre}k_norm": w[f"{p}{pre}k_norm.weight"],
+                            f"{pre}qkv": Fn.pack_weight(w1[: 3 * inner].contiguous()),
+                            f"{pre}qkv.bias": b1[: 3 * inner].contiguous(),
+                            f"{pre}mlp": Fn.pack_weight(w1[3 * inner:].contiguous(), swiglu_pairs=True),
+                            f"{pre}mlp.bias": b1[3 * inner:].contiguous(),
+                            f"{pre}mlp_proj": Fn.pack_weight(w[f"{p}{pre}mlp_proj.weight"]),
+                            f"{pre}mlp_proj.bias": w[f"{p}{pre}mlp_proj.bias"],
+                            f"{pre}linear2": Fn.pack_weight(w[f"{p}{pre}linear2.weight"]),
+                            f"{pre}linear2.bias": w[f"{p}{pre}linear2.bias"]})
             self.ss.append(blk)
         self.vl_proj_to_sa = Fn.pack_weight(w["vl_proj_to_sa.weight"])
         self.proj_out_2 = Fn.pack_weight(w["proj_out_2.weight"])
         # RoPE: DS rows [time | SA] at axis-1 positions 0 .. n_sa - 1; SS rows [time | SA]
-        # at 0 and num_temb + 1 ... (custom_msat_chain.py:81-105, the eager ids of msat.py:376-487)
+        # at 0 and num_temb + 1 ... (custom_msat_chain.py:81-105, the eager ids of msat.py:376-487);
+        # P rows at axis 0 = 1, axis 1 = 0 .. n_p - 1 in both (custom_expanded_msat_chain.py:44-85,
+        # msat.py:630-632, :706-710).  Tables of padding rows: cos 1, sin 0 (their Q/K are zero).
         nt = cfg.num_temb_tokens
         ds_pos = torch.arange(cfg.n_sa)
         ss_pos = torch.cat([torch.arange(nt), torch.arange(nt + 1, nt + 1 + cfg.n_sa_pure)])
-        self.ds_cos, self.ds_sin = (t.to(self.dev) for t in rope_tables(cfg, ds_pos, bf16_quirk))
-        self.ss_cos, self.ss_sin = (t.to(self.dev) for t in rope_tables(cfg, ss_pos, bf16_quirk))
+
+        def tables(pos, axis0=0, rows=None):
+            c, sn = rope_tables(cfg, pos, bf16_quirk, axis0)
+            if rows is not None and rows > c.shape[0]:
+                c = torch.cat([c, torch.ones(rows - c.shape[0], c.shape[1])])
+                sn = torch.cat([sn, torch.zeros(rows - sn.shape[0], sn.shape[1])])
+            return c.contiguous().to(self.dev), sn.contiguous().to(self.dev)
+
+        self.ds_cos, self.ds_sin = tables(ds_pos, rows=self.ns)
+        self.ss_cos, self.ss_sin = tables(ss_pos, rows=self.ns)
+        if self.phys:
+            self.p_cos, self.p_sin = tables(torch.arange(self.np_), axis0=1)
         # activations
-        N, nv, ns = self.N, self.nv, cfg.n_sa
+        N, nv, ns, nx, npp = self.N, self.nv, cfg.n_sa, self.nx, self.np_
         ebuf = lambda *s: torch.empty(*s, dtype=BF16, device=self.dev)  # noqa: E731
         self.x_sa, self.x_vl = ebuf(ns, cfg.sa_dim), ebuf(nv, cfg.vl_dim)
         self.h_sa, self.h_vl = Fn.PackedAct.empty(ns, cfg.sa_dim, self.dev), Fn.PackedAct.empty(nv, cfg.vl_dim,
                                                                                                  self.dev)
-        self.qkv_sa, self.qkv_vl = ebuf(ns, 3 * inner), ebuf(nv, 3 * inner)
+        # QKV rows of SA: self.ns rows, the GEMM writes the first n_sa, padding rows stay zero
+        self.qkv_sa_buf = torch.zeros(self.ns, 3 * inner, dtype=BF16, device=self.dev)
+        self.qkv_sa, self.qkv_vl = self.qkv_sa_buf[:ns], ebuf(nv, 3 * inner)
         self.q = ebuf(H, N, D)
         self.kvp = ebuf(H, Fn.kv_packed_elems(N, D))
         self.att = Fn.PackedAct.empty(N, inner, self.dev)
         self.gl_sa = Fn.PackedAct.empty(ns, self.sa_ffn_p, self.dev)
         self.gl_vl = Fn.PackedAct.empty(nv, self.vl_ffn_p, self.dev)
         self.vl_packed = Fn.PackedAct.empty(nv, cfg.vl_dim, self.dev)
-        self.x = ebuf(N, cfg.sa_dim)
-        self.h = Fn.PackedAct.empty(N, cfg.sa_dim, self.dev)
-        self.qkv = ebuf(N, 3 * inner)
-        self.gl = Fn.PackedAct.empty(N, e, self.dev)
+        self.x = ebuf(nx, cfg.sa_dim)
+        self.h = Fn.PackedAct.empty(nx, cfg.sa_dim, self.dev)
+        self.qkv_buf = torch.zeros(nv + self.ns, 3 * inner, dtype=BF16, device=self.dev)
+        self.qkv = self.qkv_buf[:nx]
+        self.gl = Fn.PackedAct.empty(nx, cfg.ss_expanded, self.dev)
         self.cat = Fn.PackedAct.empty(N, inner + cfg.ss_hidden, self.dev)
         self.mod = ebuf(cfg.n_sa_pure, cfg.sa_dim)
         self.mod_packed = Fn.PackedAct.empty(cfg.n_sa_pure, cfg.sa_dim, self.dev)
         self.out = ebuf(1, cfg.n_sa_pure, cfg.output_dim)
         self.inputs = dict(sa=ebuf(1, cfg.n_sa_pure, cfg.sa_dim), vl=ebuf(1, cfg.n_vl, cfg.vl_dim),
                            temb=ebuf(1, inner), time_token=ebuf(1, nt, cfg.sa_dim))
+        if self.phys:
+            self.x_p = ebuf(npp, cfg.sa_dim)
+            self.h_p = Fn.PackedAct.empty(npp, cfg.sa_dim, self.dev)
+            self.qkv_p = ebuf(npp, 3 * inner)
+            self.gl_p = Fn.PackedAct.empty(npp, self.sa_ffn_p, self.dev)
+            self.gl_p_ss = Fn.PackedAct.empty(npp, cfg.ss_expanded, self.dev)
+            self.mod_p = ebuf(npp, cfg.sa_dim)
+            self.mod_p_packed = Fn.PackedAct.empty(npp, cfg.sa_dim, self.dev)
+            self.out_p = ebuf(1, npp, cfg.output_dim)
+            self.proj_out_physics_2 = Fn.pack_weight(w["proj_out_physics_2.weight"])
+            self.inputs["p"] = ebuf(1, npp, cfg.sa_dim)
         if vl_mask:
             self.inputs["vl_mask"] = torch.ones(1, cfg.n_vl, dtype=torch.float32, device=self.dev)
-        # additive key bias over the N attention rows: 0, or -inf on padding and masked VL keys
+            if self.phys:
+                self.inputs["physics_mask"] = torch.ones(1, dtype=torch.float32, device=self.dev)
+        # additive key bias over the N attention rows: 0, or -inf on padding, masked VL and masked P keys
         self.key_bias = torch.zeros(N, dtype=torch.float32, device=self.dev)
         self.key_bias[cfg.n_vl:nv] = float("-inf")
+        self.key_bias[nv + ns:self.p0] = float("-inf")
         self._ninf = torch.full((), float("-inf"), dtype=torch.float32, device=self.dev)
         self._zero = torch.zeros((), dtype=torch.float32, device=self.dev)
         self.graph = None
@@ -336,28 +426,32 @@ class RldxMsat:
         self.ss_gemms = [self._ss_gemm_items(blk) for blk in self.ss]
         self.vl_proj_gemm = self._planned(
             [(self.vl_packed, self.vl_proj_to_sa, self.w["vl_proj_to_sa.bias"], self.x[:nv], None)], "bias")
-        self.out_gemm = self._planned(
-            [(self.mod_packed, self.proj_out_2, self.w["proj_out_2.bias"], self.out[0], None)], "bias")
+        out_items = [(self.mod_packed, self.proj_out_2, self.w["proj_out_2.bias"], self.out[0], None)]
+        if self.phys:
+            out_items.append((self.mod_p_packed, self.proj_out_physics_2, self.w["proj_out_physics_2.bias"],
+                              self.out_p[0], None))
+        self.out_gemm = self._planned(out_items, "bias")
         plans = [g for d in self.ds_gemms + self.ss_gemms for g in d.values()] + [self.vl_proj_gemm, self.out_gemm]
         self.ws = Fn.GemmWorkspace(max(Fn.grouped_gemm_workspace_bytes(it, epi, sk, wide) for it, epi, sk, wide in plans),
                                    self.dev)
 
     @staticmethod
-    def split_for(m: int, n: int, k: int) -> int:
-        """Split-K factor for a launch: the 82-, 64- and 18-row GEMMs of this
-        model have 24-344 output tiles; where K is long (>= 4096) a tile
-        streams a long slice of K on one CU, and splitting K by the largest
-        power of two <= min(8, K / 1024) that keeps tiles x split <= 256 (one
-        workgroup per CU) pays; with shorter K the partial-sum traffic costs
-        more than the added workgroups gain.  Measured per GEMM at the release
-        shape (us per launch, weights streaming from HBM, split 1 / chosen):
-        vl_qkv 15.3 / 12.7, sa_w3 11.7 / 9.1, vl_w3 52.1 / 23.9, mlp_proj
-        26.3 / 19.3, linear2 17.1 / 11.1; the short-K GEMMs were fastest
-        unsplit.  Tiles as the planner cuts them: 32 x 64 for up to 32 rows,
-        else 64 x 64."""
+    def split_for(m, n: int, k: int) -> int:
+        """Split-K factor for a launch (m: the rows of each group, or one int):
+        the 82-, 64- and 18-row GEMMs of this model have 24-344 output tiles;
+        where K is long (>= 4096) a tile streams a long slice of K on one CU,
+        and splitting K by the largest power of two <= min(8, K / 1024) that
+        keeps tiles x split <= 256 (one workgroup per CU) pays; with shorter K
+        the partial-sum traffic costs more than the added workgroups gain.
+        Measured per GEMM at the release shape (us per launch, weights
+        streaming from HBM, split 1 / chosen): vl_qkv 15.3 / 12.7, sa_w3 11.7 /
+        9.1, vl_w3 52.1 / 23.9, mlp_proj 26.3 / 19.3, linear2 17.1 / 11.1; the
+        short-K GEMMs were fastest unsplit.  Tiles as the planner cuts them:
+        32 x 64 for up to 32 rows, else 64 x 64, summed over the groups."""
         if k < 4096:
             return 1
-        tiles = ((m + 31) // 32 if m <= 32 else (m + 63) // 64) * (n // 64)
+        ms = [m] if isinstance(m, int) else list(m)
+        tiles = sum(((r + 31) // 32 if r <= 32 else (r + 63) // 64) for r in ms) * (n // 64)
         split = 1
         while split < 8 and split * 2 <= k // 1024 and tiles * split * 2 <= 256:
             split *= 2
@@ -373,24 +467,34 @@ class RldxMsat:
         return epi.startswith("swiglu") and n >= 12288 and split == 1
 
     def _planned(self, items, epi):
-        a, w = items[0][0], items[0][1]
-        split = self.split_for(a.m, w.n, w.k)
+        w = items[0][1]
+        split = self.split_for([it[0].m for it in items], w.n, w.k)
         return (items, epi, split, self.wide_for(w.n, epi, split))
 
     def _ds_gemm_items(self, blk: dict) -> dict:
-        nv, N = self.nv, self.N
+        nv, ns, p0, N = self.nv, self.cfg.n_sa, self.p0, self.N
+
+        def grp(sa_item, p_item):
+            return [sa_item, p_item] if self.phys else [sa_item]
+
+        P = self.phys
         return {
-            "sa_qkv": self._planned([(self.h_sa, blk["sa_qkv"], blk["sa_qkv.bias"], self.qkv_sa, None)], "bias"),
+            "sa_qkv": self._planned(grp((self.h_sa, blk["sa_qkv"], blk["sa_qkv.bias"], self.qkv_sa, None),
+                                        P and (self.h_p, blk["p_qkv"], blk["p_qkv.bias"], self.qkv_p, None)), "bias"),
             "vl_qkv": self._planned([(self.h_vl, blk["vl_qkv"], blk["vl_qkv.bias"], self.qkv_vl, None)], "bias"),
-            "sa_proj": self._planned([(self.att.rows(nv, N), blk["sa_proj"], blk["sa_proj.bias"], self.x_sa,
-                                       self.x_sa)], "residual"),
+            "sa_proj": self._planned(grp((self.att.rows(nv, nv + ns), blk["sa_proj"], blk["sa_proj.bias"], self.x_sa,
+                                          self.x_sa),
+                                         P and (self.att.rows(p0, N), blk["p_proj"], blk["p_proj.bias"], self.x_p,
+                                                self.x_p)), "residual"),
             "vl_proj": self._planned([(self.att.rows(0, nv), blk["vl_proj"], blk["vl_proj.bias"], self.x_vl,
                                        self.x_vl)], "residual"),
-            "sa_w12": self._planned([(self.h_sa, blk["sa_w12"], blk["sa_w12.bias"], self.gl_sa, None)],
+            "sa_w12": self._planned(grp((self.h_sa, blk["sa_w12"], blk["sa_w12.bias"], self.gl_sa, None),
+                                        P and (self.h_p, blk["p_w12"], blk["p_w12.bias"], self.gl_p, None)),
                                     "swiglu_packed"),
             "vl_w12": self._planned([(self.h_vl, blk["vl_w12"], blk["vl_w12.bias"], self.gl_vl, None)],
                                     "swiglu_packed"),
-            "sa_w3": self._planned([(self.gl_sa, blk["sa_w3"], blk["sa_mlp.w3.bias"], self.x_sa, self.x_sa)],
+            "sa_w3": self._planned(grp((self.gl_sa, blk["sa_w3"], blk["sa_mlp.w3.bias"], self.x_sa, self.x_sa),
+                                       P and (self.gl_p, blk["p_w3"], blk["p_mlp.w3.bias"], self.x_p, self.x_p)),
                                    "residual"),
             "vl_w3": self._planned([(self.gl_vl, blk["vl_w3"], blk["vl_mlp.w3.bias"], self.x_vl, self.x_vl)],
                                    "residual"),
@@ -398,12 +502,26 @@ class RldxMsat:
 
     def _ss_gemm_items(self, blk: dict) -> dict:
         inner, hs = self.cfg.inner, self.cfg.ss_hidden
+        nx, p0, N = self.nx, self.p0, self.N
+        cx, cp = self.cat.rows(0, nx), (self.cat.rows(p0, N) if self.phys else None)
+
+        def grp(x_item, p_item):
+            return [x_item, p_item] if self.phys else [x_item]
+
+        P = self.phys
         return {
-            "qkv": self._planned([(self.h, blk["qkv"], blk["qkv.bias"], self.qkv, None)], "bias"),
-            "mlp": self._planned([(self.h, blk["mlp"], blk["mlp.bias"], self.gl, None)], "swiglu_packed"),
-            "mlp_proj": self._planned([(self.gl, blk["mlp_proj"], blk["mlp_proj.bias"], self.cat.cols(inner, inner + hs),
-                                        None)], "bias_packed"),
-            "linear2": self._planned([(self.cat, blk["linear2"], blk["linear2.bias"], self.x, self.x)], "residual"),
+            "qkv": self._planned(grp((self.h, blk["qkv"], blk["qkv.bias"], self.qkv, None),
+                                     P and (self.h_p, blk["p_qkv"], blk["p_qkv.bias"], self.qkv_p, None)), "bias"),
+            "mlp": self._planned(grp((self.h, blk["mlp"], blk["mlp.bias"], self.gl, None),
+                                     P and (self.h_p, blk["p_mlp"], blk["p_mlp.bias"], self.gl_p_ss, None)),
+                                 "swiglu_packed"),
+            "mlp_proj": self._planned(grp((self.gl, blk["mlp_proj"], blk["mlp_proj.bias"], cx.cols(inner, inner + hs),
+                                           None),
+                                          P and (self.gl_p_ss, blk["p_mlp_proj"], blk["p_mlp_proj.bias"],
+                                                 cp.cols(inner, inner + hs), None)), "bias_packed"),
+            "linear2": self._planned(grp((cx, blk["linear2"], blk["linear2.bias"], self.x, self.x),
+                                         P and (cp, blk["p_linear2"], blk["p_linear2.bias"], self.x_p, self.x_p)),
+                                     "residual"),
         }
 
     def _gemm(self, plan) -> None:
@@ -419,17 +537,24 @@ class RldxMsat:
         N = self.N
         Fn.layernorm_pack(self.x_sa, cfg.eps, out=self.h_sa)
         Fn.layernorm_pack(self.x_vl, cfg.eps, out=self.h_vl)
+        if self.phys:
+            Fn.layernorm_pack(self.x_p, cfg.eps, out=self.h_p)
         self._gemm(gm["sa_qkv"])
         self._gemm(gm["vl_qkv"])
         specs = [Fn.StreamSpec(self.qkv_vl, blk["q_norm_vl.weight"], blk["k_norm_vl.weight"]),
-                 Fn.StreamSpec(self.qkv_sa, blk["q_norm_sa.weight"], blk["k_norm_sa.weight"], self.ds_cos,
+                 Fn.StreamSpec(self.qkv_sa_buf, blk["q_norm_sa.weight"], blk["k_norm_sa.weight"], self.ds_cos,
                                self.ds_sin)]
+        if self.phys:
+            specs.append(Fn.StreamSpec(self.qkv_p, blk["q_norm_p.weight"], blk["k_norm_p.weight"], self.p_cos,
+                                       self.p_sin))
         Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
         Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), N, key_bias=self._kb(), out=self.att)
         self._gemm(gm["sa_proj"])
         self._gemm(gm["vl_proj"])
         Fn.layernorm_pack(self.x_sa, cfg.eps, out=self.h_sa)
         Fn.layernorm_pack(self.x_vl, cfg.eps, out=self.h_vl)
+        if self.phys:
+            Fn.layernorm_pack(self.x_p, cfg.eps, out=self.h_p)
         self._gemm(gm["sa_w12"])
         self._gemm(gm["vl_w12"])
         self._gemm(gm["sa_w3"])
@@ -439,10 +564,14 @@ class RldxMsat:
         cfg = self.cfg
         nv, N, inner = self.nv, self.N, cfg.inner
         Fn.layernorm_pack(self.x, cfg.eps, out=self.h)
+        if self.phys:
+            Fn.layernorm_pack(self.x_p, cfg.eps, out=self.h_p)
         self._gemm(gm["qkv"])
         self._gemm(gm["mlp"])
-        specs = [Fn.StreamSpec(self.qkv[:nv], blk["q_norm"], blk["k_norm"]),
-                 Fn.StreamSpec(self.qkv[nv:], blk["q_norm"], blk["k_norm"], self.ss_cos, self.ss_sin)]
+        specs = [Fn.StreamSpec(self.qkv_buf[:nv], blk["q_norm"], blk["k_norm"]),
+                 Fn.StreamSpec(self.qkv_buf[nv:nv + self.ns], blk["q_norm"], blk["k_norm"], self.ss_cos, self.ss_sin)]
+        if self.phys:
+            specs.append(Fn.StreamSpec(self.qkv_p, blk["p_q_norm"], blk["p_k_norm"], self.p_cos, self.p_sin))
         Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
         Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), N, key_bias=self._kb(),
                             out=self.cat.cols(0, inner))
@@ -451,34 +580,56 @@ class RldxMsat:
 
     # -- forward --------------------------------------------------------------
     def forward(self, hidden_states: torch.Tensor, encoder_hidden_states: torch.Tensor, temb: torch.Tensor,
-                time_token: torch.Tensor, encoder_attention_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+                time_token: torch.Tensor, encoder_attention_mask: Optional[torch.Tensor] = None,
+                physics_embs: Optional[torch.Tensor] = None, physics_attention_mask: Optional[torch.Tensor] = None):
         """CustomOpMSAT.forward (custom_msat_chain.py:109-126): hidden_states
         [1, n_sa_pure, sa_dim], encoder_hidden_states [1, n_vl, vl_dim], temb
         [1, inner], time_token [1, num_temb_tokens, sa_dim] -> [1, n_sa_pure,
         output_dim] (a static buffer, overwritten by the next call).
         encoder_attention_mask [1, n_vl] (1 = visible, 0 = masked; a chain built
         with vl_mask=True): masks VL keys in every block as the eager MSAT does
-        (msat.py:517-531, blocks.py:558-575); None = every VL token visible."""
+        (msat.py:517-531, blocks.py:558-575); None = every VL token visible.
+        With a P stream (CustomOpExpandedMSAT.forward,
+        custom_expanded_msat_chain.py:87-115): physics_embs [1, n_physics,
+        sa_dim] is required and the result is {"action": [1, n_sa_pure,
+        output_dim], "physics": [1, n_physics, output_dim]};
+        physics_attention_mask [1] (1 = visible; a chain built with
+        vl_mask=True) masks every P key (msat.py:716-743)."""
         cfg = self.cfg
         nt, nv = cfg.num_temb_tokens, cfg.n_vl
         Fn._require(tuple(hidden_states.shape) == (1, cfg.n_sa_pure, cfg.sa_dim) and
                     tuple(encoder_hidden_states.shape) == (1, nv, cfg.vl_dim) and
                     tuple(temb.shape) == (1, cfg.inner) and tuple(time_token.shape) == (1, nt, cfg.sa_dim),
                     "input shapes do not match the chain's configuration (batch 1)")
+        if self.phys:
+            Fn._require(physics_embs is not None and tuple(physics_embs.shape) == (1, self.np_, cfg.sa_dim),
+                        "physics_embs must be [1, n_physics, sa_dim] for a chain with a P stream")
+        else:
+            Fn._require(physics_embs is None and physics_attention_mask is None,
+                        "physics inputs need a chain built with use_physics and n_physics > 0")
         if self.vl_mask:
             if encoder_attention_mask is None:
                 self.key_bias[:nv].zero_()
             else:
                 Fn._require(tuple(encoder_attention_mask.shape) == (1, nv), "encoder_attention_mask must be [1, n_vl]")
                 torch.where(encoder_attention_mask[0] == 0, self._ninf, self._zero, out=self.key_bias[:nv])
+            if self.phys:
+                if physics_attention_mask is None:
+                    self.key_bias[self.p0:].zero_()
+                else:
+                    Fn._require(physics_attention_mask.numel() == 1, "physics_attention_mask must be [1]")
+                    torch.where(physics_attention_mask.reshape(1).expand(self.np_) == 0, self._ninf, self._zero,
+                                out=self.key_bias[self.p0:])
         else:
-            Fn._require(encoder_attention_mask is None,
-                        "encoder_attention_mask needs a chain built with vl_mask=True")
+            Fn._require(encoder_attention_mask is None and physics_attention_mask is None,
+                        "attention masks need a chain built with vl_mask=True")
         self.x_sa[:nt].copy_(time_token[0])
         self.x_sa[nt:].copy_(hidden_states[0])
         self.x_vl[:nv].copy_(encoder_hidden_states[0])
         if self.nv > nv:
             self.x_vl[nv:].zero_()
+        if self.phys:
+            self.x_p.copy_(physics_embs[0])
         for blk, gm in zip(self.ds, self.ds_gemms):
             self._ds_block(blk, gm)
         # x = [vl_proj_to_sa(vl) | time token | SA]
@@ -487,23 +638,33 @@ class RldxMsat:
         self.x[self.nv:].copy_(self.x_sa)
         for blk, gm in zip(self.ss, self.ss_gemms):
             self._ss_block(blk, gm)
-        # AdaLN output projection (msat.py:777-781)
-        shift, scale = F.linear(F.silu(temb), self.w["proj_out_1.weight"], self.w["proj_out_1.bias"]).chunk(2, dim=1)
-        sa = F.layer_norm(self.x[self.N - cfg.n_sa_pure:], (cfg.sa_dim,), eps=1e-6)
+        # AdaLN output projections (msat.py:771-781)
+        silu_t = F.silu(temb)
+        shift, scale = F.linear(silu_t, self.w["proj_out_1.weight"], self.w["proj_out_1.bias"]).chunk(2, dim=1)
+        sa = F.layer_norm(self.x[self.nx - cfg.n_sa_pure:], (cfg.sa_dim,), eps=1e-6)
         torch.add(sa * (1 + scale), shift, out=self.mod)
         Fn.pack_act(self.mod, out=self.mod_packed)
+        if self.phys:
+            pshift, pscale = F.linear(silu_t, self.w["proj_out_physics_1.weight"],
+                                      self.w["proj_out_physics_1.bias"]).chunk(2, dim=1)
+            ph = F.layer_norm(self.x_p, (cfg.sa_dim,), eps=1e-6)
+            torch.add(ph * (1 + pscale), pshift, out=self.mod_p)
+            Fn.pack_act(self.mod_p, out=self.mod_p_packed)
         self._gemm(self.out_gemm)
+        if self.phys:
+            return {"action": self.out, "physics": self.out_p}
         return self.out
 
     __call__ = forward
 
     def _forward_static(self):
         i = self.inputs
-        return self.forward(i["sa"], i["vl"], i["temb"], i["time_token"], i.get("vl_mask"))
+        return self.forward(i["sa"], i["vl"], i["temb"], i["time_token"], i.get("vl_mask"), i.get("p"),
+                            i.get("physics_mask"))
 
     def capture(self, warmup: int = 2) -> None:
         """Record forward() on the static `inputs` buffers (with the `vl_mask`
-        buffer when built with vl_mask=True) into one hipGraph."""
+        and `physics_mask` buffers when built with vl_mask=True) into one hipGraph."""
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -516,9 +677,9 @@ class RldxMsat:
             self._forward_static()
         torch.cuda.synchronize()
 
-    def replay(self) -> torch.Tensor:
+    def replay(self):
         self.graph.replay()
-        return self.out
+        return {"action": self.out, "physics": self.out_p} if self.phys else self.out
 
 
 class MsatDispatcher:
@@ -533,14 +694,17 @@ class MsatDispatcher:
       timestep_encoder / time_token_proj, copy every input into the chain's
       static buffers and run (or replay) the chain;
     * calls the chain does not serve go to the module's own forward:
-      return_all_hidden_states=True, physics tokens on a physics-enabled module,
-      a batch other than 1, or token counts other than the chain's (shape
-      drift would corrupt the static buffers);
+      return_all_hidden_states=True, a batch other than 1, or token counts
+      (VL, SA or physics) other than the chain's (shape drift would corrupt
+      the static buffers);
     * a failure while building or running switches the dispatcher to the
       module's own forward for good, as the reference does.
-    encoder_attention_mask is served: the chain is built with vl_mask=True.
-    The returned tensor is the chain's static output buffer, overwritten by the
-    next call."""
+    encoder_attention_mask and physics_attention_mask are served: the chain is
+    built with vl_mask=True.  Physics tokens on a physics-enabled module are
+    served by the all-add-ons chain (the first call's physics token count),
+    which returns {"action", "physics"} as the eager _forward_physics does.
+    The returned tensors are the chain's static output buffers, overwritten by
+    the next call."""
 
     def __init__(self, msat: torch.nn.Module, bf16_quirk: Optional[bool] = None, graph: bool = False,
                  verbose: bool = False):
@@ -555,14 +719,14 @@ class MsatDispatcher:
         if self.verbose:
             print(f"[rldx_amd.MsatDispatcher] {msg}", flush=True)
 
-    def build(self, n_vl: int, n_sa_pure: int) -> RldxMsat:
+    def build(self, n_vl: int, n_sa_pure: int, n_physics: int = 0) -> RldxMsat:
         msat = self.msat
         sd = {k: v for k, v in msat.state_dict().items()}
         rope = getattr(msat, "rope_embedder", None)
         quirk = self.bf16_quirk
         if quirk is None:
             quirk = rope is not None and not getattr(rope, "freqs_cis_0").is_complex()
-        overrides = dict(n_vl=n_vl, n_sa_pure=n_sa_pure)
+        overrides = dict(n_vl=n_vl, n_sa_pure=n_sa_pure, n_physics=n_physics)
         if rope is not None:
             overrides.update(rope_theta=float(rope.theta), max_seq_len=int(rope.max_seq_len))
         cfg = RldxMsatCfg.from_state_dict(sd, **overrides)
@@ -577,14 +741,22 @@ class MsatDispatcher:
                   physics_attention_mask) -> Optional[str]:
         if return_all_hidden_states:
             return "return_all_hidden_states"
-        if getattr(self.msat, "use_physics", False) and physics_embs is not None:
-            return "physics tokens"
         if hidden_states.dim() != 3 or hidden_states.shape[0] != 1 or encoder_hidden_states.shape[0] != 1:
             return "batch other than 1"
+        if physics_embs is not None and physics_embs.shape[0] != 1:
+            return "batch other than 1"
         c = self.chain
-        if c is not None and (encoder_hidden_states.shape[1] != c.cfg.n_vl or hidden_states.shape[1] != c.cfg.n_sa_pure):
+        if c is not None and (encoder_hidden_states.shape[1] != c.cfg.n_vl or hidden_states.shape[1] != c.cfg.n_sa_pure
+                              or self._n_physics(physics_embs) != c.np_):
             return "token counts differ from the chain's"
         return None
+
+    def _n_physics(self, physics_embs) -> int:
+        """P tokens the eager forward would use: the physics path runs only on a
+        physics-enabled module given physics_embs (msat.py:351-363)."""
+        if physics_embs is None or not getattr(self.msat, "use_physics", False):
+            return 0
+        return int(physics_embs.shape[1])
 
     def __call__(self, hidden_states, encoder_hidden_states, timestep=None, return_all_hidden_states=False,
                  encoder_attention_mask=None, physics_embs=None, physics_attention_mask=None):
@@ -603,7 +775,7 @@ class MsatDispatcher:
             out = self.orig(*args)
             self.fallbacks += 1
             try:
-                self.build(encoder_hidden_states.shape[1], hidden_states.shape[1])
+                self.build(encoder_hidden_states.shape[1], hidden_states.shape[1], self._n_physics(physics_embs))
             except Exception as e:  # noqa: BLE001 — any build failure means the module's own forward from now on
                 self.failed = True
                 self._log(f"build failed ({e}); the module's own forward serves every call")
@@ -614,6 +786,7 @@ class MsatDispatcher:
             temb = msat.timestep_encoder(timestep)
             tt = msat.time_token_proj(temb).unsqueeze(1).repeat(1, c.cfg.num_temb_tokens, 1)
             mask = encoder_attention_mask
+            p_embs, p_mask = (physics_embs, physics_attention_mask) if c.phys else (None, None)
             if self.graph:
                 i = c.inputs
                 i["sa"].copy_(hidden_states)
@@ -624,9 +797,15 @@ class MsatDispatcher:
                     i["vl_mask"].fill_(1.0)
                 else:
                     i["vl_mask"].copy_(mask.reshape(1, -1))
+                if c.phys:
+                    i["p"].copy_(p_embs)
+                    if p_mask is None:
+                        i["physics_mask"].fill_(1.0)
+                    else:
+                        i["physics_mask"].copy_(p_mask.reshape(1))
                 out = c.replay()
             else:
-                out = c.forward(hidden_states, encoder_hidden_states, temb, tt, mask)
+                out = c.forward(hidden_states, encoder_hidden_states, temb, tt, mask, p_embs, p_mask)
             self.served += 1
             return out
         except Exception as e:  # noqa: BLE001 — as the reference: fall back for good on a hot-path failure
@@ -637,19 +816,21 @@ class MsatDispatcher:
 
 
 def install(msat: torch.nn.Module, n_vl: Optional[int] = None, n_sa_pure: Optional[int] = None,
-            bf16_quirk: Optional[bool] = None, graph: bool = False, verbose: bool = False) -> MsatDispatcher:
+            bf16_quirk: Optional[bool] = None, graph: bool = False, verbose: bool = False,
+            n_physics: int = 0) -> MsatDispatcher:
     """Route a live MSAT module's forward through an MsatDispatcher (what the
     reference's path-D dispatcher does with CustomOpMSAT,
     rldx/inference/serve_optimization.py:251-601).  With n_vl and n_sa_pure the
     chain is built now; without them, on the first call (served by the
-    module's own forward).  msat.forward keeps the reference signature
+    module's own forward); n_physics > 0 builds the all-add-ons chain for
+    that many physics tokens.  msat.forward keeps the reference signature
     forward(hidden_states, encoder_hidden_states, timestep,
     return_all_hidden_states, encoder_attention_mask, physics_embs,
     physics_attention_mask) (msat.py:1058-1082).  bf16_quirk=None detects it
     from the RoPE buffers (real-valued: the model was cast to bf16)."""
     d = MsatDispatcher(msat, bf16_quirk=bf16_quirk, graph=graph, verbose=verbose)
     if n_vl is not None and n_sa_pure is not None:
-        d.build(n_vl, n_sa_pure)
+        d.build(n_vl, n_sa_pure, n_physics)
     msat.forward = d
     msat.rldx_amd_dispatcher = d
     return d

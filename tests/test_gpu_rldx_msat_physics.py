@@ -1,0 +1,165 @@
+"""GPU parity of the all-add-ons RLDX-1 MSAT chain (RldxMsat with a physics
+stream: ExpandedDoubleStreamBlocks over [VL | SA | P], ExpandedSingleStreamBlocks
+over [VL+SA | P]) against the CPU oracle's MSAT._forward_physics restatement
+(oracle/rldx_msat_ref.py) on the same weights, at the reference's all-add-ons
+token counts (N_vl = 80, rldx/inference/action_model/README.md:28-37; 17
+physics tokens: 1 history + 16 future, physics_head.py:107-109)."""
+
+import pytest
+import torch
+
+from oracle import rldx_msat_ref as R
+from rldx_amd import rldx_msat as RM
+from tolerances import assert_bf16_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _cfg(**kw):
+    base = dict(n_vl=80, use_physics=True, n_physics=17)
+    base.update(kw)
+    return RM.RldxMsatCfg(**base)
+
+
+def _oracle(sd, inp, cfg, quirk=True, mask=None, pmask=None):
+    cpu = {k: v.cpu() for k, v in sd.items()}
+    return R.msat_forward_physics(cpu, inp["sa"].cpu(), inp["vl"].cpu(), inp["p"].cpu(), inp["temb"].cpu(),
+                                  inp["time_token"].cpu(), heads=cfg.heads, head_dim=cfg.head_dim,
+                                  ds_blocks=cfg.ds_blocks, ss_blocks=cfg.ss_blocks, theta=cfg.rope_theta,
+                                  max_seq_len=cfg.max_seq_len, bf16_quirk=quirk,
+                                  encoder_attention_mask=None if mask is None else mask.cpu(),
+                                  physics_attention_mask=None if pmask is None else pmask.cpu())
+
+
+def _run(chain, inp, mask=None, pmask=None):
+    o = chain.forward(inp["sa"], inp["vl"], inp["temb"], inp["time_token"], mask, inp["p"], pmask)
+    return o["action"].clone(), o["physics"].clone()
+
+
+def _rel(a, b):
+    return ((a - b).norm() / b.norm()).item()
+
+
+def _as_accurate_as_eager_bf16(outs, sd, inp, cfg, what, quirk=True, mask=None, pmask=None):
+    """Bound as for the no-add-ons chain: each output is no further from the
+    fp32 evaluation of the same weights and inputs than 1.5x the eager bf16
+    evaluation is, and its cosine to the bf16 oracle is >= 0.999."""
+    r16 = _oracle(sd, inp, cfg, quirk, mask, pmask)
+    sd32 = {k: v.float() for k, v in sd.items()}
+    inp32 = {k: v.float() for k, v in inp.items()}
+    r32 = _oracle(sd32, inp32, cfg, quirk, mask, pmask)
+    for name, o, a16, a32 in zip(("action", "physics"), outs, r16, r32):
+        o, a16, a32 = o.detach().cpu().double(), a16.double(), a32.double()
+        floor, got = _rel(a16, a32), _rel(o, a32)
+        cos = torch.nn.functional.cosine_similarity(o.flatten(), a16.flatten(), dim=0).item()
+        print(f"{what} / {name}: rel-L2 to fp32 {got:.2e} (eager bf16: {floor:.2e}), to the bf16 oracle "
+              f"{_rel(o, a16):.2e}, max-abs {(o - a16).abs().max().item():.3e}, cos {cos:.6f}")
+        assert torch.isfinite(o).all() and got <= 1.5 * floor and cos >= 0.999, f"{what} / {name}"
+
+
+@pytest.mark.parametrize("quirk", [True, False])
+def test_physics_msat_one_block_each(dev, quirk):
+    """1 Expanded DS + 1 Expanded SS block; the bf16 contract on both outputs
+    (output projections drawn with std 0.01, as for the no-add-ons test)."""
+    cfg = _cfg(ds_blocks=1, ss_blocks=1)
+    sd = RM.make_state_dict(cfg, dev, seed=121)
+    for k in ("proj_out_2.weight", "proj_out_physics_2.weight"):
+        sd[k] = (sd[k].float() * 0.5).to(torch.bfloat16)
+    inp = RM.make_inputs(cfg, dev, seed=122)
+    chain = RM.RldxMsat(sd, cfg, dev, bf16_quirk=quirk)
+    a, p = _run(chain, inp)
+    ra, rp = _oracle(sd, inp, cfg, quirk)
+    assert_bf16_close(a, ra, f"all-add-ons MSAT 1 + 1 action, quirk={quirk}")
+    assert_bf16_close(p, rp, f"all-add-ons MSAT 1 + 1 physics, quirk={quirk}")
+
+
+def test_physics_msat_full_model(dev):
+    """4 Expanded DS + 8 Expanded SS blocks at the release widths (1839.8 M
+    parameters), N_vl = 80, 17 physics tokens."""
+    cfg = _cfg()
+    sd = RM.make_state_dict(cfg, dev, seed=131)
+    inp = RM.make_inputs(cfg, dev, seed=132)
+    chain = RM.RldxMsat(sd, cfg, dev)
+    _as_accurate_as_eager_bf16(_run(chain, inp), sd, inp, cfg, "all-add-ons MSAT")
+
+
+def test_physics_msat_masks_in_graph_replay(dev):
+    """encoder_attention_mask and physics_attention_mask through the captured
+    graph: replays equal eager runs bit for bit, each matches the oracle with
+    the same masks, and a masked physics stream changes the action output."""
+    cfg = _cfg(ds_blocks=2, ss_blocks=2)
+    sd = RM.make_state_dict(cfg, dev, seed=141)
+    inp = RM.make_inputs(cfg, dev, seed=142)
+    chain = RM.RldxMsat(sd, cfg, dev, vl_mask=True)
+    chain.capture()
+    vmask = torch.ones(1, cfg.n_vl, device=dev)
+    vmask[:, 3:cfg.n_vl:4] = 0
+    cases = [(None, None), (vmask, None), (None, torch.zeros(1, device=dev)), (vmask, torch.ones(1, device=dev))]
+    outs = []
+    for mask, pmask in cases:
+        for k in ("sa", "vl", "temb", "time_token", "p"):
+            chain.inputs[k].copy_(inp[k])
+        chain.inputs["vl_mask"].copy_(torch.ones_like(vmask) if mask is None else mask)
+        chain.inputs["physics_mask"].fill_(1.0 if pmask is None else float(pmask.item()))
+        g = chain.replay()
+        got = (g["action"].clone(), g["physics"].clone())
+        torch.cuda.synchronize()
+        eager = _run(chain, inp, mask, pmask)
+        torch.cuda.synchronize()
+        for x, y in zip(got, eager):
+            assert torch.equal(x.view(torch.int16), y.view(torch.int16)), f"replay, masks {mask is not None}, {pmask}"
+        _as_accurate_as_eager_bf16(got, sd, inp, cfg, f"graph, vl mask {mask is not None}, physics mask {pmask}",
+                                   mask=mask, pmask=pmask)
+        outs.append(got)
+    assert (outs[2][0].float() - outs[0][0].float()).abs().max() > 1e-2, "the physics mask changed nothing"
+    assert (outs[1][0].float() - outs[0][0].float()).abs().max() > 1e-2, "the VL mask changed nothing"
+
+
+def test_dispatcher_serves_physics_calls(dev):
+    """A physics-enabled module tree (use_physics = True): the dispatcher builds
+    the all-add-ons chain from the first physics call and serves the later
+    ones (graph replay) with both masks; a call with another physics token
+    count, or none, goes to the module's own forward."""
+    cfg = _cfg(ds_blocks=1, ss_blocks=1, n_physics=9)
+    sd = RM.make_state_dict(cfg, dev, seed=151)
+    root = torch.nn.Module()
+    for k, v in sd.items():
+        *path, leaf = k.split(".")
+        m = root
+        for part in path:
+            if not hasattr(m, part):
+                m.add_module(part, torch.nn.Module())
+            m = getattr(m, part)
+        m.register_parameter(leaf, torch.nn.Parameter(v, requires_grad=False))
+    root.use_physics = True
+    g = torch.Generator(device=dev).manual_seed(152)
+    wt = (0.02 * torch.randn(cfg.inner, 1, generator=g, device=dev)).to(torch.bfloat16)
+    wtt = (0.02 * torch.randn(cfg.sa_dim, cfg.inner, generator=g, device=dev)).to(torch.bfloat16)
+    root.timestep_encoder = lambda t: (t[:, None].to(torch.bfloat16) @ wt.t())
+    root.time_token_proj = lambda temb: temb @ wtt.t()
+    calls = []
+
+    def own_forward(hidden_states, encoder_hidden_states, timestep=None, return_all_hidden_states=False,
+                    encoder_attention_mask=None, physics_embs=None, physics_attention_mask=None):
+        calls.append(physics_embs is None)
+        return None
+
+    root.forward = own_forward
+    d = RM.install(root, bf16_quirk=True, graph=True)
+    inp = RM.make_inputs(cfg, dev, seed=153)
+    t = torch.tensor([0.25], device=dev)
+    root(inp["sa"], inp["vl"], t, physics_embs=inp["p"])
+    assert d.chain is not None and d.chain.phys and d.chain.np_ == 9 and calls == [False]
+    temb = root.timestep_encoder(t)
+    ref = dict(inp, temb=temb, time_token=root.time_token_proj(temb).unsqueeze(1))
+    pmask = torch.zeros(1, device=dev)
+    vmask = torch.ones(1, cfg.n_vl, device=dev)
+    vmask[:, :7] = 0
+    o = root(inp["sa"], inp["vl"], t, encoder_attention_mask=vmask, physics_embs=inp["p"],
+             physics_attention_mask=pmask)
+    assert d.served == 1 and len(calls) == 1
+    _as_accurate_as_eager_bf16((o["action"].clone(), o["physics"].clone()), sd, ref, cfg, "dispatcher physics",
+                               mask=vmask, pmask=pmask)
+    root(inp["sa"], inp["vl"], t, physics_embs=inp["p"][:, :5])
+    root(inp["sa"], inp["vl"], t)
+    assert calls == [False, False, True] and d.served == 1 and not d.failed

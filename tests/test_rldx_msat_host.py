@@ -191,4 +191,15 @@ def test_dispatcher_unserved_calls():
     assert d._unserved(torch.zeros(2, 17, 8), torch.zeros(2, 64, 8), False, None, None) == "batch other than 1"
     assert d._unserved(x3, x3, False, torch.zeros(1, 4, 8), None) is None  # module without use_physics ignores them
     d.msat.use_physics = True
-    assert d._unserved(x3, x3, False, torch.zeros(1, 4, 8), None) == "physics tokens"
+    assert d._unserved(x3, x3, False, torch.zeros(1, 4, 8), None) is None  # served by the all-add-ons chain
+    assert d._n_physics(torch.zeros(1, 4, 8)) == 4 and d._n_physics(None) == 0
+    assert d._unserved(x3, x3, False, torch.zeros(2, 4, 8), None) == "batch other than 1"
+
+    class _Built:  # a chain built for 17 SA, 17 VL and 4 physics tokens
+        np_ = 4
+        cfg = RM.RldxMsatCfg(n_vl=17, n_sa_pure=17)
+
+    d.chain = _Built()
+    assert d._unserved(x3, x3, False, torch.zeros(1, 4, 8), None) is None
+    assert d._unserved(x3, x3, False, torch.zeros(1, 5, 8), None) == "token counts differ from the chain's"
+    assert d._unserved(x3, x3, False, None, None) == "token counts differ from the chain's"
