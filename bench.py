@@ -317,6 +317,25 @@ def kernel_lines(torch, reps: int):
         msat_params=sum(torch.Size(s_).numel() for s_ in rmc.param_shapes().values()))
     del rhead
 
+    # the same head with all add-ons: Expanded blocks with the physics stream, N_vl = 80 (cognition +
+    # memory tokens), 1 + 16 physics tokens of 37 signals (30 tactile + 7 torque), physics encoders and decoder
+    rhc = RM.RldxHeadCfg(physics_dim=37, physics_hist_len=1)
+    rmc = RM.RldxMsatCfg(n_vl=80, use_physics=True, n_physics=rhc.physics_hist_len + rhc.physics_fut_len)
+    rhead = RM.RldxActionHead(RM.RldxMsat(RM.make_state_dict(rmc, dev), rmc, dev),
+                              RM.make_head_state_dict(rmc, rhc, dev), rhc)
+    for t in (rhead.vl, rhead.state, rhead.x0, rhead.physics_hist, rhead.physics_x0):
+        t.copy_(torch.randn(t.shape, generator=gr, device=dev))
+    ms = graph_time_ms(rhead.run, 1, torch)
+    msat_ms = graph_time_ms(lambda: rhead.msat.forward(rhead.sa, rhead.vl, rhead.sd["static_tembs"][0],
+                                                       rhead.sd["static_time_tokens"][0],
+                                                       physics_embs=rhead.p_embs), 4, torch)
+    out["rldx_action_head_all_add_ons"] = dict(
+        ms=ms, msat_forward_ms=msat_ms, unit="ms per action (4 denoising steps)",
+        reference_published_ms=10.25, reference_hardware="RTX 5090, path D (rldx/inference/action_model/README.md:28-37)",
+        msat_params=sum(torch.Size(s_).numel() for s_ in rmc.param_shapes().values()), n_vl=80,
+        physics_tokens=rmc.n_physics)
+    del rhead
+
     # residual-add + norm epilogues: the reference's block-boundary shapes (launch-bound)
     # and the Qwen3-VL prefill shape 1280 x 2048 (HBM-bound)
     def rows(m, d, std=1.0):

@@ -852,6 +852,15 @@ class RldxHeadCfg:
     hidden_size: int = 1024   # decoder width (= MSAT output_dim)
     num_embodiments: int = 32
     steps: int = 4
+    # all add-ons: physics signal width (sum of physics_dims, e.g. 30 tactile + 7 torque;
+    # rldx/configs/model/rldx.py:264-285) and its history / future token counts
+    # (physics_head.py:106-109; future length = action horizon); 0 = no physics head
+    physics_dim: int = 0
+    physics_hist_len: int = 1
+
+    @property
+    def physics_fut_len(self) -> int:
+        return self.action_horizon if self.physics_dim > 0 else 0
 
 
 def make_head_state_dict(msat_cfg: RldxMsatCfg, cfg: RldxHeadCfg, device, seed: int = 13) -> dict:
@@ -875,6 +884,16 @@ def make_head_state_dict(msat_cfg: RldxMsatCfg, cfg: RldxHeadCfg, device, seed: 
           "position_embedding.weight": rnd(cfg.action_horizon, d),
           "static_tembs": rnd(cfg.steps, 1, msat_cfg.inner, std=0.5),
           "static_time_tokens": rnd(cfg.steps, 1, msat_cfg.num_temb_tokens, d, std=0.5)}
+    if cfg.physics_dim > 0:
+        # PhysicsHead (physics_head.py:111-113; physics.py:9-72): encoders physics_dim -> d -> d,
+        # decoder output_dim -> d -> physics_dim; nn.Linear weights [out, in]
+        pd, od = cfg.physics_dim, msat_cfg.output_dim
+        for enc in ("physics_cond_encoder", "physics_fut_encoder"):
+            sd.update({f"physics.{enc}.W1.weight": rnd(d, pd), f"physics.{enc}.W1.bias": rnd(d),
+                       f"physics.{enc}.W2.weight": rnd(d, 2 * d), f"physics.{enc}.W2.bias": rnd(d),
+                       f"physics.{enc}.W3.weight": rnd(d, d), f"physics.{enc}.W3.bias": rnd(d)})
+        sd.update({"physics.physics_decoder.net.0.weight": rnd(d, od), "physics.physics_decoder.net.0.bias": rnd(d),
+                   "physics.physics_decoder.net.2.weight": rnd(pd, d), "physics.physics_decoder.net.2.bias": rnd(pd)})
     return sd
 
 
@@ -894,13 +913,26 @@ def sinusoidal_time(t: torch.Tensor, width: int) -> torch.Tensor:
 class RldxActionHead:
     """Flow-matching action head of RLDX-1 with the MSAT on the rldx_amd chain;
     `run` launches one action inference (state encoder + `steps` denoising
-    iterations) on static buffers, `capture` / `replay` as one hipGraph."""
+    iterations) on static buffers, `capture` / `replay` as one hipGraph.
+
+    With a physics head (cfg.physics_dim > 0, an MSAT chain with a P stream of
+    physics_hist_len + physics_fut_len tokens) it is CustomExpandedActionHeadChain
+    .forward without the RTC prefix (rldx/inference/action_model/engine/
+    custom_expanded_action_model_chain.py:92-219): the history tokens are
+    encoded once, and per step the future physics state is encoded at the
+    step's time, the MSAT returns action and physics hidden states, and the
+    physics decoder's velocity advances the future state by the Euler step."""
 
     def __init__(self, msat: RldxMsat, head_sd: dict, cfg: RldxHeadCfg, embodiment: int = 0):
         self.msat, self.cfg, self.sd, self.e = msat, cfg, head_sd, embodiment
         dev, mc = msat.dev, msat.cfg
         Fn._require(mc.n_sa_pure == 1 + cfg.action_horizon, "MSAT SA tokens = state token + action horizon")
         Fn._require(mc.output_dim == cfg.hidden_size, "MSAT output_dim feeds the action decoder")
+        self.phys = cfg.physics_dim > 0
+        Fn._require(self.phys == msat.phys, "a physics head needs an MSAT chain with a P stream, and only then")
+        if self.phys:
+            Fn._require(msat.np_ == cfg.physics_hist_len + cfg.physics_fut_len,
+                        "MSAT physics tokens = physics history + future")
         self.dt = 1.0 / cfg.steps
         self.timesteps = [t / cfg.steps for t in range(cfg.steps)]
         e = lambda *s: torch.empty(*s, dtype=BF16, device=dev)  # noqa: E731
@@ -911,22 +943,53 @@ class RldxActionHead:
         # tau encodings of each step's time, baked (same every call)
         self.tau = [sinusoidal_time(torch.full((cfg.action_horizon,), t, device=dev), mc.sa_dim).to(BF16)
                     for t in self.timesteps]
+        if self.phys:
+            self.physics_hist = e(1, cfg.physics_hist_len, cfg.physics_dim)
+            self.physics_x0 = e(1, cfg.physics_fut_len, cfg.physics_dim)
+            self.physics_fut = e(1, cfg.physics_fut_len, cfg.physics_dim)
+            self.p_embs = e(1, msat.np_, mc.sa_dim)
+            # history positions 0 .. T_hist - 1 (physics.py:19-25), baked
+            self.hist_pos = sinusoidal_time(torch.arange(cfg.physics_hist_len, device=dev), mc.sa_dim).to(BF16)
         self.graph = None
 
+    def _lin(self, x, name):
+        return F.linear(x, self.sd[f"{name}.weight"], self.sd[f"{name}.bias"])
+
+    def _physics_encoder(self, x, pos, enc):
+        """PhysicalSignalEncoder / PhysicsNoiseEncoder.forward (physics.py:19-25,
+        :54-72): W3(silu(W2([W1 x | pos])))."""
+        h = self._lin(x, f"physics.{enc}.W1")
+        return self._lin(F.silu(self._lin(torch.cat([h, pos], dim=-1), f"physics.{enc}.W2")), f"physics.{enc}.W3")
+
     def run(self) -> torch.Tensor:
-        sd, e, mc = self.sd, self.e, self.msat.cfg
+        sd, e, mc, cfg = self.sd, self.e, self.msat.cfg, self.cfg
         h = F.relu(_cat_linear(self.state[0], sd, "state_encoder.layer1", e))
         self.sa[0, :1].copy_(_cat_linear(h, sd, "state_encoder.layer2", e))
         self.act.copy_(self.x0)
-        for i in range(self.cfg.steps):
+        if self.phys:
+            nh = cfg.physics_hist_len
+            self.p_embs[0, :nh].copy_(self._physics_encoder(self.physics_hist[0], self.hist_pos, "physics_cond_encoder"))
+            self.physics_fut.copy_(self.physics_x0)
+        for i in range(cfg.steps):
             a = _cat_linear(self.act[0], sd, "action_encoder.W1", e)
             x = _cat_linear(torch.cat([a, self.tau[i]], dim=-1), sd, "action_encoder.W2", e)
             x = x * torch.sigmoid(x)
             a = _cat_linear(x, sd, "action_encoder.W3", e)
             torch.add(a, sd["position_embedding.weight"], out=self.sa[0, 1:])
-            out = self.msat.forward(self.sa, self.vl, sd["static_tembs"][i], sd["static_time_tokens"][i])
+            if self.phys:
+                # the step's time for every future row: the same encoding as the actions' tau
+                self.p_embs[0, nh:].copy_(self._physics_encoder(self.physics_fut[0], self.tau[i][: cfg.physics_fut_len],
+                                                                "physics_fut_encoder"))
+                o = self.msat.forward(self.sa, self.vl, sd["static_tembs"][i], sd["static_time_tokens"][i],
+                                      physics_embs=self.p_embs)
+                out = o["action"]
+                ph = o["physics"][0, -cfg.physics_fut_len:]
+                pv = self._lin(F.silu(self._lin(ph, "physics.physics_decoder.net.0")), "physics.physics_decoder.net.2")
+                self.physics_fut[0].add_(pv, alpha=self.dt)
+            else:
+                out = self.msat.forward(self.sa, self.vl, sd["static_tembs"][i], sd["static_time_tokens"][i])
             hd = F.relu(_cat_linear(out[0], sd, "action_decoder.layer1", e))
-            v = _cat_linear(hd, sd, "action_decoder.layer2", e)[-self.cfg.action_horizon:]
+            v = _cat_linear(hd, sd, "action_decoder.layer2", e)[-cfg.action_horizon:]
             self.act[0].add_(v, alpha=self.dt)
         return self.act
 
