@@ -371,24 +371,35 @@ def step_gemms(step):
     n, d, inner, ffn = cfg.tokens, cfg.hidden, cfg.inner, cfg.ffn
     rows = [(s, cfg.rows(s)) for s in ("vl", "sa", "p")]
 
+    fold = step.ln_fold  # the pre-LayerNorm folded into QKV / W12, the residual stream packed (as in the step)
+    a_in = step.xp if fold else step.h
+    st = step._stats() if fold else None
+    ln = cfg.eps if fold else None
+
     def qkv(L):  # with the QK-norm / RoPE / K/V-tile epilogue, as in the step
         specs = [Fn.StreamSpec(None, w[f"{s}.q_norm"][L], w[f"{s}.k_norm"][L],
                                *((step.inp[f"{s}_cos"], step.inp[f"{s}_sin"]) if s != "vl" else ())) for s, _ in rows]
-        Fn.grouped_gemm_qkv_norm_rope([(step.h.rows(r.start, r.stop), pw[f"{s}.qkv"][L], w[f"{s}.qkv.b"][L])
+        Fn.grouped_gemm_qkv_norm_rope([(a_in.rows(r.start, r.stop), pw[f"{s}.qkv"][L], w[f"{s}.qkv.b"][L])
                                        for s, r in rows], specs, cfg.heads, cfg.head_dim, cfg.eps,
-                                      out=(step.q, step.kvp))
+                                      out=(step.q, step.kvp), ln_eps=ln, ln_stats=st)
+
+    def res_items(a, name, L):
+        if fold:
+            return [(a.rows(r.start, r.stop), pw[f"{s}.{name}"][L], w[f"{s}.{name}.b"][L],
+                     step.xp.rows(r.start, r.stop), step.xp.rows(r.start, r.stop)) for s, r in rows]
+        return [(a.rows(r.start, r.stop), pw[f"{s}.{name}"][L], w[f"{s}.{name}.b"][L], step.x[r], step.x[r])
+                for s, r in rows]
 
     def proj(L):
-        Fn.grouped_gemm([(step.att.rows(r.start, r.stop), pw[f"{s}.proj"][L], w[f"{s}.proj.b"][L], step.x[r],
-                          step.x[r]) for s, r in rows], "residual")
+        Fn.grouped_gemm(res_items(step.att, "proj", L), "residual_packed" if fold else "residual", stats_out=st)
 
     def w12(L):
-        Fn.grouped_gemm([(step.h.rows(r.start, r.stop), pw[f"{s}.w12"][L], w[f"{s}.w12.b"][L],
-                          step.gl.rows(r.start, r.stop), None) for s, r in rows], "swiglu_packed")
+        Fn.grouped_gemm([(a_in.rows(r.start, r.stop), pw[f"{s}.w12"][L], w[f"{s}.w12.b"][L],
+                          step.gl.rows(r.start, r.stop), None) for s, r in rows], "swiglu_packed",
+                        ln_eps=ln, ln_stats=st)
 
     def w3(L):
-        Fn.grouped_gemm([(step.gl.rows(r.start, r.stop), pw[f"{s}.w3"][L], w[f"{s}.w3.b"][L], step.x[r], step.x[r])
-                         for s, r in rows], "residual")
+        Fn.grouped_gemm(res_items(step.gl, "w3", L), "residual_packed" if fold else "residual", stats_out=st)
 
     def cost(nn, k, n_out, residual):
         flops = 2 * n * nn * k
@@ -611,8 +622,11 @@ def main():
     tf = ROOT / "profiles" / "gemm_w12_swiglu_traffic.json"
     if tf.exists():
         traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
-    roofline = dict(kernel="gemm_kernel<SWIGLU_PACKED>: W12 + SwiGLU grouped GEMM, 3 streams "
-                           "(512/64/32 rows: 128x128 / 64x64 / 32x64 tiles) x [8192 x 1536] weights",
+    roofline = dict(kernel="gemm_kernel<SWIGLU_PACKED, LN fold>: W12 + SwiGLU grouped GEMM with the pre-LayerNorm "
+                           "folded in, 3 streams (512/64/32 rows: 128x128 / 64x64 / 32x64 tiles) x [8192 x 1536] "
+                           "weights" if step.ln_fold else
+                    "gemm_kernel<SWIGLU_PACKED>: W12 + SwiGLU grouped GEMM, 3 streams "
+                    "(512/64/32 rows: 128x128 / 64x64 / 32x64 tiles) x [8192 x 1536] weights",
                     bound="hbm", achieved=dom["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=dom["gbs"] / HBM_PEAK_GBS, traffic=traffic, algorithmic_bytes=dom["bytes"],
                     flops=dom["flops"], us=dom["us"])

@@ -383,7 +383,7 @@ typedef struct rldx_gemm_group {
                          /* width (% 16) of a wider packed matrix whose 16-col  */
                          /* chunk at `out` is the first output column           */
   const void* residual;  /* [m, n] bf16, row stride ldr (RESIDUAL epilogue; may  */
-  int64_t ldr;           /* alias out)                                           */
+  int64_t ldr;           /* alias out); RESIDUAL_PACKED: packed order, ldr as ldo */
 } rldx_gemm_group_t;
 
 #define RLDX_GEMM_EPI_BIAS 0     /* out = bf16(a W^T + bias)                      */
@@ -391,6 +391,8 @@ typedef struct rldx_gemm_group {
 #define RLDX_GEMM_EPI_SWIGLU 2   /* out = swiglu(bf16(gate), bf16(up)), n/2 cols  */
 #define RLDX_GEMM_EPI_SWIGLU_PACKED 3 /* same, out in the packed activation order */
 #define RLDX_GEMM_EPI_BIAS_PACKED 4   /* out = bf16(a W^T + bias), packed order     */
+#define RLDX_GEMM_EPI_RESIDUAL_PACKED 5 /* RESIDUAL with out and residual in the  */
+                                        /* packed activation order (in place)      */
 
 /*
  * y_s = a_s W_s^T (+ bias_s) with the epilogue above, for 1..3 groups that
@@ -481,6 +483,78 @@ hipError_t rldx_grouped_gemm_qkv_norm_rope_bf16(const rldx_gemm_group_t* groups,
                                                 void* q_out, int64_t q_head_stride, int64_t q_row_stride,
                                                 void* kv_packed, int64_t kv_packed_head_stride, float eps,
                                                 hipStream_t stream);
+
+/*
+ * LayerNorm statistics of activation rows, for a GEMM with the pre-LayerNorm
+ * folded in: fp32 [k / 64][rows][2] (slot-major: slot j of row r at
+ * (j * rows + r) * 2), slot j of a row holding (sum, sum of squares) of some of
+ * the row's k values, the slots of a row together covering each value once (the
+ * producers below write the sums of columns [64 j, 64 j + 64), or of 128
+ * columns in one slot and zeros in the next, or the whole row in slot 0 and
+ * zeros elsewhere).
+ */
+
+/*
+ * rldx_act_pack_bf16 that also writes the rows' LayerNorm statistics
+ * (slot 0: the row's sums; the other slots zero).  k % 64 == 0; ln_stats 8-byte
+ * aligned.
+ * Replaces: the activation side of the pre-norm nn.LayerNorm of an MSAT block
+ *   (rldx/model/modules/action_model/blocks.py:804, :882), for the folded GEMMs.
+ */
+hipError_t rldx_act_pack_stats_bf16(const void* x, int64_t ldx, int64_t m, int64_t k, void* packed, float* ln_stats,
+                                    hipStream_t stream);
+
+/*
+ * rldx_grouped_gemm_ex_bf16 with the RESIDUAL or RESIDUAL_PACKED epilogue that
+ * also writes the LayerNorm statistics of the rows it stores (the updated
+ * residual stream): ln_stats_out[i] is group i's [n / 64][m][2] (8-byte aligned).
+ * The statistics are of the bf16 values stored.  Deterministic.
+ * Replaces: the residual additions of an MSAT block (blocks.py:870-889) together
+ *   with the statistics half of the next pre-norm.
+ */
+hipError_t rldx_grouped_gemm_stats_bf16(const rldx_gemm_group_t* groups, float* const* ln_stats_out,
+                                        int32_t num_groups, int64_t n, int64_t k, int32_t epilogue, int32_t split_k,
+                                        int32_t flags, void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * The pre-LayerNorm of an MSAT block folded into the grouped GEMM that consumes
+ * it: y_s = LN(a_s) W_s^T + bias_s with LN the LayerNorm over the k columns
+ * without affine parameters (eps ln_eps), from the un-normalised rows a_s
+ * (packed activation order, e.g. a residual stream kept packed by
+ * RLDX_GEMM_EPI_RESIDUAL_PACKED) and their statistics ln_stats[i] ([k / 64][m][2]
+ * as above, from rldx_grouped_gemm_stats_bf16 or rldx_act_pack_stats_bf16).
+ * w_row_sums[i] is group i's fp32 vector s[j] = sum_k W[j][k] over the n rows of
+ * W in their original order ([gate; up] for SwiGLU).  The kernel computes
+ * mean = sum / k and the biased variance sumsq / k - mean^2 (fp32, clamped at 0)
+ * per row, rstd = rsqrt(var + eps) (the hardware reciprocal square root), and
+ * rstd * (a W^T) - rstd * mean * s before the epilogue.
+ * Epilogues: BIAS and SWIGLU_PACKED (flags: RLDX_GEMM_WIDE_TILES); no split-K;
+ * k <= 2048.  Against LN(a) rounded to bf16 and then multiplied, the result skips
+ * that one rounding of the normalised rows (about 0.1 % of |y| per element); it
+ * is not bit-identical to rldx_layernorm_pack_bf16 followed by
+ * rldx_grouped_gemm_bf16.
+ * Replaces: the pre-norm nn.LayerNorm(dim, elementwise_affine=False) and the
+ *   nn.Linear calls it feeds in an MSAT block
+ *   (rldx/model/modules/action_model/blocks.py:804, :882 with :806-826, :886-888).
+ */
+hipError_t rldx_grouped_gemm_ln_bf16(const rldx_gemm_group_t* groups, const float* const* w_row_sums,
+                                     const float* const* ln_stats, int32_t num_groups, int64_t n, int64_t k,
+                                     int32_t epilogue, int32_t flags, float ln_eps, hipStream_t stream);
+
+/*
+ * rldx_grouped_gemm_qkv_norm_rope_bf16 with the pre-LayerNorm folded in, as
+ * rldx_grouped_gemm_ln_bf16 (w_row_sums per group over the 3 * heads * 128 rows
+ * of [W_q; W_k; W_v], ln_stats of the A rows, ln_eps the LayerNorm's eps; eps
+ * stays the QK-RMSNorm's).
+ * Replaces: the pre-norm + QKV nn.Linear + QK-RMSNorm + RoPE of an MSAT block
+ *   (rldx/model/modules/action_model/blocks.py:804-834).
+ */
+hipError_t rldx_grouped_gemm_qkv_norm_rope_ln_bf16(const rldx_gemm_group_t* groups, const rldx_msat_stream_t* norms,
+                                                   const float* const* w_row_sums, const float* const* ln_stats,
+                                                   int32_t num_groups, int64_t heads, int64_t head_dim, int64_t k,
+                                                   void* q_out, int64_t q_head_stride, int64_t q_row_stride,
+                                                   void* kv_packed, int64_t kv_packed_head_stride, float eps,
+                                                   float ln_eps, hipStream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Host-side diagnostics (no reference counterpart)                         */

@@ -5,6 +5,19 @@
 //   residual        out = bf16(res + bf16(y))                    (x_s += Proj_s(o_s), x_s += W3_s(...))
 //   SwiGLU          out = swiglu(bf16(y_gate), bf16(y_up))       (W12_s followed by SwiGLU),
 //                   row-major or in the packed activation order (the next GEMM's A)
+//   residual, packed   the residual epilogue on a residual stream held in the
+//                   packed activation order (read and written in place)
+// and optionally the block's pre-LayerNorm (no affine) folded in: with the row
+// sums s_n = sum_k W[n][k], LN(x) W^T = rstd (x W^T - mean s), so the GEMM
+// takes the un-normalised rows x as its A operand and applies
+// y = rstd acc - (rstd mean) s_n before the epilogue.  The row statistics come
+// from the producer of x: the residual epilogue (or the activation-pack
+// kernel) writes, per 64-column slot and row, the sum and the sum of squares
+// of the bf16 values it stores ([k / 64][m][2], slot-major, so that a wave's
+// loads of one slot for 64 consecutive rows are contiguous); the consumer
+// loads its rows' slots before its K loop and sums them outside it.  No LayerNorm-pack launch and no
+// normalised copy of x; the result differs from the eager chain only by the
+// bf16 rounding of LN(x) it skips.
 // The rounding points are those of the eager chain (addmm to bf16, then the
 // bf16 add / SwiGLU), rldx/model/modules/action_model/blocks.py:705-891 and
 // rldx/model/modules/action_model/ops.py:137-161.  The SwiGLU epilogue replaces
@@ -60,8 +73,19 @@ constexpr int kXcds = 8;
 constexpr int kThreads = 512;          // 8 waves per workgroup
 constexpr int kBufWord3 = 0x00020000;  // gfx9 raw buffer descriptor, word 3 (untyped dword data)
 
-enum { kEpiBias = 0, kEpiResidual = 1, kEpiSwiglu = 2, kEpiSwigluPacked = 3, kEpiBiasPacked = 4, kEpiQkv = 5 };
-constexpr bool packed_out(int epi) { return epi == kEpiSwigluPacked || epi == kEpiBiasPacked; }
+enum {
+  kEpiBias = 0,
+  kEpiResidual = 1,
+  kEpiSwiglu = 2,
+  kEpiSwigluPacked = 3,
+  kEpiBiasPacked = 4,
+  kEpiResidualPacked = 5,
+  kEpiQkv = 16  // internal: rldx_grouped_gemm_qkv_norm_rope_bf16
+};
+constexpr bool packed_out(int epi) {
+  return epi == kEpiSwigluPacked || epi == kEpiBiasPacked || epi == kEpiResidualPacked;
+}
+constexpr bool residual_epi(int epi) { return epi == kEpiResidual || epi == kEpiResidualPacked; }
 enum { kTile128 = 0, kTile64 = 1, kTile32 = 2, kTile64x128 = 3, kTile32x128 = 4 };
 
 __device__ __forceinline__ float bf(uint16_t b) { return bf16_bits_to_f32(b); }
@@ -118,8 +142,17 @@ using Cfg64x128D = TileCfg<2, 4, 2, 6>;
 using Cfg32x128D = TileCfg<1, 4, 2, 3>;
 
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
+// The ring during the K loop; afterwards the fp32 tiles of the K-groups and,
+// behind them, the LayerNorm-fold partial row statistics (Σx, Σx² over the
+// slots of each thread: 512 pairs).
 template <class C>
-constexpr int lds_bytes() { return cmax(C::RING * 1024, C::KG * C::TILE * 4); }
+constexpr int ln_stats_off() { return C::KG * C::TILE; }  // floats
+template <class C>
+constexpr int lds_bytes() { return cmax(C::RING * 1024, (ln_stats_off<C>() + 2 * 512) * 4); }
+// LayerNorm statistics [k / 64][m][2]: thread t of a tile of R rows sums slots
+// [q SPL, (q + 1) SPL) of row t % R (q = t / R, SPL = ceil(slots R / 512)),
+// at most kLnSlotsMax (k <= 2048 at 128-row tiles).
+constexpr int kLnSlotsMax = 8;
 constexpr int kLdsBytes = cmax(lds_bytes<Cfg128>(), cmax(lds_bytes<Cfg64>(), lds_bytes<Cfg32>()));
 static_assert(kLdsBytes <= 80 * 1024, "two workgroups per CU");
 constexpr int kLdsDeep = cmax(lds_bytes<Cfg128D>(), cmax(lds_bytes<Cfg64D>(), lds_bytes<Cfg32D>()));
@@ -145,6 +178,12 @@ struct Group {
   int m_begin, rope_ld;
   const uint16_t *qn_w, *kn_w;
   const float *cos, *sin;
+  // LayerNorm fold: fp32 row sums of W [n] (original row order) and the
+  // statistics of the A rows [m][k / 64][2] (both set, or both null)
+  const float* wsum;
+  const float* lnstats;
+  // residual epilogues: statistics of the output rows [m][n / 64][2], or null
+  float* stats_out;
 };
 
 // Outputs of the QKV epilogue: Q (H, M, 128) with strides (q_sh, q_sm), and the
@@ -162,8 +201,15 @@ struct GemmArgs {
   int num_groups;
   int n, k;  // n = rows of W (2 * N_half with the SwiGLU epilogue)
   QkvOut qkv;
-  int spread;  // != 0: the splits of a tile on different XCDs (RLDX_GEMM_SPLITS_ACROSS_XCDS)
+  int spread;    // != 0: the splits of a tile on different XCDs (RLDX_GEMM_SPLITS_ACROSS_XCDS)
+  float ln_eps;  // LayerNorm fold (kernels instantiated with LN)
 };
+
+// y' = rstd y - (rstd mean) s: the LayerNorm fold of one accumulator (one
+// fused multiply-add, so every epilogue computes the same bits)
+__device__ __forceinline__ float ln_fold(float y, float rs, float rm, float s) {
+  return __builtin_fmaf(rs, y, -(rm * s));
+}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const uint16_t* p, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p), 0, bytes, kBufWord3);
@@ -184,7 +230,7 @@ __device__ __forceinline__ void wait_barrier() {
 // K (the kernel's WIDE) only keeps the tile specializations of the wide and
 // narrow kernels apart: the host compilation pass rejects a second caller of a
 // specialization whose body holds the 16-byte LDS-load builtin.
-template <class C, int EPI, bool K>
+template <class C, int EPI, bool K, bool LN>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int item, u32x4* lds) {
   constexpr bool kSwiglu = EPI == kEpiSwiglu || EPI == kEpiSwigluPacked;
   constexpr int MB = C::MB, NB = C::NB, BNW = C::BNW, U = C::U, CH = C::CH, NSLOT = C::NSLOT;
@@ -245,9 +291,32 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
                                                         __builtin_bit_cast(bf16x8, xa[b][u]), acc[bb], 0, 0, 0);
   };
 
+  // LayerNorm fold: this thread's slots of its row, loaded before the ring
+  // (consecutive threads: consecutive rows of one slot, contiguous), summed at
+  // the prologue's wait, where they are complete (older than every ring load)
+  constexpr int RT = 32 * MB;  // tile rows
+  [[maybe_unused]] f32x2_t lv[kLnSlotsMax];
+  [[maybe_unused]] float lp1 = 0.f, lp2 = 0.f;
+  const int ln_slots = a.k / 64, ln_spl = (ln_slots * RT + kThreads - 1) / kThreads;
+  const int ln_q = static_cast<int>(threadIdx.x) / RT;
+  if constexpr (LN) {
+    const int row = min(mt * RT + static_cast<int>(threadIdx.x) % RT, G.m - 1);
+    const f32x2_t* src = reinterpret_cast<const f32x2_t*>(G.lnstats) + row;
+#pragma unroll
+    for (int j = 0; j < kLnSlotsMax; ++j)
+      lv[j] = src[static_cast<int64_t>(min(ln_q * ln_spl + j, ln_slots - 1)) * G.m];
+  }
 #pragma unroll
   for (int s = 0; s < NSLOT - 1; ++s) dma(s, s);
   wait_barrier<(NSLOT - 2) * C::ND>();
+  if constexpr (LN) {
+#pragma unroll
+    for (int j = 0; j < kLnSlotsMax; ++j)
+      if (j < ln_spl && ln_q * ln_spl + j < ln_slots) {
+        lp1 += lv[j][0];
+        lp2 += lv[j][1];
+      }
+  }
   lread(0, 0);
   int slot_next = 1, slot_dma = NSLOT - 1;  // ring slots of stages st + 1, st + NSLOT - 1
   for (int st = 0; st < lstages; st += 2) {
@@ -281,14 +350,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   const bool col_ok = col < n_out;
   // residual chunks (each is read and written by this thread, so it may alias the output)
   u32x4 pres[PER];
-  if constexpr (EPI == kEpiResidual) {
+  if constexpr (residual_epi(EPI)) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int t = static_cast<int>(threadIdx.x) + kThreads * i;
       const int row = mt * R + t / CPR;
-      pres[i] = (t < R * CPR && row < G.m && col_ok)
-                    ? *reinterpret_cast<const u32x4*>(G.res + static_cast<int64_t>(row) * G.ldr + col)
-                    : u32x4{0, 0, 0, 0};
+      const int64_t off = EPI == kEpiResidualPacked ? packed_act_offset(row, col, G.ldr)
+                                                    : static_cast<int64_t>(row) * G.ldr + col;
+      pres[i] = (t < R * CPR && row < G.m && col_ok) ? *reinterpret_cast<const u32x4*>(G.res + off)
+                                                     : u32x4{0, 0, 0, 0};
     }
   }
   float bg[8], bu[8];
@@ -296,6 +366,26 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   for (int i = 0; i < 8; ++i) {
     bg[i] = G.bias && col_ok ? bf(G.bias[col + i]) : 0.f;
     bu[i] = kSwiglu && G.bias && col_ok ? bf(G.bias[a.n / 2 + col + i]) : 0.f;
+  }
+  // LayerNorm fold: W row sums of this thread's columns (gate and up for SwiGLU)
+  [[maybe_unused]] float wg[8], wu[8];
+  if constexpr (LN) {
+    const floatx4 z = {0.f, 0.f, 0.f, 0.f};
+    const floatx4* ws = reinterpret_cast<const floatx4*>(G.wsum + col);
+    const floatx4 g0 = col_ok ? ws[0] : z, g1 = col_ok ? ws[1] : z;
+    floatx4 u0 = z, u1 = z;
+    if constexpr (kSwiglu) {
+      const floatx4* wu4 = reinterpret_cast<const floatx4*>(G.wsum + a.n / 2 + col);
+      u0 = col_ok ? wu4[0] : z;
+      u1 = col_ok ? wu4[1] : z;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      wg[i] = g0[i];
+      wg[4 + i] = g1[i];
+      wu[i] = u0[i];
+      wu[4 + i] = u1[i];
+    }
   }
   wait_barrier<0>();  // the ring's last reads and loads are done; LDS becomes the fp32 tiles
   float* tiles = reinterpret_cast<float*>(lds);
@@ -308,7 +398,28 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
         *reinterpret_cast<floatx4*>(&t[(32 * wm + l32) * C::TP + 32 * (wn * BNW + bb) + 8 * q4 + 4 * g]) =
             floatx4{acc[bb][4 * q4], acc[bb][4 * q4 + 1], acc[bb][4 * q4 + 2], acc[bb][4 * q4 + 3]};
   }
+  float* const lnst = tiles + ln_stats_off<C>();  // [kThreads / R][R][2]: thread t = q R + r's Σx, Σx²
+  if constexpr (LN) {
+    lnst[2 * threadIdx.x] = lp1;
+    lnst[2 * threadIdx.x + 1] = lp2;
+  }
   wait_barrier<0>();
+  // LayerNorm fold factors of tile row r: rstd and rstd * mean, with mean and
+  // the biased variance E[x^2] - mean^2 (clamped at 0) in fp32 and rstd from
+  // v_rsq_f32 (the fold is not bit-compatible with the eager pre-norm anyway)
+  auto ln_row = [&](int r, float& rs, float& rm) {
+    float s1 = lnst[2 * r], s2 = lnst[2 * r + 1];
+#pragma unroll
+    for (int p = 1; p < kThreads / R; ++p) {
+      s1 += lnst[(p * R + r) * 2];
+      s2 += lnst[(p * R + r) * 2 + 1];
+    }
+    const float inv_k = 1.0f / static_cast<float>(a.k);
+    const float mean = s1 * inv_k;
+    const float var = __builtin_fmaxf(__builtin_fmaf(-mean, mean, s2 * inv_k), 0.f);
+    rs = __builtin_amdgcn_rsqf(var + a.ln_eps);
+    rm = rs * mean;
+  };
   // 8 consecutive fp32 sums (K-groups in order) of tile row r from tile column tc
   auto sum8 = [&](int r, int tc, float (&v)[8]) {
     floatx4 lo = *reinterpret_cast<const floatx4*>(&tiles[r * C::TP + tc]);
@@ -365,6 +476,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
             lo += tiles[kg * C::TILE + r * C::TP + d];
             hi += tiles[kg * C::TILE + (r + 1) * C::TP + d];
           }
+          if constexpr (LN) {
+            const float sd = G.wsum[n0 + d];
+            float rs, rm;
+            ln_row(r, rs, rm);
+            lo = ln_fold(lo, rs, rm, sd);
+            ln_row(r + 1, rs, rm);
+            hi = ln_fold(hi, rs, rm, sd);
+          }
           o[e] = pack_bf16x2(mt * R + r < G.m ? lo + bd : 0.f, mt * R + r + 1 < G.m ? hi + bd : 0.f);
         }
         *reinterpret_cast<u32x4*>(kvh + ((G.m_begin + row0) >> 5) * (64 * D) + NCH * 512 + idx * 8) = o;
@@ -381,6 +500,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
       const int r = (static_cast<int>(threadIdx.x) + kThreads * i) / CPR, row = mt * R + r;
       float x[8];
       sum8(r, c8, x);
+      if constexpr (LN) {
+        float rs, rm;
+        ln_row(r, rs, rm);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = ln_fold(x[e], rs, rm, wg[e]);  // (columns n0 + c8 = col)
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t xp = pack_bf16x2(x[2 * e] + bq[2 * e], x[2 * e + 1] + bq[2 * e + 1]);
@@ -446,7 +571,32 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
 #pragma unroll
       for (int e = 0; e < 8; ++e) y[i][8 + e] = hi[e];
     }
+    if constexpr (LN) {  // (the host allows the fold only without split-K)
+      float rs, rm;
+      ln_row(r < R ? r : 0, rs, rm);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        y[i][e] = ln_fold(y[i][e], rs, rm, wg[e]);
+        if constexpr (kSwiglu) y[i][8 + e] = ln_fold(y[i][8 + e], rs, rm, wu[e]);
+      }
+    }
   }
+  // the residual epilogue's output chunk i: bf16(residual + bf16(y + bias))
+  [[maybe_unused]] auto residual_out = [&](int i) {
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[e] = pack_bf16x2(y[i][2 * e] + bg[2 * e], y[i][2 * e + 1] + bg[2 * e + 1]);
+      o[e] = pack_bf16x2(bf16x2_lo(pres[i][e]) + bf16x2_lo(o[e]), bf16x2_hi(pres[i][e]) + bf16x2_hi(o[e]));
+    }
+    return o;
+  };
+  auto store_out = [&](int row, const u32x4& o) {
+    if constexpr (packed_out(EPI))  // ldo = width of the packed matrix the output columns belong to
+      *reinterpret_cast<u32x4*>(G.out + packed_act_offset(row, col, G.ldo)) = o;
+    else
+      *reinterpret_cast<u32x4*>(G.out + static_cast<int64_t>(row) * G.ldo + col) = o;
+  };
   if (G.splits > 1) {
     // Split-K.  Each split stores its fp32 partial with device-scope stores
     // (SC1: written through to the device coherence point, not held in this
@@ -501,7 +651,37 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   for (int i = 0; i < PER; ++i) {
     const int t = static_cast<int>(threadIdx.x) + kThreads * i;
     const int r = t / CPR, row = mt * R + r;
-    if (t >= R * CPR || row >= G.m || !col_ok) continue;
+    const bool ok = t < R * CPR && row < G.m && col_ok;
+    if constexpr (residual_epi(EPI)) {
+      // row statistics of the stored values for a LayerNorm-folding consumer:
+      // Σx, Σx² over this tile's columns of the row (its CPR threads are
+      // consecutive lanes), in slot nt OC / 64 of [n / 64][m][2] (a 128-column
+      // tile writes its sums in the first of its two slots and zeros in the other)
+      if (G.stats_out) {
+        u32x4 o = ok ? residual_out(i) : u32x4{0, 0, 0, 0};
+        if (ok) store_out(row, o);
+        float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = bf16x2_lo(o[e]), hi = bf16x2_hi(o[e]);
+          s1 += lo + hi;
+          s2 += lo * lo + hi * hi;
+        }
+#pragma unroll
+        for (int mm = CPR / 2; mm >= 1; mm >>= 1) {
+          s1 += __shfl_xor(s1, mm, 64);
+          s2 += __shfl_xor(s2, mm, 64);
+        }
+        if (ok && t % CPR == 0) {
+          f32x2_t* st = reinterpret_cast<f32x2_t*>(G.stats_out) + static_cast<int64_t>(nt * (OC / 64)) * G.m + row;
+          *st = f32x2_t{s1, s2};
+          if constexpr (OC == 128)
+            if (2 * nt + 1 < a.n / 64) st[G.m] = f32x2_t{0.f, 0.f};
+        }
+        continue;
+      }
+    }
+    if (!ok) continue;
     u32x4 o;
     if constexpr (kSwiglu) {
 #pragma unroll
@@ -513,23 +693,22 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(y[i][2 * e] + bg[2 * e], y[i][2 * e + 1] + bg[2 * e + 1]);
-      if constexpr (EPI == kEpiResidual) {
+      if constexpr (residual_epi(EPI)) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           o[e] = pack_bf16x2(bf16x2_lo(pres[i][e]) + bf16x2_lo(o[e]), bf16x2_hi(pres[i][e]) + bf16x2_hi(o[e]));
       }
     }
-    if constexpr (packed_out(EPI))  // ldo = width of the packed matrix the output columns belong to
-      *reinterpret_cast<u32x4*>(G.out + packed_act_offset(row, col, G.ldo)) = o;
-    else
-      *reinterpret_cast<u32x4*>(G.out + static_cast<int64_t>(row) * G.ldo + col) = o;
+    store_out(row, o);
   }
 }
 
 // WIDE: the plan uses 128 x 128, 64 x 128 and 32 x 128 tiles (always with the
 // QKV epilogue; on request for the others).
-template <int EPI, bool DEEP, bool WIDE>
-__global__ __launch_bounds__(kThreads, DEEP ? 1 : 2) void gemm_kernel(GemmArgs a) {
+// Second launch bound: minimum waves per SIMD (2 per workgroup of 8 waves):
+// the two-workgroups-per-CU kernels keep to 128 VGPRs.
+template <int EPI, bool DEEP, bool WIDE, bool LN>
+__global__ __launch_bounds__(kThreads, DEEP ? 2 : 4) void gemm_kernel(GemmArgs a) {
   constexpr int kLds = WIDE ? (DEEP ? kLdsQkvDeep : kLdsQkv) : (DEEP ? kLdsDeep : kLdsBytes);
   __shared__ __attribute__((aligned(16))) u32x4 lds[kLds / 16];
   const int b = static_cast<int>(blockIdx.x);
@@ -544,32 +723,32 @@ __global__ __launch_bounds__(kThreads, DEEP ? 1 : 2) void gemm_kernel(GemmArgs a
   if (item >= G.items) return;
   if constexpr (WIDE && DEEP) {  // 128-column tiles (whole heads for the QKV epilogue)
     if (G.cfg == kTile128)
-      gemm_tile<Cfg128D, EPI, WIDE>(a, G, item, lds);
+      gemm_tile<Cfg128D, EPI, WIDE, LN>(a, G, item, lds);
     else if (G.cfg == kTile64x128)
-      gemm_tile<Cfg64x128D, EPI, WIDE>(a, G, item, lds);
+      gemm_tile<Cfg64x128D, EPI, WIDE, LN>(a, G, item, lds);
     else
-      gemm_tile<Cfg32x128D, EPI, WIDE>(a, G, item, lds);
+      gemm_tile<Cfg32x128D, EPI, WIDE, LN>(a, G, item, lds);
   } else if constexpr (WIDE) {
     if (G.cfg == kTile128)
-      gemm_tile<Cfg128, EPI, WIDE>(a, G, item, lds);
+      gemm_tile<Cfg128, EPI, WIDE, LN>(a, G, item, lds);
     else if (G.cfg == kTile64x128)
-      gemm_tile<Cfg64x128, EPI, WIDE>(a, G, item, lds);
+      gemm_tile<Cfg64x128, EPI, WIDE, LN>(a, G, item, lds);
     else
-      gemm_tile<Cfg32x128, EPI, WIDE>(a, G, item, lds);
+      gemm_tile<Cfg32x128, EPI, WIDE, LN>(a, G, item, lds);
   } else if constexpr (DEEP) {
     if (G.cfg == kTile128)
-      gemm_tile<Cfg128D, EPI, WIDE>(a, G, item, lds);
+      gemm_tile<Cfg128D, EPI, WIDE, LN>(a, G, item, lds);
     else if (G.cfg == kTile64)
-      gemm_tile<Cfg64D, EPI, WIDE>(a, G, item, lds);
+      gemm_tile<Cfg64D, EPI, WIDE, LN>(a, G, item, lds);
     else
-      gemm_tile<Cfg32D, EPI, WIDE>(a, G, item, lds);
+      gemm_tile<Cfg32D, EPI, WIDE, LN>(a, G, item, lds);
   } else {
     if (G.cfg == kTile128)
-      gemm_tile<Cfg128, EPI, WIDE>(a, G, item, lds);
+      gemm_tile<Cfg128, EPI, WIDE, LN>(a, G, item, lds);
     else if (G.cfg == kTile64)
-      gemm_tile<Cfg64, EPI, WIDE>(a, G, item, lds);
+      gemm_tile<Cfg64, EPI, WIDE, LN>(a, G, item, lds);
     else
-      gemm_tile<Cfg32, EPI, WIDE>(a, G, item, lds);
+      gemm_tile<Cfg32, EPI, WIDE, LN>(a, G, item, lds);
   }
 }
 
@@ -614,12 +793,32 @@ constexpr int64_t kCounterBytes = 65536;
 // *ws_bytes receives the workspace the plan needs (counters, then fp32 partials).
 // The QKV epilogue (kEpiQkv) takes each group's norm weights and RoPE tables
 // from norms[i] (the caller has checked them) and never splits.
+// w_row_sums (LayerNorm fold): one fp32 row-sum vector per group, all present;
+// only for the bias, packed-SwiGLU and QKV epilogues, without split-K.
 hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, int64_t k, int32_t epilogue,
                 int split_k, GemmArgs& args, int64_t* ws_bytes, int64_t* cnt_off, int64_t* part_off,
-                const rldx_msat_stream_t* norms = nullptr, bool wide_tiles = false) {
+                const rldx_msat_stream_t* norms = nullptr, bool wide_tiles = false,
+                const float* const* w_row_sums = nullptr, const float* const* ln_stats = nullptr,
+                float* const* stats_out = nullptr) {
   if (!groups || num_groups < 1 || num_groups > 3) return hipErrorInvalidValue;
-  if (epilogue < kEpiBias || epilogue > kEpiQkv) return hipErrorInvalidValue;
+  if (!(epilogue >= kEpiBias && epilogue <= kEpiResidualPacked) && epilogue != kEpiQkv) return hipErrorInvalidValue;
   const bool qkv = epilogue == kEpiQkv;
+  // LayerNorm fold: W row sums and A-row statistics for every group; k <= 2048
+  // (a thread of a 128-row tile sums at most kLnSlotsMax slots)
+  if ((w_row_sums == nullptr) != (ln_stats == nullptr)) return hipErrorInvalidValue;
+  if (w_row_sums) {
+    if (split_k > 1 || !(epilogue == kEpiBias || epilogue == kEpiSwigluPacked || qkv)) return hipErrorInvalidValue;
+    if (k > 64 * 4 * kLnSlotsMax) return hipErrorInvalidValue;
+    for (int i = 0; i < num_groups; ++i)
+      if (!w_row_sums[i] || reinterpret_cast<uintptr_t>(w_row_sums[i]) % 4 || !ln_stats[i] ||
+          reinterpret_cast<uintptr_t>(ln_stats[i]) % 8)
+        return hipErrorInvalidValue;
+  }
+  if (stats_out) {
+    if (!residual_epi(epilogue)) return hipErrorInvalidValue;
+    for (int i = 0; i < num_groups; ++i)
+      if (!stats_out[i] || reinterpret_cast<uintptr_t>(stats_out[i]) % 8) return hipErrorInvalidValue;
+  }
   const bool wide = qkv || wide_tiles;
   if (qkv && (norms == nullptr || split_k > 1)) return hipErrorInvalidValue;
   // k: whole stages of every K-group split (4 K-groups x 2 k-steps); n: whole 64-column blocks
@@ -650,6 +849,11 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
     if (packed_out(epilogue) && (s.ldo < 0 || s.ldo % 16 || (s.ldo > 0 && s.ldo < n_out) || s.ldo > (1 << 30)))
       return hipErrorInvalidValue;
     if (epilogue == kEpiResidual && (!s.residual || !a16(s.residual) || s.ldr < n_out || s.ldr % 8))
+      return hipErrorInvalidValue;
+    // packed residual: ldr 0 (= n_out) or the width of the packed matrix, as ldo
+    if (epilogue == kEpiResidualPacked &&
+        (!s.residual || !a16(s.residual) || s.ldr < 0 || s.ldr % 16 || (s.ldr > 0 && s.ldr < n_out) ||
+         s.ldr > (1 << 30)))
       return hipErrorInvalidValue;
     // Tile shape: 128 x 128 where the stream has rows and tiles enough to
     // occupy the chip (half the L2 traffic per flop of 64 x 64), else 64 x 64,
@@ -687,9 +891,13 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
     Group& G = args.g[cnt++];
     G = Group{static_cast<const uint16_t*>(s.a_packed), static_cast<const uint16_t*>(s.w_packed),
               static_cast<const uint16_t*>(s.bias), static_cast<uint16_t*>(s.out),
-              static_cast<const uint16_t*>(s.residual), packed_out(epilogue) && s.ldo == 0 ? n_out : s.ldo, s.ldr,
+              static_cast<const uint16_t*>(s.residual), packed_out(epilogue) && s.ldo == 0 ? n_out : s.ldo,
+              epilogue == kEpiResidualPacked && s.ldr == 0 ? n_out : s.ldr,
               static_cast<int>(s.m), cfg, mt,
               static_cast<int>(tiles * sp), 0, 0, sp, lstages / sp, nullptr, nullptr};
+    G.wsum = w_row_sums ? w_row_sums[i] : nullptr;
+    G.lnstats = ln_stats ? ln_stats[i] : nullptr;
+    G.stats_out = stats_out ? stats_out[i] : nullptr;
     if (qkv) {
       G.m_begin = static_cast<int>(m_begin);
       G.qn_w = static_cast<const uint16_t*>(norms[i].q_norm_w);
@@ -746,66 +954,56 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
   return hipSuccess;
 }
 
-hipError_t launch(const GemmArgs& args, int epilogue, hipStream_t stream, bool wide = false) {
+template <int EPI, bool LN>
+void launch_epi(const GemmArgs& args, dim3 grid, hipStream_t stream, bool deep, bool wide) {
+  const dim3 block(kThreads);
+  if (deep && wide)
+    hipLaunchKernelGGL((gemm_kernel<EPI, true, true, LN>), grid, block, 0, stream, args);
+  else if (deep)
+    hipLaunchKernelGGL((gemm_kernel<EPI, true, false, LN>), grid, block, 0, stream, args);
+  else if (wide)
+    hipLaunchKernelGGL((gemm_kernel<EPI, false, true, LN>), grid, block, 0, stream, args);
+  else
+    hipLaunchKernelGGL((gemm_kernel<EPI, false, false, LN>), grid, block, 0, stream, args);
+}
+
+template <bool LN>
+void launch_qkv(const GemmArgs& args, dim3 grid, hipStream_t stream, bool deep) {
+  if (deep)
+    hipLaunchKernelGGL((gemm_kernel<kEpiQkv, true, true, LN>), grid, dim3(kThreads), 0, stream, args);
+  else
+    hipLaunchKernelGGL((gemm_kernel<kEpiQkv, false, true, LN>), grid, dim3(kThreads), 0, stream, args);
+}
+
+// ln: the groups carry W row sums (LayerNorm fold; plan() admits it for the
+// bias, packed-SwiGLU and QKV epilogues only)
+hipError_t launch(const GemmArgs& args, int epilogue, hipStream_t stream, bool wide = false, bool ln = false) {
   if (args.num_groups == 0) return hipSuccess;
   const Group& last = args.g[args.num_groups - 1];
   const int wgs = last.wg_begin + last.per_xcd * kXcds;
-  const dim3 grid(static_cast<unsigned>(wgs)), block(kThreads);
+  const dim3 grid(static_cast<unsigned>(wgs));
   // at most one workgroup per CU (256 CUs): the deep-ring kernel
   const bool deep = wgs <= 256;
-  if (epilogue == kEpiQkv) {
-    if (deep)
-      hipLaunchKernelGGL((gemm_kernel<kEpiQkv, true, true>), grid, block, 0, stream, args);
+  if (ln) {
+    if (epilogue == kEpiQkv)
+      launch_qkv<true>(args, grid, stream, deep);
+    else if (epilogue == kEpiBias)
+      launch_epi<kEpiBias, true>(args, grid, stream, deep, wide);
+    else if (epilogue == kEpiSwigluPacked)
+      launch_epi<kEpiSwigluPacked, true>(args, grid, stream, deep, wide);
     else
-      hipLaunchKernelGGL((gemm_kernel<kEpiQkv, false, true>), grid, block, 0, stream, args);
-  } else if (wide) {
-    if (deep) {
-      if (epilogue == kEpiBias)
-        hipLaunchKernelGGL((gemm_kernel<kEpiBias, true, true>), grid, block, 0, stream, args);
-      else if (epilogue == kEpiResidual)
-        hipLaunchKernelGGL((gemm_kernel<kEpiResidual, true, true>), grid, block, 0, stream, args);
-      else if (epilogue == kEpiSwiglu)
-        hipLaunchKernelGGL((gemm_kernel<kEpiSwiglu, true, true>), grid, block, 0, stream, args);
-      else if (epilogue == kEpiSwigluPacked)
-        hipLaunchKernelGGL((gemm_kernel<kEpiSwigluPacked, true, true>), grid, block, 0, stream, args);
-      else
-        hipLaunchKernelGGL((gemm_kernel<kEpiBiasPacked, true, true>), grid, block, 0, stream, args);
-    } else {
-      if (epilogue == kEpiBias)
-        hipLaunchKernelGGL((gemm_kernel<kEpiBias, false, true>), grid, block, 0, stream, args);
-      else if (epilogue == kEpiResidual)
-        hipLaunchKernelGGL((gemm_kernel<kEpiResidual, false, true>), grid, block, 0, stream, args);
-      else if (epilogue == kEpiSwiglu)
-        hipLaunchKernelGGL((gemm_kernel<kEpiSwiglu, false, true>), grid, block, 0, stream, args);
-      else if (epilogue == kEpiSwigluPacked)
-        hipLaunchKernelGGL((gemm_kernel<kEpiSwigluPacked, false, true>), grid, block, 0, stream, args);
-      else
-        hipLaunchKernelGGL((gemm_kernel<kEpiBiasPacked, false, true>), grid, block, 0, stream, args);
-    }
-  } else {
-    if (deep) {
-      if (epilogue == kEpiBias)
-        hipLaunchKernelGGL((gemm_kernel<kEpiBias, true, false>), grid, block, 0, stream, args);
-      else if (epilogue == kEpiResidual)
-        hipLaunchKernelGGL((gemm_kernel<kEpiResidual, true, false>), grid, block, 0, stream, args);
-      else if (epilogue == kEpiSwiglu)
-        hipLaunchKernelGGL((gemm_kernel<kEpiSwiglu, true, false>), grid, block, 0, stream, args);
-      else if (epilogue == kEpiSwigluPacked)
-        hipLaunchKernelGGL((gemm_kernel<kEpiSwigluPacked, true, false>), grid, block, 0, stream, args);
-      else
-        hipLaunchKernelGGL((gemm_kernel<kEpiBiasPacked, true, false>), grid, block, 0, stream, args);
-    } else {
-      if (epilogue == kEpiBias)
-        hipLaunchKernelGGL((gemm_kernel<kEpiBias, false, false>), grid, block, 0, stream, args);
-      else if (epilogue == kEpiResidual)
-        hipLaunchKernelGGL((gemm_kernel<kEpiResidual, false, false>), grid, block, 0, stream, args);
-      else if (epilogue == kEpiSwiglu)
-        hipLaunchKernelGGL((gemm_kernel<kEpiSwiglu, false, false>), grid, block, 0, stream, args);
-      else if (epilogue == kEpiSwigluPacked)
-        hipLaunchKernelGGL((gemm_kernel<kEpiSwigluPacked, false, false>), grid, block, 0, stream, args);
-      else
-        hipLaunchKernelGGL((gemm_kernel<kEpiBiasPacked, false, false>), grid, block, 0, stream, args);
-    }
+      return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
+  switch (epilogue) {
+    case kEpiQkv: launch_qkv<false>(args, grid, stream, deep); break;
+    case kEpiBias: launch_epi<kEpiBias, false>(args, grid, stream, deep, wide); break;
+    case kEpiResidual: launch_epi<kEpiResidual, false>(args, grid, stream, deep, wide); break;
+    case kEpiSwiglu: launch_epi<kEpiSwiglu, false>(args, grid, stream, deep, wide); break;
+    case kEpiSwigluPacked: launch_epi<kEpiSwigluPacked, false>(args, grid, stream, deep, wide); break;
+    case kEpiBiasPacked: launch_epi<kEpiBiasPacked, false>(args, grid, stream, deep, wide); break;
+    case kEpiResidualPacked: launch_epi<kEpiResidualPacked, false>(args, grid, stream, deep, wide); break;
+    default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
@@ -819,9 +1017,12 @@ hipError_t launch(const GemmArgs& args, int epilogue, hipStream_t stream, bool w
 // once to bf16 — F.layer_norm's arithmetic on bf16 input.
 // One wave per row; lane j holds columns 8 (j + 64 c) .. +7.
 // ---------------------------------------------------------------------------
+// stats (optional, not with normalize): the row's Σx, Σx² for a LayerNorm-
+// folding GEMM, in slot 0 of [k / 64][m][2], zeros in the other slots.
 template <int CPL>
 __global__ __launch_bounds__(256) void rows_pack_kernel(const uint16_t* __restrict__ x, int64_t ldx, int m, int k,
-                                                        float eps, int normalize, uint16_t* __restrict__ out) {
+                                                        float eps, int normalize, uint16_t* __restrict__ out,
+                                                        float* __restrict__ stats) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= m) return;
@@ -868,28 +1069,48 @@ __global__ __launch_bounds__(256) void rows_pack_kernel(const uint16_t* __restri
     const int col = 8 * (lane + 64 * c);
     if (col < k) *reinterpret_cast<u32x4*>(out + packed_act_offset(row, col, k)) = raw[c];
   }
+  if (stats != nullptr) {  // (wave-uniform)
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c)
+      if (8 * (lane + 64 * c) < k)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          s1 += v[c][i];
+          s2 += v[c][i] * v[c][i];
+        }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      s1 += __shfl_xor(s1, o, 64);
+      s2 += __shfl_xor(s2, o, 64);
+    }
+    const int slots = k / 64;
+    f32x2_t* st = reinterpret_cast<f32x2_t*>(stats) + row;
+    for (int j = lane; j < slots; j += 64) st[static_cast<int64_t>(j) * m] = j == 0 ? f32x2_t{s1, s2} : f32x2_t{0.f, 0.f};
+  }
 }
 
 hipError_t rows_pack(const void* x, int64_t ldx, int64_t m, int64_t k, float eps, bool normalize, void* packed,
-                     hipStream_t stream) {
+                     hipStream_t stream, float* stats = nullptr) {
   if (m < 0 || k < 0) return hipErrorInvalidValue;
   if (m == 0 || k == 0) return hipSuccess;
   if (!x || !packed || !a16(x) || !a16(packed) || ldx < k || ldx % 8 || k % 16) return hipErrorInvalidValue;
+  if (stats && (normalize || k % 64 || reinterpret_cast<uintptr_t>(stats) % 8)) return hipErrorInvalidValue;
   if (m > (int64_t{1} << 30)) return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>((m + 3) / 4)), block(256);
   const auto* xp = static_cast<const uint16_t*>(x);
   auto* op = static_cast<uint16_t*>(packed);
   const int mi = static_cast<int>(m), ki = static_cast<int>(k), nz = normalize ? 1 : 0;
   if (k <= 512)
-    hipLaunchKernelGGL(rows_pack_kernel<1>, grid, block, 0, stream, xp, ldx, mi, ki, eps, nz, op);
+    hipLaunchKernelGGL(rows_pack_kernel<1>, grid, block, 0, stream, xp, ldx, mi, ki, eps, nz, op, stats);
   else if (k <= 1024)
-    hipLaunchKernelGGL(rows_pack_kernel<2>, grid, block, 0, stream, xp, ldx, mi, ki, eps, nz, op);
+    hipLaunchKernelGGL(rows_pack_kernel<2>, grid, block, 0, stream, xp, ldx, mi, ki, eps, nz, op, stats);
   else if (k <= 2048)
-    hipLaunchKernelGGL(rows_pack_kernel<4>, grid, block, 0, stream, xp, ldx, mi, ki, eps, nz, op);
+    hipLaunchKernelGGL(rows_pack_kernel<4>, grid, block, 0, stream, xp, ldx, mi, ki, eps, nz, op, stats);
   else if (k <= 4096)
-    hipLaunchKernelGGL(rows_pack_kernel<8>, grid, block, 0, stream, xp, ldx, mi, ki, eps, nz, op);
+    hipLaunchKernelGGL(rows_pack_kernel<8>, grid, block, 0, stream, xp, ldx, mi, ki, eps, nz, op, stats);
   else if (k <= 8192)
-    hipLaunchKernelGGL(rows_pack_kernel<16>, grid, block, 0, stream, xp, ldx, mi, ki, eps, nz, op);
+    hipLaunchKernelGGL(rows_pack_kernel<16>, grid, block, 0, stream, xp, ldx, mi, ki, eps, nz, op, stats);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -936,13 +1157,15 @@ extern "C" int64_t rldx_grouped_gemm_workspace_bytes(const rldx_gemm_group_t* gr
 
 namespace {
 hipError_t gemm_ws(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, int64_t k, int32_t epilogue,
-                   int32_t split_k, int32_t flags, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+                   int32_t split_k, int32_t flags, void* workspace, int64_t workspace_bytes, hipStream_t stream,
+                   float* const* stats_out = nullptr) {
   GemmArgs args;
   int64_t ws, co[3], po[3];
   if (epilogue == kEpiQkv || (flags & ~(RLDX_GEMM_WIDE_TILES | RLDX_GEMM_SPLITS_ACROSS_XCDS)))
     return hipErrorInvalidValue;
   const bool wide = (flags & RLDX_GEMM_WIDE_TILES) != 0;
-  const hipError_t e = plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po, nullptr, wide);
+  const hipError_t e = plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po, nullptr, wide, nullptr,
+                            nullptr, stats_out);
   if (e != hipSuccess) return e;
   args.spread = (flags & RLDX_GEMM_SPLITS_ACROSS_XCDS) != 0;
   if (ws > 0) {
@@ -998,12 +1221,26 @@ extern "C" hipError_t rldx_layernorm_pack_bf16(const void* x, int64_t ldx, int64
   return rows_pack(x, ldx, m, k, eps, true, packed, stream);
 }
 
-extern "C" hipError_t rldx_grouped_gemm_qkv_norm_rope_bf16(const rldx_gemm_group_t* groups,
-                                                           const rldx_msat_stream_t* norms, int32_t num_groups,
-                                                           int64_t heads, int64_t head_dim, int64_t k, void* q_out,
-                                                           int64_t q_head_stride, int64_t q_row_stride,
-                                                           void* kv_packed, int64_t kv_packed_head_stride, float eps,
-                                                           hipStream_t stream) {
+extern "C" hipError_t rldx_act_pack_stats_bf16(const void* x, int64_t ldx, int64_t m, int64_t k, void* packed,
+                                               float* ln_stats, hipStream_t stream) {
+  if (!ln_stats) return hipErrorInvalidValue;
+  return rows_pack(x, ldx, m, k, 0.f, false, packed, stream, ln_stats);
+}
+
+extern "C" hipError_t rldx_grouped_gemm_stats_bf16(const rldx_gemm_group_t* groups, float* const* ln_stats_out,
+                                                   int32_t num_groups, int64_t n, int64_t k, int32_t epilogue,
+                                                   int32_t split_k, int32_t flags, void* workspace,
+                                                   int64_t workspace_bytes, hipStream_t stream) {
+  if (!ln_stats_out) return hipErrorInvalidValue;
+  return gemm_ws(groups, num_groups, n, k, epilogue, split_k, flags, workspace, workspace_bytes, stream,
+                 ln_stats_out);
+}
+
+namespace {
+hipError_t gemm_qkv(const rldx_gemm_group_t* groups, const rldx_msat_stream_t* norms, int32_t num_groups,
+                    int64_t heads, int64_t head_dim, int64_t k, void* q_out, int64_t q_head_stride,
+                    int64_t q_row_stride, void* kv_packed, int64_t kv_packed_head_stride, float eps,
+                    const float* const* w_row_sums, const float* const* ln_stats, float ln_eps, hipStream_t stream) {
   if (!groups || !norms || num_groups < 1 || num_groups > 3) return hipErrorInvalidValue;
   if (head_dim != 128 || heads <= 0 || heads > 4096) return hipErrorInvalidValue;
   if (!q_out || !kv_packed || !a16(q_out) || !a16(kv_packed)) return hipErrorInvalidValue;
@@ -1029,11 +1266,51 @@ extern "C" hipError_t rldx_grouped_gemm_qkv_norm_rope_bf16(const rldx_gemm_group
   }
   if (m == 0) return hipSuccess;
   if (kv_packed_head_stride < (m + 31) / 32 * 64 * head_dim) return hipErrorInvalidValue;
+  if (w_row_sums && !(ln_eps >= 0.f)) return hipErrorInvalidValue;
   GemmArgs args;
   int64_t ws, co[3], po[3];
-  const hipError_t e = plan(groups, num_groups, 3 * heads * head_dim, k, kEpiQkv, 1, args, &ws, co, po, norms);
+  const hipError_t e = plan(groups, num_groups, 3 * heads * head_dim, k, kEpiQkv, 1, args, &ws, co, po, norms, false,
+                            w_row_sums, ln_stats);
   if (e != hipSuccess) return e;
   args.qkv = QkvOut{static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(kv_packed), q_head_stride, q_row_stride,
                     kv_packed_head_stride, static_cast<int>(heads * head_dim), eps};
-  return launch(args, kEpiQkv, stream);
+  args.ln_eps = ln_eps;
+  return launch(args, kEpiQkv, stream, true, w_row_sums != nullptr);
+}
+}  // namespace
+
+extern "C" hipError_t rldx_grouped_gemm_qkv_norm_rope_bf16(const rldx_gemm_group_t* groups,
+                                                           const rldx_msat_stream_t* norms, int32_t num_groups,
+                                                           int64_t heads, int64_t head_dim, int64_t k, void* q_out,
+                                                           int64_t q_head_stride, int64_t q_row_stride,
+                                                           void* kv_packed, int64_t kv_packed_head_stride, float eps,
+                                                           hipStream_t stream) {
+  return gemm_qkv(groups, norms, num_groups, heads, head_dim, k, q_out, q_head_stride, q_row_stride, kv_packed,
+                  kv_packed_head_stride, eps, nullptr, nullptr, 0.f, stream);
+}
+
+extern "C" hipError_t rldx_grouped_gemm_qkv_norm_rope_ln_bf16(
+    const rldx_gemm_group_t* groups, const rldx_msat_stream_t* norms, const float* const* w_row_sums,
+    const float* const* ln_stats, int32_t num_groups, int64_t heads, int64_t head_dim, int64_t k, void* q_out,
+    int64_t q_head_stride, int64_t q_row_stride, void* kv_packed, int64_t kv_packed_head_stride, float eps,
+    float ln_eps, hipStream_t stream) {
+  if (!w_row_sums || !ln_stats) return hipErrorInvalidValue;
+  return gemm_qkv(groups, norms, num_groups, heads, head_dim, k, q_out, q_head_stride, q_row_stride, kv_packed,
+                  kv_packed_head_stride, eps, w_row_sums, ln_stats, ln_eps, stream);
+}
+
+extern "C" hipError_t rldx_grouped_gemm_ln_bf16(const rldx_gemm_group_t* groups, const float* const* w_row_sums,
+                                                const float* const* ln_stats, int32_t num_groups, int64_t n,
+                                                int64_t k, int32_t epilogue, int32_t flags, float ln_eps,
+                                                hipStream_t stream) {
+  GemmArgs args;
+  int64_t ws, co[3], po[3];
+  if (!w_row_sums || !ln_stats || !(ln_eps >= 0.f) || epilogue == kEpiQkv || (flags & ~RLDX_GEMM_WIDE_TILES))
+    return hipErrorInvalidValue;
+  const bool wide = (flags & RLDX_GEMM_WIDE_TILES) != 0;
+  const hipError_t e = plan(groups, num_groups, n, k, epilogue, 1, args, &ws, co, po, nullptr, wide, w_row_sums,
+                            ln_stats);
+  if (e != hipSuccess) return e;
+  args.ln_eps = ln_eps;
+  return launch(args, epilogue, stream, wide, true);
 }

@@ -106,6 +106,14 @@ SIGNATURES = {
     "rldx_grouped_gemm_qkv_norm_rope_bf16": (c_i32, [ctypes.POINTER(GemmGroup), ctypes.POINTER(MsatStream), c_i32,
                                                      c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_f32,
                                                      c_vp]),
+    "rldx_grouped_gemm_ln_bf16": (c_i32, [ctypes.POINTER(GemmGroup), ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), c_i32,
+                                          c_i64, c_i64, c_i32, c_i32, c_f32, c_vp]),
+    "rldx_grouped_gemm_qkv_norm_rope_ln_bf16": (c_i32, [ctypes.POINTER(GemmGroup), ctypes.POINTER(MsatStream),
+                                                        ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), c_i32, c_i64, c_i64,
+                                                        c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_f32, c_f32, c_vp]),
+    "rldx_grouped_gemm_stats_bf16": (c_i32, [ctypes.POINTER(GemmGroup), ctypes.POINTER(c_vp), c_i32, c_i64, c_i64,
+                                             c_i32, c_i32, c_i32, c_vp, c_i64, c_vp]),
+    "rldx_act_pack_stats_bf16": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp]),
     "rldx_host_swiglu_bf16": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64]),
     "rldx_grouped_res_ln_bf16": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                          c_i64, c_i64, c_i64, c_i64, c_f32, c_vp]),
@@ -116,6 +124,7 @@ SIGNATURES = {
 
 ROPE_SIN_SIGNED = 1  # RLDX_ROPE_SIN_SIGNED
 GEMM_EPI_BIAS, GEMM_EPI_RESIDUAL, GEMM_EPI_SWIGLU, GEMM_EPI_SWIGLU_PACKED, GEMM_EPI_BIAS_PACKED = 0, 1, 2, 3, 4
+GEMM_EPI_RESIDUAL_PACKED = 5
 GEMM_WIDE_TILES = 1  # RLDX_GEMM_WIDE_TILES
 GEMM_SPLITS_ACROSS_XCDS = 2  # RLDX_GEMM_SPLITS_ACROSS_XCDS
 

@@ -493,12 +493,14 @@ def memory_attention(qkv: torch.Tensor, cos: torch.Tensor, signed_sin: torch.Ten
 # grouped GEMM (MSAT block linears)
 # ---------------------------------------------------------------------------
 class PackedWeight:
-    """A weight W [n, k] bf16 packed once into the grouped GEMM's operand order."""
+    """A weight W [n, k] bf16 packed once into the grouped GEMM's operand order,
+    with its fp32 row sums s[j] = sum_k W[j][k] (original row order), which a
+    GEMM with the LayerNorm fold needs."""
 
-    __slots__ = ("data", "n", "k", "swiglu_pairs")
+    __slots__ = ("data", "n", "k", "swiglu_pairs", "row_sums")
 
-    def __init__(self, data: torch.Tensor, n: int, k: int, swiglu_pairs: bool):
-        self.data, self.n, self.k, self.swiglu_pairs = data, n, k, swiglu_pairs
+    def __init__(self, data: torch.Tensor, n: int, k: int, swiglu_pairs: bool, row_sums: Optional[torch.Tensor] = None):
+        self.data, self.n, self.k, self.swiglu_pairs, self.row_sums = data, n, k, swiglu_pairs, row_sums
 
 
 def pack_weight(w: torch.Tensor, swiglu_pairs: bool = False) -> PackedWeight:
@@ -512,7 +514,7 @@ def pack_weight(w: torch.Tensor, swiglu_pairs: bool = False) -> PackedWeight:
     lib = _lib.load()
     _lib.check(lib.rldx_gemm_pack_weight_bf16(w.data_ptr(), w.stride(0), n, k, int(swiglu_pairs), out.data_ptr(),
                                               _stream_ptr(w)), "rldx_gemm_pack_weight_bf16")
-    return PackedWeight(out, n, k, swiglu_pairs)
+    return PackedWeight(out, n, k, swiglu_pairs, w.float().sum(dim=1).contiguous())
 
 
 class PackedAct:
@@ -551,14 +553,33 @@ class PackedAct:
         return t.permute(0, 3, 1, 2, 4).reshape(mp * 32, k)[:m]
 
 
-def pack_act(x: torch.Tensor, out: Optional[PackedAct] = None) -> PackedAct:
-    """Row-major x [m, k] -> PackedAct."""
+def ln_stats_empty(m: int, k: int, device) -> torch.Tensor:
+    """LayerNorm statistics of m rows of width k for a LayerNorm-folding GEMM:
+    fp32 [k / 64, m, 2], (sum, sum of squares) per 64-column slot, slot-major."""
+    _require(k % 64 == 0, "k must be a multiple of 64")
+    return torch.empty(k // 64, m, 2, dtype=F32, device=device)
+
+
+def _check_stats(st: torch.Tensor, m: int, k: int) -> None:
+    _on_gpu(st)
+    _require(st.dtype == F32 and tuple(st.shape) == (k // 64, m, 2) and st.is_contiguous(),
+             "LayerNorm statistics must be contiguous fp32 [k / 64, m, 2]")
+
+
+def pack_act(x: torch.Tensor, out: Optional[PackedAct] = None, stats: Optional[torch.Tensor] = None) -> PackedAct:
+    """Row-major x [m, k] -> PackedAct; with `stats` ([k / 64, m, 2] fp32) also the
+    rows' LayerNorm statistics (rldx_act_pack_stats_bf16)."""
     _on_gpu(x)
     _require(x.dtype == BF16 and x.dim() == 2 and x.stride(1) == 1, "x must be 2-D bf16, rows contiguous")
     m, k = x.shape
     out = PackedAct.empty(m, k, x.device) if out is None else out
     _require(out.m == m and out.k == k, "out shape mismatch")
     lib = _lib.load()
+    if stats is not None:
+        _check_stats(stats, m, k)
+        _lib.check(lib.rldx_act_pack_stats_bf16(x.data_ptr(), x.stride(0), m, k, out.data.data_ptr(),
+                                                stats.data_ptr(), _stream_ptr(x)), "rldx_act_pack_stats_bf16")
+        return out
     _lib.check(lib.rldx_act_pack_bf16(x.data_ptr(), x.stride(0), m, k, out.data.data_ptr(), _stream_ptr(x)),
                "rldx_act_pack_bf16")
     return out
@@ -593,8 +614,9 @@ class GemmWorkspace:
 
 
 _GEMM_EPI = {"bias": _lib.GEMM_EPI_BIAS, "residual": _lib.GEMM_EPI_RESIDUAL, "swiglu": _lib.GEMM_EPI_SWIGLU,
-             "swiglu_packed": _lib.GEMM_EPI_SWIGLU_PACKED, "bias_packed": _lib.GEMM_EPI_BIAS_PACKED}
-_PACKED_EPI = (_lib.GEMM_EPI_SWIGLU_PACKED, _lib.GEMM_EPI_BIAS_PACKED)
+             "swiglu_packed": _lib.GEMM_EPI_SWIGLU_PACKED, "bias_packed": _lib.GEMM_EPI_BIAS_PACKED,
+             "residual_packed": _lib.GEMM_EPI_RESIDUAL_PACKED}
+_PACKED_EPI = (_lib.GEMM_EPI_SWIGLU_PACKED, _lib.GEMM_EPI_BIAS_PACKED, _lib.GEMM_EPI_RESIDUAL_PACKED)
 
 
 def _gemm_groups(items: Sequence[tuple], epi: int, pack: bool):
@@ -610,7 +632,7 @@ def _gemm_groups(items: Sequence[tuple], epi: int, pack: bool):
             else:
                 a = pack_act(a)
                 keep.append(a)
-        _on_gpu(a.data, w.data, bias, res)
+        _on_gpu(a.data, w.data, bias, res if isinstance(res, torch.Tensor) else None)
         _require(w.n == n and w.k == k and a.k == k and a.ld == k, "groups must share n and k")
         swiglu = epi in (_lib.GEMM_EPI_SWIGLU, _lib.GEMM_EPI_SWIGLU_PACKED)
         _require(not swiglu or w.swiglu_pairs, "SwiGLU epilogue needs a swiglu_pairs weight")
@@ -626,12 +648,16 @@ def _gemm_groups(items: Sequence[tuple], epi: int, pack: bool):
             out_ptr, ldo = out.data_ptr(), out.stride(0)
         if bias is not None:
             _require(bias.dtype == BF16 and bias.is_contiguous() and bias.numel() == n, "bias must be [n] bf16")
+        res_ptr, ldr = None, 0
         if epi == _lib.GEMM_EPI_RESIDUAL:
             _require(res is not None and res.dtype == BF16 and res.dim() == 2 and res.stride(1) == 1 and
                      tuple(res.shape) == (m, n), "residual must be [m, n] bf16")
-        groups[i] = _lib.GemmGroup(a.data.data_ptr(), m, w.data.data_ptr(), _ptr(bias), out_ptr, ldo,
-                                   _ptr(res) if epi == _lib.GEMM_EPI_RESIDUAL else None,
-                                   res.stride(0) if epi == _lib.GEMM_EPI_RESIDUAL else 0)
+            res_ptr, ldr = res.data_ptr(), res.stride(0)
+        elif epi == _lib.GEMM_EPI_RESIDUAL_PACKED:
+            _require(isinstance(res, PackedAct) and res.m == m and res.k == n, "residual must be a PackedAct [m, n]")
+            _on_gpu(res.data)
+            res_ptr, ldr = res.data.data_ptr(), (0 if res.ld == res.k else res.ld)
+        groups[i] = _lib.GemmGroup(a.data.data_ptr(), m, w.data.data_ptr(), _ptr(bias), out_ptr, ldo, res_ptr, ldr)
     return groups, n, k, keep, w.data
 
 
@@ -646,9 +672,32 @@ def grouped_gemm_workspace_bytes(items: Sequence[tuple], epilogue: str = "bias",
     return int(r)
 
 
+def _row_sums_array(items: Sequence[tuple]):
+    sums = (ctypes.c_void_p * len(items))()
+    for i, it in enumerate(items):
+        w = it[1]
+        _require(w.row_sums is not None and w.row_sums.dtype == F32 and w.row_sums.numel() == w.n,
+                 "the LayerNorm fold needs the weight's fp32 row sums")
+        _on_gpu(w.row_sums)
+        sums[i] = w.row_sums.data_ptr()
+    return sums
+
+
+def _stats_array(items: Sequence[tuple], stats: Sequence[torch.Tensor], width: int):
+    _require(len(stats) == len(items), "one statistics tensor per group")
+    arr = (ctypes.c_void_p * len(items))()
+    for i, (it, st) in enumerate(zip(items, stats)):
+        a = it[0]
+        _check_stats(st, a.m if isinstance(a, PackedAct) else a.shape[0], width)
+        arr[i] = st.data_ptr()
+    return arr
+
+
 def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias", split_k: int = 1,
                  workspace: Optional[GemmWorkspace] = None, wide_tiles: bool = False,
-                 splits_across_xcds: bool = False) -> None:
+                 splits_across_xcds: bool = False, ln_eps: Optional[float] = None,
+                 ln_stats: Optional[Sequence[torch.Tensor]] = None,
+                 stats_out: Optional[Sequence[torch.Tensor]] = None) -> None:
     """One launch of y_s = a_s W_s^T + bias_s for up to 3 streams sharing n and k.
     items: (a PackedAct [m, k] or row-major tensor (packed first), PackedWeight,
     bias [n] or None, out, residual or None).  epilogue: "bias" (out = y),
@@ -660,10 +709,35 @@ def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias", split_k: int = 
     bytes.  wide_tiles: 64 x 128 / 32 x 128 tiles for the streams below the 128 x
     128 threshold (RLDX_GEMM_WIDE_TILES; the same results, faster or slower by
     shape).  splits_across_xcds: the splits of each tile on different XCDs
-    (RLDX_GEMM_SPLITS_ACROSS_XCDS; the same results, for tests)."""
+    (RLDX_GEMM_SPLITS_ACROSS_XCDS; the same results, for tests).
+    ln_eps, ln_stats: the LayerNorm fold (rldx_grouped_gemm_ln_bf16): each a is
+    the un-normalised rows x, ln_stats[i] their statistics ([k / 64, m, 2], from
+    a `stats_out` or pack_act(..., stats=)), and the result is LN(x) W^T (+ bias
+    ...), LN without affine parameters with this eps; epilogues "bias" and
+    "swiglu_packed", no split-K; the weights' row sums come from pack_weight.
+    stats_out: the residual epilogues also write the statistics of the rows
+    they store, stats_out[i] [n / 64, m, 2] (rldx_grouped_gemm_stats_bf16)."""
     epi = _GEMM_EPI[epilogue]
     groups, n, k, keep, wt = _gemm_groups(items, epi, pack=True)
     lib = _lib.load()
+    if ln_eps is not None:
+        _require(split_k <= 1 and not splits_across_xcds, "the LayerNorm fold does not split K")
+        _require(ln_stats is not None and stats_out is None, "the LayerNorm fold needs ln_stats")
+        sums = _row_sums_array(items)
+        stats = _stats_array(items, ln_stats, k)
+        _lib.check(lib.rldx_grouped_gemm_ln_bf16(groups, sums, stats, len(items), n, k, epi,
+                                                 _lib.GEMM_WIDE_TILES if wide_tiles else 0, float(ln_eps),
+                                                 _stream_ptr(wt)), "rldx_grouped_gemm_ln_bf16")
+        return
+    if stats_out is not None:
+        _require(epilogue in ("residual", "residual_packed"), "stats_out needs a residual epilogue")
+        outs = _stats_array(items, stats_out, n)
+        _require(split_k <= 1 or workspace is not None, "split_k > 1 needs a GemmWorkspace")
+        ws_ptr, ws_n = (workspace.data.data_ptr(), workspace.data.numel()) if split_k > 1 else (None, 0)
+        flags = (_lib.GEMM_WIDE_TILES if wide_tiles else 0) | (_lib.GEMM_SPLITS_ACROSS_XCDS if splits_across_xcds else 0)
+        _lib.check(lib.rldx_grouped_gemm_stats_bf16(groups, outs, len(items), n, k, epi, int(split_k), flags, ws_ptr,
+                                                    ws_n, _stream_ptr(wt)), "rldx_grouped_gemm_stats_bf16")
+        return
     flags = (_lib.GEMM_WIDE_TILES if wide_tiles else 0) | (_lib.GEMM_SPLITS_ACROSS_XCDS if splits_across_xcds else 0)
     if flags:
         _require(split_k <= 1 or workspace is not None, "split_k > 1 needs a GemmWorkspace")
@@ -682,7 +756,8 @@ def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias", split_k: int = 
 
 
 def grouped_gemm_qkv_norm_rope(items: Sequence[tuple], norms: Sequence[StreamSpec], num_heads: int,
-                               head_dim: int, eps: float = 1e-6, out: Optional[tuple] = None):
+                               head_dim: int, eps: float = 1e-6, out: Optional[tuple] = None,
+                               ln_eps: Optional[float] = None, ln_stats: Optional[Sequence[torch.Tensor]] = None):
     """The QKV linears of 1-3 streams (joint-sequence order) with the QK RMSNorm +
     RoPE + K/V tiling of `msat_qkv_norm_rope` in the GEMM epilogue: one launch,
     the same bits as grouped_gemm(items, "bias") followed by
@@ -690,7 +765,9 @@ def grouped_gemm_qkv_norm_rope(items: Sequence[tuple], norms: Sequence[StreamSpe
     PackedWeight [3 H D, k], bias [3 H D] or None); norms: one StreamSpec per item
     (norm weights and tables; its qkv is not read, pass None).  Every stream but
     the last has rows % 32 == 0.  Returns (q (H, M, D), kvp (H, kv_packed_elems(M,
-    D))); `out` gives them."""
+    D))); `out` gives them.  ln_eps, ln_stats: with the LayerNorm fold (each a
+    the un-normalised rows, ln_stats their statistics;
+    rldx_grouped_gemm_qkv_norm_rope_ln_bf16)."""
     _require(1 <= len(items) <= 3 and len(norms) == len(items), "1-3 groups, one StreamSpec each")
     _require(head_dim == 128, "the fused QKV epilogue needs head_dim 128")
     inner = num_heads * head_dim
@@ -720,6 +797,15 @@ def grouped_gemm_qkv_norm_rope(items: Sequence[tuple], norms: Sequence[StreamSpe
         _require(q.dtype == BF16 and q.shape == (num_heads, M, head_dim) and q.stride(2) == 1, "q out must be (H, M, D)")
         _check_kvp_out(kvp, num_heads, M, head_dim)
     _on_gpu(q, kvp)
+    if ln_eps is not None:
+        _require(ln_stats is not None, "the LayerNorm fold needs ln_stats")
+        sums = _row_sums_array(items)
+        stats = _stats_array(items, ln_stats, k)
+        _lib.check(_lib.load().rldx_grouped_gemm_qkv_norm_rope_ln_bf16(
+            groups, descs, sums, stats, len(items), num_heads, head_dim, k, q.data_ptr(), q.stride(0), q.stride(1),
+            kvp.data_ptr(), kvp.stride(0), float(eps), float(ln_eps), _stream_ptr(q)),
+            "rldx_grouped_gemm_qkv_norm_rope_ln_bf16")
+        return q, kvp
     _lib.check(_lib.load().rldx_grouped_gemm_qkv_norm_rope_bf16(
         groups, descs, len(items), num_heads, head_dim, k, q.data_ptr(), q.stride(0), q.stride(1), kvp.data_ptr(),
         kvp.stride(0), float(eps), _stream_ptr(q)), "rldx_grouped_gemm_qkv_norm_rope_bf16")

@@ -150,25 +150,31 @@ class MsatActionStep:
     """Static-buffer executor of one action step; `run()` launches it eagerly,
     `capture()` records the same launches into one hipGraph.
 
-    Per block, every launch covers all three streams:
-        LayerNorm -> packed h          rldx_layernorm_pack_bf16
-        QKV linears (+ bias) with      rldx_grouped_gemm_qkv_norm_rope_bf16
-          QK-RMSNorm + RoPE, K/V tiles   (fused_qkv=False: rldx_grouped_gemm_bf16,
-                                          then rldx_msat_qkv_norm_rope_bf16)
+    Per block (ln_fold=True, the default), 5 launches, each covering all three
+    streams; the residual stream x stays in the packed activation order:
+        QKV linears of LN(x) (+ bias)  rldx_grouped_gemm_qkv_norm_rope_ln_bf16:
+          with QK-RMSNorm + RoPE,        the pre-LayerNorm folded into the GEMM
+          K/V tiles                      (row statistics from the A chunks it streams)
         joint attention -> packed o    rldx_attention_packed_fwd_bf16
-        Proj linears, x += (in place)  rldx_grouped_gemm_bf16 (residual epilogue)
-        LayerNorm -> packed h
-        W12 linears + SwiGLU -> packed rldx_grouped_gemm_bf16 (SwiGLU epilogue)
-        W3 linears, x += (in place)    rldx_grouped_gemm_bf16 (residual epilogue)
+        Proj linears, x += (in place)  rldx_grouped_gemm_bf16 (packed residual epilogue)
+        W12 linears of LN(x) + SwiGLU  rldx_grouped_gemm_ln_bf16 (SwiGLU epilogue)
+        W3 linears, x += (in place)    rldx_grouped_gemm_bf16 (packed residual epilogue)
+    ln_fold=False runs the eager rounding of the pre-norm instead: x row-major,
+    LayerNorm -> packed h (rldx_layernorm_pack_bf16) before the QKV and W12
+    GEMMs (7 launches per block).  fused_qkv=False splits the QKV launch into
+    rldx_grouped_gemm_bf16 (or _ln_bf16) and rldx_msat_qkv_norm_rope_bf16.
     The weights are packed once, at construction, into the GEMM's operand order."""
 
-    def __init__(self, cfg: MsatStepCfg, weights: dict, inputs: dict, fused_qkv: bool = True):
+    def __init__(self, cfg: MsatStepCfg, weights: dict, inputs: dict, fused_qkv: bool = True, ln_fold: bool = True):
         self.cfg, self.w, self.inp = cfg, weights, inputs
-        self.fused_qkv = fused_qkv
+        self.fused_qkv, self.ln_fold = fused_qkv, ln_fold
         dev = inputs["vl"].device
         n, d, H, D = cfg.tokens, cfg.hidden, cfg.heads, cfg.head_dim
         e = lambda *s: torch.empty(*s, dtype=BF16, device=dev)  # noqa: E731
-        self.x = e(n, d)            # residual stream, rows VL | SA | P
+        self.x = e(n, d)            # residual stream, rows VL | SA | P (with ln_fold: the row-major staging of
+        self.xp = Fn.PackedAct.empty(n, d, dev)  # each iteration's inputs; the stream itself is xp, packed)
+        # LayerNorm statistics of each stream's rows of xp (written by their producers)
+        self.xst = {s: Fn.ln_stats_empty(cfg.rows(s).stop - cfg.rows(s).start, d, dev) for s in STREAMS}
         self.qkv = e(n, 3 * cfg.inner)
         self.q = e(H, n, D)
         self.kvp = e(H, Fn.kv_packed_elems(n, D))  # K/V in the attention kernel's packed tiles
@@ -185,10 +191,25 @@ class MsatActionStep:
                                           for L in range(cfg.blocks)]
         self.graph = None
 
+    def _stats(self) -> list:
+        return [self.xst[s] for s in STREAMS]
+
     def _gemms(self, L: int) -> dict:
         """The four grouped GEMMs of block L: (items, epilogue)."""
         cfg, w, pw = self.cfg, self.w, self.pw
         rows = [(s, cfg.rows(s)) for s in STREAMS]
+        if self.ln_fold:
+            xp = self.xp
+            return {
+                "qkv": ([(xp.rows(r.start, r.stop), pw[f"{s}.qkv"][L], w[f"{s}.qkv.b"][L], self.qkv[r], None)
+                         for s, r in rows], "bias"),
+                "proj": ([(self.att.rows(r.start, r.stop), pw[f"{s}.proj"][L], w[f"{s}.proj.b"][L],
+                           xp.rows(r.start, r.stop), xp.rows(r.start, r.stop)) for s, r in rows], "residual_packed"),
+                "w12": ([(xp.rows(r.start, r.stop), pw[f"{s}.w12"][L], w[f"{s}.w12.b"][L],
+                          self.gl.rows(r.start, r.stop), None) for s, r in rows], "swiglu_packed"),
+                "w3": ([(self.gl.rows(r.start, r.stop), pw[f"{s}.w3"][L], w[f"{s}.w3.b"][L],
+                         xp.rows(r.start, r.stop), xp.rows(r.start, r.stop)) for s, r in rows], "residual_packed"),
+            }
         return {
             "qkv": ([(self.h.rows(r.start, r.stop), pw[f"{s}.qkv"][L], w[f"{s}.qkv.b"][L], self.qkv[r], None)
                      for s, r in rows], "bias"),
@@ -204,7 +225,9 @@ class MsatActionStep:
     def _block(self, L: int) -> None:
         cfg, w = self.cfg, self.w
         gemm = self._gemms(L)
-        Fn.layernorm_pack(self.x, cfg.eps, out=self.h)
+        ln = cfg.eps if self.ln_fold else None
+        if not self.ln_fold:
+            Fn.layernorm_pack(self.x, cfg.eps, out=self.h)
         specs = [
             Fn.StreamSpec(self.qkv[cfg.rows("vl")], w["vl.q_norm"][L], w["vl.k_norm"][L]),
             Fn.StreamSpec(self.qkv[cfg.rows("sa")], w["sa.q_norm"][L], w["sa.k_norm"][L],
@@ -212,18 +235,21 @@ class MsatActionStep:
             Fn.StreamSpec(self.qkv[cfg.rows("p")], w["p.q_norm"][L], w["p.k_norm"][L],
                           self.inp["p_cos"], self.inp["p_sin"]),
         ]
+        st = self._stats() if self.ln_fold else None
         if self.fused_qkv:
             items = [(a, wt, b) for a, wt, b, _, _ in gemm["qkv"][0]]
-            Fn.grouped_gemm_qkv_norm_rope(items, specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp))
+            Fn.grouped_gemm_qkv_norm_rope(items, specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp),
+                                          ln_eps=ln, ln_stats=st)
         else:
-            Fn.grouped_gemm(*gemm["qkv"])
+            Fn.grouped_gemm(*gemm["qkv"], ln_eps=ln, ln_stats=st)
             Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
         Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), cfg.tokens, key_bias=self.inp["key_bias"],
                             out=self.att)
-        Fn.grouped_gemm(*gemm["proj"])
-        Fn.layernorm_pack(self.x, cfg.eps, out=self.h)
-        Fn.grouped_gemm(*gemm["w12"])
-        Fn.grouped_gemm(*gemm["w3"])
+        Fn.grouped_gemm(*gemm["proj"], stats_out=st)
+        if not self.ln_fold:
+            Fn.layernorm_pack(self.x, cfg.eps, out=self.h)
+        Fn.grouped_gemm(*gemm["w12"], ln_eps=ln, ln_stats=st)
+        Fn.grouped_gemm(*gemm["w3"], stats_out=st)
 
     # -- one action step ------------------------------------------------------
     def run(self, steps: int | None = None, blocks: int | None = None) -> torch.Tensor:
@@ -235,15 +261,24 @@ class MsatActionStep:
         sa = cfg.rows("sa")
         self.act.copy_(inp["x0"])
         dt = 1.0 / cfg.steps
-        for t in range(steps):
+        if self.ln_fold:  # the VL and P rows of the staging buffer stay as they are
             self.x[cfg.rows("vl")].copy_(inp["vl"])
             self.x[cfg.rows("p")].copy_(inp["p"])
+        for t in range(steps):
+            if not self.ln_fold:
+                self.x[cfg.rows("vl")].copy_(inp["vl"])
+                self.x[cfg.rows("p")].copy_(inp["p"])
             torch.addmm(w["act_in.b"], self.act, w["act_in.w"].t(), out=self.sa_in)
             self.sa_in.add_(inp["temb"][t])
             torch.add(self.sa_in, inp["pos"], out=self.x[sa])
+            if self.ln_fold:
+                for s in STREAMS:
+                    r = cfg.rows(s)
+                    Fn.pack_act(self.x[r], out=self.xp.rows(r.start, r.stop), stats=self.xst[s])
             for L in range(blocks):
                 self._block(L)
-            hs = F.layer_norm(self.x[sa], (cfg.hidden,), eps=cfg.eps)
+            x_sa = self.xp.rows(sa.start, sa.stop).unpack() if self.ln_fold else self.x[sa]
+            hs = F.layer_norm(x_sa, (cfg.hidden,), eps=cfg.eps)
             torch.addmm(w["act_out.b"], hs, w["act_out.w"].t(), out=self.vel)
             self.vel.mul_(dt)
             self.act.add_(self.vel)

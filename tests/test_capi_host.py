@@ -145,6 +145,9 @@ def test_capi_rejects_bad_arguments_without_launching():
     assert lib.rldx_llm_fused_attention_workspace_bytes(1280, 4, 128) == 4 * 40 * 64 * 128 * 2
 
 
+QKV_INTERNAL = 16  # the fused QKV epilogue's internal code: only rldx_grouped_gemm_qkv_norm_rope_bf16 takes it
+
+
 def _gemm_groups(ms, a_ptr=256, w_ptr=512, out_ptr=1024, ldo=8192):
     groups = (_lib.GemmGroup * len(ms))()
     for i, m in enumerate(ms):
@@ -192,7 +195,7 @@ def test_grouped_gemm_wide_tiles_plan():
     # RLDX_GEMM_SPLITS_ACROSS_XCDS moves workgroups, not partials: the same workspace
     assert lib.rldx_grouped_gemm_ex_workspace_bytes(_gemm_groups(msat), 3, 1536, 4096, 1, 8, 3) == wide
     assert lib.rldx_grouped_gemm_ex_workspace_bytes(_gemm_groups(msat), 3, 1536, 4096, 1, 8, 4) == -1
-    assert lib.rldx_grouped_gemm_ex_workspace_bytes(_gemm_groups(msat), 3, 4608, 1536, 5, 1, 1) == -1
+    assert lib.rldx_grouped_gemm_ex_workspace_bytes(_gemm_groups(msat), 3, 4608, 1536, QKV_INTERNAL, 1, 1) == -1
     assert lib.rldx_grouped_gemm_ex_bf16(_gemm_groups(msat), 3, 1536, 4096, 1, 1, 4, None, 0, None) == HIP_INVALID_VALUE
     assert lib.rldx_grouped_gemm_ex_bf16(_gemm_groups(msat), 3, 1536, 4096, 1, 8, 1, 4096, wide - 256,
                                          None) == HIP_INVALID_VALUE
@@ -225,8 +228,8 @@ def test_grouped_gemm_qkv_norm_rope_rejections():
     assert call(qsm=132) == HIP_INVALID_VALUE                       # Q row stride % 8
     assert call(rope_ld=60) == HIP_INVALID_VALUE                    # RoPE rows shorter than head_dim / 2
     assert call(H=0) == HIP_INVALID_VALUE
-    assert lib.rldx_grouped_gemm_bf16(_gemm_groups(msat), 3, 4608, 1536, 5, None) == HIP_INVALID_VALUE
-    assert lib.rldx_grouped_gemm_workspace_bytes(_gemm_groups(msat), 3, 4608, 1536, 5, 1) == -1
+    assert lib.rldx_grouped_gemm_bf16(_gemm_groups(msat), 3, 4608, 1536, QKV_INTERNAL, None) == HIP_INVALID_VALUE
+    assert lib.rldx_grouped_gemm_workspace_bytes(_gemm_groups(msat), 3, 4608, 1536, QKV_INTERNAL, 1) == -1
 
 
 def test_vision_attention_workspace_and_rejections():
@@ -290,7 +293,8 @@ def test_packed_output_widths_validated():
     for bad in (5640, 4080, -16):  # not a multiple of 16, narrower than the output, negative
         g = _gemm_groups((82,), ldo=bad)
         assert lib.rldx_grouped_gemm_workspace_bytes(g, 1, 4096, 6144, 4, 1) == -1
-    assert lib.rldx_grouped_gemm_workspace_bytes(_gemm_groups((82,)), 1, 4096, 6144, 5, 1) == -1  # no epilogue 5
+    for bad_epi in (6, 15, 17, -1):  # no such epilogue
+        assert lib.rldx_grouped_gemm_workspace_bytes(_gemm_groups((82,)), 1, 4096, 6144, bad_epi, 1) == -1
     st = _lib.i64_array([0, 0, 0])
     ps = _lib.i64_array([0, 24 * 64 * 64 * 3])
     for bad in (-1, 1000, 1536 - 16):
@@ -330,3 +334,53 @@ def test_llm_attention_noalloc_rejects_sizes_beyond_its_scratch():
                                                     1e-6, None) == HIP_INVALID_VALUE
     assert lib.rldx_llm_fused_attention_noalloc_bf16(p, 48 * 128, p, p, p, p, 128, 1, p, 32 * 128, 1 << 20, 32, 8, 128,
                                                     1e-6, None) == HIP_INVALID_VALUE
+
+
+def test_residual_packed_epilogue_and_layernorm_fold_rejections():
+    """RLDX_GEMM_EPI_RESIDUAL_PACKED takes a packed residual (ldr 0 or a packed
+    width, % 16); the LayerNorm-fold entries need every group's row sums and
+    statistics, a non-negative eps, the bias / packed-SwiGLU / QKV epilogues,
+    k <= 2048 and no other flag than RLDX_GEMM_WIDE_TILES; statistics out need a
+    residual epilogue.  Checked before anything is launched."""
+    lib = _lib.load()
+    for ldr, ok in ((0, True), (1536, True), (3072, True), (1544, False), (1520, False), (-16, False)):
+        g = _gemm_groups((608,), ldo=0)
+        g[0].ldr = ldr
+        assert (lib.rldx_grouped_gemm_workspace_bytes(g, 1, 1536, 4096, _lib.GEMM_EPI_RESIDUAL_PACKED, 1) == 0) == ok
+    g = _gemm_groups((608,), ldo=0)
+    g[0].residual = None
+    assert lib.rldx_grouped_gemm_workspace_bytes(g, 1, 1536, 4096, _lib.GEMM_EPI_RESIDUAL_PACKED, 1) == -1
+    ptrs = lambda *p: (ctypes.c_void_p * len(p))(*p)  # noqa: E731
+    sums, stats = ptrs(4096, 8192, 12288), ptrs(16384, 20480, 24576)
+    missing, odd = ptrs(4096, None, 12288), ptrs(4096, 8194, 12288)
+    msat = (512, 64, 32)
+    call = lib.rldx_grouped_gemm_ln_bf16
+    bias = _lib.GEMM_EPI_BIAS
+    inval = HIP_INVALID_VALUE
+    assert call(_gemm_groups(msat), None, stats, 3, 4608, 1536, bias, 0, 1e-6, None) == inval
+    assert call(_gemm_groups(msat), sums, None, 3, 4608, 1536, bias, 0, 1e-6, None) == inval
+    assert call(_gemm_groups(msat), missing, stats, 3, 4608, 1536, bias, 0, 1e-6, None) == inval
+    assert call(_gemm_groups(msat), sums, missing, 3, 4608, 1536, bias, 0, 1e-6, None) == inval
+    assert call(_gemm_groups(msat), odd, stats, 3, 4608, 1536, bias, 0, 1e-6, None) == inval
+    assert call(_gemm_groups(msat), sums, ptrs(16384, 20484, 24576), 3, 4608, 1536, bias, 0, 1e-6, None) == inval
+    for epi in (_lib.GEMM_EPI_RESIDUAL, _lib.GEMM_EPI_SWIGLU, _lib.GEMM_EPI_BIAS_PACKED,
+                _lib.GEMM_EPI_RESIDUAL_PACKED, QKV_INTERNAL):
+        assert call(_gemm_groups(msat), sums, stats, 3, 8192, 1536, epi, 0, 1e-6, None) == inval
+    assert call(_gemm_groups(msat), sums, stats, 3, 4608, 1536, bias, 2, 1e-6, None) == inval  # flag 2
+    assert call(_gemm_groups(msat), sums, stats, 3, 4608, 1536, bias, 0, -1.0, None) == inval
+    assert call(_gemm_groups(msat), sums, stats, 3, 4608, 1000, bias, 0, 1e-6, None) == inval
+    assert call(_gemm_groups(msat), sums, stats, 3, 4608, 4096, bias, 0, 1e-6, None) == inval  # k > 2048
+    d = _msat_norms(msat)
+    qkv = lib.rldx_grouped_gemm_qkv_norm_rope_ln_bf16
+    for sm, st in ((None, stats), (sums, None), (missing, stats)):
+        assert qkv(_gemm_groups(msat), d, sm, st, 3, 12, 128, 1536, 1 << 20, 608 * 128, 128, 2 << 20,
+                   19 * 64 * 128, 1e-6, 1e-6, None) == inval
+    st_out = lib.rldx_grouped_gemm_stats_bf16
+    assert st_out(_gemm_groups(msat), None, 3, 1536, 4096, _lib.GEMM_EPI_RESIDUAL, 1, 0, None, 0, None) == inval
+    for epi in (bias, _lib.GEMM_EPI_SWIGLU_PACKED, _lib.GEMM_EPI_BIAS_PACKED):
+        assert st_out(_gemm_groups(msat), stats, 3, 1536, 4096, epi, 1, 0, None, 0, None) == inval
+    assert st_out(_gemm_groups(msat), missing, 3, 1536, 4096, _lib.GEMM_EPI_RESIDUAL, 1, 0, None, 0, None) == inval
+    pack = lib.rldx_act_pack_stats_bf16
+    assert pack(4096, 1536, 10, 1536, 8192, None, None) == inval
+    assert pack(4096, 1536, 10, 1552, 8192, 16384, None) == inval  # k % 64
+    assert pack(4096, 1536, 10, 1536, 8192, 16388, None) == inval  # stats alignment

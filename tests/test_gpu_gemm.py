@@ -255,6 +255,16 @@ def test_act_pack_roundtrip(dev, m, k):
         for c in (0, k - 1, k // 3):
             off = ((r // 32) * (k // 16) + c // 16) * 512 + ((r % 32) + 32 * ((c // 8) % 2)) * 8 + c % 8
             assert d[off] == x[r, c]
+    # with the LayerNorm statistics (rldx_act_pack_stats_bf16): the same packed bits;
+    # slot 0 the row's (sum, sum of squares), the other slots zero
+    st = torch.full((k // 64, m, 2), 7.0, device=dev)
+    p2 = Fn.pack_act(x.to(dev), stats=st)
+    assert torch.equal(p2.unpack(), p.unpack())
+    xd = x.double()
+    ref = torch.stack([xd.sum(-1), (xd * xd).sum(-1)], dim=-1)
+    stc = st.cpu().double()
+    assert (stc[0] - ref).abs().max().item() <= 1e-5 * ref.abs().max().item()
+    assert not stc[1:].any()
 
 
 @pytest.mark.parametrize("m,k", [(608, 1536), (7, 4096), (64, 512)])
@@ -421,3 +431,137 @@ def test_ss_fused_mlp_swiglu_op(dev):
     wd.mul_(0.5)  # in-place update -> repacked
     assert_bf16_close(torch.ops.ss.fused_mlp_swiglu(xd, wd, bd, 1), ref.swiglu(_linear_ref(x, (w.float() * 0.5).to(BF16), b)),
                       "after weight update")
+
+
+def _ln_ref(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """LayerNorm without affine parameters in fp64, not rounded (the folded GEMM
+    skips the bf16 rounding of the normalised rows)."""
+    x = x.double()
+    mu = x.mean(-1, keepdim=True)
+    return (x - mu) / torch.sqrt(x.var(-1, unbiased=False, keepdim=True) + eps)
+
+
+@pytest.mark.parametrize("epilogue,ms,n,k,wide,shift", [("bias", (512, 64, 32), 4608, 1536, False, 0.0),
+                                                        ("swiglu_packed", (512, 64, 32), 8192, 1536, False, 0.0),
+                                                        ("swiglu_packed", (82, 18), 12288, 1536, True, 0.0),
+                                                        ("bias", (300, 18), 4608, 2048, False, 0.0),
+                                                        ("bias", (96, 33), 1024, 512, False, 3.0),
+                                                        ("swiglu_packed", (20,), 256, 384, False, -2.0)])
+def test_grouped_gemm_layernorm_fold(dev, epilogue, ms, n, k, wide, shift):
+    """The pre-LayerNorm folded into the GEMM (rldx_grouped_gemm_ln_bf16): from the
+    un-normalised rows x and their statistics (rldx_act_pack_stats_bf16), the
+    result matches LN(x) W^T + b (LN in fp64, then the epilogue's eager rounding)
+    to the bf16 contract, also for rows whose mean is 3 or 2 standard deviations
+    away from 0 (E[x^2] - mean^2 in fp32), and it agrees with the eager path
+    (LayerNorm-pack, then the GEMM) to the same bound; tile shapes 128 x 128,
+    64 x 64, 32 x 64 and the wide 64 x 128 / 32 x 128, the largest K the fold
+    takes (2048, 8 statistics slots per thread at 128-row tiles)."""
+    g = torch.Generator().manual_seed(n + k + sum(ms))
+    swiglu = epilogue.startswith("swiglu")
+    n_out = n // 2 if swiglu else n
+    items, eager_items, refs, stats = [], [], [], []
+    for m in ms:
+        x = (_rand((m, k), g).float() + shift).to(BF16)
+        # |outputs| < 4, where one bf16 ulp stays below the 2e-2 bound (the fold and the
+        # eager path round the normalised rows differently, so single roundings can flip)
+        w = _rand((n, k), g, std=(0.3 if swiglu else 0.5) * k ** -0.5)
+        b = _rand((n,), g, 0.1)
+        pw = Fn.pack_weight(w.to(dev), swiglu_pairs=swiglu)
+        mk = (lambda: Fn.PackedAct.empty(m, n_out, dev)) if swiglu else (
+            lambda: torch.empty(m, n_out, dtype=BF16, device=dev))
+        st = Fn.ln_stats_empty(m, k, dev)
+        items.append((Fn.pack_act(x.to(dev), stats=st), pw, b.to(dev), mk(), None))
+        stats.append(st)
+        eager_items.append((Fn.layernorm_pack(x.to(dev), 1e-6), pw, b.to(dev), mk(), None))
+        y = (_ln_ref(x) @ w.double().t() + b.double()).float().to(BF16)
+        refs.append(ref.swiglu(y) if swiglu else y)
+    Fn.grouped_gemm(items, epilogue, wide_tiles=wide, ln_eps=1e-6, ln_stats=stats)
+    Fn.grouped_gemm(eager_items, epilogue, wide_tiles=wide)
+    torch.cuda.synchronize()
+    for it, ei, r in zip(items, eager_items, refs):
+        got = it[3].unpack() if swiglu else it[3]
+        eager = ei[3].unpack() if swiglu else ei[3]
+        assert_bf16_close(got, r, f"LayerNorm-folded {epilogue}")
+        assert_bf16_close(got, eager, f"LayerNorm-folded {epilogue} vs LayerNorm-pack + GEMM")
+    with pytest.raises(RuntimeError):  # the fold does not split K
+        Fn.grouped_gemm(items, epilogue, split_k=2, workspace=Fn.GemmWorkspace(1 << 20, dev), ln_eps=1e-6,
+                        ln_stats=stats)
+
+
+def _slot_sums(x: torch.Tensor) -> torch.Tensor:
+    """fp64 (sum, sum of squares) of every 64-column slot of every row, slot-major:
+    [k / 64, m, 2]."""
+    v = x.double().reshape(x.shape[0], -1, 64)
+    return torch.stack([v.sum(-1), (v * v).sum(-1)], dim=-1).transpose(0, 1)
+
+
+def test_grouped_gemm_residual_packed_epilogue_bit_identical(dev):
+    """RLDX_GEMM_EPI_RESIDUAL_PACKED (the residual stream held in the packed
+    activation order, updated in place) gives the row-major residual epilogue's
+    bits, with and without split-K; with stats_out (rldx_grouped_gemm_stats_bf16)
+    the same bits again, and per row and 64-column slot the sum and sum of
+    squares of the stored values (fp32 against fp64: relative 1e-5)."""
+    g = torch.Generator().manual_seed(23)
+    n, k = 1536, 4096
+    x = _rand((608, n), g, 0.5).to(dev)
+    h = _rand((608, k), g).to(dev)
+    ws = [(_rand((n, k), g, 0.008).to(dev), _rand((n,), g, 0.1).to(dev)) for _ in range(3)]
+    rows = ((0, 512), (512, 576), (576, 608))
+    for split in (1, 4):
+        xr, xp = x.clone(), Fn.pack_act(x)
+        it_r = [(h[lo:hi], Fn.pack_weight(w), b, xr[lo:hi], xr[lo:hi]) for (lo, hi), (w, b) in zip(rows, ws)]
+        it_p = [(h[lo:hi], Fn.pack_weight(w), b, xp.rows(lo, hi), xp.rows(lo, hi)) for (lo, hi), (w, b) in zip(rows, ws)]
+        wsr = Fn.GemmWorkspace(Fn.grouped_gemm_workspace_bytes(it_r, "residual", split), dev) if split > 1 else None
+        wsp = Fn.GemmWorkspace(Fn.grouped_gemm_workspace_bytes(it_p, "residual_packed", split), dev) if split > 1 \
+            else None
+        xs = Fn.pack_act(x)
+        it_s = [(h[lo:hi], Fn.pack_weight(w), b, xs.rows(lo, hi), xs.rows(lo, hi)) for (lo, hi), (w, b) in zip(rows, ws)]
+        sts = [Fn.ln_stats_empty(hi - lo, n, dev) for lo, hi in rows]
+        Fn.grouped_gemm(it_r, "residual", split_k=split, workspace=wsr)
+        Fn.grouped_gemm(it_p, "residual_packed", split_k=split, workspace=wsp)
+        Fn.grouped_gemm(it_s, "residual_packed", split_k=split, workspace=wsp, stats_out=sts)
+        torch.cuda.synchronize()
+        assert torch.equal(xp.unpack().view(torch.int16), xr.view(torch.int16)), f"split {split}"
+        assert torch.equal(xs.unpack().view(torch.int16), xr.view(torch.int16)), f"split {split}, stats"
+        for (lo, hi), st in zip(rows, sts):
+            ref_st = _slot_sums(xr[lo:hi].cpu())
+            err = (st.cpu().double() - ref_st).abs().max().item()
+            assert err <= 1e-5 * ref_st.abs().max().item(), f"split {split}, rows {lo}: statistics off by {err}"
+
+
+@pytest.mark.parametrize("ms,H,k", [((512, 64, 32), 12, 1536), ((40,), 3, 384)])
+def test_grouped_gemm_qkv_norm_rope_layernorm_fold(dev, ms, H, k):
+    """The QKV epilogue with the LayerNorm fold is bit-identical to the folded
+    bias GEMM followed by rldx_msat_qkv_norm_rope_bf16 (same fold arithmetic in
+    both epilogues), and within the bf16 contract of the eager path (LayerNorm-
+    pack + QKV epilogue) on Q."""
+    from rldx_amd.msat_step import msat_rope_tables
+
+    g = torch.Generator().manual_seed(sum(ms) + H + k + 1)
+    D, n = 128, 3 * H * 128
+    items, eager, specs, qkv_items, stats = [], [], [], [], []
+    for i, m in enumerate(ms):
+        x = _rand((m, k), g).to(dev)
+        w = Fn.pack_weight(_rand((n, k), g, std=k ** -0.5).to(dev))
+        b = _rand((n,), g, std=0.5).to(dev)
+        # norm weights ~0.5: |Q|, |K| < 4, where one bf16 ulp stays below the 2e-2 bound
+        qw = (0.5 + 0.1 * torch.randn(D, generator=g)).to(BF16).to(dev)
+        kw = (0.5 + 0.1 * torch.randn(D, generator=g)).to(BF16).to(dev)
+        cos = sin = None
+        if i > 0:
+            ids = torch.stack([torch.zeros(m, dtype=torch.long), torch.arange(m) + 3 * i], dim=-1)
+            cos, sin = (t.to(dev) for t in msat_rope_tables(ids, D, 10000.0))
+        qkv = torch.empty(m, n, dtype=BF16, device=dev)
+        stats.append(Fn.ln_stats_empty(m, k, dev))
+        items.append((Fn.pack_act(x, stats=stats[-1]), w, b))
+        eager.append((Fn.layernorm_pack(x, 1e-6), w, b))
+        qkv_items.append((Fn.pack_act(x), w, b, qkv, None))
+        specs.append(Fn.StreamSpec(qkv, qw, kw, cos, sin))
+    q, kvp = Fn.grouped_gemm_qkv_norm_rope(items, specs, H, D, 1e-6, ln_eps=1e-6, ln_stats=stats)
+    Fn.grouped_gemm(qkv_items, "bias", ln_eps=1e-6, ln_stats=stats)
+    q2, kvp2 = Fn.msat_qkv_norm_rope(specs, H, D, 1e-6, kv_packed=True)
+    q3, _ = Fn.grouped_gemm_qkv_norm_rope(eager, specs, H, D, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(q.view(torch.int16), q2.view(torch.int16))
+    assert torch.equal(kvp.view(torch.int16), kvp2.view(torch.int16))
+    assert_bf16_close(q, q3, "QKV epilogue with the LayerNorm fold vs LayerNorm-pack + QKV epilogue")

@@ -89,3 +89,12 @@ def test_fused_qkv_epilogue_step_is_bit_identical(setup):
     fused = MsatActionStep(cfg, w, inp).run().clone()
     split = MsatActionStep(cfg, w, inp, fused_qkv=False).run().clone()
     assert torch.equal(fused.view(torch.int16), split.view(torch.int16))
+
+
+def test_step_eager_prenorm_two_blocks(setup):
+    """ln_fold=False: the LayerNorm-pack launches (the pre-norm rounded to bf16 as
+    the eager chain does) instead of the fold; the bf16 contract on 2 blocks."""
+    cfg, w, inp, wc, ic = setup
+    out = MsatActionStep(cfg, w, inp, ln_fold=False).run(steps=1, blocks=2).clone()
+    torch.set_num_threads(max(1, min(16, torch.get_num_threads())))
+    assert_bf16_close(out, R.action_step(cfg, wc, ic, steps=1, blocks=2), "2-block step, LayerNorm-pack")
