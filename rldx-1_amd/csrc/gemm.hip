@@ -291,6 +291,68 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
                                                         __builtin_bit_cast(bf16x8, xa[b][u]), acc[bb], 0, 0, 0);
   };
 
+  // ---- epilogue operands, loaded before the K loop (in flight beside the ring
+  // prologue instead of exposed at the end of the loop) ----
+  constexpr int R = 32 * MB;                       // tile rows
+  constexpr int OC = kSwiglu ? 16 * NB : 32 * NB;  // tile output columns
+  constexpr int CPR = OC / 8;                      // 16-byte output chunks per row
+  constexpr int PER = (R * CPR + kThreads - 1) / kThreads;
+  static_assert(kThreads % CPR == 0, "a thread keeps its column chunk");
+  const int n_out = kSwiglu ? a.n / 2 : a.n;
+  const int cc = 8 * (static_cast<int>(threadIdx.x) % CPR);
+  const int col = nt * OC + cc;  // global output column of this thread's chunks
+  const bool col_ok = col < n_out;
+  // residual chunks (each is read and written by this thread, so it may alias the output)
+  u32x4 pres[PER];
+  if constexpr (residual_epi(EPI)) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int t = static_cast<int>(threadIdx.x) + kThreads * i;
+      const int row = mt * R + t / CPR;
+      const int64_t off = EPI == kEpiResidualPacked ? packed_act_offset(row, col, G.ldr)
+                                                    : static_cast<int64_t>(row) * G.ldr + col;
+      pres[i] = (t < R * CPR && row < G.m && col_ok) ? *reinterpret_cast<const u32x4*>(G.res + off)
+                                                     : u32x4{0, 0, 0, 0};
+    }
+  }
+  // biases of this thread's columns (gate and up for SwiGLU) as bf16 bits, packed
+  // in pairs once loaded (at the prologue's wait)
+  uint16_t braw[16];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    braw[i] = G.bias && col_ok ? G.bias[col + i] : uint16_t{0};
+    braw[8 + i] = kSwiglu && G.bias && col_ok ? G.bias[a.n / 2 + col + i] : uint16_t{0};
+  }
+  uint32_t bpk[8];
+  // LayerNorm fold: W row sums of this thread's columns (gate and up for SwiGLU);
+  // the SwiGLU tiles load theirs after the K loop (16 more live registers through
+  // the loop would spill at two workgroups per CU)
+  [[maybe_unused]] float wg[8], wu[8];
+  auto load_wsum = [&]() {
+    const floatx4 z = {0.f, 0.f, 0.f, 0.f};
+    const floatx4* ws = reinterpret_cast<const floatx4*>(G.wsum + col);
+    const floatx4 g0 = col_ok ? ws[0] : z, g1 = col_ok ? ws[1] : z;
+    floatx4 u0 = z, u1 = z;
+    if constexpr (kSwiglu) {
+      const floatx4* wu4 = reinterpret_cast<const floatx4*>(G.wsum + a.n / 2 + col);
+      u0 = col_ok ? wu4[0] : z;
+      u1 = col_ok ? wu4[1] : z;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      wg[i] = g0[i];
+      wg[4 + i] = g1[i];
+      wu[i] = u0[i];
+      wu[4 + i] = u1[i];
+    }
+  };
+  if constexpr (LN && !kSwiglu) load_wsum();
+  // QKV epilogue: the Q or K RMSNorm weights of this thread's 8 columns of the head
+  [[maybe_unused]] u32x4 qk_w = {0, 0, 0, 0};
+  if constexpr (EPI == kEpiQkv) {
+    const int which = nt * OC / a.qkv.inner;
+    if (which < 2) qk_w = *reinterpret_cast<const u32x4*>((which == 0 ? G.qn_w : G.kn_w) + cc);
+  }
   // LayerNorm fold: this thread's slots of its row, loaded before the ring
   // (consecutive threads: consecutive rows of one slot, contiguous), summed at
   // the prologue's wait, where they are complete (older than every ring load)
@@ -317,6 +379,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
         lp2 += lv[j][1];
       }
   }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) bpk[i] = static_cast<uint32_t>(braw[2 * i]) | (static_cast<uint32_t>(braw[2 * i + 1]) << 16);
   lread(0, 0);
   int slot_next = 1, slot_dma = NSLOT - 1;  // ring slots of stages st + 1, st + NSLOT - 1
   for (int st = 0; st < lstages; st += 2) {
@@ -338,55 +402,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     }
   }
 
-  // ---- epilogue ----
-  constexpr int R = 32 * MB;                       // tile rows
-  constexpr int OC = kSwiglu ? 16 * NB : 32 * NB;  // tile output columns
-  constexpr int CPR = OC / 8;                      // 16-byte output chunks per row
-  constexpr int PER = (R * CPR + kThreads - 1) / kThreads;
-  static_assert(kThreads % CPR == 0, "a thread keeps its column chunk");
-  const int n_out = kSwiglu ? a.n / 2 : a.n;
-  const int cc = 8 * (static_cast<int>(threadIdx.x) % CPR);
-  const int col = nt * OC + cc;  // global output column of this thread's chunks
-  const bool col_ok = col < n_out;
-  // residual chunks (each is read and written by this thread, so it may alias the output)
-  u32x4 pres[PER];
-  if constexpr (residual_epi(EPI)) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int t = static_cast<int>(threadIdx.x) + kThreads * i;
-      const int row = mt * R + t / CPR;
-      const int64_t off = EPI == kEpiResidualPacked ? packed_act_offset(row, col, G.ldr)
-                                                    : static_cast<int64_t>(row) * G.ldr + col;
-      pres[i] = (t < R * CPR && row < G.m && col_ok) ? *reinterpret_cast<const u32x4*>(G.res + off)
-                                                     : u32x4{0, 0, 0, 0};
-    }
-  }
   float bg[8], bu[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    bg[i] = G.bias && col_ok ? bf(G.bias[col + i]) : 0.f;
-    bu[i] = kSwiglu && G.bias && col_ok ? bf(G.bias[a.n / 2 + col + i]) : 0.f;
+  for (int i = 0; i < 4; ++i) {
+    bg[2 * i] = bf16x2_lo(bpk[i]);
+    bg[2 * i + 1] = bf16x2_hi(bpk[i]);
+    bu[2 * i] = bf16x2_lo(bpk[4 + i]);
+    bu[2 * i + 1] = bf16x2_hi(bpk[4 + i]);
   }
-  // LayerNorm fold: W row sums of this thread's columns (gate and up for SwiGLU)
-  [[maybe_unused]] float wg[8], wu[8];
-  if constexpr (LN) {
-    const floatx4 z = {0.f, 0.f, 0.f, 0.f};
-    const floatx4* ws = reinterpret_cast<const floatx4*>(G.wsum + col);
-    const floatx4 g0 = col_ok ? ws[0] : z, g1 = col_ok ? ws[1] : z;
-    floatx4 u0 = z, u1 = z;
-    if constexpr (kSwiglu) {
-      const floatx4* wu4 = reinterpret_cast<const floatx4*>(G.wsum + a.n / 2 + col);
-      u0 = col_ok ? wu4[0] : z;
-      u1 = col_ok ? wu4[1] : z;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      wg[i] = g0[i];
-      wg[4 + i] = g1[i];
-      wu[i] = u0[i];
-      wu[4 + i] = u1[i];
-    }
-  }
+  if constexpr (LN && kSwiglu) load_wsum();
   wait_barrier<0>();  // the ring's last reads and loads are done; LDS becomes the fp32 tiles
   float* tiles = reinterpret_cast<float*>(lds);
   {
@@ -490,11 +514,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
       }
       return;
     }
-    const int c8 = 8 * (static_cast<int>(threadIdx.x) % CPR);
-    float bq[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) bq[e] = G.bias ? bf(G.bias[n0 + c8 + e]) : 0.f;
-    const u32x4 wraw = *reinterpret_cast<const u32x4*>((which == 0 ? G.qn_w : G.kn_w) + c8);
+    const int c8 = cc;               // columns n0 + c8 = col
+    const float* bq = bg;            // their biases
+    const u32x4 wraw = qk_w;         // the Q or K norm weights of those columns
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int r = (static_cast<int>(threadIdx.x) + kThreads * i) / CPR, row = mt * R + r;
