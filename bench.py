@@ -511,8 +511,31 @@ def measured_peaks(torch) -> dict:
     z = torch.empty(n, n, dtype=torch.bfloat16, device=dev)
     ms = graph_time_ms(lambda: torch.matmul(x, y, out=z), 8, torch)
     tflops = 2 * n ** 3 / (ms * 1e-3) / 1e12
-    return dict(copy_gbs=copy_gbs, matmul_bf16_tflops=tflops,
+    return dict(copy_gbs=copy_gbs, stream_gbs=stream_same_bytes(torch, 1 << 30)["gbs"],
+                matmul_bf16_tflops=tflops,
                 published=dict(hbm_gbs=HBM_PEAK_GBS, bf16_mfma_tflops=BF16_MFMA_PEAK_TFLOPS))
+
+
+def stream_same_bytes(torch, nbytes: int, reps: int = 8) -> dict:
+    """A plain elementwise kernel moving `nbytes` (torch.neg over bf16: half read,
+    half written), timed like the kernel lines: the HBM rate that size reaches
+    with library code, launch and ramp included.  From 64 MB up, three buffer
+    pairs are rotated so the 256 MB MALL cannot hold the working set."""
+    dev = torch.device("cuda:0")
+    n = max(nbytes // 4, 1)
+    copies = 3 if nbytes >= (64 << 20) else 1
+    src = [torch.ones(n, dtype=torch.bfloat16, device=dev) for _ in range(copies)]
+    dst = [torch.empty_like(src[0]) for _ in range(copies)]
+    it = {"i": 0}
+
+    def run():
+        i = it["i"] % copies
+        it["i"] += 1
+        torch.neg(src[i], out=dst[i])
+
+    ms = graph_time_ms(run, reps * copies, torch)
+    del src, dst
+    return dict(us=ms * 1e3, gbs=4 * n / (ms * 1e-3) / 1e9)
 
 
 def cpu_baseline(torch, cfg, weights, inputs, budget_s: float = 20.0):
@@ -635,10 +658,14 @@ def main():
     for v in kl.values():  # fractions against the measured peaks as well
         if isinstance(v, dict) and v.get("unit") == "GB/s":
             v["frac_of_measured_copy"] = v["achieved"] / peaks["copy_gbs"]
+            if "bytes" in v:  # and against a plain elementwise kernel moving the same bytes
+                ref = stream_same_bytes(torch, v["bytes"])
+                v["stream_same_bytes_us"] = ref["us"]
+                v["frac_of_stream_same_bytes"] = ref["us"] / v["us"]
         elif isinstance(v, dict) and v.get("unit") == "TFLOP/s":
             v["frac_of_measured_matmul"] = v["achieved"] / peaks["matmul_bf16_tflops"]
-    print(f"[bench] measured peaks: copy {peaks['copy_gbs']:.0f} GB/s, bf16 matmul {peaks['matmul_bf16_tflops']:.0f} "
-          "TFLOP/s", file=sys.stderr, flush=True)
+    print(f"[bench] measured peaks: copy {peaks['copy_gbs']:.0f} GB/s, stream {peaks['stream_gbs']:.0f} GB/s, "
+          f"bf16 matmul {peaks['matmul_bf16_tflops']:.0f} TFLOP/s", file=sys.stderr, flush=True)
 
     cpu = None
     host = None

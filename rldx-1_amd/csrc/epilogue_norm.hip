@@ -57,8 +57,6 @@ struct AddNormArgs {
   float eps;
 };
 
-__device__ __forceinline__ float bfw(uint32_t w, int half) { return half ? bf16x2_hi(w) : bf16x2_lo(w); }
-
 // One workgroup per row (64-256 threads, whole waves): thread tid holds the
 // 8-column chunks tid + nthr j, j < CPT, of the row (dim a multiple of 8,
 // 16-byte aligned rows).  Every addend's loads are issued before any
@@ -88,21 +86,34 @@ __global__ __launch_bounds__(256) void add_norm_rows_kernel(AddNormArgs a) {
       }
     }
   }
+  // bf16 sums round each pair of columns with one v_cvt_pk_bf16_f32 (round to
+  // nearest even, the rounding of f32_to_bf16_bits for every non-NaN value)
   float v[CPT][8];
 #pragma unroll
   for (int j = 0; j < CPT; ++j)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float x = bfw(raw[0][j][i >> 1], i & 1);
-#pragma unroll
-      for (int t = 1; t < kMaxTerms; ++t) {
-        if (t < G.nterms) {
-          const float y = bfw(raw[t][j][i >> 1], i & 1);
-          x = kSum == kSumBf16 ? round_bf16(x + y) : x + y;
-        }
-      }
-      v[j][i] = x;
+    for (int k = 0; k < 4; ++k) {
+      v[j][2 * k] = bf16x2_lo(raw[0][j][k]);
+      v[j][2 * k + 1] = bf16x2_hi(raw[0][j][k]);
     }
+#pragma unroll
+  for (int t = 1; t < kMaxTerms; ++t) {
+    if (t >= G.nterms) break;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float x0 = v[j][2 * k] + bf16x2_lo(raw[t][j][k]);
+        float x1 = v[j][2 * k + 1] + bf16x2_hi(raw[t][j][k]);
+        if constexpr (kSum == kSumBf16) {
+          const uint32_t r = pack_bf16x2(x0, x1);
+          x0 = bf16x2_lo(r);
+          x1 = bf16x2_hi(r);
+        }
+        v[j][2 * k] = x0;
+        v[j][2 * k + 1] = x1;
+      }
+  }
 
   __shared__ float red[2][4];
   auto row_sum = [&](float x, int slot) {
@@ -146,7 +157,7 @@ __global__ __launch_bounds__(256) void add_norm_rows_kernel(AddNormArgs a) {
     if constexpr (kNorm == kNormLayer)
       return (x - mean) * scale;
     else
-      return w * round_bf16(x * scale);
+      return w * bf16x2_lo(pack_bf16x2(x * scale, 0.f));
   };
 
   // ---- stores ----

@@ -384,8 +384,9 @@ template <typename T, int D>
 hipError_t launch_half_d(const HalfArgs& a, hipStream_t stream) {
   constexpr int V = Vec16<T>::N;
   // Heads per thread: 4 on large launches (fewer loads per element, measured
-  // +5% of HBM rate at 16K-64K tokens); small launches are latency-bound and
-  // keep one head per thread for the most parallelism.
+  // +5% of HBM rate at 16K-64K tokens; 8 measured 1-3% slower than 4); small
+  // launches are latency-bound and keep one head per thread for the most
+  // parallelism.
   const bool large = a.total_rows * (D / V) >= (int64_t{1} << 21);
   const int R = !large ? 1 : (a.hq % 4 == 0 && a.hk % 4 == 0) ? 4 : (a.hq % 2 == 0 && a.hk % 2 == 0) ? 2 : 1;
   const int64_t threads = a.total_rows / R * (D / V);

@@ -130,6 +130,28 @@ def test_rmsnorm_rope_half_bf16(dev, D, hq, hk, S):
     assert_bf16_close(ko, rk, "k")
 
 
+@pytest.mark.parametrize("dtype,D,hq,hk,S", [(torch.float32, 64, 16, 16, 4096), (torch.bfloat16, 128, 12, 4, 8192),
+                                              (torch.bfloat16, 128, 6, 2, 16384)])
+def test_rmsnorm_rope_half_large_launches(dev, dtype, D, hq, hk, S):
+    """Launches of >= 2^21 threads' worth of rows take 4 or 2 heads per thread
+    (whichever divides both head counts): the cases take 4, 4 and 2.
+    Norm weights ~0.5 keep |out| below 4: over millions of rows a normalised
+    element reaches 5, where one bf16 ulp (0.031) exceeds the 2e-2 bound and
+    the kernel's and the oracle's fp32 row sums (different orders) flip a
+    rounding now and then."""
+    g = torch.Generator().manual_seed(S + hq)
+    q = torch.randn(1, S, hq, D, generator=g).to(dtype)
+    k = torch.randn(1, S, hk, D, generator=g).to(dtype)
+    qw = (0.5 + 0.01 * torch.randn(D, generator=g)).to(dtype)
+    kw = (0.5 + 0.01 * torch.randn(D, generator=g)).to(dtype)
+    cos, sin = W.qwen_rope_cos_sin(S, D, 1e6, dtype=dtype)
+    qo, ko = Fn.qk_rmsnorm_rope_half(*(t.to(dev) for t in (q, k, qw, kw, cos, sin)))
+    rq, rk = ref.qk_rmsnorm_rope_half(q, k, qw, kw, cos, sin)
+    close = assert_fp32_close if dtype == torch.float32 else assert_bf16_close
+    close(qo, rq, "q")
+    close(ko, rk, "k")
+
+
 def _msat_streams(D, H, sizes, seed):
     g = torch.Generator().manual_seed(seed)
     inner = H * D

@@ -165,36 +165,37 @@ def test_dispatcher_serves_physics_calls(dev):
     assert calls == [False, False, True] and d.served == 1 and not d.failed
 
 
-def _head_reference_physics(head_sd, msat_sd, hc, mc, vl, state, x0, hist, px0, e=0):
-    """fp32 CPU composition of CustomExpandedActionHeadChain.forward without the
-    RTC prefix (custom_expanded_action_model_chain.py:92-219): per-embodiment
+def _head_reference_physics(head_sd, msat_sd, hc, mc, vl, state, x0, hist, px0, e=0, dtype=torch.float32):
+    """CPU composition of CustomExpandedActionHeadChain.forward without the RTC
+    prefix (custom_expanded_action_model_chain.py:92-219): per-embodiment
     encoders / decoder (embodiment_conditioned_mlp.py), the physics encoders
-    and decoder (physics.py:9-72) and the oracle's _forward_physics."""
-    f = {k: v.cpu().float() for k, v in head_sd.items()}
-    sd32 = {k: v.cpu().float() for k, v in msat_sd.items()}
+    and decoder (physics.py:9-72) and the oracle's _forward_physics, evaluated
+    in `dtype` (fp32, or bf16 eager with a rounding after every op)."""
+    f = {k: v.cpu().to(dtype) for k, v in head_sd.items()}
+    sd = {k: v.cpu().to(dtype) for k, v in msat_sd.items()}
+    F = torch.nn.functional
 
     def lin(x, name):  # CategorySpecificLinear, batch 1
-        return x @ f[f"{name}.W"][e] + f[f"{name}.b"][e]
+        return torch.addmm(f[f"{name}.b"][e], x, f[f"{name}.W"][e])
 
     def nn_lin(x, name):
-        return x @ f[f"{name}.weight"].t() + f[f"{name}.bias"]
+        return F.linear(x, f[f"{name}.weight"], f[f"{name}.bias"])
 
-    def sin_enc(t, width):  # SinusoidalPositionalEncoding over positions t [T]
+    def sin_enc(t, width):  # SinusoidalPositionalEncoding over positions t [T] (fp32), cast to the model dtype
         half = width // 2
         ex = torch.exp(-torch.arange(half, dtype=torch.float) * (torch.log(torch.tensor(10000.0)) / half))
         fr = t.float()[:, None] * ex
-        return torch.cat([torch.sin(fr), torch.cos(fr)], dim=-1)
+        return torch.cat([torch.sin(fr), torch.cos(fr)], dim=-1).to(dtype)
 
     def penc(x, pos, enc):
         h = nn_lin(x, f"physics.{enc}.W1")
-        return nn_lin(torch.nn.functional.silu(nn_lin(torch.cat([h, pos], dim=-1), f"physics.{enc}.W2")),
-                      f"physics.{enc}.W3")
+        return nn_lin(F.silu(nn_lin(torch.cat([h, pos], dim=-1), f"physics.{enc}.W2")), f"physics.{enc}.W3")
 
-    state_feat = lin(torch.relu(lin(state.cpu().float()[0], "state_encoder.layer1")), "state_encoder.layer2")
-    act = x0.cpu().float()[0]
-    hist_tok = penc(hist.cpu().float()[0], sin_enc(torch.arange(hc.physics_hist_len), mc.sa_dim),
+    state_feat = lin(torch.relu(lin(state.cpu().to(dtype)[0], "state_encoder.layer1")), "state_encoder.layer2")
+    act = x0.cpu().to(dtype)[0].clone()
+    hist_tok = penc(hist.cpu().to(dtype)[0], sin_enc(torch.arange(hc.physics_hist_len), mc.sa_dim),
                     "physics_cond_encoder")
-    fut = px0.cpu().float()[0]
+    fut = px0.cpu().to(dtype)[0].clone()
     for i in range(hc.steps):
         t = i / hc.steps
         tau = sin_enc(torch.full((hc.action_horizon,), t), mc.sa_dim)
@@ -203,15 +204,31 @@ def _head_reference_physics(head_sd, msat_sd, hc, mc, vl, state, x0, hist, px0, 
         a = lin(x * torch.sigmoid(x), "action_encoder.W3") + f["position_embedding.weight"]
         sa = torch.cat([state_feat, a])[None]
         p_embs = torch.cat([hist_tok, penc(fut, tau[: hc.physics_fut_len], "physics_fut_encoder")])[None]
-        out, ph = R.msat_forward_physics(sd32, sa, vl.cpu().float(), p_embs, f["static_tembs"][i],
+        out, ph = R.msat_forward_physics(sd, sa, vl.cpu().to(dtype), p_embs, f["static_tembs"][i],
                                          f["static_time_tokens"][i], heads=mc.heads, head_dim=mc.head_dim,
                                          ds_blocks=mc.ds_blocks, ss_blocks=mc.ss_blocks)
         v = lin(torch.relu(lin(out[0], "action_decoder.layer1")), "action_decoder.layer2")[-hc.action_horizon:]
-        act = act + v / hc.steps
-        pv = nn_lin(torch.nn.functional.silu(nn_lin(ph[0, -hc.physics_fut_len:], "physics.physics_decoder.net.0")),
+        act.add_(v, alpha=1.0 / hc.steps)
+        pv = nn_lin(F.silu(nn_lin(ph[0, -hc.physics_fut_len:], "physics.physics_decoder.net.0")),
                     "physics.physics_decoder.net.2")
-        fut = fut + pv / hc.steps
+        fut.add_(pv, alpha=1.0 / hc.steps)
     return act, fut
+
+
+def _physics_head_on_gpu(mc, hc, dev, seed, embodiment):
+    sd = RM.make_state_dict(mc, dev, seed=seed)
+    hsd = RM.make_head_state_dict(mc, hc, dev, seed=seed + 1)
+    head = RM.RldxActionHead(RM.RldxMsat(sd, mc, dev), hsd, hc, embodiment=embodiment)
+    g = torch.Generator(device=dev).manual_seed(seed + 2)
+    for t in (head.vl, head.state, head.x0, head.physics_hist, head.physics_x0):
+        t.copy_(torch.randn(t.shape, generator=g, device=dev))
+    head.capture()
+    a1 = head.replay().clone()
+    f1 = head.physics_fut.clone()
+    a2 = head.replay().clone()
+    torch.cuda.synchronize()
+    assert torch.equal(a1.view(torch.int16), a2.view(torch.int16)), "graph replays differ"
+    return head, sd, hsd, a1, f1
 
 
 def test_all_add_ons_action_head_graph_matches_fp32_composition(dev):
@@ -222,20 +239,30 @@ def test_all_add_ons_action_head_graph_matches_fp32_composition(dev):
     physics future agree to rel-L2 <= 2e-2 and replays are bitwise stable."""
     hc = RM.RldxHeadCfg(steps=2, num_embodiments=4, physics_dim=37, physics_hist_len=1)
     mc = _cfg(ds_blocks=1, ss_blocks=1, n_physics=hc.physics_hist_len + hc.physics_fut_len)
-    sd = RM.make_state_dict(mc, dev, seed=171)
-    hsd = RM.make_head_state_dict(mc, hc, dev, seed=172)
-    head = RM.RldxActionHead(RM.RldxMsat(sd, mc, dev), hsd, hc, embodiment=2)
-    g = torch.Generator(device=dev).manual_seed(173)
-    for t in (head.vl, head.state, head.x0, head.physics_hist, head.physics_x0):
-        t.copy_(torch.randn(t.shape, generator=g, device=dev))
-    head.capture()
-    a1 = head.replay().clone()
-    f1 = head.physics_fut.clone()
-    a2 = head.replay().clone()
-    torch.cuda.synchronize()
-    assert torch.equal(a1.view(torch.int16), a2.view(torch.int16))
+    head, sd, hsd, a1, f1 = _physics_head_on_gpu(mc, hc, dev, 171, 2)
     ra, rf = _head_reference_physics(hsd, sd, hc, mc, head.vl, head.state, head.x0, head.physics_hist,
                                      head.physics_x0, e=2)
     rel_a, rel_f = _rel(a1[0].cpu().double(), ra.double()), _rel(f1[0].cpu().double(), rf.double())
     print(f"all-add-ons action head: actions rel-L2 {rel_a:.2e}, physics future rel-L2 {rel_f:.2e}")
     assert torch.isfinite(a1).all() and torch.isfinite(f1).all() and rel_a <= 2e-2 and rel_f <= 2e-2
+
+
+def test_all_add_ons_action_head_full_depth_as_accurate_as_eager_bf16(dev):
+    """The all-add-ons action head at full depth: 4 denoising steps through the
+    4 + 8 Expanded-block MSAT (N_vl 80, 1 + 16 physics tokens) with both
+    decoders and Euler updates, one hipGraph.  Referee as for the full MSAT:
+    actions and physics future are each no further from the fp32 composition
+    than 1.5x the eager bf16 composition is, with cosine >= 0.999 to the latter."""
+    hc = RM.RldxHeadCfg(num_embodiments=4, physics_dim=37, physics_hist_len=1)
+    mc = _cfg(n_physics=hc.physics_hist_len + hc.physics_fut_len)
+    head, sd, hsd, a1, f1 = _physics_head_on_gpu(mc, hc, dev, 181, 1)
+    args = (hsd, sd, hc, mc, head.vl, head.state, head.x0, head.physics_hist, head.physics_x0)
+    r32 = _head_reference_physics(*args, e=1)
+    r16 = _head_reference_physics(*args, e=1, dtype=torch.bfloat16)
+    for name, o, a16, a32 in zip(("actions", "physics future"), (a1[0], f1[0]), r16, r32):
+        o, a16, a32 = o.cpu().double(), a16.double(), a32.double()
+        floor, got = _rel(a16, a32), _rel(o, a32)
+        cos = torch.nn.functional.cosine_similarity(o.flatten(), a16.flatten(), dim=0).item()
+        print(f"all-add-ons action head / {name}: rel-L2 to fp32 {got:.2e} (eager bf16: {floor:.2e}), to the bf16 "
+              f"composition {_rel(o, a16):.2e}, max-abs to bf16 {(o - a16).abs().max().item():.3e}, cos {cos:.6f}")
+        assert torch.isfinite(o).all() and got <= 1.5 * floor and cos >= 0.999, name
