@@ -8,13 +8,15 @@ Importing this module registers, backed by the gfx950 kernels of librldx_amd.so:
   ss::fused_epilogue_ln
   rldx_backbone::fused_attention   rldx_backbone::vision_attention   mem::fused_attention
   rldx_backbone::fused_epilogue_add2_rmsnorm   rldx_backbone::fused_epilogue_add3_rmsnorm
+  mem::fused_epilogue_add2_rmsnorm
   rldx_amd::swiglu           (the eager `F.silu(x1) * x2` the chains inline)
 
 Argument order and defaults follow the reference registrations
 (rldx/inference/action_model/{double,single}_stream/engine/ops/*.py,
 rldx/inference/backbone/llm/engine/ops/op_fused_llm_attention.py,
 rldx/inference/backbone/vision_encoder/engine/ops/op_fused_vision_attention.py,
-rldx/inference/memory/engine/ops/op_fused_memory_attention.py).  Additive,
+rldx/inference/memory/engine/ops/op_fused_memory_attention.py,
+op_fused_epilogue_add2_rmsnorm.py).  Additive,
 optional keyword arguments: `num_heads` / `head_dim` (the reference hard-codes
 24 x 64), `num_kv_heads` for the backbone op (reference: 32 / 8 / 128 with a
 fixed 4096-wide output), and `kv_mask` on the 3-way ops (1 = visible key,
@@ -485,4 +487,22 @@ def rldx_backbone_fused_epilogue_add3_rmsnorm(
 
 @rldx_backbone_fused_epilogue_add3_rmsnorm.register_fake
 def _(hidden, residual, deepStack, weight):
+    return torch.empty_like(hidden), torch.empty_like(hidden)
+
+
+@torch.library.custom_op("mem::fused_epilogue_add2_rmsnorm", mutates_args=())
+def mem_fused_epilogue_add2_rmsnorm(
+    hidden: torch.Tensor,
+    residual: torch.Tensor,
+    weight: torch.Tensor,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """The TransformerMemory layers' cross-layer epilogue: the same arithmetic as
+    rldx_backbone::fused_epilogue_add2_rmsnorm (the reference reuses that kernel).
+
+    Reference: memory/engine/ops/op_fused_epilogue_add2_rmsnorm.py:16-40."""
+    return Fn.fused_add2_rmsnorm(hidden, residual, weight)
+
+
+@mem_fused_epilogue_add2_rmsnorm.register_fake
+def _(hidden, residual, weight):
     return torch.empty_like(hidden), torch.empty_like(hidden)

@@ -1,0 +1,174 @@
+"""Host tests of the drop-in module mirror (rldx_amd.compat): after install(),
+the module names the reference's chains import resolve to the rldx_amd
+launchers, with the reference's function names, parameter names and defaults
+(each expected signature below is copied from the reference file cited), the
+op-registration modules bind the rldx_amd operators, and the set-up helpers
+follow their closed forms.  No compute calls: those are in
+tests/test_gpu_compat.py."""
+
+import inspect
+import sys
+
+import pytest
+import torch
+
+from rldx_amd import compat
+
+
+@pytest.fixture
+def installed():
+    yield compat.install()
+    compat.uninstall()
+
+
+# (module name as the reference imports it, function, reference parameters as (name, default), citation)
+_EMPTY = inspect.Parameter.empty
+SIGNATURES = [
+    ("double_stream.engine.kernels.vl_epilogue_ln", "fused_vl_epilogue_ln",
+     [("vl_residual", _EMPTY), ("proj_bias", _EMPTY), ("w3_bias", _EMPTY), ("w3_out", _EMPTY), ("M", None),
+      ("DIM", None), ("new_vl_out", None), ("ln_vl_out", None)], "vl_epilogue_ln.py:134-136"),
+    ("double_stream.engine.kernels.grouped_res_ln", "fused_grouped_res_ln",
+     [("sa_residual", _EMPTY), ("sa_proj_bias", _EMPTY), ("sa_proj_out", _EMPTY), ("vl_residual", _EMPTY),
+      ("vl_proj_bias", _EMPTY), ("vl_proj_out", _EMPTY), ("M_sa", None), ("M_vl", None), ("SA_DIM", None),
+      ("VL_DIM", None)], "grouped_res_ln.py:150-161"),
+    ("double_stream.engine.kernels.grouped_swiglu", "fused_grouped_swiglu",
+     [("sa_w12_out", _EMPTY), ("sa_bias", _EMPTY), ("vl_w12_out", _EMPTY), ("vl_bias", _EMPTY), ("M_sa", None),
+      ("M_vl", None), ("N_half_sa", None), ("N_half_vl", None)], "grouped_swiglu.py:213-215"),
+    ("single_stream.engine.kernels.ss_epilogue_ln", "fused_ss_epilogue_ln",
+     [("hidden", _EMPTY), ("M", None), ("DIM", None), ("residual", None), ("new_hidden_out", None),
+      ("ln_out_out", None)], "ss_epilogue_ln.py:146-148"),
+    ("single_stream.engine.kernels.fused_mlp_swiglu", "fused_mlp_swiglu",
+     [("x", _EMPTY), ("weight", _EMPTY), ("bias", _EMPTY), ("split_k", 1)], "fused_mlp_swiglu.py:199"),
+    ("llm.engine.kernels.fused_llm_attention", "forward",
+     [("qkv", _EMPTY), ("q_norm_w", _EMPTY), ("q_norm_w_rot", _EMPTY), ("k_norm_w", _EMPTY),
+      ("k_norm_w_rot", _EMPTY), ("cos", _EMPTY), ("signed_sin", _EMPTY), ("num_heads", 32), ("num_kv_heads", 8),
+      ("head_dim", 128), ("out", None)], "fused_llm_attention.py:1005-1017"),
+    ("llm.engine.kernels.fused_llm_attention", "prepare_signed_sin", [("sin", _EMPTY), ("head_dim", _EMPTY)],
+     "fused_llm_attention.py:787"),
+    ("llm.engine.kernels.fused_llm_attention", "prepare_norm_weight_rot",
+     [("norm_weight", _EMPTY), ("head_dim", _EMPTY)], "fused_llm_attention.py:798"),
+    ("llm.engine.kernels.fused_llm_attention", "prepare_fused_qkv_weight", [("layer", _EMPTY)],
+     "fused_llm_attention.py:778"),
+    ("llm.engine.kernels.fused_llm_attention", "autotune_split_m_threshold",
+     [("workloads", _EMPTY), ("candidates", (64, 128, 256, 512)), ("warmup", 3), ("iters", 10)],
+     "fused_llm_attention.py:928"),
+    ("backbone.llm.engine.kernels.fused_add2_rmsnorm", "forward",
+     [("hidden", _EMPTY), ("residual", _EMPTY), ("weight", _EMPTY)], "fused_add2_rmsnorm.py:85"),
+    ("llm.engine.kernels.fused_add3_rmsnorm", "forward",
+     [("hidden", _EMPTY), ("residual", _EMPTY), ("deepstack", _EMPTY), ("weight", _EMPTY)],
+     "fused_add3_rmsnorm.py:86"),
+    ("vision_encoder.engine.kernels.fused_vision_attention", "forward",
+     [("qkv", _EMPTY), ("rope_cos", _EMPTY), ("rope_sin", _EMPTY), ("cu_seqlens", _EMPTY), ("scaling", _EMPTY),
+      ("num_heads", _EMPTY), ("head_dim", _EMPTY)], "fused_vision_attention.py:622"),
+    ("vision_encoder.engine.kernels.fused_vision_attention", "autotune_split_m_threshold",
+     [("workloads", _EMPTY), ("candidates", (64, 128, 256, 512)), ("warmup", 3), ("iters", 10)],
+     "fused_vision_attention.py:576"),
+    ("memory.engine.kernels.fused_memory_attention", "forward",
+     [("qkv", _EMPTY), ("cos", _EMPTY), ("signed_sin", _EMPTY), ("num_heads", _EMPTY), ("head_dim", _EMPTY),
+      ("block_attn_size", _EMPTY)], "fused_memory_attention.py:228"),
+    ("memory.engine.kernels.fused_memory_attention", "prepare_rope_buffers",
+     [("rotary_emb", _EMPTY), ("position_ids", _EMPTY), ("device", _EMPTY), ("dtype", torch.bfloat16)],
+     "fused_memory_attention.py:206"),
+    ("memory.engine.kernels.fused_memory_attention", "prepare_signed_sin", [("sin", _EMPTY), ("head_dim", _EMPTY)],
+     "fused_memory_attention.py:194"),
+    ("memory.engine.kernels.fused_add2_rmsnorm", "forward",
+     [("hidden", _EMPTY), ("residual", _EMPTY), ("weight", _EMPTY)], "memory/.../fused_add2_rmsnorm.py:15"),
+]
+
+
+@pytest.mark.parametrize("module,fn,params,cite", SIGNATURES, ids=[f"{m}.{f}" for m, f, _, _ in SIGNATURES])
+def test_launcher_signature_matches_reference(installed, module, fn, params, cite):
+    """The reference's parameters, in order and with its defaults, lead the
+    mirrored signature; anything after them is an optional keyword."""
+    f = getattr(sys.modules[module], fn)
+    got = list(inspect.signature(f).parameters.values())
+    assert [(p.name, p.default) for p in got[: len(params)]] == params, cite
+    assert all(p.default is not _EMPTY for p in got[len(params):]), cite
+
+
+def test_chain_import_forms_resolve_to_the_mirror(installed):
+    """The import statements of the reference's chains, verbatim in form."""
+    from backbone.llm.engine.kernels.fused_add2_rmsnorm import forward  # memory/engine/kernels/fused_add2_rmsnorm.py:15
+    from double_stream.engine.kernels.vl_epilogue_ln import fused_vl_epilogue_ln  # custom_double_stream_chain.py:12
+    from llm.engine.kernels.fused_llm_attention import (  # custom_backbone_chain.py:21-25
+        autotune_split_m_threshold, prepare_norm_weight_rot, prepare_signed_sin)
+    from single_stream.engine.kernels.ss_epilogue_ln import fused_ss_epilogue_ln  # custom_single_stream_chain.py:11
+    from vision_encoder.engine.kernels.fused_vision_attention import autotune_split_m_threshold as v_tune  # :29-31
+
+    import double_stream.engine.ops  # noqa: F401  custom_double_stream_chain.py (ops registration)
+    import memory.engine.ops  # noqa: F401  custom_memory_chain.py:18
+    import single_stream.engine.ops  # noqa: F401
+    for f in (forward, fused_vl_epilogue_ln, autotune_split_m_threshold, prepare_norm_weight_rot, prepare_signed_sin,
+              fused_ss_epilogue_ln, v_tune):
+        assert f.__module__.startswith("rldx_amd."), f
+    assert sys.modules["rldx.inference.action_model.double_stream.engine.kernels.vl_epilogue_ln"] is \
+        sys.modules["double_stream.engine.kernels.vl_epilogue_ln"]
+    assert autotune_split_m_threshold([]) == 128 and v_tune([]) == 128
+
+
+OP_MODULES = [
+    ("double_stream.engine.ops.op_fused_attention", "fused_attention", "ds::fused_attention_2way"),
+    ("double_stream.engine.ops.op_fused_attention_3way", "fused_attention_3way", "ds::fused_attention_3way"),
+    ("double_stream.engine.ops.op_vl_epilogue_ln", "vl_epilogue_ln", "ds::vl_epilogue_ln"),
+    ("double_stream.engine.ops.op_grouped_swiglu", "grouped_swiglu", "ds::grouped_swiglu"),
+    ("double_stream.engine.ops.op_grouped_res_ln", "grouped_res_ln", "ds::grouped_res_ln"),
+    ("single_stream.engine.ops.op_fused_attention", "fused_attention", "ss::fused_attention_2way"),
+    ("single_stream.engine.ops.op_fused_attention_3way", "fused_attention_3way", "ss::fused_attention_3way"),
+    ("single_stream.engine.ops.op_fused_epilogue_ln", "fused_epilogue_ln", "ss::fused_epilogue_ln"),
+    ("single_stream.engine.ops.op_fused_mlp_swiglu", "fused_mlp_swiglu", "ss::fused_mlp_swiglu"),
+    ("llm.engine.ops.op_fused_llm_attention", "fused_llm_attention", "rldx_backbone::fused_attention"),
+    ("llm.engine.ops.op_fused_epilogue_add2_rmsnorm", "fused_epilogue_add2_rmsnorm",
+     "rldx_backbone::fused_epilogue_add2_rmsnorm"),
+    ("llm.engine.ops.op_fused_epilogue_add3_rmsnorm", "fused_epilogue_add3_rmsnorm",
+     "rldx_backbone::fused_epilogue_add3_rmsnorm"),
+    ("vision_encoder.engine.ops.op_fused_vision_attention", "vision_attention", "rldx_backbone::vision_attention"),
+    ("memory.engine.ops.op_fused_memory_attention", "fused_memory_attention", "mem::fused_attention"),
+    ("memory.engine.ops.op_fused_epilogue_add2_rmsnorm", "fused_epilogue_add2_rmsnorm",
+     "mem::fused_epilogue_add2_rmsnorm"),
+]
+
+
+@pytest.mark.parametrize("module,name,qualname", OP_MODULES, ids=[q for _, _, q in OP_MODULES])
+def test_op_modules_bind_the_rldx_amd_registrations(installed, module, name, qualname):
+    op = getattr(sys.modules[module], name)
+    assert op._qualname == qualname
+    ns, _, opname = qualname.partition("::")
+    assert getattr(getattr(torch.ops, ns), opname) is not None
+
+
+def test_setup_helpers_closed_forms(installed):
+    from llm.engine.kernels.fused_llm_attention import (prepare_fused_qkv_weight, prepare_norm_weight_rot,
+                                                        prepare_signed_sin)
+    from memory.engine.kernels.fused_memory_attention import prepare_rope_buffers
+
+    g = torch.Generator().manual_seed(5)
+    D = 8
+    sin = torch.randn(3, D, generator=g).to(torch.bfloat16)
+    s = prepare_signed_sin(sin, D)
+    assert torch.equal(s[:, : D // 2], -sin[:, : D // 2]) and torch.equal(s[:, D // 2:], sin[:, D // 2:])
+    w = torch.arange(D, dtype=torch.float32)
+    assert prepare_norm_weight_rot(w, D).tolist() == [(d + D // 2) % D for d in range(D)]
+    with pytest.raises(ValueError):
+        prepare_signed_sin(sin, D + 2)
+
+    class Attn(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.q_proj, self.k_proj, self.v_proj = (torch.nn.Linear(4, n, bias=False) for n in (6, 2, 2))
+
+    layer = torch.nn.Module()
+    layer.self_attn = Attn()
+    fused = prepare_fused_qkv_weight(layer)
+    a = layer.self_attn
+    assert torch.equal(fused, torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight]).detach())
+
+    class Rotary:  # the HF rotary-embedding call convention: (x, position_ids) -> cos, sin (1, M, D)
+        dim = D
+
+        def __call__(self, x, position_ids):
+            ang = position_ids[0, :, None].float() * torch.arange(1, D + 1).float()
+            return ang.cos()[None].to(x.dtype), ang.sin()[None].to(x.dtype)
+
+    cos, ssin = prepare_rope_buffers(Rotary(), torch.arange(5)[None], "cpu")
+    c_ref, s_ref = Rotary()(torch.empty(0, dtype=torch.bfloat16), torch.arange(5)[None])
+    assert torch.equal(cos, c_ref[0]) and torch.equal(ssin, prepare_signed_sin(s_ref[0], D))

@@ -181,6 +181,8 @@ def _opcheck_cases():
         "rldx_backbone::fused_epilogue_add3_rmsnorm": (torch.ops.rldx_backbone.fused_epilogue_add3_rmsnorm,
                                                        (rows(40, 2048), rows(40, 2048), rows(40, 2048),
                                                         rows(1, 2048)[0]), {}),
+        "mem::fused_epilogue_add2_rmsnorm": (torch.ops.mem.fused_epilogue_add2_rmsnorm,
+                                             (rows(64, 2048), rows(64, 2048), rows(1, 2048)[0]), {}),
     }
     vc = W.VitAttnCfg()
     vi = W.vit_attention_inputs(vc)
@@ -199,6 +201,7 @@ OPCHECK_CASES = [
     "ds::grouped_swiglu", "ss::fused_mlp_swiglu", "rldx_backbone::fused_attention", "rldx_amd::swiglu",
     "ds::grouped_res_ln", "ds::vl_epilogue_ln", "ss::fused_epilogue_ln", "rldx_backbone::fused_epilogue_add2_rmsnorm",
     "rldx_backbone::fused_epilogue_add3_rmsnorm", "rldx_backbone::vision_attention", "mem::fused_attention",
+    "mem::fused_epilogue_add2_rmsnorm",
 ]
 
 

@@ -74,7 +74,9 @@ def test_epilogue_fakes():
         nh, ln = torch.ops.ss.fused_epilogue_ln(e(1, 82, 1536), e(1, 82, 1536))
         a2 = torch.ops.rldx_backbone.fused_epilogue_add2_rmsnorm(e(169, 4096), e(169, 4096), e(4096))
         a3 = torch.ops.rldx_backbone.fused_epilogue_add3_rmsnorm(e(169, 4096), e(169, 4096), e(169, 4096), e(4096))
+        m2 = torch.ops.mem.fused_epilogue_add2_rmsnorm(e(1, 64, 2048), e(1, 64, 2048), e(2048))
     assert tuple(sa.shape) == (1, 18, 1536) and tuple(vl.shape) == (1, 64, 4096)
     assert tuple(nv.shape) == (1, 64, 4096) and tuple(lv.shape) == (1, 64, 4096)
     assert tuple(nh.shape) == (1, 82, 1536) and tuple(ln.shape) == (1, 82, 1536)
     assert all(tuple(t.shape) == (169, 4096) for t in (*a2, *a3))
+    assert all(tuple(t.shape) == (1, 64, 2048) for t in m2)
