@@ -67,6 +67,9 @@ hipError_t rldx_grouped_swiglu_bf16(const void* sa_x, const void* sa_bias, const
  * (rldx/inference/backbone/llm/engine/kernels/fused_llm_attention.py:787-796),
  * i.e. its first half already carries rotate_half's minus sign. */
 #define RLDX_ROPE_SIN_SIGNED 1
+/* flags bit: RoPE only -- no RMSNorm, q_w / k_w unused (may be NULL):
+ * apply_rotary_pos_emb alone (rldx/model/modules/backbone/modeling_qwen3_vl.py:377-401). */
+#define RLDX_ROPE_NO_NORM 2
 
 /*
  * q' = apply_rotary_pos_emb(q_norm(q)), k' likewise, for q [B, S, Hq, D] and
@@ -78,7 +81,8 @@ hipError_t rldx_grouped_swiglu_bf16(const void* sa_x, const void* sa_bias, const
  * q_heads or k_heads may be 0 (then q/q_w/q_out, resp. k/k_w/k_out, may be NULL).
  * Tensors, norm weights and tables are 16-byte aligned, strides multiples of
  * 16 bytes; (q_heads + k_heads) * B * S * D / 4 (fp32) or / 8 (bf16) < 2^31.
- * flags: RLDX_ROPE_SIN_SIGNED or 0.
+ * flags: RLDX_ROPE_SIN_SIGNED and / or RLDX_ROPE_NO_NORM (then q' = q cos +
+ * rotate_half(q) sin in the input type, eager rounding), or 0.
  *
  * Replaces: Qwen3VLTextRMSNorm.forward + apply_rotary_pos_emb
  *   (rldx/model/modules/backbone/modeling_qwen3_vl.py:356-371, :377-401),
@@ -624,6 +628,49 @@ hipError_t rldx_ss_epilogue_ln_bf16(const void* hidden, const void* residual, vo
 hipError_t rldx_add_rmsnorm_bf16(const void* hidden, const void* residual, const void* deepstack,
                                  const void* weight, void* new_hidden, void* normed, int64_t m, int64_t dim,
                                  float eps, hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Model-level primitives of the eager modules                               */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * RMSNorm with one rounding: out = (w * (x * rsqrt(mean(x^2) + eps))).to(x's
+ * dtype), fp32 arithmetic, over rows of `dim` values (row strides in
+ * elements).  weight [dim] is fp32 (weight_is_f32 = 1, the module's parameter)
+ * or bf16 (0, a model cast to bf16; promoted to fp32 by the product).  dim a
+ * multiple of 8 (bf16) / 4 (fp32) up to 8192 / 4096; x, out (and an fp32
+ * weight) 16-byte aligned.
+ * Replaces: RMSNorm.forward (rldx/model/modules/norms.py:7-22), the module the
+ *   MSAT's create_qk_norm_layers and the memory module instantiate.
+ */
+hipError_t rldx_rms_norm_bf16(const void* x, int64_t x_row_stride, const void* weight, int32_t weight_is_f32,
+                              void* out, int64_t out_row_stride, int64_t rows, int64_t dim, float eps,
+                              hipStream_t stream);
+hipError_t rldx_rms_norm_f32(const float* x, int64_t x_row_stride, const void* weight, int32_t weight_is_f32,
+                             float* out, int64_t out_row_stride, int64_t rows, int64_t dim, float eps,
+                             hipStream_t stream);
+
+/*
+ * Interleaved (complex) RoPE of q [B, Hq, N, D] and k [B, Hk, N, D] (strides
+ * {batch, head, seq} in elements, D contiguous; outputs likewise): pair
+ * (x[2i], x[2i+1]) times freqs[b][n][i] = (cos, sin) as complex numbers in
+ * fp32, rounded once to the input type.  freqs: complex64 as fp32 pairs,
+ * strides {batch, seq} in pairs (batch stride 0: one table for every batch
+ * entry), 16-byte aligned, even strides.  D a multiple of 8 (bf16) / 4
+ * (fp32).  q_heads or k_heads may be 0.
+ * Replaces: apply_rotary_emb (rldx/model/modules/action_model/ops.py:48-67)
+ *   with reshape_for_broadcast (:28-45).
+ */
+hipError_t rldx_rope_interleaved_bf16(const void* xq, const int64_t* q_strides, void* q_out,
+                                      const int64_t* q_out_strides, const void* xk, const int64_t* k_strides,
+                                      void* k_out, const int64_t* k_out_strides, int64_t batch, int64_t q_heads,
+                                      int64_t k_heads, int64_t seq, int64_t head_dim, const float* freqs,
+                                      const int64_t* freqs_strides, hipStream_t stream);
+hipError_t rldx_rope_interleaved_f32(const float* xq, const int64_t* q_strides, float* q_out,
+                                     const int64_t* q_out_strides, const float* xk, const int64_t* k_strides,
+                                     float* k_out, const int64_t* k_out_strides, int64_t batch, int64_t q_heads,
+                                     int64_t k_heads, int64_t seq, int64_t head_dim, const float* freqs,
+                                     const int64_t* freqs_strides, hipStream_t stream);
 
 #ifdef __cplusplus
 }

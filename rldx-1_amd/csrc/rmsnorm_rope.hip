@@ -67,6 +67,7 @@ struct HalfArgs {
   int64_t c_sb, c_ss;          // cos/sin strides ([B or 1, S, D])
   float eps;
   int sin_signed;              // sin table already carries the rotate_half sign
+  int no_norm;                 // RoPE only (apply_rotary_pos_emb): no RMSNorm, no weights
   int64_t total_rows;          // batch * seq * (hq + hk); total_rows * D / V < 2^31
   DivMagic per_tok_div;        // division by hq + hk
   DivMagic seq_div;            // division by seq
@@ -169,7 +170,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_half_kernel(HalfArgs a) {
 #pragma unroll
   for (int j = 0; j < R; ++j)
     raw[j] = valid ? *reinterpret_cast<const uint4*>(src + j * src_h + d0) : make_uint4(0, 0, 0, 0);
-  const uint4 wraw = *reinterpret_cast<const uint4*>(w + d0);
+  const uint4 wraw = a.no_norm ? make_uint4(0, 0, 0, 0) : *reinterpret_cast<const uint4*>(w + d0);
   const uint4 craw = *reinterpret_cast<const uint4*>(cs + d0);
   const uint4 sraw = *reinterpret_cast<const uint4*>(sn + d0);
   const T* we = reinterpret_cast<const T*>(&wraw);
@@ -183,24 +184,28 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_half_kernel(HalfArgs a) {
     const T* e = reinterpret_cast<const T*>(&raw[j]);
 #pragma unroll
     for (int i = 0; i < V; ++i) x[i] = load_elem<T>(e, i);
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < V; ++i) ss += x[i] * x[i];
-#pragma unroll
-    for (int m = LPR / 2; m >= 1; m >>= 1) ss += shfl_xor_f(ss, m);
-
     float y[V];
-    {
-#pragma clang fp contract(off)
-      const float rinv = 1.0f / __builtin_sqrtf(ss * (1.0f / D) + a.eps);
+    if (a.no_norm) {  // (uniform) RoPE of the input as it is
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        float xn = x[i] * rinv;
-        if constexpr (sizeof(T) == 2) {
-          // w * bf16(xn): bf16 x bf16 product, rounded to bf16.
-          y[i] = round_bf16(load_elem<T>(we, i) * round_bf16(xn));
-        } else {
-          y[i] = load_elem<T>(we, i) * xn;
+      for (int i = 0; i < V; ++i) y[i] = x[i];
+    } else {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < V; ++i) ss += x[i] * x[i];
+#pragma unroll
+      for (int m = LPR / 2; m >= 1; m >>= 1) ss += shfl_xor_f(ss, m);
+      {
+#pragma clang fp contract(off)
+        const float rinv = 1.0f / __builtin_sqrtf(ss * (1.0f / D) + a.eps);
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          float xn = x[i] * rinv;
+          if constexpr (sizeof(T) == 2) {
+            // w * bf16(xn): bf16 x bf16 product, rounded to bf16.
+            y[i] = round_bf16(load_elem<T>(we, i) * round_bf16(xn));
+          } else {
+            y[i] = load_elem<T>(we, i) * xn;
+          }
         }
       }
     }
@@ -419,8 +424,10 @@ hipError_t half_entry(const void* q, const void* k, const void* q_w, const void*
   if (!q_strides || !k_strides || !qo_strides || !ko_strides || !cs_strides) return hipErrorInvalidValue;
   if (batch == 0 || seq == 0 || hq + hk == 0) return hipSuccess;
   if (!cos || !sin) return hipErrorInvalidValue;
-  if (hq > 0 && (!q || !q_w || !q_out)) return hipErrorInvalidValue;
-  if (hk > 0 && (!k || !k_w || !k_out)) return hipErrorInvalidValue;
+  if (flags & ~(RLDX_ROPE_SIN_SIGNED | RLDX_ROPE_NO_NORM)) return hipErrorInvalidValue;
+  const bool no_norm = (flags & RLDX_ROPE_NO_NORM) != 0;
+  if (hq > 0 && (!q || (!q_w && !no_norm) || !q_out)) return hipErrorInvalidValue;
+  if (hk > 0 && (!k || (!k_w && !no_norm) || !k_out)) return hipErrorInvalidValue;
   const int V = Vec16<T>::N;
   const void* ptrs[] = {q, k, q_out, k_out, cos, sin, q_w, k_w};
   for (const void* p : ptrs)
@@ -435,7 +442,7 @@ hipError_t half_entry(const void* q, const void* k, const void* q_w, const void*
   HalfArgs a{q, k, q_w, k_w, cos, sin, q_out, k_out, batch, seq, hq, hk,
              q_strides[0], q_strides[1], q_strides[2], k_strides[0], k_strides[1], k_strides[2],
              qo_strides[0], qo_strides[1], qo_strides[2], ko_strides[0], ko_strides[1], ko_strides[2],
-             cs_strides[0], cs_strides[1], eps, (flags & RLDX_ROPE_SIN_SIGNED) ? 1 : 0,
+             cs_strides[0], cs_strides[1], eps, (flags & RLDX_ROPE_SIN_SIGNED) ? 1 : 0, no_norm ? 1 : 0,
              rows, div_magic(static_cast<uint32_t>(hq + hk)), div_magic(static_cast<uint32_t>(seq))};
   return launch_half<T>(a, head_dim, stream);
 }

@@ -120,9 +120,16 @@ SIGNATURES = {
     "rldx_vl_epilogue_ln_bf16": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_f32, c_vp]),
     "rldx_ss_epilogue_ln_bf16": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_f32, c_vp]),
     "rldx_add_rmsnorm_bf16": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_f32, c_vp]),
+    "rldx_rms_norm_bf16": (c_i32, [c_vp, c_i64, c_vp, c_i32, c_vp, c_i64, c_i64, c_i64, c_f32, c_vp]),
+    "rldx_rms_norm_f32": (c_i32, [c_vp, c_i64, c_vp, c_i32, c_vp, c_i64, c_i64, c_i64, c_f32, c_vp]),
+    "rldx_rope_interleaved_bf16": (c_i32, [c_vp, c_i64p, c_vp, c_i64p, c_vp, c_i64p, c_vp, c_i64p, c_i64, c_i64, c_i64,
+                                           c_i64, c_i64, c_vp, c_i64p, c_vp]),
+    "rldx_rope_interleaved_f32": (c_i32, [c_vp, c_i64p, c_vp, c_i64p, c_vp, c_i64p, c_vp, c_i64p, c_i64, c_i64, c_i64,
+                                          c_i64, c_i64, c_vp, c_i64p, c_vp]),
 }
 
 ROPE_SIN_SIGNED = 1  # RLDX_ROPE_SIN_SIGNED
+ROPE_NO_NORM = 2  # RLDX_ROPE_NO_NORM
 GEMM_EPI_BIAS, GEMM_EPI_RESIDUAL, GEMM_EPI_SWIGLU, GEMM_EPI_SWIGLU_PACKED, GEMM_EPI_BIAS_PACKED = 0, 1, 2, 3, 4
 GEMM_EPI_RESIDUAL_PACKED = 5
 GEMM_WIDE_TILES = 1  # RLDX_GEMM_WIDE_TILES

@@ -121,6 +121,44 @@ def install() -> dict:
     return done
 
 
+# model-level mirrors: reference module -> mirror module
+_MODEL = {
+    "rldx.model.modules.norms": __name__ + ".model.modules.norms",
+    "rldx.model.modules.action_model.ops": __name__ + ".model.modules.action_model.ops",
+    "rldx.model.modules.backbone.modeling_qwen3_vl": __name__ + ".model.modules.backbone.modeling_qwen3_vl",
+}
+
+
+def install_model() -> dict:
+    """Model-level drop-in: RMSNorm / create_norm_layer / create_qk_norm_layers
+    (rldx/model/modules/norms.py), precompute_freqs_cis / apply_rotary_emb /
+    SwiGLUFFN (action_model/ops.py), rotate_half / apply_rotary_pos_emb
+    (backbone/modeling_qwen3_vl.py).  Where the reference module imports, its
+    attributes of those names are replaced (call this before the model is
+    built: its blocks bind the names at construction); where it does not, the
+    mirror is registered under its name.  Returns {reference name: module}."""
+    done = {}
+    for ref_name, ours in _MODEL.items():
+        mod = importlib.import_module(ours)
+        try:
+            ref = importlib.import_module(ref_name)
+        except ImportError:
+            ref = None
+        if ref is not None and ref is not mod:
+            for attr in mod.__all__:
+                setattr(ref, attr, getattr(mod, attr))
+            done[ref_name] = ref
+            continue
+        _parent_packages(ref_name)
+        if sys.modules.get(ref_name) is not mod:
+            _added.append(ref_name)
+        sys.modules[ref_name] = mod
+        parent, _, leaf = ref_name.rpartition(".")
+        setattr(sys.modules[parent], leaf, mod)
+        done[ref_name] = mod
+    return done
+
+
 def uninstall() -> None:
     """Remove what install() registered (the operators stay registered)."""
     while _added:

@@ -122,18 +122,35 @@ def qk_rmsnorm_rope_half(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tenso
     `sin_is_signed`: `sin` is the pre-signed table of
     fused_llm_attention.prepare_signed_sin (first half negated).
     rldx/model/modules/backbone/modeling_qwen3_vl.py:356-401."""
+    return _rope_half(q, k, q_weight, k_weight, cos, sin, eps, sin_is_signed, q_out, k_out)
+
+
+def rope_half(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *,
+              sin_is_signed: bool = False, q_out: Optional[torch.Tensor] = None,
+              k_out: Optional[torch.Tensor] = None):
+    """Rotate-half RoPE alone, q' = q cos + rotate_half(q) sin in the input type
+    (each product and the sum rounded, as eager bf16), on the same layouts as
+    qk_rmsnorm_rope_half (RLDX_ROPE_NO_NORM).
+    rldx/model/modules/backbone/modeling_qwen3_vl.py:377-401."""
+    return _rope_half(q, k, None, None, cos, sin, 0.0, sin_is_signed, q_out, k_out)
+
+
+def _rope_half(q, k, q_weight, k_weight, cos, sin, eps, sin_is_signed, q_out, k_out):
     _on_gpu(q, k, q_weight, k_weight, cos, sin, q_out, k_out)
+    norm = q_weight is not None
     dt = q.dtype
-    _require(dt in (F32, BF16), "qk_rmsnorm_rope_half supports float32 and bfloat16")
+    _require(dt in (F32, BF16), "rotate-half RoPE supports float32 and bfloat16")
     for t in (k, q_weight, k_weight, cos, sin):
-        _require(t.dtype == dt, "all inputs must share one dtype")
+        _require(t is None or t.dtype == dt, "all inputs must share one dtype")
     _require(q.dim() == 4 and k.dim() == 4, "q and k must be [B, S, H, D]")
     B, S, Hq, D = q.shape
     _require(k.shape[0] == B and k.shape[1] == S and k.shape[3] == D, "k must be [B, S, Hk, D] matching q")
     Hk = k.shape[2]
     _require(D in (64, 128), "head_dim must be 64 or 128")
-    _require(q_weight.shape == (D,) and k_weight.shape == (D,), "norm weights must be [D]")
-    _require(q_weight.is_contiguous() and k_weight.is_contiguous(), "norm weights must be contiguous")
+    if norm:
+        _require(k_weight is not None and q_weight.shape == (D,) and k_weight.shape == (D,),
+                 "norm weights must be [D]")
+        _require(q_weight.is_contiguous() and k_weight.is_contiguous(), "norm weights must be contiguous")
     if cos.dim() == 2:
         cos = cos.unsqueeze(0)
         sin = sin.unsqueeze(0)
@@ -155,11 +172,69 @@ def qk_rmsnorm_rope_half(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tenso
         return q_out, k_out
     lib = _lib.load()
     fn = lib.rldx_qk_rmsnorm_rope_half_f32 if dt == F32 else lib.rldx_qk_rmsnorm_rope_half_bf16
-    flags = _lib.ROPE_SIN_SIGNED if sin_is_signed else 0
-    _lib.check(fn(q.data_ptr(), k.data_ptr(), q_weight.data_ptr(), k_weight.data_ptr(), cos.data_ptr(),
-                  sin.data_ptr(), q_out.data_ptr(), k_out.data_ptr(), B, S, Hq, Hk, D, qs, ks, qos, kos, css,
-                  float(eps), flags, _stream_ptr(q)), "rldx_qk_rmsnorm_rope_half")
+    flags = (_lib.ROPE_SIN_SIGNED if sin_is_signed else 0) | (0 if norm else _lib.ROPE_NO_NORM)
+    _lib.check(fn(q.data_ptr(), k.data_ptr(), _ptr(q_weight), _ptr(k_weight), cos.data_ptr(), sin.data_ptr(),
+                  q_out.data_ptr(), k_out.data_ptr(), B, S, Hq, Hk, D, qs, ks, qos, kos, css, float(eps), flags,
+                  _stream_ptr(q)), "rldx_qk_rmsnorm_rope_half")
     return q_out, k_out
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+             out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """RMSNorm with one rounding: (weight * (x * rsqrt(mean(x^2) + eps))).to(x.dtype)
+    over the last dimension, fp32 arithmetic; x bf16 or fp32, weight fp32 or bf16
+    (rldx/model/modules/norms.py:18-22; rldx_rms_norm_bf16 / _f32)."""
+    _on_gpu(x, weight, out)
+    dt = x.dtype
+    _require(dt in (F32, BF16), "rms_norm supports float32 and bfloat16 inputs")
+    _require(weight.dtype in (F32, BF16) and weight.dim() == 1 and weight.is_contiguous(),
+             "weight must be a contiguous float32 or bfloat16 vector")
+    dim = x.shape[-1]
+    _require(weight.numel() == dim, "weight must have the last dimension's size")
+    rows, ld = _rows_view(x, "x")
+    if out is None:
+        out = torch.empty(x.shape, dtype=dt, device=x.device)
+    _require(out.shape == x.shape and out.dtype == dt, "out must match x")
+    orows, old = _rows_view(out, "out")
+    if rows == 0:
+        return out
+    lib = _lib.load()
+    fn = lib.rldx_rms_norm_bf16 if dt == BF16 else lib.rldx_rms_norm_f32
+    _lib.check(fn(x.data_ptr(), ld, weight.data_ptr(), 1 if weight.dtype == F32 else 0, out.data_ptr(), old, rows, dim,
+                  float(eps), _stream_ptr(x)), "rldx_rms_norm")
+    return out
+
+
+def rope_interleaved(xq: torch.Tensor, xk: torch.Tensor, freqs_cis: torch.Tensor):
+    """Interleaved (complex) RoPE: pairs (x[2i], x[2i+1]) times freqs_cis[n][i] in
+    fp32, rounded once to the input type.  xq [B, Hq, N, D], xk [B, Hk, N, D]
+    (bf16 or fp32, D contiguous); freqs_cis complex64 [N, D/2], [1, N, D/2] or
+    [B, N, D/2].  Returns new contiguous (xq_out, xk_out)
+    (rldx/model/modules/action_model/ops.py:48-67; rldx_rope_interleaved_*)."""
+    _on_gpu(xq, xk, freqs_cis)
+    dt = xq.dtype
+    _require(dt in (F32, BF16) and xk.dtype == dt, "xq and xk must share one dtype, float32 or bfloat16")
+    _require(xq.dim() == 4 and xk.dim() == 4, "xq and xk must be [B, H, N, D]")
+    B, Hq, N, D = xq.shape
+    _require(xk.shape[0] == B and xk.shape[2] == N and xk.shape[3] == D, "xk must be [B, Hk, N, D] matching xq")
+    _require(freqs_cis.dtype == torch.complex64, "freqs_cis must be complex64")
+    f = freqs_cis if freqs_cis.dim() == 3 else freqs_cis.unsqueeze(0)
+    _require(f.dim() == 3 and f.shape[1:] == (N, D // 2) and f.shape[0] in (1, B),
+             "freqs_cis must be [N, D/2] or [B or 1, N, D/2]")
+    _require(f.stride(-1) == 1 and xq.stride(-1) == 1 and xk.stride(-1) == 1, "last dims must be contiguous")
+    fb = f.stride(0) if f.shape[0] == B and B > 1 else 0
+    qo, ko = torch.empty_like(xq, memory_format=torch.contiguous_format), torch.empty_like(
+        xk, memory_format=torch.contiguous_format)
+    if xq.numel() + xk.numel() == 0:
+        return qo, ko
+    st = lambda t: _lib.i64_array([t.stride(0), t.stride(1), t.stride(2)])  # noqa: E731
+    lib = _lib.load()
+    fn = lib.rldx_rope_interleaved_bf16 if dt == BF16 else lib.rldx_rope_interleaved_f32
+    fr = torch.view_as_real(f)
+    _lib.check(fn(xq.data_ptr(), st(xq), qo.data_ptr(), st(qo), xk.data_ptr(), st(xk), ko.data_ptr(), st(ko), B, Hq,
+                  xk.shape[1], N, D, fr.data_ptr(), _lib.i64_array([fb, f.stride(1)]), _stream_ptr(xq)),
+               "rldx_rope_interleaved")
+    return qo, ko
 
 
 # ---------------------------------------------------------------------------

@@ -87,6 +87,38 @@ def test_epilogue_norm_abi_rejects_bad_arguments_without_launching():
     assert lib.rldx_add_rmsnorm_bf16(None, None, None, None, None, None, 0, 2048, 1e-6, None) == 0
 
 
+def test_model_ops_abi_rejects_bad_arguments_without_launching():
+    lib = _lib.load()
+    p = 16  # stand-in device address, 16-byte aligned: every call below must fail validation
+    # RMSNorm: width not a multiple of 8 (bf16) / 4 (fp32), wider than 8192, row stride below the width,
+    # missing weight, negative eps, misaligned fp32 weight
+    assert lib.rldx_rms_norm_bf16(p, 12, p, 1, p, 12, 2, 12, 1e-6, None) == HIP_INVALID_VALUE
+    assert lib.rldx_rms_norm_bf16(p, 8200, p, 1, p, 8200, 2, 8200, 1e-6, None) == HIP_INVALID_VALUE
+    assert lib.rldx_rms_norm_f32(p, 6, p, 1, p, 8, 2, 6, 1e-6, None) == HIP_INVALID_VALUE
+    assert lib.rldx_rms_norm_f32(p, 64, p, 1, p, 32, 2, 64, 1e-6, None) == HIP_INVALID_VALUE
+    assert lib.rldx_rms_norm_bf16(p, 64, None, 1, p, 64, 2, 64, 1e-6, None) == HIP_INVALID_VALUE
+    assert lib.rldx_rms_norm_bf16(p, 64, p, 1, p, 64, 2, 64, -1.0, None) == HIP_INVALID_VALUE
+    assert lib.rldx_rms_norm_bf16(p, 64, p + 4, 1, p, 64, 2, 64, 1e-6, None) == HIP_INVALID_VALUE
+    assert lib.rldx_rms_norm_bf16(None, 64, None, 1, None, 64, 0, 64, 1e-6, None) == 0  # nothing to do
+    # interleaved RoPE: head_dim not a multiple of 8, odd table stride, table rows narrower than D / 2,
+    # misaligned table, missing output
+    st = _lib.i64_array([64 * 4 * 8, 64 * 8, 64])
+    fs = _lib.i64_array([0, 32])
+    args = (p, st, p, st, p, st, p, st, 1, 4, 4, 8)
+    assert lib.rldx_rope_interleaved_bf16(*args, 60, p, fs, None) == HIP_INVALID_VALUE
+    assert lib.rldx_rope_interleaved_bf16(*args, 64, p, _lib.i64_array([0, 33]), None) == HIP_INVALID_VALUE
+    assert lib.rldx_rope_interleaved_bf16(*args, 64, p, _lib.i64_array([0, 16]), None) == HIP_INVALID_VALUE
+    assert lib.rldx_rope_interleaved_bf16(*args, 64, p + 8, fs, None) == HIP_INVALID_VALUE
+    assert lib.rldx_rope_interleaved_f32(p, st, None, st, p, st, p, st, 1, 4, 4, 8, 64, p, fs,
+                                         None) == HIP_INVALID_VALUE
+    # rotate-half RoPE alone: weights may be null; unknown flag bits are rejected
+    cs = _lib.i64_array([0, 64])
+    assert lib.rldx_qk_rmsnorm_rope_half_bf16(p, p, None, None, p, p, p, p, 1, 4, 2, 2, 64, st, st, st, st, cs, 1e-6,
+                                              8, None) == HIP_INVALID_VALUE
+    assert lib.rldx_qk_rmsnorm_rope_half_bf16(p, p, None, None, p, p, p, p, 1, 4, 2, 2, 64, st, st, st, st, cs, 1e-6,
+                                              0, None) == HIP_INVALID_VALUE  # norm without weights
+
+
 def test_capi_rejects_bad_arguments_without_launching():
     lib = _lib.load()
     # ldx smaller than 2*n_half

@@ -172,3 +172,71 @@ def test_setup_helpers_closed_forms(installed):
     cos, ssin = prepare_rope_buffers(Rotary(), torch.arange(5)[None], "cpu")
     c_ref, s_ref = Rotary()(torch.empty(0, dtype=torch.bfloat16), torch.arange(5)[None])
     assert torch.equal(cos, c_ref[0]) and torch.equal(ssin, prepare_signed_sin(s_ref[0], D))
+
+
+# ---------------------------------------------------------------------------
+# model-level mirrors
+# ---------------------------------------------------------------------------
+@pytest.fixture
+def model_installed():
+    yield compat.install_model()
+    compat.uninstall()
+
+
+MODEL_SIGNATURES = [
+    ("rldx.model.modules.norms", "create_norm_layer", [("norm_type", _EMPTY), ("dim", _EMPTY), ("eps", 1e-6)],
+     "norms.py:25"),
+    ("rldx.model.modules.norms", "create_qk_norm_layers", [("qk_norm", _EMPTY), ("head_dim", _EMPTY), ("eps", 1e-6)],
+     "norms.py:44"),
+    ("rldx.model.modules.action_model.ops", "precompute_freqs_cis",
+     [("dim", _EMPTY), ("end", _EMPTY), ("theta", 10000.0)], "action_model/ops.py:11"),
+    ("rldx.model.modules.action_model.ops", "apply_rotary_emb",
+     [("xq", _EMPTY), ("xk", _EMPTY), ("freqs_cis", _EMPTY)], "action_model/ops.py:48-52"),
+    ("rldx.model.modules.backbone.modeling_qwen3_vl", "apply_rotary_pos_emb",
+     [("q", _EMPTY), ("k", _EMPTY), ("cos", _EMPTY), ("sin", _EMPTY), ("position_ids", None), ("unsqueeze_dim", 1)],
+     "modeling_qwen3_vl.py:377"),
+    ("rldx.model.modules.backbone.modeling_qwen3_vl", "rotate_half", [("x", _EMPTY)], "modeling_qwen3_vl.py:118"),
+]
+
+
+@pytest.mark.parametrize("module,fn,params,cite", MODEL_SIGNATURES, ids=[f for _, f, _, _ in MODEL_SIGNATURES])
+def test_model_function_signatures(model_installed, module, fn, params, cite):
+    f = getattr(sys.modules[module], fn)
+    assert [(p.name, p.default) for p in inspect.signature(f).parameters.values()] == params, cite
+
+
+def test_model_modules_match_reference_constructors_and_parameters(model_installed):
+    """Constructor signatures and state-dict names, so reference checkpoints load
+    (norms.py:13-16, action_model/ops.py:143-157)."""
+    from rldx.model.modules.action_model.ops import SwiGLUFFN
+    from rldx.model.modules.backbone.modeling_qwen3_vl import rotate_half
+    from rldx.model.modules.norms import RMSNorm, create_norm_layer, create_qk_norm_layers
+
+    assert [(p.name, p.default) for p in list(inspect.signature(RMSNorm.__init__).parameters.values())[1:]] == \
+        [("dim", _EMPTY), ("eps", 1e-6)]
+    assert [(p.name, p.default) for p in list(inspect.signature(SwiGLUFFN.__init__).parameters.values())[1:]] == \
+        [("in_features", _EMPTY), ("hidden_features", None), ("out_features", None), ("act_layer", None),
+         ("drop", 0.0), ("bias", True)]
+    n = RMSNorm(64)
+    assert list(n.state_dict()) == ["weight"] and n.weight.dtype == torch.float32 and torch.equal(n.weight, torch.ones(64))
+    f = SwiGLUFFN(1536, 4096)
+    assert {k: tuple(v.shape) for k, v in f.state_dict().items()} == {
+        "w12.weight": (8192, 1536), "w12.bias": (8192,), "w3.weight": (1536, 4096), "w3.bias": (1536,)}
+    assert list(SwiGLUFFN(128, 64, 32, bias=False).state_dict()) == ["w12.weight", "w3.weight"]
+    assert isinstance(create_norm_layer("rms_norm", 64), RMSNorm)
+    assert all(isinstance(m, torch.nn.Identity) for m in create_qk_norm_layers("none", 64))
+    with pytest.raises(ValueError):
+        create_norm_layer("batch_norm", 64)
+    x = torch.arange(8.0).reshape(2, 4)
+    assert torch.equal(rotate_half(x), torch.tensor([[-2.0, -3.0, 0.0, 1.0], [-6.0, -7.0, 4.0, 5.0]]))
+
+
+def test_precompute_freqs_cis_closed_form(model_installed):
+    """freqs[n][i] = exp(i n theta^(-2i/D)): unit modulus, angle n * theta^(-2i/D)."""
+    from rldx.model.modules.action_model.ops import precompute_freqs_cis
+
+    f = precompute_freqs_cis(8, 5, 100.0).to(torch.complex128)
+    n = torch.arange(5, dtype=torch.float64)[:, None]
+    ang = n * 100.0 ** (-torch.arange(0, 8, 2, dtype=torch.float64) / 8)
+    assert f.shape == (5, 4) and torch.allclose(f.abs(), torch.ones(5, 4, dtype=torch.float64), atol=1e-6)
+    assert torch.allclose(f, torch.polar(torch.ones_like(ang), ang), atol=1e-5)

@@ -11,7 +11,7 @@ import torch
 from oracle import cpu_reference as ref
 from rldx_amd import compat
 from rldx_amd import workloads as W
-from tolerances import assert_bf16_close
+from tolerances import assert_bf16_close, assert_fp32_close
 
 pytestmark = pytest.mark.gpu
 BF16 = torch.bfloat16
@@ -153,3 +153,133 @@ def test_vision_and_memory_launchers(dev, mods):
     assert_bf16_close(normed, rnorm, "memory fused_add2_rmsnorm.forward")
     new2, normed2 = torch.ops.mem.fused_epilogue_add2_rmsnorm(h.to(dev), res.to(dev), wt.to(dev))
     assert torch.equal(new2, new) and torch.equal(normed2, normed)
+
+
+# ---------------------------------------------------------------------------
+# model-level mirrors (rldx.model.modules.*)
+# ---------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def model():
+    compat.install_model()
+    yield sys.modules
+    compat.uninstall()
+
+
+@pytest.mark.parametrize("shape,wdtype", [((2, 24, 82, 64), torch.float32), ((1, 12, 608, 128), torch.bfloat16),
+                                          ((3, 7, 1536), torch.float32), ((64, 2048), torch.bfloat16),
+                                          ((5, 72), torch.float32), ((2, 4, 5, 4096), torch.float32)])
+def test_rmsnorm_module(dev, model, shape, wdtype):
+    """RMSNorm (norms.py:7-22) against the oracle's one-rounding restatement: bf16
+    rows within the bf16 contract, fp32 rows within 1e-5; weight fp32 (the
+    parameter) or bf16 (a model cast to bf16)."""
+    from rldx.model.modules.norms import RMSNorm
+
+    g = torch.Generator().manual_seed(sum(shape))
+    n = RMSNorm(shape[-1], eps=1e-6)
+    with torch.no_grad():
+        n.weight.copy_(1 + 0.1 * torch.randn(shape[-1], generator=g))
+    n = n.to(dev, wdtype)
+    x = torch.randn(*shape, generator=g).to(BF16)
+    y = n(x.to(dev))
+    r = ref.msat_rmsnorm(x, n.weight.detach().cpu(), 1e-6)
+    assert y.dtype == BF16 and y.shape == x.shape
+    assert_bf16_close(y, r, f"RMSNorm bf16 {shape}")
+    xf = torch.randn(*shape, generator=g)
+    yf = n(xf.to(dev))
+    assert yf.dtype == torch.float32
+    assert_fp32_close(yf, ref.msat_rmsnorm(xf, n.weight.detach().cpu(), 1e-6), f"RMSNorm fp32 {shape}")
+
+
+def test_layernorm_from_create_norm_layer(dev, model):
+    from rldx.model.modules.norms import create_norm_layer, create_qk_norm_layers
+
+    g = torch.Generator().manual_seed(7)
+    x = (torch.randn(2, 82, 1536, generator=g) * 2 + 0.3).to(BF16)
+    y = create_norm_layer("layer_norm", 1536)(x.to(dev))
+    assert_bf16_close(y, ref.layer_norm(x), "create_norm_layer('layer_norm')")
+    qn, kn = create_qk_norm_layers("rms_norm", 64)
+    xq = torch.randn(1, 24, 82, 64, generator=g).to(BF16)
+    assert_bf16_close(qn.to(dev)(xq.to(dev)), ref.msat_rmsnorm(xq, torch.ones(64)), "create_qk_norm_layers")
+
+
+@pytest.mark.parametrize("dtype", [BF16, torch.float32])
+@pytest.mark.parametrize("fshape", ["nd", "bnd"])
+def test_apply_rotary_emb(dev, model, dtype, fshape):
+    """Interleaved RoPE (action_model/ops.py:48-67) against the oracle's complex
+    multiplication: a permuted (non-contiguous) q, a separately shaped k, tables
+    [N, D/2] or [B, N, D/2] from precompute_freqs_cis."""
+    from rldx.model.modules.action_model.ops import apply_rotary_emb, precompute_freqs_cis
+
+    g = torch.Generator().manual_seed(11)
+    B, H, N, D = 2, 6, 37, 64
+    xq = torch.randn(B, N, H, D, generator=g).to(dtype).permute(0, 2, 1, 3)  # [B, H, N, D] view
+    xk = torch.randn(B, 2 * H, N, D, generator=g).to(dtype)
+    f = precompute_freqs_cis(D, 64)[:N]
+    if fshape == "bnd":
+        f = torch.stack([f, precompute_freqs_cis(D, 64, theta=500.0)[5:5 + N]])
+    qo, ko = apply_rotary_emb(xq.to(dev), xk.to(dev), f.to(dev))
+    fr = f if f.dim() == 3 else f.expand(B, N, D // 2)
+    rq = ref.apply_rotary_emb(xq, xq, fr)[0]
+    rk = ref.apply_rotary_emb(xk, xk, fr)[0]
+    close = assert_bf16_close if dtype == BF16 else assert_fp32_close
+    assert qo.dtype == dtype and qo.shape == (B, H, N, D) and ko.shape == (B, 2 * H, N, D)
+    close(qo, rq, f"apply_rotary_emb q {dtype} {fshape}")
+    close(ko, rk, f"apply_rotary_emb k {dtype} {fshape}")
+
+
+@pytest.mark.parametrize("dtype", [BF16, torch.float32])
+@pytest.mark.parametrize("unsqueeze_dim", [1, 2])
+def test_apply_rotary_pos_emb(dev, model, dtype, unsqueeze_dim):
+    """Rotate-half RoPE alone (modeling_qwen3_vl.py:377-401): bf16 bit-exact with
+    the eager op order (two rounded products, rounded sum), fp32 within 1e-5;
+    q [B, H, S, D] (unsqueeze_dim 1) or [B, S, H, D] (2), per-batch tables."""
+    from rldx.model.modules.backbone.modeling_qwen3_vl import apply_rotary_pos_emb
+
+    g = torch.Generator().manual_seed(13 + unsqueeze_dim)
+    B, H, Hk, S, D = 2, 8, 2, 45, 128
+    qs, ks = ((B, H, S, D), (B, Hk, S, D)) if unsqueeze_dim == 1 else ((B, S, H, D), (B, S, Hk, D))
+    q, k = torch.randn(*qs, generator=g).to(dtype), torch.randn(*ks, generator=g).to(dtype)
+    cos, sin = W.qwen_rope_cos_sin(S + 3, D, 1e6, dtype=dtype)
+    cos = torch.stack([cos[:S], cos[3:]])
+    sin = torch.stack([sin[:S], sin[3:]])
+    qo, ko = apply_rotary_pos_emb(q.to(dev), k.to(dev), cos.to(dev), sin.to(dev), unsqueeze_dim=unsqueeze_dim)
+    rq, rk = ref.apply_rotary_pos_emb(q, k, cos, sin, unsqueeze_dim=unsqueeze_dim)
+    assert qo.shape == q.shape and ko.shape == k.shape
+    if dtype == BF16:
+        assert _eq(qo, rq) and _eq(ko, rk)
+    else:
+        assert_fp32_close(qo, rq, "apply_rotary_pos_emb q fp32")
+        assert_fp32_close(ko, rk, "apply_rotary_pos_emb k fp32")
+
+
+@pytest.mark.parametrize("dims", [(1536, 4096, 1536), (4096, 10922, 4096), (1536, 6144, 1536)])
+def test_swiglu_ffn_module(dev, model, dims):
+    """SwiGLUFFN (action_model/ops.py:137-161) at the MSAT's widths (SA, VL with
+    its padded hidden 10922, SS) against an eager bf16 composition on the same
+    weights: linear (fp32 sum + bias, one rounding), silu, product, linear.
+    w3 is drawn with std 0.01 sqrt(4096 / hidden) so that |y| stays below 4
+    (above it one bf16 ulp, 0.031, exceeds the 2e-2 bound, and the GEMM's and
+    the CPU's fp32 sums, in different orders, flip a rounding now and then)."""
+    from rldx.model.modules.action_model.ops import SwiGLUFFN
+
+    i, h, o = dims
+    g = torch.Generator().manual_seed(h)
+    m = SwiGLUFFN(i, h, o)
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            std = 0.01 * (4096 / h) ** 0.5 if name == "w3.weight" else 0.02
+            p.copy_(std * torch.randn(p.shape, generator=g))
+    m = m.to(dev, BF16)
+    x = torch.randn(1, 82, i, generator=g).to(BF16)
+    y = m(x.to(dev))
+    sd = {k: v.detach().cpu() for k, v in m.state_dict().items()}
+    x12 = (x[0].float() @ sd["w12.weight"].float().t() + sd["w12.bias"].float()).to(BF16)
+    hid = ref.swiglu(x12)
+    r = (hid.float() @ sd["w3.weight"].float().t() + sd["w3.bias"].float()).to(BF16)
+    assert y.shape == (1, 82, o)
+    assert_bf16_close(y[0], r, f"SwiGLUFFN {dims}")
+    with torch.no_grad():  # an in-place weight update repacks
+        m.w3.weight.mul_(0.5)
+    y2 = m(x.to(dev))
+    r2 = (hid.float() @ (sd["w3.weight"].float() * 0.5).to(BF16).float().t() + sd["w3.bias"].float()).to(BF16)
+    assert_bf16_close(y2[0], r2, f"SwiGLUFFN {dims} after an in-place update")
