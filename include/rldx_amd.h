@@ -521,6 +521,29 @@ hipError_t rldx_grouped_gemm_stats_bf16(const rldx_gemm_group_t* groups, float* 
                                         int32_t flags, void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
+ * The grouped GEMM with a shape per group: groups[i] multiplies by its own
+ * W [n[i], k[i]] (each n a multiple of 64, each k of 128) and splits its K
+ * range over split_k[i] workgroups (NULL: no split; as in
+ * rldx_grouped_gemm_ws_bf16, the largest power of two <= split_k[i] that
+ * divides its stages), all in one launch with one epilogue (not the QKV one).
+ * For the linears of a block whose streams have different widths (the SA and
+ * VL streams of an RLDX-1 double-stream block): the short stream's tiles run
+ * beside the long one's instead of in a launch of their own.  ln_stats_out:
+ * as in rldx_grouped_gemm_stats_bf16, or NULL.  Workspace from
+ * rldx_grouped_gemm_mixed_workspace_bytes (-1: invalid call).  Each group's
+ * result is bit-identical to the same group launched alone with the same split.
+ * Replaces: the per-stream linears of DoubleStreamBlock.forward
+ *   (rldx/model/modules/action_model/blocks.py:500-609; custom_double_stream_chain.py:57-96).
+ */
+hipError_t rldx_grouped_gemm_mixed_bf16(const rldx_gemm_group_t* groups, const int64_t* n, const int64_t* k,
+                                        const int32_t* split_k, float* const* ln_stats_out, int32_t num_groups,
+                                        int32_t epilogue, int32_t flags, void* workspace, int64_t workspace_bytes,
+                                        hipStream_t stream);
+int64_t rldx_grouped_gemm_mixed_workspace_bytes(const rldx_gemm_group_t* groups, const int64_t* n, const int64_t* k,
+                                                const int32_t* split_k, int32_t num_groups, int32_t epilogue,
+                                                int32_t flags);
+
+/*
  * The pre-LayerNorm of an MSAT block folded into the grouped GEMM that consumes
  * it: y_s = LN(a_s) W_s^T + bias_s with LN the LayerNorm over the k columns
  * without affine parameters (eps ln_eps), from the un-normalised rows a_s

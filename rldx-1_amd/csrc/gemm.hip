@@ -169,6 +169,7 @@ struct Group {
   const uint16_t* res;
   int64_t ldo, ldr;
   int m, cfg, m_tiles, items;  // items = tiles x splits
+  int n, k;                     // this group's W [n, k] (n = 2 N_half with the SwiGLU epilogues)
   int wg_begin, per_xcd;        // first workgroup (multiple of 8); items per XCD
   int splits, ls_per;           // K splits across workgroups; K-group stages per split
   float* part;                  // split partials [tile][split][PER][512 threads][V]
@@ -199,7 +200,7 @@ struct QkvOut {
 struct GemmArgs {
   Group g[3];
   int num_groups;
-  int n, k;  // n = rows of W (2 * N_half with the SwiGLU epilogue)
+  int n, k;  // the first group's n, k (every group's with a uniform call); n = rows of W (2 N_half with SwiGLU)
   QkvOut qkv;
   int spread;    // != 0: the splits of a tile on different XCDs (RLDX_GEMM_SPLITS_ACROSS_XCDS)
   float ln_eps;  // LayerNorm fold (kernels instantiated with LN)
@@ -241,10 +242,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   const int l32 = lane & 31, g = lane >> 5;
   const int tile = item / G.splits, split = item % G.splits;
   const int mt = tile % G.m_tiles, nt = tile / G.m_tiles;
-  const int ksteps = a.k / 16;
+  const int ksteps = G.k / 16;
   const int lstages = G.ls_per;         // K-group stages of this split
   const int st0 = split * G.ls_per;     // its first stage
-  const int mblocks = (G.m + 31) / 32, nblocks = a.n / 32;
+  const int mblocks = (G.m + 31) / 32, nblocks = G.n / 32;
 
   // The chunks this wave loads per stage: q = wl + j WPG, k-step q / CH, chunk
   // q % CH (m-blocks first, then n-blocks; blocks past the edge re-read the
@@ -298,7 +299,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   constexpr int CPR = OC / 8;                      // 16-byte output chunks per row
   constexpr int PER = (R * CPR + kThreads - 1) / kThreads;
   static_assert(kThreads % CPR == 0, "a thread keeps its column chunk");
-  const int n_out = kSwiglu ? a.n / 2 : a.n;
+  const int n_out = kSwiglu ? G.n / 2 : G.n;
   const int cc = 8 * (static_cast<int>(threadIdx.x) % CPR);
   const int col = nt * OC + cc;  // global output column of this thread's chunks
   const bool col_ok = col < n_out;
@@ -321,7 +322,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     braw[i] = G.bias && col_ok ? G.bias[col + i] : uint16_t{0};
-    braw[8 + i] = kSwiglu && G.bias && col_ok ? G.bias[a.n / 2 + col + i] : uint16_t{0};
+    braw[8 + i] = kSwiglu && G.bias && col_ok ? G.bias[G.n / 2 + col + i] : uint16_t{0};
   }
   uint32_t bpk[8];
   // LayerNorm fold: W row sums of this thread's columns (gate and up for SwiGLU);
@@ -334,7 +335,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     const floatx4 g0 = col_ok ? ws[0] : z, g1 = col_ok ? ws[1] : z;
     floatx4 u0 = z, u1 = z;
     if constexpr (kSwiglu) {
-      const floatx4* wu4 = reinterpret_cast<const floatx4*>(G.wsum + a.n / 2 + col);
+      const floatx4* wu4 = reinterpret_cast<const floatx4*>(G.wsum + G.n / 2 + col);
       u0 = col_ok ? wu4[0] : z;
       u1 = col_ok ? wu4[1] : z;
     }
@@ -359,7 +360,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   constexpr int RT = 32 * MB;  // tile rows
   [[maybe_unused]] f32x2_t lv[kLnSlotsMax];
   [[maybe_unused]] float lp1 = 0.f, lp2 = 0.f;
-  const int ln_slots = a.k / 64, ln_spl = (ln_slots * RT + kThreads - 1) / kThreads;
+  const int ln_slots = G.k / 64, ln_spl = (ln_slots * RT + kThreads - 1) / kThreads;
   const int ln_q = static_cast<int>(threadIdx.x) / RT;
   if constexpr (LN) {
     const int row = min(mt * RT + static_cast<int>(threadIdx.x) % RT, G.m - 1);
@@ -438,7 +439,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
       s1 += lnst[(p * R + r) * 2];
       s2 += lnst[(p * R + r) * 2 + 1];
     }
-    const float inv_k = 1.0f / static_cast<float>(a.k);
+    const float inv_k = 1.0f / static_cast<float>(G.k);
     const float mean = s1 * inv_k;
     const float var = __builtin_fmaxf(__builtin_fmaf(-mean, mean, s2 * inv_k), 0.f);
     rs = __builtin_amdgcn_rsqf(var + a.ln_eps);
@@ -698,7 +699,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
           f32x2_t* st = reinterpret_cast<f32x2_t*>(G.stats_out) + static_cast<int64_t>(nt * (OC / 64)) * G.m + row;
           *st = f32x2_t{s1, s2};
           if constexpr (OC == 128)
-            if (2 * nt + 1 < a.n / 64) st[G.m] = f32x2_t{0.f, 0.f};
+            if (2 * nt + 1 < G.n / 64) st[G.m] = f32x2_t{0.f, 0.f};
         }
         continue;
       }
@@ -821,8 +822,21 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
                 int split_k, GemmArgs& args, int64_t* ws_bytes, int64_t* cnt_off, int64_t* part_off,
                 const rldx_msat_stream_t* norms = nullptr, bool wide_tiles = false,
                 const float* const* w_row_sums = nullptr, const float* const* ln_stats = nullptr,
-                float* const* stats_out = nullptr) {
+                float* const* stats_out = nullptr, const int64_t* group_n = nullptr,
+                const int64_t* group_k = nullptr, const int32_t* group_splits = nullptr) {
   if (!groups || num_groups < 1 || num_groups > 3) return hipErrorInvalidValue;
+  // per-group shapes (rldx_grouped_gemm_mixed_bf16): every group its own n, k and split
+  if ((group_n == nullptr) != (group_k == nullptr)) return hipErrorInvalidValue;
+  if (group_n) {
+    n = group_n[0];
+    k = group_k[0];
+    for (int i = 0; i < num_groups; ++i) {
+      if (group_n[i] <= 0 || group_k[i] <= 0) return hipErrorInvalidValue;
+      if (group_splits && (group_splits[i] < 1 || group_splits[i] > 64)) return hipErrorInvalidValue;
+    }
+  }
+  auto gn = [&](int i) { return group_n ? group_n[i] : n; };
+  auto gk = [&](int i) { return group_k ? group_k[i] : k; };
   if (!(epilogue >= kEpiBias && epilogue <= kEpiResidualPacked) && epilogue != kEpiQkv) return hipErrorInvalidValue;
   const bool qkv = epilogue == kEpiQkv;
   // LayerNorm fold: W row sums and A-row statistics for every group; k <= 2048
@@ -830,7 +844,8 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
   if ((w_row_sums == nullptr) != (ln_stats == nullptr)) return hipErrorInvalidValue;
   if (w_row_sums) {
     if (split_k > 1 || !(epilogue == kEpiBias || epilogue == kEpiSwigluPacked || qkv)) return hipErrorInvalidValue;
-    if (k > 64 * 4 * kLnSlotsMax) return hipErrorInvalidValue;
+    for (int i = 0; i < num_groups; ++i)
+      if (gk(i) > 64 * 4 * kLnSlotsMax) return hipErrorInvalidValue;
     for (int i = 0; i < num_groups; ++i)
       if (!w_row_sums[i] || reinterpret_cast<uintptr_t>(w_row_sums[i]) % 4 || !ln_stats[i] ||
           reinterpret_cast<uintptr_t>(ln_stats[i]) % 8)
@@ -842,19 +857,21 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
       if (!stats_out[i] || reinterpret_cast<uintptr_t>(stats_out[i]) % 8) return hipErrorInvalidValue;
   }
   const bool wide = qkv || wide_tiles;
-  if (qkv && (norms == nullptr || split_k > 1)) return hipErrorInvalidValue;
-  // k: whole stages of every K-group split (4 K-groups x 2 k-steps); n: whole 64-column blocks
-  if (n <= 0 || k <= 0 || n % 64 != 0 || k % 128 != 0) return hipErrorInvalidValue;
-  if (n > (1 << 30) || k > (1 << 30)) return hipErrorInvalidValue;
+  if (qkv && (norms == nullptr || split_k > 1 || group_n)) return hipErrorInvalidValue;
   const bool swiglu = epilogue == kEpiSwiglu || epilogue == kEpiSwigluPacked;
-  const int64_t n_out = swiglu ? n / 2 : n;
+  // k: whole stages of every K-group split (4 K-groups x 2 k-steps); n: whole 64-column blocks
+  for (int i = 0; i < num_groups; ++i)
+    if (gn(i) <= 0 || gk(i) <= 0 || gn(i) % 64 != 0 || gk(i) % 128 != 0 || gn(i) > (1 << 30) || gk(i) > (1 << 30))
+      return hipErrorInvalidValue;
   args = GemmArgs{};
   args.n = static_cast<int>(n);
   args.k = static_cast<int>(k);
-  const int ksteps = static_cast<int>(k / 16);
   int cnt = 0;
   int64_t m_begin = 0;  // joint-sequence row of the group (QKV epilogue)
   for (int i = 0; i < num_groups; ++i) {
+    const int64_t n = gn(i), k = gk(i);  // this group's shape
+    const int64_t n_out = swiglu ? n / 2 : n;
+    const int ksteps = static_cast<int>(k / 16);
     const rldx_gemm_group_t& s = groups[i];
     if (s.m < 0 || s.m > (1 << 24)) return hipErrorInvalidValue;
     if (s.m == 0) continue;
@@ -908,15 +925,17 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
     const int64_t tiles = static_cast<int64_t>(mt) * nt;
     if (tiles > (int64_t{1} << 24)) return hipErrorInvalidValue;
     const int lstages = ksteps / (2 * kg);
+    const int want = group_splits ? group_splits[i] : split_k;
     int sp = 1;
-    while (sp * 2 <= split_k && lstages % (sp * 2) == 0) sp *= 2;
+    while (sp * 2 <= want && lstages % (sp * 2) == 0) sp *= 2;
     Group& G = args.g[cnt++];
     G = Group{static_cast<const uint16_t*>(s.a_packed), static_cast<const uint16_t*>(s.w_packed),
               static_cast<const uint16_t*>(s.bias), static_cast<uint16_t*>(s.out),
               static_cast<const uint16_t*>(s.residual), packed_out(epilogue) && s.ldo == 0 ? n_out : s.ldo,
               epilogue == kEpiResidualPacked && s.ldr == 0 ? n_out : s.ldr,
               static_cast<int>(s.m), cfg, mt,
-              static_cast<int>(tiles * sp), 0, 0, sp, lstages / sp, nullptr, nullptr};
+              static_cast<int>(tiles * sp), static_cast<int>(n), static_cast<int>(k), 0, 0, sp, lstages / sp,
+              nullptr, nullptr};
     G.wsum = w_row_sums ? w_row_sums[i] : nullptr;
     G.lnstats = ln_stats ? ln_stats[i] : nullptr;
     G.stats_out = stats_out ? stats_out[i] : nullptr;
@@ -935,8 +954,8 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
   // heaviest workgroups first (they take the first slot of every CU; the short
   // streams' workgroups fill the second)
   for (int i = 1; i < cnt; ++i)
-    for (int j = i; j > 0 && tile_bytes(args.g[j].cfg, k) / args.g[j].splits >
-                                 tile_bytes(args.g[j - 1].cfg, k) / args.g[j - 1].splits;
+    for (int j = i; j > 0 && tile_bytes(args.g[j].cfg, args.g[j].k) / args.g[j].splits >
+                                 tile_bytes(args.g[j - 1].cfg, args.g[j - 1].k) / args.g[j - 1].splits;
          --j) {
       const Group t = args.g[j];
       args.g[j] = args.g[j - 1];
@@ -1180,14 +1199,15 @@ extern "C" int64_t rldx_grouped_gemm_workspace_bytes(const rldx_gemm_group_t* gr
 namespace {
 hipError_t gemm_ws(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, int64_t k, int32_t epilogue,
                    int32_t split_k, int32_t flags, void* workspace, int64_t workspace_bytes, hipStream_t stream,
-                   float* const* stats_out = nullptr) {
+                   float* const* stats_out = nullptr, const int64_t* group_n = nullptr,
+                   const int64_t* group_k = nullptr, const int32_t* group_splits = nullptr) {
   GemmArgs args;
   int64_t ws, co[3], po[3];
   if (epilogue == kEpiQkv || (flags & ~(RLDX_GEMM_WIDE_TILES | RLDX_GEMM_SPLITS_ACROSS_XCDS)))
     return hipErrorInvalidValue;
   const bool wide = (flags & RLDX_GEMM_WIDE_TILES) != 0;
   const hipError_t e = plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po, nullptr, wide, nullptr,
-                            nullptr, stats_out);
+                            nullptr, stats_out, group_n, group_k, group_splits);
   if (e != hipSuccess) return e;
   args.spread = (flags & RLDX_GEMM_SPLITS_ACROSS_XCDS) != 0;
   if (ws > 0) {
@@ -1256,6 +1276,27 @@ extern "C" hipError_t rldx_grouped_gemm_stats_bf16(const rldx_gemm_group_t* grou
   if (!ln_stats_out) return hipErrorInvalidValue;
   return gemm_ws(groups, num_groups, n, k, epilogue, split_k, flags, workspace, workspace_bytes, stream,
                  ln_stats_out);
+}
+
+extern "C" hipError_t rldx_grouped_gemm_mixed_bf16(const rldx_gemm_group_t* groups, const int64_t* n,
+                                                   const int64_t* k, const int32_t* split_k, float* const* ln_stats_out,
+                                                   int32_t num_groups, int32_t epilogue, int32_t flags,
+                                                   void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  if (!n || !k) return hipErrorInvalidValue;
+  return gemm_ws(groups, num_groups, 0, 0, epilogue, 1, flags, workspace, workspace_bytes, stream, ln_stats_out, n, k,
+                 split_k);
+}
+
+extern "C" int64_t rldx_grouped_gemm_mixed_workspace_bytes(const rldx_gemm_group_t* groups, const int64_t* n,
+                                                           const int64_t* k, const int32_t* split_k,
+                                                           int32_t num_groups, int32_t epilogue, int32_t flags) {
+  GemmArgs args;
+  int64_t ws, co[3], po[3];
+  if (!n || !k || epilogue == kEpiQkv || (flags & ~(RLDX_GEMM_WIDE_TILES | RLDX_GEMM_SPLITS_ACROSS_XCDS)) ||
+      plan(groups, num_groups, 0, 0, epilogue, 1, args, &ws, co, po, nullptr, (flags & RLDX_GEMM_WIDE_TILES) != 0,
+           nullptr, nullptr, nullptr, n, k, split_k) != hipSuccess)
+    return -1;
+  return ws;
 }
 
 namespace {

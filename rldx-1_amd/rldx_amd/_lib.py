@@ -114,6 +114,10 @@ SIGNATURES = {
     "rldx_grouped_gemm_stats_bf16": (c_i32, [ctypes.POINTER(GemmGroup), ctypes.POINTER(c_vp), c_i32, c_i64, c_i64,
                                              c_i32, c_i32, c_i32, c_vp, c_i64, c_vp]),
     "rldx_act_pack_stats_bf16": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp]),
+    "rldx_grouped_gemm_mixed_bf16": (c_i32, [ctypes.POINTER(GemmGroup), c_i64p, c_i64p, ctypes.POINTER(c_i32),
+                                             ctypes.POINTER(c_vp), c_i32, c_i32, c_i32, c_vp, c_i64, c_vp]),
+    "rldx_grouped_gemm_mixed_workspace_bytes": (c_i64, [ctypes.POINTER(GemmGroup), c_i64p, c_i64p,
+                                                        ctypes.POINTER(c_i32), c_i32, c_i32, c_i32]),
     "rldx_host_swiglu_bf16": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64]),
     "rldx_grouped_res_ln_bf16": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                          c_i64, c_i64, c_i64, c_i64, c_f32, c_vp]),

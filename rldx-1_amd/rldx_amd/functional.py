@@ -694,12 +694,17 @@ _GEMM_EPI = {"bias": _lib.GEMM_EPI_BIAS, "residual": _lib.GEMM_EPI_RESIDUAL, "sw
 _PACKED_EPI = (_lib.GEMM_EPI_SWIGLU_PACKED, _lib.GEMM_EPI_BIAS_PACKED, _lib.GEMM_EPI_RESIDUAL_PACKED)
 
 
+def _mixed(items: Sequence[tuple]) -> bool:
+    """Groups of different weight shapes (a launch of rldx_grouped_gemm_mixed_bf16)."""
+    return any((it[1].n, it[1].k) != (items[0][1].n, items[0][1].k) for it in items)
+
+
 def _gemm_groups(items: Sequence[tuple], epi: int, pack: bool):
     _require(1 <= len(items) <= 3, "between 1 and 3 groups")
-    n, k = items[0][1].n, items[0][1].k
     groups = (_lib.GemmGroup * len(items))()
     keep = []
     for i, (a, w, bias, out, res) in enumerate(items):
+        n, k = w.n, w.k
         if not isinstance(a, PackedAct):
             _require(isinstance(a, torch.Tensor) and a.dim() == 2, "a must be a PackedAct or a 2-D tensor")
             if not pack:  # shape-only query
@@ -708,7 +713,7 @@ def _gemm_groups(items: Sequence[tuple], epi: int, pack: bool):
                 a = pack_act(a)
                 keep.append(a)
         _on_gpu(a.data, w.data, bias, res if isinstance(res, torch.Tensor) else None)
-        _require(w.n == n and w.k == k and a.k == k and a.ld == k, "groups must share n and k")
+        _require(a.k == k and a.ld == k, "a must be a PackedAct [m, k] of the weight's k")
         swiglu = epi in (_lib.GEMM_EPI_SWIGLU, _lib.GEMM_EPI_SWIGLU_PACKED)
         _require(not swiglu or w.swiglu_pairs, "SwiGLU epilogue needs a swiglu_pairs weight")
         m = a.m
@@ -733,7 +738,16 @@ def _gemm_groups(items: Sequence[tuple], epi: int, pack: bool):
             _on_gpu(res.data)
             res_ptr, ldr = res.data.data_ptr(), (0 if res.ld == res.k else res.ld)
         groups[i] = _lib.GemmGroup(a.data.data_ptr(), m, w.data.data_ptr(), _ptr(bias), out_ptr, ldo, res_ptr, ldr)
-    return groups, n, k, keep, w.data
+    return groups, items[0][1].n, items[0][1].k, keep, w.data
+
+
+def _shape_arrays(items: Sequence[tuple], split_k):
+    """Per-group n, k (and split) arrays for the mixed-shape entry points."""
+    ns = _lib.i64_array([it[1].n for it in items])
+    ks = _lib.i64_array([it[1].k for it in items])
+    sp = [int(split_k)] * len(items) if isinstance(split_k, int) else [int(x) for x in split_k]
+    _require(len(sp) == len(items) and all(1 <= x <= 64 for x in sp), "one split factor in [1, 64] per group")
+    return ns, ks, (ctypes.c_int32 * len(items))(*sp), max(sp) > 1
 
 
 def grouped_gemm_workspace_bytes(items: Sequence[tuple], epilogue: str = "bias", split_k: int = 1,
@@ -741,8 +755,12 @@ def grouped_gemm_workspace_bytes(items: Sequence[tuple], epilogue: str = "bias",
     """Workspace bytes grouped_gemm(items, epilogue, split_k, workspace, wide_tiles) needs (0: no split)."""
     epi = _GEMM_EPI[epilogue]
     groups, n, k, _, _ = _gemm_groups(items, epi, pack=False)
-    r = _lib.load().rldx_grouped_gemm_ex_workspace_bytes(groups, len(items), n, k, epi, int(split_k),
-                                                         _lib.GEMM_WIDE_TILES if wide_tiles else 0)
+    flags = _lib.GEMM_WIDE_TILES if wide_tiles else 0
+    if _mixed(items) or not isinstance(split_k, int):
+        ns, ks, sp, _ = _shape_arrays(items, split_k)
+        r = _lib.load().rldx_grouped_gemm_mixed_workspace_bytes(groups, ns, ks, sp, len(items), epi, flags)
+    else:
+        r = _lib.load().rldx_grouped_gemm_ex_workspace_bytes(groups, len(items), n, k, epi, int(split_k), flags)
     _require(r >= 0, "grouped GEMM shape not supported")
     return int(r)
 
@@ -758,17 +776,18 @@ def _row_sums_array(items: Sequence[tuple]):
     return sums
 
 
-def _stats_array(items: Sequence[tuple], stats: Sequence[torch.Tensor], width: int):
+def _stats_array(items: Sequence[tuple], stats: Sequence[torch.Tensor], width: Optional[int]):
+    """Pointers to one statistics tensor per group, width columns (None: the group's own n)."""
     _require(len(stats) == len(items), "one statistics tensor per group")
     arr = (ctypes.c_void_p * len(items))()
     for i, (it, st) in enumerate(zip(items, stats)):
         a = it[0]
-        _check_stats(st, a.m if isinstance(a, PackedAct) else a.shape[0], width)
+        _check_stats(st, a.m if isinstance(a, PackedAct) else a.shape[0], it[1].n if width is None else width)
         arr[i] = st.data_ptr()
     return arr
 
 
-def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias", split_k: int = 1,
+def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias", split_k=1,
                  workspace: Optional[GemmWorkspace] = None, wide_tiles: bool = False,
                  splits_across_xcds: bool = False, ln_eps: Optional[float] = None,
                  ln_stats: Optional[Sequence[torch.Tensor]] = None,
@@ -791,10 +810,27 @@ def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias", split_k: int = 
     ...), LN without affine parameters with this eps; epilogues "bias" and
     "swiglu_packed", no split-K; the weights' row sums come from pack_weight.
     stats_out: the residual epilogues also write the statistics of the rows
-    they store, stats_out[i] [n / 64, m, 2] (rldx_grouped_gemm_stats_bf16)."""
+    they store, stats_out[i] [n / 64, m, 2] (rldx_grouped_gemm_stats_bf16).
+    Groups whose weights differ in shape (or split_k given per group) go to
+    rldx_grouped_gemm_mixed_bf16: one launch, each group its own n, k, split."""
     epi = _GEMM_EPI[epilogue]
     groups, n, k, keep, wt = _gemm_groups(items, epi, pack=True)
     lib = _lib.load()
+    if _mixed(items) or not isinstance(split_k, int):
+        _require(ln_eps is None, "the LayerNorm fold takes groups of one shape")
+        ns, ks, sp, split = _shape_arrays(items, split_k)
+        _require(not split or workspace is not None, "split factors > 1 need a GemmWorkspace")
+        if split:
+            _on_gpu(workspace.data)
+        ws_ptr, ws_n = (workspace.data.data_ptr(), workspace.data.numel()) if split else (None, 0)
+        outs = None
+        if stats_out is not None:
+            _require(epilogue in ("residual", "residual_packed"), "stats_out needs a residual epilogue")
+            outs = _stats_array(items, stats_out, None)
+        flags = (_lib.GEMM_WIDE_TILES if wide_tiles else 0) | (_lib.GEMM_SPLITS_ACROSS_XCDS if splits_across_xcds else 0)
+        _lib.check(lib.rldx_grouped_gemm_mixed_bf16(groups, ns, ks, sp, outs, len(items), epi, flags, ws_ptr, ws_n,
+                                                    _stream_ptr(wt)), "rldx_grouped_gemm_mixed_bf16")
+        return
     if ln_eps is not None:
         _require(split_k <= 1 and not splits_across_xcds, "the LayerNorm fold does not split K")
         _require(ln_stats is not None and stats_out is None, "the LayerNorm fold needs ln_stats")

@@ -233,6 +233,37 @@ def test_grouped_gemm_wide_tiles_plan():
                                          None) == HIP_INVALID_VALUE
 
 
+def test_grouped_gemm_mixed_plan_and_rejections():
+    """rldx_grouped_gemm_mixed_bf16: every group its own n, k and split; the
+    workspace is the sum of the groups' partials (each as a one-group launch of
+    its shape and split), and bad per-group shapes or splits, the QKV epilogue
+    and missing shape arrays are rejected before anything is launched."""
+    lib = _lib.load()
+    i64, i32 = _lib.i64_array, lambda v: (ctypes.c_int32 * len(v))(*v)
+    # DS-block W3 shapes: SA 18 x 1536 x 4096 (24 tiles of 32 x 64), VL 64 x 4096 x 11008 (64 tiles of 64 x 64)
+    g = _gemm_groups((18, 64))
+    ws = lib.rldx_grouped_gemm_mixed_workspace_bytes(g, i64([1536, 4096]), i64([4096, 11008]), i32([4, 2]), 2, 1, 0)
+    one = [lib.rldx_grouped_gemm_workspace_bytes(_gemm_groups((m,)), 1, n, k, 1, s)
+           for m, n, k, s in ((18, 1536, 4096, 4), (64, 4096, 11008, 2))]
+    assert ws == 65536 + sum(o - 65536 for o in one) == 65536 + 24 * 4 * 16384 + 64 * 2 * 16384
+    assert lib.rldx_grouped_gemm_mixed_workspace_bytes(g, i64([1536, 4096]), i64([4096, 11008]), i32([1, 1]), 2, 1,
+                                                       0) == 0
+    bad = [(i64([1536, 4000]), i64([4096, 11008]), i32([1, 1]), 1),      # n % 64
+           (i64([1536, 4096]), i64([4096, 11000]), i32([1, 1]), 1),      # k % 128
+           (i64([1536, 4096]), i64([4096, 11008]), i32([1, 0]), 1),      # split < 1
+           (i64([1536, 4096]), i64([4096, 11008]), i32([1, 65]), 1),     # split > 64
+           (None, i64([4096, 11008]), i32([1, 1]), 1),
+           (i64([1536, 4096]), None, i32([1, 1]), 1),
+           (i64([1536, 4096]), i64([4096, 11008]), i32([1, 1]), QKV_INTERNAL)]
+    for ns, ks, sp, epi in bad:
+        assert lib.rldx_grouped_gemm_mixed_workspace_bytes(g, ns, ks, sp, 2, epi, 0) == -1
+        assert lib.rldx_grouped_gemm_mixed_bf16(g, ns, ks, sp, None, 2, epi, 0, None, 0, None) == HIP_INVALID_VALUE
+    assert lib.rldx_grouped_gemm_mixed_bf16(g, i64([1536, 4096]), i64([4096, 11008]), i32([1, 1]), None, 2, 1, 4,
+                                            None, 0, None) == HIP_INVALID_VALUE                   # unknown flag
+    assert lib.rldx_grouped_gemm_mixed_bf16(g, i64([1536, 4096]), i64([4096, 11008]), i32([4, 2]), None, 2, 1, 0,
+                                            4096, ws - 256, None) == HIP_INVALID_VALUE            # workspace short
+
+
 def _msat_norms(ms, rope_ld=0):
     d = (_lib.MsatStream * len(ms))()
     for i, m in enumerate(ms):

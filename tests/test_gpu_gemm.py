@@ -414,6 +414,63 @@ def test_grouped_gemm_wide_tiles_bit_identical(dev, epilogue, ms, n, k, split):
         assert torch.equal(x.view(torch.int16), y.view(torch.int16))
 
 
+@pytest.mark.parametrize("epilogue,shapes,splits,wide", [
+    ("bias", ((18, 4608, 1536), (64, 4608, 4096)), (1, 2), False),
+    ("residual", ((18, 1536, 4096), (18, 1536, 4096), (64, 4096, 2816)), (4, 2, 2), False),
+    ("residual_packed", ((18, 1536, 4096), (64, 4096, 2816)), (2, 1), False),
+    ("swiglu_packed", ((18, 8192, 1536), (64, 5504, 512)), (1, 1), True),
+    ("swiglu_packed", ((40, 512, 256), (300, 256, 384), (5, 1024, 640)), (1, 2, 1), False),
+    ("bias_packed", ((100, 1024, 384), (30, 256, 512)), (2, 1), True)])
+def test_grouped_gemm_mixed_shapes_bit_identical(dev, epilogue, shapes, splits, wide):
+    """One launch of groups with different n, k and split
+    (rldx_grouped_gemm_mixed_bf16) gives every group the bits of a launch of that
+    group alone with its split; the residual epilogues' row statistics too."""
+    swiglu = epilogue.startswith("swiglu")
+    packed = epilogue.endswith("packed")
+    res_epi = epilogue.startswith("residual")
+    gg = torch.Generator().manual_seed(sum(n + k for _, n, k in shapes))
+    data = []
+    for m, n, k in shapes:
+        n_out = n // 2 if swiglu else n
+        data.append((m, n_out, _rand((m, k), gg).to(dev), _rand((n, k), gg, std=k ** -0.5).to(dev),
+                     _rand((n,), gg, std=0.5).to(dev), _rand((m, n_out), gg).to(dev) if res_epi else None))
+
+    def items():
+        out = []
+        for m, n_out, a, w, b, r in data:
+            if packed:
+                o = Fn.pack_act(r) if r is not None else Fn.PackedAct.empty(m, n_out, dev)
+                out.append((Fn.pack_act(a), Fn.pack_weight(w, swiglu_pairs=swiglu), b, o, o if res_epi else None))
+            else:
+                o = r.clone() if r is not None else torch.empty(m, n_out, dtype=BF16, device=dev)
+                out.append((Fn.pack_act(a), Fn.pack_weight(w, swiglu_pairs=swiglu), b, o, o if res_epi else None))
+        return out
+
+    def stats():
+        return [Fn.ln_stats_empty(m, n_out, dev) for m, n_out, *_ in data] if res_epi else None
+
+    mixed, st_mixed = items(), stats()
+    ws = Fn.GemmWorkspace(max(1, Fn.grouped_gemm_workspace_bytes(mixed, epilogue, list(splits), wide)), dev)
+    Fn.grouped_gemm(mixed, epilogue, split_k=list(splits), workspace=ws, wide_tiles=wide, stats_out=st_mixed)
+    alone, st_alone = items(), stats()
+    for i, (it, sp) in enumerate(zip(alone, splits)):
+        wsi = Fn.GemmWorkspace(Fn.grouped_gemm_workspace_bytes([it], epilogue, sp, wide), dev) if sp > 1 else None
+        Fn.grouped_gemm([it], epilogue, split_k=sp, workspace=wsi, wide_tiles=wide,
+                        stats_out=[st_alone[i]] if res_epi else None)
+        torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    for i, (x, y) in enumerate(zip(mixed, alone)):
+        xo, yo = (x[3].unpack(), y[3].unpack()) if packed else (x[3], y[3])
+        assert torch.equal(xo.view(torch.int16), yo.view(torch.int16)), f"group {i} {shapes[i]}"
+        if res_epi:
+            assert torch.equal(st_mixed[i], st_alone[i]), f"group {i} statistics"
+    # and against the CPU product (the layout of each group's output is its own n)
+    m, n_out, a, w, b, r = data[0]
+    y = _linear_ref(a.cpu(), w.cpu(), b.cpu())
+    if not swiglu and not res_epi:
+        assert_bf16_close((mixed[0][3].unpack() if packed else mixed[0][3]).cpu(), y)
+
+
 def test_ss_fused_mlp_swiglu_op(dev):
     import rldx_amd.ops  # noqa: F401  registers ss::fused_mlp_swiglu
 
