@@ -375,6 +375,24 @@ hipError_t rldx_act_pack_bf16(const void* x, int64_t ldx, int64_t m, int64_t k, 
 hipError_t rldx_layernorm_pack_bf16(const void* x, int64_t ldx, int64_t m, int64_t k, float eps, void* packed,
                                     hipStream_t stream);
 
+/* One row-major bf16 matrix x [m, k] (row stride ldx elements) and its packed
+ * activation buffer (rldx_act_packed_elems(m, k) elements). */
+typedef struct {
+  const void* x;
+  int64_t ldx, m, k;
+  void* packed;
+} rldx_rows_t;
+
+/*
+ * rldx_layernorm_pack_bf16 over up to 4 matrices in one launch (each its own m,
+ * k <= 8192 and eps shared): the pre-norms of the streams of one block, which
+ * the reference applies one after the other.  Each output is bit-identical to
+ * rldx_layernorm_pack_bf16 on that matrix alone.
+ * Replaces: sa_norm1 / vl_norm1 / p_norm1 and the *_norm2_mlp pre-norms of the
+ *   double-stream blocks (rldx/model/modules/action_model/blocks.py:508-520, 599-604, 804-818, 882-888).
+ */
+hipError_t rldx_layernorm_pack_many_bf16(const rldx_rows_t* rows, int32_t count, float eps, hipStream_t stream);
+
 /* One stream of a grouped GEMM. */
 typedef struct rldx_gemm_group {
   const void* a_packed;  /* [m, k] bf16 activations in the packed activation order */

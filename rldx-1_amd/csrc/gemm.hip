@@ -1060,14 +1060,33 @@ hipError_t launch(const GemmArgs& args, int epilogue, hipStream_t stream, bool w
 // ---------------------------------------------------------------------------
 // stats (optional, not with normalize): the row's Σx, Σx² for a LayerNorm-
 // folding GEMM, in slot 0 of [k / 64][m][2], zeros in the other slots.
+// Up to kRowsMax matrices per launch (the streams of a block): workgroups
+// [begin[i], begin[i + 1]) take matrix i, 4 rows each.
+constexpr int kRowsMax = 4;
+struct RowsArgs {
+  const uint16_t* x[kRowsMax];
+  uint16_t* out[kRowsMax];
+  float* stats[kRowsMax];
+  int64_t ldx[kRowsMax];
+  int m[kRowsMax], k[kRowsMax];
+  int begin[kRowsMax + 1];
+  int count, normalize;
+  float eps;
+};
+
 template <int CPL>
-__global__ __launch_bounds__(256) void rows_pack_kernel(const uint16_t* __restrict__ x, int64_t ldx, int m, int k,
-                                                        float eps, int normalize, uint16_t* __restrict__ out,
-                                                        float* __restrict__ stats) {
+__global__ __launch_bounds__(256) void rows_pack_kernel(RowsArgs a) {
+  int mi = 0;
+#pragma unroll
+  for (int i = 1; i < kRowsMax; ++i)
+    if (i < a.count && static_cast<int>(blockIdx.x) >= a.begin[i]) mi = i;
+  const int m = a.m[mi], k = a.k[mi];
+  float* __restrict__ stats = a.stats[mi];
+  uint16_t* __restrict__ out = a.out[mi];
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = (static_cast<int>(blockIdx.x) - a.begin[mi]) * 4 + (threadIdx.x >> 6);
   if (row >= m) return;
-  const uint16_t* xr = x + static_cast<int64_t>(row) * ldx;
+  const uint16_t* xr = a.x[mi] + static_cast<int64_t>(row) * a.ldx[mi];
   u32x4 raw[CPL];
   float v[CPL][8];
   float sum = 0.f;
@@ -1081,7 +1100,7 @@ __global__ __launch_bounds__(256) void rows_pack_kernel(const uint16_t* __restri
       sum += v[c][i];
     }
   }
-  if (normalize) {
+  if (a.normalize) {
 #pragma clang fp contract(off)
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
@@ -1097,7 +1116,7 @@ __global__ __launch_bounds__(256) void rows_pack_kernel(const uint16_t* __restri
         }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
-    const float rstd = 1.0f / __builtin_sqrtf(sq / static_cast<float>(k) + eps);
+    const float rstd = 1.0f / __builtin_sqrtf(sq / static_cast<float>(k) + a.eps);
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
 #pragma unroll
@@ -1131,30 +1150,62 @@ __global__ __launch_bounds__(256) void rows_pack_kernel(const uint16_t* __restri
   }
 }
 
+// Checks and launches up to kRowsMax matrices in one launch; the register
+// width (CPL chunks of 8 columns per lane) is the widest matrix's.
+hipError_t rows_pack_many(const rldx_rows_t* rows, int count, float eps, bool normalize, hipStream_t stream,
+                          float* const* stats = nullptr) {
+  if (!rows || count < 1 || count > kRowsMax) return hipErrorInvalidValue;
+  RowsArgs a{};
+  int n = 0, blocks = 0;
+  int64_t kmax = 0;
+  for (int i = 0; i < count; ++i) {
+    const rldx_rows_t& r = rows[i];
+    float* st = stats ? stats[i] : nullptr;
+    if (r.m < 0 || r.k < 0) return hipErrorInvalidValue;
+    if (r.m == 0 || r.k == 0) continue;
+    if (!r.x || !r.packed || !a16(r.x) || !a16(r.packed) || r.ldx < r.k || r.ldx % 8 || r.k % 16 || r.k > 8192)
+      return hipErrorInvalidValue;
+    if (stats && (!st || normalize || r.k % 64 || reinterpret_cast<uintptr_t>(st) % 8)) return hipErrorInvalidValue;
+    if (r.m > (int64_t{1} << 28)) return hipErrorInvalidValue;
+    a.x[n] = static_cast<const uint16_t*>(r.x);
+    a.out[n] = static_cast<uint16_t*>(r.packed);
+    a.stats[n] = st;
+    a.ldx[n] = r.ldx;
+    a.m[n] = static_cast<int>(r.m);
+    a.k[n] = static_cast<int>(r.k);
+    a.begin[n] = blocks;
+    blocks += static_cast<int>((r.m + 3) / 4);
+    kmax = r.k > kmax ? r.k : kmax;
+    ++n;
+  }
+  if (n == 0) return hipSuccess;
+  a.begin[n] = blocks;
+  a.count = n;
+  a.normalize = normalize ? 1 : 0;
+  a.eps = eps;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(256);
+  if (kmax <= 512)
+    hipLaunchKernelGGL(rows_pack_kernel<1>, grid, block, 0, stream, a);
+  else if (kmax <= 1024)
+    hipLaunchKernelGGL(rows_pack_kernel<2>, grid, block, 0, stream, a);
+  else if (kmax <= 2048)
+    hipLaunchKernelGGL(rows_pack_kernel<4>, grid, block, 0, stream, a);
+  else if (kmax <= 4096)
+    hipLaunchKernelGGL(rows_pack_kernel<8>, grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL(rows_pack_kernel<16>, grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
 hipError_t rows_pack(const void* x, int64_t ldx, int64_t m, int64_t k, float eps, bool normalize, void* packed,
                      hipStream_t stream, float* stats = nullptr) {
   if (m < 0 || k < 0) return hipErrorInvalidValue;
   if (m == 0 || k == 0) return hipSuccess;
-  if (!x || !packed || !a16(x) || !a16(packed) || ldx < k || ldx % 8 || k % 16) return hipErrorInvalidValue;
   if (stats && (normalize || k % 64 || reinterpret_cast<uintptr_t>(stats) % 8)) return hipErrorInvalidValue;
-  if (m > (int64_t{1} << 30)) return hipErrorInvalidValue;
-  const dim3 grid(static_cast<unsigned>((m + 3) / 4)), block(256);
-  const auto* xp = static_cast<const uint16_t*>(x);
-  auto* op = static_cast<uint16_t*>(packed);
-  const int mi = static_cast<int>(m), ki = static_cast<int>(k), nz = normalize ? 1 : 0;
-  if (k <= 512)
-    hipLaunchKernelGGL(rows_pack_kernel<1>, grid, block, 0, stream, xp, ldx, mi, ki, eps, nz, op, stats);
-  else if (k <= 1024)
-    hipLaunchKernelGGL(rows_pack_kernel<2>, grid, block, 0, stream, xp, ldx, mi, ki, eps, nz, op, stats);
-  else if (k <= 2048)
-    hipLaunchKernelGGL(rows_pack_kernel<4>, grid, block, 0, stream, xp, ldx, mi, ki, eps, nz, op, stats);
-  else if (k <= 4096)
-    hipLaunchKernelGGL(rows_pack_kernel<8>, grid, block, 0, stream, xp, ldx, mi, ki, eps, nz, op, stats);
-  else if (k <= 8192)
-    hipLaunchKernelGGL(rows_pack_kernel<16>, grid, block, 0, stream, xp, ldx, mi, ki, eps, nz, op, stats);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  if (m > (int64_t{1} << 28)) return hipErrorInvalidValue;
+  const rldx_rows_t r{x, ldx, m, k, packed};
+  float* const st[1] = {stats};
+  return rows_pack_many(&r, 1, eps, normalize, stream, stats ? st : nullptr);
 }
 
 }  // namespace
@@ -1261,6 +1312,11 @@ extern "C" hipError_t rldx_act_pack_bf16(const void* x, int64_t ldx, int64_t m, 
 extern "C" hipError_t rldx_layernorm_pack_bf16(const void* x, int64_t ldx, int64_t m, int64_t k, float eps,
                                                void* packed, hipStream_t stream) {
   return rows_pack(x, ldx, m, k, eps, true, packed, stream);
+}
+
+extern "C" hipError_t rldx_layernorm_pack_many_bf16(const rldx_rows_t* rows, int32_t count, float eps,
+                                                    hipStream_t stream) {
+  return rows_pack_many(rows, count, eps, true, stream);
 }
 
 extern "C" hipError_t rldx_act_pack_stats_bf16(const void* x, int64_t ldx, int64_t m, int64_t k, void* packed,

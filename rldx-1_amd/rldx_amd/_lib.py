@@ -19,6 +19,13 @@ c_vp = ctypes.c_void_p
 c_i64p = ctypes.POINTER(ctypes.c_int64)
 
 
+class Rows(ctypes.Structure):
+    """rldx_rows_t"""
+
+    _fields_ = [("x", ctypes.c_void_p), ("ldx", ctypes.c_int64), ("m", ctypes.c_int64), ("k", ctypes.c_int64),
+                ("packed", ctypes.c_void_p)]
+
+
 class GemmGroup(ctypes.Structure):
     """rldx_gemm_group_t"""
 
@@ -114,6 +121,7 @@ SIGNATURES = {
     "rldx_grouped_gemm_stats_bf16": (c_i32, [ctypes.POINTER(GemmGroup), ctypes.POINTER(c_vp), c_i32, c_i64, c_i64,
                                              c_i32, c_i32, c_i32, c_vp, c_i64, c_vp]),
     "rldx_act_pack_stats_bf16": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp]),
+    "rldx_layernorm_pack_many_bf16": (c_i32, [ctypes.POINTER(Rows), c_i32, c_f32, c_vp]),
     "rldx_grouped_gemm_mixed_bf16": (c_i32, [ctypes.POINTER(GemmGroup), c_i64p, c_i64p, ctypes.POINTER(c_i32),
                                              ctypes.POINTER(c_vp), c_i32, c_i32, c_i32, c_vp, c_i64, c_vp]),
     "rldx_grouped_gemm_mixed_workspace_bytes": (c_i64, [ctypes.POINTER(GemmGroup), c_i64p, c_i64p,

@@ -660,17 +660,39 @@ def pack_act(x: torch.Tensor, out: Optional[PackedAct] = None, stats: Optional[t
     return out
 
 
+def _check_pack_target(out: PackedAct, m: int, k: int) -> None:
+    _require(isinstance(out, PackedAct) and out.m == m and out.k == k, "out shape mismatch")
+    _require(out.ld == out.k, "out must be a whole packed matrix, not a column view")
+    _require(out.data.dtype == BF16 and out.data.numel() >= (m + 31) // 32 * 32 * k, "out buffer too small")
+    _on_gpu(out.data)
+
+
 def layernorm_pack(x: torch.Tensor, eps: float = 1e-6, out: Optional[PackedAct] = None) -> PackedAct:
     """LayerNorm without affine parameters over the last dim of x [m, k], packed."""
     _on_gpu(x)
     _require(x.dtype == BF16 and x.dim() == 2 and x.stride(1) == 1, "x must be 2-D bf16, rows contiguous")
     m, k = x.shape
     out = PackedAct.empty(m, k, x.device) if out is None else out
-    _require(out.m == m and out.k == k, "out shape mismatch")
+    _check_pack_target(out, m, k)
     lib = _lib.load()
     _lib.check(lib.rldx_layernorm_pack_bf16(x.data_ptr(), x.stride(0), m, k, float(eps), out.data.data_ptr(),
                                             _stream_ptr(x)), "rldx_layernorm_pack_bf16")
     return out
+
+
+def layernorm_pack_many(pairs: Sequence[tuple], eps: float = 1e-6) -> None:
+    """layernorm_pack of up to 4 (x [m, k], out PackedAct) pairs in one launch
+    (rldx_layernorm_pack_many_bf16): the pre-norms of a block's streams."""
+    _require(1 <= len(pairs) <= 4, "between 1 and 4 matrices")
+    rows = (_lib.Rows * len(pairs))()
+    for i, (x, out) in enumerate(pairs):
+        _on_gpu(x)
+        _require(x.dtype == BF16 and x.dim() == 2 and x.stride(1) == 1, "x must be 2-D bf16, rows contiguous")
+        _check_pack_target(out, x.shape[0], x.shape[1])
+        _require(x.device == pairs[0][0].device and out.data.device == x.device, "all matrices on one device")
+        rows[i] = _lib.Rows(x.data_ptr(), x.stride(0), x.shape[0], x.shape[1], out.data.data_ptr())
+    _lib.check(_lib.load().rldx_layernorm_pack_many_bf16(rows, len(pairs), float(eps), _stream_ptr(pairs[0][0])),
+               "rldx_layernorm_pack_many_bf16")
 
 
 class GemmWorkspace:

@@ -17,16 +17,16 @@ has its complex frequency buffers cast to bf16, which keeps cos and drops sin;
 `bf16_quirk=True` (the default, as the reference chain assumes) reproduces that
 (cos rounded to bf16, sin = 0), False uses the exact fp32 tables.
 
-Per DoubleStreamBlock (14 launches; the SA and VL streams have different
-widths, so each GEMM runs once per stream):
-    LayerNorm -> packed h_s            rldx_layernorm_pack_bf16           x2
-    QKV linears (+ bias)               rldx_grouped_gemm_bf16             x2
+Per DoubleStreamBlock (8 launches; the SA and VL streams have different
+widths, so each linear is one launch of groups with their own n and k):
+    LayerNorm -> packed h_s, both      rldx_layernorm_pack_many_bf16
+    QKV linears (+ bias)               rldx_grouped_gemm_mixed_bf16
     QK-RMSNorm + RoPE (SA rows) + K/V  rldx_msat_qkv_norm_rope_bf16
     joint attention -> packed o        rldx_attention_packed_fwd_bf16
-    proj + residual (in place)         rldx_grouped_gemm_bf16 (residual)  x2
-    LayerNorm -> packed h_s                                               x2
-    w12 + SwiGLU -> packed             rldx_grouped_gemm_bf16 (swiglu)    x2
-    w3 + residual (in place)           rldx_grouped_gemm_bf16 (residual)  x2
+    proj + residual (in place)         rldx_grouped_gemm_mixed_bf16 (residual)
+    LayerNorm -> packed h_s, both      rldx_layernorm_pack_many_bf16
+    w12 + SwiGLU -> packed             rldx_grouped_gemm_mixed_bf16 (swiglu)
+    w3 + residual (in place)           rldx_grouped_gemm_mixed_bf16 (residual)
 Per SingleStreamBlock (7 launches):
     LayerNorm -> packed h; linear1's QKV columns (+ bias); linear1's MLP columns
     + SwiGLU -> packed; QK-RMSNorm + RoPE; attention -> columns [0, inner) of
@@ -421,6 +421,9 @@ class RldxMsat:
         self._ninf = torch.full((), float("-inf"), dtype=torch.float32, device=self.dev)
         self._zero = torch.zeros((), dtype=torch.float32, device=self.dev)
         self.graph = None
+        # the pre-norms of a block's streams, one launch each time
+        self.ds_norms = [(self.x_sa, self.h_sa), (self.x_vl, self.h_vl)] + ([(self.x_p, self.h_p)] if self.phys else [])
+        self.ss_norms = [(self.x, self.h)] + ([(self.x_p, self.h_p)] if self.phys else [])
         # every GEMM of the forward on its static buffers, with its split-K factor
         self.ds_gemms = [self._ds_gemm_items(blk) for blk in self.ds]
         self.ss_gemms = [self._ss_gemm_items(blk) for blk in self.ss]
@@ -556,10 +559,7 @@ class RldxMsat:
     def _ds_block(self, blk: dict, gm: dict) -> None:
         cfg = self.cfg
         N = self.N
-        Fn.layernorm_pack(self.x_sa, cfg.eps, out=self.h_sa)
-        Fn.layernorm_pack(self.x_vl, cfg.eps, out=self.h_vl)
-        if self.phys:
-            Fn.layernorm_pack(self.x_p, cfg.eps, out=self.h_p)
+        Fn.layernorm_pack_many(self.ds_norms, cfg.eps)
         self._gemm(gm["qkv"])
         specs = [Fn.StreamSpec(self.qkv_vl, blk["q_norm_vl.weight"], blk["k_norm_vl.weight"]),
                  Fn.StreamSpec(self.qkv_sa_buf, blk["q_norm_sa.weight"], blk["k_norm_sa.weight"], self.ds_cos,
@@ -570,19 +570,14 @@ class RldxMsat:
         Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
         Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), N, key_bias=self._kb(), out=self.att)
         self._gemm(gm["proj"])
-        Fn.layernorm_pack(self.x_sa, cfg.eps, out=self.h_sa)
-        Fn.layernorm_pack(self.x_vl, cfg.eps, out=self.h_vl)
-        if self.phys:
-            Fn.layernorm_pack(self.x_p, cfg.eps, out=self.h_p)
+        Fn.layernorm_pack_many(self.ds_norms, cfg.eps)
         self._gemm(gm["w12"])
         self._gemm(gm["w3"])
 
     def _ss_block(self, blk: dict, gm: dict) -> None:
         cfg = self.cfg
         nv, N, inner = self.nv, self.N, cfg.inner
-        Fn.layernorm_pack(self.x, cfg.eps, out=self.h)
-        if self.phys:
-            Fn.layernorm_pack(self.x_p, cfg.eps, out=self.h_p)
+        Fn.layernorm_pack_many(self.ss_norms, cfg.eps)
         self._gemm(gm["qkv"])
         self._gemm(gm["mlp"])
         specs = [Fn.StreamSpec(self.qkv_buf[:nv], blk["q_norm"], blk["k_norm"]),

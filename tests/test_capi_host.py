@@ -264,6 +264,35 @@ def test_grouped_gemm_mixed_plan_and_rejections():
                                             4096, ws - 256, None) == HIP_INVALID_VALUE            # workspace short
 
 
+def test_layernorm_pack_many_rejections():
+    """rldx_layernorm_pack_many_bf16 checks every matrix before launching: 1-4
+    matrices, k % 16 == 0 and <= 8192, row stride >= k and a multiple of 8,
+    16-byte aligned pointers; empty matrices are skipped (nothing to launch)."""
+    lib = _lib.load()
+
+    def rows(*specs):
+        arr = (_lib.Rows * len(specs))()
+        for i, (x, ldx, m, k, p) in enumerate(specs):
+            arr[i] = _lib.Rows(x, ldx, m, k, p)
+        return arr
+
+    ok = (4096, 1536, 18, 1536, 8192)
+    assert lib.rldx_layernorm_pack_many_bf16(rows(ok), 0, 1e-6, None) == HIP_INVALID_VALUE
+    assert lib.rldx_layernorm_pack_many_bf16(rows(ok, ok, ok, ok, ok), 5, 1e-6, None) == HIP_INVALID_VALUE
+    for bad in [(4096, 1536, 18, 1544, 8192),       # k % 16
+                (4096, 8208, 18, 8208, 8192),       # k > 8192
+                (4096, 1532, 18, 1536, 8192),       # ldx < k
+                (4096, 1540, 18, 1536, 8192),       # ldx % 8
+                (4104, 1536, 18, 1536, 8192),       # x misaligned
+                (4096, 1536, 18, 1536, 8200),       # packed misaligned
+                (None, 1536, 18, 1536, 8192),
+                (4096, 1536, -1, 1536, 8192)]:
+        assert lib.rldx_layernorm_pack_many_bf16(rows(ok, bad), 2, 1e-6, None) == HIP_INVALID_VALUE, bad
+    # nothing to do: no launch, success
+    assert lib.rldx_layernorm_pack_many_bf16(rows((None, 0, 0, 1536, None), (None, 0, 5, 0, None)), 2, 1e-6,
+                                             None) == 0
+
+
 def _msat_norms(ms, rope_ld=0):
     d = (_lib.MsatStream * len(ms))()
     for i, m in enumerate(ms):

@@ -276,6 +276,25 @@ def test_layernorm_pack(dev, m, k):
     assert_bf16_close(p.unpack(), r, "layernorm")
 
 
+@pytest.mark.parametrize("shapes", [((18, 1536), (64, 4096)), ((18, 1536), (96, 4096), (17, 1536)),
+                                    ((82, 1536), (17, 1536)), ((300, 8192), (5, 16), (33, 512), (1, 1024))])
+def test_layernorm_pack_many_matches_one_at_a_time(dev, shapes):
+    """rldx_layernorm_pack_many_bf16 (one launch for a block's streams) gives
+    each matrix the bits of rldx_layernorm_pack_bf16 on it alone, including
+    matrices narrower than the launch's widest one and strided rows."""
+    g = torch.Generator().manual_seed(sum(m * k for m, k in shapes) % 1000)
+    xs = []
+    for m, k in shapes:
+        full = (2 * torch.randn(m, k + 64, generator=g) + 0.25).to(BF16).to(dev)
+        xs.append(full[:, :k])  # row stride k + 64
+    many = [Fn.PackedAct.empty(m, k, dev) for m, k in shapes]
+    Fn.layernorm_pack_many(list(zip(xs, many)), 1e-6)
+    one = [Fn.layernorm_pack(x, 1e-6) for x in xs]
+    torch.cuda.synchronize()
+    for (m, k), a, b in zip(shapes, many, one):
+        assert torch.equal(a.unpack().view(torch.int16), b.unpack().view(torch.int16)), f"{m} x {k}"
+
+
 def test_swiglu_packed_epilogue_matches_row_major(dev):
     g = torch.Generator().manual_seed(13)
     n, k = 8192, 1536
