@@ -227,6 +227,27 @@ hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* kv_packed, 
                                           hipStream_t stream);
 
 /*
+ * rldx_attention_packed_fwd_bf16 plus a memory-side-cache warm-up: warm_count
+ * (0..3) byte ranges warm_ptrs[i] (4-byte aligned), warm_bytes[i] long, whose
+ * whole 128-byte lines further workgroups of the same launch read (one dword
+ * each, results discarded) while the attention workgroups run.  For a chain of
+ * launches that graph replay runs one after another: the joint attention of a
+ * block is latency-bound and leaves HBM mostly idle, and the weight panels of a
+ * later linear of the block read during it are then served from the
+ * memory-side cache when that linear runs (the MSAT step warms its W3 panels
+ * here).  The attention result is bit-identical to rldx_attention_packed_fwd_bf16.
+ * Replaces: the joint attention of the double-stream blocks, as above
+ *   (rldx/model/modules/action_model/blocks.py:866; the warm-up has no counterpart there).
+ */
+hipError_t rldx_attention_packed_fwd_warm_bf16(const void* q, const void* kv_packed, const int64_t* packed_strides,
+                                               void* o, int32_t out_packed, int64_t batch, int64_t q_heads,
+                                               int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t head_dim,
+                                               const int64_t* q_strides, const int64_t* o_strides,
+                                               const float* key_bias, int64_t key_bias_batch_stride, float scale,
+                                               int32_t causal, const void* const* warm_ptrs,
+                                               const int64_t* warm_bytes, int32_t warm_count, hipStream_t stream);
+
+/*
  * The complete rldx_backbone::fused_attention operator: packed QKV
  * (seq, >= (Hq + 2*Hkv)*D) bf16 -> out (seq, Hq*D) bf16 with q_norm/k_norm
  * (Qwen3VLTextRMSNorm, eps) + rotate-half RoPE (cos / sin tables [seq, D] bf16,

@@ -48,6 +48,7 @@
 //                                lane l, element i
 //                                = V[32t + 16 s2 + 8 (i >> 2) + 4 (l >> 5) + (i & 3)][32 db + (l & 31)]
 //   keys >= Sk hold zeros.
+#include <algorithm>
 #include <mutex>
 
 #include "rldx_amd.h"
@@ -127,7 +128,35 @@ struct AttnArgs {
   int num_seqs;
   int total_rows;
   int d_store;  // output columns written per head (<= D)
+  // Memory-side-cache warm-up: the first n_work workgroups compute attention;
+  // the ones after them read one dword of every 128-byte line of up to three
+  // ranges (pf_end: cumulative line counts), pf_lpw lines each.
+  int n_work;
+  const uint32_t* pf[3];
+  int64_t pf_end[3];
+  int64_t pf_lpw;
 };
+
+// One warm-up workgroup: plain loads (they allocate in the memory-side cache on
+// the way; non-temporal loads measured no warm-up), 8 per thread in flight,
+// results folded into a register that an empty asm statement consumes.
+__device__ __forceinline__ void warm_lines(const AttnArgs& a, int w) {
+  const int64_t l0 = w * a.pf_lpw, l1 = min(l0 + a.pf_lpw, a.pf_end[2]);
+  uint32_t acc = 0;
+  for (int64_t base = l0 + static_cast<int>(threadIdx.x); base < l1; base += 8 * 256) {
+    uint32_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t l = base + j * 256;
+      const int r = l < a.pf_end[0] ? 0 : l < a.pf_end[1] ? 1 : 2;
+      const int64_t rb = r == 0 ? 0 : a.pf_end[r - 1];
+      v[j] = l < l1 ? a.pf[r][(l - rb) * 32] : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc ^= v[j];
+  }
+  asm volatile("" ::"v"(acc));
+}
 
 // Sequence s of a variable-length batch (rows [c_s, c_{s+1}) with
 // c_s = clamp(cu_seqlens[s], 0, rows)) owns the 32-row slots
@@ -264,6 +293,10 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
   constexpr int VPART = 64 * D;
   constexpr int G4 = DBLK * 4 + 1;  // float4 groups per lane and sub-block in the merge: O + (m, l)
   __shared__ floatx4 merge[NW * NSUB * G4 * 64];
+  if (static_cast<int>(blockIdx.x) >= a.n_work) {  // warm-up workgroups (no barrier, no LDS)
+    warm_lines(a, static_cast<int>(blockIdx.x) - a.n_work);
+    return;
+  }
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -277,7 +310,7 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
   // fetched into a single L2 and reused there by all of its query blocks.
   int qb, h, b;
   {
-    const int total = static_cast<int>(gridDim.x);
+    const int total = a.n_work;
     const int i = static_cast<int>(blockIdx.x);
     const int per = total / kXcds, rem = total % kXcds;
     const int xcd = i % kXcds, k = i / kXcds;
@@ -1001,14 +1034,22 @@ hipError_t launch_vit(const VitArgs& v, AttnArgs a, int64_t slots, hipStream_t s
   hipLaunchKernelGGL(vit_pack_kernel<DP>, dim3(static_cast<unsigned>(slots), static_cast<unsigned>(v.heads)),
                      dim3(256), 0, stream, v);
   a.num_q_blocks = static_cast<int>(slots);
+  a.n_work = static_cast<int>(slots * v.heads);
   hipLaunchKernelGGL((attn_fwd_kernel<DP, 1, false, false, false, true>),
                      dim3(static_cast<unsigned>(slots * v.heads)), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
 template <int D, int NSUB, bool kQNorm>
-void launch_attn_d(const AttnArgs& a, int batch, bool causal, bool has_bias, hipStream_t stream) {
-  dim3 grid(static_cast<unsigned>(a.num_q_blocks) * a.hq * batch);
+void launch_attn_d(AttnArgs a, int batch, bool causal, bool has_bias, hipStream_t stream) {
+  a.n_work = a.num_q_blocks * a.hq * batch;
+  // warm-up workgroups: about 1024 lines (128 KB) each, at most 256
+  int n_pf = 0;
+  if (a.pf_end[2] > 0) {
+    n_pf = static_cast<int>(std::min<int64_t>(256, (a.pf_end[2] + 1023) / 1024));
+    a.pf_lpw = (a.pf_end[2] + n_pf - 1) / n_pf;
+  }
+  dim3 grid(static_cast<unsigned>(a.n_work + n_pf));
   dim3 block(256);
   if (causal) {
     if (has_bias)
@@ -1126,13 +1167,15 @@ extern "C" hipError_t rldx_attention_kv_pack_bf16(const void* k, const int64_t* 
   return hipGetLastError();
 }
 
-extern "C" hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* kv_packed,
-                                                     const int64_t* packed_strides, void* o, int32_t out_packed,
-                                                     int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
-                                                     int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
-                                                     const int64_t* o_strides, const float* key_bias,
-                                                     int64_t key_bias_batch_stride, float scale, int32_t causal,
-                                                     hipStream_t stream) {
+namespace {
+// The packed-K/V attention; warm: up to three byte ranges whose 128-byte lines
+// extra workgroups of the launch read (see AttnArgs::n_work).
+hipError_t attention_packed(const void* q, const void* kv_packed, const int64_t* packed_strides, void* o,
+                            int32_t out_packed, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                            int64_t seq_k, int64_t head_dim, const int64_t* q_strides, const int64_t* o_strides,
+                            const float* key_bias, int64_t key_bias_batch_stride, float scale, int32_t causal,
+                            const void* const* warm_ptrs, const int64_t* warm_bytes, int32_t warm_count,
+                            hipStream_t stream) {
   const int64_t zero3[3] = {0, 0, 0};
   if (out_packed) {
     // 1: O is the packed [seq_q, q_heads*head_dim] matrix; > 1: O is the
@@ -1157,7 +1200,48 @@ extern "C" hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* 
   a.kv = static_cast<const uint16_t*>(kv_packed);
   a.kv_sb = packed_strides[0];
   a.kv_sh = packed_strides[1];
+  int64_t lines = 0;
+  for (int i = 0; i < warm_count; ++i) {
+    a.pf[i] = static_cast<const uint32_t*>(warm_ptrs[i]);
+    lines += warm_bytes[i] / 128;
+    a.pf_end[i] = lines;
+  }
+  for (int i = warm_count; i < 3; ++i) {
+    a.pf[i] = a.pf[0];
+    a.pf_end[i] = lines;
+  }
   return launch_attn<false>(a, head_dim, static_cast<int>(batch), causal != 0, key_bias != nullptr, stream);
+}
+}  // namespace
+
+extern "C" hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* kv_packed,
+                                                     const int64_t* packed_strides, void* o, int32_t out_packed,
+                                                     int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                                                     int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
+                                                     const int64_t* o_strides, const float* key_bias,
+                                                     int64_t key_bias_batch_stride, float scale, int32_t causal,
+                                                     hipStream_t stream) {
+  return attention_packed(q, kv_packed, packed_strides, o, out_packed, batch, q_heads, kv_heads, seq_q, seq_k,
+                          head_dim, q_strides, o_strides, key_bias, key_bias_batch_stride, scale, causal, nullptr,
+                          nullptr, 0, stream);
+}
+
+extern "C" hipError_t rldx_attention_packed_fwd_warm_bf16(
+    const void* q, const void* kv_packed, const int64_t* packed_strides, void* o, int32_t out_packed, int64_t batch,
+    int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
+    const int64_t* o_strides, const float* key_bias, int64_t key_bias_batch_stride, float scale, int32_t causal,
+    const void* const* warm_ptrs, const int64_t* warm_bytes, int32_t warm_count, hipStream_t stream) {
+  if (warm_count < 0 || warm_count > 3 || (warm_count > 0 && (!warm_ptrs || !warm_bytes))) return hipErrorInvalidValue;
+  int64_t lines = 0;
+  for (int i = 0; i < warm_count; ++i) {
+    if (warm_bytes[i] < 0 || (warm_bytes[i] > 0 && (!warm_ptrs[i] || reinterpret_cast<uintptr_t>(warm_ptrs[i]) % 4)))
+      return hipErrorInvalidValue;
+    lines += warm_bytes[i] / 128;
+  }
+  if (lines > (int64_t{1} << 40)) return hipErrorInvalidValue;
+  return attention_packed(q, kv_packed, packed_strides, o, out_packed, batch, q_heads, kv_heads, seq_q, seq_k,
+                          head_dim, q_strides, o_strides, key_bias, key_bias_batch_stride, scale, causal, warm_ptrs,
+                          warm_bytes, warm_count, stream);
 }
 
 extern "C" hipError_t rldx_attention_fwd_bf16(const void* q, const void* k, const void* v, void* o, int64_t batch,

@@ -424,11 +424,14 @@ def kv_pack(k: torch.Tensor, v: torch.Tensor, layout: str = "bhsd") -> torch.Ten
 
 def attention_packed(q: torch.Tensor, kvp: torch.Tensor, seq_k: int, *, key_bias: Optional[torch.Tensor] = None,
                      causal: bool = False, scale: Optional[float] = None, layout: str = "bhsd",
-                     out=None):
+                     out=None, warm: Optional[Sequence[torch.Tensor]] = None):
     """Attention with K/V given as packed tiles [B, Hkv, >= kv_packed_elems(seq_k, D)]
     (see kv_pack; the MSAT QKV kernel writes them directly).  `out` may be a
     PackedAct [Sq, Hq*D] (batch 1), or a column view of a wider one: O is then
-    written in the grouped GEMM's packed activation order."""
+    written in the grouped GEMM's packed activation order.  warm: up to three
+    tensors (e.g. the packed weights of a later GEMM) whose memory extra
+    workgroups of the launch read into the memory-side cache while it runs
+    (rldx_attention_packed_fwd_warm_bf16; the attention result is unchanged)."""
     _on_gpu(q, kvp, key_bias)
     _require(q.dtype == BF16 and q.dim() == 4 and q.stride(-1) == 1, "q must be 4-D bf16, last dim contiguous")
     if layout == "bhsd":
@@ -458,13 +461,20 @@ def attention_packed(q: torch.Tensor, kvp: torch.Tensor, seq_k: int, *, key_bias
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     lib = _lib.load()
-    _lib.check(lib.rldx_attention_packed_fwd_bf16(q.data_ptr(), kvp.data_ptr(),
-                                                  _lib.i64_array([kvp.stride(0), kvp.stride(1)]), o_ptr,
-                                                  (out.ld if out.ld != out.k else 1) if packed_out else 0,
-                                                  B, Hq, Hkv, Sq, seq_k, D,
-                                                  _lib.i64_array(_bhs_strides(q, layout)), _lib.i64_array(o_strides),
-                                                  kb_ptr, kb_stride, float(scale), int(bool(causal)), _stream_ptr(q)),
-               "rldx_attention_packed_fwd_bf16")
+    args = (q.data_ptr(), kvp.data_ptr(), _lib.i64_array([kvp.stride(0), kvp.stride(1)]), o_ptr,
+            (out.ld if out.ld != out.k else 1) if packed_out else 0, B, Hq, Hkv, Sq, seq_k, D,
+            _lib.i64_array(_bhs_strides(q, layout)), _lib.i64_array(o_strides), kb_ptr, kb_stride, float(scale),
+            int(bool(causal)))
+    if warm:
+        _require(len(warm) <= 3, "at most three warm-up ranges")
+        _on_gpu(*warm)
+        _require(all(t.is_contiguous() and t.device == q.device for t in warm), "warm-up tensors: contiguous, q's device")
+        ptrs = (ctypes.c_void_p * len(warm))(*[t.data_ptr() for t in warm])
+        nbytes = _lib.i64_array([t.numel() * t.element_size() for t in warm])
+        _lib.check(lib.rldx_attention_packed_fwd_warm_bf16(*args, ptrs, nbytes, len(warm), _stream_ptr(q)),
+                   "rldx_attention_packed_fwd_warm_bf16")
+    else:
+        _lib.check(lib.rldx_attention_packed_fwd_bf16(*args, _stream_ptr(q)), "rldx_attention_packed_fwd_bf16")
     return out
 
 

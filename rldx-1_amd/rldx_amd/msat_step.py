@@ -163,11 +163,15 @@ class MsatActionStep:
     LayerNorm -> packed h (rldx_layernorm_pack_bf16) before the QKV and W12
     GEMMs (7 launches per block).  fused_qkv=False splits the QKV launch into
     rldx_grouped_gemm_bf16 (or _ln_bf16) and rldx_msat_qkv_norm_rope_bf16.
+    warm_w3: the attention launch also reads the block's W3 weight panels into
+    the memory-side cache (rldx_attention_packed_fwd_warm_bf16), so the W3 GEMM
+    after Proj and W12 finds them there instead of in HBM.
     The weights are packed once, at construction, into the GEMM's operand order."""
 
-    def __init__(self, cfg: MsatStepCfg, weights: dict, inputs: dict, fused_qkv: bool = True, ln_fold: bool = True):
+    def __init__(self, cfg: MsatStepCfg, weights: dict, inputs: dict, fused_qkv: bool = True, ln_fold: bool = True,
+                 warm_w3: tuple = STREAMS):
         self.cfg, self.w, self.inp = cfg, weights, inputs
-        self.fused_qkv, self.ln_fold = fused_qkv, ln_fold
+        self.fused_qkv, self.ln_fold, self.warm_w3 = fused_qkv, ln_fold, tuple(warm_w3)
         dev = inputs["vl"].device
         n, d, H, D = cfg.tokens, cfg.hidden, cfg.heads, cfg.head_dim
         e = lambda *s: torch.empty(*s, dtype=BF16, device=dev)  # noqa: E731
@@ -243,8 +247,9 @@ class MsatActionStep:
         else:
             Fn.grouped_gemm(*gemm["qkv"], ln_eps=ln, ln_stats=st)
             Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
+        warm = [self.pw[f"{s}.w3"][L].data for s in self.warm_w3]
         Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), cfg.tokens, key_bias=self.inp["key_bias"],
-                            out=self.att)
+                            out=self.att, warm=warm)
         Fn.grouped_gemm(*gemm["proj"], stats_out=st)
         if not self.ln_fold:
             Fn.layernorm_pack(self.x, cfg.eps, out=self.h)

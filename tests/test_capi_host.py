@@ -293,6 +293,33 @@ def test_layernorm_pack_many_rejections():
                                              None) == 0
 
 
+def test_attention_warm_up_rejections():
+    """rldx_attention_packed_fwd_warm_bf16 checks its warm-up ranges before
+    anything else: 0-3 of them, non-negative lengths, 4-byte aligned non-null
+    pointers where a range is not empty."""
+    lib = _lib.load()
+    st = _lib.i64_array([0, 0, 0])
+    ps = _lib.i64_array([0, 64 * 128 * 2 * 19])
+
+    def call(ptrs, nbytes, count):
+        p = (ctypes.c_void_p * max(1, len(ptrs)))(*ptrs) if ptrs is not None else None
+        b = _lib.i64_array(nbytes) if nbytes is not None else None
+        return lib.rldx_attention_packed_fwd_warm_bf16(16, 16, ps, 16, 1, 1, 12, 12, 608, 608, 128, st, st, None, 0,
+                                                       0.088, 0, p, b, count, None)
+
+    assert call([256], [4096], 4) == HIP_INVALID_VALUE           # more than three ranges
+    assert call([256], [4096], -1) == HIP_INVALID_VALUE
+    assert call(None, [4096], 1) == HIP_INVALID_VALUE            # missing pointer array
+    assert call([256], None, 1) == HIP_INVALID_VALUE             # missing length array
+    assert call([256], [-128], 1) == HIP_INVALID_VALUE           # negative length
+    assert call([258], [4096], 1) == HIP_INVALID_VALUE           # misaligned range
+    assert call([None], [4096], 1) == HIP_INVALID_VALUE          # null range with bytes
+    # a bad attention argument is still caught with valid ranges (scale <= 0)
+    assert lib.rldx_attention_packed_fwd_warm_bf16(16, 16, ps, 16, 1, 1, 12, 12, 608, 608, 128, st, st, None, 0,
+                                                   0.0, 0, (ctypes.c_void_p * 1)(256), _lib.i64_array([4096]), 1,
+                                                   None) == HIP_INVALID_VALUE
+
+
 def _msat_norms(ms, rope_ld=0):
     d = (_lib.MsatStream * len(ms))()
     for i, m in enumerate(ms):

@@ -325,6 +325,32 @@ def test_attention_packed_output(dev):
     assert torch.equal(op.unpack(), o.view(S, H * D))
 
 
+@pytest.mark.parametrize("warm_sizes", [(4_718_592, 4_718_592, 4_718_592), (1000,), (0, 129, 12_582_912), (64,)])
+def test_attention_packed_warm_up_is_bit_identical(dev, warm_sizes):
+    """rldx_attention_packed_fwd_warm_bf16 (extra workgroups reading the lines of
+    up to three ranges) returns the bits of the plain launch, with causal and
+    key-bias variants; ranges of any length (partial last lines, empty, shorter
+    than one line) are read only inside their bytes (the warm tensors are left
+    unchanged)."""
+    g = torch.Generator().manual_seed(29)
+    H, S, D = 12, 608, 128
+    q = torch.randn(1, H, S, D, generator=g).to(BF16).to(dev)
+    k = torch.randn(1, H, S, D, generator=g).to(BF16).to(dev)
+    v = torch.randn(1, H, S, D, generator=g).to(BF16).to(dev)
+    bias = torch.zeros(S, device=dev)
+    bias[-8:] = float("-inf")
+    kvp = Fn.kv_pack(k, v)
+    warm = [torch.randint(0, 255, (n,), dtype=torch.uint8, generator=g).to(dev) for n in warm_sizes]
+    before = [t.clone() for t in warm]
+    for kb, causal in ((bias, False), (None, True)):
+        o0 = Fn.attention_packed(q, kvp, S, key_bias=kb, causal=causal, out=Fn.PackedAct.empty(S, H * D, dev))
+        o1 = Fn.attention_packed(q, kvp, S, key_bias=kb, causal=causal, out=Fn.PackedAct.empty(S, H * D, dev),
+                                 warm=warm)
+        torch.cuda.synchronize()
+        assert torch.equal(o0.unpack().view(torch.int16), o1.unpack().view(torch.int16)), f"causal {causal}"
+    assert all(torch.equal(a, b) for a, b in zip(warm, before))
+
+
 def test_concatenated_packed_operand_from_attention_and_bias_packed_gemm(dev):
     """The single-stream block's linear2 operand cat([attention, mlp_proj(...)]):
     the attention kernel writes columns [0, 1536) and a bias_packed GEMM columns
