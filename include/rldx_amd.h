@@ -508,13 +508,16 @@ int64_t rldx_grouped_gemm_ex_workspace_bytes(const rldx_gemm_group_t* groups, in
  * The QKV linears of an MSAT block with the QK-RMSNorm + RoPE + K/V tiling of
  * rldx_msat_qkv_norm_rope_bf16 in the GEMM's epilogue (one launch instead of
  * two): for 1..3 groups in joint-sequence order, y_s = a_s W_s^T + bias_s with
- * W_s [3 * heads * 128, k] packed, y = [Q | K | V] per row; groups[i].out / ldo /
- * residual are unused.  norms[i] gives stream i's Q / K norm weights and RoPE
- * tables (its qkv / qkv_row_stride are unused; rows == groups[i].m).  Q is
- * written as (H, M, 128) at q_out with strides {q_head_stride, q_row_stride},
+ * W_s [3 * heads * head_dim, k] packed, y = [Q | K | V] per row; groups[i].out /
+ * ldo / residual are unused.  norms[i] gives stream i's Q / K norm weights and
+ * RoPE tables (its qkv / qkv_row_stride are unused; rows == groups[i].m).  Q is
+ * written as (H, M, head_dim) at q_out with strides {q_head_stride, q_row_stride},
  * K and V as the packed K/V tiles at kv_packed + h * kv_packed_head_stride
- * (padding keys zero).  Every group but the last non-empty one has rows % 32 == 0
- * (a 32-key tile holds one stream); head_dim == 128; k % 128 == 0.  Results are
+ * (padding keys zero).  Each non-empty group starts a 32-key tile of the joint
+ * sequence (M = its padded rows): a group before the last with rows % 32 != 0 is
+ * followed by zero padding keys, and its padding Q rows are not written;
+ * head_dim == 128, or 64 with an even head count (a 128-column tile then holds
+ * two heads); k % 128 == 0.  Results are
  * bit-identical to rldx_grouped_gemm_bf16 (RLDX_GEMM_EPI_BIAS) followed by
  * rldx_msat_qkv_norm_rope_bf16 with kv_packed.
  * Replaces: the QKV nn.Linear calls of an MSAT block followed by its
@@ -526,6 +529,25 @@ hipError_t rldx_grouped_gemm_qkv_norm_rope_bf16(const rldx_gemm_group_t* groups,
                                                 void* q_out, int64_t q_head_stride, int64_t q_row_stride,
                                                 void* kv_packed, int64_t kv_packed_head_stride, float eps,
                                                 hipStream_t stream);
+
+/*
+ * rldx_grouped_gemm_qkv_norm_rope_bf16 with a K per group (k[i], each a
+ * multiple of 128; the same [Q | K | V] columns for every group): the QKV
+ * linears of streams of different widths in one launch (the VL (4096) and SA
+ * (1536) streams of an RLDX-1 double-stream block have this shape, head_dim
+ * 64; the RLDX-1 chain keeps its split-K QKV launch plus
+ * rldx_msat_qkv_norm_rope_bf16 there, which measured as fast: the fused
+ * epilogue does not split K).  Bit-identical to the per-group GEMMs followed by
+ * rldx_msat_qkv_norm_rope_bf16.
+ * Replaces: the per-stream QKV nn.Linear calls of DoubleStreamBlock.forward and
+ *   its QK-RMSNorm + RoPE (rldx/model/modules/action_model/blocks.py:508-537;
+ *   rldx/inference/action_model/double_stream/engine/kernels/rmsnorm_rope_ds_3way.py:22-386).
+ */
+hipError_t rldx_grouped_gemm_qkv_norm_rope_mixed_bf16(const rldx_gemm_group_t* groups,
+                                                      const rldx_msat_stream_t* norms, int32_t num_groups,
+                                                      int64_t heads, int64_t head_dim, const int64_t* k, void* q_out,
+                                                      int64_t q_head_stride, int64_t q_row_stride, void* kv_packed,
+                                                      int64_t kv_packed_head_stride, float eps, hipStream_t stream);
 
 /*
  * LayerNorm statistics of activation rows, for a GEMM with the pre-LayerNorm

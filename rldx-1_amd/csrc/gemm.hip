@@ -80,8 +80,10 @@ enum {
   kEpiSwigluPacked = 3,
   kEpiBiasPacked = 4,
   kEpiResidualPacked = 5,
-  kEpiQkv = 16  // internal: rldx_grouped_gemm_qkv_norm_rope_bf16
+  kEpiQkv = 16,   // internal: rldx_grouped_gemm_qkv_norm_rope_bf16, head_dim 128
+  kEpiQkv64 = 17  // the same, head_dim 64 (two heads per 128-column tile)
 };
+constexpr bool qkv_epi(int epi) { return epi == kEpiQkv || epi == kEpiQkv64; }
 constexpr bool packed_out(int epi) {
   return epi == kEpiSwigluPacked || epi == kEpiBiasPacked || epi == kEpiResidualPacked;
 }
@@ -193,7 +195,7 @@ struct QkvOut {
   uint16_t* q;
   uint16_t* kvp;
   int64_t q_sh, q_sm, kvp_sh;
-  int inner;  // heads * 128: columns of each of Q, K, V
+  int inner;  // heads * head_dim (a multiple of 128): columns of each of Q, K, V
   float eps;
 };
 
@@ -350,9 +352,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   if constexpr (LN && !kSwiglu) load_wsum();
   // QKV epilogue: the Q or K RMSNorm weights of this thread's 8 columns of the head
   [[maybe_unused]] u32x4 qk_w = {0, 0, 0, 0};
-  if constexpr (EPI == kEpiQkv) {
+  if constexpr (qkv_epi(EPI)) {
+    constexpr int D = EPI == kEpiQkv ? 128 : 64;
     const int which = nt * OC / a.qkv.inner;
-    if (which < 2) qk_w = *reinterpret_cast<const u32x4*>((which == 0 ? G.qn_w : G.kn_w) + cc);
+    if (which < 2) qk_w = *reinterpret_cast<const u32x4*>((which == 0 ? G.qn_w : G.kn_w) + cc % D);
   }
   // LayerNorm fold: this thread's slots of its row, loaded before the ring
   // (consecutive threads: consecutive rows of one slot, contiguous), summed at
@@ -460,33 +463,34 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
       v[4 + i] = hi[i];
     }
   };
-  if constexpr (EPI == kEpiQkv) {
-    // The tile's 128 columns are one head of Q, K or V (columns n0.. of
-    // [Q | K | V]).  Q / K rows: x = bf16(acc + bias), then the per-head RMSNorm
-    // y = bf16(w * (x * rsqrt(mean(x^2) + eps))) and, on streams with tables, the
-    // interleaved RoPE rounded once: msat_qkv_norm_rope_kernel's arithmetic with
-    // its partition of a row (16 lanes of 8 columns), so the result is the same
-    // bit for bit as this GEMM's bias epilogue followed by that kernel.  Q goes to
-    // (H, M, 128); K rows to their lanes of the packed tiles.  V is read down the
-    // fp32 tile's columns (8 keys of one column per 16-byte chunk) straight into
-    // the packed V chunks.  Keys of the stream's last 32-key tile past its rows
-    // are written as zeros (padding keys of the attention).
-    static_assert(OC == 128 && R * CPR == PER * kThreads, "QKV tiles are whole 128-column heads");
-    constexpr int D = OC;
+  if constexpr (qkv_epi(EPI)) {
+    // The tile's 128 columns are one head (head_dim 128) or two (64) of Q, K or
+    // V (columns n0.. of [Q | K | V]).  Q / K rows: x = bf16(acc + bias), then
+    // the per-head RMSNorm y = bf16(w * (x * rsqrt(mean(x^2) + eps))) and, on
+    // streams with tables, the interleaved RoPE rounded once:
+    // msat_qkv_norm_rope_kernel's arithmetic with its partition of a head's row
+    // (D / 8 lanes of 8 columns, butterfly sum over them), so the result is the
+    // same bit for bit as this GEMM's bias epilogue followed by that kernel.  Q
+    // goes to (H, M, D); K rows to their lanes of the packed tiles.  V is read
+    // down the fp32 tile's columns (8 keys of one column per 16-byte chunk)
+    // straight into the packed V chunks.  Keys of the stream's last 32-key tile
+    // past its rows are written as zeros (padding keys of the attention).
+    static_assert(OC == 128 && R * CPR == PER * kThreads, "QKV tiles are 128 columns of whole heads");
+    constexpr int D = EPI == kEpiQkv ? 128 : 64;
+    constexpr int HPT = OC / D;  // heads per tile
     const QkvOut& O = a.qkv;
-    const int n0 = nt * D;
+    const int n0 = nt * OC;
     const int which = n0 / O.inner;  // uniform per tile
-    const int h = (n0 - which * O.inner) / D;
-    uint16_t* kvh = O.kvp + h * O.kvp_sh;
+    const int h0 = (n0 - which * O.inner) / D;
     if (which == 2) {
-      constexpr int NCH = D / 16;  // 1 KB chunks per K or V part of a tile
+      constexpr int NCH = D / 16;  // 1 KB chunks per K or V part of a head's 32-key tile
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int s = static_cast<int>(threadIdx.x) + kThreads * i;
-        const int kt = s / (NCH * 64), idx = s % (NCH * 64);
+        const int kt = s / (HPT * NCH * 64), hh = s / (NCH * 64) % HPT, idx = s % (NCH * 64);
         const int cx = idx >> 6, l = idx & 63;
         // chunk cx = 2 db + s2, lane l, element e: V[16 s2 + 8 (e / 4) + 4 (l / 32) + e % 4][32 db + l % 32]
-        const int d = 32 * (cx >> 1) + (l & 31);
+        const int d = hh * D + 32 * (cx >> 1) + (l & 31);  // tile column
         const int rb = 32 * kt + 16 * (cx & 1) + 4 * (l >> 5);
         const int row0 = mt * R + 32 * kt;  // first stream row of this 32-key tile
         if (row0 >= G.m) continue;
@@ -511,11 +515,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
           }
           o[e] = pack_bf16x2(mt * R + r < G.m ? lo + bd : 0.f, mt * R + r + 1 < G.m ? hi + bd : 0.f);
         }
+        uint16_t* kvh = O.kvp + (h0 + hh) * O.kvp_sh;
         *reinterpret_cast<u32x4*>(kvh + ((G.m_begin + row0) >> 5) * (64 * D) + NCH * 512 + idx * 8) = o;
       }
       return;
     }
     const int c8 = cc;               // columns n0 + c8 = col
+    const int cd = c8 % D;           // their columns within head h0 + c8 / D
+    uint16_t* kvh = O.kvp + (h0 + c8 / D) * O.kvp_sh;
+    const int h = h0 + c8 / D;
     const float* bq = bg;            // their biases
     const u32x4 wraw = qk_w;         // the Q or K norm weights of those columns
 #pragma unroll
@@ -539,7 +547,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
 #pragma unroll
-      for (int mm = CPR / 2; mm >= 1; mm >>= 1) ss += __shfl_xor(ss, mm, 64);  // every lane takes part
+      for (int mm = D / 16; mm >= 1; mm >>= 1) ss += __shfl_xor(ss, mm, 64);  // the D / 8 lanes of the head's row
       u32x4 o;
       {
 #pragma clang fp contract(off)
@@ -553,8 +561,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
         }
         if (G.cos != nullptr) {
           const int64_t rr = min(row, G.m - 1);
-          const floatx4 c = *reinterpret_cast<const floatx4*>(G.cos + rr * G.rope_ld + c8 / 2);
-          const floatx4 sn = *reinterpret_cast<const floatx4*>(G.sin + rr * G.rope_ld + c8 / 2);
+          const floatx4 c = *reinterpret_cast<const floatx4*>(G.cos + rr * G.rope_ld + cd / 2);
+          const floatx4 sn = *reinterpret_cast<const floatx4*>(G.sin + rr * G.rope_ld + cd / 2);
 #pragma unroll
           for (int p = 0; p < 4; ++p) {
             const float re = y[2 * p], im = y[2 * p + 1];
@@ -568,11 +576,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
       const int64_t key = static_cast<int64_t>(G.m_begin) + row;
       if (row < G.m) {
         if (which == 0)
-          *reinterpret_cast<u32x4*>(O.q + h * O.q_sh + key * O.q_sm + c8) = o;
+          *reinterpret_cast<u32x4*>(O.q + h * O.q_sh + key * O.q_sm + cd) = o;
         else
-          *reinterpret_cast<u32x4*>(kvh + packed_k_offset(key, c8, D)) = o;
+          *reinterpret_cast<u32x4*>(kvh + packed_k_offset(key, cd, D)) = o;
       } else if (which == 1 && (row & ~31) < G.m) {
-        *reinterpret_cast<u32x4*>(kvh + packed_k_offset(key, c8, D)) = u32x4{0, 0, 0, 0};
+        *reinterpret_cast<u32x4*>(kvh + packed_k_offset(key, cd, D)) = u32x4{0, 0, 0, 0};
       }
     }
     return;
@@ -837,8 +845,8 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
   }
   auto gn = [&](int i) { return group_n ? group_n[i] : n; };
   auto gk = [&](int i) { return group_k ? group_k[i] : k; };
-  if (!(epilogue >= kEpiBias && epilogue <= kEpiResidualPacked) && epilogue != kEpiQkv) return hipErrorInvalidValue;
-  const bool qkv = epilogue == kEpiQkv;
+  if (!(epilogue >= kEpiBias && epilogue <= kEpiResidualPacked) && !qkv_epi(epilogue)) return hipErrorInvalidValue;
+  const bool qkv = qkv_epi(epilogue);
   // LayerNorm fold: W row sums and A-row statistics for every group; k <= 2048
   // (a thread of a 128-row tile sums at most kLnSlotsMax slots)
   if ((w_row_sums == nullptr) != (ln_stats == nullptr)) return hipErrorInvalidValue;
@@ -857,7 +865,10 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
       if (!stats_out[i] || reinterpret_cast<uintptr_t>(stats_out[i]) % 8) return hipErrorInvalidValue;
   }
   const bool wide = qkv || wide_tiles;
-  if (qkv && (norms == nullptr || split_k > 1 || group_n)) return hipErrorInvalidValue;
+  if (qkv && (norms == nullptr || split_k > 1 || group_splits)) return hipErrorInvalidValue;
+  if (qkv && group_n)  // per-group K only: every group writes the same [Q | K | V] columns
+    for (int i = 0; i < num_groups; ++i)
+      if (group_n[i] != group_n[0]) return hipErrorInvalidValue;
   const bool swiglu = epilogue == kEpiSwiglu || epilogue == kEpiSwigluPacked;
   // k: whole stages of every K-group split (4 K-groups x 2 k-steps); n: whole 64-column blocks
   for (int i = 0; i < num_groups; ++i)
@@ -947,7 +958,7 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
       G.sin = norms[i].rope_sin;
       G.rope_ld = static_cast<int>(norms[i].rope_row_stride);
     }
-    m_begin += s.m;
+    m_begin += qkv ? (s.m + 31) / 32 * 32 : s.m;  // QKV: each stream starts a 32-key tile
   }
   args.num_groups = cnt;
   if (cnt == 0) return hipSuccess;
@@ -1008,12 +1019,12 @@ void launch_epi(const GemmArgs& args, dim3 grid, hipStream_t stream, bool deep, 
     hipLaunchKernelGGL((gemm_kernel<EPI, false, false, LN>), grid, block, 0, stream, args);
 }
 
-template <bool LN>
+template <int EPI, bool LN>
 void launch_qkv(const GemmArgs& args, dim3 grid, hipStream_t stream, bool deep) {
   if (deep)
-    hipLaunchKernelGGL((gemm_kernel<kEpiQkv, true, true, LN>), grid, dim3(kThreads), 0, stream, args);
+    hipLaunchKernelGGL((gemm_kernel<EPI, true, true, LN>), grid, dim3(kThreads), 0, stream, args);
   else
-    hipLaunchKernelGGL((gemm_kernel<kEpiQkv, false, true, LN>), grid, dim3(kThreads), 0, stream, args);
+    hipLaunchKernelGGL((gemm_kernel<EPI, false, true, LN>), grid, dim3(kThreads), 0, stream, args);
 }
 
 // ln: the groups carry W row sums (LayerNorm fold; plan() admits it for the
@@ -1027,7 +1038,9 @@ hipError_t launch(const GemmArgs& args, int epilogue, hipStream_t stream, bool w
   const bool deep = wgs <= 256;
   if (ln) {
     if (epilogue == kEpiQkv)
-      launch_qkv<true>(args, grid, stream, deep);
+      launch_qkv<kEpiQkv, true>(args, grid, stream, deep);
+    else if (epilogue == kEpiQkv64)
+      launch_qkv<kEpiQkv64, true>(args, grid, stream, deep);
     else if (epilogue == kEpiBias)
       launch_epi<kEpiBias, true>(args, grid, stream, deep, wide);
     else if (epilogue == kEpiSwigluPacked)
@@ -1037,7 +1050,8 @@ hipError_t launch(const GemmArgs& args, int epilogue, hipStream_t stream, bool w
     return hipGetLastError();
   }
   switch (epilogue) {
-    case kEpiQkv: launch_qkv<false>(args, grid, stream, deep); break;
+    case kEpiQkv: launch_qkv<kEpiQkv, false>(args, grid, stream, deep); break;
+    case kEpiQkv64: launch_qkv<kEpiQkv64, false>(args, grid, stream, deep); break;
     case kEpiBias: launch_epi<kEpiBias, false>(args, grid, stream, deep, wide); break;
     case kEpiResidual: launch_epi<kEpiResidual, false>(args, grid, stream, deep, wide); break;
     case kEpiSwiglu: launch_epi<kEpiSwiglu, false>(args, grid, stream, deep, wide); break;
@@ -1232,7 +1246,7 @@ extern "C" hipError_t rldx_grouped_gemm_bf16(const rldx_gemm_group_t* groups, in
                                              int64_t k, int32_t epilogue, hipStream_t stream) {
   GemmArgs args;
   int64_t ws, co[3], po[3];
-  if (epilogue == kEpiQkv) return hipErrorInvalidValue;  // rldx_grouped_gemm_qkv_norm_rope_bf16
+  if (qkv_epi(epilogue)) return hipErrorInvalidValue;  // rldx_grouped_gemm_qkv_norm_rope_bf16
   const hipError_t e = plan(groups, num_groups, n, k, epilogue, 1, args, &ws, co, po);
   if (e != hipSuccess) return e;
   return launch(args, epilogue, stream);
@@ -1242,7 +1256,7 @@ extern "C" int64_t rldx_grouped_gemm_workspace_bytes(const rldx_gemm_group_t* gr
                                                      int64_t k, int32_t epilogue, int32_t split_k) {
   GemmArgs args;
   int64_t ws, co[3], po[3];
-  if (epilogue == kEpiQkv || plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po) != hipSuccess)
+  if (qkv_epi(epilogue) || plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po) != hipSuccess)
     return -1;
   return ws;
 }
@@ -1254,7 +1268,7 @@ hipError_t gemm_ws(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t 
                    const int64_t* group_k = nullptr, const int32_t* group_splits = nullptr) {
   GemmArgs args;
   int64_t ws, co[3], po[3];
-  if (epilogue == kEpiQkv || (flags & ~(RLDX_GEMM_WIDE_TILES | RLDX_GEMM_SPLITS_ACROSS_XCDS)))
+  if (qkv_epi(epilogue) || (flags & ~(RLDX_GEMM_WIDE_TILES | RLDX_GEMM_SPLITS_ACROSS_XCDS)))
     return hipErrorInvalidValue;
   const bool wide = (flags & RLDX_GEMM_WIDE_TILES) != 0;
   const hipError_t e = plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po, nullptr, wide, nullptr,
@@ -1292,7 +1306,7 @@ extern "C" int64_t rldx_grouped_gemm_ex_workspace_bytes(const rldx_gemm_group_t*
                                                         int32_t flags) {
   GemmArgs args;
   int64_t ws, co[3], po[3];
-  if (epilogue == kEpiQkv || (flags & ~(RLDX_GEMM_WIDE_TILES | RLDX_GEMM_SPLITS_ACROSS_XCDS)) ||
+  if (qkv_epi(epilogue) || (flags & ~(RLDX_GEMM_WIDE_TILES | RLDX_GEMM_SPLITS_ACROSS_XCDS)) ||
       plan(groups, num_groups, n, k, epilogue, split_k, args, &ws, co, po, nullptr,
            (flags & RLDX_GEMM_WIDE_TILES) != 0) != hipSuccess)
     return -1;
@@ -1348,7 +1362,7 @@ extern "C" int64_t rldx_grouped_gemm_mixed_workspace_bytes(const rldx_gemm_group
                                                            int32_t num_groups, int32_t epilogue, int32_t flags) {
   GemmArgs args;
   int64_t ws, co[3], po[3];
-  if (!n || !k || epilogue == kEpiQkv || (flags & ~(RLDX_GEMM_WIDE_TILES | RLDX_GEMM_SPLITS_ACROSS_XCDS)) ||
+  if (!n || !k || qkv_epi(epilogue) || (flags & ~(RLDX_GEMM_WIDE_TILES | RLDX_GEMM_SPLITS_ACROSS_XCDS)) ||
       plan(groups, num_groups, 0, 0, epilogue, 1, args, &ws, co, po, nullptr, (flags & RLDX_GEMM_WIDE_TILES) != 0,
            nullptr, nullptr, nullptr, n, k, split_k) != hipSuccess)
     return -1;
@@ -1359,23 +1373,24 @@ namespace {
 hipError_t gemm_qkv(const rldx_gemm_group_t* groups, const rldx_msat_stream_t* norms, int32_t num_groups,
                     int64_t heads, int64_t head_dim, int64_t k, void* q_out, int64_t q_head_stride,
                     int64_t q_row_stride, void* kv_packed, int64_t kv_packed_head_stride, float eps,
-                    const float* const* w_row_sums, const float* const* ln_stats, float ln_eps, hipStream_t stream) {
+                    const float* const* w_row_sums, const float* const* ln_stats, float ln_eps, hipStream_t stream,
+                    const int64_t* group_k = nullptr) {
   if (!groups || !norms || num_groups < 1 || num_groups > 3) return hipErrorInvalidValue;
-  if (head_dim != 128 || heads <= 0 || heads > 4096) return hipErrorInvalidValue;
+  // 128-column tiles of whole heads: head_dim 128, or 64 with an even head count
+  if (!(head_dim == 128 || (head_dim == 64 && heads % 2 == 0)) || heads <= 0 || heads > 4096)
+    return hipErrorInvalidValue;
   if (!q_out || !kv_packed || !a16(q_out) || !a16(kv_packed)) return hipErrorInvalidValue;
   if (q_head_stride < 0 || q_row_stride < 0 || q_head_stride % 8 || q_row_stride % 8 || kv_packed_head_stride % 8)
     return hipErrorInvalidValue;
+  // joint rows: each stream starts a 32-key tile of the packed K/V (the rows of
+  // a stream that is not the last are padded to a multiple of 32 with zero keys)
   int64_t m = 0;
-  int last = -1;
-  for (int i = 0; i < num_groups; ++i)
-    if (groups[i].m > 0) last = i;
   for (int i = 0; i < num_groups; ++i) {
     const rldx_gemm_group_t& g = groups[i];
     const rldx_msat_stream_t& s = norms[i];
     if (g.m < 0 || s.rows != g.m) return hipErrorInvalidValue;
     if (g.m == 0) continue;
-    // a 32-key tile of the packed K/V holds the rows of one stream only
-    if (i != last && g.m % 32) return hipErrorInvalidValue;
+    m = (m + 31) / 32 * 32;
     if (!s.q_norm_w || !s.k_norm_w || !a16(s.q_norm_w) || !a16(s.k_norm_w)) return hipErrorInvalidValue;
     if ((s.rope_cos == nullptr) != (s.rope_sin == nullptr)) return hipErrorInvalidValue;
     if (s.rope_cos && (!a16(s.rope_cos) || !a16(s.rope_sin) || s.rope_row_stride < head_dim / 2 ||
@@ -1388,15 +1403,30 @@ hipError_t gemm_qkv(const rldx_gemm_group_t* groups, const rldx_msat_stream_t* n
   if (w_row_sums && !(ln_eps >= 0.f)) return hipErrorInvalidValue;
   GemmArgs args;
   int64_t ws, co[3], po[3];
-  const hipError_t e = plan(groups, num_groups, 3 * heads * head_dim, k, kEpiQkv, 1, args, &ws, co, po, norms, false,
-                            w_row_sums, ln_stats);
+  const int epi = head_dim == 128 ? kEpiQkv : kEpiQkv64;
+  const int64_t n = 3 * heads * head_dim;
+  const int64_t ns[3] = {n, n, n};
+  const hipError_t e = plan(groups, num_groups, n, k, epi, 1, args, &ws, co, po, norms, false, w_row_sums, ln_stats,
+                            nullptr, group_k ? ns : nullptr, group_k);
   if (e != hipSuccess) return e;
   args.qkv = QkvOut{static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(kv_packed), q_head_stride, q_row_stride,
                     kv_packed_head_stride, static_cast<int>(heads * head_dim), eps};
   args.ln_eps = ln_eps;
-  return launch(args, kEpiQkv, stream, true, w_row_sums != nullptr);
+  return launch(args, epi, stream, true, w_row_sums != nullptr);
 }
 }  // namespace
+
+extern "C" hipError_t rldx_grouped_gemm_qkv_norm_rope_mixed_bf16(const rldx_gemm_group_t* groups,
+                                                                 const rldx_msat_stream_t* norms, int32_t num_groups,
+                                                                 int64_t heads, int64_t head_dim, const int64_t* k,
+                                                                 void* q_out, int64_t q_head_stride,
+                                                                 int64_t q_row_stride, void* kv_packed,
+                                                                 int64_t kv_packed_head_stride, float eps,
+                                                                 hipStream_t stream) {
+  if (!k || num_groups < 1 || num_groups > 3) return hipErrorInvalidValue;
+  return gemm_qkv(groups, norms, num_groups, heads, head_dim, k[0], q_out, q_head_stride, q_row_stride, kv_packed,
+                  kv_packed_head_stride, eps, nullptr, nullptr, 0.f, stream, k);
+}
 
 extern "C" hipError_t rldx_grouped_gemm_qkv_norm_rope_bf16(const rldx_gemm_group_t* groups,
                                                            const rldx_msat_stream_t* norms, int32_t num_groups,
@@ -1424,7 +1454,7 @@ extern "C" hipError_t rldx_grouped_gemm_ln_bf16(const rldx_gemm_group_t* groups,
                                                 hipStream_t stream) {
   GemmArgs args;
   int64_t ws, co[3], po[3];
-  if (!w_row_sums || !ln_stats || !(ln_eps >= 0.f) || epilogue == kEpiQkv || (flags & ~RLDX_GEMM_WIDE_TILES))
+  if (!w_row_sums || !ln_stats || !(ln_eps >= 0.f) || qkv_epi(epilogue) || (flags & ~RLDX_GEMM_WIDE_TILES))
     return hipErrorInvalidValue;
   const bool wide = (flags & RLDX_GEMM_WIDE_TILES) != 0;
   const hipError_t e = plan(groups, num_groups, n, k, epilogue, 1, args, &ws, co, po, nullptr, wide, w_row_sums,

@@ -118,6 +118,9 @@ SIGNATURES = {
     "rldx_grouped_gemm_qkv_norm_rope_bf16": (c_i32, [ctypes.POINTER(GemmGroup), ctypes.POINTER(MsatStream), c_i32,
                                                      c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_f32,
                                                      c_vp]),
+    "rldx_grouped_gemm_qkv_norm_rope_mixed_bf16": (c_i32, [ctypes.POINTER(GemmGroup), ctypes.POINTER(MsatStream),
+                                                           c_i32, c_i64, c_i64, c_i64p, c_vp, c_i64, c_i64, c_vp,
+                                                           c_i64, c_f32, c_vp]),
     "rldx_grouped_gemm_ln_bf16": (c_i32, [ctypes.POINTER(GemmGroup), ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), c_i32,
                                           c_i64, c_i64, c_i32, c_i32, c_f32, c_vp]),
     "rldx_grouped_gemm_qkv_norm_rope_ln_bf16": (c_i32, [ctypes.POINTER(GemmGroup), ctypes.POINTER(MsatStream),

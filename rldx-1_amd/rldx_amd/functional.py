@@ -251,15 +251,15 @@ class StreamSpec:
 
 
 def _rope_tables(s: StreamSpec, rows: int, head_dim: int, keep: list):
-    """(cos, sin, row stride) of a stream's fp32 RoPE tables [rows, head_dim/2], or (None, None, 0)."""
+    """(cos, sin, row stride) of a stream's fp32 RoPE tables [>= rows, head_dim/2], or (None, None, 0)."""
     if s.cos is None:
         _require(s.sin is None, "cos and sin go together")
         return None, None, 0
     _require(s.sin is not None, "cos and sin go together")
     c = s.cos.to(F32).contiguous() if s.cos.dtype != F32 or not s.cos.is_contiguous() else s.cos
     sn = s.sin.to(F32).contiguous() if s.sin.dtype != F32 or not s.sin.is_contiguous() else s.sin
-    _require(c.shape == (rows, head_dim // 2) and sn.shape == (rows, head_dim // 2),
-             "rope tables must be [rows, head_dim/2]")
+    _require(c.dim() == 2 and c.shape == sn.shape and c.shape[0] >= rows and c.shape[1] == head_dim // 2,
+             "rope tables must be [>= rows, head_dim/2]")
     keep += [c, sn]
     return c.data_ptr(), sn.data_ptr(), c.stride(0)
 
@@ -906,22 +906,27 @@ def grouped_gemm_qkv_norm_rope(items: Sequence[tuple], norms: Sequence[StreamSpe
     the same bits as grouped_gemm(items, "bias") followed by
     msat_qkv_norm_rope(..., kv_packed=True).  items: (a PackedAct [m, k],
     PackedWeight [3 H D, k], bias [3 H D] or None); norms: one StreamSpec per item
-    (norm weights and tables; its qkv is not read, pass None).  Every stream but
-    the last has rows % 32 == 0.  Returns (q (H, M, D), kvp (H, kv_packed_elems(M,
-    D))); `out` gives them.  ln_eps, ln_stats: with the LayerNorm fold (each a
-    the un-normalised rows, ln_stats their statistics;
-    rldx_grouped_gemm_qkv_norm_rope_ln_bf16)."""
+    (norm weights and tables; its qkv is not read, pass None).  Each stream
+    starts a 32-row block of the joint sequence: a stream before the last with
+    rows % 32 != 0 is followed by zero padding keys (its padding Q rows are not
+    written).  Returns (q (H, M, D), kvp (H, kv_packed_elems(M, D))) with M the
+    joint rows; `out` gives them.  head_dim 128, or 64 with an even head count.  Items
+    may differ in K (streams of different widths, rldx_grouped_gemm_qkv_norm_rope_mixed_bf16).
+    ln_eps, ln_stats: with the LayerNorm fold (each a the un-normalised rows,
+    ln_stats their statistics; rldx_grouped_gemm_qkv_norm_rope_ln_bf16; one K)."""
     _require(1 <= len(items) <= 3 and len(norms) == len(items), "1-3 groups, one StreamSpec each")
-    _require(head_dim == 128, "the fused QKV epilogue needs head_dim 128")
+    _require(head_dim == 128 or (head_dim == 64 and num_heads % 2 == 0),
+             "the fused QKV epilogue needs head_dim 128, or 64 with an even head count")
     inner = num_heads * head_dim
     n, k = 3 * inner, items[0][1].k
+    ks = [it[1].k for it in items]
     groups = (_lib.GemmGroup * len(items))()
     descs = (_lib.MsatStream * len(items))()
-    keep, M = [], 0
+    keep, M = [], 0  # joint rows: each non-empty stream starts a 32-row (32-key) block
     for i, ((a, w, bias), s) in enumerate(zip(items, norms)):
         _require(isinstance(a, PackedAct) and a.ld == a.k, "a must be a PackedAct")
         _on_gpu(a.data, w.data, bias, s.q_w, s.k_w, s.cos, s.sin)
-        _require(w.n == n and w.k == k and a.k == k and not w.swiglu_pairs, "weights must be [3 H D, k], shared k")
+        _require(w.n == n and a.k == w.k and not w.swiglu_pairs, "weights must be [3 H D, k] with a [m, k]")
         if bias is not None:
             _require(bias.dtype == BF16 and bias.is_contiguous() and bias.numel() == n, "bias must be [n] bf16")
         _require(s.q_w.dtype == BF16 and s.k_w.dtype == BF16 and s.q_w.numel() == head_dim and
@@ -930,7 +935,8 @@ def grouped_gemm_qkv_norm_rope(items: Sequence[tuple], norms: Sequence[StreamSpe
         cos_p, sin_p, rope_ld = _rope_tables(s, a.m, head_dim, keep)
         groups[i] = _lib.GemmGroup(a.data.data_ptr(), a.m, w.data.data_ptr(), _ptr(bias), None, 0, None, 0)
         descs[i] = _lib.MsatStream(None, 0, a.m, s.q_w.data_ptr(), s.k_w.data_ptr(), cos_p, sin_p, rope_ld)
-        M += a.m
+        if a.m:
+            M = (M + 31) // 32 * 32 + a.m
     dev = items[0][0].data.device
     if out is None:
         q = torch.empty((num_heads, M, head_dim), dtype=BF16, device=dev)
@@ -942,12 +948,18 @@ def grouped_gemm_qkv_norm_rope(items: Sequence[tuple], norms: Sequence[StreamSpe
     _on_gpu(q, kvp)
     if ln_eps is not None:
         _require(ln_stats is not None, "the LayerNorm fold needs ln_stats")
+        _require(all(x == k for x in ks), "the LayerNorm fold takes groups of one K")
         sums = _row_sums_array(items)
         stats = _stats_array(items, ln_stats, k)
         _lib.check(_lib.load().rldx_grouped_gemm_qkv_norm_rope_ln_bf16(
             groups, descs, sums, stats, len(items), num_heads, head_dim, k, q.data_ptr(), q.stride(0), q.stride(1),
             kvp.data_ptr(), kvp.stride(0), float(eps), float(ln_eps), _stream_ptr(q)),
             "rldx_grouped_gemm_qkv_norm_rope_ln_bf16")
+        return q, kvp
+    if any(x != k for x in ks):
+        _lib.check(_lib.load().rldx_grouped_gemm_qkv_norm_rope_mixed_bf16(
+            groups, descs, len(items), num_heads, head_dim, _lib.i64_array(ks), q.data_ptr(), q.stride(0), q.stride(1),
+            kvp.data_ptr(), kvp.stride(0), float(eps), _stream_ptr(q)), "rldx_grouped_gemm_qkv_norm_rope_mixed_bf16")
         return q, kvp
     _lib.check(_lib.load().rldx_grouped_gemm_qkv_norm_rope_bf16(
         groups, descs, len(items), num_heads, head_dim, k, q.data_ptr(), q.stride(0), q.stride(1), kvp.data_ptr(),

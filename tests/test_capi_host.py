@@ -339,8 +339,10 @@ def test_grouped_gemm_qkv_norm_rope_rejections():
                                                         H, D, k, q, qsh, qsm, kvp, kvsh, 1e-6, None)
 
     assert call(norm_ms=(512, 64, 31)) == HIP_INVALID_VALUE        # rows differ from the GEMM group's
-    assert call(ms=(500, 64, 32)) == HIP_INVALID_VALUE             # a stream before the last with rows % 32
-    assert call(D=64) == HIP_INVALID_VALUE                          # head_dim 128 only
+    # streams start 32-key tiles: 20 + 20 + 20 rows take 3 tiles (84 joint rows), not 2
+    assert call(ms=(20, 20, 20), kvsh=2 * 64 * 128) == HIP_INVALID_VALUE
+    assert call(D=96) == HIP_INVALID_VALUE                          # head_dim 128 or 64
+    assert call(D=64, H=3) == HIP_INVALID_VALUE                     # 64 needs an even head count (whole tiles)
     assert call(k=1000) == HIP_INVALID_VALUE                        # k % 128
     assert call(kvsh=19 * 64 * 128 - 8) == HIP_INVALID_VALUE        # packed K/V head stride too small
     assert call(q=(1 << 20) + 8) == HIP_INVALID_VALUE               # Q not 16-byte aligned
@@ -349,6 +351,20 @@ def test_grouped_gemm_qkv_norm_rope_rejections():
     assert call(H=0) == HIP_INVALID_VALUE
     assert lib.rldx_grouped_gemm_bf16(_gemm_groups(msat), 3, 4608, 1536, QKV_INTERNAL, None) == HIP_INVALID_VALUE
     assert lib.rldx_grouped_gemm_workspace_bytes(_gemm_groups(msat), 3, 4608, 1536, QKV_INTERNAL, 1) == -1
+    for internal in (QKV_INTERNAL, QKV_INTERNAL + 1):
+        assert lib.rldx_grouped_gemm_bf16(_gemm_groups(msat), 3, 4608, 1536, internal, None) == HIP_INVALID_VALUE
+
+    def mixed(ks, ms=(64, 18), D=64, H=24, kvsh=3 * 64 * 64):
+        k = _lib.i64_array(ks) if ks is not None else None
+        return lib.rldx_grouped_gemm_qkv_norm_rope_mixed_bf16(_gemm_groups(ms), _msat_norms(ms), len(ms), H, D, k,
+                                                              1 << 20, 82 * 64, 64, 1 << 24, kvsh, 1e-6, None)
+
+    # the RLDX-1 double-stream QKV shapes (VL 4096 | SA 1536, 24 x 64 heads), each with one argument wrong
+    assert mixed(None) == HIP_INVALID_VALUE                          # no K array
+    assert mixed([4096, 1500]) == HIP_INVALID_VALUE                  # k % 128
+    assert mixed([4096, 1536], ms=(40, 18), kvsh=2 * 64 * 64) == HIP_INVALID_VALUE  # 40 rows pad to 64: 3 tiles
+    assert mixed([4096, 1536], H=23) == HIP_INVALID_VALUE            # odd head count at head_dim 64
+    assert mixed([4096, 1536], kvsh=3 * 64 * 64 - 8) == HIP_INVALID_VALUE
 
 
 def test_vision_attention_workspace_and_rejections():

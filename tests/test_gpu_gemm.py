@@ -387,44 +387,69 @@ def test_concatenated_packed_operand_from_attention_and_bias_packed_gemm(dev):
     assert torch.equal(wide.unpack()[:, 1024:], sw)
 
 
-@pytest.mark.parametrize("ms,H,k", [((512, 64, 32), 12, 1536), ((1024, 64, 32), 12, 256),
-                                   ((64, 32, 20), 2, 256), ((40,), 3, 384), ((0, 96, 64), 2, 128)])
-def test_grouped_gemm_qkv_norm_rope_matches_two_launches(dev, ms, H, k):
+@pytest.mark.parametrize("ms,H,k,D", [((512, 64, 32), 12, 1536, 128), ((1024, 64, 32), 12, 256, 128),
+                                     ((64, 32, 20), 2, 256, 128), ((40,), 3, 384, 128), ((0, 96, 64), 2, 128, 128),
+                                     ((64, 18), 24, (4096, 1536), 64), ((96, 32, 17), 24, (4096, 1536, 1536), 64),
+                                     ((64, 18), 24, 1536, 64), ((40,), 2, 256, 64), ((32, 20), 4, (384, 256), 64),
+                                     ((64, 18), 12, (4096, 1536), 128), ((20, 40, 17), 4, (256, 384, 128), 64),
+                                     ((64, 18, 17), 24, 1536, 64)])
+def test_grouped_gemm_qkv_norm_rope_matches_two_launches(dev, ms, H, k, D):
     """The QKV epilogue (QK RMSNorm + RoPE + packed K/V tiles in the GEMM) is
     bit-identical to the bias GEMM followed by rldx_msat_qkv_norm_rope_bf16:
-    Q (H, M, 128) and every element of the packed K/V tiles, including the zero
+    Q (H, M, D) and every element of the packed K/V tiles, including the zero
     padding keys of a last stream whose rows are not a multiple of 32.  Shapes:
     the action step's streams (128 x 128 and 64 x 128 tiles, one workgroup per
     CU), 1024 rows (more than 256 workgroups: two per CU), short and single
-    streams, an empty stream."""
+    streams, an empty stream; head_dim 64 (two heads per tile) with the RLDX-1
+    double-stream shapes (VL 4096 | SA 1536 [| P 1536], a K per stream:
+    rldx_grouped_gemm_qkv_norm_rope_mixed_bf16) and the single-stream shape.
+    Streams before the last with rows % 32 != 0 start the next stream on a
+    32-row boundary: the reference gives them zero QKV rows up to it (as the
+    RLDX-1 chain pads its SA rows before the P stream); Q is compared on the
+    stream rows (the fused launch does not write padding Q rows), and a padding
+    key may be -0 in the reference (RoPE of a zero row) where the fused launch
+    writes +0."""
     from rldx_amd.msat_step import msat_rope_tables
 
-    g = torch.Generator().manual_seed(sum(ms) + H + k)
-    D, n = 128, 3 * H * 128
-    items, specs, qkv_items = [], [], []
+    ks = list(k) if isinstance(k, tuple) else [k] * len(ms)
+    g = torch.Generator().manual_seed(sum(ms) + H + sum(ks) + D)
+    n = 3 * H * D
+    items, specs, qkv_items, ref_specs, live_rows, M = [], [], [], [], [], 0
+    last = max(i for i, m in enumerate(ms) if m)
     for i, m in enumerate(ms):
+        k = ks[i]
+        mp = (m + 31) // 32 * 32 if i < last else m  # joint rows of the stream
+        if m:
+            live_rows += list(range((M + 31) // 32 * 32, (M + 31) // 32 * 32 + m))
+            M = (M + 31) // 32 * 32 + m
         a = Fn.pack_act(_rand((m, k), g).to(dev)) if m else Fn.PackedAct.empty(0, k, dev)
         w = Fn.pack_weight(_rand((n, k), g, std=k ** -0.5).to(dev))
         b = _rand((n,), g, std=0.5).to(dev)
         qw, kw = (1 + 0.2 * torch.randn(D, generator=g)).to(BF16).to(dev), (1 + 0.2 * torch.randn(D, generator=g)).to(BF16).to(dev)
         cos = sin = None
         if i > 0 and m:  # streams after the first carry RoPE tables
-            ids = torch.stack([torch.zeros(m, dtype=torch.long), torch.arange(m) + 3 * i], dim=-1)
+            ids = torch.stack([torch.zeros(mp, dtype=torch.long), torch.arange(mp) + 3 * i], dim=-1)
             cos, sin = (t.to(dev) for t in msat_rope_tables(ids, D, 10000.0))
-        qkv = torch.empty(m, n, dtype=BF16, device=dev)
+        qkv = torch.zeros(mp, n, dtype=BF16, device=dev)  # rows past m stay zero (padding keys)
         items.append((a, w, b))
-        qkv_items.append((a, w, b, qkv, None))
-        specs.append(Fn.StreamSpec(qkv, qw, kw, cos, sin))
-    M = sum(ms)
+        qkv_items.append((a, w, b, qkv[:m], None))
+        specs.append(Fn.StreamSpec(None, qw, kw, cos, sin))
+        ref_specs.append(Fn.StreamSpec(qkv, qw, kw, cos, sin))
     q = torch.full((H, M, D), 7.0, dtype=BF16, device=dev)
     kvp = torch.full((H, Fn.kv_packed_elems(M, D)), 5.0, dtype=BF16, device=dev)
     Fn.grouped_gemm_qkv_norm_rope(items, specs, H, D, 1e-6, out=(q, kvp))
-    Fn.grouped_gemm([it for it in qkv_items if it[0].m], "bias")
-    live = [s for s in specs if s.qkv.shape[0]]
+    for it in qkv_items:
+        if it[0].m:
+            Fn.grouped_gemm([it], "bias")
+    live = [s for s in ref_specs if s.qkv.shape[0]]
     q2, kvp2 = Fn.msat_qkv_norm_rope(live, H, D, 1e-6, kv_packed=True)
     torch.cuda.synchronize()
-    assert torch.equal(q.view(torch.int16), q2.view(torch.int16))
-    assert torch.equal(kvp.view(torch.int16), kvp2.view(torch.int16))
+    rows = torch.tensor(live_rows, device=dev)
+    assert torch.equal(q[:, rows].view(torch.int16), q2[:, rows].view(torch.int16))
+    # bits equal everywhere, except that a padding key the reference rotates as a
+    # zero row may hold -0 where the fused launch writes +0
+    same = (kvp.view(torch.int16) == kvp2.view(torch.int16)) | ((kvp == 0) & (kvp2 == 0))
+    assert bool(same.all())
 
 
 @pytest.mark.parametrize("epilogue,ms,n,k,split", [("swiglu_packed", (64,), 22016, 512, 1),
