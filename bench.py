@@ -243,6 +243,19 @@ def kernel_lines(torch, reps: int):
     out["gqa_prefill_op_28x4x1280x128"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s", bound="mfma",
                                                peak=BF16_MFMA_PEAK_TFLOPS, frac=tf / BF16_MFMA_PEAK_TFLOPS,
                                                flops=W.gqa_flops(gc))
+    # the same operator at the reference backbone's own attention shape: 32 / 8 heads x 128, 169 tokens
+    # (rldx/inference/backbone/llm/engine/kernels/fused_llm_attention.py:14, rldx/inference/backbone/README.md:5)
+    gs = W.GqaCfg(q_heads=32, kv_heads=8, seq=169)
+    gsi = W.gqa_inputs(gs)
+    sargs = (gsi["qkv"].to(dev), gsi["q_norm_w"].to(dev), None, gsi["k_norm_w"].to(dev), None, gsi["cos"].to(dev),
+             W.signed_sin(gsi["sin"]).to(dev))
+    osb = torch.empty(gs.seq, gs.q_heads * gs.head_dim, dtype=torch.bfloat16, device=dev)
+    ms = graph_time_ms(lambda: ops.llm_fused_attention(*sargs, num_heads=gs.q_heads, num_kv_heads=gs.kv_heads,
+                                                       head_dim=gs.head_dim, out=osb), reps, torch)
+    tf = W.gqa_flops(gs) / (ms * 1e-3) / 1e12
+    out["gqa_prefill_op_32x8x169x128"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s", bound="mfma",
+                                              peak=BF16_MFMA_PEAK_TFLOPS, frac=tf / BF16_MFMA_PEAK_TFLOPS,
+                                              flops=W.gqa_flops(gs))
     # attention kernel alone on pre-normalised Q/K
     M, Hq, Hkv, D = gc.seq, gc.q_heads, gc.kv_heads, gc.head_dim
     qn = torch.randn(1, M, Hq, D, device=dev).to(torch.bfloat16)
@@ -492,6 +505,12 @@ def cpu_kernel_baselines(torch) -> dict:
         lambda: ref.llm_fused_attention(gi["qkv"], gi["q_norm_w"], gi["k_norm_w"], gi["cos"], gi["sin"], gc.q_heads,
                                         gc.kv_heads, gc.head_dim),
         [gi["qkv"], gi["q_norm_w"], gi["k_norm_w"]], reps=5)
+    gs = W.GqaCfg(q_heads=32, kv_heads=8, seq=169)
+    gsi = W.gqa_inputs(gs)
+    leg("gqa_prefill_op_32x8x169x128",
+        lambda: ref.llm_fused_attention(gsi["qkv"], gsi["q_norm_w"], gsi["k_norm_w"], gsi["cos"], gsi["sin"],
+                                        gs.q_heads, gs.kv_heads, gs.head_dim),
+        [gsi["qkv"], gsi["q_norm_w"], gsi["k_norm_w"]])
     return out
 
 
