@@ -854,15 +854,16 @@ hipError_t plan(const rldx_gemm_group_t* groups, int32_t num_groups, int64_t n, 
     if (split_k > 1 || !(epilogue == kEpiBias || epilogue == kEpiSwigluPacked || qkv)) return hipErrorInvalidValue;
     for (int i = 0; i < num_groups; ++i)
       if (gk(i) > 64 * 4 * kLnSlotsMax) return hipErrorInvalidValue;
-    for (int i = 0; i < num_groups; ++i)
-      if (!w_row_sums[i] || reinterpret_cast<uintptr_t>(w_row_sums[i]) % 4 || !ln_stats[i] ||
-          reinterpret_cast<uintptr_t>(ln_stats[i]) % 8)
+    for (int i = 0; i < num_groups; ++i)  // (an empty group reads nothing)
+      if (groups[i].m != 0 && (!w_row_sums[i] || reinterpret_cast<uintptr_t>(w_row_sums[i]) % 4 || !ln_stats[i] ||
+                               reinterpret_cast<uintptr_t>(ln_stats[i]) % 8))
         return hipErrorInvalidValue;
   }
   if (stats_out) {
     if (!residual_epi(epilogue)) return hipErrorInvalidValue;
     for (int i = 0; i < num_groups; ++i)
-      if (!stats_out[i] || reinterpret_cast<uintptr_t>(stats_out[i]) % 8) return hipErrorInvalidValue;
+      if (groups[i].m != 0 && (!stats_out[i] || reinterpret_cast<uintptr_t>(stats_out[i]) % 8))
+        return hipErrorInvalidValue;
   }
   const bool wide = qkv || wide_tiles;
   if (qkv && (norms == nullptr || split_k > 1 || group_splits)) return hipErrorInvalidValue;

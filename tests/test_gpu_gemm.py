@@ -490,7 +490,9 @@ def test_grouped_gemm_wide_tiles_bit_identical(dev, epilogue, ms, n, k, split):
     ("residual_packed", ((18, 1536, 4096), (64, 4096, 2816)), (2, 1), False),
     ("swiglu_packed", ((18, 8192, 1536), (64, 5504, 512)), (1, 1), True),
     ("swiglu_packed", ((40, 512, 256), (300, 256, 384), (5, 1024, 640)), (1, 2, 1), False),
-    ("bias_packed", ((100, 1024, 384), (30, 256, 512)), (2, 1), True)])
+    ("bias_packed", ((100, 1024, 384), (30, 256, 512)), (2, 1), True),
+    ("bias", ((0, 1024, 256), (40, 512, 384)), (1, 2), False),
+    ("residual", ((33, 256, 1024), (0, 512, 128), (7, 128, 256)), (8, 1, 2), False)])
 def test_grouped_gemm_mixed_shapes_bit_identical(dev, epilogue, shapes, splits, wide):
     """One launch of groups with different n, k and split
     (rldx_grouped_gemm_mixed_bf16) gives every group the bits of a launch of that
