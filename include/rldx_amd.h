@@ -414,6 +414,42 @@ typedef struct {
  */
 hipError_t rldx_layernorm_pack_many_bf16(const rldx_rows_t* rows, int32_t count, float eps, hipStream_t stream);
 
+/*
+ * The action encoder side of one flow-matching iteration of the action step,
+ * one launch: the n action rows x = bf16(bf16(bf16(act W_in^T + b_in) + temb)
+ * + pos) (act [n, action_dim], W_in [hidden, action_dim], b_in / temb [hidden],
+ * pos [n, hidden], all bf16 row-major; the dot products in fp32) written in the
+ * packed activation order at `packed` with their LayerNorm statistics
+ * ([hidden / 64][n][2] fp32, the row's sum and sum of squares in slot 0, zeros
+ * in the others, as rldx_act_pack_stats_bf16 writes them), and up to 3 more
+ * row-major matrices rows[i] (k == hidden) packed with statistics rows_stats[i]
+ * in the same launch.  action_dim % 8 == 0 and <= 64; hidden % 64 == 0 and
+ * <= 2048; 16-byte aligned tensors.
+ * Replaces: the action encoder + baked position embedding before the MSAT and
+ *   the MSAT's input packing in the action chain's denoising loop
+ *   (rldx/inference/action_model/engine/custom_action_model_chain.py:138-141; the
+ *   synthetic action step's encoder is one Linear).
+ */
+hipError_t rldx_action_encode_pack_bf16(const void* act, int64_t n, int64_t action_dim, const void* w_in,
+                                        const void* b_in, const void* temb, const void* pos, int64_t hidden,
+                                        void* packed, float* stats, const rldx_rows_t* rows,
+                                        float* const* rows_stats, int32_t num_rows, hipStream_t stream);
+
+/*
+ * The action decoder side of the iteration and its Euler update, one launch:
+ * act = bf16(act + bf16(dt * bf16(LN(x) W_out^T + b_out))) for the n rows x of
+ * a packed activation matrix [n, hidden] (LN without affine parameters:
+ * bf16((x - mean) / sqrt(var + eps)), biased variance, fp32), W_out
+ * [action_dim, hidden], b_out [action_dim], act [n, action_dim] updated in
+ * place.  Limits as rldx_action_encode_pack_bf16.
+ * Replaces: the action decoder and the Euler step of the denoising loop
+ *   (rldx/inference/action_model/engine/custom_action_model_chain.py:166-169; the
+ *   synthetic action step's decoder is LayerNorm + one Linear).
+ */
+hipError_t rldx_action_decode_euler_bf16(const void* packed, int64_t n, int64_t hidden, float eps, const void* w_out,
+                                         const void* b_out, int64_t action_dim, float dt, void* act,
+                                         hipStream_t stream);
+
 /* One stream of a grouped GEMM. */
 typedef struct rldx_gemm_group {
   const void* a_packed;  /* [m, k] bf16 activations in the packed activation order */

@@ -130,6 +130,9 @@ SIGNATURES = {
                                              c_i32, c_i32, c_i32, c_vp, c_i64, c_vp]),
     "rldx_act_pack_stats_bf16": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp]),
     "rldx_layernorm_pack_many_bf16": (c_i32, [ctypes.POINTER(Rows), c_i32, c_f32, c_vp]),
+    "rldx_action_encode_pack_bf16": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp,
+                                             ctypes.POINTER(Rows), ctypes.POINTER(c_vp), c_i32, c_vp]),
+    "rldx_action_decode_euler_bf16": (c_i32, [c_vp, c_i64, c_i64, c_f32, c_vp, c_vp, c_i64, c_f32, c_vp, c_vp]),
     "rldx_grouped_gemm_mixed_bf16": (c_i32, [ctypes.POINTER(GemmGroup), c_i64p, c_i64p, ctypes.POINTER(c_i32),
                                              ctypes.POINTER(c_vp), c_i32, c_i32, c_i32, c_vp, c_i64, c_vp]),
     "rldx_grouped_gemm_mixed_workspace_bytes": (c_i64, [ctypes.POINTER(GemmGroup), c_i64p, c_i64p,

@@ -705,6 +705,60 @@ def layernorm_pack_many(pairs: Sequence[tuple], eps: float = 1e-6) -> None:
                "rldx_layernorm_pack_many_bf16")
 
 
+def _bf16_rows(t: torch.Tensor, shape: tuple, what: str) -> None:
+    _on_gpu(t)
+    _require(t.dtype == BF16 and tuple(t.shape) == shape and t.is_contiguous(), f"{what} must be contiguous bf16 {shape}")
+
+
+def action_encode_pack(act: torch.Tensor, w_in: torch.Tensor, b_in: torch.Tensor, temb: torch.Tensor,
+                       pos: torch.Tensor, out: PackedAct, stats: torch.Tensor,
+                       others: Sequence[tuple] = ()) -> None:
+    """One launch (rldx_action_encode_pack_bf16): out = the packed rows
+    bf16(bf16(bf16(act W_in^T + b_in) + temb) + pos) with their LayerNorm
+    statistics `stats` ([hidden / 64, n, 2]), and each (x [m, hidden], out
+    PackedAct, stats) of `others` (up to 3) packed with its statistics."""
+    n, adim = act.shape
+    hidden = w_in.shape[0]
+    _bf16_rows(act, (n, adim), "act")
+    _bf16_rows(w_in, (hidden, adim), "w_in")
+    _bf16_rows(b_in, (hidden,), "b_in")
+    _bf16_rows(temb.reshape(-1), (hidden,), "temb")
+    _bf16_rows(pos, (n, hidden), "pos")
+    _check_pack_target(out, n, hidden)
+    _check_stats(stats, n, hidden)
+    _require(len(others) <= 3, "at most 3 more matrices")
+    rows = (_lib.Rows * max(1, len(others)))()
+    sts = (ctypes.c_void_p * max(1, len(others)))()
+    for i, (x, o, st) in enumerate(others):
+        _on_gpu(x)
+        _require(x.dtype == BF16 and x.dim() == 2 and x.shape[1] == hidden and x.stride(1) == 1,
+                 "x must be 2-D bf16 [m, hidden], rows contiguous")
+        _check_pack_target(o, x.shape[0], hidden)
+        _check_stats(st, x.shape[0], hidden)
+        rows[i] = _lib.Rows(x.data_ptr(), x.stride(0), x.shape[0], hidden, o.data.data_ptr())
+        sts[i] = st.data_ptr()
+    _lib.check(_lib.load().rldx_action_encode_pack_bf16(act.data_ptr(), n, adim, w_in.data_ptr(), b_in.data_ptr(),
+                                                        temb.data_ptr(), pos.data_ptr(), hidden, out.data.data_ptr(),
+                                                        stats.data_ptr(), rows, sts, len(others), _stream_ptr(act)),
+               "rldx_action_encode_pack_bf16")
+
+
+def action_decode_euler(x: PackedAct, w_out: torch.Tensor, b_out: torch.Tensor, act: torch.Tensor, dt: float,
+                        eps: float = 1e-6) -> None:
+    """act += dt * (LN(x) W_out^T + b_out), in place, one launch
+    (rldx_action_decode_euler_bf16; each of the eager chain's roundings)."""
+    n, adim = act.shape
+    hidden = w_out.shape[1]
+    _require(isinstance(x, PackedAct) and x.m == n and x.k == hidden and x.ld == x.k, "x must be a PackedAct [n, hidden]")
+    _on_gpu(x.data)
+    _bf16_rows(w_out, (adim, hidden), "w_out")
+    _bf16_rows(b_out, (adim,), "b_out")
+    _bf16_rows(act, (n, adim), "act")
+    _lib.check(_lib.load().rldx_action_decode_euler_bf16(x.data.data_ptr(), n, hidden, float(eps), w_out.data_ptr(),
+                                                         b_out.data_ptr(), adim, float(dt), act.data_ptr(),
+                                                         _stream_ptr(act)), "rldx_action_decode_euler_bf16")
+
+
 class GemmWorkspace:
     """Device scratch of the split-K grouped GEMM: per-tile arrival counters and
     fp32 partial tiles.  Zero-filled once here; every launch leaves its counters

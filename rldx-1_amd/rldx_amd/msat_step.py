@@ -21,7 +21,8 @@ rldx/inference/action_model/model/graph_safe_action_model.py:430-485):
 
 Every block runs on the rldx_amd HIP kernels (LayerNorm, grouped GEMMs with
 fused bias / residual / SwiGLU epilogues, QK-RMSNorm + RoPE, joint attention);
-only the tiny action in/out projections around the blocks use torch.addmm.
+the tiny action in/out projections around the blocks are one HIP launch each
+per iteration (fused_io; torch.addmm and torch elementwise ops otherwise).
 Activations of the three streams share one [608, 1536] buffer (rows VL | SA |
 P) so every launch covers all streams.
 """
@@ -163,15 +164,20 @@ class MsatActionStep:
     LayerNorm -> packed h (rldx_layernorm_pack_bf16) before the QKV and W12
     GEMMs (7 launches per block).  fused_qkv=False splits the QKV launch into
     rldx_grouped_gemm_bf16 (or _ln_bf16) and rldx_msat_qkv_norm_rope_bf16.
+    fused_io (with ln_fold): each iteration's action encoder, position
+    embedding and operand packing of the three streams are one launch
+    (rldx_action_encode_pack_bf16) and its decoder + Euler update another
+    (rldx_action_decode_euler_bf16), instead of eleven torch / pack launches.
     warm_w3: the attention launch also reads the block's W3 weight panels into
     the memory-side cache (rldx_attention_packed_fwd_warm_bf16), so the W3 GEMM
     after Proj and W12 finds them there instead of in HBM.
     The weights are packed once, at construction, into the GEMM's operand order."""
 
     def __init__(self, cfg: MsatStepCfg, weights: dict, inputs: dict, fused_qkv: bool = True, ln_fold: bool = True,
-                 warm_w3: tuple = STREAMS):
+                 warm_w3: tuple = STREAMS, fused_io: bool = True):
         self.cfg, self.w, self.inp = cfg, weights, inputs
         self.fused_qkv, self.ln_fold, self.warm_w3 = fused_qkv, ln_fold, tuple(warm_w3)
+        self.fused_io = fused_io and ln_fold
         dev = inputs["vl"].device
         n, d, H, D = cfg.tokens, cfg.hidden, cfg.heads, cfg.head_dim
         e = lambda *s: torch.empty(*s, dtype=BF16, device=dev)  # noqa: E731
@@ -273,15 +279,25 @@ class MsatActionStep:
             if not self.ln_fold:
                 self.x[cfg.rows("vl")].copy_(inp["vl"])
                 self.x[cfg.rows("p")].copy_(inp["p"])
-            torch.addmm(w["act_in.b"], self.act, w["act_in.w"].t(), out=self.sa_in)
-            self.sa_in.add_(inp["temb"][t])
-            torch.add(self.sa_in, inp["pos"], out=self.x[sa])
-            if self.ln_fold:
-                for s in STREAMS:
-                    r = cfg.rows(s)
-                    Fn.pack_act(self.x[r], out=self.xp.rows(r.start, r.stop), stats=self.xst[s])
+            if self.fused_io:
+                others = [(self.x[cfg.rows(s)], self.xp.rows(cfg.rows(s).start, cfg.rows(s).stop), self.xst[s])
+                          for s in ("vl", "p")]
+                Fn.action_encode_pack(self.act, w["act_in.w"], w["act_in.b"], inp["temb"][t], inp["pos"],
+                                      self.xp.rows(sa.start, sa.stop), self.xst["sa"], others)
+            else:
+                torch.addmm(w["act_in.b"], self.act, w["act_in.w"].t(), out=self.sa_in)
+                self.sa_in.add_(inp["temb"][t])
+                torch.add(self.sa_in, inp["pos"], out=self.x[sa])
+                if self.ln_fold:
+                    for s in STREAMS:
+                        r = cfg.rows(s)
+                        Fn.pack_act(self.x[r], out=self.xp.rows(r.start, r.stop), stats=self.xst[s])
             for L in range(blocks):
                 self._block(L)
+            if self.fused_io:
+                Fn.action_decode_euler(self.xp.rows(sa.start, sa.stop), w["act_out.w"], w["act_out.b"], self.act, dt,
+                                       cfg.eps)
+                continue
             x_sa = self.xp.rows(sa.start, sa.stop).unpack() if self.ln_fold else self.x[sa]
             hs = F.layer_norm(x_sa, (cfg.hidden,), eps=cfg.eps)
             torch.addmm(w["act_out.b"], hs, w["act_out.w"].t(), out=self.vel)

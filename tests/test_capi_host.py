@@ -320,6 +320,45 @@ def test_attention_warm_up_rejections():
                                                    None) == HIP_INVALID_VALUE
 
 
+def test_action_encode_decode_rejections():
+    """rldx_action_encode_pack_bf16 / rldx_action_decode_euler_bf16 check every
+    argument before launching: action_dim % 8 and <= 64, hidden % 64 and <= 2048,
+    alignment, at most 3 more matrices with hidden columns; empty inputs launch
+    nothing."""
+    lib = _lib.load()
+    A = 4096  # a 16-byte aligned stand-in address (nothing is launched)
+
+    def enc(n=64, adim=32, hidden=1536, act=A, packed=A, stats=A, rows=None, count=0):
+        rs = (_lib.Rows * max(1, count))(*(rows or []))
+        st = (ctypes.c_void_p * max(1, count))(*([A] * count))
+        return lib.rldx_action_encode_pack_bf16(act, n, adim, A, A, A, A, hidden, packed, stats, rs, st, count, None)
+
+    assert enc(adim=30) == HIP_INVALID_VALUE
+    assert enc(adim=72) == HIP_INVALID_VALUE
+    assert enc(hidden=1500) == HIP_INVALID_VALUE
+    assert enc(hidden=4096) == HIP_INVALID_VALUE
+    assert enc(act=A + 8) == HIP_INVALID_VALUE
+    assert enc(packed=None) == HIP_INVALID_VALUE
+    assert enc(stats=A + 4) == HIP_INVALID_VALUE
+    assert enc(count=4, rows=[_lib.Rows(A, 1536, 8, 1536, A)] * 4) == HIP_INVALID_VALUE
+    assert enc(count=1, rows=[_lib.Rows(A, 1536, 8, 1024, A)]) == HIP_INVALID_VALUE   # k != hidden
+    assert enc(count=1, rows=[_lib.Rows(A, 1532, 8, 1536, A)]) == HIP_INVALID_VALUE   # ldx < k
+    assert enc(count=1, rows=[_lib.Rows(A + 2, 1536, 8, 1536, A)]) == HIP_INVALID_VALUE
+    assert enc(n=0, count=1, rows=[_lib.Rows(None, 1536, 0, 1536, None)]) == 0        # nothing to do
+
+    def dec(n=64, hidden=1536, eps=1e-6, adim=32, packed=A, act=A, b=A, dt=0.25):
+        return lib.rldx_action_decode_euler_bf16(packed, n, hidden, eps, A, b, adim, dt, act, None)
+
+    assert dec(adim=12) == HIP_INVALID_VALUE
+    assert dec(hidden=2112) == HIP_INVALID_VALUE
+    assert dec(eps=-1.0) == HIP_INVALID_VALUE
+    assert dec(dt=float("nan")) == HIP_INVALID_VALUE
+    assert dec(packed=A + 8) == HIP_INVALID_VALUE
+    assert dec(act=None) == HIP_INVALID_VALUE
+    assert dec(b=A + 1) == HIP_INVALID_VALUE
+    assert dec(n=0) == 0
+
+
 def _msat_norms(ms, rope_ld=0):
     d = (_lib.MsatStream * len(ms))()
     for i, m in enumerate(ms):

@@ -295,6 +295,67 @@ def test_layernorm_pack_many_matches_one_at_a_time(dev, shapes):
         assert torch.equal(a.unpack().view(torch.int16), b.unpack().view(torch.int16)), f"{m} x {k}"
 
 
+@pytest.mark.parametrize("n,adim,hidden,others", [(64, 32, 1536, ((512, 0), (32, 8))), (18, 16, 512, ()),
+                                                   (37, 64, 2048, ((5, 3),)), (64, 8, 256, ((40, 0), (1, 2), (7, 5)))])
+def test_action_encode_pack(dev, n, adim, hidden, others):
+    """rldx_action_encode_pack_bf16: the action rows are the eager chain
+    bf16(bf16(bf16(act W_in^T + b_in) + temb) + pos) (fp32 dot products: within
+    one bf16 rounding of the chain computed with torch in fp32 on the CPU), and
+    every matrix's packed rows and statistics are the bits rldx_act_pack_stats_bf16
+    gives for the same rows (other matrices with a row stride wider than hidden)."""
+    g = torch.Generator().manual_seed(n + adim + hidden)
+    act = _rand((n, adim), g).to(dev)
+    w_in = _rand((hidden, adim), g, std=adim ** -0.5).to(dev)
+    b_in, temb = _rand((hidden,), g, 0.5).to(dev), _rand((hidden,), g, 0.5).to(dev)
+    pos = _rand((n, hidden), g, 0.5).to(dev)
+    xs = [_rand((m, hidden + pad * 8), g).to(dev)[:, :hidden] for m, pad in others]
+    out, st = Fn.PackedAct.empty(n, hidden, dev), Fn.ln_stats_empty(n, hidden, dev)
+    o_out = [(x, Fn.PackedAct.empty(x.shape[0], hidden, dev), Fn.ln_stats_empty(x.shape[0], hidden, dev)) for x in xs]
+    Fn.action_encode_pack(act, w_in, b_in, temb, pos, out, st, o_out)
+    torch.cuda.synchronize()
+    y = out.unpack()
+    a32, w32 = act.float().cpu(), w_in.float().cpu()
+    lin = (a32 @ w32.t()) + b_in.float().cpu()
+    ref = (((lin.to(BF16).float() + temb.float().cpu()).to(BF16).float()) + pos.float().cpu()).to(BF16)
+    diff = (y.cpu().float() - ref.float()).abs()
+    # each of the three roundings may land one ulp apart (the dot products sum in another order): bound by the
+    # magnitudes that enter them
+    tol = (lin.abs() + temb.float().cpu().abs() + pos.float().cpu().abs()) * 2 ** -7 + 1e-6
+    assert (diff <= tol).all(), f"max diff {diff.max().item()}"
+    for x, o, s in [(y, out, st)] + o_out:
+        rp, rs = Fn.PackedAct.empty(x.shape[0], hidden, dev), Fn.ln_stats_empty(x.shape[0], hidden, dev)
+        Fn.pack_act(x.contiguous(), out=rp, stats=rs)
+        torch.cuda.synchronize()
+        assert torch.equal(o.unpack().view(torch.int16), rp.unpack().view(torch.int16))
+        assert torch.equal(s, rs)
+
+
+@pytest.mark.parametrize("n,adim,hidden", [(64, 32, 1536), (18, 16, 512), (5, 64, 2048)])
+def test_action_decode_euler(dev, n, adim, hidden):
+    """rldx_action_decode_euler_bf16 against the eager chain on the same packed
+    rows: act + dt * (LN(x) W_out^T + b_out) with each of its bf16 roundings
+    (torch in fp32 on the CPU): within one bf16 rounding of every step."""
+    g = torch.Generator().manual_seed(n * adim + hidden)
+    x = (2 * torch.randn(n, hidden, generator=g) + 0.3).to(BF16)
+    w_out = _rand((adim, hidden), g, std=hidden ** -0.5).to(dev)
+    b_out = _rand((adim,), g, 0.5).to(dev)
+    act = _rand((n, adim), g).to(dev)
+    act0 = act.clone()
+    dt = 0.25
+    Fn.action_decode_euler(Fn.pack_act(x.to(dev)), w_out, b_out, act, dt, 1e-6)
+    torch.cuda.synchronize()
+    hs = torch.nn.functional.layer_norm(x.float(), (hidden,), eps=1e-6).to(BF16).float()
+    w32 = w_out.float().cpu()
+    vel = (hs @ w32.t() + b_out.float().cpu()).to(BF16).float()
+    ref = (act0.float().cpu() + (vel * dt).to(BF16).float()).to(BF16)
+    diff = (act.cpu().float() - ref.float()).abs()
+    # hs may differ by one ulp per element (another mean / rsqrt evaluation) and the sums run in another order:
+    # bound the velocity error by the magnitudes summed, then the two roundings after it
+    vel_err = (hs.abs() @ w32.abs().t() + b_out.float().cpu().abs()) * 2 ** -7
+    tol = (act0.float().cpu().abs() + dt * vel.abs()) * 2 ** -7 + dt * vel_err + 1e-6
+    assert (diff <= tol).all(), f"max diff {diff.max().item()}"
+
+
 def test_swiglu_packed_epilogue_matches_row_major(dev):
     g = torch.Generator().manual_seed(13)
     n, k = 8192, 1536

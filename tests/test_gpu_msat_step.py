@@ -91,6 +91,22 @@ def test_fused_qkv_epilogue_step_is_bit_identical(setup):
     assert torch.equal(fused.view(torch.int16), split.view(torch.int16))
 
 
+def test_fused_action_io_step_is_bit_identical(setup):
+    """The action encoder + operand packing and the decoder + Euler update as
+    one launch each (rldx_action_encode_pack_bf16, rldx_action_decode_euler_bf16)
+    give the bits of the eager torch chain (addmm, adds, packs; unpack,
+    layer_norm, addmm, mul, add) over 2 iterations of 2 blocks, and with the W3
+    warm-up off as well."""
+    cfg, w, inp, _, _ = setup
+    outs = []
+    for io, warm in ((True, ("vl", "sa", "p")), (False, ("vl", "sa", "p")), (True, ())):
+        step = MsatActionStep(cfg, w, inp, fused_io=io, warm_w3=warm)
+        outs.append(step.run(steps=2, blocks=2).clone())
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    assert torch.equal(outs[0].view(torch.int16), outs[2].view(torch.int16))
+
+
 def test_step_eager_prenorm_two_blocks(setup):
     """ln_fold=False: the LayerNorm-pack launches (the pre-norm rounded to bf16 as
     the eager chain does) instead of the fold; the bf16 contract on 2 blocks."""
