@@ -128,35 +128,12 @@ struct AttnArgs {
   int num_seqs;
   int total_rows;
   int d_store;  // output columns written per head (<= D)
-  // Memory-side-cache warm-up: the first n_work workgroups compute attention;
-  // the ones after them read one dword of every 128-byte line of up to three
-  // ranges (pf_end: cumulative line counts), pf_lpw lines each.
+  // the first n_work workgroups compute attention; those after them read the
+  // lines of `warm` (rldx_attention_packed_fwd_warm_bf16)
   int n_work;
-  const uint32_t* pf[3];
-  int64_t pf_end[3];
-  int64_t pf_lpw;
+  WarmRanges warm;
 };
 
-// One warm-up workgroup: plain loads (they allocate in the memory-side cache on
-// the way; non-temporal loads measured no warm-up), 8 per thread in flight,
-// results folded into a register that an empty asm statement consumes.
-__device__ __forceinline__ void warm_lines(const AttnArgs& a, int w) {
-  const int64_t l0 = w * a.pf_lpw, l1 = min(l0 + a.pf_lpw, a.pf_end[2]);
-  uint32_t acc = 0;
-  for (int64_t base = l0 + static_cast<int>(threadIdx.x); base < l1; base += 8 * 256) {
-    uint32_t v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t l = base + j * 256;
-      const int r = l < a.pf_end[0] ? 0 : l < a.pf_end[1] ? 1 : 2;
-      const int64_t rb = r == 0 ? 0 : a.pf_end[r - 1];
-      v[j] = l < l1 ? a.pf[r][(l - rb) * 32] : 0u;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc ^= v[j];
-  }
-  asm volatile("" ::"v"(acc));
-}
 
 // Sequence s of a variable-length batch (rows [c_s, c_{s+1}) with
 // c_s = clamp(cu_seqlens[s], 0, rows)) owns the 32-row slots
@@ -294,7 +271,7 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
   constexpr int G4 = DBLK * 4 + 1;  // float4 groups per lane and sub-block in the merge: O + (m, l)
   __shared__ floatx4 merge[NW * NSUB * G4 * 64];
   if (static_cast<int>(blockIdx.x) >= a.n_work) {  // warm-up workgroups (no barrier, no LDS)
-    warm_lines(a, static_cast<int>(blockIdx.x) - a.n_work);
+    warm_lines(a.warm, static_cast<int>(blockIdx.x) - a.n_work, 256);
     return;
   }
 
@@ -1045,9 +1022,9 @@ void launch_attn_d(AttnArgs a, int batch, bool causal, bool has_bias, hipStream_
   a.n_work = a.num_q_blocks * a.hq * batch;
   // warm-up workgroups: about 1024 lines (128 KB) each, at most 256
   int n_pf = 0;
-  if (a.pf_end[2] > 0) {
-    n_pf = static_cast<int>(std::min<int64_t>(256, (a.pf_end[2] + 1023) / 1024));
-    a.pf_lpw = (a.pf_end[2] + n_pf - 1) / n_pf;
+  if (a.warm.end[2] > 0) {
+    n_pf = static_cast<int>(std::min<int64_t>(256, (a.warm.end[2] + 1023) / 1024));
+    a.warm.per_wg = (a.warm.end[2] + n_pf - 1) / n_pf;
   }
   dim3 grid(static_cast<unsigned>(a.n_work + n_pf));
   dim3 block(256);
@@ -1200,16 +1177,7 @@ hipError_t attention_packed(const void* q, const void* kv_packed, const int64_t*
   a.kv = static_cast<const uint16_t*>(kv_packed);
   a.kv_sb = packed_strides[0];
   a.kv_sh = packed_strides[1];
-  int64_t lines = 0;
-  for (int i = 0; i < warm_count; ++i) {
-    a.pf[i] = static_cast<const uint32_t*>(warm_ptrs[i]);
-    lines += warm_bytes[i] / 128;
-    a.pf_end[i] = lines;
-  }
-  for (int i = warm_count; i < 3; ++i) {
-    a.pf[i] = a.pf[0];
-    a.pf_end[i] = lines;
-  }
+  if (!warm_ranges(warm_ptrs, warm_bytes, warm_count, a.warm)) return hipErrorInvalidValue;
   return launch_attn<false>(a, head_dim, static_cast<int>(batch), causal != 0, key_bias != nullptr, stream);
 }
 }  // namespace
@@ -1231,14 +1199,8 @@ extern "C" hipError_t rldx_attention_packed_fwd_warm_bf16(
     int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
     const int64_t* o_strides, const float* key_bias, int64_t key_bias_batch_stride, float scale, int32_t causal,
     const void* const* warm_ptrs, const int64_t* warm_bytes, int32_t warm_count, hipStream_t stream) {
-  if (warm_count < 0 || warm_count > 3 || (warm_count > 0 && (!warm_ptrs || !warm_bytes))) return hipErrorInvalidValue;
-  int64_t lines = 0;
-  for (int i = 0; i < warm_count; ++i) {
-    if (warm_bytes[i] < 0 || (warm_bytes[i] > 0 && (!warm_ptrs[i] || reinterpret_cast<uintptr_t>(warm_ptrs[i]) % 4)))
-      return hipErrorInvalidValue;
-    lines += warm_bytes[i] / 128;
-  }
-  if (lines > (int64_t{1} << 40)) return hipErrorInvalidValue;
+  WarmRanges check;
+  if (!warm_ranges(warm_ptrs, warm_bytes, warm_count, check)) return hipErrorInvalidValue;
   return attention_packed(q, kv_packed, packed_strides, o, out_packed, batch, q_heads, kv_heads, seq_q, seq_k,
                           head_dim, q_strides, o_strides, key_bias, key_bias_batch_stride, scale, causal, warm_ptrs,
                           warm_bytes, warm_count, stream);

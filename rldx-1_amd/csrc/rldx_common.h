@@ -185,4 +185,54 @@ RLDX_HD int64_t packed_k_offset(int64_t key, int d0, int D) {
   return (key >> 5) * (64 * D) + ((d0 >> 4) * 64 + lane) * 8;
 }
 
+// Memory-side-cache warm-up carried by extra workgroups of a launch: up to
+// three byte ranges, `end` the cumulative counts of their whole 128-byte lines.
+struct WarmRanges {
+  const uint32_t* ptr[3];
+  int64_t end[3];
+  int64_t per_wg;  // lines per warm-up workgroup
+};
+
+// Warm-up workgroup w (of `nthreads` threads) reads one dword of each of its
+// lines: plain loads (they allocate in the memory-side cache on the way;
+// non-temporal loads measured no warm-up), 8 per thread in flight, the results
+// folded into a register that an empty asm statement consumes (no stores, no
+// LDS, no barrier).
+__device__ __forceinline__ void warm_lines(const WarmRanges& wr, int w, int nthreads) {
+  const int64_t l0 = w * wr.per_wg, l1 = min(l0 + wr.per_wg, wr.end[2]);
+  uint32_t acc = 0;
+  for (int64_t base = l0 + static_cast<int>(threadIdx.x); base < l1; base += 8 * nthreads) {
+    uint32_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t l = base + j * nthreads;
+      const int r = l < wr.end[0] ? 0 : l < wr.end[1] ? 1 : 2;
+      const int64_t rb = r == 0 ? 0 : wr.end[r - 1];
+      v[j] = l < l1 ? wr.ptr[r][(l - rb) * 32] : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc ^= v[j];
+  }
+  asm volatile("" ::"v"(acc));
+}
+
+// Host: validates up to three ranges (4-byte aligned, non-negative lengths) and
+// fills `wr` (per_wg left 0); returns false on a bad argument.
+inline bool warm_ranges(const void* const* ptrs, const int64_t* bytes, int32_t count, WarmRanges& wr) {
+  wr = WarmRanges{};
+  if (count < 0 || count > 3 || (count > 0 && (!ptrs || !bytes))) return false;
+  int64_t lines = 0;
+  for (int i = 0; i < count; ++i) {
+    if (bytes[i] < 0 || (bytes[i] > 0 && (!ptrs[i] || reinterpret_cast<uintptr_t>(ptrs[i]) % 4))) return false;
+    wr.ptr[i] = static_cast<const uint32_t*>(ptrs[i]);
+    lines += bytes[i] / 128;
+    wr.end[i] = lines;
+  }
+  for (int i = count; i < 3; ++i) {
+    wr.ptr[i] = wr.ptr[0];
+    wr.end[i] = lines;
+  }
+  return lines <= (int64_t{1} << 40);
+}
+
 }  // namespace rldx

@@ -466,12 +466,8 @@ def attention_packed(q: torch.Tensor, kvp: torch.Tensor, seq_k: int, *, key_bias
             _lib.i64_array(_bhs_strides(q, layout)), _lib.i64_array(o_strides), kb_ptr, kb_stride, float(scale),
             int(bool(causal)))
     if warm:
-        _require(len(warm) <= 3, "at most three warm-up ranges")
-        _on_gpu(*warm)
-        _require(all(t.is_contiguous() and t.device == q.device for t in warm), "warm-up tensors: contiguous, q's device")
-        ptrs = (ctypes.c_void_p * len(warm))(*[t.data_ptr() for t in warm])
-        nbytes = _lib.i64_array([t.numel() * t.element_size() for t in warm])
-        _lib.check(lib.rldx_attention_packed_fwd_warm_bf16(*args, ptrs, nbytes, len(warm), _stream_ptr(q)),
+        ptrs, nbytes, count = _warm_args(warm, q.device)
+        _lib.check(lib.rldx_attention_packed_fwd_warm_bf16(*args, ptrs, nbytes, count, _stream_ptr(q)),
                    "rldx_attention_packed_fwd_warm_bf16")
     else:
         _lib.check(lib.rldx_attention_packed_fwd_bf16(*args, _stream_ptr(q)), "rldx_attention_packed_fwd_bf16")
@@ -950,6 +946,14 @@ def grouped_gemm(items: Sequence[tuple], epilogue: str = "bias", split_k=1,
         _on_gpu(workspace.data)
         _lib.check(lib.rldx_grouped_gemm_ws_bf16(groups, len(items), n, k, epi, int(split_k), workspace.data.data_ptr(),
                                                  workspace.data.numel(), _stream_ptr(wt)), "rldx_grouped_gemm_ws_bf16")
+
+
+def _warm_args(warm: Sequence[torch.Tensor], device):
+    _require(len(warm) <= 3, "at most three warm-up ranges")
+    _on_gpu(*warm)
+    _require(all(t.is_contiguous() and t.device == device for t in warm), "warm-up tensors: contiguous, one device")
+    ptrs = (ctypes.c_void_p * max(1, len(warm)))(*[t.data_ptr() for t in warm])
+    return ptrs, _lib.i64_array([t.numel() * t.element_size() for t in warm] or [0]), len(warm)
 
 
 def grouped_gemm_qkv_norm_rope(items: Sequence[tuple], norms: Sequence[StreamSpec], num_heads: int,
