@@ -376,7 +376,10 @@ class RldxMsat:
         # activations
         N, nv, ns, nx, npp = self.N, self.nv, cfg.n_sa, self.nx, self.np_
         ebuf = lambda *s: torch.empty(*s, dtype=BF16, device=self.dev)  # noqa: E731
-        self.x_sa, self.x_vl = ebuf(ns, cfg.sa_dim), ebuf(nv, cfg.vl_dim)
+        # x = [VL->SA | time | SA] of the single-stream blocks; its SA rows are the SA residual stream of the
+        # double-stream blocks (no copy between the two)
+        self.x = ebuf(nx, cfg.sa_dim)
+        self.x_sa, self.x_vl = self.x[nv:], ebuf(nv, cfg.vl_dim)
         self.h_sa, self.h_vl = Fn.PackedAct.empty(ns, cfg.sa_dim, self.dev), Fn.PackedAct.empty(nv, cfg.vl_dim,
                                                                                                  self.dev)
         # QKV rows of SA: self.ns rows, the GEMM writes the first n_sa, padding rows stay zero
@@ -388,7 +391,6 @@ class RldxMsat:
         self.gl_sa = Fn.PackedAct.empty(ns, self.sa_ffn_p, self.dev)
         self.gl_vl = Fn.PackedAct.empty(nv, self.vl_ffn_p, self.dev)
         self.vl_packed = Fn.PackedAct.empty(nv, cfg.vl_dim, self.dev)
-        self.x = ebuf(nx, cfg.sa_dim)
         self.h = Fn.PackedAct.empty(nx, cfg.sa_dim, self.dev)
         self.qkv_buf = torch.zeros(nv + self.ns, 3 * inner, dtype=BF16, device=self.dev)
         self.qkv = self.qkv_buf[:nx]
@@ -593,7 +595,8 @@ class RldxMsat:
     # -- forward --------------------------------------------------------------
     def forward(self, hidden_states: torch.Tensor, encoder_hidden_states: torch.Tensor, temb: torch.Tensor,
                 time_token: torch.Tensor, encoder_attention_mask: Optional[torch.Tensor] = None,
-                physics_embs: Optional[torch.Tensor] = None, physics_attention_mask: Optional[torch.Tensor] = None):
+                physics_embs: Optional[torch.Tensor] = None, physics_attention_mask: Optional[torch.Tensor] = None,
+                adaln: Optional[tuple] = None):
         """CustomOpMSAT.forward (custom_msat_chain.py:109-126): hidden_states
         [1, n_sa_pure, sa_dim], encoder_hidden_states [1, n_vl, vl_dim], temb
         [1, inner], time_token [1, num_temb_tokens, sa_dim] -> [1, n_sa_pure,
@@ -606,7 +609,9 @@ class RldxMsat:
         sa_dim] is required and the result is {"action": [1, n_sa_pure,
         output_dim], "physics": [1, n_physics, output_dim]};
         physics_attention_mask [1] (1 = visible; a chain built with
-        vl_mask=True) masks every P key (msat.py:716-743)."""
+        vl_mask=True) masks every P key (msat.py:716-743).  adaln: the output
+        AdaLN's (shift, scale[, physics shift, physics scale]) for this temb,
+        precomputed with adaln_of(temb) (None: computed here)."""
         cfg = self.cfg
         nt, nv = cfg.num_temb_tokens, cfg.n_vl
         Fn._require(tuple(hidden_states.shape) == (1, cfg.n_sa_pure, cfg.sa_dim) and
@@ -646,19 +651,16 @@ class RldxMsat:
             self._ds_block(blk, gm)
         # x = [vl_proj_to_sa(vl) | time token | SA]
         Fn.pack_act(self.x_vl, out=self.vl_packed)
-        self._gemm(self.vl_proj_gemm)
-        self.x[self.nv:].copy_(self.x_sa)
+        self._gemm(self.vl_proj_gemm)  # rows [0, nv) of x; rows [nv, nx) already hold the SA stream
         for blk, gm in zip(self.ss, self.ss_gemms):
             self._ss_block(blk, gm)
         # AdaLN output projections (msat.py:771-781)
-        silu_t = F.silu(temb)
-        shift, scale = F.linear(silu_t, self.w["proj_out_1.weight"], self.w["proj_out_1.bias"]).chunk(2, dim=1)
+        shift, scale, *pmod = self.adaln_of(temb) if adaln is None else adaln
         sa = F.layer_norm(self.x[self.nx - cfg.n_sa_pure:], (cfg.sa_dim,), eps=1e-6)
         torch.add(sa * (1 + scale), shift, out=self.mod)
         Fn.pack_act(self.mod, out=self.mod_packed)
         if self.phys:
-            pshift, pscale = F.linear(silu_t, self.w["proj_out_physics_1.weight"],
-                                      self.w["proj_out_physics_1.bias"]).chunk(2, dim=1)
+            pshift, pscale = pmod
             ph = F.layer_norm(self.x_p, (cfg.sa_dim,), eps=1e-6)
             torch.add(ph * (1 + pscale), pshift, out=self.mod_p)
             Fn.pack_act(self.mod_p, out=self.mod_p_packed)
@@ -668,6 +670,19 @@ class RldxMsat:
         return self.out
 
     __call__ = forward
+
+    def adaln_of(self, temb: torch.Tensor) -> tuple:
+        """(shift, scale) of the output AdaLN for `temb` [1, inner] (and the physics
+        output's pair with a P stream): F.silu(temb) -> proj_out_1 (msat.py:771-781).
+        A caller whose temb is fixed per step (the action head's static time
+        embeddings) computes them once and passes them to forward(adaln=...)."""
+        silu_t = F.silu(temb)
+        shift, scale = F.linear(silu_t, self.w["proj_out_1.weight"], self.w["proj_out_1.bias"]).chunk(2, dim=1)
+        if not self.phys:
+            return shift, scale
+        pshift, pscale = F.linear(silu_t, self.w["proj_out_physics_1.weight"],
+                                  self.w["proj_out_physics_1.bias"]).chunk(2, dim=1)
+        return shift, scale, pshift, pscale
 
     def _forward_static(self):
         i = self.inputs
@@ -962,6 +977,8 @@ class RldxActionHead:
             self.p_embs = e(1, msat.np_, mc.sa_dim)
             # history positions 0 .. T_hist - 1 (physics.py:19-25), baked
             self.hist_pos = sinusoidal_time(torch.arange(cfg.physics_hist_len, device=dev), mc.sa_dim).to(BF16)
+        # the output AdaLN of each step's (static) time embedding, computed once
+        self.adaln = [msat.adaln_of(head_sd["static_tembs"][i]) for i in range(cfg.steps)]
         self.graph = None
 
     def _lin(self, x, name):
@@ -993,13 +1010,14 @@ class RldxActionHead:
                 self.p_embs[0, nh:].copy_(self._physics_encoder(self.physics_fut[0], self.tau[i][: cfg.physics_fut_len],
                                                                 "physics_fut_encoder"))
                 o = self.msat.forward(self.sa, self.vl, sd["static_tembs"][i], sd["static_time_tokens"][i],
-                                      physics_embs=self.p_embs)
+                                      physics_embs=self.p_embs, adaln=self.adaln[i])
                 out = o["action"]
                 ph = o["physics"][0, -cfg.physics_fut_len:]
                 pv = self._lin(F.silu(self._lin(ph, "physics.physics_decoder.net.0")), "physics.physics_decoder.net.2")
                 self.physics_fut[0].add_(pv, alpha=self.dt)
             else:
-                out = self.msat.forward(self.sa, self.vl, sd["static_tembs"][i], sd["static_time_tokens"][i])
+                out = self.msat.forward(self.sa, self.vl, sd["static_tembs"][i], sd["static_time_tokens"][i],
+                                        adaln=self.adaln[i])
             hd = F.relu(_cat_linear(out[0], sd, "action_decoder.layer1", e))
             v = _cat_linear(hd, sd, "action_decoder.layer2", e)[-cfg.action_horizon:]
             self.act[0].add_(v, alpha=self.dt)
