@@ -149,6 +149,36 @@ def graph_time_ms(fn, reps: int, torch) -> float:
     return best
 
 
+def vendor_sdpa(torch, q, k, v, *, causal=False, mask=None, reps=20):
+    """torch.nn.functional.scaled_dot_product_attention on the same bf16 shape
+    (B, H, S, D): the library attention a PyTorch-ROCm user gets, timed like the
+    kernel lines.  Only the fused backends are tried (flash = AOTriton, then
+    memory-efficient), with the same key-padding mask where the line has one;
+    `flash_unmasked_us` is the flash backend without the mask (it takes none),
+    a lower bound for the library on that shape."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    res = {}
+    for name, be in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        try:
+            with sdpa_kernel([be]):
+                ms = graph_time_ms(lambda: F.scaled_dot_product_attention(q, k, v, attn_mask=mask,
+                                                                          is_causal=causal), reps, torch)
+            res.update(us=ms * 1e3, backend=name)
+            break
+        except RuntimeError:
+            continue
+    if mask is not None and res.get("backend") != "flash":
+        try:
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+                ms = graph_time_ms(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=causal), reps, torch)
+            res["flash_unmasked_us"] = ms * 1e3
+        except RuntimeError:
+            pass
+    return res or None
+
+
 def kernel_lines(torch, reps: int):
     from oracle import cpu_reference as ref  # noqa: F401  (not used for timing; keeps import errors early)
     from rldx_amd import functional as Fn
@@ -221,6 +251,8 @@ def kernel_lines(torch, reps: int):
     out["joint_attention_16x608x128"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s", bound="mfma",
                                               peak=BF16_MFMA_PEAK_TFLOPS, frac=tf / BF16_MFMA_PEAK_TFLOPS,
                                               flops=W.joint_attn_flops(jc))
+    sdpa_mask = bias.to(torch.bfloat16).view(1, 1, 1, -1).expand(1, 1, jc.tokens, jc.tokens).contiguous()
+    out["joint_attention_16x608x128"]["vendor_sdpa"] = vendor_sdpa(torch, q, k, v, mask=sdpa_mask)
     ms = graph_time_ms(lambda: Fn.attention(q, k, v, key_bias=bias, out=o), reps, torch)
     tf = W.joint_attn_flops(jc) / (ms * 1e-3) / 1e12
     out["joint_attention_16x608x128_with_kv_pack"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s",
@@ -268,6 +300,10 @@ def kernel_lines(torch, reps: int):
     out["gqa_attention_28x4x1280x128"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s", bound="mfma",
                                               peak=BF16_MFMA_PEAK_TFLOPS, frac=tf / BF16_MFMA_PEAK_TFLOPS,
                                               flops=W.gqa_flops(gc))
+    g = Hq // Hkv  # the library kernels take K / V expanded to the query heads
+    out["gqa_attention_28x4x1280x128"]["vendor_sdpa"] = vendor_sdpa(
+        torch, qn.transpose(1, 2), kn.repeat_interleave(g, dim=2).transpose(1, 2).contiguous(),
+        vn.repeat_interleave(g, dim=2).transpose(1, 2).contiguous(), causal=True)
 
     # the step's own attention shape: 12 x 608 x 128, masked
     sc = MsatStepCfg()
@@ -285,6 +321,8 @@ def kernel_lines(torch, reps: int):
     out["step_joint_attention_12x608x128"] = dict(us=ms * 1e3, achieved=tf, unit="TFLOP/s", bound="mfma",
                                                   peak=BF16_MFMA_PEAK_TFLOPS, frac=tf / BF16_MFMA_PEAK_TFLOPS,
                                                   flops=fl)
+    out["step_joint_attention_12x608x128"]["vendor_sdpa"] = vendor_sdpa(
+        torch, qs, ks, vs, mask=bs.to(torch.bfloat16).view(1, 1, 1, -1).expand(1, 1, n, n).contiguous())
 
     # ViT attention, 2 images x 196 patches, 16 heads x 72 (RoPE + K/V packing + varlen attention)
     vc = W.VitAttnCfg()
@@ -516,13 +554,26 @@ def cpu_kernel_baselines(torch) -> dict:
 
 def measured_peaks(torch) -> dict:
     """Peaks measured on this GPU, beside the published ones: device-to-device
-    copy bandwidth (1 GiB, read + write bytes) and the bf16 MFMA throughput of a
-    library GEMM (torch.matmul 8192 x 8192 x 8192, hipBLASLt)."""
+    copy bandwidth (1 GiB, read + write bytes), the read rate of a library
+    reduction over 1 GiB, and the bf16 MFMA throughput of a library GEMM
+    (torch.matmul 8192 x 8192 x 8192, hipBLASLt)."""
     dev = torch.device("cuda:0")
     a = torch.empty(512 << 20, dtype=torch.bfloat16, device=dev)
     b = torch.empty_like(a)
     ms = graph_time_ms(lambda: b.copy_(a), 8, torch)
     copy_gbs = 2 * a.numel() * 2 / (ms * 1e-3) / 1e9
+    # read-only: a library reduction over the same 1 GiB, eager (a captured
+    # reduction records memset nodes), events on the launch stream
+    stream = torch.cuda.current_stream()
+    for _ in range(2):
+        a.sum(dtype=torch.float32)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(8):
+        a.sum(dtype=torch.float32)
+    e1.record(stream)
+    e1.synchronize()
+    read_gbs = a.numel() * 2 / (e0.elapsed_time(e1) / 8 * 1e-3) / 1e9
     del a, b
     n = 8192
     x = torch.randn(n, n, device=dev).to(torch.bfloat16)
@@ -530,7 +581,7 @@ def measured_peaks(torch) -> dict:
     z = torch.empty(n, n, dtype=torch.bfloat16, device=dev)
     ms = graph_time_ms(lambda: torch.matmul(x, y, out=z), 8, torch)
     tflops = 2 * n ** 3 / (ms * 1e-3) / 1e12
-    return dict(copy_gbs=copy_gbs, stream_gbs=stream_same_bytes(torch, 1 << 30)["gbs"],
+    return dict(copy_gbs=copy_gbs, read_sum_gbs=read_gbs, stream_gbs=stream_same_bytes(torch, 1 << 30)["gbs"],
                 matmul_bf16_tflops=tflops,
                 published=dict(hbm_gbs=HBM_PEAK_GBS, bf16_mfma_tflops=BF16_MFMA_PEAK_TFLOPS))
 
@@ -677,13 +728,15 @@ def main():
     for v in kl.values():  # fractions against the measured peaks as well
         if isinstance(v, dict) and v.get("unit") == "GB/s":
             v["frac_of_measured_copy"] = v["achieved"] / peaks["copy_gbs"]
+            v["frac_of_measured_read"] = v["achieved"] / peaks["read_sum_gbs"]
             if "bytes" in v:  # and against a plain elementwise kernel moving the same bytes
                 ref = stream_same_bytes(torch, v["bytes"])
                 v["stream_same_bytes_us"] = ref["us"]
                 v["frac_of_stream_same_bytes"] = ref["us"] / v["us"]
         elif isinstance(v, dict) and v.get("unit") == "TFLOP/s":
             v["frac_of_measured_matmul"] = v["achieved"] / peaks["matmul_bf16_tflops"]
-    print(f"[bench] measured peaks: copy {peaks['copy_gbs']:.0f} GB/s, stream {peaks['stream_gbs']:.0f} GB/s, "
+    print(f"[bench] measured peaks: copy {peaks['copy_gbs']:.0f} GB/s, read {peaks['read_sum_gbs']:.0f} GB/s, "
+          f"stream {peaks['stream_gbs']:.0f} GB/s, "
           f"bf16 matmul {peaks['matmul_bf16_tflops']:.0f} TFLOP/s", file=sys.stderr, flush=True)
 
     cpu = None
