@@ -434,19 +434,36 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   wait_barrier<0>();
   // LayerNorm fold factors of tile row r: rstd and rstd * mean, with mean and
   // the biased variance E[x^2] - mean^2 (clamped at 0) in fp32 and rstd from
-  // v_rsq_f32 (the fold is not bit-compatible with the eager pre-norm anyway)
-  auto ln_row = [&](int r, float& rs, float& rm) {
-    float s1 = lnst[2 * r], s2 = lnst[2 * r + 1];
+  // v_rsq_f32 (the fold is not bit-compatible with the eager pre-norm anyway).
+  // Thread r < R computes its row's pair once and leaves it at lnst[2 r], so
+  // every later use is two LDS reads (the V tiles of the QKV epilogue use each
+  // row's pair 64 times per workgroup).
+  if constexpr (LN) {
+    float rs = 0.f, rm = 0.f;
+    const int r = static_cast<int>(threadIdx.x);
+    if (r < R) {
+      float s1 = lnst[2 * r], s2 = lnst[2 * r + 1];
 #pragma unroll
-    for (int p = 1; p < kThreads / R; ++p) {
-      s1 += lnst[(p * R + r) * 2];
-      s2 += lnst[(p * R + r) * 2 + 1];
+      for (int p = 1; p < kThreads / R; ++p) {
+        s1 += lnst[(p * R + r) * 2];
+        s2 += lnst[(p * R + r) * 2 + 1];
+      }
+      const float inv_k = 1.0f / static_cast<float>(G.k);
+      const float mean = s1 * inv_k;
+      const float var = __builtin_fmaxf(__builtin_fmaf(-mean, mean, s2 * inv_k), 0.f);
+      rs = __builtin_amdgcn_rsqf(var + a.ln_eps);
+      rm = rs * mean;
     }
-    const float inv_k = 1.0f / static_cast<float>(G.k);
-    const float mean = s1 * inv_k;
-    const float var = __builtin_fmaxf(__builtin_fmaf(-mean, mean, s2 * inv_k), 0.f);
-    rs = __builtin_amdgcn_rsqf(var + a.ln_eps);
-    rm = rs * mean;
+    __syncthreads();  // every partial sum is read before the pairs overwrite them
+    if (r < R) {
+      lnst[2 * r] = rs;
+      lnst[2 * r + 1] = rm;
+    }
+    __syncthreads();
+  }
+  auto ln_row = [&](int r, float& rs, float& rm) {
+    rs = lnst[2 * r];
+    rm = lnst[2 * r + 1];
   };
   // 8 consecutive fp32 sums (K-groups in order) of tile row r from tile column tc
   auto sum8 = [&](int r, int tc, float (&v)[8]) {
