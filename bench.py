@@ -159,6 +159,9 @@ def vendor_sdpa(torch, q, k, v, *, causal=False, mask=None, reps=20):
     import torch.nn.functional as F
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
+    import warnings
+
+    warnings.filterwarnings("ignore", message=".*(attention|Attention|cuDNN).*")
     res = {}
     for name, be in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
         try:
@@ -735,6 +738,8 @@ def main():
                 v["frac_of_stream_same_bytes"] = ref["us"] / v["us"]
         elif isinstance(v, dict) and v.get("unit") == "TFLOP/s":
             v["frac_of_measured_matmul"] = v["achieved"] / peaks["matmul_bf16_tflops"]
+        elif isinstance(v, dict) and "gbs" in v:  # the step GEMMs: weight streaming against the read rate
+            v["frac_of_measured_read"] = v["gbs"] / peaks["read_sum_gbs"]
     print(f"[bench] measured peaks: copy {peaks['copy_gbs']:.0f} GB/s, read {peaks['read_sum_gbs']:.0f} GB/s, "
           f"stream {peaks['stream_gbs']:.0f} GB/s, "
           f"bf16 matmul {peaks['matmul_bf16_tflops']:.0f} TFLOP/s", file=sys.stderr, flush=True)
