@@ -156,16 +156,16 @@ def vendor_sdpa(torch, q, k, v, *, causal=False, mask=None, reps=20):
     memory-efficient), with the same key-padding mask where the line has one;
     `flash_unmasked_us` is the flash backend without the mask (it takes none),
     a lower bound for the library on that shape."""
+    import warnings
+
     import torch.nn.functional as F
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
-    import warnings
-
-    warnings.filterwarnings("ignore", message=".*(attention|Attention|cuDNN).*")
     res = {}
     for name, be in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
         try:
-            with sdpa_kernel([be]):
+            with sdpa_kernel([be]), warnings.catch_warnings():
+                warnings.simplefilter("ignore")  # the backend's reasons for declining a case
                 ms = graph_time_ms(lambda: F.scaled_dot_product_attention(q, k, v, attn_mask=mask,
                                                                           is_causal=causal), reps, torch)
             res.update(us=ms * 1e3, backend=name)
@@ -174,7 +174,8 @@ def vendor_sdpa(torch, q, k, v, *, causal=False, mask=None, reps=20):
             continue
     if mask is not None and res.get("backend") != "flash":
         try:
-            with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION]), warnings.catch_warnings():
+                warnings.simplefilter("ignore")
                 ms = graph_time_ms(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=causal), reps, torch)
             res["flash_unmasked_us"] = ms * 1e3
         except RuntimeError:
