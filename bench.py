@@ -59,7 +59,8 @@ def parse():
     return ap.parse_args()
 
 
-PROFILE_KERNELS = ("joint_attn", "gqa_attn", "gqa_op", "step_attn", "swiglu", "rmsnorm_rope")
+PROFILE_KERNELS = ("joint_attn", "gqa_attn", "gqa_op", "gqa_op_169", "step_attn", "vit_attn", "mem_attn", "swiglu",
+                   "rmsnorm_rope", "res_ln", "vl_ln", "add2_rmsnorm")
 
 
 def profile_launch(name: str, torch):
@@ -100,7 +101,35 @@ def profile_launch(name: str, torch):
         o = torch.empty_like(q)
         kvp = Fn.kv_pack(k, v)
         return lambda: Fn.attention_packed(q, kvp, n, key_bias=bias, out=o)
-    gc = W.GqaCfg()
+    if name == "vit_attn":  # 2 x 196 patches, 16 x 72: pack launch + varlen attention
+        vc = W.VitAttnCfg()
+        vi = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in W.vit_attention_inputs(vc).items()}
+        vws = torch.empty(Fn.vision_attention_workspace_bytes(vc.tokens, vc.images, vc.heads, vc.head_dim),
+                          dtype=torch.uint8, device=dev)
+        vo = torch.empty(vc.tokens, vc.heads * vc.head_dim, dtype=torch.bfloat16, device=dev)
+        return lambda: Fn.vision_attention(vi["qkv"], vi["rope_cos"], vi["rope_sin"], vi["cu_seqlens"],
+                                           vi["scaling"], vc.heads, vc.head_dim, out=vo, workspace=vws)
+    if name == "mem_attn":  # 64 tokens, 16 x 256, block-causal (block 16)
+        mc = W.MemAttnCfg()
+        mi = W.memory_attention_inputs(mc)
+        mq, mcos, msin = mi["qkv"].to(dev), mi["cos"].to(dev), mi["signed_sin"].to(dev)
+        mo = torch.empty(mc.tokens, mc.heads * mc.head_dim, dtype=torch.bfloat16, device=dev)
+        return lambda: Fn.memory_attention(mq, mcos, msin, mc.heads, mc.head_dim, mc.n_cog, out=mo)
+    if name in ("res_ln", "vl_ln", "add2_rmsnorm"):  # the residual-add + norm epilogues of the kernel lines
+        def rows(m, d):
+            return torch.randn(m, d, device=dev).to(torch.bfloat16)
+
+        if name == "res_ln":
+            sr, sp, sb = rows(18, 1536), rows(18, 1536), rows(1, 1536)[0]
+            vr, vp, vb = rows(128, 4096), rows(128, 4096), rows(1, 4096)[0]
+            return lambda: Fn.fused_grouped_res_ln(sr, sb, sp, vr, vb, vp)
+        if name == "vl_ln":
+            vr, vp, vb = rows(128, 4096), rows(128, 4096), rows(1, 4096)[0]
+            nv, lv = torch.empty_like(vr), torch.empty_like(vr)
+            return lambda: Fn.fused_vl_epilogue_ln(vr, vb, vb, vp, new_vl_out=nv, ln_vl_out=lv)
+        lh, lr, lw = rows(1280, 2048), rows(1280, 2048), rows(1, 2048)[0]
+        return lambda: Fn.fused_add2_rmsnorm(lh, lr, lw)
+    gc = W.GqaCfg(q_heads=32, kv_heads=8, seq=169) if name == "gqa_op_169" else W.GqaCfg()
     if name == "gqa_attn":  # causal 28/4 x 1280 x 128 on pre-normalised Q/K
         M, Hq, Hkv, D = gc.seq, gc.q_heads, gc.kv_heads, gc.head_dim
         q = torch.randn(1, M, Hq, D, device=dev).to(torch.bfloat16)
@@ -109,7 +138,8 @@ def profile_launch(name: str, torch):
         o = torch.empty_like(q)
         kvp = Fn.kv_pack(k, v, layout="bshd")
         return lambda: Fn.attention_packed(q, kvp, M, causal=True, layout="bshd", out=o)
-    # gqa_op: rldx_backbone::fused_attention (K norm + K/V tiles, then attention with the Q norm)
+    # gqa_op / gqa_op_169: rldx_backbone::fused_attention (K norm + K/V tiles, then attention with
+    # the Q norm) at 28/4 x 1280 x 128 / at the reference backbone's 32/8 x 169 x 128
     import rldx_amd.ops as ops
 
     gi = W.gqa_inputs(gc)
