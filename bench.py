@@ -771,6 +771,7 @@ def main():
             v["frac_of_measured_matmul"] = v["achieved"] / peaks["matmul_bf16_tflops"]
         elif isinstance(v, dict) and "gbs" in v:  # the step GEMMs: weight streaming against the read rate
             v["frac_of_measured_read"] = v["gbs"] / peaks["read_sum_gbs"]
+    roofline["frac_of_measured_read"] = dom["gbs"] / peaks["read_sum_gbs"]
     print(f"[bench] measured peaks: copy {peaks['copy_gbs']:.0f} GB/s, read {peaks['read_sum_gbs']:.0f} GB/s, "
           f"stream {peaks['stream_gbs']:.0f} GB/s, "
           f"bf16 matmul {peaks['matmul_bf16_tflops']:.0f} TFLOP/s", file=sys.stderr, flush=True)
