@@ -15,10 +15,11 @@ weights, one launch per block (16 weight sets, 1.2-2.9 GB, so every launch
 streams its weights from HBM as in the step).  `roofline` is the dominant kernel
 of the step: the W12 + SwiGLU grouped GEMM (3 streams x [8192 x 1536] weights),
 whose arithmetic intensity (~186 flop/B) puts it under the HBM roof.
-`roofline.traffic` is the measured HBM bytes per launch of that kernel
+`roofline.traffic` is the measured L2-miss bytes per launch of that kernel
 (rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by the same counters' reading for a
-copy of known size), read from profiles/gemm_w12_swiglu_traffic.json when that
-file is present.  cpu_baseline: the CPU oracle of the same step (torch bf16 on
+copy of known size: bytes the L2s exchange with the memory side, served by the
+256 MB MALL or by HBM), read from profiles/gemm_w12_swiglu_traffic.json when
+that file is present.  cpu_baseline: the CPU oracle of the same step (torch bf16 on
 the host cores).
 
 Profiling helpers (no JSON line):
@@ -214,7 +215,6 @@ def vendor_sdpa(torch, q, k, v, *, causal=False, mask=None, reps=20):
 
 
 def kernel_lines(torch, reps: int):
-    from oracle import cpu_reference as ref  # noqa: F401  (not used for timing; keeps import errors early)
     from rldx_amd import functional as Fn
     from rldx_amd import workloads as W
     from rldx_amd.msat_step import MsatStepCfg
@@ -561,9 +561,10 @@ def cpu_kernel_baselines(torch) -> dict:
 
     rc = W.RmsRopeCfg()
     ri = W.rmsnorm_rope_inputs(rc)
+    # the hashed tensor sets are those of tests/golden/workloads.json, so the two can be cross-checked
     leg("rmsnorm_rope_f32_256x16x64",
         lambda: ref.qk_rmsnorm_rope_half(ri["q"], ri["k"], ri["w"], ri["w"], ri["cos"], ri["sin"], rc.eps),
-        [ri["q"], ri["k"], ri["w"]])
+        [ri["q"], ri["k"], ri["w"], ri["cos"], ri["sin"]])
     sx = W.swiglu_inputs(W.SwigluCfg())["x"]
     leg("swiglu_2048x11008", lambda: ref.swiglu(sx), [sx])
     jc = W.JointAttnCfg()
@@ -576,46 +577,61 @@ def cpu_kernel_baselines(torch) -> dict:
     leg("gqa_prefill_op_28x4x1280x128",
         lambda: ref.llm_fused_attention(gi["qkv"], gi["q_norm_w"], gi["k_norm_w"], gi["cos"], gi["sin"], gc.q_heads,
                                         gc.kv_heads, gc.head_dim),
-        [gi["qkv"], gi["q_norm_w"], gi["k_norm_w"]], reps=5)
+        [gi["qkv"], gi["q_norm_w"], gi["k_norm_w"], gi["cos"], gi["sin"]], reps=5)
     gs = W.GqaCfg(q_heads=32, kv_heads=8, seq=169)
     gsi = W.gqa_inputs(gs)
     leg("gqa_prefill_op_32x8x169x128",
         lambda: ref.llm_fused_attention(gsi["qkv"], gsi["q_norm_w"], gsi["k_norm_w"], gsi["cos"], gsi["sin"],
                                         gs.q_heads, gs.kv_heads, gs.head_dim),
-        [gsi["qkv"], gsi["q_norm_w"], gsi["k_norm_w"]])
+        [gsi["qkv"], gsi["q_norm_w"], gsi["k_norm_w"], gsi["cos"], gsi["sin"]])
     return out
+
+
+def read_probe_gbs(torch, nbytes: int = 512 << 20, copies: int = 3, reps: int = 8) -> float:
+    """HBM read rate of the library's streaming read kernel (rldx_read_probe:
+    16-byte loads, 8 in flight per thread, one workgroup per CU, nothing written),
+    over `copies` rotated buffers of `nbytes` so the 256 MB MALL cannot hold
+    them; graph-timed like the kernel lines."""
+    from rldx_amd import _lib
+
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    bufs = [torch.ones(nbytes // 2, dtype=torch.bfloat16, device=dev) for _ in range(copies)]
+    words = lib.rldx_read_probe_sink_words()
+    sink = torch.zeros(words, dtype=torch.int32, device=dev)
+    it = {"i": 0}
+
+    def run():
+        b = bufs[it["i"] % copies]
+        it["i"] += 1
+        _lib.check(lib.rldx_read_probe(b.data_ptr(), nbytes, sink.data_ptr(), words,
+                                       torch.cuda.current_stream().cuda_stream), "rldx_read_probe")
+
+    ms = graph_time_ms(run, reps * copies, torch)
+    del bufs
+    return nbytes / (ms * 1e-3) / 1e9
 
 
 def measured_peaks(torch) -> dict:
     """Peaks measured on this GPU, beside the published ones: device-to-device
-    copy bandwidth (1 GiB, read + write bytes), the read rate of a library
-    reduction over 1 GiB, and the bf16 MFMA throughput of a library GEMM
-    (torch.matmul 8192 x 8192 x 8192, hipBLASLt)."""
+    copy bandwidth (1 GiB, read + write bytes), the HBM read rate of a plain
+    streaming read kernel (3 rotated 512 MiB buffers, `read_probe_gbs`), and the
+    bf16 MFMA throughput of a library GEMM (torch.matmul 8192 x 8192 x 8192,
+    hipBLASLt)."""
     dev = torch.device("cuda:0")
     a = torch.empty(512 << 20, dtype=torch.bfloat16, device=dev)
     b = torch.empty_like(a)
     ms = graph_time_ms(lambda: b.copy_(a), 8, torch)
     copy_gbs = 2 * a.numel() * 2 / (ms * 1e-3) / 1e9
-    # read-only: a library reduction over the same 1 GiB, eager (a captured
-    # reduction records memset nodes), events on the launch stream
-    stream = torch.cuda.current_stream()
-    for _ in range(2):
-        a.sum(dtype=torch.float32)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(8):
-        a.sum(dtype=torch.float32)
-    e1.record(stream)
-    e1.synchronize()
-    read_gbs = a.numel() * 2 / (e0.elapsed_time(e1) / 8 * 1e-3) / 1e9
     del a, b
+    read_gbs = read_probe_gbs(torch)
     n = 8192
     x = torch.randn(n, n, device=dev).to(torch.bfloat16)
     y = torch.randn(n, n, device=dev).to(torch.bfloat16)
     z = torch.empty(n, n, dtype=torch.bfloat16, device=dev)
     ms = graph_time_ms(lambda: torch.matmul(x, y, out=z), 8, torch)
     tflops = 2 * n ** 3 / (ms * 1e-3) / 1e12
-    return dict(copy_gbs=copy_gbs, read_sum_gbs=read_gbs, stream_gbs=stream_same_bytes(torch, 1 << 30)["gbs"],
+    return dict(copy_gbs=copy_gbs, read_gbs=read_gbs, stream_gbs=stream_same_bytes(torch, 1 << 30)["gbs"],
                 matmul_bf16_tflops=tflops,
                 published=dict(hbm_gbs=HBM_PEAK_GBS, bf16_mfma_tflops=BF16_MFMA_PEAK_TFLOPS))
 
@@ -642,8 +658,35 @@ def stream_same_bytes(torch, nbytes: int, reps: int = 8) -> dict:
     return dict(us=ms * 1e3, gbs=4 * n / (ms * 1e-3) / 1e9)
 
 
-def cpu_baseline(torch, cfg, weights, inputs, budget_s: float = 20.0):
-    """Time the CPU oracle step on the host cores; bounded sample, scaled to ms per action step."""
+def step_parity(torch, cfg, w, inp, gpu_act, r16=None) -> dict:
+    """The action step's parity record, written into the bench line.  The bf16
+    bound of the operator configs (max-abs <= 2e-2, rel-L2 <= 1e-2) holds per
+    kernel and over 2 blocks; over the full 16 blocks x 4 iterations bf16
+    roundings compound in any evaluation order (the eager bf16 oracle itself
+    lands ~2.7e-2 max-abs from an fp32 evaluation), so the full step is judged
+    against an fp32 evaluation of the same weights and inputs: rel-L2 to it at
+    most 1.5x the bf16 oracle's, and cosine to the bf16 oracle >= 0.999."""
+    from oracle import msat_step_ref as R
+
+    def cmp(a, b):
+        d = a - b
+        return dict(max_abs=d.abs().max().item(), rel_l2=(d.norm() / b.norm()).item(),
+                    cos=torch.nn.functional.cosine_similarity(a.flatten(), b.flatten(), dim=0).item())
+
+    if r16 is None:
+        r16 = R.action_step(cfg, w, inp)
+    r32 = R.action_step(cfg, {k: v.float() for k, v in w.items()}, {k: v.float() for k, v in inp.items()})
+    out, r16, r32 = gpu_act.detach().cpu().double(), r16.double(), r32.double()
+    vs16, vs32, floor = cmp(out, r16), cmp(out, r32), cmp(r16, r32)
+    ok = vs32["rel_l2"] <= 1.5 * floor["rel_l2"] and vs16["cos"] >= 0.999
+    return dict(vs_bf16_oracle=vs16, vs_fp32=vs32, bf16_oracle_vs_fp32=floor, passed=bool(ok),
+                contract="full step: rel-L2 to the fp32 evaluation <= 1.5 x the bf16 oracle's, cos to the bf16 "
+                         "oracle >= 0.999 (max-abs 2e-2 is the per-kernel and 2-block bound)")
+
+
+def cpu_baseline(torch, cfg, weights, inputs, gpu_act=None, budget_s: float = 20.0):
+    """Time the CPU oracle step on the host cores; bounded sample, scaled to ms per action step.
+    With `gpu_act` (the GPU step's actions on the same inputs) also the step's parity record."""
     from oracle import msat_step_ref as R
 
     cores = os.cpu_count() or 1
@@ -657,12 +700,13 @@ def cpu_baseline(torch, cfg, weights, inputs, budget_s: float = 20.0):
     R.action_step(cfg, w, inp, steps=1, blocks=1)
     one = time.perf_counter() - t0
     per_step_est = one * cfg.blocks * cfg.steps
+    r16 = None
     if per_step_est <= budget_s / 2:
         reps = max(1, int(budget_s / 2 / max(per_step_est, 1e-3)))
         reps = min(reps, 5)
         t0 = time.perf_counter()
         for _ in range(reps):
-            R.action_step(cfg, w, inp)
+            r16 = R.action_step(cfg, w, inp)
         ms = (time.perf_counter() - t0) / reps * 1e3
         sample = f"{reps} full action step(s) ({cfg.blocks} blocks x {cfg.steps} iterations)"
     else:
@@ -673,9 +717,12 @@ def cpu_baseline(torch, cfg, weights, inputs, budget_s: float = 20.0):
         sample = f"1 iteration x {blocks} blocks, scaled x{cfg.blocks * cfg.steps / blocks:.1f} to a full step"
     from rldx_amd import workloads as W
 
-    return dict(value=ms, unit="ms per MSAT action step", cores=torch.get_num_threads(), kind="port",
-                sample=sample + " of the CPU oracle (torch bf16 eager restatement)",
-                inputs_sha256=W.sha256_of(*(inp[k] for k in sorted(inp))))
+    res = dict(value=ms, unit="ms per MSAT action step", cores=torch.get_num_threads(), kind="port",
+               sample=sample + " of the CPU oracle (torch bf16 eager restatement)",
+               inputs_sha256=W.sha256_of(*(inp[k] for k in sorted(inp))))
+    if gpu_act is not None:
+        res["step_parity"] = step_parity(torch, cfg, w, inp, gpu_act, r16)
+    return res
 
 
 def main():
@@ -736,8 +783,8 @@ def main():
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / args.steps
-    act = step.act.float()
-    assert torch.isfinite(act).all(), "non-finite actions"
+    act = step.act.clone()  # the replays' actions, for the parity record of the CPU leg
+    assert torch.isfinite(act.float()).all(), "non-finite actions"
     print(f"[bench] action step {ms:.3f} ms", file=sys.stderr, flush=True)
 
     gl = gemm_lines(torch, step)
@@ -749,20 +796,25 @@ def main():
     tf = ROOT / "profiles" / "gemm_w12_swiglu_traffic.json"
     if tf.exists():
         traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+    # traffic: L2-miss bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated on a copy):
+    # what the L2s fetch from / write to the memory side, served by the MALL or by HBM
     roofline = dict(kernel="gemm_kernel<SWIGLU_PACKED, LN fold>: W12 + SwiGLU grouped GEMM with the pre-LayerNorm "
                            "folded in, 3 streams (512/64/32 rows: 128x128 / 64x64 / 32x64 tiles) x [8192 x 1536] "
                            "weights" if step.ln_fold else
                     "gemm_kernel<SWIGLU_PACKED>: W12 + SwiGLU grouped GEMM, 3 streams "
                     "(512/64/32 rows: 128x128 / 64x64 / 32x64 tiles) x [8192 x 1536] weights",
                     bound="hbm", achieved=dom["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=dom["gbs"] / HBM_PEAK_GBS, traffic=traffic, algorithmic_bytes=dom["bytes"],
+                    frac=dom["gbs"] / HBM_PEAK_GBS, traffic=traffic,
+                    traffic_kind="L2-miss bytes per launch (MALL + HBM): rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                                 "scaled by a device copy of known size",
+                    algorithmic_bytes=dom["bytes"],
                     flops=dom["flops"], us=dom["us"])
 
     peaks = measured_peaks(torch)
     for v in kl.values():  # fractions against the measured peaks as well
         if isinstance(v, dict) and v.get("unit") == "GB/s":
             v["frac_of_measured_copy"] = v["achieved"] / peaks["copy_gbs"]
-            v["frac_of_measured_read"] = v["achieved"] / peaks["read_sum_gbs"]
+            v["frac_of_measured_read"] = v["achieved"] / peaks["read_gbs"]
             if "bytes" in v:  # and against a plain elementwise kernel moving the same bytes
                 ref = stream_same_bytes(torch, v["bytes"])
                 v["stream_same_bytes_us"] = ref["us"]
@@ -770,17 +822,18 @@ def main():
         elif isinstance(v, dict) and v.get("unit") == "TFLOP/s":
             v["frac_of_measured_matmul"] = v["achieved"] / peaks["matmul_bf16_tflops"]
         elif isinstance(v, dict) and "gbs" in v:  # the step GEMMs: weight streaming against the read rate
-            v["frac_of_measured_read"] = v["gbs"] / peaks["read_sum_gbs"]
-    roofline["frac_of_measured_read"] = dom["gbs"] / peaks["read_sum_gbs"]
-    print(f"[bench] measured peaks: copy {peaks['copy_gbs']:.0f} GB/s, read {peaks['read_sum_gbs']:.0f} GB/s, "
+            v["frac_of_measured_read"] = v["gbs"] / peaks["read_gbs"]
+    roofline["frac_of_measured_read"] = dom["gbs"] / peaks["read_gbs"]
+    print(f"[bench] measured peaks: copy {peaks['copy_gbs']:.0f} GB/s, read {peaks['read_gbs']:.0f} GB/s, "
           f"stream {peaks['stream_gbs']:.0f} GB/s, "
           f"bf16 matmul {peaks['matmul_bf16_tflops']:.0f} TFLOP/s", file=sys.stderr, flush=True)
 
     cpu = None
     host = None
     if not args.no_cpu:
-        cpu = cpu_baseline(torch, cfg, weights, inputs)
-        print(f"[bench] cpu baseline {cpu['value']:.1f} ms", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(torch, cfg, weights, inputs, gpu_act=act)
+        print(f"[bench] cpu baseline {cpu['value']:.1f} ms; step parity {cpu['step_parity']}", file=sys.stderr,
+              flush=True)
         for name, leg in cpu_kernel_baselines(torch).items():
             kl[name]["cpu"] = leg
             if "us" in kl[name]:

@@ -289,9 +289,15 @@ int64_t rldx_llm_fused_attention_workspace_bytes(int64_t seq, int64_t kv_heads, 
  * first call there, with that device current).  Calls whose
  * rldx_llm_fused_attention_workspace_bytes(seq, kv_heads, head_dim) exceeds it
  * return hipErrorInvalidValue with nothing enqueued.  Every call on a GPU shares
- * that GPU's array: calls that overlap in time on one GPU (other streams, other
- * threads) race and must be serialised by the caller.  Same results as
- * rldx_llm_fused_attention_bf16 (the same kernels).
+ * that GPU's array, so the library serialises them on the device: each call's
+ * stream first waits for an event recorded after the previous call on that GPU
+ * (whatever stream it used), and records it after its own launches; a mutex
+ * makes this atomic across host threads.  The event is created once per
+ * device, on the first call there, beside the address lookup.  A stream under
+ * hipGraph capture skips the event: replays of a captured call are ordered
+ * only by the stream they are launched on, so a caller that replays such a
+ * graph beside other calls on the same GPU must order them itself.  Same
+ * results as rldx_llm_fused_attention_bf16 (the same kernels).
  */
 hipError_t rldx_llm_fused_attention_noalloc_bf16(const void* qkv, int64_t qkv_row_stride, const void* q_norm_w,
                                                  const void* k_norm_w, const void* cos, const void* sin,
@@ -791,6 +797,20 @@ hipError_t rldx_rope_interleaved_f32(const float* xq, const int64_t* q_strides, 
                                      float* k_out, const int64_t* k_out_strides, int64_t batch, int64_t q_heads,
                                      int64_t k_heads, int64_t seq, int64_t head_dim, const float* freqs,
                                      const int64_t* freqs_strides, hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Measurement                                                              */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Reads `bytes` (a multiple of 16) of device memory at `data` (16-byte
+ * aligned) with 16-byte vector loads and discards them: the benchmark's
+ * measured read ceiling.  `sink` holds at least rldx_read_probe_sink_words()
+ * 32-bit words of device memory the kernel may write (it almost never does).
+ * No counterpart in the reference: a measurement helper of this library.
+ */
+int64_t rldx_read_probe_sink_words(void);
+hipError_t rldx_read_probe(const void* data, int64_t bytes, void* sink, int64_t sink_words, hipStream_t stream);
 
 #ifdef __cplusplus
 }

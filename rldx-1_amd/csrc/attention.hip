@@ -1286,29 +1286,45 @@ extern "C" hipError_t rldx_llm_fused_attention_bf16(const void* qkv, int64_t qkv
 // its own copy of the array (RLDX_LLM_ATTN_NOALLOC_MAX_BYTES) until the
 // process ends; host code reaches it only through the per-device address that
 // hipGetSymbolAddress returns (the array's name is a host-side stand-in).
+//
+// Calls on one GPU are serialised on the device: each call's stream waits for
+// the event recorded after the previous call's launches (on whatever stream
+// that was), and records it again after its own; a process-wide mutex makes
+// wait + launches + record one step, so host threads cannot interleave them.
+// A stream under hipGraph capture skips the event (the graph's replays are
+// ordered by the stream they are launched on).  The address and the event are
+// set up once per device, on the first call there.
 // ---------------------------------------------------------------------------
 namespace {
 static __device__ __align__(256) unsigned char scratch[RLDX_LLM_ATTN_NOALLOC_MAX_BYTES];
 
 constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mutex;
-void* g_scratch_ptr[kMaxDevices] = {};
+struct ScratchSlot {
+  void* ptr = nullptr;
+  hipEvent_t done = nullptr;  // recorded after the last call's launches on this device
+};
+std::mutex g_scratch_mutex;  // held for the whole of a call
+ScratchSlot g_scratch[kMaxDevices];
 
-// The scratch address on the current device, resolved on the first call there.
-hipError_t scratch_on_current_device(void** out) {
+// The current device's slot, set up on the first call there (caller holds the mutex).
+hipError_t scratch_on_current_device(ScratchSlot** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-  std::lock_guard<std::mutex> lock(g_scratch_mutex);
-  if (g_scratch_ptr[dev] == nullptr) {
+  ScratchSlot& s = g_scratch[dev];
+  if (s.ptr == nullptr) {
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return e;
     if (p == nullptr) return hipErrorInvalidSymbol;
-    g_scratch_ptr[dev] = p;
+    hipEvent_t ev = nullptr;
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) return e;
+    s.done = ev;
+    s.ptr = p;
   }
-  *out = g_scratch_ptr[dev];
+  *out = &s;
   return hipSuccess;
 }
 }  // namespace
@@ -1324,12 +1340,23 @@ extern "C" hipError_t rldx_llm_fused_attention_noalloc_bf16(const void* qkv, int
   if (seq == 0) return rldx_llm_fused_attention_bf16(qkv, qkv_row_stride, q_norm_w, k_norm_w, cos, sin,
                                                      cos_row_stride, sin_is_signed, out, out_row_stride, seq, q_heads,
                                                      kv_heads, head_dim, eps, nullptr, 0, stream);
-  void* ws = nullptr;
-  const hipError_t e = scratch_on_current_device(&ws);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  ScratchSlot* slot = nullptr;
+  hipError_t e = scratch_on_current_device(&slot);
   if (e != hipSuccess) return e;
-  return rldx_llm_fused_attention_bf16(qkv, qkv_row_stride, q_norm_w, k_norm_w, cos, sin, cos_row_stride,
-                                       sin_is_signed, out, out_row_stride, seq, q_heads, kv_heads, head_dim, eps, ws,
-                                       RLDX_LLM_ATTN_NOALLOC_MAX_BYTES, stream);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing(stream, &cap);
+  if (e != hipSuccess) return e;
+  const bool ordered = cap == hipStreamCaptureStatusNone;
+  if (ordered) {  // wait for the previous call on this device, whichever stream it used
+    e = hipStreamWaitEvent(stream, slot->done, 0);
+    if (e != hipSuccess) return e;
+  }
+  e = rldx_llm_fused_attention_bf16(qkv, qkv_row_stride, q_norm_w, k_norm_w, cos, sin, cos_row_stride, sin_is_signed,
+                                    out, out_row_stride, seq, q_heads, kv_heads, head_dim, eps, slot->ptr,
+                                    RLDX_LLM_ATTN_NOALLOC_MAX_BYTES, stream);
+  if (e != hipSuccess || !ordered) return e;
+  return hipEventRecord(slot->done, stream);
 }
 
 extern "C" int64_t rldx_vision_attention_workspace_bytes(int64_t total_tokens, int64_t num_seqs, int64_t num_heads,

@@ -58,6 +58,8 @@ class MsatStream(ctypes.Structure):
 
 # name -> (restype, argtypes); must stay in sync with include/rldx_amd.h
 SIGNATURES = {
+    "rldx_read_probe_sink_words": (c_i64, []),
+    "rldx_read_probe": (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp]),
     "rldx_swiglu_bf16": (c_i32, [c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp]),
     "rldx_grouped_swiglu_bf16": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp]),
     "rldx_qk_rmsnorm_rope_half_f32": (

@@ -678,6 +678,33 @@ def test_grouped_gemm_layernorm_fold(dev, epilogue, ms, n, k, wide, shift):
                         ln_stats=stats)
 
 
+@pytest.mark.parametrize("shift", [30.0, 100.0])
+def test_grouped_gemm_layernorm_fold_large_row_offsets(dev, shift):
+    """Rows whose mean is 30 or 100 standard deviations away from 0: the fold's
+    E[x^2] - mean^2 (fp32 over K = 1536) and rstd (x W^T - mean s) cancel
+    there.  Bound: the bf16 contract against LN(x) W^T + b with LN in fp64 on
+    the same bf16 rows, and against the eager path (LayerNorm-pack, then the
+    GEMM).  The bf16 rows themselves are coarse at that offset (one ulp at 100
+    is 0.5), which both references see too."""
+    g = torch.Generator().manual_seed(int(shift))
+    m, n, k = 64, 256, 1536
+    x = (_rand((m, k), g).float() + shift).to(BF16)
+    w = _rand((n, k), g, std=0.5 * k ** -0.5)
+    b = _rand((n,), g, 0.1)
+    pw = Fn.pack_weight(w.to(dev))
+    st = Fn.ln_stats_empty(m, k, dev)
+    fold = torch.empty(m, n, dtype=BF16, device=dev)
+    eager = torch.empty(m, n, dtype=BF16, device=dev)
+    Fn.grouped_gemm([(Fn.pack_act(x.to(dev), stats=st), pw, b.to(dev), fold, None)], "bias", ln_eps=1e-6,
+                    ln_stats=[st])
+    Fn.grouped_gemm([(Fn.layernorm_pack(x.to(dev), 1e-6), pw, b.to(dev), eager, None)], "bias")
+    torch.cuda.synchronize()
+    r = (_ln_ref(x) @ w.double().t() + b.double()).float().to(BF16)
+    s = assert_bf16_close(fold, r, f"LayerNorm fold, rows {shift} sigma off zero")
+    print(f"LayerNorm fold at {shift} sigma: {s}")
+    assert_bf16_close(fold, eager, f"LayerNorm fold vs LayerNorm-pack + GEMM, rows {shift} sigma off zero")
+
+
 def _slot_sums(x: torch.Tensor) -> torch.Tensor:
     """fp64 (sum, sum of squares) of every 64-column slot of every row, slot-major:
     [k / 64, m, 2]."""

@@ -40,9 +40,14 @@ def test_step_two_blocks_one_iteration(setup):
     assert_bf16_close(out, ref, "2-block step")
 
 
-def test_step_full_chunk(setup):
+@pytest.mark.parametrize("ln_fold", [True, False])
+def test_step_full_chunk(setup, ln_fold):
+    """Full depth with the pre-LayerNorm folded into the GEMMs (the default:
+    the fold skips the bf16 rounding of LN(x) that the eager chain does) and
+    with the eager LayerNorm-pack launches (ln_fold=False), each against the
+    fp32 referee."""
     cfg, w, inp, wc, ic = setup
-    step = MsatActionStep(cfg, w, inp)
+    step = MsatActionStep(cfg, w, inp, ln_fold=ln_fold)
     out = step.run().clone().cpu().double()
     torch.set_num_threads(max(1, min(16, torch.get_num_threads())))
     r16 = R.action_step(cfg, wc, ic).double()
@@ -54,8 +59,8 @@ def test_step_full_chunk(setup):
     floor, got = rel(r16, r32), rel(out, r32)
     s = stats(out, r16)
     cos = torch.nn.functional.cosine_similarity(out.flatten(), r16.flatten(), dim=0).item()
-    print(f"full action step: rel-L2 to fp32 {got:.3e} (bf16 oracle: {floor:.3e}); to the bf16 oracle "
-          f"max-abs {s['max_abs']:.3e}, rel-L2 {s['rel_l2']:.3e}, cos {cos:.6f}; "
+    print(f"full action step (ln_fold={ln_fold}): rel-L2 to fp32 {got:.3e} (bf16 oracle: {floor:.3e}); "
+          f"to the bf16 oracle max-abs {s['max_abs']:.3e}, rel-L2 {s['rel_l2']:.3e}, cos {cos:.6f}; "
           f"max-abs to fp32 {(out - r32).abs().max().item():.3e} (bf16 oracle: {(r16 - r32).abs().max().item():.3e})")
     assert torch.isfinite(out).all()
     assert got <= 1.5 * floor and cos >= 0.999, (got, floor, cos)

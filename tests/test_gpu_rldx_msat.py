@@ -7,7 +7,7 @@ import torch
 
 from oracle import rldx_msat_ref as R
 from rldx_amd import rldx_msat as RM
-from tolerances import assert_bf16_close
+from tolerances import BF16_REL_L2, assert_bf16_close, stats
 
 pytestmark = pytest.mark.gpu
 
@@ -18,21 +18,6 @@ def _oracle(sd, inp, cfg, quirk, mask=None):
                           heads=cfg.heads, head_dim=cfg.head_dim, ds_blocks=cfg.ds_blocks, ss_blocks=cfg.ss_blocks,
                           theta=cfg.rope_theta, max_seq_len=cfg.max_seq_len, bf16_quirk=quirk,
                           encoder_attention_mask=None if mask is None else mask.cpu())
-
-
-@pytest.mark.parametrize("quirk", [True, False])
-def test_rldx_msat_one_block_each(dev, quirk):
-    """Bound: the bf16 contract (max-abs 2e-2, rel-L2 1e-2), which presumes
-    unit-scale outputs: proj_out_2 is drawn with std 0.01 so that |y| stays
-    below 2 (with 0.02 the outputs reach 3, where one bf16 ulp is 0.0156 and
-    independently rounded sums differ by up to 0.023)."""
-    cfg = RM.RldxMsatCfg(ds_blocks=1, ss_blocks=1)
-    sd = RM.make_state_dict(cfg, dev, seed=21)
-    sd["proj_out_2.weight"] = (sd["proj_out_2.weight"].float() * 0.5).to(torch.bfloat16)
-    inp = RM.make_inputs(cfg, dev, seed=22)
-    chain = RM.RldxMsat(sd, cfg, dev, bf16_quirk=quirk)
-    o = chain.forward(inp["sa"], inp["vl"], inp["temb"], inp["time_token"]).clone()
-    assert_bf16_close(o, _oracle(sd, inp, cfg, quirk), f"RLDX MSAT 1 DS + 1 SS, quirk={quirk}")
 
 
 def _rel(a, b):
@@ -55,6 +40,24 @@ def assert_as_accurate_as_eager_bf16(o, sd, inp, cfg, quirk, what, mask=None):
     print(f"{what}: rel-L2 to fp32 {got:.2e} (eager bf16: {floor:.2e}), to the bf16 oracle {_rel(o, r16):.2e}, "
           f"cos {cos:.6f}")
     assert torch.isfinite(o).all() and got <= 1.5 * floor and cos >= 0.999, what
+
+
+@pytest.mark.parametrize("quirk", [True, False])
+def test_rldx_msat_one_block_each(dev, quirk):
+    """1 DS + 1 SS block on unscaled random weights (outputs reach |y| ~ 3,
+    where one bf16 ulp is 0.0156, so independently rounded sums differ by more
+    than the unit-scale max-abs bound of 2e-2).  Bounds: rel-L2 <= 1e-2 to the
+    bf16 oracle, and the fp32 referee (no further from an fp32 evaluation than
+    1.5x the eager bf16 oracle, cosine >= 0.999); max-abs is printed."""
+    cfg = RM.RldxMsatCfg(ds_blocks=1, ss_blocks=1)
+    sd = RM.make_state_dict(cfg, dev, seed=21)
+    inp = RM.make_inputs(cfg, dev, seed=22)
+    chain = RM.RldxMsat(sd, cfg, dev, bf16_quirk=quirk)
+    o = chain.forward(inp["sa"], inp["vl"], inp["temb"], inp["time_token"]).clone()
+    s = stats(o, _oracle(sd, inp, cfg, quirk))
+    print(f"RLDX MSAT 1 DS + 1 SS, quirk={quirk}: to the bf16 oracle {s}")
+    assert s["nonfinite_mismatch"] == 0 and s["rel_l2"] <= BF16_REL_L2, s
+    assert_as_accurate_as_eager_bf16(o, sd, inp, cfg, quirk, f"RLDX MSAT 1 DS + 1 SS, quirk={quirk}")
 
 
 def test_rldx_msat_full_model(dev):
