@@ -15,7 +15,11 @@ under the names the reference imports it by -- the fully qualified
 its first directory (`double_stream.engine...`, `llm.engine...`) -- so a chain
 imported afterwards binds the MI355X launchers, and the reference's Triton op
 registrations are never imported (the rldx_amd registrations take their
-names).  Call it before importing the reference's chains.
+names).  Parent packages that are not imported yet are registered as stub
+packages whose __path__ is the reference's directory (found without importing
+anything), so the reference's package __init__ files -- some of which import
+their Triton ops -- never run, while its other submodules stay importable.
+Call it before importing the reference's chains.
 
 Mirrored launchers (reference file: function):
   action_model/double_stream/engine/kernels/vl_epilogue_ln.py    fused_vl_epilogue_ln
@@ -41,7 +45,7 @@ which have no rldx_amd kernel.
 from __future__ import annotations
 
 import importlib
-import importlib.util
+import importlib.machinery
 import sys
 import types
 from pathlib import Path
@@ -76,39 +80,46 @@ def aliases(path: str) -> list:
 
 
 def _parent_packages(name: str) -> None:
-    """Make the parent packages of `name` importable: from the reference when it
-    is on sys.path (its own package modules, imported as usual), else as empty
-    package modules (so that `import double_stream.engine.ops` also works
-    without the reference installed)."""
+    """Make the parent packages of `name` importable without running any of the
+    reference's code: a package already in sys.modules is kept; any other is
+    registered as a stub package whose __path__ lists the reference's directory
+    for it when the reference is on sys.path (located with PathFinder, which
+    imports nothing), else an empty __path__ (so that `import
+    double_stream.engine.ops` also works without the reference installed).
+    The reference's package __init__ never runs: it may import the reference's
+    own Triton ops (e.g. memory/engine/__init__.py)."""
     parts = name.split(".")[:-1]
     for i in range(1, len(parts) + 1):
         pkg = ".".join(parts[:i])
         if pkg in sys.modules:
             continue
+        parent = sys.modules[".".join(parts[:i - 1])] if i > 1 else None
+        search = list(getattr(parent, "__path__", None) or []) if parent is not None else None
         try:
-            spec = importlib.util.find_spec(pkg)
+            spec = importlib.machinery.PathFinder.find_spec(pkg, search)
         except (ImportError, ValueError):
             spec = None
-        if spec is not None:
-            importlib.import_module(pkg)
-            continue
-        mod = types.ModuleType(pkg, "package of mirrored reference modules (the reference is not installed)")
-        mod.__path__ = []
+        locs = list(spec.submodule_search_locations or []) if spec is not None else []
+        mod = types.ModuleType(pkg, "stub package of mirrored reference modules (its __init__ is not run)")
+        mod.__path__ = locs
+        mod.__spec__ = importlib.machinery.ModuleSpec(pkg, None, is_package=True)
+        mod.__spec__.submodule_search_locations = locs
         sys.modules[pkg] = mod
         _added.append(pkg)
-        if i > 1:
-            setattr(sys.modules[".".join(parts[:i - 1])], parts[i - 1], mod)
+        if parent is not None:
+            setattr(parent, parts[i - 1], mod)
 
 
 _added: list = []  # sys.modules names install() registered or created
+_rebound: list = []  # (module, attribute, original value) install_model() replaced
 
 
 def install() -> dict:
-    """Register the mirrored modules under the reference's module names.
-    Returns {reference name: module}."""
+    """Register the mirrored modules under the reference's module names, before
+    any module of the reference is imported.  Returns {reference name: module}."""
     done = {}
-    for path in modules():
-        mod = importlib.import_module(_PKG + "." + path)
+    mirrors = [(path, importlib.import_module(_PKG + "." + path)) for path in modules()]  # ours only
+    for path, mod in mirrors:
         for name in aliases(path):
             if name not in done:
                 _parent_packages(name)
@@ -129,14 +140,27 @@ _MODEL = {
 }
 
 
+_MISSING = object()
+
+
+def _rebind(module, attr: str, value) -> None:
+    _rebound.append((module, attr, getattr(module, attr, _MISSING)))
+    setattr(module, attr, value)
+
+
 def install_model() -> dict:
     """Model-level drop-in: RMSNorm / create_norm_layer / create_qk_norm_layers
     (rldx/model/modules/norms.py), precompute_freqs_cis / apply_rotary_emb /
     SwiGLUFFN (action_model/ops.py), rotate_half / apply_rotary_pos_emb
     (backbone/modeling_qwen3_vl.py).  Where the reference module imports, its
-    attributes of those names are replaced (call this before the model is
-    built: its blocks bind the names at construction); where it does not, the
-    mirror is registered under its name.  Returns {reference name: module}."""
+    attributes of those names are replaced, and so is every binding of the
+    original objects in any loaded module (the reference's blocks.py binds
+    SwiGLUFFN, apply_rotary_emb, create_norm_layer and create_qk_norm_layers by
+    value with `from ... import`, blocks.py:10-16, and importing the norms
+    module first runs rldx/__init__.py, which imports the blocks); uninstall()
+    restores every original.  Models built before the call keep the layers they
+    were built with.  Where the reference does not import, the mirror is
+    registered under its name.  Returns {reference name: module}."""
     done = {}
     for ref_name, ours in _MODEL.items():
         mod = importlib.import_module(ours)
@@ -145,8 +169,15 @@ def install_model() -> dict:
         except ImportError:
             ref = None
         if ref is not None and ref is not mod:
+            originals = {attr: getattr(ref, attr) for attr in mod.__all__ if hasattr(ref, attr)}
             for attr in mod.__all__:
-                setattr(ref, attr, getattr(mod, attr))
+                _rebind(ref, attr, getattr(mod, attr))
+            for other in list(sys.modules.values()):  # by-value bindings elsewhere
+                if other is None or other is ref or other is mod:
+                    continue
+                for attr, orig in originals.items():
+                    if getattr(other, attr, None) is orig:
+                        _rebind(other, attr, getattr(mod, attr))
             done[ref_name] = ref
             continue
         _parent_packages(ref_name)
@@ -160,6 +191,13 @@ def install_model() -> dict:
 
 
 def uninstall() -> None:
-    """Remove what install() registered (the operators stay registered)."""
+    """Remove what install() / install_model() registered and restore every
+    attribute install_model() replaced (the operators stay registered)."""
+    while _rebound:
+        module, attr, orig = _rebound.pop()
+        if orig is _MISSING:
+            delattr(module, attr)
+        else:
+            setattr(module, attr, orig)
     while _added:
         sys.modules.pop(_added.pop(), None)

@@ -726,6 +726,13 @@ class MsatDispatcher:
       the static buffers);
     * a failure while building or running switches the dispatcher to the
       module's own forward for good, as the reference does.
+    Weights: the chain holds packed copies of msat.state_dict() taken when it
+    is built.  msat.load_state_dict() (wrapped by install) and refresh() drop
+    the chain, which is rebuilt from the new weights on the next call (that
+    call is served by the module's own forward); with check_weights=True every
+    call also compares each parameter's storage and version counter with the
+    ones the chain was built from (~0.1 ms of host time per call), which
+    catches in-place updates such as param.data.copy_().
     encoder_attention_mask and physics_attention_mask are served: the chain is
     built with vl_mask=True.  Physics tokens on a physics-enabled module are
     served by the all-add-ons chain (the first call's physics token count),
@@ -734,13 +741,34 @@ class MsatDispatcher:
     the next call."""
 
     def __init__(self, msat: torch.nn.Module, bf16_quirk: Optional[bool] = None, graph: bool = False,
-                 verbose: bool = False):
+                 verbose: bool = False, check_weights: bool = False):
         self.msat, self.orig = msat, msat.forward
         self.bf16_quirk, self.graph, self.verbose = bf16_quirk, graph, verbose
+        self.check_weights = check_weights
         self.chain: Optional[RldxMsat] = None
         self.failed = False
         self.served = 0      # calls run on the chain
         self.fallbacks = 0   # calls sent to the module's own forward
+        self.rebuilds = 0    # chains dropped because the weights changed
+        self._dims = None    # (n_vl, n_sa_pure, n_physics) of the chain
+        self._stamp = None   # [(tensor, data_ptr, _version)] the chain was built from
+
+    def _weights_stamp(self) -> list:
+        return [(t, t.data_ptr(), t._version) for t in self.msat.state_dict(keep_vars=True).values()]
+
+    def weights_changed(self) -> bool:
+        """True when a parameter or buffer was replaced or modified in place since the build."""
+        cur = self.msat.state_dict(keep_vars=True).values()
+        if self._stamp is None or len(self._stamp) != len(cur):
+            return True
+        return any(t is not u or t.data_ptr() != p or t._version != v for (t, p, v), u in zip(self._stamp, cur))
+
+    def refresh(self) -> None:
+        """Drop the chain; the next call rebuilds it from the module's current weights."""
+        if self.chain is not None:
+            self.rebuilds += 1
+        self.chain = None
+        self._stamp = None
 
     def _log(self, msg: str) -> None:
         if self.verbose:
@@ -762,6 +790,8 @@ class MsatDispatcher:
         if self.graph:
             chain.capture()
         self.chain = chain
+        self._dims = (n_vl, n_sa_pure, n_physics)
+        self._stamp = self._weights_stamp()
         return chain
 
     def _unserved(self, hidden_states, encoder_hidden_states, return_all_hidden_states, physics_embs,
@@ -792,6 +822,9 @@ class MsatDispatcher:
         if self.failed:
             self.fallbacks += 1
             return self.orig(*args)
+        if self.chain is not None and self.check_weights and self.weights_changed():
+            self._log("weights changed since the build: rebuilding the chain")
+            self.refresh()
         why = self._unserved(hidden_states, encoder_hidden_states, return_all_hidden_states, physics_embs,
                              physics_attention_mask)
         if why is not None:
@@ -844,7 +877,7 @@ class MsatDispatcher:
 
 def install(msat: torch.nn.Module, n_vl: Optional[int] = None, n_sa_pure: Optional[int] = None,
             bf16_quirk: Optional[bool] = None, graph: bool = False, verbose: bool = False,
-            n_physics: int = 0) -> MsatDispatcher:
+            n_physics: int = 0, check_weights: bool = False) -> MsatDispatcher:
     """Route a live MSAT module's forward through an MsatDispatcher (what the
     reference's path-D dispatcher does with CustomOpMSAT,
     rldx/inference/serve_optimization.py:251-601).  With n_vl and n_sa_pure the
@@ -854,12 +887,22 @@ def install(msat: torch.nn.Module, n_vl: Optional[int] = None, n_sa_pure: Option
     forward(hidden_states, encoder_hidden_states, timestep,
     return_all_hidden_states, encoder_attention_mask, physics_embs,
     physics_attention_mask) (msat.py:1058-1082).  bf16_quirk=None detects it
-    from the RoPE buffers (real-valued: the model was cast to bf16)."""
-    d = MsatDispatcher(msat, bf16_quirk=bf16_quirk, graph=graph, verbose=verbose)
+    from the RoPE buffers (real-valued: the model was cast to bf16).
+    msat.load_state_dict is wrapped so that new weights drop the chain (rebuilt
+    on the next call); check_weights=True also catches in-place updates."""
+    d = MsatDispatcher(msat, bf16_quirk=bf16_quirk, graph=graph, verbose=verbose, check_weights=check_weights)
     if n_vl is not None and n_sa_pure is not None:
         d.build(n_vl, n_sa_pure, n_physics)
     msat.forward = d
     msat.rldx_amd_dispatcher = d
+    load = msat.load_state_dict
+
+    def load_state_dict(*args, **kwargs):  # new weights: the chain is rebuilt on the next call
+        res = load(*args, **kwargs)
+        d.refresh()
+        return res
+
+    msat.load_state_dict = load_state_dict
     return d
 
 

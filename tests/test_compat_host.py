@@ -240,3 +240,83 @@ def test_precompute_freqs_cis_closed_form(model_installed):
     ang = n * 100.0 ** (-torch.arange(0, 8, 2, dtype=torch.float64) / 8)
     assert f.shape == (5, 4) and torch.allclose(f.abs(), torch.ones(5, 4, dtype=torch.float64), atol=1e-6)
     assert torch.allclose(f, torch.polar(torch.ones_like(ang), ang), atol=1e-5)
+
+
+def _write(root, rel, text):
+    p = root / rel
+    p.parent.mkdir(parents=True, exist_ok=True)
+    p.write_text(text)
+
+
+@pytest.fixture
+def fake_reference(tmp_path, monkeypatch):
+    """A reference tree on sys.path whose package __init__ files have side
+    effects: rldx/__init__.py imports the model blocks (as rldx/__init__.py:66
+    does), memory/engine/__init__.py imports its own ops module, which would
+    register mem:: operators again (custom_memory_chain.py:18,25), and every
+    executed module records itself in a list."""
+    log = "import sys as _s\n_s.modules['_ref_log'].append(__name__)\n"
+    _write(tmp_path, "rldx/__init__.py", log + "from .model.modules.action_model import blocks  # noqa\n")
+    _write(tmp_path, "rldx/inference/__init__.py", log)
+    _write(tmp_path, "rldx/inference/memory/__init__.py", log)
+    _write(tmp_path, "rldx/inference/memory/engine/__init__.py",
+           log + "import memory.engine.ops  # noqa\nraise RuntimeError('reference engine package ran')\n")
+    _write(tmp_path, "rldx/inference/memory/engine/extra.py", log + "VALUE = 7\n")
+    _write(tmp_path, "rldx/model/__init__.py", log)
+    _write(tmp_path, "rldx/model/modules/__init__.py", log)
+    _write(tmp_path, "rldx/model/modules/norms.py", log + "class RMSNorm: pass\n"
+           "def create_norm_layer(*a, **k): return 'ref'\ndef create_qk_norm_layers(*a, **k): return 'ref'\n")
+    _write(tmp_path, "rldx/model/modules/action_model/__init__.py", log)
+    _write(tmp_path, "rldx/model/modules/action_model/ops.py", log + "class SwiGLUFFN: pass\n"
+           "def apply_rotary_emb(*a): return 'ref'\ndef precompute_freqs_cis(*a, **k): return 'ref'\n")
+    _write(tmp_path, "rldx/model/modules/action_model/blocks.py", log +
+           "from .ops import SwiGLUFFN, apply_rotary_emb\nfrom ..norms import create_norm_layer, "
+           "create_qk_norm_layers\n")
+    monkeypatch.syspath_prepend(str(tmp_path))
+    ran = []
+    monkeypatch.setitem(sys.modules, "_ref_log", ran)
+    before = set(sys.modules)
+    yield ran
+    compat.uninstall()
+    for name in set(sys.modules) - before:
+        if name == "rldx" or name.startswith("rldx.") or name.startswith("memory"):
+            sys.modules.pop(name, None)
+
+
+def test_install_runs_no_reference_package_init(fake_reference):
+    """install() registers the mirrors without running any reference module:
+    the fake engine package's __init__ (which re-imports its ops and raises)
+    never runs, the mirrored ops module is ours under every alias, and a
+    non-mirrored reference submodule stays importable through the stub
+    package's __path__."""
+    import importlib
+
+    done = compat.install()
+    assert fake_reference == [], f"reference modules ran: {fake_reference}"
+    ours = done["memory.engine.ops"]
+    assert ours.__name__.startswith("rldx_amd.compat.")
+    assert sys.modules["rldx.inference.memory.engine.ops"] is ours
+    extra = importlib.import_module("rldx.inference.memory.engine.extra")
+    assert extra.VALUE == 7
+    assert fake_reference == ["rldx.inference.memory.engine.extra"]
+
+
+def test_install_model_rebinds_by_value_imports_and_restores(fake_reference):
+    """install_model() replaces the norm / ops names in the reference modules
+    and in every module that bound them by value (the fake blocks.py's
+    `from .ops import SwiGLUFFN, ...`), and uninstall() restores the originals."""
+    import importlib
+
+    compat.install_model()
+    blocks = importlib.import_module("rldx.model.modules.action_model.blocks")
+    ref_ops = sys.modules["rldx.model.modules.action_model.ops"]
+    from rldx_amd.compat.model.modules import norms as our_norms
+    from rldx_amd.compat.model.modules.action_model import ops as our_ops
+
+    assert blocks.SwiGLUFFN is our_ops.SwiGLUFFN and ref_ops.SwiGLUFFN is our_ops.SwiGLUFFN
+    assert blocks.apply_rotary_emb is our_ops.apply_rotary_emb
+    assert blocks.create_norm_layer is our_norms.create_norm_layer
+    assert blocks.create_qk_norm_layers is our_norms.create_qk_norm_layers
+    compat.uninstall()
+    assert blocks.SwiGLUFFN is ref_ops.SwiGLUFFN and blocks.SwiGLUFFN.__module__ == ref_ops.__name__
+    assert blocks.apply_rotary_emb() == "ref" and blocks.create_norm_layer() == "ref"
