@@ -257,19 +257,46 @@ __device__ __forceinline__ void qnorm_rope_shared(bf16x8 (&qreg)[D / 16], const 
   for (int ks = 0; ks < KS; ++ks) qreg[ks] = __builtin_bit_cast(bf16x8, qsh[ks * 64 + lane]);
 }
 
+// Non-negative integer quotient a / b of wave-uniform operands, b >= 1.  For
+// a < 2^22 a float estimate is within 1 of the quotient (v_rcp_f32 is within
+// 1 ulp, the product rounds once more), so one correction step each way makes
+// it exact; larger a take the integer division.  The work decode of the
+// attention kernel needs four of these: the integer divisions by run-time
+// values cost ~0.45 us per workgroup.
+__device__ __forceinline__ int div_small(int a, int b) {
+  if (a >= (1 << 22)) return a / b;
+  int q = static_cast<int>(static_cast<float>(a) * __builtin_amdgcn_rcpf(static_cast<float>(b)));
+  const int r = a - q * b;
+  if (r >= b) ++q;
+  else if (r < 0) --q;
+  return q;
+}
+
+// Wait until at most N of this wave's vector-memory loads are in flight, then
+// barrier.  Inline assembly: the compiler does not track the loads that write
+// LDS directly (buffer_load ... lds).
+template <int N>
+__device__ __forceinline__ void vm_wait_barrier() {
+  static_assert(N == 4 || N == 6 || N == 8, "vmcnt immediate: the V loads of the first tile");
+  if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 template <int D, int NSUB, bool kCausal, bool kBias, bool kQNorm, bool kVarlen = false>
 __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
-  static_assert(!kVarlen || (NSUB == 1 && !kCausal && !kBias && !kQNorm),
-                "variable-length mode: 32-query blocks, no mask, no fused Q normalisation");
+  static_assert(NSUB == 1, "32-query workgroups");
+  static_assert(!kVarlen || (!kCausal && !kBias && !kQNorm),
+                "variable-length mode: no mask, no fused Q normalisation");
   constexpr int NW = 4;           // waves per workgroup; each walks its own key tiles
   constexpr int BN = kTileKeys;   // keys per tile
-  constexpr int BMW = 32 * NSUB;  // queries per workgroup (shared by the 4 waves)
   constexpr int KSTEPS = D / 16;  // MFMA k-steps over head_dim for S^T
   constexpr int DBLK = D / 32;    // 32-row blocks of O^T
   constexpr int TILE_BYTES = 128 * D;
   constexpr int VPART = 64 * D;
-  constexpr int G4 = DBLK * 4 + 1;  // float4 groups per lane and sub-block in the merge: O + (m, l)
-  __shared__ floatx4 merge[NW * NSUB * G4 * 64];
+  constexpr int G4 = DBLK * 4 + 1;  // float4 groups per lane in the merge: O + (m, l)
+  __shared__ floatx4 merge[NW * G4 * 64];
+  __shared__ u32x4 qsh[KSTEPS * 64];  // the workgroup's Q operands, loaded once and read by every wave
   if (static_cast<int>(blockIdx.x) >= a.n_work) {  // warm-up workgroups (no barrier, no LDS)
     warm_lines(a.warm, static_cast<int>(blockIdx.x) - a.n_work, 256);
     return;
@@ -293,10 +320,11 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
     const int xcd = i % kXcds, k = i / kXcds;
     const int p = xcd < rem ? xcd * (per + 1) + k : rem * (per + 1) + (xcd - rem) * per + k;
     const int nqb = a.num_q_blocks;
-    const int qi = p % nqb;
+    const int ph = __builtin_amdgcn_readfirstlane(div_small(p, nqb));  // batch * hq + head
+    const int qi = p - ph * nqb;
     qb = kCausal ? nqb - 1 - qi : qi;  // causal: longest query blocks first on each XCD
-    h = (p / nqb) % a.hq;
-    b = p / (nqb * a.hq);
+    b = __builtin_amdgcn_readfirstlane(div_small(ph, a.hq));
+    h = ph - b * a.hq;
   }
   // Query / key range of the workgroup: the whole batch entry, or (kVarlen)
   // the sequence that owns 32-row slot qb; an unused slot exits here, before
@@ -312,29 +340,36 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
     row0 = ss.start;
     tile0 = ss.base;
   }
-  const int hk = h / a.group;
-  const int q_first = qb * BMW;
-  const int k_end = kCausal ? min(sk, min(sq, q_first + BMW)) : sk;
+  const int hk = __builtin_amdgcn_readfirstlane(div_small(h, a.group));
+  const int q_first = qb * 32;
+  const int q_idx = q_first + l32;  // this lane's query
+  const int k_end = kCausal ? min(sk, min(sq, q_first + 32)) : sk;
   const int ntiles = (k_end + BN - 1) / BN;  // >= 1: q_first < sq and sk >= 1
   const int head_tiles = (sk + BN - 1) / BN;
+  const int my_tiles = (ntiles - wave + NW - 1) / NW;  // tiles wave, wave + 4, ... (0 when ntiles <= wave)
 
-  // Every load below stays inside this head's (sequence's) packed tiles: tile
-  // indices are clamped to [0, ntiles), and ntiles <= head_tiles.
+  // Every K/V load below stays inside this head's (sequence's) packed tiles:
+  // tile indices are clamped to [0, ntiles), and ntiles <= head_tiles.
   const __amdgpu_buffer_rsrc_t kvr =
       make_rsrc(a.kv + b * a.kv_sb + hk * a.kv_sh + tile0 * kv_tile_elems(D), head_tiles * TILE_BYTES);
   const int voff = lane * 16;
+  auto tile_off = [&](int i) { return min(wave + NW * i, ntiles - 1) * TILE_BYTES; };  // the wave's i-th tile
   // Bias: lane reads the 16 keys of its accumulator rows (4 runs of 4 keys); a
   // dword past sk is out of the descriptor's range and reads as 0.
   __amdgpu_buffer_rsrc_t bsr;
   if constexpr (kBias) bsr = make_rsrc(a.key_bias + b * a.kb_sb, a.sk * 4);
-  // Per-wave bias flags: bit i of `wbias` is set when tile wave + 4 i (the
-  // wave's i-th tile) has a bias entry that is not +0 / -0 (a key-padding mask
-  // is zero almost everywhere).  Only flagged tiles load and add the bias; the
-  // scan covers a wave's first 2 * kScanLoads tiles, later tiles are always
-  // treated as flagged.  The scan loads are issued first, so the wait for Q
-  // and K (in-order load counter) covers them too, and no barrier is needed.
+
+  // ---- loads, in the order they are needed: K of the first tile, the bias
+  // scan, Q, V of the first tile ----
+  u32x4 kop[KSTEPS], vop[2 * DBLK];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) kop[ks] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + ks * 1024, tile_off(0), 0);
+  // Per-wave bias flags: bit i of `wbias` is set when the wave's i-th tile has
+  // a bias entry that is not +0 / -0 (a key-padding mask is zero almost
+  // everywhere).  Only flagged tiles load and add the bias; the scan covers a
+  // wave's first 2 * kScanLoads tiles, later tiles are always treated as
+  // flagged.
   constexpr int kScanLoads = 16;
-  const int my_tiles = (ntiles - wave + NW - 1) / NW;
   uint64_t wbias = 0;
   float bscan[kScanLoads];
   if constexpr (kBias) {
@@ -346,39 +381,41 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
             float, __builtin_amdgcn_raw_buffer_load_b32(bsr, ((wave + NW * (2 * r + g)) * BN + l32) * 4, 0, 0));
     }
   }
-
-  u32x4 kop[KSTEPS], vop[2 * DBLK];
-  {
-    const int t0 = min(wave, ntiles - 1);
-    const int s0 = t0 * TILE_BYTES;
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) kop[ks] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + ks * 1024, s0, 0);
-#pragma unroll
-    for (int c = 0; c < 2 * DBLK; ++c)
-      vop[c] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + VPART + c * 1024, s0, 0);
-  }
-
-  // ---- Q^T operands: sub-block j, lane holds query l32 and d-chunk (2*ks + g) ----
-  int q_idx[NSUB];
-  bf16x8 qreg[NSUB][KSTEPS];
-#pragma unroll
-  for (int j = 0; j < NSUB; ++j) {
-    q_idx[j] = q_first + 32 * j + l32;
-    const uint16_t* qrow =
-        a.q + b * a.q_sb + h * a.q_sh + (row0 + min(q_idx[j], sq - 1)) * a.q_ss + g * 8;
+  // Q^T operands: lane holds query l32, d-chunk (2 ks + g).  Without the fused
+  // norm the workgroup loads them once: wave w copies chunks w, w + 4, ...
+  // straight into LDS (buffer_load ... lds), then every wave reads all of them.
+  bf16x8 qreg[KSTEPS];
+  const uint16_t* qbase = a.q + b * a.q_sb + h * a.q_sh + row0 * a.q_ss;
+  if constexpr (kQNorm) {
+    const uint16_t* qrow = qbase + min(q_idx, sq - 1) * a.q_ss + g * 8;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks)
-      qreg[j][ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qrow + ks * 16));
-    if constexpr (kQNorm) {
-      static_assert(NSUB == 1, "the fused Q normalisation handles one 32-query sub-block");
-      __shared__ u32x4 qsh[KSTEPS * 64];
-      qnorm_rope_shared<D>(qreg[j], a, q_idx[j], q_idx[j] < sq, wave, qsh);
-    }
+      qreg[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qrow + ks * 16));
+  } else {
+    // byte extent of the head's rows and this lane's row offset: below 2^31 (checked by the launcher)
+    const __amdgpu_buffer_rsrc_t qr =
+        make_rsrc(qbase, static_cast<int>((static_cast<int64_t>(sq - 1) * a.q_ss + D) * 2));
+    const int qoff = static_cast<int>((static_cast<int64_t>(min(q_idx, sq - 1)) * a.q_ss + g * 8) * 2);
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks)
+      if (ks % NW == wave)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (__attribute__((address_space(3))) void*)(qsh + ks * 64), 16,
+                                                 qoff, ks * 32, 0, 0);
+  }
+#pragma unroll
+  for (int cc = 0; cc < 2 * DBLK; ++cc)
+    vop[cc] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + VPART + cc * 1024, tile_off(0), 0);
+  if constexpr (kQNorm) {
+    qnorm_rope_shared<D>(qreg, a, q_idx, q_idx < sq, wave, qsh);
+  } else {
+    vm_wait_barrier<2 * DBLK>();  // this wave's Q chunks are in LDS (only V still in flight); every wave's after the barrier
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) qreg[ks] = __builtin_bit_cast(bf16x8, qsh[ks * 64 + lane]);
   }
 
-  // bias flags (NaN != 0 is true: a NaN bias is applied, not skipped), and the
-  // bias of the wave's first tile when it is flagged
-  floatx4 bnext[4] = {};
+  // bias flags (NaN != 0 is true: a NaN bias is applied, not skipped)
+  auto flagged = [&](int i) { return i >= 64 || ((wbias >> i) & 1ull); };
+  auto load_bias_of = [&](floatx4 (&dst)[4], int i) { load_bias(dst, bsr, (wave + NW * i) * BN + 4 * g); };
   if constexpr (kBias) {
 #pragma unroll
     for (int r = 0; r < kScanLoads; ++r) {
@@ -387,145 +424,157 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
       if (bal >> 32) wbias |= 1ull << (2 * r + 1);
     }
     if (my_tiles > 2 * kScanLoads) wbias |= ~0ull << (2 * kScanLoads);
-    if ((wbias & 1ull) && my_tiles > 0) load_bias(bnext, bsr, wave * BN + 4 * g);
   }
 
-  floatx16 oacc[NSUB][DBLK];
-  float m_ref[NSUB], l_part[NSUB];
+  floatx16 oacc[DBLK];
 #pragma unroll
-  for (int j = 0; j < NSUB; ++j) {
-#pragma unroll
-    for (int db = 0; db < DBLK; ++db) oacc[j][db] = floatx16{};
-    m_ref[j] = -__builtin_inff();  // reference max (log2 units) used for exp
-    l_part[j] = 0.f;               // this lane's share of the row sum
-  }
+  for (int db = 0; db < DBLK; ++db) oacc[db] = floatx16{};
+  float m_ref = -__builtin_inff();  // reference max (log2 units) used for exp
+  float l_part = 0.f;               // this lane's share of the row sum
   const float c = a.scale_log2;
+  const float kb = kLog2e / c;  // a natural-log bias in raw-score units (the score is scaled by c later)
 
-  for (int t = wave, ti = 0; t < ntiles; t += NW, ++ti) {
-    const int k0 = t * BN;
-    const int sn = min(t + NW, ntiles - 1) * TILE_BYTES;  // next tile of this wave (clamped)
-
-    // ---- S^T = K Q^T, one independent MFMA chain per sub-block ----
-    floatx16 sacc[NSUB];
-    bool active[NSUB];
+  // ---- softmax helpers (log2 domain; lane = one query, 16 of the tile's keys) ----
+  // Masking of the wave's i-th tile on its raw scores: keys past sk, the causal
+  // future and -inf biases become -inf, other biases are added (flagged tiles).
+  floatx4 bn[4] = {};  // the bias of the next flagged tile, loaded one tile ahead
+  auto mask_tile = [&](floatx16& s, int i) {
+    const int k0 = (wave + NW * i) * BN;
+    const bool btile = kBias && flagged(i);
+    if ((k0 + BN > sk) || (kCausal && k0 + BN - 1 > q_first) || btile) {
 #pragma unroll
-    for (int j = 0; j < NSUB; ++j) {
-      active[j] = !(kCausal && k0 > q_first + 32 * j + 31);  // whole tile in this sub-block's future
-      sacc[j] = floatx16{};
-      if (active[j]) {
+      for (int e = 0; e < 16; ++e) {
+        const int key = k0 + 8 * (e >> 2) + 4 * g + (e & 3);
+        float sv = s[e];
+        if constexpr (kBias) {
+          if (btile) sv += bn[e >> 2][e & 3] * kb;
+        }
+        bool ok = key < sk;
+        if constexpr (kCausal) ok = ok && (key <= q_idx);
+        s[e] = ok ? sv : -__builtin_inff();
+      }
+    }
+  };
+  // Lazy rescale: the reference max moves only when a tile max exceeds it by
+  // more than 2^8 (softmax is shift-invariant).  Both lanes of a query see the
+  // same pair maximum, so they keep the same reference.
+  auto update_max = [&](const floatx16& s) {
+    float mt = s[0];
+#pragma unroll
+    for (int e = 1; e < 16; ++e) mt = fmaxf(mt, s[e]);
+    mt *= c;
+    if (__any(mt > m_ref + kLazyThreshold)) {
+      const float mq = pair_max(mt);
+      const float new_ref = mq > m_ref + kLazyThreshold ? mq : m_ref;
+      const float alpha = (m_ref == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(m_ref - new_ref);
+      m_ref = new_ref;
+      l_part *= alpha;
+#pragma unroll
+      for (int db = 0; db < DBLK; ++db) oacc[db] *= alpha;
+    }
+  };
+  // P = exp2(s c - m) packed to bf16, its row sum; meanwhile the S^T MFMAs of
+  // a later tile (K operands `kk`) are issued between the exponentials, so the
+  // matrix pipe works during the softmax.
+  bf16x8 pop[2];
+  auto exp_pack_and_score = [&](floatx16& s, floatx16& snew) {
+    const float nm = (m_ref == -__builtin_inff()) ? 0.f : -m_ref;
+    float psum = 0.f;
+    snew = floatx16{};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], c, nm));
+      s[e] = pe;
+      psum += pe;
+#pragma unroll
+      for (int ks = e * KSTEPS / 16; ks < (e + 1) * KSTEPS / 16; ++ks)  // KSTEPS MFMAs spread over the 16 exps
+        snew = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kop[ks]), qreg[ks], snew, 0, 0, 0);
+    }
+    l_part += psum;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      floatx8 pv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pv[e] = s[s2 * 8 + e];
+      pop[s2] = __builtin_convertvector(pv, bf16x8);
+    }
+  };
+  auto pv_mma = [&]() {  // O^T += V^T P^T, two 16-key steps
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int db = 0; db < DBLK; ++db)
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vop[db * 2 + s2]), pop[s2],
+                                                           oacc[db], 0, 0, 0);
+  };
+
+  // ---- main loop, software-pipelined over the wave's tiles t_i = wave + 4 i.
+  // Per iteration i: P(t_i) V(t_i) on the matrix pipe while the VALU masks and
+  // takes the max of S(t_i+1); then the exponentials of S(t_i+1) with the
+  // S(t_i+2) MFMAs issued between them.  K operands are loaded once their
+  // tile's S MFMAs are issued, V operands once their P.V MFMAs are. ----
+  if (my_tiles > 0) {
+    floatx16 sa, sb;
+    sa = floatx16{};
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks)
+      sa = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kop[ks]), qreg[ks], sa, 0, 0, 0);
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) kop[ks] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + ks * 1024, tile_off(1), 0);
+    if constexpr (kBias) {
+      if (flagged(0)) load_bias_of(bn, 0);
+    }
+    mask_tile(sa, 0);
+    if constexpr (kBias) {
+      if (my_tiles > 1 && flagged(1)) load_bias_of(bn, 1);
+    }
+    update_max(sa);
+    exp_pack_and_score(sa, sb);  // P(t_0); S(t_1)
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) kop[ks] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + ks * 1024, tile_off(2), 0);
+    // iteration i: pop = P(t_i), vop = V(t_i), s_next = S(t_i+1), kop = K(t_i+2)
+    auto body = [&](int i, floatx16& s_next, floatx16& s_out) {
+      pv_mma();
+#pragma unroll
+      for (int cc = 0; cc < 2 * DBLK; ++cc)
+        vop[cc] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + VPART + cc * 1024, tile_off(i + 1), 0);
+      if (i + 1 < my_tiles) {
+        mask_tile(s_next, i + 1);
+        if constexpr (kBias) {
+          if (i + 2 < my_tiles && flagged(i + 2)) load_bias_of(bn, i + 2);
+        }
+        update_max(s_next);
+        exp_pack_and_score(s_next, s_out);  // P(t_i+1); S(t_i+2)
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks)
-          sacc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kop[ks]), qreg[j][ks],
-                                                            sacc[j], 0, 0, 0);
+          kop[ks] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + ks * 1024, tile_off(i + 3), 0);
       }
+    };
+    for (int i = 0; i < my_tiles; i += 2) {
+      body(i, sb, sa);
+      if (i + 1 >= my_tiles) break;
+      body(i + 1, sa, sb);
     }
-    // ---- next tile's K operands, in flight during the softmax and P.V below ----
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) kop[ks] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + ks * 1024, sn, 0);
-    floatx4 bq[4] = {};
-    bool bias_tile = false;
-    if constexpr (kBias) {
-      bias_tile = ti >= 64 || ((wbias >> ti) & 1ull);
-      if (bias_tile) {
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) bq[qq] = bnext[qq];
-      }
-      // the next flagged tile's bias, in flight during this tile's softmax and P.V
-      if (ti + 1 < my_tiles && (ti + 1 >= 64 || ((wbias >> (ti + 1)) & 1ull))) load_bias(bnext, bsr, sn / TILE_BYTES * BN + 4 * g);
-    }
-
-#pragma unroll
-    for (int j = 0; j < NSUB; ++j) {
-      if (!active[j]) continue;
-      const int qf = q_first + 32 * j;  // first query of this sub-block
-      // ---- softmax (log2 domain, lane = one query, 16 of the tile's keys) ----
-      const bool edge = (k0 + BN > sk) || (kCausal && k0 + BN - 1 > qf) || bias_tile;
-      float mt = -__builtin_inff();
-      if (!edge) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) mt = fmaxf(mt, sacc[j][e]);
-        mt *= c;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = k0 + 8 * (e >> 2) + 4 * g + (e & 3);
-          float sv = sacc[j][e] * c;
-          if constexpr (kBias) sv += bq[e >> 2][e & 3] * kLog2e;
-          bool ok = key < sk;
-          if constexpr (kCausal) ok = ok && (key <= q_idx[j]);
-          sv = ok ? sv : -__builtin_inff();
-          sacc[j][e] = sv;
-          mt = fmaxf(mt, sv);
-        }
-      }
-      if (__any(mt > m_ref[j] + kLazyThreshold)) {
-        // both lanes of a query see the same pair maximum, so they keep the same reference
-        const float mq = pair_max(mt);
-        const float new_ref = mq > m_ref[j] + kLazyThreshold ? mq : m_ref[j];
-        const float alpha = (m_ref[j] == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(m_ref[j] - new_ref);
-        m_ref[j] = new_ref;
-        l_part[j] *= alpha;
-#pragma unroll
-        for (int db = 0; db < DBLK; ++db) oacc[j][db] *= alpha;
-      }
-      const float m_use = (m_ref[j] == -__builtin_inff()) ? 0.f : m_ref[j];
-      float psum = 0.f;
-      if (!edge) {
-        const float nm = -m_use;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][e], c, nm));
-          sacc[j][e] = pe;
-          psum += pe;
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float pe = __builtin_amdgcn_exp2f(sacc[j][e] - m_use);
-          sacc[j][e] = pe;
-          psum += pe;
-        }
-      }
-      l_part[j] += psum;
-      // ---- O^T += V^T P^T, two 16-key steps ----
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        floatx8 pv;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pv[e] = sacc[j][s2 * 8 + e];
-        const bf16x8 pop = __builtin_convertvector(pv, bf16x8);
-#pragma unroll
-        for (int db = 0; db < DBLK; ++db)
-          oacc[j][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vop[db * 2 + s2]), pop,
-                                                                oacc[j][db], 0, 0, 0);
-      }
-    }
-    // ---- next tile's V operands ----
-#pragma unroll
-    for (int cc = 0; cc < 2 * DBLK; ++cc)
-      vop[cc] = __builtin_amdgcn_raw_buffer_load_b128(kvr, voff + VPART + cc * 1024, sn, 0);
   }
 
   // ---- merge the 4 waves' partial states; wave w finalises d-blocks w, w+4, ... ----
-  // LDS layout: [wave][sub-block][float4 group][lane] -> 16-byte, conflict-free accesses.
-#pragma unroll
-  for (int j = 0; j < NSUB; ++j) {
-    floatx4* mine = merge + (wave * NSUB + j) * (G4 * 64);
+  // LDS layout: [wave][float4 group][lane] -> 16-byte, conflict-free accesses.
+  {
+    floatx4* mine = merge + wave * (G4 * 64);
 #pragma unroll
     for (int db = 0; db < DBLK; ++db)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4)
         mine[(db * 4 + q4) * 64 + lane] =
-            floatx4{oacc[j][db][q4 * 4], oacc[j][db][q4 * 4 + 1], oacc[j][db][q4 * 4 + 2], oacc[j][db][q4 * 4 + 3]};
-    mine[(DBLK * 4) * 64 + lane] = floatx4{m_ref[j], l_part[j], 0.f, 0.f};
+            floatx4{oacc[db][q4 * 4], oacc[db][q4 * 4 + 1], oacc[db][q4 * 4 + 2], oacc[db][q4 * 4 + 3]};
+    mine[(DBLK * 4) * 64 + lane] = floatx4{m_ref, l_part, 0.f, 0.f};
   }
   __syncthreads();
-#pragma unroll
-  for (int j = 0; j < NSUB; ++j) {
+  {
     // every LDS read of this lane is issued before the arithmetic that uses it
     floatx4 ml[NW];
 #pragma unroll
-    for (int w = 0; w < NW; ++w) ml[w] = merge[(w * NSUB + j) * (G4 * 64) + (DBLK * 4) * 64 + lane];
+    for (int w = 0; w < NW; ++w) ml[w] = merge[w * (G4 * 64) + (DBLK * 4) * 64 + lane];
     constexpr int DPW = (DBLK + NW - 1) / NW;  // d-blocks finalised per wave
     floatx4 part[DPW][4][NW];
 #pragma unroll
@@ -535,7 +584,7 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4)
 #pragma unroll
-          for (int w = 0; w < NW; ++w) part[r][q4][w] = merge[(w * NSUB + j) * (G4 * 64) + (db * 4 + q4) * 64 + lane];
+          for (int w = 0; w < NW; ++w) part[r][q4][w] = merge[w * (G4 * 64) + (db * 4 + q4) * 64 + lane];
       }
     }
     float wgt[NW];
@@ -550,8 +599,8 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
     }
     l = pair_sum(l);
     const float inv = l > 0.f ? 1.0f / l : 0.f;
-    if (q_idx[j] < sq) {
-      uint16_t* orow = a.o + b * a.o_sb + h * a.o_sh + (row0 + q_idx[j]) * a.o_ss;
+    if (q_idx < sq) {
+      uint16_t* orow = a.o + b * a.o_sb + h * a.o_sh + (row0 + q_idx) * a.o_ss;
 #pragma unroll
       for (int r = 0; r < DPW; ++r) {
         const int db = wave + r * NW;
@@ -568,7 +617,7 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
           wv.x = pack_bf16x2(acc[0], acc[1]);
           wv.y = pack_bf16x2(acc[2], acc[3]);
           if (a.o_packed_k > 0)  // 4 consecutive columns stay inside one 8-element run
-            *reinterpret_cast<uint2*>(a.o + packed_act_offset(q_idx[j], static_cast<int64_t>(h) * D + d, a.o_packed_k)) = wv;
+            *reinterpret_cast<uint2*>(a.o + packed_act_offset(q_idx, static_cast<int64_t>(h) * D + d, a.o_packed_k)) = wv;
           else
             *reinterpret_cast<uint2*>(orow + d) = wv;
         }
@@ -1075,9 +1124,9 @@ hipError_t check_qo(const void* q, void* o, int64_t batch, int64_t q_heads, int6
   if (!a16(q) || reinterpret_cast<uintptr_t>(o) % 8) return hipErrorInvalidValue;
   for (int i = 0; i < 3; ++i)
     if (q_strides[i] % 8 || o_strides[i] % 4) return hipErrorInvalidValue;
-  // per-head packed tiles are addressed with 32-bit byte offsets
+  // per-head packed tiles and per-head query rows are addressed with 32-bit byte offsets
   if (seq_q > (1 << 24) || tiles_of(seq_k) * 128 * head_dim > (int64_t{1} << 31) - 1 || q_heads > 65535 ||
-      batch > 65535)
+      batch > 65535 || ((seq_q - 1) * q_strides[2] + head_dim) * 2 > (int64_t{1} << 31) - 1)
     return hipErrorInvalidValue;
   if (((seq_q + 31) / 32) * q_heads * batch > (int64_t{1} << 31) - 1) return hipErrorInvalidValue;  // 1-D grid
   return hipSuccess;
@@ -1382,6 +1431,7 @@ extern "C" hipError_t rldx_vision_attention_bf16(const void* qkv, const float* r
       reinterpret_cast<uintptr_t>(cu_seqlens) % 4)
     return hipErrorInvalidValue;
   if (total_tokens > (1 << 24) || num_seqs > (1 << 24) || num_heads > 65535) return hipErrorInvalidValue;
+  if (total_tokens * dp * 2 > (int64_t{1} << 31) - 1) return hipErrorInvalidValue;  // 32-bit row offsets of Q
   const int64_t slots = seq_slot_count(total_tokens, num_seqs);
   // 1-D attention grid, 32-bit byte offsets inside a head's packed tiles
   if (slots * num_heads > (int64_t{1} << 31) - 1 || slots * kv_tile_elems(dp) * 2 > (int64_t{1} << 31) - 1)
