@@ -223,6 +223,11 @@ def test_gqa_prefill_workload(dev):
     # large grids (several workgroups per CU)
     (4, 32, 8, 512, 512, 128, True, False),
     (4, 32, 32, 520, 520, 64, False, True),
+    # GQA at prefill sizes: 7 query heads per KV head at head_dim 64, 8 per KV head
+    # non-causal over two batch entries, 4 per KV head with a ragged end
+    (1, 28, 4, 1024, 1024, 64, True, False),
+    (2, 16, 2, 1024, 1024, 128, False, False),
+    (1, 32, 8, 1000, 1000, 128, True, False),
 ])
 def test_attention_shapes(dev, B, Hq, Hkv, Sq, Sk, D, causal, masked):
     g = torch.Generator().manual_seed(B * 100 + Sq + Sk + D)
@@ -304,11 +309,11 @@ def test_backbone_fused_attention_op(dev):
 
 
 @pytest.mark.parametrize("M,Hq,Hkv,D", [(100, 4, 2, 64), (333, 14, 2, 128), (257, 16, 2, 64), (169, 32, 8, 128),
-                                        (70, 12, 2, 128), (150, 10, 2, 128), (1, 8, 2, 128)])
+                                        (70, 12, 2, 128), (150, 10, 2, 128), (1, 8, 2, 128),
+                                        (1100, 28, 4, 64), (2048, 16, 2, 128), (1055, 32, 8, 128)])
 def test_backbone_fused_attention_op_shapes(dev, M, Hq, Hkv, D):
-    """Groups of 2 (one workgroup per query head) and of 4-8 query heads per KV
-    head (the heads of a group sharing K/V tiles; causal rows split over
-    workgroups from 3 query blocks on), ragged sequence ends, one token."""
+    """Groups of 2 to 8 query heads per KV head, from one token to prefill sizes
+    (1055 - 2048 tokens), ragged sequence ends, head_dim 64 and 128."""
     import rldx_amd.ops  # noqa: F401
 
     cfg = W.GqaCfg(q_heads=Hq, kv_heads=Hkv, head_dim=D, seq=M, seed=M)
