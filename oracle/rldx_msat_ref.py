@@ -19,6 +19,15 @@ The time embedding `temb` and the time token are inputs, as in the reference's
 inference chain (custom_msat_chain.py:109-126), which bakes them per step.
 With identity modulation, (1 + 0) * y + 0 and 1 * y reproduce y exactly in
 bf16, so the modulation products are not spelled out.
+
+`action_head` composes the MSAT with the action head around it
+(CustomActionHeadChain.forward, custom_action_model_chain.py:81-171): vlln,
+the state / action encoders, the RTC trained-mode prefix, the decoder and the
+Euler update.  Its pins (tests/test_rldx_msat_host.py): the Euler update in
+closed form (a decoder with zero weights moves every free row by exactly its
+bias, the prefix rows not at all), the prefix path against the unsliced
+re-lock composition (encode every row with per-row time, decode every row,
+re-lock the prefix after each step), and vlln against LayerNorm written out.
 """
 
 from __future__ import annotations
@@ -266,3 +275,68 @@ def msat_forward_physics(sd: dict, sa_embs, vl_embs, p_embs, temb, time_token, *
     action = _adaln_out(x[:, -n_pure:], temb, sd, "proj_out_1", "proj_out_2")
     physics = _adaln_out(ph, temb, sd, "proj_out_physics_1", "proj_out_physics_2")
     return action, physics
+
+
+# ---------------------------------------------------------------------------
+# The action head around the MSAT, CustomActionHeadChain.forward
+# (rldx/inference/action_model/engine/custom_action_model_chain.py:81-171), batch
+# 1, no physics: vlln, state encoder, the RTC trained-mode prefix, and per
+# denoising step action encoder + position embedding, MSAT, action decoder and
+# the Euler update.  Per-embodiment MLPs as CategorySpecificLinear
+# (rldx/model/modules/action_model/embodiment_conditioned_mlp.py): x W[e] + b[e].
+# ---------------------------------------------------------------------------
+def sinusoidal_time(t: float, rows: int, width: int, dtype) -> torch.Tensor:
+    """SinusoidalPositionalEncoding of a per-token time (embodiment_conditioned_mlp.py:14-33),
+    fp32, for `rows` tokens at time t, cast to the model dtype."""
+    half = width // 2
+    ex = torch.exp(-torch.arange(half, dtype=torch.float) * (torch.log(torch.tensor(10000.0)) / half))
+    fr = torch.full((rows, 1), float(t)) * ex
+    return torch.cat([torch.sin(fr), torch.cos(fr)], dim=-1).to(dtype)
+
+
+def action_head(head_sd: dict, msat_sd: dict, vl, state, x0, *, steps: int, heads: int, head_dim: int,
+                ds_blocks: int, ss_blocks: int, e: int = 0, prefix=None, use_vlln: bool = False,
+                vlln_eps: float = 1e-5, dtype=torch.float32):
+    """Actions [horizon, action_dim] of one inference, evaluated in `dtype` (fp32, or bf16
+    eager with a rounding after every op).  vl [1, n_vl, vl_dim], state [1, 1, state_dim],
+    x0 [1, horizon, action_dim]; prefix [1, d, action_dim] or None (RTC trained mode:
+    rows < d are the prefix for the whole call, encoded once at time 1 (:98-121); each
+    step encodes rows >= d at the step's time, decodes only the last horizon - d
+    outputs and advances only those rows (:131-170)); use_vlln: affine LayerNorm of
+    the VL embeddings (head_sd vlln.weight / vlln.bias) first (:84)."""
+    f = {k: v.cpu().to(dtype) for k, v in head_sd.items()}
+    sd = {k: v.cpu().to(dtype) for k, v in msat_sd.items()}
+
+    def lin(x, name):
+        return torch.addmm(f[f"{name}.b"][e], x, f[f"{name}.W"][e])
+
+    def encode(x, tau):  # MultiEmbodimentActionEncoder: W3(swish(W2([W1 x | tau])))
+        h = lin(torch.cat([lin(x, "action_encoder.W1"), tau], dim=-1), "action_encoder.W2")
+        return lin(h * torch.sigmoid(h), "action_encoder.W3")
+
+    vl = vl.cpu().to(dtype)
+    if use_vlln:
+        vl = F.layer_norm(vl, (vl.shape[-1],), f["vlln.weight"], f["vlln.bias"], vlln_eps)
+    horizon, width = x0.shape[1], f["position_embedding.weight"].shape[1]
+    pos = f["position_embedding.weight"]
+    d = 0 if prefix is None else prefix.shape[1]
+    state_feat = lin(torch.relu(lin(state.cpu().to(dtype)[0], "state_encoder.layer1")), "state_encoder.layer2")
+    act = x0.cpu().to(dtype)[0].clone()
+    if d > 0:
+        act[:d] = prefix.cpu().to(dtype)[0]
+        prefix_feat = encode(act[:d], sinusoidal_time(1.0, d, width, dtype)) + pos[:d]
+    for i in range(steps):
+        # the schedule i / steps is a bf16 buffer (graph_safe_action_model.py:147-153)
+        t = float(torch.tensor(i / float(steps), dtype=torch.bfloat16))
+        tau = sinusoidal_time(t, horizon, width, dtype)
+        post = encode(act[d:], tau[d:]) + pos[d:]
+        feat = torch.cat([prefix_feat, post]) if d > 0 else post
+        sa = torch.cat([state_feat, feat])[None]
+        out = msat_forward(sd, sa, vl, f["static_tembs"][i], f["static_time_tokens"][i], heads=heads,
+                           head_dim=head_dim, ds_blocks=ds_blocks, ss_blocks=ss_blocks)[0]
+        if d > 0:
+            v = lin(torch.relu(lin(out[-(horizon - d):], "action_decoder.layer1")), "action_decoder.layer2")
+        else:
+            v = lin(torch.relu(lin(out, "action_decoder.layer1")), "action_decoder.layer2")[-horizon:]
+        act[d:] = act[d:] + v * (1.0 / steps)
+    return act

@@ -35,6 +35,9 @@ Mirrored launchers (reference file: function):
   memory/engine/kernels/fused_memory_attention.py                forward, prepare_signed_sin, prepare_rope_buffers,
                                                                  prepare_fused_qkv_weight
   memory/engine/kernels/fused_add2_rmsnorm.py                    forward
+  action_model/engine/custom_action_model_chain.py               CustomActionHeadChain, build_/compile_custom_action_model_chain
+  action_model/engine/custom_expanded_action_model_chain.py      CustomExpandedActionHeadChain,
+                                                                 build_/compile_custom_expanded_action_model_chain
 and the op registration modules (engine/ops/__init__.py and op_*.py) of the
 same directories.  Not mirrored: the Triton kernel objects the reference's
 op modules launch directly (rmsnorm_rope_kernel*, the dormant

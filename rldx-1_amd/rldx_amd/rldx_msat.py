@@ -709,6 +709,24 @@ class RldxMsat:
         return {"action": self.out, "physics": self.out_p} if self.phys else self.out
 
 
+def chain_for_module(msat: torch.nn.Module, n_vl: int, n_sa_pure: int, n_physics: int = 0,
+                     bf16_quirk: Optional[bool] = None, vl_mask: bool = False) -> RldxMsat:
+    """An RldxMsat chain from a live MSAT module's state_dict() for these token
+    counts: dimensions read off the parameter shapes, RoPE theta / table length
+    off its rope_embedder; bf16_quirk=None detects the quirk from the RoPE
+    buffers (real-valued: the model was cast to bf16)."""
+    sd = {k: v for k, v in msat.state_dict().items()}
+    rope = getattr(msat, "rope_embedder", None)
+    if bf16_quirk is None:
+        bf16_quirk = rope is not None and not getattr(rope, "freqs_cis_0").is_complex()
+    overrides = dict(n_vl=n_vl, n_sa_pure=n_sa_pure, n_physics=n_physics)
+    if rope is not None:
+        overrides.update(rope_theta=float(rope.theta), max_seq_len=int(rope.max_seq_len))
+    cfg = RldxMsatCfg.from_state_dict(sd, **overrides)
+    dev = next(iter(sd.values())).device
+    return RldxMsat(sd, cfg, dev, bf16_quirk=bf16_quirk, vl_mask=vl_mask)
+
+
 class MsatDispatcher:
     """Replacement of a live MSAT module's forward by the rldx_amd chain, with
     the behaviour of the reference's path-D dispatcher (_CompiledDispatcher,
@@ -775,18 +793,7 @@ class MsatDispatcher:
             print(f"[rldx_amd.MsatDispatcher] {msg}", flush=True)
 
     def build(self, n_vl: int, n_sa_pure: int, n_physics: int = 0) -> RldxMsat:
-        msat = self.msat
-        sd = {k: v for k, v in msat.state_dict().items()}
-        rope = getattr(msat, "rope_embedder", None)
-        quirk = self.bf16_quirk
-        if quirk is None:
-            quirk = rope is not None and not getattr(rope, "freqs_cis_0").is_complex()
-        overrides = dict(n_vl=n_vl, n_sa_pure=n_sa_pure, n_physics=n_physics)
-        if rope is not None:
-            overrides.update(rope_theta=float(rope.theta), max_seq_len=int(rope.max_seq_len))
-        cfg = RldxMsatCfg.from_state_dict(sd, **overrides)
-        dev = next(iter(sd.values())).device
-        chain = RldxMsat(sd, cfg, dev, bf16_quirk=quirk, vl_mask=True)
+        chain = chain_for_module(self.msat, n_vl, n_sa_pure, n_physics, self.bf16_quirk, vl_mask=True)
         if self.graph:
             chain.capture()
         self.chain = chain
@@ -907,10 +914,11 @@ def install(msat: torch.nn.Module, n_vl: Optional[int] = None, n_sa_pure: Option
 
 
 # ---------------------------------------------------------------------------
-# The action head around the MSAT: CustomActionHeadChain.forward without the
-# RTC prefix (rldx/inference/action_model/engine/custom_action_model_chain.py:
-# 81-171): state encoder once, then per denoising step action encoder + baked
-# position embedding, MSAT, action decoder and the Euler update.
+# The action head around the MSAT: CustomActionHeadChain.forward
+# (rldx/inference/action_model/engine/custom_action_model_chain.py:81-171):
+# vlln on the VL embeddings, state encoder once, the RTC trained-mode prefix
+# encoded once, then per denoising step action encoder + baked position
+# embedding, MSAT, action decoder and the Euler update.
 # ---------------------------------------------------------------------------
 @dataclass
 class RldxHeadCfg:
@@ -927,6 +935,13 @@ class RldxHeadCfg:
     # (physics_head.py:106-109; future length = action horizon); 0 = no physics head
     physics_dim: int = 0
     physics_hist_len: int = 1
+    # RTC trained mode: the first prefix_len action rows are frozen to the
+    # previous chunk's actions (custom_action_model_chain.py:38, :98-121, :131-165)
+    prefix_len: int = 0
+    # vlln: LayerNorm of the VL embeddings at the head's entry (rldx/model/core/rldx.py:100-102;
+    # nn.LayerNorm(backbone_embedding_dim), affine, eps 1e-5); the release config leaves it off
+    use_vlln: bool = False
+    vlln_eps: float = 1e-5
 
     @property
     def physics_fut_len(self) -> int:
@@ -954,6 +969,9 @@ def make_head_state_dict(msat_cfg: RldxMsatCfg, cfg: RldxHeadCfg, device, seed: 
           "position_embedding.weight": rnd(cfg.action_horizon, d),
           "static_tembs": rnd(cfg.steps, 1, msat_cfg.inner, std=0.5),
           "static_time_tokens": rnd(cfg.steps, 1, msat_cfg.num_temb_tokens, d, std=0.5)}
+    if cfg.use_vlln:
+        sd["vlln.weight"] = (1.0 + rnd(msat_cfg.vl_dim).float()).to(BF16)
+        sd["vlln.bias"] = rnd(msat_cfg.vl_dim)
     if cfg.physics_dim > 0:
         # PhysicsHead (physics_head.py:111-113; physics.py:9-72): encoders physics_dim -> d -> d,
         # decoder output_dim -> d -> physics_dim; nn.Linear weights [out, in]
@@ -967,9 +985,15 @@ def make_head_state_dict(msat_cfg: RldxMsatCfg, cfg: RldxHeadCfg, device, seed: 
     return sd
 
 
-def _cat_linear(x, sd, name, e):
-    """CategorySpecificLinear.forward for batch 1 (embodiment_conditioned_mlp.py:49-58)."""
-    return torch.addmm(sd[f"{name}.b"][e], x, sd[f"{name}.W"][e])
+# CategorySpecificLinear layers of the head (embodiment_conditioned_mlp.py:60-82), W [E, in, out], b [E, out]
+_CAT_LINEARS = ("state_encoder.layer1", "state_encoder.layer2", "action_encoder.W1", "action_encoder.W2",
+                "action_encoder.W3", "action_decoder.layer1", "action_decoder.layer2")
+
+
+def bf16_timesteps(steps: int) -> list:
+    """The denoising schedule t = i / steps as the reference bakes it: a bf16
+    tensor (graph_safe_action_model.py:147-153), read back as floats."""
+    return torch.tensor([i / float(steps) for i in range(steps)], dtype=BF16).float().tolist()
 
 
 def sinusoidal_time(t: torch.Tensor, width: int) -> torch.Tensor:
@@ -984,29 +1008,67 @@ class RldxActionHead:
     """Flow-matching action head of RLDX-1 with the MSAT on the rldx_amd chain;
     `run` launches one action inference (state encoder + `steps` denoising
     iterations) on static buffers, `capture` / `replay` as one hipGraph.
+    Batch 1: the static buffers hold one sample (vl [1, n_vl, vl_dim], state
+    [1, 1, state_dim], x0 [1, horizon, action_dim], prefix [1, prefix_len,
+    action_dim], e_idx [1] the embodiment id); other batch sizes are served by
+    the module's own forward behind `install_action_head`.  The embodiment is
+    read on the device: run() gathers that embodiment's encoder / decoder
+    weights (W[e], b[e] of every CategorySpecificLinear) into static buffers
+    first, so one captured graph serves every embodiment.
+    timesteps: the denoising times (default: bf16_timesteps(cfg.steps), the
+    reference's bf16 schedule).
+
+    cfg.use_vlln: the VL embeddings go through the affine LayerNorm vlln
+    (head_sd "vlln.weight" / "vlln.bias") first (custom_action_model_chain.py:84).
+    cfg.prefix_len = d > 0 (RTC trained mode, :98-121, :131-165): the first d
+    action rows are `prefix` for the whole call; their encoder features (time
+    t = 1) are computed once, each step encodes and decodes only the last
+    horizon - d rows, and the Euler update advances only those.
 
     With a physics head (cfg.physics_dim > 0, an MSAT chain with a P stream of
     physics_hist_len + physics_fut_len tokens) it is CustomExpandedActionHeadChain
-    .forward without the RTC prefix (rldx/inference/action_model/engine/
-    custom_expanded_action_model_chain.py:92-219): the history tokens are
+    .forward (rldx/inference/action_model/engine/
+    custom_expanded_action_model_chain.py:84-219): the history tokens are
     encoded once, and per step the future physics state is encoded at the
     step's time, the MSAT returns action and physics hidden states, and the
     physics decoder's velocity advances the future state by the Euler step."""
 
-    def __init__(self, msat: RldxMsat, head_sd: dict, cfg: RldxHeadCfg, embodiment: int = 0):
-        self.msat, self.cfg, self.sd, self.e = msat, cfg, head_sd, embodiment
+    def __init__(self, msat: RldxMsat, head_sd: dict, cfg: RldxHeadCfg, embodiment: int = 0,
+                 timesteps: Optional[list] = None):
+        self.msat, self.cfg, self.sd = msat, cfg, head_sd
         dev, mc = msat.dev, msat.cfg
         Fn._require(mc.n_sa_pure == 1 + cfg.action_horizon, "MSAT SA tokens = state token + action horizon")
-        Fn._require(mc.output_dim == cfg.hidden_size, "MSAT output_dim feeds the action decoder")
+        Fn._require(head_sd["action_decoder.layer1.W"].shape[1] == mc.output_dim, "MSAT output_dim feeds the action decoder")
         self.phys = cfg.physics_dim > 0
         Fn._require(self.phys == msat.phys, "a physics head needs an MSAT chain with a P stream, and only then")
         if self.phys:
             Fn._require(msat.np_ == cfg.physics_hist_len + cfg.physics_fut_len,
                         "MSAT physics tokens = physics history + future")
         self.dt = 1.0 / cfg.steps
-        self.timesteps = [t / cfg.steps for t in range(cfg.steps)]
+        self.timesteps = bf16_timesteps(cfg.steps) if timesteps is None else [float(t) for t in timesteps]
+        Fn._require(len(self.timesteps) == cfg.steps, "one timestep per denoising step")
+        E = cfg.num_embodiments
+        for name in _CAT_LINEARS:
+            Fn._require(tuple(head_sd[f"{name}.W"].shape[:1]) == (E,) and tuple(head_sd[f"{name}.b"].shape[:1]) == (E,),
+                        f"{name}: one weight per embodiment ({E})")
+        Fn._require(0 <= embodiment < E, "embodiment id out of range")
+        self.e_idx = torch.full((1,), embodiment, dtype=torch.long, device=dev)
+        # the selected embodiment's weights, gathered at the top of run()
+        self.w_e = {n: torch.empty((1, *head_sd[f"{n}.W"].shape[1:]), dtype=head_sd[f"{n}.W"].dtype, device=dev)
+                    for n in _CAT_LINEARS}
+        self.b_e = {n: torch.empty((1, *head_sd[f"{n}.b"].shape[1:]), dtype=head_sd[f"{n}.b"].dtype, device=dev)
+                    for n in _CAT_LINEARS}
+        Fn._require(0 <= cfg.prefix_len < cfg.action_horizon, "0 <= prefix_len < action_horizon")
+        Fn._require(not cfg.use_vlln or ("vlln.weight" in head_sd and "vlln.bias" in head_sd),
+                    "use_vlln needs vlln.weight and vlln.bias")
         e = lambda *s: torch.empty(*s, dtype=BF16, device=dev)  # noqa: E731
         self.vl, self.state = e(1, mc.n_vl, mc.vl_dim), e(1, 1, cfg.state_dim)
+        self.vl_n = e(1, mc.n_vl, mc.vl_dim) if cfg.use_vlln else self.vl  # the MSAT's VL input
+        self.d = cfg.prefix_len
+        if self.d > 0:
+            self.prefix = e(1, self.d, cfg.action_dim)
+            # the prefix rows' time is 1 (custom_action_model_chain.py:117-121), baked
+            self.tau_one = sinusoidal_time(torch.ones(self.d, device=dev), mc.sa_dim).to(BF16)
         self.x0 = e(1, cfg.action_horizon, cfg.action_dim)
         self.act = e(1, cfg.action_horizon, cfg.action_dim)
         self.sa = e(1, mc.n_sa_pure, mc.sa_dim)
@@ -1033,37 +1095,67 @@ class RldxActionHead:
         h = self._lin(x, f"physics.{enc}.W1")
         return self._lin(F.silu(self._lin(torch.cat([h, pos], dim=-1), f"physics.{enc}.W2")), f"physics.{enc}.W3")
 
+    def set_embodiment(self, e: int) -> None:
+        """Select embodiment e for the next run / replay (range-checked on the
+        host: the gather must never index past W's first dimension)."""
+        if not 0 <= e < self.cfg.num_embodiments:
+            raise IndexError(f"embodiment id {e} out of range [0, {self.cfg.num_embodiments})")
+        self.e_idx.fill_(e)
+
+    def _cat(self, x, name):
+        """CategorySpecificLinear.forward for batch 1 (embodiment_conditioned_mlp.py:72-82):
+        x W[e] + b[e] with the gathered weights of embodiment e."""
+        return torch.addmm(self.b_e[name][0], x, self.w_e[name][0])
+
+    def _encode(self, x, tau):
+        """MultiEmbodimentActionEncoder.forward for batch 1
+        (embodiment_conditioned_mlp.py:191-227): W3(swish(W2([W1 x | tau])))."""
+        a = self._cat(x, "action_encoder.W1")
+        h = self._cat(torch.cat([a, tau], dim=-1), "action_encoder.W2")
+        return self._cat(h * torch.sigmoid(h), "action_encoder.W3")
+
     def run(self) -> torch.Tensor:
-        sd, e, mc, cfg = self.sd, self.e, self.msat.cfg, self.cfg
-        h = F.relu(_cat_linear(self.state[0], sd, "state_encoder.layer1", e))
-        self.sa[0, :1].copy_(_cat_linear(h, sd, "state_encoder.layer2", e))
+        sd, mc, cfg = self.sd, self.msat.cfg, self.cfg
+        d, H = self.d, cfg.action_horizon
+        for n in _CAT_LINEARS:
+            torch.index_select(sd[f"{n}.W"], 0, self.e_idx, out=self.w_e[n])
+            torch.index_select(sd[f"{n}.b"], 0, self.e_idx, out=self.b_e[n])
+        if cfg.use_vlln:
+            self.vl_n.copy_(F.layer_norm(self.vl, (mc.vl_dim,), sd["vlln.weight"], sd["vlln.bias"], cfg.vlln_eps))
+        h = F.relu(self._cat(self.state[0], "state_encoder.layer1"))
+        self.sa[0, :1].copy_(self._cat(h, "state_encoder.layer2"))
         self.act.copy_(self.x0)
+        if d > 0:  # the frozen prefix: its actions and (once) its encoder features
+            self.act[0, :d].copy_(self.prefix[0])
+            torch.add(self._encode(self.prefix[0], self.tau_one), sd["position_embedding.weight"][:d],
+                      out=self.sa[0, 1:1 + d])
         if self.phys:
             nh = cfg.physics_hist_len
             self.p_embs[0, :nh].copy_(self._physics_encoder(self.physics_hist[0], self.hist_pos, "physics_cond_encoder"))
             self.physics_fut.copy_(self.physics_x0)
         for i in range(cfg.steps):
-            a = _cat_linear(self.act[0], sd, "action_encoder.W1", e)
-            x = _cat_linear(torch.cat([a, self.tau[i]], dim=-1), sd, "action_encoder.W2", e)
-            x = x * torch.sigmoid(x)
-            a = _cat_linear(x, sd, "action_encoder.W3", e)
-            torch.add(a, sd["position_embedding.weight"], out=self.sa[0, 1:])
+            torch.add(self._encode(self.act[0, d:], self.tau[i][d:]), sd["position_embedding.weight"][d:],
+                      out=self.sa[0, 1 + d:])
             if self.phys:
                 # the step's time for every future row: the same encoding as the actions' tau
                 self.p_embs[0, nh:].copy_(self._physics_encoder(self.physics_fut[0], self.tau[i][: cfg.physics_fut_len],
                                                                 "physics_fut_encoder"))
-                o = self.msat.forward(self.sa, self.vl, sd["static_tembs"][i], sd["static_time_tokens"][i],
+                o = self.msat.forward(self.sa, self.vl_n, sd["static_tembs"][i], sd["static_time_tokens"][i],
                                       physics_embs=self.p_embs, adaln=self.adaln[i])
                 out = o["action"]
                 ph = o["physics"][0, -cfg.physics_fut_len:]
                 pv = self._lin(F.silu(self._lin(ph, "physics.physics_decoder.net.0")), "physics.physics_decoder.net.2")
                 self.physics_fut[0].add_(pv, alpha=self.dt)
             else:
-                out = self.msat.forward(self.sa, self.vl, sd["static_tembs"][i], sd["static_time_tokens"][i],
+                out = self.msat.forward(self.sa, self.vl_n, sd["static_tembs"][i], sd["static_time_tokens"][i],
                                         adaln=self.adaln[i])
-            hd = F.relu(_cat_linear(out[0], sd, "action_decoder.layer1", e))
-            v = _cat_linear(hd, sd, "action_decoder.layer2", e)[-cfg.action_horizon:]
-            self.act[0].add_(v, alpha=self.dt)
+            if d > 0:  # only the postfix rows are decoded and advanced (:156-170)
+                hd = F.relu(self._cat(out[0][-(H - d):], "action_decoder.layer1"))
+                v = self._cat(hd, "action_decoder.layer2")
+            else:
+                hd = F.relu(self._cat(out[0], "action_decoder.layer1"))
+                v = self._cat(hd, "action_decoder.layer2")[-H:]
+            self.act[0, d:].add_(v, alpha=self.dt)
         return self.act
 
     def capture(self, warmup: int = 2) -> None:
@@ -1082,3 +1174,207 @@ class RldxActionHead:
     def replay(self) -> torch.Tensor:
         self.graph.replay()
         return self.act
+
+
+class ActionHeadDispatcher:
+    """Replacement of a live action model's forward -- GraphSafeActionModel.forward
+    (rldx/inference/action_model/model/graph_safe_action_model.py:171-315), the
+    module the reference's chains bake (custom_action_model_chain.py:23-171,
+    custom_expanded_action_model_chain.py:84-219) -- by an RldxActionHead on the
+    rldx_amd MSAT chain, built from the module's weights at install.
+
+    Served (batch 1): vl_embs [1, n_vl, vl_dim] with the module's n_vl; state
+    [1, state_dim] or [1, 1, state_dim]; embodiment_id [1] (read on the host
+    and range-checked -- one stream sync when it lives on the GPU -- an id out
+    of range raises IndexError); init_noise [1, horizon, action_dim] or None
+    (then drawn here, as the module does); with prefix_len d > 0, prefix_actions
+    [1, d, action_dim]; on a physics model, physics_hist [1, hist_len,
+    physics_dim] and physics_init_noise or None.  The result is a new tensor
+    [1, horizon, action_dim].
+    Refused per call, to the module's own forward (counted in `fallbacks`,
+    logged with verbose=True): a batch other than 1, a VL token count other
+    than the module's, prefix_len > 0 without prefix_actions, a physics model
+    called without physics_hist (its forward then runs with no history
+    tokens).  A build failure (a module the head does not mirror: a vlln other
+    than LayerNorm / Identity, physics encoder widths other than the MSAT's
+    SA width, a physics future length other than the action horizon) sends
+    every call to the module's own forward for good, and so does a failure
+    while running, as the reference's dispatcher does
+    (rldx/inference/serve_optimization.py:251-516).
+    Weights are copied at the build; refresh() drops the head, which is
+    rebuilt from the module's current weights on the next call (served by the
+    module's own forward)."""
+
+    def __init__(self, model: torch.nn.Module, bf16_quirk: Optional[bool] = None, graph: bool = True,
+                 verbose: bool = False):
+        self.model, self.orig = model, model.forward
+        self.bf16_quirk, self.graph, self.verbose = bf16_quirk, graph, verbose
+        self.head: Optional[RldxActionHead] = None
+        self.failed = False
+        self.served = 0
+        self.fallbacks = 0
+        self.refusals: dict = {}  # reason -> calls
+
+    def _log(self, msg: str) -> None:
+        if self.verbose:
+            print(f"[rldx_amd.ActionHeadDispatcher] {msg}", flush=True)
+
+    def head_inputs(self) -> tuple:
+        """(head_sd, RldxHeadCfg, RldxMsat chain) of the module as it is now."""
+        m = self.model
+        gs = m.gs_msat
+        msat = gs._msat
+        phys = bool(getattr(m, "use_physics", False))
+        n_phys = int(getattr(gs, "n_physics", 0)) if phys else 0
+        chain = chain_for_module(msat, int(gs.n_vl), int(gs.n_sa_pure), n_phys, self.bf16_quirk)
+        mc = chain.cfg
+        dev = chain.dev
+        hsd = {}
+        with torch.no_grad():
+            for name in ("state_encoder", "action_encoder", "action_decoder"):
+                for k, v in getattr(m, name).state_dict().items():
+                    hsd[f"{name}.{k}"] = v.to(device=dev, dtype=BF16)
+            # the baked values of CustomActionHeadChain.__init__ (custom_action_model_chain.py:46-66)
+            hsd["position_embedding.weight"] = m.position_embedding(m.static_pos_ids).to(device=dev, dtype=BF16)
+            tembs, tts = [], []
+            for t in m.static_timesteps:
+                temb = msat.timestep_encoder(t.unsqueeze(0))
+                tts.append(msat.time_token_proj(temb).unsqueeze(1).repeat(1, mc.num_temb_tokens, 1))
+                tembs.append(temb)
+            hsd["static_tembs"] = torch.stack(tembs).to(device=dev, dtype=BF16)
+            hsd["static_time_tokens"] = torch.stack(tts).to(device=dev, dtype=BF16)
+            vlln = m.vlln
+            if isinstance(vlln, torch.nn.LayerNorm):
+                Fn._require(tuple(vlln.normalized_shape) == (mc.vl_dim,), "vlln must normalise the VL width")
+                ones = torch.ones(mc.vl_dim, device=dev)
+                hsd["vlln.weight"] = (vlln.weight if vlln.weight is not None else ones).to(device=dev, dtype=BF16)
+                hsd["vlln.bias"] = (vlln.bias if vlln.bias is not None else 0 * ones).to(device=dev, dtype=BF16)
+                use_vlln, eps = True, float(vlln.eps)
+            else:
+                Fn._require(isinstance(vlln, torch.nn.Identity), "vlln must be nn.LayerNorm or nn.Identity")
+                use_vlln, eps = False, 1e-5
+            kw = {}
+            if phys:
+                for enc in ("physics_cond_encoder", "physics_fut_encoder", "physics_decoder"):
+                    for k, v in getattr(m, enc).state_dict().items():
+                        hsd[f"physics.{enc}.{k}"] = v.to(device=dev, dtype=BF16)
+                for enc in ("physics_cond_encoder", "physics_fut_encoder"):
+                    Fn._require(hsd[f"physics.{enc}.W1.weight"].shape[0] == mc.sa_dim,
+                                "physics encoder width must be the MSAT SA width")
+                Fn._require(int(m.physics_fut_len) == int(m.action_horizon) and int(m.physics_hist_len) >= 1,
+                            "physics future length = action horizon, and a physics history")
+                kw = dict(physics_dim=int(m.physics_dim), physics_hist_len=int(m.physics_hist_len))
+        W1 = hsd["state_encoder.layer1.W"]
+        hc = RldxHeadCfg(state_dim=W1.shape[1], action_dim=int(m.action_dim), action_horizon=int(m.action_horizon),
+                         hidden_size=W1.shape[2], num_embodiments=W1.shape[0], steps=int(m.num_inference_timesteps),
+                         prefix_len=int(getattr(m, "prefix_len", 0)), use_vlln=use_vlln, vlln_eps=eps, **kw)
+        return hsd, hc, chain
+
+    def build(self) -> RldxActionHead:
+        hsd, hc, chain = self.head_inputs()
+        head = RldxActionHead(chain, hsd, hc, timesteps=self.model.static_timesteps.float().tolist())
+        if self.graph:
+            for buf in [head.vl, head.state, head.x0] + ([head.prefix] if head.d > 0 else []):
+                buf.zero_()
+            if head.phys:
+                for buf in (head.physics_hist, head.physics_x0):
+                    buf.zero_()
+            head.capture()
+        self.head = head
+        return head
+
+    def refresh(self) -> None:
+        """Drop the head; the next call rebuilds it from the module's current weights."""
+        self.head = None
+
+    def _unserved(self, vl_embs, state, prefix_actions, physics_hist) -> Optional[str]:
+        m = self.model
+        if vl_embs.dim() != 3 or vl_embs.shape[0] != 1 or state.shape[0] != 1:
+            return "batch other than 1"
+        if vl_embs.shape[1] != int(m.gs_msat.n_vl):
+            return "VL token count differs from the module's"
+        if int(getattr(m, "prefix_len", 0)) > 0 and prefix_actions is None:
+            return "prefix_len > 0 without prefix_actions"
+        if getattr(m, "use_physics", False) and physics_hist is None:
+            return "physics model without physics_hist"
+        return None
+
+    def _refuse(self, why: str, args, kwargs):
+        self.refusals[why] = self.refusals.get(why, 0) + 1
+        self.fallbacks += 1
+        self._log(f"served by the module's own forward: {why}")
+        return self.orig(*args, **kwargs)
+
+    def __call__(self, vl_embs, state, embodiment_id, init_noise=None, physics_hist=None, physics_init_noise=None,
+                 prefix_actions=None):
+        args = (vl_embs, state, embodiment_id)
+        kwargs = dict(init_noise=init_noise, physics_hist=physics_hist, physics_init_noise=physics_init_noise,
+                      prefix_actions=prefix_actions)
+        if self.failed:
+            self.fallbacks += 1
+            return self.orig(*args, **kwargs)
+        why = self._unserved(vl_embs, state, prefix_actions, physics_hist)
+        if why is not None:
+            return self._refuse(why, args, kwargs)
+        if self.head is None:
+            try:
+                self.build()
+            except Exception as e:  # noqa: BLE001 -- any build failure means the module's own forward from now on
+                self.failed = True
+                self._log(f"build failed ({e}); the module's own forward serves every call")
+            return self._refuse("building the head", args, kwargs)
+        h = self.head
+        h.set_embodiment(int(torch.as_tensor(embodiment_id).reshape(-1)[0]))  # IndexError out of range
+        try:
+            h.vl.copy_(vl_embs)
+            h.state.copy_(state.reshape(h.state.shape))
+            if init_noise is None:
+                h.x0.normal_()
+            else:
+                h.x0.copy_(init_noise)
+            if h.d > 0:
+                h.prefix.copy_(prefix_actions)
+            if h.phys:
+                h.physics_hist.copy_(physics_hist)
+                if physics_init_noise is None:
+                    h.physics_x0.normal_()
+                else:
+                    h.physics_x0.copy_(physics_init_noise)
+            out = (h.replay() if h.graph is not None else h.run()).clone()
+            self.served += 1
+            return out
+        except Exception as e:  # noqa: BLE001 -- as the reference: fall back for good on a hot-path failure
+            self.failed = True
+            self._log(f"hot-path failure ({e}); the module's own forward serves every call")
+            self.fallbacks += 1
+            return self.orig(*args, **kwargs)
+
+
+def install_action_head(model: torch.nn.Module, bf16_quirk: Optional[bool] = None, graph: bool = True,
+                        verbose: bool = False, build: bool = True) -> ActionHeadDispatcher:
+    """Route a live action model's forward (a GraphSafeActionModel: gs_msat
+    with _msat / n_vl / n_sa_pure / n_physics, vlln, state_encoder,
+    action_encoder, action_decoder, position_embedding, static_pos_ids,
+    static_timesteps, action_horizon, action_dim, num_inference_timesteps,
+    prefix_len and, with use_physics, the physics encoders / decoder and their
+    lengths) through an ActionHeadDispatcher.  build=True builds (and with
+    graph=True captures) the head now; otherwise the first call is served by
+    the module's own forward while it is built.  model.forward keeps the
+    reference signature forward(vl_embs, state, embodiment_id, init_noise,
+    physics_hist, physics_init_noise, prefix_actions)
+    (graph_safe_action_model.py:171-180); model.load_state_dict is wrapped so
+    that new weights drop the head (rebuilt on the next call)."""
+    d = ActionHeadDispatcher(model, bf16_quirk=bf16_quirk, graph=graph, verbose=verbose)
+    if build:
+        d.build()
+    model.forward = d
+    model.rldx_amd_dispatcher = d
+    load = model.load_state_dict
+
+    def load_state_dict(*args, **kwargs):  # new weights: the head is rebuilt on the next call
+        res = load(*args, **kwargs)
+        d.refresh()
+        return res
+
+    model.load_state_dict = load_state_dict
+    return d

@@ -190,34 +190,14 @@ def test_dispatcher_serves_masks_and_falls_back(dev, n_vl):
     assert len(msat.calls) == 3 and d.served == 3 and not d.failed
 
 
-def _head_reference(head_sd, msat_sd, hc, mc, vl, state, x0, e=0, dtype=torch.float32):
-    """CPU composition of CustomActionHeadChain.forward (custom_action_model_chain.py:81-171)
-    from the oracle MSAT and the per-embodiment MLPs of embodiment_conditioned_mlp.py,
-    evaluated in `dtype` (fp32, or bf16 eager with a rounding after every op)."""
-    f = {k: v.cpu().to(dtype) for k, v in head_sd.items()}
-    sd = {k: v.cpu().to(dtype) for k, v in msat_sd.items()}
-
-    def lin(x, name):  # CategorySpecificLinear, batch 1
-        return torch.addmm(f[f"{name}.b"][e], x, f[f"{name}.W"][e])
-
-    def tau(t, width):  # SinusoidalPositionalEncoding (fp32), cast to the model dtype
-        half = width // 2
-        ex = torch.exp(-torch.arange(half, dtype=torch.float) * (torch.log(torch.tensor(10000.0)) / half))
-        fr = torch.full((hc.action_horizon, 1), t) * ex
-        return torch.cat([torch.sin(fr), torch.cos(fr)], dim=-1).to(dtype)
-
-    state_feat = lin(torch.relu(lin(state.cpu().to(dtype)[0], "state_encoder.layer1")), "state_encoder.layer2")
-    act = x0.cpu().to(dtype)[0].clone()
-    for i in range(hc.steps):
-        a = lin(act, "action_encoder.W1")
-        x = lin(torch.cat([a, tau(i / hc.steps, mc.sa_dim)], dim=-1), "action_encoder.W2")
-        a = lin(x * torch.sigmoid(x), "action_encoder.W3") + f["position_embedding.weight"]
-        sa = torch.cat([state_feat, a])[None]
-        out = R.msat_forward(sd, sa, vl.cpu().to(dtype), f["static_tembs"][i], f["static_time_tokens"][i],
-                             heads=mc.heads, head_dim=mc.head_dim, ds_blocks=mc.ds_blocks, ss_blocks=mc.ss_blocks)
-        v = lin(torch.relu(lin(out[0], "action_decoder.layer1")), "action_decoder.layer2")[-hc.action_horizon:]
-        act.add_(v, alpha=1.0 / hc.steps)
-    return act
+def _head_reference(head_sd, msat_sd, hc, mc, head, e=0, dtype=torch.float32):
+    """The oracle's CustomActionHeadChain.forward composition (R.action_head) on the
+    head's static inputs, evaluated in `dtype` (fp32, or bf16 eager with a
+    rounding after every op)."""
+    return R.action_head(head_sd, msat_sd, head.vl, head.state, head.x0, steps=hc.steps, heads=mc.heads,
+                         head_dim=mc.head_dim, ds_blocks=mc.ds_blocks, ss_blocks=mc.ss_blocks, e=e,
+                         prefix=head.prefix if hc.prefix_len > 0 else None, use_vlln=hc.use_vlln,
+                         vlln_eps=hc.vlln_eps, dtype=dtype)
 
 
 def _head_on_gpu(mc, hc, dev, seed, embodiment):
@@ -228,6 +208,8 @@ def _head_on_gpu(mc, hc, dev, seed, embodiment):
     head.vl.copy_(torch.randn(head.vl.shape, generator=g, device=dev))
     head.state.copy_(torch.randn(head.state.shape, generator=g, device=dev))
     head.x0.copy_(torch.randn(head.x0.shape, generator=g, device=dev))
+    if hc.prefix_len > 0:
+        head.prefix.copy_(torch.randn(head.prefix.shape, generator=g, device=dev))
     head.capture()
     a1 = head.replay().clone()
     a2 = head.replay().clone()
@@ -243,10 +225,27 @@ def test_rldx_action_head_graph_matches_fp32_composition(dev):
     mc = RM.RldxMsatCfg(ds_blocks=1, ss_blocks=1)
     hc = RM.RldxHeadCfg(steps=2, num_embodiments=4)
     head, sd, hsd, a1 = _head_on_gpu(mc, hc, dev, 71, 1)
-    r = _head_reference(hsd, sd, hc, mc, head.vl, head.state, head.x0, e=1).double()
+    r = _head_reference(hsd, sd, hc, mc, head, e=1).double()
     rel = _rel(a1[0].cpu().double(), r)
     print(f"action head: rel-L2 to the fp32 composition {rel:.2e}")
     assert torch.isfinite(a1).all() and rel <= 2e-2
+
+
+@pytest.mark.parametrize("prefix_len,use_vlln", [(4, False), (0, True), (15, True)])
+def test_rldx_action_head_prefix_and_vlln_match_fp32_composition(dev, prefix_len, use_vlln):
+    """RTC trained mode (the first prefix_len rows frozen to the prefix, encoded
+    once at time 1, postfix-only decode) and vlln on the VL tokens, 1 DS + 1 SS,
+    2 steps, one hipGraph, against the oracle's fp32 composition: rel-L2 <= 2e-2,
+    the prefix rows are the prefix bit for bit, and replays are bitwise stable."""
+    mc = RM.RldxMsatCfg(ds_blocks=1, ss_blocks=1)
+    hc = RM.RldxHeadCfg(steps=2, num_embodiments=4, prefix_len=prefix_len, use_vlln=use_vlln)
+    head, sd, hsd, a1 = _head_on_gpu(mc, hc, dev, 91 + prefix_len, 2)
+    r = _head_reference(hsd, sd, hc, mc, head, e=2).double()
+    rel = _rel(a1[0].cpu().double(), r)
+    print(f"action head (prefix_len={prefix_len}, vlln={use_vlln}): rel-L2 to the fp32 composition {rel:.2e}")
+    assert torch.isfinite(a1).all() and rel <= 2e-2
+    if prefix_len > 0:
+        assert torch.equal(a1[0, :prefix_len], head.prefix[0])
 
 
 def test_rldx_action_head_release_shape_as_accurate_as_eager_bf16(dev):
@@ -260,10 +259,107 @@ def test_rldx_action_head_release_shape_as_accurate_as_eager_bf16(dev):
     hc = RM.RldxHeadCfg(num_embodiments=4)
     head, sd, hsd, a1 = _head_on_gpu(mc, hc, dev, 81, 3)
     o = a1[0].cpu().double()
-    r32 = _head_reference(hsd, sd, hc, mc, head.vl, head.state, head.x0, e=3).double()
-    r16 = _head_reference(hsd, sd, hc, mc, head.vl, head.state, head.x0, e=3, dtype=torch.bfloat16).double()
+    r32 = _head_reference(hsd, sd, hc, mc, head, e=3).double()
+    r16 = _head_reference(hsd, sd, hc, mc, head, e=3, dtype=torch.bfloat16).double()
     floor, got = _rel(r16, r32), _rel(o, r32)
     cos = torch.nn.functional.cosine_similarity(o.flatten(), r16.flatten(), dim=0).item()
     print(f"release action head: rel-L2 to fp32 {got:.2e} (eager bf16: {floor:.2e}), to the bf16 composition "
           f"{_rel(o, r16):.2e}, max-abs to bf16 {(o - r16).abs().max().item():.3e}, cos {cos:.6f}")
     assert torch.isfinite(a1).all() and got <= 1.5 * floor and cos >= 0.999
+
+
+def _live_action_model(mc, hc, sd, hsd, dev, seed):
+    """A module with GraphSafeActionModel's attributes (graph_safe_action_model.py:
+    112-153): gs_msat (_msat with its time modules, n_vl, n_sa_pure, n_physics),
+    vlln, the per-embodiment encoders / decoder under CategorySpecificLinear's
+    parameter names (W, b), the position embedding, the bf16 schedule; its own
+    forward records the call and returns "own"."""
+    m = torch.nn.Module()
+    gs = torch.nn.Module()
+    gs.add_module("_msat", _tree_with_time_modules(mc, sd, dev, seed))
+    rope = torch.nn.Module()  # a bf16-cast model's RoPE embedder: real-valued tables (the bf16 quirk)
+    rope.theta, rope.max_seq_len = mc.rope_theta, mc.max_seq_len
+    rope.register_buffer("freqs_cis_0", torch.zeros(1, dtype=torch.bfloat16, device=dev), persistent=False)
+    gs._msat.add_module("rope_embedder", rope)
+    gs.n_vl, gs.n_sa_pure, gs.n_physics = mc.n_vl, mc.n_sa_pure, 0
+    m.add_module("gs_msat", gs)
+    for enc, layers in (("state_encoder", ("layer1", "layer2")), ("action_encoder", ("W1", "W2", "W3")),
+                        ("action_decoder", ("layer1", "layer2"))):
+        mod = torch.nn.Module()
+        for layer in layers:
+            sub = torch.nn.Module()
+            sub.W = torch.nn.Parameter(hsd[f"{enc}.{layer}.W"], requires_grad=False)
+            sub.b = torch.nn.Parameter(hsd[f"{enc}.{layer}.b"], requires_grad=False)
+            mod.add_module(layer, sub)
+        m.add_module(enc, mod)
+    pe = torch.nn.Embedding(hc.action_horizon + 8, mc.sa_dim, device=dev, dtype=torch.bfloat16)
+    pe.weight.data[:hc.action_horizon] = hsd["position_embedding.weight"]
+    m.add_module("position_embedding", pe)
+    m.static_pos_ids = torch.arange(hc.action_horizon, device=dev)
+    m.static_timesteps = torch.tensor([t / hc.steps for t in range(hc.steps)], dtype=torch.bfloat16, device=dev)
+    if hc.use_vlln:
+        ln = torch.nn.LayerNorm(mc.vl_dim, device=dev, dtype=torch.bfloat16)
+        ln.weight.data.copy_(hsd["vlln.weight"])
+        ln.bias.data.copy_(hsd["vlln.bias"])
+        m.add_module("vlln", ln)
+    else:
+        m.add_module("vlln", torch.nn.Identity())
+    m.action_horizon, m.action_dim, m.num_inference_timesteps = hc.action_horizon, hc.action_dim, hc.steps
+    m.prefix_len, m.dt = hc.prefix_len, 1.0 / hc.steps
+    m.calls = []
+    m.forward = lambda *a, **k: m.calls.append((a, k)) or "own"
+    return m
+
+
+def test_install_action_head_on_a_live_model(dev):
+    """install_action_head builds the head from a live action model (weights,
+    baked position embedding and time embeddings, vlln) and serves batch-1
+    calls with the reference signature, RTC prefix and vlln included, against
+    the oracle's fp32 composition (rel-L2 <= 2e-2, prefix rows exact), for two
+    embodiments through one captured graph; a batch of 2 and a missing prefix
+    are refused to the module's own forward, an embodiment id out of range
+    raises IndexError without disabling the dispatcher."""
+    mc = RM.RldxMsatCfg(ds_blocks=1, ss_blocks=1)
+    hc = RM.RldxHeadCfg(steps=2, num_embodiments=3, prefix_len=2, use_vlln=True)
+    sd = RM.make_state_dict(mc, dev, seed=101)
+    hsd = RM.make_head_state_dict(mc, hc, dev, seed=102)
+    m = _live_action_model(mc, hc, sd, hsd, dev, 103)
+    d = RM.install_action_head(m)  # the bf16 quirk detected from the RoPE tables
+    h = d.head
+    for k in hsd:
+        if not k.startswith("static_"):
+            assert torch.equal(h.sd[k], hsd[k]), k
+    msat = m.gs_msat._msat
+    for i, t in enumerate(m.static_timesteps):
+        temb, tt = _time_inputs(msat, t.reshape(1))
+        assert torch.equal(h.sd["static_tembs"][i], temb) and torch.equal(h.sd["static_time_tokens"][i, :, :1], tt)
+    g = torch.Generator(device=dev).manual_seed(104)
+
+    def rnd(*s):
+        return torch.randn(*s, generator=g, device=dev).to(torch.bfloat16)
+
+    for e in (2, 0):
+        vl, state = rnd(1, mc.n_vl, mc.vl_dim), rnd(1, hc.state_dim)
+        x0, prefix = rnd(1, hc.action_horizon, hc.action_dim), rnd(1, 2, hc.action_dim)
+        out = m(vl, state, torch.tensor([e]), init_noise=x0, prefix_actions=prefix)
+        ref = R.action_head(h.sd, sd, vl, state[:, None], x0, steps=hc.steps, heads=mc.heads, head_dim=mc.head_dim,
+                            ds_blocks=mc.ds_blocks, ss_blocks=mc.ss_blocks, e=e, prefix=prefix, use_vlln=True).double()
+        rel = _rel(out[0].cpu().double(), ref)
+        print(f"installed action head, embodiment {e}: rel-L2 to the fp32 composition {rel:.2e}")
+        assert torch.isfinite(out).all() and rel <= 2e-2
+        assert torch.equal(out[0, :2], prefix[0])
+    assert d.served == 2 and m.calls == []
+    assert m(rnd(2, mc.n_vl, mc.vl_dim), rnd(2, hc.state_dim), torch.tensor([0, 1]), prefix_actions=rnd(2, 2, 64)) == "own"
+    assert m(vl, state, torch.tensor([1]), init_noise=x0) == "own"
+    assert d.refusals == {"batch other than 1": 1, "prefix_len > 0 without prefix_actions": 1}
+    with pytest.raises(IndexError):
+        m(vl, state, torch.tensor([3]), init_noise=x0, prefix_actions=prefix)
+    out = m(vl, state, torch.tensor([1]), prefix_actions=prefix)  # noise drawn here
+    assert not d.failed and d.served == 3 and torch.isfinite(out).all() and torch.equal(out[0, :2], prefix[0])
+    # the mirrored CustomActionHeadChain (the reference's build function) on an identical model: the same bits
+    from rldx_amd.compat.inference.action_model.engine.custom_action_model_chain import \
+        build_custom_action_model_chain
+    chain = build_custom_action_model_chain(_live_action_model(mc, hc, sd, hsd, dev, 103), dev)
+    a = chain(vl, state, torch.tensor([0]), init_noise=x0, prefix_actions=prefix)
+    b = m(vl, state, torch.tensor([0]), init_noise=x0, prefix_actions=prefix)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))

@@ -203,3 +203,121 @@ def test_dispatcher_unserved_calls():
     assert d._unserved(x3, x3, False, torch.zeros(1, 4, 8), None) is None
     assert d._unserved(x3, x3, False, torch.zeros(1, 5, 8), None) == "token counts differ from the chain's"
     assert d._unserved(x3, x3, False, None, None) == "token counts differ from the chain's"
+
+
+# ---------------------------------------------------------------------------
+# The action head oracle (R.action_head): Euler update in closed form, the RTC
+# prefix path against the unsliced re-lock composition, vlln written out.
+# ---------------------------------------------------------------------------
+def _tiny_head(seed, horizon=6, steps=2, **kw):
+    mc = RM.RldxMsatCfg(heads=2, head_dim=64, ds_blocks=1, ss_blocks=1, sa_dim=128, vl_dim=128, output_dim=64,
+                        n_vl=5, n_sa_pure=1 + horizon)
+    hc = RM.RldxHeadCfg(state_dim=8, action_dim=8, action_horizon=horizon, hidden_size=64, num_embodiments=2,
+                        steps=steps, **kw)
+    sd = {k: v.float() for k, v in RM.make_state_dict(mc, "cpu", seed=seed).items()}
+    hsd = {k: v.float() for k, v in RM.make_head_state_dict(mc, hc, "cpu", seed=seed + 1).items()}
+    g = torch.Generator().manual_seed(seed + 2)
+    io = dict(vl=torch.randn(1, mc.n_vl, mc.vl_dim, generator=g), state=torch.randn(1, 1, hc.state_dim, generator=g),
+              x0=torch.randn(1, horizon, hc.action_dim, generator=g),
+              prefix=torch.randn(1, max(hc.prefix_len, 1), hc.action_dim, generator=g)[:, :hc.prefix_len])
+    return mc, hc, sd, hsd, io
+
+
+def _head(mc, hc, sd, hsd, io, e=1, **kw):
+    return R.action_head(hsd, sd, io["vl"], io["state"], io["x0"], steps=hc.steps, heads=mc.heads,
+                         head_dim=mc.head_dim, ds_blocks=mc.ds_blocks, ss_blocks=mc.ss_blocks, e=e,
+                         prefix=io["prefix"] if hc.prefix_len > 0 else None, use_vlln=hc.use_vlln, **kw)
+
+
+def test_oracle_action_head_euler_closed_form():
+    """A decoder whose last layer has zero weights predicts its bias c[e] for
+    every row at every step, so `steps` Euler steps of dt = 1/steps move each
+    free row by exactly c[e]; the prefix rows equal the prefix exactly.  A wrong
+    dt, decode slice, embodiment index or prefix re-lock fails this."""
+    for d in (0, 2):
+        mc, hc, sd, hsd, io = _tiny_head(5, steps=4, prefix_len=d)
+        hsd["action_decoder.layer2.W"].zero_()
+        c = torch.tensor([[0.5] * 8, [-0.25 * (i + 1) for i in range(8)]])
+        hsd["action_decoder.layer2.b"].copy_(c)
+        act = _head(mc, hc, sd, hsd, io, e=1)
+        assert torch.equal(act[:d], io["prefix"][0])
+        assert torch.allclose(act[d:], io["x0"][0, d:] + c[1], atol=1e-6, rtol=0)
+
+
+def _relock_composition(mc, hc, sd, hsd, io, e=1):
+    """RTC trained mode without the chain's slicing (rldx/model/core/rldx.py:609-610
+    re-lock semantics): every step encodes all `horizon` rows with per-row time
+    (1 for the prefix rows, the step's time for the rest), runs the MSAT, decodes
+    every row, advances all rows, then writes the prefix back."""
+    H, d, w = hc.action_horizon, hc.prefix_len, mc.sa_dim
+
+    def lin(x, name):
+        return torch.addmm(hsd[f"{name}.b"][e], x, hsd[f"{name}.W"][e])
+
+    state_feat = lin(torch.relu(lin(io["state"][0], "state_encoder.layer1")), "state_encoder.layer2")
+    act = io["x0"][0].clone()
+    act[:d] = io["prefix"][0]
+    for i in range(hc.steps):
+        t = torch.full((H,), i / hc.steps)
+        t[:d] = 1.0
+        half = w // 2
+        fr = t[:, None] * torch.exp(-torch.arange(half, dtype=torch.float) * (torch.log(torch.tensor(10000.0)) / half))
+        tau = torch.cat([torch.sin(fr), torch.cos(fr)], dim=-1)
+        h = lin(torch.cat([lin(act, "action_encoder.W1"), tau], dim=-1), "action_encoder.W2")
+        feat = lin(h * torch.sigmoid(h), "action_encoder.W3") + hsd["position_embedding.weight"]
+        out = R.msat_forward(sd, torch.cat([state_feat, feat])[None], io["vl"], hsd["static_tembs"][i],
+                             hsd["static_time_tokens"][i], heads=mc.heads, head_dim=mc.head_dim,
+                             ds_blocks=mc.ds_blocks, ss_blocks=mc.ss_blocks)[0]
+        act = act + lin(torch.relu(lin(out, "action_decoder.layer1")), "action_decoder.layer2")[-H:] / hc.steps
+        act[:d] = io["prefix"][0]
+    return act
+
+
+def test_oracle_action_head_prefix_equals_the_relock_composition():
+    """The prefix path (prefix features encoded once at time 1, postfix-only
+    encode / decode) equals the unsliced composition to fp32 rounding, and
+    the prefix changes the free rows (its tokens are attended)."""
+    mc, hc, sd, hsd, io = _tiny_head(17, prefix_len=3)
+    got = _head(mc, hc, sd, hsd, io)
+    ref = _relock_composition(mc, hc, sd, hsd, io)
+    assert torch.allclose(got, ref, atol=1e-5, rtol=1e-5), (got - ref).abs().max()
+    io2 = dict(io, prefix=io["prefix"] + 0.5)
+    assert (_head(mc, hc, sd, hsd, io2)[3:] - got[3:]).abs().max() > 1e-5
+    # x0's prefix rows never matter
+    io3 = dict(io, x0=io["x0"].clone())
+    io3["x0"][:, :3] = 7.0
+    assert torch.equal(_head(mc, hc, sd, hsd, io3), got)
+
+
+def test_oracle_action_head_vlln_is_layer_norm_of_the_vl_tokens():
+    """use_vlln equals the head without it on VL tokens normalised by hand:
+    (x - mean) / sqrt(var + 1e-5) * w + b per token, biased variance."""
+    mc, hc, sd, hsd, io = _tiny_head(29, use_vlln=True)
+    x = io["vl"].double()
+    mu = x.mean(-1, keepdim=True)
+    var = ((x - mu) ** 2).mean(-1, keepdim=True)
+    vl_n = ((x - mu) / torch.sqrt(var + 1e-5) * hsd["vlln.weight"].double() + hsd["vlln.bias"].double()).float()
+    got = _head(mc, hc, sd, hsd, io)
+    hc_off = RM.RldxHeadCfg(**{**hc.__dict__, "use_vlln": False})
+    ref = _head(mc, hc_off, sd, hsd, dict(io, vl=vl_n))
+    assert torch.allclose(got, ref, atol=1e-5, rtol=1e-5), (got - ref).abs().max()
+    assert (_head(mc, hc_off, sd, hsd, io) - got).abs().max() > 1e-5
+
+
+def test_action_head_dispatcher_unserved_calls():
+    """The per-call refusals of the action-head dispatcher (no build needed)."""
+    m = torch.nn.Module()
+    m.gs_msat = torch.nn.Module()
+    m.gs_msat.n_vl = 64
+    m.prefix_len = 0
+    d = RM.ActionHeadDispatcher(m)
+    vl, st = torch.zeros(1, 64, 8), torch.zeros(1, 4)
+    assert d._unserved(vl, st, None, None) is None
+    assert d._unserved(torch.zeros(2, 64, 8), torch.zeros(2, 4), None, None) == "batch other than 1"
+    assert d._unserved(torch.zeros(1, 63, 8), st, None, None) == "VL token count differs from the module's"
+    m.prefix_len = 3
+    assert d._unserved(vl, st, None, None) == "prefix_len > 0 without prefix_actions"
+    assert d._unserved(vl, st, torch.zeros(1, 3, 8), None) is None
+    m.use_physics = True
+    assert d._unserved(vl, st, torch.zeros(1, 3, 8), None) == "physics model without physics_hist"
+    assert d._unserved(vl, st, torch.zeros(1, 3, 8), torch.zeros(1, 1, 5)) is None
