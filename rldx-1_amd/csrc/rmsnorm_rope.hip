@@ -27,6 +27,8 @@
 namespace rldx {
 namespace {
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 template <typename T>
 struct Vec16;
 template <>
@@ -122,7 +124,10 @@ __device__ void kv_tile_pack(RowFn vrow, int64_t m_total, int64_t k0, uint16_t* 
 // One thread: V consecutive elements of R heads of one token (the R heads
 // share the token's cos / sin and, within q or within k, the norm weight, so
 // those are loaded once for R rows).  R divides both hq and hk.
-template <typename T, int D, int R, bool PK = false>
+// NTL / NTS (large launches): non-temporal loads of the rows / stores of the
+// results (read once, written once; the memory-side cache keeps what the
+// rest of the launch reuses: cos / sin and the norm weights).
+template <typename T, int D, int R, bool PK = false, bool NTL = false, bool NTS = false>
 __global__ __launch_bounds__(256) void rmsnorm_rope_half_kernel(HalfArgs a) {
   constexpr int V = Vec16<T>::N;   // elements per lane
   constexpr int LPR = D / V;       // lanes per row
@@ -169,7 +174,9 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_half_kernel(HalfArgs a) {
   uint4 raw[R];
 #pragma unroll
   for (int j = 0; j < R; ++j)
-    raw[j] = valid ? *reinterpret_cast<const uint4*>(src + j * src_h + d0) : make_uint4(0, 0, 0, 0);
+    raw[j] = !valid ? make_uint4(0, 0, 0, 0)
+             : NTL ? __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + j * src_h + d0)))
+                   : *reinterpret_cast<const uint4*>(src + j * src_h + d0);
   const uint4 wraw = a.no_norm ? make_uint4(0, 0, 0, 0) : *reinterpret_cast<const uint4*>(w + d0);
   const uint4 craw = *reinterpret_cast<const uint4*>(cs + d0);
   const uint4 sraw = *reinterpret_cast<const uint4*>(sn + d0);
@@ -237,7 +244,12 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_half_kernel(HalfArgs a) {
     if constexpr (PK) {
       if (valid) *reinterpret_cast<uint4*>(a.kvp + h * a.kvp_sh + packed_k_offset(s, d0, D)) = outraw;
     } else {
-      if (valid) *reinterpret_cast<uint4*>(dst + j * dst_h + d0) = outraw;
+      if (valid) {
+        if constexpr (NTS)
+          __builtin_nontemporal_store(__builtin_bit_cast(u32x4, outraw), reinterpret_cast<u32x4*>(dst + j * dst_h + d0));
+        else
+          *reinterpret_cast<uint4*>(dst + j * dst_h + d0) = outraw;
+      }
     }
   }
 }
@@ -388,21 +400,36 @@ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 template <typename T, int D>
 hipError_t launch_half_d(const HalfArgs& a, hipStream_t stream) {
   constexpr int V = Vec16<T>::N;
-  // Heads per thread: 4 on large launches (fewer loads per element, measured
-  // +5% of HBM rate at 16K-64K tokens; 8 measured 1-3% slower than 4); small
-  // launches are latency-bound and keep one head per thread for the most
-  // parallelism.
+  // Small launches are latency-bound: one head per thread, the most
+  // parallelism.  Large launches (measured on MI355X, fp32 q / k [1, S, 16, 64],
+  // outputs bit-identical in every variant):
+  //  * rows that fit the 256 MB memory-side cache (16K tokens, 134 MB in):
+  //    4 heads per thread (fewer loads per element) and non-temporal stores,
+  //    46.3 -> 41.1 us (0.84 of 8 TB/s; a plain torch.neg of the same bytes
+  //    40.6 us); non-temporal loads there lose (47 us: the rows of a repeated
+  //    call are served from that cache);
+  //  * larger rows (64K tokens, 537 MB in): 2 heads per thread, non-temporal
+  //    loads and stores, 199.6 -> 174.3 us (0.79; torch.neg 180 us); 4 heads
+  //    184 us, 8 heads 187 us, 1 head 198 us.
   const bool large = a.total_rows * (D / V) >= (int64_t{1} << 21);
-  const int R = !large ? 1 : (a.hq % 4 == 0 && a.hk % 4 == 0) ? 4 : (a.hq % 2 == 0 && a.hk % 2 == 0) ? 2 : 1;
+  const bool past_cache = a.total_rows * D * static_cast<int64_t>(sizeof(T)) > (int64_t{256} << 20);
+  const bool by2 = a.hq % 2 == 0 && a.hk % 2 == 0, by4 = a.hq % 4 == 0 && a.hk % 4 == 0;
+  const int R = !large ? 1 : past_cache ? (by2 ? 2 : 1) : by4 ? 4 : by2 ? 2 : 1;
   const int64_t threads = a.total_rows / R * (D / V);
   const int grid = static_cast<int>((threads + 255) / 256);
   if (grid == 0) return hipSuccess;
-  if (R == 4)
-    hipLaunchKernelGGL((rmsnorm_rope_half_kernel<T, D, 4>), dim3(grid), dim3(256), 0, stream, a);
-  else if (R == 2)
-    hipLaunchKernelGGL((rmsnorm_rope_half_kernel<T, D, 2>), dim3(grid), dim3(256), 0, stream, a);
-  else
+  if (!large)
     hipLaunchKernelGGL((rmsnorm_rope_half_kernel<T, D, 1>), dim3(grid), dim3(256), 0, stream, a);
+  else if (past_cache && R == 2)
+    hipLaunchKernelGGL((rmsnorm_rope_half_kernel<T, D, 2, false, true, true>), dim3(grid), dim3(256), 0, stream, a);
+  else if (past_cache)
+    hipLaunchKernelGGL((rmsnorm_rope_half_kernel<T, D, 1, false, true, true>), dim3(grid), dim3(256), 0, stream, a);
+  else if (R == 4)
+    hipLaunchKernelGGL((rmsnorm_rope_half_kernel<T, D, 4, false, false, true>), dim3(grid), dim3(256), 0, stream, a);
+  else if (R == 2)
+    hipLaunchKernelGGL((rmsnorm_rope_half_kernel<T, D, 2, false, false, true>), dim3(grid), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((rmsnorm_rope_half_kernel<T, D, 1, false, false, true>), dim3(grid), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
