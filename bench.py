@@ -61,7 +61,7 @@ def parse():
 
 
 PROFILE_KERNELS = ("joint_attn", "gqa_attn", "gqa_op", "gqa_op_169", "step_attn", "vit_attn", "mem_attn", "swiglu",
-                   "rmsnorm_rope", "res_ln", "vl_ln", "add2_rmsnorm")
+                   "rmsnorm_rope", "rmsnorm_rope_64k", "res_ln", "vl_ln", "add2_rmsnorm")
 
 
 def profile_launch(name: str, torch):
@@ -77,8 +77,8 @@ def profile_launch(name: str, torch):
         x = W.swiglu_inputs(W.SwigluCfg())["x"].to(dev)
         y = torch.empty(x.shape[0], x.shape[1] // 2, dtype=torch.bfloat16, device=dev)
         return lambda: Fn.swiglu(x, out=y)
-    if name == "rmsnorm_rope":  # fp32 16384 x 16 x 64 (the HBM-bound sweep point)
-        rs = W.RmsRopeCfg(seq=16384)
+    if name in ("rmsnorm_rope", "rmsnorm_rope_64k"):  # fp32 16384 (or 65536) x 16 x 64, the HBM-bound sweep points
+        rs = W.RmsRopeCfg(seq=65536 if name == "rmsnorm_rope_64k" else 16384)
         shape = (rs.batch, rs.seq, rs.heads, rs.head_dim)
         q, k = torch.randn(shape, device=dev), torch.randn(shape, device=dev)
         cs, sn = (t.to(dev) for t in W.qwen_rope_cos_sin(rs.seq, rs.head_dim, rs.theta))
@@ -795,7 +795,7 @@ def main():
     traffic = None
     tf = ROOT / "profiles" / "gemm_w12_swiglu_traffic.json"
     if tf.exists():
-        traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+        traffic = json.loads(tf.read_text()).get("l2_miss_bytes_per_launch")
     # traffic: L2-miss bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated on a copy):
     # what the L2s fetch from / write to the memory side, served by the MALL or by HBM
     roofline = dict(kernel="gemm_kernel<SWIGLU_PACKED, LN fold>: W12 + SwiGLU grouped GEMM with the pre-LayerNorm "
