@@ -1203,17 +1203,32 @@ class ActionHeadDispatcher:
     (rldx/inference/serve_optimization.py:251-516).
     Weights are copied at the build; refresh() drops the head, which is
     rebuilt from the module's current weights on the next call (served by the
-    module's own forward)."""
+    module's own forward); with check_weights=True every call first checks
+    the module's parameters and buffers for replacement or in-place change
+    (tensor identity, data_ptr, _version) and refreshes on a change."""
 
     def __init__(self, model: torch.nn.Module, bf16_quirk: Optional[bool] = None, graph: bool = True,
-                 verbose: bool = False):
+                 verbose: bool = False, check_weights: bool = False):
         self.model, self.orig = model, model.forward
         self.bf16_quirk, self.graph, self.verbose = bf16_quirk, graph, verbose
+        self.check_weights = check_weights
         self.head: Optional[RldxActionHead] = None
         self.failed = False
         self.served = 0
         self.fallbacks = 0
+        self.rebuilds = 0    # heads dropped because the weights changed
         self.refusals: dict = {}  # reason -> calls
+        self._stamp = None   # [(tensor, data_ptr, _version)] the head was built from
+
+    def _weights_stamp(self) -> list:
+        return [(t, t.data_ptr(), t._version) for t in self.model.state_dict(keep_vars=True).values()]
+
+    def weights_changed(self) -> bool:
+        """True when a parameter or buffer was replaced or modified in place since the build."""
+        cur = self.model.state_dict(keep_vars=True).values()
+        if self._stamp is None or len(self._stamp) != len(cur):
+            return True
+        return any(t is not u or t.data_ptr() != p or t._version != v for (t, p, v), u in zip(self._stamp, cur))
 
     def _log(self, msg: str) -> None:
         if self.verbose:
@@ -1281,11 +1296,15 @@ class ActionHeadDispatcher:
                     buf.zero_()
             head.capture()
         self.head = head
+        self._stamp = self._weights_stamp()
         return head
 
     def refresh(self) -> None:
         """Drop the head; the next call rebuilds it from the module's current weights."""
+        if self.head is not None:
+            self.rebuilds += 1
         self.head = None
+        self._stamp = None
 
     def _unserved(self, vl_embs, state, prefix_actions, physics_hist) -> Optional[str]:
         m = self.model
@@ -1313,6 +1332,9 @@ class ActionHeadDispatcher:
         if self.failed:
             self.fallbacks += 1
             return self.orig(*args, **kwargs)
+        if self.head is not None and self.check_weights and self.weights_changed():
+            self._log("weights changed since the build: rebuilding the head")
+            self.refresh()
         why = self._unserved(vl_embs, state, prefix_actions, physics_hist)
         if why is not None:
             return self._refuse(why, args, kwargs)
@@ -1351,7 +1373,8 @@ class ActionHeadDispatcher:
 
 
 def install_action_head(model: torch.nn.Module, bf16_quirk: Optional[bool] = None, graph: bool = True,
-                        verbose: bool = False, build: bool = True) -> ActionHeadDispatcher:
+                        verbose: bool = False, build: bool = True,
+                        check_weights: bool = False) -> ActionHeadDispatcher:
     """Route a live action model's forward (a GraphSafeActionModel: gs_msat
     with _msat / n_vl / n_sa_pure / n_physics, vlln, state_encoder,
     action_encoder, action_decoder, position_embedding, static_pos_ids,
@@ -1363,8 +1386,10 @@ def install_action_head(model: torch.nn.Module, bf16_quirk: Optional[bool] = Non
     reference signature forward(vl_embs, state, embodiment_id, init_noise,
     physics_hist, physics_init_noise, prefix_actions)
     (graph_safe_action_model.py:171-180); model.load_state_dict is wrapped so
-    that new weights drop the head (rebuilt on the next call)."""
-    d = ActionHeadDispatcher(model, bf16_quirk=bf16_quirk, graph=graph, verbose=verbose)
+    that new weights drop the head (rebuilt on the next call);
+    check_weights=True also catches in-place updates."""
+    d = ActionHeadDispatcher(model, bf16_quirk=bf16_quirk, graph=graph, verbose=verbose,
+                             check_weights=check_weights)
     if build:
         d.build()
     model.forward = d

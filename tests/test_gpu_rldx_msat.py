@@ -363,3 +363,21 @@ def test_install_action_head_on_a_live_model(dev):
     a = chain(vl, state, torch.tensor([0]), init_noise=x0, prefix_actions=prefix)
     b = m(vl, state, torch.tensor([0]), init_noise=x0, prefix_actions=prefix)
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    # check_weights: an in-place update of a live weight drops the head; the call
+    # that notices it rebuilds the head and is served by the module's own
+    # forward, the next one by the rebuilt head, which matches a head built
+    # from the updated weights
+    d.check_weights = True
+    with torch.no_grad():
+        m.action_decoder.layer2.b.mul_(0.5)
+    assert m(vl, state, torch.tensor([0]), init_noise=x0, prefix_actions=prefix) == "own"
+    assert d.rebuilds == 1 and d.head is not None and d.refusals["building the head"] == 1
+    c = m(vl, state, torch.tensor([0]), init_noise=x0, prefix_actions=prefix)
+    assert d.head is not None and not d.failed
+    # a head built from a snapshot of the updated weights (the fake model's
+    # parameters share storage with hsd, so the snapshot is taken from it now)
+    hsd2 = {k: v.clone() for k, v in hsd.items()}
+    fresh = RM.install_action_head(_live_action_model(mc, hc, sd, hsd2, dev, 103), graph=False)
+    e2 = fresh.model(vl, state, torch.tensor([0]), init_noise=x0, prefix_actions=prefix)
+    assert torch.equal(c.view(torch.int16), e2.view(torch.int16))
+    assert not torch.equal(c.view(torch.int16), b.view(torch.int16))

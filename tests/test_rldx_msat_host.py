@@ -321,3 +321,26 @@ def test_action_head_dispatcher_unserved_calls():
     m.use_physics = True
     assert d._unserved(vl, st, torch.zeros(1, 3, 8), None) == "physics model without physics_hist"
     assert d._unserved(vl, st, torch.zeros(1, 3, 8), torch.zeros(1, 1, 5)) is None
+
+
+def test_action_head_dispatcher_detects_weight_changes():
+    """weights_changed(): in-place updates, replaced parameters and new buffers
+    after the stamp (no build needed); refresh() clears the stamp."""
+    m = torch.nn.Module()
+    m.lin = torch.nn.Linear(4, 4)
+    m.register_buffer("steps", torch.arange(4.0))
+    d = RM.ActionHeadDispatcher(m, check_weights=True)
+    assert d.weights_changed()  # never built
+    d._stamp = d._weights_stamp()
+    assert not d.weights_changed()
+    with torch.no_grad():
+        m.lin.weight.add_(1.0)  # in place
+    assert d.weights_changed()
+    d._stamp = d._weights_stamp()
+    m.lin.bias = torch.nn.Parameter(torch.zeros(4))  # replaced
+    assert d.weights_changed()
+    d._stamp = d._weights_stamp()
+    m.register_buffer("extra", torch.zeros(1))  # added
+    assert d.weights_changed()
+    d.refresh()
+    assert d._stamp is None and d.rebuilds == 0  # nothing built yet, nothing counted
