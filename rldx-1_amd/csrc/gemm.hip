@@ -155,13 +155,27 @@ constexpr int lds_bytes() { return cmax(C::RING * 1024, (ln_stats_off<C>() + 2 *
 // [q SPL, (q + 1) SPL) of row t % R (q = t / R, SPL = ceil(slots R / 512)),
 // at most kLnSlotsMax (k <= 2048 at 128-row tiles).
 constexpr int kLnSlotsMax = 8;
-constexpr int kLdsBytes = cmax(lds_bytes<Cfg128>(), cmax(lds_bytes<Cfg64>(), lds_bytes<Cfg32>()));
+// The last kLdsTail bytes of a kernel's LDS: the SwiGLU tiles' W row sums
+// (gate and up of at most 64 output columns, fp32, stored at the prologue for
+// the LayerNorm fold of the epilogue; kernels without WIDE tiles, whose rings
+// leave room behind them), then 16 bytes holding the split-K arrival flag, used
+// by every kernel (in a WIDE kernel inside its ring area, past its epilogue).
+constexpr int kWsumStash = 2 * 64 * 4;
+constexpr int kLdsTail = kWsumStash + 16;
+template <class C>
+constexpr int epi_bytes() { return (ln_stats_off<C>() + 2 * 512) * 4; }  // fp32 tiles + row statistics
+constexpr int kLdsBytes =
+    cmax(lds_bytes<Cfg128>(), cmax(lds_bytes<Cfg64>(), lds_bytes<Cfg32>())) + kLdsTail;
 static_assert(kLdsBytes <= 80 * 1024, "two workgroups per CU");
-constexpr int kLdsDeep = cmax(lds_bytes<Cfg128D>(), cmax(lds_bytes<Cfg64D>(), lds_bytes<Cfg32D>()));
+constexpr int kLdsDeep = cmax(lds_bytes<Cfg128D>(), cmax(lds_bytes<Cfg64D>(), lds_bytes<Cfg32D>())) + kLdsTail;
 static_assert(kLdsDeep <= 160 * 1024 && kLdsDeep >= kLdsBytes, "one workgroup per CU");
 constexpr int kLdsQkv = cmax(lds_bytes<Cfg128>(), cmax(lds_bytes<Cfg64x128>(), lds_bytes<Cfg32x128>()));
 constexpr int kLdsQkvDeep = cmax(lds_bytes<Cfg128D>(), cmax(lds_bytes<Cfg64x128D>(), lds_bytes<Cfg32x128D>()));
 static_assert(kLdsQkv <= 80 * 1024 && kLdsQkvDeep <= 160 * 1024, "QKV epilogue tiles");
+static_assert(kLdsQkv - 16 >= cmax(epi_bytes<Cfg128>(), cmax(epi_bytes<Cfg64x128>(), epi_bytes<Cfg32x128>())) &&
+                  kLdsQkvDeep - 16 >=
+                      cmax(epi_bytes<Cfg128D>(), cmax(epi_bytes<Cfg64x128D>(), epi_bytes<Cfg32x128D>())),
+              "the split-K flag of a WIDE kernel lies past its epilogue tiles");
 
 struct Group {
   const uint16_t* a;  // packed activations
@@ -234,7 +248,7 @@ __device__ __forceinline__ void wait_barrier() {
 // narrow kernels apart: the host compilation pass rejects a second caller of a
 // specialization whose body holds the 16-byte LDS-load builtin.
 template <class C, int EPI, bool K, bool LN>
-__device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int item, u32x4* lds) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int item, u32x4* lds, float* wsl) {
   constexpr bool kSwiglu = EPI == kEpiSwiglu || EPI == kEpiSwigluPacked;
   constexpr int MB = C::MB, NB = C::NB, BNW = C::BNW, U = C::U, CH = C::CH, NSLOT = C::NSLOT;
   const int lane = threadIdx.x & 63;
@@ -319,18 +333,43 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     }
   }
   // biases of this thread's columns (gate and up for SwiGLU) as bf16 bits, packed
-  // in pairs once loaded (at the prologue's wait)
+  // in pairs once loaded (at the prologue's wait).  No branch around the loads,
+  // so all of them are in flight together: they go through a descriptor bounded
+  // to the bias (a missing bias is an empty one: every read returns zero), and a
+  // chunk past the output columns reads column 0's and is zeroed when packed.
   uint16_t braw[16];
+  {
+    const __amdgpu_buffer_rsrc_t brs = rsrc(G.bias, G.bias ? G.n * 2 : 0);
+    const int bcol = col_ok ? col : 0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    braw[i] = G.bias && col_ok ? G.bias[col + i] : uint16_t{0};
-    braw[8 + i] = kSwiglu && G.bias && col_ok ? G.bias[G.n / 2 + col + i] : uint16_t{0};
+    for (int i = 0; i < 8; ++i) {
+      braw[i] = static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(brs, (bcol + i) * 2, 0, 0));
+      braw[8 + i] = kSwiglu ? static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(brs, (G.n / 2 + bcol + i) * 2, 0, 0))
+                            : uint16_t{0};
+    }
   }
   uint32_t bpk[8];
-  // LayerNorm fold: W row sums of this thread's columns (gate and up for SwiGLU);
-  // the SwiGLU tiles load theirs after the K loop (16 more live registers through
-  // the loop would spill at two workgroups per CU)
+  // LayerNorm fold: W row sums of this thread's columns (gate and up for SwiGLU).
+  // The SwiGLU tiles keep theirs in LDS through the K loop (16 more live
+  // registers would spill at two workgroups per CU): thread t < 2 OC loads one
+  // with the prologue's loads and stores it at wsl[t] (gate sums, then up sums)
+  // once the prologue's wait has passed; the epilogue reads them from there.
+  // WIDE SwiGLU tiles, whose rings leave no room for it, load theirs after the
+  // K loop.
   [[maybe_unused]] float wg[8], wu[8];
+  [[maybe_unused]] float wsv = 0.f;
+  constexpr bool kStash = LN && kSwiglu && !K;  // (WIDE rings fill their LDS)
+  if constexpr (kStash) {
+    const int t = static_cast<int>(threadIdx.x);
+    if (t < 2 * OC && nt * OC + t % OC < n_out) wsv = G.wsum[(t < OC ? 0 : G.n / 2) + nt * OC + t % OC];
+  }
+  auto load_wsum_stash = [&]() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      wg[i] = wsl[cc + i];
+      wu[i] = wsl[OC + cc + i];
+    }
+  };
   auto load_wsum = [&]() {
     const floatx4 z = {0.f, 0.f, 0.f, 0.f};
     const floatx4* ws = reinterpret_cast<const floatx4*>(G.wsum + col);
@@ -383,8 +422,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
         lp2 += lv[j][1];
       }
   }
+  if constexpr (kStash) {  // read back after the K loop, whose barriers publish it
+    if (static_cast<int>(threadIdx.x) < 2 * OC) wsl[threadIdx.x] = wsv;
+  }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) bpk[i] = static_cast<uint32_t>(braw[2 * i]) | (static_cast<uint32_t>(braw[2 * i + 1]) << 16);
+  for (int i = 0; i < 8; ++i)
+    bpk[i] = col_ok ? static_cast<uint32_t>(braw[2 * i]) | (static_cast<uint32_t>(braw[2 * i + 1]) << 16) : 0u;
   lread(0, 0);
   int slot_next = 1, slot_dma = NSLOT - 1;  // ring slots of stages st + 1, st + NSLOT - 1
   for (int st = 0; st < lstages; st += 2) {
@@ -414,7 +457,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     bu[2 * i] = bf16x2_lo(bpk[4 + i]);
     bu[2 * i + 1] = bf16x2_hi(bpk[4 + i]);
   }
-  if constexpr (LN && kSwiglu) load_wsum();
+  if constexpr (kStash) load_wsum_stash();
+  else if constexpr (LN && kSwiglu) load_wsum();
   wait_barrier<0>();  // the ring's last reads and loads are done; LDS becomes the fp32 tiles
   float* tiles = reinterpret_cast<float*>(lds);
   {
@@ -668,7 +712,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
             slot(split, i) + 4 * e, 0, kCpolDevice);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    int* last = reinterpret_cast<int*>(lds) + kLdsBytes / 4 - 1;  // past every epilogue tile, in both kernels' LDS
+    int* last = reinterpret_cast<int*>(wsl + kWsumStash / 4);  // the LDS tail: past the stash and every epilogue tile
     if (threadIdx.x == 0)
       *last = __hip_atomic_fetch_add(G.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
               static_cast<unsigned>(G.splits - 1);
@@ -759,6 +803,7 @@ template <int EPI, bool DEEP, bool WIDE, bool LN>
 __global__ __launch_bounds__(kThreads, DEEP ? 2 : 4) void gemm_kernel(GemmArgs a) {
   constexpr int kLds = WIDE ? (DEEP ? kLdsQkvDeep : kLdsQkv) : (DEEP ? kLdsDeep : kLdsBytes);
   __shared__ __attribute__((aligned(16))) u32x4 lds[kLds / 16];
+  float* const wsl = reinterpret_cast<float*>(lds) + (kLds - kLdsTail) / 4;
   const int b = static_cast<int>(blockIdx.x);
   int gi = 0;
   if (a.num_groups > 1 && b >= a.g[1].wg_begin) gi = 1;
@@ -771,32 +816,32 @@ __global__ __launch_bounds__(kThreads, DEEP ? 2 : 4) void gemm_kernel(GemmArgs a
   if (item >= G.items) return;
   if constexpr (WIDE && DEEP) {  // 128-column tiles (whole heads for the QKV epilogue)
     if (G.cfg == kTile128)
-      gemm_tile<Cfg128D, EPI, WIDE, LN>(a, G, item, lds);
+      gemm_tile<Cfg128D, EPI, WIDE, LN>(a, G, item, lds, wsl);
     else if (G.cfg == kTile64x128)
-      gemm_tile<Cfg64x128D, EPI, WIDE, LN>(a, G, item, lds);
+      gemm_tile<Cfg64x128D, EPI, WIDE, LN>(a, G, item, lds, wsl);
     else
-      gemm_tile<Cfg32x128D, EPI, WIDE, LN>(a, G, item, lds);
+      gemm_tile<Cfg32x128D, EPI, WIDE, LN>(a, G, item, lds, wsl);
   } else if constexpr (WIDE) {
     if (G.cfg == kTile128)
-      gemm_tile<Cfg128, EPI, WIDE, LN>(a, G, item, lds);
+      gemm_tile<Cfg128, EPI, WIDE, LN>(a, G, item, lds, wsl);
     else if (G.cfg == kTile64x128)
-      gemm_tile<Cfg64x128, EPI, WIDE, LN>(a, G, item, lds);
+      gemm_tile<Cfg64x128, EPI, WIDE, LN>(a, G, item, lds, wsl);
     else
-      gemm_tile<Cfg32x128, EPI, WIDE, LN>(a, G, item, lds);
+      gemm_tile<Cfg32x128, EPI, WIDE, LN>(a, G, item, lds, wsl);
   } else if constexpr (DEEP) {
     if (G.cfg == kTile128)
-      gemm_tile<Cfg128D, EPI, WIDE, LN>(a, G, item, lds);
+      gemm_tile<Cfg128D, EPI, WIDE, LN>(a, G, item, lds, wsl);
     else if (G.cfg == kTile64)
-      gemm_tile<Cfg64D, EPI, WIDE, LN>(a, G, item, lds);
+      gemm_tile<Cfg64D, EPI, WIDE, LN>(a, G, item, lds, wsl);
     else
-      gemm_tile<Cfg32D, EPI, WIDE, LN>(a, G, item, lds);
+      gemm_tile<Cfg32D, EPI, WIDE, LN>(a, G, item, lds, wsl);
   } else {
     if (G.cfg == kTile128)
-      gemm_tile<Cfg128, EPI, WIDE, LN>(a, G, item, lds);
+      gemm_tile<Cfg128, EPI, WIDE, LN>(a, G, item, lds, wsl);
     else if (G.cfg == kTile64)
-      gemm_tile<Cfg64, EPI, WIDE, LN>(a, G, item, lds);
+      gemm_tile<Cfg64, EPI, WIDE, LN>(a, G, item, lds, wsl);
     else
-      gemm_tile<Cfg32, EPI, WIDE, LN>(a, G, item, lds);
+      gemm_tile<Cfg32, EPI, WIDE, LN>(a, G, item, lds, wsl);
   }
 }
 
