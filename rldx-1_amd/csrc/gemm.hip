@@ -389,12 +389,25 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     }
   };
   if constexpr (LN && !kSwiglu) load_wsum();
-  // QKV epilogue: the Q or K RMSNorm weights of this thread's 8 columns of the head
+  // QKV epilogue: the Q or K RMSNorm weights of this thread's 8 columns of the
+  // head; on a V tile the bias (and W row sum) of the one tile column the thread
+  // packs (the same column on every pass of its V loop, see there)
   [[maybe_unused]] u32x4 qk_w = {0, 0, 0, 0};
+  [[maybe_unused]] float v_bias = 0.f, v_wsum = 0.f;
   if constexpr (qkv_epi(EPI)) {
     constexpr int D = EPI == kEpiQkv ? 128 : 64;
     const int which = nt * OC / a.qkv.inner;
-    if (which < 2) qk_w = *reinterpret_cast<const u32x4*>((which == 0 ? G.qn_w : G.kn_w) + cc % D);
+    if (which < 2) {
+      qk_w = *reinterpret_cast<const u32x4*>((which == 0 ? G.qn_w : G.kn_w) + cc % D);
+    } else {
+      constexpr int NCH = D / 16;
+      const int t = static_cast<int>(threadIdx.x);
+      const int hh = t / (NCH * 64) % (OC / D), idx = t % (NCH * 64);
+      const int d = hh * D + 32 * ((idx >> 6) >> 1) + (idx & 31);
+      const __amdgpu_buffer_rsrc_t vbr = rsrc(G.bias, G.bias ? G.n * 2 : 0);  // no bias: reads zero
+      v_bias = bf(static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(vbr, (nt * OC + d) * 2, 0, 0)));
+      if constexpr (LN) v_wsum = G.wsum[nt * OC + d];
+    }
   }
   // LayerNorm fold: this thread's slots of its row, loaded before the ring
   // (consecutive threads: consecutive rows of one slot, contiguous), summed at
@@ -545,6 +558,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     const int h0 = (n0 - which * O.inner) / D;
     if (which == 2) {
       constexpr int NCH = D / 16;  // 1 KB chunks per K or V part of a head's 32-key tile
+      static_assert(kThreads % (HPT * NCH * 64) == 0, "a thread's V column (hh, idx) is the same on every pass");
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int s = static_cast<int>(threadIdx.x) + kThreads * i;
@@ -555,7 +569,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
         const int rb = 32 * kt + 16 * (cx & 1) + 4 * (l >> 5);
         const int row0 = mt * R + 32 * kt;  // first stream row of this 32-key tile
         if (row0 >= G.m) continue;
-        const float bd = G.bias ? bf(G.bias[n0 + d]) : 0.f;
+        const float bd = v_bias;  // loaded in the prologue for this column d
         u32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -567,7 +581,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
             hi += tiles[kg * C::TILE + (r + 1) * C::TP + d];
           }
           if constexpr (LN) {
-            const float sd = G.wsum[n0 + d];
+            const float sd = v_wsum;
             float rs, rm;
             ln_row(r, rs, rm);
             lo = ln_fold(lo, rs, rm, sd);
