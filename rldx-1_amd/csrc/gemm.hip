@@ -136,10 +136,13 @@ using Cfg64x128 = TileCfg<2, 4, 2, 3>;
 using Cfg32x128 = TileCfg<1, 4, 2, 2>;
 // Deep rings for launches of at most one workgroup per CU: one workgroup alone
 // on a CU is latency-bound with the rings above (~48 KB of loads in flight,
-// about half of what a CU can stream); these keep ~96-112 KB in flight.
-using Cfg128D = TileCfg<4, 4, 2, 8>;
-using Cfg64D = TileCfg<2, 2, 1, 8>;
-using Cfg32D = TileCfg<1, 2, 1, 6>;
+// about half of what a CU can stream); these keep ~80-96 KB in flight.  Deeper
+// rings (8 / 8 / 6 slots, 112-120 KB) measured slower: every workgroup issues
+// its first NSLOT - 1 stages at once, and that initial burst of weight reads
+// delays the first stage longer than the extra depth gains in the loop.
+using Cfg128D = TileCfg<4, 4, 2, 6>;
+using Cfg64D = TileCfg<2, 2, 1, 6>;
+using Cfg32D = TileCfg<1, 2, 1, 5>;
 using Cfg64x128D = TileCfg<2, 4, 2, 6>;
 using Cfg32x128D = TileCfg<1, 4, 2, 3>;
 
@@ -236,8 +239,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const uint16_t* p, int by
 // assembly: a release fence would also wait for every LDS-bound load.
 template <int N>
 __device__ __forceinline__ void wait_barrier() {
-  static_assert(N == 0 || N == 3 || N == 4 || N == 5 || N == 12, "vmcnt immediate");  // (NSLOT - 2) * ND
+  static_assert(N == 0 || N == 3 || N == 4 || N == 5 || N == 8 || N == 9 || N == 12, "vmcnt immediate");  // (NSLOT - 2) * ND
   if constexpr (N == 12) asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (N == 9) asm volatile("s_waitcnt vmcnt(9) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if constexpr (N == 5) asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if constexpr (N == 3) asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
