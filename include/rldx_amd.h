@@ -227,6 +227,31 @@ hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* kv_packed, 
                                           hipStream_t stream);
 
 /*
+ * rldx_attention_packed_fwd_bf16 with O written to a packed activation matrix
+ * (out_packed as there, o_strides unused) by row segments, for a batch of
+ * joint sequences whose streams the GEMMs hold stream by stream (every batch
+ * entry's rows of one stream contiguous).  segments: num_segments (1..3) rows
+ * {first query row, rows stored, first packed row}, ascending and disjoint
+ * inside [0, seq_q): query row r of batch entry b with off <= r < off + rows
+ * goes to packed row base + b * rows + (r - off); query rows outside every
+ * segment (padding rows of a stream) are not stored.  Any batch >= 1; every
+ * packed row below 2^31.  The attention itself is that of
+ * rldx_attention_packed_fwd_bf16, bit for bit.
+ * Replaces: the joint attention of the double / single-stream blocks with the
+ *   [VL | SA | P] output split back into the streams
+ *   (rldx/inference/action_model/double_stream/engine/ops/op_fused_attention_3way.py:13-138,
+ *   custom_double_stream_chain.py:57-96), for a batch of B robots
+ *   (custom_action_model_chain.py:85; the reference's chained ops take one).
+ */
+hipError_t rldx_attention_packed_segments_fwd_bf16(const void* q, const void* kv_packed,
+                                                   const int64_t* packed_strides, void* o, int32_t out_packed,
+                                                   const int64_t* segments, int32_t num_segments, int64_t batch,
+                                                   int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k,
+                                                   int64_t head_dim, const int64_t* q_strides, const float* key_bias,
+                                                   int64_t key_bias_batch_stride, float scale, int32_t causal,
+                                                   hipStream_t stream);
+
+/*
  * rldx_attention_packed_fwd_bf16 plus a memory-side-cache warm-up: warm_count
  * (0..3) byte ranges warm_ptrs[i] (4-byte aligned), warm_bytes[i] long, whose
  * whole 128-byte lines further workgroups of the same launch read (one dword

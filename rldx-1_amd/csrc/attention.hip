@@ -109,6 +109,12 @@ struct AttnArgs {
   int64_t kv_sb, kv_sh;  // element strides of the packed tiles per batch / kv head
   int64_t o_sb, o_sh, o_ss;
   int64_t o_packed_k;  // > 0: O written as the packed activations of [sq, hq * D] (batch 1)
+  // packed O by row segments (o_nseg > 0, any batch): query row r of batch entry
+  // b with o_seg_off[s] <= r < o_seg_off[s] + o_seg_rows[s] goes to packed row
+  // o_seg_base[s] + b o_seg_rows[s] + r - o_seg_off[s]; rows outside every
+  // segment are not stored
+  int o_nseg;
+  int o_seg_off[3], o_seg_rows[3], o_seg_base[3];
   const float* key_bias;  // [batch, sk] additive (natural-log units) or nullptr
   int64_t kb_sb;
   int hq, hkv, group, sq, sk;
@@ -599,7 +605,19 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
     }
     l = pair_sum(l);
     const float inv = l > 0.f ? 1.0f / l : 0.f;
-    if (q_idx < sq) {
+    // packed row of this lane's query (o_packed_k > 0); constant indices into
+    // the segment arrays, so they stay scalar kernel arguments
+    int prow = q_idx;
+    bool stored = q_idx < sq;
+    if (a.o_nseg > 0) {
+      const bool s1 = a.o_nseg > 1 && q_idx >= a.o_seg_off[1], s2 = a.o_nseg > 2 && q_idx >= a.o_seg_off[2];
+      const int off = s2 ? a.o_seg_off[2] : s1 ? a.o_seg_off[1] : a.o_seg_off[0];
+      const int rows = s2 ? a.o_seg_rows[2] : s1 ? a.o_seg_rows[1] : a.o_seg_rows[0];
+      const int base = s2 ? a.o_seg_base[2] : s1 ? a.o_seg_base[1] : a.o_seg_base[0];
+      stored = stored && q_idx >= off && q_idx - off < rows;
+      prow = base + b * rows + (q_idx - off);
+    }
+    if (stored) {
       uint16_t* orow = a.o + b * a.o_sb + h * a.o_sh + (row0 + q_idx) * a.o_ss;
 #pragma unroll
       for (int r = 0; r < DPW; ++r) {
@@ -617,7 +635,7 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnArgs a) {
           wv.x = pack_bf16x2(acc[0], acc[1]);
           wv.y = pack_bf16x2(acc[2], acc[3]);
           if (a.o_packed_k > 0)  // 4 consecutive columns stay inside one 8-element run
-            *reinterpret_cast<uint2*>(a.o + packed_act_offset(q_idx, static_cast<int64_t>(h) * D + d, a.o_packed_k)) = wv;
+            *reinterpret_cast<uint2*>(a.o + packed_act_offset(prow, static_cast<int64_t>(h) * D + d, a.o_packed_k)) = wv;
           else
             *reinterpret_cast<uint2*>(orow + d) = wv;
         }
@@ -1196,18 +1214,35 @@ extern "C" hipError_t rldx_attention_kv_pack_bf16(const void* k, const int64_t* 
 namespace {
 // The packed-K/V attention; warm: up to three byte ranges whose 128-byte lines
 // extra workgroups of the launch read (see AttnArgs::n_work).
+// Row segments of a packed O (num_segments x {first query row, rows stored,
+// first packed row}): ascending, disjoint, inside [0, seq_q), every packed row
+// below 2^31.
+bool segments_ok(const int64_t* seg, int32_t n, int64_t batch, int64_t seq_q) {
+  if (!seg || n < 1 || n > 3) return false;
+  int64_t end = 0;
+  for (int s = 0; s < n; ++s) {
+    const int64_t off = seg[3 * s], rows = seg[3 * s + 1], base = seg[3 * s + 2];
+    if (off < end || rows < 0 || base < 0 || off + rows > seq_q) return false;
+    if (base + batch * rows > (int64_t{1} << 31) - 1) return false;
+    end = off + rows;
+  }
+  return true;
+}
+
 hipError_t attention_packed(const void* q, const void* kv_packed, const int64_t* packed_strides, void* o,
-                            int32_t out_packed, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
-                            int64_t seq_k, int64_t head_dim, const int64_t* q_strides, const int64_t* o_strides,
-                            const float* key_bias, int64_t key_bias_batch_stride, float scale, int32_t causal,
-                            const void* const* warm_ptrs, const int64_t* warm_bytes, int32_t warm_count,
-                            hipStream_t stream) {
+                            int32_t out_packed, const int64_t* segments, int32_t num_segments, int64_t batch,
+                            int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t head_dim,
+                            const int64_t* q_strides, const int64_t* o_strides, const float* key_bias,
+                            int64_t key_bias_batch_stride, float scale, int32_t causal, const void* const* warm_ptrs,
+                            const int64_t* warm_bytes, int32_t warm_count, hipStream_t stream) {
   const int64_t zero3[3] = {0, 0, 0};
+  if (num_segments && (!out_packed || !segments_ok(segments, num_segments, batch, seq_q)))
+    return hipErrorInvalidValue;
   if (out_packed) {
     // 1: O is the packed [seq_q, q_heads*head_dim] matrix; > 1: O is the
     // column range of a packed matrix out_packed columns wide that starts at
-    // the 16-column chunk `o`
-    if (batch > 1 || reinterpret_cast<uintptr_t>(o) % 16) return hipErrorInvalidValue;
+    // the 16-column chunk `o`; a batch needs the row segments
+    if ((batch > 1 && !num_segments) || reinterpret_cast<uintptr_t>(o) % 16) return hipErrorInvalidValue;
     if (out_packed < 0 || (out_packed > 1 && (out_packed % 16 || out_packed < q_heads * head_dim)))
       return hipErrorInvalidValue;
     o_strides = zero3;
@@ -1223,6 +1258,12 @@ hipError_t attention_packed(const void* q, const void* kv_packed, const int64_t*
   AttnArgs a{};
   fill_qo(a, q, o, q_heads, kv_heads, seq_q, seq_k, q_strides, o_strides, key_bias, key_bias_batch_stride, scale);
   a.o_packed_k = out_packed > 1 ? out_packed : (out_packed ? q_heads * head_dim : 0);
+  a.o_nseg = num_segments;
+  for (int s = 0; s < num_segments; ++s) {
+    a.o_seg_off[s] = static_cast<int>(segments[3 * s]);
+    a.o_seg_rows[s] = static_cast<int>(segments[3 * s + 1]);
+    a.o_seg_base[s] = static_cast<int>(segments[3 * s + 2]);
+  }
   a.kv = static_cast<const uint16_t*>(kv_packed);
   a.kv_sb = packed_strides[0];
   a.kv_sh = packed_strides[1];
@@ -1238,9 +1279,20 @@ extern "C" hipError_t rldx_attention_packed_fwd_bf16(const void* q, const void* 
                                                      const int64_t* o_strides, const float* key_bias,
                                                      int64_t key_bias_batch_stride, float scale, int32_t causal,
                                                      hipStream_t stream) {
-  return attention_packed(q, kv_packed, packed_strides, o, out_packed, batch, q_heads, kv_heads, seq_q, seq_k,
-                          head_dim, q_strides, o_strides, key_bias, key_bias_batch_stride, scale, causal, nullptr,
-                          nullptr, 0, stream);
+  return attention_packed(q, kv_packed, packed_strides, o, out_packed, nullptr, 0, batch, q_heads, kv_heads, seq_q,
+                          seq_k, head_dim, q_strides, o_strides, key_bias, key_bias_batch_stride, scale, causal,
+                          nullptr, nullptr, 0, stream);
+}
+
+extern "C" hipError_t rldx_attention_packed_segments_fwd_bf16(
+    const void* q, const void* kv_packed, const int64_t* packed_strides, void* o, int32_t out_packed,
+    const int64_t* segments, int32_t num_segments, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+    int64_t seq_k, int64_t head_dim, const int64_t* q_strides, const float* key_bias, int64_t key_bias_batch_stride,
+    float scale, int32_t causal, hipStream_t stream) {
+  if (!out_packed || num_segments < 1) return hipErrorInvalidValue;
+  return attention_packed(q, kv_packed, packed_strides, o, out_packed, segments, num_segments, batch, q_heads,
+                          kv_heads, seq_q, seq_k, head_dim, q_strides, nullptr, key_bias, key_bias_batch_stride,
+                          scale, causal, nullptr, nullptr, 0, stream);
 }
 
 extern "C" hipError_t rldx_attention_packed_fwd_warm_bf16(
@@ -1250,9 +1302,9 @@ extern "C" hipError_t rldx_attention_packed_fwd_warm_bf16(
     const void* const* warm_ptrs, const int64_t* warm_bytes, int32_t warm_count, hipStream_t stream) {
   WarmRanges check;
   if (!warm_ranges(warm_ptrs, warm_bytes, warm_count, check)) return hipErrorInvalidValue;
-  return attention_packed(q, kv_packed, packed_strides, o, out_packed, batch, q_heads, kv_heads, seq_q, seq_k,
-                          head_dim, q_strides, o_strides, key_bias, key_bias_batch_stride, scale, causal, warm_ptrs,
-                          warm_bytes, warm_count, stream);
+  return attention_packed(q, kv_packed, packed_strides, o, out_packed, nullptr, 0, batch, q_heads, kv_heads, seq_q,
+                          seq_k, head_dim, q_strides, o_strides, key_bias, key_bias_batch_stride, scale, causal,
+                          warm_ptrs, warm_bytes, warm_count, stream);
 }
 
 extern "C" hipError_t rldx_attention_fwd_bf16(const void* q, const void* k, const void* v, void* o, int64_t batch,

@@ -85,6 +85,10 @@ SIGNATURES = {
         c_i32,
         [c_vp, c_vp, c_i64p, c_vp, c_i32] + [c_i64] * 6 + [c_i64p] * 2 + [c_vp, c_i64, c_f32, c_i32, c_vp],
     ),
+    "rldx_attention_packed_segments_fwd_bf16": (
+        c_i32,
+        [c_vp, c_vp, c_i64p, c_vp, c_i32, c_i64p, c_i32] + [c_i64] * 6 + [c_i64p] + [c_vp, c_i64, c_f32, c_i32, c_vp],
+    ),
     "rldx_attention_packed_fwd_warm_bf16": (
         c_i32,
         [c_vp, c_vp, c_i64p, c_vp, c_i32] + [c_i64] * 6 + [c_i64p] * 2 + [c_vp, c_i64, c_f32, c_i32]

@@ -424,11 +424,16 @@ def kv_pack(k: torch.Tensor, v: torch.Tensor, layout: str = "bhsd") -> torch.Ten
 
 def attention_packed(q: torch.Tensor, kvp: torch.Tensor, seq_k: int, *, key_bias: Optional[torch.Tensor] = None,
                      causal: bool = False, scale: Optional[float] = None, layout: str = "bhsd",
-                     out=None, warm: Optional[Sequence[torch.Tensor]] = None):
+                     out=None, warm: Optional[Sequence[torch.Tensor]] = None,
+                     segments: Optional[Sequence[tuple]] = None):
     """Attention with K/V given as packed tiles [B, Hkv, >= kv_packed_elems(seq_k, D)]
     (see kv_pack; the MSAT QKV kernel writes them directly).  `out` may be a
     PackedAct [Sq, Hq*D] (batch 1), or a column view of a wider one: O is then
-    written in the grouped GEMM's packed activation order.  warm: up to three
+    written in the grouped GEMM's packed activation order.  segments (with a
+    PackedAct out, any batch): 1-3 (first query row, rows, first packed row)
+    triples; query row r of batch entry b inside a segment goes to packed row
+    first + b * rows + (r - first query row), rows outside every segment are
+    not stored (rldx_attention_packed_segments_fwd_bf16).  warm: up to three
     tensors (e.g. the packed weights of a later GEMM) whose memory extra
     workgroups of the launch read into the memory-side cache while it runs
     (rldx_attention_packed_fwd_warm_bf16; the attention result is unchanged)."""
@@ -446,10 +451,21 @@ def attention_packed(q: torch.Tensor, kvp: torch.Tensor, seq_k: int, *, key_bias
     Hkv = kvp.shape[1]
     _require(Hkv > 0 and Hq % Hkv == 0, "q heads must be a multiple of kv heads")
     packed_out = isinstance(out, PackedAct)
+    if segments is not None:
+        _require(packed_out and not warm, "segments need a PackedAct out (and no warm ranges)")
+        segments = [tuple(int(v) for v in sg) for sg in segments]
+        _require(1 <= len(segments) <= 3 and all(len(sg) == 3 for sg in segments),
+                 "segments: 1-3 (first query row, rows, first packed row) triples")
+        end = 0
+        for off, rows, base in segments:
+            _require(off >= end and rows >= 0 and base >= 0 and off + rows <= Sq and base + B * rows <= out.m,
+                     "segments must be ascending, disjoint, inside the queries and inside the packed out")
+            end = off + rows
     if packed_out:
         _on_gpu(out.data)
-        _require(B == 1 and out.m == Sq and out.k == Hq * D,
-                 "packed out must be a PackedAct [Sq, Hq*D] (or a column view of that width), batch 1")
+        _require(out.k == Hq * D and (segments is not None or (B == 1 and out.m == Sq)),
+                 "packed out must be a PackedAct [Sq, Hq*D] (or a column view of that width), batch 1, "
+                 "unless row segments map the batch into it")
         o_ptr, o_strides = out.data.data_ptr(), [0, 0, 0]
     else:
         if out is None:
@@ -465,7 +481,14 @@ def attention_packed(q: torch.Tensor, kvp: torch.Tensor, seq_k: int, *, key_bias
             (out.ld if out.ld != out.k else 1) if packed_out else 0, B, Hq, Hkv, Sq, seq_k, D,
             _lib.i64_array(_bhs_strides(q, layout)), _lib.i64_array(o_strides), kb_ptr, kb_stride, float(scale),
             int(bool(causal)))
-    if warm:
+    if segments is not None:
+        seg = _lib.i64_array([v for sg in segments for v in sg])
+        _lib.check(lib.rldx_attention_packed_segments_fwd_bf16(
+            q.data_ptr(), kvp.data_ptr(), _lib.i64_array([kvp.stride(0), kvp.stride(1)]), o_ptr,
+            out.ld if out.ld != out.k else 1, seg, len(segments), B, Hq, Hkv, Sq, seq_k, D,
+            _lib.i64_array(_bhs_strides(q, layout)), kb_ptr, kb_stride, float(scale), int(bool(causal)),
+            _stream_ptr(q)), "rldx_attention_packed_segments_fwd_bf16")
+    elif warm:
         ptrs, nbytes, count = _warm_args(warm, q.device)
         _lib.check(lib.rldx_attention_packed_fwd_warm_bf16(*args, ptrs, nbytes, count, _stream_ptr(q)),
                    "rldx_attention_packed_fwd_warm_bf16")

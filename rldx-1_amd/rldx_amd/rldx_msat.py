@@ -283,7 +283,12 @@ class RldxMsat:
     a 32-row block (the A operand of the P GEMMs): padding rows of Q/K/V are
     zero and their keys carry -inf."""
 
-    def __init__(self, sd: dict, cfg: RldxMsatCfg, device, bf16_quirk: bool = True, vl_mask: bool = False):
+    # packed weights and RoPE tables: shared by the chains of one model for every batch size
+    _WEIGHTS = ("w", "sa_ffn_p", "vl_ffn_p", "ds", "ss", "vl_proj_to_sa", "proj_out_2", "proj_out_physics_2",
+                "ds_cos", "ds_sin", "ss_cos", "ss_sin", "p_cos", "p_sin")
+
+    def __init__(self, sd: Optional[dict], cfg: RldxMsatCfg, device, bf16_quirk: bool = True, vl_mask: bool = False,
+                 batch: int = 1, weights_of: Optional["RldxMsat"] = None):
         self.cfg, self.dev = cfg, torch.device(device)
         H, D, inner = cfg.heads, cfg.head_dim, cfg.inner
         Fn._require(D in (64, 128), "head_dim must be 64 or 128")
@@ -299,6 +304,26 @@ class RldxMsat:
         self.nx = self.nv + cfg.n_sa                 # rows of the single-stream x = [VL->SA | time | SA]
         self.vl_mask = vl_mask
         self.masked = vl_mask or self.nv != cfg.n_vl or self.phys
+        self.bf16_quirk = bf16_quirk
+        Fn._require(int(batch) >= 1, "batch must be >= 1")
+        self.batch = int(batch)
+        if weights_of is None:
+            self._pack_weights(sd)
+        else:
+            Fn._require(weights_of.cfg == cfg and weights_of.dev == self.dev and weights_of.bf16_quirk == bf16_quirk,
+                        "weights_of must be a chain of the same configuration, device and RoPE tables")
+            for name in self._WEIGHTS:
+                setattr(self, name, getattr(weights_of, name, None))
+        self._alloc()
+
+    def for_batch(self, batch: int) -> "RldxMsat":
+        """A chain of this model for `batch` robots on the same packed weights
+        (nothing of them is copied): its own activation buffers, masks and plans."""
+        return RldxMsat(None, self.cfg, self.dev, self.bf16_quirk, self.vl_mask, batch=batch, weights_of=self)
+
+    def _pack_weights(self, sd: dict) -> None:
+        cfg, bf16_quirk = self.cfg, self.bf16_quirk
+        H, D, inner = cfg.heads, cfg.head_dim, cfg.inner
         for k, shape in cfg.param_shapes().items():
             Fn._require(k in sd, f"missing parameter {k}")
             Fn._require(tuple(sd[k].shape) == tuple(shape), f"{k}: shape {tuple(sd[k].shape)}, expected {shape}")
@@ -373,53 +398,68 @@ class RldxMsat:
         self.ss_cos, self.ss_sin = tables(ss_pos, rows=self.ns)
         if self.phys:
             self.p_cos, self.p_sin = tables(torch.arange(self.np_), axis0=1)
-        # activations
+        self.proj_out_physics_2 = Fn.pack_weight(w["proj_out_physics_2.weight"]) if self.phys else None
+
+    def _alloc(self) -> None:
+        """Activation buffers, masks and GEMM plans for self.batch robots.  Rows
+        of a batch: each stream's rows of every robot, robot after robot
+        (robot b's row r of a stream at b * rows + r), so that one GEMM covers a
+        stream for the whole batch; the joint attention writes its output back
+        into that order by row segments."""
+        cfg = self.cfg
+        H, D, inner = cfg.heads, cfg.head_dim, cfg.inner
+        B, nt = self.batch, cfg.num_temb_tokens
         N, nv, ns, nx, npp = self.N, self.nv, cfg.n_sa, self.nx, self.np_
         ebuf = lambda *s: torch.empty(*s, dtype=BF16, device=self.dev)  # noqa: E731
-        # x = [VL->SA | time | SA] of the single-stream blocks; its SA rows are the SA residual stream of the
-        # double-stream blocks (no copy between the two)
-        self.x = ebuf(nx, cfg.sa_dim)
-        self.x_sa, self.x_vl = self.x[nv:], ebuf(nv, cfg.vl_dim)
-        self.h_sa, self.h_vl = Fn.PackedAct.empty(ns, cfg.sa_dim, self.dev), Fn.PackedAct.empty(nv, cfg.vl_dim,
-                                                                                                 self.dev)
-        # QKV rows of SA: self.ns rows, the GEMM writes the first n_sa, padding rows stay zero
-        self.qkv_sa_buf = torch.zeros(self.ns, 3 * inner, dtype=BF16, device=self.dev)
-        self.qkv_sa, self.qkv_vl = self.qkv_sa_buf[:ns], ebuf(nv, 3 * inner)
-        self.q = ebuf(H, N, D)
-        self.kvp = ebuf(H, Fn.kv_packed_elems(N, D))
-        self.att = Fn.PackedAct.empty(N, inner, self.dev)
-        self.gl_sa = Fn.PackedAct.empty(ns, self.sa_ffn_p, self.dev)
-        self.gl_vl = Fn.PackedAct.empty(nv, self.vl_ffn_p, self.dev)
-        self.vl_packed = Fn.PackedAct.empty(nv, cfg.vl_dim, self.dev)
-        self.h = Fn.PackedAct.empty(nx, cfg.sa_dim, self.dev)
-        self.qkv_buf = torch.zeros(nv + self.ns, 3 * inner, dtype=BF16, device=self.dev)
-        self.qkv = self.qkv_buf[:nx]
-        self.gl = Fn.PackedAct.empty(nx, cfg.ss_expanded, self.dev)
-        self.cat = Fn.PackedAct.empty(N, inner + cfg.ss_hidden, self.dev)
-        self.mod = ebuf(cfg.n_sa_pure, cfg.sa_dim)
-        self.mod_packed = Fn.PackedAct.empty(cfg.n_sa_pure, cfg.sa_dim, self.dev)
-        self.out = ebuf(1, cfg.n_sa_pure, cfg.output_dim)
-        self.inputs = dict(sa=ebuf(1, cfg.n_sa_pure, cfg.sa_dim), vl=ebuf(1, cfg.n_vl, cfg.vl_dim),
-                           temb=ebuf(1, inner), time_token=ebuf(1, nt, cfg.sa_dim))
+        # x = [VL->SA | time | SA] of the single-stream blocks (B nv rows, then B n_sa); its SA rows are the SA
+        # residual stream of the double-stream blocks (no copy between the two)
+        self.x = ebuf(B * nx, cfg.sa_dim)
+        self.x_sa, self.x_vl = self.x[B * nv:], ebuf(B * nv, cfg.vl_dim)
+        self.h_sa = Fn.PackedAct.empty(B * ns, cfg.sa_dim, self.dev)
+        self.h_vl = Fn.PackedAct.empty(B * nv, cfg.vl_dim, self.dev)
+        # QKV rows of SA: the GEMM writes B n_sa rows; robot b's joint sequence reads self.ns rows from b n_sa,
+        # so with a P stream its padding rows are the next robot's first rows (their keys are masked and their
+        # outputs not stored) or, for the last robot, the zero rows at the end
+        self.qkv_sa_buf = torch.zeros(B * ns + self.ns - ns, 3 * inner, dtype=BF16, device=self.dev)
+        self.qkv_sa, self.qkv_vl = self.qkv_sa_buf[:B * ns], ebuf(B * nv, 3 * inner)
+        self.q = ebuf(B, H, N, D)
+        self.kvp = ebuf(B, H, Fn.kv_packed_elems(N, D))
+        # attention output (and the single blocks' [attention | MLP] operand): B nv VL rows, B n_sa SA rows,
+        # then from the next 32-row block (pa) B np P rows
+        self.pa = _round_up(B * (nv + ns), 32)
+        self.segments = [(0, nv, 0), (nv, ns, B * nv)] + ([(self.p0, npp, self.pa)] if self.phys else [])
+        self.att = Fn.PackedAct.empty(self.pa + B * npp, inner, self.dev)
+        self.gl_sa = Fn.PackedAct.empty(B * ns, self.sa_ffn_p, self.dev)
+        self.gl_vl = Fn.PackedAct.empty(B * nv, self.vl_ffn_p, self.dev)
+        self.vl_packed = Fn.PackedAct.empty(B * nv, cfg.vl_dim, self.dev)
+        self.h = Fn.PackedAct.empty(B * nx, cfg.sa_dim, self.dev)
+        self.qkv_buf = torch.zeros(B * nx + self.ns - ns, 3 * inner, dtype=BF16, device=self.dev)
+        self.qkv = self.qkv_buf[:B * nx]
+        self.gl = Fn.PackedAct.empty(B * nx, cfg.ss_expanded, self.dev)
+        self.cat = Fn.PackedAct.empty(self.pa + B * npp, inner + cfg.ss_hidden, self.dev)
+        self.mod = ebuf(B * cfg.n_sa_pure, cfg.sa_dim)
+        self.mod_packed = Fn.PackedAct.empty(B * cfg.n_sa_pure, cfg.sa_dim, self.dev)
+        self.out = ebuf(B, cfg.n_sa_pure, cfg.output_dim)
+        self.inputs = dict(sa=ebuf(B, cfg.n_sa_pure, cfg.sa_dim), vl=ebuf(B, cfg.n_vl, cfg.vl_dim),
+                           temb=ebuf(B, inner), time_token=ebuf(B, nt, cfg.sa_dim))
         if self.phys:
-            self.x_p = ebuf(npp, cfg.sa_dim)
-            self.h_p = Fn.PackedAct.empty(npp, cfg.sa_dim, self.dev)
-            self.qkv_p = ebuf(npp, 3 * inner)
-            self.gl_p = Fn.PackedAct.empty(npp, self.sa_ffn_p, self.dev)
-            self.gl_p_ss = Fn.PackedAct.empty(npp, cfg.ss_expanded, self.dev)
-            self.mod_p = ebuf(npp, cfg.sa_dim)
-            self.mod_p_packed = Fn.PackedAct.empty(npp, cfg.sa_dim, self.dev)
-            self.out_p = ebuf(1, npp, cfg.output_dim)
-            self.proj_out_physics_2 = Fn.pack_weight(w["proj_out_physics_2.weight"])
-            self.inputs["p"] = ebuf(1, npp, cfg.sa_dim)
-        if vl_mask:
-            self.inputs["vl_mask"] = torch.ones(1, cfg.n_vl, dtype=torch.float32, device=self.dev)
+            self.x_p = ebuf(B * npp, cfg.sa_dim)
+            self.h_p = Fn.PackedAct.empty(B * npp, cfg.sa_dim, self.dev)
+            self.qkv_p = ebuf(B * npp, 3 * inner)
+            self.gl_p = Fn.PackedAct.empty(B * npp, self.sa_ffn_p, self.dev)
+            self.gl_p_ss = Fn.PackedAct.empty(B * npp, cfg.ss_expanded, self.dev)
+            self.mod_p = ebuf(B * npp, cfg.sa_dim)
+            self.mod_p_packed = Fn.PackedAct.empty(B * npp, cfg.sa_dim, self.dev)
+            self.out_p = ebuf(B, npp, cfg.output_dim)
+            self.inputs["p"] = ebuf(B, npp, cfg.sa_dim)
+        if self.vl_mask:
+            self.inputs["vl_mask"] = torch.ones(B, cfg.n_vl, dtype=torch.float32, device=self.dev)
             if self.phys:
-                self.inputs["physics_mask"] = torch.ones(1, dtype=torch.float32, device=self.dev)
-        # additive key bias over the N attention rows: 0, or -inf on padding, masked VL and masked P keys
-        self.key_bias = torch.zeros(N, dtype=torch.float32, device=self.dev)
-        self.key_bias[cfg.n_vl:nv] = float("-inf")
-        self.key_bias[nv + ns:self.p0] = float("-inf")
+                self.inputs["physics_mask"] = torch.ones(B, dtype=torch.float32, device=self.dev)
+        # additive key bias of each robot's N attention rows: 0, or -inf on padding, masked VL and masked P keys
+        self.key_bias = torch.zeros(B, N, dtype=torch.float32, device=self.dev)
+        self.key_bias[:, cfg.n_vl:nv] = float("-inf")
+        self.key_bias[:, nv + ns:self.p0] = float("-inf")
         self._ninf = torch.full((), float("-inf"), dtype=torch.float32, device=self.dev)
         self._zero = torch.zeros((), dtype=torch.float32, device=self.dev)
         self.graph = None
@@ -430,11 +470,12 @@ class RldxMsat:
         self.ds_gemms = [self._ds_gemm_items(blk) for blk in self.ds]
         self.ss_gemms = [self._ss_gemm_items(blk) for blk in self.ss]
         self.vl_proj_gemm = self._planned(
-            [(self.vl_packed, self.vl_proj_to_sa, self.w["vl_proj_to_sa.bias"], self.x[:nv], None)], "bias")
-        out_items = [(self.mod_packed, self.proj_out_2, self.w["proj_out_2.bias"], self.out[0], None)]
+            [(self.vl_packed, self.vl_proj_to_sa, self.w["vl_proj_to_sa.bias"], self.x[:B * nv], None)], "bias")
+        out_items = [(self.mod_packed, self.proj_out_2, self.w["proj_out_2.bias"],
+                      self.out.view(B * cfg.n_sa_pure, cfg.output_dim), None)]
         if self.phys:
             out_items.append((self.mod_p_packed, self.proj_out_physics_2, self.w["proj_out_physics_2.bias"],
-                              self.out_p[0], None))
+                              self.out_p.view(B * npp, cfg.output_dim), None))
         self.out_gemm = self._planned(out_items, "bias")
         plans = [g for d in self.ds_gemms + self.ss_gemms for g in d.values()] + [self.vl_proj_gemm, self.out_gemm]
         self.ws = Fn.GemmWorkspace(max(Fn.grouped_gemm_workspace_bytes(it, epi, sk, wide) for it, epi, sk, wide in plans),
@@ -497,7 +538,9 @@ class RldxMsat:
         return {name: self._joined(g["sa_" + name], g["vl_" + name]) for name in ("qkv", "proj", "w12", "w3")}
 
     def _ds_gemm_pairs(self, blk: dict) -> dict:
-        nv, ns, p0, N = self.nv, self.cfg.n_sa, self.p0, self.N
+        B, nv, ns, pa, npp = self.batch, self.nv, self.cfg.n_sa, self.pa, self.np_
+        att_vl, att_sa, att_p = self.att.rows(0, B * nv), self.att.rows(B * nv, B * (nv + ns)), self.att.rows(
+            pa, pa + B * npp)
 
         def grp(sa_item, p_item):
             return [sa_item, p_item] if self.phys else [sa_item]
@@ -507,12 +550,11 @@ class RldxMsat:
             "sa_qkv": self._planned(grp((self.h_sa, blk["sa_qkv"], blk["sa_qkv.bias"], self.qkv_sa, None),
                                         P and (self.h_p, blk["p_qkv"], blk["p_qkv.bias"], self.qkv_p, None)), "bias"),
             "vl_qkv": self._planned([(self.h_vl, blk["vl_qkv"], blk["vl_qkv.bias"], self.qkv_vl, None)], "bias"),
-            "sa_proj": self._planned(grp((self.att.rows(nv, nv + ns), blk["sa_proj"], blk["sa_proj.bias"], self.x_sa,
-                                          self.x_sa),
-                                         P and (self.att.rows(p0, N), blk["p_proj"], blk["p_proj.bias"], self.x_p,
-                                                self.x_p)), "residual"),
-            "vl_proj": self._planned([(self.att.rows(0, nv), blk["vl_proj"], blk["vl_proj.bias"], self.x_vl,
-                                       self.x_vl)], "residual"),
+            "sa_proj": self._planned(grp((att_sa, blk["sa_proj"], blk["sa_proj.bias"], self.x_sa, self.x_sa),
+                                         P and (att_p, blk["p_proj"], blk["p_proj.bias"], self.x_p, self.x_p)),
+                                     "residual"),
+            "vl_proj": self._planned([(att_vl, blk["vl_proj"], blk["vl_proj.bias"], self.x_vl, self.x_vl)],
+                                     "residual"),
             "sa_w12": self._planned(grp((self.h_sa, blk["sa_w12"], blk["sa_w12.bias"], self.gl_sa, None),
                                         P and (self.h_p, blk["p_w12"], blk["p_w12.bias"], self.gl_p, None)),
                                     "swiglu_packed"),
@@ -527,8 +569,8 @@ class RldxMsat:
 
     def _ss_gemm_items(self, blk: dict) -> dict:
         inner, hs = self.cfg.inner, self.cfg.ss_hidden
-        nx, p0, N = self.nx, self.p0, self.N
-        cx, cp = self.cat.rows(0, nx), (self.cat.rows(p0, N) if self.phys else None)
+        B, nx, pa = self.batch, self.nx, self.pa
+        cx, cp = self.cat.rows(0, B * nx), (self.cat.rows(pa, pa + B * self.np_) if self.phys else None)
 
         def grp(x_item, p_item):
             return [x_item, p_item] if self.phys else [x_item]
@@ -558,19 +600,30 @@ class RldxMsat:
     def _kb(self):
         return self.key_bias if self.masked else None
 
+    def _qkv_norm_rope(self, streams) -> None:
+        """Q and the packed K/V tiles of every robot's joint sequence from the QKV
+        rows of its streams: streams = [(qkv rows of the whole batch, rows per
+        robot, rows in the joint sequence, q_norm, k_norm, cos, sin)] in joint
+        order; one launch per robot."""
+        cfg = self.cfg
+        for b in range(self.batch):
+            specs = [Fn.StreamSpec(qkv[b * per:b * per + rows], qn, kn, cos, sin)
+                     for qkv, per, rows, qn, kn, cos, sin in streams]
+            Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q[b], self.kvp[b]), kv_packed=True)
+
     def _ds_block(self, blk: dict, gm: dict) -> None:
         cfg = self.cfg
-        N = self.N
+        nv, ns = self.nv, cfg.n_sa
         Fn.layernorm_pack_many(self.ds_norms, cfg.eps)
         self._gemm(gm["qkv"])
-        specs = [Fn.StreamSpec(self.qkv_vl, blk["q_norm_vl.weight"], blk["k_norm_vl.weight"]),
-                 Fn.StreamSpec(self.qkv_sa_buf, blk["q_norm_sa.weight"], blk["k_norm_sa.weight"], self.ds_cos,
-                               self.ds_sin)]
+        streams = [(self.qkv_vl, nv, nv, blk["q_norm_vl.weight"], blk["k_norm_vl.weight"], None, None),
+                   (self.qkv_sa_buf, ns, self.ns, blk["q_norm_sa.weight"], blk["k_norm_sa.weight"], self.ds_cos,
+                    self.ds_sin)]
         if self.phys:
-            specs.append(Fn.StreamSpec(self.qkv_p, blk["q_norm_p.weight"], blk["k_norm_p.weight"], self.p_cos,
-                                       self.p_sin))
-        Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
-        Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), N, key_bias=self._kb(), out=self.att)
+            streams.append((self.qkv_p, self.np_, self.np_, blk["q_norm_p.weight"], blk["k_norm_p.weight"], self.p_cos,
+                            self.p_sin))
+        self._qkv_norm_rope(streams)
+        Fn.attention_packed(self.q, self.kvp, self.N, key_bias=self._kb(), out=self.att, segments=self.segments)
         self._gemm(gm["proj"])
         Fn.layernorm_pack_many(self.ds_norms, cfg.eps)
         self._gemm(gm["w12"])
@@ -578,17 +631,17 @@ class RldxMsat:
 
     def _ss_block(self, blk: dict, gm: dict) -> None:
         cfg = self.cfg
-        nv, N, inner = self.nv, self.N, cfg.inner
+        B, nv, ns, inner = self.batch, self.nv, cfg.n_sa, cfg.inner
         Fn.layernorm_pack_many(self.ss_norms, cfg.eps)
         self._gemm(gm["qkv"])
         self._gemm(gm["mlp"])
-        specs = [Fn.StreamSpec(self.qkv_buf[:nv], blk["q_norm"], blk["k_norm"]),
-                 Fn.StreamSpec(self.qkv_buf[nv:nv + self.ns], blk["q_norm"], blk["k_norm"], self.ss_cos, self.ss_sin)]
+        streams = [(self.qkv_buf, nv, nv, blk["q_norm"], blk["k_norm"], None, None),
+                   (self.qkv_buf[B * nv:], ns, self.ns, blk["q_norm"], blk["k_norm"], self.ss_cos, self.ss_sin)]
         if self.phys:
-            specs.append(Fn.StreamSpec(self.qkv_p, blk["p_q_norm"], blk["p_k_norm"], self.p_cos, self.p_sin))
-        Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True)
-        Fn.attention_packed(self.q.unsqueeze(0), self.kvp.unsqueeze(0), N, key_bias=self._kb(),
-                            out=self.cat.cols(0, inner))
+            streams.append((self.qkv_p, self.np_, self.np_, blk["p_q_norm"], blk["p_k_norm"], self.p_cos, self.p_sin))
+        self._qkv_norm_rope(streams)
+        Fn.attention_packed(self.q, self.kvp, self.N, key_bias=self._kb(), out=self.cat.cols(0, inner),
+                            segments=self.segments)
         self._gemm(gm["mlp_proj"])
         self._gemm(gm["linear2"])
 
@@ -597,72 +650,76 @@ class RldxMsat:
                 time_token: torch.Tensor, encoder_attention_mask: Optional[torch.Tensor] = None,
                 physics_embs: Optional[torch.Tensor] = None, physics_attention_mask: Optional[torch.Tensor] = None,
                 adaln: Optional[tuple] = None):
-        """CustomOpMSAT.forward (custom_msat_chain.py:109-126): hidden_states
-        [1, n_sa_pure, sa_dim], encoder_hidden_states [1, n_vl, vl_dim], temb
-        [1, inner], time_token [1, num_temb_tokens, sa_dim] -> [1, n_sa_pure,
-        output_dim] (a static buffer, overwritten by the next call).
-        encoder_attention_mask [1, n_vl] (1 = visible, 0 = masked; a chain built
+        """CustomOpMSAT.forward (custom_msat_chain.py:109-126) for the chain's
+        batch of B robots: hidden_states [B, n_sa_pure, sa_dim],
+        encoder_hidden_states [B, n_vl, vl_dim], temb [B, inner], time_token
+        [B, num_temb_tokens, sa_dim] -> [B, n_sa_pure, output_dim] (a static
+        buffer, overwritten by the next call).  Robots do not interact: each
+        one's joint attention runs over its own tokens.
+        encoder_attention_mask [B, n_vl] (1 = visible, 0 = masked; a chain built
         with vl_mask=True): masks VL keys in every block as the eager MSAT does
         (msat.py:517-531, blocks.py:558-575); None = every VL token visible.
         With a P stream (CustomOpExpandedMSAT.forward,
-        custom_expanded_msat_chain.py:87-115): physics_embs [1, n_physics,
-        sa_dim] is required and the result is {"action": [1, n_sa_pure,
-        output_dim], "physics": [1, n_physics, output_dim]};
-        physics_attention_mask [1] (1 = visible; a chain built with
-        vl_mask=True) masks every P key (msat.py:716-743).  adaln: the output
-        AdaLN's (shift, scale[, physics shift, physics scale]) for this temb,
-        precomputed with adaln_of(temb) (None: computed here)."""
+        custom_expanded_msat_chain.py:87-115): physics_embs [B, n_physics,
+        sa_dim] is required and the result is {"action": [B, n_sa_pure,
+        output_dim], "physics": [B, n_physics, output_dim]};
+        physics_attention_mask [B] (1 = visible; a chain built with
+        vl_mask=True) masks every P key of a robot (msat.py:716-743).  adaln: the
+        output AdaLN's (shift, scale[, physics shift, physics scale]) for this
+        temb, precomputed with adaln_of(temb) (None: computed here)."""
         cfg = self.cfg
-        nt, nv = cfg.num_temb_tokens, cfg.n_vl
-        Fn._require(tuple(hidden_states.shape) == (1, cfg.n_sa_pure, cfg.sa_dim) and
-                    tuple(encoder_hidden_states.shape) == (1, nv, cfg.vl_dim) and
-                    tuple(temb.shape) == (1, cfg.inner) and tuple(time_token.shape) == (1, nt, cfg.sa_dim),
-                    "input shapes do not match the chain's configuration (batch 1)")
+        B, nt, nv, d = self.batch, cfg.num_temb_tokens, cfg.n_vl, cfg.sa_dim
+        Fn._require(tuple(hidden_states.shape) == (B, cfg.n_sa_pure, d) and
+                    tuple(encoder_hidden_states.shape) == (B, nv, cfg.vl_dim) and
+                    tuple(temb.shape) == (B, cfg.inner) and tuple(time_token.shape) == (B, nt, d),
+                    f"input shapes do not match the chain's configuration (batch {B})")
         if self.phys:
-            Fn._require(physics_embs is not None and tuple(physics_embs.shape) == (1, self.np_, cfg.sa_dim),
-                        "physics_embs must be [1, n_physics, sa_dim] for a chain with a P stream")
+            Fn._require(physics_embs is not None and tuple(physics_embs.shape) == (B, self.np_, d),
+                        "physics_embs must be [B, n_physics, sa_dim] for a chain with a P stream")
         else:
             Fn._require(physics_embs is None and physics_attention_mask is None,
                         "physics inputs need a chain built with use_physics and n_physics > 0")
         if self.vl_mask:
             if encoder_attention_mask is None:
-                self.key_bias[:nv].zero_()
+                self.key_bias[:, :nv].zero_()
             else:
-                Fn._require(tuple(encoder_attention_mask.shape) == (1, nv), "encoder_attention_mask must be [1, n_vl]")
-                torch.where(encoder_attention_mask[0] == 0, self._ninf, self._zero, out=self.key_bias[:nv])
+                Fn._require(tuple(encoder_attention_mask.shape) == (B, nv), "encoder_attention_mask must be [B, n_vl]")
+                torch.where(encoder_attention_mask == 0, self._ninf, self._zero, out=self.key_bias[:, :nv])
             if self.phys:
                 if physics_attention_mask is None:
-                    self.key_bias[self.p0:].zero_()
+                    self.key_bias[:, self.p0:].zero_()
                 else:
-                    Fn._require(physics_attention_mask.numel() == 1, "physics_attention_mask must be [1]")
-                    torch.where(physics_attention_mask.reshape(1).expand(self.np_) == 0, self._ninf, self._zero,
-                                out=self.key_bias[self.p0:])
+                    Fn._require(physics_attention_mask.numel() == B, "physics_attention_mask must be [B]")
+                    torch.where(physics_attention_mask.reshape(B, 1).expand(B, self.np_) == 0, self._ninf, self._zero,
+                                out=self.key_bias[:, self.p0:])
         else:
             Fn._require(encoder_attention_mask is None and physics_attention_mask is None,
                         "attention masks need a chain built with vl_mask=True")
-        self.x_sa[:nt].copy_(time_token[0])
-        self.x_sa[nt:].copy_(hidden_states[0])
-        self.x_vl[:nv].copy_(encoder_hidden_states[0])
+        x_sa = self.x_sa.view(B, cfg.n_sa, d)
+        x_sa[:, :nt].copy_(time_token)
+        x_sa[:, nt:].copy_(hidden_states)
+        x_vl = self.x_vl.view(B, self.nv, cfg.vl_dim)
+        x_vl[:, :nv].copy_(encoder_hidden_states)
         if self.nv > nv:
-            self.x_vl[nv:].zero_()
+            x_vl[:, nv:].zero_()
         if self.phys:
-            self.x_p.copy_(physics_embs[0])
+            self.x_p.view(B, self.np_, d).copy_(physics_embs)
         for blk, gm in zip(self.ds, self.ds_gemms):
             self._ds_block(blk, gm)
         # x = [vl_proj_to_sa(vl) | time token | SA]
         Fn.pack_act(self.x_vl, out=self.vl_packed)
-        self._gemm(self.vl_proj_gemm)  # rows [0, nv) of x; rows [nv, nx) already hold the SA stream
+        self._gemm(self.vl_proj_gemm)  # rows [0, B nv) of x; rows [B nv, B nx) already hold the SA stream
         for blk, gm in zip(self.ss, self.ss_gemms):
             self._ss_block(blk, gm)
         # AdaLN output projections (msat.py:771-781)
         shift, scale, *pmod = self.adaln_of(temb) if adaln is None else adaln
-        sa = F.layer_norm(self.x[self.nx - cfg.n_sa_pure:], (cfg.sa_dim,), eps=1e-6)
-        torch.add(sa * (1 + scale), shift, out=self.mod)
+        sa = F.layer_norm(x_sa[:, nt:], (d,), eps=1e-6)
+        torch.add(sa * (1 + scale[:, None]), shift[:, None], out=self.mod.view(B, cfg.n_sa_pure, d))
         Fn.pack_act(self.mod, out=self.mod_packed)
         if self.phys:
             pshift, pscale = pmod
-            ph = F.layer_norm(self.x_p, (cfg.sa_dim,), eps=1e-6)
-            torch.add(ph * (1 + pscale), pshift, out=self.mod_p)
+            ph = F.layer_norm(self.x_p.view(B, self.np_, d), (d,), eps=1e-6)
+            torch.add(ph * (1 + pscale[:, None]), pshift[:, None], out=self.mod_p.view(B, self.np_, d))
             Fn.pack_act(self.mod_p, out=self.mod_p_packed)
         self._gemm(self.out_gemm)
         if self.phys:
@@ -672,7 +729,7 @@ class RldxMsat:
     __call__ = forward
 
     def adaln_of(self, temb: torch.Tensor) -> tuple:
-        """(shift, scale) of the output AdaLN for `temb` [1, inner] (and the physics
+        """(shift, scale) of the output AdaLN for `temb` [B, inner] (and the physics
         output's pair with a P stream): F.silu(temb) -> proj_out_1 (msat.py:771-781).
         A caller whose temb is fixed per step (the action head's static time
         embeddings) computes them once and passes them to forward(adaln=...)."""
@@ -738,8 +795,11 @@ class MsatDispatcher:
     * later calls compute temb / the time token with the module's own
       timestep_encoder / time_token_proj, copy every input into the chain's
       static buffers and run (or replay) the chain;
+    * a batch of B robots runs on a chain for B (RldxMsat.for_batch: the
+      same packed weights, its own buffers and, with graph=True, its own
+      graph), built on the first call of that batch size; up to max_batch;
     * calls the chain does not serve go to the module's own forward:
-      return_all_hidden_states=True, a batch other than 1, or token counts
+      return_all_hidden_states=True, a batch above max_batch, or token counts
       (VL, SA or physics) other than the chain's (shape drift would corrupt
       the static buffers);
     * a failure while building or running switches the dispatcher to the
@@ -759,11 +819,12 @@ class MsatDispatcher:
     the next call."""
 
     def __init__(self, msat: torch.nn.Module, bf16_quirk: Optional[bool] = None, graph: bool = False,
-                 verbose: bool = False, check_weights: bool = False):
+                 verbose: bool = False, check_weights: bool = False, max_batch: int = 16):
         self.msat, self.orig = msat, msat.forward
         self.bf16_quirk, self.graph, self.verbose = bf16_quirk, graph, verbose
-        self.check_weights = check_weights
-        self.chain: Optional[RldxMsat] = None
+        self.check_weights, self.max_batch = check_weights, int(max_batch)
+        self.chain: Optional[RldxMsat] = None   # the first chain built (batch 1), owner of the packed weights
+        self.chains: dict = {}                  # batch size -> chain on those weights
         self.failed = False
         self.served = 0      # calls run on the chain
         self.fallbacks = 0   # calls sent to the module's own forward
@@ -782,10 +843,11 @@ class MsatDispatcher:
         return any(t is not u or t.data_ptr() != p or t._version != v for (t, p, v), u in zip(self._stamp, cur))
 
     def refresh(self) -> None:
-        """Drop the chain; the next call rebuilds it from the module's current weights."""
+        """Drop the chains; the next call rebuilds them from the module's current weights."""
         if self.chain is not None:
             self.rebuilds += 1
         self.chain = None
+        self.chains = {}
         self._stamp = None
 
     def _log(self, msg: str) -> None:
@@ -797,18 +859,32 @@ class MsatDispatcher:
         if self.graph:
             chain.capture()
         self.chain = chain
+        self.chains = {1: chain}
         self._dims = (n_vl, n_sa_pure, n_physics)
         self._stamp = self._weights_stamp()
         return chain
+
+    def chain_for(self, batch: int) -> RldxMsat:
+        """The chain for `batch` robots, built on the weights of self.chain when first needed."""
+        c = self.chains.get(batch)
+        if c is None:
+            c = self.chain.for_batch(batch)
+            if self.graph:
+                c.capture()
+            self.chains[batch] = c
+        return c
 
     def _unserved(self, hidden_states, encoder_hidden_states, return_all_hidden_states, physics_embs,
                   physics_attention_mask) -> Optional[str]:
         if return_all_hidden_states:
             return "return_all_hidden_states"
-        if hidden_states.dim() != 3 or hidden_states.shape[0] != 1 or encoder_hidden_states.shape[0] != 1:
-            return "batch other than 1"
-        if physics_embs is not None and physics_embs.shape[0] != 1:
-            return "batch other than 1"
+        B = hidden_states.shape[0] if hidden_states.dim() == 3 else -1
+        if B < 1 or encoder_hidden_states.dim() != 3 or encoder_hidden_states.shape[0] != B:
+            return "inputs are not [B, tokens, width] with one batch size"
+        if B > self.max_batch:
+            return f"batch above max_batch ({self.max_batch})"
+        if physics_embs is not None and (physics_embs.dim() != 3 or physics_embs.shape[0] != B):
+            return "inputs are not [B, tokens, width] with one batch size"
         c = self.chain
         if c is not None and (encoder_hidden_states.shape[1] != c.cfg.n_vl or hidden_states.shape[1] != c.cfg.n_sa_pure
                               or self._n_physics(physics_embs) != c.np_):
@@ -848,7 +924,8 @@ class MsatDispatcher:
                 self._log(f"build failed ({e}); the module's own forward serves every call")
             return out
         try:
-            c = self.chain
+            c = self.chain_for(hidden_states.shape[0])
+            B = c.batch
             msat = self.msat
             temb = msat.timestep_encoder(timestep)
             tt = msat.time_token_proj(temb).unsqueeze(1).repeat(1, c.cfg.num_temb_tokens, 1)
@@ -863,13 +940,13 @@ class MsatDispatcher:
                 if mask is None:
                     i["vl_mask"].fill_(1.0)
                 else:
-                    i["vl_mask"].copy_(mask.reshape(1, -1))
+                    i["vl_mask"].copy_(mask.reshape(B, -1))
                 if c.phys:
                     i["p"].copy_(p_embs)
                     if p_mask is None:
                         i["physics_mask"].fill_(1.0)
                     else:
-                        i["physics_mask"].copy_(p_mask.reshape(1))
+                        i["physics_mask"].copy_(p_mask.reshape(B))
                 out = c.replay()
             else:
                 out = c.forward(hidden_states, encoder_hidden_states, temb, tt, mask, p_embs, p_mask)
@@ -884,7 +961,7 @@ class MsatDispatcher:
 
 def install(msat: torch.nn.Module, n_vl: Optional[int] = None, n_sa_pure: Optional[int] = None,
             bf16_quirk: Optional[bool] = None, graph: bool = False, verbose: bool = False,
-            n_physics: int = 0, check_weights: bool = False) -> MsatDispatcher:
+            n_physics: int = 0, check_weights: bool = False, max_batch: int = 16) -> MsatDispatcher:
     """Route a live MSAT module's forward through an MsatDispatcher (what the
     reference's path-D dispatcher does with CustomOpMSAT,
     rldx/inference/serve_optimization.py:251-601).  With n_vl and n_sa_pure the
@@ -897,7 +974,8 @@ def install(msat: torch.nn.Module, n_vl: Optional[int] = None, n_sa_pure: Option
     from the RoPE buffers (real-valued: the model was cast to bf16).
     msat.load_state_dict is wrapped so that new weights drop the chain (rebuilt
     on the next call); check_weights=True also catches in-place updates."""
-    d = MsatDispatcher(msat, bf16_quirk=bf16_quirk, graph=graph, verbose=verbose, check_weights=check_weights)
+    d = MsatDispatcher(msat, bf16_quirk=bf16_quirk, graph=graph, verbose=verbose, check_weights=check_weights,
+                       max_batch=max_batch)
     if n_vl is not None and n_sa_pure is not None:
         d.build(n_vl, n_sa_pure, n_physics)
     msat.forward = d

@@ -155,6 +155,18 @@ def test_capi_rejects_bad_arguments_without_launching():
     assert lib.rldx_attention_packed_fwd_bf16(16, 16, ps, 16, 1, 2, 2, 2, 4, 32, 128, st, st, None, 0, 1.0, 0,
                                               None) == HIP_INVALID_VALUE
     assert lib.rldx_attention_kv_pack_bf16(16, st, 16, st, 16, ps, 1, 1, 40, 128, None) == HIP_INVALID_VALUE
+    # row segments of a packed output: rejected before any launch when absent, out of order, overlapping,
+    # past seq_q, without a packed output, or mapping a packed row past 2^31
+    ps2 = _lib.i64_array([12 * 64 * 128 * 19, 64 * 128 * 19])
+
+    def seg_call(segs, out_packed=1, batch=3):
+        flat = _lib.i64_array([v for sg in segs for v in sg]) if segs else None
+        return lib.rldx_attention_packed_segments_fwd_bf16(16, 16, ps2, 16, out_packed, flat, len(segs), batch, 12,
+                                                          12, 608, 608, 128, st, None, 0, 1.0, 0, None)
+    for segs in ([], [(0, 512, 0), (500, 64, 1536)], [(512, 64, 0), (0, 512, 192)], [(0, 600, 0), (600, 9, 1800)],
+                 [(-1, 4, 0)], [(0, 4, -32)], [(0, 4, 0)] * 4, [(0, 608, (1 << 31) - 1000)]):
+        assert seg_call(segs) == HIP_INVALID_VALUE, segs
+    assert seg_call([(0, 512, 0)], out_packed=0) == HIP_INVALID_VALUE
     assert lib.rldx_msat_qkv_norm_rope_bf16(None, 1, 12, 128, 16, 16, 16, 0, 0, None, 0, 1e-6,
                                             None) == HIP_INVALID_VALUE
     s = _lib.MsatStream(16, 100, 4, 16, 16, None, None, 0)  # row stride < 3*H*D

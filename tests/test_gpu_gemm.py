@@ -386,6 +386,44 @@ def test_attention_packed_output(dev):
     assert torch.equal(op.unpack(), o.view(S, H * D))
 
 
+@pytest.mark.parametrize("H,D,S,segs", [(12, 128, 608, [(0, 512), (512, 56), (576, 32)]),
+                                        (24, 64, 96, [(0, 64), (64, 17)]),
+                                        (24, 64, 82, [(0, 82)])])
+def test_attention_packed_segments_batch(dev, H, D, S, segs):
+    """rldx_attention_packed_segments_fwd_bf16: three robots' joint sequences
+    whose output rows go to one packed matrix stream by stream (a segment's
+    rows of robot 0, then robot 1, ..., each segment from a 32-row block;
+    rows between the segments, the padding of a stream, not stored) equal
+    the strided output of the same attention row for row, bit for bit, and
+    packed rows that no segment maps keep their contents."""
+    B = 3
+    g = torch.Generator().manual_seed(23)
+    q = torch.randn(B, H, S, D, generator=g).to(BF16).to(dev)
+    k = torch.randn(B, H, S, D, generator=g).to(BF16).to(dev)
+    v = torch.randn(B, H, S, D, generator=g).to(BF16).to(dev)
+    bias = torch.zeros(B, S)
+    for b in range(B):  # a different set of masked keys per robot
+        bias[b, S - 4 - 3 * b:S - 3 * b] = float("-inf")
+    bias = bias.to(dev)
+    kvp = Fn.kv_pack(k, v)
+    o = torch.empty(B, S, H, D, dtype=BF16, device=dev)
+    Fn.attention_packed(q, kvp, S, key_bias=bias, out=o.permute(0, 2, 1, 3))
+    full, base = [], 0
+    for off, rows in segs:
+        full.append((off, rows, base))
+        base = (base + B * rows + 31) // 32 * 32
+    m = full[-1][2] + B * full[-1][1]
+    pk = Fn.PackedAct.empty(m, H * D, dev)
+    pk.data.fill_(7.0)
+    Fn.attention_packed(q, kvp, S, key_bias=bias, out=pk, segments=full)
+    expect = torch.full((m, H * D), 7.0, dtype=BF16)
+    oc = o.cpu()
+    for off, rows, first in full:
+        for b in range(B):
+            expect[first + b * rows:first + (b + 1) * rows] = oc[b, off:off + rows].reshape(rows, H * D)
+    assert torch.equal(pk.unpack().cpu().view(torch.int16), expect.view(torch.int16))
+
+
 @pytest.mark.parametrize("warm_sizes", [(4_718_592, 4_718_592, 4_718_592), (1000,), (0, 129, 12_582_912), (64,)])
 def test_attention_packed_warm_up_is_bit_identical(dev, warm_sizes):
     """rldx_attention_packed_fwd_warm_bf16 (extra workgroups reading the lines of

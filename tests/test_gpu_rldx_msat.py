@@ -87,6 +87,39 @@ def test_rldx_msat_graph_replay(dev):
     assert_as_accurate_as_eager_bf16(got, sd, inp, cfg, True, "graph replay, 2 DS + 2 SS")
 
 
+def _stack(inps):
+    return {k: torch.cat([i[k] for i in inps]) for k in inps[0]}
+
+
+def test_rldx_msat_batch_of_robots(dev):
+    """A chain for three robots (RldxMsat.for_batch: the batch-1 chain's packed
+    weights, shared) with different inputs and VL masks per robot.  Each
+    robot's output agrees with the batch-1 chain run on that robot alone
+    (rel-L2 <= 1e-2: the GEMMs of the larger batch may take other tiles or
+    splits, which order the sums differently), and the batch is as accurate
+    as the eager bf16 evaluation of the same batch (the referee above)."""
+    cfg = RM.RldxMsatCfg(ds_blocks=1, ss_blocks=1)
+    sd = RM.make_state_dict(cfg, dev, seed=61)
+    one = RM.RldxMsat(sd, cfg, dev, vl_mask=True)
+    three = one.for_batch(3)
+    assert three.batch == 3 and three.ds is one.ds and three.w is one.w
+    inps = [RM.make_inputs(cfg, dev, seed=70 + b) for b in range(3)]
+    mask = torch.ones(3, cfg.n_vl, device=dev)
+    mask[1, 5:9] = 0
+    mask[2, -3:] = 0
+    alone = [one.forward(i["sa"], i["vl"], i["temb"], i["time_token"], mask[b:b + 1]).clone()
+             for b, i in enumerate(inps)]
+    batch = _stack(inps)
+    o = three.forward(batch["sa"], batch["vl"], batch["temb"], batch["time_token"], mask).clone()
+    assert o.shape == (3, cfg.n_sa_pure, cfg.output_dim)
+    for b in range(3):
+        s = stats(o[b], alone[b][0])
+        same = (o[b].view(torch.int16) == alone[b][0].view(torch.int16)).float().mean().item()
+        print(f"robot {b}: batch of 3 vs alone {s}, bit-identical elements {same:.4f}")
+        assert s["nonfinite_mismatch"] == 0 and s["rel_l2"] <= BF16_REL_L2, (b, s)
+    assert_as_accurate_as_eager_bf16(o, sd, batch, cfg, True, "3 robots, 1 DS + 1 SS", mask=mask)
+
+
 def _module_tree(sd):
     """nn.Module tree whose state_dict() has exactly the keys of `sd` (what a
     loaded reference MSAT exposes)."""
@@ -185,9 +218,23 @@ def test_dispatcher_serves_masks_and_falls_back(dev, n_vl):
     assert torch.equal(o2.view(torch.int16), o.view(torch.int16))
     msat(inp["sa"], inp["vl"], t, return_all_hidden_states=True)
     assert len(msat.calls) == 2 and msat.calls[-1]["return_all_hidden_states"]
+    # two robots (different times and masks) run on a chain of their own, on the same packed weights
+    inp2 = RM.make_inputs(cfg, dev, seed=68)
+    t2 = torch.tensor([0.5, 0.25], device=dev)
+    mask2 = torch.cat([mask, torch.ones(1, n_vl, device=dev)])
+    mask2[1, :7] = 0
+    sa2, vl2 = torch.cat([inp["sa"], inp2["sa"]]), torch.cat([inp["vl"], inp2["vl"]])
+    ob = msat(sa2, vl2, t2, encoder_attention_mask=mask2).clone()
+    assert d.served == 4 and len(msat.calls) == 2 and d.chains[2].batch == 2 and d.chains[2].ds is d.chain.ds
+    s = stats(ob[0], om[0])
+    print(f"robot 0 of a batch of 2 vs alone: {s}")
+    assert s["nonfinite_mismatch"] == 0 and s["rel_l2"] <= BF16_REL_L2, s
+    temb2, tt2 = _time_inputs(msat, t2)
+    assert_as_accurate_as_eager_bf16(ob, sd, dict(sa=sa2, vl=vl2, temb=temb2, time_token=tt2), cfg, True,
+                                     f"dispatcher, batch of 2, n_vl={n_vl}", mask=mask2)
     short = RM.make_inputs(RM.RldxMsatCfg(ds_blocks=1, ss_blocks=1, n_vl=32), dev, seed=67)
     msat(inp["sa"], short["vl"], t)
-    assert len(msat.calls) == 3 and d.served == 3 and not d.failed
+    assert len(msat.calls) == 3 and d.served == 4 and not d.failed
 
 
 def _head_reference(head_sd, msat_sd, hc, mc, head, e=0, dtype=torch.float32):

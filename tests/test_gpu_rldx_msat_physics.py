@@ -266,3 +266,32 @@ def test_all_add_ons_action_head_full_depth_as_accurate_as_eager_bf16(dev):
         print(f"all-add-ons action head / {name}: rel-L2 to fp32 {got:.2e} (eager bf16: {floor:.2e}), to the bf16 "
               f"composition {_rel(o, a16):.2e}, max-abs to bf16 {(o - a16).abs().max().item():.3e}, cos {cos:.6f}")
         assert torch.isfinite(o).all() and got <= 1.5 * floor and cos >= 0.999, name
+
+
+def test_physics_chain_batch_of_robots(dev):
+    """The all-add-ons chain for three robots (for_batch) with different
+    inputs, VL masks and physics masks per robot: each robot's action and
+    physics outputs agree with the batch-1 chain run on that robot alone
+    (rel-L2 <= 1e-2; the larger batch's GEMMs may order sums differently) and
+    the batch is as accurate as the eager bf16 batch.  Robot b's SA padding
+    rows (its 18 SA rows are padded to 32 in the joint sequence) read the next
+    robot's QKV rows: their keys are masked and their outputs not stored, so
+    they reach no output."""
+    cfg = _cfg(ds_blocks=1, ss_blocks=1)
+    sd = RM.make_state_dict(cfg, dev, seed=63)
+    one = RM.RldxMsat(sd, cfg, dev, vl_mask=True)
+    three = one.for_batch(3)
+    inps = [RM.make_inputs(cfg, dev, seed=80 + b) for b in range(3)]
+    mask = torch.ones(3, cfg.n_vl, device=dev)
+    mask[0, 7:11] = 0
+    mask[2, -5:] = 0
+    pmask = torch.tensor([1.0, 0.0, 1.0], device=dev)
+    alone = [_run(one, i, mask[b:b + 1], pmask[b:b + 1]) for b, i in enumerate(inps)]
+    batch = {k: torch.cat([i[k] for i in inps]) for k in inps[0]}
+    outs = _run(three, batch, mask, pmask)
+    for b in range(3):
+        for name, o, a in zip(("action", "physics"), outs, alone[b]):
+            rel = _rel(o[b].double().cpu(), a[0].double().cpu())
+            print(f"robot {b} / {name}: batch of 3 vs alone rel-L2 {rel:.2e}")
+            assert torch.isfinite(o[b]).all() and rel <= 1e-2, (b, name, rel)
+    _as_accurate_as_eager_bf16(outs, sd, batch, cfg, "3 robots, physics chain", mask=mask, pmask=pmask)

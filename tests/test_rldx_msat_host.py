@@ -185,15 +185,21 @@ def test_dispatcher_falls_back_for_good_when_the_build_fails():
 
 
 def test_dispatcher_unserved_calls():
-    d = RM.MsatDispatcher(torch.nn.Module())
+    d = RM.MsatDispatcher(torch.nn.Module(), max_batch=4)
     x3 = torch.zeros(1, 17, 8)
+    mixed = "inputs are not [B, tokens, width] with one batch size"
     assert d._unserved(x3, x3, True, None, None) == "return_all_hidden_states"
-    assert d._unserved(torch.zeros(2, 17, 8), torch.zeros(2, 64, 8), False, None, None) == "batch other than 1"
+    # batches up to max_batch run on a chain of their own size
+    assert d._unserved(torch.zeros(2, 17, 8), torch.zeros(2, 17, 8), False, None, None) is None
+    assert d._unserved(torch.zeros(4, 17, 8), torch.zeros(4, 17, 8), False, None, None) is None
+    assert d._unserved(torch.zeros(5, 17, 8), torch.zeros(5, 17, 8), False, None, None) == "batch above max_batch (4)"
+    assert d._unserved(torch.zeros(2, 17, 8), torch.zeros(1, 17, 8), False, None, None) == mixed
+    assert d._unserved(torch.zeros(17, 8), torch.zeros(17, 8), False, None, None) == mixed
     assert d._unserved(x3, x3, False, torch.zeros(1, 4, 8), None) is None  # module without use_physics ignores them
     d.msat.use_physics = True
     assert d._unserved(x3, x3, False, torch.zeros(1, 4, 8), None) is None  # served by the all-add-ons chain
     assert d._n_physics(torch.zeros(1, 4, 8)) == 4 and d._n_physics(None) == 0
-    assert d._unserved(x3, x3, False, torch.zeros(2, 4, 8), None) == "batch other than 1"
+    assert d._unserved(x3, x3, False, torch.zeros(2, 4, 8), None) == mixed
 
     class _Built:  # a chain built for 17 SA, 17 VL and 4 physics tokens
         np_ = 4
