@@ -400,7 +400,15 @@ def kernel_lines(torch, reps: int):
         ms=ms, msat_forward_ms=msat_ms, unit="ms per action (4 denoising steps)",
         reference_published_ms=9.66, reference_hardware="RTX 5090, path D (rldx/inference/action_model/README.md:11-18)",
         msat_params=sum(torch.Size(s_).numel() for s_ in rmc.param_shapes().values()))
-    del rhead
+    # four robots at once (for_batch: the same packed weights, one graph; the GEMMs cover the batch)
+    rhead4 = rhead.for_batch(4)
+    for t in (rhead4.vl, rhead4.state, rhead4.x0):
+        t.copy_(torch.randn(t.shape, generator=gr, device=dev))
+    rhead4.set_embodiment([e % rhc.num_embodiments for e in range(4)])
+    ms4 = graph_time_ms(rhead4.run, 1, torch)
+    out["rldx_action_head_release_shape_4_robots"] = dict(
+        ms=ms4, ms_per_robot=ms4 / 4, batch1_ms=ms, unit="ms per call of 4 robots (4 denoising steps each)")
+    del rhead, rhead4
 
     # the same head with all add-ons: Expanded blocks with the physics stream, N_vl = 80 (cognition +
     # memory tokens), 1 + 16 physics tokens of 37 signals (30 tactile + 7 torque), physics encoders and decoder

@@ -2,9 +2,10 @@
 the action head chain built from a GraphSafeActionModel, served by the
 rldx_amd action head (vlln, state encoder, RTC trained-mode prefix, per step
 action encoder + MSAT + decoder + Euler update as one hipGraph) behind an
-ActionHeadDispatcher.  Batch 1 runs on the graph; other calls (a batch other
-than 1, a missing prefix) go to the GraphSafeActionModel's own forward, which
-computes the same actions (graph_safe_action_model.py:171-315).
+ActionHeadDispatcher.  A batch of B robots runs on a graph for B (up to the
+dispatcher's max_batch); other calls (a larger batch, a missing prefix) go to
+the GraphSafeActionModel's own forward, which computes the same actions
+(graph_safe_action_model.py:171-315).
 torch.compile is not used: the captured graph is what compilation buys the
 reference (one launch sequence per call)."""
 

@@ -3,8 +3,9 @@ the all-add-ons action head chain (with the physics head) built from a
 GraphSafeActionModel, served by the rldx_amd action head with its P stream
 (history tokens encoded once; per step the future physics state at the step's
 time, MSAT over [VL | SA | P], action and physics decoders, both Euler updates)
-as one hipGraph behind an ActionHeadDispatcher.  Batch 1 runs on the graph;
-other calls go to the GraphSafeActionModel's own forward."""
+as one hipGraph behind an ActionHeadDispatcher.  A batch of B robots runs on a
+graph for B (up to the dispatcher's max_batch); other calls go to the
+GraphSafeActionModel's own forward."""
 
 from __future__ import annotations
 

@@ -1086,13 +1086,13 @@ class RldxActionHead:
     """Flow-matching action head of RLDX-1 with the MSAT on the rldx_amd chain;
     `run` launches one action inference (state encoder + `steps` denoising
     iterations) on static buffers, `capture` / `replay` as one hipGraph.
-    Batch 1: the static buffers hold one sample (vl [1, n_vl, vl_dim], state
-    [1, 1, state_dim], x0 [1, horizon, action_dim], prefix [1, prefix_len,
-    action_dim], e_idx [1] the embodiment id); other batch sizes are served by
-    the module's own forward behind `install_action_head`.  The embodiment is
-    read on the device: run() gathers that embodiment's encoder / decoder
-    weights (W[e], b[e] of every CategorySpecificLinear) into static buffers
-    first, so one captured graph serves every embodiment.
+    Batch: the MSAT chain's (msat.batch = B robots, RldxMsat.for_batch); the
+    static buffers hold the B robots' inputs (vl [B, n_vl, vl_dim], state
+    [B, 1, state_dim], x0 [B, horizon, action_dim], prefix [B, prefix_len,
+    action_dim], e_idx [B] the robots' embodiment ids).  The embodiments are
+    read on the device: run() gathers each robot's encoder / decoder weights
+    (W[e], b[e] of every CategorySpecificLinear) into static buffers first, so
+    one captured graph serves every choice of embodiments.
     timesteps: the denoising times (default: bf16_timesteps(cfg.steps), the
     reference's bf16 schedule).
 
@@ -1130,39 +1130,49 @@ class RldxActionHead:
             Fn._require(tuple(head_sd[f"{name}.W"].shape[:1]) == (E,) and tuple(head_sd[f"{name}.b"].shape[:1]) == (E,),
                         f"{name}: one weight per embodiment ({E})")
         Fn._require(0 <= embodiment < E, "embodiment id out of range")
-        self.e_idx = torch.full((1,), embodiment, dtype=torch.long, device=dev)
-        # the selected embodiment's weights, gathered at the top of run()
-        self.w_e = {n: torch.empty((1, *head_sd[f"{n}.W"].shape[1:]), dtype=head_sd[f"{n}.W"].dtype, device=dev)
+        B = self.batch = msat.batch
+        self.e_idx = torch.full((B,), embodiment, dtype=torch.long, device=dev)
+        # each robot's embodiment weights, gathered at the top of run()
+        self.w_e = {n: torch.empty((B, *head_sd[f"{n}.W"].shape[1:]), dtype=head_sd[f"{n}.W"].dtype, device=dev)
                     for n in _CAT_LINEARS}
-        self.b_e = {n: torch.empty((1, *head_sd[f"{n}.b"].shape[1:]), dtype=head_sd[f"{n}.b"].dtype, device=dev)
+        self.b_e = {n: torch.empty((B, 1, *head_sd[f"{n}.b"].shape[1:]), dtype=head_sd[f"{n}.b"].dtype, device=dev)
                     for n in _CAT_LINEARS}
         Fn._require(0 <= cfg.prefix_len < cfg.action_horizon, "0 <= prefix_len < action_horizon")
         Fn._require(not cfg.use_vlln or ("vlln.weight" in head_sd and "vlln.bias" in head_sd),
                     "use_vlln needs vlln.weight and vlln.bias")
         e = lambda *s: torch.empty(*s, dtype=BF16, device=dev)  # noqa: E731
-        self.vl, self.state = e(1, mc.n_vl, mc.vl_dim), e(1, 1, cfg.state_dim)
-        self.vl_n = e(1, mc.n_vl, mc.vl_dim) if cfg.use_vlln else self.vl  # the MSAT's VL input
+        self.vl, self.state = e(B, mc.n_vl, mc.vl_dim), e(B, 1, cfg.state_dim)
+        self.vl_n = e(B, mc.n_vl, mc.vl_dim) if cfg.use_vlln else self.vl  # the MSAT's VL input
         self.d = cfg.prefix_len
         if self.d > 0:
-            self.prefix = e(1, self.d, cfg.action_dim)
+            self.prefix = e(B, self.d, cfg.action_dim)
             # the prefix rows' time is 1 (custom_action_model_chain.py:117-121), baked
-            self.tau_one = sinusoidal_time(torch.ones(self.d, device=dev), mc.sa_dim).to(BF16)
-        self.x0 = e(1, cfg.action_horizon, cfg.action_dim)
-        self.act = e(1, cfg.action_horizon, cfg.action_dim)
-        self.sa = e(1, mc.n_sa_pure, mc.sa_dim)
+            self.tau_one = sinusoidal_time(torch.ones(self.d, device=dev), mc.sa_dim).to(BF16).expand(B, -1, -1)
+        self.x0 = e(B, cfg.action_horizon, cfg.action_dim)
+        self.act = e(B, cfg.action_horizon, cfg.action_dim)
+        self.sa = e(B, mc.n_sa_pure, mc.sa_dim)
         # tau encodings of each step's time, baked (same every call)
         self.tau = [sinusoidal_time(torch.full((cfg.action_horizon,), t, device=dev), mc.sa_dim).to(BF16)
-                    for t in self.timesteps]
+                    .expand(B, -1, -1) for t in self.timesteps]
         if self.phys:
-            self.physics_hist = e(1, cfg.physics_hist_len, cfg.physics_dim)
-            self.physics_x0 = e(1, cfg.physics_fut_len, cfg.physics_dim)
-            self.physics_fut = e(1, cfg.physics_fut_len, cfg.physics_dim)
-            self.p_embs = e(1, msat.np_, mc.sa_dim)
+            self.physics_hist = e(B, cfg.physics_hist_len, cfg.physics_dim)
+            self.physics_x0 = e(B, cfg.physics_fut_len, cfg.physics_dim)
+            self.physics_fut = e(B, cfg.physics_fut_len, cfg.physics_dim)
+            self.p_embs = e(B, msat.np_, mc.sa_dim)
             # history positions 0 .. T_hist - 1 (physics.py:19-25), baked
-            self.hist_pos = sinusoidal_time(torch.arange(cfg.physics_hist_len, device=dev), mc.sa_dim).to(BF16)
-        # the output AdaLN of each step's (static) time embedding, computed once
-        self.adaln = [msat.adaln_of(head_sd["static_tembs"][i]) for i in range(cfg.steps)]
+            self.hist_pos = sinusoidal_time(torch.arange(cfg.physics_hist_len, device=dev), mc.sa_dim).to(BF16)\
+                .expand(B, -1, -1)
+        # every robot's static time embedding / time token of each step (custom_action_model_chain.py:125-127,
+        # expanded over the batch) and the output AdaLN of each, computed once
+        self.tembs = [head_sd["static_tembs"][i].expand(B, -1) for i in range(cfg.steps)]
+        self.time_tokens = [head_sd["static_time_tokens"][i].expand(B, -1, -1) for i in range(cfg.steps)]
+        self.adaln = [msat.adaln_of(t) for t in self.tembs]
         self.graph = None
+
+    def for_batch(self, batch: int) -> "RldxActionHead":
+        """This head for `batch` robots: an MSAT chain for the batch on the same
+        packed weights, the same head weights, buffers of its own."""
+        return RldxActionHead(self.msat.for_batch(batch), self.sd, self.cfg, timesteps=self.timesteps)
 
     def _lin(self, x, name):
         return F.linear(x, self.sd[f"{name}.weight"], self.sd[f"{name}.bias"])
@@ -1173,21 +1183,26 @@ class RldxActionHead:
         h = self._lin(x, f"physics.{enc}.W1")
         return self._lin(F.silu(self._lin(torch.cat([h, pos], dim=-1), f"physics.{enc}.W2")), f"physics.{enc}.W3")
 
-    def set_embodiment(self, e: int) -> None:
-        """Select embodiment e for the next run / replay (range-checked on the
-        host: the gather must never index past W's first dimension)."""
-        if not 0 <= e < self.cfg.num_embodiments:
-            raise IndexError(f"embodiment id {e} out of range [0, {self.cfg.num_embodiments})")
-        self.e_idx.fill_(e)
+    def set_embodiment(self, e) -> None:
+        """Select the embodiment of every robot (an int) or of each robot (a
+        sequence of B ints) for the next run / replay; range-checked on the host:
+        the gather must never index past W's first dimension."""
+        ids = [int(e)] * self.batch if isinstance(e, int) else [int(v) for v in e]
+        if len(ids) != self.batch:
+            raise ValueError(f"{len(ids)} embodiment ids for a batch of {self.batch}")
+        for v in ids:
+            if not 0 <= v < self.cfg.num_embodiments:
+                raise IndexError(f"embodiment id {v} out of range [0, {self.cfg.num_embodiments})")
+        self.e_idx.copy_(torch.tensor(ids, dtype=torch.long))
 
     def _cat(self, x, name):
-        """CategorySpecificLinear.forward for batch 1 (embodiment_conditioned_mlp.py:72-82):
-        x W[e] + b[e] with the gathered weights of embodiment e."""
-        return torch.addmm(self.b_e[name][0], x, self.w_e[name][0])
+        """CategorySpecificLinear.forward (embodiment_conditioned_mlp.py:72-82):
+        x [B, T, in] -> x W[e_b] + b[e_b] per robot b, with the gathered weights."""
+        return torch.baddbmm(self.b_e[name], x, self.w_e[name])
 
     def _encode(self, x, tau):
-        """MultiEmbodimentActionEncoder.forward for batch 1
-        (embodiment_conditioned_mlp.py:191-227): W3(swish(W2([W1 x | tau])))."""
+        """MultiEmbodimentActionEncoder.forward (embodiment_conditioned_mlp.py:191-227):
+        W3(swish(W2([W1 x | tau])))."""
         a = self._cat(x, "action_encoder.W1")
         h = self._cat(torch.cat([a, tau], dim=-1), "action_encoder.W2")
         return self._cat(h * torch.sigmoid(h), "action_encoder.W3")
@@ -1197,43 +1212,42 @@ class RldxActionHead:
         d, H = self.d, cfg.action_horizon
         for n in _CAT_LINEARS:
             torch.index_select(sd[f"{n}.W"], 0, self.e_idx, out=self.w_e[n])
-            torch.index_select(sd[f"{n}.b"], 0, self.e_idx, out=self.b_e[n])
+            torch.index_select(sd[f"{n}.b"], 0, self.e_idx, out=self.b_e[n][:, 0])
         if cfg.use_vlln:
             self.vl_n.copy_(F.layer_norm(self.vl, (mc.vl_dim,), sd["vlln.weight"], sd["vlln.bias"], cfg.vlln_eps))
-        h = F.relu(self._cat(self.state[0], "state_encoder.layer1"))
-        self.sa[0, :1].copy_(self._cat(h, "state_encoder.layer2"))
+        h = F.relu(self._cat(self.state, "state_encoder.layer1"))
+        self.sa[:, :1].copy_(self._cat(h, "state_encoder.layer2"))
         self.act.copy_(self.x0)
         if d > 0:  # the frozen prefix: its actions and (once) its encoder features
-            self.act[0, :d].copy_(self.prefix[0])
-            torch.add(self._encode(self.prefix[0], self.tau_one), sd["position_embedding.weight"][:d],
-                      out=self.sa[0, 1:1 + d])
+            self.act[:, :d].copy_(self.prefix)
+            torch.add(self._encode(self.prefix, self.tau_one), sd["position_embedding.weight"][:d],
+                      out=self.sa[:, 1:1 + d])
         if self.phys:
             nh = cfg.physics_hist_len
-            self.p_embs[0, :nh].copy_(self._physics_encoder(self.physics_hist[0], self.hist_pos, "physics_cond_encoder"))
+            self.p_embs[:, :nh].copy_(self._physics_encoder(self.physics_hist, self.hist_pos, "physics_cond_encoder"))
             self.physics_fut.copy_(self.physics_x0)
         for i in range(cfg.steps):
-            torch.add(self._encode(self.act[0, d:], self.tau[i][d:]), sd["position_embedding.weight"][d:],
-                      out=self.sa[0, 1 + d:])
+            torch.add(self._encode(self.act[:, d:], self.tau[i][:, d:]), sd["position_embedding.weight"][d:],
+                      out=self.sa[:, 1 + d:])
             if self.phys:
                 # the step's time for every future row: the same encoding as the actions' tau
-                self.p_embs[0, nh:].copy_(self._physics_encoder(self.physics_fut[0], self.tau[i][: cfg.physics_fut_len],
+                self.p_embs[:, nh:].copy_(self._physics_encoder(self.physics_fut, self.tau[i][:, :cfg.physics_fut_len],
                                                                 "physics_fut_encoder"))
-                o = self.msat.forward(self.sa, self.vl_n, sd["static_tembs"][i], sd["static_time_tokens"][i],
+                o = self.msat.forward(self.sa, self.vl_n, self.tembs[i], self.time_tokens[i],
                                       physics_embs=self.p_embs, adaln=self.adaln[i])
                 out = o["action"]
-                ph = o["physics"][0, -cfg.physics_fut_len:]
+                ph = o["physics"][:, -cfg.physics_fut_len:]
                 pv = self._lin(F.silu(self._lin(ph, "physics.physics_decoder.net.0")), "physics.physics_decoder.net.2")
-                self.physics_fut[0].add_(pv, alpha=self.dt)
+                self.physics_fut.add_(pv, alpha=self.dt)
             else:
-                out = self.msat.forward(self.sa, self.vl_n, sd["static_tembs"][i], sd["static_time_tokens"][i],
-                                        adaln=self.adaln[i])
+                out = self.msat.forward(self.sa, self.vl_n, self.tembs[i], self.time_tokens[i], adaln=self.adaln[i])
             if d > 0:  # only the postfix rows are decoded and advanced (:156-170)
-                hd = F.relu(self._cat(out[0][-(H - d):], "action_decoder.layer1"))
+                hd = F.relu(self._cat(out[:, -(H - d):], "action_decoder.layer1"))
                 v = self._cat(hd, "action_decoder.layer2")
             else:
-                hd = F.relu(self._cat(out[0], "action_decoder.layer1"))
-                v = self._cat(hd, "action_decoder.layer2")[-H:]
-            self.act[0, d:].add_(v, alpha=self.dt)
+                hd = F.relu(self._cat(out, "action_decoder.layer1"))
+                v = self._cat(hd, "action_decoder.layer2")[:, -H:]
+            self.act[:, d:].add_(v, alpha=self.dt)
         return self.act
 
     def capture(self, warmup: int = 2) -> None:
@@ -1261,16 +1275,20 @@ class ActionHeadDispatcher:
     custom_expanded_action_model_chain.py:84-219) -- by an RldxActionHead on the
     rldx_amd MSAT chain, built from the module's weights at install.
 
-    Served (batch 1): vl_embs [1, n_vl, vl_dim] with the module's n_vl; state
-    [1, state_dim] or [1, 1, state_dim]; embodiment_id [1] (read on the host
-    and range-checked -- one stream sync when it lives on the GPU -- an id out
-    of range raises IndexError); init_noise [1, horizon, action_dim] or None
-    (then drawn here, as the module does); with prefix_len d > 0, prefix_actions
-    [1, d, action_dim]; on a physics model, physics_hist [1, hist_len,
-    physics_dim] and physics_init_noise or None.  The result is a new tensor
-    [1, horizon, action_dim].
+    Served (a batch of B <= max_batch robots; each batch size on a head of its
+    own, RldxActionHead.for_batch: the same packed weights, its own buffers and
+    graph, built on the first call of that size): vl_embs [B, n_vl, vl_dim]
+    with the module's n_vl; state [B, state_dim] or [B, 1, state_dim];
+    embodiment_id [B] (read on the host and range-checked -- one stream sync
+    when it lives on the GPU -- an id out of range raises IndexError);
+    init_noise [B, horizon, action_dim] or None (then drawn here, as the module
+    does); with prefix_len d > 0, prefix_actions [B, d, action_dim]; on a
+    physics model, physics_hist [B, hist_len, physics_dim] and
+    physics_init_noise or None.  The result is a new tensor [B, horizon,
+    action_dim].
     Refused per call, to the module's own forward (counted in `fallbacks`,
-    logged with verbose=True): a batch other than 1, a VL token count other
+    logged with verbose=True): inputs of different batch sizes, a batch above
+    max_batch, a VL token count other
     than the module's, prefix_len > 0 without prefix_actions, a physics model
     called without physics_hist (its forward then runs with no history
     tokens).  A build failure (a module the head does not mirror: a vlln other
@@ -1286,11 +1304,12 @@ class ActionHeadDispatcher:
     (tensor identity, data_ptr, _version) and refreshes on a change."""
 
     def __init__(self, model: torch.nn.Module, bf16_quirk: Optional[bool] = None, graph: bool = True,
-                 verbose: bool = False, check_weights: bool = False):
+                 verbose: bool = False, check_weights: bool = False, max_batch: int = 16):
         self.model, self.orig = model, model.forward
         self.bf16_quirk, self.graph, self.verbose = bf16_quirk, graph, verbose
-        self.check_weights = check_weights
-        self.head: Optional[RldxActionHead] = None
+        self.check_weights, self.max_batch = check_weights, int(max_batch)
+        self.head: Optional[RldxActionHead] = None  # the first head built (batch 1), owner of the packed weights
+        self.heads: dict = {}                        # batch size -> head on those weights
         self.failed = False
         self.served = 0
         self.fallbacks = 0
@@ -1363,9 +1382,7 @@ class ActionHeadDispatcher:
                          prefix_len=int(getattr(m, "prefix_len", 0)), use_vlln=use_vlln, vlln_eps=eps, **kw)
         return hsd, hc, chain
 
-    def build(self) -> RldxActionHead:
-        hsd, hc, chain = self.head_inputs()
-        head = RldxActionHead(chain, hsd, hc, timesteps=self.model.static_timesteps.float().tolist())
+    def _capture(self, head: RldxActionHead) -> None:
         if self.graph:
             for buf in [head.vl, head.state, head.x0] + ([head.prefix] if head.d > 0 else []):
                 buf.zero_()
@@ -1373,21 +1390,40 @@ class ActionHeadDispatcher:
                 for buf in (head.physics_hist, head.physics_x0):
                     buf.zero_()
             head.capture()
+
+    def build(self) -> RldxActionHead:
+        hsd, hc, chain = self.head_inputs()
+        head = RldxActionHead(chain, hsd, hc, timesteps=self.model.static_timesteps.float().tolist())
+        self._capture(head)
         self.head = head
+        self.heads = {1: head}
         self._stamp = self._weights_stamp()
         return head
 
+    def head_for(self, batch: int) -> RldxActionHead:
+        """The head for `batch` robots, built on the weights of self.head when first needed."""
+        h = self.heads.get(batch)
+        if h is None:
+            h = self.head.for_batch(batch)
+            self._capture(h)
+            self.heads[batch] = h
+        return h
+
     def refresh(self) -> None:
-        """Drop the head; the next call rebuilds it from the module's current weights."""
+        """Drop the heads; the next call rebuilds them from the module's current weights."""
         if self.head is not None:
             self.rebuilds += 1
         self.head = None
+        self.heads = {}
         self._stamp = None
 
     def _unserved(self, vl_embs, state, prefix_actions, physics_hist) -> Optional[str]:
         m = self.model
-        if vl_embs.dim() != 3 or vl_embs.shape[0] != 1 or state.shape[0] != 1:
-            return "batch other than 1"
+        B = vl_embs.shape[0] if vl_embs.dim() == 3 else -1
+        if B < 1 or state.shape[0] != B or any(t is not None and t.shape[0] != B for t in (prefix_actions, physics_hist)):
+            return "inputs of different batch sizes"
+        if B > self.max_batch:
+            return f"batch above max_batch ({self.max_batch})"
         if vl_embs.shape[1] != int(m.gs_msat.n_vl):
             return "VL token count differs from the module's"
         if int(getattr(m, "prefix_len", 0)) > 0 and prefix_actions is None:
@@ -1423,8 +1459,13 @@ class ActionHeadDispatcher:
                 self.failed = True
                 self._log(f"build failed ({e}); the module's own forward serves every call")
             return self._refuse("building the head", args, kwargs)
-        h = self.head
-        h.set_embodiment(int(torch.as_tensor(embodiment_id).reshape(-1)[0]))  # IndexError out of range
+        B = vl_embs.shape[0]
+        try:
+            h = self.head_for(B)
+        except Exception as e:  # noqa: BLE001 -- a head for this batch that cannot be built: this call only
+            self._log(f"no head for a batch of {B} ({e})")
+            return self._refuse(f"building the head for a batch of {B}", args, kwargs)
+        h.set_embodiment(torch.as_tensor(embodiment_id).reshape(-1).tolist())  # IndexError out of range
         try:
             h.vl.copy_(vl_embs)
             h.state.copy_(state.reshape(h.state.shape))
@@ -1452,7 +1493,7 @@ class ActionHeadDispatcher:
 
 def install_action_head(model: torch.nn.Module, bf16_quirk: Optional[bool] = None, graph: bool = True,
                         verbose: bool = False, build: bool = True,
-                        check_weights: bool = False) -> ActionHeadDispatcher:
+                        check_weights: bool = False, max_batch: int = 16) -> ActionHeadDispatcher:
     """Route a live action model's forward (a GraphSafeActionModel: gs_msat
     with _msat / n_vl / n_sa_pure / n_physics, vlln, state_encoder,
     action_encoder, action_decoder, position_embedding, static_pos_ids,
@@ -1467,7 +1508,7 @@ def install_action_head(model: torch.nn.Module, bf16_quirk: Optional[bool] = Non
     that new weights drop the head (rebuilt on the next call);
     check_weights=True also catches in-place updates."""
     d = ActionHeadDispatcher(model, bf16_quirk=bf16_quirk, graph=graph, verbose=verbose,
-                             check_weights=check_weights)
+                             check_weights=check_weights, max_batch=max_batch)
     if build:
         d.build()
     model.forward = d

@@ -295,6 +295,42 @@ def test_rldx_action_head_prefix_and_vlln_match_fp32_composition(dev, prefix_len
         assert torch.equal(a1[0, :prefix_len], head.prefix[0])
 
 
+@pytest.mark.parametrize("prefix_len,use_vlln", [(0, False), (4, True)])
+def test_rldx_action_head_batch_of_robots(dev, prefix_len, use_vlln):
+    """An action head for three robots (for_batch: the same MSAT and head
+    weights) with their own VL tokens, states, noise, prefixes and embodiment
+    ids (gathered per robot on the device), one hipGraph: each robot's actions
+    agree with the batch-1 head run on that robot alone (rel-L2 <= 1e-2; the
+    larger batch's GEMMs may order sums differently) and with the oracle's
+    fp32 composition for that robot (rel-L2 <= 2e-2, the batch-1 head's
+    bound); the prefix rows are each robot's prefix bit for bit."""
+    mc = RM.RldxMsatCfg(ds_blocks=1, ss_blocks=1)
+    hc = RM.RldxHeadCfg(steps=2, num_embodiments=4, prefix_len=prefix_len, use_vlln=use_vlln)
+    head, sd, hsd, _ = _head_on_gpu(mc, hc, dev, 111 + prefix_len, 0)
+    three = head.for_batch(3)
+    assert three.batch == 3 and three.msat.ds is head.msat.ds and three.sd is head.sd
+    g = torch.Generator(device=dev).manual_seed(7)
+    names = ["vl", "state", "x0"] + (["prefix"] if prefix_len else [])
+    for n in names:
+        t = getattr(three, n)
+        t.copy_(torch.randn(t.shape, generator=g, device=dev))
+    emb = [2, 0, 3]
+    three.set_embodiment(emb)
+    three.capture()
+    a = three.replay().clone()
+    for b in range(3):
+        for n in names:
+            getattr(head, n).copy_(getattr(three, n)[b:b + 1])
+        head.set_embodiment(emb[b])
+        alone = head.replay().clone()
+        rel1 = _rel(a[b].cpu().double(), alone[0].cpu().double())
+        rel32 = _rel(a[b].cpu().double(), _head_reference(hsd, sd, hc, mc, head, e=emb[b]).double())
+        print(f"action head, robot {b} of 3 (embodiment {emb[b]}): vs alone {rel1:.2e}, to fp32 {rel32:.2e}")
+        assert torch.isfinite(a[b]).all() and rel1 <= 1e-2 and rel32 <= 2e-2
+        if prefix_len:
+            assert torch.equal(a[b, :prefix_len], three.prefix[b])
+
+
 def test_rldx_action_head_release_shape_as_accurate_as_eager_bf16(dev):
     """The release action head: state encoder + 4 denoising steps of action
     encoder, the 4 DS + 8 SS MSAT (24 x 64, 18 SA + 64 VL tokens) and decoder,
@@ -363,9 +399,10 @@ def test_install_action_head_on_a_live_model(dev):
     baked position embedding and time embeddings, vlln) and serves batch-1
     calls with the reference signature, RTC prefix and vlln included, against
     the oracle's fp32 composition (rel-L2 <= 2e-2, prefix rows exact), for two
-    embodiments through one captured graph; a batch of 2 and a missing prefix
-    are refused to the module's own forward, an embodiment id out of range
-    raises IndexError without disabling the dispatcher."""
+    embodiments through one captured graph; a batch of two robots with their
+    own embodiments runs on a head of its own (same weights) to the same bound;
+    a missing prefix is refused to the module's own forward, an embodiment id
+    out of range raises IndexError without disabling the dispatcher."""
     mc = RM.RldxMsatCfg(ds_blocks=1, ss_blocks=1)
     hc = RM.RldxHeadCfg(steps=2, num_embodiments=3, prefix_len=2, use_vlln=True)
     sd = RM.make_state_dict(mc, dev, seed=101)
@@ -396,13 +433,27 @@ def test_install_action_head_on_a_live_model(dev):
         assert torch.isfinite(out).all() and rel <= 2e-2
         assert torch.equal(out[0, :2], prefix[0])
     assert d.served == 2 and m.calls == []
-    assert m(rnd(2, mc.n_vl, mc.vl_dim), rnd(2, hc.state_dim), torch.tensor([0, 1]), prefix_actions=rnd(2, 2, 64)) == "own"
+    # two robots with embodiments 0 and 1: a head for the batch, on the same weights, captured on first use
+    vl2, state2 = rnd(2, mc.n_vl, mc.vl_dim), rnd(2, hc.state_dim)
+    x02, prefix2 = rnd(2, hc.action_horizon, hc.action_dim), rnd(2, 2, hc.action_dim)
+    out2 = m(vl2, state2, torch.tensor([0, 1]), init_noise=x02, prefix_actions=prefix2)
+    assert d.served == 3 and m.calls == [] and d.heads[2].batch == 2 and d.heads[2].msat.ds is h.msat.ds
+    for b in range(2):
+        ref = R.action_head(h.sd, sd, vl2[b:b + 1], state2[b:b + 1, None], x02[b:b + 1], steps=hc.steps,
+                            heads=mc.heads, head_dim=mc.head_dim, ds_blocks=mc.ds_blocks, ss_blocks=mc.ss_blocks,
+                            e=b, prefix=prefix2[b:b + 1], use_vlln=True).double()
+        rel = _rel(out2[b].cpu().double(), ref)
+        print(f"installed action head, robot {b} of 2 (embodiment {b}): rel-L2 to the fp32 composition {rel:.2e}")
+        assert torch.isfinite(out2[b]).all() and rel <= 2e-2
+        assert torch.equal(out2[b, :2], prefix2[b])
     assert m(vl, state, torch.tensor([1]), init_noise=x0) == "own"
-    assert d.refusals == {"batch other than 1": 1, "prefix_len > 0 without prefix_actions": 1}
+    assert d.refusals == {"prefix_len > 0 without prefix_actions": 1}
     with pytest.raises(IndexError):
         m(vl, state, torch.tensor([3]), init_noise=x0, prefix_actions=prefix)
+    with pytest.raises(ValueError):  # one embodiment id per robot
+        m(vl2, state2, torch.tensor([0]), init_noise=x02, prefix_actions=prefix2)
     out = m(vl, state, torch.tensor([1]), prefix_actions=prefix)  # noise drawn here
-    assert not d.failed and d.served == 3 and torch.isfinite(out).all() and torch.equal(out[0, :2], prefix[0])
+    assert not d.failed and d.served == 4 and torch.isfinite(out).all() and torch.equal(out[0, :2], prefix[0])
     # the mirrored CustomActionHeadChain (the reference's build function) on an identical model: the same bits
     from rldx_amd.compat.inference.action_model.engine.custom_action_model_chain import \
         build_custom_action_model_chain

@@ -316,10 +316,15 @@ def test_action_head_dispatcher_unserved_calls():
     m.gs_msat = torch.nn.Module()
     m.gs_msat.n_vl = 64
     m.prefix_len = 0
-    d = RM.ActionHeadDispatcher(m)
+    d = RM.ActionHeadDispatcher(m, max_batch=4)
     vl, st = torch.zeros(1, 64, 8), torch.zeros(1, 4)
+    mixed = "inputs of different batch sizes"
     assert d._unserved(vl, st, None, None) is None
-    assert d._unserved(torch.zeros(2, 64, 8), torch.zeros(2, 4), None, None) == "batch other than 1"
+    assert d._unserved(torch.zeros(2, 64, 8), torch.zeros(2, 4), None, None) is None  # a head for 2 robots
+    assert d._unserved(torch.zeros(5, 64, 8), torch.zeros(5, 4), None, None) == "batch above max_batch (4)"
+    assert d._unserved(torch.zeros(2, 64, 8), torch.zeros(1, 4), None, None) == mixed
+    assert d._unserved(torch.zeros(2, 64, 8), torch.zeros(2, 4), torch.zeros(1, 3, 8), None) == mixed
+    assert d._unserved(torch.zeros(64, 8), st, None, None) == mixed
     assert d._unserved(torch.zeros(1, 63, 8), st, None, None) == "VL token count differs from the module's"
     m.prefix_len = 3
     assert d._unserved(vl, st, None, None) == "prefix_len > 0 without prefix_actions"
