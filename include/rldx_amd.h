@@ -144,6 +144,27 @@ hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* streams, int32
                                         int64_t out_head_stride, int64_t out_row_stride, void* kv_packed,
                                         int64_t kv_packed_head_stride, float eps, hipStream_t stream);
 
+/*
+ * rldx_msat_qkv_norm_rope_bf16 for a batch of `batch` joint sequences in one
+ * launch (0..65535): sequence b reads stream i's rows from
+ * streams[i].qkv + b * stream_batch_rows[i] * qkv_row_stride (rows per
+ * sequence: streams[i].rows; robot after robot, as the GEMMs stack a stream's
+ * rows for a batch) and writes its Q / K / V at b * out_batch_stride, or its
+ * packed K/V tiles at kv_packed + b * kv_packed_batch_stride (elements).  The
+ * rows a sequence reads may run into the next one's (padding rows whose keys
+ * the attention masks); every row read must lie inside the caller's buffer.
+ * Each sequence's outputs are those of rldx_msat_qkv_norm_rope_bf16 on its rows,
+ * bit for bit.
+ * Replaces: the kernels above, called per sample for a batch of robots
+ *   (custom_action_model_chain.py:85; the reference's chained ops take one).
+ */
+hipError_t rldx_msat_qkv_norm_rope_batch_bf16(const rldx_msat_stream_t* streams, int32_t num_streams, int64_t batch,
+                                              const int64_t* stream_batch_rows, int64_t heads, int64_t head_dim,
+                                              void* q_out, void* k_out, void* v_out, int64_t out_batch_stride,
+                                              int64_t out_head_stride, int64_t out_row_stride, void* kv_packed,
+                                              int64_t kv_packed_batch_stride, int64_t kv_packed_head_stride,
+                                              float eps, hipStream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Attention                                                                */
 /* ------------------------------------------------------------------------ */

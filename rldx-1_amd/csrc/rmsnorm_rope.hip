@@ -267,6 +267,7 @@ struct MsatStream {
   const float* cos;      // [n, D/2] fp32 or nullptr (no rotary on this stream)
   const float* sin;
   int64_t rope_ld;       // row stride of cos/sin (elements)
+  int64_t b_step;        // elements from one batch entry's rows to the next's
 };
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -276,10 +277,10 @@ struct MsatArgs {
   int num_streams;
   int64_t heads;
   int64_t m_total;
-  uint16_t* q_out;  // (H, M, D) with strides
+  uint16_t* q_out;  // (B, H, M, D) with strides
   uint16_t* k_out;
   uint16_t* v_out;
-  int64_t o_sh, o_sm;  // output strides (head, row) in elements, shared by q/k/v
+  int64_t o_sb, o_sh, o_sm;  // output strides (batch, head, row) in elements, shared by q/k/v
   float eps;
   int64_t total_items;  // rows of D handled by the norm/copy role: 3*H*M, or 2*H*M with kvp
   // optional packed K/V tiles of the attention kernels (32 keys per tile, 128*D
@@ -287,7 +288,7 @@ struct MsatArgs {
   // scattered into them by the norm role; V and the K padding are written by
   // workgroups [qk_blocks, qk_blocks + H * kv_tiles)
   uint16_t* kvp;
-  int64_t kvp_sh;  // head stride in elements
+  int64_t kvp_sb, kvp_sh;  // batch / head strides in elements
   int64_t qk_blocks;
   int64_t kv_tiles;  // 32-token tiles per head
   // 32-bit index math of the norm role (host-checked: its threads < 2^31)
@@ -296,7 +297,7 @@ struct MsatArgs {
 };
 
 template <int D>
-__device__ void msat_kv_pack_block(const MsatArgs& a, int64_t vb) {
+__device__ void msat_kv_pack_block(const MsatArgs& a, int64_t vb, int64_t b) {
   const int64_t h = vb / a.kv_tiles;
   const int64_t t = vb - h * a.kv_tiles;
   const int64_t inner = a.heads * D;
@@ -305,9 +306,9 @@ __device__ void msat_kv_pack_block(const MsatArgs& a, int64_t vb) {
     if (a.num_streams > 1 && m >= a.s[1].m_begin) si = 1;
     if (a.num_streams > 2 && m >= a.s[2].m_begin) si = 2;
     const MsatStream& S = a.s[si];
-    return S.qkv + (m - S.m_begin) * S.ld + 2 * inner + h * D;
+    return S.qkv + b * S.b_step + (m - S.m_begin) * S.ld + 2 * inner + h * D;
   };
-  kv_tile_pack<D>(vrow, a.m_total, t * 32, a.kvp + h * a.kvp_sh + t * (64 * D));
+  kv_tile_pack<D>(vrow, a.m_total, t * 32, a.kvp + b * a.kvp_sb + h * a.kvp_sh + t * (64 * D));
 }
 
 template <int D>
@@ -315,8 +316,9 @@ __global__ __launch_bounds__(256) void msat_qkv_norm_rope_kernel(MsatArgs a) {
   constexpr int V = 8;
   constexpr int LPR = D / V;
   static_assert(LPR >= 2 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "unsupported head_dim");
+  const int64_t b = blockIdx.y;  // batch entry
   if (a.kvp != nullptr && static_cast<int64_t>(blockIdx.x) >= a.qk_blocks) {
-    msat_kv_pack_block<D>(a, static_cast<int64_t>(blockIdx.x) - a.qk_blocks);
+    msat_kv_pack_block<D>(a, static_cast<int64_t>(blockIdx.x) - a.qk_blocks, b);
     return;
   }
   // 32-bit index math with invariant-divisor multiplies (a 64-bit division by
@@ -338,10 +340,11 @@ __global__ __launch_bounds__(256) void msat_qkv_norm_rope_kernel(MsatArgs a) {
   const int64_t row = static_cast<int64_t>(m) - S.m_begin;
   const int64_t inner = a.heads * D;
   const int d0 = lane_in_row * V;
-  const uint16_t* src = S.qkv + row * S.ld + which * inner + static_cast<int64_t>(h) * D + d0;
+  const uint16_t* src = S.qkv + b * S.b_step + row * S.ld + which * inner + static_cast<int64_t>(h) * D + d0;
   uint16_t* dst = (a.kvp != nullptr && which == 1)
-                      ? a.kvp + h * a.kvp_sh + packed_k_offset(m, d0, D)
-                      : (which == 0 ? a.q_out : which == 1 ? a.k_out : a.v_out) + h * a.o_sh + m * a.o_sm + d0;
+                      ? a.kvp + b * a.kvp_sb + h * a.kvp_sh + packed_k_offset(m, d0, D)
+                      : (which == 0 ? a.q_out : which == 1 ? a.k_out : a.v_out) + b * a.o_sb + h * a.o_sh +
+                            m * a.o_sm + d0;
 
   uint4 raw = valid ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
   if (which == 2) {  // V passthrough (uniform per row group, but shuffles below need all lanes)
@@ -545,12 +548,16 @@ extern "C" hipError_t rldx_qk_rmsnorm_rope_half_bf16(
                               q_strides, k_strides, q_out_strides, k_out_strides, cos_strides, eps, flags, stream);
 }
 
-extern "C" hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* streams, int32_t num_streams,
-                                                   int64_t heads, int64_t head_dim, void* q_out, void* k_out,
-                                                   void* v_out, int64_t out_head_stride, int64_t out_row_stride,
-                                                   void* kv_packed, int64_t kv_packed_head_stride, float eps,
-                                                   hipStream_t stream) {
+namespace {
+hipError_t msat_qkv(const rldx_msat_stream_t* streams, int32_t num_streams, int64_t batch,
+                    const int64_t* batch_rows, int64_t heads, int64_t head_dim, void* q_out, void* k_out,
+                    void* v_out, int64_t out_batch_stride, int64_t out_head_stride, int64_t out_row_stride,
+                    void* kv_packed, int64_t kv_packed_batch_stride, int64_t kv_packed_head_stride, float eps,
+                    hipStream_t stream) {
   if (streams == nullptr || num_streams < 1 || num_streams > 3) return hipErrorInvalidValue;
+  if (batch < 0 || batch > 65535 || (batch > 1 && !batch_rows)) return hipErrorInvalidValue;
+  if (out_batch_stride % 8 || kv_packed_batch_stride % 8) return hipErrorInvalidValue;
+  if (batch == 0) return hipSuccess;
   if (head_dim != 64 && head_dim != 128) return hipErrorInvalidValue;
   if (heads <= 0 || !q_out) return hipErrorInvalidValue;
   if (!kv_packed && (!k_out || !v_out)) return hipErrorInvalidValue;
@@ -562,7 +569,7 @@ extern "C" hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* str
   int k = 0;
   for (int i = 0; i < num_streams; ++i) {
     const rldx_msat_stream_t& s = streams[i];
-    if (s.rows < 0) return hipErrorInvalidValue;
+    if (s.rows < 0 || (batch > 1 && batch_rows[i] < 0)) return hipErrorInvalidValue;
     if (s.rows == 0) continue;
     if (!s.qkv || !s.q_norm_w || !s.k_norm_w || !al16(s.qkv) || !al16(s.q_norm_w) || !al16(s.k_norm_w))
       return hipErrorInvalidValue;
@@ -573,7 +580,8 @@ extern "C" hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* str
       return hipErrorInvalidValue;
     a.s[k] = MsatStream{static_cast<const uint16_t*>(s.qkv), s.qkv_row_stride, s.rows, m,
                         static_cast<const uint16_t*>(s.q_norm_w), static_cast<const uint16_t*>(s.k_norm_w),
-                        s.rope_cos, s.rope_sin, s.rope_row_stride};
+                        s.rope_cos, s.rope_sin, s.rope_row_stride,
+                        batch > 1 ? batch_rows[i] * s.qkv_row_stride : 0};
     m += s.rows;
     ++k;
   }
@@ -584,6 +592,7 @@ extern "C" hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* str
   a.q_out = static_cast<uint16_t*>(q_out);
   a.k_out = static_cast<uint16_t*>(k_out);
   a.v_out = static_cast<uint16_t*>(v_out);
+  a.o_sb = out_batch_stride;
   a.o_sh = out_head_stride;
   a.o_sm = out_row_stride;
   a.eps = eps;
@@ -595,13 +604,38 @@ extern "C" hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* str
   a.dm_kind = div_magic(a.per_kind);
   a.dm_heads = div_magic(static_cast<uint32_t>(heads));
   a.kvp = static_cast<uint16_t*>(kv_packed);
+  a.kvp_sb = kv_packed_batch_stride;
   a.kvp_sh = kv_packed_head_stride;
   a.kv_tiles = (m + 31) / 32;
   if (kv_packed && kv_packed_head_stride < a.kv_tiles * 64 * head_dim) return hipErrorInvalidValue;
-  const int grid = static_cast<int>(a.qk_blocks + (kv_packed ? heads * a.kv_tiles : 0));
+  const dim3 grid(static_cast<unsigned>(a.qk_blocks + (kv_packed ? heads * a.kv_tiles : 0)),
+                  static_cast<unsigned>(batch));
   if (head_dim == 64)
-    hipLaunchKernelGGL(msat_qkv_norm_rope_kernel<64>, dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(msat_qkv_norm_rope_kernel<64>, grid, dim3(256), 0, stream, a);
   else
-    hipLaunchKernelGGL(msat_qkv_norm_rope_kernel<128>, dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(msat_qkv_norm_rope_kernel<128>, grid, dim3(256), 0, stream, a);
   return hipGetLastError();
+}
+}  // namespace
+
+extern "C" hipError_t rldx_msat_qkv_norm_rope_bf16(const rldx_msat_stream_t* streams, int32_t num_streams,
+                                                   int64_t heads, int64_t head_dim, void* q_out, void* k_out,
+                                                   void* v_out, int64_t out_head_stride, int64_t out_row_stride,
+                                                   void* kv_packed, int64_t kv_packed_head_stride, float eps,
+                                                   hipStream_t stream) {
+  return msat_qkv(streams, num_streams, 1, nullptr, heads, head_dim, q_out, k_out, v_out, 0, out_head_stride,
+                  out_row_stride, kv_packed, 0, kv_packed_head_stride, eps, stream);
+}
+
+extern "C" hipError_t rldx_msat_qkv_norm_rope_batch_bf16(const rldx_msat_stream_t* streams, int32_t num_streams,
+                                                         int64_t batch, const int64_t* stream_batch_rows,
+                                                         int64_t heads, int64_t head_dim, void* q_out, void* k_out,
+                                                         void* v_out, int64_t out_batch_stride,
+                                                         int64_t out_head_stride, int64_t out_row_stride,
+                                                         void* kv_packed, int64_t kv_packed_batch_stride,
+                                                         int64_t kv_packed_head_stride, float eps,
+                                                         hipStream_t stream) {
+  return msat_qkv(streams, num_streams, batch, stream_batch_rows, heads, head_dim, q_out, k_out, v_out,
+                  out_batch_stride, out_head_stride, out_row_stride, kv_packed, kv_packed_batch_stride,
+                  kv_packed_head_stride, eps, stream);
 }

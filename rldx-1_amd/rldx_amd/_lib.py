@@ -74,6 +74,11 @@ SIGNATURES = {
         c_i32,
         [ctypes.POINTER(MsatStream), c_i32, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp, c_i64, c_f32, c_vp],
     ),
+    "rldx_msat_qkv_norm_rope_batch_bf16": (
+        c_i32,
+        [ctypes.POINTER(MsatStream), c_i32, c_i64, c_i64p, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp,
+         c_i64, c_i64, c_f32, c_vp],
+    ),
     "rldx_attention_kv_packed_elems": (c_i64, [c_i64, c_i64]),
     "rldx_attention_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64]),
     "rldx_attention_kv_pack_bf16": (c_i32, [c_vp, c_i64p, c_vp, c_i64p, c_vp, c_i64p, c_i64, c_i64, c_i64, c_i64, c_vp]),

@@ -271,18 +271,25 @@ def _check_kvp_out(kvp: torch.Tensor, num_heads: int, M: int, head_dim: int) -> 
 
 
 def msat_qkv_norm_rope(streams: Sequence[StreamSpec], num_heads: int, head_dim: int, eps: float = 1e-6,
-                       out: Optional[tuple] = None, kv_packed: bool = False):
+                       out: Optional[tuple] = None, kv_packed: bool = False, batch: int = 1,
+                       batch_rows: Optional[Sequence[int]] = None):
     """Gather Q/K/V of 1-3 streams into (H, M, D) bf16 with per-stream QK RMSNorm
     (one rounding) and interleaved RoPE on the streams that carry tables.
 
     Returns (q, k, v).  With `kv_packed`, returns (q, kvp) instead: K and V are
     written as the packed K/V tiles `attention_packed` reads, kvp of shape
     (H, kv_packed_elems(M, D)) bf16.  `out` gives the output tensors in the
-    same form.
+    same form.  batch > 1 (rldx_msat_qkv_norm_rope_batch_bf16, one launch):
+    each StreamSpec's qkv holds the rows of batch entry 0 and entry b's start
+    batch_rows[i] rows further on in the same buffer (the rows of entry b may
+    run into entry b + 1's); the outputs gain a leading batch dimension
+    (B, H, M, D) / (B, H, kv_packed_elems(M, D)).
 
     rmsnorm_rope_ds.py:11-231 / rmsnorm_rope_ds_3way.py:22-386 fused layout,
     eager semantics of norms.py:18-22 and action_model/ops.py:48-67."""
     _require(1 <= len(streams) <= 3, "between 1 and 3 streams")
+    _require(batch >= 1 and (batch == 1 or (batch_rows is not None and len(batch_rows) == len(streams))),
+             "batch > 1 needs one batch_rows entry per stream")
     inner = num_heads * head_dim
     descs = (_lib.MsatStream * len(streams))()
     M = 0
@@ -297,20 +304,29 @@ def msat_qkv_norm_rope(streams: Sequence[StreamSpec], num_heads: int, head_dim: 
                  s.k_w.numel() == head_dim and s.q_w.is_contiguous() and s.k_w.is_contiguous(),
                  "norm weights must be contiguous bf16 [head_dim]")
         n = s.qkv.shape[0]
+        if batch > 1 and n > 0:  # the last entry's rows must lie inside the qkv buffer
+            last = s.qkv.storage_offset() + ((batch - 1) * int(batch_rows[i]) + n - 1) * s.qkv.stride(0) + 3 * inner
+            _require(batch_rows[i] >= 0 and last * s.qkv.element_size() <= s.qkv.untyped_storage().nbytes(),
+                     "the batch's rows of a stream run past its qkv buffer")
         cos_p, sin_p, rope_ld = _rope_tables(s, n, head_dim, keep)
         descs[i] = _lib.MsatStream(s.qkv.data_ptr(), s.qkv.stride(0), n, s.q_w.data_ptr(), s.k_w.data_ptr(),
                                    cos_p, sin_p, rope_ld)
         M += n
+    lead = (batch,) if batch > 1 else ()
     if out is None:
-        q = torch.empty((num_heads, M, head_dim), dtype=BF16, device=dev)
-        rest = ((torch.empty((num_heads, kv_packed_elems(M, head_dim)), dtype=BF16, device=dev),) if kv_packed
-                else (torch.empty_like(q), torch.empty_like(q)))
+        q = torch.empty((*lead, num_heads, M, head_dim), dtype=BF16, device=dev)
+        rest = ((torch.empty((*lead, num_heads, kv_packed_elems(M, head_dim)), dtype=BF16, device=dev),)
+                if kv_packed else (torch.empty_like(q), torch.empty_like(q)))
     else:
         q, *rest = out
-        _require(q.shape == (num_heads, M, head_dim), "q out must be (H, M, D)")
+        _require(q.shape == (*lead, num_heads, M, head_dim), "q out must be (H, M, D), or (B, H, M, D) for a batch")
         if kv_packed:
             _require(len(rest) == 1, "packed mode takes out=(q, kvp)")
-            _check_kvp_out(rest[0], num_heads, M, head_dim)
+            if batch > 1:
+                _require(rest[0].shape[0] == batch, "kvp out must be (B, H, >= kv_packed_elems(M, D)) for a batch")
+                _check_kvp_out(rest[0][0], num_heads, M, head_dim)
+            else:
+                _check_kvp_out(rest[0], num_heads, M, head_dim)
         else:
             _require(len(rest) == 2, "out=(q, k, v)")
             for t in rest:
@@ -318,16 +334,25 @@ def msat_qkv_norm_rope(streams: Sequence[StreamSpec], num_heads: int, head_dim: 
     if M == 0:
         return (q, *rest)
     lib = _lib.load()
-    if kv_packed:
+    h_ax = 1 if batch > 1 else 0
+    if batch > 1:
+        kvp = rest[0] if kv_packed else None
+        k, v = (None, None) if kv_packed else rest
+        _lib.check(lib.rldx_msat_qkv_norm_rope_batch_bf16(
+            descs, len(streams), batch, _lib.i64_array(batch_rows), num_heads, head_dim, q.data_ptr(),
+            None if kv_packed else k.data_ptr(), None if kv_packed else v.data_ptr(), q.stride(0), q.stride(1),
+            q.stride(2), kvp.data_ptr() if kv_packed else None, kvp.stride(0) if kv_packed else 0,
+            kvp.stride(1) if kv_packed else 0, float(eps), _stream_ptr(q)), "rldx_msat_qkv_norm_rope_batch_bf16")
+    elif kv_packed:
         kvp = rest[0]
         _lib.check(lib.rldx_msat_qkv_norm_rope_bf16(descs, len(streams), num_heads, head_dim, q.data_ptr(), None, None,
-                                                    q.stride(0), q.stride(1), kvp.data_ptr(), kvp.stride(0),
+                                                    q.stride(h_ax), q.stride(h_ax + 1), kvp.data_ptr(), kvp.stride(0),
                                                     float(eps), _stream_ptr(q)), "rldx_msat_qkv_norm_rope_bf16")
     else:
         k, v = rest
         _lib.check(lib.rldx_msat_qkv_norm_rope_bf16(descs, len(streams), num_heads, head_dim, q.data_ptr(),
-                                                    k.data_ptr(), v.data_ptr(), q.stride(0), q.stride(1), None, 0,
-                                                    float(eps), _stream_ptr(q)), "rldx_msat_qkv_norm_rope_bf16")
+                                                    k.data_ptr(), v.data_ptr(), q.stride(h_ax), q.stride(h_ax + 1),
+                                                    None, 0, float(eps), _stream_ptr(q)), "rldx_msat_qkv_norm_rope_bf16")
     return (q, *rest)
 
 

@@ -602,14 +602,16 @@ class RldxMsat:
 
     def _qkv_norm_rope(self, streams) -> None:
         """Q and the packed K/V tiles of every robot's joint sequence from the QKV
-        rows of its streams: streams = [(qkv rows of the whole batch, rows per
-        robot, rows in the joint sequence, q_norm, k_norm, cos, sin)] in joint
-        order; one launch per robot."""
-        cfg = self.cfg
-        for b in range(self.batch):
-            specs = [Fn.StreamSpec(qkv[b * per:b * per + rows], qn, kn, cos, sin)
-                     for qkv, per, rows, qn, kn, cos, sin in streams]
-            Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q[b], self.kvp[b]), kv_packed=True)
+        rows of its streams, one launch: streams = [(qkv rows of the whole batch,
+        rows per robot, rows in the joint sequence, q_norm, k_norm, cos, sin)] in
+        joint order."""
+        cfg, B = self.cfg, self.batch
+        specs = [Fn.StreamSpec(qkv[:rows], qn, kn, cos, sin) for qkv, per, rows, qn, kn, cos, sin in streams]
+        if B == 1:
+            Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q[0], self.kvp[0]), kv_packed=True)
+        else:
+            Fn.msat_qkv_norm_rope(specs, cfg.heads, cfg.head_dim, cfg.eps, out=(self.q, self.kvp), kv_packed=True,
+                                  batch=B, batch_rows=[st[1] for st in streams])
 
     def _ds_block(self, blk: dict, gm: dict) -> None:
         cfg = self.cfg

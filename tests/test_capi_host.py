@@ -172,6 +172,14 @@ def test_capi_rejects_bad_arguments_without_launching():
     s = _lib.MsatStream(16, 100, 4, 16, 16, None, None, 0)  # row stride < 3*H*D
     assert lib.rldx_msat_qkv_norm_rope_bf16(ctypes.byref(s), 1, 12, 128, 16, 16, 16, 0, 0, None, 0, 1e-6,
                                             None) == HIP_INVALID_VALUE
+    # batched form: batch out of range, or a negative row step between batch entries
+    s = _lib.MsatStream(16, 4608, 4, 16, 16, None, None, 0)
+    for batch, rows in ((65536, 4), (-1, 4), (2, -4)):
+        assert lib.rldx_msat_qkv_norm_rope_batch_bf16(ctypes.byref(s), 1, batch, _lib.i64_array([rows]), 12, 128, 16,
+                                                      None, None, 0, 0, 0, 16, 64 * 128, 64 * 128, 1e-6,
+                                                      None) == HIP_INVALID_VALUE
+    assert lib.rldx_msat_qkv_norm_rope_batch_bf16(ctypes.byref(s), 1, 2, None, 12, 128, 16, None, None, 0, 0, 0, 16,
+                                                  64 * 128, 64 * 128, 1e-6, None) == HIP_INVALID_VALUE
     s = _lib.MsatStream(16, 4608, 40, 16, 16, None, None, 0)  # packed head stride < 2 tiles
     assert lib.rldx_msat_qkv_norm_rope_bf16(ctypes.byref(s), 1, 12, 128, 16, None, None, 0, 0, 16, 64 * 128,
                                             1e-6, None) == HIP_INVALID_VALUE

@@ -187,6 +187,38 @@ def test_msat_qkv_norm_rope(dev, D, H, sizes):
     assert torch.equal(kvp.cpu(), packed_kv_layout(k.cpu().unsqueeze(0), v.cpu().unsqueeze(0))[0])
 
 
+@pytest.mark.parametrize("D,H,sizes,per", [(128, 12, (512, 64, 32), (512, 56, 32)), (64, 24, (96, 32, 17), (96, 18, 17)),
+                                          (64, 4, (3, 5), (3, 5))])
+def test_msat_qkv_norm_rope_batch(dev, D, H, sizes, per):
+    """rldx_msat_qkv_norm_rope_batch_bf16: three batch entries in one launch,
+    each stream's rows stacked entry after entry (`per` rows apart; where
+    per < sizes, an entry's last rows are the next entry's first, as the
+    batched RLDX chain reads its padding rows), equal bit for bit to one
+    launch per entry on the same rows, for the (q, k, v) and packed outputs."""
+    B = 3
+    g = torch.Generator().manual_seed(D + H + 7)
+    inner = H * D
+    streams = _msat_streams(D, H, sizes, seed=D + H + 1)
+    bufs = []
+    for (qkv, qw, kw, cos, sin), n, p in zip(streams, sizes, per):
+        rows = (B - 1) * p + n
+        bufs.append((torch.randn(rows, 3 * inner + 8, generator=g).to(torch.bfloat16).to(dev), qw.to(dev), kw.to(dev),
+                     None if cos is None else cos.to(dev), None if sin is None else sin.to(dev)))
+    for kv_packed in (False, True):
+        specs = [Fn.StreamSpec(buf[:n], qw, kw, cos, sin) for (buf, qw, kw, cos, sin), n in zip(bufs, sizes)]
+        got = Fn.msat_qkv_norm_rope(specs, H, D, kv_packed=kv_packed, batch=B, batch_rows=list(per))
+        for b in range(B):
+            one = [Fn.StreamSpec(buf[b * p:b * p + n], qw, kw, cos, sin)
+                   for (buf, qw, kw, cos, sin), n, p in zip(bufs, sizes, per)]
+            want = Fn.msat_qkv_norm_rope(one, H, D, kv_packed=kv_packed)
+            for x, y in zip(got, want):
+                assert torch.equal(x[b].view(torch.int16), y.view(torch.int16)), (kv_packed, b)
+    # a stream whose last entry would read past its buffer is refused on the host
+    bad = [Fn.StreamSpec(buf[:n], qw, kw, cos, sin) for (buf, qw, kw, cos, sin), n in zip(bufs, sizes)]
+    with pytest.raises(RuntimeError):
+        Fn.msat_qkv_norm_rope(bad, H, D, kv_packed=True, batch=B + 1, batch_rows=list(per))
+
+
 # ---------------------------------------------------------------------------
 # attention
 # ---------------------------------------------------------------------------
