@@ -308,6 +308,7 @@ class RldxMsat:
         Fn._require(int(batch) >= 1, "batch must be >= 1")
         self.batch = int(batch)
         if weights_of is None:
+            Fn._require(sd is not None, "a state dict, or weights_of (a chain whose packed weights to share)")
             self._pack_weights(sd)
         else:
             Fn._require(weights_of.cfg == cfg and weights_of.dev == self.dev and weights_of.bf16_quirk == bf16_quirk,
