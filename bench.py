@@ -454,13 +454,15 @@ def kernel_lines(torch, reps: int):
     return out
 
 
-def step_gemms(step):
+def step_gemms(step, pw=None):
     """The four grouped-GEMM launches of a block of `step`, as {name: (launch(L), flops, bytes)}:
     algorithmic flops and HBM bytes (weights + biases of the 3 streams, activations
-    in, outputs out, residual in) of one launch."""
+    in, outputs out, residual in) of one launch.  pw: packed weights to use instead
+    of the step's (a dict with the same keys, e.g. copies of them)."""
     from rldx_amd import functional as Fn
 
-    cfg, w, pw = step.cfg, step.w, step.pw
+    cfg, w = step.cfg, step.w
+    pw = step.pw if pw is None else pw
     n, d, inner, ffn = cfg.tokens, cfg.hidden, cfg.inner, cfg.ffn
     rows = [(s, cfg.rows(s)) for s in ("vl", "sa", "p")]
 
@@ -507,23 +509,43 @@ def step_gemms(step):
     }
 
 
+# The memory-side cache (MALL) holds 256 MB: a GEMM line cycles through at least this many bytes of weights,
+# so that every launch streams its weights from HBM as it does in the action step.
+WEIGHT_CYCLE_BYTES = 768 << 20
+
+
 def gemm_lines(torch, step) -> dict:
-    """Mean launch time of each grouped GEMM over the 16 blocks' weights (graph of 16 launches)."""
+    """Mean launch time of each grouped GEMM over the 16 blocks' weights, repeated with
+    copies of them until a graph of launches cycles through WEIGHT_CYCLE_BYTES (the
+    Proj weights of the 16 blocks, 227 MB, would otherwise stay in the MALL)."""
+    from rldx_amd import functional as Fn
+
     out = {}
     blocks = step.cfg.blocks
     for name, (fn, flops, byts) in step_gemms(step).items():
+        keys = [f"{s}.{name}" for s in ("vl", "sa", "p")]
+        wbytes = sum(step.pw[k][0].data.numel() * 2 for k in keys)
+        sets = -(-WEIGHT_CYCLE_BYTES // (wbytes * blocks))
+        fns = [fn]
+        for _ in range(1, sets):
+            alt = dict(step.pw)
+            for k in keys:
+                alt[k] = [Fn.PackedWeight(p.data.clone(), p.n, p.k, p.swiglu_pairs, p.row_sums) for p in step.pw[k]]
+            fns.append(step_gemms(step, alt)[name][0])
         it = {"L": 0}
 
         def run():
-            fn(it["L"] % blocks)
+            fns[(it["L"] // blocks) % sets](it["L"] % blocks)
             it["L"] += 1
 
-        ms = graph_time_ms(run, blocks, torch)
+        ms = graph_time_ms(run, blocks * sets, torch)
         t = ms * 1e-3
         roof_t = max(flops / (BF16_MFMA_PEAK_TFLOPS * 1e12), byts / (HBM_PEAK_GBS * 1e9))
         bound = "hbm" if byts / (HBM_PEAK_GBS * 1e9) >= flops / (BF16_MFMA_PEAK_TFLOPS * 1e12) else "mfma"
         out[f"gemm_{name}"] = dict(us=ms * 1e3, flops=flops, bytes=byts, tflops=flops / t / 1e12,
-                                   gbs=byts / t / 1e9, bound=bound, roofline_us=roof_t * 1e6, frac=roof_t / t)
+                                   gbs=byts / t / 1e9, bound=bound, roofline_us=roof_t * 1e6, frac=roof_t / t,
+                                   weight_sets=sets, weight_cycle_mb=wbytes * blocks * sets / 1e6)
+        del fns
     return out
 
 
