@@ -161,10 +161,13 @@ constexpr int kLnSlotsMax = 8;
 // The last kLdsTail bytes of a kernel's LDS: the SwiGLU tiles' W row sums
 // (gate and up of at most 64 output columns, fp32, stored at the prologue for
 // the LayerNorm fold of the epilogue; kernels without WIDE tiles, whose rings
-// leave room behind them), then 16 bytes holding the split-K arrival flag, used
-// by every kernel (in a WIDE kernel inside its ring area, past its epilogue).
+// leave room behind them), the biases of the same columns (fp32, for the
+// register epilogue of the packed SwiGLU tiles), then 16 bytes holding the
+// split-K arrival flag, used by every kernel (in a WIDE kernel inside its ring
+// area, past its epilogue).
 constexpr int kWsumStash = 2 * 64 * 4;
-constexpr int kLdsTail = kWsumStash + 16;
+constexpr int kBiasStash = 2 * 64 * 4;
+constexpr int kLdsTail = kWsumStash + kBiasStash + 16;
 template <class C>
 constexpr int epi_bytes() { return (ln_stats_off<C>() + 2 * 512) * 4; }  // fp32 tiles + row statistics
 constexpr int kLdsBytes =
@@ -342,16 +345,36 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   // so all of them are in flight together: they go through a descriptor bounded
   // to the bias (a missing bias is an empty one: every read returns zero), and a
   // chunk past the output columns reads column 0's and is zeroed when packed.
+  // Register epilogue (packed SwiGLU tiles of one K-group whose waves each hold
+  // a gate / up n-block pair, no split-K): every lane finishes the outputs of
+  // its own accumulators, so the fp32 tile never goes through LDS.  Its lanes
+  // need the biases (and W row sums) of their accumulator columns, not of a
+  // thread's output chunk: threads t < 2 OC load the bias of one column and
+  // store it at the prologue's wait, as the row sums are.
+  constexpr bool kRegEpi = EPI == kEpiSwigluPacked && C::KG == 1 && BNW == 2 && !K;
+  const bool reg_epi = kRegEpi && G.splits == 1;
   uint16_t braw[16];
   {
     const __amdgpu_buffer_rsrc_t brs = rsrc(G.bias, G.bias ? G.n * 2 : 0);
     const int bcol = col_ok ? col : 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      braw[i] = static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(brs, (bcol + i) * 2, 0, 0));
-      braw[8 + i] = kSwiglu ? static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(brs, (G.n / 2 + bcol + i) * 2, 0, 0))
-                            : uint16_t{0};
+    for (int i = 0; i < 16; ++i) braw[i] = 0;
+    if (!reg_epi) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        braw[i] = static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(brs, (bcol + i) * 2, 0, 0));
+        braw[8 + i] = kSwiglu ? static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(brs, (G.n / 2 + bcol + i) * 2, 0, 0))
+                              : uint16_t{0};
+      }
     }
+  }
+  [[maybe_unused]] float bsv = 0.f;  // register epilogue: the bias of column t % OC (gate for t < OC, else up)
+  if constexpr (kRegEpi) {
+    const int t = static_cast<int>(threadIdx.x);
+    const __amdgpu_buffer_rsrc_t brs = rsrc(G.bias, G.bias ? G.n * 2 : 0);
+    const int bc = nt * OC + t % OC;
+    if (reg_epi && t < 2 * OC && bc < n_out)
+      bsv = bf(static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(brs, ((t < OC ? 0 : G.n / 2) + bc) * 2, 0, 0)));
   }
   uint32_t bpk[8];
   // LayerNorm fold: W row sums of this thread's columns (gate and up for SwiGLU).
@@ -443,6 +466,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   if constexpr (kStash) {  // read back after the K loop, whose barriers publish it
     if (static_cast<int>(threadIdx.x) < 2 * OC) wsl[threadIdx.x] = wsv;
   }
+  if constexpr (kRegEpi) {
+    if (reg_epi && static_cast<int>(threadIdx.x) < 2 * OC) wsl[kWsumStash / 4 + threadIdx.x] = bsv;
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     bpk[i] = col_ok ? static_cast<uint32_t>(braw[2 * i]) | (static_cast<uint32_t>(braw[2 * i + 1]) << 16) : 0u;
@@ -479,7 +505,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   else if constexpr (LN && kSwiglu) load_wsum();
   wait_barrier<0>();  // the ring's last reads and loads are done; LDS becomes the fp32 tiles
   float* tiles = reinterpret_cast<float*>(lds);
-  {
+  if (!reg_epi) {
     float* t = tiles + grp * C::TILE;
 #pragma unroll
     for (int bb = 0; bb < BNW; ++bb)
@@ -527,6 +553,62 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     rs = lnst[2 * r];
     rm = lnst[2 * r + 1];
   };
+  if constexpr (kRegEpi) {
+    if (reg_epi) {
+      // Lane (l32, g) of wave (wm, wn) holds, for tile row 32 wm + l32, the gate
+      // (acc[0]) and up (acc[1]) sums of the wave's output columns
+      // 8 q4 + 4 g + c (element 4 q4 + c): the sums the fp32 tile would hand to
+      // the store phase below, finished with the same arithmetic.
+      const int r = 32 * wm + l32, row = mt * R + r;
+      float rs = 0.f, rm = 0.f;
+      if constexpr (LN) ln_row(r, rs, rm);
+      const float* bst = wsl + kWsumStash / 4;  // biases: gate [0, OC), up [OC, 2 OC); W row sums likewise at wsl
+      uint32_t od[4][2];
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int oc = 32 * wn + 8 * q4 + 4 * g;
+        const floatx4 bgv = *reinterpret_cast<const floatx4*>(bst + oc);
+        const floatx4 buv = *reinterpret_cast<const floatx4*>(bst + OC + oc);
+        float yg[4], yu[4];
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) {
+          yg[c4] = acc[0][4 * q4 + c4];
+          yu[c4] = acc[1][4 * q4 + c4];
+        }
+        if constexpr (LN) {
+          const floatx4 wgv = *reinterpret_cast<const floatx4*>(wsl + oc);
+          const floatx4 wuv = *reinterpret_cast<const floatx4*>(wsl + OC + oc);
+#pragma unroll
+          for (int c4 = 0; c4 < 4; ++c4) {
+            yg[c4] = ln_fold(yg[c4], rs, rm, wgv[c4]);
+            yu[c4] = ln_fold(yu[c4], rs, rm, wuv[c4]);
+          }
+        }
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const uint32_t gp = pack_bf16x2(yg[2 * p] + bgv[2 * p], yg[2 * p + 1] + bgv[2 * p + 1]);
+          const uint32_t up = pack_bf16x2(yu[2 * p] + buv[2 * p], yu[2 * p + 1] + buv[2 * p + 1]);
+          od[q4][p] = swiglu_bf16x2(bf16x2_lo(gp), bf16x2_hi(gp), bf16x2_lo(up), bf16x2_hi(up));
+        }
+      }
+      // 16-byte output chunks: chunk c8 (8 columns) of the wave's 32 is split
+      // over the lanes l32 and l32 + 32 (lane half g holds its columns
+      // 4 g .. 4 g + 3); the two swap halves so that lane half g stores chunk
+      // 2 pp + g whole, pp = 0, 1.
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp) {
+        const uint32_t w0 = g == 0 ? od[2 * pp + 1][0] : od[2 * pp][0];
+        const uint32_t w1 = g == 0 ? od[2 * pp + 1][1] : od[2 * pp][1];
+        const uint32_t x0 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w0), 32, 64));
+        const uint32_t x1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w1), 32, 64));
+        const u32x4 o = g == 0 ? u32x4{od[2 * pp][0], od[2 * pp][1], x0, x1}
+                               : u32x4{x0, x1, od[2 * pp + 1][0], od[2 * pp + 1][1]};
+        const int ocol = nt * OC + 32 * wn + 8 * (2 * pp + g);
+        if (row < G.m && ocol < n_out) *reinterpret_cast<u32x4*>(G.out + packed_act_offset(row, ocol, G.ldo)) = o;
+      }
+      return;
+    }
+  }
   // 8 consecutive fp32 sums (K-groups in order) of tile row r from tile column tc
   auto sum8 = [&](int r, int tc, float (&v)[8]) {
     floatx4 lo = *reinterpret_cast<const floatx4*>(&tiles[r * C::TP + tc]);
@@ -731,7 +813,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
             slot(split, i) + 4 * e, 0, kCpolDevice);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    int* last = reinterpret_cast<int*>(wsl + kWsumStash / 4);  // the LDS tail: past the stash and every epilogue tile
+    int* last = reinterpret_cast<int*>(wsl + (kWsumStash + kBiasStash) / 4);  // the LDS tail: past the stashes and every epilogue tile
     if (threadIdx.x == 0)
       *last = __hip_atomic_fetch_add(G.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
               static_cast<unsigned>(G.splits - 1);
