@@ -254,8 +254,11 @@ __device__ __forceinline__ void wait_barrier() {
 
 // K (the kernel's WIDE) only keeps the tile specializations of the wide and
 // narrow kernels apart: the host compilation pass rejects a second caller of a
-// specialization whose body holds the 16-byte LDS-load builtin.
-template <class C, int EPI, bool K, bool LN>
+// specialization whose body holds the 16-byte LDS-load builtin.  DP: the
+// kernel is a deep-ring instantiation (one workgroup per CU).  TR: the MFMAs
+// take (A chunk, W chunk), so each accumulator holds its block untransposed
+// (the V tiles of the QKV epilogue, whose lanes then hold packed V chunks).
+template <class C, int EPI, bool K, bool LN, bool DP, bool TR = false>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int item, u32x4* lds, float* wsl) {
   constexpr bool kSwiglu = EPI == kEpiSwiglu || EPI == kEpiSwigluPacked;
   constexpr int MB = C::MB, NB = C::NB, BNW = C::BNW, U = C::U, CH = C::CH, NSLOT = C::NSLOT;
@@ -311,9 +314,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   for (int bb = 0; bb < BNW; ++bb) acc[bb] = floatx16{};
   auto mma = [&](int b, int u) {
 #pragma unroll
-    for (int bb = 0; bb < BNW; ++bb)
-      acc[bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xw[b][u][bb]),
-                                                        __builtin_bit_cast(bf16x8, xa[b][u]), acc[bb], 0, 0, 0);
+    for (int bb = 0; bb < BNW; ++bb) {
+      if constexpr (TR)
+        acc[bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xa[b][u]),
+                                                          __builtin_bit_cast(bf16x8, xw[b][u][bb]), acc[bb], 0, 0, 0);
+      else
+        acc[bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, xw[b][u][bb]),
+                                                          __builtin_bit_cast(bf16x8, xa[b][u]), acc[bb], 0, 0, 0);
+    }
   };
 
   // ---- epilogue operands, loaded before the K loop (in flight beside the ring
@@ -353,13 +361,20 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   // store it at the prologue's wait, as the row sums are.
   constexpr bool kRegEpi = EPI == kEpiSwigluPacked && C::KG == 1 && BNW == 2 && !K;
   const bool reg_epi = kRegEpi && G.splits == 1;
+  // Register epilogue of the QKV epilogue (head_dim 128, one K-group, each
+  // wave two n-blocks of a head; deep-ring kernels, whose 256 VGPRs hold its
+  // operands): Q and K tiles (see there), and V tiles, which the launch runs
+  // with TR accumulators.
+  constexpr bool kRegQkv = EPI == kEpiQkv && C::KG == 1 && BNW == 2 && DP && !TR;
+  const bool reg_qkv = kRegQkv && nt * OC / a.qkv.inner < 2;
+  static_assert(!TR || (EPI == kEpiQkv && C::KG == 1 && BNW == 2 && DP), "TR: V tiles of the deep QKV launch");
   uint16_t braw[16];
   {
     const __amdgpu_buffer_rsrc_t brs = rsrc(G.bias, G.bias ? G.n * 2 : 0);
     const int bcol = col_ok ? col : 0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) braw[i] = 0;
-    if (!reg_epi) {
+    if (!reg_epi && !reg_qkv) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         braw[i] = static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(brs, (bcol + i) * 2, 0, 0));
@@ -426,8 +441,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     constexpr int D = EPI == kEpiQkv ? 128 : 64;
     const int which = nt * OC / a.qkv.inner;
     if (which < 2) {
-      qk_w = *reinterpret_cast<const u32x4*>((which == 0 ? G.qn_w : G.kn_w) + cc % D);
-    } else {
+      if (!reg_qkv) qk_w = *reinterpret_cast<const u32x4*>((which == 0 ? G.qn_w : G.kn_w) + cc % D);
+    } else if constexpr (!TR) {
       constexpr int NCH = D / 16;
       const int t = static_cast<int>(threadIdx.x);
       const int hh = t / (NCH * 64) % (OC / D), idx = t % (NCH * 64);
@@ -435,6 +450,42 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
       const __amdgpu_buffer_rsrc_t vbr = rsrc(G.bias, G.bias ? G.n * 2 : 0);  // no bias: reads zero
       v_bias = bf(static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(vbr, (nt * OC + d) * 2, 0, 0)));
       if constexpr (LN) v_wsum = G.wsum[nt * OC + d];
+    }
+  }
+  // register QKV epilogue operands, loaded with the prologue's loads: for a Q
+  // or K tile the biases and W row sums of the lane's 32 accumulator columns
+  // and the norm weights of the 4 whole 8-column chunks it stores; for a V
+  // tile (TR) the bias and W row sum of the lane's 2 columns
+  [[maybe_unused]] uint32_t rq_b[2][4][2];
+  [[maybe_unused]] floatx4 rq_ws[2][4];
+  [[maybe_unused]] u32x4 rq_w[2][2];
+  [[maybe_unused]] float rv_b[2] = {0.f, 0.f}, rv_ws[2] = {0.f, 0.f};
+  if constexpr (kRegQkv) {
+    if (reg_qkv) {
+      const __amdgpu_buffer_rsrc_t brs = rsrc(G.bias, G.bias ? G.n * 2 : 0);  // no bias: reads zero
+      const uint16_t* nw = nt * OC / a.qkv.inner == 0 ? G.qn_w : G.kn_w;
+#pragma unroll
+      for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int c0 = nt * OC + 32 * (2 * wn + bb) + 8 * q4 + 4 * g;
+          rq_b[bb][q4][0] = __builtin_amdgcn_raw_buffer_load_b32(brs, c0 * 2, 0, 0);
+          rq_b[bb][q4][1] = __builtin_amdgcn_raw_buffer_load_b32(brs, c0 * 2 + 4, 0, 0);
+          if constexpr (LN) rq_ws[bb][q4] = *reinterpret_cast<const floatx4*>(G.wsum + c0);
+        }
+#pragma unroll
+      for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) rq_w[bb][pp] = *reinterpret_cast<const u32x4*>(nw + 64 * wn + 32 * bb + 16 * pp + 8 * g);
+    }
+  }
+  if constexpr (TR) {
+    const __amdgpu_buffer_rsrc_t brs = rsrc(G.bias, G.bias ? G.n * 2 : 0);
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+      const int c0 = nt * OC + 32 * (2 * wn + bb) + l32;
+      rv_b[bb] = bf(static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(brs, c0 * 2, 0, 0)));
+      if constexpr (LN) rv_ws[bb] = G.wsum[c0];
     }
   }
   // LayerNorm fold: this thread's slots of its row, loaded before the ring
@@ -493,6 +544,23 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     }
   }
 
+  // RoPE tables of the register Q / K epilogue's chunks (streams with RoPE),
+  // loaded while the LayerNorm factors are reduced
+  [[maybe_unused]] floatx4 rq_c[2][2], rq_s[2][2];
+  if constexpr (kRegQkv) {
+    if (reg_qkv && G.cos != nullptr) {
+      const int64_t rr = min(mt * 32 * MB + 32 * wm + l32, G.m - 1);
+#pragma unroll
+      for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+          const int cd = 64 * wn + 32 * bb + 16 * pp + 8 * g;
+          rq_c[bb][pp] = *reinterpret_cast<const floatx4*>(G.cos + rr * G.rope_ld + cd / 2);
+          rq_s[bb][pp] = *reinterpret_cast<const floatx4*>(G.sin + rr * G.rope_ld + cd / 2);
+        }
+    }
+  }
+
   float bg[8], bu[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -505,7 +573,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   else if constexpr (LN && kSwiglu) load_wsum();
   wait_barrier<0>();  // the ring's last reads and loads are done; LDS becomes the fp32 tiles
   float* tiles = reinterpret_cast<float*>(lds);
-  if (!reg_epi) {
+  if (!reg_epi && !reg_qkv && !TR) {
     float* t = tiles + grp * C::TILE;
 #pragma unroll
     for (int bb = 0; bb < BNW; ++bb)
@@ -643,6 +711,144 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     const int n0 = nt * OC;
     const int which = n0 / O.inner;  // uniform per tile
     const int h0 = (n0 - which * O.inner) / D;
+    if constexpr (kRegQkv) {
+      if (reg_qkv) {
+        // Lane (l32, g) of wave (wm, wn) holds, for tile row 32 wm + l32, the
+        // sums of head columns 64 wn + 32 bb + 8 q4 + 4 g + c (acc[bb], element
+        // 4 q4 + c): halves of the head's 8-column chunks 8 wn + 4 bb + q4.  The
+        // arithmetic is the store phase's below: x = bf16(fold(acc) + bias); the
+        // chunks made whole by a swap of halves with lane l ^ 32 (lane half g
+        // keeps chunks 8 wn + 4 bb + 2 pp + g); each chunk's sum of squares in
+        // column order; then the same butterfly over the row's 16 chunks, level
+        // by level: chunk ^ 8 is the other wave of the row (through LDS), ^ 4
+        // and ^ 2 are in the lane, ^ 1 is lane l ^ 32.
+        static_assert(D == 128 && OC == 128, "one head of 128 columns per tile");
+        const int r = 32 * wm + l32, row = mt * R + r;
+        float rs = 0.f, rm = 0.f;
+        if constexpr (LN) ln_row(r, rs, rm);
+        uint32_t xp[2][4][2];
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+              float x0 = acc[bb][4 * q4 + 2 * p], x1 = acc[bb][4 * q4 + 2 * p + 1];
+              if constexpr (LN) {
+                x0 = ln_fold(x0, rs, rm, rq_ws[bb][q4][2 * p]);
+                x1 = ln_fold(x1, rs, rm, rq_ws[bb][q4][2 * p + 1]);
+              }
+              xp[bb][q4][p] = pack_bf16x2(x0 + bf16x2_lo(rq_b[bb][q4][p]), x1 + bf16x2_hi(rq_b[bb][q4][p]));
+            }
+        u32x4 xc[2][2];
+        float ss[2][2];
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+          for (int pp = 0; pp < 2; ++pp) {
+            const uint32_t w0 = g == 0 ? xp[bb][2 * pp + 1][0] : xp[bb][2 * pp][0];
+            const uint32_t w1 = g == 0 ? xp[bb][2 * pp + 1][1] : xp[bb][2 * pp][1];
+            const uint32_t o0 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w0), 32, 64));
+            const uint32_t o1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w1), 32, 64));
+            xc[bb][pp] = g == 0 ? u32x4{xp[bb][2 * pp][0], xp[bb][2 * pp][1], o0, o1}
+                                : u32x4{o0, o1, xp[bb][2 * pp + 1][0], xp[bb][2 * pp + 1][1]};
+            float s2 = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float lo = bf16x2_lo(xc[bb][pp][e]), hi = bf16x2_hi(xc[bb][pp][e]);
+              s2 += lo * lo;
+              s2 += hi * hi;
+            }
+            ss[bb][pp] = s2;
+          }
+        floatx4* const exch = reinterpret_cast<floatx4*>(tiles);  // [8 waves][64 lanes], in the ring's area
+        exch[wv * 64 + lane] = floatx4{ss[0][0], ss[0][1], ss[1][0], ss[1][1]};
+        __syncthreads();
+        const floatx4 ps = exch[(wv ^ 1) * 64 + lane];  // the row's other wave: wn ^ 1
+        const float t00 = ss[0][0] + ps[0], t01 = ss[0][1] + ps[1], t10 = ss[1][0] + ps[2], t11 = ss[1][1] + ps[3];
+        const float u0 = t00 + t10, u1 = t01 + t11;
+        const float v = u0 + u1;
+        const float sum = v + __shfl_xor(v, 32, 64);
+        uint16_t* kvh = O.kvp + h0 * O.kvp_sh;
+        const int64_t key = static_cast<int64_t>(G.m_begin) + row;
+        {
+#pragma clang fp contract(off)
+          const float rinv = 1.0f / __builtin_sqrtf(sum * (1.0f / D) + O.eps);
+#pragma unroll
+          for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+            for (int pp = 0; pp < 2; ++pp) {
+              const int cd = 64 * wn + 32 * bb + 16 * pp + 8 * g;
+              float y[8];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float xl = bf16x2_lo(xc[bb][pp][e]), xh = bf16x2_hi(xc[bb][pp][e]);
+                const uint32_t yp = pack_bf16x2(bf16x2_lo(rq_w[bb][pp][e]) * (xl * rinv),
+                                                bf16x2_hi(rq_w[bb][pp][e]) * (xh * rinv));
+                y[2 * e] = bf16x2_lo(yp);
+                y[2 * e + 1] = bf16x2_hi(yp);
+              }
+              u32x4 o;
+              if (G.cos != nullptr) {
+                const floatx4 c = rq_c[bb][pp], sn = rq_s[bb][pp];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                  const float re = y[2 * p], im = y[2 * p + 1];
+                  o[p] = pack_bf16x2(re * c[p] - im * sn[p], re * sn[p] + im * c[p]);
+                }
+              } else {
+#pragma unroll
+                for (int p = 0; p < 4; ++p) o[p] = pack_bf16x2(y[2 * p], y[2 * p + 1]);
+              }
+              if (row < G.m) {
+                if (which == 0)
+                  *reinterpret_cast<u32x4*>(O.q + h0 * O.q_sh + key * O.q_sm + cd) = o;
+                else
+                  *reinterpret_cast<u32x4*>(kvh + packed_k_offset(key, cd, D)) = o;
+              } else if (which == 1 && (row & ~31) < G.m) {
+                *reinterpret_cast<u32x4*>(kvh + packed_k_offset(key, cd, D)) = u32x4{0, 0, 0, 0};
+              }
+            }
+        }
+        return;
+      }
+    }
+    if constexpr (TR) {
+      // V tile with untransposed accumulators: lane (l32, g) of wave (wm, wn)
+      // holds head column d = 32 db + l32 (db = 2 wn + bb) of keys
+      // 32 wm + 8 q + 4 g + c (acc[bb], element 4 q + c) -- element e of packed
+      // V chunk 2 db + s2 is acc[bb][8 s2 + e], the lane's own.  The store
+      // phase's arithmetic below, without the fp32 tile.
+      constexpr int NCH = D / 16;
+      const int row0 = mt * R + 32 * wm;  // first stream row of the wave's 32-key tile
+      if (row0 < G.m) {
+        uint16_t* kvt = O.kvp + h0 * O.kvp_sh + ((G.m_begin + row0) >> 5) * (64 * D) + NCH * 512;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          float rs[8], rm[8];  // LayerNorm factors of the chunk's keys 32 wm + 16 s2 + 8 (e / 4) + 4 g + e % 4
+          if constexpr (LN) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ln_row(32 * wm + 16 * s2 + 8 * (e >> 2) + 4 * g + (e & 3), rs[e], rm[e]);
+          }
+#pragma unroll
+          for (int bb = 0; bb < 2; ++bb) {
+            u32x4 o;
+#pragma unroll
+            for (int e2 = 0; e2 < 4; ++e2) {
+              float lo = acc[bb][8 * s2 + 2 * e2], hi = acc[bb][8 * s2 + 2 * e2 + 1];
+              if constexpr (LN) {
+                lo = ln_fold(lo, rs[2 * e2], rm[2 * e2], rv_ws[bb]);
+                hi = ln_fold(hi, rs[2 * e2 + 1], rm[2 * e2 + 1], rv_ws[bb]);
+              }
+              const int k0 = row0 + 16 * s2 + 8 * (e2 >> 1) + 4 * g + 2 * (e2 & 1);
+              o[e2] = pack_bf16x2(k0 < G.m ? lo + rv_b[bb] : 0.f, k0 + 1 < G.m ? hi + rv_b[bb] : 0.f);
+            }
+            *reinterpret_cast<u32x4*>(kvt + ((2 * (2 * wn + bb) + s2) * 64 + lane) * 8) = o;
+          }
+        }
+      }
+      return;
+    }
     if (which == 2) {
       constexpr int NCH = D / 16;  // 1 KB chunks per K or V part of a head's 32-key tile
       static_assert(kThreads % (HPT * NCH * 64) == 0, "a thread's V column (hh, idx) is the same on every pass");
@@ -916,33 +1122,42 @@ __global__ __launch_bounds__(kThreads, DEEP ? 2 : 4) void gemm_kernel(GemmArgs a
   const int item = a.spread ? r : (r % kXcds) * G.per_xcd + r / kXcds;
   if (item >= G.items) return;
   if constexpr (WIDE && DEEP) {  // 128-column tiles (whole heads for the QKV epilogue)
-    if (G.cfg == kTile128)
-      gemm_tile<Cfg128D, EPI, WIDE, LN>(a, G, item, lds, wsl);
-    else if (G.cfg == kTile64x128)
-      gemm_tile<Cfg64x128D, EPI, WIDE, LN>(a, G, item, lds, wsl);
+    if (G.cfg == kTile128) {
+      if constexpr (EPI == kEpiQkv) {
+        // V tiles (the last third of [Q | K | V]) with untransposed accumulators
+        const int nt = item / G.splits / G.m_tiles;
+        if (nt * 128 / a.qkv.inner == 2)
+          gemm_tile<Cfg128D, EPI, WIDE, LN, DEEP, true>(a, G, item, lds, wsl);
+        else
+          gemm_tile<Cfg128D, EPI, WIDE, LN, DEEP>(a, G, item, lds, wsl);
+      } else {
+        gemm_tile<Cfg128D, EPI, WIDE, LN, DEEP>(a, G, item, lds, wsl);
+      }
+    } else if (G.cfg == kTile64x128)
+      gemm_tile<Cfg64x128D, EPI, WIDE, LN, DEEP>(a, G, item, lds, wsl);
     else
-      gemm_tile<Cfg32x128D, EPI, WIDE, LN>(a, G, item, lds, wsl);
+      gemm_tile<Cfg32x128D, EPI, WIDE, LN, DEEP>(a, G, item, lds, wsl);
   } else if constexpr (WIDE) {
     if (G.cfg == kTile128)
-      gemm_tile<Cfg128, EPI, WIDE, LN>(a, G, item, lds, wsl);
+      gemm_tile<Cfg128, EPI, WIDE, LN, DEEP>(a, G, item, lds, wsl);
     else if (G.cfg == kTile64x128)
-      gemm_tile<Cfg64x128, EPI, WIDE, LN>(a, G, item, lds, wsl);
+      gemm_tile<Cfg64x128, EPI, WIDE, LN, DEEP>(a, G, item, lds, wsl);
     else
-      gemm_tile<Cfg32x128, EPI, WIDE, LN>(a, G, item, lds, wsl);
+      gemm_tile<Cfg32x128, EPI, WIDE, LN, DEEP>(a, G, item, lds, wsl);
   } else if constexpr (DEEP) {
     if (G.cfg == kTile128)
-      gemm_tile<Cfg128D, EPI, WIDE, LN>(a, G, item, lds, wsl);
+      gemm_tile<Cfg128D, EPI, WIDE, LN, DEEP>(a, G, item, lds, wsl);
     else if (G.cfg == kTile64)
-      gemm_tile<Cfg64D, EPI, WIDE, LN>(a, G, item, lds, wsl);
+      gemm_tile<Cfg64D, EPI, WIDE, LN, DEEP>(a, G, item, lds, wsl);
     else
-      gemm_tile<Cfg32D, EPI, WIDE, LN>(a, G, item, lds, wsl);
+      gemm_tile<Cfg32D, EPI, WIDE, LN, DEEP>(a, G, item, lds, wsl);
   } else {
     if (G.cfg == kTile128)
-      gemm_tile<Cfg128, EPI, WIDE, LN>(a, G, item, lds, wsl);
+      gemm_tile<Cfg128, EPI, WIDE, LN, DEEP>(a, G, item, lds, wsl);
     else if (G.cfg == kTile64)
-      gemm_tile<Cfg64, EPI, WIDE, LN>(a, G, item, lds, wsl);
+      gemm_tile<Cfg64, EPI, WIDE, LN, DEEP>(a, G, item, lds, wsl);
     else
-      gemm_tile<Cfg32, EPI, WIDE, LN>(a, G, item, lds, wsl);
+      gemm_tile<Cfg32, EPI, WIDE, LN, DEEP>(a, G, item, lds, wsl);
   }
 }
 
