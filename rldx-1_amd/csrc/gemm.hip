@@ -152,8 +152,12 @@ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 // slots of each thread: 512 pairs).
 template <class C>
 constexpr int ln_stats_off() { return C::KG * C::TILE; }  // floats
+// The register epilogue of tiles with one K-group and gate / up n-block pairs
+// keeps its LayerNorm partial pairs (512 threads) and row factors past the ring.
 template <class C>
-constexpr int lds_bytes() { return cmax(C::RING * 1024, (ln_stats_off<C>() + 2 * 512) * 4); }
+constexpr int reg_ln_bytes() { return C::KG == 1 && C::BNW == 2 ? C::RING * 1024 + (2 * 512 + 2 * 32 * C::MB) * 4 : 0; }
+template <class C>
+constexpr int lds_bytes() { return cmax(cmax(C::RING * 1024, (ln_stats_off<C>() + 2 * 512) * 4), reg_ln_bytes<C>()); }
 // LayerNorm statistics [k / 64][m][2]: thread t of a tile of R rows sums slots
 // [q SPL, (q + 1) SPL) of row t % R (q = t / R, SPL = ceil(slots R / 512)),
 // at most kLnSlotsMax (k <= 2048 at 128-row tiles).
@@ -505,6 +509,43 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   }
 #pragma unroll
   for (int s = 0; s < NSLOT - 1; ++s) dma(s, s);
+  // Register epilogue with the LayerNorm fold: the row factors are reduced here,
+  // beside the ring fill, in LDS past the ring (the partial pairs of the
+  // kThreads threads, then the R rows' factors), the same sums in the same order
+  // as the store phase's reduction below; the prologue's barrier publishes them,
+  // so the epilogue needs no barrier at all.
+  float* const lnp = reinterpret_cast<float*>(lds) + C::RING * 256;
+  static_assert(!kRegEpi || (kThreads == 512 && C::RING * 1024 + (2 * kThreads + 2 * R) * 4 <= reg_ln_bytes<C>()),
+                "LayerNorm factors of the register epilogue past the ring");
+  if constexpr (kRegEpi && LN) {
+    if (reg_epi) {
+      float q1 = 0.f, q2 = 0.f;
+#pragma unroll
+      for (int j = 0; j < kLnSlotsMax; ++j)
+        if (j < ln_spl && ln_q * ln_spl + j < ln_slots) {
+          q1 += lv[j][0];
+          q2 += lv[j][1];
+        }
+      lnp[2 * threadIdx.x] = q1;
+      lnp[2 * threadIdx.x + 1] = q2;
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // (the ring loads stay in flight)
+      const int r = static_cast<int>(threadIdx.x);
+      if (r < R) {
+        float s1 = lnp[2 * r], s2 = lnp[2 * r + 1];
+#pragma unroll
+        for (int pq = 1; pq < kThreads / R; ++pq) {
+          s1 += lnp[(pq * R + r) * 2];
+          s2 += lnp[(pq * R + r) * 2 + 1];
+        }
+        const float inv_k = 1.0f / static_cast<float>(G.k);
+        const float mean = s1 * inv_k;
+        const float var = __builtin_fmaxf(__builtin_fmaf(-mean, mean, s2 * inv_k), 0.f);
+        const float rsd = __builtin_amdgcn_rsqf(var + a.ln_eps);
+        lnp[2 * kThreads + 2 * r] = rsd;
+        lnp[2 * kThreads + 2 * r + 1] = rsd * mean;
+      }
+    }
+  }
   wait_barrier<(NSLOT - 2) * C::ND>();
   if constexpr (LN) {
 #pragma unroll
@@ -544,6 +585,71 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     }
   }
 
+  if constexpr (kRegEpi) {
+    if (reg_epi) {
+      // Straight after the K loop: no operand of this epilogue is in the ring
+      // (the stashes and the LayerNorm factors lie past it, published by the
+      // loop's barriers), so no wave waits for another.
+      // Lane (l32, g) of wave (wm, wn) holds, for tile row 32 wm + l32, the gate
+      // (acc[0]) and up (acc[1]) sums of the wave's output columns
+      // 8 q4 + 4 g + c (element 4 q4 + c): the sums the fp32 tile would hand to
+      // the store phase below, finished with the same arithmetic.
+      const int r = 32 * wm + l32, row = mt * R + r;
+      float rs = 0.f, rm = 0.f;
+      if constexpr (LN) {
+        rs = lnp[2 * kThreads + 2 * r];
+        rm = lnp[2 * kThreads + 2 * r + 1];
+      }
+      const float* bst = wsl + kWsumStash / 4;  // biases: gate [0, OC), up [OC, 2 OC); W row sums likewise at wsl
+      uint32_t od[4][2];
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int oc = 32 * wn + 8 * q4 + 4 * g;
+        const floatx4 bgv = *reinterpret_cast<const floatx4*>(bst + oc);
+        const floatx4 buv = *reinterpret_cast<const floatx4*>(bst + OC + oc);
+        float yg[4], yu[4];
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) {
+          yg[c4] = acc[0][4 * q4 + c4];
+          yu[c4] = acc[1][4 * q4 + c4];
+        }
+        if constexpr (LN) {
+          const floatx4 wgv = *reinterpret_cast<const floatx4*>(wsl + oc);
+          const floatx4 wuv = *reinterpret_cast<const floatx4*>(wsl + OC + oc);
+#pragma unroll
+          for (int c4 = 0; c4 < 4; ++c4) {
+            yg[c4] = ln_fold(yg[c4], rs, rm, wgv[c4]);
+            yu[c4] = ln_fold(yu[c4], rs, rm, wuv[c4]);
+          }
+        }
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const uint32_t gp = pack_bf16x2(yg[2 * p] + bgv[2 * p], yg[2 * p + 1] + bgv[2 * p + 1]);
+          const uint32_t up = pack_bf16x2(yu[2 * p] + buv[2 * p], yu[2 * p + 1] + buv[2 * p + 1]);
+          od[q4][p] = swiglu_bf16x2(bf16x2_lo(gp), bf16x2_hi(gp), bf16x2_lo(up), bf16x2_hi(up));
+        }
+      }
+      // 16-byte output chunks: chunk c8 (8 columns) of the wave's 32 is split
+      // over the lanes l32 and l32 + 32 (lane half g holds its columns
+      // 4 g .. 4 g + 3); the two swap halves so that lane half g stores chunk
+      // 2 pp + g whole, pp = 0, 1.
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp) {
+        const uint32_t w0 = g == 0 ? od[2 * pp + 1][0] : od[2 * pp][0];
+        const uint32_t w1 = g == 0 ? od[2 * pp + 1][1] : od[2 * pp][1];
+        const uint32_t x0 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w0), 32, 64));
+        const uint32_t x1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w1), 32, 64));
+        const u32x4 o = g == 0 ? u32x4{od[2 * pp][0], od[2 * pp][1], x0, x1}
+                               : u32x4{x0, x1, od[2 * pp + 1][0], od[2 * pp + 1][1]};
+        const int ocol = nt * OC + 32 * wn + 8 * (2 * pp + g);
+        if (row < G.m && ocol < n_out) *reinterpret_cast<u32x4*>(G.out + packed_act_offset(row, ocol, G.ldo)) = o;
+      }
+      // the ring's re-loads past the last stage write LDS: none may still be in
+      // flight when the workgroup ends and its LDS is released
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      return;
+    }
+  }
   // RoPE tables of the register Q / K epilogue's chunks (streams with RoPE),
   // loaded while the LayerNorm factors are reduced
   [[maybe_unused]] floatx4 rq_c[2][2], rq_s[2][2];
@@ -621,62 +727,6 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     rs = lnst[2 * r];
     rm = lnst[2 * r + 1];
   };
-  if constexpr (kRegEpi) {
-    if (reg_epi) {
-      // Lane (l32, g) of wave (wm, wn) holds, for tile row 32 wm + l32, the gate
-      // (acc[0]) and up (acc[1]) sums of the wave's output columns
-      // 8 q4 + 4 g + c (element 4 q4 + c): the sums the fp32 tile would hand to
-      // the store phase below, finished with the same arithmetic.
-      const int r = 32 * wm + l32, row = mt * R + r;
-      float rs = 0.f, rm = 0.f;
-      if constexpr (LN) ln_row(r, rs, rm);
-      const float* bst = wsl + kWsumStash / 4;  // biases: gate [0, OC), up [OC, 2 OC); W row sums likewise at wsl
-      uint32_t od[4][2];
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int oc = 32 * wn + 8 * q4 + 4 * g;
-        const floatx4 bgv = *reinterpret_cast<const floatx4*>(bst + oc);
-        const floatx4 buv = *reinterpret_cast<const floatx4*>(bst + OC + oc);
-        float yg[4], yu[4];
-#pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4) {
-          yg[c4] = acc[0][4 * q4 + c4];
-          yu[c4] = acc[1][4 * q4 + c4];
-        }
-        if constexpr (LN) {
-          const floatx4 wgv = *reinterpret_cast<const floatx4*>(wsl + oc);
-          const floatx4 wuv = *reinterpret_cast<const floatx4*>(wsl + OC + oc);
-#pragma unroll
-          for (int c4 = 0; c4 < 4; ++c4) {
-            yg[c4] = ln_fold(yg[c4], rs, rm, wgv[c4]);
-            yu[c4] = ln_fold(yu[c4], rs, rm, wuv[c4]);
-          }
-        }
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          const uint32_t gp = pack_bf16x2(yg[2 * p] + bgv[2 * p], yg[2 * p + 1] + bgv[2 * p + 1]);
-          const uint32_t up = pack_bf16x2(yu[2 * p] + buv[2 * p], yu[2 * p + 1] + buv[2 * p + 1]);
-          od[q4][p] = swiglu_bf16x2(bf16x2_lo(gp), bf16x2_hi(gp), bf16x2_lo(up), bf16x2_hi(up));
-        }
-      }
-      // 16-byte output chunks: chunk c8 (8 columns) of the wave's 32 is split
-      // over the lanes l32 and l32 + 32 (lane half g holds its columns
-      // 4 g .. 4 g + 3); the two swap halves so that lane half g stores chunk
-      // 2 pp + g whole, pp = 0, 1.
-#pragma unroll
-      for (int pp = 0; pp < 2; ++pp) {
-        const uint32_t w0 = g == 0 ? od[2 * pp + 1][0] : od[2 * pp][0];
-        const uint32_t w1 = g == 0 ? od[2 * pp + 1][1] : od[2 * pp][1];
-        const uint32_t x0 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w0), 32, 64));
-        const uint32_t x1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w1), 32, 64));
-        const u32x4 o = g == 0 ? u32x4{od[2 * pp][0], od[2 * pp][1], x0, x1}
-                               : u32x4{x0, x1, od[2 * pp + 1][0], od[2 * pp + 1][1]};
-        const int ocol = nt * OC + 32 * wn + 8 * (2 * pp + g);
-        if (row < G.m && ocol < n_out) *reinterpret_cast<u32x4*>(G.out + packed_act_offset(row, ocol, G.ldo)) = o;
-      }
-      return;
-    }
-  }
   // 8 consecutive fp32 sums (K-groups in order) of tile row r from tile column tc
   auto sum8 = [&](int r, int tc, float (&v)[8]) {
     floatx4 lo = *reinterpret_cast<const floatx4*>(&tiles[r * C::TP + tc]);
