@@ -515,10 +515,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   // as the store phase's reduction below; the prologue's barrier publishes them,
   // so the epilogue needs no barrier at all.
   float* const lnp = reinterpret_cast<float*>(lds) + C::RING * 256;
-  static_assert(!kRegEpi || (kThreads == 512 && C::RING * 1024 + (2 * kThreads + 2 * R) * 4 <= reg_ln_bytes<C>()),
+  constexpr bool kRegAny = kRegEpi || kRegQkv || TR;
+  const bool reg_any = reg_epi || reg_qkv || TR;
+  static_assert(!kRegAny || (kThreads == 512 && C::RING * 1024 + (2 * kThreads + 2 * R) * 4 <= reg_ln_bytes<C>()),
                 "LayerNorm factors of the register epilogue past the ring");
-  if constexpr (kRegEpi && LN) {
-    if (reg_epi) {
+  // the register Q / K epilogue's cross-wave exchange (8 waves x 64 lanes x 16 B) lies past the factors
+  static_assert(!kRegQkv || C::RING * 1024 + (2 * kThreads + 2 * R) * 4 + 8 * 64 * 16 <= kLdsQkvDeep - 16,
+                "QKV register epilogue exchange past the ring");
+  if constexpr (kRegAny && LN) {
+    if (reg_any) {
       float q1 = 0.f, q2 = 0.f;
 #pragma unroll
       for (int j = 0; j < kLnSlotsMax; ++j)
@@ -667,6 +672,163 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     }
   }
 
+  if constexpr (kRegQkv || TR) {
+    // The QKV epilogue's register paths, straight after the K loop (their
+    // operands lie past the ring, published by the loop's barriers): see the
+    // store phase below for the arithmetic they reproduce.
+    constexpr int D = 128;
+    const QkvOut& O = a.qkv;
+    const int n0 = nt * OC;
+    const int which = n0 / O.inner;  // uniform per tile
+    const int h0 = (n0 - which * O.inner) / D;
+    if constexpr (kRegQkv) {
+      if (reg_qkv) {
+        // Lane (l32, g) of wave (wm, wn) holds, for tile row 32 wm + l32, the
+        // sums of head columns 64 wn + 32 bb + 8 q4 + 4 g + c (acc[bb], element
+        // 4 q4 + c): halves of the head's 8-column chunks 8 wn + 4 bb + q4.  The
+        // arithmetic is the store phase's below: x = bf16(fold(acc) + bias); the
+        // chunks made whole by a swap of halves with lane l ^ 32 (lane half g
+        // keeps chunks 8 wn + 4 bb + 2 pp + g); each chunk's sum of squares in
+        // column order; then the same butterfly over the row's 16 chunks, level
+        // by level: chunk ^ 8 is the other wave of the row (through LDS), ^ 4
+        // and ^ 2 are in the lane, ^ 1 is lane l ^ 32.
+        static_assert(D == 128 && OC == 128, "one head of 128 columns per tile");
+        const int r = 32 * wm + l32, row = mt * R + r;
+        float rs = 0.f, rm = 0.f;
+        if constexpr (LN) {
+          rs = lnp[2 * kThreads + 2 * r];
+          rm = lnp[2 * kThreads + 2 * r + 1];
+        }
+        uint32_t xp[2][4][2];
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+              float x0 = acc[bb][4 * q4 + 2 * p], x1 = acc[bb][4 * q4 + 2 * p + 1];
+              if constexpr (LN) {
+                x0 = ln_fold(x0, rs, rm, rq_ws[bb][q4][2 * p]);
+                x1 = ln_fold(x1, rs, rm, rq_ws[bb][q4][2 * p + 1]);
+              }
+              xp[bb][q4][p] = pack_bf16x2(x0 + bf16x2_lo(rq_b[bb][q4][p]), x1 + bf16x2_hi(rq_b[bb][q4][p]));
+            }
+        u32x4 xc[2][2];
+        float ss[2][2];
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+          for (int pp = 0; pp < 2; ++pp) {
+            const uint32_t w0 = g == 0 ? xp[bb][2 * pp + 1][0] : xp[bb][2 * pp][0];
+            const uint32_t w1 = g == 0 ? xp[bb][2 * pp + 1][1] : xp[bb][2 * pp][1];
+            const uint32_t o0 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w0), 32, 64));
+            const uint32_t o1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w1), 32, 64));
+            xc[bb][pp] = g == 0 ? u32x4{xp[bb][2 * pp][0], xp[bb][2 * pp][1], o0, o1}
+                                : u32x4{o0, o1, xp[bb][2 * pp + 1][0], xp[bb][2 * pp + 1][1]};
+            float s2 = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float lo = bf16x2_lo(xc[bb][pp][e]), hi = bf16x2_hi(xc[bb][pp][e]);
+              s2 += lo * lo;
+              s2 += hi * hi;
+            }
+            ss[bb][pp] = s2;
+          }
+        floatx4* const exch = reinterpret_cast<floatx4*>(lnp + 2 * kThreads + 2 * R);  // [8 waves][64 lanes], past the ring
+        exch[wv * 64 + lane] = floatx4{ss[0][0], ss[0][1], ss[1][0], ss[1][1]};
+        __syncthreads();
+        const floatx4 ps = exch[(wv ^ 1) * 64 + lane];  // the row's other wave: wn ^ 1
+        const float t00 = ss[0][0] + ps[0], t01 = ss[0][1] + ps[1], t10 = ss[1][0] + ps[2], t11 = ss[1][1] + ps[3];
+        const float u0 = t00 + t10, u1 = t01 + t11;
+        const float v = u0 + u1;
+        const float sum = v + __shfl_xor(v, 32, 64);
+        uint16_t* kvh = O.kvp + h0 * O.kvp_sh;
+        const int64_t key = static_cast<int64_t>(G.m_begin) + row;
+        {
+#pragma clang fp contract(off)
+          const float rinv = 1.0f / __builtin_sqrtf(sum * (1.0f / D) + O.eps);
+#pragma unroll
+          for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+            for (int pp = 0; pp < 2; ++pp) {
+              const int cd = 64 * wn + 32 * bb + 16 * pp + 8 * g;
+              float y[8];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float xl = bf16x2_lo(xc[bb][pp][e]), xh = bf16x2_hi(xc[bb][pp][e]);
+                const uint32_t yp = pack_bf16x2(bf16x2_lo(rq_w[bb][pp][e]) * (xl * rinv),
+                                                bf16x2_hi(rq_w[bb][pp][e]) * (xh * rinv));
+                y[2 * e] = bf16x2_lo(yp);
+                y[2 * e + 1] = bf16x2_hi(yp);
+              }
+              u32x4 o;
+              if (G.cos != nullptr) {
+                const floatx4 c = rq_c[bb][pp], sn = rq_s[bb][pp];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                  const float re = y[2 * p], im = y[2 * p + 1];
+                  o[p] = pack_bf16x2(re * c[p] - im * sn[p], re * sn[p] + im * c[p]);
+                }
+              } else {
+#pragma unroll
+                for (int p = 0; p < 4; ++p) o[p] = pack_bf16x2(y[2 * p], y[2 * p + 1]);
+              }
+              if (row < G.m) {
+                if (which == 0)
+                  *reinterpret_cast<u32x4*>(O.q + h0 * O.q_sh + key * O.q_sm + cd) = o;
+                else
+                  *reinterpret_cast<u32x4*>(kvh + packed_k_offset(key, cd, D)) = o;
+              } else if (which == 1 && (row & ~31) < G.m) {
+                *reinterpret_cast<u32x4*>(kvh + packed_k_offset(key, cd, D)) = u32x4{0, 0, 0, 0};
+              }
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // (the ring's re-loads write LDS)
+        return;
+      }
+    }
+    if constexpr (TR) {
+      // V tile with untransposed accumulators: lane (l32, g) of wave (wm, wn)
+      // holds head column d = 32 db + l32 (db = 2 wn + bb) of keys
+      // 32 wm + 8 q + 4 g + c (acc[bb], element 4 q + c) -- element e of packed
+      // V chunk 2 db + s2 is acc[bb][8 s2 + e], the lane's own.  The store
+      // phase's arithmetic below, without the fp32 tile.
+      constexpr int NCH = D / 16;
+      const int row0 = mt * R + 32 * wm;  // first stream row of the wave's 32-key tile
+      if (row0 < G.m) {
+        uint16_t* kvt = O.kvp + h0 * O.kvp_sh + ((G.m_begin + row0) >> 5) * (64 * D) + NCH * 512;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          float rs[8], rm[8];  // LayerNorm factors of the chunk's keys 32 wm + 16 s2 + 8 (e / 4) + 4 g + e % 4
+          if constexpr (LN) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int rr = 32 * wm + 16 * s2 + 8 * (e >> 2) + 4 * g + (e & 3);
+              rs[e] = lnp[2 * kThreads + 2 * rr];
+              rm[e] = lnp[2 * kThreads + 2 * rr + 1];
+            }
+          }
+#pragma unroll
+          for (int bb = 0; bb < 2; ++bb) {
+            u32x4 o;
+#pragma unroll
+            for (int e2 = 0; e2 < 4; ++e2) {
+              float lo = acc[bb][8 * s2 + 2 * e2], hi = acc[bb][8 * s2 + 2 * e2 + 1];
+              if constexpr (LN) {
+                lo = ln_fold(lo, rs[2 * e2], rm[2 * e2], rv_ws[bb]);
+                hi = ln_fold(hi, rs[2 * e2 + 1], rm[2 * e2 + 1], rv_ws[bb]);
+              }
+              const int k0 = row0 + 16 * s2 + 8 * (e2 >> 1) + 4 * g + 2 * (e2 & 1);
+              o[e2] = pack_bf16x2(k0 < G.m ? lo + rv_b[bb] : 0.f, k0 + 1 < G.m ? hi + rv_b[bb] : 0.f);
+            }
+            *reinterpret_cast<u32x4*>(kvt + ((2 * (2 * wn + bb) + s2) * 64 + lane) * 8) = o;
+          }
+        }
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // (the ring's re-loads write LDS)
+        return;
+    }
+  }
   float bg[8], bu[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -761,144 +923,6 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     const int n0 = nt * OC;
     const int which = n0 / O.inner;  // uniform per tile
     const int h0 = (n0 - which * O.inner) / D;
-    if constexpr (kRegQkv) {
-      if (reg_qkv) {
-        // Lane (l32, g) of wave (wm, wn) holds, for tile row 32 wm + l32, the
-        // sums of head columns 64 wn + 32 bb + 8 q4 + 4 g + c (acc[bb], element
-        // 4 q4 + c): halves of the head's 8-column chunks 8 wn + 4 bb + q4.  The
-        // arithmetic is the store phase's below: x = bf16(fold(acc) + bias); the
-        // chunks made whole by a swap of halves with lane l ^ 32 (lane half g
-        // keeps chunks 8 wn + 4 bb + 2 pp + g); each chunk's sum of squares in
-        // column order; then the same butterfly over the row's 16 chunks, level
-        // by level: chunk ^ 8 is the other wave of the row (through LDS), ^ 4
-        // and ^ 2 are in the lane, ^ 1 is lane l ^ 32.
-        static_assert(D == 128 && OC == 128, "one head of 128 columns per tile");
-        const int r = 32 * wm + l32, row = mt * R + r;
-        float rs = 0.f, rm = 0.f;
-        if constexpr (LN) ln_row(r, rs, rm);
-        uint32_t xp[2][4][2];
-#pragma unroll
-        for (int bb = 0; bb < 2; ++bb)
-#pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4)
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-              float x0 = acc[bb][4 * q4 + 2 * p], x1 = acc[bb][4 * q4 + 2 * p + 1];
-              if constexpr (LN) {
-                x0 = ln_fold(x0, rs, rm, rq_ws[bb][q4][2 * p]);
-                x1 = ln_fold(x1, rs, rm, rq_ws[bb][q4][2 * p + 1]);
-              }
-              xp[bb][q4][p] = pack_bf16x2(x0 + bf16x2_lo(rq_b[bb][q4][p]), x1 + bf16x2_hi(rq_b[bb][q4][p]));
-            }
-        u32x4 xc[2][2];
-        float ss[2][2];
-#pragma unroll
-        for (int bb = 0; bb < 2; ++bb)
-#pragma unroll
-          for (int pp = 0; pp < 2; ++pp) {
-            const uint32_t w0 = g == 0 ? xp[bb][2 * pp + 1][0] : xp[bb][2 * pp][0];
-            const uint32_t w1 = g == 0 ? xp[bb][2 * pp + 1][1] : xp[bb][2 * pp][1];
-            const uint32_t o0 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w0), 32, 64));
-            const uint32_t o1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w1), 32, 64));
-            xc[bb][pp] = g == 0 ? u32x4{xp[bb][2 * pp][0], xp[bb][2 * pp][1], o0, o1}
-                                : u32x4{o0, o1, xp[bb][2 * pp + 1][0], xp[bb][2 * pp + 1][1]};
-            float s2 = 0.f;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float lo = bf16x2_lo(xc[bb][pp][e]), hi = bf16x2_hi(xc[bb][pp][e]);
-              s2 += lo * lo;
-              s2 += hi * hi;
-            }
-            ss[bb][pp] = s2;
-          }
-        floatx4* const exch = reinterpret_cast<floatx4*>(tiles);  // [8 waves][64 lanes], in the ring's area
-        exch[wv * 64 + lane] = floatx4{ss[0][0], ss[0][1], ss[1][0], ss[1][1]};
-        __syncthreads();
-        const floatx4 ps = exch[(wv ^ 1) * 64 + lane];  // the row's other wave: wn ^ 1
-        const float t00 = ss[0][0] + ps[0], t01 = ss[0][1] + ps[1], t10 = ss[1][0] + ps[2], t11 = ss[1][1] + ps[3];
-        const float u0 = t00 + t10, u1 = t01 + t11;
-        const float v = u0 + u1;
-        const float sum = v + __shfl_xor(v, 32, 64);
-        uint16_t* kvh = O.kvp + h0 * O.kvp_sh;
-        const int64_t key = static_cast<int64_t>(G.m_begin) + row;
-        {
-#pragma clang fp contract(off)
-          const float rinv = 1.0f / __builtin_sqrtf(sum * (1.0f / D) + O.eps);
-#pragma unroll
-          for (int bb = 0; bb < 2; ++bb)
-#pragma unroll
-            for (int pp = 0; pp < 2; ++pp) {
-              const int cd = 64 * wn + 32 * bb + 16 * pp + 8 * g;
-              float y[8];
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const float xl = bf16x2_lo(xc[bb][pp][e]), xh = bf16x2_hi(xc[bb][pp][e]);
-                const uint32_t yp = pack_bf16x2(bf16x2_lo(rq_w[bb][pp][e]) * (xl * rinv),
-                                                bf16x2_hi(rq_w[bb][pp][e]) * (xh * rinv));
-                y[2 * e] = bf16x2_lo(yp);
-                y[2 * e + 1] = bf16x2_hi(yp);
-              }
-              u32x4 o;
-              if (G.cos != nullptr) {
-                const floatx4 c = rq_c[bb][pp], sn = rq_s[bb][pp];
-#pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                  const float re = y[2 * p], im = y[2 * p + 1];
-                  o[p] = pack_bf16x2(re * c[p] - im * sn[p], re * sn[p] + im * c[p]);
-                }
-              } else {
-#pragma unroll
-                for (int p = 0; p < 4; ++p) o[p] = pack_bf16x2(y[2 * p], y[2 * p + 1]);
-              }
-              if (row < G.m) {
-                if (which == 0)
-                  *reinterpret_cast<u32x4*>(O.q + h0 * O.q_sh + key * O.q_sm + cd) = o;
-                else
-                  *reinterpret_cast<u32x4*>(kvh + packed_k_offset(key, cd, D)) = o;
-              } else if (which == 1 && (row & ~31) < G.m) {
-                *reinterpret_cast<u32x4*>(kvh + packed_k_offset(key, cd, D)) = u32x4{0, 0, 0, 0};
-              }
-            }
-        }
-        return;
-      }
-    }
-    if constexpr (TR) {
-      // V tile with untransposed accumulators: lane (l32, g) of wave (wm, wn)
-      // holds head column d = 32 db + l32 (db = 2 wn + bb) of keys
-      // 32 wm + 8 q + 4 g + c (acc[bb], element 4 q + c) -- element e of packed
-      // V chunk 2 db + s2 is acc[bb][8 s2 + e], the lane's own.  The store
-      // phase's arithmetic below, without the fp32 tile.
-      constexpr int NCH = D / 16;
-      const int row0 = mt * R + 32 * wm;  // first stream row of the wave's 32-key tile
-      if (row0 < G.m) {
-        uint16_t* kvt = O.kvp + h0 * O.kvp_sh + ((G.m_begin + row0) >> 5) * (64 * D) + NCH * 512;
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          float rs[8], rm[8];  // LayerNorm factors of the chunk's keys 32 wm + 16 s2 + 8 (e / 4) + 4 g + e % 4
-          if constexpr (LN) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ln_row(32 * wm + 16 * s2 + 8 * (e >> 2) + 4 * g + (e & 3), rs[e], rm[e]);
-          }
-#pragma unroll
-          for (int bb = 0; bb < 2; ++bb) {
-            u32x4 o;
-#pragma unroll
-            for (int e2 = 0; e2 < 4; ++e2) {
-              float lo = acc[bb][8 * s2 + 2 * e2], hi = acc[bb][8 * s2 + 2 * e2 + 1];
-              if constexpr (LN) {
-                lo = ln_fold(lo, rs[2 * e2], rm[2 * e2], rv_ws[bb]);
-                hi = ln_fold(hi, rs[2 * e2 + 1], rm[2 * e2 + 1], rv_ws[bb]);
-              }
-              const int k0 = row0 + 16 * s2 + 8 * (e2 >> 1) + 4 * g + 2 * (e2 & 1);
-              o[e2] = pack_bf16x2(k0 < G.m ? lo + rv_b[bb] : 0.f, k0 + 1 < G.m ? hi + rv_b[bb] : 0.f);
-            }
-            *reinterpret_cast<u32x4*>(kvt + ((2 * (2 * wn + bb) + s2) * 64 + lane) * 8) = o;
-          }
-        }
-      }
-      return;
-    }
     if (which == 2) {
       constexpr int NCH = D / 16;  // 1 KB chunks per K or V part of a head's 32-key tile
       static_assert(kThreads % (HPT * NCH * 64) == 0, "a thread's V column (hh, idx) is the same on every pass");
