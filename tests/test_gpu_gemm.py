@@ -486,7 +486,8 @@ def test_concatenated_packed_operand_from_attention_and_bias_packed_gemm(dev):
     assert torch.equal(wide.unpack()[:, 1024:], sw)
 
 
-@pytest.mark.parametrize("ms,H,k,D", [((512, 64, 32), 12, 1536, 128), ((1024, 64, 32), 12, 256, 128),
+@pytest.mark.parametrize("ms,H,k,D", [((512, 64, 32), 12, 1536, 128), ((470, 64, 32), 12, 1536, 128),
+                                     ((1024, 64, 32), 12, 256, 128),
                                      ((64, 32, 20), 2, 256, 128), ((40,), 3, 384, 128), ((0, 96, 64), 2, 128, 128),
                                      ((64, 18), 24, (4096, 1536), 64), ((96, 32, 17), 24, (4096, 1536, 1536), 64),
                                      ((64, 18), 24, 1536, 64), ((40,), 2, 256, 64), ((32, 20), 4, (384, 256), 64),
@@ -498,7 +499,8 @@ def test_grouped_gemm_qkv_norm_rope_matches_two_launches(dev, ms, H, k, D):
     Q (H, M, D) and every element of the packed K/V tiles, including the zero
     padding keys of a last stream whose rows are not a multiple of 32.  Shapes:
     the action step's streams (128 x 128 and 64 x 128 tiles, one workgroup per
-    CU), 1024 rows (more than 256 workgroups: two per CU), short and single
+    CU; the 128 x 128 tiles finish in registers, also with 470 rows: a partial
+    last tile, padding keys 470-479 in its last 32-key tile), 1024 rows (more than 256 workgroups: two per CU), short and single
     streams, an empty stream; head_dim 64 (two heads per tile) with the RLDX-1
     double-stream shapes (VL 4096 | SA 1536 [| P 1536], a K per stream:
     rldx_grouped_gemm_qkv_norm_rope_mixed_bf16) and the single-stream shape.
@@ -784,7 +786,47 @@ def test_grouped_gemm_residual_packed_epilogue_bit_identical(dev):
             assert err <= 1e-5 * ref_st.abs().max().item(), f"split {split}, rows {lo}: statistics off by {err}"
 
 
-@pytest.mark.parametrize("ms,H,k", [((512, 64, 32), 12, 1536), ((40,), 3, 384)])
+@pytest.mark.parametrize("ms,n,ln", [((512, 64, 32), 8192, False), ((512, 64, 32), 8192, True),
+                                     ((300, 64, 32), 8256, False), ((300, 64, 32), 8256, True),
+                                     ((257,), 16448, True)])
+def test_swiglu_packed_register_epilogue_bit_identical(dev, ms, n, ln):
+    """The packed SwiGLU epilogue of the 128 x 128 tiles (streams of >= 256 rows)
+    finishes in registers in the narrow kernel; the wide kernel runs the same
+    tiles and K-groups through the fp32 tile and the store phase.  Both give the
+    same bits, with and without the LayerNorm fold, also for a partial last row
+    tile (300, 257 rows) and a partial last column tile (n / 2 = 4128, 8224:
+    half of the last 64-column tile past the outputs)."""
+    g = torch.Generator().manual_seed(sum(ms) + n + ln)
+    k = 1536
+    data = []
+    for m in ms:
+        x = _rand((m, k), g).to(dev)
+        w = Fn.pack_weight(_rand((n, k), g, std=0.3 * k ** -0.5).to(dev), swiglu_pairs=True)
+        b = _rand((n,), g, 0.1).to(dev)
+        data.append((x, w, b))
+    outs = []
+    for wide in (False, True):
+        items, stats = [], []
+        for x, w, b in data:
+            st = Fn.ln_stats_empty(x.shape[0], k, dev) if ln else None
+            items.append((Fn.pack_act(x, stats=st) if ln else Fn.pack_act(x), w, b,
+                          Fn.PackedAct.empty(x.shape[0], n // 2, dev), None))
+            stats.append(st)
+        Fn.grouped_gemm(items, "swiglu_packed", wide_tiles=wide, ln_eps=1e-6 if ln else None,
+                        ln_stats=stats if ln else None)
+        torch.cuda.synchronize()
+        outs.append([it[3].unpack().clone() for it in items])
+    for x, y in zip(*outs):
+        assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+    if not ln:  # and the row-major SwiGLU epilogue (store phase) gives the same bits as well
+        for (x, w, b), got in zip(data, outs[0]):
+            rm = torch.empty(x.shape[0], n // 2, dtype=BF16, device=dev)
+            Fn.grouped_gemm([(Fn.pack_act(x), w, b, rm, None)], "swiglu")
+            torch.cuda.synchronize()
+            assert torch.equal(got.view(torch.int16), rm.view(torch.int16))
+
+
+@pytest.mark.parametrize("ms,H,k", [((512, 64, 32), 12, 1536), ((64, 470), 12, 1536), ((40,), 3, 384)])
 def test_grouped_gemm_qkv_norm_rope_layernorm_fold(dev, ms, H, k):
     """The QKV epilogue with the LayerNorm fold is bit-identical to the folded
     bias GEMM followed by rldx_msat_qkv_norm_rope_bf16 (same fold arithmetic in
