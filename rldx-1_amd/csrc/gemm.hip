@@ -593,8 +593,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   if constexpr (kRegEpi) {
     if (reg_epi) {
       // Straight after the K loop: no operand of this epilogue is in the ring
-      // (the stashes and the LayerNorm factors lie past it, published by the
-      // loop's barriers), so no wave waits for another.
+      // (the stashes and the LayerNorm factors lie past it, written before the
+      // prologue's barrier), so no wave waits for another.
       // Lane (l32, g) of wave (wm, wn) holds, for tile row 32 wm + l32, the gate
       // (acc[0]) and up (acc[1]) sums of the wave's output columns
       // 8 q4 + 4 g + c (element 4 q4 + c): the sums the fp32 tile would hand to
@@ -656,7 +656,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     }
   }
   // RoPE tables of the register Q / K epilogue's chunks (streams with RoPE),
-  // loaded while the LayerNorm factors are reduced
+  // loaded after the K loop rather than held through it
   [[maybe_unused]] floatx4 rq_c[2][2], rq_s[2][2];
   if constexpr (kRegQkv) {
     if (reg_qkv && G.cos != nullptr) {
@@ -826,7 +826,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
         }
       }
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // (the ring's re-loads write LDS)
-        return;
+      return;
     }
   }
   float bg[8], bu[8];
