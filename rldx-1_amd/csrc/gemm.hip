@@ -340,10 +340,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
   const int col = nt * OC + cc;  // global output column of this thread's chunks
   const bool col_ok = col < n_out;
   // residual chunks (each is read and written by this thread, so it may alias the output)
+  // Register epilogue of the packed residual epilogue on 64 x 64 tiles (two
+  // K-groups of 2 x 2 waves, one n-block per wave) in the deep kernels: each
+  // K-group finishes half of the tile's 8-column chunks (see there).
+  constexpr bool kRegRes = EPI == kEpiResidualPacked && C::MB == 2 && C::NB == 2 && BNW == 1 && C::KG == 2 && DP;
+  const bool reg_res = kRegRes && G.splits == 1;
   u32x4 pres[PER];
   if constexpr (residual_epi(EPI)) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
+      pres[i] = u32x4{0, 0, 0, 0};
+      if (reg_res) continue;
       const int t = static_cast<int>(threadIdx.x) + kThreads * i;
       const int row = mt * R + t / CPR;
       const int64_t off = EPI == kEpiResidualPacked ? packed_act_offset(row, col, G.ldr)
@@ -378,7 +385,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
     const int bcol = col_ok ? col : 0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) braw[i] = 0;
-    if (!reg_epi && !reg_qkv) {
+    if (!reg_epi && !reg_qkv && !reg_res) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         braw[i] = static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(brs, (bcol + i) * 2, 0, 0));
@@ -490,6 +497,23 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
       const int c0 = nt * OC + 32 * (2 * wn + bb) + l32;
       rv_b[bb] = bf(static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(brs, c0 * 2, 0, 0)));
       if constexpr (LN) rv_ws[bb] = G.wsum[c0];
+    }
+  }
+  // register residual epilogue operands: the biases of the lane's columns in
+  // the two chunks its K-group finishes, and the residual chunk it stores
+  [[maybe_unused]] uint32_t rr_b[2][2];
+  [[maybe_unused]] u32x4 rr_res = {0, 0, 0, 0};
+  if constexpr (kRegRes) {
+    if (reg_res) {
+      const __amdgpu_buffer_rsrc_t brs = rsrc(G.bias, G.bias ? G.n * 2 : 0);  // no bias, or past n: reads zero
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int c0 = nt * OC + 32 * wn + 8 * (2 * grp + j) + 4 * g;
+        rr_b[j][0] = __builtin_amdgcn_raw_buffer_load_b32(brs, c0 * 2, 0, 0);
+        rr_b[j][1] = __builtin_amdgcn_raw_buffer_load_b32(brs, c0 * 2 + 4, 0, 0);
+      }
+      const int row = mt * R + 32 * wm + l32, ocol = nt * OC + 32 * wn + 8 * (2 * grp + g);
+      if (row < G.m && ocol < n_out) rr_res = *reinterpret_cast<const u32x4*>(G.res + packed_act_offset(row, ocol, G.ldr));
     }
   }
   // LayerNorm fold: this thread's slots of its row, loaded before the ring
@@ -652,6 +676,78 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Group& G, int
       // the ring's re-loads past the last stage write LDS: none may still be in
       // flight when the workgroup ends and its LDS is released
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      return;
+    }
+  }
+  if constexpr (kRegRes) {
+    if (reg_res) {
+      // Lane (l32, g) of wave (wm, wn) in K-group hg holds that group's partial
+      // sums for tile row 32 wm + l32 and columns 32 wn + 8 q4 + 4 g + c
+      // (element 4 q4 + c).  K-group hg finishes chunks q4 = 2 hg, 2 hg + 1 of
+      // the wave's 32 columns: it hands the other group its partials of the
+      // other two chunks (through LDS past the ring; the ring's last re-loads may
+      // still be in flight), adds the other group's partials of its own two, and
+      // then runs the store phase's arithmetic: bias, a swap of halves with lane
+      // l ^ 32 so that it stores chunk 2 hg + g whole, the residual, and the row
+      // statistics with the store phase's butterfly over the row's 8 chunks
+      // (chunk 4 wn + 2 hg + g: ^4 is the group's other wave, ^2 the other
+      // group, both through LDS, ^1 lane l ^ 32).
+      static_assert(C::RING * 1024 + 8 * 64 * (32 + 8) <= kLdsDeep - kLdsTail, "residual exchange past the ring");
+      const int hg = grp;
+      floatx4* const xp = reinterpret_cast<floatx4*>(lnp);  // [8 waves][64 lanes][2 float4]
+      const floatx4 lo4 = floatx4{acc[0][0], acc[0][1], acc[0][2], acc[0][3]};
+      const floatx4 lo8 = floatx4{acc[0][4], acc[0][5], acc[0][6], acc[0][7]};
+      const floatx4 hi4 = floatx4{acc[0][8], acc[0][9], acc[0][10], acc[0][11]};
+      const floatx4 hi8 = floatx4{acc[0][12], acc[0][13], acc[0][14], acc[0][15]};
+      xp[(wv * 64 + lane) * 2] = hg == 0 ? hi4 : lo4;  // the other group's chunks
+      xp[(wv * 64 + lane) * 2 + 1] = hg == 0 ? hi8 : lo8;
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      const int po = ((wv ^ 4) * 64 + lane) * 2;  // the same wave of the other group
+      const floatx4 p0 = xp[po], p1 = xp[po + 1];
+      const floatx4 m0 = hg == 0 ? lo4 : hi4, m1 = hg == 0 ? lo8 : hi8;
+      // sums in K-group order (group 0's partial first)
+      const floatx4 s0 = hg == 0 ? m0 + p0 : p0 + m0, s1v = hg == 0 ? m1 + p1 : p1 + m1;
+      uint32_t od[2][2];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        od[0][p] = pack_bf16x2(s0[2 * p] + bf16x2_lo(rr_b[0][p]), s0[2 * p + 1] + bf16x2_hi(rr_b[0][p]));
+        od[1][p] = pack_bf16x2(s1v[2 * p] + bf16x2_lo(rr_b[1][p]), s1v[2 * p + 1] + bf16x2_hi(rr_b[1][p]));
+      }
+      const uint32_t w0 = g == 0 ? od[1][0] : od[0][0], w1 = g == 0 ? od[1][1] : od[0][1];
+      const uint32_t x0 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w0), 32, 64));
+      const uint32_t x1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w1), 32, 64));
+      const u32x4 yv = g == 0 ? u32x4{od[0][0], od[0][1], x0, x1} : u32x4{x0, x1, od[1][0], od[1][1]};
+      const int row = mt * R + 32 * wm + l32, ocol = nt * OC + 32 * wn + 8 * (2 * hg + g);
+      const bool ok = row < G.m && ocol < n_out;
+      u32x4 o = {0, 0, 0, 0};
+      if (ok) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = pack_bf16x2(bf16x2_lo(rr_res[e]) + bf16x2_lo(yv[e]), bf16x2_hi(rr_res[e]) + bf16x2_hi(yv[e]));
+        *reinterpret_cast<u32x4*>(G.out + packed_act_offset(row, ocol, G.ldo)) = o;
+      }
+      if (G.stats_out) {
+        float t1 = 0.f, t2 = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = bf16x2_lo(o[e]), hi = bf16x2_hi(o[e]);
+          t1 += lo + hi;
+          t2 += lo * lo + hi * hi;
+        }
+        f32x2_t* const xs = reinterpret_cast<f32x2_t*>(lnp + 8 * 64 * 8);  // [8 waves][64 lanes], past the partials
+        xs[wv * 64 + lane] = f32x2_t{t1, t2};
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const f32x2_t a4 = xs[(wv ^ 1) * 64 + lane], a2 = xs[(wv ^ 4) * 64 + lane], a6 = xs[(wv ^ 5) * 64 + lane];
+        float u1 = t1 + a4[0], u2 = t2 + a4[1];                 // chunks c, c ^ 4
+        const float v1 = a2[0] + a6[0], v2 = a2[1] + a6[1];     // chunks c ^ 2, c ^ 6
+        u1 = u1 + v1;
+        u2 = u2 + v2;
+        u1 += __shfl_xor(u1, 32, 64);
+        u2 += __shfl_xor(u2, 32, 64);
+        if (wn == 0 && hg == 0 && g == 0 && row < G.m)
+          *(reinterpret_cast<f32x2_t*>(G.stats_out) + static_cast<int64_t>(nt * (OC / 64)) * G.m + row) = f32x2_t{u1, u2};
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // (the ring's re-loads write LDS)
       return;
     }
   }
