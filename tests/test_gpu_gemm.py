@@ -752,18 +752,23 @@ def _slot_sums(x: torch.Tensor) -> torch.Tensor:
     return torch.stack([v.sum(-1), (v * v).sum(-1)], dim=-1).transpose(0, 1)
 
 
-def test_grouped_gemm_residual_packed_epilogue_bit_identical(dev):
+@pytest.mark.parametrize("rows,k", [(((0, 512), (512, 576), (576, 608)), 4096),
+                                    (((0, 300), (320, 360), (384, 404)), 1536)])
+def test_grouped_gemm_residual_packed_epilogue_bit_identical(dev, rows, k):
     """RLDX_GEMM_EPI_RESIDUAL_PACKED (the residual stream held in the packed
     activation order, updated in place) gives the row-major residual epilogue's
     bits, with and without split-K; with stats_out (rldx_grouped_gemm_stats_bf16)
     the same bits again, and per row and 64-column slot the sum and sum of
-    squares of the stored values (fp32 against fp64: relative 1e-5)."""
-    g = torch.Generator().manual_seed(23)
-    n, k = 1536, 4096
-    x = _rand((608, n), g, 0.5).to(dev)
-    h = _rand((608, k), g).to(dev)
+    squares of the stored values (fp32 against fp64: relative 1e-5).  Without
+    split-K the 64 x 64 tiles of the launch (one workgroup per CU) finish in
+    registers; ragged streams (300 / 40 / 20 rows, each starting on a 32-row
+    boundary of the packed stream) give them a partial last row tile."""
+    g = torch.Generator().manual_seed(23 + k)
+    n = 1536
+    m_all = rows[-1][1]
+    x = _rand((m_all, n), g, 0.5).to(dev)
+    h = _rand((m_all, k), g).to(dev)
     ws = [(_rand((n, k), g, 0.008).to(dev), _rand((n,), g, 0.1).to(dev)) for _ in range(3)]
-    rows = ((0, 512), (512, 576), (576, 608))
     for split in (1, 4):
         xr, xp = x.clone(), Fn.pack_act(x)
         it_r = [(h[lo:hi], Fn.pack_weight(w), b, xr[lo:hi], xr[lo:hi]) for (lo, hi), (w, b) in zip(rows, ws)]
